@@ -1,0 +1,169 @@
+/* seeker_hip.h - C ABI of the MI355X (gfx950) speculative-decoding verify path.
+ *
+ * Drop-in boundary for the spec-decode subset of seeker-vulkan's `inference` +
+ * `models` module surface (rgcottrell/seeker binds its backend by module
+ * re-export, apps/seeker-cli/src/main.rs:22-29). A Rust crate binds this header
+ * with bindgen exactly as crates/seeker-npu/build.rs:36-50 binds npu_shim.h.
+ *
+ * Conventions (mirroring crates/seeker-npu/shim/npu_shim.h:2-18):
+ *  - every fallible call returns an int status, 0 = SH_OK; on failure the
+ *    calling thread's sh_last_error() holds a human-readable message
+ *    (the Rust side's Result<_, Box<dyn Error>> message);
+ *  - handles are opaque and owned by the caller, released with *_destroy;
+ *  - an sh_engine is driven by one host thread and owns one HIP stream;
+ *    calls that return host data are synchronous;
+ *  - host arrays are caller-allocated with explicit lengths;
+ *  - "_dev" pointers are device pointers obtained from sh_dev_alloc.
+ * Nothing here allocates on the host on behalf of the caller.
+ */
+#ifndef SEEKER_HIP_H
+#define SEEKER_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sh_engine sh_engine;
+typedef struct sh_model sh_model;
+typedef struct sh_kv sh_kv;
+typedef struct sh_qtensor sh_qtensor;
+
+enum sh_status {
+  SH_OK = 0,
+  SH_ERR_ARG = 1,         /* invalid argument / precondition (mod.rs:2326-2360 style) */
+  SH_ERR_HIP = 2,         /* HIP runtime failure */
+  SH_ERR_FORMAT = 3,      /* malformed or unsupported GGUF */
+  SH_ERR_UNSUPPORTED = 4, /* valid request this build does not implement */
+  SH_ERR_CAPACITY = 5,    /* KV capacity / size limit exceeded */
+  SH_ERR_STATE = 6        /* cache position mismatch (llama.rs:186-192) */
+};
+
+/* Sampling modes for verify / spec steps. */
+enum sh_sample_mode {
+  SH_SAMPLE_GREEDY = 0,    /* per-column argmax, lowest index on ties (sample.rs:504-514) */
+  SH_SAMPLE_COMPARE = 1,   /* reference sample-and-compare: softmax(l/T) inverse CDF in
+                              vocab-index order (ops/sampler.rs:303-368) with per-column
+                              uniforms, accept while sample == draft (sample.rs:347-361) */
+  SH_SAMPLE_REJECTION = 2  /* new: min(1, p/q) accept + residual max(0, p - q) resample */
+};
+
+typedef struct sh_sampling {
+  uint32_t mode;          /* enum sh_sample_mode */
+  float temperature;      /* > 0 for COMPARE / REJECTION */
+  uint64_t seed;          /* Philox4x64-10 key word 0 */
+  uint64_t counter;       /* Philox word offset; advanced by calls that consume uniforms */
+  const float* uniforms;  /* optional explicit host uniforms (overrides Philox), or NULL */
+} sh_sampling;
+
+typedef struct sh_model_dims {
+  uint32_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_ctx_train;
+  float rms_eps, rope_freq_base;
+  int32_t weight_type; /* GGML type id of the 2-D weights */
+  double weight_bytes; /* bytes a full-logits forward reads from the weight matrices */
+} sh_model_dims;
+
+typedef struct sh_kernel_stat {
+  char name[48];
+  uint64_t launches;
+  double total_ms;
+  double alg_bytes; /* algorithmic bytes summed over launches */
+} sh_kernel_stat;
+
+/* ---------------------------------------------------------------- misc */
+const char* sh_last_error(void);
+const char* sh_version(void);
+
+/* ------------------------------------------------------------- engine */
+/* Engine::new (crates/seeker-vulkan/src/inference/mod.rs:198). */
+int sh_engine_create(int hip_device, sh_engine** out);
+void sh_engine_destroy(sh_engine* e);
+int sh_engine_sync(sh_engine* e);
+/* Per-kernel hipEvent timing of every launch (profile.rs:25-173 analog). */
+int sh_engine_set_profiling(sh_engine* e, int on);
+int sh_engine_profile(sh_engine* e, sh_kernel_stat* out, uint32_t cap, uint32_t* n_out);
+int sh_engine_profile_reset(sh_engine* e);
+
+/* Device buffers (plain HBM allocations for kernel-level entry points). */
+int sh_dev_alloc(sh_engine* e, uint64_t bytes, void** out_dev);
+int sh_dev_free(sh_engine* e, void* dev);
+int sh_memcpy_h2d(sh_engine* e, void* dst_dev, const void* src, uint64_t bytes);
+int sh_memcpy_d2h(sh_engine* e, void* dst, const void* src_dev, uint64_t bytes);
+
+/* -------------------------------------------------------------- model */
+/* models::open + Engine::upload_weights (models/mod.rs:537, inference/mod.rs:304)
+ * for architecture "llama" (models/llama.rs:1038-1090). */
+int sh_model_load_gguf(sh_engine* e, const char* path, sh_model** out);
+int sh_model_load_gguf_memory(sh_engine* e, const void* data, uint64_t size, sh_model** out);
+void sh_model_destroy(sh_model* m);
+/* Model::{vocab_size, cache_dims} (models/mod.rs:35-37). */
+int sh_model_info(const sh_model* m, sh_model_dims* out);
+
+/* ----------------------------------------------------------------- KV */
+/* Engine::allocate_kv_cache (inference/mod.rs:318); f16 K/V. */
+int sh_kv_create(sh_engine* e, const sh_model* m, uint32_t max_seq_len, sh_kv** out);
+void sh_kv_destroy(sh_kv* kv);
+int sh_kv_position(const sh_kv* kv, uint32_t* pos);
+/* KvCache::truncate: position = min(new_pos, position) (kv_cache.rs:587-602). */
+int sh_kv_truncate(sh_kv* kv, uint32_t new_pos);
+/* Export / import positions [0, n_pos) of one layer's K (is_v = 0) or V in the
+ * reference layout [n_pos][n_head_kv][head_dim] f16 (kv_cache.rs:99-111). */
+int sh_kv_read_layer(sh_kv* kv, uint32_t layer, int is_v, uint32_t n_pos, uint16_t* out);
+int sh_kv_write_layer(sh_kv* kv, uint32_t layer, int is_v, uint32_t n_pos, const uint16_t* in);
+int sh_kv_set_position(sh_kv* kv, uint32_t pos);
+/* New (no reference counterpart): move K/V rows base+src[i] -> base+i for
+ * i < n (tree-verify path compaction), then position = base + n. */
+int sh_kv_compact(sh_kv* kv, uint32_t base, const uint32_t* src, uint32_t n);
+
+/* ------------------------------------------------------------ forward */
+/* Model::record_forward_full(tokens, pos, full_logits, ..) + readback
+ * (models/mod.rs:314-336, Engine::forward_full_readback inference/mod.rs:2427).
+ * Llama body models/llama.rs:196-441 with all-position logits
+ * (qwen35moe.rs:975-989). parents: NULL = causal chain, else tree parent index
+ * per token (-1 = attaches to the cached prefix; positions = pos + depth).
+ * logits_mode 0: none, 1: last column, 2: all columns. logits_out is [cols][V],
+ * residual_out [L][n_embd] (pre-output_norm), either may be NULL.
+ * Advances the cache position by L. */
+int sh_forward_full(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L, uint32_t pos,
+                    const int32_t* parents, int logits_mode, float* logits_out, float* residual_out);
+
+/* Greedy verify: forward [tokens] with all-position logits and return the
+ * per-column argmax ids (record_greedy per column, inference/mod.rs:2154-2167). */
+int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L, uint32_t pos,
+                     uint32_t* sampled_out);
+
+/* Engine::decode_speculative (inference/mod.rs:2108-2297) with a separate draft
+ * model (draft_tokens mod.rs:2062-2092 greedy): drafts n = clamp(n_max,1,8)
+ * tokens on device, verifies [last, d_1..d_n], accepts the longest prefix
+ * (GREEDY / COMPARE / REJECTION), truncates both caches to pos + acc + 1.
+ * emitted_out holds n + 1 entries; *n_emitted = acc + 1. drafts_out (n) may be NULL. */
+int sh_spec_step(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh_kv* dkv,
+                 uint32_t last_token, uint32_t n_max, sh_sampling* s, uint32_t* emitted_out,
+                 uint32_t* n_emitted, uint32_t* drafts_out);
+
+/* ------------------------------------------------------ kernel level */
+/* Upload a GGUF-layout quantized matrix [M rows][K] (Q8_0 or Q4_K) and repack it
+ * for the MFMA GEMV. */
+int sh_qtensor_upload(sh_engine* e, int ggml_type, const void* host_blocks, uint32_t M, uint32_t K,
+                      sh_qtensor** out);
+void sh_qtensor_destroy(sh_qtensor* t);
+/* y[j][m] (+)= sum_k deq(W)[m][k] * x[j][k], j < N (ops/matmul.rs:295-299 layout,
+ * batched columns matmul.rs:473-487, ACCUMULATE mul_mat_vec_head.slang:173-188). */
+int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_t N, float* y_dev,
+                  int accumulate);
+
+/* Acceptance kernel for a batch of B sequences with k draft positions.
+ * p_logits_dev [B][k+1][V], q_logits_dev [B][k][V] (REJECTION only, else NULL),
+ * drafts_dev [B][k] u32. GREEDY / COMPARE follow sample_and_compare
+ * (sample.rs:347-361, batched accept server/inference.rs:2859-2883);
+ * REJECTION is new. Uniforms: Philox4x64-10 key (seed, 0x5EC), word
+ * counter + 2*(b*(k+1)+i) (accept) and +1 (residual), or explicit host uniforms
+ * [B][k+1][2]. Outputs acc_len_dev [B], next_tok_dev [B] (u32). */
+int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
+                     const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s,
+                     uint32_t* acc_len_dev, uint32_t* next_tok_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,249 @@
+"""ctypes wrapper of the CPU oracle (oracle/_build/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker. The product path
+(seeker_amd / libseeker_hip.so) never imports or calls it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(_HERE, "_build", "liboracle.so")
+
+P = C.c_void_p
+U32P = C.POINTER(C.c_uint32)
+I32P = C.POINTER(C.c_int32)
+F32P = C.POINTER(C.c_float)
+U64P = C.POINTER(C.c_uint64)
+U16P = C.POINTER(C.c_uint16)
+U8P = C.POINTER(C.c_uint8)
+
+
+class SamplerCfg(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("min_p", C.c_float)]
+
+
+_SIGS = {
+    "or_f16_to_f32": (C.c_float, [C.c_uint16]),
+    "or_f32_to_f16": (C.c_uint16, [C.c_float]),
+    "or_philox4x64_10": (None, [U64P, U64P, U64P]),
+    "or_philox_word": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
+    "or_unit_f32": (C.c_float, [C.c_uint64]),
+    "or_dequant_row": (C.c_int, [C.c_int, U8P, C.c_uint64, C.c_uint64, F32P]),
+    "or_gemv": (C.c_int, [C.c_int, U8P, C.c_uint64, C.c_uint64, F32P, C.c_uint32, F32P]),
+    "or_model_open": (C.c_int, [P, C.c_uint64, C.POINTER(P)]),
+    "or_model_free": (None, [P]),
+    "or_model_dims": (None, [P, U32P]),
+    "or_kv_create": (C.c_int, [P, C.c_uint32, C.POINTER(P)]),
+    "or_kv_free": (None, [P]),
+    "or_kv_position": (C.c_uint32, [P]),
+    "or_kv_truncate": (None, [P, C.c_uint32]),
+    "or_kv_set_position": (None, [P, C.c_uint32]),
+    "or_kv_layer": (U16P, [P, C.c_uint32, C.c_int]),
+    "or_kv_compact": (None, [P, C.c_uint32, U32P, C.c_uint32]),
+    "or_forward": (C.c_int, [P, P, U32P, C.c_uint32, C.c_uint32, I32P, C.c_int, F32P, F32P]),
+    "or_argmax": (C.c_uint32, [F32P, C.c_uint32]),
+    "or_softmax": (None, [F32P, C.c_uint32, F32P]),
+    "or_sample_one": (C.c_uint32, [F32P, C.c_uint32, C.POINTER(SamplerCfg), C.c_float]),
+    "or_sample_vocab_order": (C.c_uint32, [F32P, C.c_uint32, C.c_float, C.c_float]),
+    "or_sample_and_compare": (C.c_uint32, [F32P, C.c_uint32, U32P, C.c_uint32, C.POINTER(SamplerCfg), F32P, C.c_int,
+                                           U32P]),
+    "or_rejection": (C.c_uint32, [F32P, F32P, U32P, C.c_uint32, C.c_uint32, C.c_float, F32P, F32P, U32P]),
+    "or_probs": (None, [F32P, C.c_uint32, C.c_float, F32P]),
+    "or_spec_step_greedy": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, U32P, U32P, U32P, U32P, U32P]),
+}
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = C.CDLL(LIB)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def dequant_row(qtype: int, raw: np.ndarray, row: int, k: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty(k, dtype=np.float32)
+    if lib().or_dequant_row(qtype, raw.ctypes.data_as(U8P), row, k, out.ctypes.data_as(F32P)):
+        raise ValueError("dequant failed")
+    return out
+
+
+def gemv(qtype: int, w: np.ndarray, M: int, K: int, x: np.ndarray) -> np.ndarray:
+    """x [N][K] -> y [N][M] with f64 accumulation."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = _f32(x).reshape(-1, K)
+    y = np.empty((x.shape[0], M), dtype=np.float32)
+    if lib().or_gemv(qtype, w.ctypes.data_as(U8P), M, K, x.ctypes.data_as(F32P), x.shape[0], y.ctypes.data_as(F32P)):
+        raise ValueError("gemv failed")
+    return y
+
+
+def philox_block(ctr, key):
+    c = (C.c_uint64 * 4)(*ctr)
+    k = (C.c_uint64 * 2)(*key)
+    o = (C.c_uint64 * 4)()
+    lib().or_philox4x64_10(c, k, o)
+    return list(o)
+
+
+def philox_uniforms(seed: int, stream: int, start: int, n: int) -> np.ndarray:
+    L = lib()
+    return np.array([L.or_unit_f32(L.or_philox_word(seed, stream, start + i)) for i in range(n)], dtype=np.float32)
+
+
+class Model:
+    def __init__(self, image):
+        """image: synth.GgufImage (kept alive by the caller)."""
+        self.image = image
+        h = C.c_void_p()
+        rc = lib().or_model_open(C.c_void_p(image.address), image.size, C.byref(h))
+        if rc:
+            raise ValueError(f"oracle model open failed ({rc})")
+        self.h = h
+        d = (C.c_uint32 * 7)()
+        lib().or_model_dims(h, d)
+        self.n_layer, self.d, self.n_head, self.n_kv, self.hd, self.ff, self.V = list(d)
+
+    def close(self):
+        if self.h:
+            lib().or_model_free(self.h)
+            self.h = None
+
+
+class KvCache:
+    def __init__(self, model: Model, max_seq: int):
+        h = C.c_void_p()
+        if lib().or_kv_create(model.h, max_seq, C.byref(h)):
+            raise MemoryError("oracle kv alloc")
+        self.h, self.model, self.max_seq = h, model, max_seq
+        self.pending = (C.c_uint32 * 16)()
+        self.n_pending = C.c_uint32(0)
+
+    @property
+    def position(self):
+        return lib().or_kv_position(self.h)
+
+    def truncate(self, p):
+        lib().or_kv_truncate(self.h, p)
+
+    def set_position(self, p):
+        lib().or_kv_set_position(self.h, p)
+
+    def layer(self, layer: int, is_v: bool, n_pos: int) -> np.ndarray:
+        m = self.model
+        ptr = lib().or_kv_layer(self.h, layer, int(is_v))
+        full = np.ctypeslib.as_array(ptr, shape=(self.max_seq, m.n_kv, m.hd))
+        return full[:n_pos]
+
+    def compact(self, base, src):
+        s = np.ascontiguousarray(src, dtype=np.uint32)
+        lib().or_kv_compact(self.h, base, s.ctypes.data_as(U32P), s.size)
+
+    def close(self):
+        if self.h:
+            lib().or_kv_free(self.h)
+            self.h = None
+
+
+def forward(model: Model, kv: KvCache, tokens, pos: int, parents=None, logits_mode: int = 2):
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    L = t.size
+    cols = L if logits_mode == 2 else (1 if logits_mode == 1 else 0)
+    logits = np.empty((max(cols, 1), model.V), dtype=np.float32)
+    resid = np.empty((L, model.d), dtype=np.float32)
+    par = np.ascontiguousarray(parents, dtype=np.int32) if parents is not None else None
+    rc = lib().or_forward(model.h, kv.h, t.ctypes.data_as(U32P), L, pos,
+                          par.ctypes.data_as(I32P) if par is not None else None, logits_mode,
+                          logits.ctypes.data_as(F32P), resid.ctypes.data_as(F32P))
+    if rc:
+        raise ValueError(f"oracle forward failed ({rc})")
+    return logits[:cols], resid
+
+
+def argmax(x) -> int:
+    x = _f32(x)
+    return int(lib().or_argmax(x.ctypes.data_as(F32P), x.size))
+
+
+def softmax(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().or_softmax(x.ctypes.data_as(F32P), x.size, out.ctypes.data_as(F32P))
+    return out
+
+
+def probs(x, temperature: float) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().or_probs(x.ctypes.data_as(F32P), x.size, temperature, out.ctypes.data_as(F32P))
+    return out
+
+
+def sample_one(logits, cfg: SamplerCfg, u: float) -> int:
+    x = _f32(logits)
+    return int(lib().or_sample_one(x.ctypes.data_as(F32P), x.size, C.byref(cfg), u))
+
+
+def sample_vocab_order(logits, temperature: float, u: float) -> int:
+    x = _f32(logits)
+    return int(lib().or_sample_vocab_order(x.ctypes.data_as(F32P), x.size, temperature, u))
+
+
+def sample_and_compare(logits, drafts, cfg: SamplerCfg, uniforms, mode: int = 1):
+    lg = _f32(logits)
+    n = len(drafts)
+    V = lg.shape[-1]
+    d = np.ascontiguousarray(drafts, dtype=np.uint32)
+    u = _f32(uniforms)
+    em = np.zeros(n + 1, dtype=np.uint32)
+    ne = lib().or_sample_and_compare(lg.ctypes.data_as(F32P), V, d.ctypes.data_as(U32P), n, C.byref(cfg),
+                                     u.ctypes.data_as(F32P), mode, em.ctypes.data_as(U32P))
+    return em[:ne].tolist()
+
+
+def rejection(p_logits, q_logits, drafts, temperature, u_acc, u_res):
+    p = _f32(p_logits)
+    q = _f32(q_logits)
+    k = len(drafts)
+    V = p.shape[-1]
+    d = np.ascontiguousarray(drafts, dtype=np.uint32)
+    ua, ur = _f32(u_acc), _f32(u_res)
+    nt = C.c_uint32()
+    acc = lib().or_rejection(p.ctypes.data_as(F32P), q.ctypes.data_as(F32P), d.ctypes.data_as(U32P), k, V,
+                             temperature, ua.ctypes.data_as(F32P), ur.ctypes.data_as(F32P), C.byref(nt))
+    return int(acc), int(nt.value)
+
+
+def spec_step_greedy(tgt: Model, drf: Model, tkv: KvCache, dkv: KvCache, last_token: int, n_max: int):
+    em = (C.c_uint32 * 9)()
+    dr = (C.c_uint32 * 8)()
+    ne = C.c_uint32()
+    rc = lib().or_spec_step_greedy(tgt.h, drf.h, tkv.h, dkv.h, last_token, n_max, dkv.pending,
+                                   C.byref(dkv.n_pending), em, C.byref(ne), dr)
+    if rc:
+        raise ValueError(f"oracle spec step failed ({rc})")
+    n = min(max(n_max, 1), 8)
+    return list(em)[: ne.value], list(dr)[:n]

@@ -1,0 +1,719 @@
+/* CPU oracle for the seeker speculative-decoding verify path.
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py, as the checker, never as the thing measured
+ * or shipped. See oracle.h for the numerics contract.
+ *
+ * Pinning status of each function (what checks it beyond its own formula) is
+ * listed in tests/test_oracle.py; functions no check pins are marked
+ * "parity unpinned" there.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ f16 */
+
+/* f16 -> f32 exactly as apps/seeker-cli/src/commands/run.rs:4115-4129
+ * (subnormal = mant * 2^-24, exp 31 = inf/nan, normal = (1+m/1024)*2^(e-15)). */
+float or_f16_to_f32(uint16_t h) {
+  float sign = (h >> 15) & 1 ? -1.0f : 1.0f;
+  int e = (h >> 10) & 0x1F;
+  float mant = (float)(h & 0x3FF);
+  float v;
+  if (e == 0) v = mant * ldexpf(1.0f, -24);
+  else if (e == 0x1F) v = mant == 0.0f ? INFINITY : NAN;
+  else v = (1.0f + mant / 1024.0f) * ldexpf(1.0f, e - 15);
+  return sign * v;
+}
+
+/* f32 -> f16, IEEE round-to-nearest-even, computed through double arithmetic
+ * (independent of the bit-twiddling conversion used by the product). */
+uint16_t or_f32_to_f16(float f) {
+  if (isnan(f)) return 0x7E00;
+  uint16_t sign = signbit(f) ? 0x8000 : 0;
+  double a = fabs((double)f);
+  if (a == 0.0) return sign;
+  if (a >= 65520.0) return sign | 0x7C00;
+  int e;
+  frexp(a, &e);                 /* a = m * 2^e, m in [0.5, 1) */
+  int ue = e - 1;               /* a in [2^ue, 2^(ue+1)) */
+  if (ue < -14) {               /* subnormal: units of 2^-24 */
+    double q = nearbyint(a * 16777216.0);  /* default rounding mode: ties-to-even */
+    return sign | (uint16_t)q;             /* q == 1024 gives the min normal bit pattern */
+  }
+  double q = nearbyint(ldexp(a, 10 - ue)); /* in [1024, 2048] */
+  if (q >= 2048.0) { q = 1024.0; ue += 1; }
+  if (ue > 15) return sign | 0x7C00;
+  return sign | (uint16_t)((ue + 15) << 10) | (uint16_t)((int)q - 1024);
+}
+
+/* --------------------------------------------------------------- philox */
+
+/* Philox4x64-10 (Salmon et al. SC'11), the generator numpy.random.Philox
+ * implements; pinned against numpy's random_raw(). */
+static void mulhilo(uint64_t a, uint64_t b, uint64_t* hi, uint64_t* lo) {
+  unsigned __int128 p = (unsigned __int128)a * b;
+  *hi = (uint64_t)(p >> 64);
+  *lo = (uint64_t)p;
+}
+
+void or_philox4x64_10(const uint64_t ctr[4], const uint64_t key[2], uint64_t out[4]) {
+  uint64_t x[4] = {ctr[0], ctr[1], ctr[2], ctr[3]};
+  uint64_t k[2] = {key[0], key[1]};
+  for (int r = 0; r < 10; ++r) {
+    if (r) { k[0] += 0x9E3779B97F4A7C15ull; k[1] += 0xBB67AE8584CAA73Bull; }
+    uint64_t h0, l0, h1, l1;
+    mulhilo(0xD2E7470EE14C6C93ull, x[0], &h0, &l0);
+    mulhilo(0xCA5A826395121157ull, x[2], &h1, &l1);
+    uint64_t y0 = h1 ^ x[1] ^ k[0], y2 = h0 ^ x[3] ^ k[1];
+    x[0] = y0; x[1] = l1; x[2] = y2; x[3] = l0;
+  }
+  memcpy(out, x, sizeof x);
+}
+
+uint64_t or_philox_word(uint64_t k0, uint64_t k1, uint64_t i) {
+  uint64_t ctr[4] = {i / 4 + 1, 0, 0, 0}, key[2] = {k0, k1}, out[4];
+  or_philox4x64_10(ctr, key, out);
+  return out[i % 4];
+}
+
+float or_unit_f32(uint64_t w) { return (float)(uint32_t)(w >> 40) / 16777216.0f; }
+
+/* -------------------------------------------------------------- dequant */
+
+/* Q4_K 6-bit (scale, min) unpack: run.rs:4223-4232. */
+static void q4k_scale_min(const uint8_t* s, int j, int* sc, int* m) {
+  if (j < 4) { *sc = s[j] & 63; *m = s[j + 4] & 63; }
+  else {
+    *sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+    *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+  }
+}
+
+/* run.rs:4212-4303: Q4_K y = (d*sc)*q - (dmin*m) per 32-sub-block, low nibbles
+ * of qs[32g..32g+32) are sub-block 2g, high nibbles sub-block 2g+1;
+ * Q8_0 y = d*q. F32 / F16 rows copied. */
+int or_dequant_row(int type, const uint8_t* raw, uint64_t row, uint64_t k, float* out) {
+  if (type == OR_Q4_K) {
+    if (k % 256) return 1;
+    uint64_t nb = k / 256;
+    for (uint64_t b = 0; b < nb; ++b) {
+      const uint8_t* blk = raw + (row * nb + b) * 144;
+      float d = or_f16_to_f32((uint16_t)(blk[0] | blk[1] << 8));
+      float dmin = or_f16_to_f32((uint16_t)(blk[2] | blk[3] << 8));
+      const uint8_t* sc = blk + 4;
+      const uint8_t* qs = blk + 16;
+      float* y = out + b * 256;
+      for (int g = 0; g < 4; ++g) {
+        int s1, m1, s2, m2;
+        q4k_scale_min(sc, 2 * g, &s1, &m1);
+        q4k_scale_min(sc, 2 * g + 1, &s2, &m2);
+        float d1 = d * (float)s1, mm1 = dmin * (float)m1;
+        float d2 = d * (float)s2, mm2 = dmin * (float)m2;
+        for (int l = 0; l < 32; ++l) y[64 * g + l] = d1 * (float)(qs[32 * g + l] & 0xF) - mm1;
+        for (int l = 0; l < 32; ++l) y[64 * g + 32 + l] = d2 * (float)(qs[32 * g + l] >> 4) - mm2;
+      }
+    }
+    return 0;
+  }
+  if (type == OR_Q8_0) {
+    if (k % 32) return 1;
+    uint64_t nb = k / 32;
+    for (uint64_t b = 0; b < nb; ++b) {
+      const uint8_t* blk = raw + (row * nb + b) * 34;
+      float d = or_f16_to_f32((uint16_t)(blk[0] | blk[1] << 8));
+      for (int i = 0; i < 32; ++i) out[b * 32 + i] = d * (float)(int8_t)blk[2 + i];
+    }
+    return 0;
+  }
+  if (type == OR_F32) { memcpy(out, raw + row * k * 4, k * 4); return 0; }
+  if (type == OR_F16) {
+    for (uint64_t i = 0; i < k; ++i) {
+      const uint8_t* p = raw + (row * k + i) * 2;
+      out[i] = or_f16_to_f32((uint16_t)(p[0] | p[1] << 8));
+    }
+    return 0;
+  }
+  return 2;
+}
+
+/* Batched-column GEMV, f64 accumulation (semantics of
+ * shaders/compute/mul_mat_vec_q4_k.slang:13-103 / mul_mat_vec.slang:39-100,
+ * batched columns ops/matmul.rs:473-487). */
+int or_gemv(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, uint32_t N, float* y) {
+  int err = 0;
+#pragma omp parallel
+  {
+    float* row = (float*)malloc(K * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t m = 0; m < (int64_t)M; ++m) {
+      if (or_dequant_row(type, w, (uint64_t)m, K, row)) { err = 1; continue; }
+      for (uint32_t j = 0; j < N; ++j) {
+        const float* xj = x + (uint64_t)j * K;
+        double acc = 0.0;
+        for (uint64_t k = 0; k < K; ++k) acc += (double)row[k] * (double)xj[k];
+        y[(uint64_t)j * M + m] = (float)acc;
+      }
+    }
+    free(row);
+  }
+  return err;
+}
+
+/* ----------------------------------------------------------------- GGUF */
+
+typedef struct { const char* name; uint32_t nlen; uint32_t type; uint64_t ne[4]; uint32_t nd; uint64_t off; } or_tensor;
+
+typedef struct {
+  const uint8_t* w;
+  int type;
+  uint64_t rows, cols; /* cols = contracting dim (ne0) */
+} or_mat;
+
+typedef struct {
+  const float* attn_norm; or_mat wq, wk, wv, wo;
+  const float* ffn_norm; or_mat gate, up, down;
+} or_layer;
+
+struct or_model {
+  uint32_t n_layer, d, n_head, n_kv, hd, ff, V;
+  float eps, theta;
+  or_mat embd, out;
+  const float* out_norm;
+  or_layer* L;
+};
+
+struct or_kv {
+  uint32_t n_layer, n_kv, hd, max_seq, pos;
+  uint16_t* k; /* [layer][max_seq][n_kv][hd] */
+  uint16_t* v;
+};
+
+typedef struct { const uint8_t* p; const uint8_t* end; int bad; } rd;
+
+static uint64_t rd_u(rd* r, int n) {
+  if (r->p + n > r->end) { r->bad = 1; return 0; }
+  uint64_t v = 0;
+  for (int i = 0; i < n; ++i) v |= (uint64_t)r->p[i] << (8 * i);
+  r->p += n;
+  return v;
+}
+
+static void rd_skip_value(rd* r, uint32_t t);
+static const uint8_t* rd_str(rd* r, uint32_t* len) {
+  uint64_t n = rd_u(r, 8);
+  *len = 0;
+  if (r->bad || r->p + n > r->end) { r->bad = 1; return NULL; }
+  const uint8_t* s = r->p;
+  r->p += n;
+  *len = (uint32_t)n;
+  return s;
+}
+static void rd_skip_value(rd* r, uint32_t t) {
+  static const int sz[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+  if (t == 8) { uint32_t l; rd_str(r, &l); return; }
+  if (t == 9) {
+    uint32_t et = (uint32_t)rd_u(r, 4);
+    uint64_t n = rd_u(r, 8);
+    for (uint64_t i = 0; i < n && !r->bad; ++i) rd_skip_value(r, et);
+    return;
+  }
+  if (t > 12) { r->bad = 1; return; }
+  rd_u(r, sz[t]);
+}
+
+static int streq(const uint8_t* s, uint32_t n, const char* z) { return s && strlen(z) == n && memcmp(s, z, n) == 0; }
+
+int or_model_open(const uint8_t* img, uint64_t size, or_model** out) {
+  rd r = {img, img + size, 0};
+  if (size < 24 || memcmp(img, "GGUF", 4)) return 1;
+  r.p += 4;
+  uint32_t ver = (uint32_t)rd_u(&r, 4);
+  if (ver < 2 || ver > 3) return 2;
+  uint64_t nt = rd_u(&r, 8), nkv = rd_u(&r, 8);
+  or_model* m = (or_model*)calloc(1, sizeof *m);
+  m->eps = 1e-5f; m->theta = 10000.0f;
+  uint32_t align = 32, n_kv = 0, rope_dim = 0;
+  for (uint64_t i = 0; i < nkv && !r.bad; ++i) {
+    uint32_t kl; const uint8_t* k = rd_str(&r, &kl);
+    uint32_t t = (uint32_t)rd_u(&r, 4);
+    if (t == 4 || t == 6) {
+      uint32_t v = (uint32_t)rd_u(&r, 4);
+      float f; memcpy(&f, &v, 4);
+      if (streq(k, kl, "general.alignment")) align = v;
+      else if (streq(k, kl, "llama.block_count")) m->n_layer = v;
+      else if (streq(k, kl, "llama.attention.head_count")) m->n_head = v;
+      else if (streq(k, kl, "llama.attention.head_count_kv")) n_kv = v;
+      else if (streq(k, kl, "llama.embedding_length")) m->d = v;
+      else if (streq(k, kl, "llama.feed_forward_length")) m->ff = v;
+      else if (streq(k, kl, "llama.vocab_size")) m->V = v;
+      else if (streq(k, kl, "llama.rope.dimension_count")) rope_dim = v;
+      else if (streq(k, kl, "llama.rope.freq_base")) m->theta = f;
+      else if (streq(k, kl, "llama.attention.layer_norm_rms_epsilon")) m->eps = f;
+    } else {
+      rd_skip_value(&r, t);
+    }
+  }
+  /* defaults as models/llama.rs:1038-1048 */
+  m->n_kv = n_kv ? n_kv : m->n_head;
+  if (!m->n_layer || !m->n_head || !m->d) { free(m); return 3; }
+  m->hd = m->d / m->n_head;
+  (void)rope_dim;
+  or_tensor* ts = (or_tensor*)calloc(nt, sizeof *ts);
+  for (uint64_t i = 0; i < nt && !r.bad; ++i) {
+    const uint8_t* s = rd_str(&r, &ts[i].nlen);
+    ts[i].name = (const char*)s;
+    ts[i].nd = (uint32_t)rd_u(&r, 4);
+    for (uint32_t j = 0; j < ts[i].nd && j < 4; ++j) ts[i].ne[j] = rd_u(&r, 8);
+    ts[i].type = (uint32_t)rd_u(&r, 4);
+    ts[i].off = rd_u(&r, 8);
+  }
+  if (r.bad) { free(ts); free(m); return 4; }
+  uint64_t pos = (uint64_t)(r.p - img);
+  const uint8_t* data = img + (pos + align - 1) / align * align;
+  m->L = (or_layer*)calloc(m->n_layer, sizeof(or_layer));
+  int found_out = 0, missing = 0;
+  char nm[96];
+#define FIND(NAME, DST_MAT, DST_F32)                                                       \
+  do {                                                                                     \
+    int ok = 0;                                                                            \
+    for (uint64_t t = 0; t < nt; ++t)                                                      \
+      if (streq((const uint8_t*)ts[t].name, ts[t].nlen, NAME)) {                           \
+        ok = 1;                                                                            \
+        if (DST_MAT) {                                                                     \
+          or_mat* mm = DST_MAT;                                                            \
+          mm->w = data + ts[t].off; mm->type = (int)ts[t].type;                            \
+          mm->cols = ts[t].ne[0]; mm->rows = ts[t].nd > 1 ? ts[t].ne[1] : 1;               \
+        } else {                                                                           \
+          *(DST_F32) = (const float*)(data + ts[t].off);                                   \
+        }                                                                                  \
+      }                                                                                    \
+    if (!ok) missing = 1;                                                                  \
+  } while (0)
+  FIND("token_embd.weight", &m->embd, (const float**)0);
+  FIND("output_norm.weight", (or_mat*)0, &m->out_norm);
+  for (uint64_t t = 0; t < nt; ++t)
+    if (streq((const uint8_t*)ts[t].name, ts[t].nlen, "output.weight")) found_out = 1;
+  if (found_out) FIND("output.weight", &m->out, (const float**)0);
+  else m->out = m->embd; /* tied: llama.rs:424 lm_head = output.unwrap_or(token_embd) */
+  for (uint32_t l = 0; l < m->n_layer; ++l) {
+    or_layer* L = &m->L[l];
+#define NM(S) (snprintf(nm, sizeof nm, "blk.%u." S, l), nm)
+    FIND(NM("attn_norm.weight"), (or_mat*)0, &L->attn_norm);
+    FIND(NM("attn_q.weight"), &L->wq, (const float**)0);
+    FIND(NM("attn_k.weight"), &L->wk, (const float**)0);
+    FIND(NM("attn_v.weight"), &L->wv, (const float**)0);
+    FIND(NM("attn_output.weight"), &L->wo, (const float**)0);
+    FIND(NM("ffn_norm.weight"), (or_mat*)0, &L->ffn_norm);
+    FIND(NM("ffn_gate.weight"), &L->gate, (const float**)0);
+    FIND(NM("ffn_up.weight"), &L->up, (const float**)0);
+    FIND(NM("ffn_down.weight"), &L->down, (const float**)0);
+#undef NM
+  }
+#undef FIND
+  free(ts);
+  if (missing) { free(m->L); free(m); return 5; }
+  if (!m->V) m->V = (uint32_t)m->embd.rows;
+  *out = m;
+  return 0;
+}
+
+void or_model_free(or_model* m) { if (m) { free(m->L); free(m); } }
+
+void or_model_dims(const or_model* m, uint32_t d[7]) {
+  d[0] = m->n_layer; d[1] = m->d; d[2] = m->n_head; d[3] = m->n_kv; d[4] = m->hd; d[5] = m->ff; d[6] = m->V;
+}
+
+/* ------------------------------------------------------------------- KV */
+
+/* KV layout [head_dim, n_head_kv, max_seq_len] token-major per layer
+ * (inference/kv_cache.rs:99-111); rollback is a cursor truncate
+ * (kv_cache.rs:587-602: position = min(new_pos, position)). */
+int or_kv_create(const or_model* m, uint32_t max_seq, or_kv** out) {
+  or_kv* kv = (or_kv*)calloc(1, sizeof *kv);
+  kv->n_layer = m->n_layer; kv->n_kv = m->n_kv; kv->hd = m->hd; kv->max_seq = max_seq;
+  size_t n = (size_t)m->n_layer * max_seq * m->n_kv * m->hd;
+  kv->k = (uint16_t*)calloc(n, 2);
+  kv->v = (uint16_t*)calloc(n, 2);
+  if (!kv->k || !kv->v) { free(kv->k); free(kv->v); free(kv); return 1; }
+  *out = kv;
+  return 0;
+}
+void or_kv_free(or_kv* kv) { if (kv) { free(kv->k); free(kv->v); free(kv); } }
+uint32_t or_kv_position(const or_kv* kv) { return kv->pos; }
+void or_kv_truncate(or_kv* kv, uint32_t p) { if (p < kv->pos) kv->pos = p; }
+void or_kv_set_position(or_kv* kv, uint32_t p) { kv->pos = p; }
+uint16_t* or_kv_layer(or_kv* kv, uint32_t layer, int is_v) {
+  size_t per = (size_t)kv->max_seq * kv->n_kv * kv->hd;
+  return (is_v ? kv->v : kv->k) + per * layer;
+}
+void or_kv_compact(or_kv* kv, uint32_t base, const uint32_t* src, uint32_t n) {
+  size_t row = (size_t)kv->n_kv * kv->hd;
+  for (uint32_t l = 0; l < kv->n_layer; ++l)
+    for (int isv = 0; isv < 2; ++isv) {
+      uint16_t* c = or_kv_layer(kv, l, isv);
+      for (uint32_t i = 0; i < n; ++i)
+        if (src[i] != i) memmove(c + (base + i) * row, c + (base + src[i]) * row, row * 2);
+    }
+  kv->pos = base + n;
+}
+
+/* -------------------------------------------------------------- forward */
+
+/* RMSNorm: y = x * rsqrt(mean(x^2) + eps) * w (shaders/compute/rms_norm.slang:39-55). */
+static void rms_norm(const float* x, const float* w, uint32_t n, float eps, float* y) {
+  double ss = 0.0;
+  for (uint32_t i = 0; i < n; ++i) ss += (double)x[i] * x[i];
+  double sc = 1.0 / sqrt(ss / n + (double)eps);
+  for (uint32_t i = 0; i < n; ++i) y[i] = (float)((double)x[i] * sc * (double)w[i]);
+}
+
+/* RoPE NORM mode (adjacent pairs): theta = pos * base^(-2 i0/n_dims)
+ * (shaders/include/rope_funcs.slang:37-61, theta_scale ops/rope.rs:138;
+ * freq_scale 1, ext_factor 0, attn_factor 1 per ops/rope.rs:32-45). */
+static void rope_norm(float* x, uint32_t n_head, uint32_t hd, uint32_t pos, float base) {
+  for (uint32_t h = 0; h < n_head; ++h)
+    for (uint32_t i0 = 0; i0 < hd; i0 += 2) {
+      double theta = (double)pos * pow((double)base, -(double)i0 / (double)hd);
+      double c = cos(theta), s = sin(theta);
+      float* p = x + h * hd + i0;
+      double x0 = p[0], x1 = p[1];
+      p[0] = (float)(x0 * c - x1 * s);
+      p[1] = (float)(x0 * s + x1 * c);
+    }
+}
+
+static int is_ancestor(const int32_t* parents, uint32_t a, uint32_t j) {
+  /* a is ancestor-or-self of j within the chunk */
+  int32_t x = (int32_t)j;
+  while (x >= 0) {
+    if ((uint32_t)x == a) return 1;
+    x = parents[x];
+  }
+  return 0;
+}
+
+static void matmul(const or_mat* W, const float* x, uint32_t N, float* y) {
+  or_gemv(W->type, W->w, W->rows, W->cols, x, N, y);
+}
+
+int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint32_t pos,
+               const int32_t* parents, int logits_mode, float* logits, float* residual_out) {
+  /* Preconditions as models/llama.rs:178-192. */
+  if (L == 0) return 1;
+  if (kv->pos != pos) return 2;
+  if (pos + L > kv->max_seq) return 3;
+  const uint32_t d = m->d, hd = m->hd, nh = m->n_head, nkv = m->n_kv, ff = m->ff;
+  const uint32_t dkv = hd * nkv, gqa = nh / nkv;
+  uint32_t* qpos = (uint32_t*)malloc(L * sizeof(uint32_t));
+  for (uint32_t i = 0; i < L; ++i) {
+    uint32_t depth = 0;
+    if (parents) { int32_t x = parents[i]; while (x >= 0) { ++depth; x = parents[x]; } }
+    else depth = i;
+    qpos[i] = pos + depth;
+  }
+  float* res = (float*)malloc((size_t)L * d * 4);
+  float* xn = (float*)malloc((size_t)L * d * 4);
+  float* q = (float*)malloc((size_t)L * d * 4);
+  float* k = (float*)malloc((size_t)L * dkv * 4);
+  float* v = (float*)malloc((size_t)L * dkv * 4);
+  float* att = (float*)malloc((size_t)L * d * 4);
+  float* tmp = (float*)malloc((size_t)L * d * 4);
+  float* g = (float*)malloc((size_t)L * ff * 4);
+  float* u = (float*)malloc((size_t)L * ff * 4);
+  /* get_rows (elementwise.rs:873): dequantized embedding rows. */
+  for (uint32_t i = 0; i < L; ++i) or_dequant_row(m->embd.type, m->embd.w, tokens[i], d, res + (size_t)i * d);
+  const uint32_t kvlen = pos + L;
+  const double scale = 1.0 / sqrt((double)hd);
+  for (uint32_t l = 0; l < m->n_layer; ++l) {
+    or_layer* Ly = &m->L[l];
+    for (uint32_t i = 0; i < L; ++i) rms_norm(res + (size_t)i * d, Ly->attn_norm, d, m->eps, xn + (size_t)i * d);
+    matmul(&Ly->wq, xn, L, q);
+    matmul(&Ly->wk, xn, L, k);
+    matmul(&Ly->wv, xn, L, v);
+    for (uint32_t i = 0; i < L; ++i) {
+      rope_norm(q + (size_t)i * d, nh, hd, qpos[i], m->theta);
+      rope_norm(k + (size_t)i * dkv, nkv, hd, qpos[i], m->theta);
+    }
+    /* cache write f32 -> f16 at slot pos+i (ops/cache_io.rs:191-262). */
+    uint16_t* Kc = or_kv_layer(kv, l, 0);
+    uint16_t* Vc = or_kv_layer(kv, l, 1);
+    for (uint32_t i = 0; i < L; ++i)
+      for (uint32_t e = 0; e < dkv; ++e) {
+        Kc[(size_t)(pos + i) * dkv + e] = or_f32_to_f16(k[(size_t)i * dkv + e]);
+        Vc[(size_t)(pos + i) * dkv + e] = or_f32_to_f16(v[(size_t)i * dkv + e]);
+      }
+    /* attention: prefix [0,pos) always visible; within-chunk slot pos+a visible to
+     * row j iff a <= j (causal, llama.rs:904-955) or a is an ancestor-or-self of j (tree). */
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t j = 0; j < (int64_t)L; ++j)
+      for (int64_t h = 0; h < (int64_t)nh; ++h) {
+        const uint32_t kh = (uint32_t)h / gqa;
+        const float* qv = q + (size_t)j * d + (size_t)h * hd;
+        double* s = (double*)malloc(kvlen * sizeof(double));
+        double mx = -INFINITY;
+        for (uint32_t t = 0; t < kvlen; ++t) {
+          int vis = t < pos ? 1 : (parents ? is_ancestor(parents, t - pos, (uint32_t)j) : (t - pos <= (uint32_t)j));
+          if (!vis) { s[t] = -INFINITY; continue; }
+          const uint16_t* kr = Kc + (size_t)t * dkv + (size_t)kh * hd;
+          double acc = 0.0;
+          for (uint32_t e = 0; e < hd; ++e) acc += (double)qv[e] * (double)or_f16_to_f32(kr[e]);
+          s[t] = acc * scale;
+          if (s[t] > mx) mx = s[t];
+        }
+        double sum = 0.0;
+        for (uint32_t t = 0; t < kvlen; ++t) { s[t] = s[t] == -INFINITY ? 0.0 : exp(s[t] - mx); sum += s[t]; }
+        float* o = att + (size_t)j * d + (size_t)h * hd;
+        for (uint32_t e = 0; e < hd; ++e) {
+          double acc = 0.0;
+          for (uint32_t t = 0; t < kvlen; ++t)
+            if (s[t] != 0.0) acc += s[t] * (double)or_f16_to_f32(Vc[(size_t)t * dkv + (size_t)kh * hd + e]);
+          o[e] = (float)(acc / sum);
+        }
+        free(s);
+      }
+    matmul(&Ly->wo, att, L, tmp);
+    for (size_t i = 0; i < (size_t)L * d; ++i) res[i] = res[i] + tmp[i];
+    for (uint32_t i = 0; i < L; ++i) rms_norm(res + (size_t)i * d, Ly->ffn_norm, d, m->eps, xn + (size_t)i * d);
+    matmul(&Ly->gate, xn, L, g);
+    matmul(&Ly->up, xn, L, u);
+    /* silu(x) = x / (1 + exp(-x)) (shaders/compute/silu.slang:21), then * up */
+    for (size_t i = 0; i < (size_t)L * ff; ++i) {
+      double x = g[i];
+      g[i] = (float)((x / (1.0 + exp(-x))) * (double)u[i]);
+    }
+    matmul(&Ly->down, g, L, tmp);
+    for (size_t i = 0; i < (size_t)L * d; ++i) res[i] = res[i] + tmp[i];
+  }
+  if (residual_out) memcpy(residual_out, res, (size_t)L * d * 4);
+  if (logits_mode) {
+    uint32_t j0 = logits_mode == 1 ? L - 1 : 0, nc = L - j0;
+    for (uint32_t i = 0; i < nc; ++i) rms_norm(res + (size_t)(j0 + i) * d, m->out_norm, d, m->eps, xn + (size_t)i * d);
+    matmul(&m->out, xn, nc, logits);
+  }
+  kv->pos = pos + L; /* cache_io::advance */
+  free(qpos); free(res); free(xn); free(q); free(k); free(v); free(att); free(tmp); free(g); free(u);
+  return 0;
+}
+
+/* -------------------------------------------------------------- sampler */
+
+/* argmax, lowest index on ties, NaN never selected (inference/sample.rs:504-514). */
+uint32_t or_argmax(const float* x, uint32_t n) {
+  uint32_t best = 0;
+  float bv = -INFINITY;
+  for (uint32_t i = 0; i < n; ++i) if (x[i] > bv) { bv = x[i]; best = i; }
+  return best;
+}
+
+/* softmax with the all-masked uniform fallback (inference/sample.rs:516-533),
+ * evaluated in f64. */
+void or_softmax(const float* x, uint32_t n, float* out) {
+  double mx = -INFINITY;
+  for (uint32_t i = 0; i < n; ++i) if (x[i] > mx) mx = x[i];
+  if (!isfinite(mx)) { for (uint32_t i = 0; i < n; ++i) out[i] = 1.0f / (float)(n ? n : 1); return; }
+  double* e = (double*)malloc(n * sizeof(double));
+  double s = 0.0;
+  for (uint32_t i = 0; i < n; ++i) { e[i] = exp((double)x[i] - mx); s += e[i]; }
+  for (uint32_t i = 0; i < n; ++i) out[i] = (float)(e[i] / s);
+  free(e);
+}
+
+static const float* g_sort_keys;
+static int cmp_desc(const void* a, const void* b) {
+  uint32_t i = *(const uint32_t*)a, j = *(const uint32_t*)b;
+  float x = g_sort_keys[i], y = g_sort_keys[j];
+  if (x > y) return -1;
+  if (x < y) return 1;
+  return i < j ? -1 : (i > j);
+}
+
+/* Host chain (inference/sample.rs:369-474) without bias/penalties:
+ * greedy -> argmax; else sort desc (ties by id) -> top_k -> top_p (exclusive
+ * cumulative <= p keeps the crossing token) -> min_p (log-space cutoff) ->
+ * 1/T -> softmax -> first index with cumulative >= u (clamp to last). */
+uint32_t or_sample_one(const float* logits, uint32_t V, const or_sampler_cfg* cfg, float u) {
+  if (cfg->temperature <= 0.0f) return or_argmax(logits, V);
+  uint32_t* cand = (uint32_t*)malloc(V * sizeof(uint32_t));
+  for (uint32_t i = 0; i < V; ++i) cand[i] = i;
+  g_sort_keys = logits;
+  qsort(cand, V, sizeof(uint32_t), cmp_desc);
+  uint32_t k = (cfg->top_k > 0 && cfg->top_k < V) ? cfg->top_k : V;
+  float* kept = (float*)malloc(k * sizeof(float));
+  float* pr = (float*)malloc(k * sizeof(float));
+  for (uint32_t i = 0; i < k; ++i) kept[i] = logits[cand[i]];
+  if (cfg->top_p < 1.0f && cfg->top_p > 0.0f) {
+    or_softmax(kept, k, pr);
+    double cum = 0.0;
+    for (uint32_t j = 0; j < k; ++j) { if (cum > cfg->top_p) kept[j] = -INFINITY; cum += pr[j]; }
+  }
+  if (cfg->min_p > 0.0f) {
+    float cut = kept[0] + logf(cfg->min_p);
+    for (uint32_t j = 0; j < k; ++j) if (kept[j] < cut) kept[j] = -INFINITY;
+  }
+  if (fabsf(cfg->temperature - 1.0f) > 1e-9f) {
+    float it = 1.0f / fmaxf(cfg->temperature, 1e-9f);
+    for (uint32_t j = 0; j < k; ++j) if (isfinite(kept[j])) kept[j] *= it;
+  }
+  or_softmax(kept, k, pr);
+  double cum = 0.0;
+  uint32_t ch = k - 1;
+  for (uint32_t j = 0; j < k; ++j) { cum += pr[j]; if (cum >= u) { ch = j; break; } }
+  uint32_t tok = cand[ch];
+  free(cand); free(kept); free(pr);
+  return tok;
+}
+
+void or_probs(const float* logits, uint32_t V, float T, float* out) {
+  double mx = -INFINITY;
+  for (uint32_t i = 0; i < V; ++i) if (logits[i] > mx) mx = logits[i];
+  double s = 0.0;
+  for (uint32_t i = 0; i < V; ++i) s += exp(((double)logits[i] - mx) / (double)T);
+  for (uint32_t i = 0; i < V; ++i) out[i] = (float)(exp(((double)logits[i] - mx) / (double)T) / s);
+}
+
+/* GPU full-vocab categorical (ops/sampler.rs:303-368): softmax(l/T) in vocab
+ * order, idx = first index whose cumulative probability >= u, clamped to V-1. */
+uint32_t or_sample_vocab_order(const float* logits, uint32_t V, float T, float u) {
+  double mx = -INFINITY;
+  for (uint32_t i = 0; i < V; ++i) if (logits[i] > mx) mx = logits[i];
+  double s = 0.0;
+  for (uint32_t i = 0; i < V; ++i) s += exp(((double)logits[i] - mx) / (double)T);
+  double target = (double)u * s, cum = 0.0;
+  for (uint32_t i = 0; i < V; ++i) {
+    cum += exp(((double)logits[i] - mx) / (double)T);
+    if (cum >= target) return i;
+  }
+  return V - 1;
+}
+
+/* sample_and_compare (inference/sample.rs:347-361): emit s_i, continue while
+ * i < n and s_i == d_i. One uniform per emitted position. */
+uint32_t or_sample_and_compare(const float* logits, uint32_t V, const uint32_t* drafts, uint32_t n,
+                               const or_sampler_cfg* cfg, const float* uniforms, int mode,
+                               uint32_t* emitted) {
+  uint32_t ne = 0;
+  for (uint32_t i = 0; i <= n; ++i) {
+    const float* row = logits + (size_t)i * V;
+    uint32_t t;
+    if (cfg->temperature <= 0.0f) t = or_argmax(row, V);
+    else if (mode == 1) t = or_sample_vocab_order(row, V, cfg->temperature, uniforms[i]);
+    else t = or_sample_one(row, V, cfg, uniforms[i]);
+    emitted[ne++] = t;
+    if (i < n && t == drafts[i]) continue;
+    break;
+  }
+  return ne;
+}
+
+/* Speculative rejection sampling (new; Leviathan et al. 2023, Chen et al. 2023):
+ * p_i = softmax(target_i / T), q_i = softmax(draft_i / T) in f64.
+ * Accept draft d_i iff u_acc[i] * q_i(d_i) < p_i(d_i). At the first rejection i,
+ * draw from r = max(0, p_i - q_i) (fallback p_i when r == 0) in vocab order:
+ * first v with cumsum(r)_v > u_res[i] * sum(r). All accepted: draw the bonus from
+ * p_k the same way. */
+static double row_stats(const float* l, uint32_t V, double T, double* mx_out) {
+  double mx = -INFINITY;
+  for (uint32_t i = 0; i < V; ++i) if (l[i] > mx) mx = l[i];
+  double s = 0.0;
+  for (uint32_t i = 0; i < V; ++i) s += exp(((double)l[i] - mx) / T);
+  *mx_out = mx;
+  return s;
+}
+
+uint32_t or_rejection(const float* pl, const float* ql, const uint32_t* drafts, uint32_t k, uint32_t V,
+                      float temperature, const float* u_acc, const float* u_res, uint32_t* next_tok) {
+  const double T = temperature;
+  for (uint32_t i = 0; i <= k; ++i) {
+    const float* p = pl + (size_t)i * V;
+    double pm, ps = row_stats(p, V, T, &pm);
+    if (i == k) {
+      double target = (double)u_res[i] * ps, cum = 0.0;
+      uint32_t tok = V - 1;
+      for (uint32_t v = 0; v < V; ++v) { cum += exp(((double)p[v] - pm) / T); if (cum > target) { tok = v; break; } }
+      *next_tok = tok;
+      return k;
+    }
+    const float* q = ql + (size_t)i * V;
+    double qm, qs = row_stats(q, V, T, &qm);
+    uint32_t dtok = drafts[i];
+    double pd = exp(((double)p[dtok] - pm) / T) / ps;
+    double qd = exp(((double)q[dtok] - qm) / T) / qs;
+    if ((double)u_acc[i] * qd < pd) continue;
+    double R = 0.0;
+    for (uint32_t v = 0; v < V; ++v) {
+      double r = exp(((double)p[v] - pm) / T) / ps - exp(((double)q[v] - qm) / T) / qs;
+      if (r > 0.0) R += r;
+    }
+    uint32_t tok = V - 1;
+    if (R > 0.0) {
+      double target = (double)u_res[i] * R, cum = 0.0;
+      for (uint32_t v = 0; v < V; ++v) {
+        double r = exp(((double)p[v] - pm) / T) / ps - exp(((double)q[v] - qm) / T) / qs;
+        if (r > 0.0) cum += r;
+        if (cum > target) { tok = v; break; }
+      }
+    } else {
+      double target = (double)u_res[i] * ps, cum = 0.0;
+      for (uint32_t v = 0; v < V; ++v) { cum += exp(((double)p[v] - pm) / T); if (cum > target) { tok = v; break; } }
+    }
+    *next_tok = tok;
+    return i;
+  }
+  return k;
+}
+
+/* --------------------------------------------------------- spec step */
+
+/* Engine::decode_speculative (inference/mod.rs:2108-2297), greedy path, with a
+ * separate draft model in place of the MTP head. Draft: feed the draft's pending
+ * tokens plus last_token, then n-1 greedy steps (mod.rs:2062-2092 drafts greedily).
+ * Verify [last, d_1..d_n] with all-position logits, greedy accept (mod.rs:2168-2179),
+ * truncate to pos + acc + 1 (mod.rs:2269-2270). */
+int or_spec_step_greedy(or_model* tgt, or_model* drf, or_kv* tkv, or_kv* dkv, uint32_t last_token,
+                        uint32_t n_max, uint32_t* dpending, uint32_t* n_dpending, uint32_t* emitted,
+                        uint32_t* n_emitted, uint32_t* drafts_out) {
+  uint32_t n = n_max < 1 ? 1 : (n_max > 8 ? 8 : n_max);
+  const uint32_t P = tkv->pos;
+  const uint32_t V = tgt->V;
+  float* lg = (float*)malloc((size_t)(n + 1) * V * 4);
+  uint32_t drafts[8];
+  uint32_t feed[16];
+  uint32_t nf = 0;
+  for (uint32_t i = 0; i < *n_dpending; ++i) feed[nf++] = dpending[i];
+  feed[nf++] = last_token;
+  if (dkv->pos + nf != P + 1) { free(lg); return 10; }
+  int rc = or_forward(drf, dkv, feed, nf, dkv->pos, NULL, 1, lg, NULL);
+  if (rc) { free(lg); return rc; }
+  drafts[0] = or_argmax(lg, drf->V);
+  for (uint32_t i = 1; i < n; ++i) {
+    rc = or_forward(drf, dkv, &drafts[i - 1], 1, dkv->pos, NULL, 1, lg, NULL);
+    if (rc) { free(lg); return rc; }
+    drafts[i] = or_argmax(lg, drf->V);
+  }
+  uint32_t vt[9];
+  vt[0] = last_token;
+  for (uint32_t i = 0; i < n; ++i) vt[i + 1] = drafts[i];
+  rc = or_forward(tgt, tkv, vt, n + 1, P, NULL, 2, lg, NULL);
+  if (rc) { free(lg); return rc; }
+  uint32_t ne = 0;
+  for (uint32_t i = 0; i <= n; ++i) {
+    uint32_t s = or_argmax(lg + (size_t)i * V, V);
+    emitted[ne++] = s;
+    if (i < n && s == drafts[i]) continue;
+    break;
+  }
+  uint32_t acc = ne - 1;
+  or_kv_truncate(tkv, P + acc + 1);
+  or_kv_truncate(dkv, P + acc + 1);
+  *n_dpending = 0;
+  if (acc == n) dpending[(*n_dpending)++] = drafts[n - 1];
+  *n_emitted = ne;
+  if (drafts_out) memcpy(drafts_out, drafts, n * sizeof(uint32_t));
+  free(lg);
+  return 0;
+}

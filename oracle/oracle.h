@@ -1,0 +1,105 @@
+/* CPU oracle for the seeker speculative-decoding verify path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library; it is never part of
+ * the shipped product path.
+ *
+ * This is a plain-C restatement of the reference's algorithm (rgcottrell/seeker,
+ * Rust + Vulkan/Slang), which cannot be compiled here (no Rust toolchain, no
+ * slangc, no Vulkan). Every function cites the reference file:line it follows.
+ * Numerics: f32 storage between ops (as the reference), f64 accumulation
+ * inside ops (the exact value the reference's f32 kernels approximate), K/V
+ * stored as IEEE f16 with round-to-nearest-even.
+ */
+#ifndef SEEKER_ORACLE_H
+#define SEEKER_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OR_F32 = 0, OR_F16 = 1, OR_Q8_0 = 8, OR_Q4_K = 12 };
+
+float or_f16_to_f32(uint16_t h);
+uint16_t or_f32_to_f16(float f);
+
+/* Philox4x64-10 block (numpy.random.Philox raw block for the given counter). */
+void or_philox4x64_10(const uint64_t ctr[4], const uint64_t key[2], uint64_t out[4]);
+/* Word i of stream key=(k0,k1): block (i/4 + 1, 0, 0, 0), word i % 4. */
+uint64_t or_philox_word(uint64_t k0, uint64_t k1, uint64_t i);
+float or_unit_f32(uint64_t w);
+
+/* Dequantize one row of K elements (apps/seeker-cli/src/commands/run.rs:4212-4303). */
+int or_dequant_row(int type, const uint8_t* raw, uint64_t row, uint64_t k, float* out);
+/* y[j*M + m] = sum_k deq(W)[m,k] * x[j*K + k]  (ggml layout, ops/matmul.rs:295-299). */
+int or_gemv(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, uint32_t N, float* y);
+
+typedef struct or_model or_model;
+typedef struct or_kv or_kv;
+
+/* Parse a Llama GGUF image kept in caller memory (must outlive the model). */
+int or_model_open(const uint8_t* img, uint64_t size, or_model** out);
+void or_model_free(or_model* m);
+/* n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab */
+void or_model_dims(const or_model* m, uint32_t dims[7]);
+
+int or_kv_create(const or_model* m, uint32_t max_seq, or_kv** out);
+void or_kv_free(or_kv* kv);
+uint32_t or_kv_position(const or_kv* kv);
+void or_kv_truncate(or_kv* kv, uint32_t new_pos);
+void or_kv_set_position(or_kv* kv, uint32_t pos);
+/* Raw f16 K or V of one layer in the reference layout [max_seq][n_kv][hd]. */
+uint16_t* or_kv_layer(or_kv* kv, uint32_t layer, int is_v);
+/* Move the K/V rows at slots base+src[i] to base+i (i < n, src ascending),
+ * then position = base + n. */
+void or_kv_compact(or_kv* kv, uint32_t base, const uint32_t* src, uint32_t n);
+
+/* Forward L tokens at cache position pos (llama.rs:196-441, all-position
+ * epilogue qwen35moe.rs:975-989). parents: NULL for a causal chain, else a
+ * tree (parent index within the chunk, -1 = attaches to the prefix).
+ * logits_mode: 0 none, 1 last column, 2 all columns ([L][V]).
+ * residual_out: pre-output_norm hidden state [L][d] or NULL. */
+int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint32_t pos,
+               const int32_t* parents, int logits_mode, float* logits, float* residual_out);
+
+uint32_t or_argmax(const float* x, uint32_t n);
+void or_softmax(const float* x, uint32_t n, float* out);
+
+typedef struct or_sampler_cfg {
+  float temperature;
+  uint32_t top_k;
+  float top_p;
+  float min_p;
+} or_sampler_cfg;
+
+/* Host chain sample with an explicit uniform (inference/sample.rs:369-474). */
+uint32_t or_sample_one(const float* logits, uint32_t V, const or_sampler_cfg* cfg, float u);
+/* GPU full-vocab categorical: inverse CDF in vocab-index order of softmax(l/T)
+ * (inference/ops/sampler.rs:303-368). */
+uint32_t or_sample_vocab_order(const float* logits, uint32_t V, float temperature, float u);
+/* sample_and_compare (inference/sample.rs:347-361) with explicit uniforms;
+ * mode 0: host chain (sorted order), 1: vocab-order GPU chain. Returns n emitted. */
+uint32_t or_sample_and_compare(const float* logits, uint32_t V, const uint32_t* drafts, uint32_t n,
+                               const or_sampler_cfg* cfg, const float* uniforms, int mode,
+                               uint32_t* emitted);
+
+/* Speculative rejection sampling (new: Leviathan et al. 2023). p_logits [(k+1)][V],
+ * q_logits [k][V]; u_acc[k], u_res[k+1]. Returns acc_len, writes next token. */
+uint32_t or_rejection(const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t k,
+                      uint32_t V, float temperature, const float* u_acc, const float* u_res,
+                      uint32_t* next_tok);
+/* softmax(l/T) in f64, rounded to f32. */
+void or_probs(const float* logits, uint32_t V, float temperature, float* out);
+
+/* Greedy speculative step with a separate draft model (inference/mod.rs:2108-2297):
+ * draft n tokens greedily, verify [last, d_1..d_n], accept longest matching prefix,
+ * truncate both caches. *dpending holds the draft's uncommitted tokens. */
+int or_spec_step_greedy(or_model* tgt, or_model* drf, or_kv* tkv, or_kv* dkv, uint32_t last_token,
+                        uint32_t n_max, uint32_t* dpending, uint32_t* n_dpending, uint32_t* emitted,
+                        uint32_t* n_emitted, uint32_t* drafts_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

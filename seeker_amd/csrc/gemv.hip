@@ -1,0 +1,489 @@
+// Quantized GEMV for the verify step: y[j][m] = sum_k deq(W)[m][k] * x[j][k]
+// for N <= 8 columns per launch chunk, on gfx950 MFMA.
+//
+// Semantics: the reference's batched-column matvec (ops/matmul.rs:473-487,
+// shaders/compute/mul_mat_vec_q4_k.slang:13-103 for Q4_K, mul_mat_vec.slang:39-100
+// for Q8_0), which dequantizes each weight row once and reuses it for all N
+// columns. Design here (not a translation):
+//   * Weights are repacked once at upload into 16-row tiles so each lane of a
+//     wave64 reads its MFMA A-operand bytes with two 16-byte loads.
+//   * Q4_K nibbles become exact f16 integers sc*q (<= 945) via the 0x6400 magic
+//     exponent and one packed FMA; d and dmin are applied per 256-superblock in f32.
+//   * Activations are split x = hi + lo (two f16) and fed as 16 MFMA columns
+//     (8 hi + 8 lo), so v_mfma_f32_16x16x32_f16 keeps ~22 bits of x and f32
+//     accumulation at no extra MFMA cost for N <= 8.
+//   * The Q4_K minimum term dmin * sum_s m_s * sum(x in s) is a ninth MFMA per
+//     superblock against per-sub-block column sums (XS).
+#include "sh_internal.h"
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+struct alignas(16) u32x4 { uint32_t x, y, z, w; };
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h8 as_h8(u32x4 v) { return __builtin_bit_cast(h8, v); }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// (v, v) as an f16 pair from a small non-negative integer byte.
+__device__ __forceinline__ h2 pair_of(uint32_t word, int byte) {
+  float f = (float)((word >> (8 * byte)) & 0xFFu);
+  return h2{(_Float16)f, (_Float16)f};
+}
+
+// Four f16 pairs (1024 + q) from the nibbles of one repacked word, then
+// (1024 + q) * sc - 1024 * sc = sc * q exactly (single rounding of an exact value).
+__device__ __forceinline__ h8 q4_operand(uint32_t w, h2 mult, h2 add) {
+  u32x4 r;
+  r.x = as_u32(__builtin_elementwise_fma(as_h2((w & 0x000F000Fu) | 0x64006400u), mult, add));
+  r.y = as_u32(__builtin_elementwise_fma(as_h2(((w >> 4) & 0x000F000Fu) | 0x64006400u), mult, add));
+  r.z = as_u32(__builtin_elementwise_fma(as_h2(((w >> 8) & 0x000F000Fu) | 0x64006400u), mult, add));
+  r.w = as_u32(__builtin_elementwise_fma(as_h2(((w >> 12) & 0x000F000Fu) | 0x64006400u), mult, add));
+  return as_h8(r);
+}
+
+// int8 pairs -> f16 exact: (q ^ 0x80) + 1024 as f16, minus 1152.
+__device__ __forceinline__ h8 q8_operand(uint32_t w0, uint32_t w1) {
+  const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  uint32_t a = w0 ^ 0x80808080u, b = w1 ^ 0x80808080u;
+  u32x4 r;
+  r.x = as_u32(as_h2(((a & 0xFFu) | ((a & 0xFF00u) << 8)) | 0x64006400u) + off);
+  r.y = as_u32(as_h2((((a >> 16) & 0xFFu) | ((a >> 8) & 0xFF0000u)) | 0x64006400u) + off);
+  r.z = as_u32(as_h2(((b & 0xFFu) | ((b & 0xFF00u) << 8)) | 0x64006400u) + off);
+  r.w = as_u32(as_h2((((b >> 16) & 0xFFu) | ((b >> 8) & 0xFF0000u)) | 0x64006400u) + off);
+  return as_h8(r);
+}
+
+// Slot of key kappa (0..31) inside a 32-key V block: the PV MFMA's B operand
+// (probabilities) arrives with lane group g holding keys {4g..4g+3, 16+4g..16+4g+3}.
+__device__ __forceinline__ uint32_t v_slot(uint32_t kappa) {
+  return 8u * ((kappa & 15u) >> 2) + 4u * (kappa >> 4) + (kappa & 3u);
+}
+
+// ------------------------------------------------------------------ repack
+
+// Q4_K tile-superblock (2304 B): [0,2048) 64 lanes x 8 words; lane l (row l%16,
+// group g=l/16), word m (sub-block m) holds q[32m + 8g + t], t=0..7, pair i=t/2:
+// t even at bits 4i, t odd at bits 16+4i. [2048,2112) d|dmin<<16 per row;
+// [2112,2304) the 12 packed scale bytes per row.
+__global__ void k_repack_q4k(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t M,
+                             uint32_t nsb, uint32_t dst_tile0, uint32_t tile_stride) {
+  const uint32_t tile = blockIdx.x, sb = blockIdx.y, l = threadIdx.x;
+  const uint32_t r = l & 15, g = l >> 4, row = tile * 16 + r;
+  uint8_t* out = dst + ((size_t)(dst_tile0 + tile * tile_stride) * nsb + sb) * SH_Q4K_TILE_BYTES;
+  uint32_t words[8];
+  if (row < M) {
+    const uint8_t* blk = src + ((size_t)row * nsb + sb) * 144;
+    const uint8_t* qs = blk + 16;
+    for (int m = 0; m < 8; ++m) {
+      uint32_t w = 0;
+      for (int t = 0; t < 8; ++t) {
+        uint32_t pos = 8 * g + t;
+        uint32_t byte = qs[32 * (m >> 1) + pos];
+        uint32_t q = (m & 1) ? (byte >> 4) : (byte & 0xF);
+        uint32_t shift = (t & 1) ? 16 + 4 * (t >> 1) : 4 * (t >> 1);
+        w |= q << shift;
+      }
+      words[m] = w;
+    }
+    if (g == 0) {
+      uint32_t dd = blk[0] | (blk[1] << 8) | (blk[2] << 16) | ((uint32_t)blk[3] << 24);
+      *(uint32_t*)(out + 2048 + 4 * r) = dd;
+      for (int i = 0; i < 12; ++i) out[2112 + 12 * r + i] = blk[4 + i];
+    }
+  } else {
+    for (int m = 0; m < 8; ++m) words[m] = 0;
+    if (g == 0) {
+      *(uint32_t*)(out + 2048 + 4 * r) = 0;
+      for (int i = 0; i < 12; ++i) out[2112 + 12 * r + i] = 0;
+    }
+  }
+  uint32_t* o = (uint32_t*)(out + 32 * l);
+  for (int m = 0; m < 8; ++m) o[m] = words[m];
+}
+
+// Q8_0 tile-block (544 B): [0,512) 64 lanes x 8 int8 (row l%16, k = 32b + 8g + t);
+// [512,544) f16 d per row.
+__global__ void k_repack_q8(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t M,
+                            uint32_t nb, uint32_t dst_tile0, uint32_t tile_stride) {
+  const uint32_t tile = blockIdx.x, b = blockIdx.y, l = threadIdx.x;
+  const uint32_t r = l & 15, g = l >> 4, row = tile * 16 + r;
+  uint8_t* out = dst + ((size_t)(dst_tile0 + tile * tile_stride) * nb + b) * SH_Q8_TILE_BYTES;
+  if (row < M) {
+    const uint8_t* blk = src + ((size_t)row * nb + b) * 34;
+    for (int t = 0; t < 8; ++t) out[8 * l + t] = blk[2 + 8 * g + t];
+    if (g == 0) { out[512 + 2 * r] = blk[0]; out[513 + 2 * r] = blk[1]; }
+  } else {
+    for (int t = 0; t < 8; ++t) out[8 * l + t] = 0;
+    if (g == 0) { out[512 + 2 * r] = 0; out[513 + 2 * r] = 0; }
+  }
+}
+
+// ------------------------------------------------------------------ epilogue
+
+__device__ __forceinline__ uint16_t f2h_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+
+// Final (row, col) value for rows r0..r0+3 (one lane), col < N.
+template <int EPI>
+__device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32_t col, const float v[4]) {
+  if (EPI == EPI_STORE) {
+    for (int j = 0; j < 4; ++j) ea.out[(size_t)col * ea.ldo + r0 + j] = v[j];
+  } else if (EPI == EPI_ADD) {
+    for (int j = 0; j < 4; ++j) {
+      float* p = ea.out + (size_t)col * ea.ldo + r0 + j;
+      *p = *p + v[j];
+    }
+  } else if (EPI == EPI_QKV) {
+    const int32_t pos = ea.colpos[col & 7];
+    const uint32_t slot = ea.slot0 + col;
+    if (r0 < ea.Dq) {
+      const uint32_t i0 = r0 % ea.hd;
+      const float2 cs0 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2];
+      const float2 cs1 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2 + 1];
+      float* q = ea.out + (size_t)col * ea.Dq + r0;
+      q[0] = v[0] * cs0.x - v[1] * cs0.y;
+      q[1] = v[0] * cs0.y + v[1] * cs0.x;
+      q[2] = v[2] * cs1.x - v[3] * cs1.y;
+      q[3] = v[2] * cs1.y + v[3] * cs1.x;
+    } else if (r0 < ea.Dq + ea.Dkv) {
+      const uint32_t rr = r0 - ea.Dq, kh = rr / ea.hd, i0 = rr % ea.hd;
+      const float2 cs0 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2];
+      const float2 cs1 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2 + 1];
+      float o[4];
+      o[0] = v[0] * cs0.x - v[1] * cs0.y;
+      o[1] = v[0] * cs0.y + v[1] * cs0.x;
+      o[2] = v[2] * cs1.x - v[3] * cs1.y;
+      o[3] = v[2] * cs1.y + v[3] * cs1.x;
+      uint16_t* k = ea.kc + (((size_t)ea.layer * ea.n_kv + kh) * ea.max_seq + slot) * ea.hd + i0;
+      for (int j = 0; j < 4; ++j) k[j] = f2h_bits(o[j]);
+    } else {
+      const uint32_t rr = r0 - ea.Dq - ea.Dkv, kh = rr / ea.hd, i0 = rr % ea.hd;
+      uint16_t* vb = ea.vc + (((size_t)ea.layer * ea.n_kv + kh) * (ea.max_seq / 32) + slot / 32) * ea.hd * 32;
+      const uint32_t sl = v_slot(slot & 31);
+      for (int j = 0; j < 4; ++j) vb[(size_t)(i0 + j) * 32 + sl] = f2h_bits(v[j]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ kernels
+
+// R tiles per workgroup, W waves per workgroup splitting the superblocks.
+template <int R, int W, int EPI>
+__global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles,
+                                                      uint32_t nsb, const uint16_t* __restrict__ Bx,
+                                                      const uint16_t* __restrict__ XS, uint32_t N,
+                                                      EpiArgs ea) {
+  __shared__ f4 red[W][R][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const uint32_t tile0 = blockIdx.x * R;
+  f4 y[R];
+#pragma unroll
+  for (int t = 0; t < R; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (uint32_t b = wave; b < nsb; b += W) {
+    h8 bq[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
+    const h8 bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+      const uint32_t tile = tile0 + t;
+      if (tile >= tiles) break;
+      const uint8_t* base = Wp + ((size_t)tile * nsb + b) * SH_Q4K_TILE_BYTES;
+      const u32x4 q0 = ld16(base + 32 * lane), q1 = ld16(base + 32 * lane + 16);
+      const u32x4 dd = ld16(base + 2048 + 16 * g);
+      const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
+      const uint32_t s0 = sp[0], s1 = sp[1], s2 = sp[2];
+      const uint32_t sc03 = s0 & 0x3F3F3F3Fu, m03 = s1 & 0x3F3F3F3Fu;
+      const uint32_t sc47 = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+      const uint32_t m47 = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+      const uint32_t words[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const h2 mult = pair_of(m < 4 ? sc03 : sc47, m & 3);
+        const h2 add = mult * k1024;
+        acc = mfma16(q4_operand(words[m], mult, add), bq[m], acc);
+      }
+      // Minimum term: A = m_s (lane group 0 only, k = s), B = XS (zero for g > 0).
+      u32x4 am;
+      am.x = as_u32(h2{(_Float16)(float)(m03 & 0xFF), (_Float16)(float)((m03 >> 8) & 0xFF)});
+      am.y = as_u32(h2{(_Float16)(float)((m03 >> 16) & 0xFF), (_Float16)(float)(m03 >> 24)});
+      am.z = as_u32(h2{(_Float16)(float)(m47 & 0xFF), (_Float16)(float)((m47 >> 8) & 0xFF)});
+      am.w = as_u32(h2{(_Float16)(float)((m47 >> 16) & 0xFF), (_Float16)(float)(m47 >> 24)});
+      const f4 macc = mfma16(as_h8(am), bm, f4{0.f, 0.f, 0.f, 0.f});
+      const uint32_t ddw[4] = {dd.x, dd.y, dd.z, dd.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float d = (float)as_h2(ddw[j]).x, dmin = (float)as_h2(ddw[j]).y;
+        y[t][j] = y[t][j] + d * acc[j] - dmin * macc[j];
+      }
+    }
+  }
+
+  if (W > 1) {
+#pragma unroll
+    for (int t = 0; t < R; ++t) red[wave][t][lane] = y[t];
+    __syncthreads();
+  }
+  if (EPI == EPI_SWIGLU) {
+    if (wave >= R / 2) return;
+    const int tg = 2 * wave, tu = 2 * wave + 1;
+    f4 vg = {0.f, 0.f, 0.f, 0.f}, vu = {0.f, 0.f, 0.f, 0.f};
+    if (W > 1) {
+      for (int w = 0; w < W; ++w) { vg += red[w][tg][lane]; vu += red[w][tu][lane]; }
+    } else {
+      vg = y[tg]; vu = y[tu];
+    }
+    float og[4], ou[4];
+    for (int j = 0; j < 4; ++j) {
+      og[j] = vg[j] + __shfl_xor(vg[j], 8);
+      ou[j] = vu[j] + __shfl_xor(vu[j], 8);
+    }
+    const uint32_t pair = (tile0 + tg) / 2;
+    if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
+    const uint32_t row0 = pair * 16 + 4 * g;
+    for (int j = 0; j < 4; ++j) {
+      const float x = og[j];
+      const float sl = x / (1.0f + expf(-x));
+      ea.out[(size_t)r * ea.ldo + row0 + j] = sl * ou[j];
+    }
+    return;
+  }
+  if (wave >= R) return;
+  const uint32_t tile = tile0 + wave;
+  f4 v = {0.f, 0.f, 0.f, 0.f};
+  if (W > 1) {
+    for (int w = 0; w < W; ++w) v += red[w][wave][lane];
+  } else {
+    v = y[wave];
+  }
+  float o[4];
+  for (int j = 0; j < 4; ++j) o[j] = v[j] + __shfl_xor(v[j], 8);
+  if (tile >= tiles || r >= 8 || (uint32_t)r >= N) return;
+  epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
+}
+
+template <int R, int W, int EPI>
+__global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nb,
+                                                     const uint16_t* __restrict__ Bx, uint32_t N, EpiArgs ea) {
+  __shared__ f4 red[W][R][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const uint32_t tile0 = blockIdx.x * R;
+  f4 y[R];
+#pragma unroll
+  for (int t = 0; t < R; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t b = wave; b < nb; b += W) {
+    const h8 bq = as_h8(ld16(Bx + ((size_t)b * 64 + lane) * 8));
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+      const uint32_t tile = tile0 + t;
+      if (tile >= tiles) break;
+      const uint8_t* base = Wp + ((size_t)tile * nb + b) * SH_Q8_TILE_BYTES;
+      const uint2 qw = *(const uint2*)(base + 8 * lane);
+      const uint2 dw = *(const uint2*)(base + 512 + 8 * g);
+      const f4 acc = mfma16(q8_operand(qw.x, qw.y), bq, f4{0.f, 0.f, 0.f, 0.f});
+      const float d[4] = {(float)as_h2(dw.x).x, (float)as_h2(dw.x).y, (float)as_h2(dw.y).x,
+                          (float)as_h2(dw.y).y};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[t][j] = y[t][j] + d[j] * acc[j];
+    }
+  }
+  if (W > 1) {
+#pragma unroll
+    for (int t = 0; t < R; ++t) red[wave][t][lane] = y[t];
+    __syncthreads();
+  }
+  if (EPI == EPI_SWIGLU) {
+    if (wave >= R / 2) return;
+    const int tg = 2 * wave, tu = 2 * wave + 1;
+    f4 vg = {0.f, 0.f, 0.f, 0.f}, vu = {0.f, 0.f, 0.f, 0.f};
+    if (W > 1) {
+      for (int w = 0; w < W; ++w) { vg += red[w][tg][lane]; vu += red[w][tu][lane]; }
+    } else {
+      vg = y[tg]; vu = y[tu];
+    }
+    float og[4], ou[4];
+    for (int j = 0; j < 4; ++j) {
+      og[j] = vg[j] + __shfl_xor(vg[j], 8);
+      ou[j] = vu[j] + __shfl_xor(vu[j], 8);
+    }
+    const uint32_t pair = (tile0 + tg) / 2;
+    if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
+    const uint32_t row0 = pair * 16 + 4 * g;
+    for (int j = 0; j < 4; ++j) {
+      const float x = og[j];
+      ea.out[(size_t)r * ea.ldo + row0 + j] = (x / (1.0f + expf(-x))) * ou[j];
+    }
+    return;
+  }
+  if (wave >= R) return;
+  const uint32_t tile = tile0 + wave;
+  f4 v = {0.f, 0.f, 0.f, 0.f};
+  if (W > 1) {
+    for (int w = 0; w < W; ++w) v += red[w][wave][lane];
+  } else {
+    v = y[wave];
+  }
+  float o[4];
+  for (int j = 0; j < 4; ++j) o[j] = v[j] + __shfl_xor(v[j], 8);
+  if (tile >= tiles || r >= 8 || (uint32_t)r >= N) return;
+  epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
+}
+
+// ------------------------------------------------------------------ host side
+
+void sh_qmat_free(QMat* m) {
+  if (m->d) (void)hipFree(m->d);
+  m->d = nullptr;
+}
+
+static size_t qrow_bytes(int type, uint32_t K) { return type == GGML_Q4_K ? K / 256 * 144 : K / 32 * 34; }
+
+// Upload nparts row-blocks (each a GGUF [rows][K] matrix) as one packed matrix
+// with rows concatenated. Each part's row count must be a multiple of 16.
+int sh_repack_upload_cat(sh_engine* e, int type, const uint8_t* const* parts, const uint32_t* rows, int nparts,
+                         uint32_t K, QMat* out) {
+  SH_CHECK(type == GGML_Q4_K || type == GGML_Q8_0, SH_ERR_UNSUPPORTED,
+           "weight type %d not supported (Q4_K=12, Q8_0=8)", type);
+  SH_CHECK(K % (type == GGML_Q4_K ? 256 : 32) == 0, SH_ERR_FORMAT, "K=%u not a multiple of the block", K);
+  uint32_t M = 0;
+  for (int i = 0; i < nparts; ++i) {
+    SH_CHECK(nparts == 1 || rows[i] % 16 == 0, SH_ERR_UNSUPPORTED, "concatenated part rows %u %% 16", rows[i]);
+    M += rows[i];
+  }
+  const uint32_t nblk = type == GGML_Q4_K ? K / 256 : K / 32;
+  const uint32_t tb = type == GGML_Q4_K ? SH_Q4K_TILE_BYTES : SH_Q8_TILE_BYTES;
+  QMat m;
+  m.type = type; m.M = M; m.K = K; m.tiles = (M + 15) / 16;
+  m.bytes = (size_t)m.tiles * nblk * tb;
+  m.alg_bytes = (double)M * qrow_bytes(type, K);
+  SH_HIP(hipMalloc(&m.d, m.bytes));
+  uint32_t tile0 = 0;
+  for (int i = 0; i < nparts; ++i) {
+    const size_t bytes = (size_t)rows[i] * qrow_bytes(type, K);
+    uint8_t* tmp = nullptr;
+    SH_HIP(hipMalloc(&tmp, bytes));
+    SH_HIP(hipMemcpyAsync(tmp, parts[i], bytes, hipMemcpyHostToDevice, e->stream));
+    const uint32_t ptiles = (rows[i] + 15) / 16;
+    dim3 grid(ptiles, nblk);
+    if (type == GGML_Q4_K)
+      hipLaunchKernelGGL(k_repack_q4k, grid, dim3(64), 0, e->stream, tmp, m.d, rows[i], nblk, tile0, 1u);
+    else
+      hipLaunchKernelGGL(k_repack_q8, grid, dim3(64), 0, e->stream, tmp, m.d, rows[i], nblk, tile0, 1u);
+    SH_HIP(hipGetLastError());
+    SH_HIP(hipStreamSynchronize(e->stream));
+    SH_HIP(hipFree(tmp));
+    tile0 += ptiles;
+  }
+  *out = m;
+  return SH_OK;
+}
+
+int sh_repack_upload(sh_engine* e, int type, const uint8_t* host, uint32_t M, uint32_t K, QMat* out) {
+  return sh_repack_upload_cat(e, type, &host, &M, 1, K, out);
+}
+
+// gate/up: tile t of gate -> packed tile 2t, tile t of up -> 2t+1.
+int sh_repack_upload_gu(sh_engine* e, int type, const uint8_t* gate, const uint8_t* up, uint32_t M, uint32_t K,
+                        QMat* out) {
+  SH_CHECK(type == GGML_Q4_K || type == GGML_Q8_0, SH_ERR_UNSUPPORTED, "weight type %d not supported", type);
+  SH_CHECK(M % 32 == 0, SH_ERR_UNSUPPORTED, "n_ff=%u must be a multiple of 32", M);
+  const uint32_t nblk = type == GGML_Q4_K ? K / 256 : K / 32;
+  const uint32_t tb = type == GGML_Q4_K ? SH_Q4K_TILE_BYTES : SH_Q8_TILE_BYTES;
+  QMat m;
+  m.type = type; m.M = 2 * M; m.K = K; m.tiles = 2 * (M / 16);
+  m.bytes = (size_t)m.tiles * nblk * tb;
+  m.alg_bytes = 2.0 * M * qrow_bytes(type, K);
+  SH_HIP(hipMalloc(&m.d, m.bytes));
+  const size_t bytes = (size_t)M * qrow_bytes(type, K);
+  uint8_t* tmp = nullptr;
+  SH_HIP(hipMalloc(&tmp, bytes));
+  for (int part = 0; part < 2; ++part) {
+    SH_HIP(hipMemcpyAsync(tmp, part ? up : gate, bytes, hipMemcpyHostToDevice, e->stream));
+    dim3 grid(M / 16, nblk);
+    if (type == GGML_Q4_K)
+      hipLaunchKernelGGL(k_repack_q4k, grid, dim3(64), 0, e->stream, tmp, m.d, M, nblk, (uint32_t)part, 2u);
+    else
+      hipLaunchKernelGGL(k_repack_q8, grid, dim3(64), 0, e->stream, tmp, m.d, M, nblk, (uint32_t)part, 2u);
+    SH_HIP(hipGetLastError());
+    SH_HIP(hipStreamSynchronize(e->stream));
+  }
+  SH_HIP(hipFree(tmp));
+  *out = m;
+  return SH_OK;
+}
+
+template <int R, int W, int EPI>
+static void launch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                       const EpiArgs& ea) {
+  const uint32_t grid = (w.tiles + R - 1) / R;
+  hipLaunchKernelGGL((k_gemv_q4k<R, W, EPI>), dim3(grid), dim3(64 * W), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
+                     xs, N, ea);
+}
+template <int R, int W, int EPI>
+static void launch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {
+  const uint32_t grid = (w.tiles + R - 1) / R;
+  hipLaunchKernelGGL((k_gemv_q8<R, W, EPI>), dim3(grid), dim3(64 * W), 0, e->stream, w.d, w.tiles, w.K / 32, bx, N,
+                     ea);
+}
+
+// Shape policy: keep >= ~1000 waves in flight. Small-M matrices use one tile
+// per workgroup and 8 waves splitting K; large-M ones share the activation
+// operand across 4 tiles per wave.
+template <int EPI>
+static void dispatch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                         const EpiArgs& ea) {
+  if (EPI == EPI_SWIGLU) {
+    if (w.tiles >= 4096) launch_q4k<4, 4, EPI>(e, w, bx, xs, N, ea);
+    else launch_q4k<2, 8, EPI>(e, w, bx, xs, N, ea);
+  } else if (w.tiles >= 4096) {
+    launch_q4k<4, 4, EPI>(e, w, bx, xs, N, ea);
+  } else if (w.tiles >= 1024) {
+    launch_q4k<2, 4, EPI>(e, w, bx, xs, N, ea);
+  } else {
+    launch_q4k<1, 8, EPI>(e, w, bx, xs, N, ea);
+  }
+}
+template <int EPI>
+static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {
+  if (EPI == EPI_SWIGLU) launch_q8<2, 4, EPI>(e, w, bx, N, ea);
+  else if (w.tiles >= 1024) launch_q8<2, 4, EPI>(e, w, bx, N, ea);
+  else launch_q8<1, 4, EPI>(e, w, bx, N, ea);
+}
+
+int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N, EpiKind epi,
+                   const EpiArgs& ea, const char* tag) {
+  SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "gemv chunk N=%u outside [1,8]", N);
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  if (w.type == GGML_Q4_K) {
+    switch (epi) {
+      case EPI_STORE: dispatch_q4k<EPI_STORE>(e, w, bx, xs, N, ea); break;
+      case EPI_ADD: dispatch_q4k<EPI_ADD>(e, w, bx, xs, N, ea); break;
+      case EPI_QKV: dispatch_q4k<EPI_QKV>(e, w, bx, xs, N, ea); break;
+      case EPI_SWIGLU: dispatch_q4k<EPI_SWIGLU>(e, w, bx, xs, N, ea); break;
+    }
+  } else if (w.type == GGML_Q8_0) {
+    switch (epi) {
+      case EPI_STORE: dispatch_q8<EPI_STORE>(e, w, bx, N, ea); break;
+      case EPI_ADD: dispatch_q8<EPI_ADD>(e, w, bx, N, ea); break;
+      case EPI_QKV: dispatch_q8<EPI_QKV>(e, w, bx, N, ea); break;
+      case EPI_SWIGLU: dispatch_q8<EPI_SWIGLU>(e, w, bx, N, ea); break;
+    }
+  } else {
+    SH_CHECK(false, SH_ERR_UNSUPPORTED, "gemv: weight type %d", w.type);
+  }
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, tag, w.alg_bytes, ev);
+  return SH_OK;
+}

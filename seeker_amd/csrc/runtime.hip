@@ -1,0 +1,983 @@
+// Host runtime of libseeker_hip: engine / model / KV handles, the verify
+// forward and the speculative step, behind the C ABI of include/seeker_hip.h.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "sh_internal.h"
+
+// ------------------------------------------------------------------ errors
+
+static thread_local char g_err[1024] = "";
+
+void sh_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+extern "C" const char* sh_last_error(void) { return g_err; }
+extern "C" const char* sh_version(void) { return "seeker-hip 0.1 (gfx950)"; }
+
+// ------------------------------------------------------------------ profiling
+
+void sh_prof_begin(sh_engine* e, hipEvent_t* a) {
+  *a = nullptr;
+  if (!e->profiling) return;
+  if (e->event_pool.empty()) {
+    hipEvent_t ev;
+    if (hipEventCreate(&ev) != hipSuccess) return;
+    e->event_pool.push_back(ev);
+  }
+  *a = e->event_pool.back();
+  e->event_pool.pop_back();
+  (void)hipEventRecord(*a, e->stream);
+}
+
+void sh_prof_end(sh_engine* e, const char* name, double bytes, hipEvent_t a) {
+  if (!e->profiling || !a) return;
+  hipEvent_t b;
+  if (e->event_pool.empty()) {
+    if (hipEventCreate(&b) != hipSuccess) return;
+  } else {
+    b = e->event_pool.back();
+    e->event_pool.pop_back();
+  }
+  (void)hipEventRecord(b, e->stream);
+  e->pending.push_back({name, bytes, a, b});
+}
+
+int sh_prof_flush(sh_engine* e) {
+  if (e->pending.empty()) return SH_OK;
+  SH_HIP(hipStreamSynchronize(e->stream));
+  for (auto& p : e->pending) {
+    float ms = 0.f;
+    SH_HIP(hipEventElapsedTime(&ms, p.a, p.b));
+    KStat& s = e->stats[p.name];
+    s.launches += 1;
+    s.ms += ms;
+    s.bytes += p.bytes;
+    e->event_pool.push_back(p.a);
+    e->event_pool.push_back(p.b);
+  }
+  e->pending.clear();
+  return SH_OK;
+}
+
+// ------------------------------------------------------------------ engine
+
+extern "C" int sh_engine_create(int dev, sh_engine** out) {
+  SH_CHECK(out, SH_ERR_ARG, "sh_engine_create: out is NULL");
+  int n = 0;
+  SH_HIP(hipGetDeviceCount(&n));
+  SH_CHECK(dev >= 0 && dev < n, SH_ERR_ARG, "hip device %d out of range (%d devices)", dev, n);
+  SH_HIP(hipSetDevice(dev));
+  hipDeviceProp_t prop;
+  SH_HIP(hipGetDeviceProperties(&prop, dev));
+  SH_CHECK(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0, SH_ERR_UNSUPPORTED,
+           "device %d is %s; this library is built for gfx950 only", dev, prop.gcnArchName);
+  sh_engine* e = new sh_engine();
+  e->device = dev;
+  hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+  if (err != hipSuccess) {
+    delete e;
+    sh_set_error("hipStreamCreate: %s", hipGetErrorString(err));
+    return SH_ERR_HIP;
+  }
+  *out = e;
+  return SH_OK;
+}
+
+extern "C" void sh_engine_destroy(sh_engine* e) {
+  if (!e) return;
+  (void)hipSetDevice(e->device);
+  (void)hipStreamSynchronize(e->stream);
+  for (auto& p : e->pending) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
+  for (auto ev : e->event_pool) (void)hipEventDestroy(ev);
+  (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+extern "C" int sh_engine_sync(sh_engine* e) {
+  SH_CHECK(e, SH_ERR_ARG, "engine is NULL");
+  SH_HIP(hipStreamSynchronize(e->stream));
+  return sh_prof_flush(e);
+}
+
+extern "C" int sh_engine_set_profiling(sh_engine* e, int on) {
+  SH_CHECK(e, SH_ERR_ARG, "engine is NULL");
+  int rc = sh_prof_flush(e);
+  if (rc) return rc;
+  e->profiling = on != 0;
+  return SH_OK;
+}
+
+extern "C" int sh_engine_profile(sh_engine* e, sh_kernel_stat* out, uint32_t cap, uint32_t* n_out) {
+  SH_CHECK(e && n_out, SH_ERR_ARG, "engine / n_out is NULL");
+  int rc = sh_prof_flush(e);
+  if (rc) return rc;
+  uint32_t n = 0;
+  for (auto& kv : e->stats) {
+    if (out && n < cap) {
+      std::memset(&out[n], 0, sizeof(sh_kernel_stat));
+      std::snprintf(out[n].name, sizeof out[n].name, "%s", kv.first.c_str());
+      out[n].launches = kv.second.launches;
+      out[n].total_ms = kv.second.ms;
+      out[n].alg_bytes = kv.second.bytes;
+    }
+    ++n;
+  }
+  *n_out = n;
+  return SH_OK;
+}
+
+extern "C" int sh_engine_profile_reset(sh_engine* e) {
+  SH_CHECK(e, SH_ERR_ARG, "engine is NULL");
+  int rc = sh_prof_flush(e);
+  e->stats.clear();
+  return rc;
+}
+
+extern "C" int sh_dev_alloc(sh_engine* e, uint64_t bytes, void** out) {
+  SH_CHECK(e && out, SH_ERR_ARG, "sh_dev_alloc: NULL argument");
+  SH_HIP(hipMalloc(out, bytes ? bytes : 1));
+  return SH_OK;
+}
+extern "C" int sh_dev_free(sh_engine* e, void* p) {
+  SH_CHECK(e, SH_ERR_ARG, "engine is NULL");
+  if (p) SH_HIP(hipFree(p));
+  return SH_OK;
+}
+extern "C" int sh_memcpy_h2d(sh_engine* e, void* dst, const void* src, uint64_t bytes) {
+  SH_CHECK(e && dst && src, SH_ERR_ARG, "sh_memcpy_h2d: NULL argument");
+  SH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, e->stream));
+  SH_HIP(hipStreamSynchronize(e->stream));
+  return SH_OK;
+}
+extern "C" int sh_memcpy_d2h(sh_engine* e, void* dst, const void* src, uint64_t bytes) {
+  SH_CHECK(e && dst && src, SH_ERR_ARG, "sh_memcpy_d2h: NULL argument");
+  SH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, e->stream));
+  SH_HIP(hipStreamSynchronize(e->stream));
+  return sh_prof_flush(e);
+}
+
+// ------------------------------------------------------------------ GGUF
+
+// GGUF v2/v3 reader (semantics of crates/seeker-core/src/gguf/mod.rs:161-230:
+// magic, version, u64 counts, typed metadata, tensor infos, data section
+// aligned to general.alignment (default 32)).
+namespace {
+
+struct GTensor {
+  std::string name;
+  uint32_t type = 0;
+  uint64_t ne[4] = {1, 1, 1, 1};
+  uint32_t nd = 0;
+  uint64_t off = 0;
+};
+
+struct GFile {
+  const uint8_t* base = nullptr;
+  uint64_t size = 0;
+  std::map<std::string, double> num;
+  std::map<std::string, std::string> str;
+  std::vector<GTensor> tensors;
+  const uint8_t* data = nullptr;
+  const GTensor* find(const std::string& n) const {
+    for (auto& t : tensors)
+      if (t.name == n) return &t;
+    return nullptr;
+  }
+};
+
+struct Rd {
+  const uint8_t* p;
+  const uint8_t* end;
+  bool bad = false;
+  uint64_t u(int n) {
+    if (p + n > end) { bad = true; return 0; }
+    uint64_t v = 0;
+    for (int i = 0; i < n; ++i) v |= (uint64_t)p[i] << (8 * i);
+    p += n;
+    return v;
+  }
+  std::string s() {
+    uint64_t n = u(8);
+    if (bad || n > (uint64_t)(end - p)) { bad = true; return ""; }
+    std::string r((const char*)p, n);
+    p += n;
+    return r;
+  }
+};
+
+bool skip_value(Rd& r, uint32_t t, int depth = 0) {
+  static const int sz[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+  if (depth > 4 || t > 12) return false;
+  if (t == 8) { r.s(); return !r.bad; }
+  if (t == 9) {
+    uint32_t et = (uint32_t)r.u(4);
+    uint64_t n = r.u(8);
+    for (uint64_t i = 0; i < n && !r.bad; ++i)
+      if (!skip_value(r, et, depth + 1)) return false;
+    return !r.bad;
+  }
+  r.u(sz[t]);
+  return !r.bad;
+}
+
+int parse_gguf(const uint8_t* img, uint64_t size, GFile* f) {
+  SH_CHECK(size >= 24 && std::memcmp(img, "GGUF", 4) == 0, SH_ERR_FORMAT, "not a GGUF file (bad magic)");
+  Rd r{img + 4, img + size};
+  uint32_t ver = (uint32_t)r.u(4);
+  SH_CHECK(ver == 2 || ver == 3, SH_ERR_FORMAT, "unsupported GGUF version %u", ver);
+  uint64_t nt = r.u(8), nkv = r.u(8);
+  SH_CHECK(nt < (1u << 24) && nkv < (1u << 24), SH_ERR_FORMAT, "implausible GGUF counts");
+  uint32_t align = 32;
+  for (uint64_t i = 0; i < nkv && !r.bad; ++i) {
+    std::string k = r.s();
+    uint32_t t = (uint32_t)r.u(4);
+    switch (t) {
+      case 0: f->num[k] = (double)(uint8_t)r.u(1); break;
+      case 1: f->num[k] = (double)(int8_t)r.u(1); break;
+      case 2: f->num[k] = (double)(uint16_t)r.u(2); break;
+      case 3: f->num[k] = (double)(int16_t)r.u(2); break;
+      case 4: f->num[k] = (double)(uint32_t)r.u(4); break;
+      case 5: f->num[k] = (double)(int32_t)r.u(4); break;
+      case 6: { uint32_t b = (uint32_t)r.u(4); float x; std::memcpy(&x, &b, 4); f->num[k] = x; break; }
+      case 7: f->num[k] = (double)r.u(1); break;
+      case 8: f->str[k] = r.s(); break;
+      case 10: f->num[k] = (double)r.u(8); break;
+      case 11: f->num[k] = (double)(int64_t)r.u(8); break;
+      case 12: { uint64_t b = r.u(8); double x; std::memcpy(&x, &b, 8); f->num[k] = x; break; }
+      default:
+        SH_CHECK(skip_value(r, t), SH_ERR_FORMAT, "bad GGUF metadata value type %u for %s", t, k.c_str());
+    }
+    if (k == "general.alignment" && t == 4) align = (uint32_t)f->num[k];
+  }
+  SH_CHECK(!r.bad, SH_ERR_FORMAT, "truncated GGUF metadata");
+  SH_CHECK(align && (align & (align - 1)) == 0, SH_ERR_FORMAT, "bad alignment %u", align);
+  for (uint64_t i = 0; i < nt && !r.bad; ++i) {
+    GTensor t;
+    t.name = r.s();
+    t.nd = (uint32_t)r.u(4);
+    SH_CHECK(t.nd >= 1 && t.nd <= 4, SH_ERR_FORMAT, "tensor %s has %u dims", t.name.c_str(), t.nd);
+    for (uint32_t j = 0; j < t.nd; ++j) t.ne[j] = r.u(8);
+    t.type = (uint32_t)r.u(4);
+    t.off = r.u(8);
+    f->tensors.push_back(t);
+  }
+  SH_CHECK(!r.bad, SH_ERR_FORMAT, "truncated GGUF tensor table");
+  uint64_t pos = (uint64_t)(r.p - img);
+  uint64_t start = (pos + align - 1) / align * align;
+  SH_CHECK(start <= size, SH_ERR_FORMAT, "GGUF data section past end of file");
+  f->base = img;
+  f->size = size;
+  f->data = img + start;
+  for (auto& t : f->tensors) {
+    uint64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    uint64_t bytes = 0;
+    switch (t.type) {
+      case GGML_F32: bytes = n * 4; break;
+      case GGML_F16: bytes = n * 2; break;
+      case GGML_Q8_0: bytes = n / 32 * 34; break;
+      case GGML_Q4_K: bytes = n / 256 * 144; break;
+      default: bytes = 0;
+    }
+    SH_CHECK(start + t.off + bytes <= size, SH_ERR_FORMAT, "tensor %s extends past end of file", t.name.c_str());
+  }
+  return SH_OK;
+}
+
+double num_or(const GFile& f, const char* k, double dflt, bool* found = nullptr) {
+  auto it = f.num.find(k);
+  if (found) *found = it != f.num.end();
+  return it == f.num.end() ? dflt : it->second;
+}
+
+template <class T>
+int dalloc(T** p, size_t n) {
+  SH_HIP(hipMalloc((void**)p, n * sizeof(T) ? n * sizeof(T) : 1));
+  return SH_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ model
+
+static void free_model(sh_model* m) {
+  if (!m) return;
+  for (auto& L : m->layers) {
+    (void)hipFree(L.attn_norm);
+    (void)hipFree(L.ffn_norm);
+    sh_qmat_free(&L.wqkv);
+    sh_qmat_free(&L.wo);
+    sh_qmat_free(&L.wgu);
+    sh_qmat_free(&L.wdown);
+  }
+  sh_qmat_free(&m->lm_head);
+  (void)hipFree(m->embd_raw);
+  (void)hipFree(m->out_norm);
+  (void)hipFree(m->rope);
+  Workspace& w = m->ws;
+  (void)hipFree(w.resid); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
+  (void)hipFree(w.attn); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
+  (void)hipFree(w.tokens); (void)hipFree(w.amax);
+  delete m;
+}
+
+static int ensure_rope(sh_model* m, uint32_t npos) {
+  if (npos <= m->rope_max) return SH_OK;
+  uint32_t cap = std::max<uint32_t>(npos, 1024);
+  cap = (cap + 1023) / 1024 * 1024;
+  const uint32_t half = m->hd / 2;
+  std::vector<float2> tab((size_t)cap * half);
+  // theta = pos * base^(-2 i / n_dims) (rope_funcs.slang:37-61, ops/rope.rs:138),
+  // evaluated in double and rounded once.
+  for (uint32_t p = 0; p < cap; ++p)
+    for (uint32_t i = 0; i < half; ++i) {
+      double th = (double)p * std::pow((double)m->theta, -2.0 * i / (double)m->hd);
+      tab[(size_t)p * half + i] = make_float2((float)std::cos(th), (float)std::sin(th));
+    }
+  SH_HIP(hipStreamSynchronize(m->e->stream));
+  if (m->rope) SH_HIP(hipFree(m->rope));
+  m->rope = nullptr;
+  SH_HIP(hipMalloc(&m->rope, tab.size() * sizeof(float2)));
+  SH_HIP(hipMemcpy(m->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+  m->rope_max = cap;
+  return SH_OK;
+}
+
+static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model** out) {
+  SH_CHECK(e && img && out, SH_ERR_ARG, "sh_model_load: NULL argument");
+  SH_HIP(hipSetDevice(e->device));
+  GFile f;
+  int rc = parse_gguf(img, size, &f);
+  if (rc) return rc;
+  auto arch = f.str.find("general.architecture");
+  SH_CHECK(arch != f.str.end() && arch->second == "llama", SH_ERR_UNSUPPORTED,
+           "architecture '%s' not supported (llama only)", arch == f.str.end() ? "?" : arch->second.c_str());
+  sh_model* m = new sh_model();
+  m->e = e;
+  // GGUF keys / defaults: models/llama.rs:1038-1048.
+  bool ok1, ok2, ok3, ok4, ok5;
+  m->n_layer = (uint32_t)num_or(f, "llama.block_count", 0, &ok1);
+  m->n_head = (uint32_t)num_or(f, "llama.attention.head_count", 0, &ok2);
+  m->n_kv = (uint32_t)num_or(f, "llama.attention.head_count_kv", m->n_head);
+  m->d = (uint32_t)num_or(f, "llama.embedding_length", 0, &ok3);
+  m->ff = (uint32_t)num_or(f, "llama.feed_forward_length", 0, &ok4);
+  m->n_ctx = (uint32_t)num_or(f, "llama.context_length", 0, &ok5);
+  m->theta = (float)num_or(f, "llama.rope.freq_base", 10000.0);
+  m->eps = (float)num_or(f, "llama.attention.layer_norm_rms_epsilon", 1e-5);
+  if (!(ok1 && ok2 && ok3 && ok4)) {
+    free_model(m);
+    SH_CHECK(false, SH_ERR_FORMAT, "missing required llama.* metadata");
+  }
+  if (m->n_head == 0 || m->n_kv == 0 || m->d % m->n_head || m->n_head % m->n_kv) {
+    free_model(m);
+    SH_CHECK(false, SH_ERR_FORMAT, "inconsistent head counts");
+  }
+  m->hd = m->d / m->n_head;
+  const uint32_t rope_dim = (uint32_t)num_or(f, "llama.rope.dimension_count", m->hd);
+  const GTensor* te = f.find("token_embd.weight");
+  const GTensor* on = f.find("output_norm.weight");
+  const GTensor* ow = f.find("output.weight");
+  int fail = SH_OK;
+#define FAIL(code, ...)                 \
+  do {                                  \
+    free_model(m);                      \
+    SH_CHECK(false, code, __VA_ARGS__); \
+  } while (0)
+  if (!te || !on) FAIL(SH_ERR_FORMAT, "missing token_embd / output_norm");
+  m->V = (uint32_t)num_or(f, "llama.vocab_size", (double)te->ne[1]);
+  if (rope_dim != m->hd) FAIL(SH_ERR_UNSUPPORTED, "partial RoPE (rope_dim %u != head_dim %u)", rope_dim, m->hd);
+  if (m->hd != 64 && m->hd != 128) FAIL(SH_ERR_UNSUPPORTED, "head_dim %u (64 or 128 supported)", m->hd);
+  if (te->ne[0] != m->d || te->ne[1] != m->V) FAIL(SH_ERR_FORMAT, "token_embd shape mismatch");
+  const uint32_t wtype = f.find("blk.0.attn_q.weight") ? f.find("blk.0.attn_q.weight")->type : 0;
+  if (wtype != GGML_Q4_K && wtype != GGML_Q8_0) FAIL(SH_ERR_UNSUPPORTED, "weight type %u (Q4_K / Q8_0 only)", wtype);
+  if (te->type != GGML_Q4_K && te->type != GGML_Q8_0 && te->type != GGML_F16 && te->type != GGML_F32)
+    FAIL(SH_ERR_UNSUPPORTED, "token_embd type %u", te->type);
+  // embedding (raw rows for the gather)
+  m->embd_type = (int)te->type;
+  m->embd_row_bytes = te->type == GGML_Q4_K ? m->d / 256 * 144
+                      : te->type == GGML_Q8_0 ? m->d / 32 * 34
+                      : te->type == GGML_F16  ? m->d * 2
+                                              : m->d * 4;
+  if (dalloc(&m->embd_raw, m->embd_row_bytes * m->V)) FAIL(SH_ERR_HIP, "%s", sh_last_error());
+  if (hipMemcpy(m->embd_raw, f.data + te->off, m->embd_row_bytes * m->V, hipMemcpyHostToDevice) != hipSuccess)
+    FAIL(SH_ERR_HIP, "embedding upload failed");
+  auto upload_f32 = [&](const GTensor* t, float** dst) -> int {
+    SH_CHECK(t && t->type == GGML_F32 && t->ne[0] == m->d, SH_ERR_FORMAT, "norm weight %s: f32 [%u] expected",
+             t ? t->name.c_str() : "?", m->d);
+    SH_HIP(hipMalloc(dst, m->d * 4));
+    SH_HIP(hipMemcpy(*dst, f.data + t->off, m->d * 4, hipMemcpyHostToDevice));
+    return SH_OK;
+  };
+  if ((fail = upload_f32(on, &m->out_norm))) FAIL(fail, "%s", sh_last_error());
+  // lm_head = output.unwrap_or(token_embd) (llama.rs:424)
+  const GTensor* lm = ow ? ow : te;
+  if (lm->type != GGML_Q4_K && lm->type != GGML_Q8_0) FAIL(SH_ERR_UNSUPPORTED, "lm_head type %u", lm->type);
+  if (lm->ne[0] != m->d || lm->ne[1] != m->V) FAIL(SH_ERR_FORMAT, "output.weight shape mismatch");
+  if ((fail = sh_repack_upload(e, (int)lm->type, f.data + lm->off, m->V, m->d, &m->lm_head)))
+    FAIL(fail, "%s", sh_last_error());
+  m->alg_weight_bytes += m->lm_head.alg_bytes;
+  const uint32_t dkv = m->hd * m->n_kv;
+  m->layers.resize(m->n_layer);
+  for (uint32_t l = 0; l < m->n_layer; ++l) {
+    auto get = [&](const char* s) { return f.find("blk." + std::to_string(l) + "." + s); };
+    const GTensor *an = get("attn_norm.weight"), *fn = get("ffn_norm.weight");
+    const GTensor *wq = get("attn_q.weight"), *wk = get("attn_k.weight"), *wv = get("attn_v.weight");
+    const GTensor *wo = get("attn_output.weight"), *wg = get("ffn_gate.weight"), *wu = get("ffn_up.weight");
+    const GTensor* wd = get("ffn_down.weight");
+    if (!an || !fn || !wq || !wk || !wv || !wo || !wg || !wu || !wd) FAIL(SH_ERR_FORMAT, "layer %u: missing tensor", l);
+    const GTensor* mats[7] = {wq, wk, wv, wo, wg, wu, wd};
+    for (auto* t : mats)
+      if (t->type != wtype) FAIL(SH_ERR_UNSUPPORTED, "mixed weight types in layer %u (%s)", l, t->name.c_str());
+    if (wq->ne[0] != m->d || wq->ne[1] != m->d || wk->ne[1] != dkv || wv->ne[1] != dkv || wo->ne[1] != m->d ||
+        wg->ne[1] != m->ff || wu->ne[1] != m->ff || wd->ne[0] != m->ff || wd->ne[1] != m->d)
+      FAIL(SH_ERR_FORMAT, "layer %u: weight shape mismatch", l);
+    Layer& L = m->layers[l];
+    if ((fail = upload_f32(an, &L.attn_norm)) || (fail = upload_f32(fn, &L.ffn_norm))) FAIL(fail, "%s", sh_last_error());
+    const uint8_t* parts[3] = {f.data + wq->off, f.data + wk->off, f.data + wv->off};
+    const uint32_t rows[3] = {m->d, dkv, dkv};
+    if ((fail = sh_repack_upload_cat(e, (int)wtype, parts, rows, 3, m->d, &L.wqkv))) FAIL(fail, "%s", sh_last_error());
+    if ((fail = sh_repack_upload(e, (int)wtype, f.data + wo->off, m->d, m->d, &L.wo))) FAIL(fail, "%s", sh_last_error());
+    if ((fail = sh_repack_upload_gu(e, (int)wtype, f.data + wg->off, f.data + wu->off, m->ff, m->d, &L.wgu)))
+      FAIL(fail, "%s", sh_last_error());
+    if ((fail = sh_repack_upload(e, (int)wtype, f.data + wd->off, m->d, m->ff, &L.wdown)))
+      FAIL(fail, "%s", sh_last_error());
+    m->alg_weight_bytes += L.wqkv.alg_bytes + L.wo.alg_bytes + L.wgu.alg_bytes + L.wdown.alg_bytes + 8.0 * m->d;
+  }
+  m->alg_weight_bytes += 4.0 * m->d;
+  // workspace for up to 8 columns per chunk
+  Workspace& w = m->ws;
+  w.max_cols = 8;
+  const uint32_t kmax = std::max(m->d, m->ff);
+  const size_t bx_elems = (size_t)kmax / 32 * 64 * 8;
+  const size_t xs_elems = (size_t)(kmax + 255) / 256 * 64 * 8;
+  const size_t part_floats = (size_t)m->n_kv * 64 * 64 * (m->hd + 2);  // grown on demand in forward_dev
+  if (dalloc(&w.resid, (size_t)8 * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
+      dalloc(&w.q, (size_t)8 * m->d) || dalloc(&w.attn, (size_t)8 * m->d) || dalloc(&w.h, (size_t)8 * m->ff) ||
+      dalloc(&w.logits, (size_t)8 * m->V) || dalloc(&w.fa_part, part_floats) || dalloc(&w.tokens, 128) ||
+      dalloc(&w.amax, 64))
+    FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
+  w.fa_part_floats = part_floats;
+  if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess)
+    FAIL(SH_ERR_HIP, "workspace clear failed");
+  if ((fail = ensure_rope(m, std::max<uint32_t>(m->n_ctx, 1024)))) FAIL(fail, "%s", sh_last_error());
+  if (hipDeviceSynchronize() != hipSuccess) FAIL(SH_ERR_HIP, "model upload failed");
+#undef FAIL
+  *out = m;
+  return SH_OK;
+}
+
+extern "C" int sh_model_load_gguf_memory(sh_engine* e, const void* data, uint64_t size, sh_model** out) {
+  return load_model(e, (const uint8_t*)data, size, out);
+}
+
+extern "C" int sh_model_load_gguf(sh_engine* e, const char* path, sh_model** out) {
+  SH_CHECK(path, SH_ERR_ARG, "path is NULL");
+  int fd = open(path, O_RDONLY);
+  SH_CHECK(fd >= 0, SH_ERR_ARG, "cannot open %s", path);
+  struct stat st;
+  if (fstat(fd, &st) != 0) { close(fd); SH_CHECK(false, SH_ERR_ARG, "cannot stat %s", path); }
+  void* p = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  SH_CHECK(p != MAP_FAILED, SH_ERR_ARG, "mmap %s failed", path);
+  int rc = load_model(e, (const uint8_t*)p, (uint64_t)st.st_size, out);
+  munmap(p, (size_t)st.st_size);
+  return rc;
+}
+
+extern "C" void sh_model_destroy(sh_model* m) {
+  if (!m) return;
+  (void)hipStreamSynchronize(m->e->stream);
+  free_model(m);
+}
+
+extern "C" int sh_model_info(const sh_model* m, sh_model_dims* o) {
+  SH_CHECK(m && o, SH_ERR_ARG, "sh_model_info: NULL argument");
+  o->n_layer = m->n_layer; o->n_embd = m->d; o->n_head = m->n_head; o->n_head_kv = m->n_kv;
+  o->head_dim = m->hd; o->n_ff = m->ff; o->n_vocab = m->V; o->n_ctx_train = m->n_ctx;
+  o->rms_eps = m->eps; o->rope_freq_base = m->theta;
+  o->weight_type = m->layers.empty() ? -1 : m->layers[0].wo.type;
+  o->weight_bytes = m->alg_weight_bytes;
+  return SH_OK;
+}
+
+// ------------------------------------------------------------------ KV
+
+extern "C" int sh_kv_create(sh_engine* e, const sh_model* m, uint32_t max_seq, sh_kv** out) {
+  SH_CHECK(e && m && out, SH_ERR_ARG, "sh_kv_create: NULL argument");
+  SH_CHECK(max_seq >= 1 && max_seq <= (1u << 22), SH_ERR_ARG, "max_seq_len %u out of range", max_seq);
+  sh_kv* kv = new sh_kv();
+  kv->e = e;
+  kv->n_layer = m->n_layer; kv->n_kv = m->n_kv; kv->hd = m->hd;
+  kv->max_seq = (max_seq + 31) / 32 * 32;
+  const size_t n = (size_t)kv->n_layer * kv->n_kv * kv->max_seq * kv->hd;
+  if (hipMalloc(&kv->k, n * 2) != hipSuccess || hipMalloc(&kv->v, n * 2) != hipSuccess) {
+    (void)hipFree(kv->k);
+    delete kv;
+    SH_CHECK(false, SH_ERR_HIP, "KV allocation of %zu bytes failed", n * 4);
+  }
+  // Zero-fill so never-written slots read as finite zeros.
+  SH_HIP(hipMemset(kv->k, 0, n * 2));
+  SH_HIP(hipMemset(kv->v, 0, n * 2));
+  *out = kv;
+  return SH_OK;
+}
+
+extern "C" void sh_kv_destroy(sh_kv* kv) {
+  if (!kv) return;
+  (void)hipStreamSynchronize(kv->e->stream);
+  (void)hipFree(kv->k);
+  (void)hipFree(kv->v);
+  delete kv;
+}
+
+extern "C" int sh_kv_position(const sh_kv* kv, uint32_t* pos) {
+  SH_CHECK(kv && pos, SH_ERR_ARG, "sh_kv_position: NULL argument");
+  *pos = kv->pos;
+  return SH_OK;
+}
+
+extern "C" int sh_kv_truncate(sh_kv* kv, uint32_t new_pos) {
+  SH_CHECK(kv, SH_ERR_ARG, "kv is NULL");
+  kv->pos = std::min(new_pos, kv->pos);
+  kv->pending.clear();
+  return SH_OK;
+}
+
+extern "C" int sh_kv_set_position(sh_kv* kv, uint32_t pos) {
+  SH_CHECK(kv, SH_ERR_ARG, "kv is NULL");
+  SH_CHECK(pos <= kv->max_seq, SH_ERR_CAPACITY, "position %u beyond capacity %u", pos, kv->max_seq);
+  kv->pos = pos;
+  kv->pending.clear();
+  return SH_OK;
+}
+
+static inline uint32_t v_slot_host(uint32_t kappa) { return 8u * ((kappa & 15u) >> 2) + 4u * (kappa >> 4) + (kappa & 3u); }
+
+static int kv_xfer(sh_kv* kv, uint32_t layer, int is_v, uint32_t n_pos, uint16_t* host, bool to_host) {
+  SH_CHECK(kv && host, SH_ERR_ARG, "sh_kv_*_layer: NULL argument");
+  SH_CHECK(layer < kv->n_layer && n_pos <= kv->max_seq, SH_ERR_ARG, "layer %u / n_pos %u out of range", layer, n_pos);
+  const size_t per = (size_t)kv->n_kv * kv->max_seq * kv->hd;
+  std::vector<uint16_t> buf(per);
+  uint16_t* dev = (is_v ? kv->v : kv->k) + per * layer;
+  SH_HIP(hipStreamSynchronize(kv->e->stream));
+  if (!to_host) SH_HIP(hipMemcpy(buf.data(), dev, per * 2, hipMemcpyDeviceToHost));
+  else SH_HIP(hipMemcpy(buf.data(), dev, per * 2, hipMemcpyDeviceToHost));
+  for (uint32_t h = 0; h < kv->n_kv; ++h)
+    for (uint32_t t = 0; t < n_pos; ++t)
+      for (uint32_t d = 0; d < kv->hd; ++d) {
+        size_t di = is_v ? (((size_t)h * (kv->max_seq / 32) + t / 32) * kv->hd + d) * 32 + v_slot_host(t & 31)
+                         : ((size_t)h * kv->max_seq + t) * kv->hd + d;
+        size_t hi = ((size_t)t * kv->n_kv + h) * kv->hd + d;
+        if (to_host) host[hi] = buf[di];
+        else buf[di] = host[hi];
+      }
+  if (!to_host) SH_HIP(hipMemcpy(dev, buf.data(), per * 2, hipMemcpyHostToDevice));
+  return SH_OK;
+}
+
+extern "C" int sh_kv_read_layer(sh_kv* kv, uint32_t layer, int is_v, uint32_t n_pos, uint16_t* out) {
+  return kv_xfer(kv, layer, is_v, n_pos, out, true);
+}
+extern "C" int sh_kv_write_layer(sh_kv* kv, uint32_t layer, int is_v, uint32_t n_pos, const uint16_t* in) {
+  return kv_xfer(kv, layer, is_v, n_pos, const_cast<uint16_t*>(in), false);
+}
+
+extern "C" int sh_kv_compact(sh_kv* kv, uint32_t base, const uint32_t* src, uint32_t n) {
+  SH_CHECK(kv && (src || n == 0), SH_ERR_ARG, "sh_kv_compact: NULL argument");
+  SH_CHECK(base + n <= kv->max_seq, SH_ERR_CAPACITY, "compaction beyond capacity");
+  for (uint32_t i = 0; i < n; ++i)
+    SH_CHECK(base + src[i] < kv->max_seq, SH_ERR_ARG, "compaction source %u out of range", src[i]);
+  if (n) {
+    sh_engine* e = kv->e;
+    uint32_t* d = nullptr;
+    SH_HIP(hipMallocAsync((void**)&d, n * 4, e->stream));
+    SH_HIP(hipMemcpyAsync(d, src, n * 4, hipMemcpyHostToDevice, e->stream));
+    int rc = sh_kv_compact_launch(e, kv, base, d, n);
+    if (rc) return rc;
+    SH_HIP(hipFreeAsync(d, e->stream));
+    SH_HIP(hipStreamSynchronize(e->stream));
+  }
+  kv->pos = base + n;
+  kv->pending.clear();
+  return SH_OK;
+}
+
+// ------------------------------------------------------------------ forward
+
+// One chunk of nc <= 8 columns whose token ids are already on the device at
+// m->ws.tokens[tok_off ..]. Writes K/V at slots slot0 .. slot0+nc, runs every
+// layer, and (if want_logits) the final norm + lm_head into ws.logits [nc][V].
+static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint32_t nc, uint32_t slot0,
+                         const int32_t* colpos, const uint64_t* colmask, uint32_t mask_base, bool want_logits) {
+  sh_engine* e = m->e;
+  Workspace& w = m->ws;
+  int rc;
+  if ((rc = sh_embed_launch(e, m, dev_tokens, nc, w.resid))) return rc;
+  const uint32_t dkv = m->hd * m->n_kv;
+  EpiArgs qkv;
+  qkv.out = w.q; qkv.ldo = m->d;
+  qkv.Dq = m->d; qkv.Dkv = dkv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.max_seq = kv->max_seq; qkv.slot0 = slot0;
+  qkv.rope = m->rope; qkv.kc = kv->k; qkv.vc = kv->v;
+  for (uint32_t j = 0; j < nc; ++j) qkv.colpos[j] = colpos[j];
+  FaArgs fa;
+  fa.N = nc; fa.kvlen = slot0 + nc; fa.mask_base = mask_base;
+  for (uint32_t j = 0; j < nc; ++j) fa.colmask[j] = colmask[j];
+  EpiArgs add;
+  add.out = w.resid; add.ldo = m->d;
+  EpiArgs sw;
+  sw.out = w.h; sw.ldo = m->ff;
+  for (uint32_t l = 0; l < m->n_layer; ++l) {
+    const Layer& L = m->layers[l];
+    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.attn_norm, m->eps, w.bx, w.xs, nullptr))) return rc;
+    qkv.layer = l;
+    if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
+    fa.layer = l;
+    if ((rc = sh_fa_launch(e, m, kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs))) return rc;
+    if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_ADD, add, "gemv_o"))) return rc;
+    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.ffn_norm, m->eps, w.bx, w.xs, nullptr))) return rc;
+    if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
+    if ((rc = sh_prep_launch(e, w.h, m->ff, nc, nullptr, 0.f, w.bx, w.xs, nullptr))) return rc;
+    if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_ADD, add, "gemv_down"))) return rc;
+  }
+  if (want_logits) {
+    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, m->out_norm, m->eps, w.bx, w.xs, nullptr))) return rc;
+    EpiArgs st;
+    st.out = w.logits; st.ldo = m->V;
+    if ((rc = sh_gemv_launch(e, m->lm_head, w.bx, w.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
+  }
+  return SH_OK;
+}
+
+// Column geometry of a forward call: RoPE position, visibility mask and mask
+// base per chunk. Causal chains: each chunk's columns see the cached prefix and
+// earlier columns of the chunk (mask relative to the chunk start). Trees
+// (L <= 64): positions = pos + depth, mask = ancestor-or-self relative to pos.
+struct Plan {
+  std::vector<int32_t> colpos;
+  std::vector<uint64_t> mask;
+  bool tree = false;
+};
+
+static int make_plan(uint32_t L, uint32_t pos, const int32_t* parents, Plan* p) {
+  p->colpos.resize(L);
+  p->mask.resize(L);
+  p->tree = parents != nullptr;
+  if (!parents) {
+    for (uint32_t i = 0; i < L; ++i) {
+      p->colpos[i] = (int32_t)(pos + i);
+      const uint32_t j = i % 8;
+      p->mask[i] = (j == 63) ? ~0ull : ((2ull << j) - 1ull);
+    }
+    return SH_OK;
+  }
+  SH_CHECK(L <= 64, SH_ERR_UNSUPPORTED, "tree verify supports at most 64 nodes (got %u)", L);
+  for (uint32_t i = 0; i < L; ++i) {
+    SH_CHECK(parents[i] < (int32_t)i, SH_ERR_ARG, "tree parent[%u]=%d must precede the node", i, parents[i]);
+    uint64_t mk = 1ull << i;
+    uint32_t depth = 0;
+    if (parents[i] >= 0) {
+      mk |= p->mask[parents[i]];
+      depth = (uint32_t)(p->colpos[parents[i]] - (int32_t)pos) + 1;
+    }
+    p->mask[i] = mk;
+    p->colpos[i] = (int32_t)(pos + depth);
+  }
+  return SH_OK;
+}
+
+// Runs the whole forward for L columns whose ids are at dev_tokens. If
+// logits_dst != null, copies logits of the selected columns there (device).
+static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint32_t L, uint32_t pos,
+                       const int32_t* parents, int logits_mode, float* logits_dev_out, float* resid_host,
+                       float* logits_host) {
+  sh_engine* e = m->e;
+  SH_CHECK(L >= 1, SH_ERR_ARG, "empty prompt");
+  SH_CHECK(kv->pos == pos, SH_ERR_STATE, "cache.position %u doesn't match caller-supplied position_offset %u",
+           kv->pos, pos);
+  SH_CHECK(kv->n_layer == m->n_layer && kv->n_kv == m->n_kv && kv->hd == m->hd, SH_ERR_ARG,
+           "KV cache dims do not match the model");
+  SH_CHECK((uint64_t)pos + L <= kv->max_seq, SH_ERR_CAPACITY, "positions [%u, %u) exceed KV capacity %u", pos,
+           pos + L, kv->max_seq);
+  Plan plan;
+  int rc = make_plan(L, pos, parents, &plan);
+  if (rc) return rc;
+  uint32_t maxpos = 0;
+  for (auto p : plan.colpos) maxpos = std::max<uint32_t>(maxpos, (uint32_t)p);
+  if ((rc = ensure_rope(m, maxpos + 1))) return rc;
+  const uint32_t needed_splits = (pos + L + SH_FA_KEYS_PER_SPLIT - 1) / SH_FA_KEYS_PER_SPLIT;
+  const size_t need = (size_t)m->n_kv * needed_splits * 64 * (m->hd + 2);
+  if (need > m->ws.fa_part_floats) {
+    SH_HIP(hipStreamSynchronize(e->stream));
+    SH_HIP(hipFree(m->ws.fa_part));
+    m->ws.fa_part = nullptr;
+    SH_HIP(hipMalloc(&m->ws.fa_part, need * 4));
+    m->ws.fa_part_floats = need;
+  }
+  for (uint32_t c0 = 0; c0 < L; c0 += 8) {
+    const uint32_t nc = std::min<uint32_t>(8, L - c0);
+    const bool last = c0 + nc == L;
+    const bool want = logits_mode == 2 || (logits_mode == 1 && last);
+    std::vector<uint64_t> mk(nc);
+    uint32_t mbase;
+    if (plan.tree) {
+      mbase = pos;
+      for (uint32_t j = 0; j < nc; ++j) mk[j] = plan.mask[c0 + j];
+    } else {
+      mbase = pos + c0;
+      for (uint32_t j = 0; j < nc; ++j) mk[j] = plan.mask[c0 + j];
+    }
+    if ((rc = forward_chunk(m, kv, dev_tokens + c0, nc, pos + c0, plan.colpos.data() + c0, mk.data(), mbase, want)))
+      return rc;
+    if (resid_host)
+      SH_HIP(hipMemcpyAsync(resid_host + (size_t)c0 * m->d, m->ws.resid, (size_t)nc * m->d * 4,
+                            hipMemcpyDeviceToHost, e->stream));
+    if (want) {
+      const uint32_t j0 = logits_mode == 1 ? nc - 1 : 0;
+      const uint32_t ncopy = nc - j0;
+      const uint32_t dst_col = logits_mode == 1 ? 0 : c0;
+      if (logits_dev_out)
+        SH_HIP(hipMemcpyAsync(logits_dev_out + (size_t)dst_col * m->V, m->ws.logits + (size_t)j0 * m->V,
+                              (size_t)ncopy * m->V * 4, hipMemcpyDeviceToDevice, e->stream));
+      if (logits_host)
+        SH_HIP(hipMemcpyAsync(logits_host + (size_t)dst_col * m->V, m->ws.logits + (size_t)j0 * m->V,
+                              (size_t)ncopy * m->V * 4, hipMemcpyDeviceToHost, e->stream));
+    }
+    if (resid_host || logits_host) SH_HIP(hipStreamSynchronize(e->stream));
+  }
+  kv->pos = pos + L;
+  return SH_OK;
+}
+
+static int upload_tokens(sh_model* m, const uint32_t* tokens, uint32_t L, uint32_t** dev) {
+  uint32_t* d = nullptr;
+  SH_CHECK(tokens, SH_ERR_ARG, "tokens is NULL");
+  for (uint32_t i = 0; i < L; ++i)
+    SH_CHECK(tokens[i] < m->V, SH_ERR_ARG, "token id %u out of range (vocab %u)", tokens[i], m->V);
+  SH_HIP(hipMalloc(&d, (size_t)L * 4));
+  SH_HIP(hipMemcpyAsync(d, tokens, (size_t)L * 4, hipMemcpyHostToDevice, m->e->stream));
+  *dev = d;
+  return SH_OK;
+}
+
+extern "C" int sh_forward_full(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L,
+                               uint32_t pos, const int32_t* parents, int logits_mode, float* logits_out,
+                               float* residual_out) {
+  SH_CHECK(e && m && kv, SH_ERR_ARG, "sh_forward_full: NULL handle");
+  SH_CHECK(logits_mode >= 0 && logits_mode <= 2, SH_ERR_ARG, "logits_mode %d", logits_mode);
+  SH_CHECK(L >= 1, SH_ERR_ARG, "empty prompt");
+  uint32_t* dt = nullptr;
+  int rc = upload_tokens(m, tokens, L, &dt);
+  if (rc) return rc;
+  rc = forward_dev(m, kv, dt, L, pos, parents, logits_mode, nullptr, residual_out,
+                   logits_mode ? logits_out : nullptr);
+  hipError_t se = hipStreamSynchronize(e->stream);
+  (void)hipFree(dt);
+  if (rc) return rc;
+  SH_CHECK(se == hipSuccess, SH_ERR_HIP, "forward: %s", hipGetErrorString(se));
+  kv->pending.clear();
+  return sh_prof_flush(e);
+}
+
+extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L,
+                                uint32_t pos, uint32_t* sampled_out) {
+  SH_CHECK(e && m && kv && sampled_out, SH_ERR_ARG, "sh_verify_greedy: NULL argument");
+  SH_CHECK(L >= 1 && L <= 64, SH_ERR_ARG, "verify length %u outside [1, 64]", L);
+  uint32_t* dt = nullptr;
+  int rc = upload_tokens(m, tokens, L, &dt);
+  if (rc) return rc;
+  float* lg = nullptr;
+  SH_HIP(hipMallocAsync((void**)&lg, (size_t)L * m->V * 4, e->stream));
+  uint32_t* ids = nullptr;
+  SH_HIP(hipMallocAsync((void**)&ids, 64 * 4, e->stream));
+  rc = forward_dev(m, kv, dt, L, pos, nullptr, 2, lg, nullptr, nullptr);
+  if (!rc) rc = sh_argmax_launch(e, lg, m->V, L, m->ws.amax, ids);
+  if (!rc) {
+    hipError_t ce = hipMemcpyAsync(sampled_out, ids, (size_t)L * 4, hipMemcpyDeviceToHost, e->stream);
+    if (ce != hipSuccess) { sh_set_error("verify readback: %s", hipGetErrorString(ce)); rc = SH_ERR_HIP; }
+  }
+  hipError_t se = hipStreamSynchronize(e->stream);
+  (void)hipFree(dt);
+  (void)hipFreeAsync(lg, e->stream);
+  (void)hipFreeAsync(ids, e->stream);
+  if (rc) return rc;
+  SH_CHECK(se == hipSuccess, SH_ERR_HIP, "verify: %s", hipGetErrorString(se));
+  kv->pending.clear();
+  return sh_prof_flush(e);
+}
+
+// ------------------------------------------------------------------ spec step
+
+struct SpecBufs {
+  uint32_t* tok = nullptr;     // [64]: pending..., last, d_1..d_n
+  uint32_t* samp = nullptr;    // [16]
+  float* dlogits = nullptr;    // draft logits [8][V] (REJECTION)
+  float* tlogits = nullptr;    // target logits [9][V]
+  uint32_t* pinned = nullptr;  // host staging [128]
+  uint32_t vcap = 0;
+};
+static thread_local SpecBufs g_spec;
+
+static int spec_bufs(uint32_t V) {
+  if (g_spec.tok && g_spec.vcap >= V) return SH_OK;
+  if (g_spec.tok) {
+    (void)hipFree(g_spec.tok); (void)hipFree(g_spec.samp); (void)hipFree(g_spec.dlogits);
+    (void)hipFree(g_spec.tlogits); (void)hipHostFree(g_spec.pinned);
+  }
+  SH_HIP(hipMalloc(&g_spec.tok, 64 * 4));
+  SH_HIP(hipMalloc(&g_spec.samp, 16 * 4));
+  SH_HIP(hipMalloc(&g_spec.dlogits, (size_t)8 * V * 4));
+  SH_HIP(hipMalloc(&g_spec.tlogits, (size_t)9 * V * 4));
+  SH_HIP(hipHostMalloc((void**)&g_spec.pinned, 128 * 4, hipHostMallocDefault));
+  g_spec.vcap = V;
+  return SH_OK;
+}
+
+int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts,
+                     uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter,
+                     const float* uniforms_dev, uint32_t* acc_len, uint32_t* next_tok);
+
+extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t last_token,
+                            uint32_t n_max, sh_sampling* s, uint32_t* emitted_out, uint32_t* n_emitted,
+                            uint32_t* drafts_out) {
+  SH_CHECK(e && tm && dm && tkv && dkv && emitted_out && n_emitted, SH_ERR_ARG, "sh_spec_step: NULL argument");
+  SH_CHECK(tm->V == dm->V, SH_ERR_ARG, "draft vocab %u != target vocab %u", dm->V, tm->V);
+  SH_CHECK(last_token < tm->V, SH_ERR_ARG, "last_token %u out of range", last_token);
+  const uint32_t mode = s ? s->mode : SH_SAMPLE_GREEDY;
+  SH_CHECK(mode <= SH_SAMPLE_REJECTION, SH_ERR_ARG, "sampling mode %u", mode);
+  SH_CHECK(mode == SH_SAMPLE_GREEDY || (s && s->temperature > 0.f), SH_ERR_ARG,
+           "stochastic modes need temperature > 0");
+  const uint32_t n = std::min<uint32_t>(std::max<uint32_t>(n_max, 1), 8);  // mod.rs:2121
+  const uint32_t P = tkv->pos;
+  const uint32_t np = (uint32_t)dkv->pending.size();
+  SH_CHECK(dkv->pos + np == P, SH_ERR_STATE, "draft cache position %u + %u pending != target position %u", dkv->pos,
+           np, P);
+  SH_CHECK((uint64_t)P + n + 1 <= tkv->max_seq && (uint64_t)P + n + 1 <= dkv->max_seq, SH_ERR_CAPACITY,
+           "spec lookahead exceeds KV capacity (run.rs:270-283)");
+  int rc = spec_bufs(tm->V);
+  if (rc) return rc;
+  uint32_t* hp = g_spec.pinned;
+  for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
+  hp[np] = last_token;
+  SH_HIP(hipMemcpyAsync(g_spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
+  // 1. draft n tokens greedily, ids stay on the device (tok[np+1+i] = d_{i+1}).
+  const bool rej = mode == SH_SAMPLE_REJECTION;
+  rc = forward_dev(dm, dkv, g_spec.tok, np + 1, dkv->pos, nullptr, 1, rej ? g_spec.dlogits : nullptr, nullptr,
+                   nullptr);
+  if (rc) return rc;
+  if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)(((np + 1) - 1) % 8) * dm->V, dm->V, 1, dm->ws.amax,
+                             g_spec.tok + np + 1)))
+    return rc;
+  for (uint32_t i = 1; i < n; ++i) {
+    rc = forward_dev(dm, dkv, g_spec.tok + np + i, 1, dkv->pos, nullptr, 1,
+                     rej ? g_spec.dlogits + (size_t)i * dm->V : nullptr, nullptr, nullptr);
+    if (rc) return rc;
+    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, g_spec.tok + np + 1 + i))) return rc;
+  }
+  // 2. verify [last, d_1..d_n] with all-position logits.
+  rc = forward_dev(tm, tkv, g_spec.tok + np, n + 1, P, nullptr, 2, g_spec.tlogits, nullptr, nullptr);
+  if (rc) return rc;
+  // 3. per-column decision on the device.
+  uint32_t* acc_dev = g_spec.samp + 9;
+  uint32_t* next_dev = g_spec.samp + 10;
+  if (mode == SH_SAMPLE_GREEDY) {
+    if ((rc = sh_argmax_launch(e, g_spec.tlogits, tm->V, n + 1, tm->ws.amax, g_spec.samp))) return rc;
+  } else {
+    sh_sampling ss = *s;
+    float* udev = nullptr;
+    if (s->uniforms) {
+      SH_HIP(hipMallocAsync((void**)&udev, (size_t)(n + 1) * 2 * 4, e->stream));
+      SH_HIP(hipMemcpyAsync(udev, s->uniforms, (size_t)(n + 1) * 2 * 4, hipMemcpyHostToDevice, e->stream));
+    }
+    rc = sh_accept_launch(e, g_spec.tlogits, rej ? g_spec.dlogits : nullptr, g_spec.tok + np + 1, 1, n, tm->V, &ss,
+                          udev ? 0 : s->counter, udev, acc_dev, next_dev);
+    if (udev) (void)hipFreeAsync(udev, e->stream);
+    if (rc) return rc;
+    if (!udev) s->counter += 2ull * (n + 1);
+  }
+  SH_HIP(hipMemcpyAsync(hp, g_spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
+  SH_HIP(hipMemcpyAsync(hp + 16, g_spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+  SH_HIP(hipStreamSynchronize(e->stream));
+  uint32_t drafts[8];
+  for (uint32_t i = 0; i < n; ++i) drafts[i] = hp[i];
+  uint32_t ne = 0;
+  if (mode == SH_SAMPLE_GREEDY) {
+    // host accept (inference/mod.rs:2168-2179)
+    for (uint32_t i = 0; i <= n; ++i) {
+      const uint32_t t = hp[16 + i];
+      emitted_out[ne++] = t;
+      if (i < n && t == drafts[i]) continue;
+      break;
+    }
+  } else {
+    const uint32_t acc = hp[16 + 9], nxt = hp[16 + 10];
+    for (uint32_t i = 0; i < acc; ++i) emitted_out[ne++] = drafts[i];
+    emitted_out[ne++] = nxt;
+  }
+  const uint32_t acc = ne - 1;
+  tkv->pos = P + acc + 1;                               // truncate (mod.rs:2269-2270)
+  dkv->pos = std::min(dkv->pos, P + acc + 1);
+  dkv->pending.clear();
+  if (acc == n) dkv->pending.push_back(drafts[n - 1]);  // d_n was never fed to the draft
+  *n_emitted = ne;
+  if (drafts_out) std::memcpy(drafts_out, drafts, n * 4);
+  return sh_prof_flush(e);
+}
+
+// ------------------------------------------------------------------ kernel level
+
+extern "C" int sh_qtensor_upload(sh_engine* e, int type, const void* host, uint32_t M, uint32_t K, sh_qtensor** out) {
+  SH_CHECK(e && host && out, SH_ERR_ARG, "sh_qtensor_upload: NULL argument");
+  SH_CHECK(M >= 1 && K >= 1, SH_ERR_ARG, "empty matrix");
+  sh_qtensor* t = new sh_qtensor();
+  t->e = e;
+  int rc = sh_repack_upload(e, type, (const uint8_t*)host, M, K, &t->m);
+  if (rc) { delete t; return rc; }
+  *out = t;
+  return SH_OK;
+}
+
+extern "C" void sh_qtensor_destroy(sh_qtensor* t) {
+  if (!t) return;
+  (void)hipStreamSynchronize(t->e->stream);
+  sh_qmat_free(&t->m);
+  delete t;
+}
+
+extern "C" int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_t N, float* y_dev,
+                             int accumulate) {
+  SH_CHECK(e && w && x_dev && y_dev, SH_ERR_ARG, "sh_gemv_quant: NULL argument");
+  SH_CHECK(N >= 1, SH_ERR_ARG, "N must be >= 1");
+  const uint32_t K = w->m.K;
+  uint16_t *bx = nullptr, *xs = nullptr;
+  const size_t bx_elems = (size_t)K / 32 * 64 * 8, xs_elems = (size_t)(K + 255) / 256 * 64 * 8;
+  SH_HIP(hipMallocAsync((void**)&bx, bx_elems * 2, e->stream));
+  SH_HIP(hipMallocAsync((void**)&xs, xs_elems * 2, e->stream));
+  SH_HIP(hipMemsetAsync(xs, 0, xs_elems * 2, e->stream));
+  int rc = SH_OK;
+  for (uint32_t c0 = 0; c0 < N && !rc; c0 += 8) {
+    const uint32_t nc = std::min<uint32_t>(8, N - c0);
+    rc = sh_prep_launch(e, x_dev + (size_t)c0 * K, K, nc, nullptr, 0.f, bx, xs, nullptr);
+    if (rc) break;
+    EpiArgs ea;
+    ea.out = y_dev + (size_t)c0 * w->m.M;
+    ea.ldo = w->m.M;
+    rc = sh_gemv_launch(e, w->m, bx, xs, nc, accumulate ? EPI_ADD : EPI_STORE, ea, "gemv");
+  }
+  (void)hipFreeAsync(bx, e->stream);
+  (void)hipFreeAsync(xs, e->stream);
+  if (rc) return rc;
+  SH_HIP(hipStreamSynchronize(e->stream));
+  return sh_prof_flush(e);
+}

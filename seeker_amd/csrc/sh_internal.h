@@ -1,0 +1,174 @@
+// Internal declarations shared by the HIP translation units of libseeker_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/seeker_hip.h"
+
+// ---------------------------------------------------------------- errors
+void sh_set_error(const char* fmt, ...);
+
+#define SH_HIP(call)                                                              \
+  do {                                                                            \
+    hipError_t e_ = (call);                                                       \
+    if (e_ != hipSuccess) {                                                       \
+      sh_set_error("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, \
+                   __LINE__);                                                     \
+      return SH_ERR_HIP;                                                          \
+    }                                                                             \
+  } while (0)
+
+#define SH_CHECK(cond, code, ...)   \
+  do {                              \
+    if (!(cond)) {                  \
+      sh_set_error(__VA_ARGS__);    \
+      return (code);                \
+    }                               \
+  } while (0)
+
+// GGML type ids used here (crates/seeker-core/src/gguf/types.rs).
+enum : int { GGML_F32 = 0, GGML_F16 = 1, GGML_Q8_0 = 8, GGML_Q4_K = 12 };
+
+// ------------------------------------------------------------ constants
+// Activation operand ("B") layout for the MFMA GEMV: for each 8-column chunk,
+// [K/32 blocks][64 lanes][8 f16]; lane = 16*g + c, g = (k%32)/8, c < 8 holds the
+// high f16 part of column c, c >= 8 the low part (x - f32(hi)) of column c-8.
+// XS (Q4_K minimum term): [K/256][16][8] f16, per 32-element sub-block sums
+// of each column (hi in c, lo in c+8).
+constexpr int SH_TILE_ROWS = 16;
+constexpr int SH_Q4K_TILE_BYTES = 2304;  // 16 rows x 144 B, repacked
+constexpr int SH_Q8_TILE_BYTES = 544;    // 16 rows x 34 B, repacked
+constexpr int SH_MAX_COLS = 64;          // columns per forward chunk
+constexpr int SH_FA_KEYS_PER_SPLIT = 256;
+
+// -------------------------------------------------------------- structs
+struct KStat {
+  uint64_t launches = 0;
+  double ms = 0.0;
+  double bytes = 0.0;
+};
+
+struct sh_engine {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool profiling = false;
+  std::map<std::string, KStat> stats;
+  struct Pending {
+    std::string name;
+    double bytes;
+    hipEvent_t a, b;
+  };
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> event_pool;
+};
+
+// A weight matrix on the device, repacked into MFMA tiles.
+struct QMat {
+  int type = -1;
+  uint32_t M = 0, K = 0;  // logical rows, contracting dim
+  uint32_t tiles = 0;     // ceil(M / 16)
+  uint8_t* d = nullptr;
+  size_t bytes = 0;       // packed bytes
+  double alg_bytes = 0;   // GGUF bytes of the logical matrix
+};
+
+struct sh_qtensor {
+  sh_engine* e;
+  QMat m;
+};
+
+struct Layer {
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  QMat wqkv;  // rows [q | k | v]
+  QMat wo;
+  QMat wgu;   // tiles interleaved: gate tile t at 2t, up tile t at 2t+1
+  QMat wdown;
+};
+
+struct Workspace {
+  uint32_t max_cols = 0;
+  float* resid = nullptr;     // [cols][d]
+  uint16_t* bx = nullptr;     // B operand buffer sized for max(K) x max_cols
+  uint16_t* xs = nullptr;     // XS buffer
+  float* q = nullptr;         // [cols][d] roped queries
+  float* attn = nullptr;      // [cols][d]
+  float* h = nullptr;         // [cols][ff]
+  float* logits = nullptr;    // [cols][V]
+  float* fa_part = nullptr;   // flash-attn split partials
+  uint32_t* tokens = nullptr; // [cols + 16] device token ids
+  unsigned long long* amax = nullptr;  // [cols] packed argmax keys
+  size_t fa_part_floats = 0;
+};
+
+struct sh_model {
+  sh_engine* e = nullptr;
+  uint32_t n_layer = 0, d = 0, n_head = 0, n_kv = 0, hd = 0, ff = 0, V = 0, n_ctx = 0;
+  float eps = 1e-5f, theta = 10000.f;
+  int embd_type = -1;
+  uint8_t* embd_raw = nullptr;  // token_embd in GGUF row layout (gather)
+  size_t embd_row_bytes = 0;
+  QMat lm_head;
+  float* out_norm = nullptr;
+  std::vector<Layer> layers;
+  float2* rope = nullptr;       // [rope_max][hd/2] (cos, sin)
+  uint32_t rope_max = 0;
+  Workspace ws;
+  double alg_weight_bytes = 0;  // bytes of every matrix a full-logits forward reads
+};
+
+struct sh_kv {
+  sh_engine* e = nullptr;
+  uint32_t n_layer = 0, n_kv = 0, hd = 0, max_seq = 0, pos = 0;
+  uint16_t* k = nullptr;  // [layer][n_kv][max_seq][hd] f16
+  uint16_t* v = nullptr;  // [layer][n_kv][max_seq/32][hd][32] f16, slot-permuted
+  std::vector<uint32_t> pending;  // committed tokens not yet in this cache
+};
+
+// ------------------------------------------------------------ launchers
+// All launchers enqueue on e->stream and return 0 or an SH_ERR code.
+int sh_repack_upload(sh_engine* e, int type, const uint8_t* host, uint32_t M, uint32_t K, QMat* out);
+int sh_repack_upload_gu(sh_engine* e, int type, const uint8_t* gate, const uint8_t* up, uint32_t M,
+                        uint32_t K, QMat* out);
+int sh_repack_upload_cat(sh_engine* e, int type, const uint8_t* const* parts, const uint32_t* rows,
+                         int nparts, uint32_t K, QMat* out);
+void sh_qmat_free(QMat* m);
+
+enum EpiKind { EPI_STORE = 0, EPI_ADD = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+struct EpiArgs {
+  float* out = nullptr;   // STORE/ADD: [N][ldo]; QKV: roped q [N][Dq]; SWIGLU: h [N][ldo]
+  uint32_t ldo = 0;
+  // QKV
+  uint32_t Dq = 0, Dkv = 0, hd = 0, n_kv = 0, max_seq = 0, slot0 = 0, layer = 0;
+  const float2* rope = nullptr;
+  int32_t colpos[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // RoPE position per column
+  uint16_t* kc = nullptr;
+  uint16_t* vc = nullptr;
+};
+int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                   EpiKind epi, const EpiArgs& ea, const char* tag);
+
+// Activation prep: f32 [N][K] -> B + XS; optional RMSNorm with weight.
+int sh_prep_launch(sh_engine* e, const float* x, uint32_t K, uint32_t N, const float* norm_w, float eps,
+                   uint16_t* bx, uint16_t* xs, float* y_out);
+int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uint32_t N, float* resid);
+struct FaArgs {
+  uint32_t layer = 0, N = 0;
+  uint32_t kvlen = 0;      // keys [0, kvlen) exist
+  uint32_t mask_base = 0;  // keys >= mask_base need their bit in colmask
+  uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+};
+int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
+                 float* attn_out, uint16_t* bx, uint16_t* xs);
+int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
+                     uint32_t* out_ids);
+int sh_kv_compact_launch(sh_engine* e, sh_kv* kv, uint32_t base, const uint32_t* src_dev, uint32_t n);
+
+// Profiling helpers (no-ops unless e->profiling).
+void sh_prof_begin(sh_engine* e, hipEvent_t* a);
+void sh_prof_end(sh_engine* e, const char* name, double bytes, hipEvent_t a);
+int sh_prof_flush(sh_engine* e);

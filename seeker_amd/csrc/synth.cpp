@@ -1,0 +1,296 @@
+// Synthetic GGUF model generator (host-only, OpenMP).
+//
+// Produces GGUF v3 byte images of Llama-architecture models whose weights are
+// N(0, std) draws from a counter-based Philox4x64-10 stream, quantized to Q8_0
+// or Q4_K by the quantizer below. The reference never quantizes weights (it
+// only reads GGUF files), so the quantizer is an input generator, not a parity
+// target: the GPU path and the CPU oracle both read the SAME bytes.
+//
+// Format follows the reader in crates/seeker-core/src/gguf/mod.rs:161-230
+// (magic "GGUF", version 3, u64 counts, metadata KV, tensor infos, data section
+// aligned to `general.alignment` = 32) and block layouts from
+// crates/seeker-core/src/gguf/types.rs:92-136 (Q8_0 = 32 elem / 34 B,
+// Q4_K = 256 elem / 144 B). Llama metadata keys and tensor names follow
+// crates/seeker-vulkan/src/models/llama.rs:1038-1048 and :1074-1090.
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "sh_f16.h"
+#include "sh_philox.h"
+
+namespace {
+
+enum : uint32_t { GT_F32 = 0, GT_F16 = 1, GT_Q8_0 = 8, GT_Q4_K = 12 };
+enum : uint32_t { MV_U32 = 4, MV_F32 = 6, MV_STRING = 8 };
+
+struct Buf {
+  std::vector<uint8_t> b;
+  void u32(uint32_t v) { raw(&v, 4); }
+  void u64(uint64_t v) { raw(&v, 8); }
+  void f32(float v) { raw(&v, 4); }
+  void str(const std::string& s) { u64(s.size()); raw(s.data(), s.size()); }
+  void raw(const void* p, size_t n) {
+    const uint8_t* c = (const uint8_t*)p;
+    b.insert(b.end(), c, c + n);
+  }
+};
+
+// Draw element e of the N(0,1) stream with key (seed, stream). Each Philox
+// block yields 4 u64 words; words (0,1) and (2,3) are Box-Muller pairs.
+// Counter convention matches numpy.random.Philox: block i uses counter i+1.
+inline void normals4(uint64_t seed, uint64_t stream, uint64_t block, double out[4]) {
+  uint64_t ctr[4] = {block + 1, 0, 0, 0};
+  uint64_t key[2] = {seed, stream};
+  uint64_t w[4];
+  sh_philox4x64_10(ctr, key, w);
+  for (int p = 0; p < 2; ++p) {
+    double u1 = ((double)(w[2 * p] >> 11) + 0.5) * 0x1.0p-53;
+    double u2 = ((double)(w[2 * p + 1] >> 11) + 0.5) * 0x1.0p-53;
+    double r = std::sqrt(-2.0 * std::log(u1));
+    double t = 6.283185307179586476925286766559 * u2;
+    out[2 * p] = r * std::cos(t);
+    out[2 * p + 1] = r * std::sin(t);
+  }
+}
+
+inline int round_half_up(float v) { return (int)std::floor(v + 0.5f); }
+
+// Q8_0: d = amax/127 (stored f16), q = clamp(round(x / d), -127, 127).
+void quant_q8_0_block(const float* x, uint8_t* out) {
+  float amax = 0.f;
+  for (int i = 0; i < 32; ++i) amax = std::fmax(amax, std::fabs(x[i]));
+  float d = amax / 127.f;
+  uint16_t dh = sh_f32_to_f16(d);
+  std::memcpy(out, &dh, 2);
+  for (int i = 0; i < 32; ++i) {
+    int q = d > 0.f ? round_half_up(x[i] / d) : 0;
+    q = q < -127 ? -127 : (q > 127 ? 127 : q);
+    out[2 + i] = (uint8_t)(int8_t)q;
+  }
+}
+
+// Q4_K: per 32-element sub-block s, value ~= d*sc_s*q - dmin*m_s with 6-bit
+// sc_s, m_s and 4-bit q. d = max(range_s/15)/63, dmin = max(-min_s)/63.
+void quant_q4_k_block(const float* x, uint8_t* out) {
+  float scr[8], mr[8];
+  for (int s = 0; s < 8; ++s) {
+    float mn = x[32 * s], mx = x[32 * s];
+    for (int i = 1; i < 32; ++i) {
+      mn = std::fmin(mn, x[32 * s + i]);
+      mx = std::fmax(mx, x[32 * s + i]);
+    }
+    if (mn > 0.f) mn = 0.f;
+    mr[s] = -mn;
+    scr[s] = (mx - mn) / 15.f;
+  }
+  float dmax = 0.f, mmax = 0.f;
+  for (int s = 0; s < 8; ++s) { dmax = std::fmax(dmax, scr[s]); mmax = std::fmax(mmax, mr[s]); }
+  uint16_t dh = sh_f32_to_f16(dmax / 63.f), mh = sh_f32_to_f16(mmax / 63.f);
+  float d = sh_f16_to_f32(dh), dmin = sh_f16_to_f32(mh);
+  int sc[8], m[8];
+  for (int s = 0; s < 8; ++s) {
+    int a = d > 0.f ? round_half_up(scr[s] / d) : 0;
+    int b = dmin > 0.f ? round_half_up(mr[s] / dmin) : 0;
+    sc[s] = a < 0 ? 0 : (a > 63 ? 63 : a);
+    m[s] = b < 0 ? 0 : (b > 63 ? 63 : b);
+  }
+  std::memcpy(out, &dh, 2);
+  std::memcpy(out + 2, &mh, 2);
+  uint8_t* scales = out + 4;
+  for (int j = 0; j < 4; ++j) {
+    scales[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+    scales[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+    scales[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+  }
+  uint8_t q[256];
+  for (int s = 0; s < 8; ++s) {
+    float step = d * (float)sc[s];
+    float off = dmin * (float)m[s];
+    for (int i = 0; i < 32; ++i) {
+      int v = step > 0.f ? round_half_up((x[32 * s + i] + off) / step) : 0;
+      q[32 * s + i] = (uint8_t)(v < 0 ? 0 : (v > 15 ? 15 : v));
+    }
+  }
+  uint8_t* qs = out + 16;
+  for (int g = 0; g < 4; ++g)
+    for (int l = 0; l < 32; ++l) qs[32 * g + l] = (uint8_t)(q[64 * g + l] | (q[64 * g + 32 + l] << 4));
+}
+
+struct TensorSpec {
+  std::string name;
+  uint64_t ne0, ne1;  // ne0 = contracting / innermost dim, ne1 = rows
+  uint32_t type;
+  bool ones;          // norm weight: all 1.0 (f32)
+  uint64_t offset;    // within data section
+  uint64_t bytes;
+};
+
+uint64_t tensor_bytes(uint32_t type, uint64_t n) {
+  switch (type) {
+    case GT_F32: return n * 4;
+    case GT_F16: return n * 2;
+    case GT_Q8_0: return n / 32 * 34;
+    case GT_Q4_K: return n / 256 * 144;
+  }
+  return 0;
+}
+
+void fill_tensor(const TensorSpec& t, uint64_t seed, uint64_t stream, float stdv, uint8_t* dst) {
+  const uint64_t n = t.ne0 * t.ne1;
+  if (t.ones) {
+    float one = 1.f;
+    for (uint64_t i = 0; i < n; ++i) std::memcpy(dst + 4 * i, &one, 4);
+    return;
+  }
+  const uint64_t blk = t.type == GT_Q4_K ? 256 : 32;
+  const uint64_t bbytes = t.type == GT_Q4_K ? 144 : 34;
+  const int64_t nblk = (int64_t)(n / blk);
+#pragma omp parallel for schedule(static, 256)
+  for (int64_t b = 0; b < nblk; ++b) {
+    float x[256];
+    for (uint64_t e = 0; e < blk; e += 4) {
+      double z[4];
+      normals4(seed, stream, ((uint64_t)b * blk + e) / 4, z);
+      for (int i = 0; i < 4; ++i) x[e + i] = (float)(z[i] * (double)stdv);
+    }
+    if (t.type == GT_Q4_K) quant_q4_k_block(x, dst + (uint64_t)b * bbytes);
+    else quant_q8_0_block(x, dst + (uint64_t)b * bbytes);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Configuration of a synthetic Llama model. wtype/etype are GGML type ids
+// (8 = Q8_0, 12 = Q4_K) for the 2-D weights and token_embd respectively.
+typedef struct sh_synth_llama_cfg {
+  uint32_t n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx;
+  float rms_eps, rope_base, weight_std;
+  uint32_t wtype, etype;
+  uint32_t tied;  // 1: no output.weight (lm_head = token_embd)
+  uint64_t seed;
+} sh_synth_llama_cfg;
+
+// Build a GGUF v3 image in host memory. *out is malloc'd; free with
+// sh_synth_free. Returns 0 on success.
+int sh_synth_llama_gguf(const sh_synth_llama_cfg* c, uint8_t** out, uint64_t* size) {
+  if (!c || !out || !size) return 1;
+  if (c->n_head == 0 || c->n_embd % c->n_head || c->n_head % (c->n_head_kv ? c->n_head_kv : 1)) return 2;
+  const uint32_t wt = c->wtype, et = c->etype;
+  const uint64_t qk_w = wt == GT_Q4_K ? 256 : 32, qk_e = et == GT_Q4_K ? 256 : 32;
+  const uint64_t d = c->n_embd, ff = c->n_ff, hd = d / c->n_head, dkv = hd * c->n_head_kv;
+  if (d % qk_w || ff % qk_w || d % qk_e) return 3;
+
+  std::vector<TensorSpec> ts;
+  ts.push_back({"token_embd.weight", d, c->n_vocab, et, false, 0, 0});
+  for (uint32_t i = 0; i < c->n_layer; ++i) {
+    std::string p = "blk." + std::to_string(i) + ".";
+    ts.push_back({p + "attn_norm.weight", d, 1, GT_F32, true, 0, 0});
+    ts.push_back({p + "attn_q.weight", d, d, wt, false, 0, 0});
+    ts.push_back({p + "attn_k.weight", d, dkv, wt, false, 0, 0});
+    ts.push_back({p + "attn_v.weight", d, dkv, wt, false, 0, 0});
+    ts.push_back({p + "attn_output.weight", d, d, wt, false, 0, 0});
+    ts.push_back({p + "ffn_norm.weight", d, 1, GT_F32, true, 0, 0});
+    ts.push_back({p + "ffn_gate.weight", d, ff, wt, false, 0, 0});
+    ts.push_back({p + "ffn_up.weight", d, ff, wt, false, 0, 0});
+    ts.push_back({p + "ffn_down.weight", ff, d, wt, false, 0, 0});
+  }
+  ts.push_back({"output_norm.weight", d, 1, GT_F32, true, 0, 0});
+  if (!c->tied) ts.push_back({"output.weight", d, c->n_vocab, wt, false, 0, 0});
+
+  Buf h;
+  h.raw("GGUF", 4);
+  h.u32(3);
+  h.u64(ts.size());
+  const uint64_t n_kv = 12;
+  h.u64(n_kv);
+  auto kv_str = [&](const char* k, const char* v) { h.str(k); h.u32(MV_STRING); h.str(v); };
+  auto kv_u32 = [&](const char* k, uint32_t v) { h.str(k); h.u32(MV_U32); h.u32(v); };
+  auto kv_f32 = [&](const char* k, float v) { h.str(k); h.u32(MV_F32); h.f32(v); };
+  kv_str("general.architecture", "llama");
+  kv_u32("general.alignment", 32);
+  kv_u32("llama.block_count", c->n_layer);
+  kv_u32("llama.attention.head_count", c->n_head);
+  kv_u32("llama.attention.head_count_kv", c->n_head_kv);
+  kv_u32("llama.embedding_length", c->n_embd);
+  kv_u32("llama.feed_forward_length", c->n_ff);
+  kv_u32("llama.context_length", c->n_ctx);
+  kv_u32("llama.rope.dimension_count", (uint32_t)hd);
+  kv_f32("llama.rope.freq_base", c->rope_base);
+  kv_f32("llama.attention.layer_norm_rms_epsilon", c->rms_eps);
+  kv_u32("llama.vocab_size", c->n_vocab);
+
+  uint64_t off = 0;
+  for (auto& t : ts) {
+    t.bytes = tensor_bytes(t.type, t.ne0 * t.ne1);
+    t.offset = off;
+    off += (t.bytes + 31) / 32 * 32;
+  }
+  for (auto& t : ts) {
+    h.str(t.name);
+    if (t.ne1 == 1) { h.u32(1); h.u64(t.ne0); }
+    else { h.u32(2); h.u64(t.ne0); h.u64(t.ne1); }
+    h.u32(t.type);
+    h.u64(t.offset);
+  }
+  uint64_t data_start = (h.b.size() + 31) / 32 * 32;
+  uint64_t total = data_start + off;
+  uint8_t* img = (uint8_t*)std::calloc(total, 1);
+  if (!img) return 4;
+  std::memcpy(img, h.b.data(), h.b.size());
+  for (size_t i = 0; i < ts.size(); ++i)
+    fill_tensor(ts[i], c->seed, (uint64_t)i, c->weight_std, img + data_start + ts[i].offset);
+  *out = img;
+  *size = total;
+  return 0;
+}
+
+void sh_synth_free(void* p) { std::free(p); }
+
+// Token ids uniform in [0, vocab): id = (w >> 32) * vocab >> 32 over the
+// Philox stream (seed, 0xFFFF_FFFF) word i (numpy counter convention).
+void sh_synth_tokens(uint64_t seed, uint32_t n, uint32_t vocab, uint32_t* out) {
+  for (uint32_t i = 0; i < n; ++i) {
+    uint64_t ctr[4] = {(uint64_t)(i / 4) + 1, 0, 0, 0};
+    uint64_t key[2] = {seed, 0xFFFFFFFFull};
+    uint64_t w[4];
+    sh_philox4x64_10(ctr, key, w);
+    out[i] = (uint32_t)(((w[i % 4] >> 32) * (uint64_t)vocab) >> 32);
+  }
+}
+
+// Fill n f32 values with N(mean, std) draws (stream key (seed, stream)).
+void sh_synth_normal_f32(uint64_t seed, uint64_t stream, float mean, float stdv, uint64_t n, float* out) {
+  const int64_t nb = (int64_t)((n + 3) / 4);
+#pragma omp parallel for schedule(static, 1024)
+  for (int64_t b = 0; b < nb; ++b) {
+    double z[4];
+    normals4(seed, stream, (uint64_t)b, z);
+    for (int i = 0; i < 4; ++i) {
+      uint64_t e = (uint64_t)b * 4 + i;
+      if (e < n) out[e] = (float)(mean + stdv * z[i]);
+    }
+  }
+}
+
+// Quantize rows of f32 values (n multiple of the block size) to Q8_0 / Q4_K.
+int sh_synth_quantize(uint32_t type, const float* x, uint64_t n, uint8_t* out) {
+  if (type == GT_Q8_0) {
+    if (n % 32) return 1;
+    for (uint64_t b = 0; b < n / 32; ++b) quant_q8_0_block(x + 32 * b, out + 34 * b);
+    return 0;
+  }
+  if (type == GT_Q4_K) {
+    if (n % 256) return 1;
+    for (uint64_t b = 0; b < n / 256; ++b) quant_q4_k_block(x + 256 * b, out + 144 * b);
+    return 0;
+  }
+  return 2;
+}
+
+}  // extern "C"

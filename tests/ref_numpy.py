@@ -1,0 +1,221 @@
+"""Independent numpy (float64) implementation of the pieces the C oracle
+restates, written from the GGUF block specs and the textbook formulas rather
+than from the oracle's code, so that a mistake in either one shows up as a
+disagreement. Used only by tests.
+"""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+
+Q8_0, Q4_K, F32 = 8, 12, 0
+
+
+def f16_to_f64(b: np.ndarray) -> np.ndarray:
+    return np.asarray(b, dtype=np.uint16).view(np.float16).astype(np.float64)
+
+
+def dequant_q8_0(raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    blk = np.asarray(raw, dtype=np.uint8).reshape(rows, k // 32, 34)
+    d = f16_to_f64(blk[:, :, 0:2].copy().view(np.uint16)[..., 0])
+    q = blk[:, :, 2:].view(np.int8).astype(np.float64)
+    return (d[..., None] * q).reshape(rows, k)
+
+
+def q4k_scales(sc12: np.ndarray):
+    """sc12: [..., 12] uint8 -> (sc[..., 8], m[..., 8]) per the GGUF K-quant packing."""
+    s = sc12.astype(np.int64)
+    sc = np.empty(s.shape[:-1] + (8,), dtype=np.int64)
+    m = np.empty_like(sc)
+    sc[..., :4] = s[..., 0:4] & 63
+    m[..., :4] = s[..., 4:8] & 63
+    sc[..., 4:] = (s[..., 8:12] & 0xF) | ((s[..., 0:4] >> 6) << 4)
+    m[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+    return sc, m
+
+
+def dequant_q4_k(raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    blk = np.asarray(raw, dtype=np.uint8).reshape(rows, k // 256, 144)
+    hdr = blk[:, :, 0:4].copy().view(np.uint16)
+    d = f16_to_f64(hdr[..., 0])
+    dmin = f16_to_f64(hdr[..., 1])
+    sc, m = q4k_scales(blk[:, :, 4:16])
+    qs = blk[:, :, 16:].reshape(rows, k // 256, 4, 32)
+    lo = qs & 0xF
+    hi = qs >> 4
+    q = np.stack([lo, hi], axis=3).reshape(rows, k // 256, 8, 32).astype(np.float64)  # sub-block 2g, 2g+1
+    y = d[..., None, None] * sc[..., None] * q - dmin[..., None, None] * m[..., None]
+    return y.reshape(rows, k)
+
+
+def dequant(qtype: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    if qtype == Q8_0:
+        return dequant_q8_0(raw, rows, k)
+    if qtype == Q4_K:
+        return dequant_q4_k(raw, rows, k)
+    if qtype == F32:
+        return np.asarray(raw, dtype=np.uint8).view(np.float32).astype(np.float64).reshape(rows, k)
+    raise ValueError(qtype)
+
+
+# ------------------------------------------------------------------ GGUF reader
+
+def read_gguf(buf: bytes):
+    """Minimal GGUF v3 reader: returns (metadata dict, tensors dict name -> (dims, type, data bytes))."""
+    mv = memoryview(buf)
+    assert bytes(mv[:4]) == b"GGUF"
+    ver, nt, nkv = struct.unpack_from("<IQQ", mv, 4)
+    pos = 4 + 4 + 16
+
+    def rstr(p):
+        n = struct.unpack_from("<Q", mv, p)[0]
+        return bytes(mv[p + 8:p + 8 + n]).decode(), p + 8 + n
+
+    scalar = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
+
+    def rval(t, p):
+        if t == 8:
+            return rstr(p)
+        if t == 9:
+            et, n = struct.unpack_from("<IQ", mv, p)
+            p += 12
+            vals = []
+            for _ in range(n):
+                v, p = rval(et, p)
+                vals.append(v)
+            return vals, p
+        fmt = scalar[t]
+        return struct.unpack_from(fmt, mv, p)[0], p + struct.calcsize(fmt)
+
+    meta = {}
+    for _ in range(nkv):
+        k, pos = rstr(pos)
+        t = struct.unpack_from("<I", mv, pos)[0]
+        pos += 4
+        meta[k], pos = rval(t, pos)
+    infos = []
+    for _ in range(nt):
+        name, pos = rstr(pos)
+        nd = struct.unpack_from("<I", mv, pos)[0]
+        pos += 4
+        dims = list(struct.unpack_from("<" + "Q" * nd, mv, pos))
+        pos += 8 * nd
+        typ, off = struct.unpack_from("<IQ", mv, pos)
+        pos += 12
+        infos.append((name, dims, typ, off))
+    align = meta.get("general.alignment", 32)
+    start = (pos + align - 1) // align * align
+    layout = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144)}
+    tensors = {}
+    for name, dims, typ, off in infos:
+        n = int(np.prod(dims))
+        epb, bpb = layout[typ]
+        nbytes = n // epb * bpb
+        tensors[name] = (dims, typ, np.frombuffer(buf, dtype=np.uint8, count=nbytes, offset=start + off))
+    return meta, tensors, start
+
+
+# ------------------------------------------------------------------ forward
+
+class RefLlama:
+    """float64 Llama forward with f16 K/V storage (same cache rounding as the reference)."""
+
+    def __init__(self, buf: bytes):
+        meta, T, _ = read_gguf(buf)
+        self.nl = meta["llama.block_count"]
+        self.d = meta["llama.embedding_length"]
+        self.nh = meta["llama.attention.head_count"]
+        self.nkv = meta.get("llama.attention.head_count_kv", self.nh)
+        self.ff = meta["llama.feed_forward_length"]
+        self.eps = meta.get("llama.attention.layer_norm_rms_epsilon", 1e-5)
+        self.base = meta.get("llama.rope.freq_base", 10000.0)
+        self.hd = self.d // self.nh
+
+        def mat(name):
+            dims, typ, data = T[name]
+            rows = dims[1] if len(dims) > 1 else 1
+            return dequant(typ, data, rows, dims[0])
+
+        self.emb = mat("token_embd.weight")
+        self.V = self.emb.shape[0]
+        self.out = mat("output.weight") if "output.weight" in T else self.emb
+        self.onorm = mat("output_norm.weight")[0]
+        self.layers = []
+        for i in range(self.nl):
+            g = lambda s: mat(f"blk.{i}.{s}.weight")  # noqa: E731
+            self.layers.append({k: g(k) for k in ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
+                                                 "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"]})
+        self.K = [np.zeros((0, self.nkv, self.hd)) for _ in range(self.nl)]
+        self.Vc = [np.zeros((0, self.nkv, self.hd)) for _ in range(self.nl)]
+
+    def rms(self, x, w):
+        return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * w[0] if w.ndim == 2 else None
+
+    def rope(self, x, pos):
+        # x [L, heads, hd]; adjacent pairs rotated by pos * base^(-i0/hd)
+        i0 = np.arange(0, self.hd, 2)
+        th = np.asarray(pos, dtype=np.float64)[:, None] * self.base ** (-i0 / self.hd)[None, :]
+        c, s = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+        x0, x1 = x[..., 0::2], x[..., 1::2]
+        out = np.empty_like(x)
+        out[..., 0::2] = x0 * c - x1 * s
+        out[..., 1::2] = x0 * s + x1 * c
+        return out
+
+    def forward(self, tokens, parents=None):
+        """Appends to the cache; returns (logits [L][V], residual [L][d])."""
+        L = len(tokens)
+        P = self.K[0].shape[0]
+        if parents is None:
+            parents = [i - 1 for i in range(L)]
+        depth = []
+        for i in range(L):
+            depth.append(0 if parents[i] < 0 else depth[parents[i]] + 1)
+        anc = np.zeros((L, L), dtype=bool)
+        for j in range(L):
+            x = j
+            while x >= 0:
+                anc[j, x] = True
+                x = parents[x]
+        pos = P + np.array(depth)
+        x = self.emb[np.asarray(tokens)].copy()
+        gqa = self.nh // self.nkv
+        for li, W in enumerate(self.layers):
+            h = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * W["attn_norm"][0]
+            q = (h @ W["attn_q"].T).reshape(L, self.nh, self.hd)
+            k = (h @ W["attn_k"].T).reshape(L, self.nkv, self.hd)
+            v = (h @ W["attn_v"].T).reshape(L, self.nkv, self.hd)
+            q = self.rope(q, pos)
+            k = self.rope(k, pos)
+            k16 = k.astype(np.float32).astype(np.float16).astype(np.float64)
+            v16 = v.astype(np.float32).astype(np.float16).astype(np.float64)
+            self.K[li] = np.concatenate([self.K[li], k16])
+            self.Vc[li] = np.concatenate([self.Vc[li], v16])
+            Kc, Vc = self.K[li], self.Vc[li]
+            att = np.zeros((L, self.nh, self.hd))
+            q32 = q.astype(np.float32).astype(np.float64)
+            for hh in range(self.nh):
+                kh = hh // gqa
+                s = q32[:, hh, :] @ Kc[:, kh, :].T / np.sqrt(self.hd)  # [L, P+L]
+                mask = np.ones_like(s, dtype=bool)
+                mask[:, P:] = anc
+                s = np.where(mask, s, -np.inf)
+                s = s - s.max(axis=1, keepdims=True)
+                p = np.exp(s)
+                p /= p.sum(axis=1, keepdims=True)
+                att[:, hh, :] = p @ Vc[:, kh, :]
+            att = att.reshape(L, self.d).astype(np.float32).astype(np.float64)
+            x = (x + att @ W["attn_output"].T).astype(np.float32).astype(np.float64)
+            h2 = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * W["ffn_norm"][0]
+            g = h2 @ W["ffn_gate"].T
+            u = h2 @ W["ffn_up"].T
+            a = (g / (1 + np.exp(-g)) * u).astype(np.float32).astype(np.float64)
+            x = (x + a @ W["ffn_down"].T).astype(np.float32).astype(np.float64)
+        f = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * self.onorm
+        return f @ self.out.T, x
+
+    def truncate(self, p):
+        for li in range(self.nl):
+            self.K[li] = self.K[li][:p]
+            self.Vc[li] = self.Vc[li][:p]

@@ -1,0 +1,145 @@
+"""GPU parity of the verify forward (sh_forward_full / sh_verify_greedy / KV ops)
+against the C oracle on the same synthetic GGUF bytes.
+
+Tolerances (north star): logits within 2e-2 absolute or 1e-2 relative; greedy
+ids identical. Measured errors are ~1e-5, so the tests also assert a tighter
+3e-4 x max|logit| bound to catch regressions early.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from seeker_amd import SeekerError
+from seeker_amd import synth as S
+from seeker_amd._native import GGML_Q4_K, GGML_Q8_0, SH_ERR_ARG, SH_ERR_CAPACITY, SH_ERR_STATE
+
+pytestmark = pytest.mark.gpu
+
+# configs[0] target shape (Q8_0) and a GQA Q4_K shape with the 8B head layout.
+SHAPES = {
+    "tiny_q8": S.TINY_TARGET,
+    "gqa_q4k": S.LlamaShape(2, 1024, 8, 2, 2048, 4000, 512, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K),
+}
+
+
+@pytest.fixture(scope="module", params=list(SHAPES))
+def pair(request, engine):
+    img = S.GgufImage(SHAPES[request.param], seed=0)
+    print(f"model {request.param}", flush=True)
+    gm = engine.upload_weights(img)
+    om = O.Model(img)
+    yield request.param, img, gm, om
+    gm.close()
+    om.close()
+    img.close()
+
+
+def close(a, b):
+    tol = np.maximum(2e-2, 1e-2 * np.abs(b))
+    assert np.all(np.abs(a - b) <= tol)
+    assert np.abs(a - b).max() <= 3e-4 * np.abs(b).max(), np.abs(a - b).max()
+
+
+def margins_ok(gpu, ref):
+    """Greedy ids equal; report columns whose top-2 margin is tiny."""
+    ga, ra = gpu.argmax(axis=1), ref.argmax(axis=1)
+    srt = np.sort(ref, axis=1)
+    margin = srt[:, -1] - srt[:, -2]
+    bad = np.where(ga != ra)[0]
+    assert all(margin[i] < 1e-4 for i in bad), (bad, margin[bad])
+    return int((ga != ra).sum())
+
+
+def test_prefill_and_verify(engine, pair):
+    name, img, gm, om = pair
+    V = gm.dims.n_vocab
+    prompt = S.tokens(1234, 64, V)
+    gkv = engine.allocate_kv_cache(gm, 256)
+    okv = O.KvCache(om, 256)
+    print(f"{name}: prefill 64", flush=True)
+    gl, gr = engine.forward_full_readback(gm, gkv, prompt, 0, full_logits=True)
+    ol, orr = O.forward(om, okv, prompt, 0)
+    close(gl, ol)
+    np.testing.assert_allclose(gr, orr, rtol=1e-3, atol=1e-3 * np.abs(orr).max())
+    assert margins_ok(gl, ol) == 0
+    assert gkv.position == 64
+    # verify chunk of L = 5 at P = 64
+    vt = S.tokens(99, 5, V)
+    print(f"{name}: verify 5", flush=True)
+    gl2, _ = engine.forward_full_readback(gm, gkv, vt, 64)
+    ol2, _ = O.forward(om, okv, vt, 64)
+    close(gl2, ol2)
+    # KV cache: same f16 values up to one ulp at rounding boundaries
+    for layer in range(gm.dims.n_layer):
+        for isv in (False, True):
+            g = gkv.read_layer(layer, isv, 69).astype(np.int32)
+            o = okv.layer(layer, isv, 69).astype(np.int32)
+            diff = np.abs(g - o)
+            assert diff.max() <= 1 and np.mean(diff > 0) < 0.01
+    # rollback: truncate and re-verify other tokens at the same position
+    gkv.truncate(66)
+    okv.truncate(66)
+    vt2 = S.tokens(100, 3, V)
+    ids = engine.verify_greedy(gm, gkv, vt2, 66)
+    ol3, _ = O.forward(om, okv, vt2, 66)
+    assert np.array_equal(ids, ol3.argmax(axis=1))
+    gkv.close()
+    okv.close()
+
+
+def test_tree_verify_and_compact(engine, pair):
+    name, img, gm, om = pair
+    V = gm.dims.n_vocab
+    prompt = S.tokens(7, 40, V)
+    nodes = S.tokens(8, 12, V)
+    parents = [-1, 0, 0, 0, 1, 1, 2, 3, 4, 6, 6, 7]
+    gkv = engine.allocate_kv_cache(gm, 128)
+    okv = O.KvCache(om, 128)
+    engine.forward_full_readback(gm, gkv, prompt, 0, full_logits=False)
+    O.forward(om, okv, prompt, 0, logits_mode=0)
+    print(f"{name}: tree 12", flush=True)
+    gl, _ = engine.forward_full_readback(gm, gkv, nodes, 40, parents=parents)
+    ol, _ = O.forward(om, okv, nodes, 40, parents=parents)
+    close(gl, ol)
+    # accept path 0 -> 2 -> 6 -> 9 and compact it behind the prefix
+    path = [0, 2, 6, 9]
+    gkv.compact(40, path)
+    okv.compact(40, path)
+    assert gkv.position == 44
+    for layer in range(gm.dims.n_layer):
+        g = gkv.read_layer(layer, True, 44).astype(np.int32)
+        o = okv.layer(layer, True, 44).astype(np.int32)
+        assert np.abs(g - o).max() <= 1
+    nxt = S.tokens(9, 2, V)
+    gl2, _ = engine.forward_full_readback(gm, gkv, nxt, 44)
+    ol2, _ = O.forward(om, okv, nxt, 44)
+    close(gl2, ol2)
+    gkv.close()
+    okv.close()
+
+
+def test_errors_are_reported(engine, pair):
+    name, img, gm, om = pair
+    kv = engine.allocate_kv_cache(gm, 64)
+    with pytest.raises(SeekerError) as e:
+        engine.forward_full_readback(gm, kv, [1, 2, 3], 5)        # position mismatch (llama.rs:186-192)
+    assert e.value.status == SH_ERR_STATE
+    with pytest.raises(SeekerError) as e:
+        engine.forward_full_readback(gm, kv, [gm.dims.n_vocab], 0)  # token out of range
+    assert e.value.status == SH_ERR_ARG
+    with pytest.raises(SeekerError) as e:
+        engine.forward_full_readback(gm, kv, np.zeros(65, np.uint32), 0)  # beyond capacity
+    assert e.value.status == SH_ERR_CAPACITY
+    kv.truncate(10)  # truncate never raises the position
+    assert kv.position == 0
+    kv.close()
+
+
+def test_malformed_gguf_rejected(engine):
+    from seeker_amd import _native as N
+    import ctypes as C
+    bad = np.frombuffer(b"GGUF\x07\x00\x00\x00" + b"\x00" * 32, dtype=np.uint8).copy()
+    h = C.c_void_p()
+    rc = N.lib().sh_model_load_gguf_memory(engine.h, bad.ctypes.data_as(C.c_void_p), bad.size, C.byref(h))
+    assert rc == N.SH_ERR_FORMAT
+    assert b"version" in N.lib().sh_last_error()
