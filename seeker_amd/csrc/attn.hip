@@ -54,22 +54,41 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
   const uint16_t* vbase = vc + (size_t)kh * (max_seq / 32) * HD * 32;
 
   // Q^T operands (B): lane (g, r) holds rho = 16*qt + r, d = 32c + 8g .. +8.
+  // Each query row is scaled by a power of two (max|q * s| in [2^9, 2^10)) so
+  // the f16 low halves stay normal; rscale folds 1/s into the score scale.
   h8 qhi[QT][NC], qlo[QT][NC];
   uint32_t rowcol[QT];
-  bool rowok[QT];
+  float rscale[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const uint32_t rho = qg * 16 * QT + 16 * qt + r;
-    rowok[qt] = rho < n_rows;
-    const uint32_t hq = rowok[qt] ? rho / N : 0, col = rowok[qt] ? rho % N : 0;
+    const bool ok = rho < n_rows;
+    const uint32_t hq = ok ? rho / N : 0, col = ok ? rho % N : 0;
     rowcol[qt] = col;
     const float* qp = q + (size_t)col * Dq + (size_t)(kh * gqa + hq) * HD;
+    float x[NC][8];
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        x[c][t] = ok ? qp[32 * c + 8 * g + t] : 0.f;
+        mx = fmaxf(mx, fabsf(x[c][t]));
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    int ex = 0;
+    if (mx > 0.f && mx < INFINITY) {
+      frexpf(mx, &ex);
+      ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+    }
+    const float s = ldexpf(1.0f, 10 - ex);
+    rscale[qt] = scale * ldexpf(1.0f, ex - 10);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      float x[8];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) x[t] = rowok[qt] ? qp[32 * c + 8 * g + t] : 0.f;
-      split8(x, qhi[qt][c], qlo[qt][c]);
+      for (int t = 0; t < 8; ++t) x[c][t] *= s;
+      split8(x[c], qhi[qt][c], qlo[qt][c]);
     }
   }
 
@@ -114,7 +133,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float v = s[kt][qt][j] * scale;
+          float v = s[kt][qt][j] * rscale[qt];
           if (tail) {
             const uint32_t key = key0 + 16 * kt + 4 * g + j;
             bool vis = key < fa.kvlen;
@@ -134,8 +153,10 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
         for (int t = 0; t < 8; ++t) p[t] = 0.f;
       } else {
         alpha = expf(mrow[qt] - mnew);
+        // probabilities carry a 2^12 factor (keeps their f16 low halves normal);
+        // it cancels in O / l because l is summed from the same scaled values
 #pragma unroll
-        for (int t = 0; t < 8; ++t) p[t] = expf(sv[t] - mnew);
+        for (int t = 0; t < 8; ++t) p[t] = expf(sv[t] - mnew) * 4096.0f;
       }
       mrow[qt] = mnew;
       float ps = 0.f;
@@ -166,24 +187,32 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
   // Merge the 4 waves through LDS, then write the split partial:
   // part[((kh * n_splits + split) * n_rows_pad + rho) * (HD + 2) + {d, HD: m, HD+1: l}].
   __shared__ float sm[4][QT * 16], sl[4][QT * 16];
-  __shared__ float so[4][QT * 16][HD + 1];
+  __shared__ float so[QT * 16][HD + 1];
   if (g == 0) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) { sm[wave][16 * qt + r] = mrow[qt]; sl[wave][16 * qt + r] = lrow[qt]; }
   }
   __syncthreads();
+  // waves add their rescaled outputs into one buffer in turn (wave 0 stores)
+  for (int w = 0; w < 4; ++w) {
+    if (wave == w) {
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int rho_l = 16 * qt + r;
-    float M = sm[0][rho_l];
-    for (int w = 1; w < 4; ++w) M = fmaxf(M, sm[w][rho_l]);
-    const float f = (mrow[qt] == -INFINITY) ? 0.f : expf(mrow[qt] - M);
+      for (int qt = 0; qt < QT; ++qt) {
+        const int rho_l = 16 * qt + r;
+        float M = sm[0][rho_l];
+        for (int v = 1; v < 4; ++v) M = fmaxf(M, sm[v][rho_l]);
+        const float f = (mrow[qt] == -INFINITY) ? 0.f : expf(mrow[qt] - M);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) so[wave][rho_l][16 * dt + 4 * g + j] = o[dt][qt][j] * f;
+          for (int j = 0; j < 4; ++j) {
+            float* dst = &so[rho_l][16 * dt + 4 * g + j];
+            *dst = (w == 0 ? 0.f : *dst) + o[dt][qt][j] * f;
+          }
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const uint32_t n_splits = gridDim.y;
   const uint32_t n_rows_pad = gridDim.z * 16 * QT;
   for (int idx = threadIdx.x; idx < QT * 16 * (HD + 2); idx += 256) {
@@ -192,7 +221,7 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
     for (int w = 1; w < 4; ++w) M = fmaxf(M, sm[w][rho_l]);
     float v;
     if (e < HD) {
-      v = so[0][rho_l][e] + so[1][rho_l][e] + so[2][rho_l][e] + so[3][rho_l][e];
+      v = so[rho_l][e];
     } else if (e == HD) {
       v = M;
     } else {
@@ -204,13 +233,11 @@ __global__ __launch_bounds__(256) void k_fa_split(const float* __restrict__ q, c
   }
 }
 
-// Combine the key splits of one (kv head, row), write attn [N][Dq] f32 and the
-// Wo activation operand (B hi/lo + XS sub-block sums).
+// Combine the key splits of one (kv head, row) and write attn [N][Dq] f32.
 template <int HD>
 __global__ __launch_bounds__(HD) void k_fa_combine(const float* __restrict__ part, uint32_t n_splits,
                                                    uint32_t n_rows_pad, uint32_t n_head, uint32_t N, uint32_t gqa,
-                                                   float* __restrict__ attn, uint16_t* __restrict__ bx,
-                                                   uint16_t* __restrict__ xs, uint32_t K) {
+                                                   float* __restrict__ attn) {
   const uint32_t kh = blockIdx.x, rho = blockIdx.y, d = threadIdx.x;
   if (rho >= gqa * N) return;
   const uint32_t hq = rho / N, col = rho % N, head = kh * gqa + hq;
@@ -227,29 +254,11 @@ __global__ __launch_bounds__(HD) void k_fa_combine(const float* __restrict__ par
     acc += p[s * sstride + d] * f;
   }
   const float out = L > 0.f ? acc / L : 0.f;
-  const uint32_t k = head * HD + d;
-  attn[(size_t)col * (n_head * HD) + k] = out;
-  const _Float16 hi = (_Float16)out;
-  const _Float16 lo = (_Float16)(out - (float)hi);
-  const size_t boff = ((size_t)(k / 32) * 64 + ((k % 32) / 8) * 16 + col) * 8 + (k % 8);
-  bx[boff] = __builtin_bit_cast(uint16_t, hi);
-  bx[boff + 64] = __builtin_bit_cast(uint16_t, lo);
-  // Sub-block sum over 32 consecutive d (lanes 32j .. 32j+31 of this workgroup).
-  float sum = out;
-  for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
-  if ((d & 31) == 0) {
-    const uint32_t sb = k / 32;
-    const _Float16 shi = (_Float16)sum;
-    const _Float16 slo = (_Float16)(sum - (float)shi);
-    const size_t xoff = ((size_t)(sb / 8) * 64 + col) * 8 + (sb % 8);
-    xs[xoff] = __builtin_bit_cast(uint16_t, shi);
-    xs[xoff + 64] = __builtin_bit_cast(uint16_t, slo);
-  }
-  (void)K;
+  attn[(size_t)col * (n_head * HD) + head * HD + d] = out;
 }
 
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
-                 float* attn_out, uint16_t* bx, uint16_t* xs) {
+                 float* attn_out) {
   const uint32_t gqa = m->n_head / m->n_kv;
   const uint32_t n_rows = gqa * fa.N;
   const int QT = n_rows > 16 ? 2 : 1;
@@ -285,10 +294,10 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   dim3 cgrid(m->n_kv, n_qg * 16 * QT);
   if (m->hd == 128)
     hipLaunchKernelGGL((k_fa_combine<128>), cgrid, dim3(128), 0, e->stream, part, n_splits, n_qg * 16 * QT,
-                       m->n_head, fa.N, gqa, attn_out, bx, xs, m->d);
+                       m->n_head, fa.N, gqa, attn_out);
   else
     hipLaunchKernelGGL((k_fa_combine<64>), cgrid, dim3(64), 0, e->stream, part, n_splits, n_qg * 16 * QT,
-                       m->n_head, fa.N, gqa, attn_out, bx, xs, m->d);
+                       m->n_head, fa.N, gqa, attn_out);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "fa_combine", 0.0, ev);
   return SH_OK;

@@ -133,9 +133,11 @@ __device__ __forceinline__ uint16_t f2h_bits(float x) { return __builtin_bit_cas
 template <int EPI>
 __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32_t col, const float v[4]) {
   if (EPI == EPI_STORE) {
-    for (int j = 0; j < 4; ++j) ea.out[(size_t)col * ea.ldo + r0 + j] = v[j];
+    for (int j = 0; j < 4; ++j)
+      if (r0 + j < ea.rows) ea.out[(size_t)col * ea.ldo + r0 + j] = v[j];
   } else if (EPI == EPI_ADD) {
     for (int j = 0; j < 4; ++j) {
+      if (r0 + j >= ea.rows) continue;
       float* p = ea.out + (size_t)col * ea.ldo + r0 + j;
       *p = *p + v[j];
     }
@@ -234,6 +236,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__
     for (int t = 0; t < R; ++t) red[wave][t][lane] = y[t];
     __syncthreads();
   }
+  // undo the producer's per-column power-of-two activation scale (exact)
+  const float cs = ea.cs ? ea.cs[r & 7] : 1.0f;
   if (EPI == EPI_SWIGLU) {
     if (wave >= R / 2) return;
     const int tg = 2 * wave, tu = 2 * wave + 1;
@@ -245,8 +249,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__
     }
     float og[4], ou[4];
     for (int j = 0; j < 4; ++j) {
-      og[j] = vg[j] + __shfl_xor(vg[j], 8);
-      ou[j] = vu[j] + __shfl_xor(vu[j], 8);
+      og[j] = (vg[j] + __shfl_xor(vg[j], 8)) * cs;
+      ou[j] = (vu[j] + __shfl_xor(vu[j], 8)) * cs;
     }
     const uint32_t pair = (tile0 + tg) / 2;
     if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__
     v = y[wave];
   }
   float o[4];
-  for (int j = 0; j < 4; ++j) o[j] = v[j] + __shfl_xor(v[j], 8);
+  for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * cs;
   if (tile >= tiles || r >= 8 || (uint32_t)r >= N) return;
   epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
 }
@@ -303,6 +307,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
     for (int t = 0; t < R; ++t) red[wave][t][lane] = y[t];
     __syncthreads();
   }
+  // undo the producer's per-column power-of-two activation scale (exact)
+  const float cs = ea.cs ? ea.cs[r & 7] : 1.0f;
   if (EPI == EPI_SWIGLU) {
     if (wave >= R / 2) return;
     const int tg = 2 * wave, tu = 2 * wave + 1;
@@ -314,8 +320,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
     }
     float og[4], ou[4];
     for (int j = 0; j < 4; ++j) {
-      og[j] = vg[j] + __shfl_xor(vg[j], 8);
-      ou[j] = vu[j] + __shfl_xor(vu[j], 8);
+      og[j] = (vg[j] + __shfl_xor(vg[j], 8)) * cs;
+      ou[j] = (vu[j] + __shfl_xor(vu[j], 8)) * cs;
     }
     const uint32_t pair = (tile0 + tg) / 2;
     if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
@@ -335,7 +341,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
     v = y[wave];
   }
   float o[4];
-  for (int j = 0; j < 4; ++j) o[j] = v[j] + __shfl_xor(v[j], 8);
+  for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * cs;
   if (tile >= tiles || r >= 8 || (uint32_t)r >= N) return;
   epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
 }

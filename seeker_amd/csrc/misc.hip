@@ -56,16 +56,17 @@ int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uin
 // ------------------------------------------------------------------ prep
 
 // y = x * rsqrt(mean(x^2) + eps) * w (rms_norm.slang:39-55) when w != null, else
-// y = x; then y -> GEMV activation operand: B (hi/lo f16, [K/32][64][8]) and XS
-// (per-32 sums, [K/256][64][8], lanes >= 16 stay zero). One workgroup per column.
+// y = x; then y * s -> GEMV activation operand: B (hi/lo f16, [K/32][64][8]) and
+// XS (per-32 sums, [K/256][64][8], lanes >= 16 stay zero), where s is the power
+// of two putting max|y * s| in [2^9, 2^10); cs[col] = 1/s. One workgroup per column.
 __global__ __launch_bounds__(256) void k_prep(const float* __restrict__ x, uint32_t K, const float* __restrict__ w,
                                               float eps, uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
-                                              float* __restrict__ y_out) {
+                                              float* __restrict__ cs) {
+  __shared__ float red[256];
   const uint32_t col = blockIdx.x, tid = threadIdx.x;
   const float* xc = x + (size_t)col * K;
   float scale = 1.f;
   if (w) {
-    __shared__ float red[256];
     float ss = 0.f;
     for (uint32_t i = tid; i < K; i += 256) ss += xc[i] * xc[i];
     red[tid] = ss;
@@ -75,10 +76,25 @@ __global__ __launch_bounds__(256) void k_prep(const float* __restrict__ x, uint3
       __syncthreads();
     }
     scale = 1.0f / sqrtf(red[0] / (float)K + eps);
+    __syncthreads();
   }
-  const uint32_t cb = col / 8, c = col % 8;
-  uint16_t* bxc = bx + (size_t)cb * (K / 32) * 64 * 8;
-  uint16_t* xsc = xs + (size_t)cb * ((K + 255) / 256) * 64 * 8;
+  float mx = 0.f;
+  for (uint32_t i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(w ? xc[i] * scale * w[i] : xc[i]));
+  red[tid] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  mx = red[0];
+  int ex = 0;
+  if (mx > 0.f && mx < INFINITY) {
+    frexpf(mx, &ex);  // mx = m * 2^ex, m in [0.5, 1)
+    ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+  }
+  const float ps = ldexpf(1.0f, 10 - ex);  // max|y * ps| in [2^9, 2^10)
+  if (tid == 0) cs[col] = ldexpf(1.0f, ex - 10);
+  const uint32_t c = col;
   for (uint32_t sb = tid; sb < K / 32; sb += 256) {
     float sum = 0.f;
 #pragma unroll
@@ -87,30 +103,30 @@ __global__ __launch_bounds__(256) void k_prep(const float* __restrict__ x, uint3
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const uint32_t k = sb * 32 + 8 * g + t;
-        const float y = w ? xc[k] * scale * w[k] : xc[k];
-        if (y_out) y_out[(size_t)col * K + k] = y;
+        const float y = (w ? xc[k] * scale * w[k] : xc[k]) * ps;
         sum += y;
         const _Float16 h = (_Float16)y;
         hi[t] = __builtin_bit_cast(uint16_t, h);
         lo[t] = f2hb(y - (float)h);
       }
-      uint16_t* dst = bxc + ((size_t)sb * 64 + 16 * g + c) * 8;
+      uint16_t* dst = bx + ((size_t)sb * 64 + 16 * g + c) * 8;
       *(uint4*)dst = *(uint4*)hi;
       *(uint4*)(dst + 64) = *(uint4*)lo;
     }
     const _Float16 sh = (_Float16)sum;
     const size_t xo = ((size_t)(sb / 8) * 64 + c) * 8 + (sb % 8);
-    xsc[xo] = __builtin_bit_cast(uint16_t, sh);
-    xsc[xo + 64] = f2hb(sum - (float)sh);
+    xs[xo] = __builtin_bit_cast(uint16_t, sh);
+    xs[xo + 64] = f2hb(sum - (float)sh);
   }
 }
 
 int sh_prep_launch(sh_engine* e, const float* x, uint32_t K, uint32_t N, const float* norm_w, float eps,
-                   uint16_t* bx, uint16_t* xs, float* y_out) {
+                   uint16_t* bx, uint16_t* xs, float* cs) {
   SH_CHECK(K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", K);
+  SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "prep N=%u outside [1, 8]", N);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL(k_prep, dim3(N), dim3(256), 0, e->stream, x, K, norm_w, eps, bx, xs, y_out);
+  hipLaunchKernelGGL(k_prep, dim3(N), dim3(256), 0, e->stream, x, K, norm_w, eps, bx, xs, cs);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, norm_w ? "rmsnorm_prep" : "prep", 0.0, ev);
   return SH_OK;

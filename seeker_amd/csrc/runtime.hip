@@ -329,7 +329,7 @@ static void free_model(sh_model* m) {
   Workspace& w = m->ws;
   (void)hipFree(w.resid); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
   (void)hipFree(w.attn); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
-  (void)hipFree(w.tokens); (void)hipFree(w.amax);
+  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs);
   delete m;
 }
 
@@ -466,7 +466,7 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   if (dalloc(&w.resid, (size_t)8 * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
       dalloc(&w.q, (size_t)8 * m->d) || dalloc(&w.attn, (size_t)8 * m->d) || dalloc(&w.h, (size_t)8 * m->ff) ||
       dalloc(&w.logits, (size_t)8 * m->V) || dalloc(&w.fa_part, part_floats) || dalloc(&w.tokens, 128) ||
-      dalloc(&w.amax, 64))
+      dalloc(&w.amax, 64) || dalloc(&w.cs, 8))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
   if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess)
@@ -634,27 +634,29 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
   FaArgs fa;
   fa.N = nc; fa.kvlen = slot0 + nc; fa.mask_base = mask_base;
   for (uint32_t j = 0; j < nc; ++j) fa.colmask[j] = colmask[j];
+  qkv.cs = w.cs;
   EpiArgs add;
-  add.out = w.resid; add.ldo = m->d;
+  add.out = w.resid; add.ldo = m->d; add.rows = m->d; add.cs = w.cs;
   EpiArgs sw;
-  sw.out = w.h; sw.ldo = m->ff;
+  sw.out = w.h; sw.ldo = m->ff; sw.cs = w.cs;
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
-    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.attn_norm, m->eps, w.bx, w.xs, nullptr))) return rc;
+    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.attn_norm, m->eps, w.bx, w.xs, w.cs))) return rc;
     qkv.layer = l;
     if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
     fa.layer = l;
-    if ((rc = sh_fa_launch(e, m, kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs))) return rc;
+    if ((rc = sh_fa_launch(e, m, kv, fa, w.q, w.fa_part, w.attn))) return rc;
+    if ((rc = sh_prep_launch(e, w.attn, m->d, nc, nullptr, 0.f, w.bx, w.xs, w.cs))) return rc;
     if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_ADD, add, "gemv_o"))) return rc;
-    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.ffn_norm, m->eps, w.bx, w.xs, nullptr))) return rc;
+    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.ffn_norm, m->eps, w.bx, w.xs, w.cs))) return rc;
     if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
-    if ((rc = sh_prep_launch(e, w.h, m->ff, nc, nullptr, 0.f, w.bx, w.xs, nullptr))) return rc;
+    if ((rc = sh_prep_launch(e, w.h, m->ff, nc, nullptr, 0.f, w.bx, w.xs, w.cs))) return rc;
     if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_ADD, add, "gemv_down"))) return rc;
   }
   if (want_logits) {
-    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, m->out_norm, m->eps, w.bx, w.xs, nullptr))) return rc;
+    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, m->out_norm, m->eps, w.bx, w.xs, w.cs))) return rc;
     EpiArgs st;
-    st.out = w.logits; st.ldo = m->V;
+    st.out = w.logits; st.ldo = m->V; st.rows = m->V; st.cs = w.cs;
     if ((rc = sh_gemv_launch(e, m->lm_head, w.bx, w.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
   }
   return SH_OK;
@@ -961,22 +963,27 @@ extern "C" int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_d
   SH_CHECK(N >= 1, SH_ERR_ARG, "N must be >= 1");
   const uint32_t K = w->m.K;
   uint16_t *bx = nullptr, *xs = nullptr;
+  float* cs = nullptr;
   const size_t bx_elems = (size_t)K / 32 * 64 * 8, xs_elems = (size_t)(K + 255) / 256 * 64 * 8;
   SH_HIP(hipMallocAsync((void**)&bx, bx_elems * 2, e->stream));
   SH_HIP(hipMallocAsync((void**)&xs, xs_elems * 2, e->stream));
+  SH_HIP(hipMallocAsync((void**)&cs, 8 * sizeof(float), e->stream));
   SH_HIP(hipMemsetAsync(xs, 0, xs_elems * 2, e->stream));
   int rc = SH_OK;
   for (uint32_t c0 = 0; c0 < N && !rc; c0 += 8) {
     const uint32_t nc = std::min<uint32_t>(8, N - c0);
-    rc = sh_prep_launch(e, x_dev + (size_t)c0 * K, K, nc, nullptr, 0.f, bx, xs, nullptr);
+    rc = sh_prep_launch(e, x_dev + (size_t)c0 * K, K, nc, nullptr, 0.f, bx, xs, cs);
     if (rc) break;
     EpiArgs ea;
     ea.out = y_dev + (size_t)c0 * w->m.M;
     ea.ldo = w->m.M;
+    ea.rows = w->m.M;
+    ea.cs = cs;
     rc = sh_gemv_launch(e, w->m, bx, xs, nc, accumulate ? EPI_ADD : EPI_STORE, ea, "gemv");
   }
   (void)hipFreeAsync(bx, e->stream);
   (void)hipFreeAsync(xs, e->stream);
+  (void)hipFreeAsync(cs, e->stream);
   if (rc) return rc;
   SH_HIP(hipStreamSynchronize(e->stream));
   return sh_prof_flush(e);

@@ -164,10 +164,14 @@ __global__ __launch_bounds__(256) void k_decide_reject(const float* __restrict__
   const double2* sq = stats + (size_t)B * (k + 1) + (size_t)b * k;
   if (t < k) {
     const uint32_t d = drafts[b * k + t];
-    const double pd = exp(((double)p[((size_t)b * (k + 1) + t) * V + d] - sp[t].x) * inv_t) / sp[t].y;
-    const double qd = exp(((double)q[((size_t)b * k + t) * V + d] - sq[t].x) * inv_t) / sq[t].y;
-    const float ua = uniform_at(u_dev, seed, counter + 2ull * (b * (k + 1) + t));
-    if (!((double)ua * qd < pd)) atomicMin(&first_rej, t);
+    bool accept = false;
+    if (d < V) {  // an out-of-vocab draft id is rejected
+      const double pd = exp(((double)p[((size_t)b * (k + 1) + t) * V + d] - sp[t].x) * inv_t) / sp[t].y;
+      const double qd = exp(((double)q[((size_t)b * k + t) * V + d] - sq[t].x) * inv_t) / sq[t].y;
+      const float ua = uniform_at(u_dev, seed, counter + 2ull * (b * (k + 1) + t));
+      accept = (double)ua * qd < pd;
+    }
+    if (!accept) atomicMin(&first_rej, t);
   }
   __syncthreads();
   const uint32_t i = first_rej;

@@ -102,6 +102,7 @@ struct Workspace {
   float* fa_part = nullptr;   // flash-attn split partials
   uint32_t* tokens = nullptr; // [cols + 16] device token ids
   unsigned long long* amax = nullptr;  // [cols] packed argmax keys
+  float* cs = nullptr;        // [8] inverse activation scales of the current B operand
   size_t fa_part_floats = 0;
 };
 
@@ -142,6 +143,8 @@ enum EpiKind { EPI_STORE = 0, EPI_ADD = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
 struct EpiArgs {
   float* out = nullptr;   // STORE/ADD: [N][ldo]; QKV: roped q [N][Dq]; SWIGLU: h [N][ldo]
   uint32_t ldo = 0;
+  uint32_t rows = 0xFFFFFFFFu;  // STORE/ADD: logical rows M (ragged last tile)
+  const float* cs = nullptr;    // [8] inverse activation scale per column (from sh_prep_launch)
   // QKV
   uint32_t Dq = 0, Dkv = 0, hd = 0, n_kv = 0, max_seq = 0, slot0 = 0, layer = 0;
   const float2* rope = nullptr;
@@ -152,9 +155,12 @@ struct EpiArgs {
 int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                    EpiKind epi, const EpiArgs& ea, const char* tag);
 
-// Activation prep: f32 [N][K] -> B + XS; optional RMSNorm with weight.
+// Activation prep: f32 [N][K] -> B + XS (N <= 8); optional RMSNorm with weight.
+// Each column is scaled by a power of two s so max|y*s| lies in [2^9, 2^10):
+// the f16 low halves then stay normal (an f16 subnormal keeps only 2^-24 of
+// absolute resolution) and the 32-element XS sums stay below 2^15. cs[col] = 1/s.
 int sh_prep_launch(sh_engine* e, const float* x, uint32_t K, uint32_t N, const float* norm_w, float eps,
-                   uint16_t* bx, uint16_t* xs, float* y_out);
+                   uint16_t* bx, uint16_t* xs, float* cs);
 int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uint32_t N, float* resid);
 struct FaArgs {
   uint32_t layer = 0, N = 0;
@@ -163,7 +169,7 @@ struct FaArgs {
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 };
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
-                 float* attn_out, uint16_t* bx, uint16_t* xs);
+                 float* attn_out);
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids);
 int sh_kv_compact_launch(sh_engine* e, sh_kv* kv, uint32_t base, const uint32_t* src_dev, uint32_t n);

@@ -282,12 +282,14 @@ void sh_synth_normal_f32(uint64_t seed, uint64_t stream, float mean, float stdv,
 int sh_synth_quantize(uint32_t type, const float* x, uint64_t n, uint8_t* out) {
   if (type == GT_Q8_0) {
     if (n % 32) return 1;
-    for (uint64_t b = 0; b < n / 32; ++b) quant_q8_0_block(x + 32 * b, out + 34 * b);
+#pragma omp parallel for schedule(static, 1024)
+    for (int64_t b = 0; b < (int64_t)(n / 32); ++b) quant_q8_0_block(x + 32 * b, out + 34 * b);
     return 0;
   }
   if (type == GT_Q4_K) {
     if (n % 256) return 1;
-    for (uint64_t b = 0; b < n / 256; ++b) quant_q4_k_block(x + 256 * b, out + 144 * b);
+#pragma omp parallel for schedule(static, 256)
+    for (int64_t b = 0; b < (int64_t)(n / 256); ++b) quant_q4_k_block(x + 256 * b, out + 144 * b);
     return 0;
   }
   return 2;
