@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark of the north-star path: speculative decoding on one MI355X with a
+Llama-3-8B-shape Q4_K target and a Llama-3.2-1B-shape Q4_K draft (BASELINE.json
+configs[2]), k = 7, f16 KV prefilled to 4096 positions, batch 1, greedy.
+
+A "step" is one speculative step (sh_spec_step): 7 greedy draft tokens on the
+device, one verify forward of k+1 = 8 tokens with all-position logits, greedy
+acceptance and KV rollback. value = accepted tok/s over the timed steps, the
+reference's own definition (generated tokens / decode seconds,
+apps/seeker-cli/src/commands/run.rs:702-710). Weights and KV are resident in
+HBM before timing; synthetic random-init weights (N(0, 0.02) quantized to Q4_K).
+
+Also reported: verify-step latency and HBM roofline (hipEvents inside the
+library), the dominant kernel's roofline, and the CPU oracle's speculative step
+timed on this host's cores from the same state (with a token-for-token check).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       python bench.py --profile-only   (target verify steps only, for rocprofv3)
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def verify_bytes(d, P, L):
+    """Algorithmic bytes of one verify step: every Q4_K weight matrix (144 B per
+    256 elements, lm_head included, norms and the L gathered embedding rows
+    excluded) + f16 K/V read for [0, P+L) + K/V write of L rows."""
+    dkv = d.head_dim * d.n_head_kv
+    per_layer = (2 * d.n_embd * d.n_embd + 2 * dkv * d.n_embd + 3 * d.n_ff * d.n_embd)
+    elems = d.n_layer * per_layer + d.n_vocab * d.n_embd
+    w = elems * 144 // 256
+    kv_read = 2 * d.n_layer * (P + L) * dkv * 2
+    kv_write = 2 * d.n_layer * L * dkv * 2
+    return w, kv_read, kv_write
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--k", type=int, default=7)
+    ap.add_argument("--verify-reps", type=int, default=30)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-only", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this build targets one MI355X; the verify path has no multi-GPU mode "
+              "(batch-1 verify does not shard profitably, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    from seeker_amd import Engine
+    from seeker_amd import synth as S
+
+    t0 = time.time()
+    timg = S.GgufImage(S.L8B_TARGET, seed=0)
+    dimg = None if args.profile_only else S.GgufImage(S.L1B_DRAFT, seed=1)
+    log(f"synthetic GGUF: target {timg.size / 1e9:.2f} GB" + ("" if dimg is None else f", draft {dimg.size / 1e9:.2f} GB")
+        + f" in {time.time() - t0:.1f}s")
+    eng = Engine(0)
+    t0 = time.time()
+    tm = eng.upload_weights(timg)
+    dm = None if dimg is None else eng.upload_weights(dimg)
+    log(f"upload + repack {time.time() - t0:.1f}s")
+    d = tm.dims
+    V = d.n_vocab
+    P0 = args.ctx
+    max_seq = P0 + 16 + (args.steps + args.warmup + 2) * (args.k + 1) + 64
+    tkv = eng.allocate_kv_cache(tm, max_seq)
+    dkv = None if dm is None else eng.allocate_kv_cache(dm, max_seq)
+    prompt = S.tokens(1234, P0, V)
+    t0 = time.time()
+    eng.prefill(tm, tkv, prompt[:-1], 0)
+    lg, _ = eng.forward_full_readback(tm, tkv, prompt[-1:], P0 - 1, full_logits=False, want_residual=False)
+    if dm is not None:
+        eng.prefill(dm, dkv, prompt, 0)
+    last = int(np.argmax(lg[0]))
+    log(f"prefill {P0} tokens in {time.time() - t0:.1f}s")
+
+    # ---- verify step: latency + roofline (target only) -------------------
+    vt = S.tokens(777, args.k + 1, V)
+    vt[0] = last
+    P = tkv.position
+    for _ in range(3):
+        eng.verify_greedy(tm, tkv, vt, P)
+        tkv.truncate(P)
+    lat = []
+    for _ in range(args.verify_reps):
+        t = time.perf_counter()
+        eng.verify_greedy(tm, tkv, vt, P)
+        lat.append((time.perf_counter() - t) * 1e3)
+        tkv.truncate(P)
+    eng.set_profiling(True)
+    eng.profile(reset=True)
+    for _ in range(args.verify_reps):
+        eng.verify_greedy(tm, tkv, vt, P)
+        tkv.truncate(P)
+    prof = eng.profile(reset=True)
+    eng.set_profiling(False)
+    wb, kvr, kvw = verify_bytes(d, P, args.k + 1)
+    vbytes = wb + kvr + kvw
+    vms = statistics.median(lat)
+    gemv = {n: s for n, s in prof.items() if n.startswith("gemv")}
+    dom_name = max(gemv, key=lambda n: gemv[n]["ms"])
+    dom = gemv[dom_name]
+    dom_avg_ms = dom["ms"] / dom["launches"]
+    dom_bytes = dom["bytes"] / dom["launches"]
+    kern_ms = sum(s["ms"] for s in prof.values()) / args.verify_reps
+    log(f"verify step (L={args.k + 1}, P={P}): median {vms:.3f} ms wall, {kern_ms:.3f} ms in kernels; "
+        f"{vbytes / 1e9:.3f} GB -> {vbytes / vms / 1e6:.0f} GB/s")
+    for n, s in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+        per = s["ms"] / args.verify_reps
+        gbs = s["bytes"] / s["ms"] / 1e6 if s["ms"] > 0 and s["bytes"] else 0
+        log(f"  {n:16s} {s['launches'] // args.verify_reps:4d}/step {per:8.3f} ms/step  {gbs:7.0f} GB/s")
+
+    if args.profile_only:
+        print(json.dumps({"metric": "verify-only profile run", "verify_ms": vms, "dominant": dom_name}))
+        return
+
+    # ---- CPU baseline + full-size greedy parity from the same state --------
+    cpu = None
+    parity = None
+    gpu_first = eng.decode_speculative(tm, dm, tkv, dkv, last, args.k) if args.no_cpu_baseline else None
+    if not args.no_cpu_baseline:
+        import oracle as O
+
+        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        ot, od = O.Model(timg), O.Model(dimg)
+        okt, okd = O.KvCache(ot, max_seq), O.KvCache(od, max_seq)
+        for (gkv, okv, m) in ((tkv, okt, tm), (dkv, okd, dm)):
+            n = gkv.position
+            for layer in range(m.dims.n_layer):
+                for isv in (False, True):
+                    okv.layer(layer, isv, n)[:] = gkv.read_layer(layer, isv, n)
+            okv.set_position(n)
+        t = time.perf_counter()
+        o_em, o_dr = O.spec_step_greedy(ot, od, okt, okd, last, args.k)
+        cpu_s = time.perf_counter() - t
+        g = eng.decode_speculative(tm, dm, tkv, dkv, last, args.k)
+        gpu_first = g
+        parity = {"oracle_emitted": o_em, "gpu_emitted": g.emitted, "drafts_equal": o_dr == g.drafts,
+                  "emitted_equal": o_em == g.emitted}
+        log(f"cpu oracle spec step: {cpu_s:.2f}s on {cores} threads, emitted {o_em}; gpu emitted {g.emitted}")
+        cpu = {"value": len(o_em) / cpu_s, "unit": "accepted tok/s", "cores": cores, "kind": "port",
+               "sample": f"1 speculative step (k={args.k}, greedy) from the GPU's post-prefill state "
+                         f"(ctx {P0}, same weights and KV), C oracle -O2 OpenMP f64"}
+        for x in (okt, okd):
+            x.close()
+        ot.close(); od.close()
+    last = gpu_first.last_token
+
+    # ---- timed speculative steps ------------------------------------------
+    for _ in range(args.warmup):
+        r = eng.decode_speculative(tm, dm, tkv, dkv, last, args.k)
+        last = r.last_token
+    eng.sync()
+    t = time.perf_counter()
+    emitted = 0
+    accepted = 0
+    for _ in range(args.steps):
+        r = eng.decode_speculative(tm, dm, tkv, dkv, last, args.k)
+        emitted += len(r.emitted)
+        accepted += r.accepted
+        last = r.last_token
+    eng.sync()
+    dt = time.perf_counter() - t
+    value = emitted / dt
+    log(f"{args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {emitted} tokens, "
+        f"acceptance {accepted / (args.steps * args.k):.3f}")
+
+    out = {
+        "metric": "spec-decode accepted tok/s (8B Q4_K, k=7, 1 GPU); verify HBM GB/s vs peak",
+        "value": round(value, 3),
+        "unit": "accepted tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights, f32 activations (f16 hi/lo MFMA), f16 KV",
+        "data": "synthetic: random-init N(0,0.02) Q4_K weights, uniform random prompt ids",
+        "config": {"workload": "spec decode: Llama-3-8B-shape Q4_K target + Llama-3.2-1B-shape Q4_K draft, "
+                               "k=7 (verify L=8), f16 KV ctx 4096, batch 1, greedy",
+                   "k": args.k, "ctx": P0, "batch": 1, "acceptance_rate": round(accepted / (args.steps * args.k), 4)},
+        "verify_step": {"ms": round(vms, 4), "kernel_ms": round(kern_ms, 4), "alg_bytes": vbytes,
+                        "GBps": round(vbytes / vms / 1e6, 1), "frac": round(vbytes / vms / 1e6 / HBM_PEAK_GBS, 4)},
+        "roofline": {"kernel": dom_name, "bound": "hbm", "achieved": round(dom_bytes / dom_avg_ms / 1e6, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_bytes / dom_avg_ms / 1e6 / HBM_PEAK_GBS, 4),
+                     "bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_avg_ms, 5), "traffic": None},
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(out), flush=True)
+    for x in (tkv, dkv, tm, dm):
+        x.close()
+    eng.close()
+    timg.close()
+    dimg.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -401,8 +401,18 @@ static void matmul(const or_mat* W, const float* x, uint32_t N, float* y) {
   or_gemv(W->type, W->w, W->rows, W->cols, x, N, y);
 }
 
+/* f16 -> f32 table (65536 entries of or_f16_to_f32) for the attention inner loops. */
+static float f16_lut[65536];
+static int f16_lut_ready = 0;
+static void f16_lut_init(void) {
+  if (f16_lut_ready) return;
+  for (uint32_t i = 0; i < 65536; ++i) f16_lut[i] = or_f16_to_f32((uint16_t)i);
+  f16_lut_ready = 1;
+}
+
 int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint32_t pos,
                const int32_t* parents, int logits_mode, float* logits, float* residual_out) {
+  f16_lut_init();
   /* Preconditions as models/llama.rs:178-192. */
   if (L == 0) return 1;
   if (kv->pos != pos) return 2;
@@ -461,7 +471,7 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
           if (!vis) { s[t] = -INFINITY; continue; }
           const uint16_t* kr = Kc + (size_t)t * dkv + (size_t)kh * hd;
           double acc = 0.0;
-          for (uint32_t e = 0; e < hd; ++e) acc += (double)qv[e] * (double)or_f16_to_f32(kr[e]);
+          for (uint32_t e = 0; e < hd; ++e) acc += (double)qv[e] * (double)f16_lut[kr[e]];
           s[t] = acc * scale;
           if (s[t] > mx) mx = s[t];
         }
@@ -471,7 +481,7 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
         for (uint32_t e = 0; e < hd; ++e) {
           double acc = 0.0;
           for (uint32_t t = 0; t < kvlen; ++t)
-            if (s[t] != 0.0) acc += s[t] * (double)or_f16_to_f32(Vc[(size_t)t * dkv + (size_t)kh * hd + e]);
+            if (s[t] != 0.0) acc += s[t] * (double)f16_lut[Vc[(size_t)t * dkv + (size_t)kh * hd + e]];
           o[e] = (float)(acc / sum);
         }
         free(s);

@@ -103,6 +103,12 @@ class Engine:
             resid.ctypes.data_as(N.F32P) if resid is not None else None))
         return logits, resid
 
+    def prefill(self, model: "Model", cache: "KvCache", tokens: Sequence[int], pos: int):
+        """Forward without logits (KV only; bench.rs feed_kv, :296-317)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        N.check(self._lib.sh_forward_full(self.h, model.h, cache.h, t.ctypes.data_as(N.U32P), t.size, pos, None, 0,
+                                          None, None))
+
     def verify_greedy(self, model: "Model", cache: "KvCache", tokens: Sequence[int], pos: int) -> np.ndarray:
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         out = np.zeros(t.size, dtype=np.uint32)
