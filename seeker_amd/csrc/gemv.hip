@@ -175,12 +175,62 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32
 
 // ------------------------------------------------------------------ kernels
 
-// R tiles per workgroup, W waves per workgroup splitting the superblocks.
+// One wave's operands for one 16-row tile and one 256-element superblock.
+struct Q4Tile {
+  u32x4 q0, q1, dd;
+  uint32_t s0, s1, s2;
+};
+
+__device__ __forceinline__ Q4Tile load_q4_tile(const uint8_t* base, int lane, int g, int r) {
+  Q4Tile a;
+  a.q0 = ld16(base + 32 * lane);
+  a.q1 = ld16(base + 32 * lane + 16);
+  a.dd = ld16(base + 2048 + 16 * g);
+  const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
+  a.s0 = sp[0];
+  a.s1 = sp[1];
+  a.s2 = sp[2];
+  return a;
+}
+
+// y[j] += d * sum_s sc_s * q.x - dmin * sum_s m_s * xsum_s for rows 4g+j.
+__device__ __forceinline__ void q4_tile_mma(const Q4Tile& a, const h8* bq, h8 bm, f4& y) {
+  const uint32_t sc03 = a.s0 & 0x3F3F3F3Fu, m03 = a.s1 & 0x3F3F3F3Fu;
+  const uint32_t sc47 = (a.s2 & 0x0F0F0F0Fu) | ((a.s0 >> 2) & 0x30303030u);
+  const uint32_t m47 = ((a.s2 >> 4) & 0x0F0F0F0Fu) | ((a.s1 >> 2) & 0x30303030u);
+  const uint32_t words[8] = {a.q0.x, a.q0.y, a.q0.z, a.q0.w, a.q1.x, a.q1.y, a.q1.z, a.q1.w};
+  const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const h2 mult = pair_of(m < 4 ? sc03 : sc47, m & 3);
+    const h2 add = mult * k1024;
+    acc = mfma16(q4_operand(words[m], mult, add), bq[m], acc);
+  }
+  // Minimum term: A = m_s (every lane group holds the row's m, but B = XS is
+  // zero outside lane group 0, so only k = s of group 0 contributes).
+  u32x4 am;
+  am.x = as_u32(h2{(_Float16)(float)(m03 & 0xFF), (_Float16)(float)((m03 >> 8) & 0xFF)});
+  am.y = as_u32(h2{(_Float16)(float)((m03 >> 16) & 0xFF), (_Float16)(float)(m03 >> 24)});
+  am.z = as_u32(h2{(_Float16)(float)(m47 & 0xFF), (_Float16)(float)((m47 >> 8) & 0xFF)});
+  am.w = as_u32(h2{(_Float16)(float)((m47 >> 16) & 0xFF), (_Float16)(float)(m47 >> 24)});
+  const f4 macc = mfma16(as_h8(am), bm, f4{0.f, 0.f, 0.f, 0.f});
+  const uint32_t ddw[4] = {a.dd.x, a.dd.y, a.dd.z, a.dd.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float d = (float)as_h2(ddw[j]).x, dmin = (float)as_h2(ddw[j]).y;
+    y[j] = y[j] + d * acc[j] - dmin * macc[j];
+  }
+}
+
+// Q4_K GEMV: a workgroup of W waves owns R row tiles; wave w takes the
+// superblocks b = w, w + W, ... and keeps the next superblock's weights and
+// activation operand in flight while it computes the current one. The W
+// partial sums meet in LDS; no state is shared between workgroups.
 template <int R, int W, int EPI>
-__global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles,
-                                                      uint32_t nsb, const uint16_t* __restrict__ Bx,
-                                                      const uint16_t* __restrict__ XS, uint32_t N,
-                                                      EpiArgs ea) {
+__global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                      const uint16_t* __restrict__ Bx,
+                                                      const uint16_t* __restrict__ XS, uint32_t N, EpiArgs ea) {
   __shared__ f4 red[W][R][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
@@ -189,46 +239,30 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__
 #pragma unroll
   for (int t = 0; t < R; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (uint32_t b = wave; b < nsb; b += W) {
+  struct Stage {
     h8 bq[8];
+    h8 bm;
+    Q4Tile a[R];
+  };
+  auto load = [&](uint32_t b, Stage& st) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
-    const h8 bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
+    for (int m = 0; m < 8; ++m) st.bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
+    st.bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
 #pragma unroll
     for (int t = 0; t < R; ++t) {
-      const uint32_t tile = tile0 + t;
-      if (tile >= tiles) break;
-      const uint8_t* base = Wp + ((size_t)tile * nsb + b) * SH_Q4K_TILE_BYTES;
-      const u32x4 q0 = ld16(base + 32 * lane), q1 = ld16(base + 32 * lane + 16);
-      const u32x4 dd = ld16(base + 2048 + 16 * g);
-      const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
-      const uint32_t s0 = sp[0], s1 = sp[1], s2 = sp[2];
-      const uint32_t sc03 = s0 & 0x3F3F3F3Fu, m03 = s1 & 0x3F3F3F3Fu;
-      const uint32_t sc47 = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-      const uint32_t m47 = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-      const uint32_t words[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-      const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const h2 mult = pair_of(m < 4 ? sc03 : sc47, m & 3);
-        const h2 add = mult * k1024;
-        acc = mfma16(q4_operand(words[m], mult, add), bq[m], acc);
-      }
-      // Minimum term: A = m_s (lane group 0 only, k = s), B = XS (zero for g > 0).
-      u32x4 am;
-      am.x = as_u32(h2{(_Float16)(float)(m03 & 0xFF), (_Float16)(float)((m03 >> 8) & 0xFF)});
-      am.y = as_u32(h2{(_Float16)(float)((m03 >> 16) & 0xFF), (_Float16)(float)(m03 >> 24)});
-      am.z = as_u32(h2{(_Float16)(float)(m47 & 0xFF), (_Float16)(float)((m47 >> 8) & 0xFF)});
-      am.w = as_u32(h2{(_Float16)(float)((m47 >> 16) & 0xFF), (_Float16)(float)(m47 >> 24)});
-      const f4 macc = mfma16(as_h8(am), bm, f4{0.f, 0.f, 0.f, 0.f});
-      const uint32_t ddw[4] = {dd.x, dd.y, dd.z, dd.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float d = (float)as_h2(ddw[j]).x, dmin = (float)as_h2(ddw[j]).y;
-        y[t][j] = y[t][j] + d * acc[j] - dmin * macc[j];
-      }
+      const uint32_t tile = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
+      st.a[t] = load_q4_tile(Wp + ((size_t)tile * nsb + b) * SH_Q4K_TILE_BYTES, lane, g, r);
     }
+  };
+  Stage cur, nxt;
+  uint32_t b = wave;
+  if (b < nsb) load(b, cur);
+  for (; b < nsb; b += W) {
+    const bool more = b + W < nsb;
+    if (more) load(b + W, nxt);
+#pragma unroll
+    for (int t = 0; t < R; ++t) q4_tile_mma(cur.a[t], cur.bq, cur.bm, y[t]);
+    if (more) cur = nxt;
   }
 
   if (W > 1) {
@@ -252,13 +286,11 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__
       og[j] = (vg[j] + __shfl_xor(vg[j], 8)) * cs;
       ou[j] = (vu[j] + __shfl_xor(vu[j], 8)) * cs;
     }
-    const uint32_t pair = (tile0 + tg) / 2;
     if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
-    const uint32_t row0 = pair * 16 + 4 * g;
+    const uint32_t row0 = ((tile0 + tg) / 2) * 16 + 4 * g;
     for (int j = 0; j < 4; ++j) {
       const float x = og[j];
-      const float sl = x / (1.0f + expf(-x));
-      ea.out[(size_t)r * ea.ldo + row0 + j] = sl * ou[j];
+      ea.out[(size_t)r * ea.ldo + row0 + j] = (x / (1.0f + expf(-x))) * ou[j];
     }
     return;
   }
@@ -430,11 +462,12 @@ int sh_repack_upload_gu(sh_engine* e, int type, const uint8_t* gate, const uint8
 }
 
 template <int R, int W, int EPI>
-static void launch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                       const EpiArgs& ea) {
+static int launch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                      const EpiArgs& ea) {
   const uint32_t grid = (w.tiles + R - 1) / R;
   hipLaunchKernelGGL((k_gemv_q4k<R, W, EPI>), dim3(grid), dim3(64 * W), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
                      xs, N, ea);
+  return SH_OK;
 }
 template <int R, int W, int EPI>
 static void launch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {
@@ -443,22 +476,15 @@ static void launch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t 
                      ea);
 }
 
-// Shape policy: keep >= ~1000 waves in flight. Small-M matrices use one tile
-// per workgroup and 8 waves splitting K; large-M ones share the activation
-// operand across 4 tiles per wave.
+// Shape policy: keep ~1000+ waves in flight. Small-M matrices use one tile per
+// workgroup and 8 waves splitting K; large-M ones share each activation stage
+// across 2-4 tiles per wave; gate/up waves own (gate, up) tile pairs.
 template <int EPI>
-static void dispatch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                         const EpiArgs& ea) {
-  if (EPI == EPI_SWIGLU) {
-    if (w.tiles >= 4096) launch_q4k<4, 4, EPI>(e, w, bx, xs, N, ea);
-    else launch_q4k<2, 8, EPI>(e, w, bx, xs, N, ea);
-  } else if (w.tiles >= 4096) {
-    launch_q4k<4, 4, EPI>(e, w, bx, xs, N, ea);
-  } else if (w.tiles >= 1024) {
-    launch_q4k<2, 4, EPI>(e, w, bx, xs, N, ea);
-  } else {
-    launch_q4k<1, 8, EPI>(e, w, bx, xs, N, ea);
-  }
+static int dispatch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                        const EpiArgs& ea) {
+  if (EPI == EPI_SWIGLU) return launch_q4k<2, 8, EPI>(e, w, bx, xs, N, ea);
+  if (w.tiles >= 1024) return launch_q4k<2, 4, EPI>(e, w, bx, xs, N, ea);
+  return launch_q4k<1, 8, EPI>(e, w, bx, xs, N, ea);
 }
 template <int EPI>
 static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {
@@ -473,12 +499,14 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   if (w.type == GGML_Q4_K) {
+    int rc = SH_OK;
     switch (epi) {
-      case EPI_STORE: dispatch_q4k<EPI_STORE>(e, w, bx, xs, N, ea); break;
-      case EPI_ADD: dispatch_q4k<EPI_ADD>(e, w, bx, xs, N, ea); break;
-      case EPI_QKV: dispatch_q4k<EPI_QKV>(e, w, bx, xs, N, ea); break;
-      case EPI_SWIGLU: dispatch_q4k<EPI_SWIGLU>(e, w, bx, xs, N, ea); break;
+      case EPI_STORE: rc = dispatch_q4k<EPI_STORE>(e, w, bx, xs, N, ea); break;
+      case EPI_ADD: rc = dispatch_q4k<EPI_ADD>(e, w, bx, xs, N, ea); break;
+      case EPI_QKV: rc = dispatch_q4k<EPI_QKV>(e, w, bx, xs, N, ea); break;
+      case EPI_SWIGLU: rc = dispatch_q4k<EPI_SWIGLU>(e, w, bx, xs, N, ea); break;
     }
+    if (rc) return rc;
   } else if (w.type == GGML_Q8_0) {
     switch (epi) {
       case EPI_STORE: dispatch_q8<EPI_STORE>(e, w, bx, N, ea); break;

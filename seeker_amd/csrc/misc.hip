@@ -1,10 +1,9 @@
 // Small per-column kernels of the verify step: embedding gather, RMSNorm fused
 // with the GEMV activation operand build, and greedy per-column argmax.
-#include "sh_f16.h"
 #include "sh_internal.h"
+#include "sh_operand.h"
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f2hb(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
 
 // ------------------------------------------------------------------ embed
 
@@ -55,78 +54,67 @@ int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uin
 
 // ------------------------------------------------------------------ prep
 
+constexpr int PREP_THREADS = SH_OPERAND_THREADS;
+
 // y = x * rsqrt(mean(x^2) + eps) * w (rms_norm.slang:39-55) when w != null, else
 // y = x; then y * s -> GEMV activation operand: B (hi/lo f16, [K/32][64][8]) and
 // XS (per-32 sums, [K/256][64][8], lanes >= 16 stay zero), where s is the power
-// of two putting max|y * s| in [2^9, 2^10); cs[col] = 1/s. One workgroup per column.
-__global__ __launch_bounds__(256) void k_prep(const float* __restrict__ x, uint32_t K, const float* __restrict__ w,
-                                              float eps, uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
-                                              float* __restrict__ cs) {
-  __shared__ float red[256];
+// of two putting max|y * s| in [2^9, 2^10); cs[col] = 1/s.
+// One workgroup of 1024 threads per column; each thread keeps NV float4 of the
+// column in registers, so x is read once.
+template <int NV>
+__global__ __launch_bounds__(PREP_THREADS) void k_prep(const float* __restrict__ x, uint32_t K,
+                                                       const float* __restrict__ w, float eps,
+                                                       uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
+                                                       float* __restrict__ cs) {
+  __shared__ float red_s[PREP_THREADS / 64], red_m[PREP_THREADS / 64];
   const uint32_t col = blockIdx.x, tid = threadIdx.x;
   const float* xc = x + (size_t)col * K;
-  float scale = 1.f;
-  if (w) {
-    float ss = 0.f;
-    for (uint32_t i = tid; i < K; i += 256) ss += xc[i] * xc[i];
-    red[tid] = ss;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if ((int)tid < s) red[tid] += red[tid + s];
-      __syncthreads();
-    }
-    scale = 1.0f / sqrtf(red[0] / (float)K + eps);
-    __syncthreads();
-  }
-  float mx = 0.f;
-  for (uint32_t i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(w ? xc[i] * scale * w[i] : xc[i]));
-  red[tid] = mx;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-    __syncthreads();
-  }
-  mx = red[0];
-  int ex = 0;
-  if (mx > 0.f && mx < INFINITY) {
-    frexpf(mx, &ex);  // mx = m * 2^ex, m in [0.5, 1)
-    ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
-  }
-  const float ps = ldexpf(1.0f, 10 - ex);  // max|y * ps| in [2^9, 2^10)
-  if (tid == 0) cs[col] = ldexpf(1.0f, ex - 10);
-  const uint32_t c = col;
-  for (uint32_t sb = tid; sb < K / 32; sb += 256) {
-    float sum = 0.f;
+  const uint32_t n4 = K / 4;
+  float4 v[NV];
+  float ss = 0.f, mx = 0.f;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      uint16_t hi[8], lo[8];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const uint32_t k = sb * 32 + 8 * g + t;
-        const float y = (w ? xc[k] * scale * w[k] : xc[k]) * ps;
-        sum += y;
-        const _Float16 h = (_Float16)y;
-        hi[t] = __builtin_bit_cast(uint16_t, h);
-        lo[t] = f2hb(y - (float)h);
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t q = tid + PREP_THREADS * i;
+    if (q < n4) {
+      v[i] = *(const float4*)(xc + 4 * q);
+      ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+      if (w) {
+        const float4 wv = *(const float4*)(w + 4 * q);
+        v[i].x *= wv.x; v[i].y *= wv.y; v[i].z *= wv.z; v[i].w *= wv.w;  // x*w; the 1/rms factor comes later
       }
-      uint16_t* dst = bx + ((size_t)sb * 64 + 16 * g + c) * 8;
-      *(uint4*)dst = *(uint4*)hi;
-      *(uint4*)(dst + 64) = *(uint4*)lo;
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    } else {
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const _Float16 sh = (_Float16)sum;
-    const size_t xo = ((size_t)(sb / 8) * 64 + c) * 8 + (sb % 8);
-    xs[xo] = __builtin_bit_cast(uint16_t, sh);
-    xs[xo + 64] = f2hb(sum - (float)sh);
   }
+  ss = sh_wave_sum(ss);
+  mx = sh_wave_max(mx);
+  if ((tid & 63) == 0) { red_s[tid >> 6] = ss; red_m[tid >> 6] = mx; }
+  __syncthreads();
+  ss = 0.f;
+  mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < PREP_THREADS / 64; ++i) { ss += red_s[i]; mx = fmaxf(mx, red_m[i]); }
+  const float scale = w ? 1.0f / sqrtf(ss / (float)K + eps) : 1.0f;
+  sh_operand_store<NV>(v, K, col, scale, mx, bx, xs, cs);
 }
 
 int sh_prep_launch(sh_engine* e, const float* x, uint32_t K, uint32_t N, const float* norm_w, float eps,
                    uint16_t* bx, uint16_t* xs, float* cs) {
   SH_CHECK(K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", K);
   SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "prep N=%u outside [1, 8]", N);
+  const uint32_t nv = (K / 4 + PREP_THREADS - 1) / PREP_THREADS;
+  SH_CHECK(nv <= 8, SH_ERR_UNSUPPORTED, "prep K=%u above 32768", K);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL(k_prep, dim3(N), dim3(256), 0, e->stream, x, K, norm_w, eps, bx, xs, cs);
+#define PREP(NV_) \
+  hipLaunchKernelGGL((k_prep<NV_>), dim3(N), dim3(PREP_THREADS), 0, e->stream, x, K, norm_w, eps, bx, xs, cs)
+  if (nv <= 1) PREP(1);
+  else if (nv <= 2) PREP(2);
+  else if (nv <= 4) PREP(4);
+  else PREP(8);
+#undef PREP
   SH_HIP(hipGetLastError());
   sh_prof_end(e, norm_w ? "rmsnorm_prep" : "prep", 0.0, ev);
   return SH_OK;

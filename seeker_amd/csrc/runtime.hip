@@ -87,9 +87,17 @@ extern "C" int sh_engine_create(int dev, sh_engine** out) {
   sh_engine* e = new sh_engine();
   e->device = dev;
   hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+  e->gemv_part_floats = (size_t)4 << 20;  // 16 MiB of split-K partials
+  e->gemv_counters_n = 8192;
+  if (err == hipSuccess) err = hipMalloc(&e->gemv_part, e->gemv_part_floats * sizeof(float));
+  if (err == hipSuccess) err = hipMalloc(&e->gemv_counters, e->gemv_counters_n * sizeof(uint32_t));
+  if (err == hipSuccess) err = hipMemset(e->gemv_counters, 0, e->gemv_counters_n * sizeof(uint32_t));
   if (err != hipSuccess) {
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    (void)hipFree(e->gemv_part);
+    (void)hipFree(e->gemv_counters);
     delete e;
-    sh_set_error("hipStreamCreate: %s", hipGetErrorString(err));
+    sh_set_error("engine setup: %s", hipGetErrorString(err));
     return SH_ERR_HIP;
   }
   *out = e;
@@ -102,6 +110,8 @@ extern "C" void sh_engine_destroy(sh_engine* e) {
   (void)hipStreamSynchronize(e->stream);
   for (auto& p : e->pending) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
   for (auto ev : e->event_pool) (void)hipEventDestroy(ev);
+  (void)hipFree(e->gemv_part);
+  (void)hipFree(e->gemv_counters);
   (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -329,7 +339,7 @@ static void free_model(sh_model* m) {
   Workspace& w = m->ws;
   (void)hipFree(w.resid); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
   (void)hipFree(w.attn); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
-  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs);
+  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.fa_counters);
   delete m;
 }
 
@@ -466,10 +476,11 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   if (dalloc(&w.resid, (size_t)8 * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
       dalloc(&w.q, (size_t)8 * m->d) || dalloc(&w.attn, (size_t)8 * m->d) || dalloc(&w.h, (size_t)8 * m->ff) ||
       dalloc(&w.logits, (size_t)8 * m->V) || dalloc(&w.fa_part, part_floats) || dalloc(&w.tokens, 128) ||
-      dalloc(&w.amax, 64) || dalloc(&w.cs, 8))
+      dalloc(&w.amax, 64) || dalloc(&w.cs, 8) || dalloc(&w.fa_counters, SH_FA_MAX_COUNTERS))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
-  if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess)
+  if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess ||
+      hipMemset(w.fa_counters, 0, SH_FA_MAX_COUNTERS * 4) != hipSuccess)
     FAIL(SH_ERR_HIP, "workspace clear failed");
   if ((fail = ensure_rope(m, std::max<uint32_t>(m->n_ctx, 1024)))) FAIL(fail, "%s", sh_last_error());
   if (hipDeviceSynchronize() != hipSuccess) FAIL(SH_ERR_HIP, "model upload failed");
@@ -645,8 +656,7 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
     qkv.layer = l;
     if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
     fa.layer = l;
-    if ((rc = sh_fa_launch(e, m, kv, fa, w.q, w.fa_part, w.attn))) return rc;
-    if ((rc = sh_prep_launch(e, w.attn, m->d, nc, nullptr, 0.f, w.bx, w.xs, w.cs))) return rc;
+    if ((rc = sh_fa_launch(e, m, kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
     if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_ADD, add, "gemv_o"))) return rc;
     if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.ffn_norm, m->eps, w.bx, w.xs, w.cs))) return rc;
     if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;

@@ -44,6 +44,7 @@ constexpr int SH_Q4K_TILE_BYTES = 2304;  // 16 rows x 144 B, repacked
 constexpr int SH_Q8_TILE_BYTES = 544;    // 16 rows x 34 B, repacked
 constexpr int SH_MAX_COLS = 64;          // columns per forward chunk
 constexpr int SH_FA_KEYS_PER_SPLIT = 256;
+constexpr uint32_t SH_FA_MAX_COUNTERS = 1024;  // (kv head, row group) completion counters
 
 // -------------------------------------------------------------- structs
 struct KStat {
@@ -64,6 +65,12 @@ struct sh_engine {
   };
   std::vector<Pending> pending;
   std::vector<hipEvent_t> event_pool;
+  // split-K GEMV scratch: per-split partial sums and per-tile-group counters
+  // (counters are zero between launches; the last workgroup re-arms them).
+  float* gemv_part = nullptr;
+  size_t gemv_part_floats = 0;
+  uint32_t* gemv_counters = nullptr;
+  uint32_t gemv_counters_n = 0;
 };
 
 // A weight matrix on the device, repacked into MFMA tiles.
@@ -103,6 +110,7 @@ struct Workspace {
   uint32_t* tokens = nullptr; // [cols + 16] device token ids
   unsigned long long* amax = nullptr;  // [cols] packed argmax keys
   float* cs = nullptr;        // [8] inverse activation scales of the current B operand
+  uint32_t* fa_counters = nullptr;  // [SH_FA_MAX_COUNTERS], zero between launches
   size_t fa_part_floats = 0;
 };
 
@@ -168,8 +176,10 @@ struct FaArgs {
   uint32_t mask_base = 0;  // keys >= mask_base need their bit in colmask
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 };
+// Attention for the chunk's columns, then the split combine, which writes
+// attn_out [N][n_embd] f32 and the Wo activation operand (bx, xs, cs).
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
-                 float* attn_out);
+                 float* attn_out, uint16_t* bx, uint16_t* xs, float* cs);
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids);
 int sh_kv_compact_launch(sh_engine* e, sh_kv* kv, uint32_t base, const uint32_t* src_dev, uint32_t n);
