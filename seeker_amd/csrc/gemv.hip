@@ -48,15 +48,19 @@ __device__ __forceinline__ h8 q4_operand(uint32_t w, h2 mult, h2 add) {
   return as_h8(r);
 }
 
-// int8 pairs -> f16 exact: (q ^ 0x80) + 1024 as f16, minus 1152.
+// int8 pairs -> f16 exact: (q ^ 0x80) + 1024 as f16, minus 1152. The
+// activation operand carries a 1/16 factor at k with t % 4 >= 2 (see
+// q4_operand2), so those pairs become 16 q = 16 (1024 + u) - 18432, still exact.
 __device__ __forceinline__ h8 q8_operand(uint32_t w0, uint32_t w1) {
   const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  const h2 k16 = {(_Float16)16.0f, (_Float16)16.0f};
+  const h2 off16 = {(_Float16)-18432.0f, (_Float16)-18432.0f};
   uint32_t a = w0 ^ 0x80808080u, b = w1 ^ 0x80808080u;
   u32x4 r;
   r.x = as_u32(as_h2(((a & 0xFFu) | ((a & 0xFF00u) << 8)) | 0x64006400u) + off);
-  r.y = as_u32(as_h2((((a >> 16) & 0xFFu) | ((a >> 8) & 0xFF0000u)) | 0x64006400u) + off);
+  r.y = as_u32(__builtin_elementwise_fma(as_h2((((a >> 16) & 0xFFu) | ((a >> 8) & 0xFF0000u)) | 0x64006400u), k16, off16));
   r.z = as_u32(as_h2(((b & 0xFFu) | ((b & 0xFF00u) << 8)) | 0x64006400u) + off);
-  r.w = as_u32(as_h2((((b >> 16) & 0xFFu) | ((b >> 8) & 0xFF0000u)) | 0x64006400u) + off);
+  r.w = as_u32(__builtin_elementwise_fma(as_h2((((b >> 16) & 0xFFu) | ((b >> 8) & 0xFF0000u)) | 0x64006400u), k16, off16));
   return as_h8(r);
 }
 
@@ -193,33 +197,154 @@ __device__ __forceinline__ Q4Tile load_q4_tile(const uint8_t* base, int lane, in
   return a;
 }
 
+// (a & mask) | (b & ~mask) in one v_bfi_b32 (the mask lives in an SGPR; a
+// VOP3 encoding cannot take two literal constants).
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm volatile("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+  return r;
+}
+
+// Four f16 pairs from one repacked word w (pair i: t = 2i at bits 4i, t = 2i+1
+// at bits 16+4i). Pairs 0 and 2 become 1024 + q, pairs 1 and 3 (nibbles in
+// bits 4-7 of each half) 1024 + 16q; the activation operand carries a 1/16
+// factor at those k (t % 4 >= 2), so one (mult, add) serves all four:
+// (1024 + c q) sc - 1024 sc = c sc q exactly (single rounding of an exact value).
+__device__ __forceinline__ h8 q4_operand2(uint32_t w, uint32_t magic, h2 mult, h2 add) {
+  const uint32_t w8 = w >> 8;
+  u32x4 r;
+  r.x = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x000F000Fu, w, magic)), mult, add));
+  r.y = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x00F000F0u, w, magic)), mult, add));
+  r.z = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x000F000Fu, w8, magic)), mult, add));
+  r.w = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x00F000F0u, w8, magic)), mult, add));
+  return as_h8(r);
+}
+
+// f16 pair (1024 + byte_i, 1024 + byte_j) of a word of small integers:
+// v_perm picks bytes of {magic, w}; selector 5 is magic's byte 1 (0x64).
+__device__ __forceinline__ h2 magic_pair(uint32_t w, uint32_t magic, uint32_t i, uint32_t j) {
+  return as_h2(__builtin_amdgcn_perm(magic, w, i | (5u << 8) | (j << 16) | (5u << 24)));
+}
+
 // y[j] += d * sum_s sc_s * q.x - dmin * sum_s m_s * xsum_s for rows 4g+j.
 __device__ __forceinline__ void q4_tile_mma(const Q4Tile& a, const h8* bq, h8 bm, f4& y) {
   const uint32_t sc03 = a.s0 & 0x3F3F3F3Fu, m03 = a.s1 & 0x3F3F3F3Fu;
   const uint32_t sc47 = (a.s2 & 0x0F0F0F0Fu) | ((a.s0 >> 2) & 0x30303030u);
   const uint32_t m47 = ((a.s2 >> 4) & 0x0F0F0F0Fu) | ((a.s1 >> 2) & 0x30303030u);
   const uint32_t words[8] = {a.q0.x, a.q0.y, a.q0.z, a.q0.w, a.q1.x, a.q1.y, a.q1.z, a.q1.w};
+  const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);  // f16 1024 in both halves
   const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
   f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    const h2 mult = pair_of(m < 4 ? sc03 : sc47, m & 3);
+    const h2 mult = magic_pair(m < 4 ? sc03 : sc47, magic, m & 3, m & 3) + k1024;  // (sc, sc)
     const h2 add = mult * k1024;
-    acc = mfma16(q4_operand(words[m], mult, add), bq[m], acc);
+    acc = mfma16(q4_operand2(words[m], magic, mult, add), bq[m], acc);
   }
   // Minimum term: A = m_s (every lane group holds the row's m, but B = XS is
   // zero outside lane group 0, so only k = s of group 0 contributes).
   u32x4 am;
-  am.x = as_u32(h2{(_Float16)(float)(m03 & 0xFF), (_Float16)(float)((m03 >> 8) & 0xFF)});
-  am.y = as_u32(h2{(_Float16)(float)((m03 >> 16) & 0xFF), (_Float16)(float)(m03 >> 24)});
-  am.z = as_u32(h2{(_Float16)(float)(m47 & 0xFF), (_Float16)(float)((m47 >> 8) & 0xFF)});
-  am.w = as_u32(h2{(_Float16)(float)((m47 >> 16) & 0xFF), (_Float16)(float)(m47 >> 24)});
+  am.x = as_u32(magic_pair(m03, magic, 0, 1) + k1024);
+  am.y = as_u32(magic_pair(m03, magic, 2, 3) + k1024);
+  am.z = as_u32(magic_pair(m47, magic, 0, 1) + k1024);
+  am.w = as_u32(magic_pair(m47, magic, 2, 3) + k1024);
   const f4 macc = mfma16(as_h8(am), bm, f4{0.f, 0.f, 0.f, 0.f});
   const uint32_t ddw[4] = {a.dd.x, a.dd.y, a.dd.z, a.dd.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const float d = (float)as_h2(ddw[j]).x, dmin = (float)as_h2(ddw[j]).y;
     y[j] = y[j] + d * acc[j] - dmin * macc[j];
+  }
+}
+
+// Q4_K GEMV, streaming form: a workgroup of GW = 8 waves owns T row tiles for
+// all of K. Wave w walks superblocks b = w, w + 8, ... and, inside each, the T
+// tiles (one activation operand load serves T weight tiles). The next unit's
+// weights are always in flight while the current one computes, so a wave pays
+// the HBM latency once, not once per unit. The 8 partial sums of each tile meet
+// in LDS at the end; no state is shared between workgroups.
+constexpr int GW = 8;
+template <int T, int EPI>
+__global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                       const uint16_t* __restrict__ Bx,
+                                                       const uint16_t* __restrict__ XS, uint32_t N, EpiArgs ea) {
+  constexpr int CH = T < 4 ? T : 4;  // tiles reduced per LDS round
+  __shared__ f4 red[CH][GW][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar address math
+  const int g = lane >> 4, r = lane & 15;
+  const uint32_t tile0 = blockIdx.x * T;
+  f4 y[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
+  auto a_ptr = [&](uint32_t t, uint32_t b) {
+    const uint32_t tile = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
+    return Wp + ((size_t)tile * nsb + b) * SH_Q4K_TILE_BYTES;
+  };
+  // Units run (b, t) with t fastest; two tile buffers alternate so the unit
+  // after the current one is always loading. Blocks of superblocks are taken in
+  // pairs so each buffer's parity is a compile-time constant.
+  const uint32_t nbw = (uint32_t)wave < nsb ? (nsb - 1 - wave) / GW + 1 : 0;
+  Q4Tile st[2];
+  h8 bq[8], bm;
+  auto load_b = [&](uint32_t b) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
+    bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
+  };
+  if (nbw) st[0] = load_q4_tile(a_ptr(0, wave), lane, g, r);
+  for (uint32_t i = 0; i < nbw; i += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t bi = i + h;
+      if (h == 1 && bi >= nbw) break;
+      const uint32_t b = wave + GW * bi;
+      load_b(b);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int par = (h * T + t) & 1;
+        if (t + 1 < T) st[par ^ 1] = load_q4_tile(a_ptr(t + 1, b), lane, g, r);
+        else if (bi + 1 < nbw) st[par ^ 1] = load_q4_tile(a_ptr(0, b + GW), lane, g, r);
+        q4_tile_mma(st[par], bq, bm, y[t]);
+      }
+    }
+  }
+  // Tile partials meet in LDS, CH tiles per round; wave w < CH ends up holding
+  // tile (round * CH + w), or with SwiGLU wave w < CH/2 holds the pair
+  // (gate, up) = tiles (2w, 2w + 1) of the round.
+  const float cs = ea.cs ? ea.cs[r & 7] : 1.0f;
+#pragma unroll
+  for (int c0 = 0; c0 < T; c0 += CH) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) red[i][wave][lane] = y[c0 + i];
+    __syncthreads();
+    if (EPI == EPI_SWIGLU) {
+      if (wave < CH / 2) {
+        f4 vg = {0.f, 0.f, 0.f, 0.f}, vu = {0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < GW; ++w) { vg += red[2 * wave][w][lane]; vu += red[2 * wave + 1][w][lane]; }
+        float og[4], ou[4];
+        for (int j = 0; j < 4; ++j) {
+          og[j] = (vg[j] + __shfl_xor(vg[j], 8)) * cs;
+          ou[j] = (vu[j] + __shfl_xor(vu[j], 8)) * cs;
+        }
+        const uint32_t tg = tile0 + c0 + 2 * wave;
+        if (tg < tiles && r < 8 && (uint32_t)r < N) {
+          const uint32_t row0 = (tg / 2) * 16 + 4 * g;
+          for (int j = 0; j < 4; ++j) {
+            const float x = og[j];
+            ea.out[(size_t)r * ea.ldo + row0 + j] = (x / (1.0f + expf(-x))) * ou[j];
+          }
+        }
+      }
+    } else if (wave < CH) {
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < GW; ++w) v += red[wave][w][lane];
+      float o[4];
+      for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * cs;
+      const uint32_t tile = tile0 + c0 + wave;
+      if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
+    }
+    __syncthreads();
   }
 }
 
@@ -480,11 +605,57 @@ static void launch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t 
 // workgroup and 8 waves splitting K; large-M ones share each activation stage
 // across 2-4 tiles per wave; gate/up waves own (gate, up) tile pairs.
 template <int EPI>
-static int dispatch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                        const EpiArgs& ea) {
+static int dispatch_q4k_blocked(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                                const EpiArgs& ea) {
   if (EPI == EPI_SWIGLU) return launch_q4k<2, 8, EPI>(e, w, bx, xs, N, ea);
   if (w.tiles >= 1024) return launch_q4k<2, 4, EPI>(e, w, bx, xs, N, ea);
   return launch_q4k<1, 8, EPI>(e, w, bx, xs, N, ea);
+}
+
+template <int T, int EPI>
+static int launch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                      const EpiArgs& ea) {
+  const uint32_t grid = (w.tiles + T - 1) / T;
+  hipLaunchKernelGGL((k_gemv_q4s<T, EPI>), dim3(grid), dim3(64 * GW), 0, e->stream, w.d, w.tiles, w.K / 256, bx, xs,
+                     N, ea);
+  return SH_OK;
+}
+
+// Tuning overrides (read once): SH_GEMV_KERNEL=blocked|stream, SH_GEMV_T=1..16.
+static int gemv_kernel_choice() {
+  static int v = [] {
+    const char* s = getenv("SH_GEMV_KERNEL");
+    return (s && std::string(s) == "blocked") ? 1 : 0;
+  }();
+  return v;
+}
+static uint32_t gemv_t_override() {
+  static uint32_t v = [] {
+    const char* s = getenv("SH_GEMV_T");
+    return s ? (uint32_t)atoi(s) : 0u;
+  }();
+  return v;
+}
+
+// Streaming policy: about 512 workgroups of 8 waves (two per CU), i.e. T =
+// tiles / 512 rounded down to a power of two in [1, 16] (even for SwiGLU so a
+// workgroup owns whole gate/up pairs).
+template <int EPI>
+static int dispatch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                        const EpiArgs& ea) {
+  if (gemv_kernel_choice() == 1) return dispatch_q4k_blocked<EPI>(e, w, bx, xs, N, ea);
+  uint32_t t = gemv_t_override();
+  if (!t) {
+    t = 1;
+    while (t < 8 && w.tiles / (2 * t) >= 512) t *= 2;
+  }
+  if (EPI == EPI_SWIGLU && t < 2) t = 2;
+  switch (t) {
+    case 1: return launch_q4s<1, EPI>(e, w, bx, xs, N, ea);
+    case 2: return launch_q4s<2, EPI>(e, w, bx, xs, N, ea);
+    case 4: return launch_q4s<4, EPI>(e, w, bx, xs, N, ea);
+    default: return launch_q4s<8, EPI>(e, w, bx, xs, N, ea);
+  }
 }
 template <int EPI>
 static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {

@@ -42,9 +42,12 @@ __device__ __forceinline__ void sh_operand_store(const float4 (&v)[NV], uint32_t
     float sum = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const _Float16 h = (_Float16)y[t];
+      // elements 2, 3 of every 4 carry an exact 1/16: the Q4_K kernel decodes
+      // their nibbles as 1024 + 16 q (see q4_operand2 in gemv.hip)
+      const float yt = t >= 2 ? y[t] * 0.0625f : y[t];
+      const _Float16 h = (_Float16)yt;
       hi[t] = __builtin_bit_cast(uint16_t, h);
-      lo[t] = __builtin_bit_cast(uint16_t, (_Float16)(y[t] - (float)h));
+      lo[t] = __builtin_bit_cast(uint16_t, (_Float16)(yt - (float)h));
       sum += y[t];
     }
     // 8 consecutive threads cover one 32-element sub-block
