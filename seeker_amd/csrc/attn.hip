@@ -7,16 +7,19 @@
 // flash_attn_split_k_reduce.slang. Tree verify replaces the causal triangle by
 // an ancestor-or-self bitmask per query column (new).
 //
-// Design (gfx950): one workgroup = (kv head, 256-key split, group of 16*QT
-// query rows); its 4 waves take 64 keys each and issue all their K and V loads
-// up front. The GQA rows of one kv head (gqa heads x N columns) share every K/V
-// tile, so K and V are read once per kv head. S^T = K Q^T and O^T = V^T P^T run
-// on v_mfma_f32_16x16x32_f16; Q and P are split into hi + lo f16 halves so the
+// Design (gfx950): one workgroup = (kv head, key split, group of 16*QT query
+// rows); each of its W waves takes NH 32-key blocks of the split. A wave issues
+// its query loads and then every K and V load of its keys before it waits on
+// any of them, so one HBM latency covers the whole split. The GQA rows of one
+// kv head (gqa heads x N columns) share every K/V tile, so K and V are read
+// once per kv head. S^T = K Q^T and O^T = V^T P^T run on
+// v_mfma_f32_16x16x32_f16; Q and P are split into hi + lo f16 halves so the
 // products keep ~22 bits (K and V are exact f16). V is stored per 32-key block
 // transposed ([hd][32 slots], slot order v_slot()) so the V^T operand is a
 // contiguous 16-byte load. A second kernel combines the splits in split order
 // (deterministic) per column and builds the Wo activation operand.
 #include <cfloat>
+#include <cstdlib>
 
 #include "sh_internal.h"
 #include "sh_operand.h"
@@ -40,36 +43,72 @@ __device__ __forceinline__ void split8(const float* x, h8& hi, h8& lo) {
   }
 }
 
-constexpr uint32_t FA_WAVE_KEYS = 64;
-constexpr uint32_t FA_SPLIT_KEYS = 4 * FA_WAVE_KEYS;
-static_assert(FA_SPLIT_KEYS == SH_FA_KEYS_PER_SPLIT, "split size");
+// colmask[col] by selects: a dynamic index into the kernel arguments would
+// become a memory load on the critical path.
+__device__ __forceinline__ uint64_t col_mask(const FaArgs& fa, uint32_t col) {
+  uint64_t v = fa.colmask[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) v = col == (uint32_t)i ? fa.colmask[i] : v;
+  return v;
+}
 
-template <int QT, int HD>
-__global__ __launch_bounds__(256) void k_fa(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                            const uint16_t* __restrict__ vc, uint32_t max_seq, uint32_t n_head,
-                                            uint32_t N, uint32_t gqa, FaArgs fa, float scale,
-                                            float* __restrict__ part) {
+// Partial of split `split` for padded row rho:
+// part[((kh * n_splits + split) * n_rows_pad + rho) * PS + {d < HD: O, HD: m, HD+1: l, pad}].
+template <int QT, int HD, int W, int NH>
+__global__ __launch_bounds__(64 * W) void k_fa(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                               const uint16_t* __restrict__ vc, uint32_t max_seq, uint32_t n_head,
+                                               uint32_t N, uint32_t gqa, FaArgs fa, float scale,
+                                               float* __restrict__ part) {
   constexpr int NC = HD / 32;  // d chunks of the QK contraction
   constexpr int DT = HD / 16;  // d tiles of the output
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int ROWS = 16 * QT;
+  constexpr uint32_t WAVE_KEYS = 32 * NH, SPLIT_KEYS = W * WAVE_KEYS, PS = sh_fa_part_stride(HD);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, r = lane & 15;
   const uint32_t kh = blockIdx.x, split = blockIdx.y, qg = blockIdx.z;
   const uint32_t n_splits = gridDim.y;
   const uint32_t n_rows = gqa * N;
-  const uint32_t n_rows_pad = gridDim.z * 16 * QT;
+  const uint32_t n_rows_pad = gridDim.z * ROWS;
   const uint32_t Dq = n_head * HD;
+
+  // Query rows: lane (g, r) holds rho = 16*qt + r, d = 32c + 8g .. +8. Rows past
+  // n_rows read row 0 and are zeroed.
+  const float* qp[QT];
+  uint32_t rowcol[QT];
+  float rz[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const uint32_t rho = qg * ROWS + 16 * qt + r;
+    const bool ok = rho < n_rows;
+    const uint32_t hq = ok ? rho / N : 0, col = ok ? rho % N : 0;
+    rowcol[qt] = col;
+    rz[qt] = ok ? 1.0f : 0.0f;
+    qp[qt] = q + (size_t)col * Dq + (size_t)(kh * gqa + hq) * HD + 8 * g;
+  }
+  // This wave's keys: blocks past the split's end read clamped (in-bounds) rows
+  // and are masked out below.
+  const uint32_t k_end = min((split + 1) * SPLIT_KEYS, fa.kvlen);
+  const uint32_t kw = split * SPLIT_KEYS + WAVE_KEYS * wave;
   const uint16_t* kbase = kc + (size_t)kh * max_seq * HD;
   const uint16_t* vbase = vc + (size_t)kh * (max_seq / 32) * HD * 32;
 
-  // Issue this wave's K and V loads for its (up to) two 32-key halves first.
-  const uint32_t k_end = min((split + 1) * FA_SPLIT_KEYS, fa.kvlen);
-  const uint32_t kw = split * FA_SPLIT_KEYS + FA_WAVE_KEYS * wave;
-  const bool hv0 = kw < k_end, hv1 = kw + 32 < k_end;
-  h8 kop[2][2][NC], vop[2][DT];
+  // Every load of the workgroup's inputs is issued before any is used: Q rows,
+  // then K and V. There is no branch between the loads and their uses, and the
+  // scheduling barrier keeps them from being sunk, so the split costs one
+  // memory latency.
+  float4 qraw[QT][NC][2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    if (h == 0 ? !hv0 : !hv1) continue;
-    const uint32_t key0 = kw + 32 * h;
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qraw[qt][c][0] = *(const float4*)(qp[qt] + 32 * c);
+      qraw[qt][c][1] = *(const float4*)(qp[qt] + 32 * c + 4);
+    }
+  h8 kop[NH][2][NC], vop[NH][DT];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const uint32_t key0 = min(kw + 32 * h, max_seq - 32);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -78,28 +117,26 @@ __global__ __launch_bounds__(256) void k_fa(const float* __restrict__ q, const u
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) vop[h][dt] = ld_h8(vp + (size_t)dt * 16 * 32);
   }
+  uint64_t cm[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) cm[qt] = col_mask(fa, rowcol[qt]);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // Q^T operands (B): lane (g, r) holds rho = 16*qt + r, d = 32c + 8g .. +8.
-  // Each query row is scaled by a power of two (max|q * s| in [2^9, 2^10)) so
-  // the f16 low halves stay normal; rscale folds 1/s into the score scale.
+  // Q^T operands (B). Each query row is scaled by a power of two (max|q * s| in
+  // [2^9, 2^10)) so the f16 low halves stay normal; rscale folds 1/s into the
+  // score scale.
   h8 qhi[QT][NC], qlo[QT][NC];
-  uint32_t rowcol[QT];
   float rscale[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const uint32_t rho = qg * 16 * QT + 16 * qt + r;
-    const bool ok = rho < n_rows;
-    const uint32_t hq = ok ? rho / N : 0, col = ok ? rho % N : 0;
-    rowcol[qt] = col;
-    const float* qp = q + (size_t)col * Dq + (size_t)(kh * gqa + hq) * HD;
     float x[NC][8];
     float mx = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const float4 a = ok ? *(const float4*)(qp + 32 * c + 8 * g) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 b = ok ? *(const float4*)(qp + 32 * c + 8 * g + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-      x[c][0] = a.x; x[c][1] = a.y; x[c][2] = a.z; x[c][3] = a.w;
-      x[c][4] = b.x; x[c][5] = b.y; x[c][6] = b.z; x[c][7] = b.w;
+      const float4 a = qraw[qt][c][0], b = qraw[qt][c][1];
+      const float z = rz[qt];
+      x[c][0] = a.x * z; x[c][1] = a.y * z; x[c][2] = a.z * z; x[c][3] = a.w * z;
+      x[c][4] = b.x * z; x[c][5] = b.y * z; x[c][6] = b.z * z; x[c][7] = b.w * z;
 #pragma unroll
       for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(x[c][t]));
     }
@@ -130,8 +167,7 @@ __global__ __launch_bounds__(256) void k_fa(const float* __restrict__ q, const u
   for (int qt = 0; qt < QT; ++qt) { mrow[qt] = -INFINITY; lrow[qt] = 0.f; }
 
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    if (h == 0 ? !hv0 : !hv1) continue;
+  for (int h = 0; h < NH; ++h) {
     const uint32_t key0 = kw + 32 * h;
     // S^T[key][rho] for keys key0 + 16*kt + 4g + j.
     f4 s[2][QT];
@@ -147,10 +183,9 @@ __global__ __launch_bounds__(256) void k_fa(const float* __restrict__ q, const u
         }
         s[kt][qt] = acc;
       }
-    const bool tail = key0 + 32 > fa.kvlen || key0 + 32 > fa.mask_base;
+    const bool tail = key0 + 32 > k_end || key0 + 32 > fa.mask_base;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const uint64_t cm = fa.colmask[rowcol[qt] & 7];
       float sv[8];
       float mx = -INFINITY;
 #pragma unroll
@@ -160,8 +195,8 @@ __global__ __launch_bounds__(256) void k_fa(const float* __restrict__ q, const u
           float v = s[kt][qt][j] * rscale[qt];
           if (tail) {
             const uint32_t key = key0 + 16 * kt + 4 * g + j;
-            bool vis = key < fa.kvlen;
-            if (vis && key >= fa.mask_base) vis = (cm >> (key - fa.mask_base)) & 1ull;
+            bool vis = key < k_end;
+            if (vis && key >= fa.mask_base) vis = (cm[qt] >> (key - fa.mask_base)) & 1ull;
             if (!vis) v = -INFINITY;
           }
           sv[4 * kt + j] = v;
@@ -170,18 +205,14 @@ __global__ __launch_bounds__(256) void k_fa(const float* __restrict__ q, const u
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float mnew = fmaxf(mrow[qt], mx);
-      float alpha, p[8];
-      if (mnew == -INFINITY) {
-        alpha = 1.f;
+      // nothing visible yet: keep O and l (zero) as they are
+      const bool none = mnew == -INFINITY;
+      const float alpha = none ? 1.0f : expf(mrow[qt] - mnew);
+      // probabilities carry a 2^12 factor (keeps their f16 low halves normal);
+      // it cancels in O / l because l is summed from the same scaled values
+      float p[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) p[t] = 0.f;
-      } else {
-        alpha = expf(mrow[qt] - mnew);
-        // probabilities carry a 2^12 factor (keeps their f16 low halves normal);
-        // it cancels in O / l because l is summed from the same scaled values
-#pragma unroll
-        for (int t = 0; t < 8; ++t) p[t] = expf(sv[t] - mnew) * 4096.0f;
-      }
+      for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : expf(sv[t] - mnew) * 4096.0f;
       mrow[qt] = mnew;
       float ps = 0.f;
 #pragma unroll
@@ -206,103 +237,145 @@ __global__ __launch_bounds__(256) void k_fa(const float* __restrict__ q, const u
     lrow[qt] += __shfl_xor(lrow[qt], 32);
   }
 
-  // Merge the 4 waves through LDS, then write this split's partial:
-  // part[((kh * n_splits + split) * n_rows_pad + rho) * (HD + 2) + {d, HD: m, HD+1: l}].
-  __shared__ float sm[4][QT * 16], sl[4][QT * 16];
-  __shared__ float so[QT * 16][HD + 1];
-  if (g == 0) {
+  // Waves 1..W-1 park (m, l, O) in LDS; wave 0 merges them into its own and
+  // writes the split's partial rows.
+  constexpr int WL = W > 1 ? W - 1 : 1;
+  __shared__ float sm[WL][ROWS], sl[WL][ROWS];
+  __shared__ float so[WL][ROWS][HD + 1];
+  if (W > 1) {
+    if (wave > 0) {
+      if (g == 0) {
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) { sm[wave][16 * qt + r] = mrow[qt]; sl[wave][16 * qt + r] = lrow[qt]; }
-  }
-  __syncthreads();
-  for (int w = 0; w < 4; ++w) {
-    if (wave == w) {
+        for (int qt = 0; qt < QT; ++qt) { sm[wave - 1][16 * qt + r] = mrow[qt]; sl[wave - 1][16 * qt + r] = lrow[qt]; }
+      }
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int rho_l = 16 * qt + r;
-        float M = sm[0][rho_l];
-        for (int v = 1; v < 4; ++v) M = fmaxf(M, sm[v][rho_l]);
-        const float f = (mrow[qt] == -INFINITY) ? 0.f : expf(mrow[qt] - M);
+      for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float* dst = &so[rho_l][16 * dt + 4 * g + j];
-            *dst = (w == 0 ? 0.f : *dst) + o[dt][qt][j] * f;
-          }
-      }
+          for (int j = 0; j < 4; ++j) so[wave - 1][16 * qt + r][16 * dt + 4 * g + j] = o[dt][qt][j];
     }
     __syncthreads();
+    if (wave > 0) return;
   }
-  for (int idx = threadIdx.x; idx < QT * 16 * (HD + 2); idx += 256) {
-    const int rho_l = idx / (HD + 2), e = idx % (HD + 2);
-    float M = sm[0][rho_l];
-    for (int w = 1; w < 4; ++w) M = fmaxf(M, sm[w][rho_l]);
-    float v;
-    if (e < HD) {
-      v = so[rho_l][e];
-    } else if (e == HD) {
-      v = M;
-    } else {
-      v = 0.f;
-      for (int w = 0; w < 4; ++w) v += sm[w][rho_l] == -INFINITY ? 0.f : sl[w][rho_l] * expf(sm[w][rho_l] - M);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int rl = 16 * qt + r;
+    float M = mrow[qt];
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) M = fmaxf(M, sm[w][rl]);
+    const float f0 = mrow[qt] == -INFINITY ? 0.f : expf(mrow[qt] - M);
+    float fw[WL];
+    float L = lrow[qt] * f0;
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) {
+      fw[w] = sm[w][rl] == -INFINITY ? 0.f : expf(sm[w][rl] - M);
+      L += sl[w][rl] * fw[w];
     }
-    const uint32_t rho = qg * 16 * QT + rho_l;
-    part[(((size_t)kh * n_splits + split) * n_rows_pad + rho) * (HD + 2) + e] = v;
+    float* dst = part + (((size_t)kh * n_splits + split) * n_rows_pad + qg * ROWS + rl) * PS;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = o[dt][qt][j] * f0;
+#pragma unroll
+        for (int w = 0; w < W - 1; ++w) v[j] += so[w][rl][16 * dt + 4 * g + j] * fw[w];
+      }
+      *(float4*)(dst + 16 * dt + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (g == 0) *(float4*)(dst + HD) = make_float4(M, L, 0.f, 0.f);
   }
-
 }
 
-// Combine the key splits for every head of one column (in split order), write
-// attn [N][Dq] f32 and build the Wo activation operand from it. One workgroup
-// of 1024 threads per column; thread t owns outputs 4t..4t+3 (+4096 i).
-template <int HD, int NV>
-__global__ __launch_bounds__(SH_OPERAND_THREADS) void k_fa_combine(const float* __restrict__ part, uint32_t n_splits,
-                                                                   uint32_t n_rows_pad, uint32_t n_head, uint32_t N,
-                                                                   uint32_t gqa, float* __restrict__ attn,
-                                                                   uint16_t* __restrict__ bx,
-                                                                   uint16_t* __restrict__ xs, float* __restrict__ cs) {
-  __shared__ float red_m[SH_OPERAND_THREADS / 64];
-  const uint32_t col = blockIdx.x, tid = threadIdx.x;
-  const uint32_t Dq = n_head * HD, n4 = Dq / 4;
-  const size_t sstride = (size_t)n_rows_pad * (HD + 2);
-  float4 v[NV];
-  float mx = 0.f;
+// Combine the key splits (in split order) for one 256-wide superblock of the
+// attention output of one column, write attn [N][Dq] f32 and that superblock of
+// the Wo activation operand. One wave per (superblock, column); lane l owns
+// elements 256 sb + 4l .. +3. The splits are read 8 at a time, every load
+// issued before the first is used.
+template <int HD>
+__global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ part, uint32_t n_splits,
+                                                   uint32_t n_rows_pad, uint32_t n_head, uint32_t N, uint32_t gqa,
+                                                   float* __restrict__ attn, uint16_t* __restrict__ bx,
+                                                   uint16_t* __restrict__ xs, float* __restrict__ cs) {
+  constexpr uint32_t PS = sh_fa_part_stride(HD);
+  constexpr uint32_t CH = 16;
+  const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
+  const uint32_t Dq = n_head * HD;
+  const size_t sstride = (size_t)n_rows_pad * PS;
+  const uint32_t kk = 256 * sb + 4 * lane;
+  const bool valid = kk < Dq;
+  const uint32_t k = valid ? kk : 0, head = k / HD, d = k % HD;
+  const uint32_t kh = head / gqa, rho = (head % gqa) * N + col;
+  const float* p = part + (size_t)kh * n_splits * sstride + (size_t)rho * PS;
+  float M = -INFINITY, L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t s0 = 0; s0 < n_splits; s0 += CH) {
+    float4 os[CH], ml[CH];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    const uint32_t q = tid + SH_OPERAND_THREADS * i;
-    if (q >= n4) continue;
-    const uint32_t k = 4 * q, head = k / HD, d = k % HD;
-    const uint32_t kh = head / gqa, rho = (head % gqa) * N + col;
-    const float* p = part + (size_t)kh * n_splits * sstride + (size_t)rho * (HD + 2);
-    float M = -INFINITY, L = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t s = 0; s < n_splits; ++s, p += sstride) {
-      const float ms = p[HD];
-      if (ms == -INFINITY) continue;
+    for (uint32_t j = 0; j < CH; ++j) {
+      const float* pp = p + (size_t)min(s0 + j, n_splits - 1) * sstride;
+      os[j] = *(const float4*)(pp + d);
+      ml[j] = *(const float4*)(pp + HD);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < CH; ++j) {
+      const float ms = ml[j].x;
+      if (s0 + j >= n_splits || ms == -INFINITY) continue;
       const float mn = fmaxf(M, ms);
       const float a = expf(M - mn), b = expf(ms - mn);  // M = -inf on the first split: a = 0
-      const float4 o = *(const float4*)(p + d);
-      acc.x = acc.x * a + o.x * b;
-      acc.y = acc.y * a + o.y * b;
-      acc.z = acc.z * a + o.z * b;
-      acc.w = acc.w * a + o.w * b;
-      L = L * a + p[HD + 1] * b;
+      acc.x = acc.x * a + os[j].x * b;
+      acc.y = acc.y * a + os[j].y * b;
+      acc.z = acc.z * a + os[j].z * b;
+      acc.w = acc.w * a + os[j].w * b;
+      L = L * a + ml[j].y * b;
       M = mn;
     }
-    const float il = L > 0.f ? 1.0f / L : 0.f;
-    v[i] = make_float4(acc.x * il, acc.y * il, acc.z * il, acc.w * il);
-    *(float4*)(attn + (size_t)col * Dq + k) = v[i];
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
   }
-  mx = sh_wave_max(mx);
-  if ((tid & 63) == 0) red_m[tid >> 6] = mx;
-  __syncthreads();
-  mx = 0.f;
-#pragma unroll
-  for (int i = 0; i < SH_OPERAND_THREADS / 64; ++i) mx = fmaxf(mx, red_m[i]);
-  sh_operand_store<NV>(v, Dq, col, 1.0f, mx, bx, xs, cs);
+  const float il = L > 0.f ? 1.0f / L : 0.f;
+  float4 v = make_float4(acc.x * il, acc.y * il, acc.z * il, acc.w * il);
+  if (valid) *(float4*)(attn + (size_t)col * Dq + k) = v;
+  else v = make_float4(0.f, 0.f, 0.f, 0.f);
+  sh_operand_store_sb(v, Dq, sb, col, bx, xs, cs);
+}
+
+// Keys per split: SH_FA_SPLIT=64|128|256|512 overrides; by default the largest
+// split that still gives >= 256 workgroups (every CU busy), 64 at least.
+static uint32_t fa_split_keys(uint32_t n_kv, uint32_t kvlen, uint32_t n_qg) {
+  static const uint32_t forced = [] {
+    const char* s = getenv("SH_FA_SPLIT");
+    const uint32_t v = s ? (uint32_t)atoi(s) : 0u;
+    return (v == 64 || v == 128 || v == 256 || v == 512) ? v : 0u;
+  }();
+  if (forced) return forced;
+  for (uint32_t sk = 256; sk > 64; sk /= 2)
+    if ((size_t)n_kv * n_qg * ((kvlen + sk - 1) / sk) >= 256) return sk;
+  return 64;
+}
+
+// SH_FA_WAVES=8: 256-key splits as 8 waves of 32 keys (default 4 waves of 64).
+static bool fa_wide() {
+  static const bool v = [] {
+    const char* s = getenv("SH_FA_WAVES");
+    return s && atoi(s) == 8;
+  }();
+  return v;
+}
+
+template <int QT, int HD>
+static void fa_launch_split(uint32_t split_keys, dim3 grid, hipStream_t st, const float* q, const uint16_t* kc,
+                            const uint16_t* vc, uint32_t max_seq, uint32_t n_head, uint32_t N, uint32_t gqa,
+                            const FaArgs& fa, float scale, float* part) {
+  if (split_keys == 512)
+    hipLaunchKernelGGL((k_fa<QT, HD, 8, 2>), grid, dim3(512), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
+  else if (split_keys == 256 && fa_wide())
+    hipLaunchKernelGGL((k_fa<QT, HD, 8, 1>), grid, dim3(512), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
+  else if (split_keys == 256)
+    hipLaunchKernelGGL((k_fa<QT, HD, 4, 2>), grid, dim3(256), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
+  else if (split_keys == 128)
+    hipLaunchKernelGGL((k_fa<QT, HD, 4, 1>), grid, dim3(256), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
+  else
+    hipLaunchKernelGGL((k_fa<QT, HD, 2, 1>), grid, dim3(128), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
 }
 
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
@@ -311,45 +384,43 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   const uint32_t n_rows = gqa * fa.N;
   const int QT = n_rows > 16 ? 2 : 1;
   const uint32_t n_qg = (n_rows + 16 * QT - 1) / (16 * QT);
-  const uint32_t n_splits = (fa.kvlen + FA_SPLIT_KEYS - 1) / FA_SPLIT_KEYS;
-  const size_t need = (size_t)m->n_kv * n_splits * n_qg * 16 * QT * (m->hd + 2);
+  SH_CHECK(n_qg * 16 * QT <= (uint32_t)SH_FA_MAX_ROWS, SH_ERR_UNSUPPORTED, "%u query rows per kv head above %d",
+           n_rows, SH_FA_MAX_ROWS);
+  SH_CHECK(fa.kvlen > 0, SH_ERR_ARG, "attention over zero keys");
+  const uint32_t split_keys = fa_split_keys(m->n_kv, fa.kvlen, n_qg);
+  const uint32_t n_splits = (fa.kvlen + split_keys - 1) / split_keys;
+  const uint32_t rows_pad = n_qg * 16 * QT;
+  const size_t need = (size_t)m->n_kv * n_splits * rows_pad * sh_fa_part_stride(m->hd);
   SH_CHECK(need <= m->ws.fa_part_floats, SH_ERR_CAPACITY, "attention partial buffer too small (%zu > %zu)", need,
            m->ws.fa_part_floats);
-  SH_CHECK(kv->max_seq % 32 == 0, SH_ERR_ARG, "kv max_seq must be a multiple of 32");
-  SH_CHECK(m->d <= 4 * SH_OPERAND_THREADS * 2, SH_ERR_UNSUPPORTED, "n_embd %u above 8192", m->d);
+  SH_CHECK(kv->max_seq % 32 == 0 && kv->max_seq >= 32, SH_ERR_ARG, "kv max_seq must be a positive multiple of 32");
   const size_t layer_k = (size_t)m->n_kv * kv->max_seq * m->hd;
   const uint16_t* kc = kv->k + layer_k * fa.layer;
   const uint16_t* vc = kv->v + layer_k * fa.layer;
   const float scale = 1.0f / sqrtf((float)m->hd);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  dim3 grid(m->n_kv, n_splits, n_qg);
-#define FA_LAUNCH(QT_, HD_)                                                                                  \
-  hipLaunchKernelGGL((k_fa<QT_, HD_>), grid, dim3(256), 0, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, \
-                     gqa, fa, scale, part)
+  const dim3 grid(m->n_kv, n_splits, n_qg);
   if (m->hd == 128) {
-    if (QT == 2) FA_LAUNCH(2, 128); else FA_LAUNCH(1, 128);
+    if (QT == 2) fa_launch_split<2, 128>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
+    else fa_launch_split<1, 128>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
   } else if (m->hd == 64) {
-    if (QT == 2) FA_LAUNCH(2, 64); else FA_LAUNCH(1, 64);
+    if (QT == 2) fa_launch_split<2, 64>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
+    else fa_launch_split<1, 64>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
   } else {
     SH_CHECK(false, SH_ERR_UNSUPPORTED, "head_dim %u not supported (64, 128)", m->hd);
   }
-#undef FA_LAUNCH
   SH_HIP(hipGetLastError());
   const double kv_bytes = 2.0 * m->n_kv * (double)fa.kvlen * m->hd * 2.0;
   sh_prof_end(e, "attention", kv_bytes, ev);
   sh_prof_begin(e, &ev);
-  const uint32_t rows_pad = n_qg * 16 * QT;
-  const bool two = m->d > 4 * SH_OPERAND_THREADS;
-#define FC_LAUNCH(HD_, NV_)                                                                                    \
-  hipLaunchKernelGGL((k_fa_combine<HD_, NV_>), dim3(fa.N), dim3(SH_OPERAND_THREADS), 0, e->stream, part, n_splits, \
-                     rows_pad, m->n_head, fa.N, gqa, attn_out, bx, xs, cs)
-  if (m->hd == 128) {
-    if (two) FC_LAUNCH(128, 2); else FC_LAUNCH(128, 1);
-  } else {
-    if (two) FC_LAUNCH(64, 2); else FC_LAUNCH(64, 1);
-  }
-#undef FC_LAUNCH
+  const dim3 cgrid((m->n_head * m->hd + 255) / 256, fa.N);
+  if (m->hd == 128)
+    hipLaunchKernelGGL((k_fa_combine<128>), cgrid, dim3(64), 0, e->stream, part, n_splits, rows_pad, m->n_head, fa.N,
+                       gqa, attn_out, bx, xs, cs);
+  else
+    hipLaunchKernelGGL((k_fa_combine<64>), cgrid, dim3(64), 0, e->stream, part, n_splits, rows_pad, m->n_head, fa.N,
+                       gqa, attn_out, bx, xs, cs);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "attn_combine", 0.0, ev);
   return SH_OK;

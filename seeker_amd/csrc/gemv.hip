@@ -7,18 +7,30 @@
 // columns. Design here (not a translation):
 //   * Weights are repacked once at upload into 16-row tiles so each lane of a
 //     wave64 reads its MFMA A-operand bytes with two 16-byte loads.
-//   * Q4_K nibbles become exact f16 integers sc*q (<= 945) via the 0x6400 magic
-//     exponent and one packed FMA; d and dmin are applied per 256-superblock in f32.
+//   * Q4_K nibbles become exact f16 integers c*sc*q (c = 1 or 16) via the
+//     0x6400 magic exponent and one packed FMA; d and dmin are applied per
+//     256-superblock in f32.
 //   * Activations are split x = hi + lo (two f16) and fed as 16 MFMA columns
 //     (8 hi + 8 lo), so v_mfma_f32_16x16x32_f16 keeps ~22 bits of x and f32
-//     accumulation at no extra MFMA cost for N <= 8.
+//     accumulation at no extra MFMA cost for N <= 8. Each superblock of each
+//     column carries its own power-of-two scale (cs), undone per superblock.
 //   * The Q4_K minimum term dmin * sum_s m_s * sum(x in s) is a ninth MFMA per
 //     superblock against per-sub-block column sums (XS).
+//   * Two Q4_K kernels: "wide" (8 waves own 8T different row tiles over one
+//     K-split whose activation operand sits in LDS, loaded once by direct
+//     global->LDS loads and read by all 8 waves; split-K partial sums are
+//     finished by the consumer) and "stream" (one workgroup owns T tiles over
+//     all of K, its 8 waves split K; for epilogues that need whole sums).
+#include <cstdlib>
+#include <string>
+
 #include "sh_internal.h"
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
 struct alignas(16) u32x4 { uint32_t x, y, z, w; };
 
@@ -31,26 +43,9 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// (v, v) as an f16 pair from a small non-negative integer byte.
-__device__ __forceinline__ h2 pair_of(uint32_t word, int byte) {
-  float f = (float)((word >> (8 * byte)) & 0xFFu);
-  return h2{(_Float16)f, (_Float16)f};
-}
-
-// Four f16 pairs (1024 + q) from the nibbles of one repacked word, then
-// (1024 + q) * sc - 1024 * sc = sc * q exactly (single rounding of an exact value).
-__device__ __forceinline__ h8 q4_operand(uint32_t w, h2 mult, h2 add) {
-  u32x4 r;
-  r.x = as_u32(__builtin_elementwise_fma(as_h2((w & 0x000F000Fu) | 0x64006400u), mult, add));
-  r.y = as_u32(__builtin_elementwise_fma(as_h2(((w >> 4) & 0x000F000Fu) | 0x64006400u), mult, add));
-  r.z = as_u32(__builtin_elementwise_fma(as_h2(((w >> 8) & 0x000F000Fu) | 0x64006400u), mult, add));
-  r.w = as_u32(__builtin_elementwise_fma(as_h2(((w >> 12) & 0x000F000Fu) | 0x64006400u), mult, add));
-  return as_h8(r);
-}
-
 // int8 pairs -> f16 exact: (q ^ 0x80) + 1024 as f16, minus 1152. The
-// activation operand carries a 1/16 factor at k with t % 4 >= 2 (see
-// q4_operand2), so those pairs become 16 q = 16 (1024 + u) - 18432, still exact.
+// activation operand carries a 1/16 factor at k with k % 4 >= 2, so those
+// pairs become 16 q = 16 (1024 + u) - 18432, still exact.
 __device__ __forceinline__ h8 q8_operand(uint32_t w0, uint32_t w1) {
   const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
   const h2 k16 = {(_Float16)16.0f, (_Float16)16.0f};
@@ -72,7 +67,9 @@ __device__ __forceinline__ uint32_t v_slot(uint32_t kappa) {
 
 // ------------------------------------------------------------------ repack
 
-// Q4_K tile-superblock (2304 B): [0,2048) 64 lanes x 8 words; lane l (row l%16,
+// Q4_K tile-superblock (2304 B): [0,2048) 8 words per lane, words 0-3 of lane l
+// at 16 l and words 4-7 at 1024 + 16 l (each 16-byte load of a wave reads 1 KB
+// contiguous); lane l (row l%16,
 // group g=l/16), word m (sub-block m) holds q[32m + 8g + t], t=0..7, pair i=t/2:
 // t even at bits 4i, t odd at bits 16+4i. [2048,2112) d|dmin<<16 per row;
 // [2112,2304) the 12 packed scale bytes per row.
@@ -108,8 +105,10 @@ __global__ void k_repack_q4k(const uint8_t* __restrict__ src, uint8_t* __restric
       for (int i = 0; i < 12; ++i) out[2112 + 12 * r + i] = 0;
     }
   }
-  uint32_t* o = (uint32_t*)(out + 32 * l);
-  for (int m = 0; m < 8; ++m) o[m] = words[m];
+  uint32_t* o = (uint32_t*)(out + 16 * l);
+  for (int m = 0; m < 4; ++m) o[m] = words[m];
+  o = (uint32_t*)(out + 1024 + 16 * l);
+  for (int m = 0; m < 4; ++m) o[m] = words[4 + m];
 }
 
 // Q8_0 tile-block (544 B): [0,512) 64 lanes x 8 int8 (row l%16, k = 32b + 8g + t);
@@ -129,14 +128,18 @@ __global__ void k_repack_q8(const uint8_t* __restrict__ src, uint8_t* __restrict
   }
 }
 
+
 // ------------------------------------------------------------------ epilogue
 
 __device__ __forceinline__ uint16_t f2h_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
 
-// Final (row, col) value for rows r0..r0+3 (one lane), col < N.
+// Final (row, col) value for rows r0..r0+3 (one lane), col < N; ks = split.
 template <int EPI>
-__device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32_t col, const float v[4]) {
-  if (EPI == EPI_STORE) {
+__device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32_t col, const float v[4],
+                                          uint32_t ks = 0) {
+  if (EPI == EPI_PART) {
+    *(float4*)(ea.out + ks * ea.part_stride + (size_t)col * ea.ldo + r0) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (EPI == EPI_STORE) {
     for (int j = 0; j < 4; ++j)
       if (r0 + j < ea.rows) ea.out[(size_t)col * ea.ldo + r0 + j] = v[j];
   } else if (EPI == EPI_ADD) {
@@ -177,7 +180,17 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32
   }
 }
 
-// ------------------------------------------------------------------ kernels
+// SwiGLU of a (gate, up) tile pair: h[col][16 pair + 4g + j] = silu(g) * u.
+__device__ __forceinline__ void swiglu4(const EpiArgs& ea, uint32_t pair, uint32_t g, uint32_t col, const float og[4],
+                                        const float ou[4]) {
+  const uint32_t row0 = pair * 16 + 4 * g;
+  for (int j = 0; j < 4; ++j) {
+    const float x = og[j];
+    ea.out[(size_t)col * ea.ldo + row0 + j] = (x / (1.0f + expf(-x))) * ou[j];
+  }
+}
+
+// ------------------------------------------------------------------ Q4_K core
 
 // One wave's operands for one 16-row tile and one 256-element superblock.
 struct Q4Tile {
@@ -187,8 +200,8 @@ struct Q4Tile {
 
 __device__ __forceinline__ Q4Tile load_q4_tile(const uint8_t* base, int lane, int g, int r) {
   Q4Tile a;
-  a.q0 = ld16(base + 32 * lane);
-  a.q1 = ld16(base + 32 * lane + 16);
+  a.q0 = ld16(base + 16 * lane);
+  a.q1 = ld16(base + 1024 + 16 * lane);
   a.dd = ld16(base + 2048 + 16 * g);
   const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
   a.s0 = sp[0];
@@ -208,8 +221,9 @@ __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
 // Four f16 pairs from one repacked word w (pair i: t = 2i at bits 4i, t = 2i+1
 // at bits 16+4i). Pairs 0 and 2 become 1024 + q, pairs 1 and 3 (nibbles in
 // bits 4-7 of each half) 1024 + 16q; the activation operand carries a 1/16
-// factor at those k (t % 4 >= 2), so one (mult, add) serves all four:
+// factor at those k (k % 4 >= 2), so one (mult, add) serves all four:
 // (1024 + c q) sc - 1024 sc = c sc q exactly (single rounding of an exact value).
+// `magic` holds f16 1024 in both halves.
 __device__ __forceinline__ h8 q4_operand2(uint32_t w, uint32_t magic, h2 mult, h2 add) {
   const uint32_t w8 = w >> 8;
   u32x4 r;
@@ -226,13 +240,14 @@ __device__ __forceinline__ h2 magic_pair(uint32_t w, uint32_t magic, uint32_t i,
   return as_h2(__builtin_amdgcn_perm(magic, w, i | (5u << 8) | (j << 16) | (5u << 24)));
 }
 
-// y[j] += d * sum_s sc_s * q.x - dmin * sum_s m_s * xsum_s for rows 4g+j.
-__device__ __forceinline__ void q4_tile_mma(const Q4Tile& a, const h8* bq, h8 bm, f4& y) {
+// y[j] += c * (d * sum_s sc_s * q.x - dmin * sum_s m_s * xsum_s) for rows 4g+j,
+// where c undoes the column's activation scale for this superblock.
+__device__ __forceinline__ void q4_tile_mma(const Q4Tile& a, const h8* bq, h8 bm, float c, f4& y) {
   const uint32_t sc03 = a.s0 & 0x3F3F3F3Fu, m03 = a.s1 & 0x3F3F3F3Fu;
   const uint32_t sc47 = (a.s2 & 0x0F0F0F0Fu) | ((a.s0 >> 2) & 0x30303030u);
   const uint32_t m47 = ((a.s2 >> 4) & 0x0F0F0F0Fu) | ((a.s1 >> 2) & 0x30303030u);
   const uint32_t words[8] = {a.q0.x, a.q0.y, a.q0.z, a.q0.w, a.q1.x, a.q1.y, a.q1.z, a.q1.w};
-  const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);  // f16 1024 in both halves
+  const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
   const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
   f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -253,21 +268,126 @@ __device__ __forceinline__ void q4_tile_mma(const Q4Tile& a, const h8* bq, h8 bm
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const float d = (float)as_h2(ddw[j]).x, dmin = (float)as_h2(ddw[j]).y;
-    y[j] = y[j] + d * acc[j] - dmin * macc[j];
+    y[j] = y[j] + c * (d * acc[j] - dmin * macc[j]);
   }
 }
 
-// Q4_K GEMV, streaming form: a workgroup of GW = 8 waves owns T row tiles for
-// all of K. Wave w walks superblocks b = w, w + 8, ... and, inside each, the T
-// tiles (one activation operand load serves T weight tiles). The next unit's
-// weights are always in flight while the current one computes, so a wave pays
-// the HBM latency once, not once per unit. The 8 partial sums of each tile meet
+// Row sums for one lane after the MFMA loop: the hi and lo columns (c, c + 8)
+// of the same activation column meet. Every lane must call this (it shuffles).
+__device__ __forceinline__ void col_sum4(const f4& v, float o[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = v[j] + __shfl_xor(v[j], 8);
+}
+
+// ------------------------------------------------------------------ Q4_K wide
+
+// Workgroup = WV waves; wave w owns row tiles (blockIdx.x * WV + w) * T + t over
+// the S superblocks [S * blockIdx.y, S * blockIdx.y + S) of split blockIdx.y. The
+// split's activation operand (S superblocks of B and XS, 9 KB each) is copied
+// to LDS once with direct global->LDS loads and read there by all waves. A
+// wave's S * T weight units (superblock, tile) run as straight-line code with D
+// units in flight. No state is shared between workgroups: a split writes its
+// partial sums (EPI_PART), or with one split the workgroup finishes the rows.
+constexpr int WV = 8;
+constexpr uint32_t WIDE_MAX_SB = 7;      // superblocks per split held in LDS (63 KB)
+constexpr uint32_t WIDE_MAX_UNITS = 12;  // units per wave (T * S) beyond which registers spill
+
+template <int T, int S, int D, int EPI>
+__global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                       const uint16_t* __restrict__ Bx,
+                                                       const uint16_t* __restrict__ XS,
+                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea) {
+  constexpr int U = S * T;
+  __shared__ h8 sB[S * 9 * 64];
+  __shared__ float sC[64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const uint32_t ks = blockIdx.y, kb0 = ks * S;
+  const uint32_t tile0 = (blockIdx.x * WV + wave) * T;
+
+  // Activation operand of the split -> LDS: 1 KB blocks i = 9 * sb + m (m < 8:
+  // B sub-block m, m = 8: XS), one wave instruction each.
+#pragma unroll
+  for (int i0 = 0; i0 < S * 9; i0 += WV) {
+    const uint32_t i = i0 + wave;
+    if (i < (uint32_t)(S * 9)) {
+      const uint32_t sb = kb0 + i / 9, m = i % 9;
+      const uint16_t* src = m < 8 ? Bx + ((size_t)(sb * 8 + m) * 64 + lane) * 8 : XS + ((size_t)sb * 64 + lane) * 8;
+      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(sB + i * 64), 16, 0, 0);
+    }
+  }
+  if (wave == WV - 1) {  // the split's S * 8 scales (lanes past them repeat the last)
+    const uint32_t li = (uint32_t)lane < S * 8 ? lane : S * 8 - 1;
+    __builtin_amdgcn_global_load_lds((glb_void_t*)(CS + kb0 * 8 + li), (lds_void_t*)sC, 4, 0, 0);
+  }
+
+  // Unit u = (superblock u / T, tile u % T); tiles past the end read the last
+  // tile (in bounds) and are not written.
+  auto unit_ptr = [&](int u) {
+    const uint32_t t = tile0 + u % T;
+    const uint32_t tile = t < tiles ? t : tiles - 1;
+    return Wp + ((size_t)tile * nsb + kb0 + u / T) * SH_Q4K_TILE_BYTES;
+  };
+  Q4Tile ring[D];
+#pragma unroll
+  for (int k = 0; k < D && k < U; ++k) ring[k] = load_q4_tile(unit_ptr(k), lane, g, r);
+  __builtin_amdgcn_s_waitcnt(0);  // the LDS copies (and the first weight units) have landed
+  __syncthreads();
+
+  f4 y[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
+  h8 bq[8], bm;
+  float c = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (u % T == 0) {  // next superblock: its operand from LDS
+      const h8* sp = sB + (u / T) * 9 * 64 + lane;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) bq[m] = sp[m * 64];
+      bm = sp[8 * 64];
+      c = sC[(u / T) * 8 + (lane & 7)];
+    }
+    const Q4Tile cur = ring[u % D];
+    if (u + D < U) ring[u % D] = load_q4_tile(unit_ptr(u + D), lane, g, r);
+    q4_tile_mma(cur, bq, bm, c, y[u % T]);
+  }
+
+  if (EPI == EPI_SWIGLU) {
+    // (gate, up) = tiles (2i, 2i + 1) of this wave; one split only
+#pragma unroll
+    for (int i = 0; i < T / 2; ++i) {
+      float og[4], ou[4];
+      col_sum4(y[2 * i], og);
+      col_sum4(y[2 * i + 1], ou);
+      const uint32_t tg = tile0 + 2 * i;
+      if (tg < tiles && r < 8 && (uint32_t)r < N) swiglu4(ea, tg / 2, g, r, og, ou);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float o[4];
+      col_sum4(y[t], o);
+      const uint32_t tile = tile0 + t;
+      if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o, ks);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ Q4_K stream
+
+// A workgroup of GW = 8 waves owns T row tiles for all of K. Wave w walks
+// superblocks b = w, w + 8, ... and, inside each, the T tiles (one activation
+// operand load serves T weight tiles). The next unit's weights are always in
+// flight while the current one computes. The 8 partial sums of each tile meet
 // in LDS at the end; no state is shared between workgroups.
 constexpr int GW = 8;
 template <int T, int EPI>
 __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
                                                        const uint16_t* __restrict__ Bx,
-                                                       const uint16_t* __restrict__ XS, uint32_t N, EpiArgs ea) {
+                                                       const uint16_t* __restrict__ XS,
+                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea) {
   constexpr int CH = T < 4 ? T : 4;  // tiles reduced per LDS round
   __shared__ f4 red[CH][GW][64];
   const int lane = threadIdx.x & 63;
@@ -287,10 +407,12 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
   const uint32_t nbw = (uint32_t)wave < nsb ? (nsb - 1 - wave) / GW + 1 : 0;
   Q4Tile st[2];
   h8 bq[8], bm;
+  float c = 0.f;
   auto load_b = [&](uint32_t b) {
 #pragma unroll
     for (int m = 0; m < 8; ++m) bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
     bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
+    c = CS[b * 8 + (lane & 7)];
   };
   if (nbw) st[0] = load_q4_tile(a_ptr(0, wave), lane, g, r);
   for (uint32_t i = 0; i < nbw; i += 2) {
@@ -305,14 +427,13 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
         const int par = (h * T + t) & 1;
         if (t + 1 < T) st[par ^ 1] = load_q4_tile(a_ptr(t + 1, b), lane, g, r);
         else if (bi + 1 < nbw) st[par ^ 1] = load_q4_tile(a_ptr(0, b + GW), lane, g, r);
-        q4_tile_mma(st[par], bq, bm, y[t]);
+        q4_tile_mma(st[par], bq, bm, c, y[t]);
       }
     }
   }
   // Tile partials meet in LDS, CH tiles per round; wave w < CH ends up holding
   // tile (round * CH + w), or with SwiGLU wave w < CH/2 holds the pair
   // (gate, up) = tiles (2w, 2w + 1) of the round.
-  const float cs = ea.cs ? ea.cs[r & 7] : 1.0f;
 #pragma unroll
   for (int c0 = 0; c0 < T; c0 += CH) {
 #pragma unroll
@@ -323,24 +444,16 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
         f4 vg = {0.f, 0.f, 0.f, 0.f}, vu = {0.f, 0.f, 0.f, 0.f};
         for (int w = 0; w < GW; ++w) { vg += red[2 * wave][w][lane]; vu += red[2 * wave + 1][w][lane]; }
         float og[4], ou[4];
-        for (int j = 0; j < 4; ++j) {
-          og[j] = (vg[j] + __shfl_xor(vg[j], 8)) * cs;
-          ou[j] = (vu[j] + __shfl_xor(vu[j], 8)) * cs;
-        }
+        col_sum4(vg, og);
+        col_sum4(vu, ou);
         const uint32_t tg = tile0 + c0 + 2 * wave;
-        if (tg < tiles && r < 8 && (uint32_t)r < N) {
-          const uint32_t row0 = (tg / 2) * 16 + 4 * g;
-          for (int j = 0; j < 4; ++j) {
-            const float x = og[j];
-            ea.out[(size_t)r * ea.ldo + row0 + j] = (x / (1.0f + expf(-x))) * ou[j];
-          }
-        }
+        if (tg < tiles && r < 8 && (uint32_t)r < N) swiglu4(ea, tg / 2, g, r, og, ou);
       }
     } else if (wave < CH) {
       f4 v = {0.f, 0.f, 0.f, 0.f};
       for (int w = 0; w < GW; ++w) v += red[wave][w][lane];
       float o[4];
-      for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * cs;
+      col_sum4(v, o);
       const uint32_t tile = tile0 + c0 + wave;
       if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
     }
@@ -348,94 +461,14 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
   }
 }
 
-// Q4_K GEMV: a workgroup of W waves owns R row tiles; wave w takes the
-// superblocks b = w, w + W, ... and keeps the next superblock's weights and
-// activation operand in flight while it computes the current one. The W
-// partial sums meet in LDS; no state is shared between workgroups.
-template <int R, int W, int EPI>
-__global__ __launch_bounds__(64 * W) void k_gemv_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
-                                                      const uint16_t* __restrict__ Bx,
-                                                      const uint16_t* __restrict__ XS, uint32_t N, EpiArgs ea) {
-  __shared__ f4 red[W][R][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const uint32_t tile0 = blockIdx.x * R;
-  f4 y[R];
-#pragma unroll
-  for (int t = 0; t < R; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
+// ------------------------------------------------------------------ Q8_0
 
-  struct Stage {
-    h8 bq[8];
-    h8 bm;
-    Q4Tile a[R];
-  };
-  auto load = [&](uint32_t b, Stage& st) {
-#pragma unroll
-    for (int m = 0; m < 8; ++m) st.bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
-    st.bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
-#pragma unroll
-    for (int t = 0; t < R; ++t) {
-      const uint32_t tile = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
-      st.a[t] = load_q4_tile(Wp + ((size_t)tile * nsb + b) * SH_Q4K_TILE_BYTES, lane, g, r);
-    }
-  };
-  Stage cur, nxt;
-  uint32_t b = wave;
-  if (b < nsb) load(b, cur);
-  for (; b < nsb; b += W) {
-    const bool more = b + W < nsb;
-    if (more) load(b + W, nxt);
-#pragma unroll
-    for (int t = 0; t < R; ++t) q4_tile_mma(cur.a[t], cur.bq, cur.bm, y[t]);
-    if (more) cur = nxt;
-  }
-
-  if (W > 1) {
-#pragma unroll
-    for (int t = 0; t < R; ++t) red[wave][t][lane] = y[t];
-    __syncthreads();
-  }
-  // undo the producer's per-column power-of-two activation scale (exact)
-  const float cs = ea.cs ? ea.cs[r & 7] : 1.0f;
-  if (EPI == EPI_SWIGLU) {
-    if (wave >= R / 2) return;
-    const int tg = 2 * wave, tu = 2 * wave + 1;
-    f4 vg = {0.f, 0.f, 0.f, 0.f}, vu = {0.f, 0.f, 0.f, 0.f};
-    if (W > 1) {
-      for (int w = 0; w < W; ++w) { vg += red[w][tg][lane]; vu += red[w][tu][lane]; }
-    } else {
-      vg = y[tg]; vu = y[tu];
-    }
-    float og[4], ou[4];
-    for (int j = 0; j < 4; ++j) {
-      og[j] = (vg[j] + __shfl_xor(vg[j], 8)) * cs;
-      ou[j] = (vu[j] + __shfl_xor(vu[j], 8)) * cs;
-    }
-    if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
-    const uint32_t row0 = ((tile0 + tg) / 2) * 16 + 4 * g;
-    for (int j = 0; j < 4; ++j) {
-      const float x = og[j];
-      ea.out[(size_t)r * ea.ldo + row0 + j] = (x / (1.0f + expf(-x))) * ou[j];
-    }
-    return;
-  }
-  if (wave >= R) return;
-  const uint32_t tile = tile0 + wave;
-  f4 v = {0.f, 0.f, 0.f, 0.f};
-  if (W > 1) {
-    for (int w = 0; w < W; ++w) v += red[w][wave][lane];
-  } else {
-    v = y[wave];
-  }
-  float o[4];
-  for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * cs;
-  if (tile >= tiles || r >= 8 || (uint32_t)r >= N) return;
-  epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
-}
-
+// Q8_0 GEMV: a workgroup of W waves owns R row tiles; wave w takes the 32-blocks
+// b = w, w + W, ...; the W partial sums meet in LDS.
 template <int R, int W, int EPI>
 __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nb,
-                                                     const uint16_t* __restrict__ Bx, uint32_t N, EpiArgs ea) {
+                                                     const uint16_t* __restrict__ Bx, const float* __restrict__ CS,
+                                                     uint32_t N, EpiArgs ea) {
   __shared__ f4 red[W][R][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
@@ -445,6 +478,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
   for (int t = 0; t < R; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
   for (uint32_t b = wave; b < nb; b += W) {
     const h8 bq = as_h8(ld16(Bx + ((size_t)b * 64 + lane) * 8));
+    const float c = CS[(b / 8) * 8 + (lane & 7)];
 #pragma unroll
     for (int t = 0; t < R; ++t) {
       const uint32_t tile = tile0 + t;
@@ -456,7 +490,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
       const float d[4] = {(float)as_h2(dw.x).x, (float)as_h2(dw.x).y, (float)as_h2(dw.y).x,
                           (float)as_h2(dw.y).y};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) y[t][j] = y[t][j] + d[j] * acc[j];
+      for (int j = 0; j < 4; ++j) y[t][j] = y[t][j] + c * (d[j] * acc[j]);
     }
   }
   if (W > 1) {
@@ -464,8 +498,6 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
     for (int t = 0; t < R; ++t) red[wave][t][lane] = y[t];
     __syncthreads();
   }
-  // undo the producer's per-column power-of-two activation scale (exact)
-  const float cs = ea.cs ? ea.cs[r & 7] : 1.0f;
   if (EPI == EPI_SWIGLU) {
     if (wave >= R / 2) return;
     const int tg = 2 * wave, tu = 2 * wave + 1;
@@ -476,17 +508,10 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
       vg = y[tg]; vu = y[tu];
     }
     float og[4], ou[4];
-    for (int j = 0; j < 4; ++j) {
-      og[j] = (vg[j] + __shfl_xor(vg[j], 8)) * cs;
-      ou[j] = (vu[j] + __shfl_xor(vu[j], 8)) * cs;
-    }
-    const uint32_t pair = (tile0 + tg) / 2;
+    col_sum4(vg, og);
+    col_sum4(vu, ou);
     if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
-    const uint32_t row0 = pair * 16 + 4 * g;
-    for (int j = 0; j < 4; ++j) {
-      const float x = og[j];
-      ea.out[(size_t)r * ea.ldo + row0 + j] = (x / (1.0f + expf(-x))) * ou[j];
-    }
+    swiglu4(ea, (tile0 + tg) / 2, g, r, og, ou);
     return;
   }
   if (wave >= R) return;
@@ -498,7 +523,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
     v = y[wave];
   }
   float o[4];
-  for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * cs;
+  col_sum4(v, o);
   if (tile >= tiles || r >= 8 || (uint32_t)r >= N) return;
   epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
 }
@@ -586,76 +611,127 @@ int sh_repack_upload_gu(sh_engine* e, int type, const uint8_t* gate, const uint8
   return SH_OK;
 }
 
-template <int R, int W, int EPI>
-static int launch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                      const EpiArgs& ea) {
-  const uint32_t grid = (w.tiles + R - 1) / R;
-  hipLaunchKernelGGL((k_gemv_q4k<R, W, EPI>), dim3(grid), dim3(64 * W), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
-                     xs, N, ea);
-  return SH_OK;
-}
-template <int R, int W, int EPI>
-static void launch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {
-  const uint32_t grid = (w.tiles + R - 1) / R;
-  hipLaunchKernelGGL((k_gemv_q8<R, W, EPI>), dim3(grid), dim3(64 * W), 0, e->stream, w.d, w.tiles, w.K / 32, bx, N,
-                     ea);
-}
+// ------------------------------------------------------------------ dispatch
 
-// Shape policy: keep ~1000+ waves in flight. Small-M matrices use one tile per
-// workgroup and 8 waves splitting K; large-M ones share each activation stage
-// across 2-4 tiles per wave; gate/up waves own (gate, up) tile pairs.
-template <int EPI>
-static int dispatch_q4k_blocked(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                                const EpiArgs& ea) {
-  if (EPI == EPI_SWIGLU) return launch_q4k<2, 8, EPI>(e, w, bx, xs, N, ea);
-  if (w.tiles >= 1024) return launch_q4k<2, 4, EPI>(e, w, bx, xs, N, ea);
-  return launch_q4k<1, 8, EPI>(e, w, bx, xs, N, ea);
+// Tuning overrides (read once): SH_GEMV_KERNEL=stream|wide, SH_GEMV_T (tiles
+// per wave, wide: 1|2|4, stream: 1|2|4|8), SH_GEMV_KS (wide: splits).
+static int env_u32(const char* name) {
+  const char* s = getenv(name);
+  return s ? atoi(s) : 0;
 }
-
-template <int T, int EPI>
-static int launch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                      const EpiArgs& ea) {
-  const uint32_t grid = (w.tiles + T - 1) / T;
-  hipLaunchKernelGGL((k_gemv_q4s<T, EPI>), dim3(grid), dim3(64 * GW), 0, e->stream, w.d, w.tiles, w.K / 256, bx, xs,
-                     N, ea);
-  return SH_OK;
-}
-
-// Tuning overrides (read once): SH_GEMV_KERNEL=blocked|stream, SH_GEMV_T=1..16.
 static int gemv_kernel_choice() {
-  static int v = [] {
+  static const int v = [] {
     const char* s = getenv("SH_GEMV_KERNEL");
-    return (s && std::string(s) == "blocked") ? 1 : 0;
+    if (!s) return 0;
+    return std::string(s) == "stream" ? 1 : (std::string(s) == "wide" ? 2 : 0);
   }();
   return v;
 }
 static uint32_t gemv_t_override() {
-  static uint32_t v = [] {
-    const char* s = getenv("SH_GEMV_T");
-    return s ? (uint32_t)atoi(s) : 0u;
-  }();
+  static const uint32_t v = (uint32_t)env_u32("SH_GEMV_T");
+  return v;
+}
+static uint32_t gemv_ks_override() {
+  static const uint32_t v = (uint32_t)env_u32("SH_GEMV_KS");
   return v;
 }
 
+struct WidePlan {
+  uint32_t T = 1, S = 1, KS = 1;
+};
+
+// Wide-kernel shape for a Q4_K matrix whose consumer finishes split partials:
+// T tiles per wave (1 unless overridden) and S superblocks per split, S the
+// largest divisor of K/256 up to 7 that still gives >= 256 workgroups (one per
+// CU); at most 16 splits.
+static bool wide_plan(const QMat& w, WidePlan* p) {
+  if (w.type != GGML_Q4_K || gemv_kernel_choice() == 1) return false;
+  const uint32_t nsb = w.K / 256;
+  uint32_t T = gemv_t_override();
+  if (T != 1 && T != 2 && T != 4) T = 1;
+  const uint32_t groups = (w.tiles + WV * T - 1) / (WV * T);
+  const uint32_t ks_req = gemv_ks_override();
+  uint32_t S = 0;
+  for (uint32_t s = WIDE_MAX_SB; s >= 1; --s) {
+    if (nsb % s || T * s > WIDE_MAX_UNITS) continue;
+    const uint32_t ks = nsb / s;
+    if (ks > 16) break;
+    S = s;
+    if (ks_req ? ks >= ks_req : groups * ks >= 256) break;
+  }
+  if (!S) return false;
+  p->T = T;
+  p->S = S;
+  p->KS = nsb / S;
+  return true;
+}
+
+size_t sh_gemv_part_floats(const QMat& w) {
+  WidePlan p;
+  const uint32_t ks = wide_plan(w, &p) ? p.KS : 1;
+  return (size_t)ks * 8 * w.tiles * 16;
+}
+
+template <int T, int S, int EPI>
+static void launch_q4w_s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                         const EpiArgs& ea, const WidePlan& p) {
+  constexpr int D = 4;  // weight units in flight per wave
+  const dim3 grid((w.tiles + WV * T - 1) / (WV * T), p.KS);
+  hipLaunchKernelGGL((k_gemv_q4w<T, S, D, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx, xs,
+                     ea.cs, N, ea);
+}
+template <int T, int S, int EPI>
+static void launch_q4w_if(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                          const EpiArgs& ea, const WidePlan& p) {
+  if constexpr (T * S <= (int)WIDE_MAX_UNITS) launch_q4w_s<T, S, EPI>(e, w, bx, xs, N, ea, p);
+}
+template <int T, int EPI>
+static void launch_q4w(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                       const EpiArgs& ea, const WidePlan& p) {
+  switch (p.S) {
+    case 1: launch_q4w_if<T, 1, EPI>(e, w, bx, xs, N, ea, p); break;
+    case 2: launch_q4w_if<T, 2, EPI>(e, w, bx, xs, N, ea, p); break;
+    case 3: launch_q4w_if<T, 3, EPI>(e, w, bx, xs, N, ea, p); break;
+    case 4: launch_q4w_if<T, 4, EPI>(e, w, bx, xs, N, ea, p); break;
+    case 5: launch_q4w_if<T, 5, EPI>(e, w, bx, xs, N, ea, p); break;
+    case 6: launch_q4w_if<T, 6, EPI>(e, w, bx, xs, N, ea, p); break;
+    default: launch_q4w_if<T, 7, EPI>(e, w, bx, xs, N, ea, p); break;
+  }
+}
+
+template <int T, int EPI>
+static void launch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                       const EpiArgs& ea) {
+  const uint32_t grid = (w.tiles + T - 1) / T;
+  hipLaunchKernelGGL((k_gemv_q4s<T, EPI>), dim3(grid), dim3(64 * GW), 0, e->stream, w.d, w.tiles, w.K / 256, bx, xs,
+                     ea.cs, N, ea);
+}
+
 // Streaming policy: about 512 workgroups of 8 waves (two per CU), i.e. T =
-// tiles / 512 rounded down to a power of two in [1, 16] (even for SwiGLU so a
+// tiles / 512 rounded down to a power of two in [1, 8] (even for SwiGLU so a
 // workgroup owns whole gate/up pairs).
 template <int EPI>
-static int dispatch_q4k(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                        const EpiArgs& ea) {
-  if (gemv_kernel_choice() == 1) return dispatch_q4k_blocked<EPI>(e, w, bx, xs, N, ea);
-  uint32_t t = gemv_t_override();
+static void dispatch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                         const EpiArgs& ea) {
+  uint32_t t = gemv_kernel_choice() == 1 ? gemv_t_override() : 0;
   if (!t) {
     t = 1;
     while (t < 8 && w.tiles / (2 * t) >= 512) t *= 2;
   }
   if (EPI == EPI_SWIGLU && t < 2) t = 2;
   switch (t) {
-    case 1: return launch_q4s<1, EPI>(e, w, bx, xs, N, ea);
-    case 2: return launch_q4s<2, EPI>(e, w, bx, xs, N, ea);
-    case 4: return launch_q4s<4, EPI>(e, w, bx, xs, N, ea);
-    default: return launch_q4s<8, EPI>(e, w, bx, xs, N, ea);
+    case 1: launch_q4s<1, EPI>(e, w, bx, xs, N, ea); break;
+    case 2: launch_q4s<2, EPI>(e, w, bx, xs, N, ea); break;
+    case 4: launch_q4s<4, EPI>(e, w, bx, xs, N, ea); break;
+    default: launch_q4s<8, EPI>(e, w, bx, xs, N, ea); break;
   }
+}
+
+template <int R, int W, int EPI>
+static void launch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {
+  const uint32_t grid = (w.tiles + R - 1) / R;
+  hipLaunchKernelGGL((k_gemv_q8<R, W, EPI>), dim3(grid), dim3(64 * W), 0, e->stream, w.d, w.tiles, w.K / 32, bx,
+                     ea.cs, N, ea);
 }
 template <int EPI>
 static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_t N, const EpiArgs& ea) {
@@ -665,30 +741,43 @@ static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_
 }
 
 int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N, EpiKind epi,
-                   const EpiArgs& ea, const char* tag) {
+                   const EpiArgs& ea, const char* tag, uint32_t* nparts) {
   SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "gemv chunk N=%u outside [1,8]", N);
+  SH_CHECK(ea.cs, SH_ERR_ARG, "gemv: activation scales missing");
+  uint32_t np = 1;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   if (w.type == GGML_Q4_K) {
-    int rc = SH_OK;
-    switch (epi) {
-      case EPI_STORE: rc = dispatch_q4k<EPI_STORE>(e, w, bx, xs, N, ea); break;
-      case EPI_ADD: rc = dispatch_q4k<EPI_ADD>(e, w, bx, xs, N, ea); break;
-      case EPI_QKV: rc = dispatch_q4k<EPI_QKV>(e, w, bx, xs, N, ea); break;
-      case EPI_SWIGLU: rc = dispatch_q4k<EPI_SWIGLU>(e, w, bx, xs, N, ea); break;
+    WidePlan p;
+    if (epi == EPI_PART && wide_plan(w, &p)) {
+      SH_CHECK(ea.part_cap >= p.KS, SH_ERR_CAPACITY, "gemv: %u split partials exceed the buffer (%u)", p.KS,
+               ea.part_cap);
+      np = p.KS;
+      if (p.T == 1) launch_q4w<1, EPI_PART>(e, w, bx, xs, N, ea, p);
+      else if (p.T == 2) launch_q4w<2, EPI_PART>(e, w, bx, xs, N, ea, p);
+      else launch_q4w<4, EPI_PART>(e, w, bx, xs, N, ea, p);
+    } else {
+      switch (epi) {
+        case EPI_STORE: dispatch_q4s<EPI_STORE>(e, w, bx, xs, N, ea); break;
+        case EPI_ADD: dispatch_q4s<EPI_ADD>(e, w, bx, xs, N, ea); break;
+        case EPI_QKV: dispatch_q4s<EPI_QKV>(e, w, bx, xs, N, ea); break;
+        case EPI_SWIGLU: dispatch_q4s<EPI_SWIGLU>(e, w, bx, xs, N, ea); break;
+        case EPI_PART: dispatch_q4s<EPI_PART>(e, w, bx, xs, N, ea); break;
+      }
     }
-    if (rc) return rc;
   } else if (w.type == GGML_Q8_0) {
     switch (epi) {
       case EPI_STORE: dispatch_q8<EPI_STORE>(e, w, bx, N, ea); break;
       case EPI_ADD: dispatch_q8<EPI_ADD>(e, w, bx, N, ea); break;
       case EPI_QKV: dispatch_q8<EPI_QKV>(e, w, bx, N, ea); break;
       case EPI_SWIGLU: dispatch_q8<EPI_SWIGLU>(e, w, bx, N, ea); break;
+      case EPI_PART: dispatch_q8<EPI_PART>(e, w, bx, N, ea); break;
     }
   } else {
     SH_CHECK(false, SH_ERR_UNSUPPORTED, "gemv: weight type %d", w.type);
   }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, tag, w.alg_bytes, ev);
+  if (nparts) *nparts = np;
   return SH_OK;
 }

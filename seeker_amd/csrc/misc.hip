@@ -56,67 +56,121 @@ int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uin
 
 constexpr int PREP_THREADS = SH_OPERAND_THREADS;
 
-// y = x * rsqrt(mean(x^2) + eps) * w (rms_norm.slang:39-55) when w != null, else
-// y = x; then y * s -> GEMV activation operand: B (hi/lo f16, [K/32][64][8]) and
-// XS (per-32 sums, [K/256][64][8], lanes >= 16 stay zero), where s is the power
-// of two putting max|y * s| in [2^9, 2^10); cs[col] = 1/s.
-// One workgroup of 1024 threads per column; each thread keeps NV float4 of the
-// column in registers, so x is read once.
-template <int NV>
-__global__ __launch_bounds__(PREP_THREADS) void k_prep(const float* __restrict__ x, uint32_t K,
-                                                       const float* __restrict__ w, float eps,
-                                                       uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
-                                                       float* __restrict__ cs) {
-  __shared__ float red_s[PREP_THREADS / 64], red_m[PREP_THREADS / 64];
+// acc + p[0] + p[stride] + ... (n terms, in order). Loads go out 8 at a time
+// (indices clamped in bounds, surplus terms dropped) so n partials cost
+// ceil(n / 8) memory latencies, not n.
+__device__ __forceinline__ float4 sum_parts(const float* p, size_t stride, uint32_t n, float4 acc) {
+  for (uint32_t s0 = 0; s0 < n; s0 += 8) {
+    float4 t[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) t[j] = *(const float4*)(p + (size_t)min(s0 + j, n - 1) * stride);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {
+      if (s0 + j >= n) break;
+      acc.x += t[j].x; acc.y += t[j].y; acc.z += t[j].z; acc.w += t[j].w;
+    }
+  }
+  return acc;
+}
+
+// Finish the previous GEMV and build the next one's activation operand, one
+// workgroup of 1024 threads per column (each thread keeps NV float4 of the
+// column in registers, so every input is read once):
+//   PREP_PLAIN:  v = x
+//   PREP_RESID:  v = x + sum_s part[s] (split partial sums, added in split
+//                order); x <- v (the residual stream)
+//   PREP_SWIGLU: v = silu(g) * u with g, u = sum_s part[s] at the packed gate /
+//                up rows of element i (32 (i / 16) + i % 16 and that + 16)
+// then y = v * rsqrt(mean(v^2) + eps) * w (rms_norm.slang:39-55) when w != null,
+// else y = v, and y -> operand (B, XS, per-superblock cs).
+template <int NV, int MODE>
+__global__ __launch_bounds__(PREP_THREADS) void k_prep(PrepArgs a) {
+  __shared__ float red_s[PREP_THREADS / 64];
   const uint32_t col = blockIdx.x, tid = threadIdx.x;
-  const float* xc = x + (size_t)col * K;
-  const uint32_t n4 = K / 4;
+  float* xc = a.x ? a.x + (size_t)col * a.K : nullptr;
+  const uint32_t n4 = a.K / 4;
+  const size_t pstride = (size_t)8 * a.part_ld;
+  const float* pc = a.part ? a.part + (size_t)col * a.part_ld : nullptr;
   float4 v[NV];
-  float ss = 0.f, mx = 0.f;
+  float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const uint32_t q = tid + PREP_THREADS * i;
-    if (q < n4) {
-      v[i] = *(const float4*)(xc + 4 * q);
-      ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-      if (w) {
-        const float4 wv = *(const float4*)(w + 4 * q);
-        v[i].x *= wv.x; v[i].y *= wv.y; v[i].z *= wv.z; v[i].w *= wv.w;  // x*w; the 1/rms factor comes later
-      }
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q >= n4) continue;
+    if (MODE == PREP_SWIGLU) {
+      const uint32_t k = 4 * q, rg = 32 * (k / 16) + k % 16;
+      const float4 g = sum_parts(pc + rg, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
+      const float4 u = sum_parts(pc + rg + 16, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
+      v[i] = make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
+                         (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
     } else {
-      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      v[i] = *(const float4*)(xc + 4 * q);
+      if (MODE == PREP_RESID && a.nparts) {
+        v[i] = sum_parts(pc + 4 * q, pstride, a.nparts, v[i]);
+        *(float4*)(xc + 4 * q) = v[i];
+      }
+    }
+    ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    if (a.norm_w) {
+      const float4 wv = *(const float4*)(a.norm_w + 4 * q);
+      v[i].x *= wv.x; v[i].y *= wv.y; v[i].z *= wv.z; v[i].w *= wv.w;  // x*w; the 1/rms factor comes later
     }
   }
-  ss = sh_wave_sum(ss);
-  mx = sh_wave_max(mx);
-  if ((tid & 63) == 0) { red_s[tid >> 6] = ss; red_m[tid >> 6] = mx; }
-  __syncthreads();
-  ss = 0.f;
-  mx = 0.f;
+  float scale = 1.0f;
+  if (a.norm_w) {
+    ss = sh_wave_sum(ss);
+    if ((tid & 63) == 0) red_s[tid >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < PREP_THREADS / 64; ++i) { ss += red_s[i]; mx = fmaxf(mx, red_m[i]); }
-  const float scale = w ? 1.0f / sqrtf(ss / (float)K + eps) : 1.0f;
-  sh_operand_store<NV>(v, K, col, scale, mx, bx, xs, cs);
+    for (int i = 0; i < PREP_THREADS / 64; ++i) ss += red_s[i];
+    scale = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+  }
+  sh_operand_store<NV>(v, a.K, col, scale, a.bx, a.xs, a.cs);
 }
 
-int sh_prep_launch(sh_engine* e, const float* x, uint32_t K, uint32_t N, const float* norm_w, float eps,
-                   uint16_t* bx, uint16_t* xs, float* cs) {
-  SH_CHECK(K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", K);
-  SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "prep N=%u outside [1, 8]", N);
-  const uint32_t nv = (K / 4 + PREP_THREADS - 1) / PREP_THREADS;
-  SH_CHECK(nv <= 8, SH_ERR_UNSUPPORTED, "prep K=%u above 32768", K);
+int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
+  SH_CHECK(a.K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", a.K);
+  SH_CHECK(a.N >= 1 && a.N <= 8, SH_ERR_ARG, "prep N=%u outside [1, 8]", a.N);
+  SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");
+  SH_CHECK(a.mode != PREP_RESID || a.nparts == 0 || a.part, SH_ERR_ARG, "prep partials missing");
+  const uint32_t nv = (a.K / 4 + PREP_THREADS - 1) / PREP_THREADS;
+  SH_CHECK(nv <= 8, SH_ERR_UNSUPPORTED, "prep K=%u above 32768", a.K);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-#define PREP(NV_) \
-  hipLaunchKernelGGL((k_prep<NV_>), dim3(N), dim3(PREP_THREADS), 0, e->stream, x, K, norm_w, eps, bx, xs, cs)
-  if (nv <= 1) PREP(1);
-  else if (nv <= 2) PREP(2);
-  else if (nv <= 4) PREP(4);
-  else PREP(8);
+#define PREP(NV_, M_) hipLaunchKernelGGL((k_prep<NV_, M_>), dim3(a.N), dim3(PREP_THREADS), 0, e->stream, a)
+#define PREP_NV(M_)            \
+  if (nv <= 1) PREP(1, M_);      \
+  else if (nv <= 2) PREP(2, M_); \
+  else if (nv <= 4) PREP(4, M_); \
+  else PREP(8, M_);
+  if (a.mode == PREP_SWIGLU) { PREP_NV(PREP_SWIGLU) }
+  else if (a.mode == PREP_RESID) { PREP_NV(PREP_RESID) }
+  else { PREP_NV(PREP_PLAIN) }
+#undef PREP_NV
 #undef PREP
   SH_HIP(hipGetLastError());
-  sh_prof_end(e, norm_w ? "rmsnorm_prep" : "prep", 0.0, ev);
+  sh_prof_end(e, a.norm_w ? "rmsnorm_prep" : "prep", 0.0, ev);
+  return SH_OK;
+}
+
+// y[col][m] (+)= sum_s part[s][col][m] for m < M (split partials, in split order).
+__global__ void k_part_reduce(const float* __restrict__ part, uint32_t nparts, uint32_t part_ld, uint32_t M,
+                              float* __restrict__ y, uint32_t ldy, int accumulate) {
+  const uint32_t col = blockIdx.y, m = blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  float s = accumulate ? y[(size_t)col * ldy + m] : 0.f;
+  for (uint32_t k = 0; k < nparts; ++k) s += part[((size_t)k * 8 + col) * part_ld + m];
+  y[(size_t)col * ldy + m] = s;
+}
+
+int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint32_t part_ld, uint32_t M, uint32_t N,
+                          float* y, uint32_t ldy, bool accumulate) {
+  SH_CHECK(N >= 1 && N <= 8 && M <= part_ld, SH_ERR_ARG, "partial reduce shape");
+  hipLaunchKernelGGL(k_part_reduce, dim3((M + 255) / 256, N), dim3(256), 0, e->stream, part, nparts, part_ld, M, y,
+                     ldy, accumulate ? 1 : 0);
+  SH_HIP(hipGetLastError());
   return SH_OK;
 }
 

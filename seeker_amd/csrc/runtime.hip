@@ -87,15 +87,7 @@ extern "C" int sh_engine_create(int dev, sh_engine** out) {
   sh_engine* e = new sh_engine();
   e->device = dev;
   hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
-  e->gemv_part_floats = (size_t)4 << 20;  // 16 MiB of split-K partials
-  e->gemv_counters_n = 8192;
-  if (err == hipSuccess) err = hipMalloc(&e->gemv_part, e->gemv_part_floats * sizeof(float));
-  if (err == hipSuccess) err = hipMalloc(&e->gemv_counters, e->gemv_counters_n * sizeof(uint32_t));
-  if (err == hipSuccess) err = hipMemset(e->gemv_counters, 0, e->gemv_counters_n * sizeof(uint32_t));
   if (err != hipSuccess) {
-    if (e->stream) (void)hipStreamDestroy(e->stream);
-    (void)hipFree(e->gemv_part);
-    (void)hipFree(e->gemv_counters);
     delete e;
     sh_set_error("engine setup: %s", hipGetErrorString(err));
     return SH_ERR_HIP;
@@ -110,8 +102,6 @@ extern "C" void sh_engine_destroy(sh_engine* e) {
   (void)hipStreamSynchronize(e->stream);
   for (auto& p : e->pending) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
   for (auto ev : e->event_pool) (void)hipEventDestroy(ev);
-  (void)hipFree(e->gemv_part);
-  (void)hipFree(e->gemv_counters);
   (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -338,8 +328,8 @@ static void free_model(sh_model* m) {
   (void)hipFree(m->rope);
   Workspace& w = m->ws;
   (void)hipFree(w.resid); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
-  (void)hipFree(w.attn); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
-  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.fa_counters);
+  (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
+  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs);
   delete m;
 }
 
@@ -472,15 +462,20 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   const uint32_t kmax = std::max(m->d, m->ff);
   const size_t bx_elems = (size_t)kmax / 32 * 64 * 8;
   const size_t xs_elems = (size_t)(kmax + 255) / 256 * 64 * 8;
-  const size_t part_floats = (size_t)m->n_kv * 64 * 64 * (m->hd + 2);  // grown on demand in forward_dev
+  const size_t part_floats =  // grown on demand in forward_dev
+      (size_t)m->n_kv * (4096 / SH_FA_MIN_SPLIT_KEYS) * SH_FA_MAX_ROWS * sh_fa_part_stride(m->hd);
+  size_t gpart_floats = 0;
+  for (const Layer& L : m->layers)
+    gpart_floats = std::max({gpart_floats, sh_gemv_part_floats(L.wo), sh_gemv_part_floats(L.wgu),
+                             sh_gemv_part_floats(L.wdown)});
   if (dalloc(&w.resid, (size_t)8 * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
-      dalloc(&w.q, (size_t)8 * m->d) || dalloc(&w.attn, (size_t)8 * m->d) || dalloc(&w.h, (size_t)8 * m->ff) ||
+      dalloc(&w.q, (size_t)8 * m->d) || dalloc(&w.attn, (size_t)8 * m->d) || dalloc(&w.gpart, gpart_floats) || dalloc(&w.h, (size_t)8 * m->ff) ||
       dalloc(&w.logits, (size_t)8 * m->V) || dalloc(&w.fa_part, part_floats) || dalloc(&w.tokens, 128) ||
-      dalloc(&w.amax, 64) || dalloc(&w.cs, 8) || dalloc(&w.fa_counters, SH_FA_MAX_COUNTERS))
+      dalloc(&w.amax, 64) || dalloc(&w.cs, (size_t)(kmax + 255) / 256 * 8))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
-  if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess ||
-      hipMemset(w.fa_counters, 0, SH_FA_MAX_COUNTERS * 4) != hipSuccess)
+  w.gpart_floats = gpart_floats;
+  if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess)
     FAIL(SH_ERR_HIP, "workspace clear failed");
   if ((fail = ensure_rope(m, std::max<uint32_t>(m->n_ctx, 1024)))) FAIL(fail, "%s", sh_last_error());
   if (hipDeviceSynchronize() != hipSuccess) FAIL(SH_ERR_HIP, "model upload failed");
@@ -630,8 +625,19 @@ extern "C" int sh_kv_compact(sh_kv* kv, uint32_t base, const uint32_t* src, uint
 // One chunk of nc <= 8 columns whose token ids are already on the device at
 // m->ws.tokens[tok_off ..]. Writes K/V at slots slot0 .. slot0+nc, runs every
 // layer, and (if want_logits) the final norm + lm_head into ws.logits [nc][V].
+// gate/up: SH_GU=split finishes split partials in the down prep (SwiGLU there);
+// by default one kernel produces whole sums and applies SwiGLU itself.
+static bool swiglu_epilogue() {
+  static const bool v = [] {
+    const char* s = getenv("SH_GU");
+    return !(s && std::string(s) == "split");
+  }();
+  return v;
+}
+
 static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint32_t nc, uint32_t slot0,
-                         const int32_t* colpos, const uint64_t* colmask, uint32_t mask_base, bool want_logits) {
+                         const int32_t* colpos, const uint64_t* colmask, uint32_t mask_base, bool want_logits,
+                         bool want_resid) {
   sh_engine* e = m->e;
   Workspace& w = m->ws;
   int rc;
@@ -642,32 +648,65 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
   qkv.Dq = m->d; qkv.Dkv = dkv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.max_seq = kv->max_seq; qkv.slot0 = slot0;
   qkv.rope = m->rope; qkv.kc = kv->k; qkv.vc = kv->v;
   for (uint32_t j = 0; j < nc; ++j) qkv.colpos[j] = colpos[j];
+  qkv.cs = w.cs;
   FaArgs fa;
   fa.N = nc; fa.kvlen = slot0 + nc; fa.mask_base = mask_base;
   for (uint32_t j = 0; j < nc; ++j) fa.colmask[j] = colmask[j];
-  qkv.cs = w.cs;
-  EpiArgs add;
-  add.out = w.resid; add.ldo = m->d; add.rows = m->d; add.cs = w.cs;
+  // o, gate/up and down write split partial sums, finished by the next prep
+  // (residual add, SwiGLU); ld = the matrix's padded (packed) row count.
+  auto part_args = [&](const QMat& q) {
+    EpiArgs pa;
+    pa.out = w.gpart; pa.ldo = q.tiles * 16; pa.cs = w.cs;
+    pa.part_stride = (size_t)8 * pa.ldo;
+    pa.part_cap = (uint32_t)(w.gpart_floats / pa.part_stride);
+    return pa;
+  };
   EpiArgs sw;
   sw.out = w.h; sw.ldo = m->ff; sw.cs = w.cs;
+  PrepArgs pr;
+  pr.N = nc; pr.bx = w.bx; pr.xs = w.xs; pr.cs = w.cs; pr.part = w.gpart; pr.eps = m->eps;
+  // Residual stream: embedding, then + partials of the pending o / down GEMV.
+  uint32_t pending = 0, pending_ld = 0;
+  auto resid_prep = [&](const float* norm_w) {
+    pr.mode = PREP_RESID; pr.x = w.resid; pr.K = m->d; pr.norm_w = norm_w;
+    pr.nparts = pending; pr.part_ld = pending_ld;
+    pending = 0;
+    return sh_prep_launch(e, pr);
+  };
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
-    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.attn_norm, m->eps, w.bx, w.xs, w.cs))) return rc;
+    if ((rc = resid_prep(L.attn_norm))) return rc;
     qkv.layer = l;
     if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
     fa.layer = l;
     if ((rc = sh_fa_launch(e, m, kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
-    if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_ADD, add, "gemv_o"))) return rc;
-    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, L.ffn_norm, m->eps, w.bx, w.xs, w.cs))) return rc;
-    if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
-    if ((rc = sh_prep_launch(e, w.h, m->ff, nc, nullptr, 0.f, w.bx, w.xs, w.cs))) return rc;
-    if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_ADD, add, "gemv_down"))) return rc;
+    EpiArgs po = part_args(L.wo);
+    if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", &pending))) return rc;
+    pending_ld = po.ldo;
+    if ((rc = resid_prep(L.ffn_norm))) return rc;
+    if (swiglu_epilogue()) {
+      // whole sums in one kernel, h = silu(gate) * up in its epilogue
+      if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
+      pr.mode = PREP_PLAIN; pr.x = w.h; pr.nparts = 0;
+    } else {
+      EpiArgs pg = part_args(L.wgu);
+      uint32_t ngu = 0;
+      if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
+      pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = ngu; pr.part_ld = pg.ldo;
+    }
+    pr.K = m->ff; pr.norm_w = nullptr;
+    if ((rc = sh_prep_launch(e, pr))) return rc;
+    EpiArgs pd = part_args(L.wdown);
+    if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", &pending))) return rc;
+    pending_ld = pd.ldo;
   }
   if (want_logits) {
-    if ((rc = sh_prep_launch(e, w.resid, m->d, nc, m->out_norm, m->eps, w.bx, w.xs, w.cs))) return rc;
+    if ((rc = resid_prep(m->out_norm))) return rc;
     EpiArgs st;
     st.out = w.logits; st.ldo = m->V; st.rows = m->V; st.cs = w.cs;
     if ((rc = sh_gemv_launch(e, m->lm_head, w.bx, w.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
+  } else if (want_resid && pending) {
+    if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, m->d, nc, w.resid, m->d, true))) return rc;
   }
   return SH_OK;
 }
@@ -728,8 +767,8 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
   uint32_t maxpos = 0;
   for (auto p : plan.colpos) maxpos = std::max<uint32_t>(maxpos, (uint32_t)p);
   if ((rc = ensure_rope(m, maxpos + 1))) return rc;
-  const uint32_t needed_splits = (pos + L + SH_FA_KEYS_PER_SPLIT - 1) / SH_FA_KEYS_PER_SPLIT;
-  const size_t need = (size_t)m->n_kv * needed_splits * 64 * (m->hd + 2);
+  const uint32_t needed_splits = (pos + L + SH_FA_MIN_SPLIT_KEYS - 1) / SH_FA_MIN_SPLIT_KEYS;
+  const size_t need = (size_t)m->n_kv * needed_splits * SH_FA_MAX_ROWS * sh_fa_part_stride(m->hd);
   if (need > m->ws.fa_part_floats) {
     SH_HIP(hipStreamSynchronize(e->stream));
     SH_HIP(hipFree(m->ws.fa_part));
@@ -750,7 +789,8 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
       mbase = pos + c0;
       for (uint32_t j = 0; j < nc; ++j) mk[j] = plan.mask[c0 + j];
     }
-    if ((rc = forward_chunk(m, kv, dev_tokens + c0, nc, pos + c0, plan.colpos.data() + c0, mk.data(), mbase, want)))
+    if ((rc = forward_chunk(m, kv, dev_tokens + c0, nc, pos + c0, plan.colpos.data() + c0, mk.data(), mbase, want,
+                            resid_host != nullptr)))
       return rc;
     if (resid_host)
       SH_HIP(hipMemcpyAsync(resid_host + (size_t)c0 * m->d, m->ws.resid, (size_t)nc * m->d * 4,
@@ -971,29 +1011,49 @@ extern "C" int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_d
                              int accumulate) {
   SH_CHECK(e && w && x_dev && y_dev, SH_ERR_ARG, "sh_gemv_quant: NULL argument");
   SH_CHECK(N >= 1, SH_ERR_ARG, "N must be >= 1");
-  const uint32_t K = w->m.K;
+  const uint32_t K = w->m.K, M = w->m.M;
   uint16_t *bx = nullptr, *xs = nullptr;
-  float* cs = nullptr;
+  float *cs = nullptr, *part = nullptr;
   const size_t bx_elems = (size_t)K / 32 * 64 * 8, xs_elems = (size_t)(K + 255) / 256 * 64 * 8;
+  const size_t part_floats = sh_gemv_part_floats(w->m);
   SH_HIP(hipMallocAsync((void**)&bx, bx_elems * 2, e->stream));
   SH_HIP(hipMallocAsync((void**)&xs, xs_elems * 2, e->stream));
-  SH_HIP(hipMallocAsync((void**)&cs, 8 * sizeof(float), e->stream));
+  SH_HIP(hipMallocAsync((void**)&cs, (size_t)(K + 255) / 256 * 8 * sizeof(float), e->stream));
+  SH_HIP(hipMallocAsync((void**)&part, part_floats * sizeof(float), e->stream));
   SH_HIP(hipMemsetAsync(xs, 0, xs_elems * 2, e->stream));
   int rc = SH_OK;
+  // The same kernels as the forward: split partials (finished here by a reduce)
+  // where the forward would use them, else a direct store / accumulate.
+  const bool split = w->m.type == GGML_Q4_K && part_floats > (size_t)8 * w->m.tiles * 16;
   for (uint32_t c0 = 0; c0 < N && !rc; c0 += 8) {
     const uint32_t nc = std::min<uint32_t>(8, N - c0);
-    rc = sh_prep_launch(e, x_dev + (size_t)c0 * K, K, nc, nullptr, 0.f, bx, xs, cs);
+    PrepArgs pr;
+    pr.mode = PREP_PLAIN; pr.x = const_cast<float*>(x_dev + (size_t)c0 * K); pr.K = K; pr.N = nc;
+    pr.bx = bx; pr.xs = xs; pr.cs = cs;
+    rc = sh_prep_launch(e, pr);
     if (rc) break;
-    EpiArgs ea;
-    ea.out = y_dev + (size_t)c0 * w->m.M;
-    ea.ldo = w->m.M;
-    ea.rows = w->m.M;
-    ea.cs = cs;
-    rc = sh_gemv_launch(e, w->m, bx, xs, nc, accumulate ? EPI_ADD : EPI_STORE, ea, "gemv");
+    if (split) {
+      EpiArgs pa;
+      pa.out = part; pa.ldo = w->m.tiles * 16; pa.cs = cs;
+      pa.part_stride = (size_t)8 * pa.ldo;
+      pa.part_cap = (uint32_t)(part_floats / pa.part_stride);
+      uint32_t np = 0;
+      rc = sh_gemv_launch(e, w->m, bx, xs, nc, EPI_PART, pa, "gemv", &np);
+      if (!rc)
+        rc = sh_part_reduce_launch(e, part, np, pa.ldo, M, nc, y_dev + (size_t)c0 * M, M, accumulate != 0);
+    } else {
+      EpiArgs ea;
+      ea.out = y_dev + (size_t)c0 * M;
+      ea.ldo = M;
+      ea.rows = M;
+      ea.cs = cs;
+      rc = sh_gemv_launch(e, w->m, bx, xs, nc, accumulate ? EPI_ADD : EPI_STORE, ea, "gemv");
+    }
   }
   (void)hipFreeAsync(bx, e->stream);
   (void)hipFreeAsync(xs, e->stream);
   (void)hipFreeAsync(cs, e->stream);
+  (void)hipFreeAsync(part, e->stream);
   if (rc) return rc;
   SH_HIP(hipStreamSynchronize(e->stream));
   return sh_prof_flush(e);

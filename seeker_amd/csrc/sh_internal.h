@@ -43,8 +43,10 @@ constexpr int SH_TILE_ROWS = 16;
 constexpr int SH_Q4K_TILE_BYTES = 2304;  // 16 rows x 144 B, repacked
 constexpr int SH_Q8_TILE_BYTES = 544;    // 16 rows x 34 B, repacked
 constexpr int SH_MAX_COLS = 64;          // columns per forward chunk
-constexpr int SH_FA_KEYS_PER_SPLIT = 256;
-constexpr uint32_t SH_FA_MAX_COUNTERS = 1024;  // (kv head, row group) completion counters
+constexpr int SH_FA_MIN_SPLIT_KEYS = 64;  // smallest key split of any attention launch (sizes fa_part)
+constexpr int SH_FA_MAX_ROWS = 64;        // padded query rows (gqa x columns) per kv head
+// Split partial row: O[hd], m, l, 2 pad (keeps rows 16-byte aligned).
+__host__ __device__ constexpr uint32_t sh_fa_part_stride(uint32_t hd) { return hd + 4; }
 
 // -------------------------------------------------------------- structs
 struct KStat {
@@ -65,12 +67,6 @@ struct sh_engine {
   };
   std::vector<Pending> pending;
   std::vector<hipEvent_t> event_pool;
-  // split-K GEMV scratch: per-split partial sums and per-tile-group counters
-  // (counters are zero between launches; the last workgroup re-arms them).
-  float* gemv_part = nullptr;
-  size_t gemv_part_floats = 0;
-  uint32_t* gemv_counters = nullptr;
-  uint32_t gemv_counters_n = 0;
 };
 
 // A weight matrix on the device, repacked into MFMA tiles.
@@ -104,14 +100,15 @@ struct Workspace {
   uint16_t* xs = nullptr;     // XS buffer
   float* q = nullptr;         // [cols][d] roped queries
   float* attn = nullptr;      // [cols][d]
-  float* h = nullptr;         // [cols][ff]
+  float* h = nullptr;         // [cols][ff] SwiGLU output
   float* logits = nullptr;    // [cols][V]
   float* fa_part = nullptr;   // flash-attn split partials
+  float* gpart = nullptr;     // GEMV split-K partials
   uint32_t* tokens = nullptr; // [cols + 16] device token ids
   unsigned long long* amax = nullptr;  // [cols] packed argmax keys
-  float* cs = nullptr;        // [8] inverse activation scales of the current B operand
-  uint32_t* fa_counters = nullptr;  // [SH_FA_MAX_COUNTERS], zero between launches
+  float* cs = nullptr;        // [max(K)/256][8] inverse activation scales of the current B operand
   size_t fa_part_floats = 0;
+  size_t gpart_floats = 0;
 };
 
 struct sh_model {
@@ -147,12 +144,17 @@ int sh_repack_upload_cat(sh_engine* e, int type, const uint8_t* const* parts, co
                          int nparts, uint32_t K, QMat* out);
 void sh_qmat_free(QMat* m);
 
-enum EpiKind { EPI_STORE = 0, EPI_ADD = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+// GEMV epilogues. EPI_PART writes split-K partial sums in packed row order,
+// out[ks * part_stride + col * ldo + row], finished by the consumer (the next
+// prep kernel or sh_part_reduce_launch).
+enum EpiKind { EPI_STORE = 0, EPI_ADD = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_PART = 4 };
 struct EpiArgs {
-  float* out = nullptr;   // STORE/ADD: [N][ldo]; QKV: roped q [N][Dq]; SWIGLU: h [N][ldo]
+  float* out = nullptr;   // STORE/ADD: [N][ldo]; QKV: roped q [N][Dq]; SWIGLU: h [N][ldo]; PART: partials
   uint32_t ldo = 0;
   uint32_t rows = 0xFFFFFFFFu;  // STORE/ADD: logical rows M (ragged last tile)
-  const float* cs = nullptr;    // [8] inverse activation scale per column (from sh_prep_launch)
+  const float* cs = nullptr;    // [K/256][8] inverse activation scale per superblock and column
+  size_t part_stride = 0;       // PART: floats between splits
+  uint32_t part_cap = 0;        // PART: splits the buffer holds
   // QKV
   uint32_t Dq = 0, Dkv = 0, hd = 0, n_kv = 0, max_seq = 0, slot0 = 0, layer = 0;
   const float2* rope = nullptr;
@@ -160,15 +162,36 @@ struct EpiArgs {
   uint16_t* kc = nullptr;
   uint16_t* vc = nullptr;
 };
+// Launch y = W x for N <= 8 columns; with EPI_PART, *nparts receives the
+// number of split partials written (1 for the other epilogues).
 int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                   EpiKind epi, const EpiArgs& ea, const char* tag);
+                   EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
+// Floats of partial-sum buffer the EPI_PART launches of w need (all splits).
+size_t sh_gemv_part_floats(const QMat& w);
 
-// Activation prep: f32 [N][K] -> B + XS (N <= 8); optional RMSNorm with weight.
-// Each column is scaled by a power of two s so max|y*s| lies in [2^9, 2^10):
-// the f16 low halves then stay normal (an f16 subnormal keeps only 2^-24 of
-// absolute resolution) and the 32-element XS sums stay below 2^15. cs[col] = 1/s.
-int sh_prep_launch(sh_engine* e, const float* x, uint32_t K, uint32_t N, const float* norm_w, float eps,
-                   uint16_t* bx, uint16_t* xs, float* cs);
+// Activation prep: finishes the previous GEMV (residual add of its split
+// partials, or SwiGLU of gate/up partials) and builds the next activation
+// operand B + XS + cs (N <= 8) with optional RMSNorm. Each 256-element
+// superblock of a column is scaled by a power of two s so its max|y*s| lies in
+// [2^9, 2^10): the f16 low halves then stay normal (an f16 subnormal keeps only
+// 2^-24 of absolute resolution) and the 32-element XS sums stay below 2^15.
+enum PrepMode { PREP_PLAIN = 0, PREP_RESID = 1, PREP_SWIGLU = 2 };
+struct PrepArgs {
+  int mode = PREP_PLAIN;
+  float* x = nullptr;           // PLAIN/RESID: [N][K] input; RESID writes x + partials back
+  const float* part = nullptr;  // partials [nparts][8][part_ld]
+  uint32_t nparts = 0, part_ld = 0;
+  uint32_t K = 0, N = 0;
+  const float* norm_w = nullptr;
+  float eps = 0.f;
+  uint16_t* bx = nullptr;
+  uint16_t* xs = nullptr;
+  float* cs = nullptr;
+};
+int sh_prep_launch(sh_engine* e, const PrepArgs& a);
+// y[col][m] (+)= sum of nparts split partials, m < M.
+int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint32_t part_ld, uint32_t M, uint32_t N,
+                          float* y, uint32_t ldy, bool accumulate);
 int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uint32_t N, float* resid);
 struct FaArgs {
   uint32_t layer = 0, N = 0;
@@ -177,7 +200,7 @@ struct FaArgs {
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 };
 // Attention for the chunk's columns, then the split combine, which writes
-// attn_out [N][n_embd] f32 and the Wo activation operand (bx, xs, cs).
+// attn_out [N][n_embd] f32 and the Wo activation operand (bx, xs, per-superblock cs).
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
                  float* attn_out, uint16_t* bx, uint16_t* xs, float* cs);
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
