@@ -15,7 +15,13 @@ library), the dominant kernel's roofline, and the CPU oracle's speculative step
 timed on this host's cores from the same state (with a token-for-token check).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       python bench.py --profile-only   (target verify steps only, for rocprofv3)
+       python bench.py --profile-only   (target verify steps only, for rocprofv3: the
+           KV position is set to the context length without a prefill, which leaves
+           the bytes read and the work done unchanged)
+
+roofline.traffic (HBM bytes per launch of the dominant kernel) comes from
+profiles/verify_8b_q4k_traffic.json, written from rocprofv3 FETCH_SIZE /
+WRITE_SIZE runs of `bench.py --profile-only`, when it names the same kernel.
 """
 import argparse
 import json
@@ -45,6 +51,19 @@ def verify_bytes(d, P, L):
     kv_read = 2 * d.n_layer * (P + L) * dkv * 2
     kv_write = 2 * d.n_layer * L * dkv * 2
     return w, kv_read, kv_write
+
+
+def measured_traffic(kernel_tag):
+    """HBM bytes per launch (FETCH + WRITE, calibrated) of kernel_tag from the
+    committed rocprofv3 counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "verify_8b_q4k_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(kernel_tag)
+    return None if k is None else k["fetch_bytes"] + k["write_bytes"]
 
 
 def main():
@@ -86,11 +105,15 @@ def main():
     dkv = None if dm is None else eng.allocate_kv_cache(dm, max_seq)
     prompt = S.tokens(1234, P0, V)
     t0 = time.time()
-    eng.prefill(tm, tkv, prompt[:-1], 0)
-    lg, _ = eng.forward_full_readback(tm, tkv, prompt[-1:], P0 - 1, full_logits=False, want_residual=False)
-    if dm is not None:
-        eng.prefill(dm, dkv, prompt, 0)
-    last = int(np.argmax(lg[0]))
+    if args.profile_only:
+        tkv.set_position(P0)
+        last = int(prompt[-1])
+    else:
+        eng.prefill(tm, tkv, prompt[:-1], 0)
+        lg, _ = eng.forward_full_readback(tm, tkv, prompt[-1:], P0 - 1, full_logits=False, want_residual=False)
+        if dm is not None:
+            eng.prefill(dm, dkv, prompt, 0)
+        last = int(np.argmax(lg[0]))
     log(f"prefill {P0} tokens in {time.time() - t0:.1f}s")
 
     # ---- verify step: latency + roofline (target only) -------------------
@@ -205,7 +228,8 @@ def main():
         "roofline": {"kernel": dom_name, "bound": "hbm", "achieved": round(dom_bytes / dom_avg_ms / 1e6, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_bytes / dom_avg_ms / 1e6 / HBM_PEAK_GBS, 4),
-                     "bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_avg_ms, 5), "traffic": None},
+                     "bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_avg_ms, 5),
+                     "traffic": measured_traffic(dom_name)},
         "cpu_baseline": cpu,
         "parity": parity,
     }

@@ -54,57 +54,53 @@ __device__ __forceinline__ uint64_t col_mask(const FaArgs& fa, uint32_t col) {
 
 // Partial of split `split` for padded row rho:
 // part[((kh * n_splits + split) * n_rows_pad + rho) * PS + {d < HD: O, HD: m, HD+1: l, pad}].
-template <int QT, int HD, int W, int NH>
-__global__ __launch_bounds__(64 * W) void k_fa(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                               const uint16_t* __restrict__ vc, uint32_t max_seq, uint32_t n_head,
-                                               uint32_t N, uint32_t gqa, FaArgs fa, float scale,
-                                               float* __restrict__ part) {
+//
+// Workgroup = (kv head, key split, group of 16 NQG query rows) of NQG * NKB
+// waves; wave w takes key block kb = w % NKB (NH blocks of 32 keys) for row
+// group qg = w / NKB (16 query rows). The NQG waves of one key block read the
+// same K and V (the second read hits the CU's cache).
+template <int HD, int NQG, int NKB, int NH>
+__global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                        const uint16_t* __restrict__ vc, uint32_t max_seq,
+                                                        uint32_t n_head, uint32_t N, uint32_t gqa, FaArgs fa,
+                                                        float scale, float* __restrict__ part) {
   constexpr int NC = HD / 32;  // d chunks of the QK contraction
   constexpr int DT = HD / 16;  // d tiles of the output
-  constexpr int ROWS = 16 * QT;
-  constexpr uint32_t WAVE_KEYS = 32 * NH, SPLIT_KEYS = W * WAVE_KEYS, PS = sh_fa_part_stride(HD);
+  constexpr int ROWS = 16 * NQG;
+  constexpr uint32_t WAVE_KEYS = 32 * NH, SPLIT_KEYS = NKB * WAVE_KEYS, PS = sh_fa_part_stride(HD);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kb = wave % NKB, qg = wave / NKB;
   const int g = lane >> 4, r = lane & 15;
-  const uint32_t kh = blockIdx.x, split = blockIdx.y, qg = blockIdx.z;
+  const uint32_t kh = blockIdx.x, split = blockIdx.y;
   const uint32_t n_splits = gridDim.y;
   const uint32_t n_rows = gqa * N;
   const uint32_t n_rows_pad = gridDim.z * ROWS;
   const uint32_t Dq = n_head * HD;
 
-  // Query rows: lane (g, r) holds rho = 16*qt + r, d = 32c + 8g .. +8. Rows past
-  // n_rows read row 0 and are zeroed.
-  const float* qp[QT];
-  uint32_t rowcol[QT];
-  float rz[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const uint32_t rho = qg * ROWS + 16 * qt + r;
-    const bool ok = rho < n_rows;
-    const uint32_t hq = ok ? rho / N : 0, col = ok ? rho % N : 0;
-    rowcol[qt] = col;
-    rz[qt] = ok ? 1.0f : 0.0f;
-    qp[qt] = q + (size_t)col * Dq + (size_t)(kh * gqa + hq) * HD + 8 * g;
-  }
+  // This wave's query rows: lane (g, r) holds row rho, d = 32c + 8g .. +8. Rows
+  // past n_rows read row 0 and are zeroed.
+  const uint32_t rho = blockIdx.z * ROWS + 16 * qg + r;
+  const bool ok = rho < n_rows;
+  const uint32_t hq = ok ? rho / N : 0, col = ok ? rho % N : 0;
+  const float* qp = q + (size_t)col * Dq + (size_t)(kh * gqa + hq) * HD + 8 * g;
   // This wave's keys: blocks past the split's end read clamped (in-bounds) rows
   // and are masked out below.
   const uint32_t k_end = min((split + 1) * SPLIT_KEYS, fa.kvlen);
-  const uint32_t kw = split * SPLIT_KEYS + WAVE_KEYS * wave;
+  const uint32_t kw = split * SPLIT_KEYS + WAVE_KEYS * kb;
   const uint16_t* kbase = kc + (size_t)kh * max_seq * HD;
   const uint16_t* vbase = vc + (size_t)kh * (max_seq / 32) * HD * 32;
 
-  // Every load of the workgroup's inputs is issued before any is used: Q rows,
-  // then K and V. There is no branch between the loads and their uses, and the
+  // Every load of the wave's inputs is issued before any is used: Q rows, then
+  // K and V. There is no branch between the loads and their uses, and the
   // scheduling barrier keeps them from being sunk, so the split costs one
   // memory latency.
-  float4 qraw[QT][NC][2];
+  float4 qraw[NC][2];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qraw[qt][c][0] = *(const float4*)(qp[qt] + 32 * c);
-      qraw[qt][c][1] = *(const float4*)(qp[qt] + 32 * c + 4);
-    }
+  for (int c = 0; c < NC; ++c) {
+    qraw[c][0] = *(const float4*)(qp + 32 * c);
+    qraw[c][1] = *(const float4*)(qp + 32 * c + 4);
+  }
   h8 kop[NH][2][NC], vop[NH][DT];
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
@@ -117,24 +113,21 @@ __global__ __launch_bounds__(64 * W) void k_fa(const float* __restrict__ q, cons
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) vop[h][dt] = ld_h8(vp + (size_t)dt * 16 * 32);
   }
-  uint64_t cm[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) cm[qt] = col_mask(fa, rowcol[qt]);
+  const uint64_t cm = col_mask(fa, col);
   __builtin_amdgcn_sched_barrier(0);
 
-  // Q^T operands (B). Each query row is scaled by a power of two (max|q * s| in
+  // Q^T operand (B). Each query row is scaled by a power of two (max|q * s| in
   // [2^9, 2^10)) so the f16 low halves stay normal; rscale folds 1/s into the
   // score scale.
-  h8 qhi[QT][NC], qlo[QT][NC];
-  float rscale[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
+  h8 qhi[NC], qlo[NC];
+  float rscale;
+  {
+    const float z = ok ? 1.0f : 0.0f;
     float x[NC][8];
     float mx = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const float4 a = qraw[qt][c][0], b = qraw[qt][c][1];
-      const float z = rz[qt];
+      const float4 a = qraw[c][0], b = qraw[c][1];
       x[c][0] = a.x * z; x[c][1] = a.y * z; x[c][2] = a.z * z; x[c][3] = a.w * z;
       x[c][4] = b.x * z; x[c][5] = b.y * z; x[c][6] = b.z * z; x[c][7] = b.w * z;
 #pragma unroll
@@ -148,151 +141,127 @@ __global__ __launch_bounds__(64 * W) void k_fa(const float* __restrict__ q, cons
       ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
     }
     const float s = ldexpf(1.0f, 10 - ex);
-    rscale[qt] = scale * ldexpf(1.0f, ex - 10);
+    rscale = scale * ldexpf(1.0f, ex - 10);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
 #pragma unroll
       for (int t = 0; t < 8; ++t) x[c][t] *= s;
-      split8(x[c], qhi[qt][c], qlo[qt][c]);
+      split8(x[c], qhi[c], qlo[c]);
     }
   }
 
-  f4 o[DT][QT];
+  f4 o[DT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) o[dt][qt] = f4{0.f, 0.f, 0.f, 0.f};
-  float mrow[QT], lrow[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) { mrow[qt] = -INFINITY; lrow[qt] = 0.f; }
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.f, 0.f, 0.f, 0.f};
+  float mrow = -INFINITY, lrow = 0.f;
 
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
     const uint32_t key0 = kw + 32 * h;
     // S^T[key][rho] for keys key0 + 16*kt + 4g + j.
-    f4 s[2][QT];
+    f4 sacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        acc = mfma16a(kop[h][kt][c], qhi[c], acc);
+        acc = mfma16a(kop[h][kt][c], qlo[c], acc);
+      }
+      sacc[kt] = acc;
+    }
+    const bool tail = key0 + 32 > k_end || key0 + 32 > fa.mask_base;
+    float sv[8];
+    float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          acc = mfma16a(kop[h][kt][c], qhi[qt][c], acc);
-          acc = mfma16a(kop[h][kt][c], qlo[qt][c], acc);
+      for (int j = 0; j < 4; ++j) {
+        float v = sacc[kt][j] * rscale;
+        if (tail) {
+          const uint32_t key = key0 + 16 * kt + 4 * g + j;
+          bool vis = key < k_end;
+          if (vis && key >= fa.mask_base) vis = (cm >> (key - fa.mask_base)) & 1ull;
+          if (!vis) v = -INFINITY;
         }
-        s[kt][qt] = acc;
+        sv[4 * kt + j] = v;
+        mx = fmaxf(mx, v);
       }
-    const bool tail = key0 + 32 > k_end || key0 + 32 > fa.mask_base;
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(mrow, mx);
+    // nothing visible yet: keep O and l (zero) as they are
+    const bool none = mnew == -INFINITY;
+    const float alpha = none ? 1.0f : expf(mrow - mnew);
+    // probabilities carry a 2^12 factor (keeps their f16 low halves normal);
+    // it cancels in O / l because l is summed from the same scaled values
+    float p[8];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float sv[8];
-      float mx = -INFINITY;
+    for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : expf(sv[t] - mnew) * 4096.0f;
+    mrow = mnew;
+    float ps = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+    for (int t = 0; t < 8; ++t) ps += p[t];
+    lrow = lrow * alpha + ps;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v = s[kt][qt][j] * rscale[qt];
-          if (tail) {
-            const uint32_t key = key0 + 16 * kt + 4 * g + j;
-            bool vis = key < k_end;
-            if (vis && key >= fa.mask_base) vis = (cm[qt] >> (key - fa.mask_base)) & 1ull;
-            if (!vis) v = -INFINITY;
-          }
-          sv[4 * kt + j] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(mrow[qt], mx);
-      // nothing visible yet: keep O and l (zero) as they are
-      const bool none = mnew == -INFINITY;
-      const float alpha = none ? 1.0f : expf(mrow[qt] - mnew);
-      // probabilities carry a 2^12 factor (keeps their f16 low halves normal);
-      // it cancels in O / l because l is summed from the same scaled values
-      float p[8];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : expf(sv[t] - mnew) * 4096.0f;
-      mrow[qt] = mnew;
-      float ps = 0.f;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) ps += p[t];
-      lrow[qt] = lrow[qt] * alpha + ps;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt][qt] *= alpha;
-      // P^T operand: lane slot t -> key 4g+t (t<4) or 16+4g+t-4 (t>=4), the order
-      // V blocks are stored in.
-      h8 phi, plo;
-      split8(p, phi, plo);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        o[dt][qt] = mfma16a(vop[h][dt], phi, o[dt][qt]);
-        o[dt][qt] = mfma16a(vop[h][dt], plo, o[dt][qt]);
-      }
-    }
-  }
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    lrow[qt] += __shfl_xor(lrow[qt], 16);
-    lrow[qt] += __shfl_xor(lrow[qt], 32);
-  }
-
-  // Waves 1..W-1 park (m, l, O) in LDS; wave 0 merges them into its own and
-  // writes the split's partial rows.
-  constexpr int WL = W > 1 ? W - 1 : 1;
-  __shared__ float sm[WL][ROWS], sl[WL][ROWS];
-  __shared__ float so[WL][ROWS][HD + 1];
-  if (W > 1) {
-    if (wave > 0) {
-      if (g == 0) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) { sm[wave - 1][16 * qt + r] = mrow[qt]; sl[wave - 1][16 * qt + r] = lrow[qt]; }
-      }
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) so[wave - 1][16 * qt + r][16 * dt + 4 * g + j] = o[dt][qt][j];
-    }
-    __syncthreads();
-    if (wave > 0) return;
-  }
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int rl = 16 * qt + r;
-    float M = mrow[qt];
-#pragma unroll
-    for (int w = 0; w < W - 1; ++w) M = fmaxf(M, sm[w][rl]);
-    const float f0 = mrow[qt] == -INFINITY ? 0.f : expf(mrow[qt] - M);
-    float fw[WL];
-    float L = lrow[qt] * f0;
-#pragma unroll
-    for (int w = 0; w < W - 1; ++w) {
-      fw[w] = sm[w][rl] == -INFINITY ? 0.f : expf(sm[w][rl] - M);
-      L += sl[w][rl] * fw[w];
-    }
-    float* dst = part + (((size_t)kh * n_splits + split) * n_rows_pad + qg * ROWS + rl) * PS;
+    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    // P^T operand: lane slot t -> key 4g+t (t<4) or 16+4g+t-4 (t>=4), the order
+    // V blocks are stored in.
+    h8 phi, plo;
+    split8(p, phi, plo);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      float v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[j] = o[dt][qt][j] * f0;
-#pragma unroll
-        for (int w = 0; w < W - 1; ++w) v[j] += so[w][rl][16 * dt + 4 * g + j] * fw[w];
-      }
-      *(float4*)(dst + 16 * dt + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+      o[dt] = mfma16a(vop[h][dt], phi, o[dt]);
+      o[dt] = mfma16a(vop[h][dt], plo, o[dt]);
     }
-    if (g == 0) *(float4*)(dst + HD) = make_float4(M, L, 0.f, 0.f);
   }
+  lrow += __shfl_xor(lrow, 16);
+  lrow += __shfl_xor(lrow, 32);
+
+  // Key blocks 1..NKB-1 of each row group park (m, l, O) in LDS (16-byte rows,
+  // 132-float stride); key block 0 merges them and writes the split's rows.
+  constexpr int KL = NKB > 1 ? NKB - 1 : 1;
+  __shared__ float sm[NQG][KL][16], sl[NQG][KL][16];
+  __shared__ float4 so[NQG][KL][16][HD / 4 + 1];
+  if (NKB > 1) {
+    if (kb > 0) {
+      if (g == 0) { sm[qg][kb - 1][r] = mrow; sl[qg][kb - 1][r] = lrow; }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) so[qg][kb - 1][r][4 * dt + g] = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+    }
+    __syncthreads();
+    if (kb > 0) return;
+  }
+  float M = mrow;
+#pragma unroll
+  for (int w = 0; w < NKB - 1; ++w) M = fmaxf(M, sm[qg][w][r]);
+  const float f0 = mrow == -INFINITY ? 0.f : expf(mrow - M);
+  float fw[KL];
+  float L = lrow * f0;
+#pragma unroll
+  for (int w = 0; w < NKB - 1; ++w) {
+    fw[w] = sm[qg][w][r] == -INFINITY ? 0.f : expf(sm[qg][w][r] - M);
+    L += sl[qg][w][r] * fw[w];
+  }
+  float* dst = part + (((size_t)kh * n_splits + split) * n_rows_pad + blockIdx.z * ROWS + 16 * qg + r) * PS;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    float4 v = make_float4(o[dt][0] * f0, o[dt][1] * f0, o[dt][2] * f0, o[dt][3] * f0);
+#pragma unroll
+    for (int w = 0; w < NKB - 1; ++w) {
+      const float4 u = so[qg][w][r][4 * dt + g];
+      v.x += u.x * fw[w]; v.y += u.y * fw[w]; v.z += u.z * fw[w]; v.w += u.w * fw[w];
+    }
+    *(float4*)(dst + 16 * dt + 4 * g) = v;
+  }
+  if (g == 0) *(float4*)(dst + HD) = make_float4(M, L, 0.f, 0.f);
 }
 
 // Combine the key splits (in split order) for one 256-wide superblock of the
 // attention output of one column, write attn [N][Dq] f32 and that superblock of
 // the Wo activation operand. One wave per (superblock, column); lane l owns
-// elements 256 sb + 4l .. +3. The splits are read 8 at a time, every load
-// issued before the first is used.
+// elements 256 sb + 4l .. +3. Splits are read CH at a time (every load issued
+// before the first is used); each chunk takes one exp per split.
 template <int HD>
 __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ part, uint32_t n_splits,
                                                    uint32_t n_rows_pad, uint32_t n_head, uint32_t N, uint32_t gqa,
@@ -311,26 +280,30 @@ __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ par
   float M = -INFINITY, L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (uint32_t s0 = 0; s0 < n_splits; s0 += CH) {
-    float4 os[CH], ml[CH];
+    float4 os[CH];
+    float2 ml[CH];
 #pragma unroll
     for (uint32_t j = 0; j < CH; ++j) {
       const float* pp = p + (size_t)min(s0 + j, n_splits - 1) * sstride;
       os[j] = *(const float4*)(pp + d);
-      ml[j] = *(const float4*)(pp + HD);
+      ml[j] = *(const float2*)(pp + HD);
     }
+    float mc = -INFINITY;
+#pragma unroll
+    for (uint32_t j = 0; j < CH; ++j) mc = fmaxf(mc, ml[j].x);  // repeats of the last split change nothing
+    if (mc == -INFINITY) continue;
+    const float mn = fmaxf(M, mc);
+    const float a = expf(M - mn);  // 0 on the first chunk (M = -inf)
+    acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
+    L *= a;
 #pragma unroll
     for (uint32_t j = 0; j < CH; ++j) {
-      const float ms = ml[j].x;
-      if (s0 + j >= n_splits || ms == -INFINITY) continue;
-      const float mn = fmaxf(M, ms);
-      const float a = expf(M - mn), b = expf(ms - mn);  // M = -inf on the first split: a = 0
-      acc.x = acc.x * a + os[j].x * b;
-      acc.y = acc.y * a + os[j].y * b;
-      acc.z = acc.z * a + os[j].z * b;
-      acc.w = acc.w * a + os[j].w * b;
-      L = L * a + ml[j].y * b;
-      M = mn;
+      // 0 for an empty split (m = -inf) and for the clamped repeats past the end
+      const float w = s0 + j < n_splits ? expf(ml[j].x - mn) : 0.0f;
+      acc.x += os[j].x * w; acc.y += os[j].y * w; acc.z += os[j].z * w; acc.w += os[j].w * w;
+      L += ml[j].y * w;
     }
+    M = mn;
   }
   const float il = L > 0.f ? 1.0f / L : 0.f;
   float4 v = make_float4(acc.x * il, acc.y * il, acc.z * il, acc.w * il);
@@ -339,57 +312,44 @@ __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ par
   sh_operand_store_sb(v, Dq, sb, col, bx, xs, cs);
 }
 
-// Keys per split: SH_FA_SPLIT=64|128|256|512 overrides; by default the largest
-// split that still gives >= 256 workgroups (every CU busy), 64 at least.
+// Keys per split: SH_FA_SPLIT=128|256 overrides; by default 256 while that
+// still gives >= 128 workgroups of 8 waves (4 waves per CU), else 128.
 static uint32_t fa_split_keys(uint32_t n_kv, uint32_t kvlen, uint32_t n_qg) {
   static const uint32_t forced = [] {
     const char* s = getenv("SH_FA_SPLIT");
     const uint32_t v = s ? (uint32_t)atoi(s) : 0u;
-    return (v == 64 || v == 128 || v == 256 || v == 512) ? v : 0u;
+    return (v == 128 || v == 256) ? v : 0u;
   }();
   if (forced) return forced;
-  for (uint32_t sk = 256; sk > 64; sk /= 2)
-    if ((size_t)n_kv * n_qg * ((kvlen + sk - 1) / sk) >= 256) return sk;
-  return 64;
+  return (size_t)n_kv * n_qg * ((kvlen + 255) / 256) >= 128 ? 256 : 128;
 }
 
-// SH_FA_WAVES=8: 256-key splits as 8 waves of 32 keys (default 4 waves of 64).
-static bool fa_wide() {
-  static const bool v = [] {
-    const char* s = getenv("SH_FA_WAVES");
-    return s && atoi(s) == 8;
-  }();
-  return v;
-}
-
-template <int QT, int HD>
-static void fa_launch_split(uint32_t split_keys, dim3 grid, hipStream_t st, const float* q, const uint16_t* kc,
-                            const uint16_t* vc, uint32_t max_seq, uint32_t n_head, uint32_t N, uint32_t gqa,
-                            const FaArgs& fa, float scale, float* part) {
-  if (split_keys == 512)
-    hipLaunchKernelGGL((k_fa<QT, HD, 8, 2>), grid, dim3(512), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
-  else if (split_keys == 256 && fa_wide())
-    hipLaunchKernelGGL((k_fa<QT, HD, 8, 1>), grid, dim3(512), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
-  else if (split_keys == 256)
-    hipLaunchKernelGGL((k_fa<QT, HD, 4, 2>), grid, dim3(256), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
-  else if (split_keys == 128)
-    hipLaunchKernelGGL((k_fa<QT, HD, 4, 1>), grid, dim3(256), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
+template <int HD, int NQG>
+static void fa_launch_cfg(uint32_t split_keys, dim3 grid, hipStream_t st, const float* q, const uint16_t* kc,
+                          const uint16_t* vc, uint32_t max_seq, uint32_t n_head, uint32_t N, uint32_t gqa,
+                          const FaArgs& fa, float scale, float* part) {
+  constexpr int NKB = 4;
+  const dim3 block(64 * NQG * NKB);
+  if (split_keys == 256)
+    hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 2>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale,
+                       part);
   else
-    hipLaunchKernelGGL((k_fa<QT, HD, 2, 1>), grid, dim3(128), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale, part);
+    hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 1>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale,
+                       part);
 }
 
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
                  float* attn_out, uint16_t* bx, uint16_t* xs, float* cs) {
   const uint32_t gqa = m->n_head / m->n_kv;
   const uint32_t n_rows = gqa * fa.N;
-  const int QT = n_rows > 16 ? 2 : 1;
-  const uint32_t n_qg = (n_rows + 16 * QT - 1) / (16 * QT);
-  SH_CHECK(n_qg * 16 * QT <= (uint32_t)SH_FA_MAX_ROWS, SH_ERR_UNSUPPORTED, "%u query rows per kv head above %d",
+  const int NQG = n_rows > 16 ? 2 : 1;
+  const uint32_t n_qg = (n_rows + 16 * NQG - 1) / (16 * NQG);
+  SH_CHECK(n_qg * 16 * NQG <= (uint32_t)SH_FA_MAX_ROWS, SH_ERR_UNSUPPORTED, "%u query rows per kv head above %d",
            n_rows, SH_FA_MAX_ROWS);
   SH_CHECK(fa.kvlen > 0, SH_ERR_ARG, "attention over zero keys");
   const uint32_t split_keys = fa_split_keys(m->n_kv, fa.kvlen, n_qg);
   const uint32_t n_splits = (fa.kvlen + split_keys - 1) / split_keys;
-  const uint32_t rows_pad = n_qg * 16 * QT;
+  const uint32_t rows_pad = n_qg * 16 * NQG;
   const size_t need = (size_t)m->n_kv * n_splits * rows_pad * sh_fa_part_stride(m->hd);
   SH_CHECK(need <= m->ws.fa_part_floats, SH_ERR_CAPACITY, "attention partial buffer too small (%zu > %zu)", need,
            m->ws.fa_part_floats);
@@ -402,11 +362,11 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   sh_prof_begin(e, &ev);
   const dim3 grid(m->n_kv, n_splits, n_qg);
   if (m->hd == 128) {
-    if (QT == 2) fa_launch_split<2, 128>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
-    else fa_launch_split<1, 128>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
+    if (NQG == 2) fa_launch_cfg<128, 2>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
+    else fa_launch_cfg<128, 1>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
   } else if (m->hd == 64) {
-    if (QT == 2) fa_launch_split<2, 64>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
-    else fa_launch_split<1, 64>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
+    if (NQG == 2) fa_launch_cfg<64, 2>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
+    else fa_launch_cfg<64, 1>(split_keys, grid, e->stream, q, kc, vc, kv->max_seq, m->n_head, fa.N, gqa, fa, scale, part);
   } else {
     SH_CHECK(false, SH_ERR_UNSUPPORTED, "head_dim %u not supported (64, 128)", m->hd);
   }

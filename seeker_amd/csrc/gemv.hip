@@ -272,11 +272,29 @@ __device__ __forceinline__ void q4_tile_mma(const Q4Tile& a, const h8* bq, h8 bm
   }
 }
 
-// Row sums for one lane after the MFMA loop: the hi and lo columns (c, c + 8)
-// of the same activation column meet. Every lane must call this (it shuffles).
-__device__ __forceinline__ void col_sum4(const f4& v, float o[4]) {
+// RMSNorm factor of activation column col, rsqrt(mean(x^2) + eps), from the
+// prep's per-superblock sums of squares (added in superblock order); 1 when the
+// input is not normalized.
+// Called at kernel start so its loads (8 in flight at a time) overlap the weights.
+__device__ __forceinline__ float col_rinv(const EpiArgs& ea, uint32_t col) {
+  if (!ea.ssq) return 1.0f;
+  float ss = 0.f;
+  for (uint32_t i0 = 0; i0 < ea.ssq_n; i0 += 8) {
+    float t[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o[j] = v[j] + __shfl_xor(v[j], 8);
+    for (uint32_t j = 0; j < 8; ++j) t[j] = ea.ssq[min(i0 + j, ea.ssq_n - 1) * 8 + col];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) ss += i0 + j < ea.ssq_n ? t[j] : 0.0f;
+  }
+  return 1.0f / sqrtf(ss / (float)ea.norm_K + ea.eps);
+}
+
+// Row sums for one lane after the MFMA loop: the hi and lo columns (c, c + 8)
+// of the same activation column meet, times the column's norm factor f. Every
+// lane must call this (it shuffles).
+__device__ __forceinline__ void col_sum4(const f4& v, float f, float o[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * f;
 }
 
 // ------------------------------------------------------------------ Q4_K wide
@@ -305,6 +323,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
   const int g = lane >> 4, r = lane & 15;
   const uint32_t ks = blockIdx.y, kb0 = ks * S;
   const uint32_t tile0 = (blockIdx.x * WV + wave) * T;
+  const float nf = col_rinv(ea, r & 7);
 
   // Activation operand of the split -> LDS: 1 KB blocks i = 9 * sb + m (m < 8:
   // B sub-block m, m = 8: XS), one wave instruction each.
@@ -359,8 +378,8 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
 #pragma unroll
     for (int i = 0; i < T / 2; ++i) {
       float og[4], ou[4];
-      col_sum4(y[2 * i], og);
-      col_sum4(y[2 * i + 1], ou);
+      col_sum4(y[2 * i], nf, og);
+      col_sum4(y[2 * i + 1], nf, ou);
       const uint32_t tg = tile0 + 2 * i;
       if (tg < tiles && r < 8 && (uint32_t)r < N) swiglu4(ea, tg / 2, g, r, og, ou);
     }
@@ -368,7 +387,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       float o[4];
-      col_sum4(y[t], o);
+      col_sum4(y[t], nf, o);
       const uint32_t tile = tile0 + t;
       if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o, ks);
     }
@@ -394,6 +413,7 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar address math
   const int g = lane >> 4, r = lane & 15;
   const uint32_t tile0 = blockIdx.x * T;
+  const float nf = col_rinv(ea, r & 7);
   f4 y[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
@@ -444,8 +464,8 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
         f4 vg = {0.f, 0.f, 0.f, 0.f}, vu = {0.f, 0.f, 0.f, 0.f};
         for (int w = 0; w < GW; ++w) { vg += red[2 * wave][w][lane]; vu += red[2 * wave + 1][w][lane]; }
         float og[4], ou[4];
-        col_sum4(vg, og);
-        col_sum4(vu, ou);
+        col_sum4(vg, nf, og);
+        col_sum4(vu, nf, ou);
         const uint32_t tg = tile0 + c0 + 2 * wave;
         if (tg < tiles && r < 8 && (uint32_t)r < N) swiglu4(ea, tg / 2, g, r, og, ou);
       }
@@ -453,7 +473,7 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
       f4 v = {0.f, 0.f, 0.f, 0.f};
       for (int w = 0; w < GW; ++w) v += red[wave][w][lane];
       float o[4];
-      col_sum4(v, o);
+      col_sum4(v, nf, o);
       const uint32_t tile = tile0 + c0 + wave;
       if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
     }
@@ -473,6 +493,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const uint32_t tile0 = blockIdx.x * R;
+  const float nf = col_rinv(ea, r & 7);
   f4 y[R];
 #pragma unroll
   for (int t = 0; t < R; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
@@ -508,8 +529,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
       vg = y[tg]; vu = y[tu];
     }
     float og[4], ou[4];
-    col_sum4(vg, og);
-    col_sum4(vu, ou);
+    col_sum4(vg, nf, og);
+    col_sum4(vu, nf, ou);
     if (tile0 + tg >= tiles || r >= 8 || (uint32_t)r >= N) return;
     swiglu4(ea, (tile0 + tg) / 2, g, r, og, ou);
     return;
@@ -523,7 +544,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_q8(const uint8_t* __restrict__ 
     v = y[wave];
   }
   float o[4];
-  col_sum4(v, o);
+  col_sum4(v, nf, o);
   if (tile >= tiles || r >= 8 || (uint32_t)r >= N) return;
   epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
 }
@@ -672,13 +693,25 @@ size_t sh_gemv_part_floats(const QMat& w) {
   return (size_t)ks * 8 * w.tiles * 16;
 }
 
+static uint32_t gemv_d_override() {
+  static const uint32_t v = (uint32_t)env_u32("SH_GEMV_D");
+  return v;
+}
+// D = weight units in flight per wave (SH_GEMV_D=2|4|8; default 4).
 template <int T, int S, int EPI>
 static void launch_q4w_s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                          const EpiArgs& ea, const WidePlan& p) {
-  constexpr int D = 4;  // weight units in flight per wave
   const dim3 grid((w.tiles + WV * T - 1) / (WV * T), p.KS);
-  hipLaunchKernelGGL((k_gemv_q4w<T, S, D, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx, xs,
-                     ea.cs, N, ea);
+  const uint32_t d = gemv_d_override();
+  if (d == 2)
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 2, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
+                       xs, ea.cs, N, ea);
+  else if (d == 8)
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 8, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
+                       xs, ea.cs, N, ea);
+  else
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 4, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
+                       xs, ea.cs, N, ea);
 }
 template <int T, int S, int EPI>
 static void launch_q4w_if(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,

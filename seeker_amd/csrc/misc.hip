@@ -54,8 +54,6 @@ int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uin
 
 // ------------------------------------------------------------------ prep
 
-constexpr int PREP_THREADS = SH_OPERAND_THREADS;
-
 // acc + p[0] + p[stride] + ... (n terms, in order). Loads go out 8 at a time
 // (indices clamped in bounds, surplus terms dropped) so n partials cost
 // ceil(n / 8) memory latencies, not n.
@@ -74,60 +72,47 @@ __device__ __forceinline__ float4 sum_parts(const float* p, size_t stride, uint3
 }
 
 // Finish the previous GEMV and build the next one's activation operand, one
-// workgroup of 1024 threads per column (each thread keeps NV float4 of the
-// column in registers, so every input is read once):
+// wave per (superblock, column); lane l owns elements 256 sb + 4l .. +3:
 //   PREP_PLAIN:  v = x
 //   PREP_RESID:  v = x + sum_s part[s] (split partial sums, added in split
 //                order); x <- v (the residual stream)
 //   PREP_SWIGLU: v = silu(g) * u with g, u = sum_s part[s] at the packed gate /
 //                up rows of element i (32 (i / 16) + i % 16 and that + 16)
-// then y = v * rsqrt(mean(v^2) + eps) * w (rms_norm.slang:39-55) when w != null,
-// else y = v, and y -> operand (B, XS, per-superblock cs).
-template <int NV, int MODE>
-__global__ __launch_bounds__(PREP_THREADS) void k_prep(PrepArgs a) {
-  __shared__ float red_s[PREP_THREADS / 64];
-  const uint32_t col = blockIdx.x, tid = threadIdx.x;
-  float* xc = a.x ? a.x + (size_t)col * a.K : nullptr;
-  const uint32_t n4 = a.K / 4;
+// With a norm weight w (rms_norm.slang:39-55): ssq[sb][col] = sum v^2 over the
+// superblock and y = v * w, the rsqrt(mean + eps) factor being applied by the
+// consuming GEMV; else y = v. Then y -> operand (B, XS, cs).
+template <int MODE>
+__global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
+  const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
+  const uint32_t k = 256 * sb + 4 * lane;
+  const bool valid = k < a.K;
   const size_t pstride = (size_t)8 * a.part_ld;
-  const float* pc = a.part ? a.part + (size_t)col * a.part_ld : nullptr;
-  float4 v[NV];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const uint32_t q = tid + PREP_THREADS * i;
-    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (q >= n4) continue;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (valid) {
     if (MODE == PREP_SWIGLU) {
-      const uint32_t k = 4 * q, rg = 32 * (k / 16) + k % 16;
-      const float4 g = sum_parts(pc + rg, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
-      const float4 u = sum_parts(pc + rg + 16, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
-      v[i] = make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
-                         (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
+      const float* pc = a.part + (size_t)col * a.part_ld + 32 * (k / 16) + k % 16;
+      const float4 g = sum_parts(pc, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
+      const float4 u = sum_parts(pc + 16, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
+      v = make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
+                      (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
     } else {
-      v[i] = *(const float4*)(xc + 4 * q);
+      float* xp = a.x + (size_t)col * a.K + k;
+      v = *(const float4*)xp;
       if (MODE == PREP_RESID && a.nparts) {
-        v[i] = sum_parts(pc + 4 * q, pstride, a.nparts, v[i]);
-        *(float4*)(xc + 4 * q) = v[i];
+        v = sum_parts(a.part + (size_t)col * a.part_ld + k, pstride, a.nparts, v);
+        *(float4*)xp = v;
       }
     }
-    ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-    if (a.norm_w) {
-      const float4 wv = *(const float4*)(a.norm_w + 4 * q);
-      v[i].x *= wv.x; v[i].y *= wv.y; v[i].z *= wv.z; v[i].w *= wv.w;  // x*w; the 1/rms factor comes later
+  }
+  if (a.norm_w) {
+    const float ss = sh_wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+    if (lane == 0) a.ssq[sb * 8 + col] = ss;
+    if (valid) {
+      const float4 wv = *(const float4*)(a.norm_w + k);
+      v.x *= wv.x; v.y *= wv.y; v.z *= wv.z; v.w *= wv.w;
     }
   }
-  float scale = 1.0f;
-  if (a.norm_w) {
-    ss = sh_wave_sum(ss);
-    if ((tid & 63) == 0) red_s[tid >> 6] = ss;
-    __syncthreads();
-    ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < PREP_THREADS / 64; ++i) ss += red_s[i];
-    scale = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-  }
-  sh_operand_store<NV>(v, a.K, col, scale, a.bx, a.xs, a.cs);
+  sh_operand_store_sb(v, a.K, sb, col, a.bx, a.xs, a.cs);
 }
 
 int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
@@ -135,21 +120,13 @@ int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
   SH_CHECK(a.N >= 1 && a.N <= 8, SH_ERR_ARG, "prep N=%u outside [1, 8]", a.N);
   SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");
   SH_CHECK(a.mode != PREP_RESID || a.nparts == 0 || a.part, SH_ERR_ARG, "prep partials missing");
-  const uint32_t nv = (a.K / 4 + PREP_THREADS - 1) / PREP_THREADS;
-  SH_CHECK(nv <= 8, SH_ERR_UNSUPPORTED, "prep K=%u above 32768", a.K);
+  SH_CHECK(!a.norm_w || a.ssq, SH_ERR_ARG, "prep: norm needs a sum-of-squares buffer");
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-#define PREP(NV_, M_) hipLaunchKernelGGL((k_prep<NV_, M_>), dim3(a.N), dim3(PREP_THREADS), 0, e->stream, a)
-#define PREP_NV(M_)            \
-  if (nv <= 1) PREP(1, M_);      \
-  else if (nv <= 2) PREP(2, M_); \
-  else if (nv <= 4) PREP(4, M_); \
-  else PREP(8, M_);
-  if (a.mode == PREP_SWIGLU) { PREP_NV(PREP_SWIGLU) }
-  else if (a.mode == PREP_RESID) { PREP_NV(PREP_RESID) }
-  else { PREP_NV(PREP_PLAIN) }
-#undef PREP_NV
-#undef PREP
+  const dim3 grid((a.K + 255) / 256, a.N);
+  if (a.mode == PREP_SWIGLU) hipLaunchKernelGGL((k_prep<PREP_SWIGLU>), grid, dim3(64), 0, e->stream, a);
+  else if (a.mode == PREP_RESID) hipLaunchKernelGGL((k_prep<PREP_RESID>), grid, dim3(64), 0, e->stream, a);
+  else hipLaunchKernelGGL((k_prep<PREP_PLAIN>), grid, dim3(64), 0, e->stream, a);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, a.norm_w ? "rmsnorm_prep" : "prep", 0.0, ev);
   return SH_OK;

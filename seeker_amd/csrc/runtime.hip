@@ -329,7 +329,7 @@ static void free_model(sh_model* m) {
   Workspace& w = m->ws;
   (void)hipFree(w.resid); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
   (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
-  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs);
+  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq);
   delete m;
 }
 
@@ -471,7 +471,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   if (dalloc(&w.resid, (size_t)8 * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
       dalloc(&w.q, (size_t)8 * m->d) || dalloc(&w.attn, (size_t)8 * m->d) || dalloc(&w.gpart, gpart_floats) || dalloc(&w.h, (size_t)8 * m->ff) ||
       dalloc(&w.logits, (size_t)8 * m->V) || dalloc(&w.fa_part, part_floats) || dalloc(&w.tokens, 128) ||
-      dalloc(&w.amax, 64) || dalloc(&w.cs, (size_t)(kmax + 255) / 256 * 8))
+      dalloc(&w.amax, 64) || dalloc(&w.cs, (size_t)(kmax + 255) / 256 * 8) ||
+      dalloc(&w.ssq, (size_t)(kmax + 255) / 256 * 8))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
   w.gpart_floats = gpart_floats;
@@ -649,6 +650,11 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
   qkv.rope = m->rope; qkv.kc = kv->k; qkv.vc = kv->v;
   for (uint32_t j = 0; j < nc; ++j) qkv.colpos[j] = colpos[j];
   qkv.cs = w.cs;
+  // GEMVs whose input is RMS-normalized apply the norm factor to their outputs
+  auto set_norm = [&](EpiArgs& ea) {
+    ea.ssq = w.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
+  };
+  set_norm(qkv);
   FaArgs fa;
   fa.N = nc; fa.kvlen = slot0 + nc; fa.mask_base = mask_base;
   for (uint32_t j = 0; j < nc; ++j) fa.colmask[j] = colmask[j];
@@ -663,8 +669,9 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
   };
   EpiArgs sw;
   sw.out = w.h; sw.ldo = m->ff; sw.cs = w.cs;
+  set_norm(sw);
   PrepArgs pr;
-  pr.N = nc; pr.bx = w.bx; pr.xs = w.xs; pr.cs = w.cs; pr.part = w.gpart; pr.eps = m->eps;
+  pr.N = nc; pr.bx = w.bx; pr.xs = w.xs; pr.cs = w.cs; pr.part = w.gpart; pr.eps = m->eps; pr.ssq = w.ssq;
   // Residual stream: embedding, then + partials of the pending o / down GEMV.
   uint32_t pending = 0, pending_ld = 0;
   auto resid_prep = [&](const float* norm_w) {
@@ -690,6 +697,7 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
       pr.mode = PREP_PLAIN; pr.x = w.h; pr.nparts = 0;
     } else {
       EpiArgs pg = part_args(L.wgu);
+      set_norm(pg);
       uint32_t ngu = 0;
       if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
       pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = ngu; pr.part_ld = pg.ldo;
@@ -704,6 +712,7 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
     if ((rc = resid_prep(m->out_norm))) return rc;
     EpiArgs st;
     st.out = w.logits; st.ldo = m->V; st.rows = m->V; st.cs = w.cs;
+    set_norm(st);
     if ((rc = sh_gemv_launch(e, m->lm_head, w.bx, w.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
   } else if (want_resid && pending) {
     if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, m->d, nc, w.resid, m->d, true))) return rc;

@@ -107,6 +107,7 @@ struct Workspace {
   uint32_t* tokens = nullptr; // [cols + 16] device token ids
   unsigned long long* amax = nullptr;  // [cols] packed argmax keys
   float* cs = nullptr;        // [max(K)/256][8] inverse activation scales of the current B operand
+  float* ssq = nullptr;       // [max(K)/256][8] per-superblock sums of squares of the normalized input
   size_t fa_part_floats = 0;
   size_t gpart_floats = 0;
 };
@@ -155,6 +156,11 @@ struct EpiArgs {
   const float* cs = nullptr;    // [K/256][8] inverse activation scale per superblock and column
   size_t part_stride = 0;       // PART: floats between splits
   uint32_t part_cap = 0;        // PART: splits the buffer holds
+  // RMSNorm of the input, applied to the outputs: y *= rsqrt(sum_i ssq[i][col] / norm_K + eps)
+  // over the prep's per-superblock sums of squares ssq [ssq_n][8] (null: no norm).
+  const float* ssq = nullptr;
+  uint32_t ssq_n = 0, norm_K = 0;
+  float eps = 0.f;
   // QKV
   uint32_t Dq = 0, Dkv = 0, hd = 0, n_kv = 0, max_seq = 0, slot0 = 0, layer = 0;
   const float2* rope = nullptr;
@@ -171,13 +177,17 @@ size_t sh_gemv_part_floats(const QMat& w);
 
 // Activation prep: finishes the previous GEMV (residual add of its split
 // partials, or SwiGLU of gate/up partials) and builds the next activation
-// operand B + XS + cs (N <= 8) with optional RMSNorm. Each 256-element
-// superblock of a column is scaled by a power of two s so its max|y*s| lies in
-// [2^9, 2^10): the f16 low halves then stay normal (an f16 subnormal keeps only
-// 2^-24 of absolute resolution) and the 32-element XS sums stay below 2^15.
+// operand B + XS + cs (N <= 8), one wave per (superblock, column). RMSNorm is
+// split: the prep multiplies by the norm weight and writes per-superblock sums
+// of squares; the consuming GEMV applies rsqrt(mean + eps) to its outputs
+// (EpiArgs::ssq). Each 256-element superblock of a column is scaled by a power
+// of two s so its max|y*s| lies in [2^9, 2^10): the f16 low halves then stay
+// normal (an f16 subnormal keeps only 2^-24 of absolute resolution) and the
+// 32-element XS sums stay below 2^15.
 enum PrepMode { PREP_PLAIN = 0, PREP_RESID = 1, PREP_SWIGLU = 2 };
 struct PrepArgs {
   int mode = PREP_PLAIN;
+  float* ssq = nullptr;         // with norm_w: per-superblock sums of squares [K/256][8] out
   float* x = nullptr;           // PLAIN/RESID: [N][K] input; RESID writes x + partials back
   const float* part = nullptr;  // partials [nparts][8][part_ld]
   uint32_t nparts = 0, part_ld = 0;

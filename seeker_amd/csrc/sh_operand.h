@@ -2,8 +2,6 @@
 #pragma once
 #include "sh_internal.h"
 
-constexpr int SH_OPERAND_THREADS = 1024;
-
 __device__ __forceinline__ float sh_wave_sum(float v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
   return v;
@@ -62,22 +60,5 @@ __device__ __forceinline__ void sh_operand_store_sb(float4 v, uint32_t K, uint32
       xs[xo] = __builtin_bit_cast(uint16_t, sh);
       xs[xo + 64] = __builtin_bit_cast(uint16_t, (_Float16)(sum - (float)sh));
     }
-  }
-}
-
-// Column `col` of an activation held by a 1024-thread workgroup as NV float4
-// per thread (element k = 4 * (tid + 1024 i) + t), times `pre`, becomes the
-// operand: wave w writes superblocks w + 16 i.
-template <int NV>
-__device__ __forceinline__ void sh_operand_store(const float4 (&v)[NV], uint32_t K, uint32_t col, float pre,
-                                                 uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
-                                                 float* __restrict__ cs) {
-  const uint32_t wave = threadIdx.x >> 6, nsb = (K + 255) / 256;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const uint32_t sb = wave + (SH_OPERAND_THREADS / 64) * i;
-    if (sb >= nsb) break;  // wave-uniform
-    sh_operand_store_sb(make_float4(v[i].x * pre, v[i].y * pre, v[i].z * pre, v[i].w * pre), K, sb, col, bx, xs,
-                        cs);
   }
 }
