@@ -132,6 +132,24 @@ int sh_forward_full(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens
 int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L, uint32_t pos,
                      uint32_t* sampled_out);
 
+/* Batched verify of B sequences: Engine::verify_unified (inference/mod.rs:
+ * 2316-2398) over Model::record_forward_unified_verify (models/mod.rs:212-230,
+ * Llama body models/llama.rs:620-837). Sequence s contributes seq_lens[s]
+ * columns, packed flat in tokens (column starts = prefix sums, q_starts). Its
+ * cache is caches[s] (the reference's BatchKvCache slot slots[s]); with
+ * pos_s = that cache's position, column i of s writes K/V slot pos_s + i and
+ * attends to the cached prefix plus, within the sequence, causally (parents ==
+ * NULL) or to its tree ancestors (parents, flat, = index within the sequence
+ * of the column's parent, -1 for a child of the prefix; trees <= 64 nodes).
+ * positions (flat, optional) are the RoPE positions and must equal pos_s + i
+ * (chains) or pos_s + depth (trees). Outputs, each optional: logits_out
+ * [N_total][V], sampled_out [N_total] greedy argmax per column, residual_out
+ * [N_total][n_embd] (before the output norm). Each cache advances by its
+ * seq_len; the caller truncates it to the accepted length. */
+int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B, const uint32_t* tokens,
+                      const uint32_t* seq_lens, const uint32_t* positions, const int32_t* parents,
+                      float* logits_out, uint32_t* sampled_out, float* residual_out);
+
 /* Engine::decode_speculative (inference/mod.rs:2108-2297) with a separate draft
  * model (draft_tokens mod.rs:2062-2092 greedy): drafts n = clamp(n_max,1,8)
  * tokens on device, verifies [last, d_1..d_n], accepts the longest prefix

@@ -102,6 +102,7 @@ SIGNATURES = {
     "sh_kv_compact": (C.c_int, [P, C.c_uint32, U32P, C.c_uint32]),
     "sh_forward_full": (C.c_int, [P, P, P, U32P, C.c_uint32, C.c_uint32, I32P, C.c_int, F32P, F32P]),
     "sh_verify_greedy": (C.c_int, [P, P, P, U32P, C.c_uint32, C.c_uint32, U32P]),
+    "sh_verify_unified": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, U32P, U32P, U32P, I32P, F32P, U32P, F32P]),
     "sh_spec_step": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), U32P, U32P, U32P]),
     "sh_qtensor_upload": (C.c_int, [P, C.c_int, P, C.c_uint32, C.c_uint32, C.POINTER(P)]),
     "sh_qtensor_destroy": (None, [P]),

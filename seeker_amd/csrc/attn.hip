@@ -259,14 +259,16 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
 
 // Combine the key splits (in split order) for one 256-wide superblock of the
 // attention output of one column, write attn [N][Dq] f32 and that superblock of
-// the Wo activation operand. One wave per (superblock, column); lane l owns
+// the Wo activation operand (columns col0 + j of the chunk). One wave per
+// (superblock, column); lane l owns
 // elements 256 sb + 4l .. +3. Splits are read CH at a time (every load issued
 // before the first is used); each chunk takes one exp per split.
 template <int HD>
 __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ part, uint32_t n_splits,
                                                    uint32_t n_rows_pad, uint32_t n_head, uint32_t N, uint32_t gqa,
-                                                   float* __restrict__ attn, uint16_t* __restrict__ bx,
-                                                   uint16_t* __restrict__ xs, float* __restrict__ cs) {
+                                                   uint32_t col0, float* __restrict__ attn,
+                                                   uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
+                                                   float* __restrict__ cs) {
   constexpr uint32_t PS = sh_fa_part_stride(HD);
   constexpr uint32_t CH = 16;
   const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
@@ -307,9 +309,9 @@ __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ par
   }
   const float il = L > 0.f ? 1.0f / L : 0.f;
   float4 v = make_float4(acc.x * il, acc.y * il, acc.z * il, acc.w * il);
-  if (valid) *(float4*)(attn + (size_t)col * Dq + k) = v;
+  if (valid) *(float4*)(attn + (size_t)(col0 + col) * Dq + k) = v;
   else v = make_float4(0.f, 0.f, 0.f, 0.f);
-  sh_operand_store_sb(v, Dq, sb, col, bx, xs, cs);
+  sh_operand_store_sb(v, Dq, sb, col0 + col, bx, xs, cs);
 }
 
 // Keys per split: SH_FA_SPLIT=128|256 overrides; by default 256 while that
@@ -357,7 +359,10 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   const size_t layer_k = (size_t)m->n_kv * kv->max_seq * m->hd;
   const uint16_t* kc = kv->k + layer_k * fa.layer;
   const uint16_t* vc = kv->v + layer_k * fa.layer;
+  SH_CHECK(fa.col0 + fa.N <= 8, SH_ERR_ARG, "attention columns [%u, %u) outside the chunk", fa.col0,
+           fa.col0 + fa.N);
   const float scale = 1.0f / sqrtf((float)m->hd);
+  q += (size_t)fa.col0 * m->n_head * m->hd;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   const dim3 grid(m->n_kv, n_splits, n_qg);
@@ -377,10 +382,10 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   const dim3 cgrid((m->n_head * m->hd + 255) / 256, fa.N);
   if (m->hd == 128)
     hipLaunchKernelGGL((k_fa_combine<128>), cgrid, dim3(64), 0, e->stream, part, n_splits, rows_pad, m->n_head, fa.N,
-                       gqa, attn_out, bx, xs, cs);
+                       gqa, fa.col0, attn_out, bx, xs, cs);
   else
     hipLaunchKernelGGL((k_fa_combine<64>), cgrid, dim3(64), 0, e->stream, part, n_splits, rows_pad, m->n_head, fa.N,
-                       gqa, attn_out, bx, xs, cs);
+                       gqa, fa.col0, attn_out, bx, xs, cs);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "attn_combine", 0.0, ev);
   return SH_OK;

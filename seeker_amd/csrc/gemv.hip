@@ -150,7 +150,7 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32
     }
   } else if (EPI == EPI_QKV) {
     const int32_t pos = ea.colpos[col & 7];
-    const uint32_t slot = ea.slot0 + col;
+    const uint32_t slot = ea.slot[col & 7], ms = ea.mseq[col & 7];
     if (r0 < ea.Dq) {
       const uint32_t i0 = r0 % ea.hd;
       const float2 cs0 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2];
@@ -169,11 +169,11 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32
       o[1] = v[0] * cs0.y + v[1] * cs0.x;
       o[2] = v[2] * cs1.x - v[3] * cs1.y;
       o[3] = v[2] * cs1.y + v[3] * cs1.x;
-      uint16_t* k = ea.kc + (((size_t)ea.layer * ea.n_kv + kh) * ea.max_seq + slot) * ea.hd + i0;
+      uint16_t* k = ea.kc[col & 7] + (((size_t)ea.layer * ea.n_kv + kh) * ms + slot) * ea.hd + i0;
       for (int j = 0; j < 4; ++j) k[j] = f2h_bits(o[j]);
     } else {
       const uint32_t rr = r0 - ea.Dq - ea.Dkv, kh = rr / ea.hd, i0 = rr % ea.hd;
-      uint16_t* vb = ea.vc + (((size_t)ea.layer * ea.n_kv + kh) * (ea.max_seq / 32) + slot / 32) * ea.hd * 32;
+      uint16_t* vb = ea.vc[col & 7] + (((size_t)ea.layer * ea.n_kv + kh) * (ms / 32) + slot / 32) * ea.hd * 32;
       const uint32_t sl = v_slot(slot & 31);
       for (int j = 0; j < 4; ++j) vb[(size_t)(i0 + j) * 32 + sl] = f2h_bits(v[j]);
     }

@@ -636,9 +636,23 @@ static bool swiglu_epilogue() {
   return v;
 }
 
-static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint32_t nc, uint32_t slot0,
-                         const int32_t* colpos, const uint64_t* colmask, uint32_t mask_base, bool want_logits,
-                         bool want_resid) {
+// One column of a forward chunk: the cache its K/V row goes to, the slot, and
+// the RoPE position.
+struct ColKv {
+  sh_kv* kv = nullptr;
+  uint32_t slot = 0;
+  int32_t pos = 0;
+};
+// Attention for columns [col0, col0 + ncol) of a chunk, all of one sequence
+// (cache kv): keys [0, kvlen) exist, keys >= mask_base need their colmask bit.
+struct FaSeg {
+  sh_kv* kv = nullptr;
+  uint32_t col0 = 0, ncol = 0, kvlen = 0, mask_base = 0;
+  uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+};
+
+static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
+                         const std::vector<FaSeg>& segs, bool want_logits, bool want_resid) {
   sh_engine* e = m->e;
   Workspace& w = m->ws;
   int rc;
@@ -646,18 +660,18 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
   const uint32_t dkv = m->hd * m->n_kv;
   EpiArgs qkv;
   qkv.out = w.q; qkv.ldo = m->d;
-  qkv.Dq = m->d; qkv.Dkv = dkv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.max_seq = kv->max_seq; qkv.slot0 = slot0;
-  qkv.rope = m->rope; qkv.kc = kv->k; qkv.vc = kv->v;
-  for (uint32_t j = 0; j < nc; ++j) qkv.colpos[j] = colpos[j];
+  qkv.Dq = m->d; qkv.Dkv = dkv; qkv.hd = m->hd; qkv.n_kv = m->n_kv;
+  qkv.rope = m->rope;
+  for (uint32_t j = 0; j < nc; ++j) {
+    qkv.colpos[j] = cols[j].pos; qkv.slot[j] = cols[j].slot; qkv.mseq[j] = cols[j].kv->max_seq;
+    qkv.kc[j] = cols[j].kv->k; qkv.vc[j] = cols[j].kv->v;
+  }
   qkv.cs = w.cs;
   // GEMVs whose input is RMS-normalized apply the norm factor to their outputs
   auto set_norm = [&](EpiArgs& ea) {
     ea.ssq = w.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
   };
   set_norm(qkv);
-  FaArgs fa;
-  fa.N = nc; fa.kvlen = slot0 + nc; fa.mask_base = mask_base;
-  for (uint32_t j = 0; j < nc; ++j) fa.colmask[j] = colmask[j];
   // o, gate/up and down write split partial sums, finished by the next prep
   // (residual add, SwiGLU); ld = the matrix's padded (packed) row count.
   auto part_args = [&](const QMat& q) {
@@ -685,8 +699,12 @@ static int forward_chunk(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uin
     if ((rc = resid_prep(L.attn_norm))) return rc;
     qkv.layer = l;
     if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
-    fa.layer = l;
-    if ((rc = sh_fa_launch(e, m, kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
+    for (const FaSeg& sg : segs) {
+      FaArgs fa;
+      fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
+      for (uint32_t j = 0; j < sg.ncol; ++j) fa.colmask[j] = sg.colmask[j];
+      if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
+    }
     EpiArgs po = part_args(L.wo);
     if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", &pending))) return rc;
     pending_ld = po.ldo;
@@ -757,6 +775,19 @@ static int make_plan(uint32_t L, uint32_t pos, const int32_t* parents, Plan* p) 
   return SH_OK;
 }
 
+// Grows the attention partial buffer for keys [0, max_kvlen).
+static int ensure_fa_part(sh_model* m, uint32_t max_kvlen) {
+  const uint32_t needed_splits = (max_kvlen + SH_FA_MIN_SPLIT_KEYS - 1) / SH_FA_MIN_SPLIT_KEYS;
+  const size_t need = (size_t)m->n_kv * needed_splits * SH_FA_MAX_ROWS * sh_fa_part_stride(m->hd);
+  if (need <= m->ws.fa_part_floats) return SH_OK;
+  SH_HIP(hipStreamSynchronize(m->e->stream));
+  SH_HIP(hipFree(m->ws.fa_part));
+  m->ws.fa_part = nullptr;
+  SH_HIP(hipMalloc(&m->ws.fa_part, need * 4));
+  m->ws.fa_part_floats = need;
+  return SH_OK;
+}
+
 // Runs the whole forward for L columns whose ids are at dev_tokens. If
 // logits_dst != null, copies logits of the selected columns there (device).
 static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint32_t L, uint32_t pos,
@@ -776,15 +807,7 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
   uint32_t maxpos = 0;
   for (auto p : plan.colpos) maxpos = std::max<uint32_t>(maxpos, (uint32_t)p);
   if ((rc = ensure_rope(m, maxpos + 1))) return rc;
-  const uint32_t needed_splits = (pos + L + SH_FA_MIN_SPLIT_KEYS - 1) / SH_FA_MIN_SPLIT_KEYS;
-  const size_t need = (size_t)m->n_kv * needed_splits * SH_FA_MAX_ROWS * sh_fa_part_stride(m->hd);
-  if (need > m->ws.fa_part_floats) {
-    SH_HIP(hipStreamSynchronize(e->stream));
-    SH_HIP(hipFree(m->ws.fa_part));
-    m->ws.fa_part = nullptr;
-    SH_HIP(hipMalloc(&m->ws.fa_part, need * 4));
-    m->ws.fa_part_floats = need;
-  }
+  if ((rc = ensure_fa_part(m, pos + L))) return rc;
   for (uint32_t c0 = 0; c0 < L; c0 += 8) {
     const uint32_t nc = std::min<uint32_t>(8, L - c0);
     const bool last = c0 + nc == L;
@@ -798,9 +821,14 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
       mbase = pos + c0;
       for (uint32_t j = 0; j < nc; ++j) mk[j] = plan.mask[c0 + j];
     }
-    if ((rc = forward_chunk(m, kv, dev_tokens + c0, nc, pos + c0, plan.colpos.data() + c0, mk.data(), mbase, want,
-                            resid_host != nullptr)))
-      return rc;
+    std::vector<ColKv> cols(nc);
+    for (uint32_t j = 0; j < nc; ++j) {
+      cols[j].kv = kv; cols[j].slot = pos + c0 + j; cols[j].pos = plan.colpos[c0 + j];
+    }
+    std::vector<FaSeg> segs(1);
+    segs[0].kv = kv; segs[0].col0 = 0; segs[0].ncol = nc; segs[0].kvlen = pos + c0 + nc; segs[0].mask_base = mbase;
+    for (uint32_t j = 0; j < nc; ++j) segs[0].colmask[j] = mk[j];
+    if ((rc = forward_chunk(m, dev_tokens + c0, nc, cols.data(), segs, want, resid_host != nullptr))) return rc;
     if (resid_host)
       SH_HIP(hipMemcpyAsync(resid_host + (size_t)c0 * m->d, m->ws.resid, (size_t)nc * m->d * 4,
                             hipMemcpyDeviceToHost, e->stream));
@@ -875,6 +903,102 @@ extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint
   if (rc) return rc;
   SH_CHECK(se == hipSuccess, SH_ERR_HIP, "verify: %s", hipGetErrorString(se));
   kv->pending.clear();
+  return sh_prof_flush(e);
+}
+
+extern "C" int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B,
+                                 const uint32_t* tokens, const uint32_t* seq_lens, const uint32_t* positions,
+                                 const int32_t* parents, float* logits_out, uint32_t* sampled_out,
+                                 float* residual_out) {
+  SH_CHECK(e && m && caches && tokens && seq_lens, SH_ERR_ARG, "sh_verify_unified: NULL argument");
+  SH_CHECK(B >= 1, SH_ERR_ARG, "verify_unified: empty batch");
+  // prefix-sum column starts (q_starts) and per-sequence plans
+  std::vector<uint32_t> q0(B + 1, 0);
+  std::vector<Plan> plans(B);
+  uint32_t max_kv = 0, maxpos = 0;
+  int rc;
+  for (uint32_t s = 0; s < B; ++s) {
+    sh_kv* kv = caches[s];
+    SH_CHECK(kv, SH_ERR_ARG, "verify_unified: cache %u is NULL", s);
+    for (uint32_t t = 0; t < s; ++t)
+      SH_CHECK(caches[t] != kv, SH_ERR_ARG, "verify_unified: sequences %u and %u share a cache", t, s);
+    SH_CHECK(kv->n_layer == m->n_layer && kv->n_kv == m->n_kv && kv->hd == m->hd, SH_ERR_ARG,
+             "verify_unified: cache %u dims do not match the model", s);
+    const uint32_t L = seq_lens[s];
+    SH_CHECK(L >= 1, SH_ERR_ARG, "verify_unified: sequence %u is empty", s);
+    SH_CHECK((uint64_t)kv->pos + L <= kv->max_seq, SH_ERR_CAPACITY,
+             "verify_unified: sequence %u positions [%u, %u) exceed KV capacity %u", s, kv->pos, kv->pos + L,
+             kv->max_seq);
+    q0[s + 1] = q0[s] + L;
+    if ((rc = make_plan(L, kv->pos, parents ? parents + q0[s] : nullptr, &plans[s]))) return rc;
+    if (positions)
+      for (uint32_t i = 0; i < L; ++i)
+        SH_CHECK(positions[q0[s] + i] == (uint32_t)plans[s].colpos[i], SH_ERR_ARG,
+                 "verify_unified: positions[%u] = %u, expected %d", q0[s] + i, positions[q0[s] + i],
+                 plans[s].colpos[i]);
+    max_kv = std::max(max_kv, kv->pos + L);
+    for (auto p : plans[s].colpos) maxpos = std::max<uint32_t>(maxpos, (uint32_t)p);
+  }
+  const uint32_t N = q0[B];
+  if ((rc = ensure_rope(m, maxpos + 1))) return rc;
+  if ((rc = ensure_fa_part(m, max_kv))) return rc;
+  // flat columns: cache, slot, RoPE position, owning sequence, index within it
+  std::vector<ColKv> cols(N);
+  std::vector<uint32_t> cseq(N), cidx(N);
+  for (uint32_t s = 0; s < B; ++s)
+    for (uint32_t i = 0; i < seq_lens[s]; ++i) {
+      const uint32_t j = q0[s] + i;
+      cols[j].kv = caches[s]; cols[j].slot = caches[s]->pos + i; cols[j].pos = plans[s].colpos[i];
+      cseq[j] = s; cidx[j] = i;
+    }
+  uint32_t* dt = nullptr;
+  if ((rc = upload_tokens(m, tokens, N, &dt))) return rc;
+  uint32_t* ids = nullptr;
+  if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, 8 * 4, e->stream));
+  const bool want_logits = logits_out || sampled_out;
+  for (uint32_t c0 = 0; c0 < N && !rc; c0 += 8) {
+    const uint32_t nc = std::min<uint32_t>(8, N - c0);
+    // one attention segment per run of one sequence's columns in the chunk
+    std::vector<FaSeg> segs;
+    for (uint32_t j = 0; j < nc;) {
+      const uint32_t s = cseq[c0 + j], i0 = cidx[c0 + j];
+      uint32_t n = 1;
+      while (j + n < nc && cseq[c0 + j + n] == s) ++n;
+      FaSeg sg;
+      sg.kv = caches[s]; sg.col0 = j; sg.ncol = n;
+      sg.kvlen = caches[s]->pos + i0 + n;
+      if (plans[s].tree) {
+        sg.mask_base = caches[s]->pos;
+        for (uint32_t t = 0; t < n; ++t) sg.colmask[t] = plans[s].mask[i0 + t];
+      } else {
+        sg.mask_base = caches[s]->pos + i0;
+        for (uint32_t t = 0; t < n; ++t) sg.colmask[t] = (2ull << t) - 1ull;
+      }
+      segs.push_back(sg);
+      j += n;
+    }
+    rc = forward_chunk(m, dt + c0, nc, cols.data() + c0, segs, want_logits, residual_out != nullptr);
+    if (rc) break;
+    if (residual_out)
+      SH_HIP(hipMemcpyAsync(residual_out + (size_t)c0 * m->d, m->ws.resid, (size_t)nc * m->d * 4,
+                            hipMemcpyDeviceToHost, e->stream));
+    if (logits_out)
+      SH_HIP(hipMemcpyAsync(logits_out + (size_t)c0 * m->V, m->ws.logits, (size_t)nc * m->V * 4,
+                            hipMemcpyDeviceToHost, e->stream));
+    if (sampled_out) {
+      if ((rc = sh_argmax_launch(e, m->ws.logits, m->V, nc, m->ws.amax, ids))) break;
+      SH_HIP(hipMemcpyAsync(sampled_out + c0, ids, (size_t)nc * 4, hipMemcpyDeviceToHost, e->stream));
+    }
+  }
+  hipError_t se = hipStreamSynchronize(e->stream);
+  (void)hipFree(dt);
+  if (ids) (void)hipFree(ids);
+  if (rc) return rc;
+  SH_CHECK(se == hipSuccess, SH_ERR_HIP, "verify_unified: %s", hipGetErrorString(se));
+  for (uint32_t s = 0; s < B; ++s) {
+    caches[s]->pos += seq_lens[s];
+    caches[s]->pending.clear();
+  }
   return sh_prof_flush(e);
 }
 

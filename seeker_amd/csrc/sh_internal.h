@@ -161,12 +161,16 @@ struct EpiArgs {
   const float* ssq = nullptr;
   uint32_t ssq_n = 0, norm_K = 0;
   float eps = 0.f;
-  // QKV
-  uint32_t Dq = 0, Dkv = 0, hd = 0, n_kv = 0, max_seq = 0, slot0 = 0, layer = 0;
+  // QKV: column c is roped at colpos[c] and its K/V row goes to slot slot[c] of
+  // the cache (kc[c], vc[c], capacity mseq[c]); columns may belong to different
+  // sequences' caches.
+  uint32_t Dq = 0, Dkv = 0, hd = 0, n_kv = 0, layer = 0;
   const float2* rope = nullptr;
-  int32_t colpos[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // RoPE position per column
-  uint16_t* kc = nullptr;
-  uint16_t* vc = nullptr;
+  int32_t colpos[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint32_t slot[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint32_t mseq[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint16_t* kc[8] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  uint16_t* vc[8] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
 };
 // Launch y = W x for N <= 8 columns; with EPI_PART, *nparts receives the
 // number of split partials written (1 for the other epilogues).
@@ -205,6 +209,7 @@ int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint
 int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uint32_t N, float* resid);
 struct FaArgs {
   uint32_t layer = 0, N = 0;
+  uint32_t col0 = 0;       // first column of the chunk (q, attn and operand column offset)
   uint32_t kvlen = 0;      // keys [0, kvlen) exist
   uint32_t mask_base = 0;  // keys >= mask_base need their bit in colmask
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};

@@ -27,6 +27,16 @@ class SpecStepOut:
 
 
 @dataclass
+class VerifyUnifiedOut:
+    """models/mod.rs:491-496 + the per-column samples of verify_unified: sampled [N_total],
+    logits [N_total][V] and residual [N_total][n_embd] when requested, q_starts [B]."""
+    sampled: np.ndarray
+    logits: Optional[np.ndarray]
+    residual: Optional[np.ndarray]
+    q_starts: np.ndarray
+
+
+@dataclass
 class SamplerConfig:
     """Subset of inference/sample.rs:85 used by the verify path: temperature 0
     is greedy; mode selects sample-and-compare or rejection sampling."""
@@ -115,6 +125,31 @@ class Engine:
         N.check(self._lib.sh_verify_greedy(self.h, model.h, cache.h, t.ctypes.data_as(N.U32P), t.size, pos,
                                            out.ctypes.data_as(N.U32P)))
         return out
+
+    def verify_unified(self, model: "Model", caches: Sequence["KvCache"], tokens: Sequence[int],
+                       seq_lens: Sequence[int], positions: Optional[Sequence[int]] = None,
+                       parents: Optional[Sequence[int]] = None, want_logits: bool = False,
+                       want_residual: bool = False) -> VerifyUnifiedOut:
+        """Engine::verify_unified (inference/mod.rs:2316-2398): B sequences packed flat, sequence s
+        verified against caches[s]. Greedy argmax per column; logits / residual on request.
+        Every cache advances by its seq_len (truncate to the accepted length afterwards)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        sl = np.ascontiguousarray(seq_lens, dtype=np.uint32)
+        n, b = t.size, sl.size
+        hs = (C.c_void_p * b)(*[c.h for c in caches])
+        pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.uint32)
+        par = None if parents is None else np.ascontiguousarray(parents, dtype=np.int32)
+        sampled = np.zeros(n, dtype=np.uint32)
+        logits = np.zeros((n, model.vocab_size()), dtype=np.float32) if want_logits else None
+        resid = np.zeros((n, model.dims.n_embd), dtype=np.float32) if want_residual else None
+        N.check(self._lib.sh_verify_unified(
+            self.h, model.h, C.cast(hs, C.POINTER(C.c_void_p)), b, t.ctypes.data_as(N.U32P),
+            sl.ctypes.data_as(N.U32P), None if pos is None else pos.ctypes.data_as(N.U32P),
+            None if par is None else par.ctypes.data_as(N.I32P),
+            None if logits is None else logits.ctypes.data_as(N.F32P), sampled.ctypes.data_as(N.U32P),
+            None if resid is None else resid.ctypes.data_as(N.F32P)))
+        q_starts = np.concatenate([[0], np.cumsum(sl)[:-1]]).astype(np.uint64)
+        return VerifyUnifiedOut(sampled, logits, resid, q_starts)
 
     def decode_speculative(self, target: "Model", draft: "Model", tcache: "KvCache", dcache: "KvCache",
                            last_token: int, n_max: int, sampler: Optional[N.sh_sampling] = None) -> SpecStepOut:

@@ -1,0 +1,136 @@
+"""Batched verify (sh_verify_unified, Engine::verify_unified inference/mod.rs:2316-2398)
+on the GPU.
+
+Every column's arithmetic is independent of which other columns share its
+launch (GEMV columns, per-column RMSNorm and operand scales, attention splits
+at absolute key indices), so a batch of B sequences must give bit-identical
+logits, ids, residuals and KV rows to B separate sh_forward_full calls, however
+the flat packing cuts sequences across 8-column chunks. The separate calls are
+themselves checked against the C oracle in test_gpu_forward.py; here the batch
+is also compared to the oracle per sequence.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from seeker_amd import SeekerError
+from seeker_amd import synth as S
+from seeker_amd._native import GGML_Q4_K, SH_ERR_ARG, SH_ERR_CAPACITY
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {
+    "tiny_q8": S.TINY_TARGET,
+    "gqa_q4k": S.LlamaShape(2, 1024, 8, 2, 2048, 4000, 512, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K),
+}
+
+
+@pytest.fixture(scope="module", params=list(SHAPES))
+def model(request, engine):
+    img = S.GgufImage(SHAPES[request.param], seed=0)
+    print(f"model {request.param}", flush=True)
+    gm = engine.upload_weights(img)
+    yield request.param, img, gm
+    gm.close()
+    img.close()
+
+
+def _prefilled(engine, gm, prompt, max_seq=256):
+    kv = engine.allocate_kv_cache(gm, max_seq)
+    engine.prefill(gm, kv, prompt, 0)
+    return kv
+
+
+def _kv_rows(kv, gm, lo, hi):
+    out = []
+    for layer in range(gm.dims.n_layer):
+        for isv in (False, True):
+            out.append(kv.read_layer(layer, isv, hi)[lo:hi])
+    return out
+
+
+# (prefix length, verify length) per sequence; flat packing 5 + 11 + 3 + 9 = 28
+# columns cuts sequences 1 and 3 across 8-column chunks.
+SEQS = [(20, 5), (37, 11), (5, 3), (12, 9)]
+
+
+def test_unified_equals_separate_forwards(engine, model):
+    name, img, gm = model
+    V = gm.vocab_size()
+    prompts = [S.tokens(100 + s, p, V) for s, (p, _) in enumerate(SEQS)]
+    drafts = [S.tokens(200 + s, n, V) for s, (_, n) in enumerate(SEQS)]
+    batch_kv = [_prefilled(engine, gm, pr) for pr in prompts]
+    ref_kv = [_prefilled(engine, gm, pr) for pr in prompts]
+    toks = np.concatenate(drafts)
+    lens = [n for _, n in SEQS]
+    positions = np.concatenate([np.arange(p, p + n) for p, n in SEQS])
+    out = engine.verify_unified(gm, batch_kv, toks, lens, positions=positions, want_logits=True,
+                                want_residual=True)
+    assert list(out.q_starts) == [0, 5, 16, 19]
+    for s, (p, n) in enumerate(SEQS):
+        lg, res = engine.forward_full_readback(gm, ref_kv[s], drafts[s], p, full_logits=True, want_residual=True)
+        q = int(out.q_starts[s])
+        print(f"{name} seq {s}: logits max|d| {np.abs(out.logits[q:q + n] - lg).max():.3e}", flush=True)
+        assert np.array_equal(out.logits[q:q + n], lg)
+        assert np.array_equal(out.residual[q:q + n], res)
+        assert np.array_equal(out.sampled[q:q + n], lg.argmax(axis=1).astype(np.uint32))
+        assert batch_kv[s].position == p + n
+        for a, b in zip(_kv_rows(batch_kv[s], gm, p, p + n), _kv_rows(ref_kv[s], gm, p, p + n)):
+            assert np.array_equal(a, b)
+    for kv in batch_kv + ref_kv:
+        kv.close()
+
+
+def test_unified_tree_and_chain_vs_oracle(engine, model):
+    """One tree sequence (branching 2, 2: 1 + 2 + 4 nodes below the root) next to a
+    chain; each compared bit-exactly with its own forward and, within the
+    north-star tolerance, with the oracle."""
+    name, img, gm = model
+    V = gm.vocab_size()
+    om = O.Model(img)
+    parents_tree = [-1, 0, 0, 1, 1, 2, 2]
+    seqs = [(24, S.tokens(301, 7, V), parents_tree), (16, S.tokens(302, 6, V), None)]
+    prompts = [S.tokens(400 + s, p, V) for s, (p, _, _) in enumerate(seqs)]
+    batch_kv = [_prefilled(engine, gm, pr) for pr in prompts]
+    toks = np.concatenate([t for _, t, _ in seqs])
+    lens = [len(t) for _, t, _ in seqs]
+    parents = np.array(parents_tree + [-1, 0, 1, 2, 3, 4], dtype=np.int32)
+    out = engine.verify_unified(gm, batch_kv, toks, lens, parents=parents, want_logits=True)
+    for s, (p, t, par) in enumerate(seqs):
+        q = int(out.q_starts[s])
+        n = len(t)
+        ref = _prefilled(engine, gm, prompts[s])
+        lg, _ = engine.forward_full_readback(gm, ref, t, p, full_logits=True, parents=par)
+        assert np.array_equal(out.logits[q:q + n], lg)
+        okv = O.KvCache(om, 256)
+        O.forward(om, okv, prompts[s], 0, logits_mode=0)
+        ol, _ = O.forward(om, okv, t, p, parents=par, logits_mode=2)
+        tol = np.maximum(2e-2, 1e-2 * np.abs(ol))
+        d = np.abs(out.logits[q:q + n] - ol)
+        print(f"{name} seq {s}: vs oracle max|d| {d.max():.3e}", flush=True)
+        assert np.all(d <= tol) and d.max() <= 3e-4 * np.abs(ol).max()
+        okv.close()
+        ref.close()
+    for kv in batch_kv:
+        kv.close()
+    om.close()
+
+
+def test_unified_errors(engine, model):
+    name, img, gm = model
+    V = gm.vocab_size()
+    a = _prefilled(engine, gm, S.tokens(1, 8, V), max_seq=32)
+    b = _prefilled(engine, gm, S.tokens(2, 8, V), max_seq=32)
+    t = S.tokens(3, 4, V)
+    with pytest.raises(SeekerError) as ei:
+        engine.verify_unified(gm, [a, a], np.concatenate([t, t]), [4, 4])
+    assert ei.value.status == SH_ERR_ARG
+    with pytest.raises(SeekerError) as ei:
+        engine.verify_unified(gm, [a, b], np.concatenate([t, t]), [4, 4], positions=np.arange(8))
+    assert ei.value.status == SH_ERR_ARG
+    with pytest.raises(SeekerError) as ei:
+        engine.verify_unified(gm, [a], S.tokens(4, 30, V), [30])
+    assert ei.value.status == SH_ERR_CAPACITY
+    assert a.position == 8 and b.position == 8  # failed calls leave the caches alone
+    a.close()
+    b.close()
