@@ -181,6 +181,26 @@ int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_log
                      const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s,
                      uint32_t* acc_len_dev, uint32_t* next_tok_dev);
 
+/* New (no reference counterpart): tree acceptance for B token trees of n <= 64
+ * nodes, recursive rejection sampling (SpecInfer multi-candidate speculative
+ * sampling; one candidate per step reduces to sh_accept_sample's REJECTION).
+ * Node 0 is the root (the last emitted token); parents_dev [B][n], parents[0]
+ * = -1, parents[i] < i; tokens_dev [B][n]. p_logits_dev [B][n][V] are the
+ * target logits after each node, q_logits_dev [B][n][V] the draft logits each
+ * node's children were drawn from (leaf rows unused; NULL for GREEDY). From the
+ * root, children are tried in index order: child c is accepted iff
+ * u * q(tok_c) < cur(tok_c), cur = softmax(p/T) at the node and, after each
+ * rejection, the normalised residual max(0, cur - q); with none accepted the
+ * next token is drawn from cur, after an accepted leaf from the leaf's p.
+ * GREEDY (or temperature 0) accepts the first child whose token is argmax p.
+ * Uniforms: word counter + 2(b n + c) accepts child c, + 2(b n + v) + 1 draws at
+ * node v (Philox key (seed, 0x5EC)), or explicit host uniforms [B][n][2].
+ * Outputs (device): path_dev [B][n] accepted node indices, root first;
+ * path_len_dev [B]; next_tok_dev [B]. Compact the path with sh_kv_compact. */
+int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev, const uint32_t* tokens_dev,
+                   const int32_t* parents_dev, uint32_t B, uint32_t n, uint32_t V, const sh_sampling* s,
+                   uint32_t* path_dev, uint32_t* path_len_dev, uint32_t* next_tok_dev);
+
 #ifdef __cplusplus
 }
 #endif

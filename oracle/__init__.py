@@ -54,6 +54,7 @@ _SIGS = {
     "or_sample_and_compare": (C.c_uint32, [F32P, C.c_uint32, U32P, C.c_uint32, C.POINTER(SamplerCfg), F32P, C.c_int,
                                            U32P]),
     "or_rejection": (C.c_uint32, [F32P, F32P, U32P, C.c_uint32, C.c_uint32, C.c_float, F32P, F32P, U32P]),
+    "or_tree_accept": (C.c_int, [F32P, F32P, U32P, I32P, C.c_uint32, C.c_uint32, C.c_float, F32P, U32P, U32P, U32P]),
     "or_probs": (None, [F32P, C.c_uint32, C.c_float, F32P]),
     "or_spec_step_greedy": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, U32P, U32P, U32P, U32P, U32P]),
 }
@@ -235,6 +236,25 @@ def rejection(p_logits, q_logits, drafts, temperature, u_acc, u_res):
     acc = lib().or_rejection(p.ctypes.data_as(F32P), q.ctypes.data_as(F32P), d.ctypes.data_as(U32P), k, V,
                              temperature, ua.ctypes.data_as(F32P), ur.ctypes.data_as(F32P), C.byref(nt))
     return int(acc), int(nt.value)
+
+
+def tree_accept(p_logits, q_logits, tokens, parents, temperature, u):
+    """Tree acceptance (or_tree_accept): returns (path list of node indices, next token).
+    p_logits, q_logits [n][V]; u [n][2] (accept, draw) uniforms; temperature 0 = greedy."""
+    p = _f32(p_logits)
+    q = _f32(q_logits)
+    n, V = p.shape
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    par = np.ascontiguousarray(parents, dtype=np.int32)
+    uu = _f32(u).reshape(-1)
+    path = np.zeros(n, dtype=np.uint32)
+    plen, nt = C.c_uint32(), C.c_uint32()
+    rc = lib().or_tree_accept(p.ctypes.data_as(F32P), q.ctypes.data_as(F32P), t.ctypes.data_as(U32P),
+                              par.ctypes.data_as(I32P), n, V, temperature, uu.ctypes.data_as(F32P),
+                              path.ctypes.data_as(U32P), C.byref(plen), C.byref(nt))
+    if rc:
+        raise ValueError("oracle tree_accept: malformed tree")
+    return path[: plen.value].tolist(), int(nt.value)
 
 
 def spec_step_greedy(tgt: Model, drf: Model, tkv: KvCache, dkv: KvCache, last_token: int, n_max: int):

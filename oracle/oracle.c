@@ -677,6 +677,86 @@ uint32_t or_rejection(const float* pl, const float* ql, const uint32_t* drafts, 
   return k;
 }
 
+/* Tree acceptance. The current distribution at a node starts as the target's
+ * softmax(p/T); each rejected child replaces it by max(0, cur - q) / Z (kept as
+ * the unnormalised r and its sum Z; unchanged when r is all zero). The final
+ * draw uses the unnormalised weights (softmax numerator, or r) with the first v
+ * whose vocab-order cumsum exceeds u * total, like or_rejection. All in f64. */
+int or_tree_accept(const float* pl, const float* ql, const uint32_t* tokens, const int32_t* parents, uint32_t n,
+                   uint32_t V, float temperature, const float* u, uint32_t* path, uint32_t* path_len,
+                   uint32_t* next_tok) {
+  if (n < 1 || parents[0] != -1) return -1;
+  for (uint32_t i = 1; i < n; ++i)
+    if (parents[i] < 0 || parents[i] >= (int32_t)i) return -1;
+  double* r = (double*)malloc((size_t)V * sizeof(double));
+  if (!r) return -1;
+  uint32_t v = 0, len = 1;
+  path[0] = 0;
+  for (;;) {
+    const float* p = pl + (size_t)v * V;
+    int32_t acc = -1;
+    if (temperature <= 0.f) {
+      const uint32_t t = or_argmax(p, V);
+      for (uint32_t c = v + 1; c < n && acc < 0; ++c)
+        if (parents[c] == (int32_t)v && tokens[c] == t) acc = (int32_t)c;
+      if (acc < 0) { *next_tok = t; break; }
+      v = (uint32_t)acc;
+      path[len++] = v;
+      continue;
+    }
+    const double T = temperature;
+    double pm, ps = row_stats(p, V, T, &pm);
+    const float* q = ql + (size_t)v * V;
+    double qm = 0.0, qs = 1.0;
+    int have_q = 0, resid = 0;
+    double Z = 1.0;
+    for (uint32_t c = v + 1; c < n && acc < 0; ++c) {
+      if (parents[c] != (int32_t)v) continue;
+      if (!have_q) { qs = row_stats(q, V, T, &qm); have_q = 1; }
+      const uint32_t tok = tokens[c];
+      if (tok < V) {
+        const double pc = resid ? r[tok] / Z : exp(((double)p[tok] - pm) / T) / ps;
+        const double qc = exp(((double)q[tok] - qm) / T) / qs;
+        if ((double)u[2 * c] * qc < pc) { acc = (int32_t)c; break; }
+      }
+      double R = 0.0;
+      for (uint32_t x = 0; x < V; ++x) {
+        const double cur = resid ? r[x] / Z : exp(((double)p[x] - pm) / T) / ps;
+        const double d = cur - exp(((double)q[x] - qm) / T) / qs;
+        R += d > 0.0 ? d : 0.0;
+      }
+      if (R > 0.0) {
+        for (uint32_t x = 0; x < V; ++x) {
+          const double cur = resid ? r[x] / Z : exp(((double)p[x] - pm) / T) / ps;
+          const double d = cur - exp(((double)q[x] - qm) / T) / qs;
+          r[x] = d > 0.0 ? d : 0.0;
+        }
+        Z = R;
+        resid = 1;
+      }
+    }
+    if (acc >= 0) {
+      v = (uint32_t)acc;
+      path[len++] = v;
+      continue;
+    }
+    double total = 0.0;
+    for (uint32_t x = 0; x < V; ++x) total += resid ? r[x] : exp(((double)p[x] - pm) / T);
+    const double target = (double)u[2 * v + 1] * total;
+    double cum = 0.0;
+    uint32_t tok = V - 1;
+    for (uint32_t x = 0; x < V; ++x) {
+      cum += resid ? r[x] : exp(((double)p[x] - pm) / T);
+      if (cum > target) { tok = x; break; }
+    }
+    *next_tok = tok;
+    break;
+  }
+  *path_len = len;
+  free(r);
+  return 0;
+}
+
 /* --------------------------------------------------------- spec step */
 
 /* Engine::decode_speculative (inference/mod.rs:2108-2297), greedy path, with a

@@ -89,6 +89,16 @@ uint32_t or_sample_and_compare(const float* logits, uint32_t V, const uint32_t* 
 uint32_t or_rejection(const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t k,
                       uint32_t V, float temperature, const float* u_acc, const float* u_res,
                       uint32_t* next_tok);
+/* Tree acceptance (new: recursive rejection sampling over a token tree, the
+ * multi-candidate speculative sampling of SpecInfer, Miao et al. 2024, with
+ * Chen et al. 2023's single-draft step). Node 0 is the root; parents[i] < i;
+ * p_logits [n][V] target logits at each node, q_logits [n][V] the draft logits
+ * each node's children were drawn from. u [n][2]: u[2c] accepts child c,
+ * u[2v+1] draws at node v. temperature 0: greedy. Returns 0 and writes the
+ * accepted path (root first), its length and the next token. */
+int or_tree_accept(const float* p_logits, const float* q_logits, const uint32_t* tokens, const int32_t* parents,
+                   uint32_t n, uint32_t V, float temperature, const float* u, uint32_t* path, uint32_t* path_len,
+                   uint32_t* next_tok);
 /* softmax(l/T) in f64, rounded to f32. */
 void or_probs(const float* logits, uint32_t V, float temperature, float* out);
 

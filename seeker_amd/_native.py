@@ -108,6 +108,7 @@ SIGNATURES = {
     "sh_qtensor_destroy": (None, [P]),
     "sh_gemv_quant": (C.c_int, [P, P, P, C.c_uint32, P, C.c_int]),
     "sh_accept_sample": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), P, P]),
+    "sh_tree_accept": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), P, P, P]),
 }
 
 SYNTH_SIGNATURES = {

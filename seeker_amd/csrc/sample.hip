@@ -83,10 +83,17 @@ struct RowW {
   }
 };
 
+// Weights held explicitly (the residual of a tree node after rejections).
+struct RowR {
+  const double* r;
+  __device__ __forceinline__ double w(uint32_t v) const { return r[v]; }
+};
+
 // Workgroup-wide inverse CDF: first v with cumsum(w) >= target (ge = true) or
 // > target (ge = false), where target = u * total; falls back to V-1.
 // Each thread owns a contiguous chunk, so cumsum order = vocab order.
-__device__ uint32_t wg_inverse_cdf(const RowW& rw, uint32_t V, float u, bool ge, double* total_out) {
+template <class W>
+__device__ uint32_t wg_inverse_cdf(const W& rw, uint32_t V, float u, bool ge, double* total_out) {
   __shared__ double part[257];
   __shared__ uint32_t found;
   const uint32_t t = threadIdx.x, C = (V + 255) / 256;
@@ -196,6 +203,142 @@ __global__ __launch_bounds__(256) void k_decide_reject(const float* __restrict__
   }
 }
 
+// Orderable argmax key: larger float -> larger key, ties -> lower index; NaN loses.
+__device__ __forceinline__ unsigned long long tree_amax_key(float v, uint32_t idx) {
+  if (v != v) return 0ull;
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)b << 32) | (unsigned long long)(~idx);
+}
+
+// Tree acceptance, one workgroup per tree (b): walk from the root; children of
+// the current node v are tried in index order, child c accepted iff
+// u * q(tok_c) < cur(tok_c), where cur starts as softmax(p_v / T) and after
+// each rejection becomes max(0, cur - q_v) / Z (kept unnormalised in r with its
+// sum Z; unchanged if that is all zero). With no child accepted the next token
+// is drawn from cur (softmax numerator or r, first v with cumsum > u * total);
+// an accepted leaf draws from its own p. Greedy: the child whose token is the
+// argmax of p_v. Uniform words: counter + 2 (b n + c) to accept child c,
+// counter + 2 (b n + v) + 1 to draw at v.
+__global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p, const float* __restrict__ q,
+                                                     const uint32_t* __restrict__ tokens,
+                                                     const int32_t* __restrict__ parents, uint32_t n, uint32_t V,
+                                                     double inv_t, int greedy, const float* u_dev, uint64_t seed,
+                                                     uint64_t counter, double* __restrict__ rbuf,
+                                                     uint32_t* __restrict__ path_out, uint32_t* __restrict__ path_len,
+                                                     uint32_t* __restrict__ next_tok) {
+  __shared__ float shf[4];
+  __shared__ double shd[4];
+  __shared__ unsigned long long shk[4];
+  __shared__ int s_acc;
+  __shared__ uint32_t s_path[64];
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  const float* P = p + (size_t)b * n * V;
+  const float* Q = q ? q + (size_t)b * n * V : nullptr;
+  const uint32_t* tok = tokens + (size_t)b * n;
+  const int32_t* par = parents + (size_t)b * n;
+  double* r = rbuf ? rbuf + (size_t)b * V : nullptr;
+  uint32_t v = 0, len = 1, out_tok = 0;
+  if (t == 0) s_path[0] = 0;
+  for (;;) {
+    const float* pv = P + (size_t)v * V;
+    int acc = -1;
+    if (greedy) {
+      unsigned long long best = 0ull;
+      for (uint32_t i = t; i < V; i += 256) {
+        const unsigned long long k = tree_amax_key(pv[i], i);
+        best = k > best ? k : best;
+      }
+      for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+      }
+      __syncthreads();
+      if ((t & 63) == 0) shk[t >> 6] = best;
+      __syncthreads();
+      for (int w = 0; w < 4; ++w) best = shk[w] > best ? shk[w] : best;
+      const uint32_t am = best == 0ull ? 0u : ~(uint32_t)(best & 0xFFFFFFFFull);
+      for (uint32_t c = v + 1; c < n && acc < 0; ++c)
+        if (par[c] == (int32_t)v && tok[c] == am) acc = (int)c;
+      if (acc < 0) { out_tok = am; break; }
+    } else {
+      float mx = -INFINITY;
+      for (uint32_t i = t; i < V; i += 256) mx = fmaxf(mx, pv[i]);
+      const double pm = block_max_f(mx, shf);
+      double ssum = 0.0;
+      for (uint32_t i = t; i < V; i += 256) ssum += exp(((double)pv[i] - pm) * inv_t);
+      const double ps = block_sum_d(ssum, shd);
+      const float* qv = Q + (size_t)v * V;
+      double qm = 0.0, qs = 1.0, Z = 1.0;
+      bool have_q = false, resid = false;
+      for (uint32_t c = v + 1; c < n; ++c) {
+        if (par[c] != (int32_t)v) continue;
+        if (!have_q) {
+          float qx = -INFINITY;
+          for (uint32_t i = t; i < V; i += 256) qx = fmaxf(qx, qv[i]);
+          qm = block_max_f(qx, shf);
+          double qsum = 0.0;
+          for (uint32_t i = t; i < V; i += 256) qsum += exp(((double)qv[i] - qm) * inv_t);
+          qs = block_sum_d(qsum, shd);
+          have_q = true;
+        }
+        if (t == 0) {
+          const uint32_t tc = tok[c];
+          bool ok = false;
+          if (tc < V) {
+            const double pc = resid ? r[tc] / Z : exp(((double)pv[tc] - pm) * inv_t) / ps;
+            const double qc = exp(((double)qv[tc] - qm) * inv_t) / qs;
+            ok = (double)uniform_at(u_dev, seed, counter + 2ull * ((uint64_t)b * n + c)) * qc < pc;
+          }
+          s_acc = ok ? 1 : 0;
+        }
+        __syncthreads();
+        if (s_acc) { acc = (int)c; break; }
+        // reject: cur <- max(0, cur - q) / Z (two passes; r is rewritten only
+        // after the sum over the old values is complete)
+        double part = 0.0;
+        for (uint32_t i = t; i < V; i += 256) {
+          const double cur = resid ? r[i] / Z : exp(((double)pv[i] - pm) * inv_t) / ps;
+          const double d = cur - exp(((double)qv[i] - qm) * inv_t) / qs;
+          part += d > 0.0 ? d : 0.0;
+        }
+        const double R = block_sum_d(part, shd);
+        if (R > 0.0) {
+          for (uint32_t i = t; i < V; i += 256) {
+            const double cur = resid ? r[i] / Z : exp(((double)pv[i] - pm) * inv_t) / ps;
+            const double d = cur - exp(((double)qv[i] - qm) * inv_t) / qs;
+            r[i] = d > 0.0 ? d : 0.0;
+          }
+          __syncthreads();
+          Z = R;
+          resid = true;
+        }
+      }
+      if (acc < 0) {
+        const float ud = uniform_at(u_dev, seed, counter + 2ull * ((uint64_t)b * n + v) + 1ull);
+        if (resid) {
+          __threadfence_block();
+          RowR rr{r};
+          out_tok = wg_inverse_cdf(rr, V, ud, false, nullptr);
+        } else {
+          RowW rw{pv, nullptr, pm, ps, 0.0, 1.0, inv_t};
+          out_tok = wg_inverse_cdf(rw, V, ud, false, nullptr);
+        }
+        break;
+      }
+    }
+    v = (uint32_t)acc;
+    if (t == 0) s_path[len] = v;
+    ++len;
+    __syncthreads();
+  }
+  if (t == 0) {
+    for (uint32_t i = 0; i < len; ++i) path_out[(size_t)b * n + i] = s_path[i];
+    path_len[b] = len;
+    next_tok[b] = out_tok;
+  }
+}
+
 }  // namespace
 
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
@@ -251,6 +394,49 @@ extern "C" int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const f
                             acc_len_dev, next_tok_dev);
   if (udev) (void)hipFreeAsync(udev, e->stream);
   if (rc) return rc;
+  SH_HIP(hipStreamSynchronize(e->stream));
+  return sh_prof_flush(e);
+}
+
+extern "C" int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
+                              const uint32_t* tokens_dev, const int32_t* parents_dev, uint32_t B, uint32_t n,
+                              uint32_t V, const sh_sampling* s, uint32_t* path_dev, uint32_t* path_len_dev,
+                              uint32_t* next_tok_dev) {
+  SH_CHECK(e && p_logits_dev && tokens_dev && parents_dev && s && path_dev && path_len_dev && next_tok_dev,
+           SH_ERR_ARG, "sh_tree_accept: NULL argument");
+  SH_CHECK(B >= 1 && n >= 1 && n <= 64 && V >= 1, SH_ERR_ARG, "tree_accept: B=%u n=%u V=%u (n <= 64)", B, n, V);
+  const bool greedy = s->mode == SH_SAMPLE_GREEDY || !(s->temperature > 0.f);
+  SH_CHECK(greedy || s->mode == SH_SAMPLE_REJECTION, SH_ERR_ARG, "tree_accept: mode %u (GREEDY or REJECTION)",
+           s->mode);
+  SH_CHECK(greedy || q_logits_dev, SH_ERR_ARG, "tree_accept: rejection sampling needs draft logits");
+  // tree shape is validated on the host copy (parents[i] < i, parents[0] = -1)
+  std::vector<int32_t> par((size_t)B * n);
+  SH_HIP(hipMemcpyAsync(par.data(), parents_dev, par.size() * 4, hipMemcpyDeviceToHost, e->stream));
+  SH_HIP(hipStreamSynchronize(e->stream));
+  for (uint32_t b = 0; b < B; ++b) {
+    SH_CHECK(par[(size_t)b * n] == -1, SH_ERR_ARG, "tree_accept: tree %u root parent must be -1", b);
+    for (uint32_t i = 1; i < n; ++i)
+      SH_CHECK(par[(size_t)b * n + i] >= 0 && par[(size_t)b * n + i] < (int32_t)i, SH_ERR_ARG,
+               "tree_accept: tree %u node %u parent %d must precede it", b, i, par[(size_t)b * n + i]);
+  }
+  float* udev = nullptr;
+  double* r = nullptr;
+  if (s->uniforms) {
+    const size_t nu = (size_t)B * n * 2;
+    SH_HIP(hipMallocAsync((void**)&udev, nu * 4, e->stream));
+    SH_HIP(hipMemcpyAsync(udev, s->uniforms, nu * 4, hipMemcpyHostToDevice, e->stream));
+  }
+  if (!greedy) SH_HIP(hipMallocAsync((void**)&r, (size_t)B * V * sizeof(double), e->stream));
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  hipLaunchKernelGGL(k_tree_accept, dim3(B), dim3(256), 0, e->stream, p_logits_dev, greedy ? nullptr : q_logits_dev,
+                     tokens_dev, parents_dev, n, V, greedy ? 1.0 : 1.0 / (double)s->temperature, greedy ? 1 : 0,
+                     udev, s->seed, udev ? 0ull : s->counter, r, path_dev, path_len_dev, next_tok_dev);
+  hipError_t le = hipGetLastError();
+  sh_prof_end(e, "tree_accept", 4.0 * V * B * n * (greedy ? 1 : 2), ev);
+  if (udev) (void)hipFreeAsync(udev, e->stream);
+  if (r) (void)hipFreeAsync(r, e->stream);
+  SH_CHECK(le == hipSuccess, SH_ERR_HIP, "tree_accept launch: %s", hipGetErrorString(le));
   SH_HIP(hipStreamSynchronize(e->stream));
   return sh_prof_flush(e);
 }

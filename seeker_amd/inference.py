@@ -200,6 +200,13 @@ class Engine:
         N.check(self._lib.sh_accept_sample(self.h, p_logits.ptr, q_logits.ptr if q_logits else None, drafts.ptr,
                                            B, k, V, C.byref(s), acc_len.ptr, next_tok.ptr))
 
+    def tree_accept(self, p_logits: "DeviceBuffer", q_logits: Optional["DeviceBuffer"], tokens: "DeviceBuffer",
+                    parents: "DeviceBuffer", B: int, n: int, V: int, s: N.sh_sampling, path: "DeviceBuffer",
+                    path_len: "DeviceBuffer", next_tok: "DeviceBuffer"):
+        """Tree acceptance (sh_tree_accept) over B trees of n nodes; all buffers on the device."""
+        N.check(self._lib.sh_tree_accept(self.h, p_logits.ptr, q_logits.ptr if q_logits else None, tokens.ptr,
+                                         parents.ptr, B, n, V, C.byref(s), path.ptr, path_len.ptr, next_tok.ptr))
+
 
 class DeviceBuffer:
     def __init__(self, engine: Engine, ptr: C.c_void_p, nbytes: int):

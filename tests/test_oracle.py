@@ -397,6 +397,84 @@ def test_rejection_output_distribution_is_p():
     assert chi2 < 30.0
 
 
+# ------------------------------------------------------------------ tree acceptance
+
+def _chain(k):
+    return np.arange(-1, k, dtype=np.int32)  # node i's parent is i - 1
+
+
+def test_tree_accept_chain_equals_rejection():
+    """A chain-shaped tree is the single-draft case: with u_acc[i] = u[2(i+1)] and
+    u_res[i] = u[2i+1] it must reproduce or_rejection token for token."""
+    rng = np.random.default_rng(11)
+    V, T = 40, 0.9
+    for trial in range(200):
+        k = int(rng.integers(1, 6))
+        p = (rng.standard_normal((k + 1, V)) * 2).astype(np.float32)
+        q = (p + rng.standard_normal((k + 1, V))).astype(np.float32)
+        drafts = rng.integers(0, V, k).astype(np.uint32)
+        u = rng.random((k + 1, 2)).astype(np.float32)
+        acc, nt = O.rejection(p, q[:k], drafts, T, u[1:, 0].copy(), u[:, 1].copy())
+        tokens = np.concatenate([[0], drafts]).astype(np.uint32)
+        path, nt2 = O.tree_accept(p, q, tokens, _chain(k), T, u)
+        assert path == list(range(acc + 1)) and nt2 == nt, (trial, acc, nt, path, nt2)
+
+
+def test_tree_accept_greedy_walk():
+    rng = np.random.default_rng(12)
+    V = 7
+    parents = np.array([-1, 0, 0, 0, 1, 1, 2, 4, 4], np.int32)
+    n = parents.size
+    for _ in range(300):
+        p = rng.standard_normal((n, V)).astype(np.float32)
+        tokens = rng.integers(0, V, n).astype(np.uint32)
+        path, nt = O.tree_accept(p, p, tokens, parents, 0.0, np.zeros((n, 2), np.float32))
+        v, want = 0, [0]
+        while True:
+            t = int(np.argmax(p[v]))
+            kids = [c for c in range(v + 1, n) if parents[c] == v and tokens[c] == t]
+            if not kids:
+                break
+            v = kids[0]
+            want.append(v)
+        assert path == want and nt == int(np.argmax(p[v]))
+
+
+def test_tree_accept_q_equals_p_accepts_first_child():
+    rng = np.random.default_rng(13)
+    V, T = 30, 1.0
+    parents = np.array([-1, 0, 0, 1, 1], np.int32)
+    for _ in range(50):
+        p = rng.standard_normal((5, V)).astype(np.float32)
+        tokens = rng.integers(0, V, 5).astype(np.uint32)
+        u = (rng.random((5, 2)) * 0.999).astype(np.float32)
+        path, _ = O.tree_accept(p, p, tokens, parents, T, u)
+        assert path[:3] == [0, 1, 3]
+
+
+def test_tree_accept_first_token_distribution_is_p():
+    """Losslessness: with m children drawn i.i.d. from q at the root, the first
+    token after the root (accepted child or resampled) is distributed as p."""
+    rng = np.random.default_rng(14)
+    V, T, m = 6, 1.0, 3
+    p = np.zeros((m + 1, V), np.float32)
+    q = np.zeros((m + 1, V), np.float32)
+    p[0] = rng.standard_normal(V)
+    q[0] = rng.standard_normal(V)
+    pp = O.probs(p[0], T).astype(np.float64)
+    qq = O.probs(q[0], T).astype(np.float64)
+    parents = np.array([-1] + [0] * m, np.int32)
+    n = 8000
+    cnt = np.zeros(V)
+    for _ in range(n):
+        kids = rng.choice(V, size=m, p=qq / qq.sum())
+        tokens = np.concatenate([[0], kids]).astype(np.uint32)
+        path, nt = O.tree_accept(p, q, tokens, parents, T, rng.random((m + 1, 2)).astype(np.float32))
+        cnt[int(tokens[path[1]]) if len(path) > 1 else nt] += 1
+    chi2 = np.sum((cnt - n * pp) ** 2 / (n * pp))
+    assert chi2 < 30.0, (cnt / n, pp)
+
+
 # ------------------------------------------------------------------ spec step
 
 def test_spec_greedy_lossless():
