@@ -201,6 +201,17 @@ int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const float* q_logit
                    const int32_t* parents_dev, uint32_t B, uint32_t n, uint32_t V, const sh_sampling* s,
                    uint32_t* path_dev, uint32_t* path_len_dev, uint32_t* next_tok_dev);
 
+/* New (no reference counterpart): one tree verification step for B sequences
+ * (configs[3]): sh_verify_unified over B trees of n nodes each (tokens, parents
+ * [B][n] host; node 0 = the sequence's last emitted token, parents[0] = -1),
+ * target logits kept on the device, sh_tree_accept against q_logits_dev
+ * [B][n][V] (NULL for GREEDY), then sh_kv_compact of each accepted path
+ * (node path[i] -> slot pos + i; position = pos + path_len). Outputs (host):
+ * path_out [B][n], path_len_out [B], next_tok_out [B]. */
+int sh_tree_verify_step(sh_engine* e, sh_model* target, sh_kv* const* caches, uint32_t B, uint32_t n,
+                        const uint32_t* tokens, const int32_t* parents, const float* q_logits_dev,
+                        const sh_sampling* s, uint32_t* path_out, uint32_t* path_len_out, uint32_t* next_tok_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,6 +109,8 @@ SIGNATURES = {
     "sh_gemv_quant": (C.c_int, [P, P, P, C.c_uint32, P, C.c_int]),
     "sh_accept_sample": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), P, P]),
     "sh_tree_accept": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), P, P, P]),
+    "sh_tree_verify_step": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, C.c_uint32, U32P, I32P, P,
+                                      C.POINTER(sh_sampling), U32P, U32P, U32P]),
 }
 
 SYNTH_SIGNATURES = {

@@ -906,10 +906,11 @@ extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint
   return sh_prof_flush(e);
 }
 
-extern "C" int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B,
-                                 const uint32_t* tokens, const uint32_t* seq_lens, const uint32_t* positions,
-                                 const int32_t* parents, float* logits_out, uint32_t* sampled_out,
-                                 float* residual_out) {
+// Batched verify; logits go to the host (logits_out) and/or the device
+// (logits_dev, [N_total][V]).
+static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B, const uint32_t* tokens,
+                               const uint32_t* seq_lens, const uint32_t* positions, const int32_t* parents,
+                               float* logits_out, float* logits_dev, uint32_t* sampled_out, float* residual_out) {
   SH_CHECK(e && m && caches && tokens && seq_lens, SH_ERR_ARG, "sh_verify_unified: NULL argument");
   SH_CHECK(B >= 1, SH_ERR_ARG, "verify_unified: empty batch");
   // prefix-sum column starts (q_starts) and per-sequence plans
@@ -955,7 +956,7 @@ extern "C" int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches
   if ((rc = upload_tokens(m, tokens, N, &dt))) return rc;
   uint32_t* ids = nullptr;
   if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, 8 * 4, e->stream));
-  const bool want_logits = logits_out || sampled_out;
+  const bool want_logits = logits_out || logits_dev || sampled_out;
   for (uint32_t c0 = 0; c0 < N && !rc; c0 += 8) {
     const uint32_t nc = std::min<uint32_t>(8, N - c0);
     // one attention segment per run of one sequence's columns in the chunk
@@ -985,6 +986,9 @@ extern "C" int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches
     if (logits_out)
       SH_HIP(hipMemcpyAsync(logits_out + (size_t)c0 * m->V, m->ws.logits, (size_t)nc * m->V * 4,
                             hipMemcpyDeviceToHost, e->stream));
+    if (logits_dev)
+      SH_HIP(hipMemcpyAsync(logits_dev + (size_t)c0 * m->V, m->ws.logits, (size_t)nc * m->V * 4,
+                            hipMemcpyDeviceToDevice, e->stream));
     if (sampled_out) {
       if ((rc = sh_argmax_launch(e, m->ws.logits, m->V, nc, m->ws.amax, ids))) break;
       SH_HIP(hipMemcpyAsync(sampled_out + c0, ids, (size_t)nc * 4, hipMemcpyDeviceToHost, e->stream));
@@ -1000,6 +1004,64 @@ extern "C" int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches
     caches[s]->pending.clear();
   }
   return sh_prof_flush(e);
+}
+
+extern "C" int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B,
+                                 const uint32_t* tokens, const uint32_t* seq_lens, const uint32_t* positions,
+                                 const int32_t* parents, float* logits_out, uint32_t* sampled_out,
+                                 float* residual_out) {
+  return verify_unified_impl(e, m, caches, B, tokens, seq_lens, positions, parents, logits_out, nullptr, sampled_out,
+                             residual_out);
+}
+
+extern "C" int sh_tree_verify_step(sh_engine* e, sh_model* target, sh_kv* const* caches, uint32_t B, uint32_t n,
+                                   const uint32_t* tokens, const int32_t* parents, const float* q_logits_dev,
+                                   const sh_sampling* s, uint32_t* path_out, uint32_t* path_len_out,
+                                   uint32_t* next_tok_out) {
+  SH_CHECK(e && target && caches && tokens && parents && s && path_out && path_len_out && next_tok_out, SH_ERR_ARG,
+           "sh_tree_verify_step: NULL argument");
+  SH_CHECK(B >= 1 && n >= 1 && n <= 64, SH_ERR_ARG, "tree_verify_step: B=%u n=%u (n <= 64)", B, n);
+  const uint32_t V = target->V;
+  std::vector<uint32_t> lens(B, n), base(B);
+  for (uint32_t b = 0; b < B; ++b) {
+    SH_CHECK(caches[b], SH_ERR_ARG, "tree_verify_step: cache %u is NULL", b);
+    base[b] = caches[b]->pos;
+  }
+  float* lg = nullptr;
+  uint32_t *dtok = nullptr, *dpath = nullptr, *dlen = nullptr, *dnext = nullptr;
+  int32_t* dpar = nullptr;
+  SH_HIP(hipMallocAsync((void**)&lg, (size_t)B * n * V * 4, e->stream));
+  int rc = verify_unified_impl(e, target, caches, B, tokens, lens.data(), nullptr, parents, nullptr, lg, nullptr,
+                               nullptr);
+  if (!rc) {
+    hipError_t me = hipMallocAsync((void**)&dtok, (size_t)B * n * 4, e->stream);
+    if (me == hipSuccess) me = hipMallocAsync((void**)&dpar, (size_t)B * n * 4, e->stream);
+    if (me == hipSuccess) me = hipMallocAsync((void**)&dpath, (size_t)B * n * 4, e->stream);
+    if (me == hipSuccess) me = hipMallocAsync((void**)&dlen, (size_t)B * 4, e->stream);
+    if (me == hipSuccess) me = hipMallocAsync((void**)&dnext, (size_t)B * 4, e->stream);
+    if (me == hipSuccess) me = hipMemcpyAsync(dtok, tokens, (size_t)B * n * 4, hipMemcpyHostToDevice, e->stream);
+    if (me == hipSuccess) me = hipMemcpyAsync(dpar, parents, (size_t)B * n * 4, hipMemcpyHostToDevice, e->stream);
+    if (me != hipSuccess) { sh_set_error("tree_verify_step: %s", hipGetErrorString(me)); rc = SH_ERR_HIP; }
+  }
+  if (!rc) rc = sh_tree_accept(e, lg, q_logits_dev, dtok, dpar, B, n, V, s, dpath, dlen, dnext);
+  if (!rc) {
+    hipError_t me = hipMemcpyAsync(path_out, dpath, (size_t)B * n * 4, hipMemcpyDeviceToHost, e->stream);
+    if (me == hipSuccess) me = hipMemcpyAsync(path_len_out, dlen, (size_t)B * 4, hipMemcpyDeviceToHost, e->stream);
+    if (me == hipSuccess) me = hipMemcpyAsync(next_tok_out, dnext, (size_t)B * 4, hipMemcpyDeviceToHost, e->stream);
+    if (me == hipSuccess) me = hipStreamSynchronize(e->stream);
+    if (me != hipSuccess) { sh_set_error("tree_verify_step readback: %s", hipGetErrorString(me)); rc = SH_ERR_HIP; }
+  }
+  (void)hipFreeAsync(lg, e->stream);
+  if (dtok) (void)hipFreeAsync(dtok, e->stream);
+  if (dpar) (void)hipFreeAsync(dpar, e->stream);
+  if (dpath) (void)hipFreeAsync(dpath, e->stream);
+  if (dlen) (void)hipFreeAsync(dlen, e->stream);
+  if (dnext) (void)hipFreeAsync(dnext, e->stream);
+  if (rc) return rc;
+  // keep the accepted path's K/V rows: node path[i] -> slot base + i
+  for (uint32_t b = 0; b < B && !rc; ++b)
+    rc = sh_kv_compact(caches[b], base[b], path_out + (size_t)b * n, path_len_out[b]);
+  return rc;
 }
 
 // ------------------------------------------------------------------ spec step

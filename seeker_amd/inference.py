@@ -151,6 +151,23 @@ class Engine:
         q_starts = np.concatenate([[0], np.cumsum(sl)[:-1]]).astype(np.uint64)
         return VerifyUnifiedOut(sampled, logits, resid, q_starts)
 
+    def tree_verify_step(self, target: "Model", caches: Sequence["KvCache"], tokens: np.ndarray,
+                         parents: np.ndarray, q_logits: Optional["DeviceBuffer"], s: N.sh_sampling):
+        """One tree verification step (sh_tree_verify_step) for B trees of n nodes:
+        returns (paths: list of node-index lists, next_tokens [B]); caches hold the paths."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        par = np.ascontiguousarray(parents, dtype=np.int32)
+        B, n = t.shape
+        hs = (C.c_void_p * B)(*[c.h for c in caches])
+        path = np.zeros((B, n), dtype=np.uint32)
+        plen = np.zeros(B, dtype=np.uint32)
+        nxt = np.zeros(B, dtype=np.uint32)
+        N.check(self._lib.sh_tree_verify_step(
+            self.h, target.h, C.cast(hs, C.POINTER(C.c_void_p)), B, n, t.ctypes.data_as(N.U32P),
+            par.ctypes.data_as(N.I32P), q_logits.ptr if q_logits is not None else None, C.byref(s),
+            path.ctypes.data_as(N.U32P), plen.ctypes.data_as(N.U32P), nxt.ctypes.data_as(N.U32P)))
+        return [path[b, : plen[b]].tolist() for b in range(B)], nxt
+
     def decode_speculative(self, target: "Model", draft: "Model", tcache: "KvCache", dcache: "KvCache",
                            last_token: int, n_max: int, sampler: Optional[N.sh_sampling] = None) -> SpecStepOut:
         """Engine::decode_speculative (inference/mod.rs:2108-2297) with a separate draft model."""

@@ -134,3 +134,51 @@ def test_unified_errors(engine, model):
     assert a.position == 8 and b.position == 8  # failed calls leave the caches alone
     a.close()
     b.close()
+
+
+def test_tree_verify_step(engine, model):
+    """sh_tree_verify_step = verify_unified (device logits) + tree acceptance +
+    path compaction: the path equals the oracle's acceptance on the same verify
+    logits, and decoding continues from the compacted cache as it does after a
+    plain chain forward of the accepted path."""
+    from seeker_amd._native import SH_SAMPLE_REJECTION, sh_sampling
+    name, img, gm = model
+    V = gm.vocab_size()
+    par1 = np.array([-1, 0, 0, 1, 1, 2, 2], np.int32)  # branching 2, 2
+    B, n = 3, par1.size
+    prompts = [S.tokens(500 + b, 12 + 5 * b, V) for b in range(B)]
+    tokens = np.stack([np.concatenate([[int(pr[-1])], S.tokens(600 + b, n - 1, V)]) for b, pr in
+                       enumerate(prompts)]).astype(np.uint32)
+    parents = np.tile(par1, (B, 1))
+    # reference logits from a plain batched verify of the same trees
+    ref_kv = [_prefilled(engine, gm, pr[:-1]) for pr in prompts]
+    out = engine.verify_unified(gm, ref_kv, tokens.reshape(-1), [n] * B, parents=parents.reshape(-1),
+                                want_logits=True)
+    q = S.normal_f32(9, 9, B * n * V, 0.0, 3.0).reshape(B, n, V)
+    q[0] = out.logits[:n]  # q = p: tree 0 accepts the first child at every level (path 0, 1, 3)
+    qd = engine.to_device(q)
+    s = sh_sampling()
+    s.mode, s.temperature, s.seed, s.counter = SH_SAMPLE_REJECTION, 1.0, 17, 0
+    U = O.philox_uniforms(17, 0x5EC, 0, 2 * B * n).reshape(B, n, 2)
+    kv = [_prefilled(engine, gm, pr[:-1]) for pr in prompts]
+    paths, nxt = engine.tree_verify_step(gm, kv, tokens, parents, qd, s)
+    for b in range(B):
+        lg = out.logits[b * n:(b + 1) * n]
+        opath, onext = O.tree_accept(lg, q[b], tokens[b], parents[b], 1.0, U[b])
+        print(f"{name} tree {b}: path {paths[b]} next {nxt[b]}", flush=True)
+        assert paths[b] == opath and nxt[b] == onext
+        if b == 0:
+            assert paths[b] == [0, 1, 3]
+        base = len(prompts[b]) - 1
+        assert kv[b].position == base + len(paths[b])
+        # continue after the compacted path vs after a chain forward of it
+        chain = _prefilled(engine, gm, prompts[b][:-1])
+        engine.forward_full_readback(gm, chain, tokens[b][paths[b]], base, full_logits=False)
+        a, _ = engine.forward_full_readback(gm, kv[b], [int(nxt[b])], kv[b].position, full_logits=False)
+        c, _ = engine.forward_full_readback(gm, chain, [int(nxt[b])], chain.position, full_logits=False)
+        d = np.abs(a - c).max()
+        assert d <= 3e-4 * np.abs(c).max(), d
+        chain.close()
+    qd.free()
+    for x in kv + ref_kv:
+        x.close()
