@@ -66,6 +66,100 @@ def measured_traffic(kernel_tag):
     return None if k is None else k["fetch_bytes"] + k["write_bytes"]
 
 
+def measure_acceptance(eng, reps=20):
+    """the acceptance kernel alone (REJECTION, T = 0.8), B = 32, k = 8,
+    V = 128256; target logits N(0, 3), draft = target + N(0, 1), drafts sampled
+    from the draft distribution (numpy), uniforms Philox (seed 7) in the kernel.
+    Bytes per call = 4 V B (2k + 1) (one read of every target and draft logit)."""
+    import numpy as np
+    from seeker_amd import synth as S
+    from seeker_amd._native import SH_SAMPLE_REJECTION, sh_sampling
+    B, k, V, T = 32, 8, 128256, 0.8
+    p = S.normal_f32(7, 10, B * (k + 1) * V, 0.0, 3.0).reshape(B, k + 1, V)
+    q = (p[:, :k] + S.normal_f32(7, 11, B * k * V, 0.0, 1.0).reshape(B, k, V)).astype(np.float32)
+    rng = np.random.default_rng(7)
+    z = q.reshape(B * k, V).astype(np.float64) / T
+    z = np.exp(z - z.max(axis=1, keepdims=True))
+    cdf = np.cumsum(z, axis=1)
+    u = rng.random(B * k) * cdf[:, -1]
+    drafts = np.array([int(np.searchsorted(cdf[i], u[i], side="right")) for i in range(B * k)],
+                      dtype=np.uint32).reshape(B, k)
+    pd, qd, dd = eng.to_device(p), eng.to_device(q), eng.to_device(drafts)
+    acc, nxt = eng.dev_alloc(4 * B), eng.dev_alloc(4 * B)
+    s = sh_sampling()
+    s.mode, s.temperature, s.seed, s.counter = SH_SAMPLE_REJECTION, T, 7, 0
+    for _ in range(3):
+        eng.accept_sample(pd, qd, dd, B, k, V, s, acc, nxt)
+    eng.set_profiling(True)
+    eng.profile(reset=True)
+    t = time.perf_counter()
+    for _ in range(reps):
+        eng.accept_sample(pd, qd, dd, B, k, V, s, acc, nxt)
+    wall_ms = (time.perf_counter() - t) * 1e3 / reps
+    prof = eng.profile(reset=True)
+    eng.set_profiling(False)
+    kern_ms = sum(prof[n]["ms"] for n in ("accept_stats", "accept_decide") if n in prof) / reps
+    al = acc.read(np.uint32, B)
+    for x in (pd, qd, dd, acc, nxt):
+        x.free()
+    nbytes = 4 * V * B * (2 * k + 1)
+    log(f"acceptance kernel B={B} k={k} V={V}: {kern_ms * 1e3:.1f} us in kernels, {wall_ms * 1e3:.1f} us per call")
+    return {"config": "B=32, k=8, V=128256, REJECTION T=0.8, Philox seed 7", "kernel_us": round(kern_ms * 1e3, 2),
+            "call_us": round(wall_ms * 1e3, 2), "alg_bytes": nbytes,
+            "GBps": round(nbytes / kern_ms / 1e6, 1), "frac": round(nbytes / kern_ms / 1e6 / HBM_PEAK_GBS, 4),
+            "mean_accepted": round(float(al.mean()), 3)}
+
+
+def measure_tree(eng, tm, d, P=8192, reps=3):
+    """one tree verification step (sh_tree_verify_step) on the 8B
+    target, B = 4 sequences at context 8192, trees of depth 3 with branching
+    4, 3, 2 (41 nodes with the root), REJECTION at T = 1.0 (Philox seed 11)
+    against synthetic draft logits N(0, 3), then compaction of the accepted
+    paths. The KV position is set to 8192 without a prefill (the bytes read and
+    the work are the same). Bytes per step: every weight matrix once + K/V read
+    for [0, P + 41) of each sequence + 41 K/V rows written per sequence."""
+    import numpy as np
+    from seeker_amd import synth as S
+    from seeker_amd._native import SH_SAMPLE_REJECTION, sh_sampling
+    B, branching = 4, (4, 3, 2)
+    parents, level = [-1], [0]
+    for b in branching:
+        nxt_level = []
+        for v in level:
+            for _ in range(b):
+                parents.append(v)
+                nxt_level.append(len(parents) - 1)
+        level = nxt_level
+    n = len(parents)
+    V = d.n_vocab
+    caches = [eng.allocate_kv_cache(tm, P + 64) for _ in range(B)]
+    tokens = np.stack([S.tokens(900 + b, n, V) for b in range(B)]).astype(np.uint32)
+    par = np.tile(np.array(parents, np.int32), (B, 1))
+    qd = eng.to_device(S.normal_f32(11, 12, B * n * V, 0.0, 3.0))
+    s = sh_sampling()
+    s.mode, s.temperature, s.seed, s.counter = SH_SAMPLE_REJECTION, 1.0, 11, 0
+    times, plens = [], []
+    for i in range(reps + 1):
+        for c in caches:
+            c.set_position(P)
+        t = time.perf_counter()
+        paths, _ = eng.tree_verify_step(tm, caches, tokens, par, qd, s)
+        if i:
+            times.append((time.perf_counter() - t) * 1e3)
+            plens += [len(x) for x in paths]
+    qd.free()
+    for c in caches:
+        c.close()
+    w, _, _ = verify_bytes(d, 0, 0)
+    dkv = d.head_dim * d.n_head_kv
+    kv = B * 2 * d.n_layer * ((P + n) * dkv * 2 + n * dkv * 2)
+    ms = statistics.median(times)
+    log(f"tree verify step B={B} n={n} ctx {P}: {ms:.2f} ms, mean path {np.mean(plens):.2f} nodes")
+    return {"config": f"B={B}, tree 4x3x2 ({n} nodes), ctx {P}, REJECTION T=1.0 seed 11, synthetic draft logits",
+            "ms": round(ms, 3), "alg_bytes": w + kv, "GBps": round((w + kv) / ms / 1e6, 1),
+            "frac": round((w + kv) / ms / 1e6 / HBM_PEAK_GBS, 4), "mean_path_nodes": round(float(np.mean(plens)), 3)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -75,6 +169,7 @@ def main():
     ap.add_argument("--k", type=int, default=7)
     ap.add_argument("--verify-reps", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel and tree-verify lines")
     ap.add_argument("--profile-only", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -207,6 +302,11 @@ def main():
     log(f"{args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {emitted} tokens, "
         f"acceptance {accepted / (args.steps * args.k):.3f}")
 
+    extra_acc = extra_tree = None
+    if not args.no_extra:
+        extra_acc = measure_acceptance(eng)
+        extra_tree = measure_tree(eng, tm, d)
+
     out = {
         "metric": "spec-decode accepted tok/s (8B Q4_K, k=7, 1 GPU); verify HBM GB/s vs peak",
         "value": round(value, 3),
@@ -232,6 +332,8 @@ def main():
                      "traffic": measured_traffic(dom_name)},
         "cpu_baseline": cpu,
         "parity": parity,
+        "acceptance_kernel": extra_acc,
+        "tree_verify": extra_tree,
     }
     print(json.dumps(out), flush=True)
     for x in (tkv, dkv, tm, dm):
