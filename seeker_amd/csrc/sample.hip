@@ -17,6 +17,7 @@
 // All probability arithmetic is f64 so that the token a uniform selects does
 // not depend on summation order (GPU tree vs CPU sequential).
 #include "sh_internal.h"
+#include "sh_exp.h"
 #include "sh_philox.h"
 
 namespace {
@@ -45,21 +46,119 @@ __device__ __forceinline__ float block_max_f(float v, float* sh) {
   return t;
 }
 
-// Row statistics: max and sum of exp((l - max) / T) in f64.
-__global__ __launch_bounds__(256) void k_row_stats(const float* __restrict__ p, uint32_t n_p,
-                                                   const float* __restrict__ q, uint32_t V, double inv_t,
-                                                   double2* __restrict__ stats) {
-  __shared__ float shf[4];
-  __shared__ double shd[4];
-  const uint32_t row = blockIdx.x;
+// 2^(j/64) for sh_exp_neg; each kernel that calls it copies the table to LDS.
+__constant__ double kExp2Tab[64] = SH_EXP2_TABLE_64;
+
+__device__ __forceinline__ void load_exp_table(double* tab) {
+  if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ double wave_max_d(double v) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmax(v, __shfl_xor(v, off));
+  return v;
+}
+
+// Row statistics: max and sum of exp((l - max) / T) in f64, in two steps.
+// Step 1: the rows are cut into units of 256 E logits (unit c of row r is
+// index r * nch + c), one workgroup per unit: every thread keeps its E logits
+// in registers (one HBM read), the unit max is reduced, then the f64 exp-sum
+// against it. A unit whose logits are all -inf reports (-inf, 0). The f64 exp
+// (about 25 instructions per logit) bounds this kernel, not HBM.
+constexpr int kStatE = 32;
+
+template <bool VEC, int E>
+__device__ __forceinline__ void load_unit(const float* __restrict__ p, uint32_t n_p, const float* __restrict__ q,
+                                          uint32_t V, uint32_t nch, uint32_t u, float (&v)[E]) {
+  const uint32_t row = u / nch, base = (u - row * nch) * 256 * E, t = threadIdx.x;
   const float* x = row < n_p ? p + (size_t)row * V : q + (size_t)(row - n_p) * V;
-  float mx = -INFINITY;
-  for (uint32_t i = threadIdx.x; i < V; i += 256) mx = fmaxf(mx, x[i]);
+  if (VEC) {
+#pragma unroll
+    for (int j = 0; j < E / 4; ++j) {
+      const uint32_t i = base + j * 1024 + t * 4;
+      float4 f = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      if (i < V) f = *reinterpret_cast<const float4*>(x + i);  // V % 4 == 0: whole float4 in range
+      v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const uint32_t i = base + j * 256 + t;
+      v[j] = i < V ? x[i] : -INFINITY;
+    }
+  }
+}
+
+template <int E>
+__device__ __forceinline__ double2 reduce_unit(const float (&v)[E], double inv_t, const double* tab, float* shf,
+                                               double* shd) {
+  float mx = v[0];
+#pragma unroll
+  for (int j = 1; j < E; ++j) mx = fmaxf(mx, v[j]);
   mx = block_max_f(mx, shf);
   double s = 0.0;
-  for (uint32_t i = threadIdx.x; i < V; i += 256) s += exp(((double)x[i] - (double)mx) * inv_t);
-  s = block_sum_d(s, shd);
-  if (threadIdx.x == 0) stats[row] = make_double2((double)mx, s);
+  if (mx != -INFINITY) {
+    const double m = (double)mx;
+#pragma unroll
+    for (int j = 0; j < E; ++j) s += sh_exp_neg(((double)v[j] - m) * inv_t, tab);
+  }
+  return make_double2((double)mx, block_sum_d(s, shd));
+}
+
+template <bool VEC, int E>
+__global__ __launch_bounds__(256) void k_row_part(const float* __restrict__ p, uint32_t n_p,
+                                                  const float* __restrict__ q, uint32_t V, double inv_t,
+                                                  uint32_t nch, double2* __restrict__ part) {
+  __shared__ float shf[4];
+  __shared__ double shd[4];
+  __shared__ double tab[64];
+  load_exp_table(tab);  // visible after the barriers inside block_max_f
+  float v[E];
+  load_unit<VEC, E>(p, n_p, q, V, nch, blockIdx.x, v);
+  const double2 r = reduce_unit<E>(v, inv_t, tab, shf, shd);
+  if (threadIdx.x == 0) part[blockIdx.x] = r;
+}
+
+// Step 2 (inside the consumers): one wave combines a row's chunk partials into
+// (max M, sum of s_c exp((m_c - M) / T)); every lane gets the result.
+__device__ double2 wave_row_stat(const double2* __restrict__ part, uint32_t nch, double inv_t, const double* tab) {
+  const uint32_t l = threadIdx.x & 63;
+  double M = -INFINITY;
+  for (uint32_t c = l; c < nch; c += 64) M = fmax(M, part[c].x);
+  M = wave_max_d(M);
+  double S = 0.0;
+  if (M != -INFINITY)
+    for (uint32_t c = l; c < nch; c += 64) {
+      const double2 pc = part[c];
+      if (pc.x != -INFINITY) S += pc.y * sh_exp_neg((pc.x - M) * inv_t, tab);
+    }
+  return make_double2(M, wave_sum_d(S));
+}
+
+// The same combine done by one lane for its own row, all loads of a block of
+// 16 partials issued together (blocks after the first rescale the running sum).
+__device__ double2 lane_row_stat(const double2* __restrict__ pr, uint32_t nch, double inv_t, const double* tab) {
+  double M = -INFINITY, S = 0.0;
+  for (uint32_t c0 = 0; c0 < nch; c0 += 16) {
+    double2 pc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) pc[j] = c0 + j < nch ? pr[c0 + j] : make_double2(-INFINITY, 0.0);
+    double m = M;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m = fmax(m, pc[j].x);
+    if (m != -INFINITY) {
+      if (M != -INFINITY && M != m) S *= sh_exp_neg((M - m) * inv_t, tab);
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (pc[j].x != -INFINITY) S += pc[j].y * sh_exp_neg((pc[j].x - m) * inv_t, tab);
+    }
+    M = m;
+  }
+  return make_double2(M, S);
 }
 
 __device__ __forceinline__ float uniform_at(const float* u_dev, uint64_t seed, uint64_t word) {
@@ -70,15 +169,20 @@ __device__ __forceinline__ float uniform_at(const float* u_dev, uint64_t seed, u
 }
 
 // Weight of vocab entry v for the inverse CDF: softmax numerator of p, or
-// max(0, p - q) with normalised probabilities.
+// max(0, p - q) with normalised probabilities. raw() loads, wt() computes, so
+// callers can issue a block of loads before the arithmetic.
+// The residual uses the reciprocals of the two softmax sums (ips, iqs).
 struct RowW {
   const float* p;
   const float* q;  // null: plain p
-  double pm, ps, qm, qs, inv_t;
-  __device__ __forceinline__ double w(uint32_t v) const {
-    const double a = exp(((double)p[v] - pm) * inv_t);
+  double pm, ips, qm, iqs, inv_t;
+  const double* tab;
+  using Raw = float2;
+  __device__ __forceinline__ Raw raw(uint32_t v) const { return make_float2(p[v], q ? q[v] : 0.f); }
+  __device__ __forceinline__ double wt(Raw x) const {
+    const double a = sh_exp_neg(((double)x.x - pm) * inv_t, tab);
     if (!q) return a;
-    const double r = a / ps - exp(((double)q[v] - qm) * inv_t) / qs;
+    const double r = a * ips - sh_exp_neg(((double)x.y - qm) * inv_t, tab) * iqs;
     return r > 0.0 ? r : 0.0;
   }
 };
@@ -86,62 +190,117 @@ struct RowW {
 // Weights held explicitly (the residual of a tree node after rejections).
 struct RowR {
   const double* r;
-  __device__ __forceinline__ double w(uint32_t v) const { return r[v]; }
+  using Raw = double;
+  __device__ __forceinline__ Raw raw(uint32_t v) const { return r[v]; }
+  __device__ __forceinline__ double wt(Raw x) const { return x; }
 };
 
-// Workgroup-wide inverse CDF: first v with cumsum(w) >= target (ge = true) or
-// > target (ge = false), where target = u * total; falls back to V-1.
-// Each thread owns a contiguous chunk, so cumsum order = vocab order.
+// Sum of the weights of [b0, b1) in index order, 8 loads in flight.
 template <class W>
-__device__ uint32_t wg_inverse_cdf(const W& rw, uint32_t V, float u, bool ge, double* total_out) {
-  __shared__ double part[257];
-  __shared__ uint32_t found;
-  const uint32_t t = threadIdx.x, C = (V + 255) / 256;
-  const uint32_t b0 = min(t * C, V), b1 = min(b0 + C, V);
+__device__ __forceinline__ double slice_sum(const W& rw, uint32_t b0, uint32_t b1) {
   double s = 0.0;
-  for (uint32_t v = b0; v < b1; ++v) s += rw.w(v);
-  __syncthreads();
-  part[t] = s;
-  __syncthreads();
-  if (t == 0) {  // exclusive prefix of the chunk sums, in thread (= vocab) order
-    double acc = 0.0;
-    for (int i = 0; i < 256; ++i) {
-      const double x = part[i];
-      part[i] = acc;
-      acc += x;
-    }
-    part[256] = acc;
-    found = V - 1;
+  for (uint32_t v0 = b0; v0 < b1; v0 += 8) {
+    typename W::Raw x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (v0 + j < b1) x[j] = rw.raw(v0 + j);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (v0 + j < b1) s += rw.wt(x[j]);
   }
-  __syncthreads();
-  const double total = part[256];
-  const double target = (double)u * total;
-  const double lo = part[t];
-  const bool reach = ge ? (lo + s >= target) : (lo + s > target);
-  const bool before = t == 0 || (ge ? lo < target : lo <= target);
-  if (b0 < b1 && reach && before) {
-    double cum = lo;
-    uint32_t pick = b1 - 1;
-    for (uint32_t v = b0; v < b1; ++v) {
-      cum += rw.w(v);
-      if (ge ? cum >= target : cum > target) { pick = v; break; }
-    }
-    atomicMin(&found, pick);
+  return s;
+}
+
+// First v in [b0, b1) with cum + cumsum(w over [b0, v]) > target (>= if ge);
+// b1 - 1 if none.
+template <class W>
+__device__ __forceinline__ uint32_t slice_find(const W& rw, uint32_t b0, uint32_t b1, double cum, double target,
+                                               bool ge) {
+  for (uint32_t v0 = b0; v0 < b1; v0 += 8) {
+    typename W::Raw x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (v0 + j < b1) x[j] = rw.raw(v0 + j);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (v0 + j < b1) {
+        cum += rw.wt(x[j]);
+        if (ge ? cum >= target : cum > target) return v0 + j;
+      }
   }
+  return b1 - 1;
+}
+
+// Exclusive prefix of x over the 256 threads in thread order, by wave scans:
+// ex[t] for thread t, ex[256] = the total.
+__device__ void block_exscan_d(double x, double* ex, double* wsum) {
+  const uint32_t t = threadIdx.x, l = t & 63, w = t >> 6;
+  double inc = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const double y = __shfl_up(inc, off);
+    if (l >= (uint32_t)off) inc += y;
+  }
+  double exw = __shfl_up(inc, 1);
+  if (l == 0) exw = 0.0;
+  __syncthreads();  // earlier readers of ex / wsum are done
+  if (l == 63) wsum[w] = inc;
+  __syncthreads();
+  double base = 0.0;
+  for (uint32_t i = 0; i < w; ++i) base += wsum[i];
+  ex[t] = base + exw;
+  if (t == 255) ex[256] = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  __syncthreads();
+}
+
+// Workgroup-wide inverse CDF over [lo, hi) (256 threads, each owning a
+// contiguous slice, so the prefix order is vocab order): the first v with
+// off + cumsum(w over [lo, v]) > target (ge = false) or >= target (ge = true).
+// rel: target = u * (sum over [lo, hi)) and off = 0. Falls back to hi - 1
+// when rounding leaves the sum just short of the target. *total_out (if
+// given) receives the sum over [lo, hi).
+template <class W>
+__device__ uint32_t wg_inverse_cdf(const W& rw, uint32_t lo, uint32_t hi, bool rel, float u, double off,
+                                   double target, bool ge, double* total_out) {
+  __shared__ double ex[257];
+  __shared__ double wsum[4];
+  __shared__ uint32_t found;
+  const uint32_t t = threadIdx.x, C = (hi - lo + 255) / 256;
+  const uint32_t b0 = min(lo + t * C, hi), b1 = min(b0 + C, hi);
+  const double s = slice_sum(rw, b0, b1);
+  if (t == 0) found = hi - 1;
+  block_exscan_d(s, ex, wsum);
+  const double total = ex[256];
+  if (rel) {
+    off = 0.0;
+    target = (double)u * total;
+  }
+  const double a = off + ex[t], z = off + ex[t + 1];
+  const bool reach = ge ? z >= target : z > target;
+  const bool prior = t == 0 || (ge ? a < target : a <= target);
+  if (b0 < b1 && reach && prior) atomicMin(&found, slice_find(rw, b0, b1, a, target, ge));
   __syncthreads();
   if (total_out) *total_out = total;
   return found;
 }
 
 // COMPARE: sample every column (b, i) independently.
-__global__ __launch_bounds__(256) void k_sample_cols(const float* __restrict__ p, const double2* __restrict__ stats,
-                                                     uint32_t V, double inv_t, const float* u_dev, uint64_t seed,
-                                                     uint64_t counter, uint32_t* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_sample_cols(const float* __restrict__ p, const double2* __restrict__ part,
+                                                     uint32_t nch, uint32_t V, double inv_t, const float* u_dev,
+                                                     uint64_t seed, uint64_t counter, uint32_t* __restrict__ out) {
+  __shared__ double tab[64];
+  __shared__ double2 st;
   const uint32_t row = blockIdx.x;
-  const double2 st = stats[row];
-  RowW rw{p + (size_t)row * V, nullptr, st.x, st.y, 0.0, 1.0, inv_t};
+  load_exp_table(tab);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const double2 s = wave_row_stat(part + (size_t)row * nch, nch, inv_t, tab);
+    if (threadIdx.x == 0) st = s;
+  }
+  __syncthreads();
+  RowW rw{p + (size_t)row * V, nullptr, st.x, 1.0, 0.0, 1.0, inv_t, tab};
   const float u = uniform_at(u_dev, seed, counter + 2ull * row + 1ull);
-  const uint32_t tok = wg_inverse_cdf(rw, V, u, true, nullptr);
+  const uint32_t tok = wg_inverse_cdf(rw, 0, V, true, u, 0.0, 0.0, true, nullptr);
   if (threadIdx.x == 0) out[row] = tok;
 }
 
@@ -156,47 +315,153 @@ __global__ void k_decide_compare(const uint32_t* __restrict__ samples, const uin
   next_tok[b] = samples[b * (k + 1) + i];
 }
 
-// REJECTION: one workgroup per sequence.
+constexpr uint32_t kDrawChunks = 64;  // vocab chunks of the REJECTION draw
+
+// REJECTION, step 2: one workgroup per sequence b combines the statistics of
+// b's 2k + 1 rows (one lane per row), finds the first rejected draft i (k when
+// all are accepted; draft i is accepted iff u_acc q_i(d_i) < p_i(d_i)) and
+// records i with the statistics of p_i and q_i.
 __global__ __launch_bounds__(256) void k_decide_reject(const float* __restrict__ p, const float* __restrict__ q,
-                                                       const double2* __restrict__ stats, uint32_t B, uint32_t k,
-                                                       uint32_t V, double inv_t, const uint32_t* __restrict__ drafts,
-                                                       const float* u_dev, uint64_t seed, uint64_t counter,
-                                                       uint32_t* __restrict__ acc_len,
-                                                       uint32_t* __restrict__ next_tok) {
-  __shared__ uint32_t first_rej;
+                                                       const double2* __restrict__ part, uint32_t nch, uint32_t B,
+                                                       uint32_t k, uint32_t V, double inv_t,
+                                                       const uint32_t* __restrict__ drafts, const float* u_dev,
+                                                       uint64_t seed, uint64_t counter,
+                                                       uint32_t* __restrict__ first_rej,
+                                                       double2* __restrict__ rstat) {
+  __shared__ double tab[64];
+  __shared__ double2 st[129];  // p rows 0..k, then q rows 0..k-1 (k <= 64)
+  __shared__ uint32_t fr;
   const uint32_t b = blockIdx.x, t = threadIdx.x;
-  if (t == 0) first_rej = k;
-  __syncthreads();
-  const double2* sp = stats + (size_t)b * (k + 1);
-  const double2* sq = stats + (size_t)B * (k + 1) + (size_t)b * k;
+  load_exp_table(tab);
+  if (t == 0) fr = k;
+  // the draft token's logits for the accept test (lane t < k), loaded with the partials
+  uint32_t d = 0;
+  float pl = 0.f, ql = 0.f;
   if (t < k) {
-    const uint32_t d = drafts[b * k + t];
+    d = drafts[b * k + t];
+    if (d < V) {
+      pl = p[((size_t)b * (k + 1) + t) * V + d];
+      ql = q[((size_t)b * k + t) * V + d];
+    }
+  }
+  __syncthreads();  // table
+  if (t < 2 * k + 1) {
+    const size_t grow = t <= k ? (size_t)b * (k + 1) + t : (size_t)B * (k + 1) + (size_t)b * k + (t - k - 1);
+    st[t] = lane_row_stat(part + grow * nch, nch, inv_t, tab);
+  }
+  __syncthreads();
+  if (t < k) {
     bool accept = false;
     if (d < V) {  // an out-of-vocab draft id is rejected
-      const double pd = exp(((double)p[((size_t)b * (k + 1) + t) * V + d] - sp[t].x) * inv_t) / sp[t].y;
-      const double qd = exp(((double)q[((size_t)b * k + t) * V + d] - sq[t].x) * inv_t) / sq[t].y;
+      const double2 sp = st[t], sq = st[k + 1 + t];
+      const double pd = sh_exp_neg(((double)pl - sp.x) * inv_t, tab) / sp.y;
+      const double qd = sh_exp_neg(((double)ql - sq.x) * inv_t, tab) / sq.y;
       const float ua = uniform_at(u_dev, seed, counter + 2ull * (b * (k + 1) + t));
       accept = (double)ua * qd < pd;
     }
-    if (!accept) atomicMin(&first_rej, t);
+    if (!accept) atomicMin(&fr, t);
   }
   __syncthreads();
-  const uint32_t i = first_rej;
-  const float ur = uniform_at(u_dev, seed, counter + 2ull * (b * (k + 1) + i) + 1ull);
+  if (t == 0) {
+    const uint32_t i = fr;
+    first_rej[b] = i;
+    rstat[2 * b] = st[i];
+    rstat[2 * b + 1] = i < k ? st[k + 1 + i] : make_double2(0.0, 1.0);
+  }
+}
+
+// Step 3: grid (chunk, sequence): sums of the draw weights of row i = first_rej
+// over the chunk: .x the residual max(0, p_i - q_i) (i < k only), .y the
+// softmax numerator of p_i (the draw when all are accepted or the residual is
+// all zero).
+__global__ __launch_bounds__(256) void k_draw_chunks(const float* __restrict__ p, const float* __restrict__ q,
+                                                     uint32_t k, uint32_t V, double inv_t,
+                                                     const uint32_t* __restrict__ first_rej,
+                                                     const double2* __restrict__ rstat,
+                                                     double2* __restrict__ chunk) {
+  constexpr int kPer = 8;  // elements per thread per pass
+  __shared__ double tab[64];
+  __shared__ double shd[4];
+  const uint32_t c = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  load_exp_table(tab);
+  const uint32_t i = first_rej[b];
+  const double2 sp = rstat[2 * b], sq = rstat[2 * b + 1];
+  const bool resid = i < k;
+  const uint32_t CH = (V + kDrawChunks - 1) / kDrawChunks, lo = min(c * CH, V), hi = min(lo + CH, V);
   const float* pr = p + ((size_t)b * (k + 1) + i) * V;
-  uint32_t tok;
-  if (i == k) {
-    RowW rw{pr, nullptr, sp[i].x, sp[i].y, 0.0, 1.0, inv_t};
-    tok = wg_inverse_cdf(rw, V, ur, false, nullptr);
-  } else {
-    RowW rw{pr, q + ((size_t)b * k + i) * V, sp[i].x, sp[i].y, sq[i].x, sq[i].y, inv_t};
-    double total = 0.0;
-    tok = wg_inverse_cdf(rw, V, ur, false, &total);
-    if (!(total > 0.0)) {
-      RowW rp{pr, nullptr, sp[i].x, sp[i].y, 0.0, 1.0, inv_t};
-      tok = wg_inverse_cdf(rp, V, ur, false, nullptr);
+  const float* qr = resid ? q + ((size_t)b * k + i) * V : pr;
+  __syncthreads();  // table
+  // the same weights as the pick's scan (RowW): residual and plain numerator
+  const RowW rres{pr, qr, sp.x, 1.0 / sp.y, sq.x, 1.0 / sq.y, inv_t, tab};
+  const RowW rnum{pr, nullptr, sp.x, 1.0, 0.0, 1.0, inv_t, tab};
+  double rs = 0.0, ps = 0.0;
+  for (uint32_t v0 = lo; v0 < hi; v0 += 256 * kPer) {
+    float2 x[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const uint32_t v = v0 + j * 256 + t;
+      x[j] = make_float2(v < hi ? pr[v] : -INFINITY, v < hi && resid ? qr[v] : -INFINITY);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      ps += rnum.wt(x[j]);
+      if (resid) rs += rres.wt(x[j]);
     }
   }
+  rs = block_sum_d(rs, shd);
+  ps = block_sum_d(ps, shd);
+  if (t == 0) chunk[(size_t)b * kDrawChunks + c] = make_double2(rs, ps);
+}
+
+// Step 4: one workgroup per sequence draws the next token: wave 0 scans the
+// chunk sums (residual, else p) in vocab order for target = u * total, then
+// the inverse CDF inside the crossing chunk. Without a crossing (rounding at
+// the end) the last chunk's scan falls back to V - 1, as the sequential draw.
+__global__ __launch_bounds__(256) void k_draw_pick(const float* __restrict__ p, const float* __restrict__ q,
+                                                   uint32_t k, uint32_t V, double inv_t,
+                                                   const uint32_t* __restrict__ first_rej,
+                                                   const double2* __restrict__ rstat,
+                                                   const double2* __restrict__ chunk, const float* u_dev,
+                                                   uint64_t seed, uint64_t counter, uint32_t* __restrict__ acc_len,
+                                                   uint32_t* __restrict__ next_tok) {
+  static_assert(kDrawChunks == 64, "one lane per chunk");
+  __shared__ double tab[64];
+  __shared__ uint32_t s_c;
+  __shared__ double s_off, s_target;
+  __shared__ int s_use_r;
+  const uint32_t b = blockIdx.x, t = threadIdx.x, i = first_rej[b];
+  load_exp_table(tab);
+  const double2 sp = rstat[2 * b], sq = rstat[2 * b + 1];
+  if (t < 64) {
+    const double2 cw = chunk[(size_t)b * kDrawChunks + t];
+    const int use_r = i < k && wave_sum_d(cw.x) > 0.0;
+    const double w = use_r ? cw.x : cw.y;
+    double inc = w;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const double y = __shfl_up(inc, off);
+      if (t >= (uint32_t)off) inc += y;
+    }
+    const double total = __shfl(inc, 63);
+    const float u = uniform_at(u_dev, seed, counter + 2ull * (b * (k + 1) + i) + 1ull);
+    const double target = (double)u * total;
+    const unsigned long long over = __ballot(inc > target);
+    const uint32_t cs = over ? (uint32_t)__builtin_ctzll(over) : 63u;
+    double ex = __shfl_up(inc, 1);
+    if (t == 0) ex = 0.0;
+    ex = __shfl(ex, cs);
+    if (t == 0) {
+      s_c = cs;
+      s_off = ex;
+      s_target = target;
+      s_use_r = use_r;
+    }
+  }
+  __syncthreads();
+  const uint32_t CH = (V + kDrawChunks - 1) / kDrawChunks, lo = min(s_c * CH, V), hi = min(lo + CH, V);
+  const float* pr = p + ((size_t)b * (k + 1) + i) * V;
+  RowW rw{pr, s_use_r ? q + ((size_t)b * k + i) * V : nullptr, sp.x, 1.0 / sp.y, sq.x, 1.0 / sq.y, inv_t, tab};
+  const uint32_t tok = wg_inverse_cdf(rw, lo, hi, false, 0.f, s_off, s_target, false, nullptr);
   if (t == 0) {
     acc_len[b] = i;
     next_tok[b] = tok;
@@ -232,7 +497,9 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
   __shared__ unsigned long long shk[4];
   __shared__ int s_acc;
   __shared__ uint32_t s_path[64];
+  __shared__ double tab[64];
   const uint32_t b = blockIdx.x, t = threadIdx.x;
+  load_exp_table(tab);  // the first use follows the barriers of block_max_f
   const float* P = p + (size_t)b * n * V;
   const float* Q = q ? q + (size_t)b * n * V : nullptr;
   const uint32_t* tok = tokens + (size_t)b * n;
@@ -266,7 +533,7 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
       for (uint32_t i = t; i < V; i += 256) mx = fmaxf(mx, pv[i]);
       const double pm = block_max_f(mx, shf);
       double ssum = 0.0;
-      for (uint32_t i = t; i < V; i += 256) ssum += exp(((double)pv[i] - pm) * inv_t);
+      for (uint32_t i = t; i < V; i += 256) ssum += sh_exp_neg(((double)pv[i] - pm) * inv_t, tab);
       const double ps = block_sum_d(ssum, shd);
       const float* qv = Q + (size_t)v * V;
       double qm = 0.0, qs = 1.0, Z = 1.0;
@@ -278,7 +545,7 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
           for (uint32_t i = t; i < V; i += 256) qx = fmaxf(qx, qv[i]);
           qm = block_max_f(qx, shf);
           double qsum = 0.0;
-          for (uint32_t i = t; i < V; i += 256) qsum += exp(((double)qv[i] - qm) * inv_t);
+          for (uint32_t i = t; i < V; i += 256) qsum += sh_exp_neg(((double)qv[i] - qm) * inv_t, tab);
           qs = block_sum_d(qsum, shd);
           have_q = true;
         }
@@ -286,8 +553,8 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
           const uint32_t tc = tok[c];
           bool ok = false;
           if (tc < V) {
-            const double pc = resid ? r[tc] / Z : exp(((double)pv[tc] - pm) * inv_t) / ps;
-            const double qc = exp(((double)qv[tc] - qm) * inv_t) / qs;
+            const double pc = resid ? r[tc] / Z : sh_exp_neg(((double)pv[tc] - pm) * inv_t, tab) / ps;
+            const double qc = sh_exp_neg(((double)qv[tc] - qm) * inv_t, tab) / qs;
             ok = (double)uniform_at(u_dev, seed, counter + 2ull * ((uint64_t)b * n + c)) * qc < pc;
           }
           s_acc = ok ? 1 : 0;
@@ -298,15 +565,15 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
         // after the sum over the old values is complete)
         double part = 0.0;
         for (uint32_t i = t; i < V; i += 256) {
-          const double cur = resid ? r[i] / Z : exp(((double)pv[i] - pm) * inv_t) / ps;
-          const double d = cur - exp(((double)qv[i] - qm) * inv_t) / qs;
+          const double cur = resid ? r[i] / Z : sh_exp_neg(((double)pv[i] - pm) * inv_t, tab) / ps;
+          const double d = cur - sh_exp_neg(((double)qv[i] - qm) * inv_t, tab) / qs;
           part += d > 0.0 ? d : 0.0;
         }
         const double R = block_sum_d(part, shd);
         if (R > 0.0) {
           for (uint32_t i = t; i < V; i += 256) {
-            const double cur = resid ? r[i] / Z : exp(((double)pv[i] - pm) * inv_t) / ps;
-            const double d = cur - exp(((double)qv[i] - qm) * inv_t) / qs;
+            const double cur = resid ? r[i] / Z : sh_exp_neg(((double)pv[i] - pm) * inv_t, tab) / ps;
+            const double d = cur - sh_exp_neg(((double)qv[i] - qm) * inv_t, tab) / qs;
             r[i] = d > 0.0 ? d : 0.0;
           }
           __syncthreads();
@@ -319,10 +586,10 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
         if (resid) {
           __threadfence_block();
           RowR rr{r};
-          out_tok = wg_inverse_cdf(rr, V, ud, false, nullptr);
+          out_tok = wg_inverse_cdf(rr, 0, V, true, ud, 0.0, 0.0, false, nullptr);
         } else {
-          RowW rw{pv, nullptr, pm, ps, 0.0, 1.0, inv_t};
-          out_tok = wg_inverse_cdf(rw, V, ud, false, nullptr);
+          RowW rw{pv, nullptr, pm, 1.0, 0.0, 1.0, inv_t, tab};
+          out_tok = wg_inverse_cdf(rw, 0, V, true, ud, 0.0, 0.0, false, nullptr);
         }
         break;
       }
@@ -351,30 +618,45 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   SH_CHECK(mode != SH_SAMPLE_REJECTION || q_logits, SH_ERR_ARG, "REJECTION needs draft logits");
   const double inv_t = 1.0 / (double)s->temperature;
   const uint32_t n_p = B * (k + 1), n_q = mode == SH_SAMPLE_REJECTION ? B * k : 0;
-  double2* stats = nullptr;
-  SH_HIP(hipMallocAsync((void**)&stats, (size_t)(n_p + n_q) * sizeof(double2), e->stream));
+  const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE), nrows = n_p + n_q;
+  // one scratch block: unit partials, then per-sequence draw state
+  const uint32_t nunits = nrows * nch;
+  const size_t part_b = (size_t)nunits * sizeof(double2);
+  const size_t chunk_b = (size_t)B * kDrawChunks * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
+  const size_t small_b = mode == SH_SAMPLE_COMPARE ? (size_t)n_p * 4 : (size_t)B * 4;
+  char* scratch = nullptr;
+  SH_HIP(hipMallocAsync((void**)&scratch, part_b + chunk_b + rstat_b + small_b, e->stream));
+  double2* part = reinterpret_cast<double2*>(scratch);
+  double2* chunk = reinterpret_cast<double2*>(scratch + part_b);
+  double2* rstat = reinterpret_cast<double2*>(scratch + part_b + chunk_b);
+  uint32_t* small = reinterpret_cast<uint32_t*>(scratch + part_b + chunk_b + rstat_b);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL(k_row_stats, dim3(n_p + n_q), dim3(256), 0, e->stream, p_logits, n_p, q_logits, V, inv_t, stats);
+  if (V % 4 == 0)
+    hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nunits), dim3(256), 0, e->stream, p_logits, n_p, q_logits,
+                       V, inv_t, nch, part);
+  else
+    hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nunits), dim3(256), 0, e->stream, p_logits, n_p, q_logits,
+                       V, inv_t, nch, part);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_stats", 4.0 * V * (n_p + n_q), ev);
   sh_prof_begin(e, &ev);
   if (mode == SH_SAMPLE_COMPARE) {
-    uint32_t* samples = nullptr;
-    SH_HIP(hipMallocAsync((void**)&samples, (size_t)n_p * 4, e->stream));
-    hipLaunchKernelGGL(k_sample_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, stats, V, inv_t, uniforms_dev,
-                       s->seed, counter, samples);
-    hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, samples, drafts, B, k, acc_len,
+    hipLaunchKernelGGL(k_sample_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, part, nch, V, inv_t,
+                       uniforms_dev, s->seed, counter, small);
+    hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
                        next_tok);
-    SH_HIP(hipGetLastError());
-    SH_HIP(hipFreeAsync(samples, e->stream));
   } else {
-    hipLaunchKernelGGL(k_decide_reject, dim3(B), dim3(256), 0, e->stream, p_logits, q_logits, stats, B, k, V, inv_t,
-                       drafts, uniforms_dev, s->seed, counter, acc_len, next_tok);
-    SH_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_decide_reject, dim3(B), dim3(256), 0, e->stream, p_logits, q_logits, part, nch, B, k, V,
+                       inv_t, drafts, uniforms_dev, s->seed, counter, small, rstat);
+    hipLaunchKernelGGL(k_draw_chunks, dim3(kDrawChunks, B), dim3(256), 0, e->stream, p_logits, q_logits, k, V, inv_t,
+                       small, rstat, chunk);
+    hipLaunchKernelGGL(k_draw_pick, dim3(B), dim3(256), 0, e->stream, p_logits, q_logits, k, V, inv_t, small, rstat,
+                       chunk, uniforms_dev, s->seed, counter, acc_len, next_tok);
   }
+  SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_decide", 0.0, ev);
-  SH_HIP(hipFreeAsync(stats, e->stream));
+  SH_HIP(hipFreeAsync(scratch, e->stream));
   return SH_OK;
 }
 
