@@ -113,7 +113,7 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) vop[h][dt] = ld_h8(vp + (size_t)dt * 16 * 32);
   }
-  const uint64_t cm = col_mask(fa, col);
+  const uint64_t cm = fa.masks ? fa.masks[col] : col_mask(fa, col);
   __builtin_amdgcn_sched_barrier(0);
 
   // Q^T operand (B). Each query row is scaled by a power of two (max|q * s| in
@@ -359,8 +359,8 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   const size_t layer_k = (size_t)m->n_kv * kv->max_seq * m->hd;
   const uint16_t* kc = kv->k + layer_k * fa.layer;
   const uint16_t* vc = kv->v + layer_k * fa.layer;
-  SH_CHECK(fa.col0 + fa.N <= 8, SH_ERR_ARG, "attention columns [%u, %u) outside the chunk", fa.col0,
-           fa.col0 + fa.N);
+  SH_CHECK(fa.N >= 1 && (fa.N <= 8 || fa.masks) && fa.col0 + fa.N <= SH_MAX_COLS, SH_ERR_ARG,
+           "attention columns [%u, %u) outside the chunk (more than 8 need device masks)", fa.col0, fa.col0 + fa.N);
   const float scale = 1.0f / sqrtf((float)m->hd);
   q += (size_t)fa.col0 * m->n_head * m->hd;
   hipEvent_t ev = nullptr;

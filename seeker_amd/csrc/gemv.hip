@@ -133,6 +133,39 @@ __global__ void k_repack_q8(const uint8_t* __restrict__ src, uint8_t* __restrict
 
 __device__ __forceinline__ uint16_t f2h_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
 
+// Rows r0..r0+3 of one column's fused QKV output: q rows are roped into
+// qcol, k rows roped and v rows stored as f16 in the column's cache slot
+// (V slot-permuted within its 32-key block).
+__device__ __forceinline__ void qkv_store4(const EpiArgs& ea, uint32_t r0, const float v[4], int32_t pos,
+                                           uint32_t slot, uint32_t ms, uint16_t* kc, uint16_t* vc, float* qcol) {
+  if (r0 < ea.Dq) {
+    const uint32_t i0 = r0 % ea.hd;
+    const float2 cs0 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2];
+    const float2 cs1 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2 + 1];
+    float* q = qcol + r0;
+    q[0] = v[0] * cs0.x - v[1] * cs0.y;
+    q[1] = v[0] * cs0.y + v[1] * cs0.x;
+    q[2] = v[2] * cs1.x - v[3] * cs1.y;
+    q[3] = v[2] * cs1.y + v[3] * cs1.x;
+  } else if (r0 < ea.Dq + ea.Dkv) {
+    const uint32_t rr = r0 - ea.Dq, kh = rr / ea.hd, i0 = rr % ea.hd;
+    const float2 cs0 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2];
+    const float2 cs1 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2 + 1];
+    float o[4];
+    o[0] = v[0] * cs0.x - v[1] * cs0.y;
+    o[1] = v[0] * cs0.y + v[1] * cs0.x;
+    o[2] = v[2] * cs1.x - v[3] * cs1.y;
+    o[3] = v[2] * cs1.y + v[3] * cs1.x;
+    uint16_t* k = kc + (((size_t)ea.layer * ea.n_kv + kh) * ms + slot) * ea.hd + i0;
+    for (int j = 0; j < 4; ++j) k[j] = f2h_bits(o[j]);
+  } else {
+    const uint32_t rr = r0 - ea.Dq - ea.Dkv, kh = rr / ea.hd, i0 = rr % ea.hd;
+    uint16_t* vb = vc + (((size_t)ea.layer * ea.n_kv + kh) * (ms / 32) + slot / 32) * ea.hd * 32;
+    const uint32_t sl = v_slot(slot & 31);
+    for (int j = 0; j < 4; ++j) vb[(size_t)(i0 + j) * 32 + sl] = f2h_bits(v[j]);
+  }
+}
+
 // Final (row, col) value for rows r0..r0+3 (one lane), col < N; ks = split.
 template <int EPI>
 __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32_t col, const float v[4],
@@ -149,34 +182,8 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32
       *p = *p + v[j];
     }
   } else if (EPI == EPI_QKV) {
-    const int32_t pos = ea.colpos[col & 7];
-    const uint32_t slot = ea.slot[col & 7], ms = ea.mseq[col & 7];
-    if (r0 < ea.Dq) {
-      const uint32_t i0 = r0 % ea.hd;
-      const float2 cs0 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2];
-      const float2 cs1 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2 + 1];
-      float* q = ea.out + (size_t)col * ea.Dq + r0;
-      q[0] = v[0] * cs0.x - v[1] * cs0.y;
-      q[1] = v[0] * cs0.y + v[1] * cs0.x;
-      q[2] = v[2] * cs1.x - v[3] * cs1.y;
-      q[3] = v[2] * cs1.y + v[3] * cs1.x;
-    } else if (r0 < ea.Dq + ea.Dkv) {
-      const uint32_t rr = r0 - ea.Dq, kh = rr / ea.hd, i0 = rr % ea.hd;
-      const float2 cs0 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2];
-      const float2 cs1 = ea.rope[(size_t)pos * (ea.hd / 2) + i0 / 2 + 1];
-      float o[4];
-      o[0] = v[0] * cs0.x - v[1] * cs0.y;
-      o[1] = v[0] * cs0.y + v[1] * cs0.x;
-      o[2] = v[2] * cs1.x - v[3] * cs1.y;
-      o[3] = v[2] * cs1.y + v[3] * cs1.x;
-      uint16_t* k = ea.kc[col & 7] + (((size_t)ea.layer * ea.n_kv + kh) * ms + slot) * ea.hd + i0;
-      for (int j = 0; j < 4; ++j) k[j] = f2h_bits(o[j]);
-    } else {
-      const uint32_t rr = r0 - ea.Dq - ea.Dkv, kh = rr / ea.hd, i0 = rr % ea.hd;
-      uint16_t* vb = ea.vc[col & 7] + (((size_t)ea.layer * ea.n_kv + kh) * (ms / 32) + slot / 32) * ea.hd * 32;
-      const uint32_t sl = v_slot(slot & 31);
-      for (int j = 0; j < 4; ++j) vb[(size_t)(i0 + j) * 32 + sl] = f2h_bits(v[j]);
-    }
+    qkv_store4(ea, r0, v, ea.colpos[col & 7], ea.slot[col & 7], ea.mseq[col & 7], ea.kc[col & 7], ea.vc[col & 7],
+               ea.out + (size_t)col * ea.Dq);
   }
 }
 
@@ -479,6 +486,219 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
     }
     __syncthreads();
   }
+}
+
+// ------------------------------------------------------------------ Q4_K multi-group
+
+// Decoded state of one weight tile for one superblock: the eight sub-block
+// words, the unpacked 6-bit scales and minimums, and d, dmin of the lane's rows.
+struct Q4Dec {
+  uint32_t w[8];
+  uint32_t sc03, sc47, m03, m47;
+  float d[4], dmin[4];
+};
+
+__device__ __forceinline__ Q4Dec q4_decode_setup(const Q4Tile& a) {
+  Q4Dec s;
+  s.w[0] = a.q0.x; s.w[1] = a.q0.y; s.w[2] = a.q0.z; s.w[3] = a.q0.w;
+  s.w[4] = a.q1.x; s.w[5] = a.q1.y; s.w[6] = a.q1.z; s.w[7] = a.q1.w;
+  s.sc03 = a.s0 & 0x3F3F3F3Fu;
+  s.m03 = a.s1 & 0x3F3F3F3Fu;
+  s.sc47 = (a.s2 & 0x0F0F0F0Fu) | ((a.s0 >> 2) & 0x30303030u);
+  s.m47 = ((a.s2 >> 4) & 0x0F0F0F0Fu) | ((a.s1 >> 2) & 0x30303030u);
+  const uint32_t ddw[4] = {a.dd.x, a.dd.y, a.dd.z, a.dd.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    s.d[j] = (float)as_h2(ddw[j]).x;
+    s.dmin[j] = (float)as_h2(ddw[j]).y;
+  }
+  return s;
+}
+
+// A operand of sub-block m: exact f16 c * sc_m * q (as in q4_tile_mma).
+__device__ __forceinline__ h8 q4_frag(const Q4Dec& s, int m, uint32_t magic) {
+  const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  const h2 mult = magic_pair(m < 4 ? s.sc03 : s.sc47, magic, m & 3, m & 3) + k1024;
+  return q4_operand2(s.w[m], magic, mult, mult * k1024);
+}
+
+// A operand of the minimum term: m_s at k = s (every lane group).
+__device__ __forceinline__ h8 q4_min_frag(const Q4Dec& s, uint32_t magic) {
+  const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  u32x4 am;
+  am.x = as_u32(magic_pair(s.m03, magic, 0, 1) + k1024);
+  am.y = as_u32(magic_pair(s.m03, magic, 2, 3) + k1024);
+  am.z = as_u32(magic_pair(s.m47, magic, 0, 1) + k1024);
+  am.w = as_u32(magic_pair(s.m47, magic, 2, 3) + k1024);
+  return as_h8(am);
+}
+
+// Norm factor of column c of operand group g (sums of squares of group g
+// start at g * ssq_n * 8).
+__device__ __forceinline__ float col_rinv_g(const EpiArgs& ea, uint32_t g, uint32_t c) {
+  if (!ea.ssq) return 1.0f;
+  const float* sq = ea.ssq + (size_t)g * ea.ssq_n * 8;
+  float ss = 0.f;
+  for (uint32_t i0 = 0; i0 < ea.ssq_n; i0 += 8) {
+    float t[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) t[j] = sq[min(i0 + j, ea.ssq_n - 1) * 8 + c];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) ss += i0 + j < ea.ssq_n ? t[j] : 0.0f;
+  }
+  return 1.0f / sqrtf(ss / (float)ea.norm_K + ea.eps);
+}
+
+// y = W x for G operand groups (up to 64 columns) in one pass over W. A
+// workgroup of 8 waves covers 8 T row tiles (wave w: tiles (blockIdx.x * 8 +
+// w) * T + t) over the superblocks [S blockIdx.y, S blockIdx.y + S) of split
+// blockIdx.y. Per superblock the G groups' operands (B and XS, 9 KB each, and
+// 8 scales) are copied to LDS by direct global->LDS loads, two buffers
+// alternating so superblock i + 1 (operands and weights) loads while i
+// computes; every decoded weight fragment then feeds G MFMAs. The per-
+// superblock sums go through d, dmin and the column scale in f32 as in the
+// 8-column kernels. EPI_PART writes split partials [split][col][row];
+// EPI_STORE (one split) whole rows.
+constexpr uint32_t MG_MAX_G = 8;
+
+template <int T, int G, int EPI>
+__global__ __launch_bounds__(512) void k_gemm_q4(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                  uint32_t S, const uint16_t* __restrict__ Bx,
+                                                  const uint16_t* __restrict__ XS, const float* __restrict__ CS,
+                                                  uint32_t N, EpiArgs ea) {
+  __shared__ h8 sB[2][G * 9 * 64];  // [buffer][group * 9 + fragment][lane]
+  __shared__ float sC[2][64];       // [buffer][group * 8 + column]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4, r = lane & 15;
+  const uint32_t ks = blockIdx.y, sb0 = ks * S, sb1 = min(sb0 + S, nsb);
+  const uint32_t tile0 = (blockIdx.x * 8 + wave) * T;
+  const size_t gB = (size_t)nsb * 8 * 512, gX = (size_t)nsb * 512, gC = (size_t)nsb * 8;
+  const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
+  float nf[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) nf[g] = col_rinv_g(ea, g, r & 7);
+
+  auto stage = [&](uint32_t sb, int buf) {
+    // fragment f of group g: 1 KB, one wave instruction
+    for (uint32_t fi = wave; fi < (uint32_t)(G * 9); fi += 8) {
+      const uint32_t g = fi / 9, f = fi % 9;
+      const uint16_t* src = f < 8 ? Bx + g * gB + ((size_t)(sb * 8 + f) * 64 + lane) * 8
+                                  : XS + g * gX + ((size_t)sb * 64 + lane) * 8;
+      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&sB[buf][fi * 64]), 16, 0, 0);
+    }
+    if (wave == 7) {  // the G * 8 scales (lanes past them repeat the last)
+      const uint32_t li = (uint32_t)lane < (uint32_t)(G * 8) ? (uint32_t)lane : G * 8 - 1;
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(CS + (li / 8) * gC + sb * 8 + li % 8), (lds_void_t*)sC[buf],
+                                       4, 0, 0);
+    }
+  };
+  auto a_ptr = [&](int t, uint32_t sb) {
+    const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
+    return Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
+  };
+
+  f4 y[T][G];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int g = 0; g < G; ++g) y[t][g] = f4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const Q4Tile (&at)[T], int buf) {
+    Q4Dec dec[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) dec[t] = q4_decode_setup(at[t]);
+    f4 acc[T][G];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[t][g] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      h8 a[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) a[t] = q4_frag(dec[t], m, magic);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const h8 b = sB[buf][(g * 9 + m) * 64 + lane];
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t][g] = mfma16(a[t], b, acc[t][g]);
+      }
+    }
+    h8 am[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) am[t] = q4_min_frag(dec[t], magic);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const h8 bm = sB[buf][(g * 9 + 8) * 64 + lane];
+      const float c = sC[buf][g * 8 + (lane & 7)];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const f4 macc = mfma16(am[t], bm, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          y[t][g][j] = y[t][g][j] + c * (dec[t].d[j] * acc[t][g][j] - dec[t].dmin[j] * macc[j]);
+      }
+    }
+  };
+
+  // Superblocks go in pairs so each weight buffer's index is a constant.
+  Q4Tile wa[T], wb[T];
+  stage(sb0, 0);
+#pragma unroll
+  for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, sb0), lane, g4, r);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (uint32_t sb = sb0; sb < sb1; sb += 2) {
+    if (sb + 1 < sb1) {
+      stage(sb + 1, 1);
+#pragma unroll
+      for (int t = 0; t < T; ++t) wb[t] = load_q4_tile(a_ptr(t, sb + 1), lane, g4, r);
+    }
+    compute(wa, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (sb + 1 >= sb1) break;
+    if (sb + 2 < sb1) {
+      stage(sb + 2, 0);
+#pragma unroll
+      for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, sb + 2), lane, g4, r);
+    }
+    compute(wb, 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float o[4];
+      col_sum4(y[t][g], nf[g], o);
+      const uint32_t tile = tile0 + t, col = g * 8 + r;
+      if (tile < tiles && r < 8 && col < N) epilogue4<EPI>(ea, tile * 16 + 4 * g4, col, o, ks);
+    }
+}
+
+// QKV from the multi-group kernel's split partials: per column (blockIdx.y) and
+// 4 rows per thread, the split sum, then RoPE and the KV-cache writes.
+__global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ part, uint32_t nparts,
+                                                   size_t part_stride, uint32_t ldp, EpiArgs ea, QkvCols qc) {
+  const uint32_t col = blockIdx.y, r0 = 4 * (blockIdx.x * 64 + threadIdx.x);
+  if (r0 >= ea.Dq + 2 * ea.Dkv) return;
+  const float* p = part + (size_t)col * ldp + r0;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t k0 = 0; k0 < nparts; k0 += 8) {  // 8 loads in flight, split order kept
+    float4 t[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) t[j] = *(const float4*)(p + min(k0 + j, nparts - 1) * part_stride);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      if (k0 + j < nparts) { s.x += t[j].x; s.y += t[j].y; s.z += t[j].z; s.w += t[j].w; }
+  }
+  const float v[4] = {s.x, s.y, s.z, s.w};
+  qkv_store4(ea, r0, v, qc.pos[col], qc.slot[col], qc.mseq[col], qc.kc[col], qc.vc[col],
+             ea.out + (size_t)col * ea.Dq);
 }
 
 // ------------------------------------------------------------------ Q8_0
@@ -812,5 +1032,93 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
   SH_HIP(hipGetLastError());
   sh_prof_end(e, tag, w.alg_bytes, ev);
   if (nparts) *nparts = np;
+  return SH_OK;
+}
+
+// ------------------------------------------------------------------ multi-group dispatch
+
+// Multi-group shape: T = 2 tiles per wave up to 4 groups (registers), else 1.
+// The splits depend on the matrix only, never on the column count, so a
+// column's arithmetic (superblock order within a split, split order in the
+// sum) is the same in every multi-group launch: the fewest splits (at most 16)
+// whose workgroup count at T = 2 fills the 256 CUs to at least 70 % in its last
+// round (one workgroup per CU: up to 148 KB of LDS).
+struct MgPlan {
+  uint32_t T = 1, S = 1, KS = 1;
+};
+static MgPlan mg_plan(const QMat& w, uint32_t G, bool one_split) {
+  MgPlan p;
+  p.T = G <= 4 ? 2 : 1;
+  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 15) / 16, slots = 256;
+  uint32_t best_ks = 1;
+  double best = -1.0;
+  for (uint32_t ks = 1; !one_split && ks <= 16 && ks <= nsb; ++ks) {
+    const uint32_t S = (nsb + ks - 1) / ks, k2 = (nsb + S - 1) / S, wgs = wgx * k2;
+    const double eff = (double)wgs / (double)(slots * ((wgs + slots - 1) / slots));
+    if (eff > best + 1e-9) { best = eff; best_ks = k2; }
+    if (eff >= 0.7) break;
+  }
+  p.S = (nsb + best_ks - 1) / best_ks;
+  p.KS = (nsb + p.S - 1) / p.S;
+  return p;
+}
+
+size_t sh_gemm_part_floats(const QMat& w) {
+  if (w.type != GGML_Q4_K) return 0;
+  return (size_t)mg_plan(w, MG_MAX_G, false).KS * SH_MAX_COLS * w.tiles * 16;
+}
+
+template <int T, int G, int EPI>
+static void launch_mg(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs,
+                      uint32_t N, const EpiArgs& ea, const MgPlan& p) {
+  const dim3 grid((w.tiles + 8 * T - 1) / (8 * T), p.KS);
+  hipLaunchKernelGGL((k_gemm_q4<T, G, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bx, xs, cs,
+                     N, ea);
+}
+template <int EPI>
+static void dispatch_mg(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs,
+                        uint32_t N, const EpiArgs& ea, const MgPlan& p) {
+  switch ((N + 7) / 8) {
+    case 1: launch_mg<2, 1, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 2: launch_mg<2, 2, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 3: launch_mg<2, 3, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 4: launch_mg<2, 4, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 5: launch_mg<1, 5, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 6: launch_mg<1, 6, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 7: launch_mg<1, 7, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    default: launch_mg<1, 8, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+  }
+}
+
+int sh_gemm_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs, uint32_t N,
+                   EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts) {
+  SH_CHECK(N >= 1 && N <= SH_MAX_COLS, SH_ERR_ARG, "gemm N=%u outside [1, %u]", N, SH_MAX_COLS);
+  SH_CHECK(w.type == GGML_Q4_K && w.K % 256 == 0, SH_ERR_UNSUPPORTED, "multi-group gemm needs Q4_K (type %d)",
+           w.type);
+  SH_CHECK(epi == EPI_PART || epi == EPI_STORE, SH_ERR_ARG, "multi-group gemm epilogue %d", (int)epi);
+  const MgPlan p = mg_plan(w, (N + 7) / 8, epi == EPI_STORE);
+  if (epi == EPI_PART)
+    SH_CHECK(ea.part_cap >= p.KS && ea.part_stride >= (size_t)((N + 7) / 8 * 8) * ea.ldo, SH_ERR_CAPACITY,
+             "gemm: %u split partials exceed the buffer (%u)", p.KS, ea.part_cap);
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  if (epi == EPI_PART) dispatch_mg<EPI_PART>(e, w, bx, xs, cs, N, ea, p);
+  else dispatch_mg<EPI_STORE>(e, w, bx, xs, cs, N, ea, p);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, tag, w.alg_bytes, ev);
+  if (nparts) *nparts = p.KS;
+  return SH_OK;
+}
+
+int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
+                         uint32_t N, const EpiArgs& ea, const QkvCols& qc) {
+  SH_CHECK(N >= 1 && N <= SH_MAX_COLS && ea.hd % 4 == 0, SH_ERR_ARG, "qkv finish shape");
+  const uint32_t rows = ea.Dq + 2 * ea.Dkv;
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  hipLaunchKernelGGL(k_qkv_finish, dim3((rows / 4 + 63) / 64, N), dim3(64), 0, e->stream, part, nparts, part_stride,
+                     ldp, ea, qc);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, "qkv_finish", 0.0, ev);
   return SH_OK;
 }

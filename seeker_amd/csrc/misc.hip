@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
   const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
   const uint32_t k = 256 * sb + 4 * lane;
   const bool valid = k < a.K;
-  const size_t pstride = (size_t)8 * a.part_ld;
+  const size_t pstride = (size_t)a.part_cols * a.part_ld;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (valid) {
     if (MODE == PREP_SWIGLU) {
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
   }
   if (a.norm_w) {
     const float ss = sh_wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
-    if (lane == 0) a.ssq[sb * 8 + col] = ss;
+    if (lane == 0) a.ssq[(col / 8) * sh_grp_cs(a.K) + sb * 8 + col % 8] = ss;
     if (valid) {
       const float4 wv = *(const float4*)(a.norm_w + k);
       v.x *= wv.x; v.y *= wv.y; v.z *= wv.z; v.w *= wv.w;
@@ -117,7 +117,8 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
 
 int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
   SH_CHECK(a.K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", a.K);
-  SH_CHECK(a.N >= 1 && a.N <= 8, SH_ERR_ARG, "prep N=%u outside [1, 8]", a.N);
+  SH_CHECK(a.N >= 1 && a.N <= SH_MAX_COLS, SH_ERR_ARG, "prep N=%u outside [1, %u]", a.N, SH_MAX_COLS);
+  SH_CHECK(a.part_cols >= a.N || a.nparts == 0, SH_ERR_ARG, "prep: partials hold %u columns, N=%u", a.part_cols, a.N);
   SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");
   SH_CHECK(a.mode != PREP_RESID || a.nparts == 0 || a.part, SH_ERR_ARG, "prep partials missing");
   SH_CHECK(!a.norm_w || a.ssq, SH_ERR_ARG, "prep: norm needs a sum-of-squares buffer");
@@ -133,20 +134,21 @@ int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
 }
 
 // y[col][m] (+)= sum_s part[s][col][m] for m < M (split partials, in split order).
-__global__ void k_part_reduce(const float* __restrict__ part, uint32_t nparts, uint32_t part_ld, uint32_t M,
-                              float* __restrict__ y, uint32_t ldy, int accumulate) {
+// The partials hold part_cols columns per split.
+__global__ void k_part_reduce(const float* __restrict__ part, uint32_t nparts, uint32_t part_ld, uint32_t part_cols,
+                              uint32_t M, float* __restrict__ y, uint32_t ldy, int accumulate) {
   const uint32_t col = blockIdx.y, m = blockIdx.x * blockDim.x + threadIdx.x;
   if (m >= M) return;
   float s = accumulate ? y[(size_t)col * ldy + m] : 0.f;
-  for (uint32_t k = 0; k < nparts; ++k) s += part[((size_t)k * 8 + col) * part_ld + m];
+  for (uint32_t k = 0; k < nparts; ++k) s += part[((size_t)k * part_cols + col) * part_ld + m];
   y[(size_t)col * ldy + m] = s;
 }
 
-int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint32_t part_ld, uint32_t M, uint32_t N,
-                          float* y, uint32_t ldy, bool accumulate) {
-  SH_CHECK(N >= 1 && N <= 8 && M <= part_ld, SH_ERR_ARG, "partial reduce shape");
-  hipLaunchKernelGGL(k_part_reduce, dim3((M + 255) / 256, N), dim3(256), 0, e->stream, part, nparts, part_ld, M, y,
-                     ldy, accumulate ? 1 : 0);
+int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint32_t part_ld, uint32_t part_cols,
+                          uint32_t M, uint32_t N, float* y, uint32_t ldy, bool accumulate) {
+  SH_CHECK(N >= 1 && N <= part_cols && M <= part_ld, SH_ERR_ARG, "partial reduce shape");
+  hipLaunchKernelGGL(k_part_reduce, dim3((M + 255) / 256, N), dim3(256), 0, e->stream, part, nparts, part_ld,
+                     part_cols, M, y, ldy, accumulate ? 1 : 0);
   SH_HIP(hipGetLastError());
   return SH_OK;
 }

@@ -12,6 +12,7 @@
 #include <cstring>
 
 #include "sh_internal.h"
+#include "sh_operand.h"
 
 // ------------------------------------------------------------------ errors
 
@@ -456,23 +457,31 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
     m->alg_weight_bytes += L.wqkv.alg_bytes + L.wo.alg_bytes + L.wgu.alg_bytes + L.wdown.alg_bytes + 8.0 * m->d;
   }
   m->alg_weight_bytes += 4.0 * m->d;
-  // workspace for up to 8 columns per chunk
+  {
+    auto q4 = [](const QMat& q) { return q.type == GGML_Q4_K && q.K % 256 == 0; };
+    bool ok = q4(m->lm_head);
+    for (const Layer& L : m->layers) ok = ok && q4(L.wqkv) && q4(L.wo) && q4(L.wgu) && q4(L.wdown);
+    m->mg_ok = ok;
+  }
+  // workspace for up to SH_MAX_COLS columns per chunk (operands: 8 groups of 8)
   Workspace& w = m->ws;
-  w.max_cols = 8;
-  const uint32_t kmax = std::max(m->d, m->ff);
-  const size_t bx_elems = (size_t)kmax / 32 * 64 * 8;
-  const size_t xs_elems = (size_t)(kmax + 255) / 256 * 64 * 8;
+  w.max_cols = SH_MAX_COLS;
+  const uint32_t kmax = std::max(m->d, m->ff), ngrp = SH_MAX_COLS / 8;
+  const size_t bx_elems = ngrp * sh_grp_bx(kmax);
+  const size_t xs_elems = ngrp * sh_grp_xs(kmax);
   const size_t part_floats =  // grown on demand in forward_dev
       (size_t)m->n_kv * (4096 / SH_FA_MIN_SPLIT_KEYS) * SH_FA_MAX_ROWS * sh_fa_part_stride(m->hd);
   size_t gpart_floats = 0;
   for (const Layer& L : m->layers)
     gpart_floats = std::max({gpart_floats, sh_gemv_part_floats(L.wo), sh_gemv_part_floats(L.wgu),
-                             sh_gemv_part_floats(L.wdown)});
-  if (dalloc(&w.resid, (size_t)8 * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
-      dalloc(&w.q, (size_t)8 * m->d) || dalloc(&w.attn, (size_t)8 * m->d) || dalloc(&w.gpart, gpart_floats) || dalloc(&w.h, (size_t)8 * m->ff) ||
-      dalloc(&w.logits, (size_t)8 * m->V) || dalloc(&w.fa_part, part_floats) || dalloc(&w.tokens, 128) ||
-      dalloc(&w.amax, 64) || dalloc(&w.cs, (size_t)(kmax + 255) / 256 * 8) ||
-      dalloc(&w.ssq, (size_t)(kmax + 255) / 256 * 8))
+                             sh_gemv_part_floats(L.wdown), sh_gemm_part_floats(L.wqkv), sh_gemm_part_floats(L.wo),
+                             sh_gemm_part_floats(L.wgu), sh_gemm_part_floats(L.wdown)});
+  const size_t C = SH_MAX_COLS;
+  if (dalloc(&w.resid, C * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
+      dalloc(&w.q, C * m->d) || dalloc(&w.attn, C * m->d) || dalloc(&w.gpart, gpart_floats) ||
+      dalloc(&w.h, C * m->ff) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
+      dalloc(&w.tokens, C + 64) || dalloc(&w.amax, C) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
+      dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
   w.gpart_floats = gpart_floats;
@@ -649,6 +658,7 @@ struct FaSeg {
   sh_kv* kv = nullptr;
   uint32_t col0 = 0, ncol = 0, kvlen = 0, mask_base = 0;
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const uint64_t* masks = nullptr;  // device masks of the ncol columns (required above 8 columns)
 };
 
 static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
@@ -702,7 +712,8 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     for (const FaSeg& sg : segs) {
       FaArgs fa;
       fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
-      for (uint32_t j = 0; j < sg.ncol; ++j) fa.colmask[j] = sg.colmask[j];
+      for (uint32_t j = 0; j < sg.ncol && j < 8; ++j) fa.colmask[j] = sg.colmask[j];
+      fa.masks = sg.masks;
       if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
     }
     EpiArgs po = part_args(L.wo);
@@ -733,9 +744,113 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     set_norm(st);
     if ((rc = sh_gemv_launch(e, m->lm_head, w.bx, w.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
   } else if (want_resid && pending) {
-    if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, m->d, nc, w.resid, m->d, true))) return rc;
+    if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, 8, m->d, nc, w.resid, m->d, true))) return rc;
   }
   return SH_OK;
+}
+
+// Forward of 8 < nc <= SH_MAX_COLS columns when every matrix is Q4_K: each
+// weight matrix is read once per chunk by sh_gemm_launch over ceil(nc / 8)
+// operand groups. QKV, o, gate/up and down write split partials that the next
+// step finishes (qkv_finish: RoPE + KV writes; residual prep; SwiGLU prep);
+// attention runs per piece (FaSeg) of at most 8 columns of one sequence.
+static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
+                            const std::vector<FaSeg>& segs, bool want_logits, bool want_resid) {
+  sh_engine* e = m->e;
+  Workspace& w = m->ws;
+  int rc;
+  const uint32_t ncp = (nc + 7) / 8 * 8;  // columns per split in the partial buffer
+  if ((rc = sh_embed_launch(e, m, dev_tokens, nc, w.resid))) return rc;
+  auto set_norm = [&](EpiArgs& ea) {
+    ea.ssq = w.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
+  };
+  auto part_args = [&](const QMat& q) {
+    EpiArgs pa;
+    pa.out = w.gpart; pa.ldo = q.tiles * 16; pa.cs = w.cs;
+    pa.part_stride = (size_t)ncp * pa.ldo;
+    pa.part_cap = (uint32_t)(w.gpart_floats / pa.part_stride);
+    return pa;
+  };
+  EpiArgs qkv;
+  qkv.out = w.q; qkv.Dq = m->d; qkv.Dkv = m->hd * m->n_kv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.rope = m->rope;
+  QkvCols qc;
+  for (uint32_t j = 0; j < nc; ++j) {
+    qc.pos[j] = cols[j].pos; qc.slot[j] = cols[j].slot; qc.mseq[j] = cols[j].kv->max_seq;
+    qc.kc[j] = cols[j].kv->k; qc.vc[j] = cols[j].kv->v;
+  }
+  PrepArgs pr;
+  pr.N = nc; pr.bx = w.bx; pr.xs = w.xs; pr.cs = w.cs; pr.part = w.gpart; pr.part_cols = ncp; pr.eps = m->eps;
+  pr.ssq = w.ssq;
+  uint32_t pending = 0, pending_ld = 0;
+  auto resid_prep = [&](const float* norm_w) {
+    pr.mode = PREP_RESID; pr.x = w.resid; pr.K = m->d; pr.norm_w = norm_w;
+    pr.nparts = pending; pr.part_ld = pending_ld;
+    pending = 0;
+    return sh_prep_launch(e, pr);
+  };
+  for (uint32_t l = 0; l < m->n_layer; ++l) {
+    const Layer& L = m->layers[l];
+    if ((rc = resid_prep(L.attn_norm))) return rc;
+    EpiArgs pq = part_args(L.wqkv);
+    set_norm(pq);
+    uint32_t nq = 0;
+    if ((rc = sh_gemm_launch(e, L.wqkv, w.bx, w.xs, w.cs, nc, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
+    qkv.layer = l;
+    if ((rc = sh_qkv_finish_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc))) return rc;
+    for (const FaSeg& sg : segs) {
+      FaArgs fa;
+      fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
+      for (uint32_t j = 0; j < sg.ncol && j < 8; ++j) fa.colmask[j] = sg.colmask[j];
+      fa.masks = sg.masks;
+      if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
+    }
+    EpiArgs po = part_args(L.wo);
+    if ((rc = sh_gemm_launch(e, L.wo, w.bx, w.xs, w.cs, nc, EPI_PART, po, "gemv_o", &pending))) return rc;
+    pending_ld = po.ldo;
+    if ((rc = resid_prep(L.ffn_norm))) return rc;
+    EpiArgs pg = part_args(L.wgu);
+    set_norm(pg);
+    uint32_t ngu = 0;
+    if ((rc = sh_gemm_launch(e, L.wgu, w.bx, w.xs, w.cs, nc, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
+    pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = ngu; pr.part_ld = pg.ldo; pr.K = m->ff; pr.norm_w = nullptr;
+    if ((rc = sh_prep_launch(e, pr))) return rc;
+    EpiArgs pd = part_args(L.wdown);
+    if ((rc = sh_gemm_launch(e, L.wdown, w.bx, w.xs, w.cs, nc, EPI_PART, pd, "gemv_down", &pending))) return rc;
+    pending_ld = pd.ldo;
+  }
+  if (want_logits) {
+    if ((rc = resid_prep(m->out_norm))) return rc;
+    EpiArgs st;
+    st.out = w.logits; st.ldo = m->V; st.rows = m->V; st.cs = w.cs;
+    set_norm(st);
+    if ((rc = sh_gemm_launch(e, m->lm_head, w.bx, w.xs, w.cs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
+  } else if (want_resid && pending) {
+    if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, ncp, m->d, nc, w.resid, m->d, true))) return rc;
+  }
+  return SH_OK;
+}
+
+// Columns per forward chunk: SH_MAX_COLS when the multi-group path applies
+// (all matrices Q4_K) and there are more than 8 columns, else 8.
+static uint32_t chunk_cols(const sh_model* m, uint32_t n) {
+  static const bool forced8 = [] {
+    const char* s = getenv("SH_CHUNK");
+    return s && atoi(s) == 8;
+  }();
+  return (m->mg_ok && n > 8 && !forced8) ? SH_MAX_COLS : 8;
+}
+
+// Longest attention segment on the multi-group path: SH_FA_MAX_ROWS query rows
+// (gqa x columns) per kv head.
+static uint32_t fa_seg_cols(const sh_model* m) {
+  const uint32_t gqa = m->n_head / m->n_kv;
+  return std::max<uint32_t>(8, std::min<uint32_t>(SH_MAX_COLS, (uint32_t)SH_FA_MAX_ROWS / gqa));
+}
+
+static int run_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
+                     const std::vector<FaSeg>& segs, bool want_logits, bool want_resid) {
+  return nc > 8 ? forward_chunk_mg(m, dev_tokens, nc, cols, segs, want_logits, want_resid)
+                : forward_chunk(m, dev_tokens, nc, cols, segs, want_logits, want_resid);
 }
 
 // Column geometry of a forward call: RoPE position, visibility mask and mask
@@ -808,27 +923,49 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
   for (auto p : plan.colpos) maxpos = std::max<uint32_t>(maxpos, (uint32_t)p);
   if ((rc = ensure_rope(m, maxpos + 1))) return rc;
   if ((rc = ensure_fa_part(m, pos + L))) return rc;
-  for (uint32_t c0 = 0; c0 < L; c0 += 8) {
-    const uint32_t nc = std::min<uint32_t>(8, L - c0);
+  const uint32_t CW = chunk_cols(m, L);
+  // Attention: one segment per chunk (device masks) on the multi-group path,
+  // else pieces of <= 8 columns; a causal segment's masks are relative to its
+  // first column.
+  std::vector<uint64_t> hmask(L);
+  std::vector<std::vector<FaSeg>> chunk_segs;
+  for (uint32_t c0 = 0; c0 < L; c0 += CW) {
+    const uint32_t nc = std::min<uint32_t>(CW, L - c0), piece = CW > 8 ? fa_seg_cols(m) : 8;
+    std::vector<FaSeg> segs;
+    for (uint32_t j0 = 0; j0 < nc; j0 += piece) {
+      FaSeg sg;
+      sg.kv = kv; sg.col0 = j0; sg.ncol = std::min<uint32_t>(piece, nc - j0); sg.kvlen = pos + c0 + j0 + sg.ncol;
+      sg.mask_base = plan.tree ? pos : pos + c0 + j0;
+      for (uint32_t t = 0; t < sg.ncol; ++t) {
+        const uint64_t mk = plan.tree ? plan.mask[c0 + j0 + t] : (t == 63 ? ~0ull : (2ull << t) - 1ull);
+        hmask[c0 + j0 + t] = mk;
+        if (t < 8) sg.colmask[t] = mk;
+      }
+      segs.push_back(sg);
+    }
+    chunk_segs.push_back(segs);
+  }
+  uint64_t* dmask = nullptr;
+  if (CW > 8) {
+    SH_HIP(hipMallocAsync((void**)&dmask, (size_t)L * 8, e->stream));
+    SH_HIP(hipMemcpyAsync(dmask, hmask.data(), (size_t)L * 8, hipMemcpyHostToDevice, e->stream));
+    for (size_t c = 0; c < chunk_segs.size(); ++c)
+      for (FaSeg& sg : chunk_segs[c]) sg.masks = dmask + c * CW + sg.col0;
+  }
+  struct MaskFree {  // the masks stay allocated until every launch that reads them is queued
+    sh_engine* e; uint64_t* p;
+    ~MaskFree() { if (p) (void)hipFreeAsync(p, e->stream); }
+  } mask_free{e, dmask};
+  for (uint32_t c0 = 0; c0 < L; c0 += CW) {
+    const uint32_t nc = std::min<uint32_t>(CW, L - c0);
     const bool last = c0 + nc == L;
     const bool want = logits_mode == 2 || (logits_mode == 1 && last);
-    std::vector<uint64_t> mk(nc);
-    uint32_t mbase;
-    if (plan.tree) {
-      mbase = pos;
-      for (uint32_t j = 0; j < nc; ++j) mk[j] = plan.mask[c0 + j];
-    } else {
-      mbase = pos + c0;
-      for (uint32_t j = 0; j < nc; ++j) mk[j] = plan.mask[c0 + j];
-    }
     std::vector<ColKv> cols(nc);
     for (uint32_t j = 0; j < nc; ++j) {
       cols[j].kv = kv; cols[j].slot = pos + c0 + j; cols[j].pos = plan.colpos[c0 + j];
     }
-    std::vector<FaSeg> segs(1);
-    segs[0].kv = kv; segs[0].col0 = 0; segs[0].ncol = nc; segs[0].kvlen = pos + c0 + nc; segs[0].mask_base = mbase;
-    for (uint32_t j = 0; j < nc; ++j) segs[0].colmask[j] = mk[j];
-    if ((rc = forward_chunk(m, dev_tokens + c0, nc, cols.data(), segs, want, resid_host != nullptr))) return rc;
+    const std::vector<FaSeg>& segs = chunk_segs[c0 / CW];
+    if ((rc = run_chunk(m, dev_tokens + c0, nc, cols.data(), segs, want, resid_host != nullptr))) return rc;
     if (resid_host)
       SH_HIP(hipMemcpyAsync(resid_host + (size_t)c0 * m->d, m->ws.resid, (size_t)nc * m->d * 4,
                             hipMemcpyDeviceToHost, e->stream));
@@ -955,30 +1092,45 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
   uint32_t* dt = nullptr;
   if ((rc = upload_tokens(m, tokens, N, &dt))) return rc;
   uint32_t* ids = nullptr;
-  if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, 8 * 4, e->stream));
+  if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, SH_MAX_COLS * 4, e->stream));
   const bool want_logits = logits_out || logits_dev || sampled_out;
-  for (uint32_t c0 = 0; c0 < N && !rc; c0 += 8) {
-    const uint32_t nc = std::min<uint32_t>(8, N - c0);
-    // one attention segment per run of one sequence's columns in the chunk
+  const uint32_t CW = chunk_cols(m, N);
+  // attention segments: runs of one sequence's columns in a chunk (at most 8
+  // each on the 8-column path; device masks on the multi-group path)
+  std::vector<uint64_t> hmask(N);
+  std::vector<std::vector<FaSeg>> chunk_segs;
+  for (uint32_t c0 = 0; c0 < N; c0 += CW) {
+    const uint32_t nc = std::min<uint32_t>(CW, N - c0), piece = CW > 8 ? fa_seg_cols(m) : 8;
     std::vector<FaSeg> segs;
     for (uint32_t j = 0; j < nc;) {
       const uint32_t s = cseq[c0 + j], i0 = cidx[c0 + j];
       uint32_t n = 1;
-      while (j + n < nc && cseq[c0 + j + n] == s) ++n;
+      while (j + n < nc && n < piece && cseq[c0 + j + n] == s) ++n;
       FaSeg sg;
       sg.kv = caches[s]; sg.col0 = j; sg.ncol = n;
       sg.kvlen = caches[s]->pos + i0 + n;
-      if (plans[s].tree) {
-        sg.mask_base = caches[s]->pos;
-        for (uint32_t t = 0; t < n; ++t) sg.colmask[t] = plans[s].mask[i0 + t];
-      } else {
-        sg.mask_base = caches[s]->pos + i0;
-        for (uint32_t t = 0; t < n; ++t) sg.colmask[t] = (2ull << t) - 1ull;
+      sg.mask_base = plans[s].tree ? caches[s]->pos : caches[s]->pos + i0;
+      for (uint32_t t = 0; t < n; ++t) {
+        const uint64_t mk = plans[s].tree ? plans[s].mask[i0 + t] : (t == 63 ? ~0ull : (2ull << t) - 1ull);
+        hmask[c0 + j + t] = mk;
+        if (t < 8) sg.colmask[t] = mk;
       }
       segs.push_back(sg);
       j += n;
     }
-    rc = forward_chunk(m, dt + c0, nc, cols.data() + c0, segs, want_logits, residual_out != nullptr);
+    chunk_segs.push_back(segs);
+  }
+  uint64_t* dmask = nullptr;
+  if (CW > 8) {
+    SH_HIP(hipMallocAsync((void**)&dmask, (size_t)N * 8, e->stream));
+    SH_HIP(hipMemcpyAsync(dmask, hmask.data(), (size_t)N * 8, hipMemcpyHostToDevice, e->stream));
+    for (size_t c = 0; c < chunk_segs.size(); ++c)
+      for (FaSeg& sg : chunk_segs[c]) sg.masks = dmask + c * CW + sg.col0;
+  }
+  for (uint32_t c0 = 0; c0 < N && !rc; c0 += CW) {
+    const uint32_t nc = std::min<uint32_t>(CW, N - c0);
+    const std::vector<FaSeg>& segs = chunk_segs[c0 / CW];
+    rc = run_chunk(m, dt + c0, nc, cols.data() + c0, segs, want_logits, residual_out != nullptr);
     if (rc) break;
     if (residual_out)
       SH_HIP(hipMemcpyAsync(residual_out + (size_t)c0 * m->d, m->ws.resid, (size_t)nc * m->d * 4,
@@ -997,6 +1149,7 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
   hipError_t se = hipStreamSynchronize(e->stream);
   (void)hipFree(dt);
   if (ids) (void)hipFree(ids);
+  if (dmask) (void)hipFree(dmask);
   if (rc) return rc;
   SH_CHECK(se == hipSuccess, SH_ERR_HIP, "verify_unified: %s", hipGetErrorString(se));
   for (uint32_t s = 0; s < B; ++s) {
@@ -1209,25 +1362,38 @@ extern "C" int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_d
   const uint32_t K = w->m.K, M = w->m.M;
   uint16_t *bx = nullptr, *xs = nullptr;
   float *cs = nullptr, *part = nullptr;
-  const size_t bx_elems = (size_t)K / 32 * 64 * 8, xs_elems = (size_t)(K + 255) / 256 * 64 * 8;
-  const size_t part_floats = sh_gemv_part_floats(w->m);
+  // Q4_K with more than 8 columns: the forward's multi-group kernel, 64 columns per pass
+  const bool mg = w->m.type == GGML_Q4_K && K % 256 == 0 && N > 8;
+  const uint32_t CW = mg ? SH_MAX_COLS : 8, ngrp = CW / 8;
+  const size_t bx_elems = ngrp * sh_grp_bx(K), xs_elems = ngrp * sh_grp_xs(K);
+  const size_t part_floats = mg ? sh_gemm_part_floats(w->m) : sh_gemv_part_floats(w->m);
   SH_HIP(hipMallocAsync((void**)&bx, bx_elems * 2, e->stream));
   SH_HIP(hipMallocAsync((void**)&xs, xs_elems * 2, e->stream));
-  SH_HIP(hipMallocAsync((void**)&cs, (size_t)(K + 255) / 256 * 8 * sizeof(float), e->stream));
-  SH_HIP(hipMallocAsync((void**)&part, part_floats * sizeof(float), e->stream));
+  SH_HIP(hipMallocAsync((void**)&cs, ngrp * sh_grp_cs(K) * sizeof(float), e->stream));
+  SH_HIP(hipMallocAsync((void**)&part, std::max<size_t>(part_floats, 4) * sizeof(float), e->stream));
   SH_HIP(hipMemsetAsync(xs, 0, xs_elems * 2, e->stream));
   int rc = SH_OK;
   // The same kernels as the forward: split partials (finished here by a reduce)
   // where the forward would use them, else a direct store / accumulate.
   const bool split = w->m.type == GGML_Q4_K && part_floats > (size_t)8 * w->m.tiles * 16;
-  for (uint32_t c0 = 0; c0 < N && !rc; c0 += 8) {
-    const uint32_t nc = std::min<uint32_t>(8, N - c0);
+  for (uint32_t c0 = 0; c0 < N && !rc; c0 += CW) {
+    const uint32_t nc = std::min<uint32_t>(CW, N - c0);
     PrepArgs pr;
     pr.mode = PREP_PLAIN; pr.x = const_cast<float*>(x_dev + (size_t)c0 * K); pr.K = K; pr.N = nc;
     pr.bx = bx; pr.xs = xs; pr.cs = cs;
     rc = sh_prep_launch(e, pr);
     if (rc) break;
-    if (split) {
+    if (mg) {
+      const uint32_t ncp = (nc + 7) / 8 * 8;
+      EpiArgs pa;
+      pa.out = part; pa.ldo = w->m.tiles * 16; pa.cs = cs;
+      pa.part_stride = (size_t)ncp * pa.ldo;
+      pa.part_cap = (uint32_t)(part_floats / pa.part_stride);
+      uint32_t np = 0;
+      rc = sh_gemm_launch(e, w->m, bx, xs, cs, nc, EPI_PART, pa, "gemm", &np);
+      if (!rc)
+        rc = sh_part_reduce_launch(e, part, np, pa.ldo, ncp, M, nc, y_dev + (size_t)c0 * M, M, accumulate != 0);
+    } else if (split) {
       EpiArgs pa;
       pa.out = part; pa.ldo = w->m.tiles * 16; pa.cs = cs;
       pa.part_stride = (size_t)8 * pa.ldo;
@@ -1235,7 +1401,7 @@ extern "C" int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_d
       uint32_t np = 0;
       rc = sh_gemv_launch(e, w->m, bx, xs, nc, EPI_PART, pa, "gemv", &np);
       if (!rc)
-        rc = sh_part_reduce_launch(e, part, np, pa.ldo, M, nc, y_dev + (size_t)c0 * M, M, accumulate != 0);
+        rc = sh_part_reduce_launch(e, part, np, pa.ldo, 8, M, nc, y_dev + (size_t)c0 * M, M, accumulate != 0);
     } else {
       EpiArgs ea;
       ea.out = y_dev + (size_t)c0 * M;

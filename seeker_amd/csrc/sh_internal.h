@@ -42,9 +42,9 @@ enum : int { GGML_F32 = 0, GGML_F16 = 1, GGML_Q8_0 = 8, GGML_Q4_K = 12 };
 constexpr int SH_TILE_ROWS = 16;
 constexpr int SH_Q4K_TILE_BYTES = 2304;  // 16 rows x 144 B, repacked
 constexpr int SH_Q8_TILE_BYTES = 544;    // 16 rows x 34 B, repacked
-constexpr int SH_MAX_COLS = 64;          // columns per forward chunk
+constexpr uint32_t SH_MAX_COLS = 64;     // columns per forward chunk (8 operand groups of 8)
 constexpr int SH_FA_MIN_SPLIT_KEYS = 64;  // smallest key split of any attention launch (sizes fa_part)
-constexpr int SH_FA_MAX_ROWS = 64;        // padded query rows (gqa x columns) per kv head
+constexpr int SH_FA_MAX_ROWS = 256;       // padded query rows (gqa x columns) per kv head
 // Split partial row: O[hd], m, l, 2 pad (keeps rows 16-byte aligned).
 __host__ __device__ constexpr uint32_t sh_fa_part_stride(uint32_t hd) { return hd + 4; }
 
@@ -126,6 +126,7 @@ struct sh_model {
   uint32_t rope_max = 0;
   Workspace ws;
   double alg_weight_bytes = 0;  // bytes of every matrix a full-logits forward reads
+  bool mg_ok = false;           // every matrix Q4_K: chunks above 8 columns take the multi-group path
 };
 
 struct sh_kv {
@@ -178,6 +179,23 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
                    EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
 // Floats of partial-sum buffer the EPI_PART launches of w need (all splits).
 size_t sh_gemv_part_floats(const QMat& w);
+// y = W x for N <= SH_MAX_COLS columns (operand groups of 8, Q4_K) in one pass
+// over W: EPI_PART (partials [split][8 ceil(N/8)][ldo]; *nparts = splits) or
+// EPI_STORE. The operand of group g starts at g times one group's size.
+int sh_gemm_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs, uint32_t N,
+                   EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
+size_t sh_gemm_part_floats(const QMat& w);  // for SH_MAX_COLS columns
+// Fused QKV rows from sh_gemm_launch partials: RoPE, q out, K/V into each
+// column's cache slot.
+struct QkvCols {  // per column: RoPE position, cache slot, capacity, K and V caches
+  int32_t pos[SH_MAX_COLS];
+  uint32_t slot[SH_MAX_COLS];
+  uint32_t mseq[SH_MAX_COLS];
+  uint16_t* kc[SH_MAX_COLS];
+  uint16_t* vc[SH_MAX_COLS];
+};
+int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
+                         uint32_t N, const EpiArgs& ea, const QkvCols& qc);
 
 // Activation prep: finishes the previous GEMV (residual add of its split
 // partials, or SwiGLU of gate/up partials) and builds the next activation
@@ -193,8 +211,8 @@ struct PrepArgs {
   int mode = PREP_PLAIN;
   float* ssq = nullptr;         // with norm_w: per-superblock sums of squares [K/256][8] out
   float* x = nullptr;           // PLAIN/RESID: [N][K] input; RESID writes x + partials back
-  const float* part = nullptr;  // partials [nparts][8][part_ld]
-  uint32_t nparts = 0, part_ld = 0;
+  const float* part = nullptr;  // partials [nparts][part_cols][part_ld]
+  uint32_t nparts = 0, part_ld = 0, part_cols = 8;
   uint32_t K = 0, N = 0;
   const float* norm_w = nullptr;
   float eps = 0.f;
@@ -204,8 +222,8 @@ struct PrepArgs {
 };
 int sh_prep_launch(sh_engine* e, const PrepArgs& a);
 // y[col][m] (+)= sum of nparts split partials, m < M.
-int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint32_t part_ld, uint32_t M, uint32_t N,
-                          float* y, uint32_t ldy, bool accumulate);
+int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint32_t part_ld, uint32_t part_cols,
+                          uint32_t M, uint32_t N, float* y, uint32_t ldy, bool accumulate);
 int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uint32_t N, float* resid);
 struct FaArgs {
   uint32_t layer = 0, N = 0;
@@ -213,6 +231,7 @@ struct FaArgs {
   uint32_t kvlen = 0;      // keys [0, kvlen) exist
   uint32_t mask_base = 0;  // keys >= mask_base need their bit in colmask
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const uint64_t* masks = nullptr;  // device masks per column (N up to SH_MAX_COLS); null: colmask (N <= 8)
 };
 // Attention for the chunk's columns, then the split combine, which writes
 // attn_out [N][n_embd] f32 and the Wo activation operand (bx, xs, per-superblock cs).

@@ -11,6 +11,13 @@ __device__ __forceinline__ float sh_wave_max(float v) {
   return v;
 }
 
+// Operands of more than 8 columns come in groups of 8: column col lives in
+// group col / 8 as lane column col % 8, and group g's B, XS, cs and sums of
+// squares start at g times one group's size for this K (sizes below).
+__host__ __device__ __forceinline__ size_t sh_grp_bx(uint32_t K) { return (size_t)((K + 255) / 256) * 8 * 512; }
+__host__ __device__ __forceinline__ size_t sh_grp_xs(uint32_t K) { return (size_t)((K + 255) / 256) * 512; }
+__host__ __device__ __forceinline__ size_t sh_grp_cs(uint32_t K) { return (size_t)((K + 255) / 256) * 8; }
+
 // One wave writes superblock sb (elements 256 sb .. 256 sb + 255) of column
 // `col` of the GEMV activation operand; lane l holds y[256 sb + 4l .. +3]
 // (zeros past K). The superblock is multiplied by the power of two s that puts
@@ -23,6 +30,13 @@ __device__ __forceinline__ void sh_operand_store_sb(float4 v, uint32_t K, uint32
                                                     uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
                                                     float* __restrict__ cs) {
   const uint32_t lane = threadIdx.x & 63;
+  {
+    const uint32_t g = col / 8;
+    bx += g * sh_grp_bx(K);
+    xs += g * sh_grp_xs(K);
+    cs += g * sh_grp_cs(K);
+    col %= 8;
+  }
   const float mx = sh_wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
   int ex = 0;
   if (mx > 0.f && mx < INFINITY) {

@@ -63,3 +63,37 @@ def test_gemv_q4k_lm_head_shape(engine):
     got, ref = _run(engine, GGML_Q4_K, 128256, 4096, 8, seed=5)
     assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
     assert np.array_equal(got.argmax(axis=1), ref.argmax(axis=1))
+
+
+# Multi-group kernel (Q4_K, more than 8 columns: up to 64 columns per pass over
+# the weights, split-K partials reduced in split order).
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 9), (4096, 4096, 64), (28672, 4096, 40), (4096, 14336, 33),
+                                   (6144, 4096, 164)])
+def test_gemm_q4k_multi_group(engine, M, K, N):
+    got, ref = _run(engine, GGML_Q4_K, M, K, N, seed=M + N)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
+    assert np.array_equal(got.argmax(axis=1), ref.argmax(axis=1))
+
+
+def test_gemm_q4k_multi_group_ragged_accumulate(engine):
+    got, ref = _run(engine, GGML_Q4_K, 37, 768, 21, seed=4, accumulate=True)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
+
+
+def test_gemm_q4k_columns_independent_of_batch(engine):
+    """A column's result does not depend on how many columns share the launch
+    (split shapes depend on the matrix only)."""
+    M, K = 4096, 4096
+    w = _weights(GGML_Q4_K, M, K, 11)
+    x = np.random.default_rng(11).standard_normal((64, K)).astype(np.float32)
+    qt = QTensor(engine, GGML_Q4_K, w, M, K)
+    outs = []
+    for n in (64, 20, 9):
+        xd = engine.to_device(np.ascontiguousarray(x[:n]))
+        yd = engine.to_device(np.zeros((n, M), np.float32))
+        engine.gemv(qt, xd, n, yd, False)
+        outs.append(yd.read(np.float32, n * M).reshape(n, M))
+        xd.free(); yd.free()
+    qt.close()
+    assert np.array_equal(outs[0][:20], outs[1])
+    assert np.array_equal(outs[0][:9], outs[2])

@@ -1,13 +1,18 @@
 """Batched verify (sh_verify_unified, Engine::verify_unified inference/mod.rs:2316-2398)
 on the GPU.
 
-Every column's arithmetic is independent of which other columns share its
-launch (GEMV columns, per-column RMSNorm and operand scales, attention splits
-at absolute key indices), so a batch of B sequences must give bit-identical
-logits, ids, residuals and KV rows to B separate sh_forward_full calls, however
-the flat packing cuts sequences across 8-column chunks. The separate calls are
-themselves checked against the C oracle in test_gpu_forward.py; here the batch
-is also compared to the oracle per sequence.
+Within one kernel path every column's arithmetic is independent of which
+other columns share its launch (GEMV columns, per-column RMSNorm and operand
+scales, attention splits at absolute key indices, multi-group split-K shapes
+that depend on the matrix only). Chunks of up to 8 columns take the 8-column
+GEMV kernels; longer chunks of an all-Q4_K model take the multi-group kernel.
+So a batch of B sequences gives bit-identical logits, ids, residuals and KV
+rows to B separate sh_forward_full calls whenever both take the same path,
+however the flat packing cuts sequences across chunks; across the two paths
+only the f32 summation order differs (checked to 1e-5 of the logit scale, same
+argmax). The separate calls are themselves checked against the C oracle in
+test_gpu_forward.py; here the batch is also compared to the oracle per
+sequence.
 """
 import numpy as np
 import pytest
@@ -67,24 +72,37 @@ def test_unified_equals_separate_forwards(engine, model):
     out = engine.verify_unified(gm, batch_kv, toks, lens, positions=positions, want_logits=True,
                                 want_residual=True)
     assert list(out.q_starts) == [0, 5, 16, 19]
+    multi_group = name == "gqa_q4k"  # all-Q4_K: chunks above 8 columns take the multi-group kernel
+    batch_mg = multi_group and sum(lens) > 8
     for s, (p, n) in enumerate(SEQS):
         lg, res = engine.forward_full_readback(gm, ref_kv[s], drafts[s], p, full_logits=True, want_residual=True)
         q = int(out.q_starts[s])
-        print(f"{name} seq {s}: logits max|d| {np.abs(out.logits[q:q + n] - lg).max():.3e}", flush=True)
-        assert np.array_equal(out.logits[q:q + n], lg)
-        assert np.array_equal(out.residual[q:q + n], res)
+        same_path = batch_mg == (multi_group and n > 8)
+        print(f"{name} seq {s}: logits max|d| {np.abs(out.logits[q:q + n] - lg).max():.3e} "
+              f"(same path {same_path})", flush=True)
         assert np.array_equal(out.sampled[q:q + n], lg.argmax(axis=1).astype(np.uint32))
         assert batch_kv[s].position == p + n
-        for a, b in zip(_kv_rows(batch_kv[s], gm, p, p + n), _kv_rows(ref_kv[s], gm, p, p + n)):
-            assert np.array_equal(a, b)
+        rows = zip(_kv_rows(batch_kv[s], gm, p, p + n), _kv_rows(ref_kv[s], gm, p, p + n))
+        if same_path:
+            assert np.array_equal(out.logits[q:q + n], lg)
+            assert np.array_equal(out.residual[q:q + n], res)
+            for a, b in rows:
+                assert np.array_equal(a, b)
+        else:
+            assert np.abs(out.logits[q:q + n] - lg).max() <= 1e-5 * np.abs(lg).max()
+            assert np.abs(out.residual[q:q + n] - res).max() <= 1e-5 * np.abs(res).max()
+            for a, b in rows:
+                a, b = a.astype(np.float32), b.astype(np.float32)
+                assert np.abs(a - b).max() <= 2e-3 * max(np.abs(b).max(), 1e-3)
     for kv in batch_kv + ref_kv:
         kv.close()
 
 
 def test_unified_tree_and_chain_vs_oracle(engine, model):
     """One tree sequence (branching 2, 2: 1 + 2 + 4 nodes below the root) next to a
-    chain; each compared bit-exactly with its own forward and, within the
-    north-star tolerance, with the oracle."""
+    chain; each compared with its own forward (bit-exactly on the same kernel
+    path, else to 1e-5 of the logit scale) and, within the north-star
+    tolerance, with the oracle."""
     name, img, gm = model
     V = gm.vocab_size()
     om = O.Model(img)
@@ -101,7 +119,11 @@ def test_unified_tree_and_chain_vs_oracle(engine, model):
         n = len(t)
         ref = _prefilled(engine, gm, prompts[s])
         lg, _ = engine.forward_full_readback(gm, ref, t, p, full_logits=True, parents=par)
-        assert np.array_equal(out.logits[q:q + n], lg)
+        if name == "gqa_q4k" and sum(lens) > 8 and n <= 8:  # batch multi-group, solo 8-column kernels
+            assert np.abs(out.logits[q:q + n] - lg).max() <= 1e-5 * np.abs(lg).max()
+            assert np.array_equal(out.logits[q:q + n].argmax(axis=1), lg.argmax(axis=1))
+        else:
+            assert np.array_equal(out.logits[q:q + n], lg)
         okv = O.KvCache(om, 256)
         O.forward(om, okv, prompts[s], 0, logits_mode=0)
         ol, _ = O.forward(om, okv, t, p, parents=par, logits_mode=2)
