@@ -59,7 +59,7 @@ __device__ __forceinline__ uint64_t col_mask(const FaArgs& fa, uint32_t col) {
 // waves; wave w takes key block kb = w % NKB (NH blocks of 32 keys) for row
 // group qg = w / NKB (16 query rows). The NQG waves of one key block read the
 // same K and V (the second read hits the CU's cache).
-template <int HD, int NQG, int NKB, int NH>
+template <int HD, int NQG, int NKB, int NH, bool DMASK>
 __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                         const uint16_t* __restrict__ vc, uint32_t max_seq,
                                                         uint32_t n_head, uint32_t N, uint32_t gqa, FaArgs fa,
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) vop[h][dt] = ld_h8(vp + (size_t)dt * 16 * 32);
   }
-  const uint64_t cm = fa.masks ? fa.masks[col] : col_mask(fa, col);
+  const uint64_t cm = DMASK ? fa.masks[col] : col_mask(fa, col);
   __builtin_amdgcn_sched_barrier(0);
 
   // Q^T operand (B). Each query row is scaled by a power of two (max|q * s| in
@@ -332,12 +332,20 @@ static void fa_launch_cfg(uint32_t split_keys, dim3 grid, hipStream_t st, const 
                           const FaArgs& fa, float scale, float* part) {
   constexpr int NKB = 4;
   const dim3 block(64 * NQG * NKB);
-  if (split_keys == 256)
-    hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 2>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale,
-                       part);
-  else
-    hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 1>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa, scale,
-                       part);
+  if (fa.masks) {  // columns beyond 8: masks from device memory
+    if (split_keys == 256)
+      hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 2, true>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                         scale, part);
+    else
+      hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 1, true>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                         scale, part);
+  } else if (split_keys == 256) {
+    hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 2, false>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                       scale, part);
+  } else {
+    hipLaunchKernelGGL((k_fa<HD, NQG, NKB, 1, false>), grid, block, 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                       scale, part);
+  }
 }
 
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
