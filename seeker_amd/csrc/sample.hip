@@ -606,6 +606,202 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
   }
 }
 
+// ---------------------------------------------------------------- tree REJECTION (multi-workgroup)
+
+// The same walk as k_tree_accept in REJECTION mode, with every full-vocab
+// reduction spread over kDrawChunks workgroups per tree. The residual after
+// m effective rejections at node v is never stored: cur_m(x) is recomputed
+// pointwise from the stored normalizers Z_1..Z_m with the operations of the
+// stored form (cur = r / Z, d = cur - q(x), r = max(d, 0)), so each value is
+// the one k_tree_accept would hold. A step is k_tree_step (one workgroup per
+// tree: finish the previous pass, then accept tests until the next pass is
+// needed) followed by k_tree_pass (chunk sums of that pass).
+enum : uint32_t { TS_WALK = 0, TS_ZPASS = 1, TS_DRAW = 2, TS_DONE = 3 };
+struct TreeState {
+  uint32_t v, len, mode, next, m, tok;
+  double Z[64];        // normalizers of the effective rejections at v
+  uint32_t path[64];
+};
+
+// Current distribution at a node: cur_m, the next residual summand and the
+// draw weight (softmax numerator without rejections, else the unnormalized
+// residual r_m).
+struct TreeCur {
+  double pm, ps, qm, qs, inv_t;
+  const double* Z;
+  uint32_t m;
+  const double* tab;
+  __device__ __forceinline__ double qprob(float qx) const { return sh_exp_neg(((double)qx - qm) * inv_t, tab) / qs; }
+  __device__ __forceinline__ double cur(float px, float qx) const {
+    double c = sh_exp_neg(((double)px - pm) * inv_t, tab) / ps;
+    if (m == 0) return c;
+    const double qp = qprob(qx);
+    for (uint32_t j = 0; j < m; ++j) {
+      const double d = c - qp;
+      c = (d > 0.0 ? d : 0.0) / Z[j];
+    }
+    return c;
+  }
+  __device__ __forceinline__ double resid_next(float px, float qx) const {
+    const double d = cur(px, qx) - qprob(qx);
+    return d > 0.0 ? d : 0.0;
+  }
+  __device__ __forceinline__ double draw_w(float px, float qx) const {
+    if (m == 0) return sh_exp_neg(((double)px - pm) * inv_t, tab);
+    double c = sh_exp_neg(((double)px - pm) * inv_t, tab) / ps, r = 0.0;
+    const double qp = qprob(qx);
+    for (uint32_t j = 0; j < m; ++j) {
+      const double d = c - qp;
+      r = d > 0.0 ? d : 0.0;
+      c = r / Z[j];
+    }
+    return r;
+  }
+};
+
+struct TreeDrawW {  // RowW-style access for wg_inverse_cdf
+  const float* p;
+  const float* q;
+  TreeCur tc;
+  using Raw = float2;
+  __device__ __forceinline__ Raw raw(uint32_t v) const { return make_float2(p[v], tc.m ? q[v] : 0.f); }
+  __device__ __forceinline__ double wt(Raw x) const { return tc.draw_w(x.x, x.y); }
+};
+
+// Statistics of node v of tree b: p row b n + v, q row B n + b n + v.
+__device__ __forceinline__ TreeCur tree_cur(const double2* part, uint32_t nch, uint32_t B, uint32_t n, uint32_t b,
+                                            uint32_t v, double inv_t, const double* Z, uint32_t m, const double* tab) {
+  const double2 sp = lane_row_stat(part + ((size_t)b * n + v) * nch, nch, inv_t, tab);
+  const double2 sq = lane_row_stat(part + ((size_t)B * n + (size_t)b * n + v) * nch, nch, inv_t, tab);
+  return TreeCur{sp.x, sp.y, sq.x, sq.y, inv_t, Z, m, tab};
+}
+
+__global__ __launch_bounds__(256) void k_tree_step(const float* __restrict__ p, const float* __restrict__ q,
+                                                   const uint32_t* __restrict__ tokens,
+                                                   const int32_t* __restrict__ parents, uint32_t B, uint32_t n,
+                                                   uint32_t V, double inv_t, const double2* __restrict__ part,
+                                                   uint32_t nch, const float* u_dev, uint64_t seed, uint64_t counter,
+                                                   TreeState* __restrict__ state, const double* __restrict__ chunk,
+                                                   int first, uint32_t* __restrict__ path_out,
+                                                   uint32_t* __restrict__ path_len, uint32_t* __restrict__ next_tok) {
+  __shared__ double tab[64];
+  __shared__ TreeState s;
+  __shared__ TreeCur sc;
+  __shared__ uint32_t s_c;
+  __shared__ double s_off, s_target;
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  load_exp_table(tab);
+  const float* P = p + (size_t)b * n * V;
+  const float* Q = q + (size_t)b * n * V;
+  if (t == 0) {
+    if (first) {
+      s.v = 0; s.len = 1; s.mode = TS_WALK; s.next = 1; s.m = 0; s.tok = 0; s.path[0] = 0;
+    } else {
+      s = state[b];
+    }
+  }
+  __syncthreads();
+  if (s.mode == TS_DRAW) {  // draw sums are in: pick the chunk, then the inverse CDF inside it
+    if (t == 0) {
+      sc = tree_cur(part, nch, B, n, b, s.v, inv_t, s.Z, s.m, tab);
+      const double* ch = chunk + (size_t)b * kDrawChunks;
+      double total = 0.0;
+      for (uint32_t c = 0; c < kDrawChunks; ++c) total += ch[c];
+      const float u = uniform_at(u_dev, seed, counter + 2ull * ((uint64_t)b * n + s.v) + 1ull);
+      const double target = (double)u * total;
+      double off = 0.0;
+      uint32_t cs = kDrawChunks - 1;
+      for (uint32_t c = 0; c + 1 < kDrawChunks; ++c) {
+        if (off + ch[c] > target) { cs = c; break; }
+        off += ch[c];
+      }
+      s_c = cs; s_off = off; s_target = target;
+    }
+    __syncthreads();
+    const uint32_t CH = (V + kDrawChunks - 1) / kDrawChunks, lo = min(s_c * CH, V), hi = min(lo + CH, V);
+    TreeCur tc = sc;
+    tc.Z = s.Z;
+    const TreeDrawW w{P + (size_t)s.v * V, Q + (size_t)s.v * V, tc};
+    const uint32_t tok = wg_inverse_cdf(w, lo, hi, false, 0.f, s_off, s_target, false, nullptr);
+    if (t == 0) { s.tok = tok; s.mode = TS_DONE; }
+  } else if (t == 0 && s.mode == TS_ZPASS) {  // residual sum is in
+    const double* ch = chunk + (size_t)b * kDrawChunks;
+    double R = 0.0;
+    for (uint32_t c = 0; c < kDrawChunks; ++c) R += ch[c];
+    if (R > 0.0) s.Z[s.m++] = R;
+    s.mode = TS_WALK;
+  }
+  if (t == 0) {
+    const uint32_t* tok = tokens + (size_t)b * n;
+    const int32_t* par = parents + (size_t)b * n;
+    while (s.mode == TS_WALK) {
+      uint32_t c = s.next;
+      while (c < n && par[c] != (int32_t)s.v) ++c;
+      if (c >= n) { s.mode = TS_DRAW; break; }
+      const TreeCur tc = tree_cur(part, nch, B, n, b, s.v, inv_t, s.Z, s.m, tab);
+      const uint32_t x = tok[c];
+      bool ok = false;
+      if (x < V) {
+        const float* pv = P + (size_t)s.v * V;
+        const float* qv = Q + (size_t)s.v * V;
+        const double pc = tc.cur(pv[x], qv[x]), qc = tc.qprob(qv[x]);
+        ok = (double)uniform_at(u_dev, seed, counter + 2ull * ((uint64_t)b * n + c)) * qc < pc;
+      }
+      if (ok) {
+        s.v = c; s.path[s.len++] = c; s.m = 0; s.next = c + 1;
+      } else {
+        s.next = c + 1;
+        s.mode = TS_ZPASS;
+      }
+    }
+    state[b] = s;
+    if (s.mode == TS_DONE) {
+      for (uint32_t i = 0; i < s.len; ++i) path_out[(size_t)b * n + i] = s.path[i];
+      path_len[b] = s.len;
+      next_tok[b] = s.tok;
+    }
+  }
+}
+
+// Chunk sums of the pass each tree asked for: residual summands (TS_ZPASS) or
+// draw weights (TS_DRAW) over chunk blockIdx.x of node v's vocabulary.
+__global__ __launch_bounds__(256) void k_tree_pass(const float* __restrict__ p, const float* __restrict__ q,
+                                                   uint32_t B, uint32_t n, uint32_t V, double inv_t,
+                                                   const double2* __restrict__ part, uint32_t nch,
+                                                   const TreeState* __restrict__ state, double* __restrict__ chunk) {
+  __shared__ double tab[64];
+  __shared__ double shd[4];
+  __shared__ TreeCur sc;
+  __shared__ double sZ[64];
+  const uint32_t c = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const uint32_t mode = state[b].mode;
+  if (mode != TS_ZPASS && mode != TS_DRAW) return;  // uniform in the workgroup
+  load_exp_table(tab);
+  const uint32_t v = state[b].v, m = state[b].m;
+  if (t < m) sZ[t] = state[b].Z[t];
+  __syncthreads();
+  if (t == 0) sc = tree_cur(part, nch, B, n, b, v, inv_t, sZ, m, tab);
+  __syncthreads();
+  const TreeCur tc = sc;
+  const float* pv = p + ((size_t)b * n + v) * V;
+  const float* qv = q + ((size_t)b * n + v) * V;
+  const uint32_t CH = (V + kDrawChunks - 1) / kDrawChunks, lo = min(c * CH, V), hi = min(lo + CH, V);
+  double acc = 0.0;
+  for (uint32_t x0 = lo; x0 < hi; x0 += 256 * 8) {
+    float2 xv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t x = x0 + j * 256 + t;
+      xv[j] = x < hi ? make_float2(pv[x], qv[x]) : make_float2(-INFINITY, -INFINITY);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (x0 + j * 256 + t < hi) acc += mode == TS_ZPASS ? tc.resid_next(xv[j].x, xv[j].y) : tc.draw_w(xv[j].x, xv[j].y);
+  }
+  acc = block_sum_d(acc, shd);
+  if (t == 0) chunk[(size_t)b * kDrawChunks + c] = acc;
+}
+
 }  // namespace
 
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
@@ -708,13 +904,53 @@ extern "C" int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const flo
     SH_HIP(hipMallocAsync((void**)&udev, nu * 4, e->stream));
     SH_HIP(hipMemcpyAsync(udev, s->uniforms, nu * 4, hipMemcpyHostToDevice, e->stream));
   }
-  if (!greedy) SH_HIP(hipMallocAsync((void**)&r, (size_t)B * V * sizeof(double), e->stream));
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL(k_tree_accept, dim3(B), dim3(256), 0, e->stream, p_logits_dev, greedy ? nullptr : q_logits_dev,
-                     tokens_dev, parents_dev, n, V, greedy ? 1.0 : 1.0 / (double)s->temperature, greedy ? 1 : 0,
-                     udev, s->seed, udev ? 0ull : s->counter, r, path_dev, path_len_dev, next_tok_dev);
-  hipError_t le = hipGetLastError();
+  hipError_t le = hipSuccess;
+  if (greedy) {
+    hipLaunchKernelGGL(k_tree_accept, dim3(B), dim3(256), 0, e->stream, p_logits_dev, nullptr, tokens_dev,
+                       parents_dev, n, V, 1.0, 1, udev, s->seed, udev ? 0ull : s->counter, r, path_dev, path_len_dev,
+                       next_tok_dev);
+    le = hipGetLastError();
+  } else {
+    // passes any tree can need: at most every child of every node on its path
+    // rejected, plus the draw
+    uint32_t max_passes = 0;
+    std::vector<uint32_t> nch_node(n), acc(n);
+    for (uint32_t b = 0; b < B; ++b) {
+      std::fill(nch_node.begin(), nch_node.end(), 0u);
+      for (uint32_t i = 1; i < n; ++i) ++nch_node[par[(size_t)b * n + i]];
+      for (uint32_t i = 0; i < n; ++i) {
+        acc[i] = nch_node[i] + (i ? acc[par[(size_t)b * n + i]] : 0u);
+        max_passes = std::max(max_passes, acc[i] + 1);
+      }
+    }
+    const double inv_t = 1.0 / (double)s->temperature;
+    const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE), nrows = 2 * B * n;
+    const uint64_t ctr = udev ? 0ull : s->counter;
+    const size_t part_b = (size_t)nrows * nch * sizeof(double2), st_b = (size_t)B * sizeof(TreeState);
+    char* scratch = nullptr;
+    SH_HIP(hipMallocAsync((void**)&scratch, part_b + st_b + (size_t)B * kDrawChunks * sizeof(double), e->stream));
+    double2* part = reinterpret_cast<double2*>(scratch);
+    TreeState* st = reinterpret_cast<TreeState*>(scratch + part_b);
+    double* chunk = reinterpret_cast<double*>(scratch + part_b + st_b);
+    if (V % 4 == 0)
+      hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, p_logits_dev,
+                         B * n, q_logits_dev, V, inv_t, nch, part);
+    else
+      hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, p_logits_dev,
+                         B * n, q_logits_dev, V, inv_t, nch, part);
+    for (uint32_t step = 0; step <= max_passes; ++step) {
+      hipLaunchKernelGGL(k_tree_step, dim3(B), dim3(256), 0, e->stream, p_logits_dev, q_logits_dev, tokens_dev,
+                         parents_dev, B, n, V, inv_t, part, nch, udev, s->seed, ctr, st, chunk, step == 0 ? 1 : 0,
+                         path_dev, path_len_dev, next_tok_dev);
+      if (step < max_passes)
+        hipLaunchKernelGGL(k_tree_pass, dim3(kDrawChunks, B), dim3(256), 0, e->stream, p_logits_dev, q_logits_dev,
+                           B, n, V, inv_t, part, nch, st, chunk);
+    }
+    le = hipGetLastError();
+    (void)hipFreeAsync(scratch, e->stream);
+  }
   sh_prof_end(e, "tree_accept", 4.0 * V * B * n * (greedy ? 1 : 2), ev);
   if (udev) (void)hipFreeAsync(udev, e->stream);
   if (r) (void)hipFreeAsync(r, e->stream);
