@@ -74,6 +74,10 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
   const int g = lane >> 4, r = lane & 15;
   const uint32_t kh = blockIdx.x, split = blockIdx.y;
   const uint32_t n_splits = gridDim.y;
+  // graph replay: live keys and mask base from the device base position
+  const uint32_t kbase0 = fa.dbase ? *fa.dbase : 0u;
+  const uint32_t kvlen = fa.kvlen + kbase0, mbase = fa.mask_base + kbase0;
+  if (fa.dbase && split * (uint32_t)(NKB * 32 * NH) >= kvlen) return;  // uniform: past the live keys
   const uint32_t n_rows = gqa * N;
   const uint32_t n_rows_pad = gridDim.z * ROWS;
   const uint32_t Dq = n_head * HD;
@@ -86,7 +90,7 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
   const float* qp = q + (size_t)col * Dq + (size_t)(kh * gqa + hq) * HD + 8 * g;
   // This wave's keys: blocks past the split's end read clamped (in-bounds) rows
   // and are masked out below.
-  const uint32_t k_end = min((split + 1) * SPLIT_KEYS, fa.kvlen);
+  const uint32_t k_end = min((split + 1) * SPLIT_KEYS, kvlen);
   const uint32_t kw = split * SPLIT_KEYS + WAVE_KEYS * kb;
   const uint16_t* kbase = kc + (size_t)kh * max_seq * HD;
   const uint16_t* vbase = vc + (size_t)kh * (max_seq / 32) * HD * 32;
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
       }
       sacc[kt] = acc;
     }
-    const bool tail = key0 + 32 > k_end || key0 + 32 > fa.mask_base;
+    const bool tail = key0 + 32 > k_end || key0 + 32 > mbase;
     float sv[8];
     float mx = -INFINITY;
 #pragma unroll
@@ -181,7 +185,7 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
         if (tail) {
           const uint32_t key = key0 + 16 * kt + 4 * g + j;
           bool vis = key < k_end;
-          if (vis && key >= fa.mask_base) vis = (cm >> (key - fa.mask_base)) & 1ull;
+          if (vis && key >= mbase) vis = (cm >> (key - mbase)) & 1ull;
           if (!vis) v = -INFINITY;
         }
         sv[4 * kt + j] = v;
@@ -264,13 +268,17 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
 // elements 256 sb + 4l .. +3. Splits are read CH at a time (every load issued
 // before the first is used); each chunk takes one exp per split.
 template <int HD>
-__global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ part, uint32_t n_splits,
+__global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ part, uint32_t n_layout,
                                                    uint32_t n_rows_pad, uint32_t n_head, uint32_t N, uint32_t gqa,
                                                    uint32_t col0, float* __restrict__ attn,
                                                    uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
-                                                   float* __restrict__ cs) {
+                                                   float* __restrict__ cs, const uint32_t* dbase, uint32_t kv_off,
+                                                   uint32_t split_keys) {
   constexpr uint32_t PS = sh_fa_part_stride(HD);
   constexpr uint32_t CH = 16;
+  // n_layout splits per kv head in the partial buffer; with dbase (graph
+  // replay) only those holding live keys are read
+  const uint32_t n_splits = dbase ? (*dbase + kv_off + split_keys - 1) / split_keys : n_layout;
   const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
   const uint32_t Dq = n_head * HD;
   const size_t sstride = (size_t)n_rows_pad * PS;
@@ -278,7 +286,7 @@ __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ par
   const bool valid = kk < Dq;
   const uint32_t k = valid ? kk : 0, head = k / HD, d = k % HD;
   const uint32_t kh = head / gqa, rho = (head % gqa) * N + col;
-  const float* p = part + (size_t)kh * n_splits * sstride + (size_t)rho * PS;
+  const float* p = part + (size_t)kh * n_layout * sstride + (size_t)rho * PS;
   float M = -INFINITY, L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (uint32_t s0 = 0; s0 < n_splits; s0 += CH) {
@@ -356,9 +364,12 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   const uint32_t n_qg = (n_rows + 16 * NQG - 1) / (16 * NQG);
   SH_CHECK(n_qg * 16 * NQG <= (uint32_t)SH_FA_MAX_ROWS, SH_ERR_UNSUPPORTED, "%u query rows per kv head above %d",
            n_rows, SH_FA_MAX_ROWS);
-  SH_CHECK(fa.kvlen > 0, SH_ERR_ARG, "attention over zero keys");
-  const uint32_t split_keys = fa_split_keys(m->n_kv, fa.kvlen, n_qg);
-  const uint32_t n_splits = (fa.kvlen + split_keys - 1) / split_keys;
+  SH_CHECK(fa.kvlen > 0 || fa.dbase, SH_ERR_ARG, "attention over zero keys");
+  SH_CHECK(!fa.dbase || fa.kv_cap >= fa.kvlen, SH_ERR_ARG, "attention: graph key capacity below the offset");
+  // graph replay: the split size and grid follow the capacity, not the live keys
+  const uint32_t kv_grid = fa.dbase ? fa.kv_cap : fa.kvlen;
+  const uint32_t split_keys = fa_split_keys(m->n_kv, kv_grid, n_qg);
+  const uint32_t n_splits = (kv_grid + split_keys - 1) / split_keys;
   const uint32_t rows_pad = n_qg * 16 * NQG;
   const size_t need = (size_t)m->n_kv * n_splits * rows_pad * sh_fa_part_stride(m->hd);
   SH_CHECK(need <= m->ws.fa_part_floats, SH_ERR_CAPACITY, "attention partial buffer too small (%zu > %zu)", need,
@@ -384,16 +395,16 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
     SH_CHECK(false, SH_ERR_UNSUPPORTED, "head_dim %u not supported (64, 128)", m->hd);
   }
   SH_HIP(hipGetLastError());
-  const double kv_bytes = 2.0 * m->n_kv * (double)fa.kvlen * m->hd * 2.0;
+  const double kv_bytes = 2.0 * m->n_kv * (double)kv_grid * m->hd * 2.0;
   sh_prof_end(e, "attention", kv_bytes, ev);
   sh_prof_begin(e, &ev);
   const dim3 cgrid((m->n_head * m->hd + 255) / 256, fa.N);
   if (m->hd == 128)
     hipLaunchKernelGGL((k_fa_combine<128>), cgrid, dim3(64), 0, e->stream, part, n_splits, rows_pad, m->n_head, fa.N,
-                       gqa, fa.col0, attn_out, bx, xs, cs);
+                       gqa, fa.col0, attn_out, bx, xs, cs, fa.dbase, fa.kvlen, split_keys);
   else
     hipLaunchKernelGGL((k_fa_combine<64>), cgrid, dim3(64), 0, e->stream, part, n_splits, rows_pad, m->n_head, fa.N,
-                       gqa, fa.col0, attn_out, bx, xs, cs);
+                       gqa, fa.col0, attn_out, bx, xs, cs, fa.dbase, fa.kvlen, split_keys);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "attn_combine", 0.0, ev);
   return SH_OK;

@@ -182,8 +182,9 @@ __device__ __forceinline__ void epilogue4(const EpiArgs& ea, uint32_t r0, uint32
       *p = *p + v[j];
     }
   } else if (EPI == EPI_QKV) {
-    qkv_store4(ea, r0, v, ea.colpos[col & 7], ea.slot[col & 7], ea.mseq[col & 7], ea.kc[col & 7], ea.vc[col & 7],
-               ea.out + (size_t)col * ea.Dq);
+    const uint32_t base = ea.dbase ? *ea.dbase : 0u;
+    qkv_store4(ea, r0, v, ea.colpos[col & 7] + (int32_t)base, ea.slot[col & 7] + base, ea.mseq[col & 7],
+               ea.kc[col & 7], ea.vc[col & 7], ea.out + (size_t)col * ea.Dq);
   }
 }
 

@@ -6,6 +6,8 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
+#include <functional>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -13,6 +15,10 @@
 
 #include "sh_internal.h"
 #include "sh_operand.h"
+
+// Bumped whenever a model or KV cache is destroyed: captured graphs that may
+// reference it are dropped (see graph replay below).
+static std::atomic<uint64_t> g_graph_gen{1};
 
 // ------------------------------------------------------------------ errors
 
@@ -513,6 +519,7 @@ extern "C" int sh_model_load_gguf(sh_engine* e, const char* path, sh_model** out
 }
 
 extern "C" void sh_model_destroy(sh_model* m) {
+  g_graph_gen.fetch_add(1);
   if (!m) return;
   (void)hipStreamSynchronize(m->e->stream);
   free_model(m);
@@ -551,6 +558,7 @@ extern "C" int sh_kv_create(sh_engine* e, const sh_model* m, uint32_t max_seq, s
 }
 
 extern "C" void sh_kv_destroy(sh_kv* kv) {
+  g_graph_gen.fetch_add(1);
   if (!kv) return;
   (void)hipStreamSynchronize(kv->e->stream);
   (void)hipFree(kv->k);
@@ -677,6 +685,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     qkv.kc[j] = cols[j].kv->k; qkv.vc[j] = cols[j].kv->v;
   }
   qkv.cs = w.cs;
+  qkv.dbase = cols[0].kv->graph_base;  // graph capture: one cache per forward
   // GEMVs whose input is RMS-normalized apply the norm factor to their outputs
   auto set_norm = [&](EpiArgs& ea) {
     ea.ssq = w.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
@@ -714,6 +723,8 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
       for (uint32_t j = 0; j < sg.ncol && j < 8; ++j) fa.colmask[j] = sg.colmask[j];
       fa.masks = sg.masks;
+      fa.dbase = sg.kv->graph_base;
+      fa.kv_cap = sg.kv->max_seq;
       if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
     }
     EpiArgs po = part_args(L.wo);
@@ -910,8 +921,10 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
                        float* logits_host) {
   sh_engine* e = m->e;
   SH_CHECK(L >= 1, SH_ERR_ARG, "empty prompt");
-  SH_CHECK(kv->pos == pos, SH_ERR_STATE, "cache.position %u doesn't match caller-supplied position_offset %u",
-           kv->pos, pos);
+  const bool graph = kv->graph_base != nullptr;  // pos is an offset from *graph_base at replay
+  SH_CHECK(graph || kv->pos == pos, SH_ERR_STATE,
+           "cache.position %u doesn't match caller-supplied position_offset %u", kv->pos, pos);
+  SH_CHECK(!graph || (L <= 8 && !parents), SH_ERR_UNSUPPORTED, "graph capture: chains of at most 8 columns");
   SH_CHECK(kv->n_layer == m->n_layer && kv->n_kv == m->n_kv && kv->hd == m->hd, SH_ERR_ARG,
            "KV cache dims do not match the model");
   SH_CHECK((uint64_t)pos + L <= kv->max_seq, SH_ERR_CAPACITY, "positions [%u, %u) exceed KV capacity %u", pos,
@@ -921,8 +934,10 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
   if (rc) return rc;
   uint32_t maxpos = 0;
   for (auto p : plan.colpos) maxpos = std::max<uint32_t>(maxpos, (uint32_t)p);
-  if ((rc = ensure_rope(m, maxpos + 1))) return rc;
-  if ((rc = ensure_fa_part(m, pos + L))) return rc;
+  if (!graph) {  // a capture sizes both for the cache capacity beforehand
+    if ((rc = ensure_rope(m, maxpos + 1))) return rc;
+    if ((rc = ensure_fa_part(m, pos + L))) return rc;
+  }
   const uint32_t CW = chunk_cols(m, L);
   // Attention: one segment per chunk (device masks) on the multi-group path,
   // else pieces of <= 8 columns; a causal segment's masks are relative to its
@@ -982,7 +997,7 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
     }
     if (resid_host || logits_host) SH_HIP(hipStreamSynchronize(e->stream));
   }
-  kv->pos = pos + L;
+  if (!graph) kv->pos = pos + L;
   return SH_OK;
 }
 
@@ -1016,10 +1031,75 @@ extern "C" int sh_forward_full(sh_engine* e, sh_model* m, sh_kv* kv, const uint3
   return sh_prof_flush(e);
 }
 
+struct SpecBufs {
+  uint32_t* tok = nullptr;     // [64]: pending..., last, d_1..d_n
+  uint32_t* samp = nullptr;    // [16]
+  uint32_t* base = nullptr;    // [4] graph base positions (device): draft, target
+  float* dlogits = nullptr;    // draft logits [8][V] (REJECTION)
+  float* tlogits = nullptr;    // target logits [9][V]
+  uint32_t* pinned = nullptr;  // host staging [128]
+  uint32_t vcap = 0;
+};
+static thread_local SpecBufs g_spec;
+
+static int spec_bufs(uint32_t V);
+static bool graphs_enabled(const sh_engine* e);
+static hipGraphExec_t graph_find(const std::vector<uintptr_t>& key);
+static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const std::vector<sh_kv*>& kvs,
+                         const std::vector<const uint32_t*>& bases, const std::function<int()>& body,
+                         hipGraphExec_t* out);
+
+// Greedy verify of up to 8 tokens by graph replay: tokens staged at tok[32..],
+// ids at samp[0..], base position at base[2].
+static int verify_greedy_graph(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L,
+                               uint32_t pos, uint32_t* sampled_out) {
+  int rc = spec_bufs(m->V);
+  if (rc) return rc;
+  uint32_t* hp = g_spec.pinned;
+  for (uint32_t i = 0; i < L; ++i) hp[32 + i] = tokens[i];
+  hp[66] = pos;
+  const std::vector<uintptr_t> key = {2, (uintptr_t)m, (uintptr_t)kv, (uintptr_t)kv->k, kv->max_seq, L};
+  hipGraphExec_t ex = graph_find(key);
+  if (!ex) {
+    if ((rc = ensure_rope(m, kv->max_seq)) || (rc = ensure_fa_part(m, kv->max_seq))) return rc;
+    rc = graph_capture(e, key, {kv}, {g_spec.base + 2}, [&] {
+      int r = forward_dev(m, kv, g_spec.tok + 32, L, 0, nullptr, 2, nullptr, nullptr, nullptr);
+      if (!r) r = sh_argmax_launch(e, m->ws.logits, m->V, L, m->ws.amax, g_spec.samp);
+      if (!r && hipMemcpyAsync(g_spec.pinned + 48, g_spec.samp, (size_t)L * 4, hipMemcpyDeviceToHost,
+                               e->stream) != hipSuccess) {
+        sh_set_error("verify readback capture failed");
+        r = SH_ERR_HIP;
+      }
+      return r;
+    }, &ex);
+    if (rc) return rc;
+  }
+  SH_HIP(hipMemcpyAsync(g_spec.tok + 32, hp + 32, (size_t)L * 4, hipMemcpyHostToDevice, e->stream));
+  SH_HIP(hipMemcpyAsync(g_spec.base + 2, hp + 66, 4, hipMemcpyHostToDevice, e->stream));
+  SH_HIP(hipGraphLaunch(ex, e->stream));
+  SH_HIP(hipStreamSynchronize(e->stream));
+  for (uint32_t i = 0; i < L; ++i) sampled_out[i] = hp[48 + i];
+  kv->pos = pos + L;
+  kv->pending.clear();
+  return SH_OK;
+}
+
 extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L,
                                 uint32_t pos, uint32_t* sampled_out) {
   SH_CHECK(e && m && kv && sampled_out, SH_ERR_ARG, "sh_verify_greedy: NULL argument");
   SH_CHECK(L >= 1 && L <= 64, SH_ERR_ARG, "verify length %u outside [1, 64]", L);
+  if (L <= 8 && graphs_enabled(e)) {
+    SH_CHECK(tokens, SH_ERR_ARG, "tokens is NULL");
+    for (uint32_t i = 0; i < L; ++i)
+      SH_CHECK(tokens[i] < m->V, SH_ERR_ARG, "token id %u out of range (vocab %u)", tokens[i], m->V);
+    SH_CHECK(kv->pos == pos, SH_ERR_STATE, "cache.position %u doesn't match caller-supplied position_offset %u",
+             kv->pos, pos);
+    SH_CHECK((uint64_t)pos + L <= kv->max_seq, SH_ERR_CAPACITY, "positions [%u, %u) exceed KV capacity %u", pos,
+             pos + L, kv->max_seq);
+    SH_CHECK(kv->n_layer == m->n_layer && kv->n_kv == m->n_kv && kv->hd == m->hd, SH_ERR_ARG,
+             "KV cache dims do not match the model");
+    return verify_greedy_graph(e, m, kv, tokens, L, pos, sampled_out);
+  }
   uint32_t* dt = nullptr;
   int rc = upload_tokens(m, tokens, L, &dt);
   if (rc) return rc;
@@ -1219,24 +1299,17 @@ extern "C" int sh_tree_verify_step(sh_engine* e, sh_model* target, sh_kv* const*
 
 // ------------------------------------------------------------------ spec step
 
-struct SpecBufs {
-  uint32_t* tok = nullptr;     // [64]: pending..., last, d_1..d_n
-  uint32_t* samp = nullptr;    // [16]
-  float* dlogits = nullptr;    // draft logits [8][V] (REJECTION)
-  float* tlogits = nullptr;    // target logits [9][V]
-  uint32_t* pinned = nullptr;  // host staging [128]
-  uint32_t vcap = 0;
-};
-static thread_local SpecBufs g_spec;
 
 static int spec_bufs(uint32_t V) {
   if (g_spec.tok && g_spec.vcap >= V) return SH_OK;
   if (g_spec.tok) {
-    (void)hipFree(g_spec.tok); (void)hipFree(g_spec.samp); (void)hipFree(g_spec.dlogits);
+    g_graph_gen.fetch_add(1);  // captured graphs point into these buffers
+    (void)hipFree(g_spec.tok); (void)hipFree(g_spec.samp); (void)hipFree(g_spec.base); (void)hipFree(g_spec.dlogits);
     (void)hipFree(g_spec.tlogits); (void)hipHostFree(g_spec.pinned);
   }
   SH_HIP(hipMalloc(&g_spec.tok, 64 * 4));
   SH_HIP(hipMalloc(&g_spec.samp, 16 * 4));
+  SH_HIP(hipMalloc(&g_spec.base, 4 * 4));
   SH_HIP(hipMalloc(&g_spec.dlogits, (size_t)8 * V * 4));
   SH_HIP(hipMalloc(&g_spec.tlogits, (size_t)9 * V * 4));
   SH_HIP(hipHostMalloc((void**)&g_spec.pinned, 128 * 4, hipHostMallocDefault));
@@ -1247,6 +1320,96 @@ static int spec_bufs(uint32_t V) {
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts,
                      uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter,
                      const float* uniforms_dev, uint32_t* acc_len, uint32_t* next_tok);
+
+// ------------------------------------------------------------------ graph replay
+
+// Greedy spec steps and greedy verifies replay a captured HIP graph. While one
+// is captured, each cache's sh_kv::graph_base points at a device base position and every
+// position-dependent kernel argument (RoPE position, KV slot, live keys, mask
+// base) is an offset from it, so one capture serves every position; the host
+// writes the base values before each replay. A capture is keyed by its shape,
+// models and caches, and all captures are dropped when a model or cache is
+// destroyed. SH_GRAPH=0 turns replay off; profiling runs eagerly.
+struct GraphEntry {
+  uint64_t gen = 0;
+  std::vector<uintptr_t> key;
+  hipGraphExec_t exec = nullptr;
+};
+static thread_local std::vector<GraphEntry> g_graphs;
+
+static bool graphs_enabled(const sh_engine* e) {
+  static const bool on = [] {
+    const char* s = getenv("SH_GRAPH");
+    return !(s && std::string(s) == "0");
+  }();
+  return on && !e->profiling;
+}
+
+static hipGraphExec_t graph_find(const std::vector<uintptr_t>& key) {
+  const uint64_t gen = g_graph_gen.load();
+  for (size_t i = 0; i < g_graphs.size();) {
+    if (g_graphs[i].gen != gen) {  // a model or cache it used may be gone
+      (void)hipGraphExecDestroy(g_graphs[i].exec);
+      g_graphs.erase(g_graphs.begin() + i);
+      continue;
+    }
+    if (g_graphs[i].key == key) return g_graphs[i].exec;
+    ++i;
+  }
+  return nullptr;
+}
+
+// Captures body() on the engine stream (cache kvs[i] gets graph_base =
+// bases[i] meanwhile) and caches the instantiated graph under key.
+static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const std::vector<sh_kv*>& kvs,
+                         const std::vector<const uint32_t*>& bases, const std::function<int()>& body,
+                         hipGraphExec_t* out) {
+  SH_HIP(hipStreamSynchronize(e->stream));
+  SH_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  for (size_t i = 0; i < kvs.size(); ++i) kvs[i]->graph_base = bases[i];
+  int rc = body();
+  for (sh_kv* kv : kvs) kv->graph_base = nullptr;
+  hipGraph_t g = nullptr;
+  const hipError_t ce = hipStreamEndCapture(e->stream, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  SH_CHECK(ce == hipSuccess && g, SH_ERR_HIP, "graph capture: %s", hipGetErrorString(ce));
+  hipGraphExec_t ex = nullptr;
+  const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  SH_CHECK(ie == hipSuccess, SH_ERR_HIP, "graph instantiate: %s", hipGetErrorString(ie));
+  GraphEntry ge;
+  ge.gen = g_graph_gen.load();
+  ge.key = key;
+  ge.exec = ex;
+  g_graphs.push_back(ge);
+  *out = ex;
+  return SH_OK;
+}
+
+// Draft n tokens greedily and verify [last, d_1..d_n] (greedy): draft forwards
+// at dpos (catch-up of np + 1 tokens) and dpos + np + i, the verify at tpos;
+// drafts and per-column argmax ids are copied to the pinned staging buffer.
+static int enqueue_greedy_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t n,
+                               uint32_t np, uint32_t dpos, uint32_t tpos) {
+  int rc = forward_dev(dm, dkv, g_spec.tok, np + 1, dpos, nullptr, 1, nullptr, nullptr, nullptr);
+  if (rc) return rc;
+  if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)np * dm->V, dm->V, 1, dm->ws.amax, g_spec.tok + np + 1)))
+    return rc;
+  for (uint32_t i = 1; i < n; ++i) {
+    if ((rc = forward_dev(dm, dkv, g_spec.tok + np + i, 1, dpos + np + i, nullptr, 1, nullptr, nullptr, nullptr)))
+      return rc;
+    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, g_spec.tok + np + 1 + i))) return rc;
+  }
+  if ((rc = forward_dev(tm, tkv, g_spec.tok + np, n + 1, tpos, nullptr, 2, nullptr, nullptr, nullptr))) return rc;
+  if ((rc = sh_argmax_launch(e, tm->ws.logits, tm->V, n + 1, tm->ws.amax, g_spec.samp))) return rc;
+  uint32_t* hp = g_spec.pinned;
+  SH_HIP(hipMemcpyAsync(hp, g_spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
+  SH_HIP(hipMemcpyAsync(hp + 16, g_spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+  return SH_OK;
+}
 
 extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t last_token,
                             uint32_t n_max, sh_sampling* s, uint32_t* emitted_out, uint32_t* n_emitted,
@@ -1271,8 +1434,34 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
   hp[np] = last_token;
   SH_HIP(hipMemcpyAsync(g_spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
+  const bool greedy_graph = mode == SH_SAMPLE_GREEDY && n + 1 <= 8 && graphs_enabled(e);
+  if (mode == SH_SAMPLE_GREEDY) {
+    const uint32_t d0 = dkv->pos;
+    if (greedy_graph) {
+      const std::vector<uintptr_t> key = {1, (uintptr_t)tm, (uintptr_t)dm, (uintptr_t)tkv, (uintptr_t)dkv,
+                                          (uintptr_t)tkv->k, (uintptr_t)dkv->k, tkv->max_seq, dkv->max_seq, n, np};
+      hipGraphExec_t ex = graph_find(key);
+      if (!ex) {
+        if ((rc = ensure_rope(tm, tkv->max_seq)) || (rc = ensure_rope(dm, dkv->max_seq)) ||
+            (rc = ensure_fa_part(tm, tkv->max_seq)) || (rc = ensure_fa_part(dm, dkv->max_seq)))
+          return rc;
+        rc = graph_capture(e, key, {dkv, tkv}, {g_spec.base, g_spec.base + 1},
+                           [&] { return enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, 0, 0); }, &ex);
+        if (rc) return rc;
+      }
+      hp[64] = d0;
+      hp[65] = P;
+      SH_HIP(hipMemcpyAsync(g_spec.base, hp + 64, 8, hipMemcpyHostToDevice, e->stream));
+      SH_HIP(hipGraphLaunch(ex, e->stream));
+      dkv->pos = d0 + np + n;  // what the eager forwards leave
+      tkv->pos = P + n + 1;
+    } else if ((rc = enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, d0, P))) {
+      return rc;
+    }
+  }
   // 1. draft n tokens greedily, ids stay on the device (tok[np+1+i] = d_{i+1}).
   const bool rej = mode == SH_SAMPLE_REJECTION;
+  if (mode != SH_SAMPLE_GREEDY) {
   rc = forward_dev(dm, dkv, g_spec.tok, np + 1, dkv->pos, nullptr, 1, rej ? g_spec.dlogits : nullptr, nullptr,
                    nullptr);
   if (rc) return rc;
@@ -1291,9 +1480,7 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   // 3. per-column decision on the device.
   uint32_t* acc_dev = g_spec.samp + 9;
   uint32_t* next_dev = g_spec.samp + 10;
-  if (mode == SH_SAMPLE_GREEDY) {
-    if ((rc = sh_argmax_launch(e, g_spec.tlogits, tm->V, n + 1, tm->ws.amax, g_spec.samp))) return rc;
-  } else {
+  {
     sh_sampling ss = *s;
     float* udev = nullptr;
     if (s->uniforms) {
@@ -1308,6 +1495,7 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   }
   SH_HIP(hipMemcpyAsync(hp, g_spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
   SH_HIP(hipMemcpyAsync(hp + 16, g_spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+  }
   SH_HIP(hipStreamSynchronize(e->stream));
   uint32_t drafts[8];
   for (uint32_t i = 0; i < n; ++i) drafts[i] = hp[i];

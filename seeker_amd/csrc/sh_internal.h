@@ -135,6 +135,10 @@ struct sh_kv {
   uint16_t* k = nullptr;  // [layer][n_kv][max_seq][hd] f16
   uint16_t* v = nullptr;  // [layer][n_kv][max_seq/32][hd][32] f16, slot-permuted
   std::vector<uint32_t> pending;  // committed tokens not yet in this cache
+  // Set only while a graph is being captured: forward positions in this cache
+  // are offsets from the device value *graph_base (read by the kernels at
+  // replay), and the host neither checks nor advances the position.
+  const uint32_t* graph_base = nullptr;
 };
 
 // ------------------------------------------------------------ launchers
@@ -172,6 +176,8 @@ struct EpiArgs {
   uint32_t mseq[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   uint16_t* kc[8] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   uint16_t* vc[8] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  // Graph replay: colpos and slot are offsets from the device value *dbase.
+  const uint32_t* dbase = nullptr;
 };
 // Launch y = W x for N <= 8 columns; with EPI_PART, *nparts receives the
 // number of split partials written (1 for the other epilogues).
@@ -232,6 +238,10 @@ struct FaArgs {
   uint32_t mask_base = 0;  // keys >= mask_base need their bit in colmask
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const uint64_t* masks = nullptr;  // device masks per column (N up to SH_MAX_COLS); null: colmask (N <= 8)
+  // Graph replay: kvlen and mask_base are offsets from the device value *dbase,
+  // the split grid covers kv_cap keys and splits past the live keys exit.
+  const uint32_t* dbase = nullptr;
+  uint32_t kv_cap = 0;
 };
 // Attention for the chunk's columns, then the split combine, which writes
 // attn_out [N][n_embd] f32 and the Wo activation operand (bx, xs, per-superblock cs).
