@@ -274,51 +274,13 @@ __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ par
                                                    uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
                                                    float* __restrict__ cs, const uint32_t* dbase, uint32_t kv_off,
                                                    uint32_t split_keys) {
-  constexpr uint32_t PS = sh_fa_part_stride(HD);
-  constexpr uint32_t CH = 16;
   // n_layout splits per kv head in the partial buffer; with dbase (graph
   // replay) only those holding live keys are read
   const uint32_t n_splits = dbase ? (*dbase + kv_off + split_keys - 1) / split_keys : n_layout;
   const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
-  const uint32_t Dq = n_head * HD;
-  const size_t sstride = (size_t)n_rows_pad * PS;
-  const uint32_t kk = 256 * sb + 4 * lane;
-  const bool valid = kk < Dq;
-  const uint32_t k = valid ? kk : 0, head = k / HD, d = k % HD;
-  const uint32_t kh = head / gqa, rho = (head % gqa) * N + col;
-  const float* p = part + (size_t)kh * n_layout * sstride + (size_t)rho * PS;
-  float M = -INFINITY, L = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t s0 = 0; s0 < n_splits; s0 += CH) {
-    float4 os[CH];
-    float2 ml[CH];
-#pragma unroll
-    for (uint32_t j = 0; j < CH; ++j) {
-      const float* pp = p + (size_t)min(s0 + j, n_splits - 1) * sstride;
-      os[j] = *(const float4*)(pp + d);
-      ml[j] = *(const float2*)(pp + HD);
-    }
-    float mc = -INFINITY;
-#pragma unroll
-    for (uint32_t j = 0; j < CH; ++j) mc = fmaxf(mc, ml[j].x);  // repeats of the last split change nothing
-    if (mc == -INFINITY) continue;
-    const float mn = fmaxf(M, mc);
-    const float a = expf(M - mn);  // 0 on the first chunk (M = -inf)
-    acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
-    L *= a;
-#pragma unroll
-    for (uint32_t j = 0; j < CH; ++j) {
-      // 0 for an empty split (m = -inf) and for the clamped repeats past the end
-      const float w = s0 + j < n_splits ? expf(ml[j].x - mn) : 0.0f;
-      acc.x += os[j].x * w; acc.y += os[j].y * w; acc.z += os[j].z * w; acc.w += os[j].w * w;
-      L += ml[j].y * w;
-    }
-    M = mn;
-  }
-  const float il = L > 0.f ? 1.0f / L : 0.f;
-  float4 v = make_float4(acc.x * il, acc.y * il, acc.z * il, acc.w * il);
-  if (valid) *(float4*)(attn + (size_t)(col0 + col) * Dq + k) = v;
-  else v = make_float4(0.f, 0.f, 0.f, 0.f);
+  const uint32_t Dq = n_head * HD, k = 256 * sb + 4 * lane;
+  const float4 v = sh_fa_combine4(part, n_layout, n_splits, n_rows_pad, HD, n_head, gqa, N, sb, col);
+  if (k < Dq) *(float4*)(attn + (size_t)(col0 + col) * Dq + k) = v;
   sh_operand_store_sb(v, Dq, sb, col0 + col, bx, xs, cs);
 }
 
@@ -357,7 +319,7 @@ static void fa_launch_cfg(uint32_t split_keys, dim3 grid, hipStream_t st, const 
 }
 
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
-                 float* attn_out, uint16_t* bx, uint16_t* xs, float* cs) {
+                 float* attn_out, uint16_t* bx, uint16_t* xs, float* cs, OpndSrc* combine_out) {
   const uint32_t gqa = m->n_head / m->n_kv;
   const uint32_t n_rows = gqa * fa.N;
   const int NQG = n_rows > 16 ? 2 : 1;
@@ -397,6 +359,13 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   SH_HIP(hipGetLastError());
   const double kv_bytes = 2.0 * m->n_kv * (double)kv_grid * m->hd * 2.0;
   sh_prof_end(e, "attention", kv_bytes, ev);
+  if (combine_out) {
+    SH_CHECK(fa.col0 == 0, SH_ERR_ARG, "attention: a deferred combine needs the chunk's first column");
+    OpndSrc& o = *combine_out;
+    o.kind = OPND_FA; o.fa_part = part; o.n_layout = n_splits; o.rows_pad = rows_pad; o.n_head = m->n_head;
+    o.gqa = gqa; o.hd = m->hd; o.split_keys = split_keys; o.kv_off = fa.kvlen; o.dbase = fa.dbase;
+    return SH_OK;
+  }
   sh_prof_begin(e, &ev);
   const dim3 cgrid((m->n_head * m->hd + 255) / 256, fa.N);
   if (m->hd == 128)

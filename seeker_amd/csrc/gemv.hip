@@ -25,6 +25,7 @@
 #include <string>
 
 #include "sh_internal.h"
+#include "sh_operand.h"
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -318,11 +319,16 @@ constexpr int WV = 8;
 constexpr uint32_t WIDE_MAX_SB = 7;      // superblocks per split held in LDS (63 KB)
 constexpr uint32_t WIDE_MAX_UNITS = 12;  // units per wave (T * S) beyond which registers spill
 
-template <int T, int S, int D, int EPI>
+// With SRC != OPND_STAGED the split's operand is built in LDS by the waves
+// (one wave per (superblock, column)): from f32 rows (OPND_ROWS) or by
+// combining attention split partials (OPND_FA), with the same arithmetic as
+// the prep / combine kernels; the first weight units are already in flight.
+template <int T, int S, int D, int EPI, int SRC>
 __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
                                                        const uint16_t* __restrict__ Bx,
                                                        const uint16_t* __restrict__ XS,
-                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea) {
+                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea,
+                                                       OpndSrc src) {
   constexpr int U = S * T;
   __shared__ h8 sB[S * 9 * 64];
   __shared__ float sC[64];
@@ -333,20 +339,26 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
   const uint32_t tile0 = (blockIdx.x * WV + wave) * T;
   const float nf = col_rinv(ea, r & 7);
 
-  // Activation operand of the split -> LDS: 1 KB blocks i = 9 * sb + m (m < 8:
-  // B sub-block m, m = 8: XS), one wave instruction each.
+  if (SRC == OPND_STAGED) {
+    // Activation operand of the split -> LDS: 1 KB blocks i = 9 * sb + m (m < 8:
+    // B sub-block m, m = 8: XS), one wave instruction each.
 #pragma unroll
-  for (int i0 = 0; i0 < S * 9; i0 += WV) {
-    const uint32_t i = i0 + wave;
-    if (i < (uint32_t)(S * 9)) {
-      const uint32_t sb = kb0 + i / 9, m = i % 9;
-      const uint16_t* src = m < 8 ? Bx + ((size_t)(sb * 8 + m) * 64 + lane) * 8 : XS + ((size_t)sb * 64 + lane) * 8;
-      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(sB + i * 64), 16, 0, 0);
+    for (int i0 = 0; i0 < S * 9; i0 += WV) {
+      const uint32_t i = i0 + wave;
+      if (i < (uint32_t)(S * 9)) {
+        const uint32_t sb = kb0 + i / 9, m = i % 9;
+        const uint16_t* src_p = m < 8 ? Bx + ((size_t)(sb * 8 + m) * 64 + lane) * 8 : XS + ((size_t)sb * 64 + lane) * 8;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)src_p, (lds_void_t*)(sB + i * 64), 16, 0, 0);
+      }
     }
-  }
-  if (wave == WV - 1) {  // the split's S * 8 scales (lanes past them repeat the last)
-    const uint32_t li = (uint32_t)lane < S * 8 ? lane : S * 8 - 1;
-    __builtin_amdgcn_global_load_lds((glb_void_t*)(CS + kb0 * 8 + li), (lds_void_t*)sC, 4, 0, 0);
+    if (wave == WV - 1) {  // the split's S * 8 scales (lanes past them repeat the last)
+      const uint32_t li = (uint32_t)lane < S * 8 ? lane : S * 8 - 1;
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(CS + kb0 * 8 + li), (lds_void_t*)sC, 4, 0, 0);
+    }
+  } else {
+    // zero first: XS lanes >= 16 must be 0, and unused columns stay finite
+    const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t i = threadIdx.x; i < (uint32_t)(S * 9 * 64); i += 64 * WV) sB[i] = z;
   }
 
   // Unit u = (superblock u / T, tile u % T); tiles past the end read the last
@@ -359,6 +371,50 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
   Q4Tile ring[D];
 #pragma unroll
   for (int k = 0; k < D && k < U; ++k) ring[k] = load_q4_tile(unit_ptr(k), lane, g, r);
+
+  if (SRC != OPND_STAGED) {
+    __syncthreads();  // zero fill done
+    const uint32_t K = nsb * 256;
+    const uint32_t n_live = SRC == OPND_FA && src.dbase
+                                ? (*src.dbase + src.kv_off + src.split_keys - 1) / src.split_keys
+                                : src.n_layout;
+    // wave-uniform tasks t = wave + WV i; rows are all loaded before any is used
+    constexpr int MAXT = (S * 8 + WV - 1) / WV;
+    float4 vv[MAXT];
+    if (SRC == OPND_ROWS) {
+#pragma unroll
+      for (int i = 0; i < MAXT; ++i) {
+        const uint32_t t = wave + WV * i;
+        if (t < (uint32_t)S * N) {
+          const uint32_t sb = kb0 + t / N, col = t % N;
+          vv[i] = *(const float4*)(src.x + (size_t)col * src.ldx + 256 * sb + 4 * lane);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const uint32_t t = wave + WV * i;
+      if (t >= (uint32_t)S * N) break;
+      const uint32_t sbl = t / N, col = t % N, sb = kb0 + sbl;
+      const float4 v = SRC == OPND_ROWS ? vv[i]
+                                        : sh_fa_combine4(src.fa_part, src.n_layout, n_live, src.rows_pad, src.hd,
+                                                         src.n_head, src.gqa, N, sb, col);
+      const ShOpndLane o = sh_operand_lane(v);
+      if (lane == 0) sC[sbl * 8 + col] = o.inv;
+      const uint32_t k = 256 * sb + 4 * lane;
+      if (k < K) {
+        const uint32_t m = (k % 256) / 32;
+        uint16_t* dst = (uint16_t*)(sB + (sbl * 9 + m) * 64 + ((k % 32) / 8) * 16 + col) + (k % 8);
+        *(uint2*)dst = o.hi;
+        *(uint2*)(dst + 64) = o.lo;
+        if ((lane & 7) == 0) {
+          uint16_t* xd = (uint16_t*)(sB + (sbl * 9 + 8) * 64 + col) + m;
+          xd[0] = o.shi;
+          xd[64] = o.slo;
+        }
+      }
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);  // the LDS copies (and the first weight units) have landed
   __syncthreads();
 
@@ -919,37 +975,44 @@ static uint32_t gemv_d_override() {
   return v;
 }
 // D = weight units in flight per wave (SH_GEMV_D=2|4|8; default 4).
-template <int T, int S, int EPI>
-static void launch_q4w_s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                         const EpiArgs& ea, const WidePlan& p) {
+template <int T, int S, int EPI, int SRC>
+static void launch_q4w_src(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                           const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
   const dim3 grid((w.tiles + WV * T - 1) / (WV * T), p.KS);
   const uint32_t d = gemv_d_override();
   if (d == 2)
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 2, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
-                       xs, ea.cs, N, ea);
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 2, EPI, SRC>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256,
+                       bx, xs, ea.cs, N, ea, src);
   else if (d == 8)
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 8, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
-                       xs, ea.cs, N, ea);
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 8, EPI, SRC>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256,
+                       bx, xs, ea.cs, N, ea, src);
   else
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 4, EPI>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256, bx,
-                       xs, ea.cs, N, ea);
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 4, EPI, SRC>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256,
+                       bx, xs, ea.cs, N, ea, src);
+}
+template <int T, int S, int EPI>
+static void launch_q4w_s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                         const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
+  if (src.kind == OPND_ROWS) launch_q4w_src<T, S, EPI, OPND_ROWS>(e, w, bx, xs, N, ea, p, src);
+  else if (src.kind == OPND_FA) launch_q4w_src<T, S, EPI, OPND_FA>(e, w, bx, xs, N, ea, p, src);
+  else launch_q4w_src<T, S, EPI, OPND_STAGED>(e, w, bx, xs, N, ea, p, src);
 }
 template <int T, int S, int EPI>
 static void launch_q4w_if(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                          const EpiArgs& ea, const WidePlan& p) {
-  if constexpr (T * S <= (int)WIDE_MAX_UNITS) launch_q4w_s<T, S, EPI>(e, w, bx, xs, N, ea, p);
+                          const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
+  if constexpr (T * S <= (int)WIDE_MAX_UNITS) launch_q4w_s<T, S, EPI>(e, w, bx, xs, N, ea, p, src);
 }
 template <int T, int EPI>
 static void launch_q4w(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                       const EpiArgs& ea, const WidePlan& p) {
+                       const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
   switch (p.S) {
-    case 1: launch_q4w_if<T, 1, EPI>(e, w, bx, xs, N, ea, p); break;
-    case 2: launch_q4w_if<T, 2, EPI>(e, w, bx, xs, N, ea, p); break;
-    case 3: launch_q4w_if<T, 3, EPI>(e, w, bx, xs, N, ea, p); break;
-    case 4: launch_q4w_if<T, 4, EPI>(e, w, bx, xs, N, ea, p); break;
-    case 5: launch_q4w_if<T, 5, EPI>(e, w, bx, xs, N, ea, p); break;
-    case 6: launch_q4w_if<T, 6, EPI>(e, w, bx, xs, N, ea, p); break;
-    default: launch_q4w_if<T, 7, EPI>(e, w, bx, xs, N, ea, p); break;
+    case 1: launch_q4w_if<T, 1, EPI>(e, w, bx, xs, N, ea, p, src); break;
+    case 2: launch_q4w_if<T, 2, EPI>(e, w, bx, xs, N, ea, p, src); break;
+    case 3: launch_q4w_if<T, 3, EPI>(e, w, bx, xs, N, ea, p, src); break;
+    case 4: launch_q4w_if<T, 4, EPI>(e, w, bx, xs, N, ea, p, src); break;
+    case 5: launch_q4w_if<T, 5, EPI>(e, w, bx, xs, N, ea, p, src); break;
+    case 6: launch_q4w_if<T, 6, EPI>(e, w, bx, xs, N, ea, p, src); break;
+    default: launch_q4w_if<T, 7, EPI>(e, w, bx, xs, N, ea, p, src); break;
   }
 }
 
@@ -994,22 +1057,31 @@ static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_
   else launch_q8<1, 4, EPI>(e, w, bx, N, ea);
 }
 
+uint32_t sh_gemv_fusable(const QMat& w) {
+  WidePlan p;
+  return wide_plan(w, &p) ? p.S : 0;
+}
+
 int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N, EpiKind epi,
-                   const EpiArgs& ea, const char* tag, uint32_t* nparts) {
+                   const EpiArgs& ea, const char* tag, uint32_t* nparts, const OpndSrc* src) {
   SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "gemv chunk N=%u outside [1,8]", N);
   SH_CHECK(ea.cs, SH_ERR_ARG, "gemv: activation scales missing");
+  const OpndSrc staged;
+  const OpndSrc& sr = src ? *src : staged;
   uint32_t np = 1;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
+  WidePlan p;
+  SH_CHECK(sr.kind == OPND_STAGED || (epi == EPI_PART && w.type == GGML_Q4_K && wide_plan(w, &p)),
+           SH_ERR_ARG, "gemv: a built operand needs the split-K kernel");
   if (w.type == GGML_Q4_K) {
-    WidePlan p;
     if (epi == EPI_PART && wide_plan(w, &p)) {
       SH_CHECK(ea.part_cap >= p.KS, SH_ERR_CAPACITY, "gemv: %u split partials exceed the buffer (%u)", p.KS,
                ea.part_cap);
       np = p.KS;
-      if (p.T == 1) launch_q4w<1, EPI_PART>(e, w, bx, xs, N, ea, p);
-      else if (p.T == 2) launch_q4w<2, EPI_PART>(e, w, bx, xs, N, ea, p);
-      else launch_q4w<4, EPI_PART>(e, w, bx, xs, N, ea, p);
+      if (p.T == 1) launch_q4w<1, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
+      else if (p.T == 2) launch_q4w<2, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
+      else launch_q4w<4, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
     } else {
       switch (epi) {
         case EPI_STORE: dispatch_q4s<EPI_STORE>(e, w, bx, xs, N, ea); break;

@@ -669,11 +669,29 @@ struct FaSeg {
   const uint64_t* masks = nullptr;  // device masks of the ncol columns (required above 8 columns)
 };
 
+// SH_FUSE=0 keeps the separate down prep and attention combine kernels.
+static bool fusion_enabled() {
+  static const bool v = [] {
+    const char* s = getenv("SH_FUSE");
+    return !(s && std::string(s) == "0");
+  }();
+  return v;
+}
+
 static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
                          const std::vector<FaSeg>& segs, bool want_logits, bool want_resid) {
   sh_engine* e = m->e;
   Workspace& w = m->ws;
   int rc;
+  // For chunks of at most 2 columns (the draft's single-token forwards) the
+  // down GEMV builds its operand from h and Wo combines the attention splits
+  // itself, when they take the split-K kernel: two fewer kernels per layer.
+  // Every row-group workgroup of a split builds that split's operand, which
+  // outweighs the saved launch once there are 8 columns (measured).
+  const bool fuse = fusion_enabled() && nc <= 2;
+  const uint32_t s_wo = m->layers.empty() ? 0 : sh_gemv_fusable(m->layers[0].wo);
+  const bool fuse_wo = s_wo && s_wo * nc <= 8;
+  const bool fuse_down = !m->layers.empty() && sh_gemv_fusable(m->layers[0].wdown) != 0;
   if ((rc = sh_embed_launch(e, m, dev_tokens, nc, w.resid))) return rc;
   const uint32_t dkv = m->hd * m->n_kv;
   EpiArgs qkv;
@@ -718,6 +736,9 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     if ((rc = resid_prep(L.attn_norm))) return rc;
     qkv.layer = l;
     if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
+    // one segment covering the chunk: Wo combines the attention splits itself
+    const bool fuse_o = fuse && segs.size() == 1 && segs[0].col0 == 0 && segs[0].ncol == nc && fuse_wo;
+    OpndSrc osrc;
     for (const FaSeg& sg : segs) {
       FaArgs fa;
       fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
@@ -725,16 +746,20 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       fa.masks = sg.masks;
       fa.dbase = sg.kv->graph_base;
       fa.kv_cap = sg.kv->max_seq;
-      if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
+      if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs, fuse_o ? &osrc : nullptr)))
+        return rc;
     }
     EpiArgs po = part_args(L.wo);
-    if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", &pending))) return rc;
+    if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", &pending, fuse_o ? &osrc : nullptr)))
+      return rc;
     pending_ld = po.ldo;
     if ((rc = resid_prep(L.ffn_norm))) return rc;
+    OpndSrc dsrc;  // down reads h itself when it takes the split-K kernel
     if (swiglu_epilogue()) {
       // whole sums in one kernel, h = silu(gate) * up in its epilogue
       if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
       pr.mode = PREP_PLAIN; pr.x = w.h; pr.nparts = 0;
+      if (fuse && fuse_down) { dsrc.kind = OPND_ROWS; dsrc.x = w.h; dsrc.ldx = m->ff; }
     } else {
       EpiArgs pg = part_args(L.wgu);
       set_norm(pg);
@@ -743,9 +768,11 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = ngu; pr.part_ld = pg.ldo;
     }
     pr.K = m->ff; pr.norm_w = nullptr;
-    if ((rc = sh_prep_launch(e, pr))) return rc;
+    if (dsrc.kind == OPND_STAGED && (rc = sh_prep_launch(e, pr))) return rc;
     EpiArgs pd = part_args(L.wdown);
-    if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", &pending))) return rc;
+    if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", &pending,
+                             dsrc.kind == OPND_STAGED ? nullptr : &dsrc)))
+      return rc;
     pending_ld = pd.ldo;
   }
   if (want_logits) {

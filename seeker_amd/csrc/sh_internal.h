@@ -179,10 +179,28 @@ struct EpiArgs {
   // Graph replay: colpos and slot are offsets from the device value *dbase.
   const uint32_t* dbase = nullptr;
 };
+// Where a split-K GEMV takes its activation operand from: the staged operand
+// (B/XS/cs, the default), f32 rows x [N][ldx] (the operand is built in LDS, as
+// the prep would build it, without a norm), or attention split partials (the
+// split combine is done in LDS, as k_fa_combine would do it).
+enum OpndKind { OPND_STAGED = 0, OPND_ROWS = 1, OPND_FA = 2 };
+struct OpndSrc {
+  int kind = OPND_STAGED;
+  const float* x = nullptr;  // OPND_ROWS
+  uint32_t ldx = 0;
+  const float* fa_part = nullptr;  // OPND_FA: partial layout of sh_fa_launch
+  uint32_t n_layout = 0, rows_pad = 0, n_head = 0, gqa = 0, hd = 0, split_keys = 0, kv_off = 0;
+  const uint32_t* dbase = nullptr;  // graph replay: live splits from *dbase + kv_off
+};
 // Launch y = W x for N <= 8 columns; with EPI_PART, *nparts receives the
-// number of split partials written (1 for the other epilogues).
+// number of split partials written (1 for the other epilogues). A non-staged
+// src needs the split-K kernel (sh_gemv_fusable).
 int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                   EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
+                   EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr,
+                   const OpndSrc* src = nullptr);
+// Superblocks per split when the EPI_PART launch of w takes the split-K kernel
+// (which accepts any OpndSrc), else 0.
+uint32_t sh_gemv_fusable(const QMat& w);
 // Floats of partial-sum buffer the EPI_PART launches of w need (all splits).
 size_t sh_gemv_part_floats(const QMat& w);
 // y = W x for N <= SH_MAX_COLS columns (operand groups of 8, Q4_K) in one pass
@@ -246,7 +264,9 @@ struct FaArgs {
 // Attention for the chunk's columns, then the split combine, which writes
 // attn_out [N][n_embd] f32 and the Wo activation operand (bx, xs, per-superblock cs).
 int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q, float* part,
-                 float* attn_out, uint16_t* bx, uint16_t* xs, float* cs);
+                 float* attn_out, uint16_t* bx, uint16_t* xs, float* cs, OpndSrc* combine_out = nullptr);
+// With combine_out, the combine kernel is skipped and *combine_out describes
+// the partials for a consumer that combines them itself (OPND_FA).
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids);
 int sh_kv_compact_launch(sh_engine* e, sh_kv* kv, uint32_t base, const uint32_t* src_dev, uint32_t n);

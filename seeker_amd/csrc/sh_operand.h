@@ -18,14 +18,58 @@ __host__ __device__ __forceinline__ size_t sh_grp_bx(uint32_t K) { return (size_
 __host__ __device__ __forceinline__ size_t sh_grp_xs(uint32_t K) { return (size_t)((K + 255) / 256) * 512; }
 __host__ __device__ __forceinline__ size_t sh_grp_cs(uint32_t K) { return (size_t)((K + 255) / 256) * 8; }
 
+// One lane's share of one 256-element superblock of one operand column, for
+// any destination: lane l holds y[256 sb + 4l .. +3]. The superblock is
+// multiplied by the power of two s that puts its max|y| in [2^9, 2^10) and
+// inv = 1/s, so the f16 low halves stay normal (an f16 subnormal has only
+// 2^-24 absolute resolution). hi/lo: the four elements as f16 hi + lo (elements
+// 2, 3 of every 4 carry an exact 1/16: the Q4_K kernels decode their nibbles as
+// 1024 + 16 q and the Q8_0 kernels their bytes as 16 q); shi/slo: the
+// 32-element sub-block sum of the lane's 8-lane group, valid in lanes l % 8 = 0.
+// Every lane of the wave must call this (it shuffles).
+struct ShOpndLane {
+  uint2 hi, lo;
+  uint16_t shi, slo;
+  float inv;
+};
+__device__ __forceinline__ ShOpndLane sh_operand_lane(float4 v) {
+  const float mx = sh_wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  int ex = 0;
+  if (mx > 0.f && mx < INFINITY) {
+    frexpf(mx, &ex);  // mx = m * 2^ex, m in [0.5, 1)
+    ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+  }
+  const float ps = ldexpf(1.0f, 10 - ex);
+  ShOpndLane o;
+  o.inv = ldexpf(1.0f, ex - 10);
+  const float y[4] = {v.x * ps, v.y * ps, v.z * ps, v.w * ps};
+  uint16_t hi[4], lo[4];
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float yt = t >= 2 ? y[t] * 0.0625f : y[t];
+    const _Float16 h = (_Float16)yt;
+    hi[t] = __builtin_bit_cast(uint16_t, h);
+    lo[t] = __builtin_bit_cast(uint16_t, (_Float16)(yt - (float)h));
+    sum += y[t];
+  }
+  // 8 consecutive lanes cover one 32-element sub-block
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  o.hi = *(const uint2*)hi;
+  o.lo = *(const uint2*)lo;
+  const _Float16 sh = (_Float16)sum;
+  o.shi = __builtin_bit_cast(uint16_t, sh);
+  o.slo = __builtin_bit_cast(uint16_t, (_Float16)(sum - (float)sh));
+  return o;
+}
+
 // One wave writes superblock sb (elements 256 sb .. 256 sb + 255) of column
-// `col` of the GEMV activation operand; lane l holds y[256 sb + 4l .. +3]
-// (zeros past K). The superblock is multiplied by the power of two s that puts
-// its max|y| in [2^9, 2^10) and cs[sb * 8 + col] = 1/s, so the f16 low halves
-// stay normal (an f16 subnormal has only 2^-24 absolute resolution). Layouts:
-// B (hi/lo f16, [K/32][64][8], lane 16g + c: hi of column c, lane 16g + 8 + c:
-// lo) and XS (per-32 sums, [K/256][64][8], lanes >= 16 stay zero). Every lane
-// of the wave must call this (it shuffles).
+// `col` of the GEMV activation operand in global memory (sh_operand_lane);
+// cs[sb * 8 + col] = 1/s. Layouts: B (hi/lo f16, [K/32][64][8], lane 16g + c:
+// hi of column c, lane 16g + 8 + c: lo) and XS (per-32 sums, [K/256][64][8],
+// lanes >= 16 stay zero). Every lane of the wave must call this.
 __device__ __forceinline__ void sh_operand_store_sb(float4 v, uint32_t K, uint32_t sb, uint32_t col,
                                                     uint16_t* __restrict__ bx, uint16_t* __restrict__ xs,
                                                     float* __restrict__ cs) {
@@ -37,42 +81,69 @@ __device__ __forceinline__ void sh_operand_store_sb(float4 v, uint32_t K, uint32
     cs += g * sh_grp_cs(K);
     col %= 8;
   }
-  const float mx = sh_wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-  int ex = 0;
-  if (mx > 0.f && mx < INFINITY) {
-    frexpf(mx, &ex);  // mx = m * 2^ex, m in [0.5, 1)
-    ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
-  }
-  const float ps = ldexpf(1.0f, 10 - ex);
-  if (lane == 0) cs[sb * 8 + col] = ldexpf(1.0f, ex - 10);
-  const float y[4] = {v.x * ps, v.y * ps, v.z * ps, v.w * ps};
-  uint16_t hi[4], lo[4];
-  float sum = 0.f;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    // elements 2, 3 of every 4 carry an exact 1/16: the Q4_K kernels decode
-    // their nibbles as 1024 + 16 q and the Q8_0 kernels their bytes as 16 q
-    const float yt = t >= 2 ? y[t] * 0.0625f : y[t];
-    const _Float16 h = (_Float16)yt;
-    hi[t] = __builtin_bit_cast(uint16_t, h);
-    lo[t] = __builtin_bit_cast(uint16_t, (_Float16)(yt - (float)h));
-    sum += y[t];
-  }
-  // 8 consecutive lanes cover one 32-element sub-block
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
-  sum += __shfl_xor(sum, 4);
+  const ShOpndLane o = sh_operand_lane(v);
+  if (lane == 0) cs[sb * 8 + col] = o.inv;
   const uint32_t k = 256 * sb + 4 * lane;
   if (k < K) {
     uint16_t* dst = bx + ((size_t)(k / 32) * 64 + ((k % 32) / 8) * 16 + col) * 8 + (k % 8);
-    *(uint2*)dst = *(const uint2*)hi;
-    *(uint2*)(dst + 64) = *(const uint2*)lo;
+    *(uint2*)dst = o.hi;
+    *(uint2*)(dst + 64) = o.lo;
     if ((lane & 7) == 0) {
       const uint32_t s = (k % 256) / 32;
-      const _Float16 sh = (_Float16)sum;
       const size_t xo = ((size_t)sb * 64 + col) * 8 + s;
-      xs[xo] = __builtin_bit_cast(uint16_t, sh);
-      xs[xo + 64] = __builtin_bit_cast(uint16_t, (_Float16)(sum - (float)sh));
+      xs[xo] = o.shi;
+      xs[xo + 64] = o.slo;
     }
   }
+}
+
+// Attention split combine for one lane: output elements 256 sb + 4 lane .. +3
+// of column col (a 256-wide superblock of heads), merging the n_splits key
+// splits of the partial buffer in split order, 16 at a time (every load issued
+// before the first is used, one exp per split). Partial layout:
+// part[((kh * n_layout + split) * rows_pad + rho) * (hd + 4) + {d < hd: O, hd: m,
+// hd + 1: l}], rho = (head % gqa) * N + col. Zero for elements past Dq.
+__device__ __forceinline__ float4 sh_fa_combine4(const float* __restrict__ part, uint32_t n_layout, uint32_t n_splits,
+                                                 uint32_t rows_pad, uint32_t hd, uint32_t n_head, uint32_t gqa,
+                                                 uint32_t N, uint32_t sb, uint32_t col) {
+  constexpr uint32_t CH = 16;
+  const uint32_t lane = threadIdx.x & 63, PS = hd + 4;
+  const uint32_t Dq = n_head * hd;
+  const size_t sstride = (size_t)rows_pad * PS;
+  const uint32_t kk = 256 * sb + 4 * lane;
+  const bool valid = kk < Dq;
+  const uint32_t k = valid ? kk : 0, head = k / hd, d = k % hd;
+  const uint32_t kh = head / gqa, rho = (head % gqa) * N + col;
+  const float* p = part + (size_t)kh * n_layout * sstride + (size_t)rho * PS;
+  float M = -INFINITY, L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t s0 = 0; s0 < n_splits; s0 += CH) {
+    float4 os[CH];
+    float2 ml[CH];
+#pragma unroll
+    for (uint32_t j = 0; j < CH; ++j) {
+      const float* pp = p + (size_t)min(s0 + j, n_splits - 1) * sstride;
+      os[j] = *(const float4*)(pp + d);
+      ml[j] = *(const float2*)(pp + hd);
+    }
+    float mc = -INFINITY;
+#pragma unroll
+    for (uint32_t j = 0; j < CH; ++j) mc = fmaxf(mc, ml[j].x);  // repeats of the last split change nothing
+    if (mc == -INFINITY) continue;
+    const float mn = fmaxf(M, mc);
+    const float a = expf(M - mn);  // 0 on the first chunk (M = -inf)
+    acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
+    L *= a;
+#pragma unroll
+    for (uint32_t j = 0; j < CH; ++j) {
+      // 0 for an empty split (m = -inf) and for the clamped repeats past the end
+      const float w = s0 + j < n_splits ? expf(ml[j].x - mn) : 0.0f;
+      acc.x += os[j].x * w; acc.y += os[j].y * w; acc.z += os[j].z * w; acc.w += os[j].w * w;
+      L += ml[j].y * w;
+    }
+    M = mn;
+  }
+  const float il = L > 0.f ? 1.0f / L : 0.f;
+  if (!valid) return make_float4(0.f, 0.f, 0.f, 0.f);
+  return make_float4(acc.x * il, acc.y * il, acc.z * il, acc.w * il);
 }
