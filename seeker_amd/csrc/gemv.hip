@@ -466,18 +466,38 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
 // flight while the current one computes. The 8 partial sums of each tile meet
 // in LDS at the end; no state is shared between workgroups.
 constexpr int GW = 8;
-template <int T, int EPI>
+
+// acc + p[0] + p[stride] + ... (n terms, in order), 8 loads in flight.
+__device__ __forceinline__ float4 sum_parts4(const float* p, size_t stride, uint32_t n, float4 acc) {
+  for (uint32_t i0 = 0; i0 < n; i0 += 8) {
+    float4 t[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) t[j] = *(const float4*)(p + min(i0 + j, n - 1) * stride);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      if (i0 + j < n) { acc.x += t[j].x; acc.y += t[j].y; acc.z += t[j].z; acc.w += t[j].w; }
+  }
+  return acc;
+}
+
+// SRC = OPND_RESID: before the first superblock, every workgroup builds the
+// whole operand in dynamic LDS ([nsb][9][64] h8, then nsb * 8 scales and
+// nsb * 8 sums of squares) from the residual and the pending split partials,
+// with the prep's arithmetic, and applies the RMS factor itself.
+template <int T, int EPI, int SRC>
 __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
                                                        const uint16_t* __restrict__ Bx,
                                                        const uint16_t* __restrict__ XS,
-                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea) {
+                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea,
+                                                       OpndSrc src) {
   constexpr int CH = T < 4 ? T : 4;  // tiles reduced per LDS round
   __shared__ f4 red[CH][GW][64];
+  extern __shared__ h8 dynB[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar address math
   const int g = lane >> 4, r = lane & 15;
   const uint32_t tile0 = blockIdx.x * T;
-  const float nf = col_rinv(ea, r & 7);
+  float nf = SRC == OPND_RESID ? 1.0f : col_rinv(ea, r & 7);
   f4 y[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
@@ -492,13 +512,56 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
   Q4Tile st[2];
   h8 bq[8], bm;
   float c = 0.f;
+  float* sC = (float*)(dynB + (size_t)nsb * 9 * 64);
+  float* sQ = sC + nsb * 8;
   auto load_b = [&](uint32_t b) {
+    if (SRC == OPND_RESID) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
-    bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
-    c = CS[b * 8 + (lane & 7)];
+      for (int m = 0; m < 8; ++m) bq[m] = dynB[(b * 9 + m) * 64 + lane];
+      bm = dynB[(b * 9 + 8) * 64 + lane];
+      c = sC[b * 8 + (lane & 7)];
+    } else {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
+      bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
+      c = CS[b * 8 + (lane & 7)];
+    }
   };
   if (nbw) st[0] = load_q4_tile(a_ptr(0, wave), lane, g, r);
+  if (SRC == OPND_RESID) {
+    const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t i = threadIdx.x; i < nsb * 9 * 64; i += 64 * GW) dynB[i] = z;
+    __syncthreads();
+    const uint32_t K = nsb * 256;
+    const size_t pstride = (size_t)8 * src.part_ld;
+    for (uint32_t t = wave; t < nsb * N; t += GW) {  // wave-uniform
+      const uint32_t sb = t / N, col = t % N, k = 256 * sb + 4 * lane;
+      float4 v = *(const float4*)(src.x + (size_t)col * K + k);
+      if (src.nparts) v = sum_parts4(src.part + (size_t)col * src.part_ld + k, pstride, src.nparts, v);
+      if (blockIdx.x == 0) *(float4*)(src.rout + (size_t)col * K + k) = v;
+      const float ss = sh_wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+      if (lane == 0) sQ[sb * 8 + col] = ss;
+      const float4 wv = *(const float4*)(src.norm_w + k);
+      v.x *= wv.x; v.y *= wv.y; v.z *= wv.z; v.w *= wv.w;
+      const ShOpndLane o = sh_operand_lane(v);
+      if (lane == 0) sC[sb * 8 + col] = o.inv;
+      const uint32_t m = (k % 256) / 32;
+      uint16_t* dst = (uint16_t*)(dynB + (sb * 9 + m) * 64 + ((k % 32) / 8) * 16 + col) + (k % 8);
+      *(uint2*)dst = o.hi;
+      *(uint2*)(dst + 64) = o.lo;
+      if ((lane & 7) == 0) {
+        uint16_t* xd = (uint16_t*)(dynB + (sb * 9 + 8) * 64 + col) + m;
+        xd[0] = o.shi;
+        xd[64] = o.slo;
+      }
+    }
+    __syncthreads();
+    // RMS factor of the lane's column from the superblock sums (added in superblock order)
+    const uint32_t cc = (uint32_t)(r & 7) < N ? (uint32_t)(r & 7) : 0u;
+    float tot = 0.f;
+    for (uint32_t b = 0; b < nsb; ++b) tot += sQ[b * 8 + cc];
+    nf = 1.0f / sqrtf(tot / (float)K + src.eps);
+  }
   for (uint32_t i = 0; i < nbw; i += 2) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -1016,12 +1079,19 @@ static void launch_q4w(sh_engine* e, const QMat& w, const uint16_t* bx, const ui
   }
 }
 
+// Dynamic LDS of the OPND_RESID build: the operand, its scales and sums of squares.
+static size_t resid_lds_bytes(uint32_t nsb) { return (size_t)nsb * 9 * 64 * 16 + (size_t)nsb * 8 * 4 * 2; }
+
 template <int T, int EPI>
 static void launch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                       const EpiArgs& ea) {
-  const uint32_t grid = (w.tiles + T - 1) / T;
-  hipLaunchKernelGGL((k_gemv_q4s<T, EPI>), dim3(grid), dim3(64 * GW), 0, e->stream, w.d, w.tiles, w.K / 256, bx, xs,
-                     ea.cs, N, ea);
+                       const EpiArgs& ea, const OpndSrc& src) {
+  const uint32_t grid = (w.tiles + T - 1) / T, nsb = w.K / 256;
+  if (src.kind == OPND_RESID)
+    hipLaunchKernelGGL((k_gemv_q4s<T, EPI, OPND_RESID>), dim3(grid), dim3(64 * GW), resid_lds_bytes(nsb), e->stream,
+                       w.d, w.tiles, nsb, bx, xs, ea.cs, N, ea, src);
+  else
+    hipLaunchKernelGGL((k_gemv_q4s<T, EPI, OPND_STAGED>), dim3(grid), dim3(64 * GW), 0, e->stream, w.d, w.tiles, nsb,
+                       bx, xs, ea.cs, N, ea, src);
 }
 
 // Streaming policy: about 512 workgroups of 8 waves (two per CU), i.e. T =
@@ -1029,7 +1099,7 @@ static void launch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const ui
 // workgroup owns whole gate/up pairs).
 template <int EPI>
 static void dispatch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                         const EpiArgs& ea) {
+                         const EpiArgs& ea, const OpndSrc& src) {
   uint32_t t = gemv_kernel_choice() == 1 ? gemv_t_override() : 0;
   if (!t) {
     t = 1;
@@ -1037,10 +1107,10 @@ static void dispatch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const 
   }
   if (EPI == EPI_SWIGLU && t < 2) t = 2;
   switch (t) {
-    case 1: launch_q4s<1, EPI>(e, w, bx, xs, N, ea); break;
-    case 2: launch_q4s<2, EPI>(e, w, bx, xs, N, ea); break;
-    case 4: launch_q4s<4, EPI>(e, w, bx, xs, N, ea); break;
-    default: launch_q4s<8, EPI>(e, w, bx, xs, N, ea); break;
+    case 1: launch_q4s<1, EPI>(e, w, bx, xs, N, ea, src); break;
+    case 2: launch_q4s<2, EPI>(e, w, bx, xs, N, ea, src); break;
+    case 4: launch_q4s<4, EPI>(e, w, bx, xs, N, ea, src); break;
+    default: launch_q4s<8, EPI>(e, w, bx, xs, N, ea, src); break;
   }
 }
 
@@ -1055,6 +1125,11 @@ static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_
   if (EPI == EPI_SWIGLU) launch_q8<2, 4, EPI>(e, w, bx, N, ea);
   else if (w.tiles >= 1024) launch_q8<2, 4, EPI>(e, w, bx, N, ea);
   else launch_q8<1, 4, EPI>(e, w, bx, N, ea);
+}
+
+bool sh_gemv_resid_fusable(const QMat& w, uint32_t N) {
+  // the whole-K kernel with its largest reduction buffer (4 tiles x 32 KB / 4) must fit beside the operand
+  return w.type == GGML_Q4_K && w.K % 256 == 0 && N <= 2 && resid_lds_bytes(w.K / 256) + 32768 <= 160 * 1024;
 }
 
 uint32_t sh_gemv_fusable(const QMat& w) {
@@ -1072,8 +1147,10 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   WidePlan p;
-  SH_CHECK(sr.kind == OPND_STAGED || (epi == EPI_PART && w.type == GGML_Q4_K && wide_plan(w, &p)),
-           SH_ERR_ARG, "gemv: a built operand needs the split-K kernel");
+  SH_CHECK(sr.kind == OPND_STAGED ||
+               (sr.kind == OPND_RESID ? (epi == EPI_QKV || epi == EPI_SWIGLU) && sh_gemv_resid_fusable(w, N)
+                                      : epi == EPI_PART && w.type == GGML_Q4_K && wide_plan(w, &p)),
+           SH_ERR_ARG, "gemv: this operand source does not fit this launch");
   if (w.type == GGML_Q4_K) {
     if (epi == EPI_PART && wide_plan(w, &p)) {
       SH_CHECK(ea.part_cap >= p.KS, SH_ERR_CAPACITY, "gemv: %u split partials exceed the buffer (%u)", p.KS,
@@ -1084,11 +1161,11 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
       else launch_q4w<4, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
     } else {
       switch (epi) {
-        case EPI_STORE: dispatch_q4s<EPI_STORE>(e, w, bx, xs, N, ea); break;
-        case EPI_ADD: dispatch_q4s<EPI_ADD>(e, w, bx, xs, N, ea); break;
-        case EPI_QKV: dispatch_q4s<EPI_QKV>(e, w, bx, xs, N, ea); break;
-        case EPI_SWIGLU: dispatch_q4s<EPI_SWIGLU>(e, w, bx, xs, N, ea); break;
-        case EPI_PART: dispatch_q4s<EPI_PART>(e, w, bx, xs, N, ea); break;
+        case EPI_STORE: dispatch_q4s<EPI_STORE>(e, w, bx, xs, N, ea, sr); break;
+        case EPI_ADD: dispatch_q4s<EPI_ADD>(e, w, bx, xs, N, ea, sr); break;
+        case EPI_QKV: dispatch_q4s<EPI_QKV>(e, w, bx, xs, N, ea, sr); break;
+        case EPI_SWIGLU: dispatch_q4s<EPI_SWIGLU>(e, w, bx, xs, N, ea, sr); break;
+        case EPI_PART: dispatch_q4s<EPI_PART>(e, w, bx, xs, N, ea, sr); break;
       }
     }
   } else if (w.type == GGML_Q8_0) {

@@ -334,7 +334,7 @@ static void free_model(sh_model* m) {
   (void)hipFree(m->out_norm);
   (void)hipFree(m->rope);
   Workspace& w = m->ws;
-  (void)hipFree(w.resid); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
+  (void)hipFree(w.resid); (void)hipFree(w.resid2); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
   (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
   (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq);
   delete m;
@@ -483,7 +483,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
                              sh_gemv_part_floats(L.wdown), sh_gemm_part_floats(L.wqkv), sh_gemm_part_floats(L.wo),
                              sh_gemm_part_floats(L.wgu), sh_gemm_part_floats(L.wdown)});
   const size_t C = SH_MAX_COLS;
-  if (dalloc(&w.resid, C * m->d) || dalloc(&w.bx, bx_elems) || dalloc(&w.xs, xs_elems) ||
+  if (dalloc(&w.resid, C * m->d) || dalloc(&w.resid2, C * m->d) || dalloc(&w.bx, bx_elems) ||
+      dalloc(&w.xs, xs_elems) ||
       dalloc(&w.q, C * m->d) || dalloc(&w.attn, C * m->d) || dalloc(&w.gpart, gpart_floats) ||
       dalloc(&w.h, C * m->ff) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
       dalloc(&w.tokens, C + 64) || dalloc(&w.amax, C) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
@@ -731,11 +732,30 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     pending = 0;
     return sh_prep_launch(e, pr);
   };
+  // Fused residual preps (<= 2 columns, whole-K kernels whose operand fits in
+  // LDS): QKV and gate/up build rmsnorm(resid + pending partials) themselves;
+  // the residual alternates between resid and resid2 (resid after each layer).
+  const bool fuse_rp = fuse && swiglu_epilogue() && !m->layers.empty() &&
+                       sh_gemv_resid_fusable(m->layers[0].wqkv, nc) && sh_gemv_resid_fusable(m->layers[0].wgu, nc);
+  auto resid_src = [&](const float* rin, float* rout, const float* norm_w) {
+    OpndSrc r;
+    r.kind = OPND_RESID; r.x = rin; r.rout = rout; r.part = w.gpart; r.nparts = pending; r.part_ld = pending_ld;
+    r.norm_w = norm_w; r.eps = m->eps;
+    pending = 0;
+    return r;
+  };
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
-    if ((rc = resid_prep(L.attn_norm))) return rc;
     qkv.layer = l;
-    if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
+    if (fuse_rp) {
+      const OpndSrc rs = resid_src(w.resid, w.resid2, L.attn_norm);
+      EpiArgs q2 = qkv;
+      q2.ssq = nullptr;  // the kernel applies the RMS factor it computed
+      if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, q2, "gemv_qkv", nullptr, &rs))) return rc;
+    } else {
+      if ((rc = resid_prep(L.attn_norm))) return rc;
+      if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
+    }
     // one segment covering the chunk: Wo combines the attention splits itself
     const bool fuse_o = fuse && segs.size() == 1 && segs[0].col0 == 0 && segs[0].ncol == nc && fuse_wo;
     OpndSrc osrc;
@@ -753,9 +773,17 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", &pending, fuse_o ? &osrc : nullptr)))
       return rc;
     pending_ld = po.ldo;
-    if ((rc = resid_prep(L.ffn_norm))) return rc;
     OpndSrc dsrc;  // down reads h itself when it takes the split-K kernel
-    if (swiglu_epilogue()) {
+    if (fuse_rp) {
+      const OpndSrc rs = resid_src(w.resid2, w.resid, L.ffn_norm);
+      EpiArgs s2 = sw;
+      s2.ssq = nullptr;
+      if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, s2, "gemv_gate_up", nullptr, &rs))) return rc;
+      pr.mode = PREP_PLAIN; pr.x = w.h; pr.nparts = 0;
+      if (fuse_down) { dsrc.kind = OPND_ROWS; dsrc.x = w.h; dsrc.ldx = m->ff; }
+    } else if ((rc = resid_prep(L.ffn_norm))) {
+      return rc;
+    } else if (swiglu_epilogue()) {
       // whole sums in one kernel, h = silu(gate) * up in its epilogue
       if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
       pr.mode = PREP_PLAIN; pr.x = w.h; pr.nparts = 0;

@@ -96,6 +96,7 @@ struct Layer {
 struct Workspace {
   uint32_t max_cols = 0;
   float* resid = nullptr;     // [cols][d]
+  float* resid2 = nullptr;    // [cols][d], the other half of the fused-prep residual ping-pong
   uint16_t* bx = nullptr;     // B operand buffer sized for max(K) x max_cols
   uint16_t* xs = nullptr;     // XS buffer
   float* q = nullptr;         // [cols][d] roped queries
@@ -183,11 +184,19 @@ struct EpiArgs {
 // (B/XS/cs, the default), f32 rows x [N][ldx] (the operand is built in LDS, as
 // the prep would build it, without a norm), or attention split partials (the
 // split combine is done in LDS, as k_fa_combine would do it).
-enum OpndKind { OPND_STAGED = 0, OPND_ROWS = 1, OPND_FA = 2 };
+enum OpndKind { OPND_STAGED = 0, OPND_ROWS = 1, OPND_FA = 2, OPND_RESID = 3 };
 struct OpndSrc {
   int kind = OPND_STAGED;
-  const float* x = nullptr;  // OPND_ROWS
+  const float* x = nullptr;  // OPND_ROWS; OPND_RESID: residual in [N][K]
   uint32_t ldx = 0;
+  // OPND_RESID (whole-K kernel, N <= 2): every workgroup builds the whole
+  // operand of rmsnorm(x + sum of split partials) * norm_w in LDS, workgroup 0
+  // writes x + partials to rout (another buffer: the others still read x).
+  float* rout = nullptr;
+  const float* part = nullptr;
+  uint32_t nparts = 0, part_ld = 0;
+  const float* norm_w = nullptr;
+  float eps = 0.f;
   const float* fa_part = nullptr;  // OPND_FA: partial layout of sh_fa_launch
   uint32_t n_layout = 0, rows_pad = 0, n_head = 0, gqa = 0, hd = 0, split_keys = 0, kv_off = 0;
   const uint32_t* dbase = nullptr;  // graph replay: live splits from *dbase + kv_off
@@ -199,8 +208,10 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
                    EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr,
                    const OpndSrc* src = nullptr);
 // Superblocks per split when the EPI_PART launch of w takes the split-K kernel
-// (which accepts any OpndSrc), else 0.
+// (which accepts OPND_ROWS / OPND_FA), else 0.
 uint32_t sh_gemv_fusable(const QMat& w);
+// Whether w's whole-K launches (QKV, SwiGLU) accept OPND_RESID for N columns.
+bool sh_gemv_resid_fusable(const QMat& w, uint32_t N);
 // Floats of partial-sum buffer the EPI_PART launches of w need (all splits).
 size_t sh_gemv_part_floats(const QMat& w);
 // y = W x for N <= SH_MAX_COLS columns (operand groups of 8, Q4_K) in one pass
