@@ -24,6 +24,8 @@
 #include <cstdlib>
 #include <string>
 
+#include <type_traits>
+
 #include "sh_internal.h"
 #include "sh_operand.h"
 
@@ -298,6 +300,30 @@ __device__ __forceinline__ float col_rinv(const EpiArgs& ea, uint32_t col) {
   return 1.0f / sqrtf(ss / (float)ea.norm_K + ea.eps);
 }
 
+// The same factor in two steps, so its loads overlap the weights instead of
+// delaying them: col_ssq_load at kernel start (the column's first SSQ_PRE
+// superblock sums of squares into registers), col_ssq_rinv after the main loop
+// (adds them in superblock order, reading any further ones then). Same result
+// as col_rinv, bit for bit.
+constexpr uint32_t SSQ_PRE = 16;
+__device__ __forceinline__ void col_ssq_load(const EpiArgs& ea, uint32_t col, float (&t)[SSQ_PRE]) {
+  if (!ea.ssq) return;
+#pragma unroll
+  for (uint32_t j = 0; j < SSQ_PRE; ++j) t[j] = ea.ssq[min(j, ea.ssq_n - 1) * 8 + col];
+}
+__device__ __forceinline__ float col_ssq_rinv(const EpiArgs& ea, uint32_t col, float (&t)[SSQ_PRE]) {
+  if (!ea.ssq) return 1.0f;
+  // opaque here, so the compiler cannot start the sum (and wait on the loads)
+  // before the main loop
+#pragma unroll
+  for (uint32_t j = 0; j < SSQ_PRE; ++j) asm volatile("" : "+v"(t[j]));
+  float ss = 0.f;
+#pragma unroll
+  for (uint32_t j = 0; j < SSQ_PRE; ++j) ss += j < ea.ssq_n ? t[j] : 0.0f;
+  for (uint32_t i = SSQ_PRE; i < ea.ssq_n; ++i) ss += ea.ssq[i * 8 + col];
+  return 1.0f / sqrtf(ss / (float)ea.norm_K + ea.eps);
+}
+
 // Row sums for one lane after the MFMA loop: the hi and lo columns (c, c + 8)
 // of the same activation column meet, times the column's norm factor f. Every
 // lane must call this (it shuffles).
@@ -337,7 +363,8 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
   const int g = lane >> 4, r = lane & 15;
   const uint32_t ks = blockIdx.y, kb0 = ks * S;
   const uint32_t tile0 = (blockIdx.x * WV + wave) * T;
-  const float nf = col_rinv(ea, r & 7);
+  float ssq_t[SSQ_PRE];
+  col_ssq_load(ea, r & 7, ssq_t);
 
   if (SRC == OPND_STAGED) {
     // Activation operand of the split -> LDS: 1 KB blocks i = 9 * sb + m (m < 8:
@@ -436,6 +463,7 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
     if (u + D < U) ring[u % D] = load_q4_tile(unit_ptr(u + D), lane, g, r);
     q4_tile_mma(cur, bq, bm, c, y[u % T]);
   }
+  const float nf = col_ssq_rinv(ea, r & 7, ssq_t);
 
   if (EPI == EPI_SWIGLU) {
     // (gate, up) = tiles (2i, 2i + 1) of this wave; one split only
@@ -497,7 +525,9 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar address math
   const int g = lane >> 4, r = lane & 15;
   const uint32_t tile0 = blockIdx.x * T;
-  float nf = SRC == OPND_RESID ? 1.0f : col_rinv(ea, r & 7);
+  float ssq_t[SSQ_PRE];
+  if (SRC != OPND_RESID) col_ssq_load(ea, r & 7, ssq_t);
+  float nf = 1.0f;
   f4 y[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
@@ -578,6 +608,7 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
       }
     }
   }
+  if (SRC != OPND_RESID) nf = col_ssq_rinv(ea, r & 7, ssq_t);
   // Tile partials meet in LDS, CH tiles per round; wave w < CH ends up holding
   // tile (round * CH + w), or with SwiGLU wave w < CH/2 holds the pair
   // (gate, up) = tiles (2w, 2w + 1) of the round.
@@ -605,6 +636,73 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
       if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
     }
     __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------ Q4_K deep ring
+
+// Whole-K GEMV for matrices of exactly 256 * 7 row tiles or more in one round
+// (the 8B gate/up: 1792 tiles) whose K is NB * 8 superblocks. A workgroup of GW = 8 waves owns T row tiles for all of
+// K; wave w takes superblocks w, w + 8, ... (NB of them) and, inside each, the
+// T tiles: NB * T weight units in one fully unrolled sequence with a sliding
+// window of D units in flight (unit u + D issued as unit u computes). The
+// chip-wide request stream is then steady (D units per wave, ~20 MB in all)
+// instead of one burst per superblock, so waves start computing as their first
+// units land and the last units arrive just before they are needed. The NB
+// activation operands stay in registers. With T = 7 a 1792-tile matrix is 256
+// workgroups, one per CU, in a single round. The 8 partial sums of each tile
+// meet in LDS in one round. EPI_STORE and EPI_PART (one split) only.
+template <int T, int NB, int D, int EPI>
+__global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                       const uint16_t* __restrict__ Bx,
+                                                       const uint16_t* __restrict__ XS,
+                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea) {
+  static_assert(EPI == EPI_STORE || EPI == EPI_PART, "deep-ring GEMV: store epilogues only");
+  constexpr int U = NB * T;
+  __shared__ f4 red[T][GW][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const uint32_t tile0 = blockIdx.x * T;
+  float ssq_t[SSQ_PRE];
+  col_ssq_load(ea, r & 7, ssq_t);
+  // unit u: superblock wave + GW * (u / T), tile tile0 + u % T (clamped in bounds)
+  auto unit_ptr = [&](int u) {
+    const uint32_t t = tile0 + u % T, tile = t < tiles ? t : tiles - 1;
+    return Wp + ((size_t)tile * nsb + wave + GW * (u / T)) * SH_Q4K_TILE_BYTES;
+  };
+  Q4Tile ring[D];
+#pragma unroll
+  for (int u = 0; u < D && u < U; ++u) ring[u] = load_q4_tile(unit_ptr(u), lane, g, r);
+  h8 bq[NB][8], bm[NB];
+  float c[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const uint32_t b = wave + GW * i;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bq[i][k] = as_h8(ld16(Bx + ((size_t)(b * 8 + k) * 64 + lane) * 8));
+    bm[i] = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
+    c[i] = CS[b * 8 + (lane & 7)];
+  }
+  f4 y[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    q4_tile_mma(ring[u % D], bq[u / T], bm[u / T], c[u / T], y[u % T]);
+    if (u + D < U) ring[u % D] = load_q4_tile(unit_ptr(u + D), lane, g, r);
+  }
+  const float nf = col_ssq_rinv(ea, r & 7, ssq_t);
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[t][wave][lane] = y[t];
+  __syncthreads();
+  if (wave < T) {
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < GW; ++w) v += red[wave][w][lane];
+    float o[4];
+    col_sum4(v, nf, o);
+    const uint32_t tile = tile0 + wave;
+    if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
   }
 }
 
@@ -1127,6 +1225,52 @@ static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_
   else launch_q8<1, 4, EPI>(e, w, bx, N, ea);
 }
 
+// Deep-ring policy (K of 8 or 16 superblocks): T = 7 when the tiles split
+// evenly into at least 256 workgroups of 7 (one round, one workgroup per CU).
+// Matrices that need several rounds (lm_head) run faster on k_gemv_q4s
+// (measured: 68 us against 72-77 us for 128256 x 4096), as do small ones.
+uint32_t sh_gemv_ring_t(const QMat& w) {
+  static const bool off = [] {
+    const char* s = getenv("SH_RING");
+    return s && std::string(s) == "0";
+  }();
+  if (off || w.type != GGML_Q4_K || (w.K != 2048 && w.K != 4096)) return 0;  // K = 8 NB superblocks
+  if (w.tiles % 7 == 0 && w.tiles / 7 >= 256) return 7;
+  return 0;
+}
+
+// Weight units in flight per wave: 2 and 3 time alike on 28672 x 4096
+// (16.3 / 16.4 us), 4 and more slower (16.8 us at 4, 19 us at 6).
+constexpr int RING_D = 3;
+template <int EPI>
+static void launch_q4t(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                       const EpiArgs& ea, uint32_t T) {
+  (void)T;  // 7 (sh_gemv_ring_t)
+  const dim3 grid(w.tiles / 7);
+  if (w.K == 4096)
+    hipLaunchKernelGGL((k_gemv_q4t<7, 2, RING_D, EPI>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 16u, bx, xs,
+                       ea.cs, N, ea);
+  else
+    hipLaunchKernelGGL((k_gemv_q4t<7, 1, RING_D, EPI>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 8u, bx, xs,
+                       ea.cs, N, ea);
+}
+
+int sh_gemv_ring_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                        EpiKind epi, const EpiArgs& ea, const char* tag) {
+  SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "gemv chunk N=%u outside [1,8]", N);
+  SH_CHECK(ea.cs, SH_ERR_ARG, "gemv: activation scales missing");
+  const uint32_t T = sh_gemv_ring_t(w);
+  SH_CHECK(T && (epi == EPI_STORE || epi == EPI_PART), SH_ERR_ARG, "gemv: this launch does not take the ring kernel");
+  SH_CHECK(epi != EPI_PART || ea.part_cap >= 1, SH_ERR_CAPACITY, "gemv: no room for the partial sums");
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  if (epi == EPI_STORE) launch_q4t<EPI_STORE>(e, w, bx, xs, N, ea, T);
+  else launch_q4t<EPI_PART>(e, w, bx, xs, N, ea, T);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, tag, w.alg_bytes, ev);
+  return SH_OK;
+}
+
 bool sh_gemv_resid_fusable(const QMat& w, uint32_t N) {
   // the whole-K kernel with its largest reduction buffer (4 tiles x 32 KB / 4) must fit beside the operand
   return w.type == GGML_Q4_K && w.K % 256 == 0 && N <= 2 && resid_lds_bytes(w.K / 256) + 32768 <= 160 * 1024;
@@ -1160,7 +1304,9 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
       else if (p.T == 2) launch_q4w<2, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
       else launch_q4w<4, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
     } else {
-      switch (epi) {
+      const uint32_t rt = sr.kind == OPND_STAGED && epi == EPI_STORE ? sh_gemv_ring_t(w) : 0u;
+      switch (rt ? -1 : (int)epi) {
+        case -1: launch_q4t<EPI_STORE>(e, w, bx, xs, N, ea, rt); break;
         case EPI_STORE: dispatch_q4s<EPI_STORE>(e, w, bx, xs, N, ea, sr); break;
         case EPI_ADD: dispatch_q4s<EPI_ADD>(e, w, bx, xs, N, ea, sr); break;
         case EPI_QKV: dispatch_q4s<EPI_QKV>(e, w, bx, xs, N, ea, sr); break;

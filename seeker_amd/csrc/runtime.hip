@@ -783,6 +783,12 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       if (fuse_down) { dsrc.kind = OPND_ROWS; dsrc.x = w.h; dsrc.ldx = m->ff; }
     } else if ((rc = resid_prep(L.ffn_norm))) {
       return rc;
+    } else if (swiglu_epilogue() && sh_gemv_ring_t(L.wgu)) {
+      // whole sums from the deep-ring kernel (one split); SwiGLU in the down prep
+      EpiArgs pg = part_args(L.wgu);
+      set_norm(pg);
+      if ((rc = sh_gemv_ring_launch(e, L.wgu, w.bx, w.xs, nc, EPI_PART, pg, "gemv_gate_up"))) return rc;
+      pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = 1; pr.part_ld = pg.ldo;
     } else if (swiglu_epilogue()) {
       // whole sums in one kernel, h = silu(gate) * up in its epilogue
       if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;

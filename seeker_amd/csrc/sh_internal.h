@@ -214,6 +214,13 @@ uint32_t sh_gemv_fusable(const QMat& w);
 bool sh_gemv_resid_fusable(const QMat& w, uint32_t N);
 // Floats of partial-sum buffer the EPI_PART launches of w need (all splits).
 size_t sh_gemv_part_floats(const QMat& w);
+// Tiles per workgroup of the deep-ring whole-K kernel for w, or 0 when w does
+// not take it (Q4_K with enough row tiles to fill the chip; SH_RING=0 turns it
+// off). sh_gemv_ring_launch: y = W x through that kernel, EPI_STORE or
+// EPI_PART (one split, whole sums).
+uint32_t sh_gemv_ring_t(const QMat& w);
+int sh_gemv_ring_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                        EpiKind epi, const EpiArgs& ea, const char* tag);
 // y = W x for N <= SH_MAX_COLS columns (operand groups of 8, Q4_K) in one pass
 // over W: EPI_PART (partials [split][8 ceil(N/8)][ldo]; *nparts = splits) or
 // EPI_STORE. The operand of group g starts at g times one group's size.

@@ -15,10 +15,13 @@ from seeker_amd._native import GGML_Q4_K, GGML_Q8_0, SH_ERR_ARG, SH_ERR_CAPACITY
 
 pytestmark = pytest.mark.gpu
 
-# configs[0] target shape (Q8_0) and a GQA Q4_K shape with the 8B head layout.
+# configs[0] target shape (Q8_0), a GQA Q4_K shape with the 8B head layout, and
+# one layer with the 8B FFN width (gate/up on the deep-ring kernel, SwiGLU in
+# the down prep).
 SHAPES = {
     "tiny_q8": S.TINY_TARGET,
     "gqa_q4k": S.LlamaShape(2, 1024, 8, 2, 2048, 4000, 512, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K),
+    "ffn8b_q4k": S.LlamaShape(1, 1024, 8, 2, 14336, 4000, 512, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K),
 }
 
 

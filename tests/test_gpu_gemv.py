@@ -51,11 +51,20 @@ def test_gemv_ragged_rows_and_accumulate(engine, qtype):
     assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
 
 
-@pytest.mark.parametrize("M,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("M,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (28672, 4096)])
 def test_gemv_q4k_8b_shapes(engine, M, K):
     got, ref = _run(engine, GGML_Q4_K, M, K, 8, seed=M + K)
     assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
     # greedy-relevant: per-column argmax identical
+    assert np.array_equal(got.argmax(axis=1), ref.argmax(axis=1))
+
+
+@pytest.mark.parametrize("N", [1, 3])
+def test_gemv_q4k_deep_ring_columns(engine, N):
+    """28672 x 4096 takes the deep-ring kernel (7 tiles per workgroup, 256
+    workgroups); fewer than 8 columns leave operand lanes unused."""
+    got, ref = _run(engine, GGML_Q4_K, 28672, 4096, N, seed=17 + N)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
     assert np.array_equal(got.argmax(axis=1), ref.argmax(axis=1))
 
 
