@@ -349,12 +349,62 @@ constexpr uint32_t WIDE_MAX_UNITS = 12;  // units per wave (T * S) beyond which 
 // (one wave per (superblock, column)): from f32 rows (OPND_ROWS) or by
 // combining attention split partials (OPND_FA), with the same arithmetic as
 // the prep / combine kernels; the first weight units are already in flight.
-template <int T, int S, int D, int EPI, int SRC>
+// 16-byte agent-coherent store / loads (sc1: past the non-coherent per-XCD
+// L2) for data that another workgroup of the same kernel reads. After
+// ld_coh4 x n, coh_wait ties the results to a vmcnt(0) wait before any use.
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st_coh4(float* p, float4 v) {
+  const f4v w = {v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
+}
+__device__ __forceinline__ f4v ld_coh4(const float* p) {
+  f4v v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+
+// Fused residual prep of output superblock j (the PREP_RESID prep kernel's
+// arithmetic: resid + split partials in split order, sums of squares, times
+// the norm weight, operand store), one wave per column, by the last workgroup
+// to finish j. The partials of the other workgroups are read with
+// agent-coherent loads.
+__device__ __forceinline__ void fused_prep_sb(const EpiArgs& ea, const PrepFuse& pf, uint32_t j, uint32_t nparts,
+                                              uint32_t N) {
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave >= N) return;  // wave-uniform
+  const uint32_t col = wave, k = 256 * j + 4 * lane;
+  float* xp = pf.resid + (size_t)col * pf.K + k;
+  float4 v = *(const float4*)xp;
+  const float* pc = ea.out + (size_t)col * ea.ldo + k;
+  for (uint32_t s0 = 0; s0 < nparts; s0 += 8) {
+    f4v t[8];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) t[i] = ld_coh4(pc + (size_t)min(s0 + i, nparts - 1) * ea.part_stride);
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]), "+v"(t[6]), "+v"(t[7])
+                 :
+                 : "memory");
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      if (s0 + i >= nparts) break;
+      v.x += t[i][0]; v.y += t[i][1]; v.z += t[i][2]; v.w += t[i][3];
+    }
+  }
+  *(float4*)xp = v;
+  const float ss = sh_wave_sum(sh_sq4(v));
+  if (lane == 0) pf.ssq[j * 8 + col] = ss;
+  const float4 wv = *(const float4*)(pf.norm_w + k);
+  v.x *= wv.x; v.y *= wv.y; v.z *= wv.z; v.w *= wv.w;
+  sh_operand_store_sb(v, pf.K, j, col, pf.bx, pf.xs, pf.cs);
+}
+
+template <int T, int S, int D, int EPI, int SRC, bool FP = false>
 __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
                                                        const uint16_t* __restrict__ Bx,
                                                        const uint16_t* __restrict__ XS,
                                                        const float* __restrict__ CS, uint32_t N, EpiArgs ea,
-                                                       OpndSrc src) {
+                                                       OpndSrc src, PrepFuse pf) {
+  static_assert(!FP || (EPI == EPI_PART && SRC == OPND_STAGED && (T == 1 || T == 2)), "fused prep: split-K partials");
   constexpr int U = S * T;
   __shared__ h8 sB[S * 9 * 64];
   __shared__ float sC[64];
@@ -481,8 +531,33 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
       float o[4];
       col_sum4(y[t], nf, o);
       const uint32_t tile = tile0 + t;
-      if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o, ks);
+      if (tile < tiles && r < 8 && (uint32_t)r < N) {
+        if (FP) {  // partials another workgroup will read: agent-coherent stores
+          st_coh4(ea.out + ks * ea.part_stride + (size_t)r * ea.ldo + tile * 16 + 4 * g,
+                  make_float4(o[0], o[1], o[2], o[3]));
+        } else {
+          epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o, ks);
+        }
+      }
     }
+  }
+  if (FP) {
+    // Arrival: every wave's partial stores have completed; the workgroup that
+    // completes output superblock j (row groups x splits) runs its prep.
+    __shared__ uint32_t s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    constexpr uint32_t RG_ROWS = 16 * T * WV, RG_PER_SB = 256 / RG_ROWS;
+    const uint32_t j = blockIdx.x / RG_PER_SB;
+    if (threadIdx.x == 0) {
+      const uint32_t arrivals = RG_PER_SB * gridDim.y;
+      uint32_t* cnt = pf.cnt + (size_t)j * SH_SB_CNT_STRIDE;
+      const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = old + 1 == arrivals;
+      if (old + 1 == arrivals) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (s_last) fused_prep_sb(ea, pf, j, gridDim.y, N);
   }
 }
 
@@ -569,7 +644,7 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
       float4 v = *(const float4*)(src.x + (size_t)col * K + k);
       if (src.nparts) v = sum_parts4(src.part + (size_t)col * src.part_ld + k, pstride, src.nparts, v);
       if (blockIdx.x == 0) *(float4*)(src.rout + (size_t)col * K + k) = v;
-      const float ss = sh_wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+      const float ss = sh_wave_sum(sh_sq4(v));
       if (lane == 0) sQ[sb * 8 + col] = ss;
       const float4 wv = *(const float4*)(src.norm_w + k);
       v.x *= wv.x; v.y *= wv.y; v.z *= wv.z; v.w *= wv.w;
@@ -1136,45 +1211,61 @@ static uint32_t gemv_d_override() {
   return v;
 }
 // D = weight units in flight per wave (SH_GEMV_D=2|4|8; default 4).
-template <int T, int S, int EPI, int SRC>
-static void launch_q4w_src(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                           const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
+template <int T, int S, int EPI, int SRC, bool FP>
+static void launch_q4w_fp(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                          const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse& pf) {
   const dim3 grid((w.tiles + WV * T - 1) / (WV * T), p.KS);
   const uint32_t d = gemv_d_override();
   if (d == 2)
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 2, EPI, SRC>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256,
-                       bx, xs, ea.cs, N, ea, src);
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 2, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
+                       w.K / 256, bx, xs, ea.cs, N, ea, src, pf);
   else if (d == 8)
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 8, EPI, SRC>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256,
-                       bx, xs, ea.cs, N, ea, src);
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 8, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
+                       w.K / 256, bx, xs, ea.cs, N, ea, src, pf);
   else
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 4, EPI, SRC>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles, w.K / 256,
-                       bx, xs, ea.cs, N, ea, src);
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 4, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
+                       w.K / 256, bx, xs, ea.cs, N, ea, src, pf);
+}
+template <int T, int S, int EPI, int SRC>
+static void launch_q4w_src(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                           const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse* pf) {
+  if constexpr (EPI == EPI_PART && SRC == OPND_STAGED && (T == 1 || T == 2)) {
+    if (pf) {
+      launch_q4w_fp<T, S, EPI, SRC, true>(e, w, bx, xs, N, ea, p, src, *pf);
+      return;
+    }
+  }
+  launch_q4w_fp<T, S, EPI, SRC, false>(e, w, bx, xs, N, ea, p, src, PrepFuse{});
 }
 template <int T, int S, int EPI>
 static void launch_q4w_s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                         const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
-  if (src.kind == OPND_ROWS) launch_q4w_src<T, S, EPI, OPND_ROWS>(e, w, bx, xs, N, ea, p, src);
-  else if (src.kind == OPND_FA) launch_q4w_src<T, S, EPI, OPND_FA>(e, w, bx, xs, N, ea, p, src);
-  else launch_q4w_src<T, S, EPI, OPND_STAGED>(e, w, bx, xs, N, ea, p, src);
+                         const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse* pf) {
+  if (src.kind == OPND_ROWS) launch_q4w_src<T, S, EPI, OPND_ROWS>(e, w, bx, xs, N, ea, p, src, nullptr);
+  else if (src.kind == OPND_FA) launch_q4w_src<T, S, EPI, OPND_FA>(e, w, bx, xs, N, ea, p, src, nullptr);
+  else launch_q4w_src<T, S, EPI, OPND_STAGED>(e, w, bx, xs, N, ea, p, src, pf);
 }
 template <int T, int S, int EPI>
 static void launch_q4w_if(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                          const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
-  if constexpr (T * S <= (int)WIDE_MAX_UNITS) launch_q4w_s<T, S, EPI>(e, w, bx, xs, N, ea, p, src);
+                          const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse* pf) {
+  if constexpr (T * S <= (int)WIDE_MAX_UNITS) launch_q4w_s<T, S, EPI>(e, w, bx, xs, N, ea, p, src, pf);
 }
 template <int T, int EPI>
 static void launch_q4w(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                       const EpiArgs& ea, const WidePlan& p, const OpndSrc& src) {
+                       const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse* pf = nullptr) {
   switch (p.S) {
-    case 1: launch_q4w_if<T, 1, EPI>(e, w, bx, xs, N, ea, p, src); break;
-    case 2: launch_q4w_if<T, 2, EPI>(e, w, bx, xs, N, ea, p, src); break;
-    case 3: launch_q4w_if<T, 3, EPI>(e, w, bx, xs, N, ea, p, src); break;
-    case 4: launch_q4w_if<T, 4, EPI>(e, w, bx, xs, N, ea, p, src); break;
-    case 5: launch_q4w_if<T, 5, EPI>(e, w, bx, xs, N, ea, p, src); break;
-    case 6: launch_q4w_if<T, 6, EPI>(e, w, bx, xs, N, ea, p, src); break;
-    default: launch_q4w_if<T, 7, EPI>(e, w, bx, xs, N, ea, p, src); break;
+    case 1: launch_q4w_if<T, 1, EPI>(e, w, bx, xs, N, ea, p, src, pf); break;
+    case 2: launch_q4w_if<T, 2, EPI>(e, w, bx, xs, N, ea, p, src, pf); break;
+    case 3: launch_q4w_if<T, 3, EPI>(e, w, bx, xs, N, ea, p, src, pf); break;
+    case 4: launch_q4w_if<T, 4, EPI>(e, w, bx, xs, N, ea, p, src, pf); break;
+    case 5: launch_q4w_if<T, 5, EPI>(e, w, bx, xs, N, ea, p, src, pf); break;
+    case 6: launch_q4w_if<T, 6, EPI>(e, w, bx, xs, N, ea, p, src, pf); break;
+    default: launch_q4w_if<T, 7, EPI>(e, w, bx, xs, N, ea, p, src, pf); break;
   }
+}
+
+bool sh_gemv_prep_fusable(const QMat& w) {
+  WidePlan p;
+  return wide_plan(w, &p) && (p.T == 1 || p.T == 2) && w.tiles % 16 == 0 && w.tiles / 16 <= SH_SB_CNT;
 }
 
 // Dynamic LDS of the OPND_RESID build: the operand, its scales and sums of squares.
@@ -1282,7 +1373,7 @@ uint32_t sh_gemv_fusable(const QMat& w) {
 }
 
 int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N, EpiKind epi,
-                   const EpiArgs& ea, const char* tag, uint32_t* nparts, const OpndSrc* src) {
+                   const EpiArgs& ea, const char* tag, uint32_t* nparts, const OpndSrc* src, const PrepFuse* pf) {
   SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "gemv chunk N=%u outside [1,8]", N);
   SH_CHECK(ea.cs, SH_ERR_ARG, "gemv: activation scales missing");
   const OpndSrc staged;
@@ -1295,13 +1386,16 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
                (sr.kind == OPND_RESID ? (epi == EPI_QKV || epi == EPI_SWIGLU) && sh_gemv_resid_fusable(w, N)
                                       : epi == EPI_PART && w.type == GGML_Q4_K && wide_plan(w, &p)),
            SH_ERR_ARG, "gemv: this operand source does not fit this launch");
+  SH_CHECK(!pf || (epi == EPI_PART && sr.kind == OPND_STAGED && sh_gemv_prep_fusable(w) && pf->K == w.tiles * 16 &&
+                   pf->cnt && pf->resid && pf->norm_w && pf->ssq),
+           SH_ERR_ARG, "gemv: the fused residual prep does not fit this launch");
   if (w.type == GGML_Q4_K) {
     if (epi == EPI_PART && wide_plan(w, &p)) {
       SH_CHECK(ea.part_cap >= p.KS, SH_ERR_CAPACITY, "gemv: %u split partials exceed the buffer (%u)", p.KS,
                ea.part_cap);
       np = p.KS;
-      if (p.T == 1) launch_q4w<1, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
-      else if (p.T == 2) launch_q4w<2, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
+      if (p.T == 1) launch_q4w<1, EPI_PART>(e, w, bx, xs, N, ea, p, sr, pf);
+      else if (p.T == 2) launch_q4w<2, EPI_PART>(e, w, bx, xs, N, ea, p, sr, pf);
       else launch_q4w<4, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
     } else {
       const uint32_t rt = sr.kind == OPND_STAGED && epi == EPI_STORE ? sh_gemv_ring_t(w) : 0u;

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
     }
   }
   if (a.norm_w) {
-    const float ss = sh_wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+    const float ss = sh_wave_sum(sh_sq4(v));
     if (lane == 0) a.ssq[(col / 8) * sh_grp_cs(a.K) + sb * 8 + col % 8] = ss;
     if (valid) {
       const float4 wv = *(const float4*)(a.norm_w + k);

@@ -337,6 +337,7 @@ static void free_model(sh_model* m) {
   (void)hipFree(w.resid); (void)hipFree(w.resid2); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
   (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
   (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq);
+  (void)hipFree(w.bx2); (void)hipFree(w.xs2); (void)hipFree(w.cs2); (void)hipFree(w.ssq2); (void)hipFree(w.sb_cnt);
   delete m;
 }
 
@@ -488,11 +489,14 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       dalloc(&w.q, C * m->d) || dalloc(&w.attn, C * m->d) || dalloc(&w.gpart, gpart_floats) ||
       dalloc(&w.h, C * m->ff) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
       dalloc(&w.tokens, C + 64) || dalloc(&w.amax, C) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
-      dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)))
+      dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
+      dalloc(&w.cs2, sh_grp_cs(m->d)) || dalloc(&w.ssq2, sh_grp_cs(m->d)) || dalloc(&w.sb_cnt, SH_SB_CNT * SH_SB_CNT_STRIDE))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
   w.gpart_floats = gpart_floats;
-  if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess)
+  if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess ||
+      hipMemset(w.xs2, 0, sh_grp_xs(m->d) * 2) != hipSuccess || hipMemset(w.bx2, 0, sh_grp_bx(m->d) * 2) != hipSuccess ||
+      hipMemset(w.sb_cnt, 0, SH_SB_CNT * SH_SB_CNT_STRIDE * 4) != hipSuccess)
     FAIL(SH_ERR_HIP, "workspace clear failed");
   if ((fail = ensure_rope(m, std::max<uint32_t>(m->n_ctx, 1024)))) FAIL(fail, "%s", sh_last_error());
   if (hipDeviceSynchronize() != hipSuccess) FAIL(SH_ERR_HIP, "model upload failed");
@@ -703,15 +707,25 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     qkv.colpos[j] = cols[j].pos; qkv.slot[j] = cols[j].slot; qkv.mseq[j] = cols[j].kv->max_seq;
     qkv.kc[j] = cols[j].kv->k; qkv.vc[j] = cols[j].kv->v;
   }
-  qkv.cs = w.cs;
   qkv.dbase = cols[0].kv->graph_base;  // graph capture: one cache per forward
+  // Operand the next GEMV reads. The prep kernels and the attention combine
+  // write set 0; residual preps fused into the o / down GEMVs write set 1,
+  // since other workgroups of the producing kernel may still be staging set 0.
+  struct OpSet {
+    uint16_t* bx;
+    uint16_t* xs;
+    float* cs;
+    float* ssq;
+  };
+  const OpSet set0{w.bx, w.xs, w.cs, w.ssq}, set1{w.bx2, w.xs2, w.cs2, w.ssq2};
+  OpSet cur = set0;
   // GEMVs whose input is RMS-normalized apply the norm factor to their outputs
   auto set_norm = [&](EpiArgs& ea) {
-    ea.ssq = w.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
+    ea.cs = cur.cs; ea.ssq = cur.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
   };
-  set_norm(qkv);
   // o, gate/up and down write split partial sums, finished by the next prep
-  // (residual add, SwiGLU); ld = the matrix's padded (packed) row count.
+  // (residual add, SwiGLU); ld = the matrix's padded (packed) row count. o and
+  // down read set 0 (attention combine, SwiGLU prep).
   auto part_args = [&](const QMat& q) {
     EpiArgs pa;
     pa.out = w.gpart; pa.ldo = q.tiles * 16; pa.cs = w.cs;
@@ -720,8 +734,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     return pa;
   };
   EpiArgs sw;
-  sw.out = w.h; sw.ldo = m->ff; sw.cs = w.cs;
-  set_norm(sw);
+  sw.out = w.h; sw.ldo = m->ff;
   PrepArgs pr;
   pr.N = nc; pr.bx = w.bx; pr.xs = w.xs; pr.cs = w.cs; pr.part = w.gpart; pr.eps = m->eps; pr.ssq = w.ssq;
   // Residual stream: embedding, then + partials of the pending o / down GEMV.
@@ -730,6 +743,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     pr.mode = PREP_RESID; pr.x = w.resid; pr.K = m->d; pr.norm_w = norm_w;
     pr.nparts = pending; pr.part_ld = pending_ld;
     pending = 0;
+    cur = set0;
     return sh_prep_launch(e, pr);
   };
   // Fused residual preps (<= 2 columns, whole-K kernels whose operand fits in
@@ -744,20 +758,34 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     pending = 0;
     return r;
   };
+  // Otherwise the o and down GEMVs finish the residual themselves (the last
+  // workgroup of each output superblock runs its prep), writing set 1.
+  const bool fuse_pp = fusion_enabled() && !fuse_rp && !m->layers.empty() &&
+                       sh_gemv_prep_fusable(m->layers[0].wo) && sh_gemv_prep_fusable(m->layers[0].wdown);
+  bool prepped = false;  // the operand of the next GEMV is built (set 1)
+  auto prep_fuse = [&](const float* norm_w) {
+    PrepFuse f;
+    f.resid = w.resid; f.norm_w = norm_w; f.bx = w.bx2; f.xs = w.xs2; f.cs = w.cs2; f.ssq = w.ssq2;
+    f.cnt = w.sb_cnt; f.K = m->d;
+    return f;
+  };
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
     qkv.layer = l;
     if (fuse_rp) {
       const OpndSrc rs = resid_src(w.resid, w.resid2, L.attn_norm);
       EpiArgs q2 = qkv;
+      q2.cs = w.cs;
       q2.ssq = nullptr;  // the kernel applies the RMS factor it computed
       if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, q2, "gemv_qkv", nullptr, &rs))) return rc;
     } else {
-      if ((rc = resid_prep(L.attn_norm))) return rc;
-      if ((rc = sh_gemv_launch(e, L.wqkv, w.bx, w.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
+      if (!prepped && (rc = resid_prep(L.attn_norm))) return rc;
+      set_norm(qkv);
+      if ((rc = sh_gemv_launch(e, L.wqkv, cur.bx, cur.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
     }
+    prepped = false;
     // one segment covering the chunk: Wo combines the attention splits itself
-    const bool fuse_o = fuse && segs.size() == 1 && segs[0].col0 == 0 && segs[0].ncol == nc && fuse_wo;
+    const bool fuse_o = fuse && !fuse_pp && segs.size() == 1 && segs[0].col0 == 0 && segs[0].ncol == nc && fuse_wo;
     OpndSrc osrc;
     for (const FaSeg& sg : segs) {
       FaArgs fa;
@@ -770,51 +798,73 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
         return rc;
     }
     EpiArgs po = part_args(L.wo);
-    if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", &pending, fuse_o ? &osrc : nullptr)))
-      return rc;
-    pending_ld = po.ldo;
+    if (fuse_pp) {
+      const PrepFuse pf = prep_fuse(L.ffn_norm);
+      if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", nullptr, nullptr, &pf))) return rc;
+      pending = 0;
+      cur = set1;
+      prepped = true;
+    } else {
+      if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", &pending, fuse_o ? &osrc : nullptr)))
+        return rc;
+      pending_ld = po.ldo;
+    }
     OpndSrc dsrc;  // down reads h itself when it takes the split-K kernel
     if (fuse_rp) {
       const OpndSrc rs = resid_src(w.resid2, w.resid, L.ffn_norm);
       EpiArgs s2 = sw;
+      s2.cs = w.cs;
       s2.ssq = nullptr;
       if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, s2, "gemv_gate_up", nullptr, &rs))) return rc;
       pr.mode = PREP_PLAIN; pr.x = w.h; pr.nparts = 0;
       if (fuse_down) { dsrc.kind = OPND_ROWS; dsrc.x = w.h; dsrc.ldx = m->ff; }
-    } else if ((rc = resid_prep(L.ffn_norm))) {
+    } else if (!prepped && (rc = resid_prep(L.ffn_norm))) {
       return rc;
     } else if (swiglu_epilogue() && sh_gemv_ring_t(L.wgu)) {
       // whole sums from the deep-ring kernel (one split); SwiGLU in the down prep
       EpiArgs pg = part_args(L.wgu);
       set_norm(pg);
-      if ((rc = sh_gemv_ring_launch(e, L.wgu, w.bx, w.xs, nc, EPI_PART, pg, "gemv_gate_up"))) return rc;
+      if ((rc = sh_gemv_ring_launch(e, L.wgu, cur.bx, cur.xs, nc, EPI_PART, pg, "gemv_gate_up"))) return rc;
       pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = 1; pr.part_ld = pg.ldo;
     } else if (swiglu_epilogue()) {
       // whole sums in one kernel, h = silu(gate) * up in its epilogue
-      if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
+      set_norm(sw);
+      if ((rc = sh_gemv_launch(e, L.wgu, cur.bx, cur.xs, nc, EPI_SWIGLU, sw, "gemv_gate_up"))) return rc;
       pr.mode = PREP_PLAIN; pr.x = w.h; pr.nparts = 0;
       if (fuse && fuse_down) { dsrc.kind = OPND_ROWS; dsrc.x = w.h; dsrc.ldx = m->ff; }
     } else {
       EpiArgs pg = part_args(L.wgu);
       set_norm(pg);
       uint32_t ngu = 0;
-      if ((rc = sh_gemv_launch(e, L.wgu, w.bx, w.xs, nc, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
+      if ((rc = sh_gemv_launch(e, L.wgu, cur.bx, cur.xs, nc, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
       pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = ngu; pr.part_ld = pg.ldo;
     }
+    prepped = false;
     pr.K = m->ff; pr.norm_w = nullptr;
     if (dsrc.kind == OPND_STAGED && (rc = sh_prep_launch(e, pr))) return rc;
+    cur = set0;
     EpiArgs pd = part_args(L.wdown);
-    if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", &pending,
-                             dsrc.kind == OPND_STAGED ? nullptr : &dsrc)))
-      return rc;
-    pending_ld = pd.ldo;
+    const float* next_norm = l + 1 < m->n_layer ? m->layers[l + 1].attn_norm : (want_logits ? m->out_norm : nullptr);
+    if (fuse_pp && next_norm && dsrc.kind == OPND_STAGED) {
+      const PrepFuse pf = prep_fuse(next_norm);
+      if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", nullptr, nullptr, &pf)))
+        return rc;
+      pending = 0;
+      cur = set1;
+      prepped = true;
+    } else {
+      if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", &pending,
+                               dsrc.kind == OPND_STAGED ? nullptr : &dsrc)))
+        return rc;
+      pending_ld = pd.ldo;
+    }
   }
   if (want_logits) {
-    if ((rc = resid_prep(m->out_norm))) return rc;
+    if (!prepped && (rc = resid_prep(m->out_norm))) return rc;
     EpiArgs st;
-    st.out = w.logits; st.ldo = m->V; st.rows = m->V; st.cs = w.cs;
+    st.out = w.logits; st.ldo = m->V; st.rows = m->V;
     set_norm(st);
-    if ((rc = sh_gemv_launch(e, m->lm_head, w.bx, w.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
+    if ((rc = sh_gemv_launch(e, m->lm_head, cur.bx, cur.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
   } else if (want_resid && pending) {
     if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, 8, m->d, nc, w.resid, m->d, true))) return rc;
   }

@@ -111,6 +111,14 @@ struct Workspace {
   float* ssq = nullptr;       // [max(K)/256][8] per-superblock sums of squares of the normalized input
   size_t fa_part_floats = 0;
   size_t gpart_floats = 0;
+  // Second operand set, written by residual preps fused into the o / down GEMVs
+  // (other workgroups of the producing kernel may still be staging the first):
+  // sized for K = d, 8 columns.
+  uint16_t* bx2 = nullptr;
+  uint16_t* xs2 = nullptr;
+  float* cs2 = nullptr;
+  float* ssq2 = nullptr;
+  uint32_t* sb_cnt = nullptr;  // [SH_SB_CNT x SH_SB_CNT_STRIDE] arrival counters of the fused residual prep (zero between launches)
 };
 
 struct sh_model {
@@ -201,12 +209,34 @@ struct OpndSrc {
   uint32_t n_layout = 0, rows_pad = 0, n_head = 0, gqa = 0, hd = 0, split_keys = 0, kv_off = 0;
   const uint32_t* dbase = nullptr;  // graph replay: live splits from *dbase + kv_off
 };
+// Residual prep fused into a split-K GEMV (EPI_PART, 256-row output
+// superblocks): the last workgroup to finish output superblock j (arrival
+// counter cnt[j]) adds the split partials of its rows to resid in split order,
+// writes resid, the per-superblock sums of squares and the operand of
+// resid * norm_w for the next GEMV (bx, xs, cs), as the PREP_RESID prep kernel
+// does, bit for bit. The partials travel through agent-coherent stores and
+// loads. The last arriver resets cnt[j] to zero.
+constexpr uint32_t SH_SB_CNT = 256;
+constexpr uint32_t SH_SB_CNT_STRIDE = 64;  // counters 256 bytes apart: no two share a cache line
+struct PrepFuse {
+  float* resid = nullptr;  // [N][K]
+  const float* norm_w = nullptr;
+  uint16_t* bx = nullptr;
+  uint16_t* xs = nullptr;
+  float* cs = nullptr;
+  float* ssq = nullptr;
+  uint32_t* cnt = nullptr;
+  uint32_t K = 0;          // rows of the producing GEMV = elements of the residual
+};
 // Launch y = W x for N <= 8 columns; with EPI_PART, *nparts receives the
 // number of split partials written (1 for the other epilogues). A non-staged
 // src needs the split-K kernel (sh_gemv_fusable).
 int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                    EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr,
-                   const OpndSrc* src = nullptr);
+                   const OpndSrc* src = nullptr, const PrepFuse* pf = nullptr);
+// Whether an EPI_PART launch of w can carry a PrepFuse (split-K kernel, staged
+// operand, whole 256-row output superblocks per workgroup row group).
+bool sh_gemv_prep_fusable(const QMat& w);
 // Superblocks per split when the EPI_PART launch of w takes the split-K kernel
 // (which accepts OPND_ROWS / OPND_FA), else 0.
 uint32_t sh_gemv_fusable(const QMat& w);

@@ -6,6 +6,12 @@ __device__ __forceinline__ float sh_wave_sum(float v) {
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
   return v;
 }
+// Sum of squares of a lane's four elements with explicit FMAs, so every prep
+// (kernel or fused into a GEMV) rounds it identically whatever the compiler's
+// contraction choices in the surrounding code.
+__device__ __forceinline__ float sh_sq4(float4 v) {
+  return __builtin_fmaf(v.w, v.w, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.y, v.y, v.x * v.x)));
+}
 __device__ __forceinline__ float sh_wave_max(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   return v;
