@@ -727,12 +727,33 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
 // activation operands stay in registers. With T = 7 a 1792-tile matrix is 256
 // workgroups, one per CU, in a single round. The 8 partial sums of each tile
 // meet in LDS in one round. EPI_STORE and EPI_PART (one split) only.
-template <int T, int NB, int D, int EPI>
+// Fused SwiGLU prep of h superblock j (the PREP_SWIGLU prep kernel's
+// arithmetic with one split: h = silu(gate) * up at the packed gate / up rows
+// of each element, then the down GEMV's operand), one wave per column, by the
+// last workgroup to finish the 32 packed gate / up tiles of j.
+__device__ __forceinline__ void fused_swiglu_sb(const EpiArgs& ea, const PrepFuse& pf, uint32_t j, uint32_t N) {
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave >= N) return;  // wave-uniform
+  const uint32_t col = wave, k = 256 * j + 4 * lane;
+  const float* pc = ea.out + (size_t)col * ea.ldo + 32 * (k / 16) + k % 16;
+  f4v gv = ld_coh4(pc), uv = ld_coh4(pc + 16);
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(gv), "+v"(uv) : : "memory");
+  float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = make_float4(0.f, 0.f, 0.f, 0.f);
+  g.x += gv[0]; g.y += gv[1]; g.z += gv[2]; g.w += gv[3];
+  u.x += uv[0]; u.y += uv[1]; u.z += uv[2]; u.w += uv[3];
+  const float4 v = make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
+                               (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
+  sh_operand_store_sb(v, pf.K, j, col, pf.bx, pf.xs, pf.cs);
+}
+
+template <int T, int NB, int D, int EPI, bool FS = false>
 __global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
                                                        const uint16_t* __restrict__ Bx,
                                                        const uint16_t* __restrict__ XS,
-                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea) {
+                                                       const float* __restrict__ CS, uint32_t N, EpiArgs ea,
+                                                       PrepFuse pf) {
   static_assert(EPI == EPI_STORE || EPI == EPI_PART, "deep-ring GEMV: store epilogues only");
+  static_assert(!FS || EPI == EPI_PART, "fused SwiGLU prep: gate / up sums");
   constexpr int U = NB * T;
   __shared__ f4 red[T][GW][64];
   const int lane = threadIdx.x & 63;
@@ -777,7 +798,34 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict_
     float o[4];
     col_sum4(v, nf, o);
     const uint32_t tile = tile0 + wave;
-    if (tile < tiles && r < 8 && (uint32_t)r < N) epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
+    if (tile < tiles && r < 8 && (uint32_t)r < N) {
+      if (FS) st_coh4(ea.out + (size_t)r * ea.ldo + tile * 16 + 4 * g, make_float4(o[0], o[1], o[2], o[3]));
+      else epilogue4<EPI>(ea, tile * 16 + 4 * g, (uint32_t)r, o);
+    }
+  }
+  if (FS) {
+    // Arrival at the (one or two) h superblocks this workgroup's packed tiles
+    // touch: packed tile p holds rows of h tile p / 2, so superblock j is
+    // packed tiles 32 j .. 32 j + 31, workgroups 32 j / T .. (32 j + 31) / T.
+    __shared__ uint32_t s_last[2];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const uint32_t j0 = tile0 / 32, j1 = (tile0 + T - 1) / 32;
+    if (threadIdx.x < 2) {
+      const uint32_t j = threadIdx.x == 0 ? j0 : j1;
+      uint32_t last = 0;
+      if (threadIdx.x == 0 || j1 != j0) {
+        const uint32_t wg_first = 32 * j / T, wg_last = min((32 * j + 31) / T, gridDim.x - 1);
+        uint32_t* cnt = pf.cnt + (size_t)j * SH_SB_CNT_STRIDE;
+        const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old + 1 == wg_last - wg_first + 1;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      s_last[threadIdx.x] = last;
+    }
+    __syncthreads();
+    if (s_last[0]) fused_swiglu_sb(ea, pf, j0, N);
+    if (s_last[1]) fused_swiglu_sb(ea, pf, j1, N);
   }
 }
 
@@ -1333,29 +1381,33 @@ uint32_t sh_gemv_ring_t(const QMat& w) {
 // Weight units in flight per wave: 2 and 3 time alike on 28672 x 4096
 // (16.3 / 16.4 us), 4 and more slower (16.8 us at 4, 19 us at 6).
 constexpr int RING_D = 3;
-template <int EPI>
+template <int EPI, bool FS = false>
 static void launch_q4t(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                       const EpiArgs& ea, uint32_t T) {
+                       const EpiArgs& ea, uint32_t T, const PrepFuse& pf = PrepFuse{}) {
   (void)T;  // 7 (sh_gemv_ring_t)
   const dim3 grid(w.tiles / 7);
   if (w.K == 4096)
-    hipLaunchKernelGGL((k_gemv_q4t<7, 2, RING_D, EPI>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 16u, bx, xs,
-                       ea.cs, N, ea);
+    hipLaunchKernelGGL((k_gemv_q4t<7, 2, RING_D, EPI, FS>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 16u, bx,
+                       xs, ea.cs, N, ea, pf);
   else
-    hipLaunchKernelGGL((k_gemv_q4t<7, 1, RING_D, EPI>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 8u, bx, xs,
-                       ea.cs, N, ea);
+    hipLaunchKernelGGL((k_gemv_q4t<7, 1, RING_D, EPI, FS>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 8u, bx,
+                       xs, ea.cs, N, ea, pf);
 }
 
 int sh_gemv_ring_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                        EpiKind epi, const EpiArgs& ea, const char* tag) {
+                        EpiKind epi, const EpiArgs& ea, const char* tag, const PrepFuse* swiglu) {
   SH_CHECK(N >= 1 && N <= 8, SH_ERR_ARG, "gemv chunk N=%u outside [1,8]", N);
   SH_CHECK(ea.cs, SH_ERR_ARG, "gemv: activation scales missing");
   const uint32_t T = sh_gemv_ring_t(w);
   SH_CHECK(T && (epi == EPI_STORE || epi == EPI_PART), SH_ERR_ARG, "gemv: this launch does not take the ring kernel");
   SH_CHECK(epi != EPI_PART || ea.part_cap >= 1, SH_ERR_CAPACITY, "gemv: no room for the partial sums");
+  SH_CHECK(!swiglu || (epi == EPI_PART && swiglu->K * 2 == w.tiles * 16 && swiglu->K % 256 == 0 &&
+                       swiglu->K / 256 <= SH_SB_CNT && swiglu->cnt && swiglu->bx && swiglu->xs && swiglu->cs),
+           SH_ERR_ARG, "gemv: the fused SwiGLU prep does not fit this launch");
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   if (epi == EPI_STORE) launch_q4t<EPI_STORE>(e, w, bx, xs, N, ea, T);
+  else if (swiglu) launch_q4t<EPI_PART, true>(e, w, bx, xs, N, ea, T, *swiglu);
   else launch_q4t<EPI_PART>(e, w, bx, xs, N, ea, T);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, tag, w.alg_bytes, ev);

@@ -810,6 +810,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       pending_ld = po.ldo;
     }
     OpndSrc dsrc;  // down reads h itself when it takes the split-K kernel
+    bool down_ready = false;  // the gate/up kernel built the down operand (set 0)
     if (fuse_rp) {
       const OpndSrc rs = resid_src(w.resid2, w.resid, L.ffn_norm);
       EpiArgs s2 = sw;
@@ -821,11 +822,19 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     } else if (!prepped && (rc = resid_prep(L.ffn_norm))) {
       return rc;
     } else if (swiglu_epilogue() && sh_gemv_ring_t(L.wgu)) {
-      // whole sums from the deep-ring kernel (one split); SwiGLU in the down prep
+      // whole sums from the deep-ring kernel (one split); SwiGLU in the down
+      // prep, or (reading set 1) in the kernel's own last workgroups, which
+      // write the down operand into set 0
       EpiArgs pg = part_args(L.wgu);
       set_norm(pg);
-      if ((rc = sh_gemv_ring_launch(e, L.wgu, cur.bx, cur.xs, nc, EPI_PART, pg, "gemv_gate_up"))) return rc;
+      PrepFuse sf;
+      sf.bx = w.bx; sf.xs = w.xs; sf.cs = w.cs; sf.cnt = w.sb_cnt; sf.K = m->ff;
+      const bool fuse_sw = fuse_pp && prepped;
+      if ((rc = sh_gemv_ring_launch(e, L.wgu, cur.bx, cur.xs, nc, EPI_PART, pg, "gemv_gate_up",
+                                    fuse_sw ? &sf : nullptr)))
+        return rc;
       pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = 1; pr.part_ld = pg.ldo;
+      down_ready = fuse_sw;
     } else if (swiglu_epilogue()) {
       // whole sums in one kernel, h = silu(gate) * up in its epilogue
       set_norm(sw);
@@ -841,7 +850,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     }
     prepped = false;
     pr.K = m->ff; pr.norm_w = nullptr;
-    if (dsrc.kind == OPND_STAGED && (rc = sh_prep_launch(e, pr))) return rc;
+    if (dsrc.kind == OPND_STAGED && !down_ready && (rc = sh_prep_launch(e, pr))) return rc;
     cur = set0;
     EpiArgs pd = part_args(L.wdown);
     const float* next_norm = l + 1 < m->n_layer ? m->layers[l + 1].attn_norm : (want_logits ? m->out_norm : nullptr);

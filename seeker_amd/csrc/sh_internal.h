@@ -247,10 +247,13 @@ size_t sh_gemv_part_floats(const QMat& w);
 // Tiles per workgroup of the deep-ring whole-K kernel for w, or 0 when w does
 // not take it (Q4_K with enough row tiles to fill the chip; SH_RING=0 turns it
 // off). sh_gemv_ring_launch: y = W x through that kernel, EPI_STORE or
-// EPI_PART (one split, whole sums).
+// EPI_PART (one split, whole sums). With swiglu (EPI_PART of the packed
+// gate / up matrix), the last workgroup of each 256-element superblock of h
+// also builds the down GEMV's operand of silu(gate) * up there (swiglu->bx,
+// xs, cs, cnt; K = the FFN width), as the PREP_SWIGLU prep kernel does.
 uint32_t sh_gemv_ring_t(const QMat& w);
 int sh_gemv_ring_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
-                        EpiKind epi, const EpiArgs& ea, const char* tag);
+                        EpiKind epi, const EpiArgs& ea, const char* tag, const PrepFuse* swiglu = nullptr);
 // y = W x for N <= SH_MAX_COLS columns (operand groups of 8, Q4_K) in one pass
 // over W: EPI_PART (partials [split][8 ceil(N/8)][ldo]; *nparts = splits) or
 // EPI_STORE. The operand of group g starts at g times one group's size.

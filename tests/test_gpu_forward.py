@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 SHAPES = {
     "tiny_q8": S.TINY_TARGET,
     "gqa_q4k": S.LlamaShape(2, 1024, 8, 2, 2048, 4000, 512, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K),
-    "ffn8b_q4k": S.LlamaShape(1, 1024, 8, 2, 14336, 4000, 512, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K),
+    "ffn8b_q4k": S.LlamaShape(1, 2048, 16, 4, 14336, 4000, 512, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K),
 }
 
 
