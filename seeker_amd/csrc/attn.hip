@@ -20,6 +20,7 @@
 // (deterministic) per column and builds the Wo activation operand.
 #include <cfloat>
 #include <cstdlib>
+#include <string>
 
 #include "sh_internal.h"
 #include "sh_operand.h"
@@ -27,6 +28,8 @@
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 struct alignas(16) u32x4a { uint32_t x, y, z, w; };
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
 __device__ __forceinline__ h8 ld_h8(const uint16_t* p) { return __builtin_bit_cast(h8, *(const u32x4a*)p); }
 __device__ __forceinline__ f4 mfma16a(h8 a, h8 b, f4 c) {
@@ -261,6 +264,198 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
   if (g == 0) *(float4*)(dst + HD) = make_float4(M, L, 0.f, 0.f);
 }
 
+// Workgroup = (kv head, key split of 32 NKB keys, 32 query rows) of NKB
+// waves; wave w takes the 32-key block w of the split for BOTH 16-row groups,
+// so each K and V fragment is loaded once and feeds both groups' MFMAs (k_fa
+// reads them once per row group). The NKB key blocks then merge in LDS, every
+// wave finishing some of the 32 rows, and the split's (O, m, l) rows go to the
+// partial buffer in the layout k_fa writes (k_fa_combine reads either).
+template <int HD, int NKB, bool DMASK>
+__global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                  const uint16_t* __restrict__ vc, uint32_t max_seq, uint32_t n_head,
+                                                  uint32_t N, uint32_t gqa, FaArgs fa, float scale,
+                                                  float* __restrict__ part) {
+  constexpr int NC = HD / 32, DT = HD / 16, ROWS = 32;
+  constexpr uint32_t SPLIT_KEYS = 32 * NKB, PS = sh_fa_part_stride(HD);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const uint32_t kh = blockIdx.x, split = blockIdx.y;
+  const uint32_t n_splits = gridDim.y;
+  const uint32_t kbase0 = fa.dbase ? *fa.dbase : 0u;
+  const uint32_t kvlen = fa.kvlen + kbase0, mbase = fa.mask_base + kbase0;
+  if (fa.dbase && split * SPLIT_KEYS >= kvlen) return;  // uniform: past the live keys
+  const uint32_t n_rows = gqa * N;
+  const uint32_t n_rows_pad = gridDim.z * ROWS;
+  const uint32_t Dq = n_head * HD;
+  const uint32_t k_end = min((split + 1) * SPLIT_KEYS, kvlen);
+  const uint32_t key0 = split * SPLIT_KEYS + 32 * wave;
+  const uint32_t key0c = min(key0, max_seq - 32);  // blocks past the split's end read in bounds, masked below
+  const uint16_t* kbase = kc + (size_t)kh * max_seq * HD;
+  const uint16_t* vbase = vc + (size_t)kh * (max_seq / 32) * HD * 32;
+
+  // The workgroup's 32 query rows go to LDS once (one direct global->LDS
+  // load of HD floats per row, rows padded to HD + 4 floats), not to every
+  // wave; then K and V of the wave's block, all before any wait, so the block
+  // costs one memory latency.
+  __shared__ float sq[ROWS][HD + 4];
+  for (int i = wave; i < ROWS; i += NKB) {
+    const uint32_t rho = blockIdx.z * ROWS + i;
+    const uint32_t rr = rho < n_rows ? rho : 0;  // rows past the end read row 0 and are zeroed below
+    const float* src = q + (size_t)(rr % N) * Dq + (size_t)(kh * gqa + rr / N) * HD + 4 * lane;
+    if (lane < HD / 4) __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)&sq[i][0], 16, 0, 0);
+  }
+  uint32_t col[2];
+  bool ok[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t rho = blockIdx.z * ROWS + 16 * h + r;
+    ok[h] = rho < n_rows;
+    col[h] = ok[h] ? rho % N : 0;
+  }
+  h8 kop[2][NC], vop[DT];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) kop[kt][c] = ld_h8(kbase + (size_t)(key0c + 16 * kt + r) * HD + 8 * g + 32 * c);
+  {
+    const uint16_t* vp = vbase + (size_t)(key0c / 32) * HD * 32 + (size_t)r * 32 + 8 * g;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vop[dt] = ld_h8(vp + (size_t)dt * 16 * 32);
+  }
+  uint64_t cm[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) cm[h] = DMASK ? fa.masks[col[h]] : col_mask(fa, col[h]);
+  __builtin_amdgcn_s_waitcnt(0);  // the direct LDS loads (the compiler does not track them), K and V
+  __syncthreads();
+  float4 qraw[2][NC][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float* qs = &sq[16 * h + r][8 * g];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qraw[h][c][0] = *(const float4*)(qs + 32 * c);
+      qraw[h][c][1] = *(const float4*)(qs + 32 * c + 4);
+    }
+  }
+
+  __shared__ float sm[NKB][ROWS], sl[NKB][ROWS];
+  __shared__ float4 so[NKB][ROWS][HD / 4 + 1];
+  const bool tail = key0 + 32 > k_end || key0 + 32 > mbase;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // Q^T operand of row group h, each row scaled by a power of two (max|q s|
+    // in [2^9, 2^10)) so the f16 low halves stay normal.
+    h8 qhi[NC], qlo[NC];
+    float rscale;
+    {
+      const float z = ok[h] ? 1.0f : 0.0f;
+      float x[NC][8];
+      float mx = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float4 a = qraw[h][c][0], b = qraw[h][c][1];
+        x[c][0] = a.x * z; x[c][1] = a.y * z; x[c][2] = a.z * z; x[c][3] = a.w * z;
+        x[c][4] = b.x * z; x[c][5] = b.y * z; x[c][6] = b.z * z; x[c][7] = b.w * z;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(x[c][t]));
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      int ex = 0;
+      if (mx > 0.f && mx < INFINITY) {
+        frexpf(mx, &ex);
+        ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+      }
+      const float s = ldexpf(1.0f, 10 - ex);
+      rscale = scale * ldexpf(1.0f, ex - 10);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x[c][t] *= s;
+        split8(x[c], qhi[c], qlo[c]);
+      }
+    }
+    // S^T[key][row] for keys key0 + 16 kt + 4 g + j
+    f4 sacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        acc = mfma16a(kop[kt][c], qhi[c], acc);
+        acc = mfma16a(kop[kt][c], qlo[c], acc);
+      }
+      sacc[kt] = acc;
+    }
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v = sacc[kt][j] * rscale;
+        if (tail) {
+          const uint32_t key = key0 + 16 * kt + 4 * g + j;
+          bool vis = key < k_end;
+          if (vis && key >= mbase) vis = (cm[h] >> (key - mbase)) & 1ull;
+          if (!vis) v = -INFINITY;
+        }
+        sv[4 * kt + j] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // probabilities carry a 2^12 factor (keeps their f16 low halves normal);
+    // it cancels in O / l because l is summed from the same scaled values
+    const bool none = mx == -INFINITY;
+    float p[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : expf(sv[t] - mx) * 4096.0f;
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ps += p[t];
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    h8 phi, plo;
+    split8(p, phi, plo);
+    const int row = 16 * h + r;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      f4 o = {0.f, 0.f, 0.f, 0.f};
+      o = mfma16a(vop[dt], phi, o);
+      o = mfma16a(vop[dt], plo, o);
+      so[wave][row][4 * dt + g] = make_float4(o[0], o[1], o[2], o[3]);
+    }
+    if (g == 0) { sm[wave][row] = mx; sl[wave][row] = ps; }
+  }
+  __syncthreads();
+  // Merge the key blocks in key-block order: a row's d are spread over HD / 8
+  // lanes (8 each), RPW rows per wave and pass.
+  constexpr int LPR = HD / 8, RPW = 64 / LPR;
+  const int dq = 2 * (lane % LPR);
+  for (int row = RPW * wave + lane / LPR; row < ROWS; row += RPW * NKB) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < NKB; ++b) M = fmaxf(M, sm[b][row]);
+    float L = 0.f;
+    float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+#pragma unroll
+    for (int b = 0; b < NKB; ++b) {
+      const float mb = sm[b][row];
+      const float f = mb == -INFINITY ? 0.f : expf(mb - M);
+      L += sl[b][row] * f;
+      const float4 a = so[b][row][dq], c = so[b][row][dq + 1];
+      o0.x += a.x * f; o0.y += a.y * f; o0.z += a.z * f; o0.w += a.w * f;
+      o1.x += c.x * f; o1.y += c.y * f; o1.z += c.z * f; o1.w += c.w * f;
+    }
+    float* dst = part + (((size_t)kh * n_splits + split) * n_rows_pad + blockIdx.z * ROWS + row) * PS;
+    *(float4*)(dst + 4 * dq) = o0;
+    *(float4*)(dst + 4 * dq + 4) = o1;
+    if (lane % LPR == 0) *(float4*)(dst + HD) = make_float4(M, L, 0.f, 0.f);
+  }
+}
+
 // Combine the key splits (in split order) for one 256-wide superblock of the
 // attention output of one column, write attn [N][Dq] f32 and that superblock of
 // the Wo activation operand (columns col0 + j of the chunk). One wave per
@@ -296,10 +491,37 @@ static uint32_t fa_split_keys(uint32_t n_kv, uint32_t kvlen, uint32_t n_qg) {
   return (size_t)n_kv * n_qg * ((kvlen + 255) / 256) >= 128 ? 256 : 128;
 }
 
+// Two row groups take k_fa2 (SH_FA=1: k_fa).
+static bool fa2_enabled() {
+  static const bool v = [] {
+    const char* s = getenv("SH_FA");
+    return !(s && std::string(s) == "1");
+  }();
+  return v;
+}
+
 template <int HD, int NQG>
 static void fa_launch_cfg(uint32_t split_keys, dim3 grid, hipStream_t st, const float* q, const uint16_t* kc,
                           const uint16_t* vc, uint32_t max_seq, uint32_t n_head, uint32_t N, uint32_t gqa,
                           const FaArgs& fa, float scale, float* part) {
+  if (NQG == 2 && fa2_enabled()) {
+    if (split_keys == 256) {
+      if (fa.masks)
+        hipLaunchKernelGGL((k_fa2<HD, 8, true>), grid, dim3(512), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                           scale, part);
+      else
+        hipLaunchKernelGGL((k_fa2<HD, 8, false>), grid, dim3(512), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                           scale, part);
+    } else {
+      if (fa.masks)
+        hipLaunchKernelGGL((k_fa2<HD, 4, true>), grid, dim3(256), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                           scale, part);
+      else
+        hipLaunchKernelGGL((k_fa2<HD, 4, false>), grid, dim3(256), 0, st, q, kc, vc, max_seq, n_head, N, gqa, fa,
+                           scale, part);
+    }
+    return;
+  }
   constexpr int NKB = 4;
   const dim3 block(64 * NQG * NKB);
   if (fa.masks) {  // columns beyond 8: masks from device memory

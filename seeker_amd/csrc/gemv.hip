@@ -625,10 +625,19 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
       for (int m = 0; m < 8; ++m) bq[m] = dynB[(b * 9 + m) * 64 + lane];
       bm = dynB[(b * 9 + 8) * 64 + lane];
       c = sC[b * 8 + (lane & 7)];
-    } else {
+    } else if (N >= 8) {
 #pragma unroll
       for (int m = 0; m < 8; ++m) bq[m] = as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8));
       bm = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
+      c = CS[b * 8 + (lane & 7)];
+    } else {
+      // lanes of columns >= N load nothing (their outputs are never stored):
+      // a 1-column launch fetches 1/8 of the operand
+      const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+      const bool live = (uint32_t)(lane & 7) < N;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) bq[m] = live ? as_h8(ld16(Bx + ((size_t)(b * 8 + m) * 64 + lane) * 8)) : z;
+      bm = live ? as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8)) : z;
       c = CS[b * 8 + (lane & 7)];
     }
   };

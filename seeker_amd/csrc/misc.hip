@@ -163,12 +163,13 @@ __device__ __forceinline__ unsigned long long amax_key(float v, uint32_t idx) {
   return ((unsigned long long)b << 32) | (unsigned long long)(~idx);
 }
 
-__global__ void k_amax_init(unsigned long long* keys, uint32_t N) {
-  if (threadIdx.x < N) keys[threadIdx.x] = 0ull;
-}
-
-__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, uint32_t V,
-                                                unsigned long long* keys) {
+// One kernel per argmax: each workgroup folds its 2048-logit block into the
+// column's key (atomic max), then counts itself in; the last workgroup to
+// arrive writes the ids and clears the keys and the counter for the next
+// launch (zero at allocation, so graph replays need no memset). The counter
+// lives right after the SH_MAX_COLS keys.
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, uint32_t V, uint32_t N,
+                                                unsigned long long* keys, uint32_t* __restrict__ out) {
   const uint32_t col = blockIdx.y;
   const float* row = logits + (size_t)col * V;
   unsigned long long best = 0ull;
@@ -187,27 +188,34 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
     best = o > best ? o : best;
   }
   __shared__ unsigned long long wb[4];
+  __shared__ uint32_t s_last;
   if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w) best = wb[w] > best ? wb[w] : best;
-    atomicMax(keys + col, best);
+    // the returned value orders the max before the arrival
+    const unsigned long long prev =
+        __hip_atomic_fetch_max(keys + col, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" : : "v"(prev) : "memory");
+    uint32_t* cnt = (uint32_t*)(keys + SH_MAX_COLS);
+    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    s_last = arrived == gridDim.x * gridDim.y;
+    if (s_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-__global__ void k_amax_finish(const unsigned long long* keys, uint32_t N, uint32_t* out) {
-  const uint32_t j = threadIdx.x;
-  if (j < N) out[j] = keys[j] == 0ull ? 0u : ~(uint32_t)(keys[j] & 0xFFFFFFFFull);
+  __syncthreads();
+  if (s_last && threadIdx.x < N) {
+    const unsigned long long k = __hip_atomic_load(keys + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    out[threadIdx.x] = k == 0ull ? 0u : ~(uint32_t)(k & 0xFFFFFFFFull);
+    __hip_atomic_store(keys + threadIdx.x, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids) {
-  SH_CHECK(N >= 1 && N <= 64, SH_ERR_ARG, "argmax N=%u", N);
+  SH_CHECK(N >= 1 && N <= SH_MAX_COLS, SH_ERR_ARG, "argmax N=%u", N);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL(k_amax_init, dim3(1), dim3(64), 0, e->stream, keys, N);
-  hipLaunchKernelGGL(k_argmax, dim3((V + 2047) / 2048, N), dim3(256), 0, e->stream, logits, V, keys);
-  hipLaunchKernelGGL(k_amax_finish, dim3(1), dim3(64), 0, e->stream, keys, N, out_ids);
+  hipLaunchKernelGGL(k_argmax, dim3((V + 2047) / 2048, N), dim3(256), 0, e->stream, logits, V, N, keys, out_ids);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "argmax", 4.0 * V * N, ev);
   return SH_OK;

@@ -488,7 +488,7 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       dalloc(&w.xs, xs_elems) ||
       dalloc(&w.q, C * m->d) || dalloc(&w.attn, C * m->d) || dalloc(&w.gpart, gpart_floats) ||
       dalloc(&w.h, C * m->ff) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
-      dalloc(&w.tokens, C + 64) || dalloc(&w.amax, C) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
+      dalloc(&w.tokens, C + 64) || dalloc(&w.amax, C + 8) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
       dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
       dalloc(&w.cs2, sh_grp_cs(m->d)) || dalloc(&w.ssq2, sh_grp_cs(m->d)) || dalloc(&w.sb_cnt, SH_SB_CNT * SH_SB_CNT_STRIDE))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
@@ -496,7 +496,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   w.gpart_floats = gpart_floats;
   if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess ||
       hipMemset(w.xs2, 0, sh_grp_xs(m->d) * 2) != hipSuccess || hipMemset(w.bx2, 0, sh_grp_bx(m->d) * 2) != hipSuccess ||
-      hipMemset(w.sb_cnt, 0, SH_SB_CNT * SH_SB_CNT_STRIDE * 4) != hipSuccess)
+      hipMemset(w.sb_cnt, 0, SH_SB_CNT * SH_SB_CNT_STRIDE * 4) != hipSuccess ||
+      hipMemset(w.amax, 0, (C + 8) * 8) != hipSuccess)
     FAIL(SH_ERR_HIP, "workspace clear failed");
   if ((fail = ensure_rope(m, std::max<uint32_t>(m->n_ctx, 1024)))) FAIL(fail, "%s", sh_last_error());
   if (hipDeviceSynchronize() != hipSuccess) FAIL(SH_ERR_HIP, "model upload failed");

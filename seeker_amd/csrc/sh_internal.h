@@ -106,7 +106,7 @@ struct Workspace {
   float* fa_part = nullptr;   // flash-attn split partials
   float* gpart = nullptr;     // GEMV split-K partials
   uint32_t* tokens = nullptr; // [cols + 16] device token ids
-  unsigned long long* amax = nullptr;  // [cols] packed argmax keys
+  unsigned long long* amax = nullptr;  // [SH_MAX_COLS] packed argmax keys, then the argmax arrival counter (zeroed)
   float* cs = nullptr;        // [max(K)/256][8] inverse activation scales of the current B operand
   float* ssq = nullptr;       // [max(K)/256][8] per-superblock sums of squares of the normalized input
   size_t fa_part_floats = 0;
