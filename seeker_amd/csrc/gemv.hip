@@ -349,9 +349,10 @@ constexpr uint32_t WIDE_MAX_UNITS = 12;  // units per wave (T * S) beyond which 
 // (one wave per (superblock, column)): from f32 rows (OPND_ROWS) or by
 // combining attention split partials (OPND_FA), with the same arithmetic as
 // the prep / combine kernels; the first weight units are already in flight.
-// 16-byte agent-coherent store / loads (sc1: past the non-coherent per-XCD
-// L2) for data that another workgroup of the same kernel reads. After
-// ld_coh4 x n, coh_wait ties the results to a vmcnt(0) wait before any use.
+// 16-byte agent-coherent store / load (sc1: past the non-coherent per-XCD L2)
+// for data that another workgroup of the same kernel reads. The loads are not
+// tracked by the compiler: their results pass through an asm statement
+// holding "s_waitcnt vmcnt(0)" (values as "+v" operands) before any use.
 typedef float f4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void st_coh4(float* p, float4 v) {
   const f4v w = {v.x, v.y, v.z, v.w};
@@ -1342,16 +1343,19 @@ static void launch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const ui
 
 // Streaming policy: about 512 workgroups of 8 waves (two per CU), i.e. T =
 // tiles / 512 rounded down to a power of two in [1, 8] (even for SwiGLU so a
-// workgroup owns whole gate/up pairs). An OPND_RESID launch rebuilds the
-// operand in every workgroup (residual + all pending partials), so it aims at
-// about 256 workgroups instead (draft gate/up, 1024 tiles: T = 4, 25 % faster
-// than T = 2, measured).
+// workgroup owns whole gate/up pairs); QKV about 128. An OPND_RESID launch
+// rebuilds the operand in every workgroup (residual + all pending partials),
+// so it aims at about 256 workgroups (draft gate/up, 1024 tiles: T = 4, 25 %
+// faster than T = 2, measured).
 template <int EPI>
 static void dispatch_q4s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                          const EpiArgs& ea, const OpndSrc& src) {
   uint32_t t = gemv_kernel_choice() == 1 ? gemv_t_override() : 0;
   if (!t) {
-    const uint32_t target = src.kind == OPND_RESID ? 256 : 512;
+    // QKV: every workgroup reads the whole operand (144 KB at K = 4096) for T
+    // tiles, so fewer, wider workgroups win: the 8B QKV (384 tiles) is 8 %
+    // faster at T = 2 than at 1 (T = 4 is slower).
+    const uint32_t target = src.kind == OPND_RESID ? 256 : (EPI == EPI_QKV ? 128 : 512);
     t = 1;
     while (t < 8 && w.tiles / (2 * t) >= target) t *= 2;
   }
