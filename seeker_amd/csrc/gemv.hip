@@ -1268,20 +1268,21 @@ static uint32_t gemv_d_override() {
   static const uint32_t v = (uint32_t)env_u32("SH_GEMV_D");
   return v;
 }
-// D = weight units in flight per wave (SH_GEMV_D=2|4|8; default 4).
+// D = weight units in flight per wave (SH_GEMV_D=2|4|8; default 2: the 8B
+// down is 6 % faster than at 4 and 15 % faster than at 8, Wo alike).
 template <int T, int S, int EPI, int SRC, bool FP>
 static void launch_q4w_fp(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                           const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse& pf) {
   const dim3 grid((w.tiles + WV * T - 1) / (WV * T), p.KS);
   const uint32_t d = gemv_d_override();
-  if (d == 2)
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 2, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
+  if (d == 4)
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 4, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
                        w.K / 256, bx, xs, ea.cs, N, ea, src, pf);
   else if (d == 8)
     hipLaunchKernelGGL((k_gemv_q4w<T, S, 8, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
                        w.K / 256, bx, xs, ea.cs, N, ea, src, pf);
   else
-    hipLaunchKernelGGL((k_gemv_q4w<T, S, 4, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
+    hipLaunchKernelGGL((k_gemv_q4w<T, S, 2, EPI, SRC, FP>), grid, dim3(64 * WV), 0, e->stream, w.d, w.tiles,
                        w.K / 256, bx, xs, ea.cs, N, ea, src, pf);
 }
 template <int T, int S, int EPI, int SRC>
@@ -1383,8 +1384,8 @@ static void dispatch_q8(sh_engine* e, const QMat& w, const uint16_t* bx, uint32_
 
 // Deep-ring policy (K of 8 or 16 superblocks): T = 7 when the tiles split
 // evenly into at least 256 workgroups of 7 (one round, one workgroup per CU).
-// Matrices that need several rounds (lm_head) run faster on k_gemv_q4s
-// (measured: 68 us against 72-77 us for 128256 x 4096), as do small ones.
+// At K = 4096, matrices that need several rounds (the 8B lm_head) run faster
+// on k_gemv_q4s (68 us against 72-77 us for 128256 x 4096), as do small ones.
 uint32_t sh_gemv_ring_t(const QMat& w) {
   static const bool off = [] {
     const char* s = getenv("SH_RING");
@@ -1392,6 +1393,9 @@ uint32_t sh_gemv_ring_t(const QMat& w) {
   }();
   if (off || w.type != GGML_Q4_K || (w.K != 2048 && w.K != 4096)) return 0;  // K = 8 NB superblocks
   if (w.tiles % 7 == 0 && w.tiles / 7 >= 256) return 7;
+  // K = 2048 (one superblock per wave) with several rounds of 8 tiles: the
+  // draft's tied lm_head, 45 -> 40 us per launch
+  if (w.K == 2048 && w.tiles / 8 >= 768) return 8;
   return 0;
 }
 
@@ -1401,7 +1405,11 @@ constexpr int RING_D = 3;
 template <int EPI, bool FS = false>
 static void launch_q4t(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                        const EpiArgs& ea, uint32_t T, const PrepFuse& pf = PrepFuse{}) {
-  (void)T;  // 7 (sh_gemv_ring_t)
+  if (T == 8) {  // K = 2048 only (sh_gemv_ring_t)
+    hipLaunchKernelGGL((k_gemv_q4t<8, 1, RING_D, EPI, FS>), dim3((w.tiles + 7) / 8), dim3(64 * GW), 0, e->stream, w.d,
+                       w.tiles, 8u, bx, xs, ea.cs, N, ea, pf);
+    return;
+  }
   const dim3 grid(w.tiles / 7);
   if (w.K == 4096)
     hipLaunchKernelGGL((k_gemv_q4t<7, 2, RING_D, EPI, FS>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 16u, bx,
