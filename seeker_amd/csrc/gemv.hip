@@ -762,7 +762,7 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict_
                                                        const uint16_t* __restrict__ XS,
                                                        const float* __restrict__ CS, uint32_t N, EpiArgs ea,
                                                        PrepFuse pf) {
-  static_assert(EPI == EPI_STORE || EPI == EPI_PART, "deep-ring GEMV: store epilogues only");
+  static_assert(EPI == EPI_STORE || EPI == EPI_PART || EPI == EPI_QKV, "deep-ring GEMV: per-row epilogues only");
   static_assert(!FS || EPI == EPI_PART, "fused SwiGLU prep: gate / up sums");
   constexpr int U = NB * T;
   __shared__ f4 red[T][GW][64];
@@ -1439,6 +1439,29 @@ int sh_gemv_ring_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const u
   return SH_OK;
 }
 
+// QKV through k_gemv_q4t at 2 tiles per workgroup (SH_QKV_RING=0: through
+// k_gemv_q4s). Measured on the 8B verify (384 tiles, K = 4096): 1, 3 and 4
+// tiles per workgroup and windows of 2 or 4 units are all slower.
+static bool qkv_ring_enabled() {
+  static const bool v = [] {
+    const char* s = getenv("SH_QKV_RING");
+    return !(s && std::string(s) == "0");
+  }();
+  return v;
+}
+
+template <int T>
+static void launch_q4t_qkv(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
+                           const EpiArgs& ea) {
+  const dim3 grid(w.tiles / T);
+  if (w.K == 4096)
+    hipLaunchKernelGGL((k_gemv_q4t<T, 2, RING_D, EPI_QKV>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 16u,
+                       bx, xs, ea.cs, N, ea, PrepFuse{});
+  else
+    hipLaunchKernelGGL((k_gemv_q4t<T, 1, RING_D, EPI_QKV>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 8u, bx,
+                       xs, ea.cs, N, ea, PrepFuse{});
+}
+
 bool sh_gemv_resid_fusable(const QMat& w, uint32_t N) {
   // the whole-K kernel with its largest reduction buffer (4 tiles x 32 KB / 4) must fit beside the operand
   return w.type == GGML_Q4_K && w.K % 256 == 0 && N <= 2 && resid_lds_bytes(w.K / 256) + 32768 <= 160 * 1024;
@@ -1480,7 +1503,12 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
         case -1: launch_q4t<EPI_STORE>(e, w, bx, xs, N, ea, rt); break;
         case EPI_STORE: dispatch_q4s<EPI_STORE>(e, w, bx, xs, N, ea, sr); break;
         case EPI_ADD: dispatch_q4s<EPI_ADD>(e, w, bx, xs, N, ea, sr); break;
-        case EPI_QKV: dispatch_q4s<EPI_QKV>(e, w, bx, xs, N, ea, sr); break;
+        case EPI_QKV:
+          if (qkv_ring_enabled() && sr.kind == OPND_STAGED && (w.K == 2048 || w.K == 4096) && w.tiles % 2 == 0)
+            launch_q4t_qkv<2>(e, w, bx, xs, N, ea);
+          else
+            dispatch_q4s<EPI_QKV>(e, w, bx, xs, N, ea, sr);
+          break;
         case EPI_SWIGLU: dispatch_q4s<EPI_SWIGLU>(e, w, bx, xs, N, ea, sr); break;
         case EPI_PART: dispatch_q4s<EPI_PART>(e, w, bx, xs, N, ea, sr); break;
       }
