@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
   // load of HD floats per row, rows padded to HD + 4 floats), not to every
   // wave; then K and V of the wave's block, all before any wait, so the block
   // costs one memory latency.
-  __shared__ float sq[ROWS][HD + 4];
+  __shared__ __align__(16) float sq[ROWS][HD + 4];
   for (int i = wave; i < ROWS; i += NKB) {
     const uint32_t rho = blockIdx.z * ROWS + i;
     const uint32_t rr = rho < n_rows ? rho : 0;  // rows past the end read row 0 and are zeroed below
@@ -328,54 +328,82 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
   for (int h = 0; h < 2; ++h) cm[h] = DMASK ? fa.masks[col[h]] : col_mask(fa, col[h]);
   __builtin_amdgcn_s_waitcnt(0);  // the direct LDS loads (the compiler does not track them), K and V
   __syncthreads();
-  float4 qraw[2][NC][2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float* qs = &sq[16 * h + r][8 * g];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qraw[h][c][0] = *(const float4*)(qs + 32 * c);
-      qraw[h][c][1] = *(const float4*)(qs + 32 * c + 4);
-    }
-  }
 
   __shared__ float sm[NKB][ROWS], sl[NKB][ROWS];
   __shared__ float4 so[NKB][ROWS][HD / 4 + 1];
-  const bool tail = key0 + 32 > k_end || key0 + 32 > mbase;
+  // Q^T operands, prepared once per workgroup (the waves all use the same 32
+  // rows): fragment (h, c) = rows 16 h + r, d = 8 g + 32 c .. + 7 of lane
+  // (g, r), each row scaled by a power of two (max|q s| in [2^9, 2^10)) so the
+  // f16 low halves stay normal, split hi + lo. Wave w prepares fragments w,
+  // w + NKB, ...; partial row maxima and the row factors pass through the
+  // merge buffer, the fragments through the query rows' own LDS.
+  constexpr int NF = 2 * NC, FPW = (NF + NKB - 1) / NKB;
+  float* smx = (float*)&so[0][0][0];  // [NF][64] row maxima of each fragment's 8 d
+  float* srs = smx + NF * 64;         // [2][16] row factors
+  h8* fq = (h8*)&sq[0][0];            // [NF][hi, lo][64]
+  float xq[FPW][8];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    // Q^T operand of row group h, each row scaled by a power of two (max|q s|
-    // in [2^9, 2^10)) so the f16 low halves stay normal.
-    h8 qhi[NC], qlo[NC];
-    float rscale;
-    {
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wave + NKB * i;
+    if (f < NF) {
+      const int h = f / NC, c = f % NC;
       const float z = ok[h] ? 1.0f : 0.0f;
-      float x[NC][8];
+      const float* qs = &sq[16 * h + r][8 * g + 32 * c];
+      const float4 a = *(const float4*)qs, b = *(const float4*)(qs + 4);
+      xq[i][0] = a.x * z; xq[i][1] = a.y * z; xq[i][2] = a.z * z; xq[i][3] = a.w * z;
+      xq[i][4] = b.x * z; xq[i][5] = b.y * z; xq[i][6] = b.z * z; xq[i][7] = b.w * z;
       float mx = 0.f;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const float4 a = qraw[h][c][0], b = qraw[h][c][1];
-        x[c][0] = a.x * z; x[c][1] = a.y * z; x[c][2] = a.z * z; x[c][3] = a.w * z;
-        x[c][4] = b.x * z; x[c][5] = b.y * z; x[c][6] = b.z * z; x[c][7] = b.w * z;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(x[c][t]));
-      }
+      for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(xq[i][t]));
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
+      smx[f * 64 + lane] = mx;
+    }
+  }
+  __syncthreads();  // partial maxima written; every wave is done reading its f32 rows
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wave + NKB * i;
+    if (f < NF) {
+      const int h = f / NC, c = f % NC;
+      float mx = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) mx = fmaxf(mx, smx[(h * NC + cc) * 64 + lane]);
       int ex = 0;
       if (mx > 0.f && mx < INFINITY) {
         frexpf(mx, &ex);
         ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
       }
       const float s = ldexpf(1.0f, 10 - ex);
-      rscale = scale * ldexpf(1.0f, ex - 10);
+      if (c == 0 && g == 0) srs[h * 16 + r] = scale * ldexpf(1.0f, ex - 10);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) x[c][t] *= s;
-        split8(x[c], qhi[c], qlo[c]);
-      }
+      for (int t = 0; t < 8; ++t) xq[i][t] *= s;
+      h8 hi, lo;
+      split8(xq[i], hi, lo);
+      fq[(f * 2) * 64 + lane] = hi;
+      fq[(f * 2 + 1) * 64 + lane] = lo;
     }
+  }
+  __syncthreads();
+  h8 qhi2[2][NC], qlo2[2][NC];
+  float rscale2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qhi2[h][c] = fq[((h * NC + c) * 2) * 64 + lane];
+      qlo2[h][c] = fq[((h * NC + c) * 2 + 1) * 64 + lane];
+    }
+    rscale2[h] = srs[h * 16 + r];
+  }
+  __syncthreads();  // the merge buffer is free again
+
+  const bool tail = key0 + 32 > k_end || key0 + 32 > mbase;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const h8* qhi = qhi2[h];
+    const h8* qlo = qlo2[h];
+    const float rscale = rscale2[h];
     // S^T[key][row] for keys key0 + 16 kt + 4 g + j
     f4 sacc[2];
 #pragma unroll
