@@ -502,7 +502,7 @@ __global__ __launch_bounds__(64) void k_fa_combine(const float* __restrict__ par
   const uint32_t n_splits = dbase ? (*dbase + kv_off + split_keys - 1) / split_keys : n_layout;
   const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
   const uint32_t Dq = n_head * HD, k = 256 * sb + 4 * lane;
-  const float4 v = sh_fa_combine4(part, n_layout, n_splits, n_rows_pad, HD, n_head, gqa, N, sb, col);
+  const float4 v = sh_fa_combine4<2>(part, n_layout, n_splits, n_rows_pad, HD, n_head, gqa, N, sb, col);
   if (k < Dq) *(float4*)(attn + (size_t)(col0 + col) * Dq + k) = v;
   sh_operand_store_sb(v, Dq, sb, col0 + col, bx, xs, cs);
 }

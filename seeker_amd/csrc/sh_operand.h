@@ -105,10 +105,11 @@ __device__ __forceinline__ void sh_operand_store_sb(float4 v, uint32_t K, uint32
 
 // Attention split combine for one lane: output elements 256 sb + 4 lane .. +3
 // of column col (a 256-wide superblock of heads), merging the n_splits key
-// splits of the partial buffer in split order, 16 at a time (every load issued
-// before the first is used, one exp per split). Partial layout:
+// splits of the partial buffer in split order, 16 at a time (the loads of NCH
+// such chunks issued before the first is used, one exp per split). Partial layout:
 // part[((kh * n_layout + split) * rows_pad + rho) * (hd + 4) + {d < hd: O, hd: m,
 // hd + 1: l}], rho = (head % gqa) * N + col. Zero for elements past Dq.
+template <uint32_t NCH = 1>
 __device__ __forceinline__ float4 sh_fa_combine4(const float* __restrict__ part, uint32_t n_layout, uint32_t n_splits,
                                                  uint32_t rows_pad, uint32_t hd, uint32_t n_head, uint32_t gqa,
                                                  uint32_t N, uint32_t sb, uint32_t col) {
@@ -123,31 +124,41 @@ __device__ __forceinline__ float4 sh_fa_combine4(const float* __restrict__ part,
   const float* p = part + (size_t)kh * n_layout * sstride + (size_t)rho * PS;
   float M = -INFINITY, L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t s0 = 0; s0 < n_splits; s0 += CH) {
-    float4 os[CH];
-    float2 ml[CH];
+  // NCH chunks' loads go out together: with 2, a key length just past a
+  // multiple of 16 splits (4104 keys = 17 splits of 256) costs one round trip,
+  // not two (the per-chunk arithmetic is the same for any NCH)
+  for (uint32_t s00 = 0; s00 < n_splits; s00 += NCH * CH) {
+    float4 os[NCH][CH];
+    float2 ml[NCH][CH];
 #pragma unroll
-    for (uint32_t j = 0; j < CH; ++j) {
-      const float* pp = p + (size_t)min(s0 + j, n_splits - 1) * sstride;
-      os[j] = *(const float4*)(pp + d);
-      ml[j] = *(const float2*)(pp + hd);
+    for (uint32_t hh = 0; hh < NCH; ++hh)
+#pragma unroll
+      for (uint32_t j = 0; j < CH; ++j) {
+        const float* pp = p + (size_t)min(s00 + CH * hh + j, n_splits - 1) * sstride;
+        os[hh][j] = *(const float4*)(pp + d);
+        ml[hh][j] = *(const float2*)(pp + hd);
+      }
+#pragma unroll
+    for (uint32_t hh = 0; hh < NCH; ++hh) {
+      const uint32_t s0 = s00 + CH * hh;
+      if (s0 >= n_splits) break;
+      float mc = -INFINITY;
+#pragma unroll
+      for (uint32_t j = 0; j < CH; ++j) mc = fmaxf(mc, ml[hh][j].x);  // repeats of the last split change nothing
+      if (mc == -INFINITY) continue;
+      const float mn = fmaxf(M, mc);
+      const float a = expf(M - mn);  // 0 on the first chunk (M = -inf)
+      acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
+      L *= a;
+#pragma unroll
+      for (uint32_t j = 0; j < CH; ++j) {
+        // 0 for an empty split (m = -inf) and for the clamped repeats past the end
+        const float w = s0 + j < n_splits ? expf(ml[hh][j].x - mn) : 0.0f;
+        acc.x += os[hh][j].x * w; acc.y += os[hh][j].y * w; acc.z += os[hh][j].z * w; acc.w += os[hh][j].w * w;
+        L += ml[hh][j].y * w;
+      }
+      M = mn;
     }
-    float mc = -INFINITY;
-#pragma unroll
-    for (uint32_t j = 0; j < CH; ++j) mc = fmaxf(mc, ml[j].x);  // repeats of the last split change nothing
-    if (mc == -INFINITY) continue;
-    const float mn = fmaxf(M, mc);
-    const float a = expf(M - mn);  // 0 on the first chunk (M = -inf)
-    acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
-    L *= a;
-#pragma unroll
-    for (uint32_t j = 0; j < CH; ++j) {
-      // 0 for an empty split (m = -inf) and for the clamped repeats past the end
-      const float w = s0 + j < n_splits ? expf(ml[j].x - mn) : 0.0f;
-      acc.x += os[j].x * w; acc.y += os[j].y * w; acc.z += os[j].z * w; acc.w += os[j].w * w;
-      L += ml[j].y * w;
-    }
-    M = mn;
   }
   const float il = L > 0.f ? 1.0f / L : 0.f;
   if (!valid) return make_float4(0.f, 0.f, 0.f, 0.f);
