@@ -138,6 +138,17 @@ __device__ __forceinline__ float4 sh_fa_combine4(const float* __restrict__ part,
         os[hh][j] = *(const float4*)(pp + d);
         ml[hh][j] = *(const float2*)(pp + hd);
       }
+    // NCH == 1: the first split of the next chunk comes with these loads, so a
+    // last chunk of one split (4097 keys = 16 splits of 256 + 1) needs no
+    // second round trip
+    float4 ox = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 mlx = make_float2(-INFINITY, 0.f);
+    const bool one_more = NCH == 1 && s00 + CH + 1 == n_splits;
+    if (one_more) {
+      const float* pp = p + (size_t)(s00 + CH) * sstride;
+      ox = *(const float4*)(pp + d);
+      mlx = *(const float2*)(pp + hd);
+    }
 #pragma unroll
     for (uint32_t hh = 0; hh < NCH; ++hh) {
       const uint32_t s0 = s00 + CH * hh;
@@ -158,6 +169,21 @@ __device__ __forceinline__ float4 sh_fa_combine4(const float* __restrict__ part,
         L += ml[hh][j].y * w;
       }
       M = mn;
+    }
+    if (one_more) {
+      // the one-split chunk as the loop above runs it (its clamped repeats
+      // carry weight 0)
+      if (mlx.x != -INFINITY) {
+        const float mn = fmaxf(M, mlx.x);
+        const float a = expf(M - mn);
+        acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
+        L *= a;
+        const float w = expf(mlx.x - mn);
+        acc.x += ox.x * w; acc.y += ox.y * w; acc.z += ox.z * w; acc.w += ox.w * w;
+        L += mlx.y * w;
+        M = mn;
+      }
+      break;
     }
   }
   const float il = L > 0.f ? 1.0f / L : 0.f;
