@@ -12,11 +12,14 @@ __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_c
 // same per-element arithmetic as the Q4_K / Q8_0 dequant (run.rs:4212-4303).
 __global__ void k_embed(const uint8_t* __restrict__ embd, int type, uint32_t d, size_t row_bytes,
                         const uint32_t* __restrict__ tokens, uint32_t V, float* __restrict__ resid) {
+  // workgroup (token j, 256 elements from blockIdx.y): one element per thread,
+  // so the row costs one round trip after the token id
   const uint32_t j = blockIdx.x;
   uint32_t tok = tokens[j];
   if (tok >= V) tok = V - 1;  // ids are validated on the host; clamp keeps reads in bounds
   const uint8_t* row = embd + (size_t)tok * row_bytes;
-  for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
+  const uint32_t i = blockIdx.y * 256 + threadIdx.x;
+  if (i < d) {
     float y;
     if (type == GGML_Q4_K) {
       const uint8_t* blk = row + (size_t)(i / 256) * 144;
@@ -45,8 +48,8 @@ __global__ void k_embed(const uint8_t* __restrict__ embd, int type, uint32_t d, 
 int sh_embed_launch(sh_engine* e, const sh_model* m, const uint32_t* tokens, uint32_t N, float* resid) {
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL(k_embed, dim3(N), dim3(256), 0, e->stream, m->embd_raw, m->embd_type, m->d, m->embd_row_bytes,
-                     tokens, m->V, resid);
+  hipLaunchKernelGGL(k_embed, dim3(N, (m->d + 255) / 256), dim3(256), 0, e->stream, m->embd_raw, m->embd_type, m->d,
+                     m->embd_row_bytes, tokens, m->V, resid);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "embed", (double)N * m->embd_row_bytes, ev);
   return SH_OK;
@@ -173,13 +176,20 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
   const uint32_t col = blockIdx.y;
   const float* row = logits + (size_t)col * V;
   unsigned long long best = 0ull;
-  const uint32_t per = 2048;
+  constexpr uint32_t PER_T = 8, per = 256 * PER_T;
   const uint32_t i0 = blockIdx.x * per;
   const uint32_t i1 = min(i0 + per, V);
-  for (uint32_t i = i0 + threadIdx.x; i < i1; i += 256) {
-    const float v = row[i];
-    if (v == v) {
-      const unsigned long long k = amax_key(v, i);
+  // every load of the thread goes out before the first compare (one round trip)
+  float v[PER_T];
+#pragma unroll
+  for (uint32_t j = 0; j < PER_T; ++j) {
+    const uint32_t i = i0 + threadIdx.x + 256 * j;
+    v[j] = i < i1 ? row[i] : NAN;  // NaN is never selected
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < PER_T; ++j) {
+    if (v[j] == v[j]) {
+      const unsigned long long k = amax_key(v[j], i0 + threadIdx.x + 256 * j);
       best = k > best ? k : best;
     }
   }
