@@ -2,9 +2,27 @@
 #pragma once
 #include "sh_internal.h"
 
+// Cross-lane steps through DPP (no LDS round trip, unlike __shfl_xor):
+// quad_perm(1,0,3,2) and quad_perm(2,3,0,1) pair lanes l ^ 1 and l ^ 2;
+// row_half_mirror (lane 7 - l of each 8) and row_mirror (15 - l of each 16)
+// then pair the quads and the halves of a row once every quad, resp. half,
+// holds one value in all its lanes. Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float sh_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int SH_DPP_XOR1 = 0xB1, SH_DPP_XOR2 = 0x4E, SH_DPP_HALF_MIRROR = 0x141, SH_DPP_MIRROR = 0x140;
+__device__ __forceinline__ float sh_lane(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// Sum over the wave, the same value in every lane: rows of 16 by DPP, then
+// the four row sums as (r0 + r1) + (r2 + r3).
 __device__ __forceinline__ float sh_wave_sum(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+  v += sh_dpp<SH_DPP_XOR1>(v);
+  v += sh_dpp<SH_DPP_XOR2>(v);
+  v += sh_dpp<SH_DPP_HALF_MIRROR>(v);
+  v += sh_dpp<SH_DPP_MIRROR>(v);
+  return (sh_lane(v, 0) + sh_lane(v, 16)) + (sh_lane(v, 32) + sh_lane(v, 48));
 }
 // Sum of squares of a lane's four elements with explicit FMAs, so every prep
 // (kernel or fused into a GEMV) rounds it identically whatever the compiler's
@@ -13,8 +31,11 @@ __device__ __forceinline__ float sh_sq4(float4 v) {
   return __builtin_fmaf(v.w, v.w, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.y, v.y, v.x * v.x)));
 }
 __device__ __forceinline__ float sh_wave_max(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
+  v = fmaxf(v, sh_dpp<SH_DPP_XOR1>(v));
+  v = fmaxf(v, sh_dpp<SH_DPP_XOR2>(v));
+  v = fmaxf(v, sh_dpp<SH_DPP_HALF_MIRROR>(v));
+  v = fmaxf(v, sh_dpp<SH_DPP_MIRROR>(v));
+  return fmaxf(fmaxf(sh_lane(v, 0), sh_lane(v, 16)), fmaxf(sh_lane(v, 32), sh_lane(v, 48)));
 }
 
 // Operands of more than 8 columns come in groups of 8: column col lives in
@@ -59,10 +80,11 @@ __device__ __forceinline__ ShOpndLane sh_operand_lane(float4 v) {
     lo[t] = __builtin_bit_cast(uint16_t, (_Float16)(yt - (float)h));
     sum += y[t];
   }
-  // 8 consecutive lanes cover one 32-element sub-block
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
-  sum += __shfl_xor(sum, 4);
+  // 8 consecutive lanes cover one 32-element sub-block (the pairs of an xor
+  // butterfly over lanes l ^ 1, l ^ 2, l ^ 4)
+  sum += sh_dpp<SH_DPP_XOR1>(sum);
+  sum += sh_dpp<SH_DPP_XOR2>(sum);
+  sum += sh_dpp<SH_DPP_HALF_MIRROR>(sum);
   o.hi = *(const uint2*)hi;
   o.lo = *(const uint2*)lo;
   const _Float16 sh = (_Float16)sum;
