@@ -376,6 +376,9 @@ __device__ __forceinline__ void fused_prep_sb(const EpiArgs& ea, const PrepFuse&
   const uint32_t col = wave, k = 256 * j + 4 * lane;
   float* xp = pf.resid + (size_t)col * pf.K + k;
   float4 v = *(const float4*)xp;
+  // before the coherent loads: their wait (an asm with a memory clobber) would
+  // keep this load behind it, a second round trip
+  const float4 wv = *(const float4*)(pf.norm_w + k);
   const float* pc = ea.out + (size_t)col * ea.ldo + k;
   for (uint32_t s0 = 0; s0 < nparts; s0 += 8) {
     f4v t[8];
@@ -394,7 +397,6 @@ __device__ __forceinline__ void fused_prep_sb(const EpiArgs& ea, const PrepFuse&
   *(float4*)xp = v;
   const float ss = sh_wave_sum(sh_sq4(v));
   if (lane == 0) pf.ssq[j * 8 + col] = ss;
-  const float4 wv = *(const float4*)(pf.norm_w + k);
   v.x *= wv.x; v.y *= wv.y; v.z *= wv.z; v.w *= wv.w;
   sh_operand_store_sb(v, pf.K, j, col, pf.bx, pf.xs, pf.cs);
 }

@@ -90,6 +90,9 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
   const uint32_t k = 256 * sb + 4 * lane;
   const bool valid = k < a.K;
   const size_t pstride = (size_t)a.part_cols * a.part_ld;
+  // the norm weight is read first: behind the residual store below it would be
+  // a second round trip
+  const float4 wv = a.norm_w && valid ? *(const float4*)(a.norm_w + k) : make_float4(1.f, 1.f, 1.f, 1.f);
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (valid) {
     if (MODE == PREP_SWIGLU) {
@@ -111,7 +114,6 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
     const float ss = sh_wave_sum(sh_sq4(v));
     if (lane == 0) a.ssq[(col / 8) * sh_grp_cs(a.K) + sb * 8 + col % 8] = ss;
     if (valid) {
-      const float4 wv = *(const float4*)(a.norm_w + k);
       v.x *= wv.x; v.y *= wv.y; v.z *= wv.z; v.w *= wv.w;
     }
   }
