@@ -574,13 +574,15 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
 constexpr int GW = 8;
 
 // acc + p[0] + p[stride] + ... (n terms, in order), 8 loads in flight.
+// B partials' loads per round trip (the sum is in split order for any B)
+template <uint32_t B = 8>
 __device__ __forceinline__ float4 sum_parts4(const float* p, size_t stride, uint32_t n, float4 acc) {
-  for (uint32_t i0 = 0; i0 < n; i0 += 8) {
-    float4 t[8];
+  for (uint32_t i0 = 0; i0 < n; i0 += B) {
+    float4 t[B];
 #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j) t[j] = *(const float4*)(p + min(i0 + j, n - 1) * stride);
+    for (uint32_t j = 0; j < B; ++j) t[j] = *(const float4*)(p + min(i0 + j, n - 1) * stride);
 #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j)
+    for (uint32_t j = 0; j < B; ++j)
       if (i0 + j < n) { acc.x += t[j].x; acc.y += t[j].y; acc.z += t[j].z; acc.w += t[j].w; }
   }
   return acc;
@@ -654,7 +656,10 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4s(const uint8_t* __restrict_
     for (uint32_t t = wave; t < nsb * N; t += GW) {  // wave-uniform
       const uint32_t sb = t / N, col = t % N, k = 256 * sb + 4 * lane;
       float4 v = *(const float4*)(src.x + (size_t)col * K + k);
-      if (src.nparts) v = sum_parts4(src.part + (size_t)col * src.part_ld + k, pstride, src.nparts, v);
+      // more than 8 at once (the draft's down leaves 16 K-split partials: two
+      // round trips in batches of 8)
+      if (src.nparts > 8) v = sum_parts4<16>(src.part + (size_t)col * src.part_ld + k, pstride, src.nparts, v);
+      else if (src.nparts) v = sum_parts4(src.part + (size_t)col * src.part_ld + k, pstride, src.nparts, v);
       if (blockIdx.x == 0) *(float4*)(src.rout + (size_t)col * K + k) = v;
       const float ss = sh_wave_sum(sh_sq4(v));
       if (lane == 0) sQ[sb * 8 + col] = ss;
