@@ -325,11 +325,12 @@ __device__ __forceinline__ float col_ssq_rinv(const EpiArgs& ea, uint32_t col, f
 }
 
 // Row sums for one lane after the MFMA loop: the hi and lo columns (c, c + 8)
-// of the same activation column meet, times the column's norm factor f. Every
-// lane must call this (it shuffles).
+// of the same activation column meet (lane l ^ 8 through DPP row_ror:8),
+// times the column's norm factor f. Every lane must call this.
 __device__ __forceinline__ void col_sum4(const f4& v, float f, float o[4]) {
+  constexpr int ROW_ROR8 = 0x128;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o[j] = (v[j] + __shfl_xor(v[j], 8)) * f;
+  for (int j = 0; j < 4; ++j) o[j] = (v[j] + sh_dpp<ROW_ROR8>(v[j])) * f;
 }
 
 // ------------------------------------------------------------------ Q4_K wide

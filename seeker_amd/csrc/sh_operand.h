@@ -53,7 +53,7 @@ __host__ __device__ __forceinline__ size_t sh_grp_cs(uint32_t K) { return (size_
 // 2, 3 of every 4 carry an exact 1/16: the Q4_K kernels decode their nibbles as
 // 1024 + 16 q and the Q8_0 kernels their bytes as 16 q); shi/slo: the
 // 32-element sub-block sum of the lane's 8-lane group, valid in lanes l % 8 = 0.
-// Every lane of the wave must call this (it shuffles).
+// Every lane of the wave must call this (cross-lane DPP steps).
 struct ShOpndLane {
   uint2 hi, lo;
   uint16_t shi, slo;
