@@ -98,6 +98,13 @@ int sh_model_load_gguf_memory(sh_engine* e, const void* data, uint64_t size, sh_
 void sh_model_destroy(sh_model* m);
 /* Model::{vocab_size, cache_dims} (models/mod.rs:35-37). */
 int sh_model_info(const sh_model* m, sh_model_dims* out);
+/* The validation half of models::open (models/mod.rs:537; parse_params +
+ * collect_weights, models/llama.rs:1038-1090) without a device: parses a GGUF
+ * image in caller memory, checks every tensor the model reads (shape, type,
+ * extent inside the image) and fills out as sh_model_info would. Returns
+ * SH_ERR_FORMAT for a malformed file, SH_ERR_UNSUPPORTED for a valid one this
+ * build cannot run. Touches no GPU. */
+int sh_gguf_inspect(const void* data, uint64_t size, sh_model_dims* out);
 
 /* ----------------------------------------------------------------- KV */
 /* Engine::allocate_kv_cache (inference/mod.rs:318); f16 K/V. */

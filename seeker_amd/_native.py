@@ -92,6 +92,7 @@ SIGNATURES = {
     "sh_model_load_gguf_memory": (C.c_int, [P, P, C.c_uint64, C.POINTER(P)]),
     "sh_model_destroy": (None, [P]),
     "sh_model_info": (C.c_int, [P, C.POINTER(sh_model_dims)]),
+    "sh_gguf_inspect": (C.c_int, [P, C.c_uint64, C.POINTER(sh_model_dims)]),
     "sh_kv_create": (C.c_int, [P, P, C.c_uint32, C.POINTER(P)]),
     "sh_kv_destroy": (None, [P]),
     "sh_kv_position": (C.c_int, [P, U32P]),

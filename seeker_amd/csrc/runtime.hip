@@ -176,138 +176,7 @@ extern "C" int sh_memcpy_d2h(sh_engine* e, void* dst, const void* src, uint64_t 
   return sh_prof_flush(e);
 }
 
-// ------------------------------------------------------------------ GGUF
-
-// GGUF v2/v3 reader (semantics of crates/seeker-core/src/gguf/mod.rs:161-230:
-// magic, version, u64 counts, typed metadata, tensor infos, data section
-// aligned to general.alignment (default 32)).
 namespace {
-
-struct GTensor {
-  std::string name;
-  uint32_t type = 0;
-  uint64_t ne[4] = {1, 1, 1, 1};
-  uint32_t nd = 0;
-  uint64_t off = 0;
-};
-
-struct GFile {
-  const uint8_t* base = nullptr;
-  uint64_t size = 0;
-  std::map<std::string, double> num;
-  std::map<std::string, std::string> str;
-  std::vector<GTensor> tensors;
-  const uint8_t* data = nullptr;
-  const GTensor* find(const std::string& n) const {
-    for (auto& t : tensors)
-      if (t.name == n) return &t;
-    return nullptr;
-  }
-};
-
-struct Rd {
-  const uint8_t* p;
-  const uint8_t* end;
-  bool bad = false;
-  uint64_t u(int n) {
-    if (p + n > end) { bad = true; return 0; }
-    uint64_t v = 0;
-    for (int i = 0; i < n; ++i) v |= (uint64_t)p[i] << (8 * i);
-    p += n;
-    return v;
-  }
-  std::string s() {
-    uint64_t n = u(8);
-    if (bad || n > (uint64_t)(end - p)) { bad = true; return ""; }
-    std::string r((const char*)p, n);
-    p += n;
-    return r;
-  }
-};
-
-bool skip_value(Rd& r, uint32_t t, int depth = 0) {
-  static const int sz[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
-  if (depth > 4 || t > 12) return false;
-  if (t == 8) { r.s(); return !r.bad; }
-  if (t == 9) {
-    uint32_t et = (uint32_t)r.u(4);
-    uint64_t n = r.u(8);
-    for (uint64_t i = 0; i < n && !r.bad; ++i)
-      if (!skip_value(r, et, depth + 1)) return false;
-    return !r.bad;
-  }
-  r.u(sz[t]);
-  return !r.bad;
-}
-
-int parse_gguf(const uint8_t* img, uint64_t size, GFile* f) {
-  SH_CHECK(size >= 24 && std::memcmp(img, "GGUF", 4) == 0, SH_ERR_FORMAT, "not a GGUF file (bad magic)");
-  Rd r{img + 4, img + size};
-  uint32_t ver = (uint32_t)r.u(4);
-  SH_CHECK(ver == 2 || ver == 3, SH_ERR_FORMAT, "unsupported GGUF version %u", ver);
-  uint64_t nt = r.u(8), nkv = r.u(8);
-  SH_CHECK(nt < (1u << 24) && nkv < (1u << 24), SH_ERR_FORMAT, "implausible GGUF counts");
-  uint32_t align = 32;
-  for (uint64_t i = 0; i < nkv && !r.bad; ++i) {
-    std::string k = r.s();
-    uint32_t t = (uint32_t)r.u(4);
-    switch (t) {
-      case 0: f->num[k] = (double)(uint8_t)r.u(1); break;
-      case 1: f->num[k] = (double)(int8_t)r.u(1); break;
-      case 2: f->num[k] = (double)(uint16_t)r.u(2); break;
-      case 3: f->num[k] = (double)(int16_t)r.u(2); break;
-      case 4: f->num[k] = (double)(uint32_t)r.u(4); break;
-      case 5: f->num[k] = (double)(int32_t)r.u(4); break;
-      case 6: { uint32_t b = (uint32_t)r.u(4); float x; std::memcpy(&x, &b, 4); f->num[k] = x; break; }
-      case 7: f->num[k] = (double)r.u(1); break;
-      case 8: f->str[k] = r.s(); break;
-      case 10: f->num[k] = (double)r.u(8); break;
-      case 11: f->num[k] = (double)(int64_t)r.u(8); break;
-      case 12: { uint64_t b = r.u(8); double x; std::memcpy(&x, &b, 8); f->num[k] = x; break; }
-      default:
-        SH_CHECK(skip_value(r, t), SH_ERR_FORMAT, "bad GGUF metadata value type %u for %s", t, k.c_str());
-    }
-    if (k == "general.alignment" && t == 4) align = (uint32_t)f->num[k];
-  }
-  SH_CHECK(!r.bad, SH_ERR_FORMAT, "truncated GGUF metadata");
-  SH_CHECK(align && (align & (align - 1)) == 0, SH_ERR_FORMAT, "bad alignment %u", align);
-  for (uint64_t i = 0; i < nt && !r.bad; ++i) {
-    GTensor t;
-    t.name = r.s();
-    t.nd = (uint32_t)r.u(4);
-    SH_CHECK(t.nd >= 1 && t.nd <= 4, SH_ERR_FORMAT, "tensor %s has %u dims", t.name.c_str(), t.nd);
-    for (uint32_t j = 0; j < t.nd; ++j) t.ne[j] = r.u(8);
-    t.type = (uint32_t)r.u(4);
-    t.off = r.u(8);
-    f->tensors.push_back(t);
-  }
-  SH_CHECK(!r.bad, SH_ERR_FORMAT, "truncated GGUF tensor table");
-  uint64_t pos = (uint64_t)(r.p - img);
-  uint64_t start = (pos + align - 1) / align * align;
-  SH_CHECK(start <= size, SH_ERR_FORMAT, "GGUF data section past end of file");
-  f->base = img;
-  f->size = size;
-  f->data = img + start;
-  for (auto& t : f->tensors) {
-    uint64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
-    uint64_t bytes = 0;
-    switch (t.type) {
-      case GGML_F32: bytes = n * 4; break;
-      case GGML_F16: bytes = n * 2; break;
-      case GGML_Q8_0: bytes = n / 32 * 34; break;
-      case GGML_Q4_K: bytes = n / 256 * 144; break;
-      default: bytes = 0;
-    }
-    SH_CHECK(start + t.off + bytes <= size, SH_ERR_FORMAT, "tensor %s extends past end of file", t.name.c_str());
-  }
-  return SH_OK;
-}
-
-double num_or(const GFile& f, const char* k, double dflt, bool* found = nullptr) {
-  auto it = f.num.find(k);
-  if (found) *found = it != f.num.end();
-  return it == f.num.end() ? dflt : it->second;
-}
 
 template <class T>
 int dalloc(T** p, size_t n) {
@@ -367,99 +236,52 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   SH_CHECK(e && img && out, SH_ERR_ARG, "sh_model_load: NULL argument");
   SH_HIP(hipSetDevice(e->device));
   GFile f;
-  int rc = parse_gguf(img, size, &f);
+  ModelDesc md;
+  int rc = sh_gguf_parse(img, size, &f);
+  if (!rc) rc = sh_gguf_describe(f, &md);
+  if (!rc) rc = sh_gguf_supported(md);
   if (rc) return rc;
-  auto arch = f.str.find("general.architecture");
-  SH_CHECK(arch != f.str.end() && arch->second == "llama", SH_ERR_UNSUPPORTED,
-           "architecture '%s' not supported (llama only)", arch == f.str.end() ? "?" : arch->second.c_str());
   sh_model* m = new sh_model();
   m->e = e;
-  // GGUF keys / defaults: models/llama.rs:1038-1048.
-  bool ok1, ok2, ok3, ok4, ok5;
-  m->n_layer = (uint32_t)num_or(f, "llama.block_count", 0, &ok1);
-  m->n_head = (uint32_t)num_or(f, "llama.attention.head_count", 0, &ok2);
-  m->n_kv = (uint32_t)num_or(f, "llama.attention.head_count_kv", m->n_head);
-  m->d = (uint32_t)num_or(f, "llama.embedding_length", 0, &ok3);
-  m->ff = (uint32_t)num_or(f, "llama.feed_forward_length", 0, &ok4);
-  m->n_ctx = (uint32_t)num_or(f, "llama.context_length", 0, &ok5);
-  m->theta = (float)num_or(f, "llama.rope.freq_base", 10000.0);
-  m->eps = (float)num_or(f, "llama.attention.layer_norm_rms_epsilon", 1e-5);
-  if (!(ok1 && ok2 && ok3 && ok4)) {
-    free_model(m);
-    SH_CHECK(false, SH_ERR_FORMAT, "missing required llama.* metadata");
-  }
-  if (m->n_head == 0 || m->n_kv == 0 || m->d % m->n_head || m->n_head % m->n_kv) {
-    free_model(m);
-    SH_CHECK(false, SH_ERR_FORMAT, "inconsistent head counts");
-  }
-  m->hd = m->d / m->n_head;
-  const uint32_t rope_dim = (uint32_t)num_or(f, "llama.rope.dimension_count", m->hd);
-  const GTensor* te = f.find("token_embd.weight");
-  const GTensor* on = f.find("output_norm.weight");
-  const GTensor* ow = f.find("output.weight");
+  m->n_layer = md.n_layer; m->n_head = md.n_head; m->n_kv = md.n_kv; m->d = md.d; m->ff = md.ff;
+  m->n_ctx = md.n_ctx; m->theta = md.theta; m->eps = md.eps; m->hd = md.hd; m->V = md.V;
   int fail = SH_OK;
 #define FAIL(code, ...)                 \
   do {                                  \
     free_model(m);                      \
     SH_CHECK(false, code, __VA_ARGS__); \
   } while (0)
-  if (!te || !on) FAIL(SH_ERR_FORMAT, "missing token_embd / output_norm");
-  m->V = (uint32_t)num_or(f, "llama.vocab_size", (double)te->ne[1]);
-  if (rope_dim != m->hd) FAIL(SH_ERR_UNSUPPORTED, "partial RoPE (rope_dim %u != head_dim %u)", rope_dim, m->hd);
-  if (m->hd != 64 && m->hd != 128) FAIL(SH_ERR_UNSUPPORTED, "head_dim %u (64 or 128 supported)", m->hd);
-  if (te->ne[0] != m->d || te->ne[1] != m->V) FAIL(SH_ERR_FORMAT, "token_embd shape mismatch");
-  const uint32_t wtype = f.find("blk.0.attn_q.weight") ? f.find("blk.0.attn_q.weight")->type : 0;
-  if (wtype != GGML_Q4_K && wtype != GGML_Q8_0) FAIL(SH_ERR_UNSUPPORTED, "weight type %u (Q4_K / Q8_0 only)", wtype);
-  if (te->type != GGML_Q4_K && te->type != GGML_Q8_0 && te->type != GGML_F16 && te->type != GGML_F32)
-    FAIL(SH_ERR_UNSUPPORTED, "token_embd type %u", te->type);
+  const uint32_t wtype = md.layers[0].wq.type;
   // embedding (raw rows for the gather)
-  m->embd_type = (int)te->type;
-  m->embd_row_bytes = te->type == GGML_Q4_K ? m->d / 256 * 144
-                      : te->type == GGML_Q8_0 ? m->d / 32 * 34
-                      : te->type == GGML_F16  ? m->d * 2
-                                              : m->d * 4;
+  const TRef& te = md.tok_embd;
+  m->embd_type = (int)te.type;
+  m->embd_row_bytes = te.row_bytes;
   if (dalloc(&m->embd_raw, m->embd_row_bytes * m->V)) FAIL(SH_ERR_HIP, "%s", sh_last_error());
-  if (hipMemcpy(m->embd_raw, f.data + te->off, m->embd_row_bytes * m->V, hipMemcpyHostToDevice) != hipSuccess)
+  if (hipMemcpy(m->embd_raw, te.data, m->embd_row_bytes * m->V, hipMemcpyHostToDevice) != hipSuccess)
     FAIL(SH_ERR_HIP, "embedding upload failed");
-  auto upload_f32 = [&](const GTensor* t, float** dst) -> int {
-    SH_CHECK(t && t->type == GGML_F32 && t->ne[0] == m->d, SH_ERR_FORMAT, "norm weight %s: f32 [%u] expected",
-             t ? t->name.c_str() : "?", m->d);
-    SH_HIP(hipMalloc(dst, m->d * 4));
-    SH_HIP(hipMemcpy(*dst, f.data + t->off, m->d * 4, hipMemcpyHostToDevice));
+  auto upload_f32 = [&](const TRef& t, float** dst) -> int {
+    SH_HIP(hipMalloc(dst, t.cols * 4));
+    SH_HIP(hipMemcpy(*dst, t.data, t.cols * 4, hipMemcpyHostToDevice));
     return SH_OK;
   };
-  if ((fail = upload_f32(on, &m->out_norm))) FAIL(fail, "%s", sh_last_error());
-  // lm_head = output.unwrap_or(token_embd) (llama.rs:424)
-  const GTensor* lm = ow ? ow : te;
-  if (lm->type != GGML_Q4_K && lm->type != GGML_Q8_0) FAIL(SH_ERR_UNSUPPORTED, "lm_head type %u", lm->type);
-  if (lm->ne[0] != m->d || lm->ne[1] != m->V) FAIL(SH_ERR_FORMAT, "output.weight shape mismatch");
-  if ((fail = sh_repack_upload(e, (int)lm->type, f.data + lm->off, m->V, m->d, &m->lm_head)))
-    FAIL(fail, "%s", sh_last_error());
+  if ((fail = upload_f32(md.out_norm, &m->out_norm))) FAIL(fail, "%s", sh_last_error());
+  const TRef& lm = md.output;
+  if ((fail = sh_repack_upload(e, (int)lm.type, lm.data, m->V, m->d, &m->lm_head))) FAIL(fail, "%s", sh_last_error());
   m->alg_weight_bytes += m->lm_head.alg_bytes;
   const uint32_t dkv = m->hd * m->n_kv;
   m->layers.resize(m->n_layer);
   for (uint32_t l = 0; l < m->n_layer; ++l) {
-    auto get = [&](const char* s) { return f.find("blk." + std::to_string(l) + "." + s); };
-    const GTensor *an = get("attn_norm.weight"), *fn = get("ffn_norm.weight");
-    const GTensor *wq = get("attn_q.weight"), *wk = get("attn_k.weight"), *wv = get("attn_v.weight");
-    const GTensor *wo = get("attn_output.weight"), *wg = get("ffn_gate.weight"), *wu = get("ffn_up.weight");
-    const GTensor* wd = get("ffn_down.weight");
-    if (!an || !fn || !wq || !wk || !wv || !wo || !wg || !wu || !wd) FAIL(SH_ERR_FORMAT, "layer %u: missing tensor", l);
-    const GTensor* mats[7] = {wq, wk, wv, wo, wg, wu, wd};
-    for (auto* t : mats)
-      if (t->type != wtype) FAIL(SH_ERR_UNSUPPORTED, "mixed weight types in layer %u (%s)", l, t->name.c_str());
-    if (wq->ne[0] != m->d || wq->ne[1] != m->d || wk->ne[1] != dkv || wv->ne[1] != dkv || wo->ne[1] != m->d ||
-        wg->ne[1] != m->ff || wu->ne[1] != m->ff || wd->ne[0] != m->ff || wd->ne[1] != m->d)
-      FAIL(SH_ERR_FORMAT, "layer %u: weight shape mismatch", l);
+    const LayerDesc& D = md.layers[l];
     Layer& L = m->layers[l];
-    if ((fail = upload_f32(an, &L.attn_norm)) || (fail = upload_f32(fn, &L.ffn_norm))) FAIL(fail, "%s", sh_last_error());
-    const uint8_t* parts[3] = {f.data + wq->off, f.data + wk->off, f.data + wv->off};
+    if ((fail = upload_f32(D.attn_norm, &L.attn_norm)) || (fail = upload_f32(D.ffn_norm, &L.ffn_norm)))
+      FAIL(fail, "%s", sh_last_error());
+    const uint8_t* parts[3] = {D.wq.data, D.wk.data, D.wv.data};
     const uint32_t rows[3] = {m->d, dkv, dkv};
     if ((fail = sh_repack_upload_cat(e, (int)wtype, parts, rows, 3, m->d, &L.wqkv))) FAIL(fail, "%s", sh_last_error());
-    if ((fail = sh_repack_upload(e, (int)wtype, f.data + wo->off, m->d, m->d, &L.wo))) FAIL(fail, "%s", sh_last_error());
-    if ((fail = sh_repack_upload_gu(e, (int)wtype, f.data + wg->off, f.data + wu->off, m->ff, m->d, &L.wgu)))
+    if ((fail = sh_repack_upload(e, (int)wtype, D.wo.data, m->d, m->d, &L.wo))) FAIL(fail, "%s", sh_last_error());
+    if ((fail = sh_repack_upload_gu(e, (int)wtype, D.gate.data, D.up.data, m->ff, m->d, &L.wgu)))
       FAIL(fail, "%s", sh_last_error());
-    if ((fail = sh_repack_upload(e, (int)wtype, f.data + wd->off, m->d, m->ff, &L.wdown)))
+    if ((fail = sh_repack_upload(e, (int)wtype, D.down.data, m->d, m->ff, &L.wdown)))
       FAIL(fail, "%s", sh_last_error());
     m->alg_weight_bytes += L.wqkv.alg_bytes + L.wo.alg_bytes + L.wgu.alg_bytes + L.wdown.alg_bytes + 8.0 * m->d;
   }

@@ -8,9 +8,10 @@
 #include <vector>
 
 #include "../../include/seeker_hip.h"
+#include "gguf.h"
+#include "sh_error.h"
 
 // ---------------------------------------------------------------- errors
-void sh_set_error(const char* fmt, ...);
 
 #define SH_HIP(call)                                                              \
   do {                                                                            \
@@ -22,16 +23,6 @@ void sh_set_error(const char* fmt, ...);
     }                                                                             \
   } while (0)
 
-#define SH_CHECK(cond, code, ...)   \
-  do {                              \
-    if (!(cond)) {                  \
-      sh_set_error(__VA_ARGS__);    \
-      return (code);                \
-    }                               \
-  } while (0)
-
-// GGML type ids used here (crates/seeker-core/src/gguf/types.rs).
-enum : int { GGML_F32 = 0, GGML_F16 = 1, GGML_Q8_0 = 8, GGML_Q4_K = 12 };
 
 // ------------------------------------------------------------ constants
 // Activation operand ("B") layout for the MFMA GEMV: for each 8-column chunk,
