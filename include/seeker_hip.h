@@ -158,13 +158,28 @@ int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t 
                       float* logits_out, uint32_t* sampled_out, float* residual_out);
 
 /* Engine::decode_speculative (inference/mod.rs:2108-2297) with a separate draft
- * model (draft_tokens mod.rs:2062-2092 greedy): drafts n = clamp(n_max,1,8)
- * tokens on device, verifies [last, d_1..d_n], accepts the longest prefix
- * (GREEDY / COMPARE / REJECTION), truncates both caches to pos + acc + 1.
- * emitted_out holds n + 1 entries; *n_emitted = acc + 1. drafts_out (n) may be NULL. */
+ * model: drafts n = clamp(n_max,1,8) tokens on the device, verifies [last,
+ * d_1..d_n], accepts, truncates both caches to pos + acc + 1. emitted_out
+ * holds n + 1 entries; *n_emitted = acc + 1. drafts_out (n) may be NULL.
+ *  - GREEDY (s NULL or mode 0): greedy drafts (draft_tokens mod.rs:2062-2092),
+ *    host accept of matching argmax ids (mod.rs:2168-2179).
+ *  - COMPARE: greedy drafts; each verify column i sampled in vocab order with
+ *    uniform word 2i+1, accepted while sample == draft (mod.rs:2181-2231,
+ *    sample.rs:347-361).
+ *  - REJECTION (new): draft i drawn from softmax(draft logits / T) with word
+ *    2(n+1) + i, accepted iff u_{2i} q(d) < p(d), first rejection resampled
+ *    from max(0, p - q) with word 2i+1 (bonus from p_n).
+ * Stochastic uniform words come from Philox key (seed, 0x5EC) at s->counter +
+ * word, and the step advances s->counter by 3n + 2; with s->uniforms they are
+ * uniforms[word], an array of 3n + 2 floats. */
 int sh_spec_step(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh_kv* dkv,
                  uint32_t last_token, uint32_t n_max, sh_sampling* s, uint32_t* emitted_out,
                  uint32_t* n_emitted, uint32_t* drafts_out);
+/* Readback of the last stochastic sh_spec_step of this engine, the analog of
+ * the reference's tensor taps (inference/context.rs:136-160, 283): target
+ * logits p_out [(n+1)][V] and draft logits q_out [n][V] (either may be NULL),
+ * *n_out = n, *V_out = V. SH_ERR_STATE if no stochastic step has run. */
+int sh_spec_step_logits(sh_engine* e, float* p_out, float* q_out, uint32_t* n_out, uint32_t* V_out);
 
 /* ------------------------------------------------------ kernel level */
 /* Upload a GGUF-layout quantized matrix [M rows][K] (Q8_0 or Q4_K) and repack it
@@ -187,6 +202,13 @@ int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_
 int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
                      const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s,
                      uint32_t* acc_len_dev, uint32_t* next_tok_dev);
+
+/* New (no reference counterpart): the probabilities behind REJECTION's accept
+ * tests, computed as sh_accept_sample computes them (f64 softmax of logits / T
+ * over the same row statistics): probs_dev [B][k][3] = (p_i(d_i), q_i(d_i),
+ * min(1, p_i(d_i) / q_i(d_i))) with the layouts of sh_accept_sample. */
+int sh_accept_probs(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev, const uint32_t* drafts_dev,
+                    uint32_t B, uint32_t k, uint32_t V, float temperature, double* probs_dev);
 
 /* New (no reference counterpart): tree acceptance for B token trees of n <= 64
  * nodes, recursive rejection sampling (SpecInfer multi-candidate speculative

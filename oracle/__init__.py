@@ -57,6 +57,10 @@ _SIGS = {
     "or_tree_accept": (C.c_int, [F32P, F32P, U32P, I32P, C.c_uint32, C.c_uint32, C.c_float, F32P, U32P, U32P, U32P]),
     "or_probs": (None, [F32P, C.c_uint32, C.c_float, F32P]),
     "or_spec_step_greedy": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, U32P, U32P, U32P, U32P, U32P]),
+    "or_spec_draft_token": (C.c_uint32, [C.c_int, F32P, C.c_uint32, C.c_float, C.c_float]),
+    "or_spec_accept": (C.c_uint32, [C.c_int, F32P, F32P, U32P, C.c_uint32, C.c_uint32, C.c_float, F32P, U32P]),
+    "or_spec_step": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, C.c_int, C.c_float, F32P, U32P, U32P, U32P, U32P,
+                               U32P, F32P, F32P]),
 }
 
 _lib = None
@@ -267,3 +271,53 @@ def spec_step_greedy(tgt: Model, drf: Model, tkv: KvCache, dkv: KvCache, last_to
         raise ValueError(f"oracle spec step failed ({rc})")
     n = min(max(n_max, 1), 8)
     return list(em)[: ne.value], list(dr)[:n]
+
+
+SPEC_GREEDY, SPEC_COMPARE, SPEC_REJECTION = 0, 1, 2
+
+
+def spec_uniforms(seed: int, counter: int, n: int) -> np.ndarray:
+    """The uniforms a speculative step of n drafts consumes from Philox key
+    (seed, 0x5EC) at word counter: 2(n+1) for the verify columns, then n for
+    the draft draws (sh_spec_step's layout)."""
+    return philox_uniforms(seed, 0x5EC, counter, 3 * n + 2)
+
+
+def spec_draft_token(mode: int, q_logits, T: float, u: float) -> int:
+    q = _f32(q_logits)
+    return int(lib().or_spec_draft_token(mode, q.ctypes.data_as(F32P), q.size, T, u))
+
+
+def spec_accept(mode: int, p_logits, q_logits, drafts, T: float, u) -> list:
+    p = _f32(p_logits)
+    n = len(drafts)
+    V = p.shape[-1]
+    q = _f32(q_logits) if q_logits is not None else np.zeros((max(n, 1), V), np.float32)
+    d = np.ascontiguousarray(drafts, dtype=np.uint32)
+    uu = _f32(u) if u is not None else np.zeros(2 * (n + 1), np.float32)
+    em = np.zeros(n + 1, dtype=np.uint32)
+    ne = lib().or_spec_accept(mode, p.ctypes.data_as(F32P), q.ctypes.data_as(F32P), d.ctypes.data_as(U32P), n, V, T,
+                              uu.ctypes.data_as(F32P), em.ctypes.data_as(U32P))
+    return em[:ne].tolist()
+
+
+def spec_step(tgt: Model, drf: Model, tkv: KvCache, dkv: KvCache, last_token: int, n_max: int, mode: int = 0,
+              T: float = 0.0, u=None, want_logits: bool = False):
+    """or_spec_step: returns (emitted, drafts) or, with want_logits,
+    (emitted, drafts, p_logits [(n+1)][V], q_logits [n][V])."""
+    n = min(max(n_max, 1), 8)
+    em = (C.c_uint32 * 9)()
+    dr = (C.c_uint32 * 8)()
+    ne = C.c_uint32()
+    uu = _f32(u) if u is not None else None
+    p = np.empty((n + 1, tgt.V), np.float32) if want_logits else None
+    q = np.empty((n, tgt.V), np.float32) if want_logits else None
+    rc = lib().or_spec_step(tgt.h, drf.h, tkv.h, dkv.h, last_token, n_max, mode, T,
+                            uu.ctypes.data_as(F32P) if uu is not None else None, dkv.pending,
+                            C.byref(dkv.n_pending), em, C.byref(ne), dr,
+                            p.ctypes.data_as(F32P) if p is not None else None,
+                            q.ctypes.data_as(F32P) if q is not None else None)
+    if rc:
+        raise ValueError(f"oracle spec step failed ({rc})")
+    out = (list(em)[: ne.value], list(dr)[:n])
+    return out + (p, q) if want_logits else out

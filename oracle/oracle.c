@@ -807,3 +807,96 @@ int or_spec_step_greedy(or_model* tgt, or_model* drf, or_kv* tkv, or_kv* dkv, ui
   free(lg);
   return 0;
 }
+
+/* Draft token at one draft position of a speculative step. GREEDY and
+ * COMPARE draft greedily, as the reference does (inference/mod.rs:2062-2092,
+ * record_greedy); REJECTION draws d ~ q = softmax(q_logits / T) by the
+ * vocab-order inverse CDF with uniform u, which speculative sampling needs
+ * for its output to follow the target distribution (Leviathan et al. 2023). */
+uint32_t or_spec_draft_token(int mode, const float* q_logits, uint32_t V, float T, float u) {
+  if (mode == OR_SPEC_REJECTION && T > 0.f) return or_sample_vocab_order(q_logits, V, T, u);
+  return or_argmax(q_logits, V);
+}
+
+/* Acceptance of one verify of [last, d_1..d_n]. GREEDY: emit argmax p_i while
+ * it equals d_{i+1} (host accept, inference/mod.rs:2168-2179). COMPARE: the
+ * reference's GPU stochastic path (mod.rs:2181-2231): every column sampled in
+ * vocab order with uniform u[2i+1], then sample_and_compare (sample.rs:
+ * 347-361). REJECTION: or_rejection with u_acc[i] = u[2i], u_res[i] = u[2i+1].
+ * Returns the number emitted (accepted + 1). */
+uint32_t or_spec_accept(int mode, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t n,
+                        uint32_t V, float T, const float* u, uint32_t* emitted) {
+  if (mode == OR_SPEC_GREEDY || !(T > 0.f)) {
+    uint32_t ne = 0;
+    for (uint32_t i = 0; i <= n; ++i) {
+      const uint32_t t = or_argmax(p_logits + (size_t)i * V, V);
+      emitted[ne++] = t;
+      if (i < n && t == drafts[i]) continue;
+      break;
+    }
+    return ne;
+  }
+  if (mode == OR_SPEC_COMPARE) {
+    float uc[9];
+    for (uint32_t i = 0; i <= n; ++i) uc[i] = u[2 * i + 1];
+    or_sampler_cfg cfg = {T, 0, 1.0f, 0.0f};
+    return or_sample_and_compare(p_logits, V, drafts, n, &cfg, uc, 1, emitted);
+  }
+  float ua[8], ur[9];
+  for (uint32_t i = 0; i <= n; ++i) {
+    if (i < n) ua[i] = u[2 * i];
+    ur[i] = u[2 * i + 1];
+  }
+  uint32_t nxt = 0;
+  const uint32_t acc = or_rejection(p_logits, q_logits, drafts, n, V, T, ua, ur, &nxt);
+  for (uint32_t i = 0; i < acc; ++i) emitted[i] = drafts[i];
+  emitted[acc] = nxt;
+  return acc + 1;
+}
+
+/* Engine::decode_speculative (inference/mod.rs:2108-2297) in all three modes
+ * with a separate draft model: feed the draft's pending tokens and last_token,
+ * draft n = clamp(n_max, 1, 8) tokens (or_spec_draft_token, draft i with
+ * uniform u[2(n+1) + i]), verify [last, d_1..d_n] with all-position logits,
+ * accept (or_spec_accept with u[0 .. 2(n+1))), truncate both caches to
+ * P + acc + 1 (mod.rs:2269-2270). p_out [(n+1)][V] and q_out [n][V] (either
+ * may be NULL) receive the target and draft logits of the step. */
+int or_spec_step(or_model* tgt, or_model* drf, or_kv* tkv, or_kv* dkv, uint32_t last_token, uint32_t n_max,
+                 int mode, float T, const float* u, uint32_t* dpending, uint32_t* n_dpending, uint32_t* emitted,
+                 uint32_t* n_emitted, uint32_t* drafts_out, float* p_out, float* q_out) {
+  const uint32_t n = n_max < 1 ? 1 : (n_max > 8 ? 8 : n_max);
+  const uint32_t P = tkv->pos, V = tgt->V;
+  if (drf->V != V) return 11;
+  if (mode != OR_SPEC_GREEDY && !u) return 12;
+  float* lg = (float*)malloc((size_t)(n + 1) * V * 4);
+  float* ql = (float*)malloc((size_t)n * V * 4);
+  uint32_t drafts[8], feed[16], nf = 0;
+  for (uint32_t i = 0; i < *n_dpending; ++i) feed[nf++] = dpending[i];
+  feed[nf++] = last_token;
+  int rc = dkv->pos + nf != P + 1 ? 10 : 0;
+  for (uint32_t i = 0; i < n && !rc; ++i) {
+    float* q = ql + (size_t)i * V;
+    rc = i == 0 ? or_forward(drf, dkv, feed, nf, dkv->pos, NULL, 1, q, NULL)
+                : or_forward(drf, dkv, &drafts[i - 1], 1, dkv->pos, NULL, 1, q, NULL);
+    if (!rc) drafts[i] = or_spec_draft_token(mode, q, V, T, u ? u[2 * (n + 1) + i] : 0.f);
+  }
+  uint32_t vt[9];
+  vt[0] = last_token;
+  for (uint32_t i = 0; i < n; ++i) vt[i + 1] = drafts[i];
+  if (!rc) rc = or_forward(tgt, tkv, vt, n + 1, P, NULL, 2, lg, NULL);
+  if (!rc) {
+    const uint32_t ne = or_spec_accept(mode, lg, ql, drafts, n, V, T, u, emitted);
+    const uint32_t acc = ne - 1;
+    or_kv_truncate(tkv, P + acc + 1);
+    or_kv_truncate(dkv, P + acc + 1);
+    *n_dpending = 0;
+    if (acc == n) dpending[(*n_dpending)++] = drafts[n - 1];  /* d_n was never fed to the draft */
+    *n_emitted = ne;
+    if (drafts_out) memcpy(drafts_out, drafts, n * sizeof(uint32_t));
+    if (p_out) memcpy(p_out, lg, (size_t)(n + 1) * V * 4);
+    if (q_out) memcpy(q_out, ql, (size_t)n * V * 4);
+  }
+  free(lg);
+  free(ql);
+  return rc;
+}

@@ -109,6 +109,23 @@ int or_spec_step_greedy(or_model* tgt, or_model* drf, or_kv* tkv, or_kv* dkv, ui
                         uint32_t n_max, uint32_t* dpending, uint32_t* n_dpending, uint32_t* emitted,
                         uint32_t* n_emitted, uint32_t* drafts_out);
 
+/* Sampling modes of the speculative step (the values of include/seeker_hip.h's sh_sample_mode). */
+enum { OR_SPEC_GREEDY = 0, OR_SPEC_COMPARE = 1, OR_SPEC_REJECTION = 2 };
+
+/* Draft token at one position: argmax (GREEDY, COMPARE) or a vocab-order draw
+ * from softmax(q/T) with uniform u (REJECTION). */
+uint32_t or_spec_draft_token(int mode, const float* q_logits, uint32_t V, float T, float u);
+/* Acceptance of one verify: p_logits [(n+1)][V], q_logits [n][V] (REJECTION),
+ * u [2(n+1)]: u[2i] accepts draft i, u[2i+1] samples / resamples column i.
+ * Returns the number of emitted tokens. */
+uint32_t or_spec_accept(int mode, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t n,
+                        uint32_t V, float T, const float* u, uint32_t* emitted);
+/* Speculative step in any mode (inference/mod.rs:2108-2297); u [2(n+1) + n]
+ * (NULL for GREEDY): verify-column uniforms, then one per draft draw. */
+int or_spec_step(or_model* tgt, or_model* drf, or_kv* tkv, or_kv* dkv, uint32_t last_token, uint32_t n_max,
+                 int mode, float T, const float* u, uint32_t* dpending, uint32_t* n_dpending, uint32_t* emitted,
+                 uint32_t* n_emitted, uint32_t* drafts_out, float* p_out, float* q_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,6 +81,8 @@ int sh_prof_flush(sh_engine* e) {
 
 // ------------------------------------------------------------------ engine
 
+static void free_spec_bufs(SpecBufs& sb);
+
 extern "C" int sh_engine_create(int dev, sh_engine** out) {
   SH_CHECK(out, SH_ERR_ARG, "sh_engine_create: out is NULL");
   int n = 0;
@@ -109,6 +111,9 @@ extern "C" void sh_engine_destroy(sh_engine* e) {
   (void)hipStreamSynchronize(e->stream);
   for (auto& p : e->pending) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
   for (auto ev : e->event_pool) (void)hipEventDestroy(ev);
+  for (auto& g : e->graphs) (void)hipGraphExecDestroy(g.exec);
+  e->graphs.clear();
+  free_spec_bufs(e->spec);
   (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -974,20 +979,9 @@ extern "C" int sh_forward_full(sh_engine* e, sh_model* m, sh_kv* kv, const uint3
   return sh_prof_flush(e);
 }
 
-struct SpecBufs {
-  uint32_t* tok = nullptr;     // [64]: pending..., last, d_1..d_n
-  uint32_t* samp = nullptr;    // [16]
-  uint32_t* base = nullptr;    // [4] graph base positions (device): draft, target
-  float* dlogits = nullptr;    // draft logits [8][V] (REJECTION)
-  float* tlogits = nullptr;    // target logits [9][V]
-  uint32_t* pinned = nullptr;  // host staging [128]
-  uint32_t vcap = 0;
-};
-static thread_local SpecBufs g_spec;
-
-static int spec_bufs(uint32_t V);
+static int spec_bufs(sh_engine* e, uint32_t V);
 static bool graphs_enabled(const sh_engine* e);
-static hipGraphExec_t graph_find(const std::vector<uintptr_t>& key);
+static hipGraphExec_t graph_find(sh_engine* e, const std::vector<uintptr_t>& key);
 static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const std::vector<sh_kv*>& kvs,
                          const std::vector<const uint32_t*>& bases, const std::function<int()>& body,
                          hipGraphExec_t* out);
@@ -996,19 +990,19 @@ static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const 
 // ids at samp[0..], base position at base[2].
 static int verify_greedy_graph(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* tokens, uint32_t L,
                                uint32_t pos, uint32_t* sampled_out) {
-  int rc = spec_bufs(m->V);
+  int rc = spec_bufs(e, m->V);
   if (rc) return rc;
-  uint32_t* hp = g_spec.pinned;
+  uint32_t* hp = e->spec.pinned;
   for (uint32_t i = 0; i < L; ++i) hp[32 + i] = tokens[i];
   hp[66] = pos;
   const std::vector<uintptr_t> key = {2, (uintptr_t)m, (uintptr_t)kv, (uintptr_t)kv->k, kv->max_seq, L};
-  hipGraphExec_t ex = graph_find(key);
+  hipGraphExec_t ex = graph_find(e, key);
   if (!ex) {
     if ((rc = ensure_rope(m, kv->max_seq)) || (rc = ensure_fa_part(m, kv->max_seq))) return rc;
-    rc = graph_capture(e, key, {kv}, {g_spec.base + 2}, [&] {
-      int r = forward_dev(m, kv, g_spec.tok + 32, L, 0, nullptr, 2, nullptr, nullptr, nullptr);
-      if (!r) r = sh_argmax_launch(e, m->ws.logits, m->V, L, m->ws.amax, g_spec.samp);
-      if (!r && hipMemcpyAsync(g_spec.pinned + 48, g_spec.samp, (size_t)L * 4, hipMemcpyDeviceToHost,
+    rc = graph_capture(e, key, {kv}, {e->spec.base + 2}, [&] {
+      int r = forward_dev(m, kv, e->spec.tok + 32, L, 0, nullptr, 2, nullptr, nullptr, nullptr);
+      if (!r) r = sh_argmax_launch(e, m->ws.logits, m->V, L, m->ws.amax, e->spec.samp);
+      if (!r && hipMemcpyAsync(e->spec.pinned + 48, e->spec.samp, (size_t)L * 4, hipMemcpyDeviceToHost,
                                e->stream) != hipSuccess) {
         sh_set_error("verify readback capture failed");
         r = SH_ERR_HIP;
@@ -1017,8 +1011,8 @@ static int verify_greedy_graph(sh_engine* e, sh_model* m, sh_kv* kv, const uint3
     }, &ex);
     if (rc) return rc;
   }
-  SH_HIP(hipMemcpyAsync(g_spec.tok + 32, hp + 32, (size_t)L * 4, hipMemcpyHostToDevice, e->stream));
-  SH_HIP(hipMemcpyAsync(g_spec.base + 2, hp + 66, 4, hipMemcpyHostToDevice, e->stream));
+  SH_HIP(hipMemcpyAsync(e->spec.tok + 32, hp + 32, (size_t)L * 4, hipMemcpyHostToDevice, e->stream));
+  SH_HIP(hipMemcpyAsync(e->spec.base + 2, hp + 66, 4, hipMemcpyHostToDevice, e->stream));
   SH_HIP(hipGraphLaunch(ex, e->stream));
   SH_HIP(hipStreamSynchronize(e->stream));
   for (uint32_t i = 0; i < L; ++i) sampled_out[i] = hp[48 + i];
@@ -1243,26 +1237,32 @@ extern "C" int sh_tree_verify_step(sh_engine* e, sh_model* target, sh_kv* const*
 // ------------------------------------------------------------------ spec step
 
 
-static int spec_bufs(uint32_t V) {
-  if (g_spec.tok && g_spec.vcap >= V) return SH_OK;
-  if (g_spec.tok) {
-    g_graph_gen.fetch_add(1);  // captured graphs point into these buffers
-    (void)hipFree(g_spec.tok); (void)hipFree(g_spec.samp); (void)hipFree(g_spec.base); (void)hipFree(g_spec.dlogits);
-    (void)hipFree(g_spec.tlogits); (void)hipHostFree(g_spec.pinned);
-  }
-  SH_HIP(hipMalloc(&g_spec.tok, 64 * 4));
-  SH_HIP(hipMalloc(&g_spec.samp, 16 * 4));
-  SH_HIP(hipMalloc(&g_spec.base, 4 * 4));
-  SH_HIP(hipMalloc(&g_spec.dlogits, (size_t)8 * V * 4));
-  SH_HIP(hipMalloc(&g_spec.tlogits, (size_t)9 * V * 4));
-  SH_HIP(hipHostMalloc((void**)&g_spec.pinned, 128 * 4, hipHostMallocDefault));
-  g_spec.vcap = V;
-  return SH_OK;
+static void free_spec_bufs(SpecBufs& sb) {
+  (void)hipFree(sb.tok); (void)hipFree(sb.samp); (void)hipFree(sb.base); (void)hipFree(sb.dlogits);
+  (void)hipFree(sb.tlogits); (void)hipFree(sb.udev); (void)hipFree(sb.rowstat); (void)hipHostFree(sb.pinned);
+  sb = SpecBufs();
 }
 
-int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts,
-                     uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter,
-                     const float* uniforms_dev, uint32_t* acc_len, uint32_t* next_tok);
+static int spec_bufs(sh_engine* e, uint32_t V) {
+  SpecBufs& sb = e->spec;
+  if (sb.tok && sb.vcap >= V) return SH_OK;
+  SH_HIP(hipSetDevice(e->device));
+  if (sb.tok) {
+    g_graph_gen.fetch_add(1);  // captured graphs point into these buffers
+    SH_HIP(hipStreamSynchronize(e->stream));
+    free_spec_bufs(sb);
+  }
+  SH_HIP(hipMalloc(&sb.tok, 64 * 4));
+  SH_HIP(hipMalloc(&sb.samp, 16 * 4));
+  SH_HIP(hipMalloc(&sb.base, 4 * 4));
+  SH_HIP(hipMalloc(&sb.dlogits, (size_t)8 * V * 4));
+  SH_HIP(hipMalloc(&sb.tlogits, (size_t)9 * V * 4));
+  SH_HIP(hipMalloc(&sb.udev, 32 * 4));
+  SH_HIP(hipMalloc(&sb.rowstat, 256 * sizeof(double2)));
+  SH_HIP(hipHostMalloc((void**)&sb.pinned, 128 * 4, hipHostMallocDefault));
+  sb.vcap = V;
+  return SH_OK;
+}
 
 // ------------------------------------------------------------------ graph replay
 
@@ -1273,12 +1273,6 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
 // writes the base values before each replay. A capture is keyed by its shape,
 // models and caches, and all captures are dropped when a model or cache is
 // destroyed. SH_GRAPH=0 turns replay off; profiling runs eagerly.
-struct GraphEntry {
-  uint64_t gen = 0;
-  std::vector<uintptr_t> key;
-  hipGraphExec_t exec = nullptr;
-};
-static thread_local std::vector<GraphEntry> g_graphs;
 
 static bool graphs_enabled(const sh_engine* e) {
   static const bool on = [] {
@@ -1288,15 +1282,16 @@ static bool graphs_enabled(const sh_engine* e) {
   return on && !e->profiling;
 }
 
-static hipGraphExec_t graph_find(const std::vector<uintptr_t>& key) {
+static hipGraphExec_t graph_find(sh_engine* e, const std::vector<uintptr_t>& key) {
   const uint64_t gen = g_graph_gen.load();
-  for (size_t i = 0; i < g_graphs.size();) {
-    if (g_graphs[i].gen != gen) {  // a model or cache it used may be gone
-      (void)hipGraphExecDestroy(g_graphs[i].exec);
-      g_graphs.erase(g_graphs.begin() + i);
+  std::vector<GraphEntry>& g = e->graphs;
+  for (size_t i = 0; i < g.size();) {
+    if (g[i].gen != gen) {  // a model or cache it used may be gone
+      (void)hipGraphExecDestroy(g[i].exec);
+      g.erase(g.begin() + i);
       continue;
     }
-    if (g_graphs[i].key == key) return g_graphs[i].exec;
+    if (g[i].key == key) return g[i].exec;
     ++i;
   }
   return nullptr;
@@ -1327,7 +1322,7 @@ static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const 
   ge.gen = g_graph_gen.load();
   ge.key = key;
   ge.exec = ex;
-  g_graphs.push_back(ge);
+  e->graphs.push_back(ge);
   *out = ex;
   return SH_OK;
 }
@@ -1337,20 +1332,20 @@ static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const 
 // drafts and per-column argmax ids are copied to the pinned staging buffer.
 static int enqueue_greedy_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t n,
                                uint32_t np, uint32_t dpos, uint32_t tpos) {
-  int rc = forward_dev(dm, dkv, g_spec.tok, np + 1, dpos, nullptr, 1, nullptr, nullptr, nullptr);
+  int rc = forward_dev(dm, dkv, e->spec.tok, np + 1, dpos, nullptr, 1, nullptr, nullptr, nullptr);
   if (rc) return rc;
-  if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)np * dm->V, dm->V, 1, dm->ws.amax, g_spec.tok + np + 1)))
+  if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)np * dm->V, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1)))
     return rc;
   for (uint32_t i = 1; i < n; ++i) {
-    if ((rc = forward_dev(dm, dkv, g_spec.tok + np + i, 1, dpos + np + i, nullptr, 1, nullptr, nullptr, nullptr)))
+    if ((rc = forward_dev(dm, dkv, e->spec.tok + np + i, 1, dpos + np + i, nullptr, 1, nullptr, nullptr, nullptr)))
       return rc;
-    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, g_spec.tok + np + 1 + i))) return rc;
+    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1 + i))) return rc;
   }
-  if ((rc = forward_dev(tm, tkv, g_spec.tok + np, n + 1, tpos, nullptr, 2, nullptr, nullptr, nullptr))) return rc;
-  if ((rc = sh_argmax_launch(e, tm->ws.logits, tm->V, n + 1, tm->ws.amax, g_spec.samp))) return rc;
-  uint32_t* hp = g_spec.pinned;
-  SH_HIP(hipMemcpyAsync(hp, g_spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
-  SH_HIP(hipMemcpyAsync(hp + 16, g_spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+  if ((rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, tpos, nullptr, 2, nullptr, nullptr, nullptr))) return rc;
+  if ((rc = sh_argmax_launch(e, tm->ws.logits, tm->V, n + 1, tm->ws.amax, e->spec.samp))) return rc;
+  uint32_t* hp = e->spec.pinned;
+  SH_HIP(hipMemcpyAsync(hp, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
+  SH_HIP(hipMemcpyAsync(hp + 16, e->spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
   return SH_OK;
 }
 
@@ -1371,30 +1366,30 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
            np, P);
   SH_CHECK((uint64_t)P + n + 1 <= tkv->max_seq && (uint64_t)P + n + 1 <= dkv->max_seq, SH_ERR_CAPACITY,
            "spec lookahead exceeds KV capacity (run.rs:270-283)");
-  int rc = spec_bufs(tm->V);
+  int rc = spec_bufs(e, tm->V);
   if (rc) return rc;
-  uint32_t* hp = g_spec.pinned;
+  uint32_t* hp = e->spec.pinned;
   for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
   hp[np] = last_token;
-  SH_HIP(hipMemcpyAsync(g_spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
+  SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
   const bool greedy_graph = mode == SH_SAMPLE_GREEDY && n + 1 <= 8 && graphs_enabled(e);
   if (mode == SH_SAMPLE_GREEDY) {
     const uint32_t d0 = dkv->pos;
     if (greedy_graph) {
       const std::vector<uintptr_t> key = {1, (uintptr_t)tm, (uintptr_t)dm, (uintptr_t)tkv, (uintptr_t)dkv,
                                           (uintptr_t)tkv->k, (uintptr_t)dkv->k, tkv->max_seq, dkv->max_seq, n, np};
-      hipGraphExec_t ex = graph_find(key);
+      hipGraphExec_t ex = graph_find(e, key);
       if (!ex) {
         if ((rc = ensure_rope(tm, tkv->max_seq)) || (rc = ensure_rope(dm, dkv->max_seq)) ||
             (rc = ensure_fa_part(tm, tkv->max_seq)) || (rc = ensure_fa_part(dm, dkv->max_seq)))
           return rc;
-        rc = graph_capture(e, key, {dkv, tkv}, {g_spec.base, g_spec.base + 1},
+        rc = graph_capture(e, key, {dkv, tkv}, {e->spec.base, e->spec.base + 1},
                            [&] { return enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, 0, 0); }, &ex);
         if (rc) return rc;
       }
       hp[64] = d0;
       hp[65] = P;
-      SH_HIP(hipMemcpyAsync(g_spec.base, hp + 64, 8, hipMemcpyHostToDevice, e->stream));
+      SH_HIP(hipMemcpyAsync(e->spec.base, hp + 64, 8, hipMemcpyHostToDevice, e->stream));
       SH_HIP(hipGraphLaunch(ex, e->stream));
       dkv->pos = d0 + np + n;  // what the eager forwards leave
       tkv->pos = P + n + 1;
@@ -1402,42 +1397,45 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
       return rc;
     }
   }
-  // 1. draft n tokens greedily, ids stay on the device (tok[np+1+i] = d_{i+1}).
-  const bool rej = mode == SH_SAMPLE_REJECTION;
+  // Stochastic modes: draft ids stay on the device (tok[np+1+i] = d_{i+1}):
+  // COMPARE drafts greedily, as the reference does (mod.rs:2062-2092);
+  // REJECTION draws d_i ~ q_i = softmax(draft logits / T) (vocab-order inverse
+  // CDF), which its min(1, p/q) test and residual draw need to be lossless.
+  // Uniform words per step: 2i / 2i+1 accept / (re)sample verify column i,
+  // 2(n+1) + i draw draft i (REJECTION); explicit uniforms are [3n + 2].
   if (mode != SH_SAMPLE_GREEDY) {
-  rc = forward_dev(dm, dkv, g_spec.tok, np + 1, dkv->pos, nullptr, 1, rej ? g_spec.dlogits : nullptr, nullptr,
-                   nullptr);
-  if (rc) return rc;
-  if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)(((np + 1) - 1) % 8) * dm->V, dm->V, 1, dm->ws.amax,
-                             g_spec.tok + np + 1)))
-    return rc;
-  for (uint32_t i = 1; i < n; ++i) {
-    rc = forward_dev(dm, dkv, g_spec.tok + np + i, 1, dkv->pos, nullptr, 1,
-                     rej ? g_spec.dlogits + (size_t)i * dm->V : nullptr, nullptr, nullptr);
-    if (rc) return rc;
-    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, g_spec.tok + np + 1 + i))) return rc;
-  }
-  // 2. verify [last, d_1..d_n] with all-position logits.
-  rc = forward_dev(tm, tkv, g_spec.tok + np, n + 1, P, nullptr, 2, g_spec.tlogits, nullptr, nullptr);
-  if (rc) return rc;
-  // 3. per-column decision on the device.
-  uint32_t* acc_dev = g_spec.samp + 9;
-  uint32_t* next_dev = g_spec.samp + 10;
-  {
-    sh_sampling ss = *s;
-    float* udev = nullptr;
+    const bool rej = mode == SH_SAMPLE_REJECTION;
+    const uint32_t V = tm->V, nu = 3 * n + 2;
+    const float* udev = nullptr;
+    uint64_t ctr = s->counter;
     if (s->uniforms) {
-      SH_HIP(hipMallocAsync((void**)&udev, (size_t)(n + 1) * 2 * 4, e->stream));
-      SH_HIP(hipMemcpyAsync(udev, s->uniforms, (size_t)(n + 1) * 2 * 4, hipMemcpyHostToDevice, e->stream));
+      SH_HIP(hipMemcpyAsync(e->spec.udev, s->uniforms, (size_t)nu * 4, hipMemcpyHostToDevice, e->stream));
+      udev = e->spec.udev;
+      ctr = 0;
     }
-    rc = sh_accept_launch(e, g_spec.tlogits, rej ? g_spec.dlogits : nullptr, g_spec.tok + np + 1, 1, n, tm->V, &ss,
-                          udev ? 0 : s->counter, udev, acc_dev, next_dev);
-    if (udev) (void)hipFreeAsync(udev, e->stream);
+    e->spec.last_n = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+      float* q = e->spec.dlogits + (size_t)i * V;
+      rc = i == 0 ? forward_dev(dm, dkv, e->spec.tok, np + 1, dkv->pos, nullptr, 1, q, nullptr, nullptr)
+                  : forward_dev(dm, dkv, e->spec.tok + np + i, 1, dkv->pos, nullptr, 1, q, nullptr, nullptr);
+      if (rc) return rc;
+      uint32_t* dst = e->spec.tok + np + 1 + i;
+      rc = rej ? sh_sample_rows_launch(e, q, 1, V, s->temperature, udev, s->seed, ctr + 2ull * (n + 1) + i, 1,
+                                       e->spec.rowstat, dst)
+               : sh_argmax_launch(e, q, V, 1, dm->ws.amax, dst);
+      if (rc) return rc;
+    }
+    // verify [last, d_1..d_n] with all-position logits, then the per-column decision on the device
+    rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, P, nullptr, 2, e->spec.tlogits, nullptr, nullptr);
     if (rc) return rc;
-    if (!udev) s->counter += 2ull * (n + 1);
-  }
-  SH_HIP(hipMemcpyAsync(hp, g_spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
-  SH_HIP(hipMemcpyAsync(hp + 16, g_spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+    rc = sh_accept_launch(e, e->spec.tlogits, rej ? e->spec.dlogits : nullptr, e->spec.tok + np + 1, 1, n, V, s, ctr,
+                          udev, e->spec.samp + 9, e->spec.samp + 10);
+    if (rc) return rc;
+    if (!udev) s->counter += nu;
+    SH_HIP(hipMemcpyAsync(hp, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
+    SH_HIP(hipMemcpyAsync(hp + 16, e->spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+    e->spec.last_n = n;
+    e->spec.last_V = V;
   }
   SH_HIP(hipStreamSynchronize(e->stream));
   uint32_t drafts[8];
@@ -1464,6 +1462,18 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   *n_emitted = ne;
   if (drafts_out) std::memcpy(drafts_out, drafts, n * 4);
   return sh_prof_flush(e);
+}
+
+extern "C" int sh_spec_step_logits(sh_engine* e, float* p_out, float* q_out, uint32_t* n_out, uint32_t* V_out) {
+  SH_CHECK(e && n_out, SH_ERR_ARG, "sh_spec_step_logits: NULL argument");
+  const uint32_t n = e->spec.last_n, V = e->spec.last_V;
+  SH_CHECK(n > 0, SH_ERR_STATE, "no stochastic speculative step has run on this engine");
+  SH_HIP(hipStreamSynchronize(e->stream));
+  if (p_out) SH_HIP(hipMemcpy(p_out, e->spec.tlogits, (size_t)(n + 1) * V * 4, hipMemcpyDeviceToHost));
+  if (q_out) SH_HIP(hipMemcpy(q_out, e->spec.dlogits, (size_t)n * V * 4, hipMemcpyDeviceToHost));
+  *n_out = n;
+  if (V_out) *V_out = V;
+  return SH_OK;
 }
 
 // ------------------------------------------------------------------ kernel level

@@ -284,10 +284,13 @@ __device__ uint32_t wg_inverse_cdf(const W& rw, uint32_t lo, uint32_t hi, bool r
   return found;
 }
 
-// COMPARE: sample every column (b, i) independently.
+// COMPARE: sample every column (b, i) independently; row r takes uniform
+// word word0 + wstride * r. The draft draws of a REJECTION speculative step
+// use the same sampler.
 __global__ __launch_bounds__(256) void k_sample_cols(const float* __restrict__ p, const double2* __restrict__ part,
                                                      uint32_t nch, uint32_t V, double inv_t, const float* u_dev,
-                                                     uint64_t seed, uint64_t counter, uint32_t* __restrict__ out) {
+                                                     uint64_t seed, uint64_t word0, uint64_t wstride,
+                                                     uint32_t* __restrict__ out) {
   __shared__ double tab[64];
   __shared__ double2 st;
   const uint32_t row = blockIdx.x;
@@ -299,7 +302,7 @@ __global__ __launch_bounds__(256) void k_sample_cols(const float* __restrict__ p
   }
   __syncthreads();
   RowW rw{p + (size_t)row * V, nullptr, st.x, 1.0, 0.0, 1.0, inv_t, tab};
-  const float u = uniform_at(u_dev, seed, counter + 2ull * row + 1ull);
+  const float u = uniform_at(u_dev, seed, word0 + wstride * row);
   const uint32_t tok = wg_inverse_cdf(rw, 0, V, true, u, 0.0, 0.0, true, nullptr);
   if (threadIdx.x == 0) out[row] = tok;
 }
@@ -327,7 +330,7 @@ __global__ __launch_bounds__(256) void k_decide_reject(const float* __restrict__
                                                        const uint32_t* __restrict__ drafts, const float* u_dev,
                                                        uint64_t seed, uint64_t counter,
                                                        uint32_t* __restrict__ first_rej,
-                                                       double2* __restrict__ rstat) {
+                                                       double2* __restrict__ rstat, double* __restrict__ probs) {
   __shared__ double tab[64];
   __shared__ double2 st[129];  // p rows 0..k, then q rows 0..k-1 (k <= 64)
   __shared__ uint32_t fr;
@@ -358,6 +361,15 @@ __global__ __launch_bounds__(256) void k_decide_reject(const float* __restrict__
       const double qd = sh_exp_neg(((double)ql - sq.x) * inv_t, tab) / sq.y;
       const float ua = uniform_at(u_dev, seed, counter + 2ull * (b * (k + 1) + t));
       accept = (double)ua * qd < pd;
+      if (probs) {  // p_t(d), q_t(d), accept probability min(1, p/q)
+        double* o = probs + 3 * ((size_t)b * k + t);
+        o[0] = pd;
+        o[1] = qd;
+        o[2] = qd > 0.0 ? fmin(1.0, pd / qd) : (pd > 0.0 ? 1.0 : 0.0);
+      }
+    } else if (probs) {
+      double* o = probs + 3 * ((size_t)b * k + t);
+      o[0] = o[1] = o[2] = 0.0;
     }
     if (!accept) atomicMin(&fr, t);
   }
@@ -804,9 +816,18 @@ __global__ __launch_bounds__(256) void k_tree_pass(const float* __restrict__ p, 
 
 }  // namespace
 
+size_t sh_accept_scratch_bytes(uint32_t B, uint32_t k, uint32_t V, uint32_t mode) {
+  const uint32_t n_p = B * (k + 1), n_q = mode == SH_SAMPLE_REJECTION ? B * k : 0;
+  const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
+  const size_t part_b = (size_t)(n_p + n_q) * nch * sizeof(double2);
+  const size_t chunk_b = (size_t)B * kDrawChunks * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
+  const size_t small_b = mode == SH_SAMPLE_COMPARE ? (size_t)n_p * 4 : (size_t)B * 4;
+  return part_b + chunk_b + rstat_b + (small_b + 255) / 256 * 256;
+}
+
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
                      uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter, const float* uniforms_dev,
-                     uint32_t* acc_len, uint32_t* next_tok) {
+                     uint32_t* acc_len, uint32_t* next_tok, void* scratch_in, double* probs_out) {
   SH_CHECK(B >= 1 && k >= 1 && k <= 64 && V >= 1, SH_ERR_ARG, "accept: B=%u k=%u V=%u", B, k, V);
   const uint32_t mode = s->mode;
   SH_CHECK(mode == SH_SAMPLE_COMPARE || mode == SH_SAMPLE_REJECTION, SH_ERR_ARG, "accept: mode %u", mode);
@@ -819,9 +840,8 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   const uint32_t nunits = nrows * nch;
   const size_t part_b = (size_t)nunits * sizeof(double2);
   const size_t chunk_b = (size_t)B * kDrawChunks * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
-  const size_t small_b = mode == SH_SAMPLE_COMPARE ? (size_t)n_p * 4 : (size_t)B * 4;
-  char* scratch = nullptr;
-  SH_HIP(hipMallocAsync((void**)&scratch, part_b + chunk_b + rstat_b + small_b, e->stream));
+  char* scratch = static_cast<char*>(scratch_in);
+  if (!scratch_in) SH_HIP(hipMallocAsync((void**)&scratch, sh_accept_scratch_bytes(B, k, V, mode), e->stream));
   double2* part = reinterpret_cast<double2*>(scratch);
   double2* chunk = reinterpret_cast<double2*>(scratch + part_b);
   double2* rstat = reinterpret_cast<double2*>(scratch + part_b + chunk_b);
@@ -839,12 +859,12 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   sh_prof_begin(e, &ev);
   if (mode == SH_SAMPLE_COMPARE) {
     hipLaunchKernelGGL(k_sample_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, part, nch, V, inv_t,
-                       uniforms_dev, s->seed, counter, small);
+                       uniforms_dev, s->seed, counter + 1ull, 2ull, small);
     hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
                        next_tok);
   } else {
     hipLaunchKernelGGL(k_decide_reject, dim3(B), dim3(256), 0, e->stream, p_logits, q_logits, part, nch, B, k, V,
-                       inv_t, drafts, uniforms_dev, s->seed, counter, small, rstat);
+                       inv_t, drafts, uniforms_dev, s->seed, counter, small, rstat, probs_out);
     hipLaunchKernelGGL(k_draw_chunks, dim3(kDrawChunks, B), dim3(256), 0, e->stream, p_logits, q_logits, k, V, inv_t,
                        small, rstat, chunk);
     hipLaunchKernelGGL(k_draw_pick, dim3(B), dim3(256), 0, e->stream, p_logits, q_logits, k, V, inv_t, small, rstat,
@@ -852,7 +872,27 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_decide", 0.0, ev);
-  SH_HIP(hipFreeAsync(scratch, e->stream));
+  if (!scratch_in) SH_HIP(hipFreeAsync(scratch, e->stream));
+  return SH_OK;
+}
+
+int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
+                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out) {
+  SH_CHECK(nrows >= 1 && V >= 1 && T > 0.f, SH_ERR_ARG, "sample_rows: nrows=%u V=%u T=%g", nrows, V, (double)T);
+  const double inv_t = 1.0 / (double)T;
+  const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  if (V % 4 == 0)
+    hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
+                       nullptr, V, inv_t, nch, part);
+  else
+    hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
+                       nullptr, V, inv_t, nch, part);
+  hipLaunchKernelGGL(k_sample_cols, dim3(nrows), dim3(256), 0, e->stream, logits, part, nch, V, inv_t, u_dev, seed,
+                     word0, wstride, out);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, "sample_rows", 4.0 * V * nrows, ev);
   return SH_OK;
 }
 
@@ -874,6 +914,37 @@ extern "C" int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const f
   if (rc) return rc;
   SH_HIP(hipStreamSynchronize(e->stream));
   return sh_prof_flush(e);
+}
+
+extern "C" int sh_accept_probs(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
+                               const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, float temperature,
+                               double* probs_dev) {
+  SH_CHECK(e && p_logits_dev && q_logits_dev && drafts_dev && probs_dev, SH_ERR_ARG,
+           "sh_accept_probs: NULL argument");
+  SH_CHECK(B >= 1 && k >= 1 && k <= 64 && V >= 1 && temperature > 0.f, SH_ERR_ARG,
+           "accept_probs: B=%u k=%u V=%u T=%g", B, k, V, (double)temperature);
+  const double inv_t = 1.0 / (double)temperature;
+  const uint32_t n_p = B * (k + 1), nrows = n_p + B * k, nch = (V + 256 * kStatE - 1) / (256 * kStatE);
+  const size_t part_b = (size_t)nrows * nch * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
+  char* scratch = nullptr;
+  SH_HIP(hipMallocAsync((void**)&scratch, part_b + rstat_b + (size_t)B * 4, e->stream));
+  double2* part = reinterpret_cast<double2*>(scratch);
+  double2* rstat = reinterpret_cast<double2*>(scratch + part_b);
+  uint32_t* fr = reinterpret_cast<uint32_t*>(scratch + part_b + rstat_b);
+  if (V % 4 == 0)
+    hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, p_logits_dev, n_p,
+                       q_logits_dev, V, inv_t, nch, part);
+  else
+    hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, p_logits_dev, n_p,
+                       q_logits_dev, V, inv_t, nch, part);
+  // the accept tests' probabilities; the uniform (word 0 of seed 0) does not affect them
+  hipLaunchKernelGGL(k_decide_reject, dim3(B), dim3(256), 0, e->stream, p_logits_dev, q_logits_dev, part, nch, B, k,
+                     V, inv_t, drafts_dev, nullptr, 0ull, 0ull, fr, rstat, probs_dev);
+  const hipError_t le = hipGetLastError();
+  (void)hipFreeAsync(scratch, e->stream);
+  SH_CHECK(le == hipSuccess, SH_ERR_HIP, "accept_probs launch: %s", hipGetErrorString(le));
+  SH_HIP(hipStreamSynchronize(e->stream));
+  return SH_OK;
 }
 
 extern "C" int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,

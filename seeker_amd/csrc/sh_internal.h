@@ -46,6 +46,29 @@ struct KStat {
   double bytes = 0.0;
 };
 
+// Device buffers of the speculative step, owned by the engine (its captured
+// graphs point into them).
+struct SpecBufs {
+  uint32_t* tok = nullptr;     // [64]: pending..., last, d_1..d_n; verify tokens at [32..]
+  uint32_t* samp = nullptr;    // [16]: per-column ids; acc_len at [9], next token at [10]
+  uint32_t* base = nullptr;    // [4] graph base positions (device): draft, target, verify
+  float* dlogits = nullptr;    // draft logits [8][V] of the last stochastic step
+  float* tlogits = nullptr;    // target logits [9][V] of the last stochastic step
+  float* udev = nullptr;       // [32] explicit uniforms of a stochastic step
+  double2* rowstat = nullptr;  // [256] row-statistics partials of the device draft draws
+  uint32_t* pinned = nullptr;  // host staging [128]
+  uint32_t vcap = 0;
+  uint32_t last_n = 0, last_V = 0;  // drafts and vocab of the last stochastic step (0: none)
+};
+
+// A captured HIP graph, keyed by its shape, models and caches; gen is the
+// model/cache generation it was captured under (see graph replay in runtime.hip).
+struct GraphEntry {
+  uint64_t gen = 0;
+  std::vector<uintptr_t> key;
+  hipGraphExec_t exec = nullptr;
+};
+
 struct sh_engine {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -58,6 +81,8 @@ struct sh_engine {
   };
   std::vector<Pending> pending;
   std::vector<hipEvent_t> event_pool;
+  SpecBufs spec;
+  std::vector<GraphEntry> graphs;
 };
 
 // A weight matrix on the device, repacked into MFMA tiles.
@@ -311,6 +336,20 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
 // the partials for a consumer that combines them itself (OPND_FA).
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids);
+// Draws one token per row from softmax(logits / T) by the vocab-order inverse
+// CDF (the COMPARE column sampler): row r uses uniform word word0 + wstride * r
+// (explicit u_dev[word] or Philox key (seed, 0x5EC)). part: nrows * ceil(V /
+// 8192) row-statistics partials of scratch.
+int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
+                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out);
+// Acceptance of B sequences (COMPARE / REJECTION), see sh_accept_sample;
+// uniforms_dev (explicit) or Philox words from counter. scratch: device
+// memory of sh_accept_scratch_bytes(B, k, V, mode) bytes, or null to allocate
+// it on the stream.
+size_t sh_accept_scratch_bytes(uint32_t B, uint32_t k, uint32_t V, uint32_t mode);
+int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
+                     uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter, const float* uniforms_dev,
+                     uint32_t* acc_len, uint32_t* next_tok, void* scratch = nullptr, double* probs_out = nullptr);
 int sh_kv_compact_launch(sh_engine* e, sh_kv* kv, uint32_t base, const uint32_t* src_dev, uint32_t n);
 
 // Profiling helpers (no-ops unless e->profiling).

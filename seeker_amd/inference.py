@@ -182,6 +182,18 @@ class Engine:
         em = emitted[: ne.value].tolist()
         return SpecStepOut(em, ne.value - 1, em[-1], drafts[:n].tolist())
 
+    def spec_step_logits(self):
+        """Target logits [(n+1)][V] and draft logits [n][V] of the last stochastic
+        decode_speculative on this engine (the reference's tap readback,
+        inference/context.rs:136-160)."""
+        n, V = C.c_uint32(), C.c_uint32()
+        N.check(self._lib.sh_spec_step_logits(self.h, None, None, C.byref(n), C.byref(V)))
+        p = np.empty((n.value + 1, V.value), np.float32)
+        q = np.empty((n.value, V.value), np.float32)
+        N.check(self._lib.sh_spec_step_logits(self.h, p.ctypes.data_as(N.F32P), q.ctypes.data_as(N.F32P),
+                                              C.byref(n), C.byref(V)))
+        return p, q
+
     # -- profiling ------------------------------------------------------------
     def set_profiling(self, on: bool):
         N.check(self._lib.sh_engine_set_profiling(self.h, int(on)))
@@ -216,6 +228,17 @@ class Engine:
                       B: int, k: int, V: int, s: N.sh_sampling, acc_len: "DeviceBuffer", next_tok: "DeviceBuffer"):
         N.check(self._lib.sh_accept_sample(self.h, p_logits.ptr, q_logits.ptr if q_logits else None, drafts.ptr,
                                            B, k, V, C.byref(s), acc_len.ptr, next_tok.ptr))
+
+    def accept_probs(self, p_logits: "DeviceBuffer", q_logits: "DeviceBuffer", drafts: "DeviceBuffer", B: int, k: int,
+                     V: int, temperature: float) -> np.ndarray:
+        """sh_accept_probs: [B][k][3] = (p(d), q(d), min(1, p/q)) of each REJECTION accept test."""
+        out = self.dev_alloc(B * k * 3 * 8)
+        try:
+            N.check(self._lib.sh_accept_probs(self.h, p_logits.ptr, q_logits.ptr, drafts.ptr, B, k, V, temperature,
+                                              out.ptr))
+            return out.read(np.float64, B * k * 3).reshape(B, k, 3)
+        finally:
+            out.free()
 
     def tree_accept(self, p_logits: "DeviceBuffer", q_logits: Optional["DeviceBuffer"], tokens: "DeviceBuffer",
                     parents: "DeviceBuffer", B: int, n: int, V: int, s: N.sh_sampling, path: "DeviceBuffer",

@@ -1,8 +1,10 @@
 """GPU acceptance kernel (sh_accept_sample) vs the oracle, configs[1] shapes:
 B sequences x k draft positions over vocab V, target logits N(0, 3), draft =
 target + N(0, 1), T = 0.8, uniforms from Philox4x64-10 (shared seeds) or
-passed explicitly. Accepted lengths and next tokens must be bit-identical;
-probabilities within 1e-5 (checked through the oracle's f64 softmax)."""
+passed explicitly. Accepted lengths and next tokens must be bit-identical.
+The accept-test probabilities p(d), q(d) and min(1, p/q) (sh_accept_probs)
+must match an independent numpy f64 softmax within 1e-5 absolute (north star)
+and 1e-10 relative."""
 import numpy as np
 import pytest
 
@@ -85,3 +87,26 @@ def test_explicit_uniforms(engine):
     for b in range(B):
         oa, on = O.rejection(p[b], q[b], drafts[b], 0.8, U[b, :k, 0].copy(), U[b, :, 1].copy())
         assert (a[b], n[b]) == (oa, on), b
+
+
+def test_accept_probs_match_numpy_f64(engine):
+    B, k, V, T = 8, 5, 128256, 0.8
+    print(f"accept probs B={B} k={k} V={V}", flush=True)
+    p, q, drafts = make_inputs(B, k, V, seed=17)
+    pd, qd, dd = engine.to_device(p), engine.to_device(q), engine.to_device(drafts)
+    got = engine.accept_probs(pd, qd, dd, B, k, V, T)
+    for b in (pd, qd, dd):
+        b.free()
+
+    def prob(row, tok):
+        z = row.astype(np.float64) / T
+        z = np.exp(z - z.max())
+        return z[tok] / z.sum()
+
+    for b in range(B):
+        for i in range(k):
+            d = int(drafts[b, i])
+            want_p, want_q = prob(p[b, i], d), prob(q[b, i], d)
+            want = np.array([want_p, want_q, min(1.0, want_p / want_q)])
+            assert np.all(np.abs(got[b, i] - want) <= 1e-5), (b, i)
+            assert np.allclose(got[b, i], want, rtol=1e-10, atol=0), (b, i, got[b, i], want)

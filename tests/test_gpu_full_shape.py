@@ -1,0 +1,188 @@
+"""GPU parity at the full layer shapes the bench times (BASELINE configs[2] and
+configs[3]), against the C oracle.
+
+The models have the exact Llama-3-8B layer shape (d 4096, 32 q / 8 kv heads,
+head_dim 128, FFN 14336, vocab 128256, Q4_K, theta 5e5) and the Llama-3.2-1B
+draft layer shape (d 2048, 32 / 8 heads, head_dim 64, FFN 8192, tied
+embeddings), with two layers each so the oracle finishes in seconds. Both
+caches are seeded with the same synthetic f16 K/V (N(0, 1)) up to the
+context, through sh_kv_write_layer and the oracle's cache, so no prefill is
+needed: the verify then runs the same kernel instantiations as the bench
+(8-column gate/up ring kernel with the fused SwiGLU, split-K Wo / down with
+fused residual preps, two-row-group attention over 4104 keys = 17 splits,
+lm_head over 128256 rows; the multi-group GEMM and device-mask attention for
+the 164-column tree batch at 8192 keys).
+
+Checks: logits within 2e-2 abs / 1e-2 rel (north star) and 3e-4 x max|logit|;
+greedy ids and tree paths identical; new K/V rows equal to the oracle's up to
+one f16 ulp (an f32-level difference occasionally rounds the other way).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from seeker_amd import synth as S
+from seeker_amd._native import GGML_Q4_K, SH_SAMPLE_REJECTION, sh_sampling
+
+pytestmark = pytest.mark.gpu
+
+T8B_2L = S.LlamaShape(2, 4096, 32, 8, 14336, 128256, 8192, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K)
+D1B_2L = S.LlamaShape(2, 2048, 32, 8, 8192, 128256, 8192, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K, True)
+
+
+def close(a, b):
+    err = np.abs(a - b)
+    assert np.all(err <= np.maximum(2e-2, 1e-2 * np.abs(b))), float(err.max())
+    assert err.max() <= 3e-4 * np.abs(b).max(), (float(err.max()), float(np.abs(b).max()))
+
+
+def f16_ulps(a, b):
+    """Distance in f16 ulps of two uint16 arrays of finite f16 values."""
+    def key(x):
+        x = x.astype(np.int32)
+        return np.where(x & 0x8000, -(x & 0x7FFF), x)
+    return np.abs(key(a) - key(b))
+
+
+def seed_kv(gkv, okv, dims, n_pos, seed):
+    """The same synthetic f16 K/V rows [0, n_pos) in the GPU and oracle caches."""
+    rng = np.random.default_rng(seed)
+    for layer in range(dims.n_layer):
+        for isv in (False, True):
+            rows = rng.standard_normal((n_pos, dims.n_head_kv, dims.head_dim)).astype(np.float16).view(np.uint16)
+            gkv.write_layer(layer, isv, rows)
+            okv.layer(layer, isv, n_pos)[:] = rows
+    gkv.set_position(n_pos)
+    okv.set_position(n_pos)
+
+
+def check_new_rows(gkv, okv, dims, lo, hi):
+    for layer in range(dims.n_layer):
+        for isv in (False, True):
+            g = gkv.read_layer(layer, isv, hi)[lo:hi]
+            o = okv.layer(layer, isv, hi)[lo:hi]
+            u = f16_ulps(g, o)
+            assert u.max() <= 1 and (u > 0).mean() < 0.02, (layer, isv, int(u.max()), float((u > 0).mean()))
+
+
+@pytest.fixture(scope="module")
+def target(engine):
+    img = S.GgufImage(T8B_2L, seed=0)
+    print("8B-shape 2-layer target", flush=True)
+    gm = engine.upload_weights(img)
+    om = O.Model(img)
+    yield gm, om
+    gm.close()
+    om.close()
+    img.close()
+
+
+@pytest.mark.timeout(600)
+def test_config2_verify_8_columns_at_4096(engine, target):
+    gm, om = target
+    d = gm.dims
+    P, L = 4096, 8
+    gkv, okv = engine.allocate_kv_cache(gm, P + 64), O.KvCache(om, P + 64)
+    seed_kv(gkv, okv, d, P, seed=1)
+    toks = S.tokens(11, L, d.n_vocab)
+    print("configs[2] verify L=8 at P=4096: forward_full", flush=True)
+    gl, gres = engine.forward_full_readback(gm, gkv, toks, P)
+    ol, ores = O.forward(om, okv, toks, P)
+    close(gl, ol)
+    close(gres, ores)
+    check_new_rows(gkv, okv, d, P, P + L)
+    print("configs[2] verify L=8 at P=4096: graph-replayed verify_greedy (twice)", flush=True)
+    for _ in range(2):
+        gkv.truncate(P)
+        ids = engine.verify_greedy(gm, gkv, toks, P)
+        assert np.array_equal(ids, ol.argmax(axis=1)), (ids, ol.argmax(axis=1))
+        assert gkv.position == P + L
+    check_new_rows(gkv, okv, d, P, P + L)
+    gkv.close()
+    okv.close()
+
+
+@pytest.mark.timeout(600)
+def test_config2_spec_step_with_1b_shape_draft(engine, target):
+    gm, om = target
+    dimg = S.GgufImage(D1B_2L, seed=1)
+    gd = engine.upload_weights(dimg)
+    od = O.Model(dimg)
+    P, k = 4096, 7
+    gtkv, otkv = engine.allocate_kv_cache(gm, P + 64), O.KvCache(om, P + 64)
+    gdkv, odkv = engine.allocate_kv_cache(gd, P + 64), O.KvCache(od, P + 64)
+    seed_kv(gtkv, otkv, gm.dims, P, seed=2)
+    seed_kv(gdkv, odkv, gd.dims, P, seed=3)
+    last = int(S.tokens(12, 1, gm.dims.n_vocab)[0])
+    print("configs[2] spec step k=7 (graph replay) vs the oracle", flush=True)
+    for step in range(2):
+        r = engine.decode_speculative(gm, gd, gtkv, gdkv, last, k)
+        o_em, o_dr = O.spec_step_greedy(om, od, otkv, odkv, last, k)
+        assert r.drafts == o_dr, (step, r.drafts, o_dr)
+        assert r.emitted == o_em, (step, r.emitted, o_em)
+        assert gtkv.position == otkv.position and gdkv.position == odkv.position
+        last = r.emitted[-1]
+    check_new_rows(gtkv, otkv, gm.dims, P, gtkv.position)
+    check_new_rows(gdkv, odkv, gd.dims, P, gdkv.position)
+    for x in (gtkv, gdkv, otkv, odkv, gd, od):
+        x.close()
+    dimg.close()
+
+
+def _tree_4_3_2():
+    parents, level = [-1], [0]
+    for b in (4, 3, 2):
+        nxt = []
+        for v in level:
+            for _ in range(b):
+                parents.append(v)
+                nxt.append(len(parents) - 1)
+        level = nxt
+    return np.array(parents, np.int32)
+
+
+@pytest.mark.timeout(900)
+def test_config3_tree_verify_b4_41_nodes_at_8192(engine, target):
+    gm, om = target
+    d = gm.dims
+    V = d.n_vocab
+    P, B = 8192, 4
+    par = _tree_4_3_2()
+    n = par.size
+    assert n == 41
+    caches = [engine.allocate_kv_cache(gm, P + 64) for _ in range(B)]
+    ocaches = [O.KvCache(om, P + 64) for _ in range(B)]
+    for b in range(B):
+        seed_kv(caches[b], ocaches[b], d, P, seed=10 + b)
+    tokens = np.stack([S.tokens(900 + b, n, V) for b in range(B)]).astype(np.uint32)
+    pars = np.tile(par, (B, 1))
+    print("configs[3] tree verify: batched logits (164 columns, multi-group path)", flush=True)
+    out = engine.verify_unified(gm, caches, tokens.ravel(), [n] * B, parents=pars.ravel(), want_logits=True)
+    gl = out.logits.reshape(B, n, V)
+    ol = []
+    for b in range(B):
+        print(f"  oracle tree forward, sequence {b}", flush=True)
+        lg, _ = O.forward(om, ocaches[b], tokens[b], P, parents=par)
+        close(gl[b], lg)
+        assert np.array_equal(out.sampled.reshape(B, n)[b], lg.argmax(axis=1))
+        ol.append(lg)
+    for b in range(B):
+        check_new_rows(caches[b], ocaches[b], d, P, P + n)
+        caches[b].truncate(P)
+    print("configs[3] tree verify step: REJECTION T=1.0, Philox seed 11, compaction", flush=True)
+    q = S.normal_f32(11, 12, B * n * V, 0.0, 3.0).reshape(B, n, V)
+    qd = engine.to_device(q)
+    s = sh_sampling()
+    s.mode, s.temperature, s.seed, s.counter = SH_SAMPLE_REJECTION, 1.0, 11, 0
+    paths, nxt = engine.tree_verify_step(gm, caches, tokens, pars, qd, s)
+    qd.free()
+    U = O.philox_uniforms(11, 0x5EC, 0, 2 * B * n).reshape(B, n, 2)
+    for b in range(B):
+        # the step's decisions on its own logits (bit-identical to the batched verify's)
+        want_path, want_next = O.tree_accept(gl[b], q[b], tokens[b], par, 1.0, U[b])
+        assert paths[b] == want_path and int(nxt[b]) == want_next, (b, paths[b], want_path)
+        assert caches[b].position == P + len(paths[b])
+        ocaches[b].compact(P, np.array(paths[b], np.uint32))
+        check_new_rows(caches[b], ocaches[b], d, P, P + len(paths[b]))
+    for x in caches + ocaches:
+        x.close()

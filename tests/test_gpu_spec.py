@@ -87,3 +87,100 @@ def test_forced_acceptance(engine, models):
     assert all(len(em) == 8 for em, _ in steps[:-1])
     o = _oracle_decode(ot, ot, prompt, 40, 7)
     assert out == o
+
+
+def _stochastic_lockstep(engine, gt, gd, ot, od, mode, T, seed, n_steps, k):
+    """Runs GPU stochastic spec steps and, per step, checks against the oracle:
+    (1) decisions bit-exact: the oracle's draft draws / argmaxes and its
+        acceptance (or_spec_draft_token, or_spec_accept) on the step's own GPU
+        logits with the same Philox words reproduce the GPU's drafts and
+        emitted tokens;
+    (2) numerics: the oracle's forwards of the same tokens (draft: pending +
+        last, then d_1..d_{n-1}; target: [last, d_1..d_n]) give logits within
+        2e-2 abs / 1e-2 rel (north star) and 3e-4 of max|logit| of the GPU's;
+    (3) both caches' positions equal the oracle's after the truncation."""
+    from seeker_amd._native import sh_sampling
+    prompt = S.tokens(1234, 64, gt.dims.n_vocab)
+    V = gt.dims.n_vocab
+    gtkv, gdkv = engine.allocate_kv_cache(gt, 512), engine.allocate_kv_cache(gd, 512)
+    otkv, odkv = O.KvCache(ot, 512), O.KvCache(od, 512)
+    lg, _ = engine.forward_full_readback(gt, gtkv, prompt, 0, full_logits=False, want_residual=False)
+    engine.forward_full_readback(gd, gdkv, prompt, 0, full_logits=False, want_residual=False)
+    O.forward(ot, otkv, prompt, 0, logits_mode=0)
+    O.forward(od, odkv, prompt, 0, logits_mode=0)
+    last, pending = int(lg[0].argmax()), []
+    s = sh_sampling()
+    s.mode, s.temperature, s.seed, s.counter = mode, T, seed, 0
+    accepted = 0
+    for step in range(n_steps):
+        P = gtkv.position
+        ctr = s.counter
+        r = engine.decode_speculative(gt, gd, gtkv, gdkv, last, k, s)
+        n = len(r.drafts)
+        assert s.counter == ctr + 3 * n + 2
+        pg, qg = engine.spec_step_logits()
+        u = O.spec_uniforms(seed, ctr, n)
+        for i in range(n):
+            assert O.spec_draft_token(mode, qg[i], T, float(u[2 * (n + 1) + i])) == r.drafts[i], (step, i)
+        assert O.spec_accept(mode, pg, qg, r.drafts, T, u) == r.emitted, step
+        # oracle forwards of the tokens the GPU fed
+        feed = pending + [last]
+        ql, _ = O.forward(od, odkv, feed, odkv.position, logits_mode=1)
+        oq = [ql[0]]
+        for i in range(1, n):
+            ql, _ = O.forward(od, odkv, [r.drafts[i - 1]], odkv.position, logits_mode=1)
+            oq.append(ql[0])
+        op, _ = O.forward(ot, otkv, [last] + r.drafts, P, logits_mode=2)
+        for got, want in ((qg, np.stack(oq)), (pg, op)):
+            err = np.abs(got - want)
+            assert np.all(err <= np.maximum(2e-2, 1e-2 * np.abs(want))), float(err.max())
+            assert err.max() <= 3e-4 * np.abs(want).max(), float(err.max())
+        acc = len(r.emitted) - 1
+        accepted += acc
+        otkv.truncate(P + acc + 1)
+        odkv.truncate(P + acc + 1)
+        pending = [r.drafts[-1]] if acc == n else []
+        assert gtkv.position == otkv.position == P + acc + 1
+        assert gdkv.position + len(pending) == gtkv.position and odkv.position == gdkv.position
+        last = r.emitted[-1]
+    for x in (gtkv, gdkv, otkv, odkv):
+        x.close()
+    return accepted
+
+
+@pytest.mark.parametrize("mode", [1, 2], ids=["compare", "rejection"])
+def test_stochastic_spec_step_lockstep(engine, models, mode):
+    gt, gd, ot, od = models
+    print(f"stochastic spec step lockstep, mode {mode}", flush=True)
+    acc = _stochastic_lockstep(engine, gt, gd, ot, od, mode, 0.8, seed=21 + mode, n_steps=12, k=4)
+    if mode == 2:
+        assert acc > 0  # near-uniform p and q: many sampled drafts are accepted
+
+
+def test_rejection_spec_step_draft_equals_target(engine, models):
+    """Draft == target model: q ~= p, so almost every sampled draft is accepted."""
+    gt, gd, ot, od = models
+    print("rejection spec step, draft = target", flush=True)
+    acc = _stochastic_lockstep(engine, gt, gt, ot, ot, 2, 0.8, seed=5, n_steps=6, k=4)
+    assert acc >= 6 * 4 - 2
+
+
+def test_spec_step_explicit_uniforms(engine, models):
+    """sh_sampling.uniforms (3n + 2 floats) gives the same step as the Philox words it replaces."""
+    from seeker_amd._native import SH_SAMPLE_REJECTION, sh_sampling
+    gt, gd, _, _ = models
+    prompt = S.tokens(4242, 32, gt.dims.n_vocab)
+    outs = []
+    for explicit in (False, True):
+        tkv, dkv = engine.allocate_kv_cache(gt, 256), engine.allocate_kv_cache(gd, 256)
+        engine.prefill(gt, tkv, prompt, 0)
+        engine.prefill(gd, dkv, prompt, 0)
+        s = sh_sampling()
+        s.mode, s.temperature, s.seed, s.counter = SH_SAMPLE_REJECTION, 0.8, 99, 40
+        keep = O.spec_uniforms(99, 40, 4)
+        if explicit:
+            s.uniforms = keep.ctypes.data_as(O.F32P)
+        r = engine.decode_speculative(gt, gd, tkv, dkv, int(prompt[-1]), 4, s)
+        outs.append((r.emitted, r.drafts, tkv.position))
+        tkv.close(); dkv.close()
+    assert outs[0] == outs[1]

@@ -17,6 +17,10 @@ path; its only checks are closed-form inputs + CPU restatements):
   or_rejection                    q == p always accepts; point-mass q gives accept
                                   rate p(d) and residual p with d removed; chi^2 ~ p
   or_spec_step_greedy             lossless: spec output == plain greedy decode
+  or_spec_step (all modes)        GREEDY == or_spec_step_greedy; REJECTION with draft ==
+                                  target accepts every draft; chi^2: the first emitted
+                                  token of COMPARE and REJECTION steps ~ p (planted
+                                  always-accept or reversed-residual mistakes fail it)
 """
 import json
 import os
@@ -510,3 +514,97 @@ def test_spec_greedy_lossless():
                 assert steps <= 5  # 5 tokens per step when every draft is accepted
             tkv.close(); dkv.close()
         tm.close(); dm.close()
+
+
+def _micro_models():
+    """A 2-layer target and 1-layer draft small enough for many spec steps (V 64)."""
+    tshape = S.LlamaShape(2, 128, 2, 2, 256, 64, 256, 1e-5, 1e4, 0.3, GGML_Q8_0, GGML_Q8_0)
+    dshape = S.LlamaShape(1, 128, 2, 2, 256, 64, 256, 1e-5, 1e4, 0.3, GGML_Q8_0, GGML_Q8_0)
+    return S.GgufImage(tshape, 5), S.GgufImage(dshape, 6)
+
+
+def _prefill(tm, dm, prompt, cap=128):
+    tkv, dkv = O.KvCache(tm, cap), O.KvCache(dm, cap)
+    lg, _ = O.forward(tm, tkv, prompt, 0, logits_mode=1)
+    O.forward(dm, dkv, prompt, 0, logits_mode=0)
+    return tkv, dkv, O.argmax(lg[0])
+
+
+def test_spec_step_greedy_mode_equals_greedy_step():
+    """or_spec_step in GREEDY mode is or_spec_step_greedy, step for step."""
+    ti, di = _micro_models()
+    with ti, di:
+        tm, dm = O.Model(ti), O.Model(di)
+        prompt = S.tokens(77, 12, tm.V)
+        a_t, a_d, last_a = _prefill(tm, dm, prompt)
+        b_t, b_d, last_b = _prefill(tm, dm, prompt)
+        for _ in range(12):
+            ea, da = O.spec_step_greedy(tm, dm, a_t, a_d, last_a, 3)
+            eb, db = O.spec_step(tm, dm, b_t, b_d, last_b, 3, O.SPEC_GREEDY)
+            assert (ea, da) == (eb, db)
+            assert a_t.position == b_t.position and a_d.position == b_d.position
+            last_a, last_b = ea[-1], eb[-1]
+        for x in (a_t, a_d, b_t, b_d, tm, dm):
+            x.close()
+
+
+def test_spec_step_rejection_q_equals_p_accepts_all():
+    """Draft == target: q == p exactly, so every sampled draft is accepted and
+    each REJECTION step emits n + 1 tokens; the drafts are the draws from q."""
+    ti, _ = _micro_models()
+    with ti:
+        tm = O.Model(ti)
+        prompt = S.tokens(78, 10, tm.V)
+        tkv, dkv, last = _prefill(tm, tm, prompt)
+        ctr = 0
+        for step in range(8):
+            u = O.spec_uniforms(3, ctr, 4)
+            em, dr, p, q = O.spec_step(tm, tm, tkv, dkv, last, 4, O.SPEC_REJECTION, 0.7, u, want_logits=True)
+            ctr += 3 * 4 + 2
+            assert len(em) == 5 and em[:4] == dr
+            assert np.array_equal(p[:4], q)
+            for i in range(4):  # each draft is the vocab-order draw from q_i with its own uniform
+                assert dr[i] == O.sample_vocab_order(q[i], 0.7, float(u[10 + i]))
+            last = em[-1]
+        for x in (tkv, dkv, tm):
+            x.close()
+
+
+@pytest.mark.parametrize("mode", [1, 2], ids=["compare", "rejection"])
+def test_spec_step_first_token_distribution_is_p(mode):
+    """Losslessness of the whole stochastic step: from a fixed state, the first
+    emitted token over many seeds is distributed as p_0 = softmax(target / T)
+    at the last token (draft and target differ, so rejections happen)."""
+    ti, di = _micro_models()
+    T = 0.5
+    with ti, di:
+        tm, dm = O.Model(ti), O.Model(di)
+        prompt = S.tokens(79, 8, tm.V)
+        tkv, dkv, last = _prefill(tm, dm, prompt)
+        P = tkv.position
+        n_s = 3000
+        cnt = np.zeros(tm.V)
+        p0 = None
+        rej = 0
+        for s in range(n_s):
+            u = O.spec_uniforms(100 + s, 0, 3)
+            em, dr, p, q = O.spec_step(tm, dm, tkv, dkv, last, 3, mode, T, u, want_logits=True)
+            cnt[em[0]] += 1
+            rej += em[0] != dr[0]
+            p0 = p[0] if p0 is None else p0
+            tkv.truncate(P)
+            dkv.truncate(P)
+            dkv.n_pending.value = 0
+        pp = O.probs(p0, T).astype(np.float64)
+        pp /= pp.sum()
+        e = n_s * pp
+        big = e >= 5
+        obs = np.append(cnt[big], cnt[~big].sum())
+        exp_ = np.append(e[big], e[~big].sum())
+        keep = exp_ > 0
+        chi2 = np.sum((obs[keep] - exp_[keep]) ** 2 / exp_[keep])
+        dof = keep.sum() - 1
+        assert rej > 100  # the draft's first token is often rejected
+        assert chi2 < dof + 6 * np.sqrt(2 * dof), (chi2, dof)
+        for x in (tkv, dkv, tm, dm):
+            x.close()
