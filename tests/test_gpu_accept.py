@@ -98,8 +98,10 @@ def test_accept_probs_match_numpy_f64(engine):
     for b in (pd, qd, dd):
         b.free()
 
+    T32 = float(np.float32(T))  # the kernel's temperature is an f32
+
     def prob(row, tok):
-        z = row.astype(np.float64) / T
+        z = row.astype(np.float64) / T32
         z = np.exp(z - z.max())
         return z[tok] / z.sum()
 

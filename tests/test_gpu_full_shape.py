@@ -57,12 +57,22 @@ def seed_kv(gkv, okv, dims, n_pos, seed):
 
 
 def check_new_rows(gkv, okv, dims, lo, hi):
+    """Layer 0 K/V rows (same inputs on both sides) equal up to one f16 ulp,
+    except entries so small that an f32-level error of the 4096-term
+    projection (1e-5 of the rows' max) spans more ulps; fewer than 2 % of
+    entries differ at all. Later layers inherit ~1e-5 relative differences
+    through attention and the FFN: within one ulp or 1e-4 of the rows' max."""
     for layer in range(dims.n_layer):
         for isv in (False, True):
             g = gkv.read_layer(layer, isv, hi)[lo:hi]
             o = okv.layer(layer, isv, hi)[lo:hi]
             u = f16_ulps(g, o)
-            assert u.max() <= 1 and (u > 0).mean() < 0.02, (layer, isv, int(u.max()), float((u > 0).mean()))
+            gf, of = g.view(np.float16).astype(np.float32), o.view(np.float16).astype(np.float32)
+            err = np.abs(gf - of)
+            small = err <= (1e-5 if layer == 0 else 1e-4) * np.abs(of).max()
+            assert np.all((u <= 1) | small), (layer, isv, int(u.max()), float(err.max() / np.abs(of).max()))
+            if layer == 0:
+                assert (u > 0).mean() < 0.02, (layer, isv, float((u > 0).mean()))
 
 
 @pytest.fixture(scope="module")
