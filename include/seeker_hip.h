@@ -203,6 +203,22 @@ int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_log
                      const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s,
                      uint32_t* acc_len_dev, uint32_t* next_tok_dev);
 
+/* No reference counterpart: sh_accept_sample for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, kernels and results; it
+ * calls no allocator and does not synchronize: the kernels are enqueued on the
+ * engine's stream and acc_len_dev / next_tok_dev are ready after
+ * sh_engine_sync (or any later synchronizing call). Its scratch is one static
+ * 2 MiB device array per GPU, set up by sh_engine_create, so sizes whose
+ * scratch exceeds it are refused with SH_ERR_CAPACITY (configs[1], B = 32,
+ * k = 8, V = 128256, needs 170 KiB; up to B = 64, k = 16, V = 262144 fits).
+ * Uniforms must come from Philox (s->uniforms NULL). The array is shared by
+ * every call on that GPU and keeps the last call's contents: calls that
+ * overlap on one GPU (other streams or engines) race. */
+int sh_accept_sample_noalloc(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
+                             const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s,
+                             uint32_t* acc_len_dev, uint32_t* next_tok_dev);
+
 /* New (no reference counterpart): the probabilities behind REJECTION's accept
  * tests, computed as sh_accept_sample computes them (f64 softmax of logits / T
  * over the same row statistics): probs_dev [B][k][3] = (p_i(d_i), q_i(d_i),

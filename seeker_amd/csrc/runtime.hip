@@ -93,6 +93,8 @@ extern "C" int sh_engine_create(int dev, sh_engine** out) {
   SH_HIP(hipGetDeviceProperties(&prop, dev));
   SH_CHECK(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0, SH_ERR_UNSUPPORTED,
            "device %d is %s; this library is built for gfx950 only", dev, prop.gcnArchName);
+  int rc = sh_static_scratch_init(dev);  // device-side scratch of sh_accept_sample_noalloc
+  if (rc) return rc;
   sh_engine* e = new sh_engine();
   e->device = dev;
   hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);

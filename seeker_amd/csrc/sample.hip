@@ -16,6 +16,8 @@
 //
 // All probability arithmetic is f64 so that the token a uniform selects does
 // not depend on summation order (GPU tree vs CPU sequential).
+#include <mutex>
+
 #include "sh_internal.h"
 #include "sh_exp.h"
 #include "sh_philox.h"
@@ -840,12 +842,12 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   const uint32_t nunits = nrows * nch;
   const size_t part_b = (size_t)nunits * sizeof(double2);
   const size_t chunk_b = (size_t)B * kDrawChunks * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
-  char* scratch = static_cast<char*>(scratch_in);
-  if (!scratch_in) SH_HIP(hipMallocAsync((void**)&scratch, sh_accept_scratch_bytes(B, k, V, mode), e->stream));
-  double2* part = reinterpret_cast<double2*>(scratch);
-  double2* chunk = reinterpret_cast<double2*>(scratch + part_b);
-  double2* rstat = reinterpret_cast<double2*>(scratch + part_b + chunk_b);
-  uint32_t* small = reinterpret_cast<uint32_t*>(scratch + part_b + chunk_b + rstat_b);
+  char* sbuf = static_cast<char*>(scratch_in);
+  if (!scratch_in) SH_HIP(hipMallocAsync((void**)&sbuf, sh_accept_scratch_bytes(B, k, V, mode), e->stream));
+  double2* part = reinterpret_cast<double2*>(sbuf);
+  double2* chunk = reinterpret_cast<double2*>(sbuf + part_b);
+  double2* rstat = reinterpret_cast<double2*>(sbuf + part_b + chunk_b);
+  uint32_t* small = reinterpret_cast<uint32_t*>(sbuf + part_b + chunk_b + rstat_b);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   if (V % 4 == 0)
@@ -872,7 +874,7 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_decide", 0.0, ev);
-  if (!scratch_in) SH_HIP(hipFreeAsync(scratch, e->stream));
+  if (!scratch_in) SH_HIP(hipFreeAsync(sbuf, e->stream));
   return SH_OK;
 }
 
@@ -926,11 +928,11 @@ extern "C" int sh_accept_probs(sh_engine* e, const float* p_logits_dev, const fl
   const double inv_t = 1.0 / (double)temperature;
   const uint32_t n_p = B * (k + 1), nrows = n_p + B * k, nch = (V + 256 * kStatE - 1) / (256 * kStatE);
   const size_t part_b = (size_t)nrows * nch * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
-  char* scratch = nullptr;
-  SH_HIP(hipMallocAsync((void**)&scratch, part_b + rstat_b + (size_t)B * 4, e->stream));
-  double2* part = reinterpret_cast<double2*>(scratch);
-  double2* rstat = reinterpret_cast<double2*>(scratch + part_b);
-  uint32_t* fr = reinterpret_cast<uint32_t*>(scratch + part_b + rstat_b);
+  char* sbuf = nullptr;
+  SH_HIP(hipMallocAsync((void**)&sbuf, part_b + rstat_b + (size_t)B * 4, e->stream));
+  double2* part = reinterpret_cast<double2*>(sbuf);
+  double2* rstat = reinterpret_cast<double2*>(sbuf + part_b);
+  uint32_t* fr = reinterpret_cast<uint32_t*>(sbuf + part_b + rstat_b);
   if (V % 4 == 0)
     hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, p_logits_dev, n_p,
                        q_logits_dev, V, inv_t, nch, part);
@@ -941,7 +943,7 @@ extern "C" int sh_accept_probs(sh_engine* e, const float* p_logits_dev, const fl
   hipLaunchKernelGGL(k_decide_reject, dim3(B), dim3(256), 0, e->stream, p_logits_dev, q_logits_dev, part, nch, B, k,
                      V, inv_t, drafts_dev, nullptr, 0ull, 0ull, fr, rstat, probs_dev);
   const hipError_t le = hipGetLastError();
-  (void)hipFreeAsync(scratch, e->stream);
+  (void)hipFreeAsync(sbuf, e->stream);
   SH_CHECK(le == hipSuccess, SH_ERR_HIP, "accept_probs launch: %s", hipGetErrorString(le));
   SH_HIP(hipStreamSynchronize(e->stream));
   return SH_OK;
@@ -1000,11 +1002,11 @@ extern "C" int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const flo
     const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE), nrows = 2 * B * n;
     const uint64_t ctr = udev ? 0ull : s->counter;
     const size_t part_b = (size_t)nrows * nch * sizeof(double2), st_b = (size_t)B * sizeof(TreeState);
-    char* scratch = nullptr;
-    SH_HIP(hipMallocAsync((void**)&scratch, part_b + st_b + (size_t)B * kDrawChunks * sizeof(double), e->stream));
-    double2* part = reinterpret_cast<double2*>(scratch);
-    TreeState* st = reinterpret_cast<TreeState*>(scratch + part_b);
-    double* chunk = reinterpret_cast<double*>(scratch + part_b + st_b);
+    char* sbuf = nullptr;
+    SH_HIP(hipMallocAsync((void**)&sbuf, part_b + st_b + (size_t)B * kDrawChunks * sizeof(double), e->stream));
+    double2* part = reinterpret_cast<double2*>(sbuf);
+    TreeState* st = reinterpret_cast<TreeState*>(sbuf + part_b);
+    double* chunk = reinterpret_cast<double*>(sbuf + part_b + st_b);
     if (V % 4 == 0)
       hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, p_logits_dev,
                          B * n, q_logits_dev, V, inv_t, nch, part);
@@ -1020,7 +1022,7 @@ extern "C" int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const flo
                            B, n, V, inv_t, part, nch, st, chunk);
     }
     le = hipGetLastError();
-    (void)hipFreeAsync(scratch, e->stream);
+    (void)hipFreeAsync(sbuf, e->stream);
   }
   sh_prof_end(e, "tree_accept", 4.0 * V * B * n * (greedy ? 1 : 2), ev);
   if (udev) (void)hipFreeAsync(udev, e->stream);
@@ -1028,4 +1030,50 @@ extern "C" int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const flo
   SH_CHECK(le == hipSuccess, SH_ERR_HIP, "tree_accept launch: %s", hipGetErrorString(le));
   SH_HIP(hipStreamSynchronize(e->stream));
   return sh_prof_flush(e);
+}
+
+// ------------------------------------------------------------ no-allocation acceptance
+
+// Device scratch of sh_accept_sample_noalloc: one array per GPU, held until
+// the process ends. In host code `scratch` names a host-side stand-in, not
+// device memory: every host use goes through the per-device address that
+// sh_static_scratch_init takes from hipGetSymbolAddress.
+constexpr size_t kStaticScratchBytes = (size_t)2 << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+void* g_scratch_dev[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+}  // namespace
+
+int sh_static_scratch_init(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  SH_CHECK(dev >= 0 && dev < kMaxDevices, SH_ERR_ARG, "static scratch: device %d out of range", dev);
+  if (g_scratch_dev[dev]) return SH_OK;
+  void* ptr = nullptr;
+  const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  SH_CHECK(err == hipSuccess && ptr, SH_ERR_HIP, "static scratch of device %d: hipGetSymbolAddress: %s", dev,
+           hipGetErrorString(err));
+  g_scratch_dev[dev] = ptr;
+  return SH_OK;
+}
+
+extern "C" int sh_accept_sample_noalloc(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
+                                        const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V,
+                                        const sh_sampling* s, uint32_t* acc_len_dev, uint32_t* next_tok_dev) {
+  SH_CHECK(e && p_logits_dev && drafts_dev && s && acc_len_dev && next_tok_dev, SH_ERR_ARG,
+           "sh_accept_sample_noalloc: NULL argument");
+  SH_CHECK(!s->uniforms, SH_ERR_ARG, "sh_accept_sample_noalloc takes Philox uniforms only (uniforms must be NULL)");
+  SH_CHECK(s->mode == SH_SAMPLE_COMPARE || s->mode == SH_SAMPLE_REJECTION, SH_ERR_ARG, "accept: mode %u", s->mode);
+  SH_CHECK(B >= 1 && k >= 1 && k <= 64 && V >= 1, SH_ERR_ARG, "accept: B=%u k=%u V=%u", B, k, V);
+  const size_t need = sh_accept_scratch_bytes(B, k, V, s->mode);
+  SH_CHECK(need <= kStaticScratchBytes, SH_ERR_CAPACITY,
+           "sh_accept_sample_noalloc: B=%u k=%u V=%u needs %zu scratch bytes, above the static %zu", B, k, V, need,
+           kStaticScratchBytes);
+  void* ptr = (e->device >= 0 && e->device < kMaxDevices) ? g_scratch_dev[e->device] : nullptr;
+  SH_CHECK(ptr, SH_ERR_STATE, "static scratch of device %d is not set up", e->device);
+  // nothing in the scratch needs to start at zero: every kernel writes what it reads
+  return sh_accept_launch(e, p_logits_dev, q_logits_dev, drafts_dev, B, k, V, s, s->counter, nullptr, acc_len_dev,
+                          next_tok_dev, ptr);
 }

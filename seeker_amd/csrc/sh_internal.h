@@ -347,6 +347,9 @@ int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uin
 // memory of sh_accept_scratch_bytes(B, k, V, mode) bytes, or null to allocate
 // it on the stream.
 size_t sh_accept_scratch_bytes(uint32_t B, uint32_t k, uint32_t V, uint32_t mode);
+// Takes the per-device address of sh_accept_sample_noalloc's static scratch
+// (once per device; call with that device current).
+int sh_static_scratch_init(int dev);
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
                      uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter, const float* uniforms_dev,
                      uint32_t* acc_len, uint32_t* next_tok, void* scratch = nullptr, double* probs_out = nullptr);
