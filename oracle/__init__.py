@@ -39,6 +39,8 @@ _SIGS = {
     "or_model_open": (C.c_int, [P, C.c_uint64, C.POINTER(P)]),
     "or_model_free": (None, [P]),
     "or_model_dims": (None, [P, U32P]),
+    "or_model_moe_dims": (None, [P, U32P]),
+    "or_moe_route": (None, [F32P, C.c_uint32, C.c_uint32, U32P, F32P]),
     "or_kv_create": (C.c_int, [P, C.c_uint32, C.POINTER(P)]),
     "or_kv_free": (None, [P]),
     "or_kv_position": (C.c_uint32, [P]),
@@ -131,6 +133,9 @@ class Model:
         d = (C.c_uint32 * 7)()
         lib().or_model_dims(h, d)
         self.n_layer, self.d, self.n_head, self.n_kv, self.hd, self.ff, self.V = list(d)
+        e = (C.c_uint32 * 4)()
+        lib().or_model_moe_dims(h, e)
+        self.arch, self.n_expert, self.n_used, self.expert_ff = list(e)
 
     def close(self):
         if self.h:
@@ -186,6 +191,15 @@ def forward(model: Model, kv: KvCache, tokens, pos: int, parents=None, logits_mo
     if rc:
         raise ValueError(f"oracle forward failed ({rc})")
     return logits[:cols], resid
+
+
+def moe_route(logits, k: int):
+    """or_moe_route: (ids [k], weights [k]) of one column's router logits."""
+    lg = _f32(logits)
+    ids = np.zeros(k, np.uint32)
+    w = np.zeros(k, np.float32)
+    lib().or_moe_route(lg.ctypes.data_as(F32P), lg.size, k, ids.ctypes.data_as(U32P), w.ctypes.data_as(F32P))
+    return ids, w
 
 
 def argmax(x) -> int:

@@ -176,11 +176,17 @@ typedef struct {
 
 typedef struct {
   const float* attn_norm; or_mat wq, wk, wv, wo;
+  const float* q_norm; const float* k_norm; /* qwen3 / qwen3moe: per-head RMSNorm weights [hd] */
   const float* ffn_norm; or_mat gate, up, down;
+  or_mat gate_inp, gate_exps, up_exps, down_exps; /* qwen3moe: router [E][d]; experts as E stacked slabs */
 } or_layer;
 
+enum { OR_ARCH_LLAMA = 0, OR_ARCH_QWEN3 = 1, OR_ARCH_QWEN3MOE = 2 };
+
 struct or_model {
-  uint32_t n_layer, d, n_head, n_kv, hd, ff, V;
+  int arch;
+  uint32_t n_layer, d, n_head, n_kv, hd, ff, V, q_dim;
+  uint32_t n_expert, n_used, eff;
   float eps, theta;
   or_mat embd, out;
   const float* out_norm;
@@ -228,6 +234,14 @@ static void rd_skip_value(rd* r, uint32_t t) {
 
 static int streq(const uint8_t* s, uint32_t n, const char* z) { return s && strlen(z) == n && memcmp(s, z, n) == 0; }
 
+/* Keys and defaults: models/llama.rs:1038-1048 ("llama."), models/qwen3.rs:
+ * 609-638 ("qwen3.": head_dim = attention.key_length, eps 1e-6, theta 1e6),
+ * and for "qwen3moe." the expert keys of models/qwen35moe.rs:4127-4129. */
+static int key_is(const uint8_t* k, uint32_t kl, const char* arch, const char* suffix) {
+  const size_t a = strlen(arch), b = strlen(suffix);
+  return kl == a + 1 + b && memcmp(k, arch, a) == 0 && k[a] == '.' && memcmp(k + a + 1, suffix, b) == 0;
+}
+
 int or_model_open(const uint8_t* img, uint64_t size, or_model** out) {
   rd r = {img, img + size, 0};
   if (size < 24 || memcmp(img, "GGUF", 4)) return 1;
@@ -236,38 +250,58 @@ int or_model_open(const uint8_t* img, uint64_t size, or_model** out) {
   if (ver < 2 || ver > 3) return 2;
   uint64_t nt = rd_u(&r, 8), nkv = rd_u(&r, 8);
   or_model* m = (or_model*)calloc(1, sizeof *m);
-  m->eps = 1e-5f; m->theta = 10000.0f;
-  uint32_t align = 32, n_kv = 0, rope_dim = 0;
+  m->arch = -1;
+  uint32_t align = 32, n_kv = 0, rope_dim = 0, key_len = 0;
+  float theta = -1.f, eps = -1.f;
+  const char* A = "";
   for (uint64_t i = 0; i < nkv && !r.bad; ++i) {
     uint32_t kl; const uint8_t* k = rd_str(&r, &kl);
     uint32_t t = (uint32_t)rd_u(&r, 4);
-    if (t == 4 || t == 6) {
+    if (t == 8 && streq(k, kl, "general.architecture")) {
+      uint32_t vl; const uint8_t* v = rd_str(&r, &vl);
+      if (streq(v, vl, "llama")) { m->arch = OR_ARCH_LLAMA; A = "llama"; }
+      else if (streq(v, vl, "qwen3")) { m->arch = OR_ARCH_QWEN3; A = "qwen3"; }
+      else if (streq(v, vl, "qwen3moe")) { m->arch = OR_ARCH_QWEN3MOE; A = "qwen3moe"; }
+    } else if (t == 4 || t == 6) {
       uint32_t v = (uint32_t)rd_u(&r, 4);
       float f; memcpy(&f, &v, 4);
       if (streq(k, kl, "general.alignment")) align = v;
-      else if (streq(k, kl, "llama.block_count")) m->n_layer = v;
-      else if (streq(k, kl, "llama.attention.head_count")) m->n_head = v;
-      else if (streq(k, kl, "llama.attention.head_count_kv")) n_kv = v;
-      else if (streq(k, kl, "llama.embedding_length")) m->d = v;
-      else if (streq(k, kl, "llama.feed_forward_length")) m->ff = v;
-      else if (streq(k, kl, "llama.vocab_size")) m->V = v;
-      else if (streq(k, kl, "llama.rope.dimension_count")) rope_dim = v;
-      else if (streq(k, kl, "llama.rope.freq_base")) m->theta = f;
-      else if (streq(k, kl, "llama.attention.layer_norm_rms_epsilon")) m->eps = f;
+      else if (key_is(k, kl, A, "block_count")) m->n_layer = v;
+      else if (key_is(k, kl, A, "attention.head_count")) m->n_head = v;
+      else if (key_is(k, kl, A, "attention.head_count_kv")) n_kv = v;
+      else if (key_is(k, kl, A, "attention.key_length")) key_len = v;
+      else if (key_is(k, kl, A, "embedding_length")) m->d = v;
+      else if (key_is(k, kl, A, "feed_forward_length")) m->ff = v;
+      else if (key_is(k, kl, A, "vocab_size")) m->V = v;
+      else if (key_is(k, kl, A, "rope.dimension_count")) rope_dim = v;
+      else if (key_is(k, kl, A, "rope.freq_base")) theta = f;
+      else if (key_is(k, kl, A, "attention.layer_norm_rms_epsilon")) eps = f;
+      else if (key_is(k, kl, A, "expert_count")) m->n_expert = v;
+      else if (key_is(k, kl, A, "expert_used_count")) m->n_used = v;
+      else if (key_is(k, kl, A, "expert_feed_forward_length")) m->eff = v;
     } else {
       rd_skip_value(&r, t);
     }
   }
-  /* defaults as models/llama.rs:1038-1048 */
+  if (m->arch < 0) { free(m); return 3; }
+  const int qwen = m->arch != OR_ARCH_LLAMA;
   m->n_kv = n_kv ? n_kv : m->n_head;
+  m->theta = theta > 0.f ? theta : (qwen ? 1e6f : 1e4f);
+  m->eps = eps >= 0.f ? eps : (qwen ? 1e-6f : 1e-5f);
   if (!m->n_layer || !m->n_head || !m->d) { free(m); return 3; }
-  m->hd = m->d / m->n_head;
+  m->hd = qwen && key_len ? key_len : m->d / m->n_head;
+  m->q_dim = m->n_head * m->hd;
+  if (m->arch == OR_ARCH_QWEN3MOE && (!m->n_expert || !m->n_used || !m->eff || m->n_used > m->n_expert)) {
+    free(m);
+    return 3;
+  }
   (void)rope_dim;
   or_tensor* ts = (or_tensor*)calloc(nt, sizeof *ts);
   for (uint64_t i = 0; i < nt && !r.bad; ++i) {
     const uint8_t* s = rd_str(&r, &ts[i].nlen);
     ts[i].name = (const char*)s;
     ts[i].nd = (uint32_t)rd_u(&r, 4);
+    ts[i].ne[1] = ts[i].ne[2] = ts[i].ne[3] = 1;
     for (uint32_t j = 0; j < ts[i].nd && j < 4; ++j) ts[i].ne[j] = rd_u(&r, 8);
     ts[i].type = (uint32_t)rd_u(&r, 4);
     ts[i].off = rd_u(&r, 8);
@@ -278,6 +312,7 @@ int or_model_open(const uint8_t* img, uint64_t size, or_model** out) {
   m->L = (or_layer*)calloc(m->n_layer, sizeof(or_layer));
   int found_out = 0, missing = 0;
   char nm[96];
+  /* matrices: rows = ne1 * ne2 (expert slabs stacked), cols = ne0 */
 #define FIND(NAME, DST_MAT, DST_F32)                                                       \
   do {                                                                                     \
     int ok = 0;                                                                            \
@@ -287,7 +322,7 @@ int or_model_open(const uint8_t* img, uint64_t size, or_model** out) {
         if (DST_MAT) {                                                                     \
           or_mat* mm = DST_MAT;                                                            \
           mm->w = data + ts[t].off; mm->type = (int)ts[t].type;                            \
-          mm->cols = ts[t].ne[0]; mm->rows = ts[t].nd > 1 ? ts[t].ne[1] : 1;               \
+          mm->cols = ts[t].ne[0]; mm->rows = ts[t].ne[1] * ts[t].ne[2];                    \
         } else {                                                                           \
           *(DST_F32) = (const float*)(data + ts[t].off);                                   \
         }                                                                                  \
@@ -299,7 +334,7 @@ int or_model_open(const uint8_t* img, uint64_t size, or_model** out) {
   for (uint64_t t = 0; t < nt; ++t)
     if (streq((const uint8_t*)ts[t].name, ts[t].nlen, "output.weight")) found_out = 1;
   if (found_out) FIND("output.weight", &m->out, (const float**)0);
-  else m->out = m->embd; /* tied: llama.rs:424 lm_head = output.unwrap_or(token_embd) */
+  else m->out = m->embd; /* tied: llama.rs:424 / qwen3.rs:673 lm_head = output.unwrap_or(token_embd) */
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     or_layer* L = &m->L[l];
 #define NM(S) (snprintf(nm, sizeof nm, "blk.%u." S, l), nm)
@@ -309,9 +344,20 @@ int or_model_open(const uint8_t* img, uint64_t size, or_model** out) {
     FIND(NM("attn_v.weight"), &L->wv, (const float**)0);
     FIND(NM("attn_output.weight"), &L->wo, (const float**)0);
     FIND(NM("ffn_norm.weight"), (or_mat*)0, &L->ffn_norm);
-    FIND(NM("ffn_gate.weight"), &L->gate, (const float**)0);
-    FIND(NM("ffn_up.weight"), &L->up, (const float**)0);
-    FIND(NM("ffn_down.weight"), &L->down, (const float**)0);
+    if (qwen) {
+      FIND(NM("attn_q_norm.weight"), (or_mat*)0, &L->q_norm);
+      FIND(NM("attn_k_norm.weight"), (or_mat*)0, &L->k_norm);
+    }
+    if (m->arch == OR_ARCH_QWEN3MOE) {
+      FIND(NM("ffn_gate_inp.weight"), &L->gate_inp, (const float**)0);
+      FIND(NM("ffn_gate_exps.weight"), &L->gate_exps, (const float**)0);
+      FIND(NM("ffn_up_exps.weight"), &L->up_exps, (const float**)0);
+      FIND(NM("ffn_down_exps.weight"), &L->down_exps, (const float**)0);
+    } else {
+      FIND(NM("ffn_gate.weight"), &L->gate, (const float**)0);
+      FIND(NM("ffn_up.weight"), &L->up, (const float**)0);
+      FIND(NM("ffn_down.weight"), &L->down, (const float**)0);
+    }
 #undef NM
   }
 #undef FIND
@@ -326,6 +372,10 @@ void or_model_free(or_model* m) { if (m) { free(m->L); free(m); } }
 
 void or_model_dims(const or_model* m, uint32_t d[7]) {
   d[0] = m->n_layer; d[1] = m->d; d[2] = m->n_head; d[3] = m->n_kv; d[4] = m->hd; d[5] = m->ff; d[6] = m->V;
+}
+
+void or_model_moe_dims(const or_model* m, uint32_t d[4]) {
+  d[0] = (uint32_t)m->arch; d[1] = m->n_expert; d[2] = m->n_used; d[3] = m->eff;
 }
 
 /* ------------------------------------------------------------------- KV */
@@ -387,6 +437,103 @@ static void rope_norm(float* x, uint32_t n_head, uint32_t hd, uint32_t pos, floa
     }
 }
 
+/* RoPE NEOX mode (qwen3.rs:349-350, rope_funcs.slang rope_neox): the pair
+ * (i, i + hd/2) rotated by theta_i = pos * base^(-2i/hd), i < hd/2. */
+static void rope_neox(float* x, uint32_t n_head, uint32_t hd, uint32_t pos, float base) {
+  const uint32_t half = hd / 2;
+  for (uint32_t h = 0; h < n_head; ++h)
+    for (uint32_t i = 0; i < half; ++i) {
+      double theta = (double)pos * pow((double)base, -2.0 * (double)i / (double)hd);
+      double c = cos(theta), s = sin(theta);
+      float* p = x + h * hd;
+      double x0 = p[i], x1 = p[i + half];
+      p[i] = (float)(x0 * c - x1 * s);
+      p[i + half] = (float)(x0 * s + x1 * c);
+    }
+}
+
+static uint64_t row_bytes(int type, uint64_t cols) {
+  switch (type) {
+    case OR_Q4_K: return cols / 256 * 144;
+    case OR_Q8_0: return cols / 32 * 34;
+    case OR_F16: return cols * 2;
+    default: return cols * 4;
+  }
+}
+
+/* MoE gating (topk_moe.slang, GATING_SOFTMAX with_norm as
+ * models/qwen35moe.rs:3168-3182): softmax of the E router logits (f64), the
+ * k largest probabilities in descending order, ties to the lower expert index,
+ * weights = selected probabilities / their sum, rounded to f32. */
+void or_moe_route(const float* logits, uint32_t E, uint32_t k, uint32_t* ids, float* w) {
+  double mx = -INFINITY, sum = 0.0;
+  for (uint32_t e = 0; e < E; ++e) if (logits[e] > mx) mx = logits[e];
+  double* p = (double*)malloc(E * sizeof(double));
+  for (uint32_t e = 0; e < E; ++e) { p[e] = exp((double)logits[e] - mx); sum += p[e]; }
+  for (uint32_t e = 0; e < E; ++e) p[e] /= sum;
+  double sel[64], ws = 0.0;
+  for (uint32_t j = 0; j < k; ++j) {
+    uint32_t best = 0;
+    double bv = -1.0;
+    for (uint32_t e = 0; e < E; ++e)
+      if (p[e] > bv) { bv = p[e]; best = e; }  /* strict >: the lower index wins ties */
+    ids[j] = best;
+    sel[j] = bv;
+    ws += bv;
+    p[best] = -2.0;
+  }
+  for (uint32_t j = 0; j < k; ++j) w[j] = (float)(sel[j] / ws);
+  free(p);
+}
+
+/* Routed-expert FFN of qwen3moe over L normalized columns xn [L][d] (the
+ * MoE step of models/qwen35moe.rs:3117-3182 without the shared expert):
+ * router logits = gate_inp xn (f64 accumulation, f32 store), or_moe_route,
+ * then per expert over the columns routed to it h = silu(gate_e x) * up_e x
+ * (as the dense FFN) and y = down_e h; out[c] = sum_j w_j y_j in selection
+ * order (f64 accumulation, f32 store). */
+static void moe_ffn(const or_model* m, const or_layer* Ly, const float* xn, uint32_t L, float* out) {
+  const uint32_t E = m->n_expert, K = m->n_used, ef = m->eff, d = m->d;
+  float* lg = (float*)malloc((size_t)L * E * 4);
+  uint32_t* ids = (uint32_t*)malloc((size_t)L * K * 4);
+  float* w = (float*)malloc((size_t)L * K * 4);
+  float* y = (float*)malloc((size_t)L * K * d * 4);  /* [col][slot][d] */
+  float* X = (float*)malloc((size_t)L * d * 4);
+  float* G = (float*)malloc((size_t)L * ef * 4);
+  float* U = (float*)malloc((size_t)L * ef * 4);
+  float* Y = (float*)malloc((size_t)L * d * 4);
+  uint32_t* who = (uint32_t*)malloc((size_t)L * 4);
+  or_gemv(Ly->gate_inp.type, Ly->gate_inp.w, E, d, xn, L, lg);
+  for (uint32_t c = 0; c < L; ++c) or_moe_route(lg + (size_t)c * E, E, K, ids + (size_t)c * K, w + (size_t)c * K);
+  const uint64_t gb = row_bytes(Ly->gate_exps.type, d), db = row_bytes(Ly->down_exps.type, ef);
+  for (uint32_t e = 0; e < E; ++e) {
+    uint32_t n = 0;
+    for (uint32_t c = 0; c < L; ++c)
+      for (uint32_t j = 0; j < K; ++j)
+        if (ids[(size_t)c * K + j] == e) {
+          who[n] = c * K + j;
+          memcpy(X + (size_t)n * d, xn + (size_t)c * d, (size_t)d * 4);
+          ++n;
+        }
+    if (!n) continue;
+    or_gemv(Ly->gate_exps.type, Ly->gate_exps.w + (uint64_t)e * ef * gb, ef, d, X, n, G);
+    or_gemv(Ly->up_exps.type, Ly->up_exps.w + (uint64_t)e * ef * gb, ef, d, X, n, U);
+    for (size_t i = 0; i < (size_t)n * ef; ++i) {
+      double x = G[i];
+      G[i] = (float)((x / (1.0 + exp(-x))) * (double)U[i]);
+    }
+    or_gemv(Ly->down_exps.type, Ly->down_exps.w + (uint64_t)e * d * db, d, ef, G, n, Y);
+    for (uint32_t i = 0; i < n; ++i) memcpy(y + (size_t)who[i] * d, Y + (size_t)i * d, (size_t)d * 4);
+  }
+  for (uint32_t c = 0; c < L; ++c)
+    for (uint32_t t = 0; t < d; ++t) {
+      double acc = 0.0;
+      for (uint32_t j = 0; j < K; ++j) acc += (double)w[(size_t)c * K + j] * (double)y[((size_t)c * K + j) * d + t];
+      out[(size_t)c * d + t] = (float)acc;
+    }
+  free(lg); free(ids); free(w); free(y); free(X); free(G); free(U); free(Y); free(who);
+}
+
 static int is_ancestor(const int32_t* parents, uint32_t a, uint32_t j) {
   /* a is ancestor-or-self of j within the chunk */
   int32_t x = (int32_t)j;
@@ -417,8 +564,9 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
   if (L == 0) return 1;
   if (kv->pos != pos) return 2;
   if (pos + L > kv->max_seq) return 3;
-  const uint32_t d = m->d, hd = m->hd, nh = m->n_head, nkv = m->n_kv, ff = m->ff;
+  const uint32_t d = m->d, hd = m->hd, nh = m->n_head, nkv = m->n_kv, ff = m->ff, qd = m->q_dim;
   const uint32_t dkv = hd * nkv, gqa = nh / nkv;
+  const uint32_t wide = qd > d ? qd : d;
   uint32_t* qpos = (uint32_t*)malloc(L * sizeof(uint32_t));
   for (uint32_t i = 0; i < L; ++i) {
     uint32_t depth = 0;
@@ -428,13 +576,13 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
   }
   float* res = (float*)malloc((size_t)L * d * 4);
   float* xn = (float*)malloc((size_t)L * d * 4);
-  float* q = (float*)malloc((size_t)L * d * 4);
+  float* q = (float*)malloc((size_t)L * wide * 4);
   float* k = (float*)malloc((size_t)L * dkv * 4);
   float* v = (float*)malloc((size_t)L * dkv * 4);
-  float* att = (float*)malloc((size_t)L * d * 4);
+  float* att = (float*)malloc((size_t)L * wide * 4);
   float* tmp = (float*)malloc((size_t)L * d * 4);
-  float* g = (float*)malloc((size_t)L * ff * 4);
-  float* u = (float*)malloc((size_t)L * ff * 4);
+  float* g = (float*)malloc((size_t)L * (ff ? ff : 1) * 4);
+  float* u = (float*)malloc((size_t)L * (ff ? ff : 1) * 4);
   /* get_rows (elementwise.rs:873): dequantized embedding rows. */
   for (uint32_t i = 0; i < L; ++i) or_dequant_row(m->embd.type, m->embd.w, tokens[i], d, res + (size_t)i * d);
   const uint32_t kvlen = pos + L;
@@ -445,9 +593,25 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
     matmul(&Ly->wq, xn, L, q);
     matmul(&Ly->wk, xn, L, k);
     matmul(&Ly->wv, xn, L, v);
-    for (uint32_t i = 0; i < L; ++i) {
-      rope_norm(q + (size_t)i * d, nh, hd, qpos[i], m->theta);
-      rope_norm(k + (size_t)i * dkv, nkv, hd, qpos[i], m->theta);
+    if (m->arch != OR_ARCH_LLAMA) {
+      /* per-head Q / K RMSNorm over head_dim, then NEOX RoPE (qwen3.rs:340-353) */
+      for (uint32_t i = 0; i < L; ++i) {
+        for (uint32_t h = 0; h < nh; ++h) {
+          float* x = q + (size_t)i * qd + (size_t)h * hd;
+          rms_norm(x, Ly->q_norm, hd, m->eps, x);
+        }
+        for (uint32_t h = 0; h < nkv; ++h) {
+          float* x = k + (size_t)i * dkv + (size_t)h * hd;
+          rms_norm(x, Ly->k_norm, hd, m->eps, x);
+        }
+        rope_neox(q + (size_t)i * qd, nh, hd, qpos[i], m->theta);
+        rope_neox(k + (size_t)i * dkv, nkv, hd, qpos[i], m->theta);
+      }
+    } else {
+      for (uint32_t i = 0; i < L; ++i) {
+        rope_norm(q + (size_t)i * d, nh, hd, qpos[i], m->theta);
+        rope_norm(k + (size_t)i * dkv, nkv, hd, qpos[i], m->theta);
+      }
     }
     /* cache write f32 -> f16 at slot pos+i (ops/cache_io.rs:191-262). */
     uint16_t* Kc = or_kv_layer(kv, l, 0);
@@ -463,7 +627,7 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
     for (int64_t j = 0; j < (int64_t)L; ++j)
       for (int64_t h = 0; h < (int64_t)nh; ++h) {
         const uint32_t kh = (uint32_t)h / gqa;
-        const float* qv = q + (size_t)j * d + (size_t)h * hd;
+        const float* qv = q + (size_t)j * qd + (size_t)h * hd;
         double* s = (double*)malloc(kvlen * sizeof(double));
         double mx = -INFINITY;
         for (uint32_t t = 0; t < kvlen; ++t) {
@@ -477,7 +641,7 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
         }
         double sum = 0.0;
         for (uint32_t t = 0; t < kvlen; ++t) { s[t] = s[t] == -INFINITY ? 0.0 : exp(s[t] - mx); sum += s[t]; }
-        float* o = att + (size_t)j * d + (size_t)h * hd;
+        float* o = att + (size_t)j * qd + (size_t)h * hd;
         for (uint32_t e = 0; e < hd; ++e) {
           double acc = 0.0;
           for (uint32_t t = 0; t < kvlen; ++t)
@@ -489,14 +653,18 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
     matmul(&Ly->wo, att, L, tmp);
     for (size_t i = 0; i < (size_t)L * d; ++i) res[i] = res[i] + tmp[i];
     for (uint32_t i = 0; i < L; ++i) rms_norm(res + (size_t)i * d, Ly->ffn_norm, d, m->eps, xn + (size_t)i * d);
-    matmul(&Ly->gate, xn, L, g);
-    matmul(&Ly->up, xn, L, u);
-    /* silu(x) = x / (1 + exp(-x)) (shaders/compute/silu.slang:21), then * up */
-    for (size_t i = 0; i < (size_t)L * ff; ++i) {
-      double x = g[i];
-      g[i] = (float)((x / (1.0 + exp(-x))) * (double)u[i]);
+    if (m->arch == OR_ARCH_QWEN3MOE) {
+      moe_ffn(m, Ly, xn, L, tmp);
+    } else {
+      matmul(&Ly->gate, xn, L, g);
+      matmul(&Ly->up, xn, L, u);
+      /* silu(x) = x / (1 + exp(-x)) (shaders/compute/silu.slang:21), then * up */
+      for (size_t i = 0; i < (size_t)L * ff; ++i) {
+        double x = g[i];
+        g[i] = (float)((x / (1.0 + exp(-x))) * (double)u[i]);
+      }
+      matmul(&Ly->down, g, L, tmp);
     }
-    matmul(&Ly->down, g, L, tmp);
     for (size_t i = 0; i < (size_t)L * d; ++i) res[i] = res[i] + tmp[i];
   }
   if (residual_out) memcpy(residual_out, res, (size_t)L * d * 4);

@@ -38,11 +38,17 @@ int or_gemv(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, 
 typedef struct or_model or_model;
 typedef struct or_kv or_kv;
 
-/* Parse a Llama GGUF image kept in caller memory (must outlive the model). */
+/* Parse a llama / qwen3 / qwen3moe GGUF image kept in caller memory (must
+ * outlive the model). */
 int or_model_open(const uint8_t* img, uint64_t size, or_model** out);
 void or_model_free(or_model* m);
 /* n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab */
 void or_model_dims(const or_model* m, uint32_t dims[7]);
+/* architecture (0 llama, 1 qwen3, 2 qwen3moe), n_expert, n_expert_used, expert_ff */
+void or_model_moe_dims(const or_model* m, uint32_t dims[4]);
+/* MoE gating: softmax over E logits, top-k (descending, ties to the lower
+ * index), weights renormalized to sum 1 (topk_moe.slang with_norm). */
+void or_moe_route(const float* logits, uint32_t E, uint32_t k, uint32_t* ids, float* w);
 
 int or_kv_create(const or_model* m, uint32_t max_seq, or_kv** out);
 void or_kv_free(or_kv* kv);

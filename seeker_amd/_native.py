@@ -57,6 +57,19 @@ class sh_kernel_stat(C.Structure):
     ]
 
 
+class sh_synth_cfg(C.Structure):
+    _fields_ = [
+        ("arch", C.c_uint32),
+        ("n_layer", C.c_uint32), ("n_embd", C.c_uint32), ("n_head", C.c_uint32),
+        ("n_head_kv", C.c_uint32), ("head_dim", C.c_uint32), ("n_ff", C.c_uint32), ("n_vocab", C.c_uint32),
+        ("n_ctx", C.c_uint32), ("n_expert", C.c_uint32), ("n_expert_used", C.c_uint32), ("expert_ff", C.c_uint32),
+        ("rms_eps", C.c_float), ("rope_base", C.c_float), ("weight_std", C.c_float),
+        ("norm_jitter", C.c_float), ("router_std", C.c_float),
+        ("wtype", C.c_uint32), ("etype", C.c_uint32), ("tied", C.c_uint32),
+        ("seed", C.c_uint64),
+    ]
+
+
 class sh_synth_llama_cfg(C.Structure):
     _fields_ = [
         ("n_layer", C.c_uint32), ("n_embd", C.c_uint32), ("n_head", C.c_uint32),
@@ -119,6 +132,7 @@ SIGNATURES = {
 }
 
 SYNTH_SIGNATURES = {
+    "sh_synth_gguf": (C.c_int, [C.POINTER(sh_synth_cfg), C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(C.c_uint64)]),
     "sh_synth_llama_gguf": (C.c_int, [C.POINTER(sh_synth_llama_cfg), C.POINTER(C.POINTER(C.c_uint8)),
                                       C.POINTER(C.c_uint64)]),
     "sh_synth_free": (None, [P]),

@@ -1,8 +1,8 @@
 // Synthetic GGUF model generator (host-only, OpenMP).
 //
-// Produces GGUF v3 byte images of Llama-architecture models whose weights are
-// N(0, std) draws from a counter-based Philox4x64-10 stream, quantized to Q8_0
-// or Q4_K by the quantizer below. The reference never quantizes weights (it
+// Produces GGUF v3 byte images of Llama, Qwen3 and Qwen3-MoE architecture
+// models whose weights are N(0, std) draws from a counter-based
+// Philox4x64-10 stream, quantized to Q8_0 or Q4_K by the quantizer below. The reference never quantizes weights (it
 // only reads GGUF files), so the quantizer is an input generator, not a parity
 // target: the GPU path and the CPU oracle both read the SAME bytes.
 //
@@ -10,10 +10,12 @@
 // (magic "GGUF", version 3, u64 counts, metadata KV, tensor infos, data section
 // aligned to `general.alignment` = 32) and block layouts from
 // crates/seeker-core/src/gguf/types.rs:92-136 (Q8_0 = 32 elem / 34 B,
-// Q4_K = 256 elem / 144 B). Llama metadata keys and tensor names follow
-// crates/seeker-vulkan/src/models/llama.rs:1038-1048 and :1074-1090.
+// Q4_K = 256 elem / 144 B). Metadata keys and tensor names follow
+// crates/seeker-vulkan/src/models/llama.rs:1038-1048 and :1074-1090,
+// models/qwen3.rs:591-698 and models/qwen35moe.rs:126-130, 4118-4131.
 #include <cmath>
 #include <cstdint>
+#include <functional>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -122,10 +124,10 @@ void quant_q4_k_block(const float* x, uint8_t* out) {
 
 struct TensorSpec {
   std::string name;
-  uint64_t ne0, ne1;  // ne0 = contracting / innermost dim, ne1 = rows
+  uint64_t ne0, ne1, ne2;  // ne0 = contracting / innermost dim, ne1 = rows, ne2 = expert slabs
   uint32_t type;
-  bool ones;          // norm weight: all 1.0 (f32)
-  uint64_t offset;    // within data section
+  int kind;                // 0: N(0, weight_std) quantized; 1: norm weight 1 + jitter N(0, 1); 2: f32 N(0, router_std)
+  uint64_t offset;         // within data section
   uint64_t bytes;
 };
 
@@ -139,11 +141,22 @@ uint64_t tensor_bytes(uint32_t type, uint64_t n) {
   return 0;
 }
 
-void fill_tensor(const TensorSpec& t, uint64_t seed, uint64_t stream, float stdv, uint8_t* dst) {
-  const uint64_t n = t.ne0 * t.ne1;
-  if (t.ones) {
-    float one = 1.f;
-    for (uint64_t i = 0; i < n; ++i) std::memcpy(dst + 4 * i, &one, 4);
+void fill_tensor(const TensorSpec& t, uint64_t seed, uint64_t stream, float stdv, float jitter, float router_std,
+                 uint8_t* dst) {
+  const uint64_t n = t.ne0 * t.ne1 * t.ne2;
+  if (t.kind != 0) {  // f32: norm weights (1 + jitter z) or the router (router_std z)
+    const int64_t nb = (int64_t)((n + 3) / 4);
+#pragma omp parallel for schedule(static, 256)
+    for (int64_t b = 0; b < nb; ++b) {
+      double z[4];
+      normals4(seed, stream, (uint64_t)b, z);
+      for (int i = 0; i < 4; ++i) {
+        const uint64_t e = (uint64_t)b * 4 + i;
+        if (e >= n) break;
+        const float v = t.kind == 1 ? (float)(1.0 + (double)jitter * z[i]) : (float)((double)router_std * z[i]);
+        std::memcpy(dst + 4 * e, &v, 4);
+      }
+    }
     return;
   }
   const uint64_t blk = t.type == GT_Q4_K ? 256 : 32;
@@ -166,74 +179,107 @@ void fill_tensor(const TensorSpec& t, uint64_t seed, uint64_t stream, float stdv
 
 extern "C" {
 
-// Configuration of a synthetic Llama model. wtype/etype are GGML type ids
-// (8 = Q8_0, 12 = Q4_K) for the 2-D weights and token_embd respectively.
-typedef struct sh_synth_llama_cfg {
-  uint32_t n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx;
-  float rms_eps, rope_base, weight_std;
+// Configuration of a synthetic model. arch: 0 llama (models/llama.rs:1038-1090),
+// 1 qwen3 (models/qwen3.rs:591-698: decoupled head_dim, attn_q_norm /
+// attn_k_norm), 2 qwen3moe (qwen3 attention; ffn_gate_inp f32 [n_embd,
+// n_expert] router and 3-D ffn_{gate,up,down}_exps slabs, the layout of
+// models/qwen35moe.rs:126-130). wtype/etype are GGML type ids (8 = Q8_0,
+// 12 = Q4_K) of the matrices and token_embd. head_dim 0 = n_embd / n_head.
+typedef struct sh_synth_cfg {
+  uint32_t arch;
+  uint32_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_ctx;
+  uint32_t n_expert, n_expert_used, expert_ff;
+  float rms_eps, rope_base, weight_std, norm_jitter, router_std;
   uint32_t wtype, etype;
   uint32_t tied;  // 1: no output.weight (lm_head = token_embd)
   uint64_t seed;
-} sh_synth_llama_cfg;
+} sh_synth_cfg;
 
 // Build a GGUF v3 image in host memory. *out is malloc'd; free with
 // sh_synth_free. Returns 0 on success.
-int sh_synth_llama_gguf(const sh_synth_llama_cfg* c, uint8_t** out, uint64_t* size) {
-  if (!c || !out || !size) return 1;
-  if (c->n_head == 0 || c->n_embd % c->n_head || c->n_head % (c->n_head_kv ? c->n_head_kv : 1)) return 2;
+int sh_synth_gguf(const sh_synth_cfg* c, uint8_t** out, uint64_t* size) {
+  if (!c || !out || !size || c->arch > 2) return 1;
+  if (c->n_head == 0 || c->n_head % (c->n_head_kv ? c->n_head_kv : 1)) return 2;
+  if (c->head_dim == 0 && c->n_embd % c->n_head) return 2;
+  const bool qwen = c->arch != 0, moe = c->arch == 2;
   const uint32_t wt = c->wtype, et = c->etype;
   const uint64_t qk_w = wt == GT_Q4_K ? 256 : 32, qk_e = et == GT_Q4_K ? 256 : 32;
-  const uint64_t d = c->n_embd, ff = c->n_ff, hd = d / c->n_head, dkv = hd * c->n_head_kv;
-  if (d % qk_w || ff % qk_w || d % qk_e) return 3;
+  const uint64_t d = c->n_embd, ff = c->n_ff, hd = c->head_dim ? c->head_dim : d / c->n_head;
+  const uint64_t qd = hd * c->n_head, dkv = hd * c->n_head_kv, E = c->n_expert, ef = c->expert_ff;
+  if (d % qk_w || qd % qk_w || d % qk_e || (!moe && ff % qk_w) || (moe && (ef % qk_w || !E || !c->n_expert_used)))
+    return 3;
 
   std::vector<TensorSpec> ts;
-  ts.push_back({"token_embd.weight", d, c->n_vocab, et, false, 0, 0});
+  ts.push_back({"token_embd.weight", d, c->n_vocab, 1, et, 0, 0, 0});
   for (uint32_t i = 0; i < c->n_layer; ++i) {
     std::string p = "blk." + std::to_string(i) + ".";
-    ts.push_back({p + "attn_norm.weight", d, 1, GT_F32, true, 0, 0});
-    ts.push_back({p + "attn_q.weight", d, d, wt, false, 0, 0});
-    ts.push_back({p + "attn_k.weight", d, dkv, wt, false, 0, 0});
-    ts.push_back({p + "attn_v.weight", d, dkv, wt, false, 0, 0});
-    ts.push_back({p + "attn_output.weight", d, d, wt, false, 0, 0});
-    ts.push_back({p + "ffn_norm.weight", d, 1, GT_F32, true, 0, 0});
-    ts.push_back({p + "ffn_gate.weight", d, ff, wt, false, 0, 0});
-    ts.push_back({p + "ffn_up.weight", d, ff, wt, false, 0, 0});
-    ts.push_back({p + "ffn_down.weight", ff, d, wt, false, 0, 0});
+    ts.push_back({p + "attn_norm.weight", d, 1, 1, GT_F32, 1, 0, 0});
+    ts.push_back({p + "attn_q.weight", d, qd, 1, wt, 0, 0, 0});
+    ts.push_back({p + "attn_k.weight", d, dkv, 1, wt, 0, 0, 0});
+    ts.push_back({p + "attn_v.weight", d, dkv, 1, wt, 0, 0, 0});
+    if (qwen) {
+      ts.push_back({p + "attn_q_norm.weight", hd, 1, 1, GT_F32, 1, 0, 0});
+      ts.push_back({p + "attn_k_norm.weight", hd, 1, 1, GT_F32, 1, 0, 0});
+    }
+    ts.push_back({p + "attn_output.weight", qd, d, 1, wt, 0, 0, 0});
+    ts.push_back({p + "ffn_norm.weight", d, 1, 1, GT_F32, 1, 0, 0});
+    if (moe) {
+      ts.push_back({p + "ffn_gate_inp.weight", d, E, 1, GT_F32, 2, 0, 0});
+      ts.push_back({p + "ffn_gate_exps.weight", d, ef, E, wt, 0, 0, 0});
+      ts.push_back({p + "ffn_up_exps.weight", d, ef, E, wt, 0, 0, 0});
+      ts.push_back({p + "ffn_down_exps.weight", ef, d, E, wt, 0, 0, 0});
+    } else {
+      ts.push_back({p + "ffn_gate.weight", d, ff, 1, wt, 0, 0, 0});
+      ts.push_back({p + "ffn_up.weight", d, ff, 1, wt, 0, 0, 0});
+      ts.push_back({p + "ffn_down.weight", ff, d, 1, wt, 0, 0, 0});
+    }
   }
-  ts.push_back({"output_norm.weight", d, 1, GT_F32, true, 0, 0});
-  if (!c->tied) ts.push_back({"output.weight", d, c->n_vocab, wt, false, 0, 0});
+  ts.push_back({"output_norm.weight", d, 1, 1, GT_F32, 1, 0, 0});
+  if (!c->tied) ts.push_back({"output.weight", d, c->n_vocab, 1, wt, 0, 0, 0});
 
+  const std::string A = c->arch == 0 ? "llama" : (c->arch == 1 ? "qwen3" : "qwen3moe");
   Buf h;
+  std::vector<std::function<void()>> kvs;
+  auto kv_str = [&](std::string k, std::string v) { kvs.push_back([&h, k, v] { h.str(k); h.u32(MV_STRING); h.str(v); }); };
+  auto kv_u32 = [&](std::string k, uint32_t v) { kvs.push_back([&h, k, v] { h.str(k); h.u32(MV_U32); h.u32(v); }); };
+  auto kv_f32 = [&](std::string k, float v) { kvs.push_back([&h, k, v] { h.str(k); h.u32(MV_F32); h.f32(v); }); };
+  kv_str("general.architecture", A);
+  kv_u32("general.alignment", 32);
+  kv_u32(A + ".block_count", c->n_layer);
+  kv_u32(A + ".attention.head_count", c->n_head);
+  kv_u32(A + ".attention.head_count_kv", c->n_head_kv);
+  kv_u32(A + ".embedding_length", c->n_embd);
+  if (!moe) kv_u32(A + ".feed_forward_length", c->n_ff);
+  kv_u32(A + ".context_length", c->n_ctx);
+  kv_u32(A + ".rope.dimension_count", (uint32_t)hd);
+  kv_f32(A + ".rope.freq_base", c->rope_base);
+  kv_f32(A + ".attention.layer_norm_rms_epsilon", c->rms_eps);
+  kv_u32(A + ".vocab_size", c->n_vocab);
+  if (qwen) {
+    kv_u32(A + ".attention.key_length", (uint32_t)hd);
+    kv_u32(A + ".attention.value_length", (uint32_t)hd);
+  }
+  if (moe) {
+    kv_u32(A + ".expert_count", c->n_expert);
+    kv_u32(A + ".expert_used_count", c->n_expert_used);
+    kv_u32(A + ".expert_feed_forward_length", c->expert_ff);
+  }
   h.raw("GGUF", 4);
   h.u32(3);
   h.u64(ts.size());
-  const uint64_t n_kv = 12;
-  h.u64(n_kv);
-  auto kv_str = [&](const char* k, const char* v) { h.str(k); h.u32(MV_STRING); h.str(v); };
-  auto kv_u32 = [&](const char* k, uint32_t v) { h.str(k); h.u32(MV_U32); h.u32(v); };
-  auto kv_f32 = [&](const char* k, float v) { h.str(k); h.u32(MV_F32); h.f32(v); };
-  kv_str("general.architecture", "llama");
-  kv_u32("general.alignment", 32);
-  kv_u32("llama.block_count", c->n_layer);
-  kv_u32("llama.attention.head_count", c->n_head);
-  kv_u32("llama.attention.head_count_kv", c->n_head_kv);
-  kv_u32("llama.embedding_length", c->n_embd);
-  kv_u32("llama.feed_forward_length", c->n_ff);
-  kv_u32("llama.context_length", c->n_ctx);
-  kv_u32("llama.rope.dimension_count", (uint32_t)hd);
-  kv_f32("llama.rope.freq_base", c->rope_base);
-  kv_f32("llama.attention.layer_norm_rms_epsilon", c->rms_eps);
-  kv_u32("llama.vocab_size", c->n_vocab);
+  h.u64(kvs.size());
+  for (auto& f : kvs) f();
 
   uint64_t off = 0;
   for (auto& t : ts) {
-    t.bytes = tensor_bytes(t.type, t.ne0 * t.ne1);
+    t.bytes = tensor_bytes(t.type, t.ne0 * t.ne1 * t.ne2);
     t.offset = off;
     off += (t.bytes + 31) / 32 * 32;
   }
   for (auto& t : ts) {
     h.str(t.name);
-    if (t.ne1 == 1) { h.u32(1); h.u64(t.ne0); }
+    if (t.ne2 > 1) { h.u32(3); h.u64(t.ne0); h.u64(t.ne1); h.u64(t.ne2); }
+    else if (t.ne1 == 1) { h.u32(1); h.u64(t.ne0); }
     else { h.u32(2); h.u64(t.ne0); h.u64(t.ne1); }
     h.u32(t.type);
     h.u64(t.offset);
@@ -244,10 +290,31 @@ int sh_synth_llama_gguf(const sh_synth_llama_cfg* c, uint8_t** out, uint64_t* si
   if (!img) return 4;
   std::memcpy(img, h.b.data(), h.b.size());
   for (size_t i = 0; i < ts.size(); ++i)
-    fill_tensor(ts[i], c->seed, (uint64_t)i, c->weight_std, img + data_start + ts[i].offset);
+    fill_tensor(ts[i], c->seed, (uint64_t)i, c->weight_std, c->norm_jitter, c->router_std,
+                img + data_start + ts[i].offset);
   *out = img;
   *size = total;
   return 0;
+}
+
+// The Llama subset of sh_synth_cfg (norm weights all 1).
+typedef struct sh_synth_llama_cfg {
+  uint32_t n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx;
+  float rms_eps, rope_base, weight_std;
+  uint32_t wtype, etype;
+  uint32_t tied;
+  uint64_t seed;
+} sh_synth_llama_cfg;
+
+int sh_synth_llama_gguf(const sh_synth_llama_cfg* c, uint8_t** out, uint64_t* size) {
+  if (!c) return 1;
+  sh_synth_cfg g{};
+  g.arch = 0;
+  g.n_layer = c->n_layer; g.n_embd = c->n_embd; g.n_head = c->n_head; g.n_head_kv = c->n_head_kv;
+  g.n_ff = c->n_ff; g.n_vocab = c->n_vocab; g.n_ctx = c->n_ctx;
+  g.rms_eps = c->rms_eps; g.rope_base = c->rope_base; g.weight_std = c->weight_std;
+  g.wtype = c->wtype; g.etype = c->etype; g.tied = c->tied; g.seed = c->seed;
+  return sh_synth_gguf(&g, out, size);
 }
 
 void sh_synth_free(void* p) { std::free(p); }

@@ -1,4 +1,5 @@
-"""Synthetic inputs: Llama GGUF images with N(0, std) weights and random prompts.
+"""Synthetic inputs: Llama / Qwen3 / Qwen3-MoE GGUF images with N(0, std)
+weights and random prompts.
 
 The configurations of BASELINE.json are reproduced here by name. Weights are
 quantized by the generator in csrc/synth.cpp; the reference reads GGUF files
@@ -30,6 +31,13 @@ class LlamaShape:
     wtype: int = N.GGML_Q4_K
     etype: int = N.GGML_Q4_K
     tied: bool = False
+    arch: int = 0            # 0 llama, 1 qwen3, 2 qwen3moe
+    head_dim: int = 0        # 0: n_embd / n_head
+    n_expert: int = 0
+    n_expert_used: int = 0
+    expert_ff: int = 0
+    norm_jitter: float = 0.0  # norm weights 1 + jitter * N(0, 1) (0: all ones)
+    router_std: float = 0.0   # f32 router weights N(0, router_std)
 
 
 # tiny Llama target / 1-layer draft, Q8_0.
@@ -38,18 +46,28 @@ TINY_DRAFT = LlamaShape(1, 512, 8, 8, 1408, 32000, 1024, 1e-5, 1e4, 0.02, N.GGML
 # Llama-3-8B-shape target, Llama-3.2-1B-shape draft (tied), Q4_K.
 L8B_TARGET = LlamaShape(32, 4096, 32, 8, 14336, 128256, 8192, 1e-5, 5e5, 0.02, N.GGML_Q4_K, N.GGML_Q4_K)
 L1B_DRAFT = LlamaShape(16, 2048, 32, 8, 8192, 128256, 8192, 1e-5, 5e5, 0.02, N.GGML_Q4_K, N.GGML_Q4_K, True)
+# Qwen3-30B-A3B-shape MoE target (router logits ~ N(0, 1): f32 router
+# weights N(0, 1/sqrt(n_embd)) against a unit-RMS normalized input) and the
+# Qwen3-0.6B-shape draft (tied embeddings), Q4_K.
+Q30B_A3B_TARGET = LlamaShape(48, 2048, 32, 4, 0, 151936, 40960, 1e-6, 1e6, 0.02, N.GGML_Q4_K, N.GGML_Q4_K, False,
+                             arch=2, head_dim=128, n_expert=128, n_expert_used=8, expert_ff=768, norm_jitter=0.1,
+                             router_std=2048 ** -0.5)
+Q06B_DRAFT = LlamaShape(28, 1024, 16, 8, 3072, 151936, 40960, 1e-6, 1e6, 0.02, N.GGML_Q4_K, N.GGML_Q4_K, True,
+                        arch=1, head_dim=128, norm_jitter=0.1)
 
 
 class GgufImage:
     """A GGUF byte image owned by the synth library (freed on close)."""
 
     def __init__(self, shape: LlamaShape, seed: int):
-        cfg = N.sh_synth_llama_cfg(
-            shape.n_layer, shape.n_embd, shape.n_head, shape.n_head_kv, shape.n_ff, shape.n_vocab, shape.n_ctx,
-            shape.rms_eps, shape.rope_base, shape.weight_std, shape.wtype, shape.etype, int(shape.tied), seed)
+        cfg = N.sh_synth_cfg(
+            shape.arch, shape.n_layer, shape.n_embd, shape.n_head, shape.n_head_kv, shape.head_dim, shape.n_ff,
+            shape.n_vocab, shape.n_ctx, shape.n_expert, shape.n_expert_used, shape.expert_ff, shape.rms_eps,
+            shape.rope_base, shape.weight_std, shape.norm_jitter, shape.router_std, shape.wtype, shape.etype,
+            int(shape.tied), seed)
         ptr = C.POINTER(C.c_uint8)()
         size = C.c_uint64()
-        rc = N.synth().sh_synth_llama_gguf(C.byref(cfg), C.byref(ptr), C.byref(size))
+        rc = N.synth().sh_synth_gguf(C.byref(cfg), C.byref(ptr), C.byref(size))
         if rc:
             raise N.SeekerError(rc, f"synthetic GGUF generation failed ({shape})")
         self.shape = shape

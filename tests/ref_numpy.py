@@ -219,3 +219,134 @@ class RefLlama:
         for li in range(self.nl):
             self.K[li] = self.K[li][:p]
             self.Vc[li] = self.Vc[li][:p]
+
+
+class RefQwen(RefLlama):
+    """float64 Qwen3 / Qwen3-MoE forward: decoupled head_dim (attention.key_length),
+    per-head RMSNorm of q and k with learned [head_dim] weights before a
+    rotate-half ("NEOX") RoPE that pairs element i with i + head_dim/2, and for
+    qwen3moe a routed FFN: softmax router, top-k experts by probability (ties
+    to the lower index), weights divided by their sum, weighted sum of
+    per-expert SwiGLU FFNs."""
+
+    def __init__(self, buf: bytes):
+        meta, T, _ = read_gguf(buf)
+        self.arch = meta["general.architecture"]
+        A = self.arch + "."
+        self.nl = meta[A + "block_count"]
+        self.d = meta[A + "embedding_length"]
+        self.nh = meta[A + "attention.head_count"]
+        self.nkv = meta.get(A + "attention.head_count_kv", self.nh)
+        self.hd = meta.get(A + "attention.key_length", self.d // self.nh)
+        self.eps = meta.get(A + "attention.layer_norm_rms_epsilon", 1e-6)
+        self.base = meta.get(A + "rope.freq_base", 1e6)
+        self.moe = self.arch == "qwen3moe"
+        if self.moe:
+            self.E = meta[A + "expert_count"]
+            self.k = meta[A + "expert_used_count"]
+            self.ef = meta[A + "expert_feed_forward_length"]
+
+        def mat(name):
+            dims, typ, data = T[name]
+            rows = int(np.prod(dims[1:])) if len(dims) > 1 else 1
+            return dequant(typ, data, rows, dims[0])
+
+        self.emb = mat("token_embd.weight")
+        self.V = self.emb.shape[0]
+        self.out = mat("output.weight") if "output.weight" in T else self.emb
+        self.onorm = mat("output_norm.weight")[0]
+        self.layers = []
+        names = ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "attn_q_norm", "attn_k_norm", "ffn_norm"]
+        names += ["ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"] if self.moe else \
+            ["ffn_gate", "ffn_up", "ffn_down"]
+        for i in range(self.nl):
+            W = {k: mat(f"blk.{i}.{k}.weight") for k in names}
+            if self.moe:
+                W["ffn_gate_exps"] = W["ffn_gate_exps"].reshape(self.E, self.ef, self.d)
+                W["ffn_up_exps"] = W["ffn_up_exps"].reshape(self.E, self.ef, self.d)
+                W["ffn_down_exps"] = W["ffn_down_exps"].reshape(self.E, self.d, self.ef)
+            self.layers.append(W)
+        self.K = [np.zeros((0, self.nkv, self.hd)) for _ in range(self.nl)]
+        self.Vc = [np.zeros((0, self.nkv, self.hd)) for _ in range(self.nl)]
+
+    def rope(self, x, pos):
+        half = self.hd // 2
+        th = np.asarray(pos, dtype=np.float64)[:, None] * self.base ** (-2.0 * np.arange(half) / self.hd)[None, :]
+        c, s = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+        a, b = x[..., :half], x[..., half:]
+        return np.concatenate([a * c - b * s, a * s + b * c], axis=-1)
+
+    def headnorm(self, x, w):
+        return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * w[0]
+
+    def route(self, logits):
+        z = np.exp(logits - logits.max())
+        p = z / z.sum()
+        order = np.argsort(-p, kind="stable")[: self.k]  # descending, lower index first on ties
+        return order, p[order] / p[order].sum()
+
+    def ffn(self, W, h2):
+        if not self.moe:
+            g = h2 @ W["ffn_gate"].T
+            u = h2 @ W["ffn_up"].T
+            a = (g / (1 + np.exp(-g)) * u).astype(np.float32).astype(np.float64)
+            return a @ W["ffn_down"].T
+        out = np.zeros_like(h2)
+        logits = (h2 @ W["ffn_gate_inp"].T).astype(np.float32).astype(np.float64)
+        for c in range(h2.shape[0]):
+            ids, w = self.route(logits[c])
+            w = w.astype(np.float32).astype(np.float64)
+            for e, we in zip(ids, w):
+                g = W["ffn_gate_exps"][e] @ h2[c]
+                u = W["ffn_up_exps"][e] @ h2[c]
+                a = (g / (1 + np.exp(-g)) * u).astype(np.float32).astype(np.float64)
+                out[c] += we * (W["ffn_down_exps"][e] @ a).astype(np.float32).astype(np.float64)
+        return out
+
+    def forward(self, tokens, parents=None):
+        L = len(tokens)
+        P = self.K[0].shape[0]
+        if parents is None:
+            parents = [i - 1 for i in range(L)]
+        depth = []
+        for i in range(L):
+            depth.append(0 if parents[i] < 0 else depth[parents[i]] + 1)
+        anc = np.zeros((L, L), dtype=bool)
+        for j in range(L):
+            x = j
+            while x >= 0:
+                anc[j, x] = True
+                x = parents[x]
+        pos = P + np.array(depth)
+        x = self.emb[np.asarray(tokens)].copy()
+        gqa = self.nh // self.nkv
+        for li, W in enumerate(self.layers):
+            h = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * W["attn_norm"][0]
+            q = (h @ W["attn_q"].T).astype(np.float32).astype(np.float64).reshape(L, self.nh, self.hd)
+            k = (h @ W["attn_k"].T).astype(np.float32).astype(np.float64).reshape(L, self.nkv, self.hd)
+            v = (h @ W["attn_v"].T).reshape(L, self.nkv, self.hd)
+            q = self.rope(self.headnorm(q, W["attn_q_norm"]), pos)
+            k = self.rope(self.headnorm(k, W["attn_k_norm"]), pos)
+            k16 = k.astype(np.float32).astype(np.float16).astype(np.float64)
+            v16 = v.astype(np.float32).astype(np.float16).astype(np.float64)
+            self.K[li] = np.concatenate([self.K[li], k16])
+            self.Vc[li] = np.concatenate([self.Vc[li], v16])
+            Kc, Vc = self.K[li], self.Vc[li]
+            att = np.zeros((L, self.nh, self.hd))
+            q32 = q.astype(np.float32).astype(np.float64)
+            for hh in range(self.nh):
+                kh = hh // gqa
+                s = q32[:, hh, :] @ Kc[:, kh, :].T / np.sqrt(self.hd)
+                mask = np.ones_like(s, dtype=bool)
+                mask[:, P:] = anc
+                s = np.where(mask, s, -np.inf)
+                s = s - s.max(axis=1, keepdims=True)
+                p = np.exp(s)
+                p /= p.sum(axis=1, keepdims=True)
+                att[:, hh, :] = p @ Vc[:, kh, :]
+            att = att.reshape(L, self.nh * self.hd).astype(np.float32).astype(np.float64)
+            x = (x + att @ W["attn_output"].T).astype(np.float32).astype(np.float64)
+            h2 = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * W["ffn_norm"][0]
+            x = (x + self.ffn(W, h2)).astype(np.float32).astype(np.float64)
+        f = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * self.onorm
+        return f @ self.out.T, x

@@ -608,3 +608,66 @@ def test_spec_step_first_token_distribution_is_p(mode):
         assert chi2 < dof + 6 * np.sqrt(2 * dof), (chi2, dof)
         for x in (tkv, dkv, tm, dm):
             x.close()
+
+
+# ------------------------------------------------------------------ qwen3 / qwen3moe
+
+QWEN3_SMALL = S.LlamaShape(2, 256, 4, 2, 512, 700, 256, 1e-6, 1e6, 0.02, GGML_Q4_K, GGML_Q4_K, True, arch=1,
+                           head_dim=128, norm_jitter=0.2)
+QWEN3MOE_SMALL = S.LlamaShape(2, 256, 4, 2, 0, 700, 256, 1e-6, 1e6, 0.05, GGML_Q4_K, GGML_Q4_K, False, arch=2,
+                              head_dim=128, n_expert=16, n_expert_used=4, expert_ff=256, norm_jitter=0.2,
+                              router_std=1 / 16)
+
+
+@pytest.mark.parametrize("shape", [QWEN3_SMALL, QWEN3MOE_SMALL], ids=["qwen3", "qwen3moe"])
+def test_qwen_forward_matches_numpy(shape):
+    """Decoupled head_dim (q width 512 > n_embd 256), per-head Q/K RMSNorm with
+    non-unit weights, NEOX RoPE, and for qwen3moe the routed FFN, against the
+    independent numpy f64 forward; then a second chunk (prefix + causal) and a
+    tree chunk."""
+    with S.GgufImage(shape, seed=12) as img:
+        ref = R.RefQwen(bytes(img.bytes()))
+        m = O.Model(img)
+        assert m.arch == shape.arch and m.hd == 128
+        kv = O.KvCache(m, 64)
+        toks = S.tokens(5, 10, m.V)
+        lg, res = O.forward(m, kv, toks, 0)
+        rl, rr = ref.forward(toks)
+        # row 0 attends to itself only: f32-level agreement; later rows also see
+        # other rows' f16 V, where an f32-level difference occasionally rounds
+        # to the neighbouring f16 (one ulp, ~1e-4 of the row after attention)
+        np.testing.assert_allclose(res[0], rr[0], rtol=1e-5, atol=1e-5 * np.abs(rr[0]).max())
+        np.testing.assert_allclose(lg[0], rl[0], rtol=1e-4, atol=1e-4 * np.abs(rl[0]).max())
+        np.testing.assert_allclose(res, rr, rtol=1e-3, atol=5e-4 * np.abs(rr).max())
+        np.testing.assert_allclose(lg, rl, rtol=1e-3, atol=1e-3 * np.abs(rl).max())
+        par = [-1, 0, 0, 1]
+        t2 = S.tokens(6, 4, m.V)
+        lg2, _ = O.forward(m, kv, t2, 10, parents=par)
+        rl2, _ = ref.forward(t2, parents=par)
+        np.testing.assert_allclose(lg2, rl2, rtol=1e-3, atol=1e-3 * np.abs(rl2).max())
+        for li in range(m.n_layer):  # layer 0 from the same inputs: one f16 ulp at most
+            k = kv.layer(li, False, 14).view(np.float16).astype(np.float64)
+            if li == 0:
+                r = ref.K[li].astype(np.float16).view(np.uint16).astype(np.int32)
+                assert np.abs(kv.layer(li, False, 14).astype(np.int32) - r).max() <= 1
+            assert np.abs(k - ref.K[li]).max() <= 1e-3 * np.abs(ref.K[li]).max()
+        kv.close()
+        m.close()
+
+
+def test_moe_route_closed_forms():
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        E, k = 128, 8
+        lg = rng.standard_normal(E).astype(np.float32)
+        ids, w = O.moe_route(lg, k)
+        # top-k of the softmax = top-k of the logits (monotone), in descending order
+        want = np.argsort(-lg.astype(np.float64), kind="stable")[:k]
+        assert list(ids) == list(want)
+        assert abs(float(w.astype(np.float64).sum()) - 1.0) < 1e-6
+        assert np.all(np.diff(w) <= 0)
+        # weights are softmax restricted to the selection: w_i / w_j = exp(l_i - l_j)
+        np.testing.assert_allclose(w[1:] / w[0], np.exp(lg[ids[1:]].astype(np.float64) - lg[ids[0]]), rtol=1e-6)
+    # ties go to the lower expert index
+    ids, w = O.moe_route(np.array([0.5, 2.0, 2.0, 1.0, 2.0], np.float32), 3)
+    assert list(ids) == [1, 2, 4] and np.allclose(w, 1 / 3)
