@@ -1060,6 +1060,187 @@ __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ par
              ea.out + (size_t)col * ea.Dq);
 }
 
+// QKV of a qwen3 layer from split partials (models/qwen3.rs:330-362): one
+// workgroup of hd threads per (head, column), thread i owning row i of the
+// head. The split sum; for q and k heads the per-head RMSNorm over head_dim
+// with weight w[i] (rms_norm.slang:39-55 over rows of head_dim) and RoPE, NEOX
+// (pair (i, i + hd/2), rope_funcs.slang rope_neox) or NORM (pair (2j, 2j+1));
+// q rows to ea.out [col][Dq], roped k rows and raw v rows to the column's
+// cache slot (V slot-permuted within its 32-key block).
+__global__ __launch_bounds__(128) void k_qkv_finish_head(const float* __restrict__ part, uint32_t nparts,
+                                                          size_t part_stride, uint32_t ldp, EpiArgs ea, QkvCols qc,
+                                                          const float* __restrict__ q_norm,
+                                                          const float* __restrict__ k_norm, float eps, int neox) {
+  __shared__ float sy[128];
+  __shared__ float sw[2];
+  const uint32_t h = blockIdx.x, col = blockIdx.y, i = threadIdx.x, hd = ea.hd, half = hd / 2;
+  const uint32_t nq = ea.Dq / hd, nkv = ea.n_kv;
+  const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
+  const uint32_t hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
+  const uint32_t row = kind == 0 ? hh * hd + i : (kind == 1 ? ea.Dq + hh * hd + i : ea.Dq + ea.Dkv + hh * hd + i);
+  const float* p = part + (size_t)col * ldp + row;
+  float v = 0.f;
+  for (uint32_t k0 = 0; k0 < nparts; k0 += 8) {  // 8 loads in flight, split order kept
+    float t[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) t[j] = p[(size_t)min(k0 + j, nparts - 1) * part_stride];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      if (k0 + j < nparts) v += t[j];
+  }
+  const int32_t pos = qc.pos[col];
+  const uint32_t slot = qc.slot[col], ms = qc.mseq[col];
+  if (kind == 2) {
+    uint16_t* vb = qc.vc[col] + (((size_t)ea.layer * nkv + hh) * (ms / 32) + slot / 32) * hd * 32;
+    vb[(size_t)i * 32 + v_slot(slot & 31)] = f2h_bits(v);
+    return;  // uniform per workgroup
+  }
+  const float* w = kind == 0 ? q_norm : k_norm;
+  if (w) {
+    float ss = v * v;
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((i & 63) == 0) sw[i >> 6] = ss;
+    __syncthreads();
+    ss = hd > 64 ? sw[0] + sw[1] : sw[0];
+    v = v * (1.0f / sqrtf(ss / (float)hd + eps)) * w[i];
+  }
+  sy[i] = v;
+  __syncthreads();
+  float o;
+  if (neox) {
+    const uint32_t j = i < half ? i : i - half;
+    const float2 cs = ea.rope[(size_t)pos * half + j];
+    o = i < half ? v * cs.x - sy[i + half] * cs.y : sy[i - half] * cs.y + v * cs.x;
+  } else {
+    const float2 cs = ea.rope[(size_t)pos * half + i / 2];
+    o = (i & 1) ? sy[i - 1] * cs.y + v * cs.x : v * cs.x - sy[i + 1] * cs.y;
+  }
+  if (kind == 0) {
+    ea.out[(size_t)col * ea.Dq + row] = o;
+  } else {
+    qc.kc[col][(((size_t)ea.layer * nkv + hh) * ms + slot) * hd + i] = f2h_bits(o);
+  }
+}
+
+// ------------------------------------------------------------------ Q4_K expert-indirect
+
+// Expert-indirect GEMM of a routed MoE FFN (the MUL_MAT_ID matvec of
+// ops/moe.rs:164 / mul_mat_vec_q4_k.slang's id variant, here batched over the
+// columns routed to each expert): W holds E expert slabs of tiles_e row tiles.
+// Chunk c of the routing plan, info[1 + 3c .. +3] = (expert e, first sorted
+// pair p0, n <= 8 pairs), multiplies slab e by the operand columns col[p]
+// (the pairs' input columns, gathered lane by lane from the operand groups;
+// col == null: column p) and stores the slab's rows for pair p at out[p][row]
+// (EPI_STORE, whole K in one workgroup). Grid: max chunks x rb_e row blocks
+// of 8 T tiles; workgroups past info[0] chunks exit at once. The superblock
+// pipeline (operand fragments staged in LDS by direct loads, two buffers) is
+// the multi-group kernel's with one gathered group.
+template <int T>
+__global__ __launch_bounds__(512) void k_moe_gemm_q4(const uint8_t* __restrict__ Wp, uint32_t tiles_e,
+                                                      uint32_t nsb, uint32_t rb_e, const uint16_t* __restrict__ Bx,
+                                                      const uint16_t* __restrict__ XS, const float* __restrict__ CS,
+                                                      const uint32_t* __restrict__ info,
+                                                      const uint32_t* __restrict__ gcol, EpiArgs ea) {
+  __shared__ h8 sB[2][9 * 64];
+  __shared__ float sC[2][64];
+  const uint32_t chunk = blockIdx.x / rb_e, rb = blockIdx.x % rb_e;
+  if (chunk >= info[0]) return;  // uniform per workgroup
+  const uint32_t e = info[1 + 3 * chunk], p0 = info[2 + 3 * chunk], n = info[3 + 3 * chunk];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4, r = lane & 15;
+  const uint32_t tile0 = (rb * 8 + wave) * T;
+  const size_t gB = (size_t)nsb * 8 * 512, gX = (size_t)nsb * 512, gC = (size_t)nsb * 8;
+  const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
+  // this lane's column slot (lane & 7) and the operand column it gathers
+  const uint32_t slot = (uint32_t)(lane & 7) < n ? (uint32_t)(lane & 7) : n - 1;
+  const uint32_t col = gcol ? gcol[p0 + slot] : p0 + slot;
+  const uint32_t cg = col / 8, cl = col % 8;
+  const float nf = col_rinv_g(ea, cg, cl);
+  const uint8_t* We = Wp + (size_t)e * tiles_e * nsb * SH_Q4K_TILE_BYTES;
+
+  auto stage = [&](uint32_t sb, int buf) {
+    for (uint32_t fi = wave; fi < 9u; fi += 8) {
+      const uint16_t* src;
+      if (fi < 8) {
+        src = Bx + cg * gB + ((size_t)(sb * 8 + fi) * 64 + 16 * g4 + cl + 8 * ((lane >> 3) & 1)) * 8;
+      } else {  // XS: lanes 0-15 hold the sums (hi, lo), the rest zero
+        const uint32_t ls = lane < 16 ? cl + 8 * ((lane >> 3) & 1) : (uint32_t)lane;
+        src = XS + cg * gX + ((size_t)sb * 64 + ls) * 8;
+      }
+      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&sB[buf][fi * 64]), 16, 0, 0);
+    }
+    if (wave == 7)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(CS + cg * gC + sb * 8 + cl), (lds_void_t*)sC[buf], 4, 0, 0);
+  };
+  auto a_ptr = [&](int t, uint32_t sb) {
+    const uint32_t tt = tile0 + t < tiles_e ? tile0 + t : tiles_e - 1;  // clamp keeps loads in the slab
+    return We + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
+  };
+  f4 y[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Q4Tile (&at)[T], int buf) {
+    Q4Dec dec[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) dec[t] = q4_decode_setup(at[t]);
+    f4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const h8 b = sB[buf][m * 64 + lane];
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[t] = mfma16(q4_frag(dec[t], m, magic), b, acc[t]);
+    }
+    const h8 bm = sB[buf][8 * 64 + lane];
+    const float c = sC[buf][lane & 7];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const f4 macc = mfma16(q4_min_frag(dec[t], magic), bm, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[t][j] = y[t][j] + c * (dec[t].d[j] * acc[t][j] - dec[t].dmin[j] * macc[j]);
+    }
+  };
+  Q4Tile wa[T], wb[T];
+  stage(0, 0);
+#pragma unroll
+  for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, 0), lane, g4, r);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (uint32_t sb = 0; sb < nsb; sb += 2) {
+    if (sb + 1 < nsb) {
+      stage(sb + 1, 1);
+#pragma unroll
+      for (int t = 0; t < T; ++t) wb[t] = load_q4_tile(a_ptr(t, sb + 1), lane, g4, r);
+    }
+    compute(wa, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (sb + 1 >= nsb) break;
+    if (sb + 2 < nsb) {
+      stage(sb + 2, 0);
+#pragma unroll
+      for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, sb + 2), lane, g4, r);
+    }
+    compute(wb, 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    float o[4];
+    col_sum4(y[t], nf, o);
+    const uint32_t tile = tile0 + t;
+    if (tile < tiles_e && (uint32_t)r < n) {
+      const uint32_t r0 = tile * 16 + 4 * g4;
+      float* dst = ea.out + (size_t)(p0 + r) * ea.ldo + r0;
+      for (int j = 0; j < 4; ++j)
+        if (r0 + j < ea.rows) dst[j] = o[j];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ Q8_0
 
 // Q8_0 GEMV: a workgroup of W waves owns R row tiles; wave w takes the 32-blocks
@@ -1623,5 +1804,38 @@ int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_
                      ldp, ea, qc);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "qkv_finish", 0.0, ev);
+  return SH_OK;
+}
+
+int sh_qkv_finish_head_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
+                              uint32_t N, const EpiArgs& ea, const QkvCols& qc, const float* q_norm,
+                              const float* k_norm, float eps, bool neox) {
+  SH_CHECK(N >= 1 && N <= SH_MAX_COLS && (ea.hd == 64 || ea.hd == 128) && ea.Dq % ea.hd == 0, SH_ERR_ARG,
+           "qkv head finish shape");
+  const uint32_t heads = ea.Dq / ea.hd + 2 * ea.n_kv;
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  hipLaunchKernelGGL(k_qkv_finish_head, dim3(heads, N), dim3(ea.hd), 0, e->stream, part, nparts, part_stride, ldp, ea,
+                     qc, q_norm, k_norm, eps, neox ? 1 : 0);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, "qkv_finish", 0.0, ev);
+  return SH_OK;
+}
+
+int sh_moe_gemm_launch(sh_engine* e, const QMat& w, uint32_t n_expert, const uint16_t* bx, const uint16_t* xs,
+                       const float* cs, uint32_t max_chunks, const uint32_t* info, const uint32_t* gcol,
+                       const EpiArgs& ea, const char* tag, double alg_bytes) {
+  SH_CHECK(w.type == GGML_Q4_K && w.K % 256 == 0 && n_expert >= 1 && w.tiles % n_expert == 0, SH_ERR_UNSUPPORTED,
+           "expert gemm needs Q4_K expert slabs of whole tiles");
+  SH_CHECK(ea.out && ea.ldo >= w.M / n_expert, SH_ERR_ARG, "expert gemm output");
+  const uint32_t tiles_e = w.tiles / n_expert, nsb = w.K / 256;
+  constexpr int T = 1;
+  const uint32_t rb_e = (tiles_e + 8 * T - 1) / (8 * T);
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  hipLaunchKernelGGL((k_moe_gemm_q4<T>), dim3(max_chunks * rb_e), dim3(512), 0, e->stream, w.d, tiles_e, nsb, rb_e,
+                     bx, xs, cs, info, gcol, ea);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, tag, alg_bytes, ev);
   return SH_OK;
 }

@@ -310,8 +310,24 @@ int sh_gguf_describe(const GFile& f, ModelDesc* m) {
 }
 
 int sh_gguf_supported(const ModelDesc& m) {
-  SH_CHECK(m.arch == ARCH_LLAMA, SH_ERR_UNSUPPORTED, "architecture %d: this build runs llama only", m.arch);
   const uint32_t wt = m.layers.empty() ? (uint32_t)GGML_Q4_K : m.layers[0].wq.type;
+  if (m.arch != ARCH_LLAMA) {
+    // qwen3 / qwen3moe run on the multi-group Q4_K kernels
+    SH_CHECK(m.output.type == GGML_Q4_K, SH_ERR_UNSUPPORTED, "qwen lm_head type %u (Q4_K only)", m.output.type);
+    for (uint32_t l = 0; l < m.n_layer; ++l) {
+      const LayerDesc& L = m.layers[l];
+      for (const TRef* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down, &L.gate_exps, &L.up_exps,
+                            &L.down_exps})
+        if (t->present())
+          SH_CHECK(t->type == GGML_Q4_K, SH_ERR_UNSUPPORTED, "layer %u: qwen matrix type %u (Q4_K only)", l, t->type);
+      if (L.gate_inp.present())
+        SH_CHECK(L.gate_inp.type == GGML_F32, SH_ERR_UNSUPPORTED, "layer %u: router type %u (f32 only)", l,
+                 L.gate_inp.type);
+    }
+    SH_CHECK(m.arch != ARCH_QWEN3MOE || (m.n_expert <= 1024 && m.d % 4 == 0 && (m.d + m.n_expert) * 4 <= 60 * 1024),
+             SH_ERR_UNSUPPORTED, "moe: %u experts at n_embd %u", m.n_expert, m.d);
+    return SH_OK;
+  }
   SH_CHECK(wt == GGML_Q4_K || wt == GGML_Q8_0, SH_ERR_UNSUPPORTED, "weight type %u (Q4_K / Q8_0 only)", wt);
   for (uint32_t l = 0; l < m.n_layer; ++l) {
     const LayerDesc& L = m.layers[l];
@@ -338,7 +354,8 @@ extern "C" int sh_gguf_inspect(const void* data, uint64_t size, sh_model_dims* o
   out->weight_type = m.layers.empty() ? -1 : (int32_t)m.layers[0].wo.type;
   double bytes = (double)m.output.rows * (double)m.output.row_bytes;
   for (const LayerDesc& L : m.layers)
-    for (const TRef* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
+    for (const TRef* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down, &L.gate_exps, &L.up_exps,
+                          &L.down_exps})
       if (t->present()) bytes += (double)t->rows * (double)t->row_bytes * (double)t->n_mat;
   out->weight_bytes = bytes;
   return SH_OK;

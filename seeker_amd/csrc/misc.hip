@@ -122,7 +122,7 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
 
 int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
   SH_CHECK(a.K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", a.K);
-  SH_CHECK(a.N >= 1 && a.N <= SH_MAX_COLS, SH_ERR_ARG, "prep N=%u outside [1, %u]", a.N, SH_MAX_COLS);
+  SH_CHECK(a.N >= 1 && a.N <= SH_MAX_PREP_COLS, SH_ERR_ARG, "prep N=%u outside [1, %u]", a.N, SH_MAX_PREP_COLS);
   SH_CHECK(a.part_cols >= a.N || a.nparts == 0, SH_ERR_ARG, "prep: partials hold %u columns, N=%u", a.part_cols, a.N);
   SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");
   SH_CHECK(a.mode != PREP_RESID || a.nparts == 0 || a.part, SH_ERR_ARG, "prep partials missing");

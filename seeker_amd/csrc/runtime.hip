@@ -204,6 +204,11 @@ static void free_model(sh_model* m) {
     sh_qmat_free(&L.wo);
     sh_qmat_free(&L.wgu);
     sh_qmat_free(&L.wdown);
+    (void)hipFree(L.q_norm);
+    (void)hipFree(L.k_norm);
+    (void)hipFree(L.router);
+    sh_qmat_free(&L.wgu_exps);
+    sh_qmat_free(&L.wdown_exps);
   }
   sh_qmat_free(&m->lm_head);
   (void)hipFree(m->embd_raw);
@@ -214,6 +219,9 @@ static void free_model(sh_model* m) {
   (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
   (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq);
   (void)hipFree(w.bx2); (void)hipFree(w.xs2); (void)hipFree(w.cs2); (void)hipFree(w.ssq2); (void)hipFree(w.sb_cnt);
+  (void)hipFree(w.moe_ids); (void)hipFree(w.moe_wts); (void)hipFree(w.moe_info); (void)hipFree(w.moe_col);
+  (void)hipFree(w.moe_slot); (void)hipFree(w.moe_hgu); (void)hipFree(w.moe_bx); (void)hipFree(w.moe_xs);
+  (void)hipFree(w.moe_cs); (void)hipFree(w.moe_y);
   delete m;
 }
 
@@ -252,6 +260,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   m->e = e;
   m->n_layer = md.n_layer; m->n_head = md.n_head; m->n_kv = md.n_kv; m->d = md.d; m->ff = md.ff;
   m->n_ctx = md.n_ctx; m->theta = md.theta; m->eps = md.eps; m->hd = md.hd; m->V = md.V;
+  m->arch = md.arch; m->q_dim = md.q_dim(); m->neox = md.neox;
+  m->n_expert = md.n_expert; m->n_used = md.n_expert_used; m->eff = md.expert_ff;
   int fail = SH_OK;
 #define FAIL(code, ...)                 \
   do {                                  \
@@ -282,27 +292,47 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
     Layer& L = m->layers[l];
     if ((fail = upload_f32(D.attn_norm, &L.attn_norm)) || (fail = upload_f32(D.ffn_norm, &L.ffn_norm)))
       FAIL(fail, "%s", sh_last_error());
+    if (D.q_norm.present() &&
+        ((fail = upload_f32(D.q_norm, &L.q_norm)) || (fail = upload_f32(D.k_norm, &L.k_norm))))
+      FAIL(fail, "%s", sh_last_error());
     const uint8_t* parts[3] = {D.wq.data, D.wk.data, D.wv.data};
-    const uint32_t rows[3] = {m->d, dkv, dkv};
+    const uint32_t rows[3] = {m->q_dim, dkv, dkv};
     if ((fail = sh_repack_upload_cat(e, (int)wtype, parts, rows, 3, m->d, &L.wqkv))) FAIL(fail, "%s", sh_last_error());
-    if ((fail = sh_repack_upload(e, (int)wtype, D.wo.data, m->d, m->d, &L.wo))) FAIL(fail, "%s", sh_last_error());
-    if ((fail = sh_repack_upload_gu(e, (int)wtype, D.gate.data, D.up.data, m->ff, m->d, &L.wgu)))
-      FAIL(fail, "%s", sh_last_error());
-    if ((fail = sh_repack_upload(e, (int)wtype, D.down.data, m->d, m->ff, &L.wdown)))
-      FAIL(fail, "%s", sh_last_error());
+    if ((fail = sh_repack_upload(e, (int)wtype, D.wo.data, m->d, m->q_dim, &L.wo))) FAIL(fail, "%s", sh_last_error());
+    if (m->n_expert) {
+      const size_t rb = (size_t)m->n_expert * m->d * 4;
+      if (hipMalloc(&L.router, rb) != hipSuccess ||
+          hipMemcpy(L.router, D.gate_inp.data, rb, hipMemcpyHostToDevice) != hipSuccess)
+        FAIL(SH_ERR_HIP, "router upload failed");
+      if ((fail = sh_repack_upload_gu(e, GGML_Q4_K, D.gate_exps.data, D.up_exps.data, m->n_expert * m->eff, m->d,
+                                      &L.wgu_exps)))
+        FAIL(fail, "%s", sh_last_error());
+      if ((fail = sh_repack_upload(e, GGML_Q4_K, D.down_exps.data, m->n_expert * m->d, m->eff, &L.wdown_exps)))
+        FAIL(fail, "%s", sh_last_error());
+      m->alg_weight_bytes += L.wgu_exps.alg_bytes + L.wdown_exps.alg_bytes + 4.0 * m->n_expert * m->d;
+    } else {
+      if ((fail = sh_repack_upload_gu(e, (int)wtype, D.gate.data, D.up.data, m->ff, m->d, &L.wgu)))
+        FAIL(fail, "%s", sh_last_error());
+      if ((fail = sh_repack_upload(e, (int)wtype, D.down.data, m->d, m->ff, &L.wdown)))
+        FAIL(fail, "%s", sh_last_error());
+    }
     m->alg_weight_bytes += L.wqkv.alg_bytes + L.wo.alg_bytes + L.wgu.alg_bytes + L.wdown.alg_bytes + 8.0 * m->d;
   }
   m->alg_weight_bytes += 4.0 * m->d;
   {
     auto q4 = [](const QMat& q) { return q.type == GGML_Q4_K && q.K % 256 == 0; };
     bool ok = q4(m->lm_head);
-    for (const Layer& L : m->layers) ok = ok && q4(L.wqkv) && q4(L.wo) && q4(L.wgu) && q4(L.wdown);
+    for (const Layer& L : m->layers)
+      ok = ok && q4(L.wqkv) && q4(L.wo) &&
+           (m->n_expert ? q4(L.wgu_exps) && q4(L.wdown_exps) : q4(L.wgu) && q4(L.wdown));
     m->mg_ok = ok;
+    if (m->arch != ARCH_LLAMA && !ok) FAIL(SH_ERR_UNSUPPORTED, "qwen models run on Q4_K matrices only");
   }
   // workspace for up to SH_MAX_COLS columns per chunk (operands: 8 groups of 8)
   Workspace& w = m->ws;
   w.max_cols = SH_MAX_COLS;
-  const uint32_t kmax = std::max(m->d, m->ff), ngrp = SH_MAX_COLS / 8;
+  const uint32_t kmax = std::max({m->d, m->ff, m->q_dim, m->eff}), ngrp = SH_MAX_COLS / 8;
+  const uint32_t wide = std::max(m->d, m->q_dim);  // q and attention rows
   const size_t bx_elems = ngrp * sh_grp_bx(kmax);
   const size_t xs_elems = ngrp * sh_grp_xs(kmax);
   const size_t part_floats =  // grown on demand in forward_dev
@@ -315,8 +345,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   const size_t C = SH_MAX_COLS;
   if (dalloc(&w.resid, C * m->d) || dalloc(&w.resid2, C * m->d) || dalloc(&w.bx, bx_elems) ||
       dalloc(&w.xs, xs_elems) ||
-      dalloc(&w.q, C * m->d) || dalloc(&w.attn, C * m->d) || dalloc(&w.gpart, gpart_floats) ||
-      dalloc(&w.h, C * m->ff) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
+      dalloc(&w.q, C * wide) || dalloc(&w.attn, C * wide) || dalloc(&w.gpart, gpart_floats) ||
+      dalloc(&w.h, C * std::max(m->ff, 1u)) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
       dalloc(&w.tokens, C + 64) || dalloc(&w.amax, C + 8) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
       dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
       dalloc(&w.cs2, sh_grp_cs(m->d)) || dalloc(&w.ssq2, sh_grp_cs(m->d)) || dalloc(&w.sb_cnt, SH_SB_CNT * SH_SB_CNT_STRIDE))
@@ -328,6 +358,18 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       hipMemset(w.sb_cnt, 0, SH_SB_CNT * SH_SB_CNT_STRIDE * 4) != hipSuccess ||
       hipMemset(w.amax, 0, (C + 8) * 8) != hipSuccess)
     FAIL(SH_ERR_HIP, "workspace clear failed");
+  if (m->n_expert) {
+    const size_t P = C * m->n_used, ng = (P + 7) / 8;
+    const size_t info = 1 + 3 * (size_t)sh_moe_max_chunks((uint32_t)P, m->n_expert);
+    if (dalloc(&w.moe_ids, P) || dalloc(&w.moe_wts, P) || dalloc(&w.moe_info, info) || dalloc(&w.moe_col, P) ||
+        dalloc(&w.moe_slot, P) || dalloc(&w.moe_hgu, P * 2 * m->eff) || dalloc(&w.moe_bx, ng * sh_grp_bx(m->eff)) ||
+        dalloc(&w.moe_xs, ng * sh_grp_xs(m->eff)) || dalloc(&w.moe_cs, ng * sh_grp_cs(m->eff)) ||
+        dalloc(&w.moe_y, P * m->d))
+      FAIL(SH_ERR_HIP, "moe workspace allocation: %s", sh_last_error());
+    if (hipMemset(w.moe_xs, 0, ng * sh_grp_xs(m->eff) * 2) != hipSuccess ||
+        hipMemset(w.moe_bx, 0, ng * sh_grp_bx(m->eff) * 2) != hipSuccess)
+      FAIL(SH_ERR_HIP, "moe workspace clear failed");
+  }
   if ((fail = ensure_rope(m, std::max<uint32_t>(m->n_ctx, 1024)))) FAIL(fail, "%s", sh_last_error());
   if (hipDeviceSynchronize() != hipSuccess) FAIL(SH_ERR_HIP, "model upload failed");
 #undef FAIL
@@ -710,7 +752,40 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
   return SH_OK;
 }
 
-// Forward of 8 < nc <= SH_MAX_COLS columns when every matrix is Q4_K: each
+// Routed-expert FFN of a qwen3moe layer over a chunk's nc columns
+// (models/qwen35moe.rs:3117-3182 without the shared expert): w.resid holds x
+// (attention added) and the staged operand x * ffn_norm with its RMS sums of
+// squares. Router + top-k per column, the routing plan (pairs grouped by
+// expert), gate/up of every routed expert over its columns (one pass over
+// each active expert's slab), SwiGLU + down operand over the pairs, down,
+// then the routing-weighted sum added to w.resid.
+static int moe_ffn(sh_model* m, const Layer& L, uint32_t nc) {
+  sh_engine* e = m->e;
+  Workspace& w = m->ws;
+  const uint32_t k = m->n_used, P = nc * k, E = m->n_expert, mc = sh_moe_max_chunks(P, E);
+  int rc;
+  if ((rc = sh_moe_route_launch(e, w.resid, L.ffn_norm, L.router, m->d, E, k, m->eps, nc, w.moe_ids, w.moe_wts)))
+    return rc;
+  if ((rc = sh_moe_plan_launch(e, w.moe_ids, P, E, k, w.moe_info, w.moe_col, w.moe_slot))) return rc;
+  EpiArgs gu;
+  gu.out = w.moe_hgu; gu.ldo = 2 * m->eff; gu.rows = 2 * m->eff;
+  gu.ssq = w.ssq; gu.ssq_n = (m->d + 255) / 256; gu.norm_K = m->d; gu.eps = m->eps;
+  if ((rc = sh_moe_gemm_launch(e, L.wgu_exps, E, w.bx, w.xs, w.cs, mc, w.moe_info, w.moe_col, gu, "moe_gate_up", 0.0)))
+    return rc;
+  PrepArgs pr;
+  pr.mode = PREP_SWIGLU; pr.part = w.moe_hgu; pr.nparts = 1; pr.part_ld = 2 * m->eff; pr.part_cols = P;
+  pr.K = m->eff; pr.N = P; pr.bx = w.moe_bx; pr.xs = w.moe_xs; pr.cs = w.moe_cs;
+  if ((rc = sh_prep_launch(e, pr))) return rc;
+  EpiArgs dn;
+  dn.out = w.moe_y; dn.ldo = m->d; dn.rows = m->d;
+  if ((rc = sh_moe_gemm_launch(e, L.wdown_exps, E, w.moe_bx, w.moe_xs, w.moe_cs, mc, w.moe_info, nullptr, dn,
+                               "moe_down", 0.0)))
+    return rc;
+  return sh_moe_combine_launch(e, w.moe_y, w.moe_slot, w.moe_wts, k, m->d, nc, w.resid);
+}
+
+// Forward of 8 < nc <= SH_MAX_COLS columns when every matrix is Q4_K (and of
+// any chunk of a qwen3 / qwen3moe model): each
 // weight matrix is read once per chunk by sh_gemm_launch over ceil(nc / 8)
 // operand groups. QKV, o, gate/up and down write split partials that the next
 // step finishes (qkv_finish: RoPE + KV writes; residual prep; SwiGLU prep);
@@ -733,7 +808,7 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     return pa;
   };
   EpiArgs qkv;
-  qkv.out = w.q; qkv.Dq = m->d; qkv.Dkv = m->hd * m->n_kv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.rope = m->rope;
+  qkv.out = w.q; qkv.Dq = m->q_dim; qkv.Dkv = m->hd * m->n_kv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.rope = m->rope;
   QkvCols qc;
   for (uint32_t j = 0; j < nc; ++j) {
     qc.pos[j] = cols[j].pos; qc.slot[j] = cols[j].slot; qc.mseq[j] = cols[j].kv->max_seq;
@@ -757,7 +832,10 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     uint32_t nq = 0;
     if ((rc = sh_gemm_launch(e, L.wqkv, w.bx, w.xs, w.cs, nc, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
     qkv.layer = l;
-    if ((rc = sh_qkv_finish_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc))) return rc;
+    rc = m->neox ? sh_qkv_finish_head_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc, L.q_norm, L.k_norm,
+                                             m->eps, true)
+                 : sh_qkv_finish_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc);
+    if (rc) return rc;
     for (const FaSeg& sg : segs) {
       FaArgs fa;
       fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
@@ -769,6 +847,10 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     if ((rc = sh_gemm_launch(e, L.wo, w.bx, w.xs, w.cs, nc, EPI_PART, po, "gemv_o", &pending))) return rc;
     pending_ld = po.ldo;
     if ((rc = resid_prep(L.ffn_norm))) return rc;
+    if (m->n_expert) {  // routed experts add into the residual themselves
+      if ((rc = moe_ffn(m, L, nc))) return rc;
+      continue;
+    }
     EpiArgs pg = part_args(L.wgu);
     set_norm(pg);
     uint32_t ngu = 0;
@@ -810,8 +892,8 @@ static uint32_t fa_seg_cols(const sh_model* m) {
 
 static int run_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
                      const std::vector<FaSeg>& segs, bool want_logits, bool want_resid) {
-  return nc > 8 ? forward_chunk_mg(m, dev_tokens, nc, cols, segs, want_logits, want_resid)
-                : forward_chunk(m, dev_tokens, nc, cols, segs, want_logits, want_resid);
+  return (nc > 8 || m->arch != ARCH_LLAMA) ? forward_chunk_mg(m, dev_tokens, nc, cols, segs, want_logits, want_resid)
+                                           : forward_chunk(m, dev_tokens, nc, cols, segs, want_logits, want_resid);
 }
 
 // Column geometry of a forward call: RoPE position, visibility mask and mask
@@ -874,7 +956,8 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
   const bool graph = kv->graph_base != nullptr;  // pos is an offset from *graph_base at replay
   SH_CHECK(graph || kv->pos == pos, SH_ERR_STATE,
            "cache.position %u doesn't match caller-supplied position_offset %u", kv->pos, pos);
-  SH_CHECK(!graph || (L <= 8 && !parents), SH_ERR_UNSUPPORTED, "graph capture: chains of at most 8 columns");
+  SH_CHECK(!graph || (L <= 8 && !parents && m->arch == ARCH_LLAMA), SH_ERR_UNSUPPORTED,
+           "graph capture: llama chains of at most 8 columns");
   SH_CHECK(kv->n_layer == m->n_layer && kv->n_kv == m->n_kv && kv->hd == m->hd, SH_ERR_ARG,
            "KV cache dims do not match the model");
   SH_CHECK((uint64_t)pos + L <= kv->max_seq, SH_ERR_CAPACITY, "positions [%u, %u) exceed KV capacity %u", pos,
@@ -1027,7 +1110,7 @@ extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint
                                 uint32_t pos, uint32_t* sampled_out) {
   SH_CHECK(e && m && kv && sampled_out, SH_ERR_ARG, "sh_verify_greedy: NULL argument");
   SH_CHECK(L >= 1 && L <= 64, SH_ERR_ARG, "verify length %u outside [1, 64]", L);
-  if (L <= 8 && graphs_enabled(e)) {
+  if (L <= 8 && graphs_enabled(e) && m->arch == ARCH_LLAMA) {
     SH_CHECK(tokens, SH_ERR_ARG, "tokens is NULL");
     for (uint32_t i = 0; i < L; ++i)
       SH_CHECK(tokens[i] < m->V, SH_ERR_ARG, "token id %u out of range (vocab %u)", tokens[i], m->V);
@@ -1374,7 +1457,8 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
   hp[np] = last_token;
   SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
-  const bool greedy_graph = mode == SH_SAMPLE_GREEDY && n + 1 <= 8 && graphs_enabled(e);
+  const bool greedy_graph = mode == SH_SAMPLE_GREEDY && n + 1 <= 8 && graphs_enabled(e) && tm->arch == ARCH_LLAMA &&
+                            dm->arch == ARCH_LLAMA;
   if (mode == SH_SAMPLE_GREEDY) {
     const uint32_t d0 = dkv->pos;
     if (greedy_graph) {

@@ -34,6 +34,7 @@ constexpr int SH_TILE_ROWS = 16;
 constexpr int SH_Q4K_TILE_BYTES = 2304;  // 16 rows x 144 B, repacked
 constexpr int SH_Q8_TILE_BYTES = 544;    // 16 rows x 34 B, repacked
 constexpr uint32_t SH_MAX_COLS = 64;     // columns per forward chunk (8 operand groups of 8)
+constexpr uint32_t SH_MAX_PREP_COLS = 512;  // operand columns one prep builds (the MoE down operand: pairs)
 constexpr int SH_FA_MIN_SPLIT_KEYS = 64;  // smallest key split of any attention launch (sizes fa_part)
 constexpr int SH_FA_MAX_ROWS = 256;       // padded query rows (gqa x columns) per kv head
 // Split partial row: O[hd], m, l, 2 pad (keeps rows 16-byte aligned).
@@ -103,10 +104,18 @@ struct sh_qtensor {
 struct Layer {
   float* attn_norm = nullptr;
   float* ffn_norm = nullptr;
+  float* q_norm = nullptr;  // qwen3 / qwen3moe: per-head RMSNorm weights [hd]
+  float* k_norm = nullptr;
   QMat wqkv;  // rows [q | k | v]
   QMat wo;
   QMat wgu;   // tiles interleaved: gate tile t at 2t, up tile t at 2t+1
   QMat wdown;
+  // qwen3moe routed experts: router f32 [E][d]; gate/up slabs of all experts
+  // stacked (expert e's tiles interleaved like wgu, contiguous per expert),
+  // down slabs stacked ([E][d] rows)
+  float* router = nullptr;
+  QMat wgu_exps;
+  QMat wdown_exps;
 };
 
 struct Workspace {
@@ -135,11 +144,28 @@ struct Workspace {
   float* cs2 = nullptr;
   float* ssq2 = nullptr;
   uint32_t* sb_cnt = nullptr;  // [SH_SB_CNT x SH_SB_CNT_STRIDE] arrival counters of the fused residual prep (zero between launches)
+  // routed-expert FFN (qwen3moe), P = columns x n_used pairs: router output,
+  // routing plan, gate/up rows per sorted pair, down operand over the pairs
+  // (P / 8 groups of K = expert_ff), down rows per sorted pair
+  uint32_t* moe_ids = nullptr;   // [cols][n_used]
+  float* moe_wts = nullptr;      // [cols][n_used]
+  uint32_t* moe_info = nullptr;  // chunk table (count, then (expert, first pair, n) per chunk)
+  uint32_t* moe_col = nullptr;   // [P] input column of sorted pair s
+  uint32_t* moe_slot = nullptr;  // [P] sorted position of pair (col, j)
+  float* moe_hgu = nullptr;      // [P][2 expert_ff]
+  uint16_t* moe_bx = nullptr;
+  uint16_t* moe_xs = nullptr;
+  float* moe_cs = nullptr;
+  float* moe_y = nullptr;        // [P][d]
 };
 
 struct sh_model {
   sh_engine* e = nullptr;
+  int arch = ARCH_LLAMA;
   uint32_t n_layer = 0, d = 0, n_head = 0, n_kv = 0, hd = 0, ff = 0, V = 0, n_ctx = 0;
+  uint32_t q_dim = 0;  // n_head * hd (= d for llama)
+  uint32_t n_expert = 0, n_used = 0, eff = 0;  // qwen3moe routed experts
+  bool neox = false;   // NEOX RoPE + per-head Q/K RMSNorm (qwen3 / qwen3moe)
   float eps = 1e-5f, theta = 10000.f;
   int embd_type = -1;
   uint8_t* embd_raw = nullptr;  // token_embd in GGUF row layout (gather)
@@ -287,6 +313,18 @@ struct QkvCols {  // per column: RoPE position, cache slot, capacity, K and V ca
 };
 int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
                          uint32_t N, const EpiArgs& ea, const QkvCols& qc);
+// The same from partials for qwen3-style attention: per-head RMSNorm of q and
+// k (weights q_norm / k_norm [hd], null: none) and NEOX or NORM RoPE.
+int sh_qkv_finish_head_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
+                              uint32_t N, const EpiArgs& ea, const QkvCols& qc, const float* q_norm,
+                              const float* k_norm, float eps, bool neox);
+// Expert-indirect y = W_e x for routed MoE FFNs: w stacks n_expert slabs
+// (rows M / n_expert each); chunk table info = (n_chunks, then (expert, p0, n)
+// per chunk), pair p's operand column gcol[p] (null: p), outputs
+// ea.out[p][row] for rows < ea.rows (EPI_STORE). One launch covers max_chunks.
+int sh_moe_gemm_launch(sh_engine* e, const QMat& w, uint32_t n_expert, const uint16_t* bx, const uint16_t* xs,
+                       const float* cs, uint32_t max_chunks, const uint32_t* info, const uint32_t* gcol,
+                       const EpiArgs& ea, const char* tag, double alg_bytes);
 
 // Activation prep: finishes the previous GEMV (residual add of its split
 // partials, or SwiGLU of gate/up partials) and builds the next activation
@@ -311,6 +349,7 @@ struct PrepArgs {
   uint16_t* xs = nullptr;
   float* cs = nullptr;
 };
+// N <= SH_MAX_PREP_COLS; the operand buffers hold ceil(N / 8) groups.
 int sh_prep_launch(sh_engine* e, const PrepArgs& a);
 // y[col][m] (+)= sum of nparts split partials, m < M.
 int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint32_t part_ld, uint32_t part_cols,
@@ -342,6 +381,15 @@ int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, 
 // 8192) row-statistics partials of scratch.
 int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
                           uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out);
+// Routed-expert FFN pieces (moe.hip): router + top-k per column (ids, wts
+// [N][k]), the routing plan over P = N k pairs, the weighted sum into resid.
+uint32_t sh_moe_max_chunks(uint32_t P, uint32_t E);
+int sh_moe_route_launch(sh_engine* e, const float* x, const float* norm_w, const float* router, uint32_t d, uint32_t E,
+                        uint32_t k, float eps, uint32_t N, uint32_t* ids, float* wts);
+int sh_moe_plan_launch(sh_engine* e, const uint32_t* ids, uint32_t P, uint32_t E, uint32_t k, uint32_t* info,
+                       uint32_t* pair_col, uint32_t* slot_of);
+int sh_moe_combine_launch(sh_engine* e, const float* y, const uint32_t* slot_of, const float* wts, uint32_t k,
+                          uint32_t d, uint32_t N, float* resid);
 // Acceptance of B sequences (COMPARE / REJECTION), see sh_accept_sample;
 // uniforms_dev (explicit) or Philox words from counter. scratch: device
 // memory of sh_accept_scratch_bytes(B, k, V, mode) bytes, or null to allocate
