@@ -160,6 +160,68 @@ def measure_tree(eng, tm, d, P=8192, reps=3):
             "frac": round((w + kv) / ms / 1e6 / HBM_PEAK_GBS, 4), "mean_path_nodes": round(float(np.mean(plens)), 3)}
 
 
+def measure_moe(eng, P=16384, B=8, L=7, reps=5):
+    """batched verify (sh_verify_unified) of B = 8 sequences x L = k+1 = 7
+    columns on the Qwen3-30B-A3B-shape Q4_K MoE target (48 layers, d 2048, 32 / 4
+    heads, head_dim 128, 128 experts top-8, expert FFN 768, vocab 151936) at
+    context 16384 (KV positions set without a prefill: the same bytes read and
+    work done). Algorithmic bytes: attention / router / lm_head matrices once,
+    the expected number of distinct routed experts per layer, 128 (1 -
+    (120/128)^56) = 124.6, times one expert's gate + up + down bytes, plus K/V
+    read for [0, P + L) of each sequence and the L new rows written."""
+    import numpy as np
+    from seeker_amd import synth as S
+    sh = S.Q30B_A3B_TARGET
+    t0 = time.time()
+    img = S.GgufImage(sh, seed=2)
+    log(f"moe target GGUF {img.size / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    m = eng.upload_weights(img)
+    img.close()
+    log(f"moe upload + repack {time.time() - t0:.1f}s")
+    d = m.dims
+    V = d.n_vocab
+    caches = [eng.allocate_kv_cache(m, P + 64) for _ in range(B)]
+    toks = np.concatenate([S.tokens(700 + b, L, V) for b in range(B)])
+    times = []
+    for i in range(reps + 2):
+        for c in caches:
+            c.set_position(P)
+        eng.sync()
+        t = time.perf_counter()
+        eng.verify_unified(m, caches, toks, [L] * B)
+        if i >= 2:
+            times.append((time.perf_counter() - t) * 1e3)
+    for c in caches:
+        c.set_position(P)
+    eng.set_profiling(True)
+    eng.profile(reset=True)
+    eng.verify_unified(m, caches, toks, [L] * B)
+    prof = eng.profile(reset=True)
+    eng.set_profiling(False)
+    q4 = 144 / 256
+    qd, kvd = d.n_head * d.head_dim, d.n_head_kv * d.head_dim
+    dense = d.n_layer * (d.n_embd * (qd + 2 * kvd) + qd * d.n_embd) * q4 + V * d.n_embd * q4
+    router = d.n_layer * sh.n_expert * d.n_embd * 4
+    N = B * L
+    distinct = sh.n_expert * (1 - (1 - sh.n_expert_used / sh.n_expert) ** N)
+    experts = d.n_layer * distinct * 3 * sh.expert_ff * d.n_embd * q4
+    kv = B * d.n_layer * 2 * ((P + L) * kvd * 2 + L * kvd * 2)
+    nbytes = dense + router + experts + kv
+    ms = statistics.median(times)
+    for c in caches:
+        c.close()
+    m.close()
+    kern = {n: round(v["ms"], 4) for n, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
+    log(f"moe verify B={B} L={L} ctx {P}: {ms:.2f} ms, {nbytes / 1e9:.2f} GB -> {nbytes / ms / 1e6:.0f} GB/s")
+    for n, v in list(kern.items())[:8]:
+        log(f"  {n:16s} {v:8.3f} ms")
+    return {"config": f"Qwen3-30B-A3B-shape Q4_K MoE target, B={B} x L={L} (k=6), ctx {P}, greedy ids",
+            "ms": round(ms, 3), "alg_bytes": int(nbytes), "expected_distinct_experts_per_layer": round(distinct, 2),
+            "GBps": round(nbytes / ms / 1e6, 1), "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "kernel_ms": kern}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,7 +231,8 @@ def main():
     ap.add_argument("--k", type=int, default=7)
     ap.add_argument("--verify-reps", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel and tree-verify lines")
+    ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel, tree and MoE lines")
+    ap.add_argument("--moe-only", action="store_true", help="only the configs[4] MoE verify measurement")
     ap.add_argument("--profile-only", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -181,6 +244,11 @@ def main():
 
     from seeker_amd import Engine
     from seeker_amd import synth as S
+
+    if args.moe_only:
+        with Engine(0) as eng:
+            print(json.dumps({"metric": "moe verify step", "moe_verify": measure_moe(eng)}), flush=True)
+        return
 
     t0 = time.time()
     timg = S.GgufImage(S.L8B_TARGET, seed=0)
@@ -302,7 +370,7 @@ def main():
     log(f"{args.steps} spec steps: {dt * 1e3 / args.steps:.3f} ms/step, {emitted} tokens, "
         f"acceptance {accepted / (args.steps * args.k):.3f}")
 
-    extra_acc = extra_tree = None
+    extra_acc = extra_tree = extra_moe = None
     if not args.no_extra:
         extra_acc = measure_acceptance(eng)
         extra_tree = measure_tree(eng, tm, d)
@@ -334,13 +402,16 @@ def main():
         "parity": parity,
         "acceptance_kernel": extra_acc,
         "tree_verify": extra_tree,
+        "moe_verify": None,
     }
-    print(json.dumps(out), flush=True)
     for x in (tkv, dkv, tm, dm):
         x.close()
-    eng.close()
     timg.close()
     dimg.close()
+    if not args.no_extra:  # the 8B models are freed first: the MoE target is 17 GB
+        out["moe_verify"] = measure_moe(eng)
+    print(json.dumps(out), flush=True)
+    eng.close()
 
 
 if __name__ == "__main__":
