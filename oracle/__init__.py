@@ -66,6 +66,8 @@ _SIGS = {
 }
 
 _lib = None
+_lib_fast = None
+LIB_FAST = os.path.join(_HERE, "_build", "liboracle_fast.so")
 
 
 def build():
@@ -84,6 +86,23 @@ def lib():
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def lib_fast():
+    """The timing build (f32 accumulation, -O3 AVX2/FMA) for the CPU baseline; it
+    shares the check build's object layouts, so models and caches opened by one
+    may be passed to the other."""
+    global _lib_fast
+    if _lib_fast is None:
+        if not os.path.exists(LIB_FAST):
+            build()
+        L = C.CDLL(LIB_FAST)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib_fast = L
+    return _lib_fast
 
 
 def _f32(a):
@@ -275,11 +294,13 @@ def tree_accept(p_logits, q_logits, tokens, parents, temperature, u):
     return path[: plen.value].tolist(), int(nt.value)
 
 
-def spec_step_greedy(tgt: Model, drf: Model, tkv: KvCache, dkv: KvCache, last_token: int, n_max: int):
+def spec_step_greedy(tgt: Model, drf: Model, tkv: KvCache, dkv: KvCache, last_token: int, n_max: int,
+                     fast: bool = False):
+    """or_spec_step_greedy; fast=True runs the timing build (f32 accumulation)."""
     em = (C.c_uint32 * 9)()
     dr = (C.c_uint32 * 8)()
     ne = C.c_uint32()
-    rc = lib().or_spec_step_greedy(tgt.h, drf.h, tkv.h, dkv.h, last_token, n_max, dkv.pending,
+    rc = (lib_fast() if fast else lib()).or_spec_step_greedy(tgt.h, drf.h, tkv.h, dkv.h, last_token, n_max, dkv.pending,
                                    C.byref(dkv.n_pending), em, C.byref(ne), dr)
     if rc:
         raise ValueError(f"oracle spec step failed ({rc})")

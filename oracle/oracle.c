@@ -15,6 +15,18 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* Accumulation type of the GEMV and attention dot products: f64 in the check
+ * build (the parity reference), f32 with vectorized reductions in the timing
+ * build (-DOR_FAST: the reference's own arithmetic, FLOAT_TYPE=float in
+ * shaders/compute/mul_mat_vec_q4_k.slang:4, used as the CPU baseline). */
+#ifdef OR_FAST
+typedef float or_acc;
+#define OR_SIMD_SUM _Pragma("omp simd reduction(+ : acc)")
+#else
+typedef double or_acc;
+#define OR_SIMD_SUM
+#endif
+
 /* ------------------------------------------------------------------ f16 */
 
 /* f16 -> f32 exactly as apps/seeker-cli/src/commands/run.rs:4115-4129
@@ -154,8 +166,9 @@ int or_gemv(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, 
       if (or_dequant_row(type, w, (uint64_t)m, K, row)) { err = 1; continue; }
       for (uint32_t j = 0; j < N; ++j) {
         const float* xj = x + (uint64_t)j * K;
-        double acc = 0.0;
-        for (uint64_t k = 0; k < K; ++k) acc += (double)row[k] * (double)xj[k];
+        or_acc acc = 0;
+        OR_SIMD_SUM
+        for (uint64_t k = 0; k < K; ++k) acc += (or_acc)row[k] * (or_acc)xj[k];
         y[(uint64_t)j * M + m] = (float)acc;
       }
     }
@@ -634,8 +647,9 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
           int vis = t < pos ? 1 : (parents ? is_ancestor(parents, t - pos, (uint32_t)j) : (t - pos <= (uint32_t)j));
           if (!vis) { s[t] = -INFINITY; continue; }
           const uint16_t* kr = Kc + (size_t)t * dkv + (size_t)kh * hd;
-          double acc = 0.0;
-          for (uint32_t e = 0; e < hd; ++e) acc += (double)qv[e] * (double)f16_lut[kr[e]];
+          or_acc acc = 0;
+          OR_SIMD_SUM
+          for (uint32_t e = 0; e < hd; ++e) acc += (or_acc)qv[e] * (or_acc)f16_lut[kr[e]];
           s[t] = acc * scale;
           if (s[t] > mx) mx = s[t];
         }
