@@ -132,6 +132,61 @@ int or_dequant_row(int type, const uint8_t* raw, uint64_t row, uint64_t k, float
     }
     return 0;
   }
+  if (type == OR_Q5_K) {
+    /* llama.cpp dequantize_row_q5_K (the reference's Q5_K shaders,
+     * shaders/compute/mul_mat_vec_q5_k.slang): the Q4_K scale / min unpack,
+     * low nibble from qs as in Q4_K, fifth bit (16) = bit s of qh[l] for
+     * sub-block s, l = element % 32. */
+    if (k % 256) return 1;
+    uint64_t nb = k / 256;
+    for (uint64_t b = 0; b < nb; ++b) {
+      const uint8_t* blk = raw + (row * nb + b) * 176;
+      float d = or_f16_to_f32((uint16_t)(blk[0] | blk[1] << 8));
+      float dmin = or_f16_to_f32((uint16_t)(blk[2] | blk[3] << 8));
+      const uint8_t* sc = blk + 4;
+      const uint8_t* qh = blk + 16;
+      const uint8_t* qs = blk + 48;
+      float* y = out + b * 256;
+      for (int s = 0; s < 8; ++s) {
+        int scv, mv;
+        q4k_scale_min(sc, s, &scv, &mv);
+        float d1 = d * (float)scv, m1 = dmin * (float)mv;
+        for (int l = 0; l < 32; ++l) {
+          int q = (qs[32 * (s / 2) + l] >> (4 * (s % 2))) & 0xF;
+          if (qh[l] & (1u << s)) q += 16;
+          y[32 * s + l] = d1 * (float)q - m1;
+        }
+      }
+    }
+    return 0;
+  }
+  if (type == OR_Q6_K) {
+    /* run.rs:4257-4291: q = low nibble | top two bits << 4, value
+     * d * scales[e / 16] * (q - 32). */
+    if (k % 256) return 1;
+    uint64_t nb = k / 256;
+    for (uint64_t b = 0; b < nb; ++b) {
+      const uint8_t* blk = raw + (row * nb + b) * 210;
+      const uint8_t* ql = blk;
+      const uint8_t* qh = blk + 128;
+      const int8_t* sc = (const int8_t*)(blk + 192);
+      float d = or_f16_to_f32((uint16_t)(blk[208] | blk[209] << 8));
+      float* y = out + b * 256;
+      for (int n = 0; n < 2; ++n)
+        for (int l = 0; l < 32; ++l) {
+          const int is = l / 16;
+          const int q1 = ((ql[64 * n + l] & 0xF) | ((qh[32 * n + l] & 3) << 4)) - 32;
+          const int q2 = ((ql[64 * n + l + 32] & 0xF) | (((qh[32 * n + l] >> 2) & 3) << 4)) - 32;
+          const int q3 = ((ql[64 * n + l] >> 4) | (((qh[32 * n + l] >> 4) & 3) << 4)) - 32;
+          const int q4 = ((ql[64 * n + l + 32] >> 4) | (((qh[32 * n + l] >> 6) & 3) << 4)) - 32;
+          y[128 * n + l] = d * (float)sc[8 * n + is] * (float)q1;
+          y[128 * n + l + 32] = d * (float)sc[8 * n + is + 2] * (float)q2;
+          y[128 * n + l + 64] = d * (float)sc[8 * n + is + 4] * (float)q3;
+          y[128 * n + l + 96] = d * (float)sc[8 * n + is + 6] * (float)q4;
+        }
+    }
+    return 0;
+  }
   if (type == OR_Q8_0) {
     if (k % 32) return 1;
     uint64_t nb = k / 32;
@@ -468,6 +523,8 @@ static void rope_neox(float* x, uint32_t n_head, uint32_t hd, uint32_t pos, floa
 static uint64_t row_bytes(int type, uint64_t cols) {
   switch (type) {
     case OR_Q4_K: return cols / 256 * 144;
+    case OR_Q5_K: return cols / 256 * 176;
+    case OR_Q6_K: return cols / 256 * 210;
     case OR_Q8_0: return cols / 32 * 34;
     case OR_F16: return cols * 2;
     default: return cols * 4;

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-enum { OR_F32 = 0, OR_F16 = 1, OR_Q8_0 = 8, OR_Q4_K = 12 };
+enum { OR_F32 = 0, OR_F16 = 1, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14 };
 
 float or_f16_to_f32(uint16_t h);
 uint16_t or_f32_to_f16(float f);

@@ -17,7 +17,7 @@ SYNTH_PATH = os.path.join(_HERE, "libseeker_synth.so")
 SH_OK, SH_ERR_ARG, SH_ERR_HIP, SH_ERR_FORMAT, SH_ERR_UNSUPPORTED, SH_ERR_CAPACITY, SH_ERR_STATE = range(7)
 # enum sh_sample_mode
 SH_SAMPLE_GREEDY, SH_SAMPLE_COMPARE, SH_SAMPLE_REJECTION = 0, 1, 2
-GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K = 0, 1, 8, 12
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 1, 8, 12, 13, 14
 
 
 class SeekerError(RuntimeError):
@@ -66,7 +66,7 @@ class sh_synth_cfg(C.Structure):
         ("rms_eps", C.c_float), ("rope_base", C.c_float), ("weight_std", C.c_float),
         ("norm_jitter", C.c_float), ("router_std", C.c_float),
         ("wtype", C.c_uint32), ("etype", C.c_uint32), ("tied", C.c_uint32),
-        ("seed", C.c_uint64),
+        ("seed", C.c_uint64), ("out_type", C.c_uint32), ("mix", C.c_uint32),
     ]
 
 

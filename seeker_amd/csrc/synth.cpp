@@ -13,6 +13,7 @@
 // Q4_K = 256 elem / 144 B). Metadata keys and tensor names follow
 // crates/seeker-vulkan/src/models/llama.rs:1038-1048 and :1074-1090,
 // models/qwen3.rs:591-698 and models/qwen35moe.rs:126-130, 4118-4131.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <functional>
@@ -26,7 +27,7 @@
 
 namespace {
 
-enum : uint32_t { GT_F32 = 0, GT_F16 = 1, GT_Q8_0 = 8, GT_Q4_K = 12 };
+enum : uint32_t { GT_F32 = 0, GT_F16 = 1, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q5_K = 13, GT_Q6_K = 14 };
 enum : uint32_t { MV_U32 = 4, MV_F32 = 6, MV_STRING = 8 };
 
 struct Buf {
@@ -122,6 +123,90 @@ void quant_q4_k_block(const float* x, uint8_t* out) {
     for (int l = 0; l < 32; ++l) qs[32 * g + l] = (uint8_t)(q[64 * g + l] | (q[64 * g + 32 + l] << 4));
 }
 
+// Q5_K (176 B / 256): d, dmin, the Q4_K 6-bit scale / min packing, qh[32],
+// qs[128]; element e of sub-block s (l = e % 32) keeps its low nibble in
+// qs[32 (s / 2) + l] (bits 4 (s % 2)) and its fifth bit as bit s of qh[l]
+// (the dequant order of llama.cpp's dequantize_row_q5_K). A min/max quantizer
+// per 32-element sub-block with 31 steps.
+void quant_q5_k_block(const float* x, uint8_t* out) {
+  float scr[8], mr[8];
+  for (int s = 0; s < 8; ++s) {
+    float mn = x[32 * s], mx = x[32 * s];
+    for (int i = 1; i < 32; ++i) {
+      mn = std::fmin(mn, x[32 * s + i]);
+      mx = std::fmax(mx, x[32 * s + i]);
+    }
+    if (mn > 0.f) mn = 0.f;
+    mr[s] = -mn;
+    scr[s] = (mx - mn) / 31.f;
+  }
+  float dmax = 0.f, mmax = 0.f;
+  for (int s = 0; s < 8; ++s) { dmax = std::fmax(dmax, scr[s]); mmax = std::fmax(mmax, mr[s]); }
+  uint16_t dh = sh_f32_to_f16(dmax / 63.f), mh = sh_f32_to_f16(mmax / 63.f);
+  float d = sh_f16_to_f32(dh), dmin = sh_f16_to_f32(mh);
+  int sc[8], m[8];
+  for (int s = 0; s < 8; ++s) {
+    int a = d > 0.f ? round_half_up(scr[s] / d) : 0;
+    int b = dmin > 0.f ? round_half_up(mr[s] / dmin) : 0;
+    sc[s] = a < 0 ? 0 : (a > 63 ? 63 : a);
+    m[s] = b < 0 ? 0 : (b > 63 ? 63 : b);
+  }
+  std::memset(out, 0, 176);
+  std::memcpy(out, &dh, 2);
+  std::memcpy(out + 2, &mh, 2);
+  uint8_t* scales = out + 4;
+  for (int j = 0; j < 4; ++j) {
+    scales[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+    scales[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+    scales[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+  }
+  uint8_t* qh = out + 16;
+  uint8_t* qs = out + 48;
+  for (int s = 0; s < 8; ++s) {
+    float step = d * (float)sc[s], off = dmin * (float)m[s];
+    for (int l = 0; l < 32; ++l) {
+      int v = step > 0.f ? round_half_up((x[32 * s + l] + off) / step) : 0;
+      v = v < 0 ? 0 : (v > 31 ? 31 : v);
+      qs[32 * (s / 2) + l] |= (uint8_t)((v & 0xF) << (4 * (s % 2)));
+      if (v & 16) qh[l] |= (uint8_t)(1u << s);
+    }
+  }
+}
+
+// Q6_K (210 B / 256): ql[128], qh[64], int8 scales[16], d; element e (n =
+// e / 128, g = e % 128 / 32, l = e % 32) keeps its low nibble in ql[64 n + l +
+// 32 (g % 2)] (bits 4 (g / 2)) and its top two bits in qh[32 n + l] (bits 2 g),
+// value d * scales[e / 16] * (q - 32) (run.rs:4257-4291). Symmetric per
+// 16-element sub-block, 31 steps each way.
+void quant_q6_k_block(const float* x, uint8_t* out) {
+  float ss[16], smax = 0.f;
+  for (int s = 0; s < 16; ++s) {
+    float a = 0.f;
+    for (int i = 0; i < 16; ++i) a = std::fmax(a, std::fabs(x[16 * s + i]));
+    ss[s] = a / 31.f;
+    smax = std::fmax(smax, ss[s]);
+  }
+  const uint16_t dh = sh_f32_to_f16(smax / 127.f);
+  const float d = sh_f16_to_f32(dh);
+  std::memset(out, 0, 210);
+  uint8_t* ql = out;
+  uint8_t* qh = out + 128;
+  int8_t* sc = (int8_t*)(out + 192);
+  for (int s = 0; s < 16; ++s) {
+    int v = d > 0.f ? round_half_up(ss[s] / d) : 0;
+    sc[s] = (int8_t)(v < 0 ? 0 : (v > 127 ? 127 : v));
+  }
+  for (int e = 0; e < 256; ++e) {
+    const float step = d * (float)sc[e / 16];
+    int q = step > 0.f ? round_half_up(x[e] / step) + 32 : 32;
+    q = q < 0 ? 0 : (q > 63 ? 63 : q);
+    const int n = e / 128, g = e % 128 / 32, l = e % 32;
+    ql[64 * n + l + 32 * (g % 2)] |= (uint8_t)((q & 0xF) << (4 * (g / 2)));
+    qh[32 * n + l] |= (uint8_t)((q >> 4) << (2 * g));
+  }
+  std::memcpy(out + 208, &dh, 2);
+}
+
 struct TensorSpec {
   std::string name;
   uint64_t ne0, ne1, ne2;  // ne0 = contracting / innermost dim, ne1 = rows, ne2 = expert slabs
@@ -137,6 +222,8 @@ uint64_t tensor_bytes(uint32_t type, uint64_t n) {
     case GT_F16: return n * 2;
     case GT_Q8_0: return n / 32 * 34;
     case GT_Q4_K: return n / 256 * 144;
+    case GT_Q5_K: return n / 256 * 176;
+    case GT_Q6_K: return n / 256 * 210;
   }
   return 0;
 }
@@ -159,8 +246,9 @@ void fill_tensor(const TensorSpec& t, uint64_t seed, uint64_t stream, float stdv
     }
     return;
   }
-  const uint64_t blk = t.type == GT_Q4_K ? 256 : 32;
-  const uint64_t bbytes = t.type == GT_Q4_K ? 144 : 34;
+  const bool kq = t.type == GT_Q4_K || t.type == GT_Q5_K || t.type == GT_Q6_K;
+  const uint64_t blk = kq ? 256 : 32;
+  const uint64_t bbytes = tensor_bytes(t.type, blk);
   const int64_t nblk = (int64_t)(n / blk);
 #pragma omp parallel for schedule(static, 256)
   for (int64_t b = 0; b < nblk; ++b) {
@@ -170,8 +258,11 @@ void fill_tensor(const TensorSpec& t, uint64_t seed, uint64_t stream, float stdv
       normals4(seed, stream, ((uint64_t)b * blk + e) / 4, z);
       for (int i = 0; i < 4; ++i) x[e + i] = (float)(z[i] * (double)stdv);
     }
-    if (t.type == GT_Q4_K) quant_q4_k_block(x, dst + (uint64_t)b * bbytes);
-    else quant_q8_0_block(x, dst + (uint64_t)b * bbytes);
+    uint8_t* o = dst + (uint64_t)b * bbytes;
+    if (t.type == GT_Q4_K) quant_q4_k_block(x, o);
+    else if (t.type == GT_Q5_K) quant_q5_k_block(x, o);
+    else if (t.type == GT_Q6_K) quant_q6_k_block(x, o);
+    else quant_q8_0_block(x, o);
   }
 }
 
@@ -193,6 +284,8 @@ typedef struct sh_synth_cfg {
   uint32_t wtype, etype;
   uint32_t tied;  // 1: no output.weight (lm_head = token_embd)
   uint64_t seed;
+  uint32_t out_type;  // output.weight type (0: wtype)
+  uint32_t mix;       // 1: attn_v and ffn_down of even layers in Q6_K (the Q4_K_M-style mix)
 } sh_synth_cfg;
 
 // Build a GGUF v3 image in host memory. *out is malloc'd; free with
@@ -203,7 +296,9 @@ int sh_synth_gguf(const sh_synth_cfg* c, uint8_t** out, uint64_t* size) {
   if (c->head_dim == 0 && c->n_embd % c->n_head) return 2;
   const bool qwen = c->arch != 0, moe = c->arch == 2;
   const uint32_t wt = c->wtype, et = c->etype;
-  const uint64_t qk_w = wt == GT_Q4_K ? 256 : 32, qk_e = et == GT_Q4_K ? 256 : 32;
+  auto blk = [](uint32_t t) -> uint64_t { return (t == GT_Q4_K || t == GT_Q5_K || t == GT_Q6_K) ? 256 : 32; };
+  const uint64_t qk_w = std::max(blk(wt), c->mix ? (uint64_t)256 : (uint64_t)1), qk_e = blk(et);
+  const uint32_t ot = c->out_type ? c->out_type : wt;
   const uint64_t d = c->n_embd, ff = c->n_ff, hd = c->head_dim ? c->head_dim : d / c->n_head;
   const uint64_t qd = hd * c->n_head, dkv = hd * c->n_head_kv, E = c->n_expert, ef = c->expert_ff;
   if (d % qk_w || qd % qk_w || d % qk_e || (!moe && ff % qk_w) || (moe && (ef % qk_w || !E || !c->n_expert_used)))
@@ -216,7 +311,8 @@ int sh_synth_gguf(const sh_synth_cfg* c, uint8_t** out, uint64_t* size) {
     ts.push_back({p + "attn_norm.weight", d, 1, 1, GT_F32, 1, 0, 0});
     ts.push_back({p + "attn_q.weight", d, qd, 1, wt, 0, 0, 0});
     ts.push_back({p + "attn_k.weight", d, dkv, 1, wt, 0, 0, 0});
-    ts.push_back({p + "attn_v.weight", d, dkv, 1, wt, 0, 0, 0});
+    const uint32_t mt = (c->mix == 1 && i % 2 == 0) ? (uint32_t)GT_Q6_K : wt;  // attn_v / ffn_down
+    ts.push_back({p + "attn_v.weight", d, dkv, 1, mt, 0, 0, 0});
     if (qwen) {
       ts.push_back({p + "attn_q_norm.weight", hd, 1, 1, GT_F32, 1, 0, 0});
       ts.push_back({p + "attn_k_norm.weight", hd, 1, 1, GT_F32, 1, 0, 0});
@@ -231,11 +327,11 @@ int sh_synth_gguf(const sh_synth_cfg* c, uint8_t** out, uint64_t* size) {
     } else {
       ts.push_back({p + "ffn_gate.weight", d, ff, 1, wt, 0, 0, 0});
       ts.push_back({p + "ffn_up.weight", d, ff, 1, wt, 0, 0, 0});
-      ts.push_back({p + "ffn_down.weight", ff, d, 1, wt, 0, 0, 0});
+      ts.push_back({p + "ffn_down.weight", ff, d, 1, mt, 0, 0, 0});
     }
   }
   ts.push_back({"output_norm.weight", d, 1, 1, GT_F32, 1, 0, 0});
-  if (!c->tied) ts.push_back({"output.weight", d, c->n_vocab, 1, wt, 0, 0, 0});
+  if (!c->tied) ts.push_back({"output.weight", d, c->n_vocab, 1, ot, 0, 0, 0});
 
   const std::string A = c->arch == 0 ? "llama" : (c->arch == 1 ? "qwen3" : "qwen3moe");
   Buf h;
@@ -347,6 +443,16 @@ void sh_synth_normal_f32(uint64_t seed, uint64_t stream, float mean, float stdv,
 
 // Quantize rows of f32 values (n multiple of the block size) to Q8_0 / Q4_K.
 int sh_synth_quantize(uint32_t type, const float* x, uint64_t n, uint8_t* out) {
+  if (type == GT_Q5_K || type == GT_Q6_K) {
+    if (n % 256) return 1;
+    const uint64_t bb = tensor_bytes(type, 256);
+#pragma omp parallel for schedule(static, 256)
+    for (int64_t b = 0; b < (int64_t)(n / 256); ++b) {
+      if (type == GT_Q5_K) quant_q5_k_block(x + 256 * b, out + bb * b);
+      else quant_q6_k_block(x + 256 * b, out + bb * b);
+    }
+    return 0;
+  }
   if (type == GT_Q8_0) {
     if (n % 32) return 1;
 #pragma omp parallel for schedule(static, 1024)

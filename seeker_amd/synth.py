@@ -38,6 +38,8 @@ class LlamaShape:
     expert_ff: int = 0
     norm_jitter: float = 0.0  # norm weights 1 + jitter * N(0, 1) (0: all ones)
     router_std: float = 0.0   # f32 router weights N(0, router_std)
+    out_type: int = 0         # output.weight type (0: wtype)
+    mix: int = 0              # 1: attn_v / ffn_down of even layers in Q6_K (Q4_K_M-style)
 
 
 # tiny Llama target / 1-layer draft, Q8_0.
@@ -64,7 +66,7 @@ class GgufImage:
             shape.arch, shape.n_layer, shape.n_embd, shape.n_head, shape.n_head_kv, shape.head_dim, shape.n_ff,
             shape.n_vocab, shape.n_ctx, shape.n_expert, shape.n_expert_used, shape.expert_ff, shape.rms_eps,
             shape.rope_base, shape.weight_std, shape.norm_jitter, shape.router_std, shape.wtype, shape.etype,
-            int(shape.tied), seed)
+            int(shape.tied), seed, shape.out_type, shape.mix)
         ptr = C.POINTER(C.c_uint8)()
         size = C.c_uint64()
         rc = N.synth().sh_synth_gguf(C.byref(cfg), C.byref(ptr), C.byref(size))
@@ -114,9 +116,9 @@ def normal_f32(seed: int, stream: int, n: int, mean: float = 0.0, std: float = 1
 
 
 def quantize(qtype: int, x: np.ndarray) -> np.ndarray:
-    """Quantize a flat f32 array (rows contiguous) to GGUF Q8_0 / Q4_K blocks."""
+    """Quantize a flat f32 array (rows contiguous) to GGUF Q8_0 / Q4_K / Q5_K / Q6_K blocks."""
     x = np.ascontiguousarray(x, dtype=np.float32).ravel()
-    blk, bb = (256, 144) if qtype == N.GGML_Q4_K else (32, 34)
+    blk, bb = {N.GGML_Q4_K: (256, 144), N.GGML_Q5_K: (256, 176), N.GGML_Q6_K: (256, 210)}.get(qtype, (32, 34))
     out = np.zeros(x.size // blk * bb, dtype=np.uint8)
     rc = N.synth().sh_synth_quantize(qtype, x.ctypes.data_as(N.F32P), x.size,
                                      out.ctypes.data_as(C.POINTER(C.c_uint8)))

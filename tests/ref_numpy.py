@@ -49,11 +49,49 @@ def dequant_q4_k(raw: np.ndarray, rows: int, k: int) -> np.ndarray:
     return y.reshape(rows, k)
 
 
+def dequant_q5_k(raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """GGUF Q5_K: [d f16, dmin f16, scales 12, qh 32, qs 128]; the value of element
+    32 s + l is d sc_s (nibble + 16 * (bit s of qh[l])) - dmin m_s."""
+    blk = np.asarray(raw, dtype=np.uint8).reshape(rows, k // 256, 176)
+    hdr = blk[:, :, 0:4].copy().view(np.uint16)
+    d, dmin = f16_to_f64(hdr[..., 0]), f16_to_f64(hdr[..., 1])
+    sc, m = q4k_scales(blk[:, :, 4:16])
+    qh = blk[:, :, 16:48].astype(np.int64)                         # [.., l]
+    qs = blk[:, :, 48:].reshape(rows, k // 256, 4, 32)
+    nib = np.stack([qs & 0xF, qs >> 4], axis=3).reshape(rows, k // 256, 8, 32).astype(np.int64)
+    hi = (qh[:, :, None, :] >> np.arange(8)[None, None, :, None]) & 1  # [.., s, l]
+    q = (nib + 16 * hi).astype(np.float64)
+    y = d[..., None, None] * sc[..., None] * q - dmin[..., None, None] * m[..., None]
+    return y.reshape(rows, k)
+
+
+def dequant_q6_k(raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """GGUF Q6_K: [ql 128, qh 64, scales int8 16, d f16]; element 128 n + 32 g + l
+    has the nibble (g // 2) of ql[64 n + 32 (g % 2) + l] and bits 2g..2g+1 of
+    qh[32 n + l] on top, value d * scales[e // 16] * (q - 32)."""
+    blk = np.asarray(raw, dtype=np.uint8).reshape(rows, k // 256, 210)
+    ql = blk[:, :, :128].reshape(rows, k // 256, 2, 2, 32).astype(np.int64)   # [n, g%2, l]
+    qh = blk[:, :, 128:192].reshape(rows, k // 256, 2, 32).astype(np.int64)   # [n, l]
+    sc = blk[:, :, 192:208].view(np.int8).astype(np.float64)                 # [16]
+    d = f16_to_f64(blk[:, :, 208:210].copy().view(np.uint16)[..., 0])
+    q = np.empty((rows, k // 256, 2, 4, 32), dtype=np.int64)
+    for g in range(4):
+        nib = (ql[:, :, :, g % 2, :] >> (4 * (g // 2))) & 0xF
+        q[:, :, :, g, :] = nib | (((qh >> (2 * g)) & 3) << 4)
+    q = (q - 32).reshape(rows, k // 256, 256).astype(np.float64)
+    s = np.repeat(sc, 16, axis=-1)
+    return (d[..., None] * s * q).reshape(rows, k)
+
+
 def dequant(qtype: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
     if qtype == Q8_0:
         return dequant_q8_0(raw, rows, k)
     if qtype == Q4_K:
         return dequant_q4_k(raw, rows, k)
+    if qtype == 13:
+        return dequant_q5_k(raw, rows, k)
+    if qtype == 14:
+        return dequant_q6_k(raw, rows, k)
     if qtype == F32:
         return np.asarray(raw, dtype=np.uint8).view(np.float32).astype(np.float64).reshape(rows, k)
     raise ValueError(qtype)
@@ -106,7 +144,7 @@ def read_gguf(buf: bytes):
         infos.append((name, dims, typ, off))
     align = meta.get("general.alignment", 32)
     start = (pos + align - 1) // align * align
-    layout = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144)}
+    layout = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
     tensors = {}
     for name, dims, typ, off in infos:
         n = int(np.prod(dims))

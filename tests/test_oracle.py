@@ -671,3 +671,81 @@ def test_moe_route_closed_forms():
     # ties go to the lower expert index
     ids, w = O.moe_route(np.array([0.5, 2.0, 2.0, 1.0, 2.0], np.float32), 3)
     assert list(ids) == [1, 2, 4] and np.allclose(w, 1 / 3)
+
+
+# ------------------------------------------------------------------ Q5_K / Q6_K
+
+GGML_Q5_K, GGML_Q6_K = 13, 14
+
+
+@pytest.mark.parametrize("qtype,bb", [(GGML_Q5_K, 176), (GGML_Q6_K, 210)], ids=["q5k", "q6k"])
+def test_kquant_dequant_random_bytes_match_numpy(qtype, bb):
+    """Arbitrary block bytes (every bit pattern of qs / qh / scales) with finite f16
+    d / dmin, against the independent numpy dequant."""
+    rng = np.random.default_rng(9)
+    rows, k = 5, 768
+    raw = rng.integers(0, 256, rows * k // 256 * bb, dtype=np.uint8).reshape(rows, k // 256, bb)
+    half = np.float16(rng.standard_normal((rows, k // 256, 2)) * 0.01).view(np.uint8).reshape(rows, k // 256, 4)
+    if qtype == GGML_Q5_K:
+        raw[:, :, 0:4] = half
+    else:
+        raw[:, :, 208:210] = half[:, :, :2]
+    raw = raw.ravel()
+    ref = R.dequant(qtype, raw, rows, k)
+    for r in range(rows):
+        np.testing.assert_allclose(O.dequant_row(qtype, raw, r, k), ref[r], rtol=1e-6, atol=1e-12)
+
+
+@pytest.mark.parametrize("qtype", [GGML_Q5_K, GGML_Q6_K], ids=["q5k", "q6k"])
+def test_kquant_quantizer_roundtrip(qtype):
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal(4 * 512).astype(np.float32) * 0.02
+    y = np.concatenate([O.dequant_row(qtype, S.quantize(qtype, x), r, 512) for r in range(4)])
+    step = np.abs(x).max() / (31 if qtype == GGML_Q6_K else 15)  # 5 / 6 bits
+    assert np.abs(y - x).max() <= step
+
+
+def test_q6k_special_block():
+    blk = np.zeros(210, dtype=np.uint8)
+    blk[208:210] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[192:208] = np.arange(16, dtype=np.int8).view(np.uint8) - 8  # scales -8 .. 7
+    blk[0:128] = 0x00
+    blk[128:192] = 0xAA            # top bits 2 for every element: q = 32 -> value 0
+    assert np.all(O.dequant_row(GGML_Q6_K, blk, 0, 256) == 0.0)
+    blk[128:192] = 0xFF            # q = 48 + nibble 0: (48 - 32) = 16
+    y = O.dequant_row(GGML_Q6_K, blk, 0, 256)
+    np.testing.assert_array_equal(y, 0.5 * 16 * np.repeat(np.arange(16) - 8, 16))
+
+
+def test_q5k_special_block():
+    blk = np.zeros(176, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[4] = 1                     # sub-block 0: sc 1, m 0
+    blk[16:48] = 0x01              # fifth bit of every element of sub-block 0
+    blk[48:80] = 0x0F              # nibble 15 in sub-block 0 (low), 0 in sub-block 1 (high)
+    y = O.dequant_row(GGML_Q5_K, blk, 0, 256)
+    assert np.all(y[:32] == 31.0) and np.all(y[32:] == 0.0)
+
+
+MIXED_Q4KM = S.LlamaShape(2, 256, 4, 2, 512, 700, 256, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K, out_type=GGML_Q6_K,
+                          mix=1)
+MIXED_Q5K = S.LlamaShape(2, 256, 4, 2, 512, 700, 256, 1e-5, 5e5, 0.02, GGML_Q5_K, GGML_Q4_K, out_type=GGML_Q6_K)
+
+
+@pytest.mark.parametrize("shape", [MIXED_Q4KM, MIXED_Q5K], ids=["q4km_mix", "q5k_base"])
+def test_mixed_type_forward_matches_numpy(shape):
+    """Q4_K_M-style mixes (attn_v / ffn_down of even layers and output in Q6_K)
+    and a Q5_K base with a Q6_K lm_head, against the numpy f64 forward."""
+    with S.GgufImage(shape, seed=13) as img:
+        meta, T, _ = R.read_gguf(bytes(img.bytes()))
+        assert T["output.weight"][1] == GGML_Q6_K
+        ref = R.RefLlama(bytes(img.bytes()))
+        m = O.Model(img)
+        kv = O.KvCache(m, 32)
+        toks = S.tokens(5, 8, m.V)
+        lg, res = O.forward(m, kv, toks, 0)
+        rl, rr = ref.forward(toks)
+        np.testing.assert_allclose(res[0], rr[0], rtol=1e-5, atol=1e-5 * np.abs(rr[0]).max())
+        np.testing.assert_allclose(lg, rl, rtol=1e-3, atol=1e-3 * np.abs(rl).max())
+        kv.close()
+        m.close()
