@@ -92,7 +92,11 @@ int sh_memcpy_d2h(sh_engine* e, void* dst, const void* src_dev, uint64_t bytes);
 
 /* -------------------------------------------------------------- model */
 /* models::open + Engine::upload_weights (models/mod.rs:537, inference/mod.rs:304)
- * for architecture "llama" (models/llama.rs:1038-1090). */
+ * for architectures "llama" (models/llama.rs:1038-1090), "qwen3" and
+ * "qwen3moe" (models/qwen3.rs). Weight types: every matrix a K-quant (Q4_K,
+ * Q5_K, Q6_K in any mix, e.g. Q4_K_M / Q5_K_M files; routed experts Q4_K), or
+ * llama layers uniformly Q4_K or Q8_0; token_embd any of these, F16 or F32.
+ * SH_ERR_UNSUPPORTED otherwise. */
 int sh_model_load_gguf(sh_engine* e, const char* path, sh_model** out);
 int sh_model_load_gguf_memory(sh_engine* e, const void* data, uint64_t size, sh_model** out);
 void sh_model_destroy(sh_model* m);
@@ -182,7 +186,8 @@ int sh_spec_step(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh
 int sh_spec_step_logits(sh_engine* e, float* p_out, float* q_out, uint32_t* n_out, uint32_t* V_out);
 
 /* ------------------------------------------------------ kernel level */
-/* Upload a GGUF-layout quantized matrix [M rows][K] (Q8_0 or Q4_K) and repack it
+/* Upload a GGUF-layout quantized matrix [M rows][K] (Q8_0, Q4_K, Q5_K or Q6_K;
+ * the reference's mul_mat_vec_q4_k / q5_k / q6_k / q8_0 shaders) and repack it
  * for the MFMA GEMV. */
 int sh_qtensor_upload(sh_engine* e, int ggml_type, const void* host_blocks, uint32_t M, uint32_t K,
                       sh_qtensor** out);

@@ -114,6 +114,117 @@ __global__ void k_repack_q4k(const uint8_t* __restrict__ src, uint8_t* __restric
   for (int m = 0; m < 4; ++m) o[m] = words[4 + m];
 }
 
+// Nibble word m of lane (row, group g) in the Q4_K tile layout from a row's
+// 128 packed nibble bytes: element 32 m + 8 g + t is (qs[32 (m / 2) + 8 g + t]
+// >> 4 (m % 2)) & 15 (the Q4_K / Q5_K low nibbles; Q6_K maps its quarters onto
+// this with its own byte offsets).
+__device__ __forceinline__ uint32_t nibble_word(const uint8_t* qs, uint32_t byte0, uint32_t shift) {
+  uint32_t w = 0;
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t q = (qs[byte0 + t] >> shift) & 0xF;
+    w |= q << ((t & 1) ? 16 + 4 * (t >> 1) : 4 * (t >> 1));
+  }
+  return w;
+}
+
+// Position, relative to its sub-block's base bit, of the high bits of element
+// t of a lane's 8 in the repacked high-bit words: t0 0, t1 16, t2 4, t3 20,
+// t4 X, t5 16 + X, t6 4 + X, t7 20 + X, with X = 1 for Q5_K (one bit per
+// element) and X = 2 for Q6_K (two bits, at the position and the one above).
+// Shifting the word so the base lands on bit 4 puts t0 / t1 on bits 4 / 20 and
+// t2 / t3 on 8 / 24, right above the nibbles of the f16 pairs (t0, t1) (nibbles
+// at bits 0 / 16) and (t2, t3) (nibbles at 4 / 20); shifting by X less does the
+// same for t4..t7.
+__device__ __forceinline__ uint32_t hbit_pos(int t, int X) {
+  return 16 * (t & 1) + 4 * ((t >> 1) & 1) + X * ((t >> 2) & 1);
+}
+
+// Q5_K tile-superblock (2816 B): [0,2048) the low-nibble words as in Q4_K;
+// [2048,2560) two high-bit words per lane at 2048 + 8 l, word h holding
+// sub-blocks 4h..4h+3 at bases 0, 2, 8, 10 (element t of sub-block m: bit
+// base(m) + hbit_pos(t, 1)); [2560,2624) d|dmin<<16 per row; [2624,2816) the 12
+// scale bytes per row. GGUF block_q5_K (176 B): d, dmin, scales[12], qh[32],
+// qs[128]; element 32 m + p: low nibble as Q4_K, fifth bit (qh[p] >> m) & 1.
+__global__ void k_repack_q5k(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t M,
+                             uint32_t nsb, uint32_t dst_tile0, uint32_t tile_stride) {
+  const uint32_t tile = blockIdx.x, sb = blockIdx.y, l = threadIdx.x;
+  const uint32_t r = l & 15, g = l >> 4, row = tile * 16 + r;
+  uint8_t* out = dst + ((size_t)(dst_tile0 + tile * tile_stride) * nsb + sb) * SH_Q5K_TILE_BYTES;
+  uint32_t words[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hw[2] = {0, 0};
+  if (row < M) {
+    const uint8_t* blk = src + ((size_t)row * nsb + sb) * 176;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + 48;
+    for (int m = 0; m < 8; ++m) {
+      words[m] = nibble_word(qs, 32 * (m >> 1) + 8 * g, 4 * (m & 1));
+      const uint32_t base = (m & 1) * 2 + ((m >> 1) & 1) * 8;
+      for (int t = 0; t < 8; ++t) hw[m >> 2] |= ((qh[8 * g + t] >> m) & 1u) << (base + hbit_pos(t, 1));
+    }
+  }
+  if (g == 0) {
+    uint32_t dd = 0;
+    uint8_t sc[12] = {0};
+    if (row < M) {
+      const uint8_t* blk = src + ((size_t)row * nsb + sb) * 176;
+      dd = blk[0] | (blk[1] << 8) | (blk[2] << 16) | ((uint32_t)blk[3] << 24);
+      for (int i = 0; i < 12; ++i) sc[i] = blk[4 + i];
+    }
+    *(uint32_t*)(out + 2560 + 4 * r) = dd;
+    for (int i = 0; i < 12; ++i) out[2624 + 12 * r + i] = sc[i];
+  }
+  uint32_t* o = (uint32_t*)(out + 16 * l);
+  for (int m = 0; m < 4; ++m) o[m] = words[m];
+  o = (uint32_t*)(out + 1024 + 16 * l);
+  for (int m = 0; m < 4; ++m) o[m] = words[4 + m];
+  o = (uint32_t*)(out + 2048 + 8 * l);
+  o[0] = hw[0];
+  o[1] = hw[1];
+}
+
+// Q6_K tile-superblock (3360 B): [0,2048) the low-nibble words in the Q4_K
+// layout; [2048,3072) four high-bit words per lane at 2048 + 16 l, word h
+// holding sub-blocks 2h, 2h + 1 at bases 0, 8 (element t: two bits at base +
+// hbit_pos(t, 2)); [3072,3328) per
+// row 16 int8 scales, the even-indexed 8 then the odd-indexed 8 (lane group g
+// reads its 8: scale 2 m + g / 2 for sub-block m); [3328,3360) f16 d per row.
+// GGUF block_q6_K (210 B): ql[128], qh[64], scales[16], d; element
+// 128 n + 32 s + p: (ql[64 n + 32 (s & 1) + p] >> 4 (s >> 1)) & 15 |
+// ((qh[32 n + p] >> 2 s) & 3) << 4, value d * scales[e / 16] * (q - 32).
+__global__ void k_repack_q6k(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t M,
+                             uint32_t nsb, uint32_t dst_tile0, uint32_t tile_stride) {
+  const uint32_t tile = blockIdx.x, sb = blockIdx.y, l = threadIdx.x;
+  const uint32_t r = l & 15, g = l >> 4, row = tile * 16 + r;
+  uint8_t* out = dst + ((size_t)(dst_tile0 + tile * tile_stride) * nsb + sb) * SH_Q6K_TILE_BYTES;
+  uint32_t words[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hw[4] = {0, 0, 0, 0};
+  const uint8_t* blk = src + ((size_t)(row < M ? row : 0) * nsb + sb) * 210;
+  if (row < M) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    for (int m = 0; m < 8; ++m) {
+      const uint32_t n = m >> 2, s = m & 3;
+      words[m] = nibble_word(ql, 64 * n + 32 * (s & 1) + 8 * g, 4 * (s >> 1));
+      const uint32_t base = 8 * (m & 1);
+      for (int t = 0; t < 8; ++t)
+        hw[m >> 1] |= ((qh[32 * n + 8 * g + t] >> (2 * s)) & 3u) << (base + hbit_pos(t, 2));
+    }
+  }
+  if (g == 0) {
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    for (int i = 0; i < 8; ++i) {
+      out[3072 + 16 * r + i] = row < M ? (uint8_t)sc[2 * i] : 0;
+      out[3072 + 16 * r + 8 + i] = row < M ? (uint8_t)sc[2 * i + 1] : 0;
+    }
+    out[3328 + 2 * r] = row < M ? blk[208] : 0;
+    out[3329 + 2 * r] = row < M ? blk[209] : 0;
+  }
+  uint32_t* o = (uint32_t*)(out + 16 * l);
+  for (int m = 0; m < 4; ++m) o[m] = words[m];
+  o = (uint32_t*)(out + 1024 + 16 * l);
+  for (int m = 0; m < 4; ++m) o[m] = words[4 + m];
+  o = (uint32_t*)(out + 2048 + 16 * l);
+  for (int m = 0; m < 4; ++m) o[m] = hw[m];
+}
+
 // Q8_0 tile-block (544 B): [0,512) 64 lanes x 8 int8 (row l%16, k = 32b + 8g + t);
 // [512,544) f16 d per row.
 __global__ void k_repack_q8(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t M,
@@ -908,23 +1019,233 @@ __device__ __forceinline__ float col_rinv_g(const EpiArgs& ea, uint32_t g, uint3
   return 1.0f / sqrtf(ss / (float)ea.norm_K + ea.eps);
 }
 
-// y = W x for G operand groups (up to 64 columns) in one pass over W. A
-// workgroup of 8 waves covers 8 T row tiles (wave w: tiles (blockIdx.x * 8 +
-// w) * T + t) over the superblocks [S blockIdx.y, S blockIdx.y + S) of split
-// blockIdx.y. Per superblock the G groups' operands (B and XS, 9 KB each, and
-// 8 scales) are copied to LDS by direct global->LDS loads, two buffers
-// alternating so superblock i + 1 (operands and weights) loads while i
-// computes; every decoded weight fragment then feeds G MFMAs. The per-
-// superblock sums go through d, dmin and the column scale in f32 as in the
-// 8-column kernels. EPI_PART writes split partials [split][col][row];
-// EPI_STORE (one split) whole rows.
+// ------------------------------------------------------------------ Q5_K / Q6_K fragments
+
+// One wave's operands of one (16-row tile, superblock) of Q5_K: the Q4_K
+// words plus two high-bit words per lane (tile layout at k_repack_q5k).
+struct Q5Tile {
+  u32x4 q0, q1, dd;
+  uint32_t h0, h1;
+  uint32_t s0, s1, s2;
+};
+struct Q5Dec {
+  uint32_t w[8], h[2];
+  uint32_t sc03, sc47, m03, m47;
+  float d[4], dmin[4];
+};
+__device__ __forceinline__ Q5Tile load_q5_tile(const uint8_t* base, int lane, int g, int r) {
+  Q5Tile a;
+  a.q0 = ld16(base + 16 * lane);
+  a.q1 = ld16(base + 1024 + 16 * lane);
+  const uint2 h = *(const uint2*)(base + 2048 + 8 * lane);
+  a.h0 = h.x;
+  a.h1 = h.y;
+  a.dd = ld16(base + 2560 + 16 * g);
+  const uint32_t* sp = (const uint32_t*)(base + 2624 + 12 * r);
+  a.s0 = sp[0];
+  a.s1 = sp[1];
+  a.s2 = sp[2];
+  return a;
+}
+__device__ __forceinline__ Q5Dec q5_decode_setup(const Q5Tile& a) {
+  Q4Tile b;
+  b.q0 = a.q0; b.q1 = a.q1; b.dd = a.dd; b.s0 = a.s0; b.s1 = a.s1; b.s2 = a.s2;
+  const Q4Dec q = q4_decode_setup(b);
+  Q5Dec s;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) s.w[m] = q.w[m];
+  s.h[0] = a.h0;
+  s.h[1] = a.h1;
+  s.sc03 = q.sc03; s.sc47 = q.sc47; s.m03 = q.m03; s.m47 = q.m47;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { s.d[j] = q.d[j]; s.dmin[j] = q.dmin[j]; }
+  return s;
+}
+
+// w shifted left by n (n >= 0) or right by -n; n is a constant after unrolling.
+__device__ __forceinline__ uint32_t shl_signed(uint32_t w, int n) { return n >= 0 ? w << n : w >> -n; }
+
+// A operand of Q5_K sub-block m: exact f16 c sc_m q5 with q5 = nibble + 16 h.
+// The fifth bit goes into the magic's mantissa right above the nibble (bit 4
+// of a half for the pairs decoded as 1024 + q, bit 8 for those decoded as
+// 1024 + 16 q), so (1024 + c q5) sc - 1024 sc = c sc q5 stays one exact FMA
+// (c sc q5 <= 16 * 63 * 31 < 2^15, 11 significant bits).
+__device__ __forceinline__ h8 q5_frag(const Q5Dec& s, int m, uint32_t magic) {
+  const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  const int base = (m & 1) * 2 + ((m >> 1) & 1) * 8;
+  const uint32_t hw = s.h[m >> 2];
+  const uint32_t hx = shl_signed(hw, 4 - base), hz = shl_signed(hw, 3 - base);
+  const uint32_t w = s.w[m], w8 = w >> 8;
+  const h2 mult = magic_pair(m < 4 ? s.sc03 : s.sc47, magic, m & 3, m & 3) + k1024;
+  const h2 add = mult * k1024;
+  u32x4 r;
+  r.x = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x000F000Fu, w, bfi(0x00100010u, hx, magic))), mult, add));
+  r.y = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x00F000F0u, w, bfi(0x01000100u, hx, magic))), mult, add));
+  r.z = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x000F000Fu, w8, bfi(0x00100010u, hz, magic))), mult, add));
+  r.w = as_u32(__builtin_elementwise_fma(as_h2(bfi(0x00F000F0u, w8, bfi(0x01000100u, hz, magic))), mult, add));
+  return as_h8(r);
+}
+__device__ __forceinline__ h8 q5_min_frag(const Q5Dec& s, uint32_t magic) {
+  Q4Dec q;
+  q.m03 = s.m03;
+  q.m47 = s.m47;
+  return q4_min_frag(q, magic);
+}
+
+// One wave's operands of one (16-row tile, superblock) of Q6_K (tile layout at
+// k_repack_q6k): the nibble words, four high-bit words, the lane's 8 scales
+// (sub-block m: byte m) and d of the lane's 4 output rows.
+struct Q6Tile {
+  u32x4 q0, q1, h;
+  uint2 sc, d;
+};
+struct Q6Dec {
+  uint32_t w[8], h[4];
+  uint32_t sl03, sl47, sh03, sh47;
+  float d[4];
+};
+__device__ __forceinline__ Q6Tile load_q6_tile(const uint8_t* base, int lane, int g, int r) {
+  Q6Tile a;
+  a.q0 = ld16(base + 16 * lane);
+  a.q1 = ld16(base + 1024 + 16 * lane);
+  a.h = ld16(base + 2048 + 16 * lane);
+  a.sc = *(const uint2*)(base + 3072 + 16 * r + 8 * (g >> 1));
+  a.d = *(const uint2*)(base + 3328 + 8 * g);
+  return a;
+}
+// A scale sc (int8) is split as 16 sh + sl, sl = sc & 15 in [0, 15] and sh =
+// sc >> 4 in [-8, 7]; the bytes below are sl and sh + 8 (the latter as the
+// high nibble with its top bit flipped: u ^ 8 = sh + 8 for u = sc >> 4 & 15).
+__device__ __forceinline__ Q6Dec q6_decode_setup(const Q6Tile& a) {
+  Q6Dec s;
+  s.w[0] = a.q0.x; s.w[1] = a.q0.y; s.w[2] = a.q0.z; s.w[3] = a.q0.w;
+  s.w[4] = a.q1.x; s.w[5] = a.q1.y; s.w[6] = a.q1.z; s.w[7] = a.q1.w;
+  s.h[0] = a.h.x; s.h[1] = a.h.y; s.h[2] = a.h.z; s.h[3] = a.h.w;
+  s.sl03 = a.sc.x & 0x0F0F0F0Fu;
+  s.sl47 = a.sc.y & 0x0F0F0F0Fu;
+  s.sh03 = ((a.sc.x >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+  s.sh47 = ((a.sc.y >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+  s.d[0] = (float)as_h2(a.d.x).x;
+  s.d[1] = (float)as_h2(a.d.x).y;
+  s.d[2] = (float)as_h2(a.d.y).x;
+  s.d[3] = (float)as_h2(a.d.y).y;
+  return s;
+}
+// The two A operands of Q6_K sub-block m, exact f16 c sl (q - 32) and
+// c sh (q - 32), c = 1 or 16 by pair; the sums combine as acc_l + 16 acc_h
+// (= sc (q - 32) summed, a product that would need 13 bits in one f16). The
+// 6-bit q = nibble + 16 hi2 is decoded as 1024 + q (or 1024 + 16 q, at most
+// 2032) with the two high bits in the mantissa above the nibble; the FMA's
+// addend -(1024 + 32 c) s removes both offsets: |c s (q - 32)| <= 7680 exactly.
+__device__ __forceinline__ void q6_frag(const Q6Dec& s, int m, uint32_t magic, h8 (&a)[2]) {
+  const h2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  const h2 k1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const h2 k1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+  const h2 k1536 = {(_Float16)-1536.0f, (_Float16)-1536.0f};
+  const int base = (m & 1) * 8;
+  const uint32_t hw = s.h[m >> 1];
+  const uint32_t hx = shl_signed(hw, 4 - base), hz = shl_signed(hw, 2 - base);
+  const uint32_t w = s.w[m], w8 = w >> 8;
+  const h2 ml = magic_pair(m < 4 ? s.sl03 : s.sl47, magic, m & 3, m & 3) + k1024;
+  const h2 mh = magic_pair(m < 4 ? s.sh03 : s.sh47, magic, m & 3, m & 3) + k1032;
+  const h2 px = as_h2(bfi(0x000F000Fu, w, bfi(0x00300030u, hx, magic)));
+  const h2 py = as_h2(bfi(0x00F000F0u, w, bfi(0x03000300u, hx, magic)));
+  const h2 pz = as_h2(bfi(0x000F000Fu, w8, bfi(0x00300030u, hz, magic)));
+  const h2 pw = as_h2(bfi(0x00F000F0u, w8, bfi(0x03000300u, hz, magic)));
+  const h2 l1 = ml * k1056, l16 = ml * k1536, h1 = mh * k1056, h16 = mh * k1536;
+  u32x4 r;
+  r.x = as_u32(__builtin_elementwise_fma(px, ml, l1));
+  r.y = as_u32(__builtin_elementwise_fma(py, ml, l16));
+  r.z = as_u32(__builtin_elementwise_fma(pz, ml, l1));
+  r.w = as_u32(__builtin_elementwise_fma(pw, ml, l16));
+  a[0] = as_h8(r);
+  r.x = as_u32(__builtin_elementwise_fma(px, mh, h1));
+  r.y = as_u32(__builtin_elementwise_fma(py, mh, h16));
+  r.z = as_u32(__builtin_elementwise_fma(pz, mh, h1));
+  r.w = as_u32(__builtin_elementwise_fma(pw, mh, h16));
+  a[1] = as_h8(r);
+}
+
+// Weight formats of the multi-group GEMM: tile bytes, one wave's loads of a
+// (tile, superblock), the per-superblock decode setup, the A fragments of
+// sub-block m (NA per sub-block, each against the same B), whether the
+// minimum term (XS operand) applies, and the superblock's contribution
+// d * sum - dmin * min for output row j.
+struct FmtQ4K {
+  static constexpr uint32_t kTile = SH_Q4K_TILE_BYTES;
+  static constexpr int NA = 1;
+  static constexpr bool kMin = true;
+  using Tile = Q4Tile;
+  using Dec = Q4Dec;
+  static __device__ __forceinline__ Tile load(const uint8_t* b, int lane, int g, int r) {
+    return load_q4_tile(b, lane, g, r);
+  }
+  static __device__ __forceinline__ Dec setup(const Tile& a) { return q4_decode_setup(a); }
+  static __device__ __forceinline__ void frag(const Dec& s, int m, uint32_t magic, h8 (&a)[NA]) {
+    a[0] = q4_frag(s, m, magic);
+  }
+  static __device__ __forceinline__ h8 min_frag(const Dec& s, uint32_t magic) { return q4_min_frag(s, magic); }
+  static __device__ __forceinline__ float term(const Dec& s, const f4 (&acc)[NA], float macc, int j) {
+    return s.d[j] * acc[0][j] - s.dmin[j] * macc;
+  }
+};
+struct FmtQ5K {
+  static constexpr uint32_t kTile = SH_Q5K_TILE_BYTES;
+  static constexpr int NA = 1;
+  static constexpr bool kMin = true;
+  using Tile = Q5Tile;
+  using Dec = Q5Dec;
+  static __device__ __forceinline__ Tile load(const uint8_t* b, int lane, int g, int r) {
+    return load_q5_tile(b, lane, g, r);
+  }
+  static __device__ __forceinline__ Dec setup(const Tile& a) { return q5_decode_setup(a); }
+  static __device__ __forceinline__ void frag(const Dec& s, int m, uint32_t magic, h8 (&a)[NA]) {
+    a[0] = q5_frag(s, m, magic);
+  }
+  static __device__ __forceinline__ h8 min_frag(const Dec& s, uint32_t magic) { return q5_min_frag(s, magic); }
+  static __device__ __forceinline__ float term(const Dec& s, const f4 (&acc)[NA], float macc, int j) {
+    return s.d[j] * acc[0][j] - s.dmin[j] * macc;
+  }
+};
+struct FmtQ6K {
+  static constexpr uint32_t kTile = SH_Q6K_TILE_BYTES;
+  static constexpr int NA = 2;
+  static constexpr bool kMin = false;
+  using Tile = Q6Tile;
+  using Dec = Q6Dec;
+  static __device__ __forceinline__ Tile load(const uint8_t* b, int lane, int g, int r) {
+    return load_q6_tile(b, lane, g, r);
+  }
+  static __device__ __forceinline__ Dec setup(const Tile& a) { return q6_decode_setup(a); }
+  static __device__ __forceinline__ void frag(const Dec& s, int m, uint32_t magic, h8 (&a)[NA]) {
+    q6_frag(s, m, magic, a);
+  }
+  static __device__ __forceinline__ h8 min_frag(const Dec&, uint32_t) { return h8{}; }
+  static __device__ __forceinline__ float term(const Dec& s, const f4 (&acc)[NA], float, int j) {
+    return s.d[j] * __builtin_fmaf(16.0f, acc[1][j], acc[0][j]);
+  }
+};
+
+// y = W x for G operand groups (up to 64 columns) in one pass over W, W in
+// any K-quant format F. A workgroup of 8 waves covers 8 T row tiles (wave w:
+// tiles (blockIdx.x * 8 + w) * T + t) over the superblocks [S blockIdx.y,
+// S blockIdx.y + S) of split blockIdx.y. Per superblock the G groups' operands
+// (B and XS, 9 KB each, and 8 scales) are copied to LDS by direct
+// global->LDS loads, two buffers alternating so superblock i + 1 (operands and
+// weights) loads while i computes; every decoded weight fragment then feeds G
+// MFMAs. The per-superblock sums go through d (and dmin) and the column scale
+// in f32 as in the 8-column kernels. EPI_PART writes split partials
+// [split][col][row]; EPI_STORE (one split) whole rows.
 constexpr uint32_t MG_MAX_G = 8;
 
-template <int T, int G, int EPI>
-__global__ __launch_bounds__(512) void k_gemm_q4(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+template <class F, int T, int G, int EPI>
+__global__ __launch_bounds__(512) void k_gemm_kq(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
                                                   uint32_t S, const uint16_t* __restrict__ Bx,
                                                   const uint16_t* __restrict__ XS, const float* __restrict__ CS,
                                                   uint32_t N, EpiArgs ea) {
+  using Tile = typename F::Tile;
+  using Dec = typename F::Dec;
+  constexpr int NA = F::NA;
   __shared__ h8 sB[2][G * 9 * 64];  // [buffer][group * 9 + fragment][lane]
   __shared__ float sC[2][64];       // [buffer][group * 8 + column]
   const int lane = threadIdx.x & 63;
@@ -939,9 +1260,10 @@ __global__ __launch_bounds__(512) void k_gemm_q4(const uint8_t* __restrict__ Wp,
   for (int g = 0; g < G; ++g) nf[g] = col_rinv_g(ea, g, r & 7);
 
   auto stage = [&](uint32_t sb, int buf) {
-    // fragment f of group g: 1 KB, one wave instruction
+    // fragment f of group g: 1 KB, one wave instruction (XS only with a minimum term)
     for (uint32_t fi = wave; fi < (uint32_t)(G * 9); fi += 8) {
       const uint32_t g = fi / 9, f = fi % 9;
+      if (!F::kMin && f == 8) continue;
       const uint16_t* src = f < 8 ? Bx + g * gB + ((size_t)(sb * 8 + f) * 64 + lane) * 8
                                   : XS + g * gX + ((size_t)sb * 64 + lane) * 8;
       __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&sB[buf][fi * 64]), 16, 0, 0);
@@ -954,7 +1276,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4(const uint8_t* __restrict__ Wp,
   };
   auto a_ptr = [&](int t, uint32_t sb) {
     const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
-    return Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
+    return Wp + ((size_t)tt * nsb + sb) * F::kTile;
   };
 
   f4 y[T][G];
@@ -963,56 +1285,63 @@ __global__ __launch_bounds__(512) void k_gemm_q4(const uint8_t* __restrict__ Wp,
 #pragma unroll
     for (int g = 0; g < G; ++g) y[t][g] = f4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const Q4Tile (&at)[T], int buf) {
-    Q4Dec dec[T];
+  auto compute = [&](const Tile (&at)[T], int buf) {
+    Dec dec[T];
 #pragma unroll
-    for (int t = 0; t < T; ++t) dec[t] = q4_decode_setup(at[t]);
-    f4 acc[T][G];
+    for (int t = 0; t < T; ++t) dec[t] = F::setup(at[t]);
+    f4 acc[T][G][NA];
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[t][g] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < NA; ++i) acc[t][g][i] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      h8 a[T];
+      h8 a[T][NA];
 #pragma unroll
-      for (int t = 0; t < T; ++t) a[t] = q4_frag(dec[t], m, magic);
+      for (int t = 0; t < T; ++t) F::frag(dec[t], m, magic, a[t]);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const h8 b = sB[buf][(g * 9 + m) * 64 + lane];
 #pragma unroll
-        for (int t = 0; t < T; ++t) acc[t][g] = mfma16(a[t], b, acc[t][g]);
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int i = 0; i < NA; ++i) acc[t][g][i] = mfma16(a[t][i], b, acc[t][g][i]);
       }
     }
     h8 am[T];
+    if constexpr (F::kMin) {
 #pragma unroll
-    for (int t = 0; t < T; ++t) am[t] = q4_min_frag(dec[t], magic);
+      for (int t = 0; t < T; ++t) am[t] = F::min_frag(dec[t], magic);
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const h8 bm = sB[buf][(g * 9 + 8) * 64 + lane];
+      h8 bm;
+      if constexpr (F::kMin) bm = sB[buf][(g * 9 + 8) * 64 + lane];
       const float c = sC[buf][g * 8 + (lane & 7)];
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const f4 macc = mfma16(am[t], bm, f4{0.f, 0.f, 0.f, 0.f});
+        f4 macc = f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (F::kMin) macc = mfma16(am[t], bm, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          y[t][g][j] = y[t][g][j] + c * (dec[t].d[j] * acc[t][g][j] - dec[t].dmin[j] * macc[j]);
+        for (int j = 0; j < 4; ++j) y[t][g][j] = y[t][g][j] + c * F::term(dec[t], acc[t][g], macc[j], j);
       }
     }
   };
 
   // Superblocks go in pairs so each weight buffer's index is a constant.
-  Q4Tile wa[T], wb[T];
+  Tile wa[T], wb[T];
   stage(sb0, 0);
 #pragma unroll
-  for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, sb0), lane, g4, r);
+  for (int t = 0; t < T; ++t) wa[t] = F::load(a_ptr(t, sb0), lane, g4, r);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (uint32_t sb = sb0; sb < sb1; sb += 2) {
     if (sb + 1 < sb1) {
       stage(sb + 1, 1);
 #pragma unroll
-      for (int t = 0; t < T; ++t) wb[t] = load_q4_tile(a_ptr(t, sb + 1), lane, g4, r);
+      for (int t = 0; t < T; ++t) wb[t] = F::load(a_ptr(t, sb + 1), lane, g4, r);
     }
     compute(wa, 0);
     __builtin_amdgcn_s_waitcnt(0);
@@ -1021,7 +1350,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4(const uint8_t* __restrict__ Wp,
     if (sb + 2 < sb1) {
       stage(sb + 2, 0);
 #pragma unroll
-      for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, sb + 2), lane, g4, r);
+      for (int t = 0; t < T; ++t) wa[t] = F::load(a_ptr(t, sb + 2), lane, g4, r);
     }
     compute(wb, 1);
     __builtin_amdgcn_s_waitcnt(0);
@@ -1046,6 +1375,11 @@ __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ par
   const uint32_t col = blockIdx.y, r0 = 4 * (blockIdx.x * 64 + threadIdx.x);
   if (r0 >= ea.Dq + 2 * ea.Dkv) return;
   const float* p = part + (size_t)col * ldp + r0;
+  if (qc.vpart && r0 >= ea.Dq + ea.Dkv) {  // v rows of their own matrix (4 rows never straddle: hd % 4 == 0)
+    p = qc.vpart + (size_t)col * qc.vldp + (r0 - ea.Dq - ea.Dkv);
+    nparts = qc.vnparts;
+    part_stride = qc.vstride;
+  }
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
   for (uint32_t k0 = 0; k0 < nparts; k0 += 8) {  // 8 loads in flight, split order kept
     float4 t[8];
@@ -1079,6 +1413,11 @@ __global__ __launch_bounds__(128) void k_qkv_finish_head(const float* __restrict
   const uint32_t hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
   const uint32_t row = kind == 0 ? hh * hd + i : (kind == 1 ? ea.Dq + hh * hd + i : ea.Dq + ea.Dkv + hh * hd + i);
   const float* p = part + (size_t)col * ldp + row;
+  if (kind == 2 && qc.vpart) {  // v rows of their own matrix
+    p = qc.vpart + (size_t)col * qc.vldp + hh * hd + i;
+    nparts = qc.vnparts;
+    part_stride = qc.vstride;
+  }
   float v = 0.f;
   for (uint32_t k0 = 0; k0 < nparts; k0 += 8) {  // 8 loads in flight, split order kept
     float t[8];
@@ -1316,25 +1655,52 @@ void sh_qmat_free(QMat* m) {
   m->d = nullptr;
 }
 
-static size_t qrow_bytes(int type, uint32_t K) { return type == GGML_Q4_K ? K / 256 * 144 : K / 32 * 34; }
+static size_t qrow_bytes(int type, uint32_t K) {
+  switch (type) {
+    case GGML_Q4_K: return (size_t)K / 256 * 144;
+    case GGML_Q5_K: return (size_t)K / 256 * 176;
+    case GGML_Q6_K: return (size_t)K / 256 * 210;
+    default: return (size_t)K / 32 * 34;  // Q8_0
+  }
+}
+static uint32_t q_block_elems(int type) { return type == GGML_Q8_0 ? 32u : 256u; }
+static uint32_t q_tile_bytes(int type) {
+  switch (type) {
+    case GGML_Q4_K: return SH_Q4K_TILE_BYTES;
+    case GGML_Q5_K: return SH_Q5K_TILE_BYTES;
+    case GGML_Q6_K: return SH_Q6K_TILE_BYTES;
+    default: return SH_Q8_TILE_BYTES;
+  }
+}
+static bool q_repackable(int type) { return sh_is_kquant(type) || type == GGML_Q8_0; }
 
-// Upload nparts row-blocks (each a GGUF [rows][K] matrix) as one packed matrix
-// with rows concatenated. Each part's row count must be a multiple of 16.
+// Repack rows [0, M) of one GGUF matrix (on the device at src) into tiles
+// dst_tile0 + t * tile_stride of dst.
+static void launch_repack(sh_engine* e, int type, const uint8_t* src, uint8_t* dst, uint32_t M, uint32_t nblk,
+                          uint32_t tile0, uint32_t stride) {
+  const dim3 grid((M + 15) / 16, nblk);
+  switch (type) {
+    case GGML_Q4_K: hipLaunchKernelGGL(k_repack_q4k, grid, dim3(64), 0, e->stream, src, dst, M, nblk, tile0, stride); break;
+    case GGML_Q5_K: hipLaunchKernelGGL(k_repack_q5k, grid, dim3(64), 0, e->stream, src, dst, M, nblk, tile0, stride); break;
+    case GGML_Q6_K: hipLaunchKernelGGL(k_repack_q6k, grid, dim3(64), 0, e->stream, src, dst, M, nblk, tile0, stride); break;
+    default: hipLaunchKernelGGL(k_repack_q8, grid, dim3(64), 0, e->stream, src, dst, M, nblk, tile0, stride); break;
+  }
+}
+
 int sh_repack_upload_cat(sh_engine* e, int type, const uint8_t* const* parts, const uint32_t* rows, int nparts,
                          uint32_t K, QMat* out) {
-  SH_CHECK(type == GGML_Q4_K || type == GGML_Q8_0, SH_ERR_UNSUPPORTED,
-           "weight type %d not supported (Q4_K=12, Q8_0=8)", type);
-  SH_CHECK(K % (type == GGML_Q4_K ? 256 : 32) == 0, SH_ERR_FORMAT, "K=%u not a multiple of the block", K);
+  SH_CHECK(q_repackable(type), SH_ERR_UNSUPPORTED, "weight type %d not supported (Q4_K=12, Q5_K=13, Q6_K=14, Q8_0=8)",
+           type);
+  SH_CHECK(K % q_block_elems(type) == 0, SH_ERR_FORMAT, "K=%u not a multiple of the block", K);
   uint32_t M = 0;
   for (int i = 0; i < nparts; ++i) {
     SH_CHECK(nparts == 1 || rows[i] % 16 == 0, SH_ERR_UNSUPPORTED, "concatenated part rows %u %% 16", rows[i]);
     M += rows[i];
   }
-  const uint32_t nblk = type == GGML_Q4_K ? K / 256 : K / 32;
-  const uint32_t tb = type == GGML_Q4_K ? SH_Q4K_TILE_BYTES : SH_Q8_TILE_BYTES;
+  const uint32_t nblk = K / q_block_elems(type);
   QMat m;
   m.type = type; m.M = M; m.K = K; m.tiles = (M + 15) / 16;
-  m.bytes = (size_t)m.tiles * nblk * tb;
+  m.bytes = (size_t)m.tiles * nblk * q_tile_bytes(type);
   m.alg_bytes = (double)M * qrow_bytes(type, K);
   SH_HIP(hipMalloc(&m.d, m.bytes));
   uint32_t tile0 = 0;
@@ -1343,16 +1709,11 @@ int sh_repack_upload_cat(sh_engine* e, int type, const uint8_t* const* parts, co
     uint8_t* tmp = nullptr;
     SH_HIP(hipMalloc(&tmp, bytes));
     SH_HIP(hipMemcpyAsync(tmp, parts[i], bytes, hipMemcpyHostToDevice, e->stream));
-    const uint32_t ptiles = (rows[i] + 15) / 16;
-    dim3 grid(ptiles, nblk);
-    if (type == GGML_Q4_K)
-      hipLaunchKernelGGL(k_repack_q4k, grid, dim3(64), 0, e->stream, tmp, m.d, rows[i], nblk, tile0, 1u);
-    else
-      hipLaunchKernelGGL(k_repack_q8, grid, dim3(64), 0, e->stream, tmp, m.d, rows[i], nblk, tile0, 1u);
+    launch_repack(e, type, tmp, m.d, rows[i], nblk, tile0, 1u);
     SH_HIP(hipGetLastError());
     SH_HIP(hipStreamSynchronize(e->stream));
     SH_HIP(hipFree(tmp));
-    tile0 += ptiles;
+    tile0 += (rows[i] + 15) / 16;
   }
   *out = m;
   return SH_OK;
@@ -1365,13 +1726,13 @@ int sh_repack_upload(sh_engine* e, int type, const uint8_t* host, uint32_t M, ui
 // gate/up: tile t of gate -> packed tile 2t, tile t of up -> 2t+1.
 int sh_repack_upload_gu(sh_engine* e, int type, const uint8_t* gate, const uint8_t* up, uint32_t M, uint32_t K,
                         QMat* out) {
-  SH_CHECK(type == GGML_Q4_K || type == GGML_Q8_0, SH_ERR_UNSUPPORTED, "weight type %d not supported", type);
+  SH_CHECK(q_repackable(type), SH_ERR_UNSUPPORTED, "weight type %d not supported", type);
   SH_CHECK(M % 32 == 0, SH_ERR_UNSUPPORTED, "n_ff=%u must be a multiple of 32", M);
-  const uint32_t nblk = type == GGML_Q4_K ? K / 256 : K / 32;
-  const uint32_t tb = type == GGML_Q4_K ? SH_Q4K_TILE_BYTES : SH_Q8_TILE_BYTES;
+  SH_CHECK(K % q_block_elems(type) == 0, SH_ERR_FORMAT, "K=%u not a multiple of the block", K);
+  const uint32_t nblk = K / q_block_elems(type);
   QMat m;
   m.type = type; m.M = 2 * M; m.K = K; m.tiles = 2 * (M / 16);
-  m.bytes = (size_t)m.tiles * nblk * tb;
+  m.bytes = (size_t)m.tiles * nblk * q_tile_bytes(type);
   m.alg_bytes = 2.0 * M * qrow_bytes(type, K);
   SH_HIP(hipMalloc(&m.d, m.bytes));
   const size_t bytes = (size_t)M * qrow_bytes(type, K);
@@ -1379,11 +1740,7 @@ int sh_repack_upload_gu(sh_engine* e, int type, const uint8_t* gate, const uint8
   SH_HIP(hipMalloc(&tmp, bytes));
   for (int part = 0; part < 2; ++part) {
     SH_HIP(hipMemcpyAsync(tmp, part ? up : gate, bytes, hipMemcpyHostToDevice, e->stream));
-    dim3 grid(M / 16, nblk);
-    if (type == GGML_Q4_K)
-      hipLaunchKernelGGL(k_repack_q4k, grid, dim3(64), 0, e->stream, tmp, m.d, M, nblk, (uint32_t)part, 2u);
-    else
-      hipLaunchKernelGGL(k_repack_q8, grid, dim3(64), 0, e->stream, tmp, m.d, M, nblk, (uint32_t)part, 2u);
+    launch_repack(e, type, tmp, m.d, M, nblk, (uint32_t)part, 2u);
     SH_HIP(hipGetLastError());
     SH_HIP(hipStreamSynchronize(e->stream));
   }
@@ -1748,37 +2105,44 @@ static MgPlan mg_plan(const QMat& w, uint32_t G, bool one_split) {
 }
 
 size_t sh_gemm_part_floats(const QMat& w) {
-  if (w.type != GGML_Q4_K) return 0;
+  if (!sh_is_kquant(w.type)) return 0;
   return (size_t)mg_plan(w, MG_MAX_G, false).KS * SH_MAX_COLS * w.tiles * 16;
 }
 
-template <int T, int G, int EPI>
+template <class F, int T, int G, int EPI>
 static void launch_mg(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs,
                       uint32_t N, const EpiArgs& ea, const MgPlan& p) {
   const dim3 grid((w.tiles + 8 * T - 1) / (8 * T), p.KS);
-  hipLaunchKernelGGL((k_gemm_q4<T, G, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bx, xs, cs,
-                     N, ea);
+  hipLaunchKernelGGL((k_gemm_kq<F, T, G, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bx, xs,
+                     cs, N, ea);
 }
-template <int EPI>
+template <class F, int EPI>
 static void dispatch_mg(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs,
                         uint32_t N, const EpiArgs& ea, const MgPlan& p) {
   switch ((N + 7) / 8) {
-    case 1: launch_mg<2, 1, EPI>(e, w, bx, xs, cs, N, ea, p); break;
-    case 2: launch_mg<2, 2, EPI>(e, w, bx, xs, cs, N, ea, p); break;
-    case 3: launch_mg<2, 3, EPI>(e, w, bx, xs, cs, N, ea, p); break;
-    case 4: launch_mg<2, 4, EPI>(e, w, bx, xs, cs, N, ea, p); break;
-    case 5: launch_mg<1, 5, EPI>(e, w, bx, xs, cs, N, ea, p); break;
-    case 6: launch_mg<1, 6, EPI>(e, w, bx, xs, cs, N, ea, p); break;
-    case 7: launch_mg<1, 7, EPI>(e, w, bx, xs, cs, N, ea, p); break;
-    default: launch_mg<1, 8, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 1: launch_mg<F, 2, 1, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 2: launch_mg<F, 2, 2, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 3: launch_mg<F, 2, 3, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 4: launch_mg<F, 2, 4, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 5: launch_mg<F, 1, 5, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 6: launch_mg<F, 1, 6, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    case 7: launch_mg<F, 1, 7, EPI>(e, w, bx, xs, cs, N, ea, p); break;
+    default: launch_mg<F, 1, 8, EPI>(e, w, bx, xs, cs, N, ea, p); break;
   }
+}
+template <int EPI>
+static void dispatch_mg_fmt(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs,
+                            uint32_t N, const EpiArgs& ea, const MgPlan& p) {
+  if (w.type == GGML_Q5_K) dispatch_mg<FmtQ5K, EPI>(e, w, bx, xs, cs, N, ea, p);
+  else if (w.type == GGML_Q6_K) dispatch_mg<FmtQ6K, EPI>(e, w, bx, xs, cs, N, ea, p);
+  else dispatch_mg<FmtQ4K, EPI>(e, w, bx, xs, cs, N, ea, p);
 }
 
 int sh_gemm_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs, uint32_t N,
                    EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts) {
   SH_CHECK(N >= 1 && N <= SH_MAX_COLS, SH_ERR_ARG, "gemm N=%u outside [1, %u]", N, SH_MAX_COLS);
-  SH_CHECK(w.type == GGML_Q4_K && w.K % 256 == 0, SH_ERR_UNSUPPORTED, "multi-group gemm needs Q4_K (type %d)",
-           w.type);
+  SH_CHECK(sh_is_kquant(w.type) && w.K % 256 == 0, SH_ERR_UNSUPPORTED,
+           "multi-group gemm needs a K-quant (Q4_K / Q5_K / Q6_K; type %d)", w.type);
   SH_CHECK(epi == EPI_PART || epi == EPI_STORE, SH_ERR_ARG, "multi-group gemm epilogue %d", (int)epi);
   const MgPlan p = mg_plan(w, (N + 7) / 8, epi == EPI_STORE);
   if (epi == EPI_PART)
@@ -1786,8 +2150,8 @@ int sh_gemm_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
              "gemm: %u split partials exceed the buffer (%u)", p.KS, ea.part_cap);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  if (epi == EPI_PART) dispatch_mg<EPI_PART>(e, w, bx, xs, cs, N, ea, p);
-  else dispatch_mg<EPI_STORE>(e, w, bx, xs, cs, N, ea, p);
+  if (epi == EPI_PART) dispatch_mg_fmt<EPI_PART>(e, w, bx, xs, cs, N, ea, p);
+  else dispatch_mg_fmt<EPI_STORE>(e, w, bx, xs, cs, N, ea, p);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, tag, w.alg_bytes, ev);
   if (nparts) *nparts = p.KS;

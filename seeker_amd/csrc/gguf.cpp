@@ -163,6 +163,7 @@ int u32_key(const GFile& f, const std::string& k, uint32_t* out, bool required, 
 bool matrix_type(uint32_t t) {
   return t == GGML_Q4_K || t == GGML_Q8_0 || t == GGML_Q5_K || t == GGML_Q6_K;
 }
+static bool sh_kquant_type(uint32_t t) { return t == GGML_Q4_K || t == GGML_Q5_K || t == GGML_Q6_K; }
 
 // Looks up a tensor and checks it is a rows x cols matrix (n_mat slabs) of a
 // known type; vectors (rows = 0) must be f32 [cols].
@@ -255,8 +256,6 @@ int sh_gguf_describe(const GFile& f, ModelDesc* m) {
                     kBig)))
     return rc;
   if ((rc = get_tensor(f, "token_embd.weight", m->d, m->V, 1, true, &m->tok_embd))) return rc;
-  SH_CHECK(m->tok_embd.type != GGML_Q5_K && m->tok_embd.type != GGML_Q6_K, SH_ERR_UNSUPPORTED,
-           "token_embd type %u (Q4_K, Q8_0, F16, F32 supported)", m->tok_embd.type);
   if ((rc = get_tensor(f, "output_norm.weight", m->d, 0, 1, true, &m->out_norm))) return rc;
   // lm_head = output.unwrap_or(token_embd) (llama.rs:424, qwen3.rs:673)
   if ((rc = get_tensor(f, "output.weight", m->d, m->V, 1, false, &m->output))) return rc;
@@ -303,39 +302,40 @@ int sh_gguf_describe(const GFile& f, ModelDesc* m) {
       if (t->present())
         SH_CHECK(matrix_type(t->type), SH_ERR_UNSUPPORTED, "layer %u: matrix type %u (K-quants and Q8_0 supported)",
                  l, t->type);
-    SH_CHECK(L.wq.type == L.wk.type && L.wk.type == L.wv.type, SH_ERR_UNSUPPORTED,
-             "layer %u: attn_q/k/v types %u/%u/%u differ", l, L.wq.type, L.wk.type, L.wv.type);
+    // attn_v may differ (Q4_K_M-style files keep it in Q6_K on some layers)
+    SH_CHECK(L.wq.type == L.wk.type, SH_ERR_UNSUPPORTED, "layer %u: attn_q/k types %u/%u differ", l, L.wq.type,
+             L.wk.type);
   }
   return SH_OK;
 }
 
+// What the device path runs: the fused 8-column path takes llama models whose
+// layer matrices are uniformly Q4_K or uniformly Q8_0 (lm_head Q4_K or Q8_0);
+// the multi-group path takes any mix of K-quants (Q4_K / Q5_K / Q6_K, routed
+// experts Q4_K) for every architecture. token_embd may be any type the reader
+// knows (the gather dequantizes rows).
 int sh_gguf_supported(const ModelDesc& m) {
+  bool all_kq = sh_kquant_type(m.output.type), uniform = m.arch == ARCH_LLAMA;
   const uint32_t wt = m.layers.empty() ? (uint32_t)GGML_Q4_K : m.layers[0].wq.type;
-  if (m.arch != ARCH_LLAMA) {
-    // qwen3 / qwen3moe run on the multi-group Q4_K kernels
-    SH_CHECK(m.output.type == GGML_Q4_K, SH_ERR_UNSUPPORTED, "qwen lm_head type %u (Q4_K only)", m.output.type);
-    for (uint32_t l = 0; l < m.n_layer; ++l) {
-      const LayerDesc& L = m.layers[l];
-      for (const TRef* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down, &L.gate_exps, &L.up_exps,
-                            &L.down_exps})
-        if (t->present())
-          SH_CHECK(t->type == GGML_Q4_K, SH_ERR_UNSUPPORTED, "layer %u: qwen matrix type %u (Q4_K only)", l, t->type);
-      if (L.gate_inp.present())
-        SH_CHECK(L.gate_inp.type == GGML_F32, SH_ERR_UNSUPPORTED, "layer %u: router type %u (f32 only)", l,
-                 L.gate_inp.type);
-    }
-    SH_CHECK(m.arch != ARCH_QWEN3MOE || (m.n_expert <= 1024 && m.d % 4 == 0 && (m.d + m.n_expert) * 4 <= 60 * 1024),
-             SH_ERR_UNSUPPORTED, "moe: %u experts at n_embd %u", m.n_expert, m.d);
-    return SH_OK;
-  }
-  SH_CHECK(wt == GGML_Q4_K || wt == GGML_Q8_0, SH_ERR_UNSUPPORTED, "weight type %u (Q4_K / Q8_0 only)", wt);
+  uniform = uniform && (wt == GGML_Q4_K || wt == GGML_Q8_0) &&
+            (m.output.type == GGML_Q4_K || m.output.type == GGML_Q8_0);
   for (uint32_t l = 0; l < m.n_layer; ++l) {
     const LayerDesc& L = m.layers[l];
     for (const TRef* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
-      SH_CHECK(t->type == wt, SH_ERR_UNSUPPORTED, "mixed weight types in layer %u (%u and %u)", l, t->type, wt);
+      if (t->present()) {
+        all_kq = all_kq && sh_kquant_type(t->type);
+        uniform = uniform && t->type == wt;
+      }
+    if (L.gate_inp.present())
+      SH_CHECK(L.gate_inp.type == GGML_F32, SH_ERR_UNSUPPORTED, "layer %u: router type %u (f32 only)", l,
+               L.gate_inp.type);
   }
-  SH_CHECK(m.output.type == GGML_Q4_K || m.output.type == GGML_Q8_0, SH_ERR_UNSUPPORTED, "lm_head type %u",
-           m.output.type);
+  SH_CHECK(all_kq || uniform, SH_ERR_UNSUPPORTED,
+           "weight types: the matrices must all be K-quants (Q4_K / Q5_K / Q6_K), or llama layers uniformly Q4_K or "
+           "Q8_0 (first layer type %u, lm_head %u)",
+           wt, m.output.type);
+  SH_CHECK(m.arch != ARCH_QWEN3MOE || (m.n_expert <= 1024 && m.d % 4 == 0 && (m.d + m.n_expert) * 4 <= 60 * 1024),
+           SH_ERR_UNSUPPORTED, "moe: %u experts at n_embd %u", m.n_expert, m.d);
   return SH_OK;
 }
 

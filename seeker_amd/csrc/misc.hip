@@ -9,7 +9,8 @@ __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_c
 
 // get_rows of a quantized token_embd (elementwise.rs:873, get_rows_q4_k.slang,
 // get_rows_quant.slang): resid[j][i] = deq(token_embd)[tokens[j]][i], with the
-// same per-element arithmetic as the Q4_K / Q8_0 dequant (run.rs:4212-4303).
+// same per-element arithmetic as the Q4_K / Q6_K / Q8_0 dequant
+// (run.rs:4212-4303) and llama.cpp's dequantize_row_q5_K for Q5_K.
 __global__ void k_embed(const uint8_t* __restrict__ embd, int type, uint32_t d, size_t row_bytes,
                         const uint32_t* __restrict__ tokens, uint32_t V, float* __restrict__ resid) {
   // workgroup (token j, 256 elements from blockIdx.y): one element per thread,
@@ -33,6 +34,27 @@ __global__ void k_embed(const uint8_t* __restrict__ embd, int type, uint32_t d, 
       const uint8_t byte = blk[16 + 32 * (s / 2) + l];
       const uint32_t q = (s & 1) ? (byte >> 4) : (byte & 0xF);
       y = (dd * (float)scv) * (float)q - dmin * (float)mv;
+    } else if (type == GGML_Q5_K) {
+      // Q4_K's scale / min unpack and nibble, fifth bit (qh[l] >> s) & 1
+      const uint8_t* blk = row + (size_t)(i / 256) * 176;
+      const uint32_t e = i % 256, s = e / 32, l = e % 32;
+      const float dd = h2f((uint16_t)(blk[0] | blk[1] << 8));
+      const float dmin = h2f((uint16_t)(blk[2] | blk[3] << 8));
+      const uint8_t* sc = blk + 4;
+      int scv, mv;
+      if (s < 4) { scv = sc[s] & 63; mv = sc[s + 4] & 63; }
+      else { scv = (sc[s + 4] & 0xF) | ((sc[s - 4] >> 6) << 4); mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4); }
+      const uint8_t byte = blk[48 + 32 * (s / 2) + l];
+      const uint32_t q = ((s & 1) ? (byte >> 4) : (byte & 0xF)) | (((blk[16 + l] >> s) & 1u) << 4);
+      y = (dd * (float)scv) * (float)q - dmin * (float)mv;
+    } else if (type == GGML_Q6_K) {
+      // element 128 n + 32 s + l: 6-bit q from ql / qh, d * scales[e / 16] * (q - 32)
+      const uint8_t* blk = row + (size_t)(i / 256) * 210;
+      const uint32_t e = i % 256, n = e / 128, s = (e % 128) / 32, l = e % 32;
+      const uint32_t lo = (blk[64 * n + 32 * (s & 1) + l] >> (4 * (s >> 1))) & 0xF;
+      const uint32_t hi = (blk[128 + 32 * n + l] >> (2 * s)) & 3;
+      const float dd = h2f((uint16_t)(blk[208] | blk[209] << 8));
+      y = dd * (float)(int8_t)blk[192 + e / 16] * (float)((int)(lo | hi << 4) - 32);
     } else if (type == GGML_Q8_0) {
       const uint8_t* blk = row + (size_t)(i / 32) * 34;
       y = h2f((uint16_t)(blk[0] | blk[1] << 8)) * (float)(int8_t)blk[2 + i % 32];

@@ -201,6 +201,7 @@ static void free_model(sh_model* m) {
     (void)hipFree(L.attn_norm);
     (void)hipFree(L.ffn_norm);
     sh_qmat_free(&L.wqkv);
+    sh_qmat_free(&L.wv);
     sh_qmat_free(&L.wo);
     sh_qmat_free(&L.wgu);
     sh_qmat_free(&L.wdown);
@@ -268,7 +269,6 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
     free_model(m);                      \
     SH_CHECK(false, code, __VA_ARGS__); \
   } while (0)
-  const uint32_t wtype = md.layers[0].wq.type;
   // embedding (raw rows for the gather)
   const TRef& te = md.tok_embd;
   m->embd_type = (int)te.type;
@@ -295,10 +295,16 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
     if (D.q_norm.present() &&
         ((fail = upload_f32(D.q_norm, &L.q_norm)) || (fail = upload_f32(D.k_norm, &L.k_norm))))
       FAIL(fail, "%s", sh_last_error());
+    // q and k share a type (checked by the reader); v joins them when its type matches
     const uint8_t* parts[3] = {D.wq.data, D.wk.data, D.wv.data};
     const uint32_t rows[3] = {m->q_dim, dkv, dkv};
-    if ((fail = sh_repack_upload_cat(e, (int)wtype, parts, rows, 3, m->d, &L.wqkv))) FAIL(fail, "%s", sh_last_error());
-    if ((fail = sh_repack_upload(e, (int)wtype, D.wo.data, m->d, m->q_dim, &L.wo))) FAIL(fail, "%s", sh_last_error());
+    const bool v_own = D.wv.type != D.wq.type;
+    if ((fail = sh_repack_upload_cat(e, (int)D.wq.type, parts, rows, v_own ? 2 : 3, m->d, &L.wqkv)))
+      FAIL(fail, "%s", sh_last_error());
+    if (v_own && (fail = sh_repack_upload(e, (int)D.wv.type, D.wv.data, dkv, m->d, &L.wv)))
+      FAIL(fail, "%s", sh_last_error());
+    if ((fail = sh_repack_upload(e, (int)D.wo.type, D.wo.data, m->d, m->q_dim, &L.wo)))
+      FAIL(fail, "%s", sh_last_error());
     if (m->n_expert) {
       const size_t rb = (size_t)m->n_expert * m->d * 4;
       if (hipMalloc(&L.router, rb) != hipSuccess ||
@@ -311,22 +317,31 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
         FAIL(fail, "%s", sh_last_error());
       m->alg_weight_bytes += L.wgu_exps.alg_bytes + L.wdown_exps.alg_bytes + 4.0 * m->n_expert * m->d;
     } else {
-      if ((fail = sh_repack_upload_gu(e, (int)wtype, D.gate.data, D.up.data, m->ff, m->d, &L.wgu)))
+      if ((fail = sh_repack_upload_gu(e, (int)D.gate.type, D.gate.data, D.up.data, m->ff, m->d, &L.wgu)))
         FAIL(fail, "%s", sh_last_error());
-      if ((fail = sh_repack_upload(e, (int)wtype, D.down.data, m->d, m->ff, &L.wdown)))
+      if ((fail = sh_repack_upload(e, (int)D.down.type, D.down.data, m->d, m->ff, &L.wdown)))
         FAIL(fail, "%s", sh_last_error());
     }
-    m->alg_weight_bytes += L.wqkv.alg_bytes + L.wo.alg_bytes + L.wgu.alg_bytes + L.wdown.alg_bytes + 8.0 * m->d;
+    m->alg_weight_bytes +=
+        L.wqkv.alg_bytes + L.wv.alg_bytes + L.wo.alg_bytes + L.wgu.alg_bytes + L.wdown.alg_bytes + 8.0 * m->d;
   }
   m->alg_weight_bytes += 4.0 * m->d;
   {
-    auto q4 = [](const QMat& q) { return q.type == GGML_Q4_K && q.K % 256 == 0; };
-    bool ok = q4(m->lm_head);
+    // multi-group path: every matrix a K-quant (the experts Q4_K); fused path
+    // (llama, <= 8 columns): the layers uniformly Q4_K or Q8_0, lm_head either
+    auto kq = [](const QMat& q) { return sh_is_kquant(q.type) && q.K % 256 == 0; };
+    bool ok = kq(m->lm_head);
     for (const Layer& L : m->layers)
-      ok = ok && q4(L.wqkv) && q4(L.wo) &&
-           (m->n_expert ? q4(L.wgu_exps) && q4(L.wdown_exps) : q4(L.wgu) && q4(L.wdown));
+      ok = ok && kq(L.wqkv) && (!L.wv.d || kq(L.wv)) && kq(L.wo) &&
+           (m->n_expert ? L.wgu_exps.type == GGML_Q4_K && L.wdown_exps.type == GGML_Q4_K : kq(L.wgu) && kq(L.wdown));
     m->mg_ok = ok;
-    if (m->arch != ARCH_LLAMA && !ok) FAIL(SH_ERR_UNSUPPORTED, "qwen models run on Q4_K matrices only");
+    bool fused = m->arch == ARCH_LLAMA && (m->lm_head.type == GGML_Q4_K || m->lm_head.type == GGML_Q8_0);
+    const int lt = m->layers[0].wqkv.type;
+    for (const Layer& L : m->layers)
+      fused = fused && !L.wv.d && L.wqkv.type == lt && L.wo.type == lt && L.wgu.type == lt && L.wdown.type == lt &&
+              (lt == GGML_Q4_K || lt == GGML_Q8_0);
+    m->fused_ok = fused;
+    if (!ok && !fused) FAIL(SH_ERR_UNSUPPORTED, "weight types: neither all K-quants nor uniform Q4_K / Q8_0 layers");
   }
   // workspace for up to SH_MAX_COLS columns per chunk (operands: 8 groups of 8)
   Workspace& w = m->ws;
@@ -340,8 +355,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   size_t gpart_floats = 0;
   for (const Layer& L : m->layers)
     gpart_floats = std::max({gpart_floats, sh_gemv_part_floats(L.wo), sh_gemv_part_floats(L.wgu),
-                             sh_gemv_part_floats(L.wdown), sh_gemm_part_floats(L.wqkv), sh_gemm_part_floats(L.wo),
-                             sh_gemm_part_floats(L.wgu), sh_gemm_part_floats(L.wdown)});
+                             sh_gemv_part_floats(L.wdown), sh_gemm_part_floats(L.wqkv) + sh_gemm_part_floats(L.wv),
+                             sh_gemm_part_floats(L.wo), sh_gemm_part_floats(L.wgu), sh_gemm_part_floats(L.wdown)});
   const size_t C = SH_MAX_COLS;
   if (dalloc(&w.resid, C * m->d) || dalloc(&w.resid2, C * m->d) || dalloc(&w.bx, bx_elems) ||
       dalloc(&w.xs, xs_elems) ||
@@ -831,6 +846,16 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     set_norm(pq);
     uint32_t nq = 0;
     if ((rc = sh_gemm_launch(e, L.wqkv, w.bx, w.xs, w.cs, nc, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
+    qc.vpart = nullptr;
+    if (L.wv.d) {  // v in a weight type of its own: its partials follow q / k's
+      EpiArgs pv = part_args(L.wv);
+      set_norm(pv);
+      pv.out = w.gpart + nq * pq.part_stride;
+      pv.part_cap = (uint32_t)((w.gpart_floats - nq * pq.part_stride) / pv.part_stride);
+      uint32_t nv = 0;
+      if ((rc = sh_gemm_launch(e, L.wv, w.bx, w.xs, w.cs, nc, EPI_PART, pv, "gemv_v", &nv))) return rc;
+      qc.vpart = pv.out; qc.vnparts = nv; qc.vldp = pv.ldo; qc.vstride = pv.part_stride;
+    }
     qkv.layer = l;
     rc = m->neox ? sh_qkv_finish_head_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc, L.q_norm, L.k_norm,
                                              m->eps, true)
@@ -874,13 +899,14 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
 }
 
 // Columns per forward chunk: SH_MAX_COLS when the multi-group path applies
-// (all matrices Q4_K) and there are more than 8 columns, else 8.
+// (all matrices K-quants) and takes the chunk (more than 8 columns, or a model
+// the fused path cannot run), else 8.
 static uint32_t chunk_cols(const sh_model* m, uint32_t n) {
   static const bool forced8 = [] {
     const char* s = getenv("SH_CHUNK");
     return s && atoi(s) == 8;
   }();
-  return (m->mg_ok && n > 8 && !forced8) ? SH_MAX_COLS : 8;
+  return (m->mg_ok && (n > 8 || !m->fused_ok) && !forced8) ? SH_MAX_COLS : 8;
 }
 
 // Longest attention segment on the multi-group path: SH_FA_MAX_ROWS query rows
@@ -892,7 +918,7 @@ static uint32_t fa_seg_cols(const sh_model* m) {
 
 static int run_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
                      const std::vector<FaSeg>& segs, bool want_logits, bool want_resid) {
-  return (nc > 8 || m->arch != ARCH_LLAMA) ? forward_chunk_mg(m, dev_tokens, nc, cols, segs, want_logits, want_resid)
+  return (nc > 8 || !m->fused_ok) ? forward_chunk_mg(m, dev_tokens, nc, cols, segs, want_logits, want_resid)
                                            : forward_chunk(m, dev_tokens, nc, cols, segs, want_logits, want_resid);
 }
 
@@ -956,8 +982,8 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
   const bool graph = kv->graph_base != nullptr;  // pos is an offset from *graph_base at replay
   SH_CHECK(graph || kv->pos == pos, SH_ERR_STATE,
            "cache.position %u doesn't match caller-supplied position_offset %u", kv->pos, pos);
-  SH_CHECK(!graph || (L <= 8 && !parents && m->arch == ARCH_LLAMA), SH_ERR_UNSUPPORTED,
-           "graph capture: llama chains of at most 8 columns");
+  SH_CHECK(!graph || (L <= 8 && !parents && m->fused_ok), SH_ERR_UNSUPPORTED,
+           "graph capture: chains of at most 8 columns on the fused (uniform Q4_K / Q8_0 llama) path");
   SH_CHECK(kv->n_layer == m->n_layer && kv->n_kv == m->n_kv && kv->hd == m->hd, SH_ERR_ARG,
            "KV cache dims do not match the model");
   SH_CHECK((uint64_t)pos + L <= kv->max_seq, SH_ERR_CAPACITY, "positions [%u, %u) exceed KV capacity %u", pos,
@@ -1110,7 +1136,7 @@ extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint
                                 uint32_t pos, uint32_t* sampled_out) {
   SH_CHECK(e && m && kv && sampled_out, SH_ERR_ARG, "sh_verify_greedy: NULL argument");
   SH_CHECK(L >= 1 && L <= 64, SH_ERR_ARG, "verify length %u outside [1, 64]", L);
-  if (L <= 8 && graphs_enabled(e) && m->arch == ARCH_LLAMA) {
+  if (L <= 8 && graphs_enabled(e) && m->fused_ok) {
     SH_CHECK(tokens, SH_ERR_ARG, "tokens is NULL");
     for (uint32_t i = 0; i < L; ++i)
       SH_CHECK(tokens[i] < m->V, SH_ERR_ARG, "token id %u out of range (vocab %u)", tokens[i], m->V);
@@ -1457,8 +1483,8 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
   hp[np] = last_token;
   SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
-  const bool greedy_graph = mode == SH_SAMPLE_GREEDY && n + 1 <= 8 && graphs_enabled(e) && tm->arch == ARCH_LLAMA &&
-                            dm->arch == ARCH_LLAMA;
+  const bool greedy_graph = mode == SH_SAMPLE_GREEDY && n + 1 <= 8 && graphs_enabled(e) && tm->fused_ok &&
+                            dm->fused_ok;
   if (mode == SH_SAMPLE_GREEDY) {
     const uint32_t d0 = dkv->pos;
     if (greedy_graph) {
@@ -1589,8 +1615,9 @@ extern "C" int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_d
   const uint32_t K = w->m.K, M = w->m.M;
   uint16_t *bx = nullptr, *xs = nullptr;
   float *cs = nullptr, *part = nullptr;
-  // Q4_K with more than 8 columns: the forward's multi-group kernel, 64 columns per pass
-  const bool mg = w->m.type == GGML_Q4_K && K % 256 == 0 && N > 8;
+  // Q4_K with more than 8 columns, and Q5_K / Q6_K at any width: the forward's
+  // multi-group kernel, 64 columns per pass
+  const bool mg = sh_is_kquant(w->m.type) && K % 256 == 0 && (N > 8 || w->m.type != GGML_Q4_K);
   const uint32_t CW = mg ? SH_MAX_COLS : 8, ngrp = CW / 8;
   const size_t bx_elems = ngrp * sh_grp_bx(K), xs_elems = ngrp * sh_grp_xs(K);
   const size_t part_floats = mg ? sh_gemm_part_floats(w->m) : sh_gemv_part_floats(w->m);

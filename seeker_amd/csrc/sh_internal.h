@@ -33,6 +33,12 @@
 constexpr int SH_TILE_ROWS = 16;
 constexpr int SH_Q4K_TILE_BYTES = 2304;  // 16 rows x 144 B, repacked
 constexpr int SH_Q8_TILE_BYTES = 544;    // 16 rows x 34 B, repacked
+constexpr int SH_Q5K_TILE_BYTES = 2816;  // 16 rows x 176 B, repacked
+constexpr int SH_Q6K_TILE_BYTES = 3360;  // 16 rows x 210 B, repacked
+// K-quants (256-element superblocks) that the multi-group GEMM decodes.
+__host__ __device__ constexpr bool sh_is_kquant(int type) {
+  return type == GGML_Q4_K || type == GGML_Q5_K || type == GGML_Q6_K;
+}
 constexpr uint32_t SH_MAX_COLS = 64;     // columns per forward chunk (8 operand groups of 8)
 constexpr uint32_t SH_MAX_PREP_COLS = 512;  // operand columns one prep builds (the MoE down operand: pairs)
 constexpr int SH_FA_MIN_SPLIT_KEYS = 64;  // smallest key split of any attention launch (sizes fa_part)
@@ -106,7 +112,8 @@ struct Layer {
   float* ffn_norm = nullptr;
   float* q_norm = nullptr;  // qwen3 / qwen3moe: per-head RMSNorm weights [hd]
   float* k_norm = nullptr;
-  QMat wqkv;  // rows [q | k | v]
+  QMat wqkv;  // rows [q | k | v], or [q | k] when v is in another weight type
+  QMat wv;    // v rows of their own (empty when they sit in wqkv)
   QMat wo;
   QMat wgu;   // tiles interleaved: gate tile t at 2t, up tile t at 2t+1
   QMat wdown;
@@ -177,7 +184,8 @@ struct sh_model {
   uint32_t rope_max = 0;
   Workspace ws;
   double alg_weight_bytes = 0;  // bytes of every matrix a full-logits forward reads
-  bool mg_ok = false;           // every matrix Q4_K: chunks above 8 columns take the multi-group path
+  bool mg_ok = false;     // every matrix a K-quant: the multi-group path can run any chunk
+  bool fused_ok = false;  // llama with uniform Q4_K / Q8_0 layers: chunks of <= 8 columns take the fused path
 };
 
 struct sh_kv {
@@ -310,6 +318,11 @@ struct QkvCols {  // per column: RoPE position, cache slot, capacity, K and V ca
   uint32_t mseq[SH_MAX_COLS];
   uint16_t* kc[SH_MAX_COLS];
   uint16_t* vc[SH_MAX_COLS];
+  // V rows from a matrix of their own (attn_v in another weight type than
+  // attn_q / attn_k): its split partials [split][col][row], row 0 = first v row
+  const float* vpart = nullptr;
+  uint32_t vnparts = 0, vldp = 0;
+  size_t vstride = 0;
 };
 int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
                          uint32_t N, const EpiArgs& ea, const QkvCols& qc);

@@ -42,6 +42,20 @@ def test_synthetic_config_images():
         assert abs(d.rope_freq_base - shape.rope_base) < 1e-3
 
 
+@pytest.mark.parametrize("kw", [dict(wtype=12, etype=12, out_type=14, mix=1), dict(wtype=13, etype=14, out_type=14,
+                                                                                  mix=1), dict(wtype=14, etype=13)],
+                         ids=["q4km", "q5km_q6k_embd", "q6k_q5k_embd"])
+def test_kquant_mix_images_accepted(kw):
+    """K-quant mixes (Q4_K_M / Q5_K_M-style: attn_v and ffn_down of even layers
+    and output in Q6_K; Q5_K / Q6_K token embeddings) are accepted."""
+    import dataclasses
+    shape = dataclasses.replace(S.LlamaShape(2, 512, 8, 4, 1024, 300, 512), **kw)
+    with S.GgufImage(shape, seed=1) as img:
+        rc, d, msg = inspect(bytes(img.bytes()))
+    assert rc == N.SH_OK, msg
+    assert (d.n_layer, d.n_embd, d.n_ff) == (2, 512, 1024)
+
+
 def _malformed():
     """(name, image bytes, expected status) for each malformed case."""
     cases = []
@@ -81,8 +95,12 @@ def _malformed():
     add("kv count beyond metadata", lambda im: setattr(im, "n_kv", 50))
     add("architecture", lambda im: im.set_meta("general.architecture", 8, "gpt9"), N.SH_ERR_UNSUPPORTED)
     add("negative eps", lambda im: im.set_meta("llama.attention.layer_norm_rms_epsilon", 6, -1.0))
-    add("mixed q/k/v types", lambda im: (setattr(im.tensor("blk.0.attn_k.weight"), "type", 12),
-                                         setattr(im.tensor("blk.0.attn_k.weight"), "ne", [256, 128])),
+    add("attn_q/k types differ", lambda im: (setattr(im.tensor("blk.0.attn_k.weight"), "type", 12),
+                                             setattr(im.tensor("blk.0.attn_k.weight"), "ne", [256, 128])),
+        N.SH_ERR_UNSUPPORTED)
+    # Q8_0 layers with one K-quant matrix: neither all K-quants (the multi-group
+    # path) nor uniform layers (the fused path)
+    add("Q8_0 layers with a Q6_K attn_v", lambda im: setattr(im.tensor("blk.0.attn_v.weight"), "type", 14),
         N.SH_ERR_UNSUPPORTED)
     add("extra metadata array", lambda im: im.set_meta("general.junk", 9, list(range(4))))
     return cases
