@@ -1461,11 +1461,12 @@ __global__ __launch_bounds__(128) void k_qkv_finish_head(const float* __restrict
   }
 }
 
-// ------------------------------------------------------------------ Q4_K expert-indirect
+// ------------------------------------------------------------------ K-quant expert-indirect
 
 // Expert-indirect GEMM of a routed MoE FFN (the MUL_MAT_ID matvec of
-// ops/moe.rs:164 / mul_mat_vec_q4_k.slang's id variant, here batched over the
-// columns routed to each expert): W holds E expert slabs of tiles_e row tiles.
+// ops/moe.rs:164 / the mul_mat_vec_q*_k shaders' id variant, here batched over
+// the columns routed to each expert), W in K-quant format F: E expert slabs of
+// tiles_e row tiles.
 // Chunk c of the routing plan, info[1 + 3c .. +3] = (expert e, first sorted
 // pair p0, n <= 8 pairs), multiplies slab e by the operand columns col[p]
 // (the pairs' input columns, gathered lane by lane from the operand groups;
@@ -1474,12 +1475,15 @@ __global__ __launch_bounds__(128) void k_qkv_finish_head(const float* __restrict
 // of 8 T tiles; workgroups past info[0] chunks exit at once. The superblock
 // pipeline (operand fragments staged in LDS by direct loads, two buffers) is
 // the multi-group kernel's with one gathered group.
-template <int T>
-__global__ __launch_bounds__(512) void k_moe_gemm_q4(const uint8_t* __restrict__ Wp, uint32_t tiles_e,
+template <class F, int T>
+__global__ __launch_bounds__(512) void k_moe_gemm_kq(const uint8_t* __restrict__ Wp, uint32_t tiles_e,
                                                       uint32_t nsb, uint32_t rb_e, const uint16_t* __restrict__ Bx,
                                                       const uint16_t* __restrict__ XS, const float* __restrict__ CS,
                                                       const uint32_t* __restrict__ info,
                                                       const uint32_t* __restrict__ gcol, EpiArgs ea) {
+  using Tile = typename F::Tile;
+  using Dec = typename F::Dec;
+  constexpr int NA = F::NA;
   __shared__ h8 sB[2][9 * 64];
   __shared__ float sC[2][64];
   const uint32_t chunk = blockIdx.x / rb_e, rb = blockIdx.x % rb_e;
@@ -1496,10 +1500,10 @@ __global__ __launch_bounds__(512) void k_moe_gemm_q4(const uint8_t* __restrict__
   const uint32_t col = gcol ? gcol[p0 + slot] : p0 + slot;
   const uint32_t cg = col / 8, cl = col % 8;
   const float nf = col_rinv_g(ea, cg, cl);
-  const uint8_t* We = Wp + (size_t)e * tiles_e * nsb * SH_Q4K_TILE_BYTES;
+  const uint8_t* We = Wp + (size_t)e * tiles_e * nsb * F::kTile;
 
   auto stage = [&](uint32_t sb, int buf) {
-    for (uint32_t fi = wave; fi < 9u; fi += 8) {
+    for (uint32_t fi = wave; fi < (F::kMin ? 9u : 8u); fi += 8) {
       const uint16_t* src;
       if (fi < 8) {
         src = Bx + cg * gB + ((size_t)(sb * 8 + fi) * 64 + 16 * g4 + cl + 8 * ((lane >> 3) & 1)) * 8;
@@ -1514,44 +1518,53 @@ __global__ __launch_bounds__(512) void k_moe_gemm_q4(const uint8_t* __restrict__
   };
   auto a_ptr = [&](int t, uint32_t sb) {
     const uint32_t tt = tile0 + t < tiles_e ? tile0 + t : tiles_e - 1;  // clamp keeps loads in the slab
-    return We + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
+    return We + ((size_t)tt * nsb + sb) * F::kTile;
   };
   f4 y[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) y[t] = f4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const Q4Tile (&at)[T], int buf) {
-    Q4Dec dec[T];
+  auto compute = [&](const Tile (&at)[T], int buf) {
+    Dec dec[T];
 #pragma unroll
-    for (int t = 0; t < T; ++t) dec[t] = q4_decode_setup(at[t]);
-    f4 acc[T];
+    for (int t = 0; t < T; ++t) dec[t] = F::setup(at[t]);
+    f4 acc[T][NA];
 #pragma unroll
-    for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int i = 0; i < NA; ++i) acc[t][i] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const h8 b = sB[buf][m * 64 + lane];
 #pragma unroll
-      for (int t = 0; t < T; ++t) acc[t] = mfma16(q4_frag(dec[t], m, magic), b, acc[t]);
+      for (int t = 0; t < T; ++t) {
+        h8 a[NA];
+        F::frag(dec[t], m, magic, a);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) acc[t][i] = mfma16(a[i], b, acc[t][i]);
+      }
     }
-    const h8 bm = sB[buf][8 * 64 + lane];
+    h8 bm;
+    if constexpr (F::kMin) bm = sB[buf][8 * 64 + lane];
     const float c = sC[buf][lane & 7];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const f4 macc = mfma16(q4_min_frag(dec[t], magic), bm, f4{0.f, 0.f, 0.f, 0.f});
+      f4 macc = f4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (F::kMin) macc = mfma16(F::min_frag(dec[t], magic), bm, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int j = 0; j < 4; ++j) y[t][j] = y[t][j] + c * (dec[t].d[j] * acc[t][j] - dec[t].dmin[j] * macc[j]);
+      for (int j = 0; j < 4; ++j) y[t][j] = y[t][j] + c * F::term(dec[t], acc[t], macc[j], j);
     }
   };
-  Q4Tile wa[T], wb[T];
+  Tile wa[T], wb[T];
   stage(0, 0);
 #pragma unroll
-  for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, 0), lane, g4, r);
+  for (int t = 0; t < T; ++t) wa[t] = F::load(a_ptr(t, 0), lane, g4, r);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (uint32_t sb = 0; sb < nsb; sb += 2) {
     if (sb + 1 < nsb) {
       stage(sb + 1, 1);
 #pragma unroll
-      for (int t = 0; t < T; ++t) wb[t] = load_q4_tile(a_ptr(t, sb + 1), lane, g4, r);
+      for (int t = 0; t < T; ++t) wb[t] = F::load(a_ptr(t, sb + 1), lane, g4, r);
     }
     compute(wa, 0);
     __builtin_amdgcn_s_waitcnt(0);
@@ -1560,7 +1573,7 @@ __global__ __launch_bounds__(512) void k_moe_gemm_q4(const uint8_t* __restrict__
     if (sb + 2 < nsb) {
       stage(sb + 2, 0);
 #pragma unroll
-      for (int t = 0; t < T; ++t) wa[t] = load_q4_tile(a_ptr(t, sb + 2), lane, g4, r);
+      for (int t = 0; t < T; ++t) wa[t] = F::load(a_ptr(t, sb + 2), lane, g4, r);
     }
     compute(wb, 1);
     __builtin_amdgcn_s_waitcnt(0);
@@ -2189,16 +2202,24 @@ int sh_qkv_finish_head_launch(sh_engine* e, const float* part, uint32_t nparts, 
 int sh_moe_gemm_launch(sh_engine* e, const QMat& w, uint32_t n_expert, const uint16_t* bx, const uint16_t* xs,
                        const float* cs, uint32_t max_chunks, const uint32_t* info, const uint32_t* gcol,
                        const EpiArgs& ea, const char* tag, double alg_bytes) {
-  SH_CHECK(w.type == GGML_Q4_K && w.K % 256 == 0 && n_expert >= 1 && w.tiles % n_expert == 0, SH_ERR_UNSUPPORTED,
-           "expert gemm needs Q4_K expert slabs of whole tiles");
+  SH_CHECK(sh_is_kquant(w.type) && w.K % 256 == 0 && n_expert >= 1 && w.tiles % n_expert == 0, SH_ERR_UNSUPPORTED,
+           "expert gemm needs K-quant expert slabs of whole tiles");
   SH_CHECK(ea.out && ea.ldo >= w.M / n_expert, SH_ERR_ARG, "expert gemm output");
   const uint32_t tiles_e = w.tiles / n_expert, nsb = w.K / 256;
   constexpr int T = 1;
   const uint32_t rb_e = (tiles_e + 8 * T - 1) / (8 * T);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL((k_moe_gemm_q4<T>), dim3(max_chunks * rb_e), dim3(512), 0, e->stream, w.d, tiles_e, nsb, rb_e,
-                     bx, xs, cs, info, gcol, ea);
+  const dim3 grid(max_chunks * rb_e);
+  if (w.type == GGML_Q5_K)
+    hipLaunchKernelGGL((k_moe_gemm_kq<FmtQ5K, T>), grid, dim3(512), 0, e->stream, w.d, tiles_e, nsb, rb_e, bx, xs, cs,
+                       info, gcol, ea);
+  else if (w.type == GGML_Q6_K)
+    hipLaunchKernelGGL((k_moe_gemm_kq<FmtQ6K, T>), grid, dim3(512), 0, e->stream, w.d, tiles_e, nsb, rb_e, bx, xs, cs,
+                       info, gcol, ea);
+  else
+    hipLaunchKernelGGL((k_moe_gemm_kq<FmtQ4K, T>), grid, dim3(512), 0, e->stream, w.d, tiles_e, nsb, rb_e, bx, xs, cs,
+                       info, gcol, ea);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, tag, alg_bytes, ev);
   return SH_OK;

@@ -288,8 +288,10 @@ int sh_gguf_describe(const GFile& f, ModelDesc* m) {
       SH_CHECK(L.gate_inp.type == GGML_F32 || matrix_type(L.gate_inp.type), SH_ERR_UNSUPPORTED,
                "layer %u: router type %u", l, L.gate_inp.type);
       for (const TRef* t : {&L.gate_exps, &L.up_exps, &L.down_exps})
-        SH_CHECK(t->type == GGML_Q4_K, SH_ERR_UNSUPPORTED, "layer %u: expert weights of type %u (Q4_K supported)", l,
-                 t->type);
+        SH_CHECK(sh_kquant_type(t->type), SH_ERR_UNSUPPORTED,
+                 "layer %u: expert weights of type %u (Q4_K / Q5_K / Q6_K supported)", l, t->type);
+      SH_CHECK(L.gate_exps.type == L.up_exps.type, SH_ERR_UNSUPPORTED, "layer %u: ffn_gate_exps / ffn_up_exps types differ",
+               l);
     } else {
       if ((rc = get_tensor(f, b + "ffn_gate.weight", m->d, m->ff, 1, true, &L.gate)) ||
           (rc = get_tensor(f, b + "ffn_up.weight", m->d, m->ff, 1, true, &L.up)) ||
@@ -311,8 +313,8 @@ int sh_gguf_describe(const GFile& f, ModelDesc* m) {
 
 // What the device path runs: the fused 8-column path takes llama models whose
 // layer matrices are uniformly Q4_K or uniformly Q8_0 (lm_head Q4_K or Q8_0);
-// the multi-group path takes any mix of K-quants (Q4_K / Q5_K / Q6_K, routed
-// experts Q4_K) for every architecture. token_embd may be any type the reader
+// the multi-group path takes any mix of K-quants (Q4_K / Q5_K / Q6_K, the
+// routed experts included) for every architecture. token_embd may be any type the reader
 // knows (the gather dequantizes rows).
 int sh_gguf_supported(const ModelDesc& m) {
   bool all_kq = sh_kquant_type(m.output.type), uniform = m.arch == ARCH_LLAMA;
@@ -321,7 +323,7 @@ int sh_gguf_supported(const ModelDesc& m) {
             (m.output.type == GGML_Q4_K || m.output.type == GGML_Q8_0);
   for (uint32_t l = 0; l < m.n_layer; ++l) {
     const LayerDesc& L = m.layers[l];
-    for (const TRef* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
+    for (const TRef* t : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down, &L.gate_exps, &L.up_exps, &L.down_exps})
       if (t->present()) {
         all_kq = all_kq && sh_kquant_type(t->type);
         uniform = uniform && t->type == wt;

@@ -1,7 +1,7 @@
 // Routed-expert (MoE) FFN of a qwen3moe layer: router + top-k, the routing
 // plan that groups (column, expert) pairs by expert, and the weighted sum of
 // the experts' outputs into the residual. The expert matrices themselves run
-// on the expert-indirect Q4_K GEMM (k_moe_gemm_q4 in gemv.hip).
+// on the expert-indirect K-quant GEMM (k_moe_gemm_kq in gemv.hip).
 //
 // Semantics follow the reference's MoE step (models/qwen35moe.rs:3117-3182,
 // ops/moe.rs, topk_moe.slang): softmax gating over the experts, the n_used

@@ -310,10 +310,11 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       if (hipMalloc(&L.router, rb) != hipSuccess ||
           hipMemcpy(L.router, D.gate_inp.data, rb, hipMemcpyHostToDevice) != hipSuccess)
         FAIL(SH_ERR_HIP, "router upload failed");
-      if ((fail = sh_repack_upload_gu(e, GGML_Q4_K, D.gate_exps.data, D.up_exps.data, m->n_expert * m->eff, m->d,
-                                      &L.wgu_exps)))
+      if ((fail = sh_repack_upload_gu(e, (int)D.gate_exps.type, D.gate_exps.data, D.up_exps.data,
+                                      m->n_expert * m->eff, m->d, &L.wgu_exps)))
         FAIL(fail, "%s", sh_last_error());
-      if ((fail = sh_repack_upload(e, GGML_Q4_K, D.down_exps.data, m->n_expert * m->d, m->eff, &L.wdown_exps)))
+      if ((fail = sh_repack_upload(e, (int)D.down_exps.type, D.down_exps.data, m->n_expert * m->d, m->eff,
+                                   &L.wdown_exps)))
         FAIL(fail, "%s", sh_last_error());
       m->alg_weight_bytes += L.wgu_exps.alg_bytes + L.wdown_exps.alg_bytes + 4.0 * m->n_expert * m->d;
     } else {
@@ -327,13 +328,13 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   }
   m->alg_weight_bytes += 4.0 * m->d;
   {
-    // multi-group path: every matrix a K-quant (the experts Q4_K); fused path
+    // multi-group path: every matrix a K-quant (the experts included); fused path
     // (llama, <= 8 columns): the layers uniformly Q4_K or Q8_0, lm_head either
     auto kq = [](const QMat& q) { return sh_is_kquant(q.type) && q.K % 256 == 0; };
     bool ok = kq(m->lm_head);
     for (const Layer& L : m->layers)
       ok = ok && kq(L.wqkv) && (!L.wv.d || kq(L.wv)) && kq(L.wo) &&
-           (m->n_expert ? L.wgu_exps.type == GGML_Q4_K && L.wdown_exps.type == GGML_Q4_K : kq(L.wgu) && kq(L.wdown));
+           (m->n_expert ? kq(L.wgu_exps) && kq(L.wdown_exps) : kq(L.wgu) && kq(L.wdown));
     m->mg_ok = ok;
     bool fused = m->arch == ARCH_LLAMA && (m->lm_head.type == GGML_Q4_K || m->lm_head.type == GGML_Q8_0);
     const int lt = m->layers[0].wqkv.type;

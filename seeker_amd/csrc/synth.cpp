@@ -285,7 +285,7 @@ typedef struct sh_synth_cfg {
   uint32_t tied;  // 1: no output.weight (lm_head = token_embd)
   uint64_t seed;
   uint32_t out_type;  // output.weight type (0: wtype)
-  uint32_t mix;       // 1: attn_v and ffn_down of even layers in Q6_K (the Q4_K_M-style mix)
+  uint32_t mix;       // 1: attn_v and ffn_down(_exps) of even layers in Q6_K (the Q4_K_M-style mix)
 } sh_synth_cfg;
 
 // Build a GGUF v3 image in host memory. *out is malloc'd; free with
@@ -323,7 +323,7 @@ int sh_synth_gguf(const sh_synth_cfg* c, uint8_t** out, uint64_t* size) {
       ts.push_back({p + "ffn_gate_inp.weight", d, E, 1, GT_F32, 2, 0, 0});
       ts.push_back({p + "ffn_gate_exps.weight", d, ef, E, wt, 0, 0, 0});
       ts.push_back({p + "ffn_up_exps.weight", d, ef, E, wt, 0, 0, 0});
-      ts.push_back({p + "ffn_down_exps.weight", ef, d, E, wt, 0, 0, 0});
+      ts.push_back({p + "ffn_down_exps.weight", ef, d, E, mt, 0, 0, 0});
     } else {
       ts.push_back({p + "ffn_gate.weight", d, ff, 1, wt, 0, 0, 0});
       ts.push_back({p + "ffn_up.weight", d, ff, 1, wt, 0, 0, 0});

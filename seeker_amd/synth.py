@@ -39,7 +39,7 @@ class LlamaShape:
     norm_jitter: float = 0.0  # norm weights 1 + jitter * N(0, 1) (0: all ones)
     router_std: float = 0.0   # f32 router weights N(0, router_std)
     out_type: int = 0         # output.weight type (0: wtype)
-    mix: int = 0              # 1: attn_v / ffn_down of even layers in Q6_K (Q4_K_M-style)
+    mix: int = 0              # 1: attn_v / ffn_down(_exps) of even layers in Q6_K (Q4_K_M-style)
 
 
 # tiny Llama target / 1-layer draft, Q8_0.

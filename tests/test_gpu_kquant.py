@@ -13,8 +13,9 @@ activation's hi + lo f16 split and f32 accumulation), argmax identical.
 
 Models: Q4_K_M-style (attn_v / ffn_down of even layers and output in Q6_K),
 Q5_K_M-style (Q5_K base, the same Q6_K layers), a qwen3 with a Q6_K token
-embedding tied as lm_head, and a qwen3moe (Q4_K experts) with Q6_K attn_v on
-even layers and a Q6_K lm_head. They run on the multi-group path at every
+embedding tied as lm_head, and a qwen3moe with Q6_K attn_v and
+ffn_down_exps on even layers (the expert-indirect GEMM in Q6_K) and a Q6_K
+lm_head. They run on the multi-group path at every
 chunk width; chunks of 1, 5, 8, 12 and 64 columns, a tree, greedy
 verification and greedy speculative steps are
 compared with the oracle (logits within 2e-2 abs / 1e-2 rel and 3e-4 x
