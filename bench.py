@@ -147,6 +147,14 @@ def measure_tree(eng, tm, d, P=8192, reps=3):
         if i:
             times.append((time.perf_counter() - t) * 1e3)
             plens += [len(x) for x in paths]
+    for c in caches:
+        c.set_position(P)
+    eng.set_profiling(True)
+    eng.profile(reset=True)
+    eng.tree_verify_step(tm, caches, tokens, par, qd, s)
+    prof = eng.profile(reset=True)
+    eng.set_profiling(False)
+    kern = {k: round(v["ms"], 4) for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
     qd.free()
     for c in caches:
         c.close()
@@ -155,9 +163,12 @@ def measure_tree(eng, tm, d, P=8192, reps=3):
     kv = B * 2 * d.n_layer * ((P + n) * dkv * 2 + n * dkv * 2)
     ms = statistics.median(times)
     log(f"tree verify step B={B} n={n} ctx {P}: {ms:.2f} ms, mean path {np.mean(plens):.2f} nodes")
+    for k, v in list(kern.items())[:10]:
+        log(f"  {k:16s} {v:8.3f} ms")
     return {"config": f"B={B}, tree 4x3x2 ({n} nodes), ctx {P}, REJECTION T=1.0 seed 11, synthetic draft logits",
             "ms": round(ms, 3), "alg_bytes": w + kv, "GBps": round((w + kv) / ms / 1e6, 1),
-            "frac": round((w + kv) / ms / 1e6 / HBM_PEAK_GBS, 4), "mean_path_nodes": round(float(np.mean(plens)), 3)}
+            "frac": round((w + kv) / ms / 1e6 / HBM_PEAK_GBS, 4), "mean_path_nodes": round(float(np.mean(plens)), 3),
+            "kernel_ms": kern}
 
 
 def measure_moe(eng, P=16384, B=8, L=7, reps=5):
@@ -233,6 +244,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel, tree and MoE lines")
     ap.add_argument("--moe-only", action="store_true", help="only the configs[4] MoE verify measurement")
+    ap.add_argument("--tree-only", action="store_true", help="only the configs[3] tree verify measurement")
     ap.add_argument("--profile-only", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -248,6 +260,14 @@ def main():
     if args.moe_only:
         with Engine(0) as eng:
             print(json.dumps({"metric": "moe verify step", "moe_verify": measure_moe(eng)}), flush=True)
+        return
+    if args.tree_only:
+        img = S.GgufImage(S.L8B_TARGET, seed=0)
+        with Engine(0) as eng:
+            tm = eng.upload_weights(img)
+            img.close()
+            print(json.dumps({"metric": "tree verify step", "tree_verify": measure_tree(eng, tm, tm.dims)}), flush=True)
+            tm.close()
         return
 
     t0 = time.time()

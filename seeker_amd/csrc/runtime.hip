@@ -217,10 +217,10 @@ static void free_model(sh_model* m) {
   (void)hipFree(m->rope);
   Workspace& w = m->ws;
   (void)hipFree(w.resid); (void)hipFree(w.resid2); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
-  (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part);
+  (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part); (void)hipFree(w.fab_part);
   (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq);
   (void)hipFree(w.bx2); (void)hipFree(w.xs2); (void)hipFree(w.cs2); (void)hipFree(w.ssq2); (void)hipFree(w.sb_cnt);
-  (void)hipFree(w.moe_ids); (void)hipFree(w.moe_wts); (void)hipFree(w.moe_info); (void)hipFree(w.moe_col);
+  (void)hipFree(w.moe_logits); (void)hipFree(w.moe_ids); (void)hipFree(w.moe_wts); (void)hipFree(w.moe_info); (void)hipFree(w.moe_col);
   (void)hipFree(w.moe_slot); (void)hipFree(w.moe_hgu); (void)hipFree(w.moe_bx); (void)hipFree(w.moe_xs);
   (void)hipFree(w.moe_cs); (void)hipFree(w.moe_y);
   delete m;
@@ -377,7 +377,7 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   if (m->n_expert) {
     const size_t P = C * m->n_used, ng = (P + 7) / 8;
     const size_t info = 1 + 3 * (size_t)sh_moe_max_chunks((uint32_t)P, m->n_expert);
-    if (dalloc(&w.moe_ids, P) || dalloc(&w.moe_wts, P) || dalloc(&w.moe_info, info) || dalloc(&w.moe_col, P) ||
+    if (dalloc(&w.moe_logits, C * m->n_expert) || dalloc(&w.moe_ids, P) || dalloc(&w.moe_wts, P) || dalloc(&w.moe_info, info) || dalloc(&w.moe_col, P) ||
         dalloc(&w.moe_slot, P) || dalloc(&w.moe_hgu, P * 2 * m->eff) || dalloc(&w.moe_bx, ng * sh_grp_bx(m->eff)) ||
         dalloc(&w.moe_xs, ng * sh_grp_xs(m->eff)) || dalloc(&w.moe_cs, ng * sh_grp_cs(m->eff)) ||
         dalloc(&w.moe_y, P * m->d))
@@ -560,7 +560,18 @@ struct FaSeg {
   uint32_t col0 = 0, ncol = 0, kvlen = 0, mask_base = 0;
   uint64_t colmask[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const uint64_t* masks = nullptr;  // device masks of the ncol columns (required above 8 columns)
+  const uint64_t* hmasks = nullptr;  // host masks of the ncol columns (live for the whole forward)
 };
+
+// SH_FAB=0: attention of the multi-group path per segment (k_fa / k_fa2 and
+// one combine per segment) instead of one batched launch per layer.
+static bool fab_enabled() {
+  static const bool v = [] {
+    const char* s = getenv("SH_FAB");
+    return !(s && std::string(s) == "0");
+  }();
+  return v;
+}
 
 // SH_FUSE=0 keeps the separate down prep and attention combine kernels.
 static bool fusion_enabled() {
@@ -780,9 +791,9 @@ static int moe_ffn(sh_model* m, const Layer& L, uint32_t nc) {
   Workspace& w = m->ws;
   const uint32_t k = m->n_used, P = nc * k, E = m->n_expert, mc = sh_moe_max_chunks(P, E);
   int rc;
-  if ((rc = sh_moe_route_launch(e, w.resid, L.ffn_norm, L.router, m->d, E, k, m->eps, nc, w.moe_ids, w.moe_wts)))
+  if ((rc = sh_moe_route_launch(e, w.resid, L.ffn_norm, L.router, m->d, E, m->eps, nc, w.moe_logits))) return rc;
+  if ((rc = sh_moe_plan_launch(e, w.moe_logits, nc, E, k, w.moe_ids, w.moe_wts, w.moe_info, w.moe_col, w.moe_slot)))
     return rc;
-  if ((rc = sh_moe_plan_launch(e, w.moe_ids, P, E, k, w.moe_info, w.moe_col, w.moe_slot))) return rc;
   EpiArgs gu;
   gu.out = w.moe_hgu; gu.ldo = 2 * m->eff; gu.rows = 2 * m->eff;
   gu.ssq = w.ssq; gu.ssq_n = (m->d + 255) / 256; gu.norm_K = m->d; gu.eps = m->eps;
@@ -840,6 +851,22 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     pending = 0;
     return sh_prep_launch(e, pr);
   };
+  // batched attention: one plan for the chunk's segments, one launch per layer
+  struct FabGuard {
+    sh_engine* e; FabLaunch fl;
+    ~FabGuard() { sh_fab_free(e, fl); }
+  } fab{e, FabLaunch{}};
+  bool use_fab = fab_enabled();
+  for (const FaSeg& sg : segs) use_fab = use_fab && sg.hmasks;
+  if (use_fab) {
+    std::vector<FabSegIn> fin(segs.size());
+    for (size_t i = 0; i < segs.size(); ++i) {
+      const FaSeg& sg = segs[i];
+      fin[i].kv = sg.kv; fin[i].col0 = sg.col0; fin[i].ncol = sg.ncol; fin[i].kvlen = sg.kvlen;
+      fin[i].mask_base = sg.mask_base; fin[i].hmasks = sg.hmasks;
+    }
+    if ((rc = sh_fab_plan(e, m, fin.data(), (uint32_t)fin.size(), nc, &fab.fl))) return rc;
+  }
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
     if ((rc = resid_prep(L.attn_norm))) return rc;
@@ -862,12 +889,16 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
                                              m->eps, true)
                  : sh_qkv_finish_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc);
     if (rc) return rc;
-    for (const FaSeg& sg : segs) {
-      FaArgs fa;
-      fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
-      for (uint32_t j = 0; j < sg.ncol && j < 8; ++j) fa.colmask[j] = sg.colmask[j];
-      fa.masks = sg.masks;
-      if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
+    if (use_fab) {
+      if ((rc = sh_fab_launch(e, m, fab.fl, l, w.q, w.attn, w.bx, w.xs, w.cs))) return rc;
+    } else {
+      for (const FaSeg& sg : segs) {
+        FaArgs fa;
+        fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
+        for (uint32_t j = 0; j < sg.ncol && j < 8; ++j) fa.colmask[j] = sg.colmask[j];
+        fa.masks = sg.masks;
+        if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
+      }
     }
     EpiArgs po = part_args(L.wo);
     if ((rc = sh_gemm_launch(e, L.wo, w.bx, w.xs, w.cs, nc, EPI_PART, po, "gemv_o", &pending))) return rc;
@@ -1016,6 +1047,7 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
         hmask[c0 + j0 + t] = mk;
         if (t < 8) sg.colmask[t] = mk;
       }
+      sg.hmasks = hmask.data() + c0 + j0;
       segs.push_back(sg);
     }
     chunk_segs.push_back(segs);
@@ -1244,6 +1276,7 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
         hmask[c0 + j + t] = mk;
         if (t < 8) sg.colmask[t] = mk;
       }
+      sg.hmasks = hmask.data() + c0 + j;
       segs.push_back(sg);
       j += n;
     }

@@ -142,6 +142,8 @@ struct Workspace {
   float* cs = nullptr;        // [max(K)/256][8] inverse activation scales of the current B operand
   float* ssq = nullptr;       // [max(K)/256][8] per-superblock sums of squares of the normalized input
   size_t fa_part_floats = 0;
+  float* fab_part = nullptr;  // batched attention partials of every segment of a chunk (grown on demand)
+  size_t fab_part_floats = 0;
   size_t gpart_floats = 0;
   // Second operand set, written by residual preps fused into the o / down GEMVs
   // (other workgroups of the producing kernel may still be staging the first):
@@ -154,6 +156,7 @@ struct Workspace {
   // routed-expert FFN (qwen3moe), P = columns x n_used pairs: router output,
   // routing plan, gate/up rows per sorted pair, down operand over the pairs
   // (P / 8 groups of K = expert_ff), down rows per sorted pair
+  float* moe_logits = nullptr;   // [cols][n_expert] router logits
   uint32_t* moe_ids = nullptr;   // [cols][n_used]
   float* moe_wts = nullptr;      // [cols][n_used]
   uint32_t* moe_info = nullptr;  // chunk table (count, then (expert, first pair, n) per chunk)
@@ -386,6 +389,36 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
                  float* attn_out, uint16_t* bx, uint16_t* xs, float* cs, OpndSrc* combine_out = nullptr);
 // With combine_out, the combine kernel is skipped and *combine_out describes
 // the partials for a consumer that combines them itself (OPND_FA).
+
+// Batched attention (attn_batch.hip): every segment of a forward chunk in one
+// launch per layer, then one combine launch. A segment is a run of one
+// sequence's columns with its own cache, key count and per-column masks.
+struct FabSegIn {
+  const sh_kv* kv = nullptr;
+  uint32_t col0 = 0, ncol = 0;    // chunk columns [col0, col0 + ncol)
+  uint32_t kvlen = 0;             // keys [0, kvlen) exist
+  uint32_t mask_base = 0;         // keys >= mask_base need their bit in the column mask
+  const uint64_t* hmasks = nullptr;  // host: ncol masks (bit i: key mask_base + i)
+};
+struct FabSeg {  // device descriptor of a segment
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint64_t* masks;  // ncol masks (device)
+  uint64_t part_off;      // floats into the partial buffer: [n_kv][nsplit * kp][rows_pad][hd + 4]
+  uint32_t max_seq, kvlen, mask_base, col0, ncol, rows_pad, nsplit;
+};
+struct FabLaunch {
+  uint8_t* dev = nullptr;  // device tables (segments, work items, column -> segment, masks)
+  const FabSeg* segs = nullptr;
+  const uint32_t* work = nullptr;    // (segment << 16 | key split) per workgroup
+  const uint32_t* colseg = nullptr;  // segment of each chunk column
+  float* part = nullptr;
+  uint32_t nseg = 0, nwork = 0, nc = 0, tps = 0, rgw = 1, kp = 1;
+};
+int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, uint32_t nc, FabLaunch* out);
+int sh_fab_launch(sh_engine* e, const sh_model* m, const FabLaunch& fl, uint32_t layer, const float* q, float* attn_out,
+                  uint16_t* bx, uint16_t* xs, float* cs);
+void sh_fab_free(sh_engine* e, FabLaunch& fl);
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids);
 // Draws one token per row from softmax(logits / T) by the vocab-order inverse
@@ -394,13 +427,14 @@ int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, 
 // 8192) row-statistics partials of scratch.
 int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
                           uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out);
-// Routed-expert FFN pieces (moe.hip): router + top-k per column (ids, wts
-// [N][k]), the routing plan over P = N k pairs, the weighted sum into resid.
+// Routed-expert FFN pieces (moe.hip): router logits [N][E] of the RMS-normed
+// columns, top-k per column (ids, wts [N][k]) with the routing plan over
+// P = N k pairs, the weighted sum into resid.
 uint32_t sh_moe_max_chunks(uint32_t P, uint32_t E);
 int sh_moe_route_launch(sh_engine* e, const float* x, const float* norm_w, const float* router, uint32_t d, uint32_t E,
-                        uint32_t k, float eps, uint32_t N, uint32_t* ids, float* wts);
-int sh_moe_plan_launch(sh_engine* e, const uint32_t* ids, uint32_t P, uint32_t E, uint32_t k, uint32_t* info,
-                       uint32_t* pair_col, uint32_t* slot_of);
+                        float eps, uint32_t N, float* logits);
+int sh_moe_plan_launch(sh_engine* e, const float* logits, uint32_t N, uint32_t E, uint32_t k, uint32_t* ids,
+                       float* wts, uint32_t* info, uint32_t* pair_col, uint32_t* slot_of);
 int sh_moe_combine_launch(sh_engine* e, const float* y, const uint32_t* slot_of, const float* wts, uint32_t k,
                           uint32_t d, uint32_t N, float* resid);
 // Acceptance of B sequences (COMPARE / REJECTION), see sh_accept_sample;

@@ -89,8 +89,12 @@ def test_unified_equals_separate_forwards(engine, model):
             for a, b in rows:
                 assert np.array_equal(a, b)
         else:
-            assert np.abs(out.logits[q:q + n] - lg).max() <= 1e-5 * np.abs(lg).max()
-            assert np.abs(out.residual[q:q + n] - res).max() <= 1e-5 * np.abs(res).max()
+            # different kernels: the 8-column path's attention (expf, one key
+            # block per wave, split combine) and the batched path's (exp2,
+            # 64-key tiles, other split boundaries) round differently; both
+            # stay within 3e-4 max of the oracle (test_unified_tree_and_chain_vs_oracle)
+            assert np.abs(out.logits[q:q + n] - lg).max() <= 5e-5 * np.abs(lg).max()
+            assert np.abs(out.residual[q:q + n] - res).max() <= 5e-5 * np.abs(res).max()
             for a, b in rows:
                 a, b = a.astype(np.float32), b.astype(np.float32)
                 assert np.abs(a - b).max() <= 2e-3 * max(np.abs(b).max(), 1e-3)
