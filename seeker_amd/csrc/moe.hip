@@ -12,41 +12,32 @@
 #include <algorithm>
 
 #include "sh_internal.h"
+#include "sh_operand.h"
 
 namespace {
 
 constexpr uint32_t kMaxExperts = 1024;
 
-// Orderable key: larger logit first, then the lower expert index; NaN loses.
-__device__ __forceinline__ unsigned long long route_key(float v, uint32_t e) {
-  if (v != v) return 0ull;
-  uint32_t b = __builtin_bit_cast(uint32_t, v);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((unsigned long long)b << 32) | (unsigned long long)(~e);
-}
-// The logit a (nonzero) key carries.
-__device__ __forceinline__ float key_logit(unsigned long long key) {
-  const uint32_t b = (uint32_t)(key >> 32);
-  return __builtin_bit_cast(float, (b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b);
-}
-
 // Router logits, one wave per (8 experts, CPW columns): logits[col][e] =
 // rinv(col) * sum_i R[e][i] (x[col][i] norm_w[i]), rinv = 1 / sqrt(mean(x^2) +
 // eps) (the RMSNorm factor is linear, so it is applied to the dot product).
 // Lane l holds elements 4 l + 256 j (j < d / 256) of each of the wave's
-// columns in registers; every router row is read as 16-byte loads and the
-// sums reduce across the wave. The whole launch spreads the router over
-// E / 8 x ceil(N / CPW) waves instead of one workgroup per column walking all
-// E rows.
+// columns in registers; router rows go two ahead of their use (16-byte loads),
+// and the sums reduce across the wave by DPP steps. The launch spreads the
+// router over E / 8 x ceil(N / CPW) waves.
 template <int NJ>
 __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ norm_w,
                                                    const float* __restrict__ R, uint32_t d, uint32_t E, uint32_t N,
                                                    float eps, float* __restrict__ logits) {
-  constexpr int CPW = 32 / NJ, EPW = 8;
+  constexpr int CPW = NJ <= 8 ? 32 / NJ : 1, EPW = 8;
   const uint32_t lane = threadIdx.x, nj = d / 256;
   const uint32_t e0 = blockIdx.x * EPW, c0 = blockIdx.y * CPW;
+  auto load_row = [&](float4 (&rv)[NJ], uint32_t e) {
+    const float* r = R + (size_t)min(e, E - 1) * d + 4 * lane;  // past the last expert: a clamped (unused) read
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) rv[j] = (uint32_t)j < nj ? *(const float4*)(r + 256 * j) : float4{0.f, 0.f, 0.f, 0.f};
+  };
   float4 xv[CPW][NJ];
-  float rinv[CPW];
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     const uint32_t col = c0 + c < N ? c0 + c : N - 1;  // past the last column: a clamped (unused) read
@@ -54,66 +45,59 @@ __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, 
 #pragma unroll
     for (int j = 0; j < NJ; ++j) xv[c][j] = (uint32_t)j < nj ? *(const float4*)(xc + 256 * j) : float4{0.f, 0.f, 0.f, 0.f};
   }
+  float4 rv[2][NJ];
+  load_row(rv[0], e0);
+  load_row(rv[1], e0 + 1);
+  float rinv[CPW];
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      ss = __builtin_fmaf(xv[c][j].x, xv[c][j].x, ss);
-      ss = __builtin_fmaf(xv[c][j].y, xv[c][j].y, ss);
-      ss = __builtin_fmaf(xv[c][j].z, xv[c][j].z, ss);
-      ss = __builtin_fmaf(xv[c][j].w, xv[c][j].w, ss);
-    }
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-    rinv[c] = 1.0f / sqrtf(ss / (float)d + eps);
+    for (int j = 0; j < NJ; ++j) ss += sh_sq4(xv[c][j]);
+    rinv[c] = 1.0f / sqrtf(sh_wave_sum(ss) / (float)d + eps);
   }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    if ((uint32_t)j >= nj) break;
-    const float4 w = *(const float4*)(norm_w + 4 * lane + 256 * j);
+    const float4 w = (uint32_t)j < nj ? *(const float4*)(norm_w + 4 * lane + 256 * j) : float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       xv[c][j].x *= w.x; xv[c][j].y *= w.y; xv[c][j].z *= w.z; xv[c][j].w *= w.w;
     }
   }
-  // Experts in pairs, both pairs' rows in flight before the first sums.
 #pragma unroll
-  for (int ep = 0; ep < EPW; ep += 2) {
-    float4 rv[2][NJ];
+  for (int ei = 0; ei < EPW; ++ei) {
+    const int b = ei & 1;
+    float acc[CPW];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t e = min(e0 + ep + h, E - 1);  // past the last expert: a clamped (unused) read
-      const float* r = R + (size_t)e * d + 4 * lane;
+    for (int c = 0; c < CPW; ++c) {
+      float a = 0.f;
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        rv[h][j] = (uint32_t)j < nj ? *(const float4*)(r + 256 * j) : float4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int c = 0; c < CPW; ++c) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          acc = __builtin_fmaf(rv[h][j].x, xv[c][j].x, acc);
-          acc = __builtin_fmaf(rv[h][j].y, xv[c][j].y, acc);
-          acc = __builtin_fmaf(rv[h][j].z, xv[c][j].z, acc);
-          acc = __builtin_fmaf(rv[h][j].w, xv[c][j].w, acc);
-        }
-        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-        const uint32_t e = e0 + ep + h;
-        if (lane == 0 && c0 + c < N && e < E) logits[(size_t)(c0 + c) * E + e] = acc * rinv[c];
+      for (int j = 0; j < NJ; ++j) {
+        a = __builtin_fmaf(rv[b][j].x, xv[c][j].x, a);
+        a = __builtin_fmaf(rv[b][j].y, xv[c][j].y, a);
+        a = __builtin_fmaf(rv[b][j].z, xv[c][j].z, a);
+        a = __builtin_fmaf(rv[b][j].w, xv[c][j].w, a);
       }
+      acc[c] = a;
+    }
+    if (ei + 2 < EPW) load_row(rv[b], e0 + ei + 2);
+    const uint32_t e = e0 + ei;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const float sum = sh_wave_sum(acc[c]);
+      if (lane == 0 && c0 + c < N && e < E) logits[(size_t)(c0 + c) * E + e] = sum * rinv[c];
+    }
   }
 }
 
-// Top-k selection and routing plan in one workgroup of 512 threads for
+// Top-k selection and routing plan in one workgroup of 1024 threads for
 // P = N k <= 512 (column, slot) pairs.
-//  * Top-k: wave w takes columns w, w + 8, ...; lane l holds logits l, l + 64,
-//    ...; k rounds pick the largest remaining logit (softmax is monotone, so
-//    this is the top-k of the probabilities; ties to the lower expert index)
-//    and the weights exp(l_j - l_max) / sum over the selection in f64 (the
-//    full softmax denominator cancels in the renormalization).
+//  * Top-k: wave w takes columns w, w + 16, ...; lane l holds logits l, l + 64,
+//    ...; k rounds pick the largest remaining logit (a DPP wave max, then the
+//    lowest expert index holding it by ballot; softmax is monotone, so this is
+//    the top-k of the probabilities, ties to the lower expert index), and the
+//    weights exp(l_j - l_max) / sum over the selection in f64 (the full
+//    softmax denominator cancels in the renormalization).
 //  * Plan: pair p = column * k + slot has expert ids[p]. Pairs are sorted by
 //    expert, within an expert by p: a bitmap of pairs per expert gives each
 //    pair's rank by population counts, a wave scan over the experts their
@@ -122,7 +106,7 @@ __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, 
 //    info[0] = number of chunks, info[1 + 3c .. +3] = (expert, first sorted
 //    pair, count), chunks in expert order.
 template <int RL>
-__global__ __launch_bounds__(512) void k_moe_plan(const float* __restrict__ logits, uint32_t N, uint32_t E,
+__global__ __launch_bounds__(1024) void k_moe_plan(const float* __restrict__ logits, uint32_t N, uint32_t E,
                                                   uint32_t k, uint32_t* __restrict__ ids, float* __restrict__ wts,
                                                   uint32_t* __restrict__ info, uint32_t* __restrict__ pair_col,
                                                   uint32_t* __restrict__ slot_of) {
@@ -132,46 +116,73 @@ __global__ __launch_bounds__(512) void k_moe_plan(const float* __restrict__ logi
   __shared__ uint32_t cnt[kMaxExperts], off[kMaxExperts], cbase[kMaxExperts];
   const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint32_t P = N * k, nw = (P + 31) / 32;
-  for (uint32_t i = t; i < E * NW; i += 512) bm[i] = 0u;
-  for (uint32_t col = wave; col < N; col += 8) {
-    const float* lg = logits + (size_t)col * E;
+  for (uint32_t i = t; i < E * NW; i += 1024) bm[i] = 0u;
+  for (uint32_t cb = wave; cb < N; cb += 64) {  // the wave's next 4 columns cb + 16 i: loads issued together
+    float pre[4][RL];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+      for (uint32_t r = 0; r < RL; ++r) {
+        const uint32_t col = cb + 16 * i;
+        pre[i][r] = col < N && lane + 64 * r < E ? logits[(size_t)col * E + lane + 64 * r] : -INFINITY;
+      }
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t col = cb + 16 * i;
+    if (col >= N) break;
+    // lane l holds experts l, l + 64, ...; NaN ranks as -inf
     float lv[RL];
+    bool taken[RL];
 #pragma unroll
-    for (uint32_t r = 0; r < RL; ++r) lv[r] = lane + 64 * r < E ? lg[lane + 64 * r] : -INFINITY;
-    float lmax = 0.f;
-    double wsel = 0.0, wsum = 0.0;  // lane j keeps selection j's weight
-    for (uint32_t j = 0; j < k; ++j) {
-      unsigned long long best = 0ull;
-#pragma unroll
-      for (uint32_t r = 0; r < RL; ++r)
-        if (lane + 64 * r < E) {
-          const unsigned long long key = lv[r] == -INFINITY ? 0ull : route_key(lv[r], lane + 64 * r);
-          best = key > best ? key : best;
-        }
-      for (int o = 32; o >= 1; o >>= 1) {
-        const unsigned long long ob = __shfl_xor(best, o);
-        best = ob > best ? ob : best;
-      }
-      const uint32_t e = best ? ~(uint32_t)(best & 0xFFFFFFFFull) : 0u;
-      const float l = best ? key_logit(best) : lg[e];  // no key: every logit NaN or -inf (expert 0)
-      if (j == 0) lmax = l;
-#pragma unroll
-      for (uint32_t r = 0; r < RL; ++r)
-        if (lane + 64 * r == e) lv[r] = -INFINITY;
-      const double w = exp((double)l - (double)lmax);
-      wsum += w;
-      if (lane == j) wsel = w;
-      if (lane == 0) {
-        ids[(size_t)col * k + j] = e;
-        sid[col * k + j] = min(e, E - 1);
-      }
+    for (uint32_t r = 0; r < RL; ++r) {
+      const float v = pre[i][r];
+      lv[r] = v != v ? -INFINITY : v;
+      taken[r] = lane + 64 * r >= E;
     }
-    if (lane < k) wts[(size_t)col * k + lane] = (float)(wsel / wsum);
+    // round j: the largest value not yet taken (DPP wave max), then the lowest
+    // expert index holding it (ballots, lowest r first); lane j keeps it
+    uint32_t sel_e = 0;
+    float sel_l = 0.f;
+    for (uint32_t j = 0; j < k; ++j) {
+      float lm = -INFINITY;
+#pragma unroll
+      for (uint32_t r = 0; r < RL; ++r) lm = taken[r] ? lm : fmaxf(lm, lv[r]);
+      const float m = sh_wave_max(lm);
+      uint32_t e = 0;
+      bool found = false;
+#pragma unroll
+      for (uint32_t r = 0; r < RL; ++r) {
+        const unsigned long long b = __ballot(!taken[r] && lv[r] == m);
+        if (!found && b) {
+          e = 64 * r + (uint32_t)__ffsll((long long)b) - 1;
+          found = true;
+        }
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < RL; ++r) taken[r] = taken[r] || lane + 64 * r == e;
+      if (lane == j) { sel_e = e; sel_l = m; }
+    }
+    // weights exp(l_j - l_0) / sum_j exp(l_j - l_0) in f64, summed in selection order
+    const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sel_l)));
+    const double w = lane < k ? exp((double)sel_l - (double)l0) : 0.0;
+    double wsum = 0.0;
+    for (uint32_t j = 0; j < k; ++j) {  // lane j's weight, read lane by lane (uniform j)
+      const unsigned long long wb = __builtin_bit_cast(unsigned long long, w);
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)wb, (int)j);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(wb >> 32), (int)j);
+      wsum += __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+    }
+    if (lane < k) {
+      ids[(size_t)col * k + lane] = sel_e;
+      wts[(size_t)col * k + lane] = (float)(w / wsum);
+      sid[col * k + lane] = min(sel_e, E - 1);
+    }
+  }
   }
   __syncthreads();
   if (t < P) atomicOr(&bm[sid[t] * NW + (t >> 5)], 1u << (t & 31));
   __syncthreads();
-  for (uint32_t x = t; x < E; x += 512) {
+  for (uint32_t x = t; x < E; x += 1024) {
     uint32_t n = 0;
     for (uint32_t w = 0; w < nw; ++w) n += __popc(bm[x * NW + w]);
     cnt[x] = n;
@@ -206,7 +217,7 @@ __global__ __launch_bounds__(512) void k_moe_plan(const float* __restrict__ logi
     pair_col[s] = t / k;
     slot_of[t] = s;
   }
-  for (uint32_t x = t; x < E; x += 512) {
+  for (uint32_t x = t; x < E; x += 1024) {
     const uint32_t n = cnt[x];
     for (uint32_t c = 0; 8 * c < n; ++c) {
       uint32_t* o = info + 1 + 3 * (cbase[x] + c);
@@ -242,12 +253,12 @@ int sh_moe_route_launch(sh_engine* e, const float* x, const float* norm_w, const
            "moe route: n_embd %u (a multiple of 256 up to 4096)", d);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  if (d <= 2048)
+  if (d <= 2048)  // 4 columns per wave
     hipLaunchKernelGGL(k_moe_logits<8>, dim3((E + 7) / 8, (N + 3) / 4), dim3(64), 0, e->stream, x, norm_w, router, d,
                        E, N, eps, logits);
-  else
-    hipLaunchKernelGGL(k_moe_logits<16>, dim3((E + 7) / 8, (N + 1) / 2), dim3(64), 0, e->stream, x, norm_w, router,
-                       d, E, N, eps, logits);
+  else  // 1 column per wave
+    hipLaunchKernelGGL(k_moe_logits<16>, dim3((E + 7) / 8, N), dim3(64), 0, e->stream, x, norm_w, router, d, E, N,
+                       eps, logits);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "moe_route", 4.0 * E * d, ev);
   return SH_OK;
@@ -260,13 +271,13 @@ int sh_moe_plan_launch(sh_engine* e, const float* logits, uint32_t N, uint32_t E
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   if (E <= 128)
-    hipLaunchKernelGGL(k_moe_plan<2>, dim3(1), dim3(512), 0, e->stream, logits, N, E, k, ids, wts, info, pair_col,
+    hipLaunchKernelGGL(k_moe_plan<2>, dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info, pair_col,
                        slot_of);
   else if (E <= 256)
-    hipLaunchKernelGGL(k_moe_plan<4>, dim3(1), dim3(512), 0, e->stream, logits, N, E, k, ids, wts, info, pair_col,
+    hipLaunchKernelGGL(k_moe_plan<4>, dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info, pair_col,
                        slot_of);
   else
-    hipLaunchKernelGGL(k_moe_plan<kMaxExperts / 64>, dim3(1), dim3(512), 0, e->stream, logits, N, E, k, ids, wts,
+    hipLaunchKernelGGL(k_moe_plan<kMaxExperts / 64>, dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts,
                        info, pair_col, slot_of);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "moe_plan", 0.0, ev);

@@ -573,6 +573,22 @@ static bool fab_enabled() {
   return v;
 }
 
+struct FabGuard {  // a chunk's batched-attention plan, freed (stream-ordered) at scope end
+  sh_engine* e;
+  FabLaunch fl;
+  ~FabGuard() { sh_fab_free(e, fl); }
+};
+
+static int plan_fab(sh_model* m, const std::vector<FaSeg>& segs, uint32_t nc, FabGuard* g) {
+  std::vector<FabSegIn> fin(segs.size());
+  for (size_t i = 0; i < segs.size(); ++i) {
+    const FaSeg& sg = segs[i];
+    fin[i].kv = sg.kv; fin[i].col0 = sg.col0; fin[i].ncol = sg.ncol; fin[i].kvlen = sg.kvlen;
+    fin[i].mask_base = sg.mask_base; fin[i].hmasks = sg.hmasks;
+  }
+  return sh_fab_plan(m->e, m, fin.data(), (uint32_t)fin.size(), nc, &g->fl);
+}
+
 // SH_FUSE=0 keeps the separate down prep and attention combine kernels.
 static bool fusion_enabled() {
   static const bool v = [] {
@@ -852,21 +868,10 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     return sh_prep_launch(e, pr);
   };
   // batched attention: one plan for the chunk's segments, one launch per layer
-  struct FabGuard {
-    sh_engine* e; FabLaunch fl;
-    ~FabGuard() { sh_fab_free(e, fl); }
-  } fab{e, FabLaunch{}};
+  FabGuard fab{e, FabLaunch{}};
   bool use_fab = fab_enabled();
   for (const FaSeg& sg : segs) use_fab = use_fab && sg.hmasks;
-  if (use_fab) {
-    std::vector<FabSegIn> fin(segs.size());
-    for (size_t i = 0; i < segs.size(); ++i) {
-      const FaSeg& sg = segs[i];
-      fin[i].kv = sg.kv; fin[i].col0 = sg.col0; fin[i].ncol = sg.ncol; fin[i].kvlen = sg.kvlen;
-      fin[i].mask_base = sg.mask_base; fin[i].hmasks = sg.hmasks;
-    }
-    if ((rc = sh_fab_plan(e, m, fin.data(), (uint32_t)fin.size(), nc, &fab.fl))) return rc;
-  }
+  if (use_fab && (rc = plan_fab(m, segs, nc, &fab))) return rc;
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
     if ((rc = resid_prep(L.attn_norm))) return rc;
