@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "sh_internal.h"
+#include "sh_dma.h"
 #include "sh_operand.h"
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -62,23 +63,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// One wave's 16-byte-per-lane direct load global -> LDS (lane l writes
-// lds + 16 l). Issued as inline asm so the compiler's wait insertion does not
-// treat it as an LDS write (it would drain every load in flight, the prefetch
-// included, before each LDS read); the kernel waits for these loads itself
-// (s_waitcnt vmcnt) before the barrier that publishes a buffer. The compiler
-// cannot count them, so its own waits for other loads only come out stricter.
-// M0 is written here without the compiler's knowledge (it warns that a
-// reserved register is clobbered): the kernels of this file make no other use
-// of M0 (checked in their gfx950 assembly), so nothing live is overwritten.
-__device__ __forceinline__ void dma16(const uint16_t* src, const uint16_t* lds) {
-  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)lds;
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(a) : "memory", "m0");
-#pragma clang diagnostic pop
 }
 
 constexpr int kTK = 64;     // keys per tile
@@ -129,14 +113,14 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
       const int qc = 64 * i + lane, row = qc / CPR, c = qc % CPR;
       const uint32_t key = min(key0 + (uint32_t)row, max_seq - 1);  // past the cache: in bounds, masked
       const uint16_t* src = kb + (size_t)key * HD + 8 * (c ^ (row % CPR));
-      dma16(src, &sK[512 * i]);
+      sh_dma16(src, &sK[512 * i]);
     }
 #pragma unroll
     for (int i = wave; i < VI; i += kWaves) {
       const int qc = 64 * i + lane, c = qc & 3, dra = qc >> 2, blk = dra / HD, dr = dra % HD;
       const uint32_t vblk = min(key0 / 32 + (uint32_t)blk, max_seq / 32 - 1);
       const uint16_t* src = vb + ((size_t)vblk * HD + dr) * 32 + 8 * (c ^ ((dr >> 2) & 3));
-      dma16(src, &sV[512 * i]);
+      sh_dma16(src, &sV[512 * i]);
     }
   };
   issue(0u, std::integral_constant<int, 0>{});
@@ -203,7 +187,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
     // flight on every path, the compiler's own waits before the LDS reads stay
     // at NLD instead of draining the prefetch.
     issue(t + 1 < ntiles ? t + 1 : t, std::integral_constant<int, 1 - buf>{});
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD) : "memory");
+    sh_wait_vm<NLD>();
     lds_barrier();
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
@@ -293,7 +277,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
     step(t, std::integral_constant<int, 0>{});
     if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write may land after the workgroup ends
+  sh_wait_vm<0>();  // no LDS write may land after the workgroup ends
 
   const uint32_t nsv = sg.nsplit * KP, vs = split * KP + kp;
   float* pbase = part + sg.part_off + ((size_t)kh * nsv + vs) * sg.rows_pad * PS;

@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "sh_internal.h"
+#include "sh_dma.h"
 #include "sh_operand.h"
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -36,6 +37,15 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
 struct alignas(16) u32x4 { uint32_t x, y, z, w; };
+
+// An opaque use of loaded registers: the compiler must finish their loads
+// here. The double-buffered GEMMs pin the first tile before their loop: the
+// compiler may sink those loads below the preamble's wait, and at the loop
+// head, after the asm stage loads it cannot count, it would then wait for
+// every load in flight (the prefetch included) before the first use.
+__device__ __forceinline__ void pin32(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin32(u32x4& v) { pin32(v.x); pin32(v.y); pin32(v.z); pin32(v.w); }
+__device__ __forceinline__ void pin32(uint2& v) { pin32(v.x); pin32(v.y); }
 
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -318,6 +328,7 @@ __device__ __forceinline__ void swiglu4(const EpiArgs& ea, uint32_t pair, uint32
 struct Q4Tile {
   u32x4 q0, q1, dd;
   uint32_t s0, s1, s2;
+  __device__ void pin() { pin32(q0); pin32(q1); pin32(dd); pin32(s0); pin32(s1); pin32(s2); }
 };
 
 __device__ __forceinline__ Q4Tile load_q4_tile(const uint8_t* base, int lane, int g, int r) {
@@ -1027,6 +1038,7 @@ struct Q5Tile {
   u32x4 q0, q1, dd;
   uint32_t h0, h1;
   uint32_t s0, s1, s2;
+  __device__ void pin() { pin32(q0); pin32(q1); pin32(dd); pin32(h0); pin32(h1); pin32(s0); pin32(s1); pin32(s2); }
 };
 struct Q5Dec {
   uint32_t w[8], h[2];
@@ -1098,6 +1110,7 @@ __device__ __forceinline__ h8 q5_min_frag(const Q5Dec& s, uint32_t magic) {
 struct Q6Tile {
   u32x4 q0, q1, h;
   uint2 sc, d;
+  __device__ void pin() { pin32(q0); pin32(q1); pin32(h); pin32(sc); pin32(d); }
 };
 struct Q6Dec {
   uint32_t w[8], h[4];
@@ -1266,12 +1279,11 @@ __global__ __launch_bounds__(512) void k_gemm_kq(const uint8_t* __restrict__ Wp,
       if (!F::kMin && f == 8) continue;
       const uint16_t* src = f < 8 ? Bx + g * gB + ((size_t)(sb * 8 + f) * 64 + lane) * 8
                                   : XS + g * gX + ((size_t)sb * 64 + lane) * 8;
-      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&sB[buf][fi * 64]), 16, 0, 0);
+      sh_dma16(src, &sB[buf][fi * 64]);
     }
     if (wave == 7) {  // the G * 8 scales (lanes past them repeat the last)
       const uint32_t li = (uint32_t)lane < (uint32_t)(G * 8) ? (uint32_t)lane : G * 8 - 1;
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(CS + (li / 8) * gC + sb * 8 + li % 8), (lds_void_t*)sC[buf],
-                                       4, 0, 0);
+      sh_dma4(CS + (li / 8) * gC + sb * 8 + li % 8, sC[buf]);
     }
   };
   auto a_ptr = [&](int t, uint32_t sb) {
@@ -1337,6 +1349,8 @@ __global__ __launch_bounds__(512) void k_gemm_kq(const uint8_t* __restrict__ Wp,
   for (int t = 0; t < T; ++t) wa[t] = F::load(a_ptr(t, sb0), lane, g4, r);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+#pragma unroll
+  for (int t = 0; t < T; ++t) wa[t].pin();
   for (uint32_t sb = sb0; sb < sb1; sb += 2) {
     if (sb + 1 < sb1) {
       stage(sb + 1, 1);
@@ -1511,10 +1525,10 @@ __global__ __launch_bounds__(512) void k_moe_gemm_kq(const uint8_t* __restrict__
         const uint32_t ls = lane < 16 ? cl + 8 * ((lane >> 3) & 1) : (uint32_t)lane;
         src = XS + cg * gX + ((size_t)sb * 64 + ls) * 8;
       }
-      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(&sB[buf][fi * 64]), 16, 0, 0);
+      sh_dma16(src, &sB[buf][fi * 64]);
     }
     if (wave == 7)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(CS + cg * gC + sb * 8 + cl), (lds_void_t*)sC[buf], 4, 0, 0);
+      sh_dma4(CS + cg * gC + sb * 8 + cl, sC[buf]);
   };
   auto a_ptr = [&](int t, uint32_t sb) {
     const uint32_t tt = tile0 + t < tiles_e ? tile0 + t : tiles_e - 1;  // clamp keeps loads in the slab
@@ -1560,6 +1574,8 @@ __global__ __launch_bounds__(512) void k_moe_gemm_kq(const uint8_t* __restrict__
   for (int t = 0; t < T; ++t) wa[t] = F::load(a_ptr(t, 0), lane, g4, r);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+#pragma unroll
+  for (int t = 0; t < T; ++t) wa[t].pin();
   for (uint32_t sb = 0; sb < nsb; sb += 2) {
     if (sb + 1 < nsb) {
       stage(sb + 1, 1);
