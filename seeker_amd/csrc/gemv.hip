@@ -1308,19 +1308,29 @@ __global__ __launch_bounds__(512) void k_gemm_kq(const uint8_t* __restrict__ Wp,
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int i = 0; i < NA; ++i) acc[t][g][i] = f4{0.f, 0.f, 0.f, 0.f};
+    // B fragments one sub-block ahead in registers (the G reads of sub-block
+    // m + 1, or the minimum term's after the last, go out before sub-block
+    // m's MFMAs): without this each MFMA waited on the LDS read just before it
+    h8 bb[2][G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) bb[0][g] = sB[buf][(g * 9) * 64 + lane];
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
+      const int cur = m & 1;
+      if (m < 7 || F::kMin) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) bb[cur ^ 1][g] = sB[buf][(g * 9 + m + 1) * 64 + lane];
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this sub-block's MFMAs
       h8 a[T][NA];
 #pragma unroll
       for (int t = 0; t < T; ++t) F::frag(dec[t], m, magic, a[t]);
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const h8 b = sB[buf][(g * 9 + m) * 64 + lane];
+      for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
-          for (int i = 0; i < NA; ++i) acc[t][g][i] = mfma16(a[t][i], b, acc[t][g][i]);
-      }
+          for (int i = 0; i < NA; ++i) acc[t][g][i] = mfma16(a[t][i], bb[cur][g], acc[t][g][i]);
     }
     h8 am[T];
     if constexpr (F::kMin) {
@@ -1329,8 +1339,7 @@ __global__ __launch_bounds__(512) void k_gemm_kq(const uint8_t* __restrict__ Wp,
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      h8 bm;
-      if constexpr (F::kMin) bm = sB[buf][(g * 9 + 8) * 64 + lane];
+      const h8 bm = bb[0][g];  // the minimum term's fragment (read during sub-block 7)
       const float c = sC[buf][g * 8 + (lane & 7)];
 #pragma unroll
       for (int t = 0; t < T; ++t) {
@@ -2111,15 +2120,18 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
 // The splits depend on the matrix only, never on the column count, so a
 // column's arithmetic (superblock order within a split, split order in the
 // sum) is the same in every multi-group launch: the fewest splits (at most 16)
-// whose workgroup count at T = 2 fills the 256 CUs to at least 70 % in its last
-// round (one workgroup per CU: up to 148 KB of LDS).
+// whose workgroup count at T = 1 (8 row tiles per workgroup, the launches of
+// more than 32 columns) fills the 256 CUs to at least 70 % in its last round
+// (one workgroup per CU: up to 148 KB of LDS). Every split costs a round trip
+// of [columns][rows] f32 partials through HBM; at 64 columns that outweighs
+// the CU fill the T = 2 launches (at most 32 columns) lose to it.
 struct MgPlan {
   uint32_t T = 1, S = 1, KS = 1;
 };
 static MgPlan mg_plan(const QMat& w, uint32_t G, bool one_split) {
   MgPlan p;
   p.T = G <= 4 ? 2 : 1;
-  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 15) / 16, slots = 256;
+  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 7) / 8, slots = 256;
   uint32_t best_ks = 1;
   double best = -1.0;
   for (uint32_t ks = 1; !one_split && ks <= 16 && ks <= nsb; ++ks) {
