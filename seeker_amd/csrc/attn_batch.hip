@@ -14,8 +14,8 @@
 // blocks, [hd][32] each) go global -> LDS by direct 16-byte loads, double
 // buffered, so tile t + 1 is in flight while tile t is used. The LDS images
 // are XOR-swizzled (K: 16-byte chunk c of key row j at c ^ (j % chunks per
-// row); V: chunk c of d row at c ^ (d / 4 % 4)), so the MFMA operand reads of
-// 16 rows hit 16 different bank groups. Each wave owns RGW groups of 16 query
+// row); V: chunk c of d row at c ^ (d / 2 % 4)), so the 8 lanes of an MFMA
+// operand read that share a 128-byte bank window hit 8 different 16-byte slots. Each wave owns RGW groups of 16 query
 // rows (rows split over waves, not keys, so every K/V tile is read once from
 // HBM for all R rows) and keeps their Q operands (hi + lo f16, a power-of-two
 // scale per row) and running (m, l, O) in registers across the split. With
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
     for (int i = wave; i < VI; i += kWaves) {
       const int qc = 64 * i + lane, c = qc & 3, dra = qc >> 2, blk = dra / HD, dr = dra % HD;
       const uint32_t vblk = min(key0 / 32 + (uint32_t)blk, max_seq / 32 - 1);
-      const uint16_t* src = vb + ((size_t)vblk * HD + dr) * 32 + 8 * (c ^ ((dr >> 2) & 3));
+      const uint16_t* src = vb + ((size_t)vblk * HD + dr) * 32 + 8 * (c ^ ((dr >> 1) & 3));
       sh_dma16(src, &sV[512 * i]);
     }
   };
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int dr = 16 * dt + r;
-        vop[dt] = lds_h8(&sV[(bb * HD + dr) * 32 + 8 * (g ^ ((dr >> 2) & 3))]);
+        vop[dt] = lds_h8(&sV[(bb * HD + dr) * 32 + 8 * (g ^ ((dr >> 1) & 3))]);
       }
       const bool tail = key0 + 32 > key_end || key0 + 32 > mbase;
 #pragma unroll
@@ -356,8 +356,16 @@ int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, ui
   // a tile over pairs of waves (KP = 2) when no segment has more than 2 row
   // groups; tiles per split chosen for about 512 workgroups (two per CU) and
   // at least 4 keys per split for every row.
+  static const int forced_rgw = [] {  // SH_FAB_RGW=1|2: row groups per wave (measurement switch)
+    const char* v = getenv("SH_FAB_RGW");
+    return v ? atoi(v) : 0;
+  }();
+  // One row group per wave by default: segments above 4 row groups go in row
+  // chunks of 4 whose K/V re-reads hit L2; two per wave (SH_FAB_RGW=2) leaves
+  // waves idle at the tile barriers when a chunk's count is not a multiple of 4
+  // (tree verify attention 3.8 vs 4.6 ms per step, measured).
   out->kp = max_rg <= 2 ? 2 : 1;
-  out->rgw = max_rg <= 4 ? 1 : 2;
+  out->rgw = (out->kp == 1 && forced_rgw == 2) ? 2 : 1;
   const uint32_t rows_max = 16 * max_rg;
   // (a split's partials are rows x (hd + 4) floats against keys x 2 hd f16 of
   // K/V: keys >= 4 rows keeps them under a quarter of the K/V bytes)
