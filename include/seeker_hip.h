@@ -160,6 +160,18 @@ int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint32_t* token
 int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B, const uint32_t* tokens,
                       const uint32_t* seq_lens, const uint32_t* positions, const int32_t* parents,
                       float* logits_out, uint32_t* sampled_out, float* residual_out);
+/* sh_verify_unified with the owning sequence's sampler per column, as the
+ * reference's verify_unified (samplers[col_seq[i]].record_chain,
+ * inference/mod.rs:2375-2386): samplers[s] (B entries) is GREEDY (argmax) or
+ * COMPARE (softmax(l / T) inverse CDF in vocab order, ops/sampler.rs:303-368);
+ * the j-th column of sequence s takes uniforms[j] of its explicit array, else
+ * Philox word counter + j of key (seed, 0x5EC); each COMPARE sampler's counter
+ * advances by seq_lens[s]. REJECTION is refused (it needs draft logits:
+ * sh_accept_sample). samplers NULL: sh_verify_unified. */
+int sh_verify_unified_sampled(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B, const uint32_t* tokens,
+                              const uint32_t* seq_lens, const uint32_t* positions, const int32_t* parents,
+                              sh_sampling* samplers, float* logits_out, uint32_t* sampled_out,
+                              float* residual_out);
 
 /* Engine::decode_speculative (inference/mod.rs:2108-2297) with a separate draft
  * model: drafts n = clamp(n_max,1,8) tokens on the device, verifies [last,

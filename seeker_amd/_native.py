@@ -117,6 +117,8 @@ SIGNATURES = {
     "sh_forward_full": (C.c_int, [P, P, P, U32P, C.c_uint32, C.c_uint32, I32P, C.c_int, F32P, F32P]),
     "sh_verify_greedy": (C.c_int, [P, P, P, U32P, C.c_uint32, C.c_uint32, U32P]),
     "sh_verify_unified": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, U32P, U32P, U32P, I32P, F32P, U32P, F32P]),
+    "sh_verify_unified_sampled": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, U32P, U32P, U32P, I32P,
+                                            P, F32P, U32P, F32P]),
     "sh_spec_step": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), U32P, U32P, U32P]),
     "sh_spec_step_logits": (C.c_int, [P, F32P, F32P, U32P, U32P]),
     "sh_accept_sample_noalloc": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling),

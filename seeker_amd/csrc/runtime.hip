@@ -1213,9 +1213,23 @@ extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint
 // (logits_dev, [N_total][V]).
 static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B, const uint32_t* tokens,
                                const uint32_t* seq_lens, const uint32_t* positions, const int32_t* parents,
-                               float* logits_out, float* logits_dev, uint32_t* sampled_out, float* residual_out) {
+                               float* logits_out, float* logits_dev, uint32_t* sampled_out, float* residual_out,
+                               sh_sampling* samplers = nullptr) {
   SH_CHECK(e && m && caches && tokens && seq_lens, SH_ERR_ARG, "sh_verify_unified: NULL argument");
   SH_CHECK(B >= 1, SH_ERR_ARG, "verify_unified: empty batch");
+  // per-sequence samplers: GREEDY (argmax) or COMPARE-style temperature
+  // sampling of every column (REJECTION needs draft logits: sh_accept_sample)
+  bool any_stoch = false;
+  if (samplers)
+    for (uint32_t s = 0; s < B; ++s) {
+      const sh_sampling& sp = samplers[s];
+      SH_CHECK(sp.mode == SH_SAMPLE_GREEDY || sp.mode == SH_SAMPLE_COMPARE, SH_ERR_ARG,
+               "verify_unified: sequence %u sampler mode %u (GREEDY or COMPARE)", s, sp.mode);
+      SH_CHECK(sp.mode == SH_SAMPLE_GREEDY || sp.temperature > 0.f, SH_ERR_ARG,
+               "verify_unified: sequence %u temperature %g", s, (double)sp.temperature);
+      any_stoch = any_stoch || sp.mode == SH_SAMPLE_COMPARE;
+    }
+  SH_CHECK(!any_stoch || sampled_out, SH_ERR_ARG, "verify_unified: samplers without sampled_out");
   // prefix-sum column starts (q_starts) and per-sequence plans
   std::vector<uint32_t> q0(B + 1, 0);
   std::vector<Plan> plans(B);
@@ -1310,6 +1324,36 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
                             hipMemcpyDeviceToDevice, e->stream));
     if (sampled_out) {
       if ((rc = sh_argmax_launch(e, m->ws.logits, m->V, nc, m->ws.amax, ids))) break;
+      if (any_stoch) {
+        // column c of sequence s (its j-th): uniform j of s's explicit array,
+        // else Philox word counter + j of key (seed, 0x5EC)
+        std::vector<SampRow> rows(nc);
+        bool chunk_stoch = false;
+        for (uint32_t c = 0; c < nc; ++c) {
+          const uint32_t sq = cseq[c0 + c], j = cidx[c0 + c];
+          const sh_sampling& sp = samplers[sq];
+          SampRow& r = rows[c];
+          r = SampRow{};
+          r.greedy = sp.mode == SH_SAMPLE_GREEDY ? 1u : 0u;
+          r.inv_t = r.greedy ? 1.0 : 1.0 / (double)sp.temperature;
+          r.seed = sp.seed;
+          r.word = sp.counter + j;
+          r.explicit_u = sp.uniforms ? 1u : 0u;
+          r.u = sp.uniforms ? sp.uniforms[j] : 0.f;
+          chunk_stoch = chunk_stoch || !r.greedy;
+        }
+        if (chunk_stoch) {
+          SampRow* rdev = nullptr;
+          double2* part = nullptr;
+          SH_HIP(hipMallocAsync((void**)&rdev, nc * sizeof(SampRow), e->stream));
+          SH_HIP(hipMallocAsync((void**)&part, sh_sample_rows_part_bytes(nc, m->V), e->stream));
+          SH_HIP(hipMemcpyAsync(rdev, rows.data(), nc * sizeof(SampRow), hipMemcpyHostToDevice, e->stream));
+          rc = sh_sample_rows_tab_launch(e, m->ws.logits, nc, m->V, rdev, part, ids);
+          (void)hipFreeAsync(rdev, e->stream);
+          (void)hipFreeAsync(part, e->stream);
+          if (rc) break;
+        }
+      }
       SH_HIP(hipMemcpyAsync(sampled_out + c0, ids, (size_t)nc * 4, hipMemcpyDeviceToHost, e->stream));
     }
   }
@@ -1322,6 +1366,7 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
   for (uint32_t s = 0; s < B; ++s) {
     caches[s]->pos += seq_lens[s];
     caches[s]->pending.clear();
+    if (samplers && samplers[s].mode == SH_SAMPLE_COMPARE) samplers[s].counter += seq_lens[s];
   }
   return sh_prof_flush(e);
 }
@@ -1332,6 +1377,14 @@ extern "C" int sh_verify_unified(sh_engine* e, sh_model* m, sh_kv* const* caches
                                  float* residual_out) {
   return verify_unified_impl(e, m, caches, B, tokens, seq_lens, positions, parents, logits_out, nullptr, sampled_out,
                              residual_out);
+}
+
+extern "C" int sh_verify_unified_sampled(sh_engine* e, sh_model* m, sh_kv* const* caches, uint32_t B,
+                                         const uint32_t* tokens, const uint32_t* seq_lens, const uint32_t* positions,
+                                         const int32_t* parents, sh_sampling* samplers, float* logits_out,
+                                         uint32_t* sampled_out, float* residual_out) {
+  return verify_unified_impl(e, m, caches, B, tokens, seq_lens, positions, parents, logits_out, nullptr, sampled_out,
+                             residual_out, samplers);
 }
 
 extern "C" int sh_tree_verify_step(sh_engine* e, sh_model* target, sh_kv* const* caches, uint32_t B, uint32_t n,

@@ -114,13 +114,15 @@ __device__ __forceinline__ double2 reduce_unit(const float (&v)[E], double inv_t
 template <bool VEC, int E>
 __global__ __launch_bounds__(256) void k_row_part(const float* __restrict__ p, uint32_t n_p,
                                                   const float* __restrict__ q, uint32_t V, double inv_t,
-                                                  uint32_t nch, double2* __restrict__ part) {
+                                                  uint32_t nch, double2* __restrict__ part,
+                                                  const SampRow* __restrict__ rows = nullptr) {
   __shared__ float shf[4];
   __shared__ double shd[4];
   __shared__ double tab[64];
   load_exp_table(tab);  // visible after the barriers inside block_max_f
   float v[E];
   load_unit<VEC, E>(p, n_p, q, V, nch, blockIdx.x, v);
+  if (rows) inv_t = rows[blockIdx.x / nch].inv_t;  // per-row temperature (a row's units are consecutive)
   const double2 r = reduce_unit<E>(v, inv_t, tab, shf, shd);
   if (threadIdx.x == 0) part[blockIdx.x] = r;
 }
@@ -305,6 +307,31 @@ __global__ __launch_bounds__(256) void k_sample_cols(const float* __restrict__ p
   __syncthreads();
   RowW rw{p + (size_t)row * V, nullptr, st.x, 1.0, 0.0, 1.0, inv_t, tab};
   const float u = uniform_at(u_dev, seed, word0 + wstride * row);
+  const uint32_t tok = wg_inverse_cdf(rw, 0, V, true, u, 0.0, 0.0, true, nullptr);
+  if (threadIdx.x == 0) out[row] = tok;
+}
+
+// Per-row sampling of a batched verify: row r is drawn from softmax(p_r *
+// rows[r].inv_t) in vocab order with uniform rows[r].u (explicit) or Philox
+// word rows[r].word of key (rows[r].seed, 0x5EC); greedy rows keep the argmax
+// already in out[r].
+__global__ __launch_bounds__(256) void k_sample_rows_tab(const float* __restrict__ p, const double2* __restrict__ part,
+                                                         uint32_t nch, uint32_t V, const SampRow* __restrict__ rows,
+                                                         uint32_t* __restrict__ out) {
+  __shared__ double tab[64];
+  __shared__ double2 st;
+  const uint32_t row = blockIdx.x;
+  const SampRow sr = rows[row];
+  if (sr.greedy) return;  // uniform: the whole workgroup leaves
+  load_exp_table(tab);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const double2 s = wave_row_stat(part + (size_t)row * nch, nch, sr.inv_t, tab);
+    if (threadIdx.x == 0) st = s;
+  }
+  __syncthreads();
+  RowW rw{p + (size_t)row * V, nullptr, st.x, 1.0, 0.0, 1.0, sr.inv_t, tab};
+  const float u = sr.explicit_u ? sr.u : uniform_at(nullptr, sr.seed, sr.word);
   const uint32_t tok = wg_inverse_cdf(rw, 0, V, true, u, 0.0, 0.0, true, nullptr);
   if (threadIdx.x == 0) out[row] = tok;
 }
@@ -896,6 +923,28 @@ int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uin
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "sample_rows", 4.0 * V * nrows, ev);
   return SH_OK;
+}
+
+int sh_sample_rows_tab_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, const SampRow* rows_dev,
+                              double2* part, uint32_t* out) {
+  SH_CHECK(nrows >= 1 && V >= 1, SH_ERR_ARG, "sample_rows_tab: nrows=%u V=%u", nrows, V);
+  const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  if (V % 4 == 0)
+    hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
+                       nullptr, V, 1.0, nch, part, rows_dev);
+  else
+    hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
+                       nullptr, V, 1.0, nch, part, rows_dev);
+  hipLaunchKernelGGL(k_sample_rows_tab, dim3(nrows), dim3(256), 0, e->stream, logits, part, nch, V, rows_dev, out);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, "sample_rows", 4.0 * V * nrows, ev);
+  return SH_OK;
+}
+
+size_t sh_sample_rows_part_bytes(uint32_t nrows, uint32_t V) {
+  return (size_t)nrows * ((V + 256 * kStatE - 1) / (256 * kStatE)) * sizeof(double2);
 }
 
 extern "C" int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,

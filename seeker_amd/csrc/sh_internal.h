@@ -427,6 +427,21 @@ int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, 
 // 8192) row-statistics partials of scratch.
 int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
                           uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out);
+// Per-row parameters of the batched verify's column sampling.
+struct SampRow {
+  double inv_t;       // 1 / temperature
+  uint64_t seed;      // Philox key word 0
+  uint64_t word;      // Philox word (uniform index)
+  float u;            // explicit uniform (explicit_u)
+  uint32_t greedy;    // keep the argmax already in out[row]
+  uint32_t explicit_u;
+  uint32_t pad;
+};
+// Draws row r of logits [nrows][V] by rows_dev[r] (greedy rows untouched);
+// part: sh_sample_rows_part_bytes(nrows, V) of scratch.
+int sh_sample_rows_tab_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, const SampRow* rows_dev,
+                              double2* part, uint32_t* out);
+size_t sh_sample_rows_part_bytes(uint32_t nrows, uint32_t V);
 // Routed-expert FFN pieces (moe.hip): router logits [N][E] of the RMS-normed
 // columns, top-k per column (ids, wts [N][k]) with the routing plan over
 // P = N k pairs, the weighted sum into resid.

@@ -129,10 +129,13 @@ class Engine:
     def verify_unified(self, model: "Model", caches: Sequence["KvCache"], tokens: Sequence[int],
                        seq_lens: Sequence[int], positions: Optional[Sequence[int]] = None,
                        parents: Optional[Sequence[int]] = None, want_logits: bool = False,
-                       want_residual: bool = False) -> VerifyUnifiedOut:
+                       want_residual: bool = False, samplers: Optional[Sequence[N.sh_sampling]] = None
+                       ) -> VerifyUnifiedOut:
         """Engine::verify_unified (inference/mod.rs:2316-2398): B sequences packed flat, sequence s
-        verified against caches[s]. Greedy argmax per column; logits / residual on request.
-        Every cache advances by its seq_len (truncate to the accepted length afterwards)."""
+        verified against caches[s]. Every column sampled by its sequence's sampler (samplers[s]:
+        GREEDY or COMPARE, sh_verify_unified_sampled; None: greedy argmax); logits / residual on
+        request. Every cache advances by its seq_len (truncate to the accepted length afterwards);
+        each COMPARE sampler's counter advances by its seq_len."""
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         sl = np.ascontiguousarray(seq_lens, dtype=np.uint32)
         n, b = t.size, sl.size
@@ -142,12 +145,18 @@ class Engine:
         sampled = np.zeros(n, dtype=np.uint32)
         logits = np.zeros((n, model.vocab_size()), dtype=np.float32) if want_logits else None
         resid = np.zeros((n, model.dims.n_embd), dtype=np.float32) if want_residual else None
-        N.check(self._lib.sh_verify_unified(
-            self.h, model.h, C.cast(hs, C.POINTER(C.c_void_p)), b, t.ctypes.data_as(N.U32P),
-            sl.ctypes.data_as(N.U32P), None if pos is None else pos.ctypes.data_as(N.U32P),
-            None if par is None else par.ctypes.data_as(N.I32P),
-            None if logits is None else logits.ctypes.data_as(N.F32P), sampled.ctypes.data_as(N.U32P),
-            None if resid is None else resid.ctypes.data_as(N.F32P)))
+        args = (self.h, model.h, C.cast(hs, C.POINTER(C.c_void_p)), b, t.ctypes.data_as(N.U32P),
+                sl.ctypes.data_as(N.U32P), None if pos is None else pos.ctypes.data_as(N.U32P),
+                None if par is None else par.ctypes.data_as(N.I32P))
+        outs = (None if logits is None else logits.ctypes.data_as(N.F32P), sampled.ctypes.data_as(N.U32P),
+                None if resid is None else resid.ctypes.data_as(N.F32P))
+        if samplers is None:
+            N.check(self._lib.sh_verify_unified(*args, *outs))
+        else:
+            arr = (N.sh_sampling * b)(*samplers)
+            N.check(self._lib.sh_verify_unified_sampled(*args, C.cast(arr, C.c_void_p), *outs))
+            for s_in, s_out in zip(samplers, arr):
+                s_in.counter = s_out.counter
         q_starts = np.concatenate([[0], np.cumsum(sl)[:-1]]).astype(np.uint64)
         return VerifyUnifiedOut(sampled, logits, resid, q_starts)
 

@@ -19,6 +19,7 @@ import pytest
 
 import oracle as O
 from seeker_amd import SeekerError
+from seeker_amd import _native as N
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K, SH_ERR_ARG, SH_ERR_CAPACITY
 
@@ -208,3 +209,57 @@ def test_tree_verify_step(engine, model):
     qd.free()
     for x in kv + ref_kv:
         x.close()
+
+
+def test_unified_sampled_per_sequence(engine, model):
+    """sh_verify_unified_sampled: every column sampled with its own sequence's
+    sampler (samplers[col_seq[i]].record_chain, inference/mod.rs:2375-2386).
+    Greedy sequences keep the argmax; COMPARE sequences draw column j from
+    softmax(l / T) in vocab order with Philox word counter + j of key
+    (seed, 0x5EC) or with their explicit uniforms[j], checked against the
+    oracle's sampler on the same returned logits."""
+    from seeker_amd._native import SH_SAMPLE_COMPARE, SH_SAMPLE_GREEDY, SH_SAMPLE_REJECTION, sh_sampling
+    name, img, gm = model
+    V = gm.vocab_size()
+    prompts = [S.tokens(700 + s, p, V) for s, (p, _) in enumerate(SEQS)]
+    drafts = [S.tokens(800 + s, n, V) for s, (_, n) in enumerate(SEQS)]
+    lens = [n for _, n in SEQS]
+    toks = np.concatenate(drafts)
+    u_explicit = S.normal_f32(3, 3, lens[2], 0.5, 0.2).clip(0.01, 0.99).astype(np.float32)
+    cfg = [(SH_SAMPLE_GREEDY, 0.0, 0, 0, None), (SH_SAMPLE_COMPARE, 0.8, 5, 7, None),
+           (SH_SAMPLE_COMPARE, 1.3, 0, 0, u_explicit), (SH_SAMPLE_COMPARE, 0.5, 9, 0, None)]
+    samplers = []
+    for mode, t, seed, ctr, u in cfg:
+        sp = sh_sampling()
+        sp.mode, sp.temperature, sp.seed, sp.counter = mode, t, seed, ctr
+        if u is not None:
+            sp.uniforms = u.ctypes.data_as(N.F32P)
+        samplers.append(sp)
+    kv = [_prefilled(engine, gm, pr) for pr in prompts]
+    # a REJECTION sampler is refused before anything runs
+    bad = sh_sampling()
+    bad.mode, bad.temperature = SH_SAMPLE_REJECTION, 1.0
+    with pytest.raises(SeekerError) as ei:
+        engine.verify_unified(gm, kv, toks, lens, samplers=[samplers[0], bad, samplers[2], samplers[3]])
+    assert ei.value.status == SH_ERR_ARG
+    assert [k.position for k in kv] == [p for p, _ in SEQS]
+    out = engine.verify_unified(gm, kv, toks, lens, want_logits=True, samplers=samplers)
+    differs = 0
+    for s, (mode, t, seed, ctr, u) in enumerate(cfg):
+        q, n = int(out.q_starts[s]), lens[s]
+        lg = out.logits[q:q + n]
+        got = out.sampled[q:q + n]
+        if mode == SH_SAMPLE_GREEDY:
+            want = lg.argmax(axis=1)
+            assert samplers[s].counter == 0
+        else:
+            us = u if u is not None else O.philox_uniforms(seed, 0x5EC, ctr, n)
+            want = [O.sample_vocab_order(lg[j], t, float(us[j])) for j in range(n)]
+            assert samplers[s].counter == ctr + n
+            differs += int(np.sum(got != lg.argmax(axis=1)))
+        print(f"{name} seq {s}: sampled {list(got)} want {list(want)}", flush=True)
+        assert np.array_equal(got, np.asarray(want, dtype=np.uint32))
+        assert kv[s].position == SEQS[s][0] + n
+    assert differs > 0  # small random-init logits: temperature sampling leaves the argmax
+    for k in kv:
+        k.close()
