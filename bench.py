@@ -66,6 +66,47 @@ def measured_traffic(kernel_tag):
     return None if k is None else k["fetch_bytes"] + k["write_bytes"]
 
 
+def measure_draft(eng, P=4096, reps=30):
+    """The draft forward alone (1B shape, 1 column, context P): eager
+    sh_forward_full calls with greedy logits at KV position P (set without a
+    prefill; the bytes read and the work are the same), then a pass with
+    per-kernel profiling events. Bytes per forward: every weight matrix once +
+    f16 K/V read for [0, P + 1) + one K/V row written."""
+    import numpy as np
+    from seeker_amd import synth as S
+    img = S.GgufImage(S.L1B_DRAFT, seed=1)
+    dm = eng.upload_weights(img)
+    img.close()
+    d = dm.dims
+    kv = eng.allocate_kv_cache(dm, P + 64)
+    tok = [int(S.tokens(5, 1, d.n_vocab)[0])]
+    for _ in range(3):
+        kv.set_position(P)
+        eng.forward_full_readback(dm, kv, tok, P, full_logits=False, want_residual=False)
+    lat = []
+    for _ in range(reps):
+        kv.set_position(P)
+        t = time.perf_counter()
+        eng.forward_full_readback(dm, kv, tok, P, full_logits=False, want_residual=False)
+        lat.append((time.perf_counter() - t) * 1e3)
+    eng.set_profiling(True)
+    eng.profile(reset=True)
+    for _ in range(reps):
+        kv.set_position(P)
+        eng.forward_full_readback(dm, kv, tok, P, full_logits=False, want_residual=False)
+    prof = eng.profile(reset=True)
+    eng.set_profiling(False)
+    kv.close()
+    dm.close()
+    w, kr, kw = verify_bytes(d, P, 1)
+    kern_ms = sum(s["ms"] for s in prof.values()) / reps
+    per = {n: round(s["ms"] / reps * 1e3, 2) for n, s in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
+    log(f"draft forward (P={P}): median {statistics.median(lat):.3f} ms eager wall, {kern_ms:.3f} ms in kernels; "
+        f"us/forward by kernel {per}")
+    return {"config": f"1B draft shape, 1 column, ctx {P}, eager", "wall_ms": round(statistics.median(lat), 4),
+            "kernel_ms": round(kern_ms, 4), "alg_bytes": w + kr + kw, "kernel_us": per}
+
+
 def measure_acceptance(eng, reps=20):
     """the acceptance kernel alone (REJECTION, T = 0.8), B = 32, k = 8,
     V = 128256; target logits N(0, 3), draft = target + N(0, 1), drafts sampled
@@ -245,6 +286,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel, tree and MoE lines")
     ap.add_argument("--moe-only", action="store_true", help="only the configs[4] MoE verify measurement")
     ap.add_argument("--tree-only", action="store_true", help="only the configs[3] tree verify measurement")
+    ap.add_argument("--acceptance-only", action="store_true", help="only the configs[1] acceptance measurement")
+    ap.add_argument("--draft-only", action="store_true", help="only the draft forward (eager, per-kernel events)")
     ap.add_argument("--profile-only", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -260,6 +303,14 @@ def main():
     if args.moe_only:
         with Engine(0) as eng:
             print(json.dumps({"metric": "moe verify step", "moe_verify": measure_moe(eng)}), flush=True)
+        return
+    if args.draft_only:
+        with Engine(0) as eng:
+            print(json.dumps({"metric": "draft forward", "draft": measure_draft(eng, args.ctx)}), flush=True)
+        return
+    if args.acceptance_only:
+        with Engine(0) as eng:
+            print(json.dumps({"metric": "acceptance kernel", "acceptance": measure_acceptance(eng)}), flush=True)
         return
     if args.tree_only:
         img = S.GgufImage(S.L8B_TARGET, seed=0)

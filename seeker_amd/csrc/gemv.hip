@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "sh_internal.h"
+#include "sh_coherent.h"
 #include "sh_dma.h"
 #include "sh_operand.h"
 
@@ -472,20 +473,11 @@ constexpr uint32_t WIDE_MAX_UNITS = 12;  // units per wave (T * S) beyond which 
 // (one wave per (superblock, column)): from f32 rows (OPND_ROWS) or by
 // combining attention split partials (OPND_FA), with the same arithmetic as
 // the prep / combine kernels; the first weight units are already in flight.
-// 16-byte agent-coherent store / load (sc1: past the non-coherent per-XCD L2)
-// for data that another workgroup of the same kernel reads. The loads are not
-// tracked by the compiler: their results pass through an asm statement
-// holding "s_waitcnt vmcnt(0)" (values as "+v" operands) before any use.
-typedef float f4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void st_coh4(float* p, float4 v) {
-  const f4v w = {v.x, v.y, v.z, v.w};
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
-}
-__device__ __forceinline__ f4v ld_coh4(const float* p) {
-  f4v v;
-  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
+// 16-byte agent-coherent store / load of four floats for data that another
+// workgroup of the same kernel reads (the protocol of sh_coherent.h).
+typedef sh_f4v f4v;
+__device__ __forceinline__ void st_coh4(float* p, float4 v) { sh_st_coh16(p, f4v{v.x, v.y, v.z, v.w}); }
+__device__ __forceinline__ f4v ld_coh4(const float* p) { return sh_ld_coh16(p); }
 
 // Fused residual prep of output superblock j (the PREP_RESID prep kernel's
 // arithmetic: resid + split partials in split order, sums of squares, times

@@ -65,12 +65,16 @@ __device__ __forceinline__ double wave_max_d(double v) {
   return v;
 }
 
-// Row statistics: max and sum of exp((l - max) / T) in f64, in two steps.
+// Row statistics: max and sum of exp((l - max) / T), in two steps.
 // Step 1: the rows are cut into units of 256 E logits (unit c of row r is
 // index r * nch + c), one workgroup per unit: every thread keeps its E logits
-// in registers (one HBM read), the unit max is reduced, then the f64 exp-sum
-// against it. A unit whose logits are all -inf reports (-inf, 0). The f64 exp
-// (about 25 instructions per logit) bounds this kernel, not HBM.
+// in registers (one HBM read), the unit max is reduced, then the exp-sum
+// against it. A unit whose logits are all -inf reports (-inf, 0). The terms
+// are the hardware exp2 (v_exp_f32, 1 ulp) of (l - max) * log2(e) / T in f32,
+// summed in f64: the sum is within ~1e-6 relative of the exact one (it only
+// normalises probabilities, whose bound is 1e-5), and one f32 exp per logit
+// leaves the kernel bound by HBM. Draws resolve their CDF crossings with f64
+// weights computed in the draw kernels themselves, never with these sums.
 constexpr int kStatE = 32;
 
 template <bool VEC, int E>
@@ -96,17 +100,16 @@ __device__ __forceinline__ void load_unit(const float* __restrict__ p, uint32_t 
 }
 
 template <int E>
-__device__ __forceinline__ double2 reduce_unit(const float (&v)[E], double inv_t, const double* tab, float* shf,
-                                               double* shd) {
+__device__ __forceinline__ double2 reduce_unit(const float (&v)[E], double inv_t, float* shf, double* shd) {
   float mx = v[0];
 #pragma unroll
   for (int j = 1; j < E; ++j) mx = fmaxf(mx, v[j]);
   mx = block_max_f(mx, shf);
   double s = 0.0;
   if (mx != -INFINITY) {
-    const double m = (double)mx;
+    const float c = (float)(inv_t * 1.4426950408889634074);  // log2(e) / T
 #pragma unroll
-    for (int j = 0; j < E; ++j) s += sh_exp_neg(((double)v[j] - m) * inv_t, tab);
+    for (int j = 0; j < E; ++j) s += (double)__builtin_amdgcn_exp2f((v[j] - mx) * c);  // -inf -> 0
   }
   return make_double2((double)mx, block_sum_d(s, shd));
 }
@@ -118,12 +121,10 @@ __global__ __launch_bounds__(256) void k_row_part(const float* __restrict__ p, u
                                                   const SampRow* __restrict__ rows = nullptr) {
   __shared__ float shf[4];
   __shared__ double shd[4];
-  __shared__ double tab[64];
-  load_exp_table(tab);  // visible after the barriers inside block_max_f
   float v[E];
   load_unit<VEC, E>(p, n_p, q, V, nch, blockIdx.x, v);
   if (rows) inv_t = rows[blockIdx.x / nch].inv_t;  // per-row temperature (a row's units are consecutive)
-  const double2 r = reduce_unit<E>(v, inv_t, tab, shf, shd);
+  const double2 r = reduce_unit<E>(v, inv_t, shf, shd);
   if (threadIdx.x == 0) part[blockIdx.x] = r;
 }
 
@@ -183,11 +184,15 @@ struct RowW {
   const double* tab;
   using Raw = float2;
   __device__ __forceinline__ Raw raw(uint32_t v) const { return make_float2(p[v], q ? q[v] : 0.f); }
-  __device__ __forceinline__ double wt(Raw x) const {
-    const double a = sh_exp_neg(((double)x.x - pm) * inv_t, tab);
-    if (!q) return a;
-    const double r = a * ips - sh_exp_neg(((double)x.y - qm) * inv_t, tab) * iqs;
+  __device__ __forceinline__ double num(float pl) const { return sh_exp_neg(((double)pl - pm) * inv_t, tab); }
+  // residual weight from the p numerator a and the draft logit ql
+  __device__ __forceinline__ double resid(double a, float ql) const {
+    const double r = a * ips - sh_exp_neg(((double)ql - qm) * inv_t, tab) * iqs;
     return r > 0.0 ? r : 0.0;
+  }
+  __device__ __forceinline__ double wt(Raw x) const {
+    const double a = num(x.x);
+    return q ? resid(a, x.y) : a;
   }
 };
 
@@ -432,9 +437,9 @@ __global__ __launch_bounds__(256) void k_draw_chunks(const float* __restrict__ p
   const float* pr = p + ((size_t)b * (k + 1) + i) * V;
   const float* qr = resid ? q + ((size_t)b * k + i) * V : pr;
   __syncthreads();  // table
-  // the same weights as the pick's scan (RowW): residual and plain numerator
+  // the same weights as the pick's scan (RowW): the p numerator once per
+  // element, the residual from it
   const RowW rres{pr, qr, sp.x, 1.0 / sp.y, sq.x, 1.0 / sq.y, inv_t, tab};
-  const RowW rnum{pr, nullptr, sp.x, 1.0, 0.0, 1.0, inv_t, tab};
   double rs = 0.0, ps = 0.0;
   for (uint32_t v0 = lo; v0 < hi; v0 += 256 * kPer) {
     float2 x[kPer];
@@ -445,8 +450,9 @@ __global__ __launch_bounds__(256) void k_draw_chunks(const float* __restrict__ p
     }
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      ps += rnum.wt(x[j]);
-      if (resid) rs += rres.wt(x[j]);
+      const double a = rres.num(x[j].x);
+      ps += a;
+      if (resid) rs += rres.resid(a, x[j].y);
     }
   }
   rs = block_sum_d(rs, shd);
