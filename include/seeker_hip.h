@@ -54,6 +54,19 @@ typedef struct sh_sampling {
   uint64_t seed;          /* Philox4x64-10 key word 0 */
   uint64_t counter;       /* Philox word offset; advanced by calls that consume uniforms */
   const float* uniforms;  /* optional explicit host uniforms (overrides Philox), or NULL */
+  /* Candidate filters of the reference's chain (SamplerConfig, sample.rs:85;
+   * order sample.rs:369-473 / ops/sampler.rs:41-132), COMPARE only; zero
+   * disables each. top_k in 1..256 (or >= V when V <= 256): a column draws
+   * among its top_k logits sorted descending (ties to the lower id) after
+   * top_p (0 < p < 1: drop once the cumulative softmax before a candidate
+   * exceeds p), min_p (> 0: drop logits below max + ln min_p) and 1/T, in
+   * that order, first candidate whose cumulative probability reaches u.
+   * top_p / min_p without top_k, and top_k above 256, are refused
+   * (SH_ERR_UNSUPPORTED). */
+  uint32_t top_k;
+  float top_p;
+  float min_p;
+  uint32_t reserved;      /* zero */
 } sh_sampling;
 
 typedef struct sh_model_dims {

@@ -35,6 +35,10 @@ class sh_sampling(C.Structure):
         ("seed", C.c_uint64),
         ("counter", C.c_uint64),
         ("uniforms", C.POINTER(C.c_float)),
+        ("top_k", C.c_uint32),
+        ("top_p", C.c_float),
+        ("min_p", C.c_float),
+        ("reserved", C.c_uint32),
     ]
 
 

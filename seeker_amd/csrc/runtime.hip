@@ -1227,6 +1227,10 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
                "verify_unified: sequence %u sampler mode %u (GREEDY or COMPARE)", s, sp.mode);
       SH_CHECK(sp.mode == SH_SAMPLE_GREEDY || sp.temperature > 0.f, SH_ERR_ARG,
                "verify_unified: sequence %u temperature %g", s, (double)sp.temperature);
+      if (sp.mode == SH_SAMPLE_COMPARE) {
+        SampRow chk{};
+        if (int frc = sh_samprow_filters(sp, m->V, chk)) return frc;
+      }
       any_stoch = any_stoch || sp.mode == SH_SAMPLE_COMPARE;
     }
   SH_CHECK(!any_stoch || sampled_out, SH_ERR_ARG, "verify_unified: samplers without sampled_out");
@@ -1328,7 +1332,7 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
         // column c of sequence s (its j-th): uniform j of s's explicit array,
         // else Philox word counter + j of key (seed, 0x5EC)
         std::vector<SampRow> rows(nc);
-        bool chunk_stoch = false;
+        bool chunk_plain = false, chunk_filt = false;
         for (uint32_t c = 0; c < nc; ++c) {
           const uint32_t sq = cseq[c0 + c], j = cidx[c0 + c];
           const sh_sampling& sp = samplers[sq];
@@ -1340,15 +1344,17 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
           r.word = sp.counter + j;
           r.explicit_u = sp.uniforms ? 1u : 0u;
           r.u = sp.uniforms ? sp.uniforms[j] : 0.f;
-          chunk_stoch = chunk_stoch || !r.greedy;
+          if (!r.greedy) (void)sh_samprow_filters(sp, m->V, r);  // checked before the forward
+          chunk_plain = chunk_plain || (!r.greedy && !r.top_k);
+          chunk_filt = chunk_filt || (!r.greedy && r.top_k);
         }
-        if (chunk_stoch) {
+        if (chunk_plain || chunk_filt) {
           SampRow* rdev = nullptr;
           double2* part = nullptr;
           SH_HIP(hipMallocAsync((void**)&rdev, nc * sizeof(SampRow), e->stream));
           SH_HIP(hipMallocAsync((void**)&part, sh_sample_rows_part_bytes(nc, m->V), e->stream));
           SH_HIP(hipMemcpyAsync(rdev, rows.data(), nc * sizeof(SampRow), hipMemcpyHostToDevice, e->stream));
-          rc = sh_sample_rows_tab_launch(e, m->ws.logits, nc, m->V, rdev, part, ids);
+          rc = sh_sample_rows_tab_launch(e, m->ws.logits, nc, m->V, rdev, part, ids, chunk_plain, chunk_filt);
           (void)hipFreeAsync(rdev, e->stream);
           (void)hipFreeAsync(part, e->stream);
           if (rc) break;
@@ -1560,6 +1566,11 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   SH_CHECK(last_token < tm->V, SH_ERR_ARG, "last_token %u out of range", last_token);
   const uint32_t mode = s ? s->mode : SH_SAMPLE_GREEDY;
   SH_CHECK(mode <= SH_SAMPLE_REJECTION, SH_ERR_ARG, "sampling mode %u", mode);
+  if (mode == SH_SAMPLE_REJECTION) {
+    SampRow chk{};
+    if (int frc = sh_samprow_filters(*s, tm->V, chk)) return frc;
+    SH_CHECK(!chk.top_k, SH_ERR_UNSUPPORTED, "candidate filters (top_k / top_p / min_p) apply to COMPARE only");
+  }
   SH_CHECK(mode == SH_SAMPLE_GREEDY || (s && s->temperature > 0.f), SH_ERR_ARG,
            "stochastic modes need temperature > 0");
   const uint32_t n = std::min<uint32_t>(std::max<uint32_t>(n_max, 1), 8);  // mod.rs:2121

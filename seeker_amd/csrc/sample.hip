@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void k_sample_rows_tab(const float* __restrict
   __shared__ double2 st;
   const uint32_t row = blockIdx.x;
   const SampRow sr = rows[row];
-  if (sr.greedy) return;  // uniform: the whole workgroup leaves
+  if (sr.greedy || sr.top_k) return;  // uniform: the whole workgroup leaves (filtered rows: k_sample_filtered_tab)
   load_exp_table(tab);
   __syncthreads();
   if (threadIdx.x < 64) {
@@ -338,6 +338,250 @@ __global__ __launch_bounds__(256) void k_sample_rows_tab(const float* __restrict
   RowW rw{p + (size_t)row * V, nullptr, st.x, 1.0, 0.0, 1.0, sr.inv_t, tab};
   const float u = sr.explicit_u ? sr.u : uniform_at(nullptr, sr.seed, sr.word);
   const uint32_t tok = wg_inverse_cdf(rw, 0, V, true, u, 0.0, 0.0, true, nullptr);
+  if (threadIdx.x == 0) out[row] = tok;
+}
+
+// ------------------------------------------------------------ filtered sampling
+//
+// The reference's sampler chain with candidate filters (host order,
+// inference/sample.rs:369-473, which the GPU chain mirrors,
+// ops/sampler.rs:41-132): the top_k (1..256) largest logits, sorted by logit
+// descending with ties to the lower id -> top_p (softmax of the candidates;
+// a candidate is dropped once the cumulative probability BEFORE it exceeds
+// p, so the crossing one stays) -> min_p (logit below max + ln min_p
+// dropped) -> logits times 1/T -> softmax -> the first candidate whose
+// cumulative probability reaches u (the last one when rounding leaves the
+// sum short). Softmaxes take f64 exps of the f32 logits and f32
+// probabilities, cumulative sums in f64 in candidate order, as the C oracle.
+//
+// One workgroup per row: the top_k-th largest logit by a three-pass radix
+// select over orderable keys (11, 11, 10 bits; LDS histograms), one pass to
+// collect the candidates (ties at the threshold by index order), a bitonic
+// sort of the <= 256 candidates, then the chain on one thread per candidate
+// with the order-dependent sums on one thread.
+constexpr uint32_t kTopKMax = 256;
+
+struct FiltCfg {
+  uint32_t k;        // candidates (1..kTopKMax)
+  float top_p;       // used when top_p_on
+  float log_min_p;   // ln(min_p), used when min_p_on
+  float inv_t;       // 1 / max(T, 1e-9) as f32, used when temp_on
+  uint32_t flags;    // 1 top_p_on, 2 min_p_on, 4 temp_on
+};
+
+__device__ __forceinline__ uint32_t ord_key(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  if (v != v) return 0u;  // NaN sorts last
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Exclusive prefix of per-thread counts over the 256 threads (thread order).
+__device__ __forceinline__ uint32_t block_exscan_u(uint32_t x, uint32_t* wsum, uint32_t* total) {
+  const uint32_t t = threadIdx.x, l = t & 63, w = t >> 6;
+  uint32_t inc = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(inc, off);
+    if (l >= (uint32_t)off) inc += y;
+  }
+  __syncthreads();
+  if (l == 63) wsum[w] = inc;
+  __syncthreads();
+  uint32_t base = 0;
+  for (uint32_t i = 0; i < w; ++i) base += wsum[i];
+  if (total) *total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  return base + inc - x;
+}
+
+// softmax of n (<= 256) candidate logits as the C oracle's or_softmax: f64
+// exps against the max, summed in order, f32 probabilities. pr[j] for j < n.
+__device__ void cand_softmax(const float* kept, uint32_t n, float* pr, double* e, const double* tab) {
+  __shared__ double s_sum;
+  __shared__ float s_mx;
+  const uint32_t t = threadIdx.x;
+  if (t == 0) {
+    float mx = -INFINITY;
+    for (uint32_t j = 0; j < n; ++j) mx = fmaxf(mx, kept[j]);
+    s_mx = mx;
+  }
+  __syncthreads();
+  const double mx = (double)s_mx;
+  const bool fin = s_mx > -INFINITY && s_mx < INFINITY;
+  if (t < n && fin) e[t] = kept[t] == -INFINITY ? 0.0 : sh_exp_neg((double)kept[t] - mx, tab);
+  __syncthreads();
+  if (t == 0 && fin) {
+    double s = 0.0;
+    for (uint32_t j = 0; j < n; ++j) s += e[j];
+    s_sum = s;
+  }
+  __syncthreads();
+  if (t < n) pr[t] = fin ? (float)(e[t] / s_sum) : 1.0f / (float)n;
+  __syncthreads();
+}
+
+// The filtered draw of one row (256 threads) with uniform u; returns the id.
+__device__ uint32_t sample_filtered_row(const float* __restrict__ x, uint32_t V, const FiltCfg& cf, float u,
+                                        const double* tab) {
+  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t wsum[4];
+  __shared__ uint32_t s_prefix, s_need, s_n;
+  __shared__ unsigned long long cand[kTopKMax];
+  __shared__ float kept[kTopKMax], pr[kTopKMax];
+  __shared__ double e[kTopKMax];
+  __shared__ uint32_t s_ch;
+  const uint32_t t = threadIdx.x, k = cf.k;
+  // ---- radix select: the k-th largest key (prefix) and how many of the
+  // keys equal to it are taken (need)
+  if (t == 0) { s_prefix = 0; s_need = k; }
+  constexpr int kShift[3] = {21, 10, 0};
+  constexpr int kBits[3] = {11, 11, 10};
+#pragma unroll
+  for (int ps = 0; ps < 3; ++ps) {
+    const uint32_t nb = 1u << kBits[ps];
+    for (uint32_t i = t; i < 2048; i += 256) hist[i] = 0;
+    __syncthreads();
+    const uint32_t hi_shift = kShift[ps] + kBits[ps];  // bits above this digit must match the prefix
+    const uint32_t prefix = s_prefix, need = s_need;     // read before this pass's crossing thread writes
+    for (uint32_t i = t; i < V; i += 256) {
+      const uint32_t key = ord_key(x[i]);
+      if (hi_shift == 32 || (key >> hi_shift) == (prefix >> hi_shift))
+        atomicAdd(&hist[(key >> kShift[ps]) & (nb - 1)], 1u);
+    }
+    __syncthreads();
+    // thread t owns bins [8 t, 8 t + 8) counted from the top (bin nb - 1 - i)
+    const uint32_t per = nb / 256;
+    uint32_t c = 0;
+    for (uint32_t j = 0; j < per; ++j) c += hist[nb - 1 - (per * t + j)];
+    const uint32_t above = block_exscan_u(c, wsum, nullptr);
+    if (above < need && above + c >= need) {  // the crossing bin is in this thread's range
+      uint32_t a = above;
+      for (uint32_t j = 0; j < per; ++j) {
+        const uint32_t bin = nb - 1 - (per * t + j), h = hist[bin];
+        if (a + h >= need) {
+          s_prefix = prefix | (bin << kShift[ps]);
+          s_need = need - a;
+          break;
+        }
+        a += h;
+      }
+    }
+    __syncthreads();
+  }
+  const uint32_t tau = s_prefix, ties = s_need;  // keys > tau: k - ties of them; plus `ties` keys == tau
+  // ---- collect: keys above tau in any order, ties at tau by index
+  if (t == 0) s_n = 0;
+  __syncthreads();
+  uint32_t n_eq = 0;
+  for (uint32_t i = t; i < V; i += 256) {
+    const uint32_t key = ord_key(x[i]);
+    if (key > tau) {
+      const uint32_t pos = atomicAdd(&s_n, 1u);
+      if (pos < kTopKMax) cand[pos] = ((unsigned long long)key << 32) | (unsigned long long)(~i);
+    }
+    n_eq += key == tau;
+  }
+  uint32_t eq_total;
+  (void)block_exscan_u(n_eq, wsum, &eq_total);
+  if (eq_total == ties) {  // every key equal to tau is taken
+    for (uint32_t i = t; i < V; i += 256)
+      if (ord_key(x[i]) == tau) {
+        const uint32_t pos = atomicAdd(&s_n, 1u);
+        if (pos < kTopKMax) cand[pos] = ((unsigned long long)tau << 32) | (unsigned long long)(~i);
+      }
+  } else {  // the first `ties` of them in index order: thread t owns a contiguous slice
+    const uint32_t C = (V + 255) / 256, b0 = min(t * C, V), b1 = min(b0 + C, V);
+    uint32_t mine = 0;
+    for (uint32_t i = b0; i < b1; ++i) mine += ord_key(x[i]) == tau;
+    uint32_t rank = block_exscan_u(mine, wsum, nullptr);
+    const uint32_t base = k - ties;
+    for (uint32_t i = b0; i < b1 && rank < ties; ++i)
+      if (ord_key(x[i]) == tau) {
+        cand[base + rank] = ((unsigned long long)tau << 32) | (unsigned long long)(~i);
+        ++rank;
+      }
+  }
+  __syncthreads();
+  // ---- bitonic sort of the k candidates, descending (padding sorts last)
+  if (t >= k) cand[t] = 0ull;
+  __syncthreads();
+  for (uint32_t size = 2; size <= kTopKMax; size <<= 1)
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t j = t ^ stride;
+      if (j > t) {
+        const unsigned long long a = cand[t], b = cand[j];
+        const bool desc = (t & size) == 0;
+        if (desc ? a < b : a > b) { cand[t] = b; cand[j] = a; }
+      }
+      __syncthreads();
+    }
+  // ---- the chain over the sorted candidates
+  if (t < k) kept[t] = key_value((uint32_t)(cand[t] >> 32));
+  __syncthreads();
+  if (cf.flags & 1u) {  // top_p
+    cand_softmax(kept, k, pr, e, tab);
+    if (t == 0) {
+      double cum = 0.0;
+      for (uint32_t j = 0; j < k; ++j) {
+        if (cum > (double)cf.top_p) kept[j] = -INFINITY;
+        cum += (double)pr[j];
+      }
+    }
+    __syncthreads();
+  }
+  if (cf.flags & 2u) {  // min_p, against the largest candidate
+    const float cut = kept[0] + cf.log_min_p;
+    __syncthreads();
+    if (t < k && kept[t] < cut) kept[t] = -INFINITY;
+    __syncthreads();
+  }
+  if (cf.flags & 4u) {  // temperature
+    if (t < k && kept[t] > -INFINITY && kept[t] < INFINITY) kept[t] *= cf.inv_t;
+    __syncthreads();
+  }
+  cand_softmax(kept, k, pr, e, tab);
+  if (t == 0) {
+    double cum = 0.0;
+    uint32_t ch = k - 1;
+    for (uint32_t j = 0; j < k; ++j) {
+      cum += (double)pr[j];
+      if (cum >= (double)u) { ch = j; break; }
+    }
+    s_ch = ch;
+  }
+  __syncthreads();
+  return ~(uint32_t)(cand[s_ch] & 0xFFFFFFFFull);
+}
+
+// COMPARE with filters: row r of p draws with Philox word word0 + wstride r
+// (or explicit u_dev[...]), as k_sample_cols.
+__global__ __launch_bounds__(256) void k_sample_filtered_cols(const float* __restrict__ p, uint32_t V, FiltCfg cf,
+                                                              const float* u_dev, uint64_t seed, uint64_t word0,
+                                                              uint64_t wstride, uint32_t* __restrict__ out) {
+  __shared__ double tab[64];
+  const uint32_t row = blockIdx.x;
+  load_exp_table(tab);
+  __syncthreads();
+  const float u = uniform_at(u_dev, seed, word0 + wstride * row);
+  const uint32_t tok = sample_filtered_row(p + (size_t)row * V, V, cf, u, tab);
+  if (threadIdx.x == 0) out[row] = tok;
+}
+
+// Batched verify rows with filters (rows[r].top_k > 0); other rows are left alone.
+__global__ __launch_bounds__(256) void k_sample_filtered_tab(const float* __restrict__ p, uint32_t V,
+                                                             const SampRow* __restrict__ rows,
+                                                             uint32_t* __restrict__ out) {
+  __shared__ double tab[64];
+  const uint32_t row = blockIdx.x;
+  const SampRow sr = rows[row];
+  if (sr.greedy || sr.top_k == 0) return;  // uniform
+  load_exp_table(tab);
+  __syncthreads();
+  const FiltCfg cf{sr.top_k, sr.top_p, sr.log_min_p, sr.inv_t_f, sr.filt_flags};
+  const float u = sr.explicit_u ? sr.u : uniform_at(nullptr, sr.seed, sr.word);
+  const uint32_t tok = sample_filtered_row(p + (size_t)row * V, V, cf, u, tab);
   if (threadIdx.x == 0) out[row] = tok;
 }
 
@@ -868,6 +1112,10 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   SH_CHECK(mode == SH_SAMPLE_COMPARE || mode == SH_SAMPLE_REJECTION, SH_ERR_ARG, "accept: mode %u", mode);
   SH_CHECK(s->temperature > 0.f, SH_ERR_ARG, "accept: temperature must be > 0");
   SH_CHECK(mode != SH_SAMPLE_REJECTION || q_logits, SH_ERR_ARG, "REJECTION needs draft logits");
+  SampRow filt{};
+  if (int rc = sh_samprow_filters(*s, V, filt)) return rc;
+  SH_CHECK(!filt.top_k || mode == SH_SAMPLE_COMPARE, SH_ERR_UNSUPPORTED,
+           "candidate filters (top_k / top_p / min_p) apply to COMPARE only");
   const double inv_t = 1.0 / (double)s->temperature;
   const uint32_t n_p = B * (k + 1), n_q = mode == SH_SAMPLE_REJECTION ? B * k : 0;
   const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE), nrows = n_p + n_q;
@@ -883,16 +1131,24 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   uint32_t* small = reinterpret_cast<uint32_t*>(sbuf + part_b + chunk_b + rstat_b);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  if (V % 4 == 0)
+  if (filt.top_k) {  // the filtered draw reads its rows itself
+  } else if (V % 4 == 0) {
     hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nunits), dim3(256), 0, e->stream, p_logits, n_p, q_logits,
                        V, inv_t, nch, part);
-  else
+  } else {
     hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nunits), dim3(256), 0, e->stream, p_logits, n_p, q_logits,
                        V, inv_t, nch, part);
+  }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_stats", 4.0 * V * (n_p + n_q), ev);
   sh_prof_begin(e, &ev);
-  if (mode == SH_SAMPLE_COMPARE) {
+  if (mode == SH_SAMPLE_COMPARE && filt.top_k) {
+    const FiltCfg cf{filt.top_k, filt.top_p, filt.log_min_p, filt.inv_t_f, filt.filt_flags};
+    hipLaunchKernelGGL(k_sample_filtered_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, V, cf, uniforms_dev,
+                       s->seed, counter + 1ull, 2ull, small);
+    hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
+                       next_tok);
+  } else if (mode == SH_SAMPLE_COMPARE) {
     hipLaunchKernelGGL(k_sample_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, part, nch, V, inv_t,
                        uniforms_dev, s->seed, counter + 1ull, 2ull, small);
     hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
@@ -932,18 +1188,22 @@ int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uin
 }
 
 int sh_sample_rows_tab_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, const SampRow* rows_dev,
-                              double2* part, uint32_t* out) {
+                              double2* part, uint32_t* out, bool plain, bool filtered) {
   SH_CHECK(nrows >= 1 && V >= 1, SH_ERR_ARG, "sample_rows_tab: nrows=%u V=%u", nrows, V);
   const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  if (V % 4 == 0)
-    hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
-                       nullptr, V, 1.0, nch, part, rows_dev);
-  else
-    hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
-                       nullptr, V, 1.0, nch, part, rows_dev);
-  hipLaunchKernelGGL(k_sample_rows_tab, dim3(nrows), dim3(256), 0, e->stream, logits, part, nch, V, rows_dev, out);
+  if (plain) {
+    if (V % 4 == 0)
+      hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
+                         nullptr, V, 1.0, nch, part, rows_dev);
+    else
+      hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
+                         nullptr, V, 1.0, nch, part, rows_dev);
+    hipLaunchKernelGGL(k_sample_rows_tab, dim3(nrows), dim3(256), 0, e->stream, logits, part, nch, V, rows_dev, out);
+  }
+  if (filtered)
+    hipLaunchKernelGGL(k_sample_filtered_tab, dim3(nrows), dim3(256), 0, e->stream, logits, V, rows_dev, out);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "sample_rows", 4.0 * V * nrows, ev);
   return SH_OK;
@@ -951,6 +1211,25 @@ int sh_sample_rows_tab_launch(sh_engine* e, const float* logits, uint32_t nrows,
 
 size_t sh_sample_rows_part_bytes(uint32_t nrows, uint32_t V) {
   return (size_t)nrows * ((V + 256 * kStatE - 1) / (256 * kStatE)) * sizeof(double2);
+}
+
+int sh_samprow_filters(const sh_sampling& s, uint32_t V, SampRow& r) {
+  const bool top_p_on = s.top_p < 1.0f && s.top_p > 0.0f, min_p_on = s.min_p > 0.0f;
+  r.top_k = 0;
+  r.filt_flags = 0;
+  if (s.top_k == 0) {
+    SH_CHECK(!top_p_on && !min_p_on, SH_ERR_UNSUPPORTED,
+             "top_p / min_p need top_k in 1..%u (the GPU chain filters sorted top_k candidates)", kTopKMax);
+    return SH_OK;
+  }
+  const uint32_t k = s.top_k < V ? s.top_k : V;  // as the host chain (sample.rs:404-409)
+  SH_CHECK(k <= kTopKMax, SH_ERR_UNSUPPORTED, "top_k %u (of V = %u) above %u", s.top_k, V, kTopKMax);
+  r.top_k = k;
+  r.top_p = s.top_p;
+  r.log_min_p = min_p_on ? logf(s.min_p) : 0.0f;
+  r.inv_t_f = 1.0f / fmaxf(s.temperature, 1e-9f);
+  r.filt_flags = (top_p_on ? 1u : 0u) | (min_p_on ? 2u : 0u) | (fabsf(s.temperature - 1.0f) > 1e-9f ? 4u : 0u);
+  return SH_OK;
 }
 
 extern "C" int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
@@ -1015,6 +1294,8 @@ extern "C" int sh_tree_accept(sh_engine* e, const float* p_logits_dev, const flo
   SH_CHECK(greedy || s->mode == SH_SAMPLE_REJECTION, SH_ERR_ARG, "tree_accept: mode %u (GREEDY or REJECTION)",
            s->mode);
   SH_CHECK(greedy || q_logits_dev, SH_ERR_ARG, "tree_accept: rejection sampling needs draft logits");
+  SH_CHECK(greedy || (s->top_k == 0 && !(s->top_p > 0.f && s->top_p < 1.f) && !(s->min_p > 0.f)),
+           SH_ERR_UNSUPPORTED, "tree_accept: candidate filters (top_k / top_p / min_p) apply to COMPARE only");
   // tree shape is validated on the host copy (parents[i] < i, parents[0] = -1)
   std::vector<int32_t> par((size_t)B * n);
   SH_HIP(hipMemcpyAsync(par.data(), parents_dev, par.size() * 4, hipMemcpyDeviceToHost, e->stream));

@@ -435,12 +435,20 @@ struct SampRow {
   float u;            // explicit uniform (explicit_u)
   uint32_t greedy;    // keep the argmax already in out[row]
   uint32_t explicit_u;
+  uint32_t top_k;     // > 0: the filtered chain (sh_sample_filters)
+  float top_p, log_min_p, inv_t_f;
+  uint32_t filt_flags;
   uint32_t pad;
 };
-// Draws row r of logits [nrows][V] by rows_dev[r] (greedy rows untouched);
-// part: sh_sample_rows_part_bytes(nrows, V) of scratch.
+// The candidate filters of s for vocabulary V into r (top_k, top_p,
+// log_min_p, inv_t_f, filt_flags; top_k 0 = none); SH_ERR_UNSUPPORTED for
+// combinations the GPU chain does not take.
+int sh_samprow_filters(const sh_sampling& s, uint32_t V, SampRow& r);
+// Draws row r of logits [nrows][V] by rows_dev[r] (greedy rows untouched):
+// the temperature-only rows when plain, the filtered rows (top_k > 0) when
+// filtered; part: sh_sample_rows_part_bytes(nrows, V) of scratch.
 int sh_sample_rows_tab_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, const SampRow* rows_dev,
-                              double2* part, uint32_t* out);
+                              double2* part, uint32_t* out, bool plain, bool filtered);
 size_t sh_sample_rows_part_bytes(uint32_t nrows, uint32_t V);
 // Routed-expert FFN pieces (moe.hip): router logits [N][E] of the RMS-normed
 // columns, top-k per column (ids, wts [N][k]) with the routing plan over

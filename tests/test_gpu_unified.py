@@ -217,7 +217,8 @@ def test_unified_sampled_per_sequence(engine, model):
     Greedy sequences keep the argmax; COMPARE sequences draw column j from
     softmax(l / T) in vocab order with Philox word counter + j of key
     (seed, 0x5EC) or with their explicit uniforms[j], checked against the
-    oracle's sampler on the same returned logits."""
+    oracle's sampler on the same returned logits (the filtered chain against
+    or_sample_one)."""
     from seeker_amd._native import SH_SAMPLE_COMPARE, SH_SAMPLE_GREEDY, SH_SAMPLE_REJECTION, sh_sampling
     name, img, gm = model
     V = gm.vocab_size()
@@ -226,14 +227,18 @@ def test_unified_sampled_per_sequence(engine, model):
     lens = [n for _, n in SEQS]
     toks = np.concatenate(drafts)
     u_explicit = S.normal_f32(3, 3, lens[2], 0.5, 0.2).clip(0.01, 0.99).astype(np.float32)
+    # the last sequence samples through the candidate filters (top_k 50, top_p 0.9, min_p 0.05)
     cfg = [(SH_SAMPLE_GREEDY, 0.0, 0, 0, None), (SH_SAMPLE_COMPARE, 0.8, 5, 7, None),
            (SH_SAMPLE_COMPARE, 1.3, 0, 0, u_explicit), (SH_SAMPLE_COMPARE, 0.5, 9, 0, None)]
+    filters = [None, None, None, (50, 0.9, 0.05)]
     samplers = []
-    for mode, t, seed, ctr, u in cfg:
+    for (mode, t, seed, ctr, u), f in zip(cfg, filters):
         sp = sh_sampling()
         sp.mode, sp.temperature, sp.seed, sp.counter = mode, t, seed, ctr
         if u is not None:
             sp.uniforms = u.ctypes.data_as(N.F32P)
+        if f is not None:
+            sp.top_k, sp.top_p, sp.min_p = f
         samplers.append(sp)
     kv = [_prefilled(engine, gm, pr) for pr in prompts]
     # a REJECTION sampler is refused before anything runs
@@ -252,6 +257,11 @@ def test_unified_sampled_per_sequence(engine, model):
         if mode == SH_SAMPLE_GREEDY:
             want = lg.argmax(axis=1)
             assert samplers[s].counter == 0
+        elif filters[s] is not None:
+            us = O.philox_uniforms(seed, 0x5EC, ctr, n)
+            ocfg = O.SamplerCfg(t, *filters[s])
+            want = [O.sample_one(lg[j], ocfg, float(us[j])) for j in range(n)]
+            assert samplers[s].counter == ctr + n
         else:
             us = u if u is not None else O.philox_uniforms(seed, 0x5EC, ctr, n)
             want = [O.sample_vocab_order(lg[j], t, float(us[j])) for j in range(n)]

@@ -749,3 +749,34 @@ def test_mixed_type_forward_matches_numpy(shape):
         np.testing.assert_allclose(lg, rl, rtol=1e-3, atol=1e-3 * np.abs(rl).max())
         kv.close()
         m.close()
+
+
+def test_sample_one_filters_closed_forms():
+    """The host chain's candidate filters (inference/sample.rs:404-473) on rows
+    whose filtered distributions are known in closed form."""
+    probs = np.array([0.05, 0.5, 0.15, 0.3])  # sorted desc: ids 1, 3, 2, 0
+    lg = np.log(probs).astype(np.float32)
+    # top_p 0.6: exclusive cumulative 0, 0.5, 0.8 -> ids 1, 3 kept (the crossing one stays),
+    # renormalised 0.625 / 0.375
+    c = O.SamplerCfg(1.0, 0, 0.6, 0.0)
+    assert O.sample_one(lg, c, 0.6) == 1
+    assert O.sample_one(lg, c, 0.63) == 3
+    assert O.sample_one(lg, c, 0.999) == 3
+    # top_p 0.5: exclusive cumulative of id 3 is 0.5, not above 0.5 -> still kept
+    assert O.sample_one(lg, O.SamplerCfg(1.0, 0, 0.5, 0.0), 0.999) == 3
+    # min_p 0.4: keep p >= 0.4 * 0.5 = 0.2 -> ids 1, 3 (0.15 dropped)
+    c = O.SamplerCfg(1.0, 0, 1.0, 0.4)
+    assert O.sample_one(lg, c, 0.999) == 3
+    assert O.sample_one(lg, c, 0.62) == 1
+    # top_k 3 then T = 2: weights sqrt(p) over ids 1, 3, 2
+    w = np.sqrt(np.array([0.5, 0.3, 0.15]))
+    cum = np.cumsum(w / w.sum())
+    c = O.SamplerCfg(2.0, 3, 1.0, 0.0)
+    for u, want in [(cum[0] - 1e-3, 1), (cum[0] + 1e-3, 3), (cum[1] + 1e-3, 2), (0.9999, 2)]:
+        assert O.sample_one(lg, c, float(u)) == want, u
+    # top_p before min_p: top_p 0.6 keeps ids 1, 3; min_p 0.7 then keeps id 1 only
+    assert O.sample_one(lg, O.SamplerCfg(1.0, 0, 0.6, 0.7), 0.999) == 1
+    # ties at the top_k threshold go to the lower id
+    t = np.array([1.0, 2.0, 2.0, 0.0, 2.0], np.float32)
+    assert O.sample_one(t, O.SamplerCfg(1.0, 2, 1.0, 0.0), 0.999) == 2
+    assert O.sample_one(t, O.SamplerCfg(1.0, 2, 1.0, 0.0), 0.1) == 1
