@@ -25,6 +25,11 @@
 #include "sh_internal.h"
 #include "sh_operand.h"
 
+// Scores run in base 2: the score scale carries log2(e), exponentials are the
+// hardware exp2 (v_exp_f32), and the split maxima go out in natural units
+// (times ln 2), the units the split combine works in.
+constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.69314718055994531f;
+
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 struct alignas(16) u32x4a { uint32_t x, y, z, w; };
@@ -199,12 +204,12 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
     const float mnew = fmaxf(mrow, mx);
     // nothing visible yet: keep O and l (zero) as they are
     const bool none = mnew == -INFINITY;
-    const float alpha = none ? 1.0f : expf(mrow - mnew);
+    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(mrow - mnew);
     // probabilities carry a 2^12 factor (keeps their f16 low halves normal);
     // it cancels in O / l because l is summed from the same scaled values
     float p[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : expf(sv[t] - mnew) * 4096.0f;
+    for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : __builtin_amdgcn_exp2f(sv[t] - mnew) * 4096.0f;
     mrow = mnew;
     float ps = 0.f;
 #pragma unroll
@@ -242,12 +247,12 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
   float M = mrow;
 #pragma unroll
   for (int w = 0; w < NKB - 1; ++w) M = fmaxf(M, sm[qg][w][r]);
-  const float f0 = mrow == -INFINITY ? 0.f : expf(mrow - M);
+  const float f0 = mrow == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow - M);
   float fw[KL];
   float L = lrow * f0;
 #pragma unroll
   for (int w = 0; w < NKB - 1; ++w) {
-    fw[w] = sm[qg][w][r] == -INFINITY ? 0.f : expf(sm[qg][w][r] - M);
+    fw[w] = sm[qg][w][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sm[qg][w][r] - M);
     L += sl[qg][w][r] * fw[w];
   }
   float* dst = part + (((size_t)kh * n_splits + split) * n_rows_pad + blockIdx.z * ROWS + 16 * qg + r) * PS;
@@ -261,7 +266,7 @@ __global__ __launch_bounds__(64 * NQG * NKB) void k_fa(const float* __restrict__
     }
     *(float4*)(dst + 16 * dt + 4 * g) = v;
   }
-  if (g == 0) *(float4*)(dst + HD) = make_float4(M, L, 0.f, 0.f);
+  if (g == 0) *(float4*)(dst + HD) = make_float4(M * kLn2, L, 0.f, 0.f);  // natural units for the combine
 }
 
 // Workgroup = (kv head, key split of 32 NKB keys, 32 query rows) of NKB
@@ -439,7 +444,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
     const bool none = mx == -INFINITY;
     float p[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : expf(sv[t] - mx) * 4096.0f;
+    for (int t = 0; t < 8; ++t) p[t] = none ? 0.0f : __builtin_amdgcn_exp2f(sv[t] - mx) * 4096.0f;
     float ps = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; ++t) ps += p[t];
@@ -471,7 +476,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
 #pragma unroll
     for (int b = 0; b < NKB; ++b) {
       const float mb = sm[b][row];
-      const float f = mb == -INFINITY ? 0.f : expf(mb - M);
+      const float f = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
       L += sl[b][row] * f;
       const float4 a = so[b][row][dq], c = so[b][row][dq + 1];
       o0.x += a.x * f; o0.y += a.y * f; o0.z += a.z * f; o0.w += a.w * f;
@@ -480,7 +485,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
     float* dst = part + (((size_t)kh * n_splits + split) * n_rows_pad + blockIdx.z * ROWS + row) * PS;
     *(float4*)(dst + 4 * dq) = o0;
     *(float4*)(dst + 4 * dq + 4) = o1;
-    if (lane % LPR == 0) *(float4*)(dst + HD) = make_float4(M, L, 0.f, 0.f);
+    if (lane % LPR == 0) *(float4*)(dst + HD) = make_float4(M * kLn2, L, 0.f, 0.f);  // natural units
   }
 }
 
@@ -592,7 +597,7 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
   const uint16_t* vc = kv->v + layer_k * fa.layer;
   SH_CHECK(fa.N >= 1 && (fa.N <= 8 || fa.masks) && fa.col0 + fa.N <= SH_MAX_COLS, SH_ERR_ARG,
            "attention columns [%u, %u) outside the chunk (more than 8 need device masks)", fa.col0, fa.col0 + fa.N);
-  const float scale = 1.0f / sqrtf((float)m->hd);
+  const float scale = kLog2e / sqrtf((float)m->hd);  // scores in base 2
   q += (size_t)fa.col0 * m->n_head * m->hd;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);

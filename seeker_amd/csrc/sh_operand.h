@@ -128,7 +128,7 @@ __device__ __forceinline__ void sh_operand_store_sb(float4 v, uint32_t K, uint32
 // Attention split combine for one lane: output elements 256 sb + 4 lane .. +3
 // of column col (a 256-wide superblock of heads), merging the n_splits key
 // splits of the partial buffer in split order, 16 at a time (the loads of NCH
-// such chunks issued before the first is used, one exp per split). Partial layout:
+// such chunks issued before the first is used, one hardware exp2 per split). Partial layout:
 // part[((kh * n_layout + split) * rows_pad + rho) * (hd + 4) + {d < hd: O, hd: m,
 // hd + 1: l}], rho = (head % gqa) * N + col. Zero for elements past Dq.
 template <uint32_t NCH = 1>
@@ -180,13 +180,13 @@ __device__ __forceinline__ float4 sh_fa_combine4(const float* __restrict__ part,
       for (uint32_t j = 0; j < CH; ++j) mc = fmaxf(mc, ml[hh][j].x);  // repeats of the last split change nothing
       if (mc == -INFINITY) continue;
       const float mn = fmaxf(M, mc);
-      const float a = expf(M - mn);  // 0 on the first chunk (M = -inf)
+      const float a = __builtin_amdgcn_exp2f((M - mn) * 1.4426950408889634f);  // 0 on the first chunk (M = -inf)
       acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
       L *= a;
 #pragma unroll
       for (uint32_t j = 0; j < CH; ++j) {
         // 0 for an empty split (m = -inf) and for the clamped repeats past the end
-        const float w = s0 + j < n_splits ? expf(ml[hh][j].x - mn) : 0.0f;
+        const float w = s0 + j < n_splits ? __builtin_amdgcn_exp2f((ml[hh][j].x - mn) * 1.4426950408889634f) : 0.0f;
         acc.x += os[hh][j].x * w; acc.y += os[hh][j].y * w; acc.z += os[hh][j].z * w; acc.w += os[hh][j].w * w;
         L += ml[hh][j].y * w;
       }
@@ -197,10 +197,10 @@ __device__ __forceinline__ float4 sh_fa_combine4(const float* __restrict__ part,
       // carry weight 0)
       if (mlx.x != -INFINITY) {
         const float mn = fmaxf(M, mlx.x);
-        const float a = expf(M - mn);
+        const float a = __builtin_amdgcn_exp2f((M - mn) * 1.4426950408889634f);
         acc.x *= a; acc.y *= a; acc.z *= a; acc.w *= a;
         L *= a;
-        const float w = expf(mlx.x - mn);
+        const float w = __builtin_amdgcn_exp2f((mlx.x - mn) * 1.4426950408889634f);
         acc.x += ox.x * w; acc.y += ox.y * w; acc.z += ox.z * w; acc.w += ox.w * w;
         L += mlx.y * w;
         M = mn;
