@@ -92,12 +92,16 @@ __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, 
 
 // Top-k selection and routing plan in one workgroup of 1024 threads for
 // P = N k <= 512 (column, slot) pairs.
-//  * Top-k: wave w takes columns w, w + 16, ...; lane l holds logits l, l + 64,
-//    ...; k rounds pick the largest remaining logit (a DPP wave max, then the
-//    lowest expert index holding it by ballot; softmax is monotone, so this is
-//    the top-k of the probabilities, ties to the lower expert index), and the
-//    weights exp(l_j - l_max) / sum over the selection in f64 (the full
-//    softmax denominator cancels in the renormalization).
+//  * Top-k: k rounds pick the largest remaining logit, then the lowest expert
+//    index holding it (softmax is monotone, so this is the top-k of the
+//    probabilities, ties to the lower expert index), and the weights
+//    exp(l_j - l_max) / sum over the selection in f64, summed in selection
+//    order (the full softmax denominator cancels in the renormalization).
+//    For k <= 8 (G8) an 8-lane group takes a column, so a wave selects for 8
+//    columns at once (12 -> ~2 us for 56 columns of 128 experts); otherwise
+//    wave w takes columns w, w + 16, ... with lane l holding logits l, l + 64,
+//    ... (DPP wave max, then the lowest index by ballot). Both give the same
+//    selections and weights.
 //  * Plan: pair p = column * k + slot has expert ids[p]. Pairs are sorted by
 //    expert, within an expert by p: a bitmap of pairs per expert gives each
 //    pair's rank by population counts, a wave scan over the experts their
@@ -105,7 +109,13 @@ __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, 
 //    pair_col[s]. Each expert's run of pairs is cut into chunks of at most 8:
 //    info[0] = number of chunks, info[1 + 3c .. +3] = (expert, first sorted
 //    pair, count), chunks in expert order.
-template <int RL>
+template <int SHIFT_CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, SHIFT_CTRL, 0xF, 0xF, false);
+}
+
+// G8: top-k by 8-lane groups (k <= 8, E <= 64 RL), else one wave per column.
+template <int RL, bool G8>
 __global__ __launch_bounds__(1024) void k_moe_plan(const float* __restrict__ logits, uint32_t N, uint32_t E,
                                                   uint32_t k, uint32_t* __restrict__ ids, float* __restrict__ wts,
                                                   uint32_t* __restrict__ info, uint32_t* __restrict__ pair_col,
@@ -117,67 +127,121 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const float* __restrict__ log
   const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint32_t P = N * k, nw = (P + 31) / 32;
   for (uint32_t i = t; i < E * NW; i += 1024) bm[i] = 0u;
-  for (uint32_t cb = wave; cb < N; cb += 64) {  // the wave's next 4 columns cb + 16 i: loads issued together
-    float pre[4][RL];
+  if constexpr (G8) {
+    // 8 lanes per column, 8 columns per wave: lane q of a group holds experts
+    // q, q + 8, ... (VPL of them); a round is a local max, a 3-step DPP max
+    // over the group, the lowest index holding it (local search, 3-step DPP
+    // min), so all of a wave's columns select at once
+    constexpr uint32_t VPL = 8 * RL;  // experts per lane: E <= 8 * VPL
+    const uint32_t q = lane & 7, grp = lane >> 3;
+    for (uint32_t pass = 0; 128 * pass < N; ++pass) {  // uniform over the wave
+      const uint32_t col = 128 * pass + 8 * wave + grp;
+      const bool active = col < N;
+      // a taken expert (and the padding past E) holds NaN: fmaxf skips it and
+      // no comparison matches it; NaN logits rank as -inf
+      float lv[VPL];
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i)
-#pragma unroll
-      for (uint32_t r = 0; r < RL; ++r) {
-        const uint32_t col = cb + 16 * i;
-        pre[i][r] = col < N && lane + 64 * r < E ? logits[(size_t)col * E + lane + 64 * r] : -INFINITY;
+      for (uint32_t r = 0; r < VPL; ++r) {
+        const uint32_t ex = q + 8 * r;
+        const float v = active && ex < E ? logits[(size_t)col * E + ex] : -INFINITY;
+        lv[r] = ex >= E ? __builtin_nanf("") : (v != v ? -INFINITY : v);
       }
+      uint32_t sel_e = 0;
+      float sel_l = 0.f, l0 = 0.f;
+      for (uint32_t j = 0; j < k; ++j) {
+        float lm = lv[0];
 #pragma unroll
-  for (uint32_t i = 0; i < 4; ++i) {
-    const uint32_t col = cb + 16 * i;
-    if (col >= N) break;
-    // lane l holds experts l, l + 64, ...; NaN ranks as -inf
-    float lv[RL];
-    bool taken[RL];
+        for (uint32_t r = 1; r < VPL; ++r) lm = fmaxf(lm, lv[r]);
+        lm = fmaxf(lm, sh_dpp<SH_DPP_XOR1>(lm));
+        lm = fmaxf(lm, sh_dpp<SH_DPP_XOR2>(lm));
+        const float m = fmaxf(lm, sh_dpp<SH_DPP_HALF_MIRROR>(lm));
+        uint32_t rr = VPL;
 #pragma unroll
-    for (uint32_t r = 0; r < RL; ++r) {
-      const float v = pre[i][r];
-      lv[r] = v != v ? -INFINITY : v;
-      taken[r] = lane + 64 * r >= E;
+        for (int r = VPL - 1; r >= 0; --r)
+          if (lv[r] == m) rr = (uint32_t)r;
+        uint32_t ce = rr < VPL ? q + 8 * rr : 0xFFFFFFFFu;
+        ce = min(ce, dpp_u32<SH_DPP_XOR1>(ce));
+        ce = min(ce, dpp_u32<SH_DPP_XOR2>(ce));
+        const uint32_t e = min(ce, dpp_u32<SH_DPP_HALF_MIRROR>(ce));
+#pragma unroll
+        for (uint32_t r = 0; r < VPL; ++r)
+          if (e == q + 8 * r) lv[r] = __builtin_nanf("");
+        if (q == j) { sel_e = e; sel_l = m; }
+        if (j == 0) l0 = m;
+      }
+      // weights exp(l_j - l_0) / sum_j exp(l_j - l_0) in f64, summed in selection order
+      const double w = q < k ? exp((double)sel_l - (double)l0) : 0.0;
+      double wsum = 0.0;
+      for (uint32_t j = 0; j < k; ++j) wsum += __shfl(w, (int)(8 * grp + j));
+      if (active && q < k) {
+        ids[(size_t)col * k + q] = sel_e;
+        wts[(size_t)col * k + q] = (float)(w / wsum);
+        sid[col * k + q] = min(sel_e, E - 1);
+      }
     }
-    // round j: the largest value not yet taken (DPP wave max), then the lowest
-    // expert index holding it (ballots, lowest r first); lane j keeps it
-    uint32_t sel_e = 0;
-    float sel_l = 0.f;
-    for (uint32_t j = 0; j < k; ++j) {
-      float lm = -INFINITY;
-#pragma unroll
-      for (uint32_t r = 0; r < RL; ++r) lm = taken[r] ? lm : fmaxf(lm, lv[r]);
-      const float m = sh_wave_max(lm);
-      uint32_t e = 0;
-      bool found = false;
-#pragma unroll
-      for (uint32_t r = 0; r < RL; ++r) {
-        const unsigned long long b = __ballot(!taken[r] && lv[r] == m);
-        if (!found && b) {
-          e = 64 * r + (uint32_t)__ffsll((long long)b) - 1;
-          found = true;
+  } else {
+    for (uint32_t cb = wave; cb < N; cb += 64) {  // the wave's next 4 columns cb + 16 i: loads issued together
+      float pre[4][RL];
+  #pragma unroll
+      for (uint32_t i = 0; i < 4; ++i)
+  #pragma unroll
+        for (uint32_t r = 0; r < RL; ++r) {
+          const uint32_t col = cb + 16 * i;
+          pre[i][r] = col < N && lane + 64 * r < E ? logits[(size_t)col * E + lane + 64 * r] : -INFINITY;
         }
+  #pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t col = cb + 16 * i;
+      if (col >= N) break;
+      // lane l holds experts l, l + 64, ...; NaN ranks as -inf
+      float lv[RL];
+      bool taken[RL];
+  #pragma unroll
+      for (uint32_t r = 0; r < RL; ++r) {
+        const float v = pre[i][r];
+        lv[r] = v != v ? -INFINITY : v;
+        taken[r] = lane + 64 * r >= E;
       }
-#pragma unroll
-      for (uint32_t r = 0; r < RL; ++r) taken[r] = taken[r] || lane + 64 * r == e;
-      if (lane == j) { sel_e = e; sel_l = m; }
+      // round j: the largest value not yet taken (DPP wave max), then the lowest
+      // expert index holding it (ballots, lowest r first); lane j keeps it
+      uint32_t sel_e = 0;
+      float sel_l = 0.f;
+      for (uint32_t j = 0; j < k; ++j) {
+        float lm = -INFINITY;
+  #pragma unroll
+        for (uint32_t r = 0; r < RL; ++r) lm = taken[r] ? lm : fmaxf(lm, lv[r]);
+        const float m = sh_wave_max(lm);
+        uint32_t e = 0;
+        bool found = false;
+  #pragma unroll
+        for (uint32_t r = 0; r < RL; ++r) {
+          const unsigned long long b = __ballot(!taken[r] && lv[r] == m);
+          if (!found && b) {
+            e = 64 * r + (uint32_t)__ffsll((long long)b) - 1;
+            found = true;
+          }
+        }
+  #pragma unroll
+        for (uint32_t r = 0; r < RL; ++r) taken[r] = taken[r] || lane + 64 * r == e;
+        if (lane == j) { sel_e = e; sel_l = m; }
+      }
+      // weights exp(l_j - l_0) / sum_j exp(l_j - l_0) in f64, summed in selection order
+      const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sel_l)));
+      const double w = lane < k ? exp((double)sel_l - (double)l0) : 0.0;
+      double wsum = 0.0;
+      for (uint32_t j = 0; j < k; ++j) {  // lane j's weight, read lane by lane (uniform j)
+        const unsigned long long wb = __builtin_bit_cast(unsigned long long, w);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)wb, (int)j);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(wb >> 32), (int)j);
+        wsum += __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+      }
+      if (lane < k) {
+        ids[(size_t)col * k + lane] = sel_e;
+        wts[(size_t)col * k + lane] = (float)(w / wsum);
+        sid[col * k + lane] = min(sel_e, E - 1);
+      }
     }
-    // weights exp(l_j - l_0) / sum_j exp(l_j - l_0) in f64, summed in selection order
-    const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sel_l)));
-    const double w = lane < k ? exp((double)sel_l - (double)l0) : 0.0;
-    double wsum = 0.0;
-    for (uint32_t j = 0; j < k; ++j) {  // lane j's weight, read lane by lane (uniform j)
-      const unsigned long long wb = __builtin_bit_cast(unsigned long long, w);
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)wb, (int)j);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(wb >> 32), (int)j);
-      wsum += __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
     }
-    if (lane < k) {
-      ids[(size_t)col * k + lane] = sel_e;
-      wts[(size_t)col * k + lane] = (float)(w / wsum);
-      sid[col * k + lane] = min(sel_e, E - 1);
-    }
-  }
   }
   __syncthreads();
   if (t < P) atomicOr(&bm[sid[t] * NW + (t >> 5)], 1u << (t & 31));
@@ -264,20 +328,36 @@ int sh_moe_route_launch(sh_engine* e, const float* x, const float* norm_w, const
   return SH_OK;
 }
 
+// SH_MOE_PLAN=wave: the wave-per-column top-k for every k (measurement switch).
+static bool moe_plan_g8() {
+  static const bool v = [] {
+    const char* s = getenv("SH_MOE_PLAN");
+    return !(s && std::string(s) == "wave");
+  }();
+  return v;
+}
+
 int sh_moe_plan_launch(sh_engine* e, const float* logits, uint32_t N, uint32_t E, uint32_t k, uint32_t* ids,
                        float* wts, uint32_t* info, uint32_t* pair_col, uint32_t* slot_of) {
   SH_CHECK(N >= 1 && k >= 1 && k <= 64 && k <= E && N * k <= 512 && E <= kMaxExperts, SH_ERR_ARG,
            "moe plan: N=%u k=%u E=%u", N, k, E);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  if (E <= 128)
-    hipLaunchKernelGGL(k_moe_plan<2>, dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info, pair_col,
-                       slot_of);
+  const bool g8 = k <= 8 && moe_plan_g8();
+  if (E <= 128 && g8)
+    hipLaunchKernelGGL((k_moe_plan<2, true>), dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info,
+                       pair_col, slot_of);
+  else if (E <= 256 && g8)
+    hipLaunchKernelGGL((k_moe_plan<4, true>), dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info,
+                       pair_col, slot_of);
+  else if (E <= 128)
+    hipLaunchKernelGGL((k_moe_plan<2, false>), dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info,
+                       pair_col, slot_of);
   else if (E <= 256)
-    hipLaunchKernelGGL(k_moe_plan<4>, dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info, pair_col,
-                       slot_of);
+    hipLaunchKernelGGL((k_moe_plan<4, false>), dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts, info,
+                       pair_col, slot_of);
   else
-    hipLaunchKernelGGL(k_moe_plan<kMaxExperts / 64>, dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts,
+    hipLaunchKernelGGL((k_moe_plan<kMaxExperts / 64, false>), dim3(1), dim3(1024), 0, e->stream, logits, N, E, k, ids, wts,
                        info, pair_col, slot_of);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "moe_plan", 0.0, ev);
