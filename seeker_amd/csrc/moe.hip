@@ -18,26 +18,20 @@ namespace {
 
 constexpr uint32_t kMaxExperts = 1024;
 
-// Router logits, one wave per (8 experts, CPW columns): logits[col][e] =
+// Router logits, one wave per (EPW experts, CPW columns): logits[col][e] =
 // rinv(col) * sum_i R[e][i] (x[col][i] norm_w[i]), rinv = 1 / sqrt(mean(x^2) +
 // eps) (the RMSNorm factor is linear, so it is applied to the dot product).
 // Lane l holds elements 4 l + 256 j (j < d / 256) of each of the wave's
-// columns in registers; router rows go two ahead of their use (16-byte loads),
-// and the sums reduce across the wave by DPP steps. The launch spreads the
-// router over E / 8 x ceil(N / CPW) waves.
-template <int NJ>
+// columns and router rows in registers, every load issued at the start (one
+// memory latency per wave), and the sums reduce across the wave by DPP steps.
+// The launch spreads the router over E / EPW x ceil(N / CPW) waves.
+template <int NJ, int EPW, int CPW>
 __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, const float* __restrict__ norm_w,
                                                    const float* __restrict__ R, uint32_t d, uint32_t E, uint32_t N,
                                                    float eps, float* __restrict__ logits) {
-  constexpr int CPW = NJ <= 8 ? 32 / NJ : 1, EPW = 8;
   const uint32_t lane = threadIdx.x, nj = d / 256;
   const uint32_t e0 = blockIdx.x * EPW, c0 = blockIdx.y * CPW;
-  auto load_row = [&](float4 (&rv)[NJ], uint32_t e) {
-    const float* r = R + (size_t)min(e, E - 1) * d + 4 * lane;  // past the last expert: a clamped (unused) read
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) rv[j] = (uint32_t)j < nj ? *(const float4*)(r + 256 * j) : float4{0.f, 0.f, 0.f, 0.f};
-  };
-  float4 xv[CPW][NJ];
+  float4 xv[CPW][NJ], rv[EPW][NJ];
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     const uint32_t col = c0 + c < N ? c0 + c : N - 1;  // past the last column: a clamped (unused) read
@@ -45,9 +39,12 @@ __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, 
 #pragma unroll
     for (int j = 0; j < NJ; ++j) xv[c][j] = (uint32_t)j < nj ? *(const float4*)(xc + 256 * j) : float4{0.f, 0.f, 0.f, 0.f};
   }
-  float4 rv[2][NJ];
-  load_row(rv[0], e0);
-  load_row(rv[1], e0 + 1);
+#pragma unroll
+  for (int ei = 0; ei < EPW; ++ei) {
+    const float* r = R + (size_t)min(e0 + ei, E - 1) * d + 4 * lane;  // past the last expert: a clamped (unused) read
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) rv[ei][j] = (uint32_t)j < nj ? *(const float4*)(r + 256 * j) : float4{0.f, 0.f, 0.f, 0.f};
+  }
   float rinv[CPW];
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
@@ -66,25 +63,18 @@ __global__ __launch_bounds__(64) void k_moe_logits(const float* __restrict__ x, 
   }
 #pragma unroll
   for (int ei = 0; ei < EPW; ++ei) {
-    const int b = ei & 1;
-    float acc[CPW];
+    const uint32_t e = e0 + ei;
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       float a = 0.f;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        a = __builtin_fmaf(rv[b][j].x, xv[c][j].x, a);
-        a = __builtin_fmaf(rv[b][j].y, xv[c][j].y, a);
-        a = __builtin_fmaf(rv[b][j].z, xv[c][j].z, a);
-        a = __builtin_fmaf(rv[b][j].w, xv[c][j].w, a);
+        a = __builtin_fmaf(rv[ei][j].x, xv[c][j].x, a);
+        a = __builtin_fmaf(rv[ei][j].y, xv[c][j].y, a);
+        a = __builtin_fmaf(rv[ei][j].z, xv[c][j].z, a);
+        a = __builtin_fmaf(rv[ei][j].w, xv[c][j].w, a);
       }
-      acc[c] = a;
-    }
-    if (ei + 2 < EPW) load_row(rv[b], e0 + ei + 2);
-    const uint32_t e = e0 + ei;
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const float sum = sh_wave_sum(acc[c]);
+      const float sum = sh_wave_sum(a);
       if (lane == 0 && c0 + c < N && e < E) logits[(size_t)(c0 + c) * E + e] = sum * rinv[c];
     }
   }
@@ -317,12 +307,12 @@ int sh_moe_route_launch(sh_engine* e, const float* x, const float* norm_w, const
            "moe route: n_embd %u (a multiple of 256 up to 4096)", d);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  if (d <= 2048)  // 4 columns per wave
-    hipLaunchKernelGGL(k_moe_logits<8>, dim3((E + 7) / 8, (N + 3) / 4), dim3(64), 0, e->stream, x, norm_w, router, d,
+  if (d <= 2048)  // 4 experts x 2 columns per wave
+    hipLaunchKernelGGL((k_moe_logits<8, 4, 2>), dim3((E + 3) / 4, (N + 1) / 2), dim3(64), 0, e->stream, x, norm_w,
+                       router, d, E, N, eps, logits);
+  else  // 2 experts x 1 column per wave
+    hipLaunchKernelGGL((k_moe_logits<16, 2, 1>), dim3((E + 1) / 2, N), dim3(64), 0, e->stream, x, norm_w, router, d,
                        E, N, eps, logits);
-  else  // 1 column per wave
-    hipLaunchKernelGGL(k_moe_logits<16>, dim3((E + 7) / 8, N), dim3(64), 0, e->stream, x, norm_w, router, d, E, N,
-                       eps, logits);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "moe_route", 4.0 * E * d, ev);
   return SH_OK;
