@@ -363,7 +363,7 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       dalloc(&w.xs, xs_elems) ||
       dalloc(&w.q, C * wide) || dalloc(&w.attn, C * wide) || dalloc(&w.gpart, gpart_floats) ||
       dalloc(&w.h, C * std::max(m->ff, 1u)) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
-      dalloc(&w.tokens, C + 64) || dalloc(&w.amax, C + 8) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
+      dalloc(&w.tokens, C + 64) || dalloc(&w.amax, SH_AMAX_WORDS) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
       dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
       dalloc(&w.cs2, sh_grp_cs(m->d)) || dalloc(&w.ssq2, sh_grp_cs(m->d)) || dalloc(&w.sb_cnt, SH_SB_CNT * SH_SB_CNT_STRIDE))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
@@ -372,7 +372,7 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   if (hipMemset(w.xs, 0, xs_elems * 2) != hipSuccess || hipMemset(w.bx, 0, bx_elems * 2) != hipSuccess ||
       hipMemset(w.xs2, 0, sh_grp_xs(m->d) * 2) != hipSuccess || hipMemset(w.bx2, 0, sh_grp_bx(m->d) * 2) != hipSuccess ||
       hipMemset(w.sb_cnt, 0, SH_SB_CNT * SH_SB_CNT_STRIDE * 4) != hipSuccess ||
-      hipMemset(w.amax, 0, (C + 8) * 8) != hipSuccess)
+      hipMemset(w.amax, 0, SH_AMAX_WORDS * 8) != hipSuccess)
     FAIL(SH_ERR_HIP, "workspace clear failed");
   if (m->n_expert) {
     const size_t P = C * m->n_used, ng = (P + 7) / 8;

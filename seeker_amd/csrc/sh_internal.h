@@ -40,6 +40,9 @@ __host__ __device__ constexpr bool sh_is_kquant(int type) {
   return type == GGML_Q4_K || type == GGML_Q5_K || type == GGML_Q6_K;
 }
 constexpr uint32_t SH_MAX_COLS = 64;     // columns per forward chunk (8 operand groups of 8)
+// argmax workspace (64-bit words): SH_MAX_COLS keys, then one arrival counter
+// per column, 64 bytes apart
+constexpr uint32_t SH_AMAX_WORDS = SH_MAX_COLS + 8 * SH_MAX_COLS;
 constexpr uint32_t SH_MAX_PREP_COLS = 512;  // operand columns one prep builds (the MoE down operand: pairs)
 constexpr int SH_FA_MIN_SPLIT_KEYS = 64;  // smallest key split of any attention launch (sizes fa_part)
 constexpr int SH_FA_MAX_ROWS = 256;       // padded query rows (gqa x columns) per kv head
@@ -138,7 +141,7 @@ struct Workspace {
   float* fa_part = nullptr;   // flash-attn split partials
   float* gpart = nullptr;     // GEMV split-K partials
   uint32_t* tokens = nullptr; // [cols + 16] device token ids
-  unsigned long long* amax = nullptr;  // [SH_MAX_COLS] packed argmax keys, then the argmax arrival counter (zeroed)
+  unsigned long long* amax = nullptr;  // SH_AMAX_WORDS: packed argmax keys, then per-column arrival counters (zeroed)
   float* cs = nullptr;        // [max(K)/256][8] inverse activation scales of the current B operand
   float* ssq = nullptr;       // [max(K)/256][8] per-superblock sums of squares of the normalized input
   size_t fa_part_floats = 0;
