@@ -23,6 +23,7 @@
 #include <string>
 
 #include "sh_internal.h"
+#include "sh_dma.h"
 #include "sh_operand.h"
 
 // Scores run in base 2: the score scale carries log2(e), exponentials are the
@@ -40,6 +41,10 @@ __device__ __forceinline__ h8 ld_h8(const uint16_t* p) { return __builtin_bit_ca
 __device__ __forceinline__ f4 mfma16a(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
+
+// Workgroup barrier that waits for this wave's LDS accesses only (no vmcnt
+// drain, unlike __syncthreads).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Split 8 f32 into hi and lo f16 vectors.
 __device__ __forceinline__ void split8(const float* x, h8& hi, h8& lo) {
@@ -308,7 +313,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
     const uint32_t rho = blockIdx.z * ROWS + i;
     const uint32_t rr = rho < n_rows ? rho : 0;  // rows past the end read row 0 and are zeroed below
     const float* src = q + (size_t)(rr % N) * Dq + (size_t)(kh * gqa + rr / N) * HD + 4 * lane;
-    if (lane < HD / 4) __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)&sq[i][0], 16, 0, 0);
+    if (lane < HD / 4) sh_dma16(src, &sq[i][0]);
   }
   uint32_t col[2];
   bool ok[2];
@@ -331,8 +336,15 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
   uint64_t cm[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) cm[h] = DMASK ? fa.masks[col[h]] : col_mask(fa, col[h]);
-  __builtin_amdgcn_s_waitcnt(0);  // the direct LDS loads (the compiler does not track them), K and V
-  __syncthreads();
+  // The query rows (direct LDS loads, which the compiler does not track) were
+  // issued before this wave's 2 NC + DT K and V loads (and any mask loads),
+  // and loads return in order: with at most 2 NC + DT loads in flight the
+  // query rows have landed, while K and V may still be arriving during the
+  // query preparation below (the compiler waits for them before their first
+  // uses). The barriers until then wait for LDS only; __syncthreads would
+  // drain the K and V loads too.
+  sh_wait_vm<2 * NC + DT>();
+  lds_barrier();
 
   __shared__ float sm[NKB][ROWS], sl[NKB][ROWS];
   __shared__ float4 so[NKB][ROWS][HD / 4 + 1];
@@ -365,7 +377,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
       smx[f * 64 + lane] = mx;
     }
   }
-  __syncthreads();  // partial maxima written; every wave is done reading its f32 rows
+  lds_barrier();  // partial maxima written; every wave is done reading its f32 rows
 #pragma unroll
   for (int i = 0; i < FPW; ++i) {
     const int f = wave + NKB * i;
@@ -389,7 +401,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
       fq[(f * 2 + 1) * 64 + lane] = lo;
     }
   }
-  __syncthreads();
+  lds_barrier();
   h8 qhi2[2][NC], qlo2[2][NC];
   float rscale2[2];
 #pragma unroll
@@ -401,7 +413,7 @@ __global__ __launch_bounds__(64 * NKB) void k_fa2(const float* __restrict__ q, c
     }
     rscale2[h] = srs[h * 16 + r];
   }
-  __syncthreads();  // the merge buffer is free again
+  lds_barrier();  // the merge buffer is free again
 
   const bool tail = key0 + 32 > k_end || key0 + 32 > mbase;
 #pragma unroll
