@@ -36,6 +36,8 @@ _SIGS = {
     "or_unit_f32": (C.c_float, [C.c_uint64]),
     "or_dequant_row": (C.c_int, [C.c_int, U8P, C.c_uint64, C.c_uint64, F32P]),
     "or_gemv": (C.c_int, [C.c_int, U8P, C.c_uint64, C.c_uint64, F32P, C.c_uint32, F32P]),
+    "or_gemv16": (C.c_int, [C.c_int, U8P, C.c_uint64, C.c_uint64, F32P, C.c_uint32, F32P]),
+    "or_model_set_mm16": (None, [P, C.c_int]),
     "or_model_open": (C.c_int, [P, C.c_uint64, C.POINTER(P)]),
     "or_model_free": (None, [P]),
     "or_model_dims": (None, [P, U32P]),
@@ -127,6 +129,18 @@ def gemv(qtype: int, w: np.ndarray, M: int, K: int, x: np.ndarray) -> np.ndarray
     return y
 
 
+def gemv16(qtype: int, w: np.ndarray, M: int, K: int, x: np.ndarray) -> np.ndarray:
+    """x [N][K] -> y [N][M] with the wide GEMM's f16 weights and activations
+    (or_gemv16), f64 accumulation."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = _f32(x).reshape(-1, K)
+    y = np.empty((x.shape[0], M), dtype=np.float32)
+    if lib().or_gemv16(qtype, w.ctypes.data_as(U8P), M, K, x.ctypes.data_as(F32P), x.shape[0],
+                       y.ctypes.data_as(F32P)):
+        raise ValueError("gemv16 failed")
+    return y
+
+
 def philox_block(ctr, key):
     c = (C.c_uint64 * 4)(*ctr)
     k = (C.c_uint64 * 2)(*key)
@@ -155,6 +169,10 @@ class Model:
         e = (C.c_uint32 * 4)()
         lib().or_model_moe_dims(h, e)
         self.arch, self.n_expert, self.n_used, self.expert_ff = list(e)
+
+    def set_mm16(self, on: bool):
+        """Dense matmuls of later forwards with the wide GEMM's f16 operands."""
+        lib().or_model_set_mm16(self.h, 1 if on else 0)
 
     def close(self):
         if self.h:

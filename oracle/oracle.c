@@ -232,6 +232,38 @@ int or_gemv(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, 
   return err;
 }
 
+/* The reference's wide GEMM (N >= 32 columns, shaders/compute/mul_mm_cm.slang,
+ * dispatched by ops/matmul.rs:433-446): every weight dequantized in f32
+ * (stage_a_tile, e.g. the Q4_K line dall * sc * nibble - dmin * mb) and
+ * rounded to f16, every activation rounded to f16 (the B staging, line 971),
+ * products accumulated in f32 by the cooperative matrix; here in f64. The
+ * dequantized row of or_dequant_row is that f32 value for every format. */
+int or_gemv16(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, uint32_t N, float* y) {
+  int err = 0;
+  double* xh = (double*)malloc((size_t)N * K * sizeof(double));
+  for (uint64_t i = 0; i < (uint64_t)N * K; ++i) xh[i] = (double)or_f16_to_f32(or_f32_to_f16(x[i]));
+#pragma omp parallel
+  {
+    float* row = (float*)malloc(K * sizeof(float));
+    double* rh = (double*)malloc(K * sizeof(double));
+#pragma omp for schedule(static)
+    for (int64_t m = 0; m < (int64_t)M; ++m) {
+      if (or_dequant_row(type, w, (uint64_t)m, K, row)) { err = 1; continue; }
+      for (uint64_t k = 0; k < K; ++k) rh[k] = (double)or_f16_to_f32(or_f32_to_f16(row[k]));
+      for (uint32_t j = 0; j < N; ++j) {
+        const double* xj = xh + (uint64_t)j * K;
+        double acc = 0.0;
+        for (uint64_t k = 0; k < K; ++k) acc += rh[k] * xj[k];
+        y[(uint64_t)j * M + m] = (float)acc;
+      }
+    }
+    free(row);
+    free(rh);
+  }
+  free(xh);
+  return err;
+}
+
 /* ----------------------------------------------------------------- GGUF */
 
 typedef struct { const char* name; uint32_t nlen; uint32_t type; uint64_t ne[4]; uint32_t nd; uint64_t off; } or_tensor;
@@ -259,6 +291,7 @@ struct or_model {
   or_mat embd, out;
   const float* out_norm;
   or_layer* L;
+  int mm16; /* dense matmuls with the wide GEMM's f16 operands (or_gemv16) */
 };
 
 struct or_kv {
@@ -614,9 +647,12 @@ static int is_ancestor(const int32_t* parents, uint32_t a, uint32_t j) {
   return 0;
 }
 
-static void matmul(const or_mat* W, const float* x, uint32_t N, float* y) {
-  or_gemv(W->type, W->w, W->rows, W->cols, x, N, y);
+static void matmul(const or_model* m, const or_mat* W, const float* x, uint32_t N, float* y) {
+  if (m->mm16) or_gemv16(W->type, W->w, W->rows, W->cols, x, N, y);
+  else or_gemv(W->type, W->w, W->rows, W->cols, x, N, y);
 }
+
+void or_model_set_mm16(or_model* m, int on) { m->mm16 = on != 0; }
 
 /* f16 -> f32 table (65536 entries of or_f16_to_f32) for the attention inner loops. */
 static float f16_lut[65536];
@@ -660,9 +696,9 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     or_layer* Ly = &m->L[l];
     for (uint32_t i = 0; i < L; ++i) rms_norm(res + (size_t)i * d, Ly->attn_norm, d, m->eps, xn + (size_t)i * d);
-    matmul(&Ly->wq, xn, L, q);
-    matmul(&Ly->wk, xn, L, k);
-    matmul(&Ly->wv, xn, L, v);
+    matmul(m, &Ly->wq, xn, L, q);
+    matmul(m, &Ly->wk, xn, L, k);
+    matmul(m, &Ly->wv, xn, L, v);
     if (m->arch != OR_ARCH_LLAMA) {
       /* per-head Q / K RMSNorm over head_dim, then NEOX RoPE (qwen3.rs:340-353) */
       for (uint32_t i = 0; i < L; ++i) {
@@ -721,20 +757,20 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
         }
         free(s);
       }
-    matmul(&Ly->wo, att, L, tmp);
+    matmul(m, &Ly->wo, att, L, tmp);
     for (size_t i = 0; i < (size_t)L * d; ++i) res[i] = res[i] + tmp[i];
     for (uint32_t i = 0; i < L; ++i) rms_norm(res + (size_t)i * d, Ly->ffn_norm, d, m->eps, xn + (size_t)i * d);
     if (m->arch == OR_ARCH_QWEN3MOE) {
       moe_ffn(m, Ly, xn, L, tmp);
     } else {
-      matmul(&Ly->gate, xn, L, g);
-      matmul(&Ly->up, xn, L, u);
+      matmul(m, &Ly->gate, xn, L, g);
+      matmul(m, &Ly->up, xn, L, u);
       /* silu(x) = x / (1 + exp(-x)) (shaders/compute/silu.slang:21), then * up */
       for (size_t i = 0; i < (size_t)L * ff; ++i) {
         double x = g[i];
         g[i] = (float)((x / (1.0 + exp(-x))) * (double)u[i]);
       }
-      matmul(&Ly->down, g, L, tmp);
+      matmul(m, &Ly->down, g, L, tmp);
     }
     for (size_t i = 0; i < (size_t)L * d; ++i) res[i] = res[i] + tmp[i];
   }
@@ -742,7 +778,7 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
   if (logits_mode) {
     uint32_t j0 = logits_mode == 1 ? L - 1 : 0, nc = L - j0;
     for (uint32_t i = 0; i < nc; ++i) rms_norm(res + (size_t)(j0 + i) * d, m->out_norm, d, m->eps, xn + (size_t)i * d);
-    matmul(&m->out, xn, nc, logits);
+    matmul(m, &m->out, xn, nc, logits);
   }
   kv->pos = pos + L; /* cache_io::advance */
   free(qpos); free(res); free(xn); free(q); free(k); free(v); free(att); free(tmp); free(g); free(u);

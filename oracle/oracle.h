@@ -35,6 +35,10 @@ int or_dequant_row(int type, const uint8_t* raw, uint64_t row, uint64_t k, float
 /* y[j*M + m] = sum_k deq(W)[m,k] * x[j*K + k]  (ggml layout, ops/matmul.rs:295-299). */
 int or_gemv(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, uint32_t N, float* y);
 
+/* The reference's wide-GEMM arithmetic (mul_mm_cm.slang, N >= 32): f16(dequant)
+ * times f16(x), accumulated (here in f64). */
+int or_gemv16(int type, const uint8_t* w, uint64_t M, uint64_t K, const float* x, uint32_t N, float* y);
+
 typedef struct or_model or_model;
 typedef struct or_kv or_kv;
 
@@ -42,6 +46,9 @@ typedef struct or_kv or_kv;
  * outlive the model). */
 int or_model_open(const uint8_t* img, uint64_t size, or_model** out);
 void or_model_free(or_model* m);
+/* Dense matmuls of later or_forward calls through or_gemv16 (on != 0) or
+ * or_gemv (the MoE router and experts always use or_gemv). */
+void or_model_set_mm16(or_model* m, int on);
 /* n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab */
 void or_model_dims(const or_model* m, uint32_t dims[7]);
 /* architecture (0 llama, 1 qwen3, 2 qwen3moe), n_expert, n_expert_used, expert_ff */

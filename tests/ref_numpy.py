@@ -156,11 +156,19 @@ def read_gguf(buf: bytes):
 
 # ------------------------------------------------------------------ forward
 
+def _r16(a):
+    """f64 values rounded to f32, then to f16 (IEEE nearest-even), back as f64."""
+    return np.asarray(a).astype(np.float32).astype(np.float16).astype(np.float64)
+
+
 class RefLlama:
     """float64 Llama forward with f16 K/V storage (same cache rounding as the reference)."""
 
-    def __init__(self, buf: bytes):
+    def __init__(self, buf: bytes, mm16: bool = False):
+        """mm16: the dense matmuls with the reference's wide-GEMM operands
+        (mul_mm_cm.slang): f16-rounded f32 weights and f16-rounded inputs."""
         meta, T, _ = read_gguf(buf)
+        self.mm16 = mm16
         self.nl = meta["llama.block_count"]
         self.d = meta["llama.embedding_length"]
         self.nh = meta["llama.attention.head_count"]
@@ -186,6 +194,19 @@ class RefLlama:
                                                  "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"]})
         self.K = [np.zeros((0, self.nkv, self.hd)) for _ in range(self.nl)]
         self.Vc = [np.zeros((0, self.nkv, self.hd)) for _ in range(self.nl)]
+        if mm16:
+            self.out = _r16(self.out)
+            for W in self.layers:
+                for k in ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]:
+                    W[k] = _r16(W[k])
+
+    def mm(self, x, w):
+        """x @ w.T; in mm16 mode the input rounded to f16 (w already is) and the
+        output stored as f32, as the reference's f32 tensors hold it (the same
+        storage points as the C oracle, so both round the same f32 values to f16)."""
+        if not self.mm16:
+            return x @ w.T
+        return (_r16(x) @ w.T).astype(np.float32).astype(np.float64)
 
     def rms(self, x, w):
         return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * w[0] if w.ndim == 2 else None
@@ -221,9 +242,9 @@ class RefLlama:
         gqa = self.nh // self.nkv
         for li, W in enumerate(self.layers):
             h = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * W["attn_norm"][0]
-            q = (h @ W["attn_q"].T).reshape(L, self.nh, self.hd)
-            k = (h @ W["attn_k"].T).reshape(L, self.nkv, self.hd)
-            v = (h @ W["attn_v"].T).reshape(L, self.nkv, self.hd)
+            q = self.mm(h, W["attn_q"]).reshape(L, self.nh, self.hd)
+            k = self.mm(h, W["attn_k"]).reshape(L, self.nkv, self.hd)
+            v = self.mm(h, W["attn_v"]).reshape(L, self.nkv, self.hd)
             q = self.rope(q, pos)
             k = self.rope(k, pos)
             k16 = k.astype(np.float32).astype(np.float16).astype(np.float64)
@@ -244,14 +265,14 @@ class RefLlama:
                 p /= p.sum(axis=1, keepdims=True)
                 att[:, hh, :] = p @ Vc[:, kh, :]
             att = att.reshape(L, self.d).astype(np.float32).astype(np.float64)
-            x = (x + att @ W["attn_output"].T).astype(np.float32).astype(np.float64)
+            x = (x + self.mm(att, W["attn_output"])).astype(np.float32).astype(np.float64)
             h2 = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * W["ffn_norm"][0]
-            g = h2 @ W["ffn_gate"].T
-            u = h2 @ W["ffn_up"].T
+            g = self.mm(h2, W["ffn_gate"])
+            u = self.mm(h2, W["ffn_up"])
             a = (g / (1 + np.exp(-g)) * u).astype(np.float32).astype(np.float64)
-            x = (x + a @ W["ffn_down"].T).astype(np.float32).astype(np.float64)
+            x = (x + self.mm(a, W["ffn_down"])).astype(np.float32).astype(np.float64)
         f = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + self.eps) * self.onorm
-        return f @ self.out.T, x
+        return self.mm(f, self.out), x
 
     def truncate(self, p):
         for li in range(self.nl):

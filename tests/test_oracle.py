@@ -8,6 +8,8 @@ path; its only checks are closed-form inputs + CPU restatements):
   or_dequant_row (Q8_0, Q4_K)     independent numpy dequant (tests/ref_numpy.py) +
                                   closed-form special blocks (d=0, sc=1 m=0, q=15)
   or_gemv                         numpy f64 matmul of independently dequantized rows
+  or_gemv16 / or_forward mm16     numpy f16 casts of the same rows and inputs; the
+                                  mm16 numpy Llama (ref_numpy.RefLlama(mm16=True))
   or_forward                      independent numpy f64 Llama (ref_numpy.RefLlama),
                                   causal == incremental decode, chain tree == causal,
                                   branch == its own path
@@ -169,6 +171,33 @@ def test_gemv_matches_numpy(qtype):
     np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("qtype", [GGML_Q8_0, GGML_Q4_K])
+def test_gemv16_matches_numpy(qtype):
+    """The wide-GEMM arithmetic: weights are the f32 dequantized values (exact
+    in f64 here, then rounded once to f32) rounded to f16, inputs rounded to
+    f16, as numpy's nearest-even casts give them; a mistake that skips either
+    rounding moves y by ~1e-4 relative, far above the tolerance."""
+    rng = np.random.default_rng(14)
+    M, K, N = 40, 512, 3
+    raw, _ = (_rand_q4k if qtype == GGML_Q4_K else _rand_q8)(rng, M, K)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    y = O.gemv16(qtype, raw, M, K, x)
+    w16 = R.dequant(qtype, raw, M, K).astype(np.float32).astype(np.float16).astype(np.float64)
+    ref = x.astype(np.float16).astype(np.float64) @ w16.T
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-7)
+    exact = O.gemv(qtype, raw, M, K, x)
+    assert np.abs(exact - y).max() > 1e-5 * np.abs(exact).max()  # the roundings are there
+    # f16 special cases of the inputs: overflow to inf, subnormals kept
+    xs = np.zeros((1, K), np.float32)
+    xs[0, 0], xs[0, 1] = 70000.0, 3e-6
+    ys = O.gemv16(qtype, raw, M, K, xs)
+    w0 = R.dequant(qtype, raw, M, K)[:, 1].astype(np.float32).astype(np.float16).astype(np.float64)
+    w00 = R.dequant(qtype, raw, M, K)[:, 0]
+    keep = w00 == 0
+    np.testing.assert_allclose(ys[0][keep], (w0 * np.float64(np.float16(3e-6)))[keep], rtol=1e-12)
+    assert np.all(np.isinf(ys[0][~keep]))
+
+
 # ------------------------------------------------------------------ forward
 
 SMALL_Q8 = S.LlamaShape(2, 256, 4, 2, 512, 1000, 256, 1e-5, 1e4, 0.02, GGML_Q8_0, GGML_Q8_0)
@@ -217,6 +246,29 @@ def test_forward_matches_numpy(small):
         diff = np.abs(k - r)
         assert diff.max() <= 1 and np.mean(diff > 0) < 0.01
     kv.close()
+    m.close()
+
+
+def test_forward_mm16_matches_numpy(small):
+    """or_forward with the wide-GEMM operands against the numpy Llama doing the
+    same roundings, and away from the exact forward."""
+    ref = R.RefLlama(bytes(small.bytes()), mm16=True)
+    m = O.Model(small)
+    m.set_mm16(True)
+    kv = O.KvCache(m, 64)
+    toks = S.tokens(5, 12, m.V)
+    lg, res = O.forward(m, kv, toks, 0)
+    rl, rr = ref.forward(toks)
+    # both store the same f32 values at the same points, so they round the
+    # same values to f16: equal up to f64 summation order
+    np.testing.assert_allclose(res, rr, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(lg, rl, rtol=1e-6, atol=1e-6 * np.abs(rl).max())
+    m.set_mm16(False)
+    kv2 = O.KvCache(m, 64)
+    lg0, _ = O.forward(m, kv2, toks, 0)
+    assert np.abs(lg0 - lg).max() > 1e-4 * np.abs(lg0).max()
+    kv.close()
+    kv2.close()
     m.close()
 
 
