@@ -207,6 +207,8 @@ def measure_tree(eng, tm, d, P=8192, reps=3):
     for k, v in list(kern.items())[:10]:
         log(f"  {k:16s} {v:8.3f} ms")
     return {"config": f"B={B}, tree 4x3x2 ({n} nodes), ctx {P}, REJECTION T=1.0 seed 11, synthetic draft logits",
+            "arithmetic": ("reference wide-GEMM (f16 weights and activations, f32 accumulation; "
+                           "ops/matmul.rs:433-446)" if tm.wide_f16 else "f32-level (hi/lo f16 activations)"),
             "ms": round(ms, 3), "alg_bytes": w + kv, "GBps": round((w + kv) / ms / 1e6, 1),
             "frac": round((w + kv) / ms / 1e6 / HBM_PEAK_GBS, 4), "mean_path_nodes": round(float(np.mean(plens)), 3),
             "kernel_ms": kern}
@@ -405,6 +407,8 @@ def main():
         except (OSError, StopIteration):
             pass
         ot, od = O.Model(timg), O.Model(dimg)
+        ot.set_mm16(2 if tm.wide_f16 else 0)  # wide calls as the GPU computes them
+        od.set_mm16(2 if dm.wide_f16 else 0)
         okt, okd = O.KvCache(ot, max_seq), O.KvCache(od, max_seq)
         for (gkv, okv, m) in ((tkv, okt, tm), (dkv, okd, dm)):
             n = gkv.position

@@ -115,6 +115,19 @@ int sh_model_load_gguf_memory(sh_engine* e, const void* data, uint64_t size, sh_
 void sh_model_destroy(sh_model* m);
 /* Model::{vocab_size, cache_dims} (models/mod.rs:35-37). */
 int sh_model_info(const sh_model* m, sh_model_dims* out);
+/* Wide-GEMM arithmetic (ops/matmul.rs:406-446): the reference computes every
+ * dense matmul of N >= 32 columns with its cooperative-matrix GEMM
+ * (mul_mm_cm.slang: weights dequantized in f32 and rounded to f16, activations
+ * rounded to f16, f32 accumulation) unless SEEKER_MM_CM=0. Here forward calls
+ * of >= 32 columns (a batched verify counts all of its columns) do the same
+ * when the model allows it (no routed experts, every matrix Q4_K) and the
+ * switch is on (default on; SH_WIDE_F16=0 in the environment at upload turns
+ * it off); otherwise they keep the f32-level path of narrower calls.
+ * sh_model_wide_f16: *on = 1 when wide calls take the f16 arithmetic.
+ * sh_model_set_wide_f16: on = 0 / 1; SH_ERR_UNSUPPORTED for 1 on a model
+ * that does not allow it. */
+int sh_model_wide_f16(const sh_model* m, int* on);
+int sh_model_set_wide_f16(sh_model* m, int on);
 /* The validation half of models::open (models/mod.rs:537; parse_params +
  * collect_weights, models/llama.rs:1038-1090) without a device: parses a GGUF
  * image in caller memory, checks every tensor the model reads (shape, type,
@@ -221,6 +234,12 @@ void sh_qtensor_destroy(sh_qtensor* t);
  * batched columns matmul.rs:473-487, ACCUMULATE mul_mat_vec_head.slang:173-188). */
 int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_t N, float* y_dev,
                   int accumulate);
+/* The reference's wide GEMM for N >= 32 columns (ops/matmul.rs:433-446,
+ * mul_mm_cm.slang): y[j][m] (+)= sum_k f16(deq(W)[m][k]) * f16(x[j][k]) with
+ * f32 accumulation, W Q4_K; the kernels the forward uses for calls of >= 32
+ * columns (sh_model_wide_f16). Any N >= 1 (64 columns per pass). */
+int sh_gemm_wide16(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_t N, float* y_dev,
+                   int accumulate);
 
 /* Acceptance kernel for a batch of B sequences with k draft positions.
  * p_logits_dev [B][k+1][V], q_logits_dev [B][k][V] (REJECTION only, else NULL),

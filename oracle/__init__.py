@@ -170,9 +170,11 @@ class Model:
         lib().or_model_moe_dims(h, e)
         self.arch, self.n_expert, self.n_used, self.expert_ff = list(e)
 
-    def set_mm16(self, on: bool):
-        """Dense matmuls of later forwards with the wide GEMM's f16 operands."""
-        lib().or_model_set_mm16(self.h, 1 if on else 0)
+    def set_mm16(self, mode):
+        """Dense matmuls of later forwards with the wide GEMM's f16 operands:
+        False / 0 never, True / 1 always, 2 in forward calls of >= 32 columns
+        (the reference's dispatch, ops/matmul.rs:433-446)."""
+        lib().or_model_set_mm16(self.h, int(mode))
 
     def close(self):
         if self.h:

@@ -291,7 +291,9 @@ struct or_model {
   or_mat embd, out;
   const float* out_norm;
   or_layer* L;
-  int mm16; /* dense matmuls with the wide GEMM's f16 operands (or_gemv16) */
+  int mm16; /* dense matmuls with the wide GEMM's f16 operands (or_gemv16): 0 never,
+             * 1 always, 2 in forward calls of >= 32 columns (ops/matmul.rs:433-446) */
+  uint32_t call_cols; /* columns of the forward call in progress */
 };
 
 struct or_kv {
@@ -648,11 +650,11 @@ static int is_ancestor(const int32_t* parents, uint32_t a, uint32_t j) {
 }
 
 static void matmul(const or_model* m, const or_mat* W, const float* x, uint32_t N, float* y) {
-  if (m->mm16) or_gemv16(W->type, W->w, W->rows, W->cols, x, N, y);
+  if (m->mm16 == 1 || (m->mm16 == 2 && m->call_cols >= 32)) or_gemv16(W->type, W->w, W->rows, W->cols, x, N, y);
   else or_gemv(W->type, W->w, W->rows, W->cols, x, N, y);
 }
 
-void or_model_set_mm16(or_model* m, int on) { m->mm16 = on != 0; }
+void or_model_set_mm16(or_model* m, int mode) { m->mm16 = mode >= 0 && mode <= 2 ? mode : 0; }
 
 /* f16 -> f32 table (65536 entries of or_f16_to_f32) for the attention inner loops. */
 static float f16_lut[65536];
@@ -670,6 +672,7 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
   if (L == 0) return 1;
   if (kv->pos != pos) return 2;
   if (pos + L > kv->max_seq) return 3;
+  m->call_cols = L;
   const uint32_t d = m->d, hd = m->hd, nh = m->n_head, nkv = m->n_kv, ff = m->ff, qd = m->q_dim;
   const uint32_t dkv = hd * nkv, gqa = nh / nkv;
   const uint32_t wide = qd > d ? qd : d;

@@ -48,7 +48,9 @@ int or_model_open(const uint8_t* img, uint64_t size, or_model** out);
 void or_model_free(or_model* m);
 /* Dense matmuls of later or_forward calls through or_gemv16 (on != 0) or
  * or_gemv (the MoE router and experts always use or_gemv). */
-void or_model_set_mm16(or_model* m, int on);
+/* 0: exact dense matmuls; 1: all as or_gemv16; 2: as or_gemv16 in forward
+ * calls of >= 32 columns (the reference's wide-GEMM dispatch). */
+void or_model_set_mm16(or_model* m, int mode);
 /* n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab */
 void or_model_dims(const or_model* m, uint32_t dims[7]);
 /* architecture (0 llama, 1 qwen3, 2 qwen3moe), n_expert, n_expert_used, expert_ff */

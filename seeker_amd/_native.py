@@ -109,6 +109,8 @@ SIGNATURES = {
     "sh_model_load_gguf_memory": (C.c_int, [P, P, C.c_uint64, C.POINTER(P)]),
     "sh_model_destroy": (None, [P]),
     "sh_model_info": (C.c_int, [P, C.POINTER(sh_model_dims)]),
+    "sh_model_wide_f16": (C.c_int, [P, C.POINTER(C.c_int)]),
+    "sh_model_set_wide_f16": (C.c_int, [P, C.c_int]),
     "sh_gguf_inspect": (C.c_int, [P, C.c_uint64, C.POINTER(sh_model_dims)]),
     "sh_kv_create": (C.c_int, [P, P, C.c_uint32, C.POINTER(P)]),
     "sh_kv_destroy": (None, [P]),
@@ -131,6 +133,7 @@ SIGNATURES = {
     "sh_qtensor_upload": (C.c_int, [P, C.c_int, P, C.c_uint32, C.c_uint32, C.POINTER(P)]),
     "sh_qtensor_destroy": (None, [P]),
     "sh_gemv_quant": (C.c_int, [P, P, P, C.c_uint32, P, C.c_int]),
+    "sh_gemm_wide16": (C.c_int, [P, P, P, C.c_uint32, P, C.c_int]),
     "sh_accept_sample": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), P, P]),
     "sh_tree_accept": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), P, P, P]),
     "sh_tree_verify_step": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, C.c_uint32, U32P, I32P, P,

@@ -298,19 +298,27 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
 
 // Split combine per (superblock of the attention output, chunk column): the
 // column's segment gives its partials; writes attn [nc][Dq] and the column's
-// superblock of the Wo operand.
+// superblock of the Wo operand (with bh: the f16 row bh[c][Dq] of the wide
+// f16 GEMM instead).
 template <int HD>
 __global__ __launch_bounds__(64) void k_fab_combine(const FabSeg* __restrict__ segs, const uint32_t* __restrict__ colseg,
                                                     const float* __restrict__ part, uint32_t n_head, uint32_t gqa,
                                                     uint32_t kp, float* __restrict__ attn, uint16_t* __restrict__ bx,
-                                                    uint16_t* __restrict__ xs, float* __restrict__ cs) {
+                                                    uint16_t* __restrict__ xs, float* __restrict__ cs,
+                                                    uint16_t* __restrict__ bh) {
   const uint32_t sb = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
   const FabSeg& sg = segs[colseg[c]];
   const uint32_t Dq = n_head * HD, k = 256 * sb + 4 * lane, nsv = sg.nsplit * kp;
   const float4 v = sh_fa_combine4<2>(part + sg.part_off, nsv, nsv, sg.rows_pad, HD, n_head, gqa, sg.ncol, sb,
                                      c - sg.col0);
   if (k < Dq) *(float4*)(attn + (size_t)c * Dq + k) = v;
-  sh_operand_store_sb(v, Dq, sb, c, bx, xs, cs);
+  if (bh) {
+    typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+    const hv4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    if (k < Dq) *(uint2*)(bh + (size_t)c * Dq + k) = __builtin_bit_cast(uint2, h);
+  } else {
+    sh_operand_store_sb(v, Dq, sb, c, bx, xs, cs);
+  }
 }
 
 template <int HD, int RGW, int KP>
@@ -435,7 +443,7 @@ void sh_fab_free(sh_engine* e, FabLaunch& fl) {
 }
 
 int sh_fab_launch(sh_engine* e, const sh_model* m, const FabLaunch& fl, uint32_t layer, const float* q, float* attn_out,
-                  uint16_t* bx, uint16_t* xs, float* cs) {
+                  uint16_t* bx, uint16_t* xs, float* cs, uint16_t* bh) {
   const uint32_t gqa = m->n_head / m->n_kv;
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)m->hd);
   hipEvent_t ev = nullptr;
@@ -448,10 +456,10 @@ int sh_fab_launch(sh_engine* e, const sh_model* m, const FabLaunch& fl, uint32_t
   const dim3 cgrid((m->n_head * m->hd + 255) / 256, fl.nc);
   if (m->hd == 128)
     hipLaunchKernelGGL((k_fab_combine<128>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head, gqa,
-                       fl.kp, attn_out, bx, xs, cs);
+                       fl.kp, attn_out, bx, xs, cs, bh);
   else
     hipLaunchKernelGGL((k_fab_combine<64>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head, gqa,
-                       fl.kp, attn_out, bx, xs, cs);
+                       fl.kp, attn_out, bx, xs, cs, bh);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "attn_combine", 0.0, ev);
   return SH_OK;

@@ -1383,6 +1383,215 @@ __global__ __launch_bounds__(512) void k_gemm_kq(const uint8_t* __restrict__ Wp,
     }
 }
 
+// ------------------------------------------------------------------ wide f16 GEMM
+
+// The reference's arithmetic for matmuls of N >= 32 columns
+// (ops/matmul.rs:433-446 -> mul_mm_cm.slang): every weight dequantized in f32
+// and rounded to f16 (stage_a_tile, the Q4_K line
+// f16(dall * sc * nibble - dmin * mb)), every activation rounded to f16,
+// products accumulated in f32. Here the activations arrive as f16 rows
+// bh[col][k] (k_prep16_*), the weights are decoded from the Q4_K tiles into
+// the MFMA A fragment as f16(fma(d sc, q, -dmin m)) (one rounding from the
+// exact value; the f32 product then f16 of the reference may differ in the last
+// f16 bit), and v_mfma_f32_16x16x32_f16 accumulates over the whole K-split.
+
+// The part of a Q4_K tile-superblock one lane needs for its A row r = lane % 16:
+// the eight sub-block words, d | dmin of row r and its 12 scale bytes.
+struct Q4TileR {
+  u32x4 q0, q1;
+  uint32_t dd, s0, s1, s2;
+  __device__ void pin() { pin32(q0); pin32(q1); pin32(dd); pin32(s0); pin32(s1); pin32(s2); }
+};
+__device__ __forceinline__ Q4TileR load_q4_tile_r(const uint8_t* base, int lane, int r) {
+  Q4TileR a;
+  a.q0 = ld16(base + 16 * lane);
+  a.q1 = ld16(base + 1024 + 16 * lane);
+  a.dd = *(const uint32_t*)(base + 2048 + 4 * r);
+  const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
+  a.s0 = sp[0];
+  a.s1 = sp[1];
+  a.s2 = sp[2];
+  return a;
+}
+// Per superblock: the words and, per sub-block m, the lane row's a_m = d sc_m
+// (as 2^24 a_m and 2^20 a_m, exact power-of-two scalings) and b_m = dmin m_m
+// (the Q4_K 6-bit unpack of q4_decode_setup).
+struct Q4DecR {
+  uint32_t w[8];
+  float a24[8], a20[8], nb[8];
+};
+__device__ __forceinline__ Q4DecR q4r_setup(const Q4TileR& t) {
+  Q4DecR s;
+  s.w[0] = t.q0.x; s.w[1] = t.q0.y; s.w[2] = t.q0.z; s.w[3] = t.q0.w;
+  s.w[4] = t.q1.x; s.w[5] = t.q1.y; s.w[6] = t.q1.z; s.w[7] = t.q1.w;
+  const uint32_t sc03 = t.s0 & 0x3F3F3F3Fu, m03 = t.s1 & 0x3F3F3F3Fu;
+  const uint32_t sc47 = (t.s2 & 0x0F0F0F0Fu) | ((t.s0 >> 2) & 0x30303030u);
+  const uint32_t m47 = ((t.s2 >> 4) & 0x0F0F0F0Fu) | ((t.s1 >> 2) & 0x30303030u);
+  const float d24 = (float)as_h2(t.dd).x * 16777216.0f, ndmin = -(float)as_h2(t.dd).y;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    s.a24[j] = d24 * (float)((sc03 >> (8 * j)) & 0xFFu);
+    s.a24[4 + j] = d24 * (float)((sc47 >> (8 * j)) & 0xFFu);
+    s.nb[j] = ndmin * (float)((m03 >> (8 * j)) & 0xFFu);
+    s.nb[4 + j] = ndmin * (float)((m47 >> (8 * j)) & 0xFFu);
+  }
+#pragma unroll
+  for (int m = 0; m < 8; ++m) s.a20[m] = s.a24[m] * 0.0625f;
+  return s;
+}
+// A fragment of sub-block m: element t (k = 32 m + 8 g + t) = f16(a_m q_t - b_m).
+// A nibble masked in place is an f16 subnormal: q 2^-24 (pairs t = 0, 1 and 4,
+// 5, nibbles at bits 0 / 16) or q 2^-20 (t = 2, 3 and 6, 7, at bits 4 / 20),
+// which v_fma_mix reads exactly (f16 denormals are kept), so with 2^24 a_m and
+// 2^20 a_m every product is a_m q. v_fma_mixlo / mixhi_f16 round the exact
+// a q - b once to f16 (written as asm: left to itself the compiler mixes these
+// with f32 FMAs plus conversions, which round twice and cost more).
+__device__ __forceinline__ uint32_t fma_mix_pair(uint32_t p, float a, float c) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(r)
+      : "v"(p), "v"(a), "v"(c));
+  return r;
+}
+__device__ __forceinline__ h8 q4r_frag16(const Q4DecR& s, int m) {
+  const uint32_t w = s.w[m], w8 = w >> 8;
+  u32x4 r;
+  r.x = fma_mix_pair(w & 0x000F000Fu, s.a24[m], s.nb[m]);
+  r.y = fma_mix_pair(w & 0x00F000F0u, s.a20[m], s.nb[m]);
+  r.z = fma_mix_pair(w8 & 0x000F000Fu, s.a24[m], s.nb[m]);
+  r.w = fma_mix_pair(w8 & 0x00F000F0u, s.a20[m], s.nb[m]);
+  return as_h8(r);
+}
+
+// y = W x over N <= 16 NC columns of f16 rows bh [N][ldb] (K of W), W Q4_K. A
+// workgroup of 8 waves covers 8 row tiles (wave w: tile blockIdx.x * 8 + w;
+// two waves per SIMD hide each other's decode latencies) over the
+// superblocks of split blockIdx.y. Every
+// operand goes through a ring of three LDS stages filled by direct
+// global->LDS loads two superblocks ahead of the compute: per superblock the
+// NC x 8 B fragments (16 columns x 32 k each; columns past N read column
+// N - 1, their sums are dropped) and the wave's weight tile (2304 B, as two
+// 1 KB and one 256 B load). All of a wave's loads are its own asm
+// loads, so the wait for a stage is an exact count of the loads issued after
+// it. Each weight tile's f16 fragment feeds NC MFMAs; the sums stay in the
+// MFMA accumulators over the whole split. EPI_PART: partials
+// [split][col][row]; EPI_STORE (one split): out[col][row], rows < ea.rows.
+template <int NC>
+struct G16Smem {
+  static constexpr int kStages = NC <= 2 ? 4 : 3;       // ring depth within the LDS
+
+  static constexpr uint32_t kB = NC * 8 * 64;           // h8 elements of one stage's B fragments
+  static constexpr uint32_t kW = 8 * SH_Q4K_TILE_BYTES;  // bytes of one stage's weight tiles
+};
+
+template <int NC, int EPI>
+__global__ __launch_bounds__(512) void k_gemm16_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                    uint32_t S, const uint16_t* __restrict__ Bh, uint32_t ldb,
+                                                    uint32_t N, EpiArgs ea) {
+  constexpr int T = 1, WV = 8;
+  constexpr uint32_t kB = G16Smem<NC>::kB, kW = G16Smem<NC>::kW;
+  constexpr int kLoads = NC + 3 * T;  // one wave's direct loads per stage
+  constexpr int G16_STAGES = G16Smem<NC>::kStages;
+  __shared__ h8 sB[G16_STAGES][kB];
+  __shared__ __attribute__((aligned(16))) uint8_t sW[G16_STAGES][kW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4, r = lane & 15;
+  const uint32_t ks = blockIdx.y, sb0 = ks * S, sb1 = min(sb0 + S, nsb), nst = sb1 - sb0;
+  const uint32_t tile0 = (blockIdx.x * WV + wave) * T;
+
+  auto issue = [&](uint32_t sb, int buf) {
+    for (uint32_t fi = wave; fi < (uint32_t)(NC * 8); fi += WV) {  // NC per wave
+      const uint32_t c = fi >> 3, m = fi & 7;
+      const uint32_t col = min(16 * c + (uint32_t)r, N - 1);
+      sh_dma16(Bh + (size_t)col * ldb + 256 * sb + 32 * m + 8 * g4, &sB[buf][fi * 64]);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
+      const uint8_t* src = Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
+      uint8_t* dst = &sW[buf][(wave * T + t) * SH_Q4K_TILE_BYTES];
+      sh_dma16(src + 16 * lane, dst);
+      sh_dma16(src + 1024 + 16 * lane, dst + 1024);
+      sh_dma4(src + 2048 + 4 * lane, dst + 2048);
+    }
+  };
+
+  f4 acc[T][NC];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf) {
+    Q4DecR dec[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint8_t* w = &sW[buf][(wave * T + t) * SH_Q4K_TILE_BYTES];
+      Q4TileR a;
+      a.q0 = *(const u32x4*)(w + 16 * lane);
+      a.q1 = *(const u32x4*)(w + 1024 + 16 * lane);
+      a.dd = *(const uint32_t*)(w + 2048 + 4 * r);
+      const uint32_t* sp = (const uint32_t*)(w + 2112 + 12 * r);
+      a.s0 = sp[0];
+      a.s1 = sp[1];
+      a.s2 = sp[2];
+      dec[t] = q4r_setup(a);
+    }
+    h8 bb[2][NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) bb[0][c] = sB[buf][(c * 8) * 64 + lane];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int cur = m & 1;
+      if (m < 7) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) bb[cur ^ 1][c] = sB[buf][(c * 8 + m + 1) * 64 + lane];
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this sub-block's MFMAs
+      h8 a[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) a[t] = q4r_frag16(dec[t], m);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t][c] = mfma16(a[t], bb[cur][c], acc[t][c]);
+    }
+  };
+
+  constexpr int kAhead = G16_STAGES - 1;  // stages in flight ahead of the compute
+  for (int j = 0; j < kAhead; ++j)
+    if ((uint32_t)j < nst) issue(sb0 + j, j);
+  for (uint32_t i = 0; i < nst; ++i) {
+    // stage i landed (the later ones may still be in flight), and every wave
+    // is done with stage i - 1, whose buffer stage i + kAhead now refills
+    const uint32_t later = min(nst - 1 - i, (uint32_t)(kAhead - 1));
+    if (later >= 2) sh_wait_vm<2 * kLoads>();
+    else if (later == 1) sh_wait_vm<kLoads>();
+    else sh_wait_vm<0>();
+    __syncthreads();
+    if (i + kAhead < nst) issue(sb0 + i + kAhead, (i + kAhead) % G16_STAGES);
+    compute(i % G16_STAGES);
+  }
+
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t tile = tile0 + t, col = 16 * c + r, row0 = tile * 16 + 4 * g4;
+      if (tile >= tiles || col >= N) continue;
+      const f4 v = acc[t][c];
+      if (EPI == EPI_PART) {
+        *(float4*)(ea.out + ks * ea.part_stride + (size_t)col * ea.ldo + row0) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (row0 + j < ea.rows) ea.out[(size_t)col * ea.ldo + row0 + j] = v[j];
+      }
+    }
+}
+
 // QKV from the multi-group kernel's split partials: per column (blockIdx.y) and
 // 4 rows per thread, the split sum, then RoPE and the KV-cache writes.
 __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ part, uint32_t nparts,
@@ -2185,6 +2394,66 @@ int sh_gemm_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
   sh_prof_begin(e, &ev);
   if (epi == EPI_PART) dispatch_mg_fmt<EPI_PART>(e, w, bx, xs, cs, N, ea, p);
   else dispatch_mg_fmt<EPI_STORE>(e, w, bx, xs, cs, N, ea, p);
+  SH_HIP(hipGetLastError());
+  sh_prof_end(e, tag, w.alg_bytes, ev);
+  if (nparts) *nparts = p.KS;
+  return SH_OK;
+}
+
+// K-splits of a wide f16 GEMM: 8-tile workgroups, one per CU (the 150 KB LDS
+// ring), at most the splits the multi-group plan sizes the partial buffer for.
+// The split count minimises rounds x (superblocks per workgroup + 2), the 2
+// standing for the ring's fill before the first superblock computes.
+static MgPlan plan16(const QMat& w, bool one_split) {
+  MgPlan p;
+  p.T = 1;
+  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 7) / 8, slots = 256;
+  const uint32_t cap = one_split ? 1 : mg_plan(w, MG_MAX_G, false).KS;
+  uint32_t best_ks = 1;
+  uint64_t best = ~0ull;
+  for (uint32_t ks = 1; ks <= cap && ks <= nsb; ++ks) {
+    const uint32_t S = (nsb + ks - 1) / ks, k2 = (nsb + S - 1) / S, wgs = wgx * k2;
+    const uint64_t cost = (uint64_t)((wgs + slots - 1) / slots) * (S + 2);
+    if (cost < best) { best = cost; best_ks = k2; }
+  }
+  p.S = (nsb + best_ks - 1) / best_ks;
+  p.KS = (nsb + p.S - 1) / p.S;
+  return p;
+}
+
+template <int NC, int EPI>
+static void launch16(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, const EpiArgs& ea,
+                     const MgPlan& p) {
+  const dim3 grid((w.tiles + 7) / 8, p.KS);
+  hipLaunchKernelGGL((k_gemm16_q4k<NC, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bh,
+                     ldb, N, ea);
+}
+template <int EPI>
+static void dispatch16(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, const EpiArgs& ea,
+                       const MgPlan& p) {
+  switch ((N + 15) / 16) {
+    case 1: launch16<1, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 2: launch16<2, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 3: launch16<3, EPI>(e, w, bh, ldb, N, ea, p); break;
+    default: launch16<4, EPI>(e, w, bh, ldb, N, ea, p); break;
+  }
+}
+
+int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, EpiKind epi,
+                     const EpiArgs& ea, const char* tag, uint32_t* nparts) {
+  SH_CHECK(N >= 1 && N <= SH_MAX_COLS, SH_ERR_ARG, "f16 gemm N=%u outside [1, %u]", N, SH_MAX_COLS);
+  SH_CHECK(w.type == GGML_Q4_K && w.K % 256 == 0 && ldb >= w.K && ldb % 8 == 0, SH_ERR_UNSUPPORTED,
+           "f16 gemm needs Q4_K (type %d) and an operand of at least K = %u halves per column (ldb %u)", w.type, w.K,
+           ldb);
+  SH_CHECK(epi == EPI_PART || epi == EPI_STORE, SH_ERR_ARG, "f16 gemm epilogue %d", (int)epi);
+  const MgPlan p = plan16(w, epi == EPI_STORE);
+  if (epi == EPI_PART)
+    SH_CHECK(ea.part_cap >= p.KS && ea.part_stride >= (size_t)((N + 7) / 8 * 8) * ea.ldo, SH_ERR_CAPACITY,
+             "f16 gemm: %u split partials exceed the buffer (%u)", p.KS, ea.part_cap);
+  hipEvent_t ev = nullptr;
+  sh_prof_begin(e, &ev);
+  if (epi == EPI_PART) dispatch16<EPI_PART>(e, w, bh, ldb, N, ea, p);
+  else dispatch16<EPI_STORE>(e, w, bh, ldb, N, ea, p);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, tag, w.alg_bytes, ev);
   if (nparts) *nparts = p.KS;

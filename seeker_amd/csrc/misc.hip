@@ -142,8 +142,90 @@ __global__ __launch_bounds__(64) void k_prep(PrepArgs a) {
   sh_operand_store_sb(v, a.K, sb, col, a.bx, a.xs, a.cs);
 }
 
+__device__ __forceinline__ void store_h4(uint16_t* p, float4 v) {
+  typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+  const hv4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  *(uint2*)p = __builtin_bit_cast(uint2, h);
+}
+
+// Operand of the wide f16 GEMM (the reference's mul_mm_cm input staging,
+// mul_mm_cm.slang:969-971: every activation rounded to f16) for
+// PREP_PLAIN / PREP_RESID, one 1024-thread workgroup per column (four elements
+// per thread and pass, one pass for K <= 4096): v as in k_prep; with a norm
+// weight the RMS factor over the whole column first, then
+// bh = f16((v * rsqrt(mean + eps)) * w) in rms_norm.slang:39-55's order.
+template <int MODE>
+__global__ __launch_bounds__(1024) void k_prep16_rows(PrepArgs a) {
+  const uint32_t col = blockIdx.x, tid = threadIdx.x;
+  const size_t pstride = (size_t)a.part_cols * a.part_ld;
+  float* xc = a.x + (size_t)col * a.K;
+  float ss = 0.f;
+  for (uint32_t k = 4 * tid; k < a.K; k += 4096) {
+    float4 v = *(const float4*)(xc + k);
+    if (MODE == PREP_RESID && a.nparts) {
+      v = sum_parts(a.part + (size_t)col * a.part_ld + k, pstride, a.nparts, v);
+      *(float4*)(xc + k) = v;
+    }
+    ss += sh_sq4(v);
+  }
+  float rinv = 1.0f;
+  if (a.norm_w) {
+    __shared__ float s_part[16];
+    ss = sh_wave_sum(ss);
+    if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) ss += (s_part[i] + s_part[i + 1]) + (s_part[i + 2] + s_part[i + 3]);
+    rinv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+  }
+  uint16_t* out = a.bh + (size_t)col * a.ldb;
+  for (uint32_t k = 4 * tid; k < a.K; k += 4096) {
+    float4 v = *(const float4*)(xc + k);  // this thread's own store above, if any
+    if (a.norm_w) {
+      const float4 w = *(const float4*)(a.norm_w + k);
+      v = make_float4((rinv * v.x) * w.x, (rinv * v.y) * w.y, (rinv * v.z) * w.z, (rinv * v.w) * w.w);
+    }
+    store_h4(out + k, v);
+  }
+}
+
+// PREP_SWIGLU for the wide f16 GEMM: bh = f16(silu(g) * u), one wave per
+// (superblock, column) as in k_prep.
+__global__ __launch_bounds__(64) void k_prep16_swiglu(PrepArgs a) {
+  const uint32_t sb = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
+  const uint32_t k = 256 * sb + 4 * lane;
+  if (k >= a.K) return;
+  const size_t pstride = (size_t)a.part_cols * a.part_ld;
+  const float* pc = a.part + (size_t)col * a.part_ld + 32 * (k / 16) + k % 16;
+  const float4 g = sum_parts(pc, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
+  const float4 u = sum_parts(pc + 16, pstride, a.nparts, make_float4(0.f, 0.f, 0.f, 0.f));
+  const float4 v = make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
+                               (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
+  store_h4(a.bh + (size_t)col * a.ldb + k, v);
+}
+
 int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
   SH_CHECK(a.K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", a.K);
+  if (a.bh) {
+    SH_CHECK(a.N >= 1 && a.N <= SH_MAX_COLS && a.ldb >= a.K, SH_ERR_ARG, "f16 prep N=%u (at most %u), ldb %u < K %u",
+             a.N, SH_MAX_COLS, a.ldb, a.K);
+    SH_CHECK(a.part_cols >= a.N || a.nparts == 0, SH_ERR_ARG, "prep: partials hold %u columns, N=%u", a.part_cols,
+             a.N);
+    SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");
+    SH_CHECK(a.mode != PREP_RESID || a.nparts == 0 || a.part, SH_ERR_ARG, "prep partials missing");
+    hipEvent_t ev = nullptr;
+    sh_prof_begin(e, &ev);
+    if (a.mode == PREP_SWIGLU)
+      hipLaunchKernelGGL(k_prep16_swiglu, dim3((a.K + 255) / 256, a.N), dim3(64), 0, e->stream, a);
+    else if (a.mode == PREP_RESID)
+      hipLaunchKernelGGL((k_prep16_rows<PREP_RESID>), dim3(a.N), dim3(1024), 0, e->stream, a);
+    else
+      hipLaunchKernelGGL((k_prep16_rows<PREP_PLAIN>), dim3(a.N), dim3(1024), 0, e->stream, a);
+    SH_HIP(hipGetLastError());
+    sh_prof_end(e, a.norm_w ? "rmsnorm_prep" : "prep", 0.0, ev);
+    return SH_OK;
+  }
   SH_CHECK(a.N >= 1 && a.N <= SH_MAX_PREP_COLS, SH_ERR_ARG, "prep N=%u outside [1, %u]", a.N, SH_MAX_PREP_COLS);
   SH_CHECK(a.part_cols >= a.N || a.nparts == 0, SH_ERR_ARG, "prep: partials hold %u columns, N=%u", a.part_cols, a.N);
   SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");

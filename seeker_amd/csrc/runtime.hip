@@ -218,7 +218,7 @@ static void free_model(sh_model* m) {
   Workspace& w = m->ws;
   (void)hipFree(w.resid); (void)hipFree(w.resid2); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
   (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part); (void)hipFree(w.fab_part);
-  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq);
+  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq); (void)hipFree(w.bh);
   (void)hipFree(w.bx2); (void)hipFree(w.xs2); (void)hipFree(w.cs2); (void)hipFree(w.ssq2); (void)hipFree(w.sb_cnt);
   (void)hipFree(w.moe_logits); (void)hipFree(w.moe_ids); (void)hipFree(w.moe_wts); (void)hipFree(w.moe_info); (void)hipFree(w.moe_col);
   (void)hipFree(w.moe_slot); (void)hipFree(w.moe_hgu); (void)hipFree(w.moe_bx); (void)hipFree(w.moe_xs);
@@ -343,6 +343,13 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
               (lt == GGML_Q4_K || lt == GGML_Q8_0);
     m->fused_ok = fused;
     if (!ok && !fused) FAIL(SH_ERR_UNSUPPORTED, "weight types: neither all K-quants nor uniform Q4_K / Q8_0 layers");
+    bool w16 = m->n_expert == 0 && m->lm_head.type == GGML_Q4_K;
+    for (const Layer& L : m->layers)
+      w16 = w16 && !L.wv.d && L.wqkv.type == GGML_Q4_K && L.wo.type == GGML_Q4_K && L.wgu.type == GGML_Q4_K &&
+            L.wdown.type == GGML_Q4_K;
+    m->wide16_ok = w16;
+    const char* env16 = getenv("SH_WIDE_F16");
+    m->wide16 = w16 && !(env16 && atoi(env16) == 0);
   }
   // workspace for up to SH_MAX_COLS columns per chunk (operands: 8 groups of 8)
   Workspace& w = m->ws;
@@ -364,7 +371,7 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       dalloc(&w.q, C * wide) || dalloc(&w.attn, C * wide) || dalloc(&w.gpart, gpart_floats) ||
       dalloc(&w.h, C * std::max(m->ff, 1u)) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
       dalloc(&w.tokens, C + 64) || dalloc(&w.amax, SH_AMAX_WORDS) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
-      dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
+      dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bh, C * kmax) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
       dalloc(&w.cs2, sh_grp_cs(m->d)) || dalloc(&w.ssq2, sh_grp_cs(m->d)) || dalloc(&w.sb_cnt, SH_SB_CNT * SH_SB_CNT_STRIDE))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
@@ -425,6 +432,20 @@ extern "C" int sh_model_info(const sh_model* m, sh_model_dims* o) {
   o->rms_eps = m->eps; o->rope_freq_base = m->theta;
   o->weight_type = m->layers.empty() ? -1 : m->layers[0].wo.type;
   o->weight_bytes = m->alg_weight_bytes;
+  return SH_OK;
+}
+
+extern "C" int sh_model_wide_f16(const sh_model* m, int* on) {
+  SH_CHECK(m && on, SH_ERR_ARG, "sh_model_wide_f16: NULL argument");
+  *on = m->wide16 ? 1 : 0;
+  return SH_OK;
+}
+
+extern "C" int sh_model_set_wide_f16(sh_model* m, int on) {
+  SH_CHECK(m, SH_ERR_ARG, "sh_model_set_wide_f16: NULL model");
+  SH_CHECK(!on || m->wide16_ok, SH_ERR_UNSUPPORTED,
+           "wide f16 GEMMs need a model without routed experts whose matrices are all Q4_K");
+  m->wide16 = on != 0;
   return SH_OK;
 }
 
@@ -857,15 +878,23 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     qc.pos[j] = cols[j].pos; qc.slot[j] = cols[j].slot; qc.mseq[j] = cols[j].kv->max_seq;
     qc.kc[j] = cols[j].kv->k; qc.vc[j] = cols[j].kv->v;
   }
+  // Wide calls (m->call16) stage f16 rows in w.bh and run every dense matmul
+  // through sh_gemm16_launch; else the hi/lo operand groups and sh_gemm_launch.
+  const bool f16 = m->call16;
   PrepArgs pr;
   pr.N = nc; pr.bx = w.bx; pr.xs = w.xs; pr.cs = w.cs; pr.part = w.gpart; pr.part_cols = ncp; pr.eps = m->eps;
   pr.ssq = w.ssq;
+  if (f16) pr.bh = w.bh;
   uint32_t pending = 0, pending_ld = 0;
   auto resid_prep = [&](const float* norm_w) {
-    pr.mode = PREP_RESID; pr.x = w.resid; pr.K = m->d; pr.norm_w = norm_w;
+    pr.mode = PREP_RESID; pr.x = w.resid; pr.K = m->d; pr.norm_w = norm_w; pr.ldb = m->d;
     pr.nparts = pending; pr.part_ld = pending_ld;
     pending = 0;
     return sh_prep_launch(e, pr);
+  };
+  auto gemm = [&](const QMat& q, EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* np) {
+    return f16 ? sh_gemm16_launch(e, q, w.bh, q.K, nc, epi, ea, tag, np)
+               : sh_gemm_launch(e, q, w.bx, w.xs, w.cs, nc, epi, ea, tag, np);
   };
   // batched attention: one plan for the chunk's segments, one launch per layer
   FabGuard fab{e, FabLaunch{}};
@@ -878,7 +907,7 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     EpiArgs pq = part_args(L.wqkv);
     set_norm(pq);
     uint32_t nq = 0;
-    if ((rc = sh_gemm_launch(e, L.wqkv, w.bx, w.xs, w.cs, nc, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
+    if ((rc = gemm(L.wqkv, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
     qc.vpart = nullptr;
     if (L.wv.d) {  // v in a weight type of its own: its partials follow q / k's
       EpiArgs pv = part_args(L.wv);
@@ -886,7 +915,7 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
       pv.out = w.gpart + nq * pq.part_stride;
       pv.part_cap = (uint32_t)((w.gpart_floats - nq * pq.part_stride) / pv.part_stride);
       uint32_t nv = 0;
-      if ((rc = sh_gemm_launch(e, L.wv, w.bx, w.xs, w.cs, nc, EPI_PART, pv, "gemv_v", &nv))) return rc;
+      if ((rc = gemm(L.wv, EPI_PART, pv, "gemv_v", &nv))) return rc;
       qc.vpart = pv.out; qc.vnparts = nv; qc.vldp = pv.ldo; qc.vstride = pv.part_stride;
     }
     qkv.layer = l;
@@ -895,7 +924,7 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
                  : sh_qkv_finish_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc);
     if (rc) return rc;
     if (use_fab) {
-      if ((rc = sh_fab_launch(e, m, fab.fl, l, w.q, w.attn, w.bx, w.xs, w.cs))) return rc;
+      if ((rc = sh_fab_launch(e, m, fab.fl, l, w.q, w.attn, w.bx, w.xs, w.cs, f16 ? w.bh : nullptr))) return rc;
     } else {
       for (const FaSeg& sg : segs) {
         FaArgs fa;
@@ -904,9 +933,14 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
         fa.masks = sg.masks;
         if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
       }
+      if (f16) {  // the attention rows as the Wo operand
+        PrepArgs pa = pr;
+        pa.mode = PREP_PLAIN; pa.x = w.attn; pa.K = m->q_dim; pa.ldb = m->q_dim; pa.norm_w = nullptr; pa.nparts = 0;
+        if ((rc = sh_prep_launch(e, pa))) return rc;
+      }
     }
     EpiArgs po = part_args(L.wo);
-    if ((rc = sh_gemm_launch(e, L.wo, w.bx, w.xs, w.cs, nc, EPI_PART, po, "gemv_o", &pending))) return rc;
+    if ((rc = gemm(L.wo, EPI_PART, po, "gemv_o", &pending))) return rc;
     pending_ld = po.ldo;
     if ((rc = resid_prep(L.ffn_norm))) return rc;
     if (m->n_expert) {  // routed experts add into the residual themselves
@@ -916,11 +950,12 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     EpiArgs pg = part_args(L.wgu);
     set_norm(pg);
     uint32_t ngu = 0;
-    if ((rc = sh_gemm_launch(e, L.wgu, w.bx, w.xs, w.cs, nc, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
+    if ((rc = gemm(L.wgu, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
     pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = ngu; pr.part_ld = pg.ldo; pr.K = m->ff; pr.norm_w = nullptr;
+    pr.ldb = m->ff;
     if ((rc = sh_prep_launch(e, pr))) return rc;
     EpiArgs pd = part_args(L.wdown);
-    if ((rc = sh_gemm_launch(e, L.wdown, w.bx, w.xs, w.cs, nc, EPI_PART, pd, "gemv_down", &pending))) return rc;
+    if ((rc = gemm(L.wdown, EPI_PART, pd, "gemv_down", &pending))) return rc;
     pending_ld = pd.ldo;
   }
   if (want_logits) {
@@ -928,7 +963,7 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     EpiArgs st;
     st.out = w.logits; st.ldo = m->V; st.rows = m->V; st.cs = w.cs;
     set_norm(st);
-    if ((rc = sh_gemm_launch(e, m->lm_head, w.bx, w.xs, w.cs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
+    if ((rc = gemm(m->lm_head, EPI_STORE, st, "gemv_lm_head", nullptr))) return rc;
   } else if (want_resid && pending) {
     if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, ncp, m->d, nc, w.resid, m->d, true))) return rc;
   }
@@ -955,7 +990,7 @@ static uint32_t fa_seg_cols(const sh_model* m) {
 
 static int run_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, const ColKv* cols,
                      const std::vector<FaSeg>& segs, bool want_logits, bool want_resid) {
-  return (nc > 8 || !m->fused_ok) ? forward_chunk_mg(m, dev_tokens, nc, cols, segs, want_logits, want_resid)
+  return (nc > 8 || !m->fused_ok || m->call16) ? forward_chunk_mg(m, dev_tokens, nc, cols, segs, want_logits, want_resid)
                                            : forward_chunk(m, dev_tokens, nc, cols, segs, want_logits, want_resid);
 }
 
@@ -1034,6 +1069,7 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
     if ((rc = ensure_rope(m, maxpos + 1))) return rc;
     if ((rc = ensure_fa_part(m, pos + L))) return rc;
   }
+  m->call16 = m->wide16 && L >= SH_WIDE16_COLS;  // one matmul of L columns in the reference
   const uint32_t CW = chunk_cols(m, L);
   // Attention: one segment per chunk (device masks) on the multi-group path,
   // else pieces of <= 8 columns; a causal segment's masks are relative to its
@@ -1278,6 +1314,7 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
   uint32_t* ids = nullptr;
   if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, SH_MAX_COLS * 4, e->stream));
   const bool want_logits = logits_out || logits_dev || sampled_out;
+  m->call16 = m->wide16 && N >= SH_WIDE16_COLS;  // the reference's batch is one matmul of N columns
   const uint32_t CW = chunk_cols(m, N);
   // attention segments: runs of one sequence's columns in a chunk (at most 8
   // each on the 8-column path; device masks on the multi-group path)
@@ -1771,6 +1808,40 @@ extern "C" int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_d
   (void)hipFreeAsync(bx, e->stream);
   (void)hipFreeAsync(xs, e->stream);
   (void)hipFreeAsync(cs, e->stream);
+  (void)hipFreeAsync(part, e->stream);
+  if (rc) return rc;
+  SH_HIP(hipStreamSynchronize(e->stream));
+  return sh_prof_flush(e);
+}
+
+extern "C" int sh_gemm_wide16(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_t N, float* y_dev,
+                              int accumulate) {
+  SH_CHECK(e && w && x_dev && y_dev, SH_ERR_ARG, "sh_gemm_wide16: NULL argument");
+  SH_CHECK(N >= 1, SH_ERR_ARG, "N must be >= 1");
+  SH_CHECK(w->m.type == GGML_Q4_K && w->m.K % 256 == 0, SH_ERR_UNSUPPORTED,
+           "sh_gemm_wide16: Q4_K with K a multiple of 256 (type %d)", w->m.type);
+  const uint32_t K = w->m.K, M = w->m.M, CW = SH_MAX_COLS, ncp_max = CW;
+  const size_t part_floats = sh_gemm_part_floats(w->m);
+  uint16_t* bh = nullptr;
+  float* part = nullptr;
+  SH_HIP(hipMallocAsync((void**)&bh, (size_t)CW * K * 2, e->stream));
+  SH_HIP(hipMallocAsync((void**)&part, std::max<size_t>(part_floats, 4) * sizeof(float), e->stream));
+  int rc = SH_OK;
+  for (uint32_t c0 = 0; c0 < N && !rc; c0 += CW) {
+    const uint32_t nc = std::min<uint32_t>(CW, N - c0), ncp = (nc + 7) / 8 * 8;
+    PrepArgs pr;
+    pr.mode = PREP_PLAIN; pr.x = const_cast<float*>(x_dev + (size_t)c0 * K); pr.K = K; pr.N = nc;
+    pr.bh = bh; pr.ldb = K;
+    if ((rc = sh_prep_launch(e, pr))) break;
+    EpiArgs pa;
+    pa.out = part; pa.ldo = w->m.tiles * 16;
+    pa.part_stride = (size_t)ncp * pa.ldo;
+    pa.part_cap = (uint32_t)(part_floats / ((size_t)ncp_max * pa.ldo));
+    uint32_t np = 0;
+    rc = sh_gemm16_launch(e, w->m, bh, K, nc, EPI_PART, pa, "gemm16", &np);
+    if (!rc) rc = sh_part_reduce_launch(e, part, np, pa.ldo, ncp, M, nc, y_dev + (size_t)c0 * M, M, accumulate != 0);
+  }
+  (void)hipFreeAsync(bh, e->stream);
   (void)hipFreeAsync(part, e->stream);
   if (rc) return rc;
   SH_HIP(hipStreamSynchronize(e->stream));

@@ -45,6 +45,7 @@ constexpr uint32_t SH_MAX_COLS = 64;     // columns per forward chunk (8 operand
 constexpr uint32_t SH_AMAX_WORDS = SH_MAX_COLS + 8 * SH_MAX_COLS;
 constexpr uint32_t SH_MAX_PREP_COLS = 512;  // operand columns one prep builds (the MoE down operand: pairs)
 constexpr int SH_FA_MIN_SPLIT_KEYS = 64;  // smallest key split of any attention launch (sizes fa_part)
+constexpr uint32_t SH_WIDE16_COLS = 32;  // the reference's wide-GEMM threshold (ops/matmul.rs:433-446)
 constexpr int SH_FA_MAX_ROWS = 256;       // padded query rows (gqa x columns) per kv head
 // Split partial row: O[hd], m, l, 2 pad (keeps rows 16-byte aligned).
 __host__ __device__ constexpr uint32_t sh_fa_part_stride(uint32_t hd) { return hd + 4; }
@@ -144,6 +145,7 @@ struct Workspace {
   unsigned long long* amax = nullptr;  // SH_AMAX_WORDS: packed argmax keys, then per-column arrival counters (zeroed)
   float* cs = nullptr;        // [max(K)/256][8] inverse activation scales of the current B operand
   float* ssq = nullptr;       // [max(K)/256][8] per-superblock sums of squares of the normalized input
+  uint16_t* bh = nullptr;     // [cols][max(K)] f16 operand rows of the wide f16 GEMM
   size_t fa_part_floats = 0;
   float* fab_part = nullptr;  // batched attention partials of every segment of a chunk (grown on demand)
   size_t fab_part_floats = 0;
@@ -192,6 +194,14 @@ struct sh_model {
   double alg_weight_bytes = 0;  // bytes of every matrix a full-logits forward reads
   bool mg_ok = false;     // every matrix a K-quant: the multi-group path can run any chunk
   bool fused_ok = false;  // llama with uniform Q4_K / Q8_0 layers: chunks of <= 8 columns take the fused path
+  // Forward calls of at least SH_WIDE16_COLS columns compute every dense matmul
+  // as the reference's wide GEMM does (f16 weights and activations, f32
+  // accumulation; sh_gemm16_launch): wide16_ok when the model allows it (no
+  // routed experts, every matrix Q4_K), wide16 the switch (default on where
+  // allowed), call16 set for the forward call in progress.
+  bool wide16_ok = false;
+  bool wide16 = false;
+  bool call16 = false;
 };
 
 struct sh_kv {
@@ -316,6 +326,12 @@ int sh_gemv_ring_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const u
 int sh_gemm_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, const float* cs, uint32_t N,
                    EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
 size_t sh_gemm_part_floats(const QMat& w);  // for SH_MAX_COLS columns
+// y = W x with the reference's wide-GEMM arithmetic (f16 weights and
+// activations, f32 accumulation) for N <= SH_MAX_COLS columns of f16 rows
+// bh[col * ldb + k] (k_prep16_*), W Q4_K: EPI_PART (partials as
+// sh_gemm_launch's; *nparts = splits) or EPI_STORE (out[col][row]).
+int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, EpiKind epi,
+                     const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
 // Fused QKV rows from sh_gemm_launch partials: RoPE, q out, K/V into each
 // column's cache slot.
 struct QkvCols {  // per column: RoPE position, cache slot, capacity, K and V caches
@@ -367,6 +383,11 @@ struct PrepArgs {
   uint16_t* bx = nullptr;
   uint16_t* xs = nullptr;
   float* cs = nullptr;
+  // With bh: the operand of the wide f16 GEMM instead, bh[col * ldb + k] =
+  // f16(y) with the RMS norm applied (y = (v * rsqrt(mean v^2 + eps)) * w),
+  // as the reference's wide GEMM stages its input; ssq, bx, xs, cs unused.
+  uint16_t* bh = nullptr;
+  uint32_t ldb = 0;
 };
 // N <= SH_MAX_PREP_COLS; the operand buffers hold ceil(N / 8) groups.
 int sh_prep_launch(sh_engine* e, const PrepArgs& a);
@@ -420,7 +441,7 @@ struct FabLaunch {
 };
 int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, uint32_t nc, FabLaunch* out);
 int sh_fab_launch(sh_engine* e, const sh_model* m, const FabLaunch& fl, uint32_t layer, const float* q, float* attn_out,
-                  uint16_t* bx, uint16_t* xs, float* cs);
+                  uint16_t* bx, uint16_t* xs, float* cs, uint16_t* bh = nullptr);
 void sh_fab_free(sh_engine* e, FabLaunch& fl);
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids);

@@ -233,6 +233,11 @@ class Engine:
     def gemv(self, w: "QTensor", x: "DeviceBuffer", n: int, y: "DeviceBuffer", accumulate: bool = False):
         N.check(self._lib.sh_gemv_quant(self.h, w.h, x.ptr, n, y.ptr, int(accumulate)))
 
+    def gemm_wide16(self, w: "QTensor", x: "DeviceBuffer", n: int, y: "DeviceBuffer", accumulate: bool = False):
+        """The reference's wide-GEMM arithmetic (f16 weights and activations, f32
+        accumulation; ops/matmul.rs:433-446), Q4_K."""
+        N.check(self._lib.sh_gemm_wide16(self.h, w.h, x.ptr, n, y.ptr, int(accumulate)))
+
     def accept_sample(self, p_logits: "DeviceBuffer", q_logits: Optional["DeviceBuffer"], drafts: "DeviceBuffer",
                       B: int, k: int, V: int, s: N.sh_sampling, acc_len: "DeviceBuffer", next_tok: "DeviceBuffer"):
         N.check(self._lib.sh_accept_sample(self.h, p_logits.ptr, q_logits.ptr if q_logits else None, drafts.ptr,
@@ -303,6 +308,19 @@ class Model:
 
     def vocab_size(self) -> int:
         return self.dims.n_vocab
+
+    @property
+    def wide_f16(self) -> bool:
+        """Whether forward calls of >= 32 columns take the reference's wide-GEMM
+        arithmetic (f16 weights and activations, f32 accumulation;
+        ops/matmul.rs:406-446)."""
+        on = C.c_int()
+        N.check(self.engine._lib.sh_model_wide_f16(self.h, C.byref(on)))
+        return bool(on.value)
+
+    @wide_f16.setter
+    def wide_f16(self, on: bool):
+        N.check(self.engine._lib.sh_model_set_wide_f16(self.h, 1 if on else 0))
 
     def close(self):
         if self.h:

@@ -3,12 +3,15 @@ against the C oracle on the same synthetic GGUF bytes.
 
 Tolerances (north star): logits within 2e-2 absolute or 1e-2 relative; greedy
 ids identical. Measured errors are ~1e-5, so the tests also assert a tighter
-3e-4 x max|logit| bound to catch regressions early.
+3e-4 x max|logit| bound to catch regressions early; after a wide call (>= 32
+columns on the all-Q4_K models, the reference's f16 wide-GEMM arithmetic) the
+bounds of tests/parity.py.
 """
 import numpy as np
 import pytest
 
 import oracle as O
+from parity import ids_agree, kv_layer0_ok, logits_close
 from seeker_amd import SeekerError
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K, GGML_Q8_0, SH_ERR_ARG, SH_ERR_CAPACITY, SH_ERR_STATE
@@ -31,19 +34,18 @@ def pair(request, engine):
     print(f"model {request.param}", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
+    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
     yield request.param, img, gm, om
     gm.close()
     om.close()
     img.close()
 
 
-def close(a, b):
-    tol = np.maximum(2e-2, 1e-2 * np.abs(b))
-    assert np.all(np.abs(a - b) <= tol)
-    assert np.abs(a - b).max() <= 3e-4 * np.abs(b).max(), np.abs(a - b).max()
+def close(a, b, wide=False):
+    logits_close(a, b, wide)
 
 
-def kv_close(g_bits, o_bits, layer):
+def kv_close(g_bits, o_bits, layer, wide=False):
     """Same f16 cache entries. Layer 0 sees identical inputs on both sides, so its
     entries may differ only where the f32 value sits on an f16 rounding boundary
     (one ulp, a small fraction). A one-ulp f16 flip is a 2^-11 relative change,
@@ -55,21 +57,11 @@ def kv_close(g_bits, o_bits, layer):
     print(f"kv layer {layer}: max|d|={np.abs(g - o).max():.3e} scale={np.abs(o).max():.3e} differing={frac:.4f}",
           flush=True)
     if layer == 0:
-        # one ulp, or ~1e-6 of the layer scale for entries near zero
-        assert np.all(np.abs(g - o) <= np.abs(o) * 2.0 ** -10 + 1e-6 * np.abs(o).max())
-        assert frac < 0.01
+        # one ulp, or a small fraction of the layer scale for entries near zero
+        assert kv_layer0_ok(g, o, wide)
+        assert frac < (0.05 if wide else 0.01)
     else:
-        assert np.abs(g - o).max() <= 1e-3 * np.abs(o).max()
-
-
-def margins_ok(gpu, ref):
-    """Greedy ids equal; report columns whose top-2 margin is tiny."""
-    ga, ra = gpu.argmax(axis=1), ref.argmax(axis=1)
-    srt = np.sort(ref, axis=1)
-    margin = srt[:, -1] - srt[:, -2]
-    bad = np.where(ga != ra)[0]
-    assert all(margin[i] < 1e-4 for i in bad), (bad, margin[bad])
-    return int((ga != ra).sum())
+        assert np.abs(g - o).max() <= (4e-3 if wide else 1e-3) * np.abs(o).max()
 
 
 def test_prefill_and_verify(engine, pair):
@@ -78,30 +70,35 @@ def test_prefill_and_verify(engine, pair):
     prompt = S.tokens(1234, 64, V)
     gkv = engine.allocate_kv_cache(gm, 256)
     okv = O.KvCache(om, 256)
-    print(f"{name}: prefill 64", flush=True)
+    wide = gm.wide_f16  # the 64-column prefill is a wide call
+    print(f"{name}: prefill 64 (wide f16 {wide})", flush=True)
     gl, gr = engine.forward_full_readback(gm, gkv, prompt, 0, full_logits=True)
     ol, orr = O.forward(om, okv, prompt, 0)
-    close(gl, ol)
-    np.testing.assert_allclose(gr, orr, rtol=1e-3, atol=1e-3 * np.abs(orr).max())
-    assert margins_ok(gl, ol) == 0
+    close(gl, ol, wide)
+    np.testing.assert_allclose(gr, orr, rtol=1e-3, atol=(4e-3 if wide else 1e-3) * np.abs(orr).max())
+    ids_agree(gl, ol, wide)
     assert gkv.position == 64
     # verify chunk of L = 5 at P = 64
     vt = S.tokens(99, 5, V)
     print(f"{name}: verify 5", flush=True)
     gl2, _ = engine.forward_full_readback(gm, gkv, vt, 64)
     ol2, _ = O.forward(om, okv, vt, 64)
-    close(gl2, ol2)
+    close(gl2, ol2, wide)
     # KV cache: same f16 values up to one ulp at rounding boundaries
     for layer in range(gm.dims.n_layer):
         for isv in (False, True):
-            kv_close(gkv.read_layer(layer, isv, 69), okv.layer(layer, isv, 69), layer)
+            kv_close(gkv.read_layer(layer, isv, 69), okv.layer(layer, isv, 69), layer, wide)
     # rollback: truncate and re-verify other tokens at the same position
     gkv.truncate(66)
     okv.truncate(66)
     vt2 = S.tokens(100, 3, V)
     ids = engine.verify_greedy(gm, gkv, vt2, 66)
     ol3, _ = O.forward(om, okv, vt2, 66)
-    assert np.array_equal(ids, ol3.argmax(axis=1))
+    if wide:  # near-ties of the oracle allowed, as for the logits above
+        bad = np.where(ids != ol3.argmax(axis=1))[0]
+        assert all(ol3[i].max() - ol3[i, ids[i]] <= 2 * 1.5e-3 * np.abs(ol3).max() for i in bad)
+    else:
+        assert np.array_equal(ids, ol3.argmax(axis=1))
     gkv.close()
     okv.close()
 
@@ -114,25 +111,72 @@ def test_tree_verify_and_compact(engine, pair):
     parents = [-1, 0, 0, 0, 1, 1, 2, 3, 4, 6, 6, 7]
     gkv = engine.allocate_kv_cache(gm, 128)
     okv = O.KvCache(om, 128)
+    wide = gm.wide_f16  # the 40-column prefill is a wide call
     engine.forward_full_readback(gm, gkv, prompt, 0, full_logits=False)
     O.forward(om, okv, prompt, 0, logits_mode=0)
     print(f"{name}: tree 12", flush=True)
     gl, _ = engine.forward_full_readback(gm, gkv, nodes, 40, parents=parents)
     ol, _ = O.forward(om, okv, nodes, 40, parents=parents)
-    close(gl, ol)
+    close(gl, ol, wide)
     # accept path 0 -> 2 -> 6 -> 9 and compact it behind the prefix
     path = [0, 2, 6, 9]
     gkv.compact(40, path)
     okv.compact(40, path)
     assert gkv.position == 44
     for layer in range(gm.dims.n_layer):
-        kv_close(gkv.read_layer(layer, True, 44), okv.layer(layer, True, 44), layer)
+        kv_close(gkv.read_layer(layer, True, 44), okv.layer(layer, True, 44), layer, wide)
     nxt = S.tokens(9, 2, V)
     gl2, _ = engine.forward_full_readback(gm, gkv, nxt, 44)
     ol2, _ = O.forward(om, okv, nxt, 44)
-    close(gl2, ol2)
+    close(gl2, ol2, wide)
     gkv.close()
     okv.close()
+
+
+def test_wide_calls_follow_reference_f16(engine, pair):
+    """A call of >= 32 columns on an all-Q4_K model computes its matmuls with
+    the reference's wide-GEMM operands (ops/matmul.rs:433-446): its logits sit
+    clearly closer to the oracle in mode 2 (same f16 roundings) than to the
+    exact oracle, and the other way round with the switch off; a narrow call is
+    bit-identical either way."""
+    name, img, gm, om = pair
+    if not gm.wide_f16:
+        pytest.skip("model without the wide f16 path (not all Q4_K)")
+    V = gm.dims.n_vocab
+    toks = S.tokens(21, 40, V)
+    res = {}
+    for on in (True, False):
+        gm.wide_f16 = on
+        gkv = engine.allocate_kv_cache(gm, 64)
+        gl, _ = engine.forward_full_readback(gm, gkv, toks, 0)
+        nl, _ = engine.forward_full_readback(gm, gkv, toks[:6], 40)
+        res[on] = (gl, nl)
+        gkv.close()
+    gm.wide_f16 = True
+    ref = {}
+    for mode in (2, 0):
+        om.set_mm16(mode)
+        okv = O.KvCache(om, 64)
+        ref[mode], _ = O.forward(om, okv, toks, 0)
+        okv.close()
+    om.set_mm16(2)
+    d = {(on, mode): float(np.abs(res[on][0] - ref[mode]).max()) for on in (True, False) for mode in (2, 0)}
+    print(f"{name}: wide call max|d| {d}", flush=True)
+    assert d[(True, 2)] < 0.75 * d[(True, 0)]
+    assert d[(False, 0)] < 0.75 * d[(False, 2)]
+    logits_close(res[True][0], ref[2], wide=True)
+    # the 6-column call after differs only through the cache the wide call wrote
+    g1 = engine.allocate_kv_cache(gm, 64)
+    engine.forward_full_readback(gm, g1, toks[:20], 0)
+    a, _ = engine.forward_full_readback(gm, g1, toks[20:26], 20)
+    gm.wide_f16 = False
+    g2 = engine.allocate_kv_cache(gm, 64)
+    engine.forward_full_readback(gm, g2, toks[:20], 0)
+    b, _ = engine.forward_full_readback(gm, g2, toks[20:26], 20)
+    gm.wide_f16 = True
+    assert np.array_equal(a, b)
+    g1.close()
+    g2.close()
 
 
 def test_errors_are_reported(engine, pair):

@@ -185,6 +185,7 @@ def model(request, engine):
     print(f"model {request.param}", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
+    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
     yield request.param, gm, om
     gm.close()
     om.close()
@@ -225,6 +226,8 @@ def test_mixed_spec_steps_match_oracle(engine):
     t_img, d_img = S.GgufImage(Q4KM, seed=41), S.GgufImage(Q5KM, seed=42)
     gt, gd = engine.upload_weights(t_img), engine.upload_weights(d_img)
     ot, od = O.Model(t_img), O.Model(d_img)
+    ot.set_mm16(2 if gt.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    od.set_mm16(2 if gd.wide_f16 else 0)
     V = gt.dims.n_vocab
     prompt = S.tokens(77, 24, V)
     gtkv, gdkv = engine.allocate_kv_cache(gt, 256), engine.allocate_kv_cache(gd, 256)

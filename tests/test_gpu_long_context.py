@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from parity import ids_agree, logits_close
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K
 
@@ -23,16 +24,15 @@ SHAPE = S.LlamaShape(1, 512, 8, 2, 1024, 4000, 4096, 1e-5, 5e5, 0.02, GGML_Q4_K,
 P = 2100
 
 
-def close(a, b):
-    tol = np.maximum(2e-2, 1e-2 * np.abs(b))
-    assert np.all(np.abs(a - b) <= tol)
-    assert np.abs(a - b).max() <= 3e-4 * np.abs(b).max(), np.abs(a - b).max()
+def close(a, b, wide=False):
+    logits_close(a, b, wide)  # after a wide prefill: the bounds of tests/parity.py
 
 
 def test_seventeen_attention_splits(engine):
     img = S.GgufImage(SHAPE, seed=21)
     gm = engine.upload_weights(img)
     om = O.Model(img)
+    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
     V = gm.dims.n_vocab
     gkv = engine.allocate_kv_cache(gm, 2304)
     okv = O.KvCache(om, 2304)
@@ -45,10 +45,14 @@ def test_seventeen_attention_splits(engine):
         print(f"verify {n} columns at {P}", flush=True)
         gl, _ = engine.forward_full_readback(gm, gkv, toks, P)
         ol, _ = O.forward(om, okv, toks, P)
-        close(gl, ol)
+        close(gl, ol, gm.wide_f16)
         gkv.truncate(P)
         ids = engine.verify_greedy(gm, gkv, toks, P)
-        assert np.array_equal(ids, ol.argmax(axis=1)), (ids, ol.argmax(axis=1))
+        if gm.wide_f16:  # prefill >= 32 columns: near-ties of the oracle allowed
+            bad = np.where(ids != ol.argmax(axis=1))[0]
+            assert all(ol[i].max() - ol[i, ids[i]] <= 3e-3 * np.abs(ol).max() for i in bad), (ids, ol.argmax(axis=1))
+        else:
+            assert np.array_equal(ids, ol.argmax(axis=1)), (ids, ol.argmax(axis=1))
         gkv.truncate(P)
         okv.truncate(P)
     gkv.close()

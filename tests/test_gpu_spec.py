@@ -21,6 +21,8 @@ def models(engine):
     di = S.GgufImage(S.TINY_DRAFT, seed=1)
     gt, gd = engine.upload_weights(ti), engine.upload_weights(di)
     ot, od = O.Model(ti), O.Model(di)
+    ot.set_mm16(2 if gt.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    od.set_mm16(2 if gd.wide_f16 else 0)
     yield gt, gd, ot, od
     for m in (gt, gd, ot, od):
         m.close()

@@ -111,6 +111,7 @@ def test_unified_tree_and_chain_vs_oracle(engine, model):
     name, img, gm = model
     V = gm.vocab_size()
     om = O.Model(img)
+    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
     parents_tree = [-1, 0, 0, 1, 1, 2, 2]
     seqs = [(24, S.tokens(301, 7, V), parents_tree), (16, S.tokens(302, 6, V), None)]
     prompts = [S.tokens(400 + s, p, V) for s, (p, _, _) in enumerate(seqs)]

@@ -1,0 +1,75 @@
+"""GPU parity of the wide f16 GEMM (C ABI sh_gemm_wide16, the kernels of forward
+calls of >= 32 columns) against the oracle's or_gemv16.
+
+The reference computes matmuls of N >= 32 columns with its cooperative-matrix
+GEMM (ops/matmul.rs:433-446, mul_mm_cm.slang): weights dequantized in f32 and
+rounded to f16, activations rounded to f16, f32 accumulation. or_gemv16 takes
+the same f16 operands and sums in f64, so the GPU differs from it only by f32
+summation order and by weights whose f16 rounding of the exact a q - b and of
+the oracle's twice-rounded f32 value differ in the last bit: bound 2e-5 x
+max|y|. The same outputs sit ~1e-4 of max|y| from the exact f64 GEMV (the f16
+rounding of the operands), which the test also checks, so a kernel that kept
+f32-level operands would fail the first bound.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from seeker_amd import QTensor
+from seeker_amd import synth as S
+from seeker_amd._native import GGML_Q4_K, GGML_Q8_0
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(engine, M, K, N, seed=0, accumulate=False):
+    print(f"wide16 case M={M} K={K} N={N} acc={accumulate}", flush=True)
+    w = S.quantize(GGML_Q4_K, S.normal_f32(seed, 1, M * K, 0.0, 0.02))
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    y0 = rng.standard_normal((N, M)).astype(np.float32) if accumulate else np.zeros((N, M), np.float32)
+    qt = QTensor(engine, GGML_Q4_K, w, M, K)
+    xd, yd = engine.to_device(x), engine.to_device(y0)
+    engine.gemm_wide16(qt, xd, N, yd, accumulate)
+    got = yd.read(np.float32, N * M).reshape(N, M)
+    add = y0 if accumulate else 0
+    ref16 = O.gemv16(GGML_Q4_K, w, M, K, x) + add
+    exact = O.gemv(GGML_Q4_K, w, M, K, x) + add
+    xd.free(); yd.free(); qt.close()
+    return got, ref16, exact
+
+
+@pytest.mark.parametrize("N", [1, 13, 32, 47, 64, 70])
+def test_wide16_small(engine, N):
+    got, ref, exact = _run(engine, 80, 512, N, seed=N)
+    scale = np.abs(ref).max()
+    err, dex = np.abs(got - ref).max() / scale, np.abs(got - exact).max() / scale
+    print(f"  vs or_gemv16 {err:.2e}, vs exact {dex:.2e}", flush=True)
+    assert err < 2e-5, err
+    assert dex > 4 * err
+
+
+def test_wide16_ragged_rows_and_accumulate(engine):
+    got, ref, _ = _run(engine, 37, 768, 40, seed=3, accumulate=True)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
+
+
+@pytest.mark.parametrize("M,K,N", [(6144, 4096, 41), (4096, 4096, 64), (28672, 4096, 48), (4096, 14336, 36),
+                                   (128256, 4096, 33)])
+def test_wide16_8b_shapes(engine, M, K, N):
+    got, ref, exact = _run(engine, M, K, N, seed=M + K + N)
+    scale = np.abs(ref).max()
+    err, dex = np.abs(got - ref).max() / scale, np.abs(got - exact).max() / scale
+    print(f"  vs or_gemv16 {err:.2e}, vs exact {dex:.2e}", flush=True)
+    assert err < 2e-5, err
+    assert np.array_equal(got.argmax(axis=1), ref.argmax(axis=1))
+
+
+def test_wide16_refuses_other_types(engine):
+    from seeker_amd import SeekerError
+    w = S.quantize(GGML_Q8_0, S.normal_f32(1, 1, 64 * 256, 0.0, 0.02))
+    qt = QTensor(engine, GGML_Q8_0, w, 64, 256)
+    xd, yd = engine.to_device(np.ones((32, 256), np.float32)), engine.to_device(np.zeros((32, 64), np.float32))
+    with pytest.raises(SeekerError):
+        engine.gemm_wide16(qt, xd, 32, yd)
+    xd.free(); yd.free(); qt.close()

@@ -272,6 +272,34 @@ def test_forward_mm16_matches_numpy(small):
     m.close()
 
 
+def test_forward_mm16_auto_follows_call_width(small):
+    """Mode 2 (the reference's dispatch, ops/matmul.rs:433-446): a forward call
+    of >= 32 columns equals mode 1 exactly, one of fewer columns equals mode 0
+    exactly (the width is the call's, so a later narrow call after a wide
+    prefill is exact again)."""
+    m = O.Model(small)
+    out = {}
+    for mode in (0, 1, 2):
+        m.set_mm16(mode)
+        kv = O.KvCache(m, 96)
+        wide, _ = O.forward(m, kv, S.tokens(6, 40, m.V), 0)
+        narrow, _ = O.forward(m, kv, S.tokens(7, 5, m.V), 40)
+        out[mode] = (wide, narrow)
+        kv.close()
+    assert np.array_equal(out[2][0], out[1][0]) and not np.array_equal(out[2][0], out[0][0])
+    # the narrow call reads the wide call's K/V: mode 2 matches mode 1's cache
+    # and mode 0's matmuls, so it equals neither whole; rerun it from mode 1's
+    # cache with exact matmuls
+    m.set_mm16(1)
+    kv = O.KvCache(m, 96)
+    O.forward(m, kv, S.tokens(6, 40, m.V), 0)
+    m.set_mm16(0)
+    narrow0, _ = O.forward(m, kv, S.tokens(7, 5, m.V), 40)
+    assert np.array_equal(out[2][1], narrow0)
+    kv.close()
+    m.close()
+
+
 def test_forward_incremental_equals_batch(small):
     m = O.Model(small)
     toks = S.tokens(7, 9, m.V)
