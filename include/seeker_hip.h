@@ -237,7 +237,7 @@ int sh_gemv_quant(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_
 /* The reference's wide GEMM for N >= 32 columns (ops/matmul.rs:433-446,
  * mul_mm_cm.slang): y[j][m] (+)= sum_k f16(deq(W)[m][k]) * f16(x[j][k]) with
  * f32 accumulation, W Q4_K; the kernels the forward uses for calls of >= 32
- * columns (sh_model_wide_f16). Any N >= 1 (64 columns per pass). */
+ * columns (sh_model_wide_f16). Any N >= 1 (192 columns per pass). */
 int sh_gemm_wide16(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32_t N, float* y_dev,
                    int accumulate);
 

@@ -1592,6 +1592,135 @@ __global__ __launch_bounds__(512) void k_gemm16_q4k(const uint8_t* __restrict__ 
     }
 }
 
+// y = W x over 64 < N <= 16 NC columns (up to 192) of f16 rows bh [N][ldb],
+// W Q4_K: one pass over the weights for every column of a wide call. A
+// workgroup of 8 waves (two per SIMD) covers 16 row tiles, wave w tiles
+// (blockIdx.x * 8 + w) * 2 + t, over the superblocks of split blockIdx.y, in
+// stages of half a superblock (sub-blocks 4h .. 4h + 3). A wave decodes each
+// of its 2 tiles' f16 fragments once per sub-block and feeds it to NC MFMAs,
+// each B fragment read from LDS feeds 2: the decode is ~2.5 VALU instructions
+// per MFMA at 192 columns. B goes through two LDS buffers by direct loads and
+// the weight words to registers, both one stage ahead of the compute.
+template <int NC, int EPI>
+__global__ __launch_bounds__(512) void k_gemm16w_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                     uint32_t S, const uint16_t* __restrict__ Bh, uint32_t ldb,
+                                                     uint32_t N, EpiArgs ea) {
+  constexpr int T = 2, WV = 8;
+  __shared__ h8 sB[2][NC * 4 * 64];  // [buffer][(column group * 4 + sub-block) * 64 + lane]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4, r = lane & 15;
+  const uint32_t ks = blockIdx.y, sb0 = ks * S, sb1 = min(sb0 + S, nsb), nst = 2 * (sb1 - sb0);
+  const uint32_t tile0 = (blockIdx.x * WV + wave) * T;
+  const uint8_t* tb[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)  // clamped tiles keep the loads in bounds; their sums are dropped
+    tb[t] = Wp + (size_t)(tile0 + t < tiles ? tile0 + t : tiles - 1) * nsb * SH_Q4K_TILE_BYTES;
+
+  struct WStage {
+    u32x4 q[T];
+    uint32_t dd[T], s0[T], s1[T], s2[T];
+  };
+  auto load_w = [&](uint32_t s, WStage& w) __attribute__((always_inline)) {
+    const uint32_t sb = sb0 + (s >> 1), h = s & 1;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint8_t* base = tb[t] + (size_t)sb * SH_Q4K_TILE_BYTES;
+      w.q[t] = ld16(base + 1024 * h + 16 * lane);
+      w.dd[t] = *(const uint32_t*)(base + 2048 + 4 * r);
+      const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
+      w.s0[t] = sp[0];
+      w.s1[t] = sp[1];
+      w.s2[t] = sp[2];
+    }
+  };
+  auto issue_b = [&](uint32_t s, int buf) __attribute__((always_inline)) {
+    const uint32_t sb = sb0 + (s >> 1), h = s & 1;
+    for (uint32_t fi = wave; fi < (uint32_t)(NC * 4); fi += WV) {  // NC / 2 per wave
+      const uint32_t c = fi >> 2, mp = fi & 3;
+      const uint32_t col = min(16 * c + (uint32_t)r, N - 1);
+      sh_dma16(Bh + (size_t)col * ldb + 256 * sb + 32 * (4 * h + mp) + 8 * g4, &sB[buf][fi * 64]);
+    }
+  };
+
+  f4 acc[T][NC];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const WStage& w, int buf, int h) __attribute__((always_inline)) {
+    // the Q4_K 6-bit unpack of sub-blocks 4h .. 4h + 3 (q4_decode_setup)
+    uint32_t scw[T], mw[T];
+    float d24[T], ndmin[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      scw[t] = h == 0 ? (w.s0[t] & 0x3F3F3F3Fu) : ((w.s2[t] & 0x0F0F0F0Fu) | ((w.s0[t] >> 2) & 0x30303030u));
+      mw[t] = h == 0 ? (w.s1[t] & 0x3F3F3F3Fu) : (((w.s2[t] >> 4) & 0x0F0F0F0Fu) | ((w.s1[t] >> 2) & 0x30303030u));
+      d24[t] = (float)as_h2(w.dd[t]).x * 16777216.0f;
+      ndmin[t] = -(float)as_h2(w.dd[t]).y;
+    }
+#pragma unroll
+    for (int mp = 0; mp < 4; ++mp) {
+      h8 a[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float a24 = d24[t] * (float)((scw[t] >> (8 * mp)) & 0xFFu), a20 = a24 * 0.0625f;
+        const float nb = ndmin[t] * (float)((mw[t] >> (8 * mp)) & 0xFFu);
+        const uint32_t word = mp == 0 ? w.q[t].x : mp == 1 ? w.q[t].y : mp == 2 ? w.q[t].z : w.q[t].w;
+        const uint32_t w8 = word >> 8;
+        u32x4 v;
+        v.x = fma_mix_pair(word & 0x000F000Fu, a24, nb);
+        v.y = fma_mix_pair(word & 0x00F000F0u, a20, nb);
+        v.z = fma_mix_pair(w8 & 0x000F000Fu, a24, nb);
+        v.w = fma_mix_pair(w8 & 0x00F000F0u, a20, nb);
+        a[t] = as_h8(v);
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const h8 b = sB[buf][(c * 4 + mp) * 64 + lane];
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t][c] = mfma16(a[t], b, acc[t][c]);
+      }
+    }
+  };
+
+  WStage w0, w1;
+  issue_b(0, 0);
+  load_w(0, w0);
+  auto step = [&](uint32_t s, WStage& cur, WStage& nxt, int u) __attribute__((always_inline)) {
+    // B and weights of stage s landed; every wave is done with stage s - 1's
+    // B buffer, which stage s + 1 now refills (its weights follow its B)
+    sh_wait_vm<0>();
+    __syncthreads();
+    if (s + 1 < nst) {
+      issue_b(s + 1, (u + 1) & 1);
+      load_w(s + 1, nxt);
+    }
+    compute(cur, u & 1, u & 1);
+  };
+  for (uint32_t s = 0; s < nst; s += 2) {
+    step(s, w0, w1, 0);
+    if (s + 1 < nst) step(s + 1, w1, w0, 1);
+  }
+
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t tile = tile0 + t, col = 16 * c + r, row0 = tile * 16 + 4 * g4;
+      if (tile >= tiles || col >= N) continue;
+      const f4 v = acc[t][c];
+      if (EPI == EPI_PART) {
+        *(float4*)(ea.out + ks * ea.part_stride + (size_t)col * ea.ldo + row0) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (row0 + j < ea.rows) ea.out[(size_t)col * ea.ldo + row0 + j] = v[j];
+      }
+    }
+}
+
 // QKV from the multi-group kernel's split partials: per column (blockIdx.y) and
 // 4 rows per thread, the split sum, then RoPE and the KV-cache writes.
 __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ part, uint32_t nparts,
@@ -2421,6 +2550,40 @@ static MgPlan plan16(const QMat& w, bool one_split) {
   return p;
 }
 
+// K-splits of the wide (more than 64 columns) f16 GEMM: 16-tile workgroups, one
+// per CU, at most 8 splits (sh_gemm16_part_floats sizes the partials for
+// them); same cost model as plan16.
+static MgPlan plan16w(const QMat& w, bool one_split) {
+  MgPlan p;
+  p.T = 2;
+  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 15) / 16, slots = 256;
+  const uint32_t cap = one_split ? 1 : 8;
+  uint32_t best_ks = 1;
+  uint64_t best = ~0ull;
+  for (uint32_t ks = 1; ks <= cap && ks <= nsb; ++ks) {
+    const uint32_t S = (nsb + ks - 1) / ks, k2 = (nsb + S - 1) / S, wgs = wgx * k2;
+    const uint64_t cost = (uint64_t)((wgs + slots - 1) / slots) * (S + 2);
+    if (cost < best) { best = cost; best_ks = k2; }
+  }
+  p.S = (nsb + best_ks - 1) / best_ks;
+  p.KS = (nsb + p.S - 1) / p.S;
+  return p;
+}
+
+size_t sh_gemm16_part_floats(const QMat& w) {
+  if (w.type != GGML_Q4_K || w.K % 256) return 0;
+  return std::max((size_t)plan16w(w, false).KS * SH_MAX_COLS16, (size_t)plan16(w, false).KS * SH_MAX_COLS) *
+         w.tiles * 16;
+}
+
+template <int NC, int EPI>
+static void launch16w(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, const EpiArgs& ea,
+                      const MgPlan& p) {
+  const dim3 grid((w.tiles + 15) / 16, p.KS);
+  hipLaunchKernelGGL((k_gemm16w_q4k<NC, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bh,
+                     ldb, N, ea);
+}
+
 template <int NC, int EPI>
 static void launch16(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, const EpiArgs& ea,
                      const MgPlan& p) {
@@ -2435,18 +2598,26 @@ static void dispatch16(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t
     case 1: launch16<1, EPI>(e, w, bh, ldb, N, ea, p); break;
     case 2: launch16<2, EPI>(e, w, bh, ldb, N, ea, p); break;
     case 3: launch16<3, EPI>(e, w, bh, ldb, N, ea, p); break;
-    default: launch16<4, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 4: launch16<4, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 5: launch16w<5, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 6: launch16w<6, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 7: launch16w<7, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 8: launch16w<8, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 9: launch16w<9, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 10: launch16w<10, EPI>(e, w, bh, ldb, N, ea, p); break;
+    case 11: launch16w<11, EPI>(e, w, bh, ldb, N, ea, p); break;
+    default: launch16w<12, EPI>(e, w, bh, ldb, N, ea, p); break;
   }
 }
 
 int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, EpiKind epi,
                      const EpiArgs& ea, const char* tag, uint32_t* nparts) {
-  SH_CHECK(N >= 1 && N <= SH_MAX_COLS, SH_ERR_ARG, "f16 gemm N=%u outside [1, %u]", N, SH_MAX_COLS);
+  SH_CHECK(N >= 1 && N <= SH_MAX_COLS16, SH_ERR_ARG, "f16 gemm N=%u outside [1, %u]", N, SH_MAX_COLS16);
   SH_CHECK(w.type == GGML_Q4_K && w.K % 256 == 0 && ldb >= w.K && ldb % 8 == 0, SH_ERR_UNSUPPORTED,
            "f16 gemm needs Q4_K (type %d) and an operand of at least K = %u halves per column (ldb %u)", w.type, w.K,
            ldb);
   SH_CHECK(epi == EPI_PART || epi == EPI_STORE, SH_ERR_ARG, "f16 gemm epilogue %d", (int)epi);
-  const MgPlan p = plan16(w, epi == EPI_STORE);
+  const MgPlan p = N > SH_MAX_COLS ? plan16w(w, epi == EPI_STORE) : plan16(w, epi == EPI_STORE);
   if (epi == EPI_PART)
     SH_CHECK(ea.part_cap >= p.KS && ea.part_stride >= (size_t)((N + 7) / 8 * 8) * ea.ldo, SH_ERR_CAPACITY,
              "f16 gemm: %u split partials exceed the buffer (%u)", p.KS, ea.part_cap);

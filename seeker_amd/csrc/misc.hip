@@ -208,8 +208,8 @@ __global__ __launch_bounds__(64) void k_prep16_swiglu(PrepArgs a) {
 int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
   SH_CHECK(a.K % 32 == 0, SH_ERR_ARG, "prep K=%u not a multiple of 32", a.K);
   if (a.bh) {
-    SH_CHECK(a.N >= 1 && a.N <= SH_MAX_COLS && a.ldb >= a.K, SH_ERR_ARG, "f16 prep N=%u (at most %u), ldb %u < K %u",
-             a.N, SH_MAX_COLS, a.ldb, a.K);
+    SH_CHECK(a.N >= 1 && a.N <= SH_MAX_COLS16 && a.ldb >= a.K, SH_ERR_ARG,
+             "f16 prep N=%u (at most %u), ldb %u < K %u", a.N, SH_MAX_COLS16, a.ldb, a.K);
     SH_CHECK(a.part_cols >= a.N || a.nparts == 0, SH_ERR_ARG, "prep: partials hold %u columns, N=%u", a.part_cols,
              a.N);
     SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");
@@ -327,10 +327,14 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
 
 int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, unsigned long long* keys,
                      uint32_t* out_ids) {
-  SH_CHECK(N >= 1 && N <= SH_MAX_COLS, SH_ERR_ARG, "argmax N=%u", N);
+  SH_CHECK(N >= 1 && N <= SH_MAX_COLS16, SH_ERR_ARG, "argmax N=%u", N);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  hipLaunchKernelGGL(k_argmax, dim3((V + 2047) / 2048, N), dim3(256), 0, e->stream, logits, V, N, keys, out_ids);
+  for (uint32_t c0 = 0; c0 < N; c0 += SH_MAX_COLS) {  // SH_MAX_COLS keys: launches of at most that many columns
+    const uint32_t n = std::min<uint32_t>(SH_MAX_COLS, N - c0);
+    hipLaunchKernelGGL(k_argmax, dim3((V + 2047) / 2048, n), dim3(256), 0, e->stream, logits + (size_t)c0 * V, V, n,
+                       keys, out_ids + c0);
+  }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "argmax", 4.0 * V * N, ev);
   return SH_OK;

@@ -351,9 +351,10 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
     const char* env16 = getenv("SH_WIDE_F16");
     m->wide16 = w16 && !(env16 && atoi(env16) == 0);
   }
-  // workspace for up to SH_MAX_COLS columns per chunk (operands: 8 groups of 8)
+  // workspace for up to SH_MAX_COLS columns per chunk (operands: 8 groups of 8),
+  // SH_MAX_COLS16 for the wide f16 calls of a model that takes them
   Workspace& w = m->ws;
-  w.max_cols = SH_MAX_COLS;
+  w.max_cols = m->wide16_ok ? SH_MAX_COLS16 : SH_MAX_COLS;
   const uint32_t kmax = std::max({m->d, m->ff, m->q_dim, m->eff}), ngrp = SH_MAX_COLS / 8;
   const uint32_t wide = std::max(m->d, m->q_dim);  // q and attention rows
   const size_t bx_elems = ngrp * sh_grp_bx(kmax);
@@ -365,7 +366,11 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
     gpart_floats = std::max({gpart_floats, sh_gemv_part_floats(L.wo), sh_gemv_part_floats(L.wgu),
                              sh_gemv_part_floats(L.wdown), sh_gemm_part_floats(L.wqkv) + sh_gemm_part_floats(L.wv),
                              sh_gemm_part_floats(L.wo), sh_gemm_part_floats(L.wgu), sh_gemm_part_floats(L.wdown)});
-  const size_t C = SH_MAX_COLS;
+  if (m->wide16_ok)
+    for (const Layer& L : m->layers)
+      gpart_floats = std::max({gpart_floats, sh_gemm16_part_floats(L.wqkv), sh_gemm16_part_floats(L.wo),
+                               sh_gemm16_part_floats(L.wgu), sh_gemm16_part_floats(L.wdown)});
+  const size_t C = w.max_cols;
   if (dalloc(&w.resid, C * m->d) || dalloc(&w.resid2, C * m->d) || dalloc(&w.bx, bx_elems) ||
       dalloc(&w.xs, xs_elems) ||
       dalloc(&w.q, C * wide) || dalloc(&w.attn, C * wide) || dalloc(&w.gpart, gpart_floats) ||
@@ -873,11 +878,28 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
   };
   EpiArgs qkv;
   qkv.out = w.q; qkv.Dq = m->q_dim; qkv.Dkv = m->hd * m->n_kv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.rope = m->rope;
-  QkvCols qc;
-  for (uint32_t j = 0; j < nc; ++j) {
-    qc.pos[j] = cols[j].pos; qc.slot[j] = cols[j].slot; qc.mseq[j] = cols[j].kv->max_seq;
-    qc.kc[j] = cols[j].kv->k; qc.vc[j] = cols[j].kv->v;
-  }
+  // the QKV finish runs over pieces of at most SH_MAX_COLS columns (its column
+  // table is a kernel argument)
+  auto qkv_finish = [&](const float* part, uint32_t np, size_t pstride, uint32_t ldp, const Layer& L,
+                        const float* vpart, uint32_t vnp, uint32_t vldp, size_t vstride) {
+    for (uint32_t c0 = 0; c0 < nc; c0 += SH_MAX_COLS) {
+      const uint32_t n = std::min<uint32_t>(SH_MAX_COLS, nc - c0);
+      QkvCols qc;
+      for (uint32_t j = 0; j < n; ++j) {
+        const ColKv& c = cols[c0 + j];
+        qc.pos[j] = c.pos; qc.slot[j] = c.slot; qc.mseq[j] = c.kv->max_seq; qc.kc[j] = c.kv->k; qc.vc[j] = c.kv->v;
+      }
+      if (vpart) { qc.vpart = vpart + (size_t)c0 * vldp; qc.vnparts = vnp; qc.vldp = vldp; qc.vstride = vstride; }
+      EpiArgs q = qkv;
+      q.out = qkv.out + (size_t)c0 * m->q_dim;
+      const float* p0 = part + (size_t)c0 * ldp;
+      const int rc = m->neox ? sh_qkv_finish_head_launch(e, p0, np, pstride, ldp, n, q, qc, L.q_norm, L.k_norm, m->eps,
+                                                         true)
+                             : sh_qkv_finish_launch(e, p0, np, pstride, ldp, n, q, qc);
+      if (rc) return rc;
+    }
+    return (int)SH_OK;
+  };
   // Wide calls (m->call16) stage f16 rows in w.bh and run every dense matmul
   // through sh_gemm16_launch; else the hi/lo operand groups and sh_gemm_launch.
   const bool f16 = m->call16;
@@ -900,6 +922,8 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
   FabGuard fab{e, FabLaunch{}};
   bool use_fab = fab_enabled();
   for (const FaSeg& sg : segs) use_fab = use_fab && sg.hmasks;
+  SH_CHECK(use_fab || nc <= SH_MAX_COLS, SH_ERR_UNSUPPORTED,
+           "chunks of more than %u columns need the batched attention (device masks)", SH_MAX_COLS);
   if (use_fab && (rc = plan_fab(m, segs, nc, &fab))) return rc;
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
@@ -908,21 +932,19 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     set_norm(pq);
     uint32_t nq = 0;
     if ((rc = gemm(L.wqkv, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
-    qc.vpart = nullptr;
+    const float* vpart = nullptr;
+    uint32_t nv = 0, vldp = 0;
+    size_t vstride = 0;
     if (L.wv.d) {  // v in a weight type of its own: its partials follow q / k's
       EpiArgs pv = part_args(L.wv);
       set_norm(pv);
       pv.out = w.gpart + nq * pq.part_stride;
       pv.part_cap = (uint32_t)((w.gpart_floats - nq * pq.part_stride) / pv.part_stride);
-      uint32_t nv = 0;
       if ((rc = gemm(L.wv, EPI_PART, pv, "gemv_v", &nv))) return rc;
-      qc.vpart = pv.out; qc.vnparts = nv; qc.vldp = pv.ldo; qc.vstride = pv.part_stride;
+      vpart = pv.out; vldp = pv.ldo; vstride = pv.part_stride;
     }
     qkv.layer = l;
-    rc = m->neox ? sh_qkv_finish_head_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc, L.q_norm, L.k_norm,
-                                             m->eps, true)
-                 : sh_qkv_finish_launch(e, w.gpart, nq, pq.part_stride, pq.ldo, nc, qkv, qc);
-    if (rc) return rc;
+    if ((rc = qkv_finish(w.gpart, nq, pq.part_stride, pq.ldo, L, vpart, nv, vldp, vstride))) return rc;
     if (use_fab) {
       if ((rc = sh_fab_launch(e, m, fab.fl, l, w.q, w.attn, w.bx, w.xs, w.cs, f16 ? w.bh : nullptr))) return rc;
     } else {
@@ -978,6 +1000,7 @@ static uint32_t chunk_cols(const sh_model* m, uint32_t n) {
     const char* s = getenv("SH_CHUNK");
     return s && atoi(s) == 8;
   }();
+  if (m->call16 && !forced8) return SH_MAX_COLS16;
   return (m->mg_ok && (n > 8 || !m->fused_ok) && !forced8) ? SH_MAX_COLS : 8;
 }
 
@@ -1312,7 +1335,7 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
   uint32_t* dt = nullptr;
   if ((rc = upload_tokens(m, tokens, N, &dt))) return rc;
   uint32_t* ids = nullptr;
-  if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, SH_MAX_COLS * 4, e->stream));
+  if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, SH_MAX_COLS16 * 4, e->stream));
   const bool want_logits = logits_out || logits_dev || sampled_out;
   m->call16 = m->wide16 && N >= SH_WIDE16_COLS;  // the reference's batch is one matmul of N columns
   const uint32_t CW = chunk_cols(m, N);
@@ -1820,8 +1843,8 @@ extern "C" int sh_gemm_wide16(sh_engine* e, const sh_qtensor* w, const float* x_
   SH_CHECK(N >= 1, SH_ERR_ARG, "N must be >= 1");
   SH_CHECK(w->m.type == GGML_Q4_K && w->m.K % 256 == 0, SH_ERR_UNSUPPORTED,
            "sh_gemm_wide16: Q4_K with K a multiple of 256 (type %d)", w->m.type);
-  const uint32_t K = w->m.K, M = w->m.M, CW = SH_MAX_COLS, ncp_max = CW;
-  const size_t part_floats = sh_gemm_part_floats(w->m);
+  const uint32_t K = w->m.K, M = w->m.M, CW = SH_MAX_COLS16;
+  const size_t part_floats = sh_gemm16_part_floats(w->m);
   uint16_t* bh = nullptr;
   float* part = nullptr;
   SH_HIP(hipMallocAsync((void**)&bh, (size_t)CW * K * 2, e->stream));
@@ -1836,7 +1859,7 @@ extern "C" int sh_gemm_wide16(sh_engine* e, const sh_qtensor* w, const float* x_
     EpiArgs pa;
     pa.out = part; pa.ldo = w->m.tiles * 16;
     pa.part_stride = (size_t)ncp * pa.ldo;
-    pa.part_cap = (uint32_t)(part_floats / ((size_t)ncp_max * pa.ldo));
+    pa.part_cap = (uint32_t)(part_floats / pa.part_stride);
     uint32_t np = 0;
     rc = sh_gemm16_launch(e, w->m, bh, K, nc, EPI_PART, pa, "gemm16", &np);
     if (!rc) rc = sh_part_reduce_launch(e, part, np, pa.ldo, ncp, M, nc, y_dev + (size_t)c0 * M, M, accumulate != 0);

@@ -46,6 +46,7 @@ constexpr uint32_t SH_AMAX_WORDS = SH_MAX_COLS + 8 * SH_MAX_COLS;
 constexpr uint32_t SH_MAX_PREP_COLS = 512;  // operand columns one prep builds (the MoE down operand: pairs)
 constexpr int SH_FA_MIN_SPLIT_KEYS = 64;  // smallest key split of any attention launch (sizes fa_part)
 constexpr uint32_t SH_WIDE16_COLS = 32;  // the reference's wide-GEMM threshold (ops/matmul.rs:433-446)
+constexpr uint32_t SH_MAX_COLS16 = 192;  // columns per forward chunk of a wide f16 call (12 MFMA groups of 16)
 constexpr int SH_FA_MAX_ROWS = 256;       // padded query rows (gqa x columns) per kv head
 // Split partial row: O[hd], m, l, 2 pad (keeps rows 16-byte aligned).
 __host__ __device__ constexpr uint32_t sh_fa_part_stride(uint32_t hd) { return hd + 4; }
@@ -332,6 +333,8 @@ size_t sh_gemm_part_floats(const QMat& w);  // for SH_MAX_COLS columns
 // sh_gemm_launch's; *nparts = splits) or EPI_STORE (out[col][row]).
 int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, EpiKind epi,
                      const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
+// Partial floats sh_gemm16_launch's EPI_PART needs for up to SH_MAX_COLS16 columns.
+size_t sh_gemm16_part_floats(const QMat& w);
 // Fused QKV rows from sh_gemm_launch partials: RoPE, q out, K/V into each
 // column's cache slot.
 struct QkvCols {  // per column: RoPE position, cache slot, capacity, K and V caches

@@ -39,7 +39,7 @@ def _run(engine, M, K, N, seed=0, accumulate=False):
     return got, ref16, exact
 
 
-@pytest.mark.parametrize("N", [1, 13, 32, 47, 64, 70])
+@pytest.mark.parametrize("N", [1, 13, 32, 47, 64, 70, 129, 164, 192, 200])
 def test_wide16_small(engine, N):
     got, ref, exact = _run(engine, 80, 512, N, seed=N)
     scale = np.abs(ref).max()
@@ -55,7 +55,8 @@ def test_wide16_ragged_rows_and_accumulate(engine):
 
 
 @pytest.mark.parametrize("M,K,N", [(6144, 4096, 41), (4096, 4096, 64), (28672, 4096, 48), (4096, 14336, 36),
-                                   (128256, 4096, 33)])
+                                   (128256, 4096, 33), (28672, 4096, 164), (4096, 14336, 164), (6144, 4096, 192),
+                                   (128256, 4096, 100)])
 def test_wide16_8b_shapes(engine, M, K, N):
     got, ref, exact = _run(engine, M, K, N, seed=M + K + N)
     scale = np.abs(ref).max()
