@@ -1662,6 +1662,12 @@ __global__ __launch_bounds__(512) void k_gemm16w_q4k(const uint8_t* __restrict__
     }
 #pragma unroll
     for (int mp = 0; mp < 4; ++mp) {
+      // every B fragment of the sub-block requested before the decode, so the
+      // LDS latency overlaps it and the MFMAs below never wait on a read
+      h8 bb[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) bb[c] = sB[buf][(c * 4 + mp) * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);
       h8 a[T];
 #pragma unroll
       for (int t = 0; t < T; ++t) {
@@ -1676,12 +1682,11 @@ __global__ __launch_bounds__(512) void k_gemm16w_q4k(const uint8_t* __restrict__
         v.w = fma_mix_pair(w8 & 0x00F000F0u, a20, nb);
         a[t] = as_h8(v);
       }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const h8 b = sB[buf][(c * 4 + mp) * 64 + lane];
+      for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int t = 0; t < T; ++t) acc[t][c] = mfma16(a[t], b, acc[t][c]);
-      }
+        for (int t = 0; t < T; ++t) acc[t][c] = mfma16(a[t], bb[c], acc[t][c]);
     }
   };
 
