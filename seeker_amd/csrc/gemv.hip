@@ -2556,19 +2556,22 @@ static MgPlan plan16(const QMat& w, bool one_split) {
 }
 
 // K-splits of the wide (more than 64 columns) f16 GEMM: 16-tile workgroups, one
-// per CU, at most 8 splits (sh_gemm16_part_floats sizes the partials for
-// them); same cost model as plan16.
-static MgPlan plan16w(const QMat& w, bool one_split) {
+// per CU, at most 16 splits. Estimated time (us): rounds x (superblocks per
+// workgroup + 2, the ring's fill) x 0.58 NC (a 16-tile workgroup's superblock
+// at NC groups of 16 columns, measured on the 8B gate/up) plus the split
+// partials' write and read by the finishing kernel at ~4 TB/s.
+static MgPlan plan16w(const QMat& w, bool one_split, uint32_t N) {
   MgPlan p;
   p.T = 2;
-  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 15) / 16, slots = 256;
-  const uint32_t cap = one_split ? 1 : 8;
+  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 15) / 16, slots = 256, NC = (N + 15) / 16;
+  const uint32_t cap = one_split ? 1 : 16;
   uint32_t best_ks = 1;
-  uint64_t best = ~0ull;
+  double best = 1e300;
   for (uint32_t ks = 1; ks <= cap && ks <= nsb; ++ks) {
     const uint32_t S = (nsb + ks - 1) / ks, k2 = (nsb + S - 1) / S, wgs = wgx * k2;
-    const uint64_t cost = (uint64_t)((wgs + slots - 1) / slots) * (S + 2);
-    if (cost < best) { best = cost; best_ks = k2; }
+    const double part_us = k2 > 1 ? (double)k2 * ((N + 7) / 8 * 8) * w.tiles * 16 * 8.0 / 4e6 : 0.0;
+    const double cost = (double)((wgs + slots - 1) / slots) * (S + 2) * 0.58 * NC + part_us;
+    if (cost < best - 1e-9) { best = cost; best_ks = k2; }
   }
   p.S = (nsb + best_ks - 1) / best_ks;
   p.KS = (nsb + p.S - 1) / p.S;
@@ -2577,8 +2580,10 @@ static MgPlan plan16w(const QMat& w, bool one_split) {
 
 size_t sh_gemm16_part_floats(const QMat& w) {
   if (w.type != GGML_Q4_K || w.K % 256) return 0;
-  return std::max((size_t)plan16w(w, false).KS * SH_MAX_COLS16, (size_t)plan16(w, false).KS * SH_MAX_COLS) *
-         w.tiles * 16;
+  size_t cols = (size_t)plan16(w, false).KS * SH_MAX_COLS;  // split-columns of the widest partial set
+  for (uint32_t N = SH_MAX_COLS + 1; N <= SH_MAX_COLS16; ++N)
+    cols = std::max(cols, (size_t)plan16w(w, false, N).KS * ((N + 7) / 8 * 8));
+  return cols * w.tiles * 16;
 }
 
 template <int NC, int EPI>
@@ -2622,7 +2627,7 @@ int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t l
            "f16 gemm needs Q4_K (type %d) and an operand of at least K = %u halves per column (ldb %u)", w.type, w.K,
            ldb);
   SH_CHECK(epi == EPI_PART || epi == EPI_STORE, SH_ERR_ARG, "f16 gemm epilogue %d", (int)epi);
-  const MgPlan p = N > SH_MAX_COLS ? plan16w(w, epi == EPI_STORE) : plan16(w, epi == EPI_STORE);
+  const MgPlan p = N > SH_MAX_COLS ? plan16w(w, epi == EPI_STORE, N) : plan16(w, epi == EPI_STORE);
   if (epi == EPI_PART)
     SH_CHECK(ea.part_cap >= p.KS && ea.part_stride >= (size_t)((N + 7) / 8 * 8) * ea.ldo, SH_ERR_CAPACITY,
              "f16 gemm: %u split partials exceed the buffer (%u)", p.KS, ea.part_cap);
