@@ -396,8 +396,14 @@ int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, ui
     part_floats += (size_t)m->n_kv * d.nsplit * out->kp * d.rows_pad * PS;
     const uint32_t RG = d.rows_pad / 16;
     const uint32_t nch = out->kp == 1 ? (RG + 4 * out->rgw - 1) / (4 * out->rgw) : 1u;
-    for (uint32_t sp = 0; sp < d.nsplit; ++sp)
-      for (uint32_t rc = 0; rc < nch; ++rc) work.push_back((s << 20) | (sp << 4) | rc);
+    // The row chunks of one (segment, split) read the same K/V tiles: groups of
+    // 8 splits go out chunk by chunk, so a split's chunks are 8 workgroups
+    // apart and land on one XCD (workgroups are dealt to the 8 XCDs in turn),
+    // where the later chunks find the tiles in that XCD's L2.
+    for (uint32_t sp0 = 0; sp0 < d.nsplit; sp0 += 8)
+      for (uint32_t rc = 0; rc < nch; ++rc)
+        for (uint32_t sp = sp0; sp < std::min<uint32_t>(sp0 + 8, d.nsplit); ++sp)
+          work.push_back((s << 20) | (sp << 4) | rc);
   }
   // device tables: segments, work items, column -> segment, masks
   const size_t o_work = ((size_t)nseg * sizeof(FabSeg) + 255) / 256 * 256;
