@@ -1726,6 +1726,133 @@ __global__ __launch_bounds__(512) void k_gemm16w_q4k(const uint8_t* __restrict__
     }
 }
 
+// y = W x for 64 < N <= 192 columns in column blocks of 16 NCH columns: a
+// workgroup of 8 waves covers 16 row tiles (wave w: tiles 2 (16 rb + w) + t)
+// and one column block over the superblocks of split blockIdx.y. The ncb
+// column blocks of a row block are 8 workgroups apart, so they run on one XCD
+// and the later ones find the weight tiles in its L2. Every operand goes
+// through a ring of three LDS stages of half a superblock (B fragments and the
+// waves' weight words with their row headers) filled by direct loads two
+// stages ahead; all of a wave's loads are its own asm loads, so the wait for
+// a stage is an exact count. Each decoded fragment feeds NCH MFMAs, each B
+// fragment 2.
+template <int NCH, int EPI>
+__global__ __launch_bounds__(512) void k_gemm16h_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                     uint32_t S, const uint16_t* __restrict__ Bh, uint32_t ldb,
+                                                     uint32_t N, uint32_t ncb, EpiArgs ea) {
+  constexpr int T = 2, WV = 8, STG = 3;
+  constexpr uint32_t kB = NCH * 4 * 64;                  // h8 of one stage's B fragments
+  constexpr uint32_t kTW = 1280;                         // one tile's stage: 1 KB of words + the 256 B row header
+  constexpr int kLoadsMin = (NCH * 4) / WV + 2 * T;      // fewest direct loads of one wave per stage
+  __shared__ h8 sB[STG][kB];
+  __shared__ __attribute__((aligned(16))) uint8_t sW[STG][WV * T * kTW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4, r = lane & 15;
+  const uint32_t grp = blockIdx.x / (8 * ncb), within = blockIdx.x % (8 * ncb);
+  const uint32_t cb = within / 8, rb = grp * 8 + within % 8;
+  if (rb * WV * T >= tiles) return;  // whole workgroup: the last group of 8 row blocks may be short
+  const uint32_t tile0 = (rb * WV + wave) * T, col0 = cb * NCH * 16;
+  const uint32_t ks = blockIdx.y, sb0 = ks * S, sb1 = min(sb0 + S, nsb), nst = 2 * (sb1 - sb0);
+
+  auto issue = [&](uint32_t s, int buf) __attribute__((always_inline)) {
+    const uint32_t sb = sb0 + (s >> 1), h = s & 1;
+    for (uint32_t fi = wave; fi < (uint32_t)(NCH * 4); fi += WV) {
+      const uint32_t c = fi >> 2, mp = fi & 3;
+      const uint32_t col = min(col0 + 16 * c + (uint32_t)r, N - 1);
+      sh_dma16(Bh + (size_t)col * ldb + 256 * sb + 32 * (4 * h + mp) + 8 * g4, &sB[buf][fi * 64]);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
+      const uint8_t* src = Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
+      uint8_t* dst = &sW[buf][(wave * T + t) * kTW];
+      sh_dma16(src + 1024 * h + 16 * lane, dst);
+      sh_dma4(src + 2048 + 4 * lane, dst + 1024);
+    }
+  };
+
+  f4 acc[T][NCH];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf, uint32_t h) __attribute__((always_inline)) {
+    u32x4 q[T];
+    uint32_t scw[T], mw[T];
+    float d24[T], ndmin[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint8_t* wt = &sW[buf][(wave * T + t) * kTW];
+      q[t] = *(const u32x4*)(wt + 16 * lane);
+      const uint32_t dd = *(const uint32_t*)(wt + 1024 + 4 * r);
+      const uint32_t* sp = (const uint32_t*)(wt + 1024 + 64 + 12 * r);
+      const uint32_t s0 = sp[0], s1 = sp[1], s2 = sp[2];
+      // the Q4_K 6-bit unpack of sub-blocks 4h .. 4h + 3 (q4_decode_setup)
+      scw[t] = h == 0 ? (s0 & 0x3F3F3F3Fu) : ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u));
+      mw[t] = h == 0 ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+      d24[t] = (float)as_h2(dd).x * 16777216.0f;
+      ndmin[t] = -(float)as_h2(dd).y;
+    }
+#pragma unroll
+    for (int mp = 0; mp < 4; ++mp) {
+      h8 bb[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) bb[c] = sB[buf][(c * 4 + mp) * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);
+      h8 a[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float a24 = d24[t] * (float)((scw[t] >> (8 * mp)) & 0xFFu), a20 = a24 * 0.0625f;
+        const float nb = ndmin[t] * (float)((mw[t] >> (8 * mp)) & 0xFFu);
+        const uint32_t word = mp == 0 ? q[t].x : mp == 1 ? q[t].y : mp == 2 ? q[t].z : q[t].w;
+        const uint32_t w8 = word >> 8;
+        u32x4 v;
+        v.x = fma_mix_pair(word & 0x000F000Fu, a24, nb);
+        v.y = fma_mix_pair(word & 0x00F000F0u, a20, nb);
+        v.z = fma_mix_pair(w8 & 0x000F000Fu, a24, nb);
+        v.w = fma_mix_pair(w8 & 0x00F000F0u, a20, nb);
+        a[t] = as_h8(v);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t][c] = mfma16(a[t], bb[c], acc[t][c]);
+    }
+  };
+
+#pragma unroll
+  for (int j = 0; j < STG - 1; ++j)
+    if ((uint32_t)j < nst) issue(j, j);
+  for (uint32_t s = 0; s < nst; ++s) {
+    // stage s landed (stage s + 1 may still be in flight), and every wave is
+    // done with stage s - 1, whose buffer stage s + 2 now refills
+    if (s + 1 < nst) sh_wait_vm<kLoadsMin>();
+    else sh_wait_vm<0>();
+    __syncthreads();
+    if (s + STG - 1 < nst) issue(s + STG - 1, (s + STG - 1) % STG);
+    compute(s % STG, s & 1);
+  }
+
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const uint32_t tile = tile0 + t, col = col0 + 16 * c + r, row0 = tile * 16 + 4 * g4;
+      if (tile >= tiles || col >= N) continue;
+      const f4 v = acc[t][c];
+      if (EPI == EPI_PART) {
+        *(float4*)(ea.out + ks * ea.part_stride + (size_t)col * ea.ldo + row0) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (row0 + j < ea.rows) ea.out[(size_t)col * ea.ldo + row0 + j] = v[j];
+      }
+    }
+}
+
 // QKV from the multi-group kernel's split partials: per column (blockIdx.y) and
 // 4 rows per thread, the split sum, then RoPE and the KV-cache writes.
 __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ part, uint32_t nparts,
@@ -2578,12 +2705,80 @@ static MgPlan plan16w(const QMat& w, bool one_split, uint32_t N) {
   return p;
 }
 
+// Column blocks of the column-block kernel (k_gemm16h_q4k) for N columns: at
+// most 6 groups of 16 per block, the blocks as even as the groups allow.
+struct G16hShape {
+  uint32_t ncb = 1, nch = 1;
+};
+static G16hShape shape16h(uint32_t N) {
+  G16hShape g;
+  const uint32_t NC = (N + 15) / 16;
+  g.ncb = (NC + 5) / 6;
+  g.nch = (NC + g.ncb - 1) / g.ncb;
+  return g;
+}
+// K-splits of the column-block kernel: 16-tile workgroups, one per CU (the
+// 132 KB LDS ring), cost as plan16w with the block's groups.
+static MgPlan plan16h(const QMat& w, bool one_split, uint32_t N) {
+  MgPlan p;
+  p.T = 2;
+  const G16hShape g = shape16h(N);
+  const uint32_t nsb = w.K / 256, wgx = (w.tiles + 15) / 16 * g.ncb, slots = 256;
+  const uint32_t cap = one_split ? 1 : 16;
+  uint32_t best_ks = 1;
+  double best = 1e300;
+  for (uint32_t ks = 1; ks <= cap && ks <= nsb; ++ks) {
+    const uint32_t S = (nsb + ks - 1) / ks, k2 = (nsb + S - 1) / S, wgs = wgx * k2;
+    const double part_us = k2 > 1 ? (double)k2 * ((N + 7) / 8 * 8) * w.tiles * 16 * 8.0 / 4e6 : 0.0;
+    const double cost = (double)((wgs + slots - 1) / slots) * (S + 1) * 0.58 * g.nch + part_us;
+    if (cost < best - 1e-9) { best = cost; best_ks = k2; }
+  }
+  p.S = (nsb + best_ks - 1) / best_ks;
+  p.KS = (nsb + p.S - 1) / p.S;
+  return p;
+}
+// Which kernel takes a call of more than 64 columns: k_gemm16w_q4k (one pass
+// over the weights) unless its split plan leaves more than 40 % of the CUs
+// idle (the 8B Wo at 164 columns: 128 workgroups), where the column blocks
+// give the 16-tile workgroups twice the parallelism (measured 0.58 vs 0.72 ms
+// per tree step; the gate/up, down and QKV shapes are faster one pass).
+// SH_G16H=0 / 1 forces either kernel.
+static bool use16h(const QMat& w, bool one_split, uint32_t N) {
+  static const int forced = [] {
+    const char* e = getenv("SH_G16H");
+    return e && *e ? atoi(e) : -1;
+  }();
+  if (forced >= 0) return forced != 0;
+  const MgPlan p = plan16w(w, one_split, N);
+  return (uint64_t)(w.tiles + 15) / 16 * p.KS * 10 < 256 * 6;
+}
+
 size_t sh_gemm16_part_floats(const QMat& w) {
   if (w.type != GGML_Q4_K || w.K % 256) return 0;
   size_t cols = (size_t)plan16(w, false).KS * SH_MAX_COLS;  // split-columns of the widest partial set
   for (uint32_t N = SH_MAX_COLS + 1; N <= SH_MAX_COLS16; ++N)
-    cols = std::max(cols, (size_t)plan16w(w, false, N).KS * ((N + 7) / 8 * 8));
+    cols = std::max({cols, (size_t)plan16w(w, false, N).KS * ((N + 7) / 8 * 8),
+                     (size_t)plan16h(w, false, N).KS * ((N + 7) / 8 * 8)});
   return cols * w.tiles * 16;
+}
+
+template <int NCH, int EPI>
+static void launch16h(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, uint32_t ncb,
+                      const EpiArgs& ea, const MgPlan& p) {
+  const uint32_t nrb = (w.tiles + 15) / 16;
+  const dim3 grid((nrb + 7) / 8 * 8 * ncb, p.KS);
+  hipLaunchKernelGGL((k_gemm16h_q4k<NCH, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bh,
+                     ldb, N, ncb, ea);
+}
+template <int EPI>
+static void dispatch16h(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N,
+                        const EpiArgs& ea, const MgPlan& p) {
+  const G16hShape g = shape16h(N);
+  switch (g.nch) {
+    case 4: launch16h<4, EPI>(e, w, bh, ldb, N, g.ncb, ea, p); break;
+    case 5: launch16h<5, EPI>(e, w, bh, ldb, N, g.ncb, ea, p); break;
+    default: launch16h<6, EPI>(e, w, bh, ldb, N, g.ncb, ea, p); break;
+  }
 }
 
 template <int NC, int EPI>
@@ -2627,14 +2822,22 @@ int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t l
            "f16 gemm needs Q4_K (type %d) and an operand of at least K = %u halves per column (ldb %u)", w.type, w.K,
            ldb);
   SH_CHECK(epi == EPI_PART || epi == EPI_STORE, SH_ERR_ARG, "f16 gemm epilogue %d", (int)epi);
-  const MgPlan p = N > SH_MAX_COLS ? plan16w(w, epi == EPI_STORE, N) : plan16(w, epi == EPI_STORE);
+  const bool h = N > SH_MAX_COLS && use16h(w, epi == EPI_STORE, N);
+  const MgPlan p = h ? plan16h(w, epi == EPI_STORE, N)
+                     : N > SH_MAX_COLS ? plan16w(w, epi == EPI_STORE, N) : plan16(w, epi == EPI_STORE);
   if (epi == EPI_PART)
     SH_CHECK(ea.part_cap >= p.KS && ea.part_stride >= (size_t)((N + 7) / 8 * 8) * ea.ldo, SH_ERR_CAPACITY,
              "f16 gemm: %u split partials exceed the buffer (%u)", p.KS, ea.part_cap);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
-  if (epi == EPI_PART) dispatch16<EPI_PART>(e, w, bh, ldb, N, ea, p);
-  else dispatch16<EPI_STORE>(e, w, bh, ldb, N, ea, p);
+  if (h) {
+    if (epi == EPI_PART) dispatch16h<EPI_PART>(e, w, bh, ldb, N, ea, p);
+    else dispatch16h<EPI_STORE>(e, w, bh, ldb, N, ea, p);
+  } else if (epi == EPI_PART) {
+    dispatch16<EPI_PART>(e, w, bh, ldb, N, ea, p);
+  } else {
+    dispatch16<EPI_STORE>(e, w, bh, ldb, N, ea, p);
+  }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, tag, w.alg_bytes, ev);
   if (nparts) *nparts = p.KS;
