@@ -10,9 +10,10 @@
 //
 // Design (gfx950). A segment has R = gqa x ncol query rows per kv head (up to
 // 256). A workgroup of 4 waves owns (segment, key split, kv head) and streams
-// the split's keys in tiles of 64: K (64 rows of hd f16) and V (two 32-key
-// blocks, [hd][32] each) go global -> LDS by direct 16-byte loads, double
-// buffered, so tile t + 1 is in flight while tile t is used. The LDS images
+// the split's keys in tiles (32 keys in a ring of 3 buffers, or 64 keys
+// double buffered with KP = 2 below): K (rows of hd f16) and V (32-key blocks,
+// [hd][32] each) go global -> LDS by direct 16-byte loads, so the next tiles
+// are in flight while tile t is used. The LDS images
 // are XOR-swizzled (K: 16-byte chunk c of key row j at c ^ (j % chunks per
 // row); V: chunk c of d row at c ^ (d / 2 % 4)), so the 8 lanes of an MFMA
 // operand read that share a 128-byte bank window hit 8 different 16-byte slots. Each wave owns RGW groups of 16 query
@@ -68,21 +69,32 @@ __device__ __forceinline__ void lds_barrier() {
 constexpr int kTK = 64;     // keys per tile
 constexpr int kWaves = 4;   // waves per workgroup
 
-template <int HD, int RGW, int KP>
-__global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict__ segs, const uint32_t* __restrict__ work,
+// TK keys per tile, NS tiles in the LDS ring (NS - 1 in flight while one is
+// used). KP = 2 takes 64-key tiles (its two 32-key blocks go to two waves),
+// double buffered. KP = 1 takes 32-key tiles in a ring of 3: 48 KB of LDS at
+// hd 128 instead of 64 KB, so three workgroups share a CU (three waves per
+// SIMD instead of two; the tree verify's attention 2.56 -> 2.12 ms per step,
+// where a ring of 4 at two workgroups per CU measured no gain: the waves wait
+// on their own MFMA / exp / LDS chains, not on the loads).
+template <int HD, int RGW, int KP, int NS = (KP == 2 ? 2 : 3)>
+__global__ __launch_bounds__(64 * kWaves, (KP == 1 && RGW == 1) ? 3 : 2) void k_fab(const FabSeg* __restrict__ segs, const uint32_t* __restrict__ work,
                                                      const float* __restrict__ q, uint32_t n_head, uint32_t gqa,
                                                      uint32_t n_kv, uint32_t layer, uint32_t tps, float scale_log2,
                                                      float* __restrict__ part) {
+  constexpr int TK = KP == 2 ? kTK : 32;  // keys per tile
+  constexpr int NB = TK / 32;             // 32-key blocks per tile
   constexpr int NC = HD / 32, DT = HD / 16, CPR = HD / 8;
-  constexpr int KI = kTK * CPR / 64;   // wave instructions of one K tile (1 KB each)
-  constexpr int VI = 2 * HD * 4 / 64;  // ... of one V tile
+  constexpr int KI = TK * CPR / 64;    // wave instructions of one K tile (1 KB each)
+  constexpr int VI = NB * HD * 4 / 64;  // ... of one V tile
   constexpr int NLD = (KI + VI) / kWaves;  // per wave per tile
   constexpr int WG = kWaves / KP;      // waves per key phase
   constexpr uint32_t PS = sh_fa_part_stride(HD);
   static_assert((KI + VI) % kWaves == 0, "tile loads must spread evenly over the waves");
-  // two buffers, selected at compile time (tiles go in pairs)
-  __shared__ __align__(16) uint16_t sK0[kTK * HD], sK1[kTK * HD];
-  __shared__ __align__(16) uint16_t sV0[2 * HD * 32], sV1[2 * HD * 32];
+  static_assert(KP == 1 || NB == 2, "KP = 2 splits a tile's two key blocks over two waves");
+  static_assert(NS >= 2 && NS <= 4 && (NS - 1) * NLD < 64, "ring depth");
+  // NS buffers, selected at compile time (tiles go in groups of NS)
+  __shared__ __align__(16) uint16_t sKr[NS][TK * HD];
+  __shared__ __align__(16) uint16_t sVr[NS][NB * HD * 32];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -98,16 +110,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
   const uint32_t kvlen = sg.kvlen, mbase = sg.mask_base, max_seq = sg.max_seq;
   const uint32_t key_begin = split * tps * kTK;
   const uint32_t key_end = min(key_begin + tps * kTK, kvlen);
-  const uint32_t ntiles = (key_end - key_begin + kTK - 1) / kTK;
+  const uint32_t ntiles = (key_end - key_begin + TK - 1) / TK;
   const size_t lstride = (size_t)n_kv * max_seq * HD;
   const uint16_t* kb = sg.k + layer * lstride + (size_t)kh * max_seq * HD;
   const uint16_t* vb = sg.v + layer * lstride + (size_t)kh * max_seq * HD;
 
   auto issue = [&](uint32_t t, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    uint16_t* sK = buf ? sK1 : sK0;
-    uint16_t* sV = buf ? sV1 : sV0;
-    const uint32_t key0 = key_begin + t * kTK;
+    uint16_t* sK = sKr[buf];
+    uint16_t* sV = sVr[buf];
+    const uint32_t key0 = key_begin + t * TK;
 #pragma unroll
     for (int i = wave; i < KI; i += kWaves) {
       const int qc = 64 * i + lane, row = qc / CPR, c = qc % CPR;
@@ -123,7 +135,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
       sh_dma16(src, &sV[512 * i]);
     }
   };
+  // the first NS - 1 tiles (past the split's end: tile 0 again, into an idle
+  // buffer, so every path keeps the same count of loads in flight)
   issue(0u, std::integral_constant<int, 0>{});
+  if constexpr (NS > 2) issue(1u < ntiles ? 1u : 0u, std::integral_constant<int, 1>{});
+  if constexpr (NS > 3) issue(2u < ntiles ? 2u : 0u, std::integral_constant<int, 2>{});
 
   // The wave's row groups: rgi = rc RGc + wg + WG i. Lane (g, r) holds row
   // 16 rgi + r, d = 32 c + 8 g .. + 7 of the Q^T operand.
@@ -180,19 +196,20 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
 
   auto step = [&](uint32_t t, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    const uint16_t* sK = buf ? sK1 : sK0;
-    const uint16_t* sV = buf ? sV1 : sV0;
-    // The next tile's loads go out unconditionally (the last tile re-reads
-    // itself, from L2, into the idle buffer): with the same count of loads in
-    // flight on every path, the compiler's own waits before the LDS reads stay
-    // at NLD instead of draining the prefetch.
-    issue(t + 1 < ntiles ? t + 1 : t, std::integral_constant<int, 1 - buf>{});
-    sh_wait_vm<NLD>();
+    const uint16_t* sK = sKr[buf];
+    const uint16_t* sV = sVr[buf];
+    // Tile t + NS - 1's loads go out unconditionally (past the last tile, tile
+    // t again, from L2, into the idle buffer the previous step released): with
+    // the same count of loads in flight on every path, the compiler's own
+    // waits before the LDS reads stay at (NS - 1) NLD instead of draining the
+    // prefetch.
+    issue(t + NS - 1 < ntiles ? t + NS - 1 : t, std::integral_constant<int, (buf + NS - 1) % NS>{});
+    sh_wait_vm<(NS - 1) * NLD>();
     lds_barrier();
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
+    for (int bb = 0; bb < NB; ++bb) {
       if (KP == 2 && bb != kp) continue;
-      const uint32_t key0 = key_begin + t * kTK + 32 * bb;
+      const uint32_t key0 = key_begin + t * TK + 32 * bb;
       // scores of every row group from the K fragments first, then the V
       // fragments: K and V operands are never live together
       f4 sacc[RGW][2];
@@ -273,9 +290,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_fab(const FabSeg* __restrict
     }
     lds_barrier();  // every wave is done with this buffer before it is refilled
   };
-  for (uint32_t t = 0; t < ntiles; t += 2) {
+  for (uint32_t t = 0; t < ntiles; t += NS) {
     step(t, std::integral_constant<int, 0>{});
     if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+    if constexpr (NS > 2) if (t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2 % NS>{});
+    if constexpr (NS > 3) if (t + 3 < ntiles) step(t + 3, std::integral_constant<int, 3 % NS>{});
   }
   sh_wait_vm<0>();  // no LDS write may land after the workgroup ends
 
@@ -362,8 +381,8 @@ int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, ui
   // Geometry of the launch: rows split over the 4 waves (RGW groups of 16 per
   // wave, segments above 4 RGW groups in row chunks), or the two key blocks of
   // a tile over pairs of waves (KP = 2) when no segment has more than 2 row
-  // groups; tiles per split chosen for about 512 workgroups (two per CU) and
-  // at least 4 keys per split for every row.
+  // groups; tiles per split chosen for about 512 workgroups and at least 4
+  // keys per split for every row.
   static const int forced_rgw = [] {  // SH_FAB_RGW=1|2: row groups per wave (measurement switch)
     const char* v = getenv("SH_FAB_RGW");
     return v ? atoi(v) : 0;
