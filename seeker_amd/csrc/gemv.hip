@@ -1875,8 +1875,13 @@ __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ par
       if (k0 + j < nparts) { s.x += t[j].x; s.y += t[j].y; s.z += t[j].z; s.w += t[j].w; }
   }
   const float v[4] = {s.x, s.y, s.z, s.w};
-  qkv_store4(ea, r0, v, qc.pos[col], qc.slot[col], qc.mseq[col], qc.kc[col], qc.vc[col],
-             ea.out + (size_t)col * ea.Dq);
+  if (qc.tab) {
+    const QkvColDev t = qc.tab[col];
+    qkv_store4(ea, r0, v, t.pos, t.slot, t.mseq, t.kc, t.vc, ea.out + (size_t)col * ea.Dq);
+  } else {
+    qkv_store4(ea, r0, v, qc.pos[col], qc.slot[col], qc.mseq[col], qc.kc[col], qc.vc[col],
+               ea.out + (size_t)col * ea.Dq);
+  }
 }
 
 // QKV of a qwen3 layer from split partials (models/qwen3.rs:330-362): one
@@ -2846,7 +2851,8 @@ int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t l
 
 int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
                          uint32_t N, const EpiArgs& ea, const QkvCols& qc) {
-  SH_CHECK(N >= 1 && N <= SH_MAX_COLS && ea.hd % 4 == 0, SH_ERR_ARG, "qkv finish shape");
+  SH_CHECK(N >= 1 && N <= (qc.tab ? (uint32_t)SH_MAX_COLS16 : (uint32_t)SH_MAX_COLS) && ea.hd % 4 == 0, SH_ERR_ARG,
+           "qkv finish shape");
   const uint32_t rows = ea.Dq + 2 * ea.Dkv;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
@@ -2860,7 +2866,7 @@ int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_
 int sh_qkv_finish_head_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
                               uint32_t N, const EpiArgs& ea, const QkvCols& qc, const float* q_norm,
                               const float* k_norm, float eps, bool neox) {
-  SH_CHECK(N >= 1 && N <= SH_MAX_COLS && (ea.hd == 64 || ea.hd == 128) && ea.Dq % ea.hd == 0, SH_ERR_ARG,
+  SH_CHECK(!qc.tab && N >= 1 && N <= SH_MAX_COLS && (ea.hd == 64 || ea.hd == 128) && ea.Dq % ea.hd == 0, SH_ERR_ARG,
            "qkv head finish shape");
   const uint32_t heads = ea.Dq / ea.hd + 2 * ea.n_kv;
   hipEvent_t ev = nullptr;

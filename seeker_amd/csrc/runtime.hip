@@ -218,7 +218,7 @@ static void free_model(sh_model* m) {
   Workspace& w = m->ws;
   (void)hipFree(w.resid); (void)hipFree(w.resid2); (void)hipFree(w.bx); (void)hipFree(w.xs); (void)hipFree(w.q);
   (void)hipFree(w.attn); (void)hipFree(w.gpart); (void)hipFree(w.h); (void)hipFree(w.logits); (void)hipFree(w.fa_part); (void)hipFree(w.fab_part);
-  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq); (void)hipFree(w.bh);
+  (void)hipFree(w.tokens); (void)hipFree(w.amax); (void)hipFree(w.cs); (void)hipFree(w.ssq); (void)hipFree(w.bh); (void)hipFree(w.qtab);
   (void)hipFree(w.bx2); (void)hipFree(w.xs2); (void)hipFree(w.cs2); (void)hipFree(w.ssq2); (void)hipFree(w.sb_cnt);
   (void)hipFree(w.moe_logits); (void)hipFree(w.moe_ids); (void)hipFree(w.moe_wts); (void)hipFree(w.moe_info); (void)hipFree(w.moe_col);
   (void)hipFree(w.moe_slot); (void)hipFree(w.moe_hgu); (void)hipFree(w.moe_bx); (void)hipFree(w.moe_xs);
@@ -376,7 +376,7 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       dalloc(&w.q, C * wide) || dalloc(&w.attn, C * wide) || dalloc(&w.gpart, gpart_floats) ||
       dalloc(&w.h, C * std::max(m->ff, 1u)) || dalloc(&w.logits, C * m->V) || dalloc(&w.fa_part, part_floats) ||
       dalloc(&w.tokens, C + 64) || dalloc(&w.amax, SH_AMAX_WORDS) || dalloc(&w.cs, ngrp * sh_grp_cs(kmax)) ||
-      dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bh, C * kmax) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
+      dalloc(&w.ssq, ngrp * sh_grp_cs(kmax)) || dalloc(&w.bh, C * kmax) || dalloc(&w.qtab, C) || dalloc(&w.bx2, sh_grp_bx(m->d)) || dalloc(&w.xs2, sh_grp_xs(m->d)) ||
       dalloc(&w.cs2, sh_grp_cs(m->d)) || dalloc(&w.ssq2, sh_grp_cs(m->d)) || dalloc(&w.sb_cnt, SH_SB_CNT * SH_SB_CNT_STRIDE))
     FAIL(SH_ERR_HIP, "workspace allocation: %s", sh_last_error());
   w.fa_part_floats = part_floats;
@@ -878,10 +878,26 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
   };
   EpiArgs qkv;
   qkv.out = w.q; qkv.Dq = m->q_dim; qkv.Dkv = m->hd * m->n_kv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.rope = m->rope;
-  // the QKV finish runs over pieces of at most SH_MAX_COLS columns (its column
-  // table is a kernel argument)
+  // The QKV finish takes its column table as a kernel argument, in pieces of at
+  // most SH_MAX_COLS columns; a wider chunk of a non-NEOX model uploads the
+  // table once (w.qtab, read by every layer) and finishes in one launch.
+  const bool qtab = nc > SH_MAX_COLS && !m->neox;
+  if (qtab) {
+    std::vector<QkvColDev> t(nc);
+    for (uint32_t j = 0; j < nc; ++j) {
+      const ColKv& c = cols[j];
+      t[j].pos = c.pos; t[j].slot = c.slot; t[j].mseq = c.kv->max_seq; t[j].pad = 0; t[j].kc = c.kv->k; t[j].vc = c.kv->v;
+    }
+    SH_HIP(hipMemcpyAsync(w.qtab, t.data(), (size_t)nc * sizeof(QkvColDev), hipMemcpyHostToDevice, e->stream));
+  }
   auto qkv_finish = [&](const float* part, uint32_t np, size_t pstride, uint32_t ldp, const Layer& L,
                         const float* vpart, uint32_t vnp, uint32_t vldp, size_t vstride) {
+    if (qtab) {
+      QkvCols qc;
+      qc.tab = w.qtab;
+      if (vpart) { qc.vpart = vpart; qc.vnparts = vnp; qc.vldp = vldp; qc.vstride = vstride; }
+      return sh_qkv_finish_launch(e, part, np, pstride, ldp, nc, qkv, qc);
+    }
     for (uint32_t c0 = 0; c0 < nc; c0 += SH_MAX_COLS) {
       const uint32_t n = std::min<uint32_t>(SH_MAX_COLS, nc - c0);
       QkvCols qc;

@@ -130,6 +130,7 @@ struct Layer {
   QMat wdown_exps;
 };
 
+struct QkvColDev;
 struct Workspace {
   uint32_t max_cols = 0;
   float* resid = nullptr;     // [cols][d]
@@ -147,6 +148,7 @@ struct Workspace {
   float* cs = nullptr;        // [max(K)/256][8] inverse activation scales of the current B operand
   float* ssq = nullptr;       // [max(K)/256][8] per-superblock sums of squares of the normalized input
   uint16_t* bh = nullptr;     // [cols][max(K)] f16 operand rows of the wide f16 GEMM
+  QkvColDev* qtab = nullptr;  // [cols] the chunk's QKV finish column table
   size_t fa_part_floats = 0;
   float* fab_part = nullptr;  // batched attention partials of every segment of a chunk (grown on demand)
   size_t fab_part_floats = 0;
@@ -337,7 +339,16 @@ int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t l
 size_t sh_gemm16_part_floats(const QMat& w);
 // Fused QKV rows from sh_gemm_launch partials: RoPE, q out, K/V into each
 // column's cache slot.
+struct QkvColDev {  // one column of a device-resident column table
+  int32_t pos;
+  uint32_t slot, mseq, pad;
+  uint16_t* kc;
+  uint16_t* vc;
+};
 struct QkvCols {  // per column: RoPE position, cache slot, capacity, K and V caches
+  // With tab set, the columns come from that device table (up to
+  // SH_MAX_COLS16 of them) and the arrays below are unused.
+  const QkvColDev* tab = nullptr;
   int32_t pos[SH_MAX_COLS];
   uint32_t slot[SH_MAX_COLS];
   uint32_t mseq[SH_MAX_COLS];
