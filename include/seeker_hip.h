@@ -247,7 +247,11 @@ int sh_gemm_wide16(sh_engine* e, const sh_qtensor* w, const float* x_dev, uint32
  * (sample.rs:347-361, batched accept server/inference.rs:2859-2883);
  * REJECTION is new. Uniforms: Philox4x64-10 key (seed, 0x5EC), word
  * counter + 2*(b*(k+1)+i) (accept) and +1 (residual), or explicit host uniforms
- * [B][k+1][2]. Outputs acc_len_dev [B], next_tok_dev [B] (u32). */
+ * [B][k+1][2]. Outputs acc_len_dev [B], next_tok_dev [B] (u32), enqueued on
+ * the engine stream: ready after sh_engine_sync or any later synchronizing
+ * call (with explicit uniforms the call itself waits, since the caller may
+ * reuse that host array). The scratch (row partials, draw state) is the
+ * engine's own, grown on the first call of a size and reused by later calls. */
 int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
                      const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s,
                      uint32_t* acc_len_dev, uint32_t* next_tok_dev);
@@ -262,8 +266,12 @@ int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const float* q_log
  * scratch exceeds it are refused with SH_ERR_CAPACITY (configs[1], B = 32,
  * k = 8, V = 128256, needs 170 KiB; up to B = 64, k = 16, V = 262144 fits).
  * Uniforms must come from Philox (s->uniforms NULL). The array is shared by
- * every call on that GPU and keeps the last call's contents: calls that
- * overlap on one GPU (other streams or engines) race. */
+ * every call on that GPU and keeps the last call's contents; calls from other
+ * streams or engines on that GPU are ordered through one per-device event
+ * (each call's stream waits for the previous call's kernels), so they take the
+ * array in turn. A caller capturing the call into a HIP graph must not replay
+ * that graph concurrently with other no-alloc calls on the same GPU: replays
+ * do not pass through that event. */
 int sh_accept_sample_noalloc(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
                              const uint32_t* drafts_dev, uint32_t B, uint32_t k, uint32_t V, const sh_sampling* s,
                              uint32_t* acc_len_dev, uint32_t* next_tok_dev);

@@ -116,6 +116,7 @@ extern "C" void sh_engine_destroy(sh_engine* e) {
   for (auto& g : e->graphs) (void)hipGraphExecDestroy(g.exec);
   e->graphs.clear();
   free_spec_bufs(e->spec);
+  for (void* p : e->scr) (void)hipFree(p);
   (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -158,6 +159,21 @@ extern "C" int sh_engine_profile_reset(sh_engine* e) {
   int rc = sh_prof_flush(e);
   e->stats.clear();
   return rc;
+}
+
+int sh_engine_scratch(sh_engine* e, int slot, size_t bytes, void** out) {
+  SH_CHECK(slot >= 0 && slot < 4, SH_ERR_ARG, "scratch slot %d", slot);
+  if (bytes > e->scr_bytes[slot]) {
+    SH_HIP(hipStreamSynchronize(e->stream));
+    if (e->scr[slot]) SH_HIP(hipFree(e->scr[slot]));
+    e->scr[slot] = nullptr;
+    e->scr_bytes[slot] = 0;
+    const size_t cap = (bytes + 4095) / 4096 * 4096;
+    SH_HIP(hipMalloc(&e->scr[slot], cap));
+    e->scr_bytes[slot] = cap;
+  }
+  *out = e->scr[slot];
+  return SH_OK;
 }
 
 extern "C" int sh_dev_alloc(sh_engine* e, uint64_t bytes, void** out) {

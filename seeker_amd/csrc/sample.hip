@@ -1124,7 +1124,9 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   const size_t part_b = (size_t)nunits * sizeof(double2);
   const size_t chunk_b = (size_t)B * kDrawChunks * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
   char* sbuf = static_cast<char*>(scratch_in);
-  if (!scratch_in) SH_HIP(hipMallocAsync((void**)&sbuf, sh_accept_scratch_bytes(B, k, V, mode), e->stream));
+  if (!sbuf) {
+    if (int rc = sh_engine_scratch(e, SCR_ACCEPT, sh_accept_scratch_bytes(B, k, V, mode), (void**)&sbuf)) return rc;
+  }
   double2* part = reinterpret_cast<double2*>(sbuf);
   double2* chunk = reinterpret_cast<double2*>(sbuf + part_b);
   double2* rstat = reinterpret_cast<double2*>(sbuf + part_b + chunk_b);
@@ -1163,7 +1165,6 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_decide", 0.0, ev);
-  if (!scratch_in) SH_HIP(hipFreeAsync(sbuf, e->stream));
   return SH_OK;
 }
 
@@ -1237,19 +1238,24 @@ extern "C" int sh_accept_sample(sh_engine* e, const float* p_logits_dev, const f
                                 uint32_t* acc_len_dev, uint32_t* next_tok_dev) {
   SH_CHECK(e && p_logits_dev && drafts_dev && s && acc_len_dev && next_tok_dev, SH_ERR_ARG,
            "sh_accept_sample: NULL argument");
+  SH_CHECK(s->mode == SH_SAMPLE_COMPARE || s->mode == SH_SAMPLE_REJECTION, SH_ERR_ARG, "accept: mode %u", s->mode);
+  SH_CHECK(B >= 1 && k >= 1 && k <= 64 && V >= 1, SH_ERR_ARG, "accept: B=%u k=%u V=%u", B, k, V);
+  // engine scratch, reused call after call: no allocation once it has grown
+  void* sbuf = nullptr;
+  int rc = sh_engine_scratch(e, SCR_ACCEPT, sh_accept_scratch_bytes(B, k, V, s->mode), &sbuf);
+  if (rc) return rc;
   float* udev = nullptr;
   if (s->uniforms) {
     const size_t n = (size_t)B * (k + 1) * 2;
-    SH_HIP(hipMallocAsync((void**)&udev, n * 4, e->stream));
+    if ((rc = sh_engine_scratch(e, SCR_UNIFORMS, n * 4, (void**)&udev))) return rc;
     SH_HIP(hipMemcpyAsync(udev, s->uniforms, n * 4, hipMemcpyHostToDevice, e->stream));
   }
   // explicit uniforms are indexed from 0; Philox words from s->counter
-  int rc = sh_accept_launch(e, p_logits_dev, q_logits_dev, drafts_dev, B, k, V, s, udev ? 0 : s->counter, udev,
-                            acc_len_dev, next_tok_dev);
-  if (udev) (void)hipFreeAsync(udev, e->stream);
+  rc = sh_accept_launch(e, p_logits_dev, q_logits_dev, drafts_dev, B, k, V, s, udev ? 0 : s->counter, udev,
+                        acc_len_dev, next_tok_dev, sbuf);
   if (rc) return rc;
-  SH_HIP(hipStreamSynchronize(e->stream));
-  return sh_prof_flush(e);
+  if (udev) SH_HIP(hipStreamSynchronize(e->stream));  // the caller may reuse its uniform array on return
+  return sh_prof_flush(e);  // waits for the stream only when profiling
 }
 
 extern "C" int sh_accept_probs(sh_engine* e, const float* p_logits_dev, const float* q_logits_dev,
@@ -1380,6 +1386,10 @@ static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 namespace {
 constexpr int kMaxDevices = 64;
 void* g_scratch_dev[kMaxDevices] = {};
+// Per device: an event recorded after the last no-alloc call's kernels, which
+// the next call's stream waits on, so calls from different streams or
+// engines take the array in turn instead of racing on it.
+hipEvent_t g_scratch_ev[kMaxDevices] = {};
 std::mutex g_scratch_mu;
 }  // namespace
 
@@ -1391,6 +1401,10 @@ int sh_static_scratch_init(int dev) {
   const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
   SH_CHECK(err == hipSuccess && ptr, SH_ERR_HIP, "static scratch of device %d: hipGetSymbolAddress: %s", dev,
            hipGetErrorString(err));
+  hipEvent_t ev = nullptr;
+  const hipError_t eerr = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  SH_CHECK(eerr == hipSuccess, SH_ERR_HIP, "static scratch of device %d: event: %s", dev, hipGetErrorString(eerr));
+  g_scratch_ev[dev] = ev;
   g_scratch_dev[dev] = ptr;
   return SH_OK;
 }
@@ -1407,9 +1421,16 @@ extern "C" int sh_accept_sample_noalloc(sh_engine* e, const float* p_logits_dev,
   SH_CHECK(need <= kStaticScratchBytes, SH_ERR_CAPACITY,
            "sh_accept_sample_noalloc: B=%u k=%u V=%u needs %zu scratch bytes, above the static %zu", B, k, V, need,
            kStaticScratchBytes);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
   void* ptr = (e->device >= 0 && e->device < kMaxDevices) ? g_scratch_dev[e->device] : nullptr;
   SH_CHECK(ptr, SH_ERR_STATE, "static scratch of device %d is not set up", e->device);
+  hipEvent_t ev = g_scratch_ev[e->device];
+  // after the previous call's kernels, whichever stream they ran on
+  SH_HIP(hipStreamWaitEvent(e->stream, ev, 0));
   // nothing in the scratch needs to start at zero: every kernel writes what it reads
-  return sh_accept_launch(e, p_logits_dev, q_logits_dev, drafts_dev, B, k, V, s, s->counter, nullptr, acc_len_dev,
-                          next_tok_dev, ptr);
+  const int rc = sh_accept_launch(e, p_logits_dev, q_logits_dev, drafts_dev, B, k, V, s, s->counter, nullptr,
+                                  acc_len_dev, next_tok_dev, ptr);
+  if (rc) return rc;
+  SH_HIP(hipEventRecord(ev, e->stream));
+  return SH_OK;
 }

@@ -95,7 +95,16 @@ struct sh_engine {
   std::vector<hipEvent_t> event_pool;
   SpecBufs spec;
   std::vector<GraphEntry> graphs;
+  // Device scratch kept by the engine and reused by later calls (the engine
+  // stream orders them): grown on demand by sh_engine_scratch.
+  void* scr[4] = {nullptr, nullptr, nullptr, nullptr};
+  size_t scr_bytes[4] = {0, 0, 0, 0};
 };
+// Scratch slots of sh_engine_scratch.
+enum ScratchSlot { SCR_ACCEPT = 0, SCR_UNIFORMS = 1, SCR_TREE = 2, SCR_SMALL = 3 };
+// *out = the engine's scratch of slot, at least `bytes` long. Growing it
+// waits for the stream (earlier launches may still read the old block).
+int sh_engine_scratch(sh_engine* e, int slot, size_t bytes, void** out);
 
 // A weight matrix on the device, repacked into MFMA tiles.
 struct QMat {
