@@ -276,6 +276,71 @@ def measure_moe(eng, P=16384, B=8, L=7, reps=5):
             "kernel_ms": kern}
 
 
+def measure_moe_spec(eng, P=16384, B=8, k=6, steps=6, warmup=1):
+    """configs[4] as a batch-8 spec decode (sh_spec_step_batch, the server's step,
+    server/inference.rs:2777-2924): the Qwen3-30B-A3B-shape Q4_K MoE target (48
+    layers) and the Qwen3-0.6B-shape Q4_K draft (28 layers), 8 sequences at
+    context 16384 (both caches' positions set without a prefill: the same bytes
+    read and work done), k = 6 greedy drafts per sequence, one batched verify
+    of 8 x 7 columns, per-sequence acceptance and rollback. Accepted tok/s =
+    emitted tokens / wall time over the timed steps (run.rs:702-710's count);
+    draft ms per position = (step - verify) / k, verify ms from the batched
+    verify of the same columns timed alone."""
+    import numpy as np
+    from seeker_amd import synth as S
+    t0 = time.time()
+    timg = S.GgufImage(S.Q30B_A3B_TARGET, seed=2)
+    dimg = S.GgufImage(S.Q06B_DRAFT, seed=3)
+    tm, dm = eng.upload_weights(timg), eng.upload_weights(dimg)
+    timg.close()
+    dimg.close()
+    log(f"moe spec: target + draft synthesized and uploaded in {time.time() - t0:.1f}s")
+    V = tm.dims.n_vocab
+    tk = [eng.allocate_kv_cache(tm, P + 64) for _ in range(B)]
+    dk = [eng.allocate_kv_cache(dm, P + 64) for _ in range(B)]
+    for c in tk + dk:
+        c.set_position(P)
+    last = [int(t) for t in S.tokens(710, B, V)]
+    emitted = accepted = 0
+    for _ in range(warmup):
+        em, _ = eng.spec_step_batch(tm, dm, tk, dk, last, k)
+        last = [e[-1] for e in em]
+    eng.sync()
+    t = time.perf_counter()
+    for _ in range(steps):
+        em, _ = eng.spec_step_batch(tm, dm, tk, dk, last, k)
+        emitted += sum(len(e) for e in em)
+        accepted += sum(len(e) - 1 for e in em)
+        last = [e[-1] for e in em]
+    eng.sync()
+    dt = time.perf_counter() - t
+    # the verify of the same shape alone (the step's verify share)
+    toks = np.concatenate([S.tokens(720 + b, k + 1, V) for b in range(B)])
+    vt = []
+    for i in range(4):
+        for c in tk:
+            c.set_position(P)
+        eng.sync()
+        t1 = time.perf_counter()
+        eng.verify_unified(tm, tk, toks, [k + 1] * B)
+        if i >= 1:
+            vt.append((time.perf_counter() - t1) * 1e3)
+    v_ms = statistics.median(vt)
+    step_ms = dt * 1e3 / steps
+    for c in tk + dk:
+        c.close()
+    tm.close()
+    dm.close()
+    out = {"config": f"configs[4]: Qwen3-30B-A3B-shape Q4_K MoE target + Qwen3-0.6B-shape Q4_K draft, B={B}, k={k}, "
+                     f"ctx {P}, greedy, batched spec step (sh_spec_step_batch)",
+           "tok_s": round(emitted / dt, 2), "ms_per_step": round(step_ms, 3),
+           "acceptance_rate": round(accepted / (steps * B * k), 4), "verify_ms": round(v_ms, 3),
+           "verify_share": round(v_ms / step_ms, 4), "draft_ms_per_position": round((step_ms - v_ms) / k, 3),
+           "steps": steps}
+    log(f"moe spec decode B={B} k={k} ctx {P}: {step_ms:.2f} ms/step, {emitted / dt:.1f} tok/s, verify {v_ms:.2f} ms")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -287,6 +352,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel, tree and MoE lines")
     ap.add_argument("--moe-only", action="store_true", help="only the configs[4] MoE verify measurement")
+    ap.add_argument("--moe-spec-only", action="store_true", help="only the configs[4] batched spec-decode measurement")
     ap.add_argument("--tree-only", action="store_true", help="only the configs[3] tree verify measurement")
     ap.add_argument("--acceptance-only", action="store_true", help="only the configs[1] acceptance measurement")
     ap.add_argument("--draft-only", action="store_true", help="only the draft forward (eager, per-kernel events)")
@@ -305,6 +371,10 @@ def main():
     if args.moe_only:
         with Engine(0) as eng:
             print(json.dumps({"metric": "moe verify step", "moe_verify": measure_moe(eng)}), flush=True)
+        return
+    if args.moe_spec_only:
+        with Engine(0) as eng:
+            print(json.dumps({"metric": "moe spec decode", "moe_spec": measure_moe_spec(eng)}), flush=True)
         return
     if args.draft_only:
         with Engine(0) as eng:
@@ -409,6 +479,8 @@ def main():
         ot, od = O.Model(timg), O.Model(dimg)
         ot.set_mm16(2 if tm.wide_f16 else 0)  # wide calls as the GPU computes them
         od.set_mm16(2 if dm.wide_f16 else 0)
+        ot.set_attn_cm1(tm.cm1_attention)  # the verify's cm1 attention as the GPU computes it
+        od.set_attn_cm1(dm.cm1_attention)
         okt, okd = O.KvCache(ot, max_seq), O.KvCache(od, max_seq)
         for (gkv, okv, m) in ((tkv, okt, tm), (dkv, okd, dm)):
             n = gkv.position
@@ -510,6 +582,7 @@ def main():
         "acceptance_kernel": extra_acc,
         "tree_verify": extra_tree,
         "moe_verify": None,
+        "moe_spec": None,
     }
     for x in (tkv, dkv, tm, dm):
         x.close()
@@ -517,6 +590,7 @@ def main():
     dimg.close()
     if not args.no_extra:  # the 8B models are freed first: the MoE target is 17 GB
         out["moe_verify"] = measure_moe(eng)
+        out["moe_spec"] = measure_moe_spec(eng)
     print(json.dumps(out), flush=True)
     eng.close()
 

@@ -128,6 +128,19 @@ int sh_model_info(const sh_model* m, sh_model_dims* out);
  * that does not allow it. */
 int sh_model_wide_f16(const sh_model* m, int* on);
 int sh_model_set_wide_f16(sh_model* m, int on);
+/* Masked attention (ops/flash_attn.rs:442-471): the reference computes the
+ * attention of every forward of more than one token (the causal mask of
+ * models/llama.rs:216-222) with flash_attn_cm1.slang: q * scale * log2(e)
+ * staged as f16, keys in 64-key blocks, P rounded to f16, P V accumulated per
+ * 16-key chunk in f16, the output held in f16 and rescaled in f16 per block,
+ * 1/L in f32. Here sh_forward_full / sh_verify_greedy / the verify and
+ * draft catch-up forwards of sh_spec_step do the same for calls of more than
+ * one column without tree parents, when the switch is on (default on;
+ * SH_FA_CM=0 in the environment at upload turns it off). Single-column calls,
+ * trees and batched verifies keep the f32-level attention (the reference's
+ * scalar flash_attn.slang, ops/flash_attn.rs:488-632, 819-1016). */
+int sh_model_cm1_attention(const sh_model* m, int* on);
+int sh_model_set_cm1_attention(sh_model* m, int on);
 /* The validation half of models::open (models/mod.rs:537; parse_params +
  * collect_weights, models/llama.rs:1038-1090) without a device: parses a GGUF
  * image in caller memory, checks every tensor the model reads (shape, type,
@@ -217,6 +230,29 @@ int sh_verify_unified_sampled(sh_engine* e, sh_model* m, sh_kv* const* caches, u
 int sh_spec_step(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh_kv* dkv,
                  uint32_t last_token, uint32_t n_max, sh_sampling* s, uint32_t* emitted_out,
                  uint32_t* n_emitted, uint32_t* drafts_out);
+/* Engine::draft_tokens (inference/mod.rs:2062-2092) with a separate draft
+ * model: n = clamp(n_max, 1, 8) greedy drafts after last_token, fed through
+ * the draft cache dkv (its pending tokens first, as sh_spec_step leaves them),
+ * each argmax feeding the next position on the device; drafts_out [n]. The
+ * cache advances by its pending count + n (d_n is not fed) and its pending
+ * tokens are cleared: truncate it to the accepted length afterwards. */
+int sh_draft_tokens(sh_engine* e, sh_model* draft, sh_kv* dkv, uint32_t last_token, uint32_t n_max,
+                    uint32_t* drafts_out);
+/* The reference server's batched speculative step (server/inference.rs:
+ * 2777-2924) for B sequences with their own target caches tkv[s], draft caches
+ * dkv[s] and last tokens: n = clamp(n_max, 1, 8) greedy drafts per sequence,
+ * the drafts of all sequences at one position drafted in one batched forward
+ * of the draft model (the reference drafts each sequence with draft_tokens,
+ * :2806-2812); one sh_verify_unified of every sequence's [last, d_1..d_n] with
+ * its sampler (samplers NULL: greedy; else GREEDY or COMPARE per sequence, as
+ * sh_verify_unified_sampled); per sequence the longest prefix whose sampled
+ * token equals the draft is accepted (:2859-2883) and both caches are truncated
+ * to pos + acc + 1. emitted_out [B][n + 1] (row s holds n_emitted[s] tokens),
+ * drafts_out [B][n] (may be NULL). Draft caches carry d_n as pending after a
+ * fully accepted step, as in sh_spec_step. */
+int sh_spec_step_batch(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* const* tkv, sh_kv* const* dkv,
+                       uint32_t B, const uint32_t* last_tokens, uint32_t n_max, sh_sampling* samplers,
+                       uint32_t* emitted_out, uint32_t* n_emitted, uint32_t* drafts_out);
 /* Readback of the last stochastic sh_spec_step of this engine, the analog of
  * the reference's tensor taps (inference/context.rs:136-160, 283): target
  * logits p_out [(n+1)][V] and draft logits q_out [n][V] (either may be NULL),

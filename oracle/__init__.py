@@ -38,6 +38,10 @@ _SIGS = {
     "or_gemv": (C.c_int, [C.c_int, U8P, C.c_uint64, C.c_uint64, F32P, C.c_uint32, F32P]),
     "or_gemv16": (C.c_int, [C.c_int, U8P, C.c_uint64, C.c_uint64, F32P, C.c_uint32, F32P]),
     "or_model_set_mm16": (None, [P, C.c_int]),
+    "or_model_set_attn_cm1": (None, [P, C.c_int]),
+    "or_f64_to_f16": (C.c_uint16, [C.c_double]),
+    "or_attn_cm1": (None, [F32P, U16P, U16P, C.c_size_t, C.c_uint32, C.c_uint32, U8P, F32P]),
+    "or_attn_cm1_core": (None, [U16P, U16P, U16P, C.c_size_t, C.c_uint32, C.c_uint32, U8P, F32P]),
     "or_model_open": (C.c_int, [P, C.c_uint64, C.POINTER(P)]),
     "or_model_free": (None, [P]),
     "or_model_dims": (None, [P, U32P]),
@@ -169,6 +173,7 @@ class Model:
         e = (C.c_uint32 * 4)()
         lib().or_model_moe_dims(h, e)
         self.arch, self.n_expert, self.n_used, self.expert_ff = list(e)
+        self.attn_cm1 = False
 
     def set_mm16(self, mode):
         """Dense matmuls of later forwards with the wide GEMM's f16 operands:
@@ -176,10 +181,38 @@ class Model:
         (the reference's dispatch, ops/matmul.rs:433-446)."""
         lib().or_model_set_mm16(self.h, int(mode))
 
+    def set_attn_cm1(self, on):
+        """Causal forward calls of more than one column compute attention with
+        the reference's cooperative-matrix flash attention arithmetic
+        (or_attn_cm1: flash_attn_cm1.slang, ops/flash_attn.rs:442-471)."""
+        self.attn_cm1 = bool(on)
+        lib().or_model_set_attn_cm1(self.h, int(bool(on)))
+
     def close(self):
         if self.h:
             lib().or_model_free(self.h)
             self.h = None
+
+
+def attn_cm1(q, k16, v16, visible=None, staged=False) -> np.ndarray:
+    """or_attn_cm1 over keys k16 / v16 [n_keys][hd] (uint16 f16 bits) for one
+    query row q [hd]: f32 values staged to f16 by the shader's scale, or (staged)
+    the staged f16 bits themselves (or_attn_cm1_core)."""
+    k16 = np.ascontiguousarray(k16, dtype=np.uint16)
+    v16 = np.ascontiguousarray(v16, dtype=np.uint16)
+    n, hd = k16.shape
+    out = np.empty(hd, np.float32)
+    vis = np.ascontiguousarray(visible, dtype=np.uint8) if visible is not None else None
+    vp = vis.ctypes.data_as(U8P) if vis is not None else None
+    if staged:
+        q16 = np.ascontiguousarray(q, dtype=np.uint16)
+        lib().or_attn_cm1_core(q16.ctypes.data_as(U16P), k16.ctypes.data_as(U16P), v16.ctypes.data_as(U16P), hd, hd,
+                               n, vp, out.ctypes.data_as(F32P))
+    else:
+        qq = _f32(q)
+        lib().or_attn_cm1(qq.ctypes.data_as(F32P), k16.ctypes.data_as(U16P), v16.ctypes.data_as(U16P), hd, hd, n, vp,
+                          out.ctypes.data_as(F32P))
+    return out
 
 
 class KvCache:
@@ -217,7 +250,16 @@ class KvCache:
             self.h = None
 
 
-def forward(model: Model, kv: KvCache, tokens, pos: int, parents=None, logits_mode: int = 2):
+def forward(model: Model, kv: KvCache, tokens, pos: int, parents=None, logits_mode: int = 2, batched=False):
+    """or_forward. batched: the call stands for one sequence of a batched
+    verify, whose attention is the reference's scalar kernel
+    (ops/flash_attn.rs:819-1016) whatever set_attn_cm1 says."""
+    if batched:
+        lib().or_model_set_attn_cm1(model.h, 0)
+        try:
+            return forward(model, kv, tokens, pos, parents, logits_mode)
+        finally:
+            lib().or_model_set_attn_cm1(model.h, int(bool(model.attn_cm1)))
     t = np.ascontiguousarray(tokens, dtype=np.uint32)
     L = t.size
     cols = L if logits_mode == 2 else (1 if logits_mode == 1 else 0)

@@ -43,11 +43,15 @@ float or_f16_to_f32(uint16_t h) {
 }
 
 /* f32 -> f16, IEEE round-to-nearest-even, computed through double arithmetic
- * (independent of the bit-twiddling conversion used by the product). */
-uint16_t or_f32_to_f16(float f) {
+ * (independent of the bit-twiddling conversion used by the product). A float
+ * widens to double exactly, so this is or_f64_to_f16 of the same value. */
+uint16_t or_f32_to_f16(float f) { return or_f64_to_f16((double)f); }
+
+/* double -> f16 with one IEEE round-to-nearest-even rounding of the double value. */
+uint16_t or_f64_to_f16(double f) {
   if (isnan(f)) return 0x7E00;
   uint16_t sign = signbit(f) ? 0x8000 : 0;
-  double a = fabs((double)f);
+  double a = fabs(f);
   if (a == 0.0) return sign;
   if (a >= 65520.0) return sign | 0x7C00;
   int e;
@@ -294,6 +298,8 @@ struct or_model {
   int mm16; /* dense matmuls with the wide GEMM's f16 operands (or_gemv16): 0 never,
              * 1 always, 2 in forward calls of >= 32 columns (ops/matmul.rs:433-446) */
   uint32_t call_cols; /* columns of the forward call in progress */
+  int attn_cm1; /* causal forward calls of > 1 column: attention with flash_attn_cm1's
+                 * f16 arithmetic (or_attn_cm1) instead of the exact softmax */
 };
 
 struct or_kv {
@@ -665,6 +671,87 @@ static void f16_lut_init(void) {
   f16_lut_ready = 1;
 }
 
+void or_model_set_attn_cm1(or_model* m, int on) { m->attn_cm1 = on != 0; }
+
+/* The reference's masked attention, shaders/compute/flash_attn_cm1.slang (taken
+ * by every forward of L > 1 tokens on an f16 cache, ops/flash_attn.rs:442-471;
+ * single pass up to 16384 keys, :1393-1410), for one query row: keys in
+ * 64-key blocks from key 0 (Bc, :39); per block the row maximum over its
+ * visible keys (:300-312, the running maximum starting at -1e30, :173), the
+ * f16 output rescaled by the f16 factor (:314-320), P = exp2(S - M) rounded to
+ * f16 (:322-334), P V summed per 16-key chunk into an f16 accumulator (the
+ * f16-accumulating coopmat MMA, :349-358) and added to the f16 output
+ * (:363-374); O = f32(O16) / L at the end (:398-411). S is the f32 dot product
+ * of the staged f16 q (see or_attn_cm1) with the f16 keys, computed here
+ * exactly and rounded to f32 once; the order of the reference's sums inside one
+ * MMA, of its exp2 and of its L sum are not pinned. L is kept in double. */
+#define H2F(h) f16_lut[(uint16_t)(h)]
+void or_attn_cm1_core(const uint16_t* q16, const uint16_t* k, const uint16_t* v, size_t kv_stride, uint32_t hd,
+                      uint32_t n_keys, const uint8_t* visible, float* out) {
+  enum { BC = 64, CH = 16 };
+  f16_lut_init();
+  uint16_t o16[512];
+  float qf[512];
+  for (uint32_t e = 0; e < hd; ++e) { o16[e] = 0; qf[e] = H2F(q16[e]); }
+  float M = -1.0e30f;
+  double L = 0.0;
+  for (uint32_t k0 = 0; k0 < n_keys; k0 += BC) {
+    float S[BC], P[BC];
+    uint16_t p16[BC];
+    int vis[BC];
+    float rowmax = -1.0e30f;
+    for (uint32_t c = 0; c < BC; ++c) {
+      const uint32_t t = k0 + c;
+      vis[c] = t < n_keys && (!visible || visible[t]);
+      S[c] = -INFINITY;
+      if (!vis[c]) continue;
+      const uint16_t* kr = k + (size_t)t * kv_stride;
+      double acc = 0.0;
+      for (uint32_t e = 0; e < hd; ++e) acc += (double)qf[e] * (double)H2F(kr[e]);
+      S[c] = (float)acc;
+      if (S[c] > rowmax) rowmax = S[c];
+    }
+    const float Mn = rowmax > M ? rowmax : M;
+    const float ef = exp2f(M - Mn);
+    L = (double)ef * L;
+    const double e16 = H2F(or_f32_to_f16(ef));
+    for (uint32_t d = 0; d < hd; ++d) o16[d] = or_f64_to_f16(e16 * (double)H2F(o16[d]));
+    for (uint32_t c = 0; c < BC; ++c) {
+      P[c] = vis[c] ? exp2f(S[c] - Mn) : 0.0f;
+      L += P[c];
+      p16[c] = or_f32_to_f16(P[c]);
+    }
+    for (uint32_t d = 0; d < hd; ++d) {
+      uint16_t acc16 = 0;
+      for (uint32_t c0 = 0; c0 < BC; c0 += CH) {
+        double sacc = H2F(acc16);
+        for (uint32_t c = c0; c < c0 + CH; ++c)
+          if (vis[c]) sacc += (double)H2F(p16[c]) * (double)H2F(v[(size_t)(k0 + c) * kv_stride + d]);
+        acc16 = or_f64_to_f16(sacc);
+      }
+      o16[d] = or_f64_to_f16((double)H2F(o16[d]) + (double)H2F(acc16));
+    }
+    M = Mn;
+  }
+  const float Lf = (float)L;
+  const float inv = Lf == 0.0f ? 0.0f : 1.0f / Lf;
+  for (uint32_t d = 0; d < hd; ++d) out[d] = H2F(o16[d]) * inv;
+}
+
+/* Q staging of flash_attn_cm1.slang:155-171: f16(q * (scale * log2 e)) with the
+ * f32 product scale * LOG2E (scale = 1 / sqrt(head_dim) in f32,
+ * models/llama.rs:237), then the row as or_attn_cm1_core. */
+#undef H2F
+
+void or_attn_cm1(const float* q, const uint16_t* k, const uint16_t* v, size_t kv_stride, uint32_t hd, uint32_t n_keys,
+                 const uint8_t* visible, float* out) {
+  const float scale = 1.0f / sqrtf((float)hd);
+  const float qs = scale * 1.44269504088896340736f;
+  uint16_t q16[512];
+  for (uint32_t e = 0; e < hd; ++e) q16[e] = or_f32_to_f16(q[e] * qs);
+  or_attn_cm1_core(q16, k, v, kv_stride, hd, n_keys, visible, out);
+}
+
 int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint32_t pos,
                const int32_t* parents, int logits_mode, float* logits, float* residual_out) {
   f16_lut_init();
@@ -732,11 +819,18 @@ int or_forward(or_model* m, or_kv* kv, const uint32_t* tokens, uint32_t L, uint3
       }
     /* attention: prefix [0,pos) always visible; within-chunk slot pos+a visible to
      * row j iff a <= j (causal, llama.rs:904-955) or a is an ancestor-or-self of j (tree). */
+    const int cm1 = m->attn_cm1 && L > 1 && !parents;
 #pragma omp parallel for collapse(2) schedule(static)
     for (int64_t j = 0; j < (int64_t)L; ++j)
       for (int64_t h = 0; h < (int64_t)nh; ++h) {
         const uint32_t kh = (uint32_t)h / gqa;
         const float* qv = q + (size_t)j * qd + (size_t)h * hd;
+        if (cm1) {
+          /* row j of the causal chunk sees keys [0, pos + j] */
+          or_attn_cm1(qv, Kc + (size_t)kh * hd, Vc + (size_t)kh * hd, dkv, hd, pos + (uint32_t)j + 1, NULL,
+                      att + (size_t)j * qd + (size_t)h * hd);
+          continue;
+        }
         double* s = (double*)malloc(kvlen * sizeof(double));
         double mx = -INFINITY;
         for (uint32_t t = 0; t < kvlen; ++t) {

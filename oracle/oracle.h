@@ -13,6 +13,7 @@
  */
 #ifndef SEEKER_ORACLE_H
 #define SEEKER_ORACLE_H
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -23,6 +24,7 @@ enum { OR_F32 = 0, OR_F16 = 1, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K 
 
 float or_f16_to_f32(uint16_t h);
 uint16_t or_f32_to_f16(float f);
+uint16_t or_f64_to_f16(double f);
 
 /* Philox4x64-10 block (numpy.random.Philox raw block for the given counter). */
 void or_philox4x64_10(const uint64_t ctr[4], const uint64_t key[2], uint64_t out[4]);
@@ -51,6 +53,19 @@ void or_model_free(or_model* m);
 /* 0: exact dense matmuls; 1: all as or_gemv16; 2: as or_gemv16 in forward
  * calls of >= 32 columns (the reference's wide-GEMM dispatch). */
 void or_model_set_mm16(or_model* m, int mode);
+/* on != 0: causal forward calls of more than one column compute attention with
+ * the reference's cooperative-matrix flash attention arithmetic (or_attn_cm1,
+ * flash_attn_cm1.slang via ops/flash_attn.rs:442-471); single-column calls and
+ * trees keep the exact softmax. Default off. */
+void or_model_set_attn_cm1(or_model* m, int on);
+/* flash_attn_cm1.slang for one query row q [hd] (f32, staged to f16 as the
+ * shader does) over keys [0, n_keys) of an f16 cache whose key t row starts at
+ * k + t * kv_stride (v likewise); visible[t] != 0 marks visible keys (NULL: all).
+ * out [hd] f32. or_attn_cm1_core takes the staged f16 q16 directly. */
+void or_attn_cm1(const float* q, const uint16_t* k, const uint16_t* v, size_t kv_stride, uint32_t hd,
+                 uint32_t n_keys, const uint8_t* visible, float* out);
+void or_attn_cm1_core(const uint16_t* q16, const uint16_t* k, const uint16_t* v, size_t kv_stride, uint32_t hd,
+                      uint32_t n_keys, const uint8_t* visible, float* out);
 /* n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab */
 void or_model_dims(const or_model* m, uint32_t dims[7]);
 /* architecture (0 llama, 1 qwen3, 2 qwen3moe), n_expert, n_expert_used, expert_ff */

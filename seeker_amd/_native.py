@@ -111,6 +111,8 @@ SIGNATURES = {
     "sh_model_info": (C.c_int, [P, C.POINTER(sh_model_dims)]),
     "sh_model_wide_f16": (C.c_int, [P, C.POINTER(C.c_int)]),
     "sh_model_set_wide_f16": (C.c_int, [P, C.c_int]),
+    "sh_model_cm1_attention": (C.c_int, [P, C.POINTER(C.c_int)]),
+    "sh_model_set_cm1_attention": (C.c_int, [P, C.c_int]),
     "sh_gguf_inspect": (C.c_int, [P, C.c_uint64, C.POINTER(sh_model_dims)]),
     "sh_kv_create": (C.c_int, [P, P, C.c_uint32, C.POINTER(P)]),
     "sh_kv_destroy": (None, [P]),
@@ -125,6 +127,9 @@ SIGNATURES = {
     "sh_verify_unified": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, U32P, U32P, U32P, I32P, F32P, U32P, F32P]),
     "sh_verify_unified_sampled": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, U32P, U32P, U32P, I32P,
                                             P, F32P, U32P, F32P]),
+    "sh_draft_tokens": (C.c_int, [P, P, P, C.c_uint32, C.c_uint32, U32P]),
+    "sh_spec_step_batch": (C.c_int, [P, P, P, C.POINTER(P), C.POINTER(P), C.c_uint32, U32P, C.c_uint32, P, U32P, U32P,
+                                     U32P]),
     "sh_spec_step": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), U32P, U32P, U32P]),
     "sh_spec_step_logits": (C.c_int, [P, F32P, F32P, U32P, U32P]),
     "sh_accept_sample_noalloc": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling),

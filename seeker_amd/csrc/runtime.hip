@@ -239,6 +239,7 @@ static void free_model(sh_model* m) {
   (void)hipFree(w.moe_logits); (void)hipFree(w.moe_ids); (void)hipFree(w.moe_wts); (void)hipFree(w.moe_info); (void)hipFree(w.moe_col);
   (void)hipFree(w.moe_slot); (void)hipFree(w.moe_hgu); (void)hipFree(w.moe_bx); (void)hipFree(w.moe_xs);
   (void)hipFree(w.moe_cs); (void)hipFree(w.moe_y);
+  (void)hipFree(w.fa16_pv); (void)hipFree(w.fa16_ml); (void)hipFree(w.fa16_smax); (void)hipFree(w.fa16_flag);
   delete m;
 }
 
@@ -255,6 +256,7 @@ static int ensure_rope(sh_model* m, uint32_t npos) {
       double th = (double)p * std::pow((double)m->theta, -2.0 * i / (double)m->hd);
       tab[(size_t)p * half + i] = make_float2((float)std::cos(th), (float)std::sin(th));
     }
+  g_graph_gen.fetch_add(1);  // captured graphs may read the old table
   SH_HIP(hipStreamSynchronize(m->e->stream));
   if (m->rope) SH_HIP(hipFree(m->rope));
   m->rope = nullptr;
@@ -366,6 +368,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
     m->wide16_ok = w16;
     const char* env16 = getenv("SH_WIDE_F16");
     m->wide16 = w16 && !(env16 && atoi(env16) == 0);
+    const char* envcm = getenv("SH_FA_CM");
+    m->fa16 = !(envcm && atoi(envcm) == 0);
   }
   // workspace for up to SH_MAX_COLS columns per chunk (operands: 8 groups of 8),
   // SH_MAX_COLS16 for the wide f16 calls of a model that takes them
@@ -467,6 +471,18 @@ extern "C" int sh_model_set_wide_f16(sh_model* m, int on) {
   SH_CHECK(!on || m->wide16_ok, SH_ERR_UNSUPPORTED,
            "wide f16 GEMMs need a model without routed experts whose matrices are all Q4_K");
   m->wide16 = on != 0;
+  return SH_OK;
+}
+
+extern "C" int sh_model_cm1_attention(const sh_model* m, int* on) {
+  SH_CHECK(m && on, SH_ERR_ARG, "sh_model_cm1_attention: NULL argument");
+  *on = m->fa16 ? 1 : 0;
+  return SH_OK;
+}
+
+extern "C" int sh_model_set_cm1_attention(sh_model* m, int on) {
+  SH_CHECK(m, SH_ERR_ARG, "sh_model_set_cm1_attention: NULL model");
+  m->fa16 = on != 0;
   return SH_OK;
 }
 
@@ -742,7 +758,9 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     }
     prepped = false;
     // one segment covering the chunk: Wo combines the attention splits itself
-    const bool fuse_o = fuse && !fuse_pp && segs.size() == 1 && segs[0].col0 == 0 && segs[0].ncol == nc && fuse_wo;
+    // (cm1 attention builds the Wo operand in its own chain kernel)
+    const bool fuse_o = !m->call_cm1 && fuse && !fuse_pp && segs.size() == 1 && segs[0].col0 == 0 &&
+                        segs[0].ncol == nc && fuse_wo;
     OpndSrc osrc;
     for (const FaSeg& sg : segs) {
       FaArgs fa;
@@ -751,8 +769,10 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       fa.masks = sg.masks;
       fa.dbase = sg.kv->graph_base;
       fa.kv_cap = sg.kv->max_seq;
-      if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs, fuse_o ? &osrc : nullptr)))
-        return rc;
+      rc = m->call_cm1 ? sh_fa16_launch(e, m, sg.kv, fa, w.q, w.attn, w.bx, w.xs, w.cs)
+                       : sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs,
+                                      fuse_o ? &osrc : nullptr);
+      if (rc) return rc;
     }
     EpiArgs po = part_args(L.wo);
     if (fuse_pp) {
@@ -951,10 +971,15 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
                : sh_gemm_launch(e, q, w.bx, w.xs, w.cs, nc, epi, ea, tag, np);
   };
   // batched attention: one plan for the chunk's segments, one launch per layer
+  // a causal single-sequence call (m->call_cm1): the chunk's columns as one
+  // cm1 attention launch
+  const bool cm1 = m->call_cm1;
+  SH_CHECK(!cm1 || (segs.front().col0 == 0 && segs.back().col0 + segs.back().ncol == nc), SH_ERR_ARG,
+           "cm1 attention: the segments must cover the chunk");
   FabGuard fab{e, FabLaunch{}};
-  bool use_fab = fab_enabled();
+  bool use_fab = !cm1 && fab_enabled();
   for (const FaSeg& sg : segs) use_fab = use_fab && sg.hmasks;
-  SH_CHECK(use_fab || nc <= SH_MAX_COLS, SH_ERR_UNSUPPORTED,
+  SH_CHECK(cm1 || use_fab || nc <= SH_MAX_COLS, SH_ERR_UNSUPPORTED,
            "chunks of more than %u columns need the batched attention (device masks)", SH_MAX_COLS);
   if (use_fab && (rc = plan_fab(m, segs, nc, &fab))) return rc;
   for (uint32_t l = 0; l < m->n_layer; ++l) {
@@ -977,7 +1002,14 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     }
     qkv.layer = l;
     if ((rc = qkv_finish(w.gpart, nq, pq.part_stride, pq.ldo, L, vpart, nv, vldp, vstride))) return rc;
-    if (use_fab) {
+    if (cm1) {
+      FaArgs fa;
+      fa.layer = l; fa.N = nc; fa.col0 = 0; fa.kvlen = segs.back().kvlen; fa.mask_base = segs.front().mask_base;
+      fa.dbase = segs.front().kv->graph_base;
+      fa.kv_cap = segs.front().kv->max_seq;
+      if ((rc = sh_fa16_launch(e, m, segs.front().kv, fa, w.q, w.attn, w.bx, w.xs, w.cs, f16 ? w.bh : nullptr)))
+        return rc;
+    } else if (use_fab) {
       if ((rc = sh_fab_launch(e, m, fab.fl, l, w.q, w.attn, w.bx, w.xs, w.cs, f16 ? w.bh : nullptr))) return rc;
     } else {
       for (const FaSeg& sg : segs) {
@@ -1091,11 +1123,37 @@ static int ensure_fa_part(sh_model* m, uint32_t max_kvlen) {
   const uint32_t needed_splits = (max_kvlen + SH_FA_MIN_SPLIT_KEYS - 1) / SH_FA_MIN_SPLIT_KEYS;
   const size_t need = (size_t)m->n_kv * needed_splits * SH_FA_MAX_ROWS * sh_fa_part_stride(m->hd);
   if (need <= m->ws.fa_part_floats) return SH_OK;
+  g_graph_gen.fetch_add(1);  // captured graphs may point into the old buffer
   SH_HIP(hipStreamSynchronize(m->e->stream));
   SH_HIP(hipFree(m->ws.fa_part));
   m->ws.fa_part = nullptr;
   SH_HIP(hipMalloc(&m->ws.fa_part, need * 4));
   m->ws.fa_part_floats = need;
+  return SH_OK;
+}
+
+// Grows the cm1 attention buffers for chunks of up to ncol columns over keys
+// [0, kv_cap). Captured graphs may point into the old buffers: they are
+// dropped.
+static int ensure_fa16(sh_model* m, uint32_t kv_cap, uint32_t ncol) {
+  const uint32_t gqa = m->n_head / m->n_kv;
+  Workspace& w = m->ws;
+  const size_t pvh = sh_fa16_pv_halves(m->n_kv, m->hd, gqa, ncol, kv_cap);
+  const size_t sw = sh_fa16_sync_words(m->n_kv, gqa, ncol, kv_cap);
+  if (pvh <= w.fa16_pv_halves && sw <= w.fa16_sync_words) return SH_OK;
+  const size_t P = std::max(pvh, w.fa16_pv_halves), W = std::max(sw, w.fa16_sync_words);
+  g_graph_gen.fetch_add(1);
+  SH_HIP(hipStreamSynchronize(m->e->stream));
+  (void)hipFree(w.fa16_pv); (void)hipFree(w.fa16_ml); (void)hipFree(w.fa16_smax); (void)hipFree(w.fa16_flag);
+  w.fa16_pv = nullptr; w.fa16_ml = nullptr; w.fa16_smax = nullptr; w.fa16_flag = nullptr;
+  w.fa16_pv_halves = w.fa16_sync_words = 0;
+  SH_HIP(hipMalloc(&w.fa16_pv, P * 2));
+  SH_HIP(hipMalloc(&w.fa16_ml, P / m->hd * sizeof(float2)));
+  SH_HIP(hipMalloc(&w.fa16_smax, W * 32 * sizeof(float)));
+  SH_HIP(hipMalloc(&w.fa16_flag, (W + 1) * sizeof(uint32_t)));
+  SH_HIP(hipMemsetAsync(w.fa16_flag, 0, (W + 1) * sizeof(uint32_t), m->e->stream));
+  w.fa16_pv_halves = P;
+  w.fa16_sync_words = W;
   return SH_OK;
 }
 
@@ -1125,7 +1183,11 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
     if ((rc = ensure_fa_part(m, pos + L))) return rc;
   }
   m->call16 = m->wide16 && L >= SH_WIDE16_COLS;  // one matmul of L columns in the reference
+  // a masked forward of more than one token: the reference's cm1 attention
+  // (models/llama.rs:216-222, ops/flash_attn.rs:442-471)
+  m->call_cm1 = m->fa16 && L > 1 && !parents;
   const uint32_t CW = chunk_cols(m, L);
+  if (m->call_cm1 && !graph && (rc = ensure_fa16(m, pos + L, std::min(L, CW)))) return rc;
   // Attention: one segment per chunk (device masks) on the multi-group path,
   // else pieces of <= 8 columns; a causal segment's masks are relative to its
   // first column.
@@ -1149,7 +1211,7 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
     chunk_segs.push_back(segs);
   }
   uint64_t* dmask = nullptr;
-  if (CW > 8) {
+  if (CW > 8 && !m->call_cm1) {
     SH_HIP(hipMallocAsync((void**)&dmask, (size_t)L * 8, e->stream));
     SH_HIP(hipMemcpyAsync(dmask, hmask.data(), (size_t)L * 8, hipMemcpyHostToDevice, e->stream));
     for (size_t c = 0; c < chunk_segs.size(); ++c)
@@ -1235,10 +1297,12 @@ static int verify_greedy_graph(sh_engine* e, sh_model* m, sh_kv* kv, const uint3
   uint32_t* hp = e->spec.pinned;
   for (uint32_t i = 0; i < L; ++i) hp[32 + i] = tokens[i];
   hp[66] = pos;
-  const std::vector<uintptr_t> key = {2, (uintptr_t)m, (uintptr_t)kv, (uintptr_t)kv->k, kv->max_seq, L};
+  const std::vector<uintptr_t> key = {2, (uintptr_t)m, (uintptr_t)kv, (uintptr_t)kv->k, kv->max_seq, L, m->fa16};
   hipGraphExec_t ex = graph_find(e, key);
   if (!ex) {
-    if ((rc = ensure_rope(m, kv->max_seq)) || (rc = ensure_fa_part(m, kv->max_seq))) return rc;
+    if ((rc = ensure_rope(m, kv->max_seq)) || (rc = ensure_fa_part(m, kv->max_seq)) ||
+        (rc = ensure_fa16(m, kv->max_seq, L)))
+      return rc;
     rc = graph_capture(e, key, {kv}, {e->spec.base + 2}, [&] {
       int r = forward_dev(m, kv, e->spec.tok + 32, L, 0, nullptr, 2, nullptr, nullptr, nullptr);
       if (!r) r = sh_argmax_launch(e, m->ws.logits, m->V, L, m->ws.amax, e->spec.samp);
@@ -1370,6 +1434,7 @@ static int verify_unified_impl(sh_engine* e, sh_model* m, sh_kv* const* caches, 
   if (sampled_out) SH_HIP(hipMallocAsync((void**)&ids, SH_MAX_COLS16 * 4, e->stream));
   const bool want_logits = logits_out || logits_dev || sampled_out;
   m->call16 = m->wide16 && N >= SH_WIDE16_COLS;  // the reference's batch is one matmul of N columns
+  m->call_cm1 = false;  // the batched attention is the reference's scalar kernel (ops/flash_attn.rs:819-1016)
   const uint32_t CW = chunk_cols(m, N);
   // attention segments: runs of one sequence's columns in a chunk (at most 8
   // each on the 8-column path; device masks on the multi-group path)
@@ -1684,11 +1749,13 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
     const uint32_t d0 = dkv->pos;
     if (greedy_graph) {
       const std::vector<uintptr_t> key = {1, (uintptr_t)tm, (uintptr_t)dm, (uintptr_t)tkv, (uintptr_t)dkv,
-                                          (uintptr_t)tkv->k, (uintptr_t)dkv->k, tkv->max_seq, dkv->max_seq, n, np};
+                                          (uintptr_t)tkv->k, (uintptr_t)dkv->k, tkv->max_seq, dkv->max_seq, n, np,
+                                          tm->fa16, dm->fa16};
       hipGraphExec_t ex = graph_find(e, key);
       if (!ex) {
         if ((rc = ensure_rope(tm, tkv->max_seq)) || (rc = ensure_rope(dm, dkv->max_seq)) ||
-            (rc = ensure_fa_part(tm, tkv->max_seq)) || (rc = ensure_fa_part(dm, dkv->max_seq)))
+            (rc = ensure_fa_part(tm, tkv->max_seq)) || (rc = ensure_fa_part(dm, dkv->max_seq)) ||
+            (rc = ensure_fa16(tm, tkv->max_seq, n + 1)) || (rc = ensure_fa16(dm, dkv->max_seq, np + 1)))
           return rc;
         rc = graph_capture(e, key, {dkv, tkv}, {e->spec.base, e->spec.base + 1},
                            [&] { return enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, 0, 0); }, &ex);
@@ -1769,6 +1836,119 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   *n_emitted = ne;
   if (drafts_out) std::memcpy(drafts_out, drafts, n * 4);
   return sh_prof_flush(e);
+}
+
+// Engine::draft_tokens (inference/mod.rs:2062-2092) with a separate draft
+// model: the cache's pending tokens and last_token, then n - 1 single-token
+// forwards, each argmax feeding the next embedding on the device; the ids come
+// back at the end. The cache advances by its pending count + n (d_n is not fed).
+extern "C" int sh_draft_tokens(sh_engine* e, sh_model* dm, sh_kv* dkv, uint32_t last_token, uint32_t n_max,
+                               uint32_t* drafts_out) {
+  SH_CHECK(e && dm && dkv && drafts_out, SH_ERR_ARG, "sh_draft_tokens: NULL argument");
+  SH_CHECK(last_token < dm->V, SH_ERR_ARG, "last_token %u out of range", last_token);
+  const uint32_t n = std::min<uint32_t>(std::max<uint32_t>(n_max, 1), 8);  // mod.rs:2072
+  const uint32_t np = (uint32_t)dkv->pending.size();
+  SH_CHECK((uint64_t)dkv->pos + np + n <= dkv->max_seq, SH_ERR_CAPACITY, "draft lookahead exceeds KV capacity");
+  int rc = spec_bufs(e, dm->V);
+  if (rc) return rc;
+  uint32_t* hp = e->spec.pinned;
+  for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
+  hp[np] = last_token;
+  SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
+  if ((rc = forward_dev(dm, dkv, e->spec.tok, np + 1, dkv->pos, nullptr, 1, nullptr, nullptr, nullptr))) return rc;
+  if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1))) return rc;
+  for (uint32_t i = 1; i < n; ++i) {
+    if ((rc = forward_dev(dm, dkv, e->spec.tok + np + i, 1, dkv->pos, nullptr, 1, nullptr, nullptr, nullptr)))
+      return rc;
+    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1 + i))) return rc;
+  }
+  SH_HIP(hipMemcpyAsync(hp, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
+  SH_HIP(hipStreamSynchronize(e->stream));
+  std::memcpy(drafts_out, hp, n * 4);
+  dkv->pending.clear();
+  return sh_prof_flush(e);
+}
+
+// The batched speculative step of the reference's server (server/inference.rs:
+// 2777-2924): drafts for every sequence, one verify_unified over all of them,
+// per-sequence acceptance and rollback. The drafts of all sequences at one
+// draft position go through the draft model as one batched forward (one
+// column per sequence; a sequence's first position also carries its pending
+// tokens), where the reference calls draft_tokens per sequence
+// (server/inference.rs:2806-2812).
+extern "C" int sh_spec_step_batch(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* const* tkv, sh_kv* const* dkv,
+                                  uint32_t B, const uint32_t* last_tokens, uint32_t n_max, sh_sampling* samplers,
+                                  uint32_t* emitted_out, uint32_t* n_emitted, uint32_t* drafts_out) {
+  SH_CHECK(e && tm && dm && tkv && dkv && last_tokens && emitted_out && n_emitted, SH_ERR_ARG,
+           "sh_spec_step_batch: NULL argument");
+  SH_CHECK(B >= 1, SH_ERR_ARG, "spec_step_batch: empty batch");
+  SH_CHECK(tm->V == dm->V, SH_ERR_ARG, "draft vocab %u != target vocab %u", dm->V, tm->V);
+  const uint32_t n = std::min<uint32_t>(std::max<uint32_t>(n_max, 1), 8);
+  std::vector<uint32_t> P(B), np(B);
+  for (uint32_t s = 0; s < B; ++s) {
+    SH_CHECK(tkv[s] && dkv[s], SH_ERR_ARG, "spec_step_batch: cache %u is NULL", s);
+    SH_CHECK(last_tokens[s] < tm->V, SH_ERR_ARG, "spec_step_batch: last token %u of sequence %u", last_tokens[s], s);
+    P[s] = tkv[s]->pos;
+    np[s] = (uint32_t)dkv[s]->pending.size();
+    SH_CHECK(dkv[s]->pos + np[s] == P[s], SH_ERR_STATE, "sequence %u: draft cache %u + %u pending != target %u", s,
+             dkv[s]->pos, np[s], P[s]);
+    SH_CHECK((uint64_t)P[s] + n + 1 <= tkv[s]->max_seq && (uint64_t)P[s] + n + 1 <= dkv[s]->max_seq,
+             SH_ERR_CAPACITY, "sequence %u: spec lookahead exceeds KV capacity (run.rs:270-283)", s);
+    if (samplers)
+      SH_CHECK(samplers[s].mode == SH_SAMPLE_GREEDY || samplers[s].mode == SH_SAMPLE_COMPARE, SH_ERR_ARG,
+               "spec_step_batch: sequence %u sampler mode %u (GREEDY or COMPARE)", s, samplers[s].mode);
+  }
+  // drafts: position 1 takes each sequence's pending tokens and last token,
+  // positions 2..n its previous draft
+  std::vector<uint32_t> drafts((size_t)B * n), toks, lens(B), ids;
+  for (uint32_t i = 0; i < n; ++i) {
+    toks.clear();
+    for (uint32_t s = 0; s < B; ++s) {
+      if (i == 0) {
+        for (uint32_t t : dkv[s]->pending) toks.push_back(t);
+        toks.push_back(last_tokens[s]);
+        lens[s] = np[s] + 1;
+      } else {
+        toks.push_back(drafts[(size_t)s * n + i - 1]);
+        lens[s] = 1;
+      }
+    }
+    ids.assign(toks.size(), 0u);
+    int rc = verify_unified_impl(e, dm, dkv, B, toks.data(), lens.data(), nullptr, nullptr, nullptr, nullptr,
+                                 ids.data(), nullptr);
+    if (rc) return rc;
+    uint32_t q = 0;
+    for (uint32_t s = 0; s < B; ++s) {
+      q += lens[s];
+      drafts[(size_t)s * n + i] = ids[q - 1];
+    }
+  }
+  // verify [last, d_1..d_n] of every sequence in one batch
+  toks.clear();
+  for (uint32_t s = 0; s < B; ++s) {
+    toks.push_back(last_tokens[s]);
+    for (uint32_t i = 0; i < n; ++i) toks.push_back(drafts[(size_t)s * n + i]);
+    lens[s] = n + 1;
+  }
+  ids.assign(toks.size(), 0u);
+  int rc = verify_unified_impl(e, tm, tkv, B, toks.data(), lens.data(), nullptr, nullptr, nullptr, nullptr,
+                               ids.data(), nullptr, samplers);
+  if (rc) return rc;
+  // per-sequence acceptance (server/inference.rs:2859-2883) and rollback
+  for (uint32_t s = 0; s < B; ++s) {
+    const uint32_t* col = ids.data() + (size_t)s * (n + 1);
+    const uint32_t* d = drafts.data() + (size_t)s * n;
+    uint32_t acc = 0;
+    while (acc < n && col[acc] == d[acc]) ++acc;
+    for (uint32_t i = 0; i <= acc; ++i) emitted_out[(size_t)s * (n + 1) + i] = col[i];
+    n_emitted[s] = acc + 1;
+    tkv[s]->pos = P[s] + acc + 1;
+    dkv[s]->pos = std::min(dkv[s]->pos, P[s] + acc + 1);
+    dkv[s]->pending.clear();
+    if (acc == n) dkv[s]->pending.push_back(d[n - 1]);  // d_n was never fed to the draft
+    if (drafts_out) std::memcpy(drafts_out + (size_t)s * n, d, n * 4);
+  }
+  return SH_OK;
 }
 
 extern "C" int sh_spec_step_logits(sh_engine* e, float* p_out, float* q_out, uint32_t* n_out, uint32_t* V_out) {

@@ -161,6 +161,14 @@ struct Workspace {
   size_t fa_part_floats = 0;
   float* fab_part = nullptr;  // batched attention partials of every segment of a chunk (grown on demand)
   size_t fab_part_floats = 0;
+  // cm1 attention (sh_fa16_launch, grown on demand): per 64-key block and row
+  // the f16 P V accumulator, (M, l); per split the row maxima and a look-back
+  // flag (zero between launches), then one error word
+  uint16_t* fa16_pv = nullptr;
+  float2* fa16_ml = nullptr;
+  float* fa16_smax = nullptr;
+  uint32_t* fa16_flag = nullptr;
+  size_t fa16_pv_halves = 0, fa16_sync_words = 0;
   size_t gpart_floats = 0;
   // Second operand set, written by residual preps fused into the o / down GEMVs
   // (other workgroups of the producing kernel may still be staging the first):
@@ -214,6 +222,12 @@ struct sh_model {
   bool wide16_ok = false;
   bool wide16 = false;
   bool call16 = false;
+  // Causal single-sequence forward calls of more than one column compute
+  // their attention with the reference's cooperative-matrix flash attention
+  // arithmetic (sh_fa16_launch): fa16 the switch (default on; SH_FA_CM=0 at
+  // upload turns it off), call_cm1 set for the forward call in progress.
+  bool fa16 = true;
+  bool call_cm1 = false;
 };
 
 struct sh_kv {
@@ -436,6 +450,32 @@ int sh_fa_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs&
                  float* attn_out, uint16_t* bx, uint16_t* xs, float* cs, OpndSrc* combine_out = nullptr);
 // With combine_out, the combine kernel is skipped and *combine_out describes
 // the partials for a consumer that combines them itself (OPND_FA).
+
+// Attention of a single-sequence causal chunk (columns [col0, col0 + N) of the
+// forward chunk, keys [0, kvlen), chunk keys from mask_base) with the
+// reference's cooperative-matrix flash attention arithmetic (attn16.hip):
+// writes attn_out [N][n_head * hd] and the Wo operand (hi/lo groups bx, xs,
+// cs, or with bh the f16 rows of the wide f16 GEMM). Graph replay as
+// sh_fa_launch (fa.dbase, fa.kv_cap).
+struct Fa16Args {
+  const float* q = nullptr;  // roped queries of the call's first column [N][n_head * hd]
+  const uint16_t* kc = nullptr;
+  const uint16_t* vc = nullptr;
+  uint32_t max_seq = 0, n_head = 0, n_kv = 0, gqa = 0, ncol = 0, col0 = 0, kvlen = 0, mask_base = 0;
+  const uint32_t* dbase = nullptr;
+  uint32_t n_rg = 0, nbmax = 0, max_splits = 0;
+  float qs = 0.f;  // f32(f32(1 / sqrt(hd)) * f32(log2 e))
+  uint16_t* pv = nullptr;
+  float2* ml = nullptr;
+  float* smax = nullptr;
+  uint32_t* flag = nullptr;
+  uint32_t* err = nullptr;
+};
+int sh_fa16_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q,
+                   float* attn_out, uint16_t* bx, uint16_t* xs, float* cs, uint16_t* bh = nullptr);
+// Buffer sizes sh_fa16_launch needs for N columns over keys [0, kv_cap).
+size_t sh_fa16_pv_halves(uint32_t n_kv, uint32_t hd, uint32_t gqa, uint32_t ncol, uint32_t kv_cap);
+size_t sh_fa16_sync_words(uint32_t n_kv, uint32_t gqa, uint32_t ncol, uint32_t kv_cap);
 
 // Batched attention (attn_batch.hip): every segment of a forward chunk in one
 // launch per layer, then one combine launch. A segment is a run of one

@@ -191,6 +191,41 @@ class Engine:
         em = emitted[: ne.value].tolist()
         return SpecStepOut(em, ne.value - 1, em[-1], drafts[:n].tolist())
 
+    def draft_tokens(self, draft: "Model", dcache: "KvCache", last_token: int, n_max: int) -> list:
+        """Engine::draft_tokens (inference/mod.rs:2062-2092): greedy drafts of a separate
+        draft model from its cache (pending tokens first); the cache advances by
+        pending + n and is truncated by the caller to the accepted length."""
+        n = min(max(n_max, 1), 8)
+        out = np.zeros(n, dtype=np.uint32)
+        N.check(self._lib.sh_draft_tokens(self.h, draft.h, dcache.h, last_token, n_max, out.ctypes.data_as(N.U32P)))
+        return out.tolist()
+
+    def spec_step_batch(self, target: "Model", draft: "Model", tcaches: Sequence["KvCache"],
+                        dcaches: Sequence["KvCache"], last_tokens: Sequence[int], n_max: int,
+                        samplers: Optional[Sequence[N.sh_sampling]] = None):
+        """The server's batched speculative step (sh_spec_step_batch, server/inference.rs:2777-2924):
+        returns (emitted per sequence, drafts per sequence)."""
+        B = len(tcaches)
+        n = min(max(n_max, 1), 8)
+        th = (C.c_void_p * B)(*[c.h for c in tcaches])
+        dh = (C.c_void_p * B)(*[c.h for c in dcaches])
+        last = np.ascontiguousarray(last_tokens, dtype=np.uint32)
+        em = np.zeros((B, n + 1), dtype=np.uint32)
+        ne = np.zeros(B, dtype=np.uint32)
+        dr = np.zeros((B, n), dtype=np.uint32)
+        arr = None
+        if samplers is not None:
+            arr = (N.sh_sampling * B)(*samplers)
+        N.check(self._lib.sh_spec_step_batch(self.h, target.h, draft.h, C.cast(th, C.POINTER(C.c_void_p)),
+                                             C.cast(dh, C.POINTER(C.c_void_p)), B, last.ctypes.data_as(N.U32P),
+                                             n_max, C.cast(arr, C.c_void_p) if arr is not None else None,
+                                             em.ctypes.data_as(N.U32P), ne.ctypes.data_as(N.U32P),
+                                             dr.ctypes.data_as(N.U32P)))
+        if samplers is not None:
+            for s_in, s_out in zip(samplers, arr):
+                s_in.counter = s_out.counter
+        return [em[s, : ne[s]].tolist() for s in range(B)], [dr[s].tolist() for s in range(B)]
+
     def spec_step_logits(self):
         """Target logits [(n+1)][V] and draft logits [n][V] of the last stochastic
         decode_speculative on this engine (the reference's tap readback,
@@ -321,6 +356,20 @@ class Model:
     @wide_f16.setter
     def wide_f16(self, on: bool):
         N.check(self.engine._lib.sh_model_set_wide_f16(self.h, 1 if on else 0))
+
+    @property
+    def cm1_attention(self) -> bool:
+        """Causal forward calls of more than one column compute attention with
+        the reference's cooperative-matrix flash attention arithmetic
+        (flash_attn_cm1.slang via ops/flash_attn.rs:442-471): f16 staged q,
+        64-key blocks, f16 P, f16 P V accumulators and output."""
+        on = C.c_int()
+        N.check(self.engine._lib.sh_model_cm1_attention(self.h, C.byref(on)))
+        return bool(on.value)
+
+    @cm1_attention.setter
+    def cm1_attention(self, on: bool):
+        N.check(self.engine._lib.sh_model_set_cm1_attention(self.h, 1 if on else 0))
 
     def close(self):
         if self.h:

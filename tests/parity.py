@@ -15,6 +15,14 @@ oracle): bound 1.5e-3 x max, inside the north star's 2e-2 abs / 1e-2 rel.
 A test whose caches were filled by a wide call keeps the wide bound for later
 narrow calls, which read those K/V rows.
 
+Causal calls of more than one column compute attention with the reference's
+cooperative-matrix flash attention arithmetic (flash_attn_cm1.slang via
+ops/flash_attn.rs:442-471: f16 staged q, f16 P, f16 P V accumulators and
+output) when the model's switch is on (the default), and the oracle follows
+with set_attn_cm1: there too an f32-level difference of a score can flip one
+f16 rounding, so such calls, and later calls that read the K/V they shaped,
+take the wide bounds (pair() returns whether they apply).
+
 Greedy ids: equal, except a column whose oracle top-2 margin is smaller than
 twice the largest logit difference seen (a near-tie of the oracle itself).
 """
@@ -56,3 +64,14 @@ def kv_layer0_ok(g, o, wide=False):
     measured up to 6e-4 of the scale, 1-2 ulps of the largest entries)."""
     floor = (2e-4 if wide else 1e-6) * np.abs(o).max()
     return bool(np.all(np.abs(g - o) <= np.abs(o) * 2.0 ** -10 + floor))
+
+
+def pair(om, gm):
+    """Give the oracle model om the arithmetic of the GPU model gm: the wide
+    GEMM's f16 operands for calls of >= 32 columns (mode 2) and the cm1
+    attention for causal calls of more than one column. Returns whether the
+    wide bounds apply to calls after a multi-column call (f16 roundings in
+    play)."""
+    om.set_mm16(2 if gm.wide_f16 else 0)
+    om.set_attn_cm1(gm.cm1_attention)
+    return bool(gm.wide_f16 or gm.cm1_attention)

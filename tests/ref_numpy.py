@@ -161,14 +161,57 @@ def _r16(a):
     return np.asarray(a).astype(np.float32).astype(np.float16).astype(np.float64)
 
 
+def attn_cm1(q, K, V, vis):
+    """The reference's flash_attn_cm1.slang arithmetic for query rows q [R][hd]
+    (f32 values) over f16 keys / values K, V [n][hd] with visibility vis
+    [R][n], written with numpy's own float16 / float32 conversions: q staged as
+    f16(q * f32(f32(1 / sqrt(hd)) * f32(log2 e))); per 64-key block from key 0
+    the row maximum, the f16 output rescaled by f16(exp2(m_old - m_new)),
+    P = exp2(S - m) rounded to f16, P V added into an f16 accumulator per
+    16-key chunk, that added to the f16 output; out = f32(O) * f32(1 / L)."""
+    R, hd = q.shape
+    n = K.shape[0]
+    qs = np.float32(np.float32(1.0) / np.sqrt(np.float32(hd))) * np.float32(1.4426950408889634)
+    q16 = (q.astype(np.float32) * qs).astype(np.float16).astype(np.float64)
+    Kf = np.asarray(K, np.float64)
+    Vf = np.asarray(V, np.float64)
+    M = np.full(R, -1e30, np.float32)
+    Lsum = np.zeros(R)
+    O = np.zeros((R, hd), np.float16)
+    for k0 in range(0, n, 64):
+        k1 = min(k0 + 64, n)
+        vb = vis[:, k0:k1]
+        S = (q16 @ Kf[k0:k1].T).astype(np.float32)
+        S = np.where(vb, S, np.float32(-np.inf))
+        Mn = np.maximum(np.maximum(S.max(axis=1), np.float32(-1e30)), M)
+        e = np.exp2((M - Mn).astype(np.float64)).astype(np.float32)
+        Lsum = e.astype(np.float64) * Lsum
+        O = (e.astype(np.float16).astype(np.float64)[:, None] * O.astype(np.float64)).astype(np.float16)
+        Pm = np.where(vb, np.exp2((S - Mn[:, None]).astype(np.float64)).astype(np.float32), np.float32(0))
+        Lsum = Lsum + Pm.astype(np.float64).sum(axis=1)
+        P16 = Pm.astype(np.float16).astype(np.float64)
+        acc = np.zeros((R, hd), np.float16)
+        for c0 in range(0, k1 - k0, 16):
+            c1 = min(c0 + 16, k1 - k0)
+            acc = (acc.astype(np.float64) + P16[:, c0:c1] @ Vf[k0 + c0:k0 + c1]).astype(np.float16)
+        O = (O.astype(np.float64) + acc.astype(np.float64)).astype(np.float16)
+        M = Mn
+    Lf = Lsum.astype(np.float32)
+    inv = np.where(Lf == 0, np.float32(0), np.float32(1) / np.where(Lf == 0, np.float32(1), Lf))
+    return (O.astype(np.float32) * inv[:, None]).astype(np.float64)
+
+
 class RefLlama:
     """float64 Llama forward with f16 K/V storage (same cache rounding as the reference)."""
 
-    def __init__(self, buf: bytes, mm16: bool = False):
+    def __init__(self, buf: bytes, mm16: bool = False, cm1: bool = False):
         """mm16: the dense matmuls with the reference's wide-GEMM operands
-        (mul_mm_cm.slang): f16-rounded f32 weights and f16-rounded inputs."""
+        (mul_mm_cm.slang): f16-rounded f32 weights and f16-rounded inputs.
+        cm1: causal calls of more than one column compute attention with the
+        reference's cooperative-matrix flash attention arithmetic (attn_cm1)."""
         meta, T, _ = read_gguf(buf)
         self.mm16 = mm16
+        self.cm1 = cm1
         self.nl = meta["llama.block_count"]
         self.d = meta["llama.embedding_length"]
         self.nh = meta["llama.attention.head_count"]
@@ -254,8 +297,14 @@ class RefLlama:
             Kc, Vc = self.K[li], self.Vc[li]
             att = np.zeros((L, self.nh, self.hd))
             q32 = q.astype(np.float32).astype(np.float64)
+            causal = all(parents[i] == i - 1 for i in range(L))
             for hh in range(self.nh):
                 kh = hh // gqa
+                if self.cm1 and L > 1 and causal:
+                    vis = np.ones((L, P + L), dtype=bool)
+                    vis[:, P:] = anc
+                    att[:, hh, :] = attn_cm1(q32[:, hh, :], Kc[:, kh, :], Vc[:, kh, :], vis)
+                    continue
                 s = q32[:, hh, :] @ Kc[:, kh, :].T / np.sqrt(self.hd)  # [L, P+L]
                 mask = np.ones_like(s, dtype=bool)
                 mask[:, P:] = anc

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from parity import ids_agree, logits_close
+from parity import ids_agree, logits_close, pair
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K
 
@@ -26,7 +26,7 @@ def test_draft_shape_one_and_two_columns(engine):
     img = S.GgufImage(SHAPE, seed=22)
     gm = engine.upload_weights(img)
     om = O.Model(img)
-    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    wide = pair(om, gm)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
     V = gm.dims.n_vocab
     gkv = engine.allocate_kv_cache(gm, 128)
     okv = O.KvCache(om, 128)
@@ -38,10 +38,10 @@ def test_draft_shape_one_and_two_columns(engine):
         print(f"draft shape: verify {n} columns", flush=True)
         gl, _ = engine.forward_full_readback(gm, gkv, toks, 48)
         ol, _ = O.forward(om, okv, toks, 48)
-        close(gl, ol, gm.wide_f16)
+        close(gl, ol, wide)
         gkv.truncate(48)
         ids = engine.verify_greedy(gm, gkv, toks, 48)
-        if gm.wide_f16:  # prefill >= 32 columns: near-ties of the oracle allowed
+        if wide:  # f16 roundings in the prefill: near-ties of the oracle allowed
             bad = np.where(ids != ol.argmax(axis=1))[0]
             assert all(ol[i].max() - ol[i, ids[i]] <= 3e-3 * np.abs(ol).max() for i in bad), (ids, ol.argmax(axis=1))
         else:

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from parity import ids_agree, kv_layer0_ok, logits_close
+from parity import ids_agree, kv_layer0_ok, logits_close, pair as pair_oracle
 from seeker_amd import SeekerError
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K, GGML_Q8_0, SH_ERR_ARG, SH_ERR_CAPACITY, SH_ERR_STATE
@@ -34,7 +34,7 @@ def pair(request, engine):
     print(f"model {request.param}", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
-    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    pair_oracle(om, gm)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
     yield request.param, img, gm, om
     gm.close()
     om.close()
@@ -70,8 +70,8 @@ def test_prefill_and_verify(engine, pair):
     prompt = S.tokens(1234, 64, V)
     gkv = engine.allocate_kv_cache(gm, 256)
     okv = O.KvCache(om, 256)
-    wide = gm.wide_f16  # the 64-column prefill is a wide call
-    print(f"{name}: prefill 64 (wide f16 {wide})", flush=True)
+    wide = gm.wide_f16 or gm.cm1_attention  # the 64-column prefill: wide GEMMs, cm1 attention
+    print(f"{name}: prefill 64 (f16 roundings {wide})", flush=True)
     gl, gr = engine.forward_full_readback(gm, gkv, prompt, 0, full_logits=True)
     ol, orr = O.forward(om, okv, prompt, 0)
     close(gl, ol, wide)
@@ -111,7 +111,7 @@ def test_tree_verify_and_compact(engine, pair):
     parents = [-1, 0, 0, 0, 1, 1, 2, 3, 4, 6, 6, 7]
     gkv = engine.allocate_kv_cache(gm, 128)
     okv = O.KvCache(om, 128)
-    wide = gm.wide_f16  # the 40-column prefill is a wide call
+    wide = gm.wide_f16 or gm.cm1_attention  # the 40-column prefill: wide GEMMs, cm1 attention
     engine.forward_full_readback(gm, gkv, prompt, 0, full_logits=False)
     O.forward(om, okv, prompt, 0, logits_mode=0)
     print(f"{name}: tree 12", flush=True)
@@ -177,6 +177,61 @@ def test_wide_calls_follow_reference_f16(engine, pair):
     assert np.array_equal(a, b)
     g1.close()
     g2.close()
+
+
+def test_masked_calls_follow_reference_cm1(engine, pair):
+    """A causal call of more than one column computes its attention with the
+    reference's flash_attn_cm1 arithmetic (f16 staged q, 64-key blocks, f16 P,
+    f16 P V accumulators and output, ops/flash_attn.rs:442-471): with the same
+    synthetic f16 K/V in both caches (1000 positions, 16 blocks), the 8-column
+    verify sits clearly closer to the oracle's cm1 attention than to its exact
+    softmax, and the other way round with the switch off; a one-column call is
+    unchanged by the switch."""
+    name, img, gm, om = pair
+    d = gm.dims
+    V = d.n_vocab
+    P = 1000
+    vt = S.tokens(62, 8, V)
+    rng = np.random.default_rng(63)
+    rows = [rng.standard_normal((P, d.n_head_kv, d.head_dim)).astype(np.float16).view(np.uint16)
+            for _ in range(2 * d.n_layer)]
+
+    def seeded(gkv, okv):
+        for layer in range(d.n_layer):
+            for isv in (0, 1):
+                r = rows[2 * layer + isv]
+                if gkv is not None:
+                    gkv.write_layer(layer, bool(isv), r)
+                if okv is not None:
+                    okv.layer(layer, bool(isv), P)[:] = r
+        for c in (gkv, okv):
+            if c is not None:
+                c.set_position(P)
+
+    res, one = {}, {}
+    for on in (True, False):
+        gkv = engine.allocate_kv_cache(gm, P + 32)
+        seeded(gkv, None)
+        gm.cm1_attention = on
+        res[on], _ = engine.forward_full_readback(gm, gkv, vt, P)
+        gkv.truncate(P)
+        one[on], _ = engine.forward_full_readback(gm, gkv, vt[:1], P)
+        gkv.close()
+    gm.cm1_attention = True
+    ref = {}
+    for on in (True, False):
+        okv = O.KvCache(om, P + 32)
+        seeded(None, okv)
+        om.set_attn_cm1(on)
+        ref[on], _ = O.forward(om, okv, vt, P)
+        okv.close()
+    om.set_attn_cm1(True)
+    dd = {(g, o): float(np.abs(res[g] - ref[o]).max()) for g in (True, False) for o in (True, False)}
+    print(f"{name}: 8-column verify max|d| (gpu cm1, oracle cm1) {dd}", flush=True)
+    assert dd[(True, True)] < 0.5 * dd[(True, False)]
+    assert dd[(False, False)] < 0.5 * dd[(False, True)]
+    logits_close(res[True], ref[True], wide=True)
+    assert np.array_equal(one[True], one[False])
 
 
 def test_errors_are_reported(engine, pair):

@@ -18,13 +18,16 @@ greedy ids and tree paths identical; new K/V rows equal to the oracle's up to
 one f16 ulp (an f32-level difference occasionally rounds the other way). The
 164-column tree batch is a wide call: it computes every matmul with the
 reference's f16 wide-GEMM operands, compared with the oracle in mode 2 under
-the wide bounds of tests/parity.py.
+the wide bounds of tests/parity.py. The 8-column verify computes its attention
+with the reference's cm1 arithmetic (f16 q, P, P V accumulators and output),
+compared with the oracle doing the same under the same wide bounds, and
+clearly closer to it than to the exact softmax.
 """
 import numpy as np
 import pytest
 
 import oracle as O
-from parity import ids_agree, kv_layer0_ok, logits_close
+from parity import ids_agree, kv_layer0_ok, logits_close, pair
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K, SH_SAMPLE_REJECTION, sh_sampling
 
@@ -83,7 +86,7 @@ def target(engine):
     print("8B-shape 2-layer target", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
-    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    pair(om, gm)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
     yield gm, om
     gm.close()
     om.close()
@@ -98,19 +101,30 @@ def test_config2_verify_8_columns_at_4096(engine, target):
     gkv, okv = engine.allocate_kv_cache(gm, P + 64), O.KvCache(om, P + 64)
     seed_kv(gkv, okv, d, P, seed=1)
     toks = S.tokens(11, L, d.n_vocab)
-    print("configs[2] verify L=8 at P=4096: forward_full", flush=True)
+    cm1 = gm.cm1_attention  # the 8-column verify's attention: the reference's cm1 arithmetic
+    print(f"configs[2] verify L=8 at P=4096: forward_full (cm1 attention {cm1})", flush=True)
     gl, gres = engine.forward_full_readback(gm, gkv, toks, P)
     ol, ores = O.forward(om, okv, toks, P)
-    close(gl, ol)
-    close(gres, ores)
-    check_new_rows(gkv, okv, d, P, P + L)
+    close(gl, ol, cm1)
+    close(gres, ores, cm1)
+    check_new_rows(gkv, okv, d, P, P + L, cm1)
     print("configs[2] verify L=8 at P=4096: graph-replayed verify_greedy (twice)", flush=True)
     for _ in range(2):
         gkv.truncate(P)
         ids = engine.verify_greedy(gm, gkv, toks, P)
-        assert np.array_equal(ids, ol.argmax(axis=1)), (ids, ol.argmax(axis=1))
+        ids_agree(gl, ol, cm1)  # the graph replays the same kernels as forward_full
+        assert np.array_equal(ids, gl.argmax(axis=1)), (ids, gl.argmax(axis=1))
         assert gkv.position == P + L
-    check_new_rows(gkv, okv, d, P, P + L)
+    check_new_rows(gkv, okv, d, P, P + L, cm1)
+    if cm1:
+        # the attention follows the cm1 oracle clearly more closely than the exact one
+        om.set_attn_cm1(False)
+        okv.set_position(P)
+        ol0, _ = O.forward(om, okv, toks, P)
+        om.set_attn_cm1(True)
+        d1, d0 = float(np.abs(gl - ol).max()), float(np.abs(gl - ol0).max())
+        print(f"configs[2] verify: max|d| to the cm1 oracle {d1:.3e}, to the exact oracle {d0:.3e}", flush=True)
+        assert d1 < 0.5 * d0
     gkv.close()
     okv.close()
 
@@ -121,7 +135,7 @@ def test_config2_spec_step_with_1b_shape_draft(engine, target):
     dimg = S.GgufImage(D1B_2L, seed=1)
     gd = engine.upload_weights(dimg)
     od = O.Model(dimg)
-    od.set_mm16(2 if gd.wide_f16 else 0)
+    wide = pair(od, gd) or gm.cm1_attention
     P, k = 4096, 7
     gtkv, otkv = engine.allocate_kv_cache(gm, P + 64), O.KvCache(om, P + 64)
     gdkv, odkv = engine.allocate_kv_cache(gd, P + 64), O.KvCache(od, P + 64)
@@ -136,8 +150,8 @@ def test_config2_spec_step_with_1b_shape_draft(engine, target):
         assert r.emitted == o_em, (step, r.emitted, o_em)
         assert gtkv.position == otkv.position and gdkv.position == odkv.position
         last = r.emitted[-1]
-    check_new_rows(gtkv, otkv, gm.dims, P, gtkv.position)
-    check_new_rows(gdkv, odkv, gd.dims, P, gdkv.position)
+    check_new_rows(gtkv, otkv, gm.dims, P, gtkv.position, wide)
+    check_new_rows(gdkv, odkv, gd.dims, P, gdkv.position, wide)
     for x in (gtkv, gdkv, otkv, odkv, gd, od):
         x.close()
     dimg.close()
@@ -176,8 +190,8 @@ def test_config3_tree_verify_b4_41_nodes_at_8192(engine, target):
     ol = []
     for b in range(B):
         print(f"  oracle tree forward, sequence {b}", flush=True)
-        lg, _ = O.forward(om, ocaches[b], tokens[b], P, parents=par)
-        wide = gm.wide_f16  # 164 columns: one wide call
+        lg, _ = O.forward(om, ocaches[b], tokens[b], P, parents=par, batched=True)
+        wide = gm.wide_f16  # 164 columns: one wide call (trees keep the f32-level attention)
         close(gl[b], lg, wide)
         ids_agree(gl[b], lg, wide)
         assert np.array_equal(out.sampled.reshape(B, n)[b], gl[b].argmax(axis=1))

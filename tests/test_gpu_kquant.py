@@ -25,6 +25,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from parity import ids_agree, logits_close, pair
 from seeker_amd import QTensor
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K, GGML_Q5_K, GGML_Q6_K
@@ -161,10 +162,8 @@ def test_kquant_columns_independent_of_batch(engine):
 # ------------------------------------------------------------------ models
 
 
-def close(a, b):
-    err = np.abs(a - b)
-    assert np.all(err <= np.maximum(2e-2, 1e-2 * np.abs(b))), float(err.max())
-    assert err.max() <= 3e-4 * np.abs(b).max(), (float(err.max()), float(np.abs(b).max()))
+def close(a, b, wide=False):
+    logits_close(a, b, wide)  # north star + 3e-4 x max, or the f16-rounding bounds of tests/parity.py
 
 
 Q4KM = S.LlamaShape(3, 512, 8, 4, 1024, 3000, 1024, 1e-5, 5e5, 0.02, GGML_Q4_K, GGML_Q4_K, out_type=GGML_Q6_K,
@@ -185,7 +184,7 @@ def model(request, engine):
     print(f"model {request.param}", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
-    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    pair(om, gm)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
     yield request.param, gm, om
     gm.close()
     om.close()
@@ -201,22 +200,24 @@ def test_mixed_chunks_match_oracle(engine, model):
     engine.prefill(gm, gkv, prompt, 0)
     O.forward(om, okv, prompt, 0, logits_mode=0)
     pos = 40
+    wide = gm.wide_f16 or gm.cm1_attention  # the prefill's f16 roundings (cm1 attention)
     for n in (1, 5, 8, 12, 64):
         toks = S.tokens(80 + n, n, V)
         print(f"{name}: verify {n} columns at {pos}", flush=True)
         gl, gres = engine.forward_full_readback(gm, gkv, toks, pos)
         ol, ores = O.forward(om, okv, toks, pos)
-        close(gl, ol)
-        close(gres, ores)
+        close(gl, ol, wide)
+        close(gres, ores, wide)
         gkv.truncate(pos)
-        assert np.array_equal(engine.verify_greedy(gm, gkv, toks, pos), ol.argmax(axis=1))
+        assert np.array_equal(engine.verify_greedy(gm, gkv, toks, pos), gl.argmax(axis=1))
+        ids_agree(gl, ol, wide)
         pos += n
     par = [-1, 0, 0, 1, 1, 2, 3]
     toks = S.tokens(99, len(par), V)
     print(f"{name}: tree of 7 at {pos}", flush=True)
     gl, _ = engine.forward_full_readback(gm, gkv, toks, pos, parents=par)
     ol, _ = O.forward(om, okv, toks, pos, parents=par)
-    close(gl, ol)
+    close(gl, ol, wide)
     gkv.close()
     okv.close()
 
@@ -226,8 +227,8 @@ def test_mixed_spec_steps_match_oracle(engine):
     t_img, d_img = S.GgufImage(Q4KM, seed=41), S.GgufImage(Q5KM, seed=42)
     gt, gd = engine.upload_weights(t_img), engine.upload_weights(d_img)
     ot, od = O.Model(t_img), O.Model(d_img)
-    ot.set_mm16(2 if gt.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
-    od.set_mm16(2 if gd.wide_f16 else 0)
+    pair(ot, gt)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
+    pair(od, gd)
     V = gt.dims.n_vocab
     prompt = S.tokens(77, 24, V)
     gtkv, gdkv = engine.allocate_kv_cache(gt, 256), engine.allocate_kv_cache(gd, 256)

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from parity import ids_agree, logits_close
+from parity import ids_agree, logits_close, pair
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K
 
@@ -43,7 +43,7 @@ def model(request, engine):
     print(f"model {request.param}", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
-    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    pair(om, gm)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
     yield request.param, gm, om
     gm.close()
     om.close()
@@ -61,7 +61,8 @@ def test_chunks_match_oracle(engine, model):
     V = gm.dims.n_vocab
     gkv, okv = engine.allocate_kv_cache(gm, 512), O.KvCache(om, 512)
     prompt = S.tokens(70, 40, V)
-    wide = gm.wide_f16  # the 40-column prefill (and the 64-column verify) are wide calls
+    # the 40-column prefill (and the 64-column verify): wide GEMMs, cm1 attention
+    wide = gm.wide_f16 or gm.cm1_attention
     print(f"{name}: prefill 40", flush=True)
     engine.prefill(gm, gkv, prompt, 0)
     O.forward(om, okv, prompt, 0, logits_mode=0)
@@ -105,11 +106,13 @@ def test_batched_verify_matches_oracle(engine, model):
     drafts = [S.tokens(400 + s, n, V) for s, (_, n) in enumerate(seqs)]
     print(f"{name}: batched verify 4 sequences", flush=True)
     out = engine.verify_unified(gm, gk, np.concatenate(drafts), [n for _, n in seqs], want_logits=True)
+    wide = gm.wide_f16 or gm.cm1_attention  # the prefills' f16 roundings
     for s, (p, n) in enumerate(seqs):
-        ol, _ = O.forward(om, ok[s], drafts[s], p)
+        ol, _ = O.forward(om, ok[s], drafts[s], p, batched=True)
         q = int(out.q_starts[s])
-        close(out.logits[q:q + n], ol)
-        assert np.array_equal(out.sampled[q:q + n], ol.argmax(axis=1))
+        close(out.logits[q:q + n], ol, wide)
+        ids_agree(out.logits[q:q + n], ol, wide)
+        assert np.array_equal(out.sampled[q:q + n], out.logits[q:q + n].argmax(axis=1))
         assert gk[s].position == p + n
     for x in gk + ok:
         x.close()
@@ -151,7 +154,7 @@ def test_config4_moe_verify_b8_l7_at_16384(engine):
     print("configs[4] batched verify 8 x 7 at 16384", flush=True)
     out = engine.verify_unified(gm, gk, np.concatenate(toks), [L] * B, want_logits=True)
     for b in range(B):
-        ol, _ = O.forward(om, ok[b], toks[b], P)
+        ol, _ = O.forward(om, ok[b], toks[b], P, batched=True)
         close(out.logits[b * L:(b + 1) * L], ol)
         assert np.array_equal(out.sampled[b * L:(b + 1) * L], ol.argmax(axis=1))
     for x in gk + ok:
@@ -167,7 +170,7 @@ def test_qwen3_06b_draft_shape(engine):
     print("Qwen3-0.6B-shape draft, 2 layers", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
-    om.set_mm16(2 if gm.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
+    wide = pair(om, gm)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
     V = gm.dims.n_vocab
     gkv, okv = engine.allocate_kv_cache(gm, 4200), O.KvCache(om, 4200)
     _seed_kv(gkv, okv, gm.dims, 4096, np.random.default_rng(5))
@@ -176,8 +179,9 @@ def test_qwen3_06b_draft_shape(engine):
         toks = S.tokens(600 + n, n, V)
         gl, _ = engine.forward_full_readback(gm, gkv, toks, pos)
         ol, _ = O.forward(om, okv, toks, pos)
-        close(gl, ol)
-        assert np.array_equal(gl.argmax(axis=1), ol.argmax(axis=1))
+        f16 = wide and n > 1 or pos > 4096  # two-column calls and the K/V they shaped: f16 roundings
+        close(gl, ol, f16)
+        ids_agree(gl, ol, f16)
         pos += n
     for x in (gkv, okv, gm, om):
         x.close()
@@ -190,8 +194,8 @@ def test_spec_step_qwen3_draft_moe_target(engine):
     t_img, d_img = S.GgufImage(QWEN3MOE, seed=7), S.GgufImage(QWEN3, seed=8)
     gt, gd = engine.upload_weights(t_img), engine.upload_weights(d_img)
     ot, od = O.Model(t_img), O.Model(d_img)
-    ot.set_mm16(2 if gt.wide_f16 else 0)  # wide calls: the reference's f16 GEMM arithmetic
-    od.set_mm16(2 if gd.wide_f16 else 0)
+    pair(ot, gt)  # the reference's wide-GEMM and cm1 attention arithmetic where the GPU uses them
+    pair(od, gd)
     V = gt.dims.n_vocab
     prompt = S.tokens(77, 24, V)
     gtkv, gdkv = engine.allocate_kv_cache(gt, 256), engine.allocate_kv_cache(gd, 256)
@@ -211,3 +215,49 @@ def test_spec_step_qwen3_draft_moe_target(engine):
         x.close()
     t_img.close()
     d_img.close()
+
+
+@pytest.mark.timeout(900)
+def test_config4_batched_spec_step_b8_k6_at_16384(engine):
+    """configs[4] as the batch-8 spec decode it is (sh_spec_step_batch, the
+    server's step, server/inference.rs:2777-2924): greedy drafts of the
+    Qwen3-0.6B-shape draft for all 8 sequences (one batched draft forward per
+    position), one batched verify of the Qwen3-30B-A3B-shape MoE target over
+    8 x 7 columns at 16384 cached keys (two layers each, the same synthetic
+    f16 K/V in both sides' caches), per-sequence acceptance and rollback. Three
+    steps equal the oracle's single-sequence greedy steps token for token (its
+    attention set to the batched path's scalar arithmetic), with the same
+    cache positions."""
+    timg, dimg = S.GgufImage(T30B_2L, seed=0), S.GgufImage(D06B_2L, seed=1)
+    print("configs[4] batched spec step: 2-layer target and draft", flush=True)
+    gt, gd = engine.upload_weights(timg), engine.upload_weights(dimg)
+    ot, od = O.Model(timg), O.Model(dimg)
+    for om in (ot, od):
+        om.set_mm16(0)        # 56 / 8 columns on models without the wide path
+        om.set_attn_cm1(False)  # the batched verify's attention: the scalar kernel's arithmetic
+    V, P, B, k = gt.dims.n_vocab, 16384, 8, 6
+    rng = np.random.default_rng(6)
+    gtk, gdk, otk, odk = [], [], [], []
+    for b in range(B):
+        g, o = engine.allocate_kv_cache(gt, P + 32), O.KvCache(ot, P + 32)
+        _seed_kv(g, o, gt.dims, P, rng)
+        gtk.append(g)
+        otk.append(o)
+        g, o = engine.allocate_kv_cache(gd, P + 32), O.KvCache(od, P + 32)
+        _seed_kv(g, o, gd.dims, P, rng)
+        gdk.append(g)
+        odk.append(o)
+    last = [int(t) for t in S.tokens(800, B, V)]
+    for step in range(3):
+        print(f"configs[4] batched spec step {step}", flush=True)
+        em, dr = engine.spec_step_batch(gt, gd, gtk, gdk, last, k)
+        for b in range(B):
+            o_em, o_dr = O.spec_step_greedy(ot, od, otk[b], odk[b], last[b], k)
+            assert dr[b] == o_dr, (step, b, dr[b], o_dr)
+            assert em[b] == o_em, (step, b, em[b], o_em)
+            assert gtk[b].position == otk[b].position == gdk[b].position + len(em[b]) // (k + 1)
+        last = [e[-1] for e in em]
+    for x in gtk + gdk + otk + odk + [gt, gd, ot, od]:
+        x.close()
+    timg.close()
+    dimg.close()

@@ -10,6 +10,10 @@ path; its only checks are closed-form inputs + CPU restatements):
   or_gemv                         numpy f64 matmul of independently dequantized rows
   or_gemv16 / or_forward mm16     numpy f16 casts of the same rows and inputs; the
                                   mm16 numpy Llama (ref_numpy.RefLlama(mm16=True))
+  or_attn_cm1 / forward cm1       closed forms on exactly representable rows (block
+                                  rescale, f16 chunk and output accumulators, the
+                                  f16 rescale factor), staging by numpy's roundings,
+                                  the numpy cm1 Llama (RefLlama(cm1=True))
   or_forward                      independent numpy f64 Llama (ref_numpy.RefLlama),
                                   causal == incremental decode, chain tree == causal,
                                   branch == its own path
@@ -298,6 +302,149 @@ def test_forward_mm16_auto_follows_call_width(small):
     assert np.array_equal(out[2][1], narrow0)
     kv.close()
     m.close()
+
+
+# ------------------------------------------------------- cm1 attention
+
+def _f16(x):
+    return np.asarray(x, np.float16).view(np.uint16)
+
+
+def _cm1_keys(n, hd, s_of_key, v_of_key):
+    """Staged q = e_0 (f16 1.0) and keys whose score is exactly s_of_key[t]
+    (K[t][0] = s), values V[t][0] = v_of_key[t] (other d zero)."""
+    q16 = _f16(np.eye(1, hd, 0, dtype=np.float32)[0])
+    K = np.zeros((n, hd), np.float32)
+    V = np.zeros((n, hd), np.float32)
+    K[:, 0] = s_of_key
+    V[:, 0] = v_of_key
+    return q16, _f16(K), _f16(V)
+
+
+def test_cm1_exact_on_representable_inputs():
+    """Integer scores and small integer values keep every intermediate of the
+    cm1 arithmetic exact (P = 2^(s - m), every f16 sum representable), so the
+    row equals the closed form sum 2^(s_t - M) v_t / sum 2^(s_t - M) bit for
+    bit, through four blocks (the last one partial) whose running maximum
+    rises in block 2: a dropped or reversed rescale, a dropped chunk or key, or
+    a wrong normalisation changes the result."""
+    rng = np.random.default_rng(3)
+    n, hd = 200, 64
+    s = rng.integers(0, 3, n).astype(np.float32)
+    s[140] = 4.0  # the maximum arrives in block 2
+    v = rng.integers(-2, 3, n).astype(np.float32)
+    q16, K, V = _cm1_keys(n, hd, s, v)
+    out = O.attn_cm1(q16, K, V, staged=True)
+    w = np.exp2(s.astype(np.float64) - 4.0)
+    num, den = float(np.sum(w * v)), float(np.sum(w))
+    assert out[0] == np.float32(num) * (np.float32(1.0) / np.float32(den))
+    assert np.all(out[1:] == 0)
+    # keys marked invisible drop out exactly (here: every key with s == 1)
+    vis = s != 1
+    out2 = O.attn_cm1(q16, K, V, visible=vis.astype(np.uint8), staged=True)
+    num2, den2 = float(np.sum((w * v)[vis])), float(np.sum(w[vis]))
+    assert out2[0] == np.float32(num2) * (np.float32(1.0) / np.float32(den2))
+
+
+def test_cm1_f16_accumulators_round():
+    """The P V chunk accumulator and the running output are f16 (the reference's
+    f16-accumulating MMA and f16 output registers): with all scores 0 (P = 1),
+    a block whose chunks add 2048 + 1 + 1 + 3 keeps 2052 (f16 spacing 2 above
+    2048, ties to even), and 2048 followed by blocks adding 1 each stays 2048;
+    an f32 accumulator would give 2053 and 2050."""
+    hd = 64
+    v = np.zeros(64, np.float32)
+    v[0], v[16], v[32], v[48] = 2048, 1, 1, 3
+    q16, K, V = _cm1_keys(64, hd, np.zeros(64, np.float32), v)
+    out = O.attn_cm1(q16, K, V, staged=True)
+    assert out[0] == np.float32(2052.0) * (np.float32(1.0) / np.float32(64.0))
+    v = np.zeros(192, np.float32)
+    v[0], v[64], v[128] = 2048, 1, 1
+    q16, K, V = _cm1_keys(192, hd, np.zeros(192, np.float32), v)
+    out = O.attn_cm1(q16, K, V, staged=True)
+    assert out[0] == np.float32(2048.0) * (np.float32(1.0) / np.float32(192.0))
+
+
+def test_cm1_rescale_factor_is_f16():
+    """A running maximum that rises by 0.5 rescales the f16 output by
+    f16(2^-0.5) = 0.70703125 (flash_attn_cm1.slang casts the factor to f16),
+    not by 0.70710678."""
+    hd = 64
+    s = np.zeros(128, np.float32)
+    s[64] = 0.5
+    v = np.zeros(128, np.float32)
+    v[0] = 1.0
+    q16, K, V = _cm1_keys(128, hd, s, v)
+    out = O.attn_cm1(q16, K, V, staged=True)
+    e = np.float32(2.0 ** -0.5)
+    L = 64.0 * float(e) + 1.0 + 63.0 * float(e)  # block 0 rescaled, block 1: one key at the max
+    assert abs(float(out[0]) * L - 0.70703125) < 2e-7
+    assert abs(float(out[0]) * L - 2.0 ** -0.5) > 5e-5
+
+
+def test_cm1_staging_and_distance_from_exact():
+    """or_attn_cm1 stages q as f16(q * f32(f32(1/sqrt(hd)) * f32(log2 e)))
+    (numpy's own roundings here) and then equals or_attn_cm1_core; on random
+    rows it sits within 1e-2 of the exact softmax attention of its relative
+    scale, and away from it."""
+    rng = np.random.default_rng(5)
+    for hd, n in ((64, 70), (128, 300)):
+        K = rng.normal(0, 1, (n, hd)).astype(np.float16)
+        V = rng.normal(0, 1, (n, hd)).astype(np.float16)
+        q = rng.normal(0, 0.5, hd).astype(np.float32)
+        qs = np.float32(np.float32(1.0) / np.sqrt(np.float32(hd))) * np.float32(1.4426950408889634)
+        q16 = (q * qs).astype(np.float16).view(np.uint16)
+        a = O.attn_cm1(q, K.view(np.uint16), V.view(np.uint16))
+        b = O.attn_cm1(q16, K.view(np.uint16), V.view(np.uint16), staged=True)
+        assert np.array_equal(a, b)
+        sc = K.astype(np.float64) @ q.astype(np.float64) / np.sqrt(hd)
+        p = np.exp(sc - sc.max())
+        ex = p @ V.astype(np.float64) / p.sum()
+        d = np.abs(a - ex).max() / np.abs(ex).max()
+        assert 1e-6 < d < 1e-2, d
+
+
+def test_forward_cm1_matches_numpy(small):
+    """or_forward with cm1 attention against the numpy Llama doing the same
+    roundings (ref_numpy.attn_cm1), and away from the exact forward. The two
+    sides store f32 values that differ in their last bits (and ~1 % of their
+    f16 K/V entries by one ulp), and the f16 steps turn some of those into
+    2^-11 flips: over 70 keys (two 64-key blocks) they agree to ~1.4e-4 of the
+    logit scale while each sits 3-4e-4 from the exact forward. A one-column
+    call and a tree call are unchanged by the switch."""
+    ref = R.RefLlama(bytes(small.bytes()), cm1=True)
+    m = O.Model(small)
+    m.set_attn_cm1(True)
+    kv = O.KvCache(m, 96)
+    toks = S.tokens(5, 70, m.V)
+    lg, res = O.forward(m, kv, toks, 0)
+    rl, rr = ref.forward(toks)
+    m.set_attn_cm1(False)
+    kv0 = O.KvCache(m, 96)
+    lg0, _ = O.forward(m, kv0, toks, 0)
+    sc = np.abs(rl).max()
+    err, dist = np.abs(lg - rl).max() / sc, np.abs(lg0 - lg).max() / sc
+    assert err <= 2.5e-4 and dist >= 2.5e-4 and err <= 0.5 * dist, (err, dist)
+    np.testing.assert_allclose(res, rr, rtol=1e-3, atol=5e-4 * np.abs(rr).max())
+    # 12 keys (one block, no flips from the KV yet): much closer than to exact
+    kv1, kv2 = O.KvCache(m, 96), O.KvCache(m, 96)
+    ref1 = R.RefLlama(bytes(small.bytes()), cm1=True)
+    m.set_attn_cm1(True)
+    a, _ = O.forward(m, kv1, toks[:12], 0)
+    b, _ = ref1.forward(toks[:12])
+    m.set_attn_cm1(False)
+    c, _ = O.forward(m, kv2, toks[:12], 0)
+    assert np.abs(a - b).max() <= 0.1 * np.abs(a - c).max()
+    kv1.close(); kv2.close()
+    # one column / a tree: the exact softmax whatever the switch
+    one = {}
+    for on in (False, True):
+        m.set_attn_cm1(on)
+        kv0.set_position(70)
+        one[on] = (O.forward(m, kv0, S.tokens(6, 1, m.V), 70)[0],
+                   O.forward(m, kv0, S.tokens(7, 3, m.V), 71, parents=[-1, 0, 0])[0])
+    assert np.array_equal(one[False][0], one[True][0]) and np.array_equal(one[False][1], one[True][1])
+    kv.close(); kv0.close(); m.close()
 
 
 def test_forward_incremental_equals_batch(small):
