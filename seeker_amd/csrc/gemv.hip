@@ -2759,7 +2759,8 @@ static bool use16h(const QMat& w, bool one_split, uint32_t N) {
 }
 
 size_t sh_gemm16_part_floats(const QMat& w) {
-  if (w.type != GGML_Q4_K || w.K % 256) return 0;
+  if (w.type != GGML_Q4_K) return sh_gemm16x_part_floats(w);
+  if (w.K % 256) return 0;
   size_t cols = (size_t)plan16(w, false).KS * SH_MAX_COLS;  // split-columns of the widest partial set
   for (uint32_t N = SH_MAX_COLS + 1; N <= SH_MAX_COLS16; ++N)
     cols = std::max({cols, (size_t)plan16w(w, false, N).KS * ((N + 7) / 8 * 8),
@@ -2822,6 +2823,7 @@ static void dispatch16(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t
 
 int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, EpiKind epi,
                      const EpiArgs& ea, const char* tag, uint32_t* nparts) {
+  if (w.type != GGML_Q4_K) return sh_gemm16x_launch(e, w, bh, ldb, N, epi, ea, tag, nparts);  // gemm16x.hip
   SH_CHECK(N >= 1 && N <= SH_MAX_COLS16, SH_ERR_ARG, "f16 gemm N=%u outside [1, %u]", N, SH_MAX_COLS16);
   SH_CHECK(w.type == GGML_Q4_K && w.K % 256 == 0 && ldb >= w.K && ldb % 8 == 0, SH_ERR_UNSUPPORTED,
            "f16 gemm needs Q4_K (type %d) and an operand of at least K = %u halves per column (ldb %u)", w.type, w.K,

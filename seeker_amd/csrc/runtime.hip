@@ -361,10 +361,13 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
               (lt == GGML_Q4_K || lt == GGML_Q8_0);
     m->fused_ok = fused;
     if (!ok && !fused) FAIL(SH_ERR_UNSUPPORTED, "weight types: neither all K-quants nor uniform Q4_K / Q8_0 layers");
-    bool w16 = m->n_expert == 0 && m->lm_head.type == GGML_Q4_K;
+    // wide f16 GEMMs: every dense matrix (the routed experts keep the
+    // reference's f32 expert path) in a format the f16 GEMMs take
+    auto g16 = [](const QMat& q) { return q.type == GGML_Q4_K ? q.K % 256 == 0 : sh_gemm16x_ok(q); };
+    bool w16 = g16(m->lm_head);
     for (const Layer& L : m->layers)
-      w16 = w16 && !L.wv.d && L.wqkv.type == GGML_Q4_K && L.wo.type == GGML_Q4_K && L.wgu.type == GGML_Q4_K &&
-            L.wdown.type == GGML_Q4_K;
+      w16 = w16 && g16(L.wqkv) && (!L.wv.d || g16(L.wv)) && g16(L.wo) &&
+            (m->n_expert ? true : g16(L.wgu) && g16(L.wdown));
     m->wide16_ok = w16;
     const char* env16 = getenv("SH_WIDE_F16");
     m->wide16 = w16 && !(env16 && atoi(env16) == 0);
@@ -1030,6 +1033,13 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     pending_ld = po.ldo;
     if ((rc = resid_prep(L.ffn_norm))) return rc;
     if (m->n_expert) {  // routed experts add into the residual themselves
+      if (f16) {
+        // the experts take the f32-level operand (the reference's expert
+        // matvec is not its wide GEMM): built from the updated residual
+        PrepArgs px = pr;
+        px.bh = nullptr; px.mode = PREP_RESID; px.x = w.resid; px.K = m->d; px.norm_w = L.ffn_norm; px.nparts = 0;
+        if ((rc = sh_prep_launch(e, px))) return rc;
+      }
       if ((rc = moe_ffn(m, L, nc))) return rc;
       continue;
     }
@@ -2053,8 +2063,9 @@ extern "C" int sh_gemm_wide16(sh_engine* e, const sh_qtensor* w, const float* x_
                               int accumulate) {
   SH_CHECK(e && w && x_dev && y_dev, SH_ERR_ARG, "sh_gemm_wide16: NULL argument");
   SH_CHECK(N >= 1, SH_ERR_ARG, "N must be >= 1");
-  SH_CHECK(w->m.type == GGML_Q4_K && w->m.K % 256 == 0, SH_ERR_UNSUPPORTED,
-           "sh_gemm_wide16: Q4_K with K a multiple of 256 (type %d)", w->m.type);
+  SH_CHECK((w->m.type == GGML_Q4_K && w->m.K % 256 == 0) || sh_gemm16x_ok(w->m), SH_ERR_UNSUPPORTED,
+           "sh_gemm_wide16: Q4_K, Q5_K, Q6_K (K a multiple of 256) or Q8_0 (of 32); type %d, K %u", w->m.type,
+           w->m.K);
   const uint32_t K = w->m.K, M = w->m.M, CW = SH_MAX_COLS16;
   const size_t part_floats = sh_gemm16_part_floats(w->m);
   uint16_t* bh = nullptr;

@@ -353,13 +353,20 @@ int sh_gemm_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
                    EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
 size_t sh_gemm_part_floats(const QMat& w);  // for SH_MAX_COLS columns
 // y = W x with the reference's wide-GEMM arithmetic (f16 weights and
-// activations, f32 accumulation) for N <= SH_MAX_COLS columns of f16 rows
-// bh[col * ldb + k] (k_prep16_*), W Q4_K: EPI_PART (partials as
-// sh_gemm_launch's; *nparts = splits) or EPI_STORE (out[col][row]).
+// activations, f32 accumulation) for N <= SH_MAX_COLS16 columns of f16 rows
+// bh[col * ldb + k] (k_prep16_*), W Q4_K, Q5_K, Q6_K or Q8_0: EPI_PART
+// (partials as sh_gemm_launch's; *nparts = splits) or EPI_STORE (out[col][row]).
 int sh_gemm16_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, EpiKind epi,
                      const EpiArgs& ea, const char* tag, uint32_t* nparts = nullptr);
 // Partial floats sh_gemm16_launch's EPI_PART needs for up to SH_MAX_COLS16 columns.
 size_t sh_gemm16_part_floats(const QMat& w);
+// The same arithmetic for Q8_0, Q5_K and Q6_K weights (gemm16x.hip), which
+// sh_gemm16_launch hands these types to: whether w takes it, its partial
+// floats, the launch.
+bool sh_gemm16x_ok(const QMat& w);
+size_t sh_gemm16x_part_floats(const QMat& w);
+int sh_gemm16x_launch(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, EpiKind epi,
+                      const EpiArgs& ea, const char* tag, uint32_t* nparts);
 // Fused QKV rows from sh_gemm_launch partials: RoPE, q out, K/V into each
 // column's cache slot.
 struct QkvColDev {  // one column of a device-resident column table

@@ -52,7 +52,9 @@ def ids_agree(gpu, ref, wide=False, err=None):
     rows = np.arange(ref.shape[0])
     margin = ref[rows, ra] - ref[rows, ga]
     assert all(margin[i] <= tie for i in bad), (bad, margin[bad], tie)
-    assert len(bad) <= max(1, ref.shape[0] // 50), (len(bad), ref.shape[0])
+    # f16 operands widen the near-tie band, so wide calls may flip twice as many
+    limit = max(2, ref.shape[0] // 25) if wide else max(1, ref.shape[0] // 50)
+    assert len(bad) <= limit, (len(bad), ref.shape[0])
     return int(len(bad))
 
 

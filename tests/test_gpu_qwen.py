@@ -141,7 +141,11 @@ def test_config4_moe_verify_b8_l7_at_16384(engine):
     print("configs[4] 2-layer Qwen3-30B-A3B shape", flush=True)
     gm = engine.upload_weights(img)
     om = O.Model(img)
-    assert not gm.wide_f16  # routed experts keep the f32-level path
+    # the batch of 56 columns is one wide call: its dense matmuls take the
+    # wide GEMM's f16 operands (the routed experts keep the f32-level path);
+    # the oracle's per-sequence calls of 7 columns then need mode 1
+    wide = gm.wide_f16
+    om.set_mm16(1 if wide else 0)
     V, P, B, L = gm.dims.n_vocab, 16384, 8, 7
     rng = np.random.default_rng(4)
     gk, ok = [], []
@@ -155,8 +159,9 @@ def test_config4_moe_verify_b8_l7_at_16384(engine):
     out = engine.verify_unified(gm, gk, np.concatenate(toks), [L] * B, want_logits=True)
     for b in range(B):
         ol, _ = O.forward(om, ok[b], toks[b], P, batched=True)
-        close(out.logits[b * L:(b + 1) * L], ol)
-        assert np.array_equal(out.sampled[b * L:(b + 1) * L], ol.argmax(axis=1))
+        close(out.logits[b * L:(b + 1) * L], ol, wide)
+        ids_agree(out.logits[b * L:(b + 1) * L], ol, wide)
+        assert np.array_equal(out.sampled[b * L:(b + 1) * L], out.logits[b * L:(b + 1) * L].argmax(axis=1))
     for x in gk + ok:
         x.close()
     gm.close()
@@ -224,16 +229,18 @@ def test_config4_batched_spec_step_b8_k6_at_16384(engine):
     Qwen3-0.6B-shape draft for all 8 sequences (one batched draft forward per
     position), one batched verify of the Qwen3-30B-A3B-shape MoE target over
     8 x 7 columns at 16384 cached keys (two layers each, the same synthetic
-    f16 K/V in both sides' caches), per-sequence acceptance and rollback. Three
-    steps equal the oracle's single-sequence greedy steps token for token (its
-    attention set to the batched path's scalar arithmetic), with the same
+    f16 K/V in both sides' caches; a wide call: f16 dense matmuls), per-sequence
+    acceptance and rollback. Three steps equal the oracle's single-sequence
+    greedy steps token for token (its attention set to the batched path's
+    scalar arithmetic, its target matmuls to the wide GEMM's), with the same
     cache positions."""
     timg, dimg = S.GgufImage(T30B_2L, seed=0), S.GgufImage(D06B_2L, seed=1)
     print("configs[4] batched spec step: 2-layer target and draft", flush=True)
     gt, gd = engine.upload_weights(timg), engine.upload_weights(dimg)
     ot, od = O.Model(timg), O.Model(dimg)
+    ot.set_mm16(1 if gt.wide_f16 else 0)  # every target call is the 56-column batched verify: a wide call
+    od.set_mm16(0)  # the batched draft forwards: 8 (first position: up to 16) columns
     for om in (ot, od):
-        om.set_mm16(0)        # 56 / 8 columns on models without the wide path
         om.set_attn_cm1(False)  # the batched verify's attention: the scalar kernel's arithmetic
     V, P, B, k = gt.dims.n_vocab, 16384, 8, 6
     rng = np.random.default_rng(6)

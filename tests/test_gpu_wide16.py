@@ -17,7 +17,7 @@ import pytest
 import oracle as O
 from seeker_amd import QTensor
 from seeker_amd import synth as S
-from seeker_amd._native import GGML_Q4_K, GGML_Q8_0
+from seeker_amd._native import GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_Q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -66,11 +66,28 @@ def test_wide16_8b_shapes(engine, M, K, N):
     assert np.array_equal(got.argmax(axis=1), ref.argmax(axis=1))
 
 
-def test_wide16_refuses_other_types(engine):
-    from seeker_amd import SeekerError
-    w = S.quantize(GGML_Q8_0, S.normal_f32(1, 1, 64 * 256, 0.0, 0.02))
-    qt = QTensor(engine, GGML_Q8_0, w, 64, 256)
-    xd, yd = engine.to_device(np.ones((32, 256), np.float32)), engine.to_device(np.zeros((32, 64), np.float32))
-    with pytest.raises(SeekerError):
-        engine.gemm_wide16(qt, xd, 32, yd)
+@pytest.mark.parametrize("qtype", [GGML_Q8_0, GGML_Q5_K, GGML_Q6_K], ids=["q8_0", "q5k", "q6k"])
+@pytest.mark.parametrize("M,K,N", [(80, 512, 32), (37, 1536, 70), (512, 1408, 45), (4000, 512, 192)])
+def test_wide16_other_formats(engine, qtype, M, K, N):
+    """The reference's wide GEMM has Q8_0, Q5_K and Q6_K variants too
+    (mmcm_variant, ops/matmul.rs:238-290): f16(f32 dequant) weights in the
+    oracle's order of f32 operations, so only the summation order differs from
+    or_gemv16."""
+    if qtype != GGML_Q8_0 and K % 256:
+        K = K // 256 * 256
+    print(f"wide16 {qtype} M={M} K={K} N={N}", flush=True)
+    w = S.quantize(qtype, S.normal_f32(M + K, 2, M * K, 0.0, 0.02))
+    rng = np.random.default_rng(N)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    qt = QTensor(engine, qtype, w, M, K)
+    xd, yd = engine.to_device(x), engine.to_device(np.zeros((N, M), np.float32))
+    engine.gemm_wide16(qt, xd, N, yd, False)
+    got = yd.read(np.float32, N * M).reshape(N, M)
+    ref = O.gemv16(qtype, w, M, K, x)
+    exact = O.gemv(qtype, w, M, K, x)
     xd.free(); yd.free(); qt.close()
+    scale = np.abs(ref).max()
+    err, dex = np.abs(got - ref).max() / scale, np.abs(got - exact).max() / scale
+    print(f"  vs or_gemv16 {err:.2e}, vs exact {dex:.2e}", flush=True)
+    assert err < 1e-5, err
+    assert dex > 4 * err
