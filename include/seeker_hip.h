@@ -96,6 +96,10 @@ int sh_engine_sync(sh_engine* e);
 int sh_engine_set_profiling(sh_engine* e, int on);
 int sh_engine_profile(sh_engine* e, sh_kernel_stat* out, uint32_t cap, uint32_t* n_out);
 int sh_engine_profile_reset(sh_engine* e);
+/* Graph replay counters: graphs captured and graph launches so far (the
+ * reference's replay cache, inference/mod.rs:88-103, 988-1180, has the same
+ * record-once / replay-per-step split). Diagnostic; no compute. */
+int sh_engine_graph_stats(sh_engine* e, uint64_t* captures, uint64_t* launches);
 
 /* Device buffers (plain HBM allocations for kernel-level entry points). */
 int sh_dev_alloc(sh_engine* e, uint64_t bytes, void** out_dev);
@@ -226,7 +230,11 @@ int sh_verify_unified_sampled(sh_engine* e, sh_model* m, sh_kv* const* caches, u
  *    from max(0, p - q) with word 2i+1 (bonus from p_n).
  * Stochastic uniform words come from Philox key (seed, 0x5EC) at s->counter +
  * word, and the step advances s->counter by 3n + 2; with s->uniforms they are
- * uniforms[word], an array of 3n + 2 floats. */
+ * uniforms[word], an array of 3n + 2 floats.
+ * Every mode replays one captured HIP graph per (models, caches, n, pending
+ * count, sampling parameters): positions, the Philox key and the word base are
+ * device words written before each replay (the reference's single-submit
+ * step with DecodeDyn patching, inference/mod.rs:2181-2231, decode_dyn.rs). */
 int sh_spec_step(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh_kv* dkv,
                  uint32_t last_token, uint32_t n_max, sh_sampling* s, uint32_t* emitted_out,
                  uint32_t* n_emitted, uint32_t* drafts_out);
@@ -235,7 +243,8 @@ int sh_spec_step(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh
  * the draft cache dkv (its pending tokens first, as sh_spec_step leaves them),
  * each argmax feeding the next position on the device; drafts_out [n]. The
  * cache advances by its pending count + n (d_n is not fed) and its pending
- * tokens are cleared: truncate it to the accepted length afterwards. */
+ * tokens are cleared: truncate it to the accepted length afterwards. Replays
+ * one captured HIP graph per (model, cache, n, pending count). */
 int sh_draft_tokens(sh_engine* e, sh_model* draft, sh_kv* dkv, uint32_t last_token, uint32_t n_max,
                     uint32_t* drafts_out);
 /* The reference server's batched speculative step (server/inference.rs:

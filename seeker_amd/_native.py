@@ -101,6 +101,7 @@ SIGNATURES = {
     "sh_engine_set_profiling": (C.c_int, [P, C.c_int]),
     "sh_engine_profile": (C.c_int, [P, C.POINTER(sh_kernel_stat), C.c_uint32, U32P]),
     "sh_engine_profile_reset": (C.c_int, [P]),
+    "sh_engine_graph_stats": (C.c_int, [P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "sh_dev_alloc": (C.c_int, [P, C.c_uint64, C.POINTER(P)]),
     "sh_dev_free": (C.c_int, [P, P]),
     "sh_memcpy_h2d": (C.c_int, [P, P, P, C.c_uint64]),

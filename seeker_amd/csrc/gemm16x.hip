@@ -62,7 +62,6 @@ __device__ __forceinline__ uint32_t nib_word(const uint8_t* b, int lane, uint32_
 // Q8_0 tile-block (544 B): 64 lanes x 8 int8 (row l % 16, k = 8 g + t), then
 // the rows' f16 d.
 struct W8 {
-  static constexpr uint32_t kType = GGML_Q8_0;
   static __device__ __forceinline__ h8 frag(const uint8_t* Wp, uint32_t tile, uint32_t nunits, uint32_t u, int lane,
                                             int g, int r) {
     const uint8_t* b = Wp + ((size_t)tile * nunits + u) * SH_Q8_TILE_BYTES;
@@ -80,7 +79,6 @@ struct W8 {
 // Q5_K tile-superblock (2816 B, see k_repack_q5k): low nibbles as Q4_K, two
 // high-bit words per lane, d | dmin << 16 and the 12 scale bytes per row.
 struct W5 {
-  static constexpr uint32_t kType = GGML_Q5_K;
   static __device__ __forceinline__ h8 frag(const uint8_t* Wp, uint32_t tile, uint32_t nunits, uint32_t u, int lane,
                                             int g, int r) {
     const uint32_t nsb = nunits / 8, sb = u >> 3, m = u & 7;
@@ -105,7 +103,6 @@ struct W5 {
 // layout, four high-bit words per lane, 16 int8 scales per row (even indices,
 // then odd), the rows' f16 d.
 struct W6 {
-  static constexpr uint32_t kType = GGML_Q6_K;
   static __device__ __forceinline__ h8 frag(const uint8_t* Wp, uint32_t tile, uint32_t nunits, uint32_t u, int lane,
                                             int g, int r) {
     const uint32_t nsb = nunits / 8, sb = u >> 3, m = u & 7;
@@ -141,7 +138,6 @@ __global__ __launch_bounds__(512) void k_gemm16x(const uint8_t* __restrict__ Wp,
   const uint16_t* brow[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) brow[c] = Bh + (size_t)min(16 * c + (uint32_t)r, N - 1) * ldb + 8 * g;
-#pragma unroll 4
   for (uint32_t u = u0; u < u1; ++u) {
     const h8 a = F::frag(Wp, tt, nunits, u, lane, g, r);
 #pragma unroll

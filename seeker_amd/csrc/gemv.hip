@@ -1879,7 +1879,8 @@ __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ par
     const QkvColDev t = qc.tab[col];
     qkv_store4(ea, r0, v, t.pos, t.slot, t.mseq, t.kc, t.vc, ea.out + (size_t)col * ea.Dq);
   } else {
-    qkv_store4(ea, r0, v, qc.pos[col], qc.slot[col], qc.mseq[col], qc.kc[col], qc.vc[col],
+    const uint32_t b0 = ea.dbase ? *ea.dbase : 0u;  // graph replay: offsets from the device base
+    qkv_store4(ea, r0, v, qc.pos[col] + (int32_t)b0, qc.slot[col] + b0, qc.mseq[col], qc.kc[col], qc.vc[col],
                ea.out + (size_t)col * ea.Dq);
   }
 }
@@ -1917,8 +1918,9 @@ __global__ __launch_bounds__(128) void k_qkv_finish_head(const float* __restrict
     for (uint32_t j = 0; j < 8; ++j)
       if (k0 + j < nparts) v += t[j];
   }
-  const int32_t pos = qc.pos[col];
-  const uint32_t slot = qc.slot[col], ms = qc.mseq[col];
+  const uint32_t b0 = ea.dbase ? *ea.dbase : 0u;  // graph replay: offsets from the device base
+  const int32_t pos = qc.pos[col] + (int32_t)b0;
+  const uint32_t slot = qc.slot[col] + b0, ms = qc.mseq[col];
   if (kind == 2) {
     uint16_t* vb = qc.vc[col] + (((size_t)ea.layer * nkv + hh) * (ms / 32) + slot / 32) * hd * 32;
     vb[(size_t)i * 32 + v_slot(slot & 31)] = f2h_bits(v);
@@ -2855,6 +2857,7 @@ int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_
                          uint32_t N, const EpiArgs& ea, const QkvCols& qc) {
   SH_CHECK(N >= 1 && N <= (qc.tab ? (uint32_t)SH_MAX_COLS16 : (uint32_t)SH_MAX_COLS) && ea.hd % 4 == 0, SH_ERR_ARG,
            "qkv finish shape");
+  SH_CHECK(!(qc.tab && ea.dbase), SH_ERR_ARG, "qkv finish: a device column table has no graph base");
   const uint32_t rows = ea.Dq + 2 * ea.Dkv;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);

@@ -164,6 +164,7 @@ extern "C" int sh_engine_profile_reset(sh_engine* e) {
 int sh_engine_scratch(sh_engine* e, int slot, size_t bytes, void** out) {
   SH_CHECK(slot >= 0 && slot < 4, SH_ERR_ARG, "scratch slot %d", slot);
   if (bytes > e->scr_bytes[slot]) {
+    g_graph_gen.fetch_add(1);  // captured graphs may point into the old block
     SH_HIP(hipStreamSynchronize(e->stream));
     if (e->scr[slot]) SH_HIP(hipFree(e->scr[slot]));
     e->scr[slot] = nullptr;
@@ -917,6 +918,7 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
   };
   EpiArgs qkv;
   qkv.out = w.q; qkv.Dq = m->q_dim; qkv.Dkv = m->hd * m->n_kv; qkv.hd = m->hd; qkv.n_kv = m->n_kv; qkv.rope = m->rope;
+  qkv.dbase = cols[0].kv->graph_base;  // graph capture: one cache per forward
   // The QKV finish takes its column table as a kernel argument, in pieces of at
   // most SH_MAX_COLS columns; a wider chunk of a non-NEOX model uploads the
   // table once (w.qtab, read by every layer) and finishes in one launch.
@@ -980,8 +982,12 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
   SH_CHECK(!cm1 || (segs.front().col0 == 0 && segs.back().col0 + segs.back().ncol == nc), SH_ERR_ARG,
            "cm1 attention: the segments must cover the chunk");
   FabGuard fab{e, FabLaunch{}};
-  bool use_fab = !cm1 && fab_enabled();
+  // one sequence's chain of at most 8 columns (the draft's forwards, graph
+  // captures) takes the split attention with its masks as kernel arguments
+  const bool single8 = segs.size() == 1 && segs[0].ncol <= 8;
+  bool use_fab = !cm1 && fab_enabled() && !single8;
   for (const FaSeg& sg : segs) use_fab = use_fab && sg.hmasks;
+  SH_CHECK(!qkv.dbase || cm1 || single8, SH_ERR_UNSUPPORTED, "graph capture: one chain of at most 8 columns");
   SH_CHECK(cm1 || use_fab || nc <= SH_MAX_COLS, SH_ERR_UNSUPPORTED,
            "chunks of more than %u columns need the batched attention (device masks)", SH_MAX_COLS);
   if (use_fab && (rc = plan_fab(m, segs, nc, &fab))) return rc;
@@ -1020,6 +1026,8 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
         fa.layer = l; fa.N = sg.ncol; fa.kvlen = sg.kvlen; fa.mask_base = sg.mask_base; fa.col0 = sg.col0;
         for (uint32_t j = 0; j < sg.ncol && j < 8; ++j) fa.colmask[j] = sg.colmask[j];
         fa.masks = sg.masks;
+        fa.dbase = sg.kv->graph_base;
+        fa.kv_cap = sg.kv->max_seq;
         if ((rc = sh_fa_launch(e, m, sg.kv, fa, w.q, w.fa_part, w.attn, w.bx, w.xs, w.cs))) return rc;
       }
       if (f16) {  // the attention rows as the Wo operand
@@ -1069,6 +1077,13 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
 // Columns per forward chunk: SH_MAX_COLS when the multi-group path applies
 // (all matrices K-quants) and takes the chunk (more than 8 columns, or a model
 // the fused path cannot run), else 8.
+static uint32_t chunk_cols(const sh_model* m, uint32_t n);
+
+// Models whose forwards of up to 8 columns a HIP graph can capture: the fused
+// path and the multi-group path (neither does host work between launches for
+// such a chain).
+static bool graph_model_ok(const sh_model* m) { return m->fused_ok || m->mg_ok; }
+
 static uint32_t chunk_cols(const sh_model* m, uint32_t n) {
   static const bool forced8 = [] {
     const char* s = getenv("SH_CHUNK");
@@ -1177,8 +1192,8 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
   const bool graph = kv->graph_base != nullptr;  // pos is an offset from *graph_base at replay
   SH_CHECK(graph || kv->pos == pos, SH_ERR_STATE,
            "cache.position %u doesn't match caller-supplied position_offset %u", kv->pos, pos);
-  SH_CHECK(!graph || (L <= 8 && !parents && m->fused_ok), SH_ERR_UNSUPPORTED,
-           "graph capture: chains of at most 8 columns on the fused (uniform Q4_K / Q8_0 llama) path");
+  SH_CHECK(!graph || (L <= 8 && !parents && graph_model_ok(m)), SH_ERR_UNSUPPORTED,
+           "graph capture: chains of at most 8 columns");
   SH_CHECK(kv->n_layer == m->n_layer && kv->n_kv == m->n_kv && kv->hd == m->hd, SH_ERR_ARG,
            "KV cache dims do not match the model");
   SH_CHECK((uint64_t)pos + L <= kv->max_seq, SH_ERR_CAPACITY, "positions [%u, %u) exceed KV capacity %u", pos,
@@ -1221,7 +1236,7 @@ static int forward_dev(sh_model* m, sh_kv* kv, const uint32_t* dev_tokens, uint3
     chunk_segs.push_back(segs);
   }
   uint64_t* dmask = nullptr;
-  if (CW > 8 && !m->call_cm1) {
+  if (CW > 8 && !m->call_cm1 && L > 8) {  // <= 8 columns: one segment, masks as kernel arguments
     SH_HIP(hipMallocAsync((void**)&dmask, (size_t)L * 8, e->stream));
     SH_HIP(hipMemcpyAsync(dmask, hmask.data(), (size_t)L * 8, hipMemcpyHostToDevice, e->stream));
     for (size_t c = 0; c < chunk_segs.size(); ++c)
@@ -1297,6 +1312,7 @@ static hipGraphExec_t graph_find(sh_engine* e, const std::vector<uintptr_t>& key
 static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const std::vector<sh_kv*>& kvs,
                          const std::vector<const uint32_t*>& bases, const std::function<int()>& body,
                          hipGraphExec_t* out);
+static int graph_launch(sh_engine* e, hipGraphExec_t ex);
 
 // Greedy verify of up to 8 tokens by graph replay: tokens staged at tok[32..],
 // ids at samp[0..], base position at base[2].
@@ -1327,7 +1343,7 @@ static int verify_greedy_graph(sh_engine* e, sh_model* m, sh_kv* kv, const uint3
   }
   SH_HIP(hipMemcpyAsync(e->spec.tok + 32, hp + 32, (size_t)L * 4, hipMemcpyHostToDevice, e->stream));
   SH_HIP(hipMemcpyAsync(e->spec.base + 2, hp + 66, 4, hipMemcpyHostToDevice, e->stream));
-  SH_HIP(hipGraphLaunch(ex, e->stream));
+  if ((rc = graph_launch(e, ex))) return rc;
   SH_HIP(hipStreamSynchronize(e->stream));
   for (uint32_t i = 0; i < L; ++i) sampled_out[i] = hp[48 + i];
   kv->pos = pos + L;
@@ -1339,7 +1355,7 @@ extern "C" int sh_verify_greedy(sh_engine* e, sh_model* m, sh_kv* kv, const uint
                                 uint32_t pos, uint32_t* sampled_out) {
   SH_CHECK(e && m && kv && sampled_out, SH_ERR_ARG, "sh_verify_greedy: NULL argument");
   SH_CHECK(L >= 1 && L <= 64, SH_ERR_ARG, "verify length %u outside [1, 64]", L);
-  if (L <= 8 && graphs_enabled(e) && m->fused_ok) {
+  if (L <= 8 && graphs_enabled(e) && graph_model_ok(m)) {
     SH_CHECK(tokens, SH_ERR_ARG, "tokens is NULL");
     for (uint32_t i = 0; i < L; ++i)
       SH_CHECK(tokens[i] < m->V, SH_ERR_ARG, "token id %u out of range (vocab %u)", tokens[i], m->V);
@@ -1630,7 +1646,8 @@ static int spec_bufs(sh_engine* e, uint32_t V) {
   }
   SH_HIP(hipMalloc(&sb.tok, 64 * 4));
   SH_HIP(hipMalloc(&sb.samp, 16 * 4));
-  SH_HIP(hipMalloc(&sb.base, 4 * 4));
+  SH_HIP(hipMalloc(&sb.base, 8 * 4));
+  sb.rng = reinterpret_cast<uint64_t*>(sb.base + 4);
   SH_HIP(hipMalloc(&sb.dlogits, (size_t)8 * V * 4));
   SH_HIP(hipMalloc(&sb.tlogits, (size_t)9 * V * 4));
   SH_HIP(hipMalloc(&sb.udev, 32 * 4));
@@ -1699,17 +1716,34 @@ static int graph_capture(sh_engine* e, const std::vector<uintptr_t>& key, const 
   ge.key = key;
   ge.exec = ex;
   e->graphs.push_back(ge);
+  ++e->graph_captures;
   *out = ex;
   return SH_OK;
 }
 
-// Draft n tokens greedily and verify [last, d_1..d_n] (greedy): draft forwards
-// at dpos (catch-up of np + 1 tokens) and dpos + np + i, the verify at tpos;
-// drafts and per-column argmax ids are copied to the pinned staging buffer.
-static int enqueue_greedy_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t n,
-                               uint32_t np, uint32_t dpos, uint32_t tpos) {
+static int graph_launch(sh_engine* e, hipGraphExec_t ex) {
+  SH_HIP(hipGraphLaunch(ex, e->stream));
+  ++e->graph_launches;
+  return SH_OK;
+}
+
+extern "C" int sh_engine_graph_stats(sh_engine* e, uint64_t* captures, uint64_t* launches) {
+  SH_CHECK(e && captures && launches, SH_ERR_ARG, "sh_engine_graph_stats: NULL argument");
+  *captures = e->graph_captures;
+  *launches = e->graph_launches;
+  return SH_OK;
+}
+
+// Greedy drafts (Engine::draft_tokens, inference/mod.rs:2062-2092): the
+// catch-up forward of the np pending tokens and last at dpos, then n - 1
+// single-token forwards at dpos + np + i, each argmax feeding the next
+// embedding on the device (tok[np + 1 + i] = d_{i+1}); the ids are copied to
+// the pinned staging buffer when copy_out is set.
+static int enqueue_drafts(sh_engine* e, sh_model* dm, sh_kv* dkv, uint32_t n, uint32_t np, uint32_t dpos,
+                          bool copy_out) {
   int rc = forward_dev(dm, dkv, e->spec.tok, np + 1, dpos, nullptr, 1, nullptr, nullptr, nullptr);
   if (rc) return rc;
+  // the chunk's logits are [np + 1][V]: the last column's row
   if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)np * dm->V, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1)))
     return rc;
   for (uint32_t i = 1; i < n; ++i) {
@@ -1717,12 +1751,66 @@ static int enqueue_greedy_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* 
       return rc;
     if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1 + i))) return rc;
   }
+  if (copy_out)
+    SH_HIP(hipMemcpyAsync(e->spec.pinned, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
+  return SH_OK;
+}
+
+// Draft n tokens greedily and verify [last, d_1..d_n] (greedy): drafts at dpos,
+// the verify at tpos; drafts and per-column argmax ids are copied to the pinned
+// staging buffer.
+static int enqueue_greedy_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t n,
+                               uint32_t np, uint32_t dpos, uint32_t tpos) {
+  int rc = enqueue_drafts(e, dm, dkv, n, np, dpos, true);
+  if (rc) return rc;
   if ((rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, tpos, nullptr, 2, nullptr, nullptr, nullptr))) return rc;
   if ((rc = sh_argmax_launch(e, tm->ws.logits, tm->V, n + 1, tm->ws.amax, e->spec.samp))) return rc;
+  SH_HIP(hipMemcpyAsync(e->spec.pinned + 16, e->spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+  return SH_OK;
+}
+
+// Stochastic step (COMPARE / REJECTION): draft ids stay on the device
+// (tok[np+1+i] = d_{i+1}). COMPARE drafts greedily, as the reference does
+// (mod.rs:2062-2092); REJECTION draws d_i ~ q_i = softmax(draft logits / T)
+// (vocab-order inverse CDF), which its min(1, p/q) test and residual draw need
+// to be lossless. Draft forwards at dpos (catch-up) and dpos + np + i, the
+// verify [last, d_1..d_n] at tpos with all-position logits, then the
+// per-column decision on the device. Uniform words per step: 2i / 2i+1 accept
+// / (re)sample verify column i, 2(n+1) + i draw draft i (REJECTION); explicit
+// uniforms (udev) are [3n + 2], else Philox words from ctr, or from the device
+// words rng (graph replay: key and word base written before each replay).
+static int enqueue_stoch_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t n,
+                              uint32_t np, uint32_t dpos, uint32_t tpos, const sh_sampling* s, const float* udev,
+                              uint64_t ctr, const uint64_t* rng) {
+  const bool rej = s->mode == SH_SAMPLE_REJECTION;
+  const uint32_t V = tm->V;
+  int rc;
+  for (uint32_t i = 0; i < n; ++i) {
+    float* q = e->spec.dlogits + (size_t)i * V;
+    rc = i == 0 ? forward_dev(dm, dkv, e->spec.tok, np + 1, dpos, nullptr, 1, q, nullptr, nullptr)
+                : forward_dev(dm, dkv, e->spec.tok + np + i, 1, dpos + np + i, nullptr, 1, q, nullptr, nullptr);
+    if (rc) return rc;
+    uint32_t* dst = e->spec.tok + np + 1 + i;
+    rc = rej ? sh_sample_rows_launch(e, q, 1, V, s->temperature, udev, s->seed, ctr + 2ull * (n + 1) + i, 1,
+                                     e->spec.rowstat, dst, rng)
+             : sh_argmax_launch(e, q, V, 1, dm->ws.amax, dst);
+    if (rc) return rc;
+  }
+  rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, tpos, nullptr, 2, e->spec.tlogits, nullptr, nullptr);
+  if (rc) return rc;
+  rc = sh_accept_launch(e, e->spec.tlogits, rej ? e->spec.dlogits : nullptr, e->spec.tok + np + 1, 1, n, V, s, ctr,
+                        udev, e->spec.samp + 9, e->spec.samp + 10, nullptr, nullptr, rng);
+  if (rc) return rc;
   uint32_t* hp = e->spec.pinned;
   SH_HIP(hipMemcpyAsync(hp, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
   SH_HIP(hipMemcpyAsync(hp + 16, e->spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
   return SH_OK;
+}
+
+static uint32_t f32_bits(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  return u;
 }
 
 extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t last_token,
@@ -1733,11 +1821,11 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   SH_CHECK(last_token < tm->V, SH_ERR_ARG, "last_token %u out of range", last_token);
   const uint32_t mode = s ? s->mode : SH_SAMPLE_GREEDY;
   SH_CHECK(mode <= SH_SAMPLE_REJECTION, SH_ERR_ARG, "sampling mode %u", mode);
-  if (mode == SH_SAMPLE_REJECTION) {
-    SampRow chk{};
-    if (int frc = sh_samprow_filters(*s, tm->V, chk)) return frc;
-    SH_CHECK(!chk.top_k, SH_ERR_UNSUPPORTED, "candidate filters (top_k / top_p / min_p) apply to COMPARE only");
-  }
+  SampRow filt{};
+  if (mode != SH_SAMPLE_GREEDY)
+    if (int frc = sh_samprow_filters(*s, tm->V, filt)) return frc;
+  SH_CHECK(mode != SH_SAMPLE_REJECTION || !filt.top_k, SH_ERR_UNSUPPORTED,
+           "candidate filters (top_k / top_p / min_p) apply to COMPARE only");
   SH_CHECK(mode == SH_SAMPLE_GREEDY || (s && s->temperature > 0.f), SH_ERR_ARG,
            "stochastic modes need temperature > 0");
   const uint32_t n = std::min<uint32_t>(std::max<uint32_t>(n_max, 1), 8);  // mod.rs:2121
@@ -1753,71 +1841,63 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
   hp[np] = last_token;
   SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
-  const bool greedy_graph = mode == SH_SAMPLE_GREEDY && n + 1 <= 8 && graphs_enabled(e) && tm->fused_ok &&
-                            dm->fused_ok;
-  if (mode == SH_SAMPLE_GREEDY) {
-    const uint32_t d0 = dkv->pos;
-    if (greedy_graph) {
-      const std::vector<uintptr_t> key = {1, (uintptr_t)tm, (uintptr_t)dm, (uintptr_t)tkv, (uintptr_t)dkv,
-                                          (uintptr_t)tkv->k, (uintptr_t)dkv->k, tkv->max_seq, dkv->max_seq, n, np,
-                                          tm->fa16, dm->fa16};
-      hipGraphExec_t ex = graph_find(e, key);
-      if (!ex) {
-        if ((rc = ensure_rope(tm, tkv->max_seq)) || (rc = ensure_rope(dm, dkv->max_seq)) ||
-            (rc = ensure_fa_part(tm, tkv->max_seq)) || (rc = ensure_fa_part(dm, dkv->max_seq)) ||
-            (rc = ensure_fa16(tm, tkv->max_seq, n + 1)) || (rc = ensure_fa16(dm, dkv->max_seq, np + 1)))
-          return rc;
-        rc = graph_capture(e, key, {dkv, tkv}, {e->spec.base, e->spec.base + 1},
-                           [&] { return enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, 0, 0); }, &ex);
-        if (rc) return rc;
-      }
-      hp[64] = d0;
-      hp[65] = P;
-      SH_HIP(hipMemcpyAsync(e->spec.base, hp + 64, 8, hipMemcpyHostToDevice, e->stream));
-      SH_HIP(hipGraphLaunch(ex, e->stream));
-      dkv->pos = d0 + np + n;  // what the eager forwards leave
-      tkv->pos = P + n + 1;
-    } else if ((rc = enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, d0, P))) {
-      return rc;
-    }
+  // The whole step replays one captured graph (the reference records a step as
+  // one submit, inference/mod.rs:2181-2231): every position-dependent argument
+  // is an offset from the device words base[0] (draft) / base[1] (target), and
+  // the stochastic modes read their Philox key and word base from rng
+  // (decode_dyn.rs:25-204 patches the same per-step values).
+  const bool graph = n + 1 <= 8 && np + 1 <= 8 && graphs_enabled(e) && graph_model_ok(tm) && graph_model_ok(dm);
+  const uint32_t d0 = dkv->pos, V = tm->V;
+  const float* udev = nullptr;
+  uint64_t ctr = mode == SH_SAMPLE_GREEDY ? 0 : s->counter;
+  if (mode != SH_SAMPLE_GREEDY && s->uniforms) {
+    SH_HIP(hipMemcpyAsync(e->spec.udev, s->uniforms, (size_t)(3 * n + 2) * 4, hipMemcpyHostToDevice, e->stream));
+    udev = e->spec.udev;
+    ctr = 0;
   }
-  // Stochastic modes: draft ids stay on the device (tok[np+1+i] = d_{i+1}):
-  // COMPARE drafts greedily, as the reference does (mod.rs:2062-2092);
-  // REJECTION draws d_i ~ q_i = softmax(draft logits / T) (vocab-order inverse
-  // CDF), which its min(1, p/q) test and residual draw need to be lossless.
-  // Uniform words per step: 2i / 2i+1 accept / (re)sample verify column i,
-  // 2(n+1) + i draw draft i (REJECTION); explicit uniforms are [3n + 2].
+  e->spec.last_n = 0;
+  if (graph) {
+    const std::vector<uintptr_t> key = {mode == SH_SAMPLE_GREEDY ? 1u : 3u, (uintptr_t)tm, (uintptr_t)dm,
+                                        (uintptr_t)tkv, (uintptr_t)dkv, (uintptr_t)tkv->k, (uintptr_t)dkv->k,
+                                        tkv->max_seq, dkv->max_seq, n, np, tm->fa16, dm->fa16, mode,
+                                        mode == SH_SAMPLE_GREEDY ? 0u : f32_bits(s->temperature),
+                                        mode == SH_SAMPLE_GREEDY ? 0u : s->top_k,
+                                        mode == SH_SAMPLE_GREEDY ? 0u : f32_bits(s->top_p),
+                                        mode == SH_SAMPLE_GREEDY ? 0u : f32_bits(s->min_p), udev ? 1u : 0u};
+    hipGraphExec_t ex = graph_find(e, key);
+    if (!ex) {
+      // everything a capture reads is sized beforehand (nothing allocates while capturing)
+      if ((rc = ensure_rope(tm, tkv->max_seq)) || (rc = ensure_rope(dm, dkv->max_seq)) ||
+          (rc = ensure_fa_part(tm, tkv->max_seq)) || (rc = ensure_fa_part(dm, dkv->max_seq)) ||
+          (rc = ensure_fa16(tm, tkv->max_seq, n + 1)) || (rc = ensure_fa16(dm, dkv->max_seq, np + 1)))
+        return rc;
+      if (mode != SH_SAMPLE_GREEDY) {
+        void* sb = nullptr;
+        if ((rc = sh_engine_scratch(e, SCR_ACCEPT, sh_accept_scratch_bytes(1, n, V, mode), &sb))) return rc;
+      }
+      rc = graph_capture(e, key, {dkv, tkv}, {e->spec.base, e->spec.base + 1}, [&] {
+        return mode == SH_SAMPLE_GREEDY
+                   ? enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, 0, 0)
+                   : enqueue_stoch_step(e, tm, dm, tkv, dkv, n, np, 0, 0, s, udev, 0, udev ? nullptr : e->spec.rng);
+      }, &ex);
+      if (rc) return rc;
+    }
+    hp[64] = d0;
+    hp[65] = P;
+    uint64_t* hr = reinterpret_cast<uint64_t*>(hp + 68);
+    hr[0] = mode == SH_SAMPLE_GREEDY ? 0 : s->seed;
+    hr[1] = ctr;
+    SH_HIP(hipMemcpyAsync(e->spec.base, hp + 64, 8 * 4, hipMemcpyHostToDevice, e->stream));
+    if ((rc = graph_launch(e, ex))) return rc;
+    dkv->pos = d0 + np + n;  // what the eager forwards leave
+    tkv->pos = P + n + 1;
+  } else {
+    rc = mode == SH_SAMPLE_GREEDY ? enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, d0, P)
+                                  : enqueue_stoch_step(e, tm, dm, tkv, dkv, n, np, d0, P, s, udev, ctr, nullptr);
+    if (rc) return rc;
+  }
   if (mode != SH_SAMPLE_GREEDY) {
-    const bool rej = mode == SH_SAMPLE_REJECTION;
-    const uint32_t V = tm->V, nu = 3 * n + 2;
-    const float* udev = nullptr;
-    uint64_t ctr = s->counter;
-    if (s->uniforms) {
-      SH_HIP(hipMemcpyAsync(e->spec.udev, s->uniforms, (size_t)nu * 4, hipMemcpyHostToDevice, e->stream));
-      udev = e->spec.udev;
-      ctr = 0;
-    }
-    e->spec.last_n = 0;
-    for (uint32_t i = 0; i < n; ++i) {
-      float* q = e->spec.dlogits + (size_t)i * V;
-      rc = i == 0 ? forward_dev(dm, dkv, e->spec.tok, np + 1, dkv->pos, nullptr, 1, q, nullptr, nullptr)
-                  : forward_dev(dm, dkv, e->spec.tok + np + i, 1, dkv->pos, nullptr, 1, q, nullptr, nullptr);
-      if (rc) return rc;
-      uint32_t* dst = e->spec.tok + np + 1 + i;
-      rc = rej ? sh_sample_rows_launch(e, q, 1, V, s->temperature, udev, s->seed, ctr + 2ull * (n + 1) + i, 1,
-                                       e->spec.rowstat, dst)
-               : sh_argmax_launch(e, q, V, 1, dm->ws.amax, dst);
-      if (rc) return rc;
-    }
-    // verify [last, d_1..d_n] with all-position logits, then the per-column decision on the device
-    rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, P, nullptr, 2, e->spec.tlogits, nullptr, nullptr);
-    if (rc) return rc;
-    rc = sh_accept_launch(e, e->spec.tlogits, rej ? e->spec.dlogits : nullptr, e->spec.tok + np + 1, 1, n, V, s, ctr,
-                          udev, e->spec.samp + 9, e->spec.samp + 10);
-    if (rc) return rc;
-    if (!udev) s->counter += nu;
-    SH_HIP(hipMemcpyAsync(hp, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
-    SH_HIP(hipMemcpyAsync(hp + 16, e->spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
+    if (!udev) s->counter += 3 * n + 2;
     e->spec.last_n = n;
     e->spec.last_V = V;
   }
@@ -1851,7 +1931,9 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
 // Engine::draft_tokens (inference/mod.rs:2062-2092) with a separate draft
 // model: the cache's pending tokens and last_token, then n - 1 single-token
 // forwards, each argmax feeding the next embedding on the device; the ids come
-// back at the end. The cache advances by its pending count + n (d_n is not fed).
+// back at the end. The cache advances by its pending count + n (d_n is not
+// fed). Replays a captured graph (positions from base[0]) where the model
+// allows.
 extern "C" int sh_draft_tokens(sh_engine* e, sh_model* dm, sh_kv* dkv, uint32_t last_token, uint32_t n_max,
                                uint32_t* drafts_out) {
   SH_CHECK(e && dm && dkv && drafts_out, SH_ERR_ARG, "sh_draft_tokens: NULL argument");
@@ -1865,14 +1947,26 @@ extern "C" int sh_draft_tokens(sh_engine* e, sh_model* dm, sh_kv* dkv, uint32_t 
   for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
   hp[np] = last_token;
   SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
-  if ((rc = forward_dev(dm, dkv, e->spec.tok, np + 1, dkv->pos, nullptr, 1, nullptr, nullptr, nullptr))) return rc;
-  if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1))) return rc;
-  for (uint32_t i = 1; i < n; ++i) {
-    if ((rc = forward_dev(dm, dkv, e->spec.tok + np + i, 1, dkv->pos, nullptr, 1, nullptr, nullptr, nullptr)))
-      return rc;
-    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1 + i))) return rc;
+  const uint32_t d0 = dkv->pos;
+  if (np + 1 <= 8 && graphs_enabled(e) && graph_model_ok(dm)) {
+    const std::vector<uintptr_t> key = {4, (uintptr_t)dm, (uintptr_t)dkv, (uintptr_t)dkv->k, dkv->max_seq, n, np,
+                                        dm->fa16};
+    hipGraphExec_t ex = graph_find(e, key);
+    if (!ex) {
+      if ((rc = ensure_rope(dm, dkv->max_seq)) || (rc = ensure_fa_part(dm, dkv->max_seq)) ||
+          (rc = ensure_fa16(dm, dkv->max_seq, np + 1)))
+        return rc;
+      rc = graph_capture(e, key, {dkv}, {e->spec.base}, [&] { return enqueue_drafts(e, dm, dkv, n, np, 0, true); },
+                         &ex);
+      if (rc) return rc;
+    }
+    hp[64] = d0;
+    SH_HIP(hipMemcpyAsync(e->spec.base, hp + 64, 4, hipMemcpyHostToDevice, e->stream));
+    if ((rc = graph_launch(e, ex))) return rc;
+    dkv->pos = d0 + np + n;
+  } else if ((rc = enqueue_drafts(e, dm, dkv, n, np, d0, true))) {
+    return rc;
   }
-  SH_HIP(hipMemcpyAsync(hp, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
   SH_HIP(hipStreamSynchronize(e->stream));
   std::memcpy(drafts_out, hp, n * 4);
   dkv->pending.clear();

@@ -166,6 +166,15 @@ __device__ double2 lane_row_stat(const double2* __restrict__ pr, uint32_t nch, d
   return make_double2(M, S);
 }
 
+// Graph replay: the Philox key and word base come from the device words
+// rng[0] and rng[1], which the host writes before each replay.
+__device__ __forceinline__ void rng_from_dev(const uint64_t* rng, uint64_t& seed, uint64_t& word) {
+  if (rng) {
+    seed = rng[0];
+    word += rng[1];
+  }
+}
+
 __device__ __forceinline__ float uniform_at(const float* u_dev, uint64_t seed, uint64_t word) {
   if (u_dev) return u_dev[word];
   uint64_t ctr[4] = {word / 4 + 1, 0, 0, 0}, key[2] = {seed, kUniformStream}, out[4];
@@ -299,10 +308,11 @@ __device__ uint32_t wg_inverse_cdf(const W& rw, uint32_t lo, uint32_t hi, bool r
 __global__ __launch_bounds__(256) void k_sample_cols(const float* __restrict__ p, const double2* __restrict__ part,
                                                      uint32_t nch, uint32_t V, double inv_t, const float* u_dev,
                                                      uint64_t seed, uint64_t word0, uint64_t wstride,
-                                                     uint32_t* __restrict__ out) {
+                                                     uint32_t* __restrict__ out, const uint64_t* rng) {
   __shared__ double tab[64];
   __shared__ double2 st;
   const uint32_t row = blockIdx.x;
+  rng_from_dev(rng, seed, word0);
   load_exp_table(tab);
   __syncthreads();
   if (threadIdx.x < 64) {
@@ -559,9 +569,11 @@ __device__ uint32_t sample_filtered_row(const float* __restrict__ x, uint32_t V,
 // (or explicit u_dev[...]), as k_sample_cols.
 __global__ __launch_bounds__(256) void k_sample_filtered_cols(const float* __restrict__ p, uint32_t V, FiltCfg cf,
                                                               const float* u_dev, uint64_t seed, uint64_t word0,
-                                                              uint64_t wstride, uint32_t* __restrict__ out) {
+                                                              uint64_t wstride, uint32_t* __restrict__ out,
+                                                              const uint64_t* rng) {
   __shared__ double tab[64];
   const uint32_t row = blockIdx.x;
+  rng_from_dev(rng, seed, word0);
   load_exp_table(tab);
   __syncthreads();
   const float u = uniform_at(u_dev, seed, word0 + wstride * row);
@@ -608,11 +620,13 @@ __global__ __launch_bounds__(256) void k_decide_reject(const float* __restrict__
                                                        const uint32_t* __restrict__ drafts, const float* u_dev,
                                                        uint64_t seed, uint64_t counter,
                                                        uint32_t* __restrict__ first_rej,
-                                                       double2* __restrict__ rstat, double* __restrict__ probs) {
+                                                       double2* __restrict__ rstat, double* __restrict__ probs,
+                                                       const uint64_t* rng) {
   __shared__ double tab[64];
   __shared__ double2 st[129];  // p rows 0..k, then q rows 0..k-1 (k <= 64)
   __shared__ uint32_t fr;
   const uint32_t b = blockIdx.x, t = threadIdx.x;
+  rng_from_dev(rng, seed, counter);
   load_exp_table(tab);
   if (t == 0) fr = k;
   // the draft token's logits for the accept test (lane t < k), loaded with the partials
@@ -714,13 +728,14 @@ __global__ __launch_bounds__(256) void k_draw_pick(const float* __restrict__ p, 
                                                    const double2* __restrict__ rstat,
                                                    const double2* __restrict__ chunk, const float* u_dev,
                                                    uint64_t seed, uint64_t counter, uint32_t* __restrict__ acc_len,
-                                                   uint32_t* __restrict__ next_tok) {
+                                                   uint32_t* __restrict__ next_tok, const uint64_t* rng) {
   static_assert(kDrawChunks == 64, "one lane per chunk");
   __shared__ double tab[64];
   __shared__ uint32_t s_c;
   __shared__ double s_off, s_target;
   __shared__ int s_use_r;
   const uint32_t b = blockIdx.x, t = threadIdx.x, i = first_rej[b];
+  rng_from_dev(rng, seed, counter);
   load_exp_table(tab);
   const double2 sp = rstat[2 * b], sq = rstat[2 * b + 1];
   if (t < 64) {
@@ -1106,7 +1121,8 @@ size_t sh_accept_scratch_bytes(uint32_t B, uint32_t k, uint32_t V, uint32_t mode
 
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
                      uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter, const float* uniforms_dev,
-                     uint32_t* acc_len, uint32_t* next_tok, void* scratch_in, double* probs_out) {
+                     uint32_t* acc_len, uint32_t* next_tok, void* scratch_in, double* probs_out,
+                     const uint64_t* rng_dev) {
   SH_CHECK(B >= 1 && k >= 1 && k <= 64 && V >= 1, SH_ERR_ARG, "accept: B=%u k=%u V=%u", B, k, V);
   const uint32_t mode = s->mode;
   SH_CHECK(mode == SH_SAMPLE_COMPARE || mode == SH_SAMPLE_REJECTION, SH_ERR_ARG, "accept: mode %u", mode);
@@ -1147,21 +1163,21 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   if (mode == SH_SAMPLE_COMPARE && filt.top_k) {
     const FiltCfg cf{filt.top_k, filt.top_p, filt.log_min_p, filt.inv_t_f, filt.filt_flags};
     hipLaunchKernelGGL(k_sample_filtered_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, V, cf, uniforms_dev,
-                       s->seed, counter + 1ull, 2ull, small);
+                       s->seed, counter + 1ull, 2ull, small, rng_dev);
     hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
                        next_tok);
   } else if (mode == SH_SAMPLE_COMPARE) {
     hipLaunchKernelGGL(k_sample_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, part, nch, V, inv_t,
-                       uniforms_dev, s->seed, counter + 1ull, 2ull, small);
+                       uniforms_dev, s->seed, counter + 1ull, 2ull, small, rng_dev);
     hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
                        next_tok);
   } else {
     hipLaunchKernelGGL(k_decide_reject, dim3(B), dim3(256), 0, e->stream, p_logits, q_logits, part, nch, B, k, V,
-                       inv_t, drafts, uniforms_dev, s->seed, counter, small, rstat, probs_out);
+                       inv_t, drafts, uniforms_dev, s->seed, counter, small, rstat, probs_out, rng_dev);
     hipLaunchKernelGGL(k_draw_chunks, dim3(kDrawChunks, B), dim3(256), 0, e->stream, p_logits, q_logits, k, V, inv_t,
                        small, rstat, chunk);
     hipLaunchKernelGGL(k_draw_pick, dim3(B), dim3(256), 0, e->stream, p_logits, q_logits, k, V, inv_t, small, rstat,
-                       chunk, uniforms_dev, s->seed, counter, acc_len, next_tok);
+                       chunk, uniforms_dev, s->seed, counter, acc_len, next_tok, rng_dev);
   }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_decide", 0.0, ev);
@@ -1169,7 +1185,8 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
 }
 
 int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
-                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out) {
+                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out,
+                          const uint64_t* rng_dev) {
   SH_CHECK(nrows >= 1 && V >= 1 && T > 0.f, SH_ERR_ARG, "sample_rows: nrows=%u V=%u T=%g", nrows, V, (double)T);
   const double inv_t = 1.0 / (double)T;
   const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
@@ -1182,7 +1199,7 @@ int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uin
     hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
                        nullptr, V, inv_t, nch, part);
   hipLaunchKernelGGL(k_sample_cols, dim3(nrows), dim3(256), 0, e->stream, logits, part, nch, V, inv_t, u_dev, seed,
-                     word0, wstride, out);
+                     word0, wstride, out, rng_dev);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "sample_rows", 4.0 * V * nrows, ev);
   return SH_OK;
@@ -1281,7 +1298,7 @@ extern "C" int sh_accept_probs(sh_engine* e, const float* p_logits_dev, const fl
                        q_logits_dev, V, inv_t, nch, part);
   // the accept tests' probabilities; the uniform (word 0 of seed 0) does not affect them
   hipLaunchKernelGGL(k_decide_reject, dim3(B), dim3(256), 0, e->stream, p_logits_dev, q_logits_dev, part, nch, B, k,
-                     V, inv_t, drafts_dev, nullptr, 0ull, 0ull, fr, rstat, probs_dev);
+                     V, inv_t, drafts_dev, nullptr, 0ull, 0ull, fr, rstat, probs_dev, nullptr);
   const hipError_t le = hipGetLastError();
   (void)hipFreeAsync(sbuf, e->stream);
   SH_CHECK(le == hipSuccess, SH_ERR_HIP, "accept_probs launch: %s", hipGetErrorString(le));

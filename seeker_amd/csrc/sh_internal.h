@@ -63,12 +63,13 @@ struct KStat {
 struct SpecBufs {
   uint32_t* tok = nullptr;     // [64]: pending..., last, d_1..d_n; verify tokens at [32..]
   uint32_t* samp = nullptr;    // [16]: per-column ids; acc_len at [9], next token at [10]
-  uint32_t* base = nullptr;    // [4] graph base positions (device): draft, target, verify
+  uint32_t* base = nullptr;    // [8] graph base positions (device): draft, target, verify; [4..7] = rng
   float* dlogits = nullptr;    // draft logits [8][V] of the last stochastic step
   float* tlogits = nullptr;    // target logits [9][V] of the last stochastic step
   float* udev = nullptr;       // [32] explicit uniforms of a stochastic step
   double2* rowstat = nullptr;  // [256] row-statistics partials of the device draft draws
-  uint32_t* pinned = nullptr;  // host staging [128]
+  uint64_t* rng = nullptr;     // = base + 4: Philox key and word base of a replayed stochastic step
+  uint32_t* pinned = nullptr;  // host staging [128]; [64..71] go to base[0..7]
   uint32_t vcap = 0;
   uint32_t last_n = 0, last_V = 0;  // drafts and vocab of the last stochastic step (0: none)
 };
@@ -99,6 +100,7 @@ struct sh_engine {
   // stream orders them): grown on demand by sh_engine_scratch.
   void* scr[4] = {nullptr, nullptr, nullptr, nullptr};
   size_t scr_bytes[4] = {0, 0, 0, 0};
+  uint64_t graph_captures = 0, graph_launches = 0;  // replay counters (sh_engine_graph_stats)
 };
 // Scratch slots of sh_engine_scratch.
 enum ScratchSlot { SCR_ACCEPT = 0, SCR_UNIFORMS = 1, SCR_TREE = 2, SCR_SMALL = 3 };
@@ -518,9 +520,11 @@ int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, 
 // Draws one token per row from softmax(logits / T) by the vocab-order inverse
 // CDF (the COMPARE column sampler): row r uses uniform word word0 + wstride * r
 // (explicit u_dev[word] or Philox key (seed, 0x5EC)). part: nrows * ceil(V /
-// 8192) row-statistics partials of scratch.
+// 8192) row-statistics partials of scratch. rng_dev (graph replay): the key
+// and a word base added to word0 are read from the device words rng_dev[0..1].
 int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
-                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out);
+                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out,
+                          const uint64_t* rng_dev = nullptr);
 // Per-row parameters of the batched verify's column sampling.
 struct SampRow {
   double inv_t;       // 1 / temperature
@@ -564,7 +568,8 @@ size_t sh_accept_scratch_bytes(uint32_t B, uint32_t k, uint32_t V, uint32_t mode
 int sh_static_scratch_init(int dev);
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
                      uint32_t k, uint32_t V, const sh_sampling* s, uint64_t counter, const float* uniforms_dev,
-                     uint32_t* acc_len, uint32_t* next_tok, void* scratch = nullptr, double* probs_out = nullptr);
+                     uint32_t* acc_len, uint32_t* next_tok, void* scratch = nullptr, double* probs_out = nullptr,
+                     const uint64_t* rng_dev = nullptr);
 int sh_kv_compact_launch(sh_engine* e, sh_kv* kv, uint32_t base, const uint32_t* src_dev, uint32_t n);
 
 // Profiling helpers (no-ops unless e->profiling).

@@ -242,6 +242,12 @@ class Engine:
     def set_profiling(self, on: bool):
         N.check(self._lib.sh_engine_set_profiling(self.h, int(on)))
 
+    def graph_stats(self):
+        """(graphs captured, graph launches) so far on this engine."""
+        c, l = C.c_uint64(), C.c_uint64()
+        N.check(self._lib.sh_engine_graph_stats(self.h, C.byref(c), C.byref(l)))
+        return c.value, l.value
+
     def profile(self, reset: bool = False) -> dict:
         n = C.c_uint32()
         N.check(self._lib.sh_engine_profile(self.h, None, 0, C.byref(n)))
