@@ -107,6 +107,77 @@ def measure_draft(eng, P=4096, reps=30):
             "kernel_ms": round(kern_ms, 4), "alg_bytes": w + kr + kw, "kernel_us": per}
 
 
+def measure_rejection(eng, tm, dm, tkv, dkv, last, k, steps, warmup=2, T=0.8, seed=5):
+    """REJECTION spec steps at temperature T (graph-replayed like the greedy
+    steps): draft i drawn from softmax(q / T), accepted iff u q(d) < p(d),
+    first rejection resampled from max(0, p - q)."""
+    from seeker_amd._native import sh_sampling
+    s = sh_sampling()
+    s.mode, s.temperature, s.seed, s.counter = 2, T, seed, 0
+    for _ in range(warmup):
+        last = eng.decode_speculative(tm, dm, tkv, dkv, last, k, s).last_token
+    eng.sync()
+    t = time.perf_counter()
+    emitted = accepted = 0
+    for _ in range(steps):
+        r = eng.decode_speculative(tm, dm, tkv, dkv, last, k, s)
+        emitted += len(r.emitted)
+        accepted += r.accepted
+        last = r.last_token
+    eng.sync()
+    dt = time.perf_counter() - t
+    log(f"REJECTION T={T}: {dt * 1e3 / steps:.3f} ms/step, {emitted} tokens, acceptance {accepted / (steps * k):.3f}")
+    return {"temperature": T, "ms_per_step": round(dt * 1e3 / steps, 4), "tok_s": round(emitted / dt, 2),
+            "acceptance_rate": round(accepted / (steps * k), 4), "steps": steps}, last
+
+
+def measure_forced(eng, tm, dm, tkv, dkv, last, k, steps, warmup=2):
+    """The forced-acceptance diagnostic: every step's drafts are the target's
+    greedy continuation (single-token target forwards from the same state,
+    computed outside the timed steps), fed through the draft model by
+    sh_spec_step_forced, so a step does a real step's work and accepts all k
+    drafts. tok/s = emitted tokens / summed step wall times. A near-tie where
+    the 8-column verify's argmax differs from the single-token forward's ends
+    the continuation early: it is recomputed from there (untimed)."""
+    cont, j = [], 0
+
+    def extend():
+        P = tkv.position
+        c = [last]
+        for i in range((steps + warmup - done) * (k + 1) + k):
+            c.append(int(eng.verify_greedy(tm, tkv, [c[-1]], P + i)[0]))
+        tkv.truncate(P)
+        return c
+    times, emitted, accepted, resyncs = [], 0, 0, 0
+    done = 0
+    while done < steps + warmup:
+        if j + k + 1 >= len(cont):
+            cont, j = extend(), 0
+        t = time.perf_counter()
+        r = eng.decode_speculative_forced(tm, dm, tkv, dkv, cont[j], cont[j + 1:j + 1 + k])
+        dt = time.perf_counter() - t
+        if done >= warmup:
+            times.append(dt)
+            emitted += len(r.emitted)
+            accepted += r.accepted
+        done += 1
+        last = r.last_token
+        if r.emitted != cont[j + 1:j + 2 + k]:
+            resyncs += 1
+            cont, j = [], 0
+        else:
+            j += len(r.emitted)
+    total = sum(times)
+    log(f"forced acceptance: {total * 1e3 / steps:.3f} ms/step, {emitted} tokens in {steps} steps, "
+        f"{emitted / total:.1f} tok/s ({resyncs} continuation resyncs)")
+    return {"tok_s": round(emitted / total, 2), "ms_per_step": round(total * 1e3 / steps, 4),
+            "acceptance_rate": round(accepted / (steps * k), 4), "steps": steps, "resyncs": resyncs,
+            "definition": "measured: each step's drafts are the target's greedy continuation (single-token target "
+                          "forwards), fed through the draft model (sh_spec_step_forced: the draft forwards run over "
+                          "them), so every draft is accepted; tokens emitted / summed step wall times "
+                          "(apps/seeker-cli/src/commands/run.rs:702-710 counts emitted tokens)"}, last
+
+
 def measure_acceptance(eng, reps=20):
     """the acceptance kernel alone (REJECTION, T = 0.8), B = 32, k = 8,
     V = 128256; target logits N(0, 3), draft = target + N(0, 1), drafts sampled
@@ -420,6 +491,7 @@ def main():
         if dm is not None:
             eng.prefill(dm, dkv, prompt, 0)
         last = int(np.argmax(lg[0]))
+    last0 = last  # the token after the prefill: each stepped leg below starts from (P0, last0)
     log(f"prefill {P0} tokens in {time.time() - t0:.1f}s")
 
     # ---- verify step: latency + roofline (target only) -------------------
@@ -544,6 +616,12 @@ def main():
                    "GBps": round((dw + dkr + dkw) / d_ms / 1e6, 1),
                    "frac": round((dw + dkr + dkw) / d_ms / 1e6 / HBM_PEAK_GBS, 4),
                    "method": "(spec step ms - verify ms) / k, graph-replayed steps"}
+    for kv in (tkv, dkv):
+        kv.truncate(P0)
+    rej, _ = measure_rejection(eng, tm, dm, tkv, dkv, last0, args.k, args.steps)
+    for kv in (tkv, dkv):
+        kv.truncate(P0)
+    forced, _ = measure_forced(eng, tm, dm, tkv, dkv, last0, args.k, args.steps)
     extra_acc = extra_tree = extra_moe = None
     if not args.no_extra:
         extra_acc = measure_acceptance(eng)
@@ -572,10 +650,8 @@ def main():
                      "frac": round(dom_bytes / dom_avg_ms / 1e6 / HBM_PEAK_GBS, 4),
                      "bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_avg_ms, 5),
                      "traffic": measured_traffic(dom_name)},
-        "forced_acceptance": {"tok_s": round((args.k + 1) / (dt / args.steps), 2),
-                              "definition": "k+1 tokens per step at the measured step time: the draft and verify "
-                                            "work of a step does not depend on how many drafts are accepted "
-                                            "(apps/seeker-cli/src/commands/run.rs:702-710 counts emitted tokens)"},
+        "forced_acceptance": forced,
+        "rejection_step": rej,
         "draft_forward": draft_stats,
         "cpu_baseline": cpu,
         "parity": parity,

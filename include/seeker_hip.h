@@ -238,6 +238,15 @@ int sh_verify_unified_sampled(sh_engine* e, sh_model* m, sh_kv* const* caches, u
 int sh_spec_step(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh_kv* dkv,
                  uint32_t last_token, uint32_t n_max, sh_sampling* s, uint32_t* emitted_out,
                  uint32_t* n_emitted, uint32_t* drafts_out);
+/* Measurement diagnostic, no counterpart in the reference: a greedy
+ * sh_spec_step whose drafts are forced_drafts[0..n) instead of the draft
+ * model's argmax ids. The draft forwards still run, over the forced ids, so a
+ * step does the same work (and replays the same graph shape) as a real one.
+ * For the forced-acceptance throughput: drafts that replay the target's greedy
+ * continuation are all accepted. Caches and pending tokens as sh_spec_step. */
+int sh_spec_step_forced(sh_engine* e, sh_model* target, sh_model* draft, sh_kv* tkv, sh_kv* dkv,
+                        uint32_t last_token, uint32_t n_max, const uint32_t* forced_drafts,
+                        uint32_t* emitted_out, uint32_t* n_emitted);
 /* Engine::draft_tokens (inference/mod.rs:2062-2092) with a separate draft
  * model: n = clamp(n_max, 1, 8) greedy drafts after last_token, fed through
  * the draft cache dkv (its pending tokens first, as sh_spec_step leaves them),

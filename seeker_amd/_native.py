@@ -129,6 +129,7 @@ SIGNATURES = {
     "sh_verify_unified_sampled": (C.c_int, [P, P, C.POINTER(P), C.c_uint32, U32P, U32P, U32P, I32P,
                                             P, F32P, U32P, F32P]),
     "sh_draft_tokens": (C.c_int, [P, P, P, C.c_uint32, C.c_uint32, U32P]),
+    "sh_spec_step_forced": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, U32P, U32P, C.POINTER(C.c_uint32)]),
     "sh_spec_step_batch": (C.c_int, [P, P, P, C.POINTER(P), C.POINTER(P), C.c_uint32, U32P, C.c_uint32, P, U32P, U32P,
                                      U32P]),
     "sh_spec_step": (C.c_int, [P, P, P, P, P, C.c_uint32, C.c_uint32, C.POINTER(sh_sampling), U32P, U32P, U32P]),

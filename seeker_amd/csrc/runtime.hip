@@ -1738,18 +1738,20 @@ extern "C" int sh_engine_graph_stats(sh_engine* e, uint64_t* captures, uint64_t*
 // catch-up forward of the np pending tokens and last at dpos, then n - 1
 // single-token forwards at dpos + np + i, each argmax feeding the next
 // embedding on the device (tok[np + 1 + i] = d_{i+1}); the ids are copied to
-// the pinned staging buffer when copy_out is set.
+// the pinned staging buffer when copy_out is set. forced: the drafts are
+// already staged in tok (the forced-acceptance diagnostic); the argmax ids go
+// to tok[48 + i] instead and the work is the same.
 static int enqueue_drafts(sh_engine* e, sh_model* dm, sh_kv* dkv, uint32_t n, uint32_t np, uint32_t dpos,
-                          bool copy_out) {
+                          bool copy_out, bool forced = false) {
+  uint32_t* ids = forced ? e->spec.tok + 48 : e->spec.tok + np + 1;
   int rc = forward_dev(dm, dkv, e->spec.tok, np + 1, dpos, nullptr, 1, nullptr, nullptr, nullptr);
   if (rc) return rc;
   // the chunk's logits are [np + 1][V]: the last column's row
-  if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)np * dm->V, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1)))
-    return rc;
+  if ((rc = sh_argmax_launch(e, dm->ws.logits + (size_t)np * dm->V, dm->V, 1, dm->ws.amax, ids))) return rc;
   for (uint32_t i = 1; i < n; ++i) {
     if ((rc = forward_dev(dm, dkv, e->spec.tok + np + i, 1, dpos + np + i, nullptr, 1, nullptr, nullptr, nullptr)))
       return rc;
-    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, e->spec.tok + np + 1 + i))) return rc;
+    if ((rc = sh_argmax_launch(e, dm->ws.logits, dm->V, 1, dm->ws.amax, ids + i))) return rc;
   }
   if (copy_out)
     SH_HIP(hipMemcpyAsync(e->spec.pinned, e->spec.tok + np + 1, n * 4, hipMemcpyDeviceToHost, e->stream));
@@ -1760,8 +1762,8 @@ static int enqueue_drafts(sh_engine* e, sh_model* dm, sh_kv* dkv, uint32_t n, ui
 // the verify at tpos; drafts and per-column argmax ids are copied to the pinned
 // staging buffer.
 static int enqueue_greedy_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t n,
-                               uint32_t np, uint32_t dpos, uint32_t tpos) {
-  int rc = enqueue_drafts(e, dm, dkv, n, np, dpos, true);
+                               uint32_t np, uint32_t dpos, uint32_t tpos, bool forced) {
+  int rc = enqueue_drafts(e, dm, dkv, n, np, dpos, true, forced);
   if (rc) return rc;
   if ((rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, tpos, nullptr, 2, nullptr, nullptr, nullptr))) return rc;
   if ((rc = sh_argmax_launch(e, tm->ws.logits, tm->V, n + 1, tm->ws.amax, e->spec.samp))) return rc;
@@ -1813,9 +1815,9 @@ static uint32_t f32_bits(float x) {
   return u;
 }
 
-extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t last_token,
-                            uint32_t n_max, sh_sampling* s, uint32_t* emitted_out, uint32_t* n_emitted,
-                            uint32_t* drafts_out) {
+static int spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t last_token,
+                     uint32_t n_max, sh_sampling* s, const uint32_t* forced, uint32_t* emitted_out,
+                     uint32_t* n_emitted, uint32_t* drafts_out) {
   SH_CHECK(e && tm && dm && tkv && dkv && emitted_out && n_emitted, SH_ERR_ARG, "sh_spec_step: NULL argument");
   SH_CHECK(tm->V == dm->V, SH_ERR_ARG, "draft vocab %u != target vocab %u", dm->V, tm->V);
   SH_CHECK(last_token < tm->V, SH_ERR_ARG, "last_token %u out of range", last_token);
@@ -1840,7 +1842,14 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   uint32_t* hp = e->spec.pinned;
   for (uint32_t i = 0; i < np; ++i) hp[i] = dkv->pending[i];
   hp[np] = last_token;
-  SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1) * 4, hipMemcpyHostToDevice, e->stream));
+  if (forced) {
+    SH_CHECK(mode == SH_SAMPLE_GREEDY, SH_ERR_ARG, "forced drafts are greedy steps");
+    for (uint32_t i = 0; i < n; ++i) {
+      SH_CHECK(forced[i] < tm->V, SH_ERR_ARG, "forced draft %u out of range", forced[i]);
+      hp[np + 1 + i] = forced[i];
+    }
+  }
+  SH_HIP(hipMemcpyAsync(e->spec.tok, hp, (np + 1 + (forced ? n : 0)) * 4, hipMemcpyHostToDevice, e->stream));
   // The whole step replays one captured graph (the reference records a step as
   // one submit, inference/mod.rs:2181-2231): every position-dependent argument
   // is an offset from the device words base[0] (draft) / base[1] (target), and
@@ -1863,7 +1872,8 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
                                         mode == SH_SAMPLE_GREEDY ? 0u : f32_bits(s->temperature),
                                         mode == SH_SAMPLE_GREEDY ? 0u : s->top_k,
                                         mode == SH_SAMPLE_GREEDY ? 0u : f32_bits(s->top_p),
-                                        mode == SH_SAMPLE_GREEDY ? 0u : f32_bits(s->min_p), udev ? 1u : 0u};
+                                        mode == SH_SAMPLE_GREEDY ? 0u : f32_bits(s->min_p), udev ? 1u : 0u,
+                                        forced ? 1u : 0u};
     hipGraphExec_t ex = graph_find(e, key);
     if (!ex) {
       // everything a capture reads is sized beforehand (nothing allocates while capturing)
@@ -1877,7 +1887,7 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
       }
       rc = graph_capture(e, key, {dkv, tkv}, {e->spec.base, e->spec.base + 1}, [&] {
         return mode == SH_SAMPLE_GREEDY
-                   ? enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, 0, 0)
+                   ? enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, 0, 0, forced != nullptr)
                    : enqueue_stoch_step(e, tm, dm, tkv, dkv, n, np, 0, 0, s, udev, 0, udev ? nullptr : e->spec.rng);
       }, &ex);
       if (rc) return rc;
@@ -1892,7 +1902,7 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
     dkv->pos = d0 + np + n;  // what the eager forwards leave
     tkv->pos = P + n + 1;
   } else {
-    rc = mode == SH_SAMPLE_GREEDY ? enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, d0, P)
+    rc = mode == SH_SAMPLE_GREEDY ? enqueue_greedy_step(e, tm, dm, tkv, dkv, n, np, d0, P, forced != nullptr)
                                   : enqueue_stoch_step(e, tm, dm, tkv, dkv, n, np, d0, P, s, udev, ctr, nullptr);
     if (rc) return rc;
   }
@@ -1926,6 +1936,19 @@ extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv
   *n_emitted = ne;
   if (drafts_out) std::memcpy(drafts_out, drafts, n * 4);
   return sh_prof_flush(e);
+}
+
+extern "C" int sh_spec_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv, uint32_t last_token,
+                            uint32_t n_max, sh_sampling* s, uint32_t* emitted_out, uint32_t* n_emitted,
+                            uint32_t* drafts_out) {
+  return spec_step(e, tm, dm, tkv, dkv, last_token, n_max, s, nullptr, emitted_out, n_emitted, drafts_out);
+}
+
+extern "C" int sh_spec_step_forced(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* tkv, sh_kv* dkv,
+                                   uint32_t last_token, uint32_t n_max, const uint32_t* forced_drafts,
+                                   uint32_t* emitted_out, uint32_t* n_emitted) {
+  SH_CHECK(forced_drafts, SH_ERR_ARG, "sh_spec_step_forced: forced_drafts is NULL");
+  return spec_step(e, tm, dm, tkv, dkv, last_token, n_max, nullptr, forced_drafts, emitted_out, n_emitted, nullptr);
 }
 
 // Engine::draft_tokens (inference/mod.rs:2062-2092) with a separate draft

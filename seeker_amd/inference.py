@@ -191,6 +191,20 @@ class Engine:
         em = emitted[: ne.value].tolist()
         return SpecStepOut(em, ne.value - 1, em[-1], drafts[:n].tolist())
 
+    def decode_speculative_forced(self, target: "Model", draft: "Model", tcache: "KvCache", dcache: "KvCache",
+                                  last_token: int, forced_drafts: Sequence[int]) -> SpecStepOut:
+        """sh_spec_step_forced: a greedy step whose drafts are forced_drafts (the
+        draft forwards run over them); the forced-acceptance measurement."""
+        n = len(forced_drafts)
+        fd = np.ascontiguousarray(forced_drafts, dtype=np.uint32)
+        emitted = np.zeros(9, dtype=np.uint32)
+        ne = C.c_uint32()
+        N.check(self._lib.sh_spec_step_forced(self.h, target.h, draft.h, tcache.h, dcache.h, last_token, n,
+                                              fd.ctypes.data_as(N.U32P), emitted.ctypes.data_as(N.U32P),
+                                              C.byref(ne)))
+        em = emitted[: ne.value].tolist()
+        return SpecStepOut(em, ne.value - 1, em[-1], fd.tolist())
+
     def draft_tokens(self, draft: "Model", dcache: "KvCache", last_token: int, n_max: int) -> list:
         """Engine::draft_tokens (inference/mod.rs:2062-2092): greedy drafts of a separate
         draft model from its cache (pending tokens first); the cache advances by

@@ -192,3 +192,33 @@ def test_draft_tokens_with_pending_match_oracle(engine, replay):
     for x in (tkv, dkv, okv, gm, om):
         x.close()
     img.close()
+
+
+def test_forced_drafts_replay_the_greedy_continuation(engine):
+    """sh_spec_step_forced with the target's greedy continuation as drafts
+    accepts every draft; the emitted stream is that continuation and the
+    steps replay graphs (one shape with no pending token, one with)."""
+    print("forced-acceptance steps", flush=True)
+    ti, di, gt, gd = _models(engine, S.TINY_TARGET, S.TINY_DRAFT, 0, 1)
+    V, k = gt.dims.n_vocab, 5
+    prompt = S.tokens(77, 40, V)
+    # the continuation: single-token greedy forwards of the target
+    ckv = engine.allocate_kv_cache(gt, 512)
+    lg, _ = engine.forward_full_readback(gt, ckv, prompt, 0, full_logits=False, want_residual=False)
+    cont = [int(lg[0].argmax())]
+    for i in range(6 * (k + 1) + k):
+        cont.append(int(engine.verify_greedy(gt, ckv, [cont[-1]], len(prompt) + i)[0]))
+    ckv.close()
+    tkv, dkv, last = _prefilled(engine, gt, gd, prompt)
+    assert last == cont[0]
+    c0, l0 = engine.graph_stats()
+    j = 0
+    for step in range(6):
+        r = engine.decode_speculative_forced(gt, gd, tkv, dkv, cont[j], cont[j + 1:j + 1 + k])
+        assert r.emitted == cont[j + 1:j + 2 + k], step
+        j += len(r.emitted)
+        assert tkv.position == len(prompt) + j
+    c1, l1 = engine.graph_stats()
+    assert l1 - l0 == 6 and c1 - c0 >= 1
+    for x in (tkv, dkv, gt, gd, ti, di):
+        x.close()
