@@ -428,6 +428,9 @@ def main():
     ap.add_argument("--acceptance-only", action="store_true", help="only the configs[1] acceptance measurement")
     ap.add_argument("--draft-only", action="store_true", help="only the draft forward (eager, per-kernel events)")
     ap.add_argument("--profile-only", action="store_true")
+    ap.add_argument("--spec-eager", action="store_true",
+                    help="only greedy spec steps, launched kernel by kernel (no graph replay): the step's kernel mix "
+                         "for a kernel tracer")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build targets one MI355X; the verify path has no multi-GPU mode "
@@ -447,6 +450,8 @@ def main():
         with Engine(0) as eng:
             print(json.dumps({"metric": "moe spec decode", "moe_spec": measure_moe_spec(eng)}), flush=True)
         return
+    if args.spec_eager:
+        os.environ["SH_GRAPH"] = "0"  # read once, at the first step
     if args.draft_only:
         with Engine(0) as eng:
             print(json.dumps({"metric": "draft forward", "draft": measure_draft(eng, args.ctx)}), flush=True)
@@ -493,6 +498,17 @@ def main():
         last = int(np.argmax(lg[0]))
     last0 = last  # the token after the prefill: each stepped leg below starts from (P0, last0)
     log(f"prefill {P0} tokens in {time.time() - t0:.1f}s")
+    if args.spec_eager:
+        for i in range(args.warmup + args.steps):
+            if i == args.warmup:
+                eng.sync()
+                t = time.perf_counter()
+            last = eng.decode_speculative(tm, dm, tkv, dkv, last, args.k).last_token
+        eng.sync()
+        ms = (time.perf_counter() - t) * 1e3 / args.steps
+        print(json.dumps({"metric": "eager spec steps", "ms_per_step": round(ms, 4), "steps": args.steps,
+                          "graph_stats": eng.graph_stats()}), flush=True)
+        return
 
     # ---- verify step: latency + roofline (target only) -------------------
     vt = S.tokens(777, args.k + 1, V)

@@ -14,28 +14,30 @@
 // The f16 output is a sequential chain over the blocks (each step rounds), so
 // the work splits in two kernels:
 //   k_fa16:       everything that does not depend on the chain, in parallel
-//                 over (key split of 4 blocks, group of 32 query rows, kv
+//                 over (key split of kW blocks, group of 32 query rows, kv
 //                 head): per block S (one v_mfma_f32_16x16x32_f16 per 32 of
 //                 head_dim: K and the staged q are f16 already), the block
 //                 maxima, the running maximum M_j of every block (the maxima
 //                 of earlier splits arrive by a look-back over per-split
-//                 flags), P16, l_j = sum P and the block's f16 P V accumulator
+//                 words), P16, l_j = sum P and the block's f16 P V accumulator
 //                 (v_mfma_f32_16x16x16_f16 per 16-key chunk, rounded to f16
 //                 after each chunk); writes PV16_j, M_j and l_j per row.
-//   k_fa16_chain: one wave per (column, 256 outputs): the chain O16 <-
-//                 f16(f16(e_j) O16) + PV16_j (packed f16 multiply and add,
-//                 each rounded once) and L <- e_j L + l_j over the row's blocks,
-//                 then O = f32(O16) / L as the attention row and the Wo
-//                 operand; it also clears the look-back flags for the next
-//                 launch.
+//   k_fa16_chain: one workgroup per (column, 256 outputs): the rows' PV16_j
+//                 and (M_j, l_j) staged in LDS with all loads in flight, then
+//                 one output per thread: the chain O16 <- f16(f16(e_j) O16) +
+//                 PV16_j (f16 multiply and add, each rounded once) and L <-
+//                 e_j L + l_j over the row's blocks, then O = f32(O16) / L as
+//                 the attention row and the Wo operand; it also resets the
+//                 look-back words for the next launch.
 //
-// Look-back: the workgroup of split s publishes its 32 row maxima (agent-
-// coherent stores, sh_coherent.h) and then a flag, and waits for the flags of
-// splits 0 .. s-1 of its (row group, kv head) only. The split is the fastest
-// grid index, so those workgroups were dispatched before it (workgroups are
-// dispatched in order of their linear index) and none of them waits on it:
-// every wait ends. A spin bound keeps even a broken dispatch order from
-// hanging the GPU (the maxima then come out wrong, not stuck).
+// Look-back: the workgroup of split s publishes its 32 row maxima with
+// agent-coherent stores (sh_coherent.h) into words that hold kUnset until
+// then (the data is its own flag: a maximum is never that NaN pattern), and
+// polls the words of splits 0 .. s-1 of its (row group, kv head) only. The
+// split is the fastest grid index, so those workgroups were dispatched before
+// it (workgroups are dispatched in order of their linear index) and none of
+// them waits on it: every wait ends. A spin bound keeps even a broken dispatch
+// order from hanging the GPU (the maxima then come out wrong, not stuck).
 #include <cstdlib>
 
 #include "sh_internal.h"
@@ -52,7 +54,9 @@ struct alignas(16) u32x4a { uint32_t x, y, z, w; };
 
 constexpr float kNegBig = -1.0e30f;  // the shader's running-maximum start (NEG_BIG)
 constexpr int kW = 4;                // waves (64-key blocks) per split
+constexpr int kNG = 2 * kW;          // groups of 32 threads (look-back rows)
 constexpr uint32_t kSpinMax = 1u << 20;
+constexpr uint32_t kUnset = 0xFFFFFFFFu;  // a look-back word not yet published (a NaN: never a maximum)
 
 __device__ __forceinline__ h8 ld_h8(const uint16_t* p) { return __builtin_bit_cast(h8, *(const u32x4a*)p); }
 
@@ -83,8 +87,27 @@ __global__ __launch_bounds__(64 * kW) void k_fa16(Fa16Args a) {
   const uint32_t k0 = blk * 64;
   const uint32_t Dq = a.n_head * HD;
 
-  // every load first: K and V of the block (clamped rows stay in bounds and
-  // are masked), then the queries of the two 16-row tiles
+  // every load first, all in flight before any use: the queries of the two
+  // 16-row tiles (first: loads complete in order, so their staging waits for
+  // them only), then K and V of the block (clamped rows stay in bounds and are
+  // masked)
+  f4 qraw[2][NC][2];
+  uint32_t col[2];
+  bool rok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const uint32_t rho = rho0 + 16 * rt + r;
+    rok[rt] = rho < R;
+    const uint32_t rr = rok[rt] ? rho : 0u;
+    col[rt] = rr / a.gqa;
+    const float* qp = a.q + (size_t)col[rt] * Dq + (size_t)(kh * a.gqa + rr % a.gqa) * HD + 8 * g;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qraw[rt][c][0] = *(const f4*)(qp + 32 * c);
+      qraw[rt][c][1] = *(const f4*)(qp + 32 * c + 4);
+    }
+  }
+  asm volatile("" ::: "memory");  // the K / V loads stay behind the query loads
   const uint16_t* kbase = a.kc + (size_t)kh * a.max_seq * HD;
   const uint16_t* vbase = a.vc + (size_t)kh * (a.max_seq / 32) * HD * 32;
   h8 kop[4][NC], vop[2][DT];
@@ -100,30 +123,19 @@ __global__ __launch_bounds__(64 * kW) void k_fa16(Fa16Args a) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) vop[h][dt] = ld_h8(vbase + ((size_t)vb * HD + 16 * dt + r) * 32 + 8 * g);
   }
-  float4 qraw[2][NC][2];
-  uint32_t col[2];
-  bool rok[2];
+  asm volatile("" ::: "memory");  // ... and are all issued before the first use:
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const uint32_t rho = rho0 + 16 * rt + r;
-    rok[rt] = rho < R;
-    const uint32_t rr = rok[rt] ? rho : 0u;
-    col[rt] = rr / a.gqa;
-    const float* qp = a.q + (size_t)col[rt] * Dq + (size_t)(kh * a.gqa + rr % a.gqa) * HD + 8 * g;
+  for (int rt = 0; rt < 2; ++rt)  // the staging below cannot move above this point
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qraw[rt][c][0] = *(const float4*)(qp + 32 * c);
-      qraw[rt][c][1] = *(const float4*)(qp + 32 * c + 4);
-    }
-  }
+    for (int c = 0; c < NC; ++c) asm volatile("" : "+v"(qraw[rt][c][0]), "+v"(qraw[rt][c][1]));
   // staged queries: f16(q * qs), the f32 product rounded once more to f16
   h8 qop[2][NC];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const float x[8] = {qraw[rt][c][0].x, qraw[rt][c][0].y, qraw[rt][c][0].z, qraw[rt][c][0].w,
-                          qraw[rt][c][1].x, qraw[rt][c][1].y, qraw[rt][c][1].z, qraw[rt][c][1].w};
+      const float x[8] = {qraw[rt][c][0][0], qraw[rt][c][0][1], qraw[rt][c][0][2], qraw[rt][c][0][3],
+                          qraw[rt][c][1][0], qraw[rt][c][1][1], qraw[rt][c][1][2], qraw[rt][c][1][3]};
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         float y = x[t] * a.qs;
@@ -166,51 +178,49 @@ __global__ __launch_bounds__(64 * kW) void k_fa16(Fa16Args a) {
     bmx[rt] = m;
   }
   __shared__ float sbm[kW][32];
-  __shared__ float sred[8][32];
+  __shared__ float sred[kNG][32];
   __shared__ float sinc[32];
   if (g == 0) {
     sbm[wave][r] = bmx[0];
     sbm[wave][16 + r] = bmx[1];
   }
   __syncthreads();
-  // publish the split's row maxima, then its flag
+  // publish the split's row maxima
   const size_t sync0 = ((size_t)kh * a.n_rg + rg) * a.max_splits;
-  if (wave == 0) {
-    if (lane < 32) {
-      float m = sbm[0][lane];
+  if (wave == 0 && lane < 32) {
+    float m = sbm[0][lane];
 #pragma unroll
-      for (int w = 1; w < kW; ++w) m = fmaxf(m, sbm[w][lane]);
-      sh_st_coh4(a.smax + (sync0 + split) * 32 + lane, __builtin_bit_cast(uint32_t, m));
-    }
-    sh_stores_done();
-    if (lane == 0) __hip_atomic_store(a.flag + sync0 + split, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int w = 1; w < kW; ++w) m = fmaxf(m, sbm[w][lane]);
+    sh_st_coh4(a.smax + (sync0 + split) * 32 + lane, __builtin_bit_cast(uint32_t, m));
   }
-  // look-back: every earlier split's flag, then the maximum of their maxima
-  for (uint32_t j = threadIdx.x; j < split; j += 64 * kW) {
-    uint32_t spins = 0;
-    while (__hip_atomic_load(a.flag + sync0 + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-      if (++spins > kSpinMax) {
-        __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-  }
-  __syncthreads();
+  // look-back: the maxima of every earlier split, each word polled until set
   {
-    const uint32_t row = threadIdx.x & 31, jj = threadIdx.x >> 5;  // 8 groups of 32 rows
+    const uint32_t row = threadIdx.x & 31, jj = threadIdx.x >> 5;  // group jj: splits jj mod kNG
     float m = kNegBig;
-    for (uint32_t j0 = jj; j0 < split; j0 += 8 * 8) {
+    for (uint32_t j0 = jj; j0 < split; j0 += kNG * 8) {
       uint32_t v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const uint32_t j = j0 + 8 * u;
+        const uint32_t j = j0 + kNG * u;
         v[u] = j < split ? sh_ld_coh4(a.smax + (sync0 + j) * 32 + row) : __builtin_bit_cast(uint32_t, kNegBig);
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) sh_coh_wait(v[u]);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) m = fmaxf(m, __builtin_bit_cast(float, v[u]));
+      for (int u = 0; u < 8; ++u) {
+        uint32_t spins = 0;
+        while (v[u] == kUnset) {  // only words of earlier splits start unset
+          if (++spins > kSpinMax) {
+            __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v[u] = __builtin_bit_cast(uint32_t, kNegBig);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          v[u] = sh_ld_coh4(a.smax + (sync0 + j0 + kNG * u) * 32 + row);
+          sh_coh_wait(v[u]);
+        }
+        m = fmaxf(m, __builtin_bit_cast(float, v[u]));
+      }
     }
     sred[jj][row] = m;
   }
@@ -218,7 +228,7 @@ __global__ __launch_bounds__(64 * kW) void k_fa16(Fa16Args a) {
   if (threadIdx.x < 32) {
     float m = sred[0][threadIdx.x];
 #pragma unroll
-    for (int u = 1; u < 8; ++u) m = fmaxf(m, sred[u][threadIdx.x]);
+    for (int u = 1; u < kNG; ++u) m = fmaxf(m, sred[u][threadIdx.x]);
     sinc[threadIdx.x] = m;
   }
   __syncthreads();
@@ -279,63 +289,97 @@ __global__ __launch_bounds__(64 * kW) void k_fa16(Fa16Args a) {
 }
 
 // The output chain of the rows' blocks, then attn [N][Dq] and the Wo operand
-// (the hi/lo groups, or with bh the f16 rows of the wide f16 GEMM). Lane l of
-// wave (sb, col) owns outputs 256 sb + 4 l .. +3.
+// (the hi/lo groups, or with bh the f16 rows of the wide f16 GEMM). The
+// workgroup (sb, col) owns outputs 256 sb .. +255 of column col (NH heads of
+// HD); thread t owns output 256 sb + t. Blocks go through LDS in chunks of CB:
+// every thread first issues its 16 loads of the chunk's PV16 rows, then the
+// chain reads LDS.
 template <int HD>
-__global__ __launch_bounds__(64) void k_fa16_chain(Fa16Args a, float* __restrict__ attn, uint16_t* __restrict__ bx,
-                                                   uint16_t* __restrict__ xs, float* __restrict__ cs,
-                                                   uint16_t* __restrict__ bh) {
-  constexpr int CH = 16;
-  const uint32_t sb = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
-  {  // the look-back flags start at zero in the next launch
-    const uint32_t nflag = a.n_kv * a.n_rg * a.max_splits;
-    const uint32_t tid = (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane, nthr = gridDim.x * gridDim.y * 64;
-    for (uint32_t i = tid; i < nflag; i += nthr) a.flag[i] = 0u;
+__global__ __launch_bounds__(256) void k_fa16_chain(Fa16Args a, float* __restrict__ attn, uint16_t* __restrict__ bx,
+                                                    uint16_t* __restrict__ xs, float* __restrict__ cs,
+                                                    uint16_t* __restrict__ bh) {
+  constexpr int NH = 256 / HD, CB = 128, PPB = NH * HD / 8;  // 16-byte pieces per block
+  constexpr int NLD = CB * PPB / 256;                          // loads per thread per chunk
+  static_assert(NLD == 16, "16 loads per thread");
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  __shared__ u4v pvs[CB * PPB];  // [block][local head][d / 8]
+  __shared__ float2 mls[CB][NH];
+  __shared__ float outf[256];
+  const uint32_t sb = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+  {  // the look-back words start unset in the next launch
+    const uint32_t nword = a.n_kv * a.n_rg * a.max_splits * 32;
+    const uint32_t tid = (blockIdx.y * gridDim.x + blockIdx.x) * 256 + t, nthr = gridDim.x * gridDim.y * 256;
+    for (uint32_t i = tid; i < nword; i += nthr) a.smax[i] = __builtin_bit_cast(float, kUnset);
   }
   const uint32_t kb0 = a.dbase ? *a.dbase : 0u;
   const uint32_t kvlen = a.kvlen + kb0, mbase = a.mask_base + kb0;
-  const uint32_t Dq = a.n_head * HD, kk = 256 * sb + 4 * lane;
-  const bool valid = kk < Dq;
-  const uint32_t k = valid ? kk : 0u, head = k / HD, d = k % HD;
-  const uint32_t kh = head / a.gqa, rho = c * a.gqa + head % a.gqa, rg = rho / 32, row = rho % 32;
+  const uint32_t Dq = a.n_head * HD, h0 = 256 * sb / HD;
   const uint32_t nb = (min(mbase + c, kvlen - 1)) / 64 + 1;
-  const size_t base = ((size_t)kh * a.n_rg + rg) * a.nbmax;
-  const float2* ml = a.ml + base * 32 + row;
-  const uint16_t* pv = a.pv + (base * 32 + row) * HD + d;
+  // row of local head hh: kv head, row group and row of query row c * gqa + head % gqa
+  auto rowbase = [&](uint32_t hh) {
+    const uint32_t head = h0 + hh, kh = head / a.gqa, rho = c * a.gqa + head % a.gqa;
+    return (((size_t)kh * a.n_rg + rho / 32) * a.nbmax) * 32 + rho % 32;  // + 32 j: block j's row
+  };
+  const uint32_t hl = t / HD, d = t % HD;
+  const bool valid = 256 * sb + t < Dq;
   float Mp = kNegBig, L = 0.f;
-  h2 o01 = {(_Float16)0.f, (_Float16)0.f}, o23 = o01;
-  for (uint32_t j0 = 0; j0 < nb; j0 += CH) {
-    float2 m[CH];
-    uint2 p[CH];
+  _Float16 o = (_Float16)0.f;
+  for (uint32_t j0 = 0; j0 < nb; j0 += CB) {
+    const uint32_t nbc = min((uint32_t)CB, nb - j0);
+    u4v buf[NLD];
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const uint32_t j = min(j0 + u, nb - 1);
-      m[u] = ml[(size_t)j * 32];
-      p[u] = *(const uint2*)(pv + (size_t)j * 32 * HD);
+    for (int i = 0; i < NLD; ++i) {
+      const uint32_t p = t + 256 * i, jb = p / PPB, hh = (p % PPB) / (HD / 8), d8 = p % (HD / 8);
+      buf[i] = u4v{0u, 0u, 0u, 0u};
+      if (jb < nbc && h0 + hh < a.n_head)
+        buf[i] = *(const u4v*)(a.pv + (rowbase(hh) + 32 * (size_t)(j0 + jb)) * HD + 8 * d8);
+    }
+    for (uint32_t i = t; i < nbc * NH; i += 256) {
+      const uint32_t jb = i / NH, hh = i % NH;
+      if (h0 + hh < a.n_head) mls[jb][hh] = a.ml[rowbase(hh) + 32 * (size_t)(j0 + jb)];
     }
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      if (j0 + u >= nb) continue;
-      const float e = __builtin_amdgcn_exp2f(Mp - m[u].x);
-      L = e * L + m[u].y;
-      const _Float16 eh = (_Float16)e;
-      const h2 e2 = {eh, eh};
-      const h2 p01 = __builtin_bit_cast(h2, p[u].x), p23 = __builtin_bit_cast(h2, p[u].y);
-      o01 = o01 * e2;  // f16(f16(e) O16)
-      o23 = o23 * e2;
-      asm volatile("" : "+v"(o01), "+v"(o23));  // two roundings, not a fused multiply-add
-      o01 = o01 + p01;  // f16(O16 + PV16)
-      o23 = o23 + p23;
-      Mp = m[u].x;
+    for (int i = 0; i < NLD; ++i) {
+      const uint32_t p = t + 256 * i, jb = p / PPB, hh = (p % PPB) / (HD / 8);
+      if (jb < nbc && h0 + hh < a.n_head) pvs[p] = buf[i];
     }
+    __syncthreads();
+    if (valid) {
+      const _Float16* pvh = reinterpret_cast<const _Float16*>(pvs) + hl * HD + d;
+      for (uint32_t jb0 = 0; jb0 < nbc; jb0 += 8) {
+        // 8 blocks' LDS reads in flight, then their steps
+        float2 m[8];
+        _Float16 p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const uint32_t jb = min(jb0 + u, nbc - 1);
+          m[u] = mls[jb][hl];
+          p[u] = pvh[(size_t)jb * PPB * 8];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (jb0 + u >= nbc) break;
+          const float e = __builtin_amdgcn_exp2f(Mp - m[u].x);
+          L = e * L + m[u].y;
+          o = o * (_Float16)e;  // f16(f16(e) O16)
+          asm volatile("" : "+v"(o));  // two roundings, not a fused multiply-add
+          o = o + p[u];  // f16(O16 + PV16)
+          Mp = m[u].x;
+        }
+      }
+    }
+    __syncthreads();
   }
   const float il = L == 0.f ? 0.f : 1.0f / L;
-  float4 v = make_float4((float)o01[0] * il, (float)o01[1] * il, (float)o23[0] * il, (float)o23[1] * il);
-  if (!valid) v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (valid) *(float4*)(attn + (size_t)(a.col0 + c) * Dq + k) = v;
+  outf[t] = valid ? (float)o * il : 0.f;
+  __syncthreads();
+  if (t >= 64) return;
+  const float4 v = make_float4(outf[4 * t], outf[4 * t + 1], outf[4 * t + 2], outf[4 * t + 3]);
+  const uint32_t k = 256 * sb + 4 * t;
+  if (k < Dq) *(float4*)(attn + (size_t)(a.col0 + c) * Dq + k) = v;
   if (bh) {
     const h4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-    if (valid) *(uint2*)(bh + (size_t)(a.col0 + c) * Dq + k) = __builtin_bit_cast(uint2, h);
+    if (k < Dq) *(uint2*)(bh + (size_t)(a.col0 + c) * Dq + k) = __builtin_bit_cast(uint2, h);
   } else {
     sh_operand_store_sb(v, Dq, sb, a.col0 + c, bx, xs, cs);
   }
@@ -380,7 +424,7 @@ int sh_fa16_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArg
   SH_CHECK(sh_fa16_pv_halves(m->n_kv, m->hd, gqa, fa.N, kv_grid) <= w.fa16_pv_halves &&
                sh_fa16_sync_words(m->n_kv, gqa, fa.N, kv_grid) <= w.fa16_sync_words,
            SH_ERR_CAPACITY, "cm1 attention buffers too small");
-  a.pv = w.fa16_pv; a.ml = w.fa16_ml; a.smax = w.fa16_smax; a.flag = w.fa16_flag; a.err = w.fa16_flag + w.fa16_sync_words;
+  a.pv = w.fa16_pv; a.ml = w.fa16_ml; a.smax = w.fa16_smax; a.err = w.fa16_flag + w.fa16_sync_words;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   const dim3 grid(a.max_splits, a.n_rg, m->n_kv);
@@ -391,9 +435,9 @@ int sh_fa16_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArg
   sh_prof_begin(e, &ev);
   const dim3 cgrid((m->n_head * m->hd + 255) / 256, fa.N);
   if (m->hd == 128)
-    hipLaunchKernelGGL(k_fa16_chain<128>, cgrid, dim3(64), 0, e->stream, a, attn_out, bx, xs, cs, bh);
+    hipLaunchKernelGGL(k_fa16_chain<128>, cgrid, dim3(256), 0, e->stream, a, attn_out, bx, xs, cs, bh);
   else
-    hipLaunchKernelGGL(k_fa16_chain<64>, cgrid, dim3(64), 0, e->stream, a, attn_out, bx, xs, cs, bh);
+    hipLaunchKernelGGL(k_fa16_chain<64>, cgrid, dim3(256), 0, e->stream, a, attn_out, bx, xs, cs, bh);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "attn_combine", 0.0, ev);
   return SH_OK;

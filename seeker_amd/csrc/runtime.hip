@@ -1177,6 +1177,7 @@ static int ensure_fa16(sh_model* m, uint32_t kv_cap, uint32_t ncol) {
   SH_HIP(hipMalloc(&w.fa16_smax, W * 32 * sizeof(float)));
   SH_HIP(hipMalloc(&w.fa16_flag, (W + 1) * sizeof(uint32_t)));
   SH_HIP(hipMemsetAsync(w.fa16_flag, 0, (W + 1) * sizeof(uint32_t), m->e->stream));
+  SH_HIP(hipMemsetAsync(w.fa16_smax, 0xFF, W * 32 * sizeof(float), m->e->stream));  // look-back words unset
   w.fa16_pv_halves = P;
   w.fa16_sync_words = W;
   return SH_OK;

@@ -476,9 +476,8 @@ struct Fa16Args {
   float qs = 0.f;  // f32(f32(1 / sqrt(hd)) * f32(log2 e))
   uint16_t* pv = nullptr;
   float2* ml = nullptr;
-  float* smax = nullptr;
-  uint32_t* flag = nullptr;
-  uint32_t* err = nullptr;
+  float* smax = nullptr;   // look-back words [n_kv][n_rg][max_splits][32], unset between launches
+  uint32_t* err = nullptr;  // set when a look-back wait gave up
 };
 int sh_fa16_launch(sh_engine* e, const sh_model* m, const sh_kv* kv, const FaArgs& fa, const float* q,
                    float* attn_out, uint16_t* bx, uint16_t* xs, float* cs, uint16_t* bh = nullptr);
