@@ -434,7 +434,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build targets one MI355X; the verify path has no multi-GPU mode "
-              "(batch-1 verify does not shard profitably, see DESIGN.md)", file=sys.stderr)
+              "(a batch-1 verify does not shard profitably: tensor parallelism would add two all-reduces "
+              "per layer)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

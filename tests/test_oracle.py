@@ -1,7 +1,7 @@
 """CPU tests that pin the C oracle before it is trusted as the parity reference.
 
 What pins each oracle function (the reference ships no golden vectors for this
-path, SURVEY 8c; its only checks are closed-form inputs + CPU restatements):
+path; its only checks are closed-form inputs + CPU restatements):
 
   or_f16_to_f32 / or_f32_to_f16  exhaustive / randomized vs numpy float16 (IEEE RNE)
   or_philox4x64_10 / word         numpy.random.Philox raw words (tests/golden fixture)
