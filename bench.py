@@ -431,6 +431,7 @@ def main():
     ap.add_argument("--spec-eager", action="store_true",
                     help="only greedy spec steps, launched kernel by kernel (no graph replay): the step's kernel mix "
                          "for a kernel tracer")
+    ap.add_argument("--spec-mode", type=int, default=0, help="sampling mode of --spec-eager (0 greedy, 2 REJECTION)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build targets one MI355X; the verify path has no multi-GPU mode "
@@ -500,11 +501,16 @@ def main():
     last0 = last  # the token after the prefill: each stepped leg below starts from (P0, last0)
     log(f"prefill {P0} tokens in {time.time() - t0:.1f}s")
     if args.spec_eager:
+        s = None
+        if args.spec_mode:
+            from seeker_amd._native import sh_sampling
+            s = sh_sampling()
+            s.mode, s.temperature, s.seed, s.counter = args.spec_mode, 0.8, 5, 0
         for i in range(args.warmup + args.steps):
             if i == args.warmup:
                 eng.sync()
                 t = time.perf_counter()
-            last = eng.decode_speculative(tm, dm, tkv, dkv, last, args.k).last_token
+            last = eng.decode_speculative(tm, dm, tkv, dkv, last, args.k, s).last_token
         eng.sync()
         ms = (time.perf_counter() - t) * 1e3 / args.steps
         print(json.dumps({"metric": "eager spec steps", "ms_per_step": round(ms, 4), "steps": args.steps,

@@ -1652,7 +1652,7 @@ static int spec_bufs(sh_engine* e, uint32_t V) {
   SH_HIP(hipMalloc(&sb.dlogits, (size_t)8 * V * 4));
   SH_HIP(hipMalloc(&sb.tlogits, (size_t)9 * V * 4));
   SH_HIP(hipMalloc(&sb.udev, 32 * 4));
-  SH_HIP(hipMalloc(&sb.rowstat, 256 * sizeof(double2)));
+  SH_HIP(hipMalloc(&sb.rowstat, SpecBufs::kRowstatBytes));
   SH_HIP(hipHostMalloc((void**)&sb.pinned, 128 * 4, hipHostMallocDefault));
   sb.vcap = V;
   return SH_OK;
@@ -1795,7 +1795,7 @@ static int enqueue_stoch_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* t
     if (rc) return rc;
     uint32_t* dst = e->spec.tok + np + 1 + i;
     rc = rej ? sh_sample_rows_launch(e, q, 1, V, s->temperature, udev, s->seed, ctr + 2ull * (n + 1) + i, 1,
-                                     e->spec.rowstat, dst, rng)
+                                     e->spec.rowstat, SpecBufs::kRowstatBytes, dst, rng)
              : sh_argmax_launch(e, q, V, 1, dm->ws.amax, dst);
     if (rc) return rc;
   }

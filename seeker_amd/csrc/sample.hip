@@ -19,6 +19,7 @@
 #include <mutex>
 
 #include "sh_internal.h"
+#include "sh_coherent.h"
 #include "sh_exp.h"
 #include "sh_philox.h"
 
@@ -114,13 +115,19 @@ __device__ __forceinline__ double2 reduce_unit(const float (&v)[E], double inv_t
   return make_double2((double)mx, block_sum_d(s, shd));
 }
 
+constexpr uint32_t kCntStride = 64;  // arrival counters 256 bytes apart: no two share a cache line
+
 template <bool VEC, int E>
 __global__ __launch_bounds__(256) void k_row_part(const float* __restrict__ p, uint32_t n_p,
                                                   const float* __restrict__ q, uint32_t V, double inv_t,
                                                   uint32_t nch, double2* __restrict__ part,
-                                                  const SampRow* __restrict__ rows = nullptr) {
+                                                  const SampRow* __restrict__ rows = nullptr,
+                                                  uint32_t* __restrict__ zero_cnt = nullptr, uint32_t nzero = 0) {
   __shared__ float shf[4];
   __shared__ double shd[4];
+  // the arrival counters of the kernel that follows start at zero
+  if (zero_cnt && blockIdx.x == 0)
+    for (uint32_t j = threadIdx.x; j < nzero; j += 256) zero_cnt[(size_t)j * kCntStride] = 0u;
   float v[E];
   load_unit<VEC, E>(p, n_p, q, V, nch, blockIdx.x, v);
   if (rows) inv_t = rows[blockIdx.x / nch].inv_t;  // per-row temperature (a row's units are consecutive)
@@ -563,6 +570,92 @@ __device__ uint32_t sample_filtered_row(const float* __restrict__ x, uint32_t V,
   }
   __syncthreads();
   return ~(uint32_t)(cand[s_ch] & 0xFFFFFFFFull);
+}
+
+// k_sample_cols for rows of many logits, spread over kSampChunks workgroups
+// per row (grid (chunk c, row)): each sums its chunk's softmax numerators
+// (the weights k_sample_cols sums, in f64) and stores the sum at agent scope;
+// the last workgroup of the row to arrive (a counter zeroed by k_row_part,
+// reset by that workgroup) scans the chunk sums in vocab order for the first
+// chunk whose running sum reaches u * total and draws inside it, as
+// k_sample_cols does over the whole row (first v whose running sum reaches
+// u * total).
+constexpr uint32_t kSampChunks = 64;
+__global__ __launch_bounds__(256) void k_sample_chunks(const float* __restrict__ p, const double2* __restrict__ part,
+                                                       uint32_t nch, uint32_t V, double inv_t, const float* u_dev,
+                                                       uint64_t seed, uint64_t word0, uint64_t wstride,
+                                                       double2* __restrict__ csum, uint32_t* __restrict__ cnt,
+                                                       uint32_t* __restrict__ out, const uint64_t* rng) {
+  static_assert(kSampChunks == 64, "one lane per chunk");
+  constexpr int kPer = 8;  // elements per thread per pass
+  __shared__ double tab[64];
+  __shared__ double2 st;
+  __shared__ double shd[4];
+  __shared__ uint32_t s_last, s_c;
+  __shared__ double s_off, s_target;
+  const uint32_t c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+  rng_from_dev(rng, seed, word0);
+  load_exp_table(tab);
+  __syncthreads();
+  if (t < 64) {
+    const double2 s2 = wave_row_stat(part + (size_t)row * nch, nch, inv_t, tab);
+    if (t == 0) st = s2;
+  }
+  __syncthreads();
+  const float* pr = p + (size_t)row * V;
+  const RowW rw{pr, nullptr, st.x, 1.0, 0.0, 1.0, inv_t, tab};
+  const uint32_t CH = (V + kSampChunks - 1) / kSampChunks, lo = min(c * CH, V), hi = min(lo + CH, V);
+  double ps = 0.0;
+  for (uint32_t v0 = lo; v0 < hi; v0 += 256 * kPer) {
+    float x[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const uint32_t v = v0 + j * 256 + t;
+      x[j] = v < hi ? pr[v] : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) ps += rw.num(x[j]);
+  }
+  ps = block_sum_d(ps, shd);
+  if (t == 0) {
+    sh_st_coh16(csum + (size_t)row * kSampChunks + c, sh_pack_d2(ps, 0.0));
+    sh_stores_done();
+    uint32_t* cr = cnt + (size_t)row * kCntStride;
+    const uint32_t old = __hip_atomic_fetch_add(cr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = old + 1 == kSampChunks;
+    if (last) __hip_atomic_store(cr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;  // uniform in the workgroup
+  if (t < 64) {
+    sh_f4v cv = sh_ld_coh16(csum + (size_t)row * kSampChunks + t);
+    sh_coh_wait(cv);
+    double w, unused;
+    sh_unpack_d2(cv, w, unused);
+    double inc = w;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const double y = __shfl_up(inc, off);
+      if (t >= (uint32_t)off) inc += y;
+    }
+    const double total = __shfl(inc, 63);
+    const double target = (double)uniform_at(u_dev, seed, word0 + wstride * row) * total;
+    const unsigned long long over = __ballot(inc >= target);
+    const uint32_t cs = over ? (uint32_t)__builtin_ctzll(over) : 63u;
+    double ex = __shfl_up(inc, 1);
+    if (t == 0) ex = 0.0;
+    ex = __shfl(ex, cs);
+    if (t == 0) {
+      s_c = cs;
+      s_off = ex;
+      s_target = target;
+    }
+  }
+  __syncthreads();
+  const uint32_t plo = min(s_c * CH, V), phi = min(plo + CH, V);
+  const uint32_t tok = wg_inverse_cdf(rw, plo, phi, false, 0.f, s_off, s_target, true, nullptr);
+  if (t == 0) out[row] = tok;
 }
 
 // COMPARE with filters: row r of p draws with Philox word word0 + wstride r
@@ -1110,13 +1203,49 @@ __global__ __launch_bounds__(256) void k_tree_pass(const float* __restrict__ p, 
 
 }  // namespace
 
+// Rows of at least this many logits draw through k_sample_chunks.
+constexpr uint32_t kChunkedMinV = 8192;
+static size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+// The chunked draw's chunk sums and arrival counters for nrows rows.
+static size_t chunked_bytes(uint32_t nrows) {
+  return round256((size_t)nrows * kSampChunks * sizeof(double2)) + (size_t)nrows * kCntStride * 4;
+}
+
 size_t sh_accept_scratch_bytes(uint32_t B, uint32_t k, uint32_t V, uint32_t mode) {
   const uint32_t n_p = B * (k + 1), n_q = mode == SH_SAMPLE_REJECTION ? B * k : 0;
   const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
   const size_t part_b = (size_t)(n_p + n_q) * nch * sizeof(double2);
   const size_t chunk_b = (size_t)B * kDrawChunks * sizeof(double2), rstat_b = (size_t)B * 2 * sizeof(double2);
   const size_t small_b = mode == SH_SAMPLE_COMPARE ? (size_t)n_p * 4 : (size_t)B * 4;
-  return part_b + chunk_b + rstat_b + (small_b + 255) / 256 * 256;
+  const size_t samp_b = mode == SH_SAMPLE_COMPARE && V >= kChunkedMinV ? chunked_bytes(n_p) : 0;
+  return round256(part_b + chunk_b + rstat_b + round256(small_b)) + samp_b;
+}
+
+size_t sh_sample_rows_scratch_bytes(uint32_t nrows, uint32_t V) {
+  const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
+  return round256((size_t)nrows * nch * sizeof(double2)) + (V >= kChunkedMinV ? chunked_bytes(nrows) : 0);
+}
+
+// COMPARE draws of nrows rows of p: over the whole row per workgroup, or for
+// wide rows in kSampChunks chunks per row (scratch at samp: chunked_bytes).
+static void launch_sample_cols(sh_engine* e, const float* p, const double2* part, uint32_t nch, uint32_t nrows,
+                               uint32_t V, double inv_t, const float* u_dev, uint64_t seed, uint64_t word0,
+                               uint64_t wstride, char* samp, uint32_t* out, const uint64_t* rng) {
+  if (V >= kChunkedMinV) {
+    double2* csum = reinterpret_cast<double2*>(samp);
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(samp + round256((size_t)nrows * kSampChunks * sizeof(double2)));
+    hipLaunchKernelGGL(k_sample_chunks, dim3(kSampChunks, nrows), dim3(256), 0, e->stream, p, part, nch, V, inv_t,
+                       u_dev, seed, word0, wstride, csum, cnt, out, rng);
+  } else {
+    hipLaunchKernelGGL(k_sample_cols, dim3(nrows), dim3(256), 0, e->stream, p, part, nch, V, inv_t, u_dev, seed,
+                       word0, wstride, out, rng);
+  }
+}
+// The counters k_row_part zeroes for launch_sample_cols (null: none).
+static uint32_t* sample_cols_cnt(char* samp, uint32_t nrows, uint32_t V) {
+  return V >= kChunkedMinV ? reinterpret_cast<uint32_t*>(samp + round256((size_t)nrows * kSampChunks *
+                                                                                sizeof(double2)))
+                           : nullptr;
 }
 
 int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits, const uint32_t* drafts, uint32_t B,
@@ -1147,15 +1276,18 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
   double2* chunk = reinterpret_cast<double2*>(sbuf + part_b);
   double2* rstat = reinterpret_cast<double2*>(sbuf + part_b + chunk_b);
   uint32_t* small = reinterpret_cast<uint32_t*>(sbuf + part_b + chunk_b + rstat_b);
+  const size_t small_b = mode == SH_SAMPLE_COMPARE ? (size_t)n_p * 4 : (size_t)B * 4;
+  char* samp = sbuf + round256(part_b + chunk_b + rstat_b + round256(small_b));  // the chunked COMPARE draw
+  uint32_t* zc = mode == SH_SAMPLE_COMPARE ? sample_cols_cnt(samp, n_p, V) : nullptr;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   if (filt.top_k) {  // the filtered draw reads its rows itself
   } else if (V % 4 == 0) {
     hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nunits), dim3(256), 0, e->stream, p_logits, n_p, q_logits,
-                       V, inv_t, nch, part);
+                       V, inv_t, nch, part, nullptr, zc, n_p);
   } else {
     hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nunits), dim3(256), 0, e->stream, p_logits, n_p, q_logits,
-                       V, inv_t, nch, part);
+                       V, inv_t, nch, part, nullptr, zc, n_p);
   }
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "accept_stats", 4.0 * V * (n_p + n_q), ev);
@@ -1167,8 +1299,8 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
     hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
                        next_tok);
   } else if (mode == SH_SAMPLE_COMPARE) {
-    hipLaunchKernelGGL(k_sample_cols, dim3(n_p), dim3(256), 0, e->stream, p_logits, part, nch, V, inv_t,
-                       uniforms_dev, s->seed, counter + 1ull, 2ull, small, rng_dev);
+    launch_sample_cols(e, p_logits, part, nch, n_p, V, inv_t, uniforms_dev, s->seed, counter + 1ull, 2ull, samp,
+                       small, rng_dev);
     hipLaunchKernelGGL(k_decide_compare, dim3((B + 63) / 64), dim3(64), 0, e->stream, small, drafts, B, k, acc_len,
                        next_tok);
   } else {
@@ -1185,21 +1317,25 @@ int sh_accept_launch(sh_engine* e, const float* p_logits, const float* q_logits,
 }
 
 int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
-                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out,
-                          const uint64_t* rng_dev) {
+                          uint64_t seed, uint64_t word0, uint64_t wstride, void* scratch, size_t scratch_bytes,
+                          uint32_t* out, const uint64_t* rng_dev) {
   SH_CHECK(nrows >= 1 && V >= 1 && T > 0.f, SH_ERR_ARG, "sample_rows: nrows=%u V=%u T=%g", nrows, V, (double)T);
+  SH_CHECK(sh_sample_rows_scratch_bytes(nrows, V) <= scratch_bytes, SH_ERR_CAPACITY,
+           "sample_rows: scratch of %zu bytes below %zu", scratch_bytes, sh_sample_rows_scratch_bytes(nrows, V));
   const double inv_t = 1.0 / (double)T;
   const uint32_t nch = (V + 256 * kStatE - 1) / (256 * kStatE);
+  double2* part = static_cast<double2*>(scratch);
+  char* samp = static_cast<char*>(scratch) + round256((size_t)nrows * nch * sizeof(double2));
+  uint32_t* zc = sample_cols_cnt(samp, nrows, V);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   if (V % 4 == 0)
     hipLaunchKernelGGL((k_row_part<true, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
-                       nullptr, V, inv_t, nch, part);
+                       nullptr, V, inv_t, nch, part, nullptr, zc, nrows);
   else
     hipLaunchKernelGGL((k_row_part<false, kStatE>), dim3(nrows * nch), dim3(256), 0, e->stream, logits, nrows,
-                       nullptr, V, inv_t, nch, part);
-  hipLaunchKernelGGL(k_sample_cols, dim3(nrows), dim3(256), 0, e->stream, logits, part, nch, V, inv_t, u_dev, seed,
-                     word0, wstride, out, rng_dev);
+                       nullptr, V, inv_t, nch, part, nullptr, zc, nrows);
+  launch_sample_cols(e, logits, part, nch, nrows, V, inv_t, u_dev, seed, word0, wstride, samp, out, rng_dev);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "sample_rows", 4.0 * V * nrows, ev);
   return SH_OK;

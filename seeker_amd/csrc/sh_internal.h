@@ -67,7 +67,8 @@ struct SpecBufs {
   float* dlogits = nullptr;    // draft logits [8][V] of the last stochastic step
   float* tlogits = nullptr;    // target logits [9][V] of the last stochastic step
   float* udev = nullptr;       // [32] explicit uniforms of a stochastic step
-  double2* rowstat = nullptr;  // [256] row-statistics partials of the device draft draws
+  static constexpr size_t kRowstatBytes = 16384;  // scratch of the device draft draws (one row)
+  double2* rowstat = nullptr;  // the device draft draws' scratch (sh_sample_rows_launch)
   uint64_t* rng = nullptr;     // = base + 4: Philox key and word base of a replayed stochastic step
   uint32_t* pinned = nullptr;  // host staging [128]; [64..71] go to base[0..7]
   uint32_t vcap = 0;
@@ -522,8 +523,11 @@ int sh_argmax_launch(sh_engine* e, const float* logits, uint32_t V, uint32_t N, 
 // 8192) row-statistics partials of scratch. rng_dev (graph replay): the key
 // and a word base added to word0 are read from the device words rng_dev[0..1].
 int sh_sample_rows_launch(sh_engine* e, const float* logits, uint32_t nrows, uint32_t V, float T, const float* u_dev,
-                          uint64_t seed, uint64_t word0, uint64_t wstride, double2* part, uint32_t* out,
-                          const uint64_t* rng_dev = nullptr);
+                          uint64_t seed, uint64_t word0, uint64_t wstride, void* scratch, size_t scratch_bytes,
+                          uint32_t* out, const uint64_t* rng_dev = nullptr);
+// Device scratch sh_sample_rows_launch needs: row-statistics partials and, for
+// rows of many logits, the chunked draw's sums and counters.
+size_t sh_sample_rows_scratch_bytes(uint32_t nrows, uint32_t V);
 // Per-row parameters of the batched verify's column sampling.
 struct SampRow {
   double inv_t;       // 1 / temperature
