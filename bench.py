@@ -285,6 +285,55 @@ def measure_tree(eng, tm, d, P=8192, reps=3):
             "kernel_ms": kern}
 
 
+def measure_q4km(eng, P=4096, L=8, reps=30):
+    """The configs[2] verify (L = 8 at context 4096) on a Q4_K_M-style 8B: the
+    attn_v and ffn_down of every other layer and output.weight in Q6_K, the rest
+    Q4_K (llama.cpp's Q4_K_M mix). Such a model runs on the multi-group path
+    (graph-replayed), not on the tuned uniform-Q4_K GEMVs. KV positions set
+    without a prefill. Algorithmic bytes: the model's weight bytes (Q6_K at
+    210 B per 256 elements) + K/V read and written."""
+    import dataclasses
+    import numpy as np
+    from seeker_amd import synth as S
+    from seeker_amd._native import GGML_Q6_K
+    sh = dataclasses.replace(S.L8B_TARGET, out_type=GGML_Q6_K, mix=1)
+    t0 = time.time()
+    img = S.GgufImage(sh, seed=3)
+    m = eng.upload_weights(img)
+    img.close()
+    log(f"Q4_K_M-style 8B synthesized and uploaded in {time.time() - t0:.1f}s")
+    d = m.dims
+    kv = eng.allocate_kv_cache(m, P + 64)
+    toks = S.tokens(778, L, d.n_vocab)
+    times = []
+    for i in range(reps + 3):
+        kv.set_position(P)
+        eng.sync()
+        t = time.perf_counter()
+        eng.verify_greedy(m, kv, toks, P)
+        if i >= 3:
+            times.append((time.perf_counter() - t) * 1e3)
+    kv.set_position(P)
+    eng.set_profiling(True)
+    eng.profile(reset=True)
+    eng.verify_greedy(m, kv, toks, P)
+    prof = eng.profile(reset=True)
+    eng.set_profiling(False)
+    for n, st in sorted(prof.items(), key=lambda kv_: -kv_[1]["ms"]):
+        log(f"  {n:16s} {st['launches']:4d}/step {st['ms']:8.3f} ms/step")
+    _, kvr, kvw = verify_bytes(d, P, L)
+    wb = int(d.weight_bytes)
+    ms = statistics.median(times)
+    kv.close()
+    m.close()
+    log(f"Q4_K_M-style 8B verify (L={L}, P={P}): {ms:.3f} ms, {(wb + kvr + kvw) / ms / 1e6:.0f} GB/s")
+    return {"config": "Llama-3-8B shape, Q4_K_M-style mix (Q6_K attn_v / ffn_down of even layers and output), "
+                      f"L={L}, ctx {P}, multi-group path, graph-replayed",
+            "ms": round(ms, 4), "alg_bytes": wb + kvr + kvw,
+            "GBps": round((wb + kvr + kvw) / ms / 1e6, 1),
+            "frac": round((wb + kvr + kvw) / ms / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 def measure_moe(eng, P=16384, B=8, L=7, reps=5):
     """batched verify (sh_verify_unified) of B = 8 sequences x L = k+1 = 7
     columns on the Qwen3-30B-A3B-shape Q4_K MoE target (48 layers, d 2048, 32 / 4
@@ -423,6 +472,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel, tree and MoE lines")
     ap.add_argument("--moe-only", action="store_true", help="only the configs[4] MoE verify measurement")
+    ap.add_argument("--q4km-only", action="store_true", help="only the Q4_K_M-style 8B verify measurement")
     ap.add_argument("--moe-spec-only", action="store_true", help="only the configs[4] batched spec-decode measurement")
     ap.add_argument("--tree-only", action="store_true", help="only the configs[3] tree verify measurement")
     ap.add_argument("--acceptance-only", action="store_true", help="only the configs[1] acceptance measurement")
@@ -457,6 +507,10 @@ def main():
     if args.draft_only:
         with Engine(0) as eng:
             print(json.dumps({"metric": "draft forward", "draft": measure_draft(eng, args.ctx)}), flush=True)
+        return
+    if args.q4km_only:
+        with Engine(0) as eng:
+            print(json.dumps({"metric": "Q4_K_M-style 8B verify", "q4km_verify": measure_q4km(eng)}), flush=True)
         return
     if args.acceptance_only:
         with Engine(0) as eng:
@@ -680,6 +734,7 @@ def main():
         "parity": parity,
         "acceptance_kernel": extra_acc,
         "tree_verify": extra_tree,
+        "q4km_verify": None,
         "moe_verify": None,
         "moe_spec": None,
     }
@@ -688,6 +743,7 @@ def main():
     timg.close()
     dimg.close()
     if not args.no_extra:  # the 8B models are freed first: the MoE target is 17 GB
+        out["q4km_verify"] = measure_q4km(eng)
         out["moe_verify"] = measure_moe(eng)
         out["moe_spec"] = measure_moe_spec(eng)
     print(json.dumps(out), flush=True)

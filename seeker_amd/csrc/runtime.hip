@@ -971,9 +971,25 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     pending = 0;
     return sh_prep_launch(e, pr);
   };
+  // At most 8 columns (one operand group), a Q4_K matrix takes the tuned GEMVs
+  // of the fused path: the same split-partial layout and operand, and the
+  // deep ring (one split) for the 8B-size gate/up. Mixed-type models
+  // (Q4_K_M-style) and qwen3 chains keep this path for their structure and get
+  // those kernels for their Q4_K matrices.
+  static const bool tuned_small = [] {
+    const char* s = getenv("SH_MG_TUNED");
+    return !(s && atoi(s) == 0);
+  }();
   auto gemm = [&](const QMat& q, EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* np) {
-    return f16 ? sh_gemm16_launch(e, q, w.bh, q.K, nc, epi, ea, tag, np)
-               : sh_gemm_launch(e, q, w.bx, w.xs, w.cs, nc, epi, ea, tag, np);
+    if (f16) return sh_gemm16_launch(e, q, w.bh, q.K, nc, epi, ea, tag, np);
+    if (tuned_small && nc <= 8 && q.type == GGML_Q4_K && (epi == EPI_PART || epi == EPI_STORE)) {
+      if (epi == EPI_PART && sh_gemv_ring_t(q) && q.tiles % 7 == 0) {
+        if (np) *np = 1;
+        return sh_gemv_ring_launch(e, q, w.bx, w.xs, nc, EPI_PART, ea, tag, nullptr);
+      }
+      return sh_gemv_launch(e, q, w.bx, w.xs, nc, epi, ea, tag, np);
+    }
+    return sh_gemm_launch(e, q, w.bx, w.xs, w.cs, nc, epi, ea, tag, np);
   };
   // batched attention: one plan for the chunk's segments, one launch per layer
   // a causal single-sequence call (m->call_cm1): the chunk's columns as one
