@@ -1857,7 +1857,7 @@ __global__ __launch_bounds__(512) void k_gemm16h_q4k(const uint8_t* __restrict__
 // 4 rows per thread, the split sum, then RoPE and the KV-cache writes.
 __global__ __launch_bounds__(64) void k_qkv_finish(const float* __restrict__ part, uint32_t nparts,
                                                    size_t part_stride, uint32_t ldp, EpiArgs ea, QkvCols qc) {
-  const uint32_t col = blockIdx.y, r0 = 4 * (blockIdx.x * 64 + threadIdx.x);
+  const uint32_t col = blockIdx.y, r0 = qc.row0 + 4 * (blockIdx.x * 64 + threadIdx.x);
   if (r0 >= ea.Dq + 2 * ea.Dkv) return;
   const float* p = part + (size_t)col * ldp + r0;
   if (qc.vpart && r0 >= ea.Dq + ea.Dkv) {  // v rows of their own matrix (4 rows never straddle: hd % 4 == 0)
@@ -2858,7 +2858,9 @@ int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_
   SH_CHECK(N >= 1 && N <= (qc.tab ? (uint32_t)SH_MAX_COLS16 : (uint32_t)SH_MAX_COLS) && ea.hd % 4 == 0, SH_ERR_ARG,
            "qkv finish shape");
   SH_CHECK(!(qc.tab && ea.dbase), SH_ERR_ARG, "qkv finish: a device column table has no graph base");
-  const uint32_t rows = ea.Dq + 2 * ea.Dkv;
+  SH_CHECK(qc.row0 % 4 == 0 && qc.row0 < ea.Dq + 2 * ea.Dkv && (qc.row0 < ea.Dq + ea.Dkv || qc.vpart), SH_ERR_ARG,
+           "qkv finish: first row %u", qc.row0);
+  const uint32_t rows = ea.Dq + 2 * ea.Dkv - qc.row0;
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
   hipLaunchKernelGGL(k_qkv_finish, dim3((rows / 4 + 63) / 64, N), dim3(64), 0, e->stream, part, nparts, part_stride,

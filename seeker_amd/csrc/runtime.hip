@@ -355,11 +355,18 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
       ok = ok && kq(L.wqkv) && (!L.wv.d || kq(L.wv)) && kq(L.wo) &&
            (m->n_expert ? kq(L.wgu_exps) && kq(L.wdown_exps) : kq(L.wgu) && kq(L.wdown));
     m->mg_ok = ok;
-    bool fused = m->arch == ARCH_LLAMA && (m->lm_head.type == GGML_Q4_K || m->lm_head.type == GGML_Q8_0);
+    // fused path: llama, QKV / Wo / gate-up of every layer uniformly Q4_K or
+    // Q8_0; with Q4_K layers (Q4_K_M-style mixes) a V matrix of its own, the
+    // down matrices and lm_head may be other K-quants (multi-group GEMM on the
+    // same operand)
     const int lt = m->layers[0].wqkv.type;
+    const bool q4 = lt == GGML_Q4_K;
+    auto side = [&](const QMat& q) { return q.type == lt || (q4 && kq(q)); };
+    bool fused = m->arch == ARCH_LLAMA && (lt == GGML_Q4_K || lt == GGML_Q8_0) &&
+                 (m->lm_head.type == GGML_Q4_K || m->lm_head.type == GGML_Q8_0 || (q4 && kq(m->lm_head)));
     for (const Layer& L : m->layers)
-      fused = fused && !L.wv.d && L.wqkv.type == lt && L.wo.type == lt && L.wgu.type == lt && L.wdown.type == lt &&
-              (lt == GGML_Q4_K || lt == GGML_Q8_0);
+      fused = fused && L.wqkv.type == lt && L.wo.type == lt && L.wgu.type == lt && side(L.wdown) &&
+              (!L.wv.d || (q4 && kq(L.wv)));
     m->fused_ok = fused;
     if (!ok && !fused) FAIL(SH_ERR_UNSUPPORTED, "weight types: neither all K-quants nor uniform Q4_K / Q8_0 layers");
     // wide f16 GEMMs: every dense matrix (the routed experts keep the
@@ -388,7 +395,8 @@ static int load_model(sh_engine* e, const uint8_t* img, uint64_t size, sh_model*
   size_t gpart_floats = 0;
   for (const Layer& L : m->layers)
     gpart_floats = std::max({gpart_floats, sh_gemv_part_floats(L.wo), sh_gemv_part_floats(L.wgu),
-                             sh_gemv_part_floats(L.wdown), sh_gemm_part_floats(L.wqkv) + sh_gemm_part_floats(L.wv),
+                             sh_gemv_part_floats(L.wdown), sh_gemv_part_floats(L.wv),
+                             sh_gemm_part_floats(L.wqkv) + sh_gemm_part_floats(L.wv),
                              sh_gemm_part_floats(L.wo), sh_gemm_part_floats(L.wgu), sh_gemm_part_floats(L.wdown)});
   if (m->wide16_ok)
     for (const Layer& L : m->layers)
@@ -673,7 +681,14 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
   const bool fuse = fusion_enabled() && nc <= 2;
   const uint32_t s_wo = m->layers.empty() ? 0 : sh_gemv_fusable(m->layers[0].wo);
   const bool fuse_wo = s_wo && s_wo * nc <= 8;
-  const bool fuse_down = !m->layers.empty() && sh_gemv_fusable(m->layers[0].wdown) != 0;
+  // Mixed-type models (Q4_K_M-style): V in a matrix of its own and the down /
+  // lm_head matrices in another K-quant take the multi-group GEMM on the same
+  // staged operand; the fusions that need the tuned kernels are then decided
+  // per layer.
+  const int lt = m->layers.empty() ? GGML_Q4_K : m->layers[0].wqkv.type;
+  auto tuned = [&](const QMat& q) { return q.type == lt; };
+  bool any_wv = false;
+  for (const Layer& L : m->layers) any_wv = any_wv || L.wv.d != nullptr;
   if ((rc = sh_embed_launch(e, m, dev_tokens, nc, w.resid))) return rc;
   const uint32_t dkv = m->hd * m->n_kv;
   EpiArgs qkv;
@@ -726,7 +741,8 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
   // Fused residual preps (<= 2 columns, whole-K kernels whose operand fits in
   // LDS): QKV and gate/up build rmsnorm(resid + pending partials) themselves;
   // the residual alternates between resid and resid2 (resid after each layer).
-  const bool fuse_rp = fuse && swiglu_epilogue() && !m->layers.empty() &&
+  // A V matrix of its own needs the staged operand: no fused residual preps.
+  const bool fuse_rp = fuse && swiglu_epilogue() && !m->layers.empty() && !any_wv &&
                        sh_gemv_resid_fusable(m->layers[0].wqkv, nc) && sh_gemv_resid_fusable(m->layers[0].wgu, nc);
   auto resid_src = [&](const float* rin, float* rout, const float* norm_w) {
     OpndSrc r;
@@ -737,8 +753,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
   };
   // Otherwise the o and down GEMVs finish the residual themselves (the last
   // workgroup of each output superblock runs its prep), writing set 1.
-  const bool fuse_pp = fusion_enabled() && !fuse_rp && !m->layers.empty() &&
-                       sh_gemv_prep_fusable(m->layers[0].wo) && sh_gemv_prep_fusable(m->layers[0].wdown);
+  const bool fuse_pp0 = fusion_enabled() && !fuse_rp;
   bool prepped = false;  // the operand of the next GEMV is built (set 1)
   auto prep_fuse = [&](const float* norm_w) {
     PrepFuse f;
@@ -746,9 +761,19 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     f.cnt = w.sb_cnt; f.K = m->d;
     return f;
   };
+  // a matrix of the layers' type on the tuned GEMVs, another K-quant on the
+  // multi-group GEMM (EPI_PART / EPI_STORE on the staged operand)
+  auto gemv_any = [&](const QMat& q, const OpSet& op, EpiKind epi, const EpiArgs& ea, const char* tag,
+                      uint32_t* np) {
+    return tuned(q) ? sh_gemv_launch(e, q, op.bx, op.xs, nc, epi, ea, tag, np)
+                    : sh_gemm_launch(e, q, op.bx, op.xs, op.cs, nc, epi, ea, tag, np);
+  };
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
     qkv.layer = l;
+    const bool fuse_pp = fuse_pp0 && sh_gemv_prep_fusable(L.wo) && tuned(L.wo);  // Wo's fused residual prep
+    const bool fuse_ppd = fuse_pp0 && tuned(L.wdown) && sh_gemv_prep_fusable(L.wdown);  // down's
+    const bool fuse_down = tuned(L.wdown) && sh_gemv_fusable(L.wdown) != 0;
     if (fuse_rp) {
       const OpndSrc rs = resid_src(w.resid, w.resid2, L.attn_norm);
       EpiArgs q2 = qkv;
@@ -759,6 +784,20 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       if (!prepped && (rc = resid_prep(L.attn_norm))) return rc;
       set_norm(qkv);
       if ((rc = sh_gemv_launch(e, L.wqkv, cur.bx, cur.xs, nc, EPI_QKV, qkv, "gemv_qkv"))) return rc;
+      if (L.wv.d) {  // V rows from a matrix of their own: split partials, then the cache rows
+        EpiArgs pv = part_args(L.wv);
+        set_norm(pv);
+        uint32_t nv = 0;
+        if ((rc = gemv_any(L.wv, cur, EPI_PART, pv, "gemv_v", &nv))) return rc;
+        QkvCols qc;
+        for (uint32_t j = 0; j < nc; ++j) {
+          qc.pos[j] = cols[j].pos; qc.slot[j] = cols[j].slot; qc.mseq[j] = cols[j].kv->max_seq;
+          qc.kc[j] = cols[j].kv->k; qc.vc[j] = cols[j].kv->v;
+        }
+        qc.vpart = pv.out; qc.vnparts = nv; qc.vldp = pv.ldo; qc.vstride = pv.part_stride;
+        qc.row0 = m->d + dkv;  // the V rows only: q and k came out of the QKV epilogue
+        if ((rc = sh_qkv_finish_launch(e, pv.out, nv, pv.part_stride, pv.ldo, nc, qkv, qc))) return rc;
+      }
     }
     prepped = false;
     // one segment covering the chunk: Wo combines the attention splits itself
@@ -779,7 +818,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       if (rc) return rc;
     }
     EpiArgs po = part_args(L.wo);
-    if (fuse_pp) {
+    if (fuse_pp) {  // (Wo is always of the layers' type on this path)
       const PrepFuse pf = prep_fuse(L.ffn_norm);
       if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", nullptr, nullptr, &pf))) return rc;
       pending = 0;
@@ -810,7 +849,7 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
       set_norm(pg);
       PrepFuse sf;
       sf.bx = w.bx; sf.xs = w.xs; sf.cs = w.cs; sf.cnt = w.sb_cnt; sf.K = m->ff;
-      const bool fuse_sw = fuse_pp && prepped;
+      const bool fuse_sw = prepped;  // gate/up reads set 1 (Wo's fused prep), so its tail may write set 0
       if ((rc = sh_gemv_ring_launch(e, L.wgu, cur.bx, cur.xs, nc, EPI_PART, pg, "gemv_gate_up",
                                     fuse_sw ? &sf : nullptr)))
         return rc;
@@ -835,13 +874,16 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     cur = set0;
     EpiArgs pd = part_args(L.wdown);
     const float* next_norm = l + 1 < m->n_layer ? m->layers[l + 1].attn_norm : (want_logits ? m->out_norm : nullptr);
-    if (fuse_pp && next_norm && dsrc.kind == OPND_STAGED) {
+    if (fuse_ppd && next_norm && dsrc.kind == OPND_STAGED) {
       const PrepFuse pf = prep_fuse(next_norm);
       if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", nullptr, nullptr, &pf)))
         return rc;
       pending = 0;
       cur = set1;
       prepped = true;
+    } else if (!tuned(L.wdown)) {
+      if ((rc = gemv_any(L.wdown, set0, EPI_PART, pd, "gemv_down", &pending))) return rc;
+      pending_ld = pd.ldo;
     } else {
       if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", &pending,
                                dsrc.kind == OPND_STAGED ? nullptr : &dsrc)))
@@ -854,7 +896,11 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     EpiArgs st;
     st.out = w.logits; st.ldo = m->V; st.rows = m->V;
     set_norm(st);
-    if ((rc = sh_gemv_launch(e, m->lm_head, cur.bx, cur.xs, nc, EPI_STORE, st, "gemv_lm_head"))) return rc;
+    const bool lm_tuned = m->lm_head.type == GGML_Q4_K || m->lm_head.type == GGML_Q8_0;
+    if ((rc = lm_tuned ? sh_gemv_launch(e, m->lm_head, cur.bx, cur.xs, nc, EPI_STORE, st, "gemv_lm_head")
+                       : sh_gemm_launch(e, m->lm_head, cur.bx, cur.xs, cur.cs, nc, EPI_STORE, st, "gemv_lm_head",
+                                        nullptr)))
+      return rc;
   } else if (want_resid && pending) {
     if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, 8, m->d, nc, w.resid, m->d, true))) return rc;
   }

@@ -392,6 +392,9 @@ struct QkvCols {  // per column: RoPE position, cache slot, capacity, K and V ca
   const float* vpart = nullptr;
   uint32_t vnparts = 0, vldp = 0;
   size_t vstride = 0;
+  // first row to finish (multiple of 4): Dq + Dkv finishes the V rows only
+  // (k_qkv_finish; q and k rows came from elsewhere)
+  uint32_t row0 = 0;
 };
 int sh_qkv_finish_launch(sh_engine* e, const float* part, uint32_t nparts, size_t part_stride, uint32_t ldp,
                          uint32_t N, const EpiArgs& ea, const QkvCols& qc);
