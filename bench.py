@@ -202,12 +202,19 @@ def measure_acceptance(eng, reps=20):
     s.mode, s.temperature, s.seed, s.counter = SH_SAMPLE_REJECTION, T, 7, 0
     for _ in range(3):
         eng.accept_sample(pd, qd, dd, B, k, V, s, acc, nxt)
-    eng.set_profiling(True)
-    eng.profile(reset=True)
+    eng.sync()
+    # the call as a caller sees it: back-to-back calls on the engine stream,
+    # one synchronization at the end (no per-launch events)
     t = time.perf_counter()
     for _ in range(reps):
         eng.accept_sample(pd, qd, dd, B, k, V, s, acc, nxt)
+    eng.sync()
     wall_ms = (time.perf_counter() - t) * 1e3 / reps
+    # kernel time: the same calls with per-launch events
+    eng.set_profiling(True)
+    eng.profile(reset=True)
+    for _ in range(reps):
+        eng.accept_sample(pd, qd, dd, B, k, V, s, acc, nxt)
     prof = eng.profile(reset=True)
     eng.set_profiling(False)
     kern_ms = sum(prof[n]["ms"] for n in ("accept_stats", "accept_decide") if n in prof) / reps

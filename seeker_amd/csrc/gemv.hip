@@ -1726,6 +1726,135 @@ __global__ __launch_bounds__(512) void k_gemm16w_q4k(const uint8_t* __restrict__
     }
 }
 
+// k_gemm16w_q4k with a deeper weight pipeline: the weight words and row
+// headers (16 tiles x 1280 B per stage of half a superblock, from HBM) go
+// through a ring of three LDS buffers two stages ahead of the compute, B
+// through two buffers one stage ahead (from L2). Every load is the wave's own
+// direct load, issued per step as B(s + 1), then W(s + 2), so the wait for
+// stage s leaves exactly the 2 T weight loads of stage s + 1 in flight.
+// LDS: 2 x NC x 4 KB + 3 x 20 KB (156 KB at NC = 12).
+template <int NC, int EPI>
+__global__ __launch_bounds__(512) void k_gemm16w3_q4k(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+                                                      uint32_t S, const uint16_t* __restrict__ Bh, uint32_t ldb,
+                                                      uint32_t N, EpiArgs ea) {
+  constexpr int T = 2, WV = 8, WSTG = 3;
+  constexpr uint32_t kTW = 1280;  // one tile's stage: 1 KB of words + the 256 B row header
+  __shared__ h8 sB[2][NC * 4 * 64];  // [buffer][(column group * 4 + sub-block) * 64 + lane]
+  __shared__ __attribute__((aligned(16))) uint8_t sW[WSTG][WV * T * kTW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4, r = lane & 15;
+  const uint32_t ks = blockIdx.y, sb0 = ks * S, sb1 = min(sb0 + S, nsb), nst = 2 * (sb1 - sb0);
+  const uint32_t tile0 = (blockIdx.x * WV + wave) * T;
+
+  auto issue_b = [&](uint32_t s, int buf) __attribute__((always_inline)) {
+    const uint32_t sb = sb0 + (s >> 1), h = s & 1;
+    for (uint32_t fi = wave; fi < (uint32_t)(NC * 4); fi += WV) {  // NC / 2 per wave
+      const uint32_t c = fi >> 2, mp = fi & 3;
+      const uint32_t col = min(16 * c + (uint32_t)r, N - 1);
+      sh_dma16(Bh + (size_t)col * ldb + 256 * sb + 32 * (4 * h + mp) + 8 * g4, &sB[buf][fi * 64]);
+    }
+  };
+  auto issue_w = [&](uint32_t s, int buf) __attribute__((always_inline)) {
+    const uint32_t sb = sb0 + (s >> 1), h = s & 1;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
+      const uint8_t* src = Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
+      uint8_t* dst = &sW[buf][(wave * T + t) * kTW];
+      sh_dma16(src + 1024 * h + 16 * lane, dst);
+      sh_dma4(src + 2048 + 4 * lane, dst + 1024);
+    }
+  };
+
+  f4 acc[T][NC];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int bb_buf, int w_buf, uint32_t h) __attribute__((always_inline)) {
+    u32x4 q[T];
+    uint32_t scw[T], mw[T];
+    float d24[T], ndmin[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint8_t* wt = &sW[w_buf][(wave * T + t) * kTW];
+      q[t] = *(const u32x4*)(wt + 16 * lane);
+      const uint32_t dd = *(const uint32_t*)(wt + 1024 + 4 * r);
+      const uint32_t* sp = (const uint32_t*)(wt + 1024 + 64 + 12 * r);
+      const uint32_t s0 = sp[0], s1 = sp[1], s2 = sp[2];
+      // the Q4_K 6-bit unpack of sub-blocks 4h .. 4h + 3 (q4_decode_setup)
+      scw[t] = h == 0 ? (s0 & 0x3F3F3F3Fu) : ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u));
+      mw[t] = h == 0 ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+      d24[t] = (float)as_h2(dd).x * 16777216.0f;
+      ndmin[t] = -(float)as_h2(dd).y;
+    }
+#pragma unroll
+    for (int mp = 0; mp < 4; ++mp) {
+      h8 bb[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) bb[c] = sB[bb_buf][(c * 4 + mp) * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);
+      h8 a[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float a24 = d24[t] * (float)((scw[t] >> (8 * mp)) & 0xFFu), a20 = a24 * 0.0625f;
+        const float nb = ndmin[t] * (float)((mw[t] >> (8 * mp)) & 0xFFu);
+        const uint32_t word = mp == 0 ? q[t].x : mp == 1 ? q[t].y : mp == 2 ? q[t].z : q[t].w;
+        const uint32_t w8 = word >> 8;
+        u32x4 v;
+        v.x = fma_mix_pair(word & 0x000F000Fu, a24, nb);
+        v.y = fma_mix_pair(word & 0x00F000F0u, a20, nb);
+        v.z = fma_mix_pair(w8 & 0x000F000Fu, a24, nb);
+        v.w = fma_mix_pair(w8 & 0x00F000F0u, a20, nb);
+        a[t] = as_h8(v);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t][c] = mfma16(a[t], bb[c], acc[t][c]);
+    }
+  };
+
+  // prologue: W(0), B(0), W(1) (the same order as the steps' B(s + 1), W(s + 2))
+  issue_w(0, 0);
+  issue_b(0, 0);
+  if (nst > 1) issue_w(1, 1);
+  for (uint32_t s = 0; s < nst; ++s) {
+    // B(s) and W(s) landed (W(s + 1), issued after them, may still be in
+    // flight); every wave is done with stage s - 1's buffers, which B(s + 1)
+    // and W(s + 2) now refill
+    if (s + 1 < nst) sh_wait_vm<2 * T>();
+    else sh_wait_vm<0>();
+    __syncthreads();
+    // the buffer indices as wave-uniform values (the direct loads take their
+    // LDS address in M0)
+    const int wb = __builtin_amdgcn_readfirstlane((int)(s % WSTG));
+    const int bb = __builtin_amdgcn_readfirstlane((int)(s & 1));
+    if (s + 1 < nst) issue_b(s + 1, bb ^ 1);
+    if (s + 2 < nst) issue_w(s + 2, wb == 0 ? 2 : wb - 1);
+    compute(bb, wb, s & 1);
+  }
+
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t tile = tile0 + t, col = 16 * c + r, row0 = tile * 16 + 4 * g4;
+      if (tile >= tiles || col >= N) continue;
+      const f4 v = acc[t][c];
+      if (EPI == EPI_PART) {
+        *(float4*)(ea.out + ks * ea.part_stride + (size_t)col * ea.ldo + row0) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (row0 + j < ea.rows) ea.out[(size_t)col * ea.ldo + row0 + j] = v[j];
+      }
+    }
+}
+
 // y = W x for 64 < N <= 192 columns in column blocks of 16 NCH columns: a
 // workgroup of 8 waves covers 16 row tiles (wave w: tiles 2 (16 rb + w) + t)
 // and one column block over the superblocks of split blockIdx.y. The ncb
@@ -2794,9 +2923,17 @@ static void dispatch16h(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_
 template <int NC, int EPI>
 static void launch16w(sh_engine* e, const QMat& w, const uint16_t* bh, uint32_t ldb, uint32_t N, const EpiArgs& ea,
                       const MgPlan& p) {
+  static const bool deep = [] {
+    const char* s = getenv("SH_G16W3");
+    return !(s && atoi(s) == 0);
+  }();
   const dim3 grid((w.tiles + 15) / 16, p.KS);
-  hipLaunchKernelGGL((k_gemm16w_q4k<NC, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bh,
-                     ldb, N, ea);
+  if (deep)
+    hipLaunchKernelGGL((k_gemm16w3_q4k<NC, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bh,
+                       ldb, N, ea);
+  else
+    hipLaunchKernelGGL((k_gemm16w_q4k<NC, EPI>), grid, dim3(512), 0, e->stream, w.d, w.tiles, w.K / 256, p.S, bh,
+                       ldb, N, ea);
 }
 
 template <int NC, int EPI>
