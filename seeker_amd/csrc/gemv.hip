@@ -332,15 +332,26 @@ struct Q4Tile {
   __device__ void pin() { pin32(q0); pin32(q1); pin32(dd); pin32(s0); pin32(s1); pin32(s2); }
 };
 
+// Weight loads are non-temporal (the `nt` hint): every weight byte is read
+// once per forward, and the hint keeps the stream from displacing what is read
+// again (K/V, operands) in the caches. Measured on the box: the 8B gate/up
+// 21.95 -> 21.5 us per launch, the spec step 6.36 -> 6.33 ms, a 512 MB stream
+// 94 -> 88 us.
+__device__ __forceinline__ u32x4 ldw16(const uint8_t* p) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const u4 v = __builtin_nontemporal_load((const u4*)p);
+  return u32x4{v[0], v[1], v[2], v[3]};
+}
+__device__ __forceinline__ uint32_t ldw4(const uint8_t* p) { return __builtin_nontemporal_load((const uint32_t*)p); }
 __device__ __forceinline__ Q4Tile load_q4_tile(const uint8_t* base, int lane, int g, int r) {
   Q4Tile a;
-  a.q0 = ld16(base + 16 * lane);
-  a.q1 = ld16(base + 1024 + 16 * lane);
-  a.dd = ld16(base + 2048 + 16 * g);
-  const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
-  a.s0 = sp[0];
-  a.s1 = sp[1];
-  a.s2 = sp[2];
+  a.q0 = ldw16(base + 16 * lane);
+  a.q1 = ldw16(base + 1024 + 16 * lane);
+  a.dd = ldw16(base + 2048 + 16 * g);
+  const uint8_t* sp = base + 2112 + 12 * r;
+  a.s0 = ldw4(sp);
+  a.s1 = ldw4(sp + 4);
+  a.s2 = ldw4(sp + 8);
   return a;
 }
 
@@ -1039,8 +1050,8 @@ struct Q5Dec {
 };
 __device__ __forceinline__ Q5Tile load_q5_tile(const uint8_t* base, int lane, int g, int r) {
   Q5Tile a;
-  a.q0 = ld16(base + 16 * lane);
-  a.q1 = ld16(base + 1024 + 16 * lane);
+  a.q0 = ldw16(base + 16 * lane);
+  a.q1 = ldw16(base + 1024 + 16 * lane);
   const uint2 h = *(const uint2*)(base + 2048 + 8 * lane);
   a.h0 = h.x;
   a.h1 = h.y;
@@ -1111,9 +1122,9 @@ struct Q6Dec {
 };
 __device__ __forceinline__ Q6Tile load_q6_tile(const uint8_t* base, int lane, int g, int r) {
   Q6Tile a;
-  a.q0 = ld16(base + 16 * lane);
-  a.q1 = ld16(base + 1024 + 16 * lane);
-  a.h = ld16(base + 2048 + 16 * lane);
+  a.q0 = ldw16(base + 16 * lane);
+  a.q1 = ldw16(base + 1024 + 16 * lane);
+  a.h = ldw16(base + 2048 + 16 * lane);
   a.sc = *(const uint2*)(base + 3072 + 16 * r + 8 * (g >> 1));
   a.d = *(const uint2*)(base + 3328 + 8 * g);
   return a;
@@ -1404,8 +1415,8 @@ struct Q4TileR {
 };
 __device__ __forceinline__ Q4TileR load_q4_tile_r(const uint8_t* base, int lane, int r) {
   Q4TileR a;
-  a.q0 = ld16(base + 16 * lane);
-  a.q1 = ld16(base + 1024 + 16 * lane);
+  a.q0 = ldw16(base + 16 * lane);
+  a.q1 = ldw16(base + 1024 + 16 * lane);
   a.dd = *(const uint32_t*)(base + 2048 + 4 * r);
   const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
   a.s0 = sp[0];
@@ -1512,9 +1523,9 @@ __global__ __launch_bounds__(512) void k_gemm16_q4k(const uint8_t* __restrict__ 
       const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
       const uint8_t* src = Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
       uint8_t* dst = &sW[buf][(wave * T + t) * SH_Q4K_TILE_BYTES];
-      sh_dma16(src + 16 * lane, dst);
-      sh_dma16(src + 1024 + 16 * lane, dst + 1024);
-      sh_dma4(src + 2048 + 4 * lane, dst + 2048);
+      sh_dma16_nt(src + 16 * lane, dst);
+      sh_dma16_nt(src + 1024 + 16 * lane, dst + 1024);
+      sh_dma4_nt(src + 2048 + 4 * lane, dst + 2048);
     }
   };
 
@@ -1626,7 +1637,7 @@ __global__ __launch_bounds__(512) void k_gemm16w_q4k(const uint8_t* __restrict__
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const uint8_t* base = tb[t] + (size_t)sb * SH_Q4K_TILE_BYTES;
-      w.q[t] = ld16(base + 1024 * h + 16 * lane);
+      w.q[t] = ldw16(base + 1024 * h + 16 * lane);
       w.dd[t] = *(const uint32_t*)(base + 2048 + 4 * r);
       const uint32_t* sp = (const uint32_t*)(base + 2112 + 12 * r);
       w.s0[t] = sp[0];
@@ -1762,8 +1773,8 @@ __global__ __launch_bounds__(512) void k_gemm16w3_q4k(const uint8_t* __restrict_
       const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
       const uint8_t* src = Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
       uint8_t* dst = &sW[buf][(wave * T + t) * kTW];
-      sh_dma16(src + 1024 * h + 16 * lane, dst);
-      sh_dma4(src + 2048 + 4 * lane, dst + 1024);
+      sh_dma16_nt(src + 1024 * h + 16 * lane, dst);
+      sh_dma4_nt(src + 2048 + 4 * lane, dst + 1024);
     }
   };
 
@@ -1896,8 +1907,8 @@ __global__ __launch_bounds__(512) void k_gemm16h_q4k(const uint8_t* __restrict__
       const uint32_t tt = tile0 + t < tiles ? tile0 + t : tiles - 1;  // clamp keeps loads in bounds
       const uint8_t* src = Wp + ((size_t)tt * nsb + sb) * SH_Q4K_TILE_BYTES;
       uint8_t* dst = &sW[buf][(wave * T + t) * kTW];
-      sh_dma16(src + 1024 * h + 16 * lane, dst);
-      sh_dma4(src + 2048 + 4 * lane, dst + 1024);
+      sh_dma16_nt(src + 1024 * h + 16 * lane, dst);
+      sh_dma4_nt(src + 2048 + 4 * lane, dst + 1024);
     }
   };
 

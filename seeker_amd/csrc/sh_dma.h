@@ -34,6 +34,15 @@ __device__ __forceinline__ void sh_dma4(const void* src, const void* lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(sh_lds_addr(lds))
                : "memory", "m0");
 }
+// The same with the non-temporal hint, for streams read once (weights).
+__device__ __forceinline__ void sh_dma16_nt(const void* src, const void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(sh_lds_addr(lds))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void sh_dma4_nt(const void* src, const void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt" ::"v"(src), "s"(sh_lds_addr(lds))
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Waits until at most N of this wave's vector-memory loads are in flight.
