@@ -3042,10 +3042,23 @@ int sh_moe_gemm_launch(sh_engine* e, const QMat& w, uint32_t n_expert, const uin
            "expert gemm needs K-quant expert slabs of whole tiles");
   SH_CHECK(ea.out && ea.ldo >= w.M / n_expert, SH_ERR_ARG, "expert gemm output");
   const uint32_t tiles_e = w.tiles / n_expert, nsb = w.K / 256;
-  constexpr int T = 1;
-  const uint32_t rb_e = (tiles_e + 8 * T - 1) / (8 * T);
   hipEvent_t ev = nullptr;
   sh_prof_begin(e, &ev);
+  // Q4_K slabs of 8 or more superblocks (the experts' gate/up) with two tiles
+  // per wave: twice the weight bytes in flight per wave at one workgroup per
+  // CU (132 VGPRs), 2.85 -> 2.72 ms per step of the 8 x 7-column
+  // Qwen3-30B-A3B-shape verify; the 768-wide down (3 superblocks) is faster
+  // with one (1.52 vs 1.74 ms), four is slower for both
+  if (w.type == GGML_Q4_K && nsb >= 8) {
+    const uint32_t rb2 = (tiles_e + 15) / 16;
+    hipLaunchKernelGGL((k_moe_gemm_kq<FmtQ4K, 2>), dim3(max_chunks * rb2), dim3(512), 0, e->stream, w.d, tiles_e, nsb,
+                       rb2, bx, xs, cs, info, gcol, ea);
+    SH_HIP(hipGetLastError());
+    sh_prof_end(e, tag, alg_bytes, ev);
+    return SH_OK;
+  }
+  constexpr int T = 1;
+  const uint32_t rb_e = (tiles_e + 8 * T - 1) / (8 * T);
   const dim3 grid(max_chunks * rb_e);
   if (w.type == GGML_Q5_K)
     hipLaunchKernelGGL((k_moe_gemm_kq<FmtQ5K, T>), grid, dim3(512), 0, e->stream, w.d, tiles_e, nsb, rb_e, bx, xs, cs,
