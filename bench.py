@@ -34,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA, MI355X
 
 
 def log(*a):
@@ -178,7 +179,7 @@ def measure_forced(eng, tm, dm, tkv, dkv, last, k, steps, warmup=2):
                           "(apps/seeker-cli/src/commands/run.rs:702-710 counts emitted tokens)"}, last
 
 
-def measure_acceptance(eng, reps=20):
+def measure_acceptance(eng, reps=20, cpu=True):
     """the acceptance kernel alone (REJECTION, T = 0.8), B = 32, k = 8,
     V = 128256; target logits N(0, 3), draft = target + N(0, 1), drafts sampled
     from the draft distribution (numpy), uniforms Philox (seed 7) in the kernel.
@@ -218,15 +219,30 @@ def measure_acceptance(eng, reps=20):
     prof = eng.profile(reset=True)
     eng.set_profiling(False)
     kern_ms = sum(prof[n]["ms"] for n in ("accept_stats", "accept_decide") if n in prof) / reps
-    al = acc.read(np.uint32, B)
+    al, nt = acc.read(np.uint32, B), nxt.read(np.uint32, B)
     for x in (pd, qd, dd, acc, nxt):
         x.free()
     nbytes = 4 * V * B * (2 * k + 1)
     log(f"acceptance kernel B={B} k={k} V={V}: {kern_ms * 1e3:.1f} us in kernels, {wall_ms * 1e3:.1f} us per call")
-    return {"config": "B=32, k=8, V=128256, REJECTION T=0.8, Philox seed 7", "kernel_us": round(kern_ms * 1e3, 2),
-            "call_us": round(wall_ms * 1e3, 2), "alg_bytes": nbytes,
-            "GBps": round(nbytes / kern_ms / 1e6, 1), "frac": round(nbytes / kern_ms / 1e6 / HBM_PEAK_GBS, 4),
-            "mean_accepted": round(float(al.mean()), 3)}
+    out = {"config": "B=32, k=8, V=128256, REJECTION T=0.8, Philox seed 7", "kernel_us": round(kern_ms * 1e3, 2),
+           "call_us": round(wall_ms * 1e3, 2), "alg_bytes": nbytes,
+           "GBps": round(nbytes / kern_ms / 1e6, 1), "frac": round(nbytes / kern_ms / 1e6 / HBM_PEAK_GBS, 4),
+           "mean_accepted": round(float(al.mean()), 3)}
+    if cpu:
+        # the C oracle's rejection rule (f64, one thread) over the same logits,
+        # drafts and Philox words: the CPU time of the same call, and the check
+        # that every sequence's (accepted length, next token) is the GPU's
+        import oracle as O
+        U = O.philox_uniforms(7, 0x5EC, 0, 2 * B * (k + 1)).reshape(B, k + 1, 2)
+        t = time.perf_counter()
+        ref = [O.rejection(p[b], q[b], drafts[b], T, U[b, :k, 0].copy(), U[b, :, 1].copy()) for b in range(B)]
+        cpu_ms = (time.perf_counter() - t) * 1e3
+        same = sum(int(al[b]) == ref[b][0] and int(nt[b]) == ref[b][1] for b in range(B))
+        log(f"acceptance on the CPU (C oracle, 1 thread): {cpu_ms:.1f} ms per call; {same}/{B} sequences equal")
+        out["cpu_baseline"] = {"value": round(cpu_ms * 1e3, 1), "unit": "us per call", "cores": 1, "kind": "port",
+                               "sample": f"the whole call: {B} sequences, f64 C restatement (oracle/oracle.c)"}
+        out["parity"] = {"sequences_equal": same, "sequences": B}
+    return out
 
 
 def measure_tree(eng, tm, d, P=8192, reps=3):
@@ -284,11 +300,21 @@ def measure_tree(eng, tm, d, P=8192, reps=3):
     log(f"tree verify step B={B} n={n} ctx {P}: {ms:.2f} ms, mean path {np.mean(plens):.2f} nodes")
     for k, v in list(kern.items())[:10]:
         log(f"  {k:16s} {v:8.3f} ms")
+    # the dense matmuls' rate: 2 x (every weight element) x the B n columns
+    # against the summed event time of their GEMM kernels (split partials
+    # written; their finishing kernels are counted under the preps)
+    gemm_ms = sum(v for k, v in kern.items() if k.startswith("gemv_"))
+    elems = w * 256 // 144
+    gemm_tflops = 2.0 * elems * B * n / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
+    log(f"  dense GEMMs: {gemm_ms:.3f} ms, {gemm_tflops:.0f} TFLOP/s ({gemm_tflops / MFMA_F16_PEAK_TFLOPS:.3f} of "
+        f"the dense f16 MFMA peak)")
     return {"config": f"B={B}, tree 4x3x2 ({n} nodes), ctx {P}, REJECTION T=1.0 seed 11, synthetic draft logits",
             "arithmetic": ("reference wide-GEMM (f16 weights and activations, f32 accumulation; "
                            "ops/matmul.rs:433-446)" if tm.wide_f16 else "f32-level (hi/lo f16 activations)"),
             "ms": round(ms, 3), "alg_bytes": w + kv, "GBps": round((w + kv) / ms / 1e6, 1),
             "frac": round((w + kv) / ms / 1e6 / HBM_PEAK_GBS, 4), "mean_path_nodes": round(float(np.mean(plens)), 3),
+            "gemm": {"ms": round(gemm_ms, 4), "flop": 2 * elems * B * n, "TFLOPs": round(gemm_tflops, 1),
+                     "mfma_frac": round(gemm_tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS},
             "kernel_ms": kern}
 
 
@@ -475,7 +501,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--k", type=int, default=7)
-    ap.add_argument("--verify-reps", type=int, default=30)
+    ap.add_argument("--verify-reps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the acceptance-kernel, tree and MoE lines")
     ap.add_argument("--moe-only", action="store_true", help="only the configs[4] MoE verify measurement")
