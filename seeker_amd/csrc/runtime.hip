@@ -952,8 +952,19 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
   int rc;
   const uint32_t ncp = (nc + 7) / 8 * 8;  // columns per split in the partial buffer
   if ((rc = sh_embed_launch(e, m, dev_tokens, nc, w.resid))) return rc;
+  // Operand the next GEMV reads: set 0 from the prep kernels and the attention
+  // combine, set 1 from a residual prep fused into Wo / down (below).
+  struct OpSet {
+    uint16_t* bx;
+    uint16_t* xs;
+    float* cs;
+    float* ssq;
+  };
+  const OpSet set0{w.bx, w.xs, w.cs, w.ssq}, set1{w.bx2, w.xs2, w.cs2, w.ssq2};
+  OpSet cur = set0;
+  // GEMVs whose input is RMS-normalized apply the norm factor to their outputs
   auto set_norm = [&](EpiArgs& ea) {
-    ea.ssq = w.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
+    ea.cs = cur.cs; ea.ssq = cur.ssq; ea.ssq_n = (m->d + 255) / 256; ea.norm_K = m->d; ea.eps = m->eps;
   };
   auto part_args = [&](const QMat& q) {
     EpiArgs pa;
@@ -1015,6 +1026,7 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     pr.mode = PREP_RESID; pr.x = w.resid; pr.K = m->d; pr.norm_w = norm_w; pr.ldb = m->d;
     pr.nparts = pending; pr.part_ld = pending_ld;
     pending = 0;
+    cur = set0;
     return sh_prep_launch(e, pr);
   };
   // At most 8 columns (one operand group), a Q4_K matrix takes the tuned GEMVs
@@ -1026,17 +1038,31 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     const char* s = getenv("SH_MG_TUNED");
     return !(s && atoi(s) == 0);
   }();
-  auto gemm = [&](const QMat& q, EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* np) {
+  auto gemm = [&](const QMat& q, const OpSet& op, EpiKind epi, const EpiArgs& ea, const char* tag, uint32_t* np) {
     if (f16) return sh_gemm16_launch(e, q, w.bh, q.K, nc, epi, ea, tag, np);
     if (tuned_small && nc <= 8 && q.type == GGML_Q4_K && (epi == EPI_PART || epi == EPI_STORE)) {
       if (epi == EPI_PART && sh_gemv_ring_t(q) && q.tiles % 7 == 0) {
         if (np) *np = 1;
-        return sh_gemv_ring_launch(e, q, w.bx, w.xs, nc, EPI_PART, ea, tag, nullptr);
+        return sh_gemv_ring_launch(e, q, op.bx, op.xs, nc, EPI_PART, ea, tag, nullptr);
       }
-      return sh_gemv_launch(e, q, w.bx, w.xs, nc, epi, ea, tag, np);
+      return sh_gemv_launch(e, q, op.bx, op.xs, nc, epi, ea, tag, np);
     }
-    return sh_gemm_launch(e, q, w.bx, w.xs, w.cs, nc, epi, ea, tag, np);
+    return sh_gemm_launch(e, q, op.bx, op.xs, op.cs, nc, epi, ea, tag, np);
   };
+  // On those kernels a dense model's Wo and down finish the residual
+  // themselves, as on the fused path: the last workgroup of each output
+  // superblock adds the split partials, applies the next RMSNorm and writes
+  // the operand into set 1, so no prep kernel runs between them and the next
+  // GEMV (the arithmetic of the prep kernel, bit for bit).
+  const bool pfuse = !f16 && tuned_small && nc <= 8 && !m->n_expert && fusion_enabled();
+  auto prep_fusable = [&](const QMat& q) { return pfuse && q.type == GGML_Q4_K && sh_gemv_prep_fusable(q); };
+  auto prep_fuse = [&](const float* norm_w) {
+    PrepFuse pf;
+    pf.resid = w.resid; pf.norm_w = norm_w; pf.bx = w.bx2; pf.xs = w.xs2; pf.cs = w.cs2; pf.ssq = w.ssq2;
+    pf.cnt = w.sb_cnt; pf.K = m->d;
+    return pf;
+  };
+  bool prepped = false;  // the operand of the next GEMV is built (set 1)
   // batched attention: one plan for the chunk's segments, one launch per layer
   // a causal single-sequence call (m->call_cm1): the chunk's columns as one
   // cm1 attention launch
@@ -1055,11 +1081,11 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
   if (use_fab && (rc = plan_fab(m, segs, nc, &fab))) return rc;
   for (uint32_t l = 0; l < m->n_layer; ++l) {
     const Layer& L = m->layers[l];
-    if ((rc = resid_prep(L.attn_norm))) return rc;
+    if (!prepped && (rc = resid_prep(L.attn_norm))) return rc;
     EpiArgs pq = part_args(L.wqkv);
     set_norm(pq);
     uint32_t nq = 0;
-    if ((rc = gemm(L.wqkv, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
+    if ((rc = gemm(L.wqkv, cur, EPI_PART, pq, "gemv_qkv", &nq))) return rc;
     const float* vpart = nullptr;
     uint32_t nv = 0, vldp = 0;
     size_t vstride = 0;
@@ -1068,10 +1094,12 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
       set_norm(pv);
       pv.out = w.gpart + nq * pq.part_stride;
       pv.part_cap = (uint32_t)((w.gpart_floats - nq * pq.part_stride) / pv.part_stride);
-      if ((rc = gemm(L.wv, EPI_PART, pv, "gemv_v", &nv))) return rc;
+      if ((rc = gemm(L.wv, cur, EPI_PART, pv, "gemv_v", &nv))) return rc;
       vpart = pv.out; vldp = pv.ldo; vstride = pv.part_stride;
     }
     qkv.layer = l;
+    prepped = false;
+    cur = set0;  // the attention writes the Wo operand into set 0
     if ((rc = qkv_finish(w.gpart, nq, pq.part_stride, pq.ldo, L, vpart, nv, vldp, vstride))) return rc;
     if (cm1) {
       FaArgs fa;
@@ -1099,9 +1127,17 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
       }
     }
     EpiArgs po = part_args(L.wo);
-    if ((rc = gemm(L.wo, EPI_PART, po, "gemv_o", &pending))) return rc;
-    pending_ld = po.ldo;
-    if ((rc = resid_prep(L.ffn_norm))) return rc;
+    if (prep_fusable(L.wo)) {
+      const PrepFuse pf = prep_fuse(L.ffn_norm);
+      if ((rc = sh_gemv_launch(e, L.wo, w.bx, w.xs, nc, EPI_PART, po, "gemv_o", nullptr, nullptr, &pf))) return rc;
+      pending = 0;
+      cur = set1;
+      prepped = true;
+    } else {
+      if ((rc = gemm(L.wo, set0, EPI_PART, po, "gemv_o", &pending))) return rc;
+      pending_ld = po.ldo;
+    }
+    if (!prepped && (rc = resid_prep(L.ffn_norm))) return rc;
     if (m->n_expert) {  // routed experts add into the residual themselves
       if (f16) {
         // the experts take the f32-level operand (the reference's expert
@@ -1116,20 +1152,32 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
     EpiArgs pg = part_args(L.wgu);
     set_norm(pg);
     uint32_t ngu = 0;
-    if ((rc = gemm(L.wgu, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
+    if ((rc = gemm(L.wgu, cur, EPI_PART, pg, "gemv_gate_up", &ngu))) return rc;
+    prepped = false;
+    cur = set0;
     pr.mode = PREP_SWIGLU; pr.x = nullptr; pr.nparts = ngu; pr.part_ld = pg.ldo; pr.K = m->ff; pr.norm_w = nullptr;
     pr.ldb = m->ff;
     if ((rc = sh_prep_launch(e, pr))) return rc;
     EpiArgs pd = part_args(L.wdown);
-    if ((rc = gemm(L.wdown, EPI_PART, pd, "gemv_down", &pending))) return rc;
-    pending_ld = pd.ldo;
+    const float* next_norm = l + 1 < m->n_layer ? m->layers[l + 1].attn_norm : (want_logits ? m->out_norm : nullptr);
+    if (next_norm && prep_fusable(L.wdown)) {
+      const PrepFuse pf = prep_fuse(next_norm);
+      if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", nullptr, nullptr, &pf)))
+        return rc;
+      pending = 0;
+      cur = set1;
+      prepped = true;
+    } else {
+      if ((rc = gemm(L.wdown, set0, EPI_PART, pd, "gemv_down", &pending))) return rc;
+      pending_ld = pd.ldo;
+    }
   }
   if (want_logits) {
-    if ((rc = resid_prep(m->out_norm))) return rc;
+    if (!prepped && (rc = resid_prep(m->out_norm))) return rc;
     EpiArgs st;
-    st.out = w.logits; st.ldo = m->V; st.rows = m->V; st.cs = w.cs;
+    st.out = w.logits; st.ldo = m->V; st.rows = m->V;
     set_norm(st);
-    if ((rc = gemm(m->lm_head, EPI_STORE, st, "gemv_lm_head", nullptr))) return rc;
+    if ((rc = gemm(m->lm_head, cur, EPI_STORE, st, "gemv_lm_head", nullptr))) return rc;
   } else if (want_resid && pending) {
     if ((rc = sh_part_reduce_launch(e, w.gpart, pending, pending_ld, ncp, m->d, nc, w.resid, m->d, true))) return rc;
   }
