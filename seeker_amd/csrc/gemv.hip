@@ -2106,9 +2106,13 @@ __global__ __launch_bounds__(128) void k_qkv_finish_head(const float* __restrict
 // (EPI_STORE, whole K in one workgroup). Grid: max chunks x rb_e row blocks
 // of 8 T tiles; workgroups past info[0] chunks exit at once. The superblock
 // pipeline (operand fragments staged in LDS by direct loads, two buffers) is
-// the multi-group kernel's with one gathered group.
+// the multi-group kernel's with one gathered group. T = 2 is held to 128
+// VGPRs (4 waves per SIMD: two workgroups per CU; 132 unbounded, one spilled
+// register at the bound): the experts' gate/up 2.74 -> 2.50 ms per step of the
+// 8 x 7-column Qwen3-30B-A3B-shape verify. Three workgroups of T = 1 per CU
+// (80 VGPRs, spills) made the down slower (1.53 -> 1.60 ms).
 template <class F, int T>
-__global__ __launch_bounds__(512) void k_moe_gemm_kq(const uint8_t* __restrict__ Wp, uint32_t tiles_e,
+__global__ __launch_bounds__(512, T == 2 ? 4 : 2) void k_moe_gemm_kq(const uint8_t* __restrict__ Wp, uint32_t tiles_e,
                                                       uint32_t nsb, uint32_t rb_e, const uint16_t* __restrict__ Bx,
                                                       const uint16_t* __restrict__ XS, const float* __restrict__ CS,
                                                       const uint32_t* __restrict__ info,
