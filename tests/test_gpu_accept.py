@@ -11,6 +11,7 @@ import pytest
 
 import oracle as O
 from seeker_amd import synth as S
+from parity import record
 from seeker_amd._native import SH_SAMPLE_COMPARE, SH_SAMPLE_REJECTION, sh_sampling
 
 pytestmark = pytest.mark.gpu
@@ -195,4 +196,5 @@ def test_rejection_many_seeds(engine):
     for x in (pdv, qdv, ddv, accd, nxtd):
         x.free()
     print(f"mean accepted {n_acc / (n_seeds * B):.3f}", flush=True)
+    record("rejection_seeds", n_seeds * B, mism)
     assert mism == tight_mism, (mism, tight_mism)
