@@ -264,14 +264,6 @@ int sh_part_reduce_launch(sh_engine* e, const float* part, uint32_t nparts, uint
 
 // ------------------------------------------------------------------ argmax
 
-// Orderable key: larger float -> larger key; ties -> lower index wins
-// (host argmax semantics, inference/sample.rs:504-514). NaN never wins.
-__device__ __forceinline__ unsigned long long amax_key(float v, uint32_t idx) {
-  uint32_t b = __builtin_bit_cast(uint32_t, v);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((unsigned long long)b << 32) | (unsigned long long)(~idx);
-}
-
 // One kernel per argmax: each workgroup folds its 2048-logit block into the
 // column's key (atomic max), then counts itself in on its column's counter;
 // the column's last workgroup to arrive writes its id and clears the key and
@@ -295,10 +287,8 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
   }
 #pragma unroll
   for (uint32_t j = 0; j < PER_T; ++j) {
-    if (v[j] == v[j]) {
-      const unsigned long long k = amax_key(v[j], i0 + threadIdx.x + 256 * j);
-      best = k > best ? k : best;
-    }
+    const unsigned long long k = sh_amax_key(v[j], i0 + threadIdx.x + 256 * j);  // NaN padding: key 0
+    best = k > best ? k : best;
   }
   for (int off = 32; off >= 1; off >>= 1) {
     const unsigned long long o = __shfl_xor(best, off);
@@ -319,7 +309,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
     if (last) {
       __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const unsigned long long k = __hip_atomic_load(keys + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      out[col] = k == 0ull ? 0u : ~(uint32_t)(k & 0xFFFFFFFFull);
+      out[col] = sh_amax_index(k);
       __hip_atomic_store(keys + col, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }

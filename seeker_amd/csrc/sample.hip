@@ -867,14 +867,6 @@ __global__ __launch_bounds__(256) void k_draw_pick(const float* __restrict__ p, 
   }
 }
 
-// Orderable argmax key: larger float -> larger key, ties -> lower index; NaN loses.
-__device__ __forceinline__ unsigned long long tree_amax_key(float v, uint32_t idx) {
-  if (v != v) return 0ull;
-  uint32_t b = __builtin_bit_cast(uint32_t, v);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((unsigned long long)b << 32) | (unsigned long long)(~idx);
-}
-
 // Tree acceptance, one workgroup per tree (b): walk from the root; children of
 // the current node v are tried in index order, child c accepted iff
 // u * q(tok_c) < cur(tok_c), where cur starts as softmax(p_v / T) and after
@@ -912,7 +904,7 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
     if (greedy) {
       unsigned long long best = 0ull;
       for (uint32_t i = t; i < V; i += 256) {
-        const unsigned long long k = tree_amax_key(pv[i], i);
+        const unsigned long long k = sh_amax_key(pv[i], i);
         best = k > best ? k : best;
       }
       for (int off = 32; off >= 1; off >>= 1) {
@@ -923,7 +915,7 @@ __global__ __launch_bounds__(256) void k_tree_accept(const float* __restrict__ p
       if ((t & 63) == 0) shk[t >> 6] = best;
       __syncthreads();
       for (int w = 0; w < 4; ++w) best = shk[w] > best ? shk[w] : best;
-      const uint32_t am = best == 0ull ? 0u : ~(uint32_t)(best & 0xFFFFFFFFull);
+      const uint32_t am = sh_amax_index(best);
       for (uint32_t c = v + 1; c < n && acc < 0; ++c)
         if (par[c] == (int32_t)v && tok[c] == am) acc = (int)c;
       if (acc < 0) { out_tok = am; break; }

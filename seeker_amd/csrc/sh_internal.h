@@ -11,6 +11,23 @@
 #include "gguf.h"
 #include "sh_error.h"
 
+// Orderable argmax key: a larger float gives a larger key, ties the lower
+// index. NaN and -inf give 0 and never win, so a row with no value above -inf
+// yields index 0: the host rule (the first x[i] > best, best starting at -inf;
+// inference/sample.rs:504-514). One definition for every argmax on the device
+// (k_argmax, the greedy tree walk), so their semantics cannot drift apart.
+__device__ __forceinline__ unsigned long long sh_amax_key(float v, uint32_t idx) {
+  if (!(v > -__builtin_inff())) return 0ull;
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)b << 32) | (unsigned long long)(~idx);
+}
+// The index a reduced key stands for (0 for the key 0 of a row without a value
+// above -inf).
+__device__ __forceinline__ uint32_t sh_amax_index(unsigned long long k) {
+  return k == 0ull ? 0u : ~(uint32_t)(k & 0xFFFFFFFFull);
+}
+
 // ---------------------------------------------------------------- errors
 
 #define SH_HIP(call)                                                              \

@@ -116,3 +116,45 @@ def test_tree_malformed_rejected(engine):
     with pytest.raises(SeekerError) as e:
         run_gpu(engine, p, q, tokens, bad, SH_SAMPLE_REJECTION, 1.0, seed=1)
     assert e.value.status == SH_ERR_ARG
+
+
+def test_greedy_argmax_special_values(engine):
+    """Greedy argmax on rows with NaN, +-inf and ties, through the greedy tree
+    walk (the same device key, sh_amax_key, as k_argmax): the host rule of
+    inference/sample.rs:504-514 as or_argmax states it (the first x[i] > best,
+    best from -inf): NaN and -inf never win, a row without a value above -inf
+    gives 0, ties give the lowest index. Each tree's root row is one case; its
+    first child carries the root's expected argmax, so the walk accepts it and
+    the next token is the child row's argmax (a second case)."""
+    print("greedy argmax special values", flush=True)
+    V, nan, inf = 300, np.float32(np.nan), np.float32(np.inf)
+    rng = np.random.default_rng(5)
+    rows = []
+    r = rng.standard_normal(V).astype(np.float32); r[rng.integers(0, V, 40)] = nan; rows.append(r)  # NaNs sprinkled
+    rows.append(np.full(V, nan, np.float32))                                                          # all NaN
+    rows.append(np.full(V, -inf, np.float32))                                                         # all -inf
+    r = np.full(V, -inf, np.float32); r[0] = nan; rows.append(r)                                      # NaN, then -inf
+    r = np.full(V, -inf, np.float32); r[150] = r[200] = 5.0; rows.append(r)                           # tie
+    r = rng.standard_normal(V).astype(np.float32); r[77] = r[99] = inf; rows.append(r)                # +inf tie
+    r = np.full(V, nan, np.float32); r[3] = inf; rows.append(r)                                       # NaN, +inf
+    r = np.full(V, -inf, np.float32); r[5] = np.float32(-3e38); rows.append(r)                        # lowest finite
+    r = np.full(V, nan, np.float32); r[290] = -1.0; r[10] = -1.0; rows.append(r)                      # tie among NaN
+    r = rng.standard_normal(V).astype(np.float32); r[::2] = -inf; rows.append(r)                      # half -inf
+    B, n = len(rows) // 2, 3
+    par = np.array([-1, 0, 0], np.int32)
+    p = np.zeros((B, n, V), np.float32)
+    tokens = np.zeros((B, n), np.uint32)
+    for b in range(B):
+        p[b, 0], p[b, 1] = rows[2 * b], rows[2 * b + 1]
+        p[b, 2] = rng.standard_normal(V).astype(np.float32)
+        tokens[b, 1] = O.argmax(p[b, 0])
+        tokens[b, 2] = (O.argmax(p[b, 0]) + 1) % V
+    q = np.zeros_like(p)
+    parents = np.tile(par, (B, 1))
+    paths, nxt = run_gpu(engine, p, q, tokens, parents, SH_SAMPLE_GREEDY, 0.0, 0)
+    for b in range(B):
+        want_path, want_next = O.tree_accept(p[b], q[b], tokens[b], par, 0.0, np.zeros((n, 2), np.float32))
+        assert want_path == [0, 1], (b, want_path)
+        assert (paths[b], int(nxt[b])) == (want_path, want_next), (b, paths[b], int(nxt[b]), want_next)
+    # the oracle's rule itself on the cases above
+    assert [O.argmax(x) for x in rows[1:9]] == [0, 0, 0, 150, 77, 3, 5, 10]
