@@ -1137,15 +1137,21 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
       if ((rc = gemm(L.wo, set0, EPI_PART, po, "gemv_o", &pending))) return rc;
       pending_ld = po.ldo;
     }
-    if (!prepped && (rc = resid_prep(L.ffn_norm))) return rc;
+    if (m->n_expert && f16) {
+      // the experts take the f32-level operand (the reference's expert matvec
+      // is not its wide GEMM) and the router reads the residual, so one
+      // f32-level prep adds Wo's partials and builds that operand (the f16
+      // rows of a wide prep would go unread; same sums in the same order)
+      PrepArgs px = pr;
+      px.bh = nullptr; px.mode = PREP_RESID; px.x = w.resid; px.K = m->d; px.norm_w = L.ffn_norm;
+      px.nparts = pending; px.part_ld = pending_ld;
+      pending = 0;
+      cur = set0;
+      if ((rc = sh_prep_launch(e, px))) return rc;
+    } else if (!prepped && (rc = resid_prep(L.ffn_norm))) {
+      return rc;
+    }
     if (m->n_expert) {  // routed experts add into the residual themselves
-      if (f16) {
-        // the experts take the f32-level operand (the reference's expert
-        // matvec is not its wide GEMM): built from the updated residual
-        PrepArgs px = pr;
-        px.bh = nullptr; px.mode = PREP_RESID; px.x = w.resid; px.K = m->d; px.norm_w = L.ffn_norm; px.nparts = 0;
-        if ((rc = sh_prep_launch(e, px))) return rc;
-      }
       if ((rc = moe_ffn(m, L, nc))) return rc;
       continue;
     }
