@@ -154,6 +154,10 @@ __device__ __forceinline__ void store_h4(uint16_t* p, float4 v) {
 // per thread and pass, one pass for K <= 4096): v as in k_prep; with a norm
 // weight the RMS factor over the whole column first, then
 // bh = f16((v * rsqrt(mean + eps)) * w) in rms_norm.slang:39-55's order.
+// PREP_MOE_COMBINE adds the routed experts' weighted outputs to x first, as
+// k_moe_combine does (moe.hip: per element a fused multiply-add chain over the
+// selection order from 0, then one add to x), so the combine and the next
+// layer's operand rows are one launch.
 template <int MODE>
 __global__ __launch_bounds__(1024) void k_prep16_rows(PrepArgs a) {
   const uint32_t col = blockIdx.x, tid = threadIdx.x;
@@ -164,6 +168,20 @@ __global__ __launch_bounds__(1024) void k_prep16_rows(PrepArgs a) {
     float4 v = *(const float4*)(xc + k);
     if (MODE == PREP_RESID && a.nparts) {
       v = sum_parts(a.part + (size_t)col * a.part_ld + k, pstride, a.nparts, v);
+      *(float4*)(xc + k) = v;
+    }
+    if (MODE == PREP_MOE_COMBINE) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (uint32_t j = 0; j < a.moe_k; ++j) {
+        const uint32_t s = a.moe_slot[(size_t)col * a.moe_k + j];
+        const float wt = a.moe_wts[(size_t)col * a.moe_k + j];
+        const float4 y = *(const float4*)(a.moe_y + (size_t)s * a.K + k);
+        acc.x = __builtin_fmaf(wt, y.x, acc.x);
+        acc.y = __builtin_fmaf(wt, y.y, acc.y);
+        acc.z = __builtin_fmaf(wt, y.z, acc.z);
+        acc.w = __builtin_fmaf(wt, y.w, acc.w);
+      }
+      v.x += acc.x; v.y += acc.y; v.z += acc.z; v.w += acc.w;
       *(float4*)(xc + k) = v;
     }
     ss += sh_sq4(v);
@@ -214,18 +232,23 @@ int sh_prep_launch(sh_engine* e, const PrepArgs& a) {
              a.N);
     SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");
     SH_CHECK(a.mode != PREP_RESID || a.nparts == 0 || a.part, SH_ERR_ARG, "prep partials missing");
+    SH_CHECK(a.mode != PREP_MOE_COMBINE || (a.moe_y && a.moe_slot && a.moe_wts && a.moe_k >= 1 && a.K % 4 == 0),
+             SH_ERR_ARG, "prep: expert outputs missing");
     hipEvent_t ev = nullptr;
     sh_prof_begin(e, &ev);
     if (a.mode == PREP_SWIGLU)
       hipLaunchKernelGGL(k_prep16_swiglu, dim3((a.K + 255) / 256, a.N), dim3(64), 0, e->stream, a);
     else if (a.mode == PREP_RESID)
       hipLaunchKernelGGL((k_prep16_rows<PREP_RESID>), dim3(a.N), dim3(1024), 0, e->stream, a);
+    else if (a.mode == PREP_MOE_COMBINE)
+      hipLaunchKernelGGL((k_prep16_rows<PREP_MOE_COMBINE>), dim3(a.N), dim3(1024), 0, e->stream, a);
     else
       hipLaunchKernelGGL((k_prep16_rows<PREP_PLAIN>), dim3(a.N), dim3(1024), 0, e->stream, a);
     SH_HIP(hipGetLastError());
     sh_prof_end(e, a.norm_w ? "rmsnorm_prep" : "prep", 0.0, ev);
     return SH_OK;
   }
+  SH_CHECK(a.mode != PREP_MOE_COMBINE, SH_ERR_ARG, "prep: the expert combine builds f16 rows only");
   SH_CHECK(a.N >= 1 && a.N <= SH_MAX_PREP_COLS, SH_ERR_ARG, "prep N=%u outside [1, %u]", a.N, SH_MAX_PREP_COLS);
   SH_CHECK(a.part_cols >= a.N || a.nparts == 0, SH_ERR_ARG, "prep: partials hold %u columns, N=%u", a.part_cols, a.N);
   SH_CHECK(a.mode == PREP_SWIGLU ? (a.part && a.nparts > 0) : a.x != nullptr, SH_ERR_ARG, "prep inputs missing");

@@ -913,8 +913,10 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
 // squares. Router + top-k per column, the routing plan (pairs grouped by
 // expert), gate/up of every routed expert over its columns (one pass over
 // each active expert's slab), SwiGLU + down operand over the pairs, down,
-// then the routing-weighted sum added to w.resid.
-static int moe_ffn(sh_model* m, const Layer& L, uint32_t nc) {
+// then the routing-weighted sum added to w.resid. With next_norm on a wide
+// call the sum goes in with the next operand's f16 rows (w.bh, RMSNorm by
+// next_norm) in one launch.
+static int moe_ffn(sh_model* m, const Layer& L, uint32_t nc, const float* next_norm = nullptr) {
   sh_engine* e = m->e;
   Workspace& w = m->ws;
   const uint32_t k = m->n_used, P = nc * k, E = m->n_expert, mc = sh_moe_max_chunks(P, E);
@@ -936,6 +938,13 @@ static int moe_ffn(sh_model* m, const Layer& L, uint32_t nc) {
   if ((rc = sh_moe_gemm_launch(e, L.wdown_exps, E, w.moe_bx, w.moe_xs, w.moe_cs, mc, w.moe_info, nullptr, dn,
                                "moe_down", 0.0)))
     return rc;
+  if (next_norm && m->call16) {
+    PrepArgs pc;
+    pc.mode = PREP_MOE_COMBINE; pc.x = w.resid; pc.K = m->d; pc.N = nc; pc.norm_w = next_norm; pc.eps = m->eps;
+    pc.bh = w.bh; pc.ldb = m->d;
+    pc.moe_y = w.moe_y; pc.moe_slot = w.moe_slot; pc.moe_wts = w.moe_wts; pc.moe_k = k;
+    return sh_prep_launch(e, pc);
+  }
   return sh_moe_combine_launch(e, w.moe_y, w.moe_slot, w.moe_wts, k, m->d, nc, w.resid);
 }
 
@@ -1152,7 +1161,12 @@ static int forward_chunk_mg(sh_model* m, const uint32_t* dev_tokens, uint32_t nc
       return rc;
     }
     if (m->n_expert) {  // routed experts add into the residual themselves
-      if ((rc = moe_ffn(m, L, nc))) return rc;
+      // on a wide call the next operand's f16 rows come with the expert sum
+      const float* next_norm =
+          !f16 ? nullptr : (l + 1 < m->n_layer ? m->layers[l + 1].attn_norm : (want_logits ? m->out_norm : nullptr));
+      if ((rc = moe_ffn(m, L, nc, next_norm))) return rc;
+      prepped = next_norm != nullptr;
+      cur = set0;
       continue;
     }
     EpiArgs pg = part_args(L.wgu);

@@ -437,7 +437,7 @@ int sh_moe_gemm_launch(sh_engine* e, const QMat& w, uint32_t n_expert, const uin
 // of two s so its max|y*s| lies in [2^9, 2^10): the f16 low halves then stay
 // normal (an f16 subnormal keeps only 2^-24 of absolute resolution) and the
 // 32-element XS sums stay below 2^15.
-enum PrepMode { PREP_PLAIN = 0, PREP_RESID = 1, PREP_SWIGLU = 2 };
+enum PrepMode { PREP_PLAIN = 0, PREP_RESID = 1, PREP_SWIGLU = 2, PREP_MOE_COMBINE = 3 };
 struct PrepArgs {
   int mode = PREP_PLAIN;
   float* ssq = nullptr;         // with norm_w: per-superblock sums of squares [K/256][8] out
@@ -455,6 +455,13 @@ struct PrepArgs {
   // as the reference's wide GEMM stages its input; ssq, bx, xs, cs unused.
   uint16_t* bh = nullptr;
   uint32_t ldb = 0;
+  // PREP_MOE_COMBINE (with bh only): x += sum_j wts[col k + j] y[slot_of[col k
+  // + j]] first (the routed experts' weighted sum, k_moe_combine's
+  // arithmetic), then the operand as PREP_RESID without partials.
+  const float* moe_y = nullptr;
+  const uint32_t* moe_slot = nullptr;
+  const float* moe_wts = nullptr;
+  uint32_t moe_k = 0;
 };
 // N <= SH_MAX_PREP_COLS; the operand buffers hold ceil(N / 8) groups.
 int sh_prep_launch(sh_engine* e, const PrepArgs& a);
