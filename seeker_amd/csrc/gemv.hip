@@ -889,8 +889,8 @@ __device__ __forceinline__ void fused_swiglu_sb(const EpiArgs& ea, const PrepFus
   sh_operand_store_sb(v, pf.K, j, col, pf.bx, pf.xs, pf.cs);
 }
 
-template <int T, int NB, int D, int EPI, bool FS = false>
-__global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
+template <int T, int NB, int D, int EPI, bool FS = false, int WV = GW>
+__global__ __launch_bounds__(64 * WV) void k_gemv_q4t(const uint8_t* __restrict__ Wp, uint32_t tiles, uint32_t nsb,
                                                        const uint16_t* __restrict__ Bx,
                                                        const uint16_t* __restrict__ XS,
                                                        const float* __restrict__ CS, uint32_t N, EpiArgs ea,
@@ -898,17 +898,25 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict_
   static_assert(EPI == EPI_STORE || EPI == EPI_PART || EPI == EPI_QKV, "deep-ring GEMV: per-row epilogues only");
   static_assert(!FS || EPI == EPI_PART, "fused SwiGLU prep: gate / up sums");
   constexpr int U = NB * T;
-  __shared__ f4 red[T][GW][64];
+  __shared__ f4 red[T][WV][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, r = lane & 15;
   const uint32_t tile0 = blockIdx.x * T;
-  float ssq_t[SSQ_PRE];
-  col_ssq_load(ea, r & 7, ssq_t);
-  // unit u: superblock wave + GW * (u / T), tile tile0 + u % T (clamped in bounds)
+  // the RMS sums of squares: in registers, or (16 waves, registers tight)
+  // staged in LDS by the first threads; both add them in superblock order
+  constexpr bool SSQ_LDS = WV > GW;
+  __shared__ float s_ssq[SSQ_LDS ? 64 * WV : 1];
+  float ssq_t[SSQ_LDS ? 1 : SSQ_PRE];
+  if constexpr (SSQ_LDS) {
+    if (ea.ssq && threadIdx.x < ea.ssq_n * 8) s_ssq[threadIdx.x] = ea.ssq[threadIdx.x];
+  } else {
+    col_ssq_load(ea, r & 7, ssq_t);
+  }
+  // unit u: superblock wave + WV * (u / T), tile tile0 + u % T (clamped in bounds)
   auto unit_ptr = [&](int u) {
     const uint32_t t = tile0 + u % T, tile = t < tiles ? t : tiles - 1;
-    return Wp + ((size_t)tile * nsb + wave + GW * (u / T)) * SH_Q4K_TILE_BYTES;
+    return Wp + ((size_t)tile * nsb + wave + WV * (u / T)) * SH_Q4K_TILE_BYTES;
   };
   Q4Tile ring[D];
 #pragma unroll
@@ -917,7 +925,7 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict_
   float c[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
-    const uint32_t b = wave + GW * i;
+    const uint32_t b = wave + WV * i;
 #pragma unroll
     for (int k = 0; k < 8; ++k) bq[i][k] = as_h8(ld16(Bx + ((size_t)(b * 8 + k) * 64 + lane) * 8));
     bm[i] = as_h8(ld16(XS + ((size_t)b * 64 + lane) * 8));
@@ -931,13 +939,19 @@ __global__ __launch_bounds__(64 * GW) void k_gemv_q4t(const uint8_t* __restrict_
     q4_tile_mma(ring[u % D], bq[u / T], bm[u / T], c[u / T], y[u % T]);
     if (u + D < U) ring[u % D] = load_q4_tile(unit_ptr(u + D), lane, g, r);
   }
-  const float nf = col_ssq_rinv(ea, r & 7, ssq_t);
+  float nf = 1.0f;
+  if constexpr (!SSQ_LDS) nf = col_ssq_rinv(ea, r & 7, ssq_t);
 #pragma unroll
   for (int t = 0; t < T; ++t) red[t][wave][lane] = y[t];
   __syncthreads();
+  if (SSQ_LDS && ea.ssq) {
+    float ss = 0.f;
+    for (uint32_t i = 0; i < ea.ssq_n; ++i) ss += s_ssq[i * 8 + (r & 7)];
+    nf = 1.0f / sqrtf(ss / (float)ea.norm_K + ea.eps);
+  }
   if (wave < T) {
     f4 v = {0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < GW; ++w) v += red[wave][w][lane];
+    for (int w = 0; w < WV; ++w) v += red[wave][w][lane];
     float o[4];
     col_sum4(v, nf, o);
     const uint32_t tile = tile0 + wave;
@@ -2608,7 +2622,17 @@ static void launch_q4t(sh_engine* e, const QMat& w, const uint16_t* bx, const ui
     return;
   }
   const dim3 grid(w.tiles / 7);
-  if (w.K == 4096)
+  // K = 4096: 16 waves of one superblock each (4 waves per SIMD; the 8B
+  // gate/up 21.5 -> 20.4 us per launch, window 2 and 3 alike) unless
+  // SH_RING16=0 (8 waves of two superblocks, 254 VGPRs: 2 waves per SIMD)
+  static const bool ring16 = [] {
+    const char* s = getenv("SH_RING16");
+    return !(s && std::string(s) == "0");
+  }();
+  if (w.K == 4096 && ring16)
+    hipLaunchKernelGGL((k_gemv_q4t<7, 1, 2, EPI, FS, 16>), grid, dim3(64 * 16), 0, e->stream, w.d, w.tiles, 16u, bx,
+                       xs, ea.cs, N, ea, pf);
+  else if (w.K == 4096)
     hipLaunchKernelGGL((k_gemv_q4t<7, 2, RING_D, EPI, FS>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 16u, bx,
                        xs, ea.cs, N, ea, pf);
   else
@@ -2622,6 +2646,8 @@ int sh_gemv_ring_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const u
   SH_CHECK(ea.cs, SH_ERR_ARG, "gemv: activation scales missing");
   const uint32_t T = sh_gemv_ring_t(w);
   SH_CHECK(T && (epi == EPI_STORE || epi == EPI_PART), SH_ERR_ARG, "gemv: this launch does not take the ring kernel");
+  // the 16-wave kernel stages the sums of squares with one thread each
+  SH_CHECK(!ea.ssq || ea.ssq_n * 8 <= 64 * 16, SH_ERR_ARG, "gemv: %u superblock sums of squares", ea.ssq_n);
   SH_CHECK(epi != EPI_PART || ea.part_cap >= 1, SH_ERR_CAPACITY, "gemv: no room for the partial sums");
   SH_CHECK(!swiglu || (epi == EPI_PART && swiglu->K * 2 == w.tiles * 16 && swiglu->K % 256 == 0 &&
                        swiglu->K / 256 <= SH_SB_CNT && swiglu->cnt && swiglu->bx && swiglu->xs && swiglu->cs),
