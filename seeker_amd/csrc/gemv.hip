@@ -903,9 +903,11 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4t(const uint8_t* __restrict_
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, r = lane & 15;
   const uint32_t tile0 = blockIdx.x * T;
-  // the RMS sums of squares: in registers, or (16 waves, registers tight)
-  // staged in LDS by the first threads; both add them in superblock order
-  constexpr bool SSQ_LDS = WV > GW;
+  // the RMS sums of squares: in registers, or staged in LDS by the first
+  // threads (16 waves, registers tight; T = 8: 126 instead of 178 VGPRs, two
+  // workgroups per CU, the draft's lm_head 38.3 -> 30.5 us); both add them in
+  // superblock order
+  constexpr bool SSQ_LDS = WV > GW || T == 8;
   __shared__ float s_ssq[SSQ_LDS ? 64 * WV : 1];
   float ssq_t[SSQ_LDS ? 1 : SSQ_PRE];
   if constexpr (SSQ_LDS) {
