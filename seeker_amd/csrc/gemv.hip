@@ -2618,7 +2618,12 @@ constexpr int RING_D = 3;
 template <int EPI, bool FS = false>
 static void launch_q4t(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                        const EpiArgs& ea, uint32_t T, const PrepFuse& pf = PrepFuse{}) {
-  if (T == 8) {  // K = 2048 only (sh_gemv_ring_t)
+  if (T == 8 && w.K == 4096) {  // 16 waves of one superblock each
+    hipLaunchKernelGGL((k_gemv_q4t<8, 1, RING_D, EPI, FS, 16>), dim3(w.tiles / 8), dim3(64 * 16), 0, e->stream, w.d,
+                       w.tiles, 16u, bx, xs, ea.cs, N, ea, pf);
+    return;
+  }
+  if (T == 8) {  // K = 2048
     hipLaunchKernelGGL((k_gemv_q4t<8, 1, RING_D, EPI, FS>), dim3((w.tiles + 7) / 8), dim3(64 * GW), 0, e->stream, w.d,
                        w.tiles, 8u, bx, xs, ea.cs, N, ea, pf);
     return;
@@ -2723,7 +2728,17 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
       else if (p.T == 2) launch_q4w<2, EPI_PART>(e, w, bx, xs, N, ea, p, sr, pf);
       else launch_q4w<4, EPI_PART>(e, w, bx, xs, N, ea, p, sr);
     } else {
-      const uint32_t rt = sr.kind == OPND_STAGED && epi == EPI_STORE ? sh_gemv_ring_t(w) : 0u;
+      uint32_t rt = sr.kind == OPND_STAGED && epi == EPI_STORE ? sh_gemv_ring_t(w) : 0u;
+      // K = 4096 stores of several rounds of 8 tiles (the 8B lm_head): the
+      // 16-wave ring, 70 -> 63 us per launch against k_gemv_q4s<8> (228 VGPRs,
+      // one workgroup of two waves per SIMD); SH_LM16=0: the stream kernel
+      static const bool lm16 = [] {
+        const char* s = getenv("SH_LM16");
+        return !(s && std::string(s) == "0");
+      }();
+      if (lm16 && !rt && sr.kind == OPND_STAGED && epi == EPI_STORE && w.type == GGML_Q4_K && w.K == 4096 &&
+          w.tiles % 8 == 0 && w.tiles / 8 >= 768)
+        rt = 8;
       switch (rt ? -1 : (int)epi) {
         case -1: launch_q4t<EPI_STORE>(e, w, bx, xs, N, ea, rt); break;
         case EPI_STORE: dispatch_q4s<EPI_STORE>(e, w, bx, xs, N, ea, sr); break;
