@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from parity import NARROW_REL, WIDE_REL, pair
+from parity import NARROW_REL, WIDE_REL, logits_close, pair, record
 from seeker_amd import synth as S
 
 pytestmark = pytest.mark.gpu
@@ -172,6 +172,67 @@ def test_stochastic_spec_step_lockstep(engine, models, mode):
     acc = _stochastic_lockstep(engine, gt, gd, ot, od, mode, 0.8, seed=21 + mode, n_steps=12, k=4)
     if mode == 2:
         assert acc > 0  # near-uniform p and q: many sampled drafts are accepted
+
+
+def _stream_vs_own(engine, gt, gd, ot, od, mode, T, seed, k, n_steps):
+    """The GPU's stochastic speculative decode against the oracle's own
+    (or_spec_step on the oracle's own logits, the same Philox words), step
+    after step until the streams part. Returns (steps equal, 1 if they
+    parted). A parting step must be a near tie: the two sides' logits of the
+    rows that decided it agree within the parity bounds, and the oracle's rule
+    on the GPU's own logits gives the GPU's tokens (a draw or accept test
+    within rounding of its threshold flips; nothing else may)."""
+    from seeker_amd._native import sh_sampling
+    prompt = S.tokens(777 + seed, 64, gt.dims.n_vocab)
+    gtkv, gdkv = engine.allocate_kv_cache(gt, 512), engine.allocate_kv_cache(gd, 512)
+    otkv, odkv = O.KvCache(ot, 512), O.KvCache(od, 512)
+    lg, _ = engine.forward_full_readback(gt, gtkv, prompt, 0, full_logits=False, want_residual=False)
+    engine.forward_full_readback(gd, gdkv, prompt, 0, full_logits=False, want_residual=False)
+    ol, _ = O.forward(ot, otkv, prompt, 0, logits_mode=1)
+    O.forward(od, odkv, prompt, 0, logits_mode=0)
+    last = int(lg[0].argmax())
+    assert last == O.argmax(ol[0])
+    s = sh_sampling()
+    s.mode, s.temperature, s.seed, s.counter = mode, T, seed, 0
+    wide = gt.cm1_attention or gt.wide_f16
+    equal, parted = 0, 0
+    for step in range(n_steps):
+        ctr = s.counter
+        r = engine.decode_speculative(gt, gd, gtkv, gdkv, last, k, s)
+        pg, qg = engine.spec_step_logits()
+        u = O.spec_uniforms(seed, ctr, len(r.drafts))
+        em, dr, po, qo = O.spec_step(ot, od, otkv, odkv, last, k, mode, T, u, want_logits=True)
+        if em == r.emitted and dr == r.drafts:
+            assert gtkv.position == otkv.position
+            equal += 1
+            last = em[-1]
+            continue
+        j = next((i for i in range(len(dr)) if dr[i] != r.drafts[i]), len(dr) - 1)
+        logits_close(np.asarray(qg[: j + 1]), np.asarray(qo[: j + 1]), wide)
+        logits_close(np.asarray(pg[: j + 1]), np.asarray(po[: j + 1]), wide)
+        assert O.spec_accept(mode, pg, qg, r.drafts, T, u) == r.emitted, step
+        print(f"  seed {seed}: streams part at step {step} (near tie)", flush=True)
+        parted = 1
+        break
+    for x in (gtkv, gdkv, otkv, odkv):
+        x.close()
+    return equal, parted
+
+
+@pytest.mark.parametrize("mode", [1, 2], ids=["compare", "rejection"])
+def test_stochastic_stream_equals_oracle_own(engine, models, mode):
+    """End to end over 4 seeds x 16 steps: the GPU's token stream equals the
+    oracle's own stochastic decode up to a near tie (see _stream_vs_own); the
+    steps compared and the near ties are recorded in the parity log."""
+    gt, gd, ot, od = models
+    print(f"stochastic stream vs the oracle's own decode, mode {mode}", flush=True)
+    equal = parted = 0
+    for seed in range(4):
+        e, p = _stream_vs_own(engine, gt, gd, ot, od, mode, 0.8, 31 + 10 * seed + mode, 4, 16)
+        equal += e
+        parted += p
+    record("stochastic_stream_steps", equal + parted, parted)
+    assert equal >= 32, (equal, parted)
 
 
 def test_rejection_spec_step_draft_equals_target(engine, models):
