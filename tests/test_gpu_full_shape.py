@@ -27,7 +27,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from parity import ids_agree, kv_layer0_ok, logits_close, pair
+from parity import ids_agree, kv_layer0_ok, logits_close, pair, record
 from seeker_amd import synth as S
 from seeker_amd._native import GGML_Q4_K, SH_SAMPLE_REJECTION, sh_sampling
 
@@ -207,12 +207,19 @@ def test_config3_tree_verify_b4_41_nodes_at_8192(engine, target):
     paths, nxt = engine.tree_verify_step(gm, caches, tokens, pars, qd, s)
     qd.free()
     U = O.philox_uniforms(11, 0x5EC, 0, 2 * B * n).reshape(B, n, 2)
+    own_differ = 0
     for b in range(B):
         # the step's decisions on its own logits (bit-identical to the batched verify's)
         want_path, want_next = O.tree_accept(gl[b], q[b], tokens[b], par, 1.0, U[b])
         assert paths[b] == want_path and int(nxt[b]) == want_next, (b, paths[b], want_path)
+        # end to end: the oracle's decision on its own logits; with the logits
+        # within the bounds (checked above) and the rule reproducing the GPU on
+        # the GPU's logits (just asserted), a difference can only be a near tie
+        own_path, own_next = O.tree_accept(ol[b], q[b], tokens[b], par, 1.0, U[b])
+        own_differ += int(own_path != paths[b] or own_next != int(nxt[b]))
         assert caches[b].position == P + len(paths[b])
         ocaches[b].compact(P, np.array(paths[b], np.uint32))
         check_new_rows(caches[b], ocaches[b], d, P, P + len(paths[b]), wide)
+    record("tree_paths_oracle_own_logits", B, own_differ)
     for x in caches + ocaches:
         x.close()
