@@ -4,7 +4,15 @@ ops/sampler.rs:41-132): top_k candidates sorted by logit descending (ties to
 the lower id) -> top_p (exclusive cumulative <= p keeps the crossing
 candidate) -> min_p (log-space cutoff against the largest) -> 1/T -> softmax
 -> first candidate whose cumulative probability reaches u. Every draw must
-equal the C oracle's or_sample_one on the same logits and uniform."""
+equal the C oracle's or_sample_one on the same logits and uniform.
+
+Both sides run the top_p cut and the inverse CDF with f64 softmax terms and
+f64 running sums; the reference's host chain uses f32 exp, sums and
+cumulative sums (inference/sample.rs:420-470, 518-533). At a candidate whose
+cumulative probability lies within f32 rounding of top_p, or a uniform within
+f32 rounding of a CDF boundary, the reference can pick the neighbouring
+token: these tests pin the GPU to the f64 chain, and parity with the
+reference's f32 chain is unpinned there."""
 import numpy as np
 import pytest
 
