@@ -533,7 +533,8 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_q4w(const uint8_t* __restrict_
                                                        const uint16_t* __restrict__ XS,
                                                        const float* __restrict__ CS, uint32_t N, EpiArgs ea,
                                                        OpndSrc src, PrepFuse pf) {
-  static_assert(!FP || (EPI == EPI_PART && SRC == OPND_STAGED && (T == 1 || T == 2)), "fused prep: split-K partials");
+  static_assert(!FP || (EPI == EPI_PART && (SRC == OPND_STAGED || SRC == OPND_ROWS) && (T == 1 || T == 2)),
+                "fused prep: split-K partials");
   constexpr int U = S * T;
   __shared__ h8 sB[S * 9 * 64];
   __shared__ float sC[64];
@@ -2501,7 +2502,7 @@ static void launch_q4w_fp(sh_engine* e, const QMat& w, const uint16_t* bx, const
 template <int T, int S, int EPI, int SRC>
 static void launch_q4w_src(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                            const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse* pf) {
-  if constexpr (EPI == EPI_PART && SRC == OPND_STAGED && (T == 1 || T == 2)) {
+  if constexpr (EPI == EPI_PART && (SRC == OPND_STAGED || SRC == OPND_ROWS) && (T == 1 || T == 2)) {
     if (pf) {
       launch_q4w_fp<T, S, EPI, SRC, true>(e, w, bx, xs, N, ea, p, src, *pf);
       return;
@@ -2512,7 +2513,7 @@ static void launch_q4w_src(sh_engine* e, const QMat& w, const uint16_t* bx, cons
 template <int T, int S, int EPI>
 static void launch_q4w_s(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                          const EpiArgs& ea, const WidePlan& p, const OpndSrc& src, const PrepFuse* pf) {
-  if (src.kind == OPND_ROWS) launch_q4w_src<T, S, EPI, OPND_ROWS>(e, w, bx, xs, N, ea, p, src, nullptr);
+  if (src.kind == OPND_ROWS) launch_q4w_src<T, S, EPI, OPND_ROWS>(e, w, bx, xs, N, ea, p, src, pf);
   else if (src.kind == OPND_FA) launch_q4w_src<T, S, EPI, OPND_FA>(e, w, bx, xs, N, ea, p, src, nullptr);
   else launch_q4w_src<T, S, EPI, OPND_STAGED>(e, w, bx, xs, N, ea, p, src, pf);
 }
@@ -2716,7 +2717,8 @@ int sh_gemv_launch(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16
                (sr.kind == OPND_RESID ? (epi == EPI_QKV || epi == EPI_SWIGLU) && sh_gemv_resid_fusable(w, N)
                                       : epi == EPI_PART && w.type == GGML_Q4_K && wide_plan(w, &p)),
            SH_ERR_ARG, "gemv: this operand source does not fit this launch");
-  SH_CHECK(!pf || (epi == EPI_PART && sr.kind == OPND_STAGED && sh_gemv_prep_fusable(w) && pf->K == w.tiles * 16 &&
+  SH_CHECK(!pf || (epi == EPI_PART && (sr.kind == OPND_STAGED || sr.kind == OPND_ROWS) && sh_gemv_prep_fusable(w) &&
+                   pf->K == w.tiles * 16 &&
                    pf->cnt && pf->resid && pf->norm_w && pf->ssq),
            SH_ERR_ARG, "gemv: the fused residual prep does not fit this launch");
   if (w.type == GGML_Q4_K) {

@@ -884,6 +884,16 @@ static int forward_chunk(sh_model* m, const uint32_t* dev_tokens, uint32_t nc, c
     } else if (!tuned(L.wdown)) {
       if ((rc = gemv_any(L.wdown, set0, EPI_PART, pd, "gemv_down", &pending))) return rc;
       pending_ld = pd.ldo;
+    } else if (fuse_rp && l + 1 == m->n_layer && want_logits && dsrc.kind == OPND_ROWS &&
+               sh_gemv_prep_fusable(L.wdown)) {
+      // the last down of a 1-2 column chunk finishes the residual and the
+      // lm_head's operand itself (set 1): no prep kernel before the lm_head
+      const PrepFuse pf = prep_fuse(m->out_norm);
+      if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", nullptr, &dsrc, &pf)))
+        return rc;
+      pending = 0;
+      cur = set1;
+      prepped = true;
     } else {
       if ((rc = sh_gemv_launch(e, L.wdown, w.bx, w.xs, nc, EPI_PART, pd, "gemv_down", &pending,
                                dsrc.kind == OPND_STAGED ? nullptr : &dsrc)))
