@@ -77,10 +77,13 @@ constexpr int kWaves = 4;   // waves per workgroup
 // where a ring of 4 at two workgroups per CU measured no gain: the waves wait
 // on their own MFMA / exp / LDS chains, not on the loads).
 template <int HD, int RGW, int KP, int NS = (KP == 2 ? 2 : 3)>
-__global__ __launch_bounds__(64 * kWaves, (KP == 1 && RGW == 1) ? 3 : 2) void k_fab(const FabSeg* __restrict__ segs, const uint32_t* __restrict__ work,
+__global__ __launch_bounds__(64 * kWaves, (KP == 1 && RGW == 1) ? (NS == 2 ? 4 : 3) : 2) void k_fab(const FabSeg* __restrict__ segs, const uint32_t* __restrict__ work,
                                                      const float* __restrict__ q, uint32_t n_head, uint32_t gqa,
                                                      uint32_t n_kv, uint32_t layer, uint32_t tps, float scale_log2,
                                                      float* __restrict__ part) {
+  // LEAN (2-deep ring, one row group, one key phase): K and V fragments in
+  // halves, under 128 VGPRs, so four workgroups share a CU
+  constexpr bool LEAN = NS == 2 && KP == 1 && RGW == 1;
   constexpr int TK = KP == 2 ? kTK : 32;  // keys per tile
   constexpr int NB = TK / 32;             // 32-key blocks per tile
   constexpr int NC = HD / 32, DT = HD / 16, CPR = HD / 8;
@@ -213,7 +216,24 @@ __global__ __launch_bounds__(64 * kWaves, (KP == 1 && RGW == 1) ? 3 : 2) void k_
       // scores of every row group from the K fragments first, then the V
       // fragments: K and V operands are never live together
       f4 sacc[RGW][2];
-      {
+      if constexpr (LEAN) {
+        // one 16-key tile's K fragments at a time (16 registers, not 32)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          h8 kop[NC];
+          const int row = 32 * bb + 16 * kt + r;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) kop[c] = lds_h8(&sK[row * HD + 8 * ((4 * c + g) ^ (row % CPR))]);
+          f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            acc = mfma16b(kop[c], qhi[0][c], acc);
+            acc = mfma16b(kop[c], qlo[0][c], acc);
+          }
+          sacc[0][kt] = acc;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
         h8 kop[2][NC];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
@@ -236,12 +256,18 @@ __global__ __launch_bounds__(64 * kWaves, (KP == 1 && RGW == 1) ? 3 : 2) void k_
           }
         }
       }
-      h8 vop[DT];
+      // V fragments: all DT, or (LEAN) the first half now, the second after
+      // the first half's products
+      constexpr int VH = LEAN ? DT / 2 : DT;
+      auto load_v = [&](h8* vv, int dt0) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int dr = 16 * dt + r;
-        vop[dt] = lds_h8(&sV[(bb * HD + dr) * 32 + 8 * (g ^ ((dr >> 1) & 3))]);
-      }
+        for (int j = 0; j < VH; ++j) {
+          const int dr = 16 * (dt0 + j) + r;
+          vv[j] = lds_h8(&sV[(bb * HD + dr) * 32 + 8 * (g ^ ((dr >> 1) & 3))]);
+        }
+      };
+      h8 vop[VH];
+      load_v(vop, 0);
       const bool tail = key0 + 32 > key_end || key0 + 32 > mbase;
 #pragma unroll
       for (int i = 0; i < RGW; ++i) {
@@ -281,10 +307,20 @@ __global__ __launch_bounds__(64 * kWaves, (KP == 1 && RGW == 1) ? 3 : 2) void k_
         h8 phi, plo;
         split8b(p, phi, plo);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        for (int dt = 0; dt < VH; ++dt) {
           o[i][dt] *= alpha;
           o[i][dt] = mfma16b(vop[dt], phi, o[i][dt]);
           o[i][dt] = mfma16b(vop[dt], plo, o[i][dt]);
+        }
+        if constexpr (LEAN) {
+          __builtin_amdgcn_sched_barrier(0);
+          load_v(vop, VH);
+#pragma unroll
+          for (int dt = 0; dt < VH; ++dt) {
+            o[i][VH + dt] *= alpha;
+            o[i][VH + dt] = mfma16b(vop[dt], phi, o[i][VH + dt]);
+            o[i][VH + dt] = mfma16b(vop[dt], plo, o[i][VH + dt]);
+          }
         }
       }
     }
@@ -340,17 +376,29 @@ __global__ __launch_bounds__(64) void k_fab_combine(const FabSeg* __restrict__ s
   }
 }
 
-template <int HD, int RGW, int KP>
+template <int HD, int RGW, int KP, int NS = (KP == 2 ? 2 : 3)>
 void launch_fab(const FabLaunch& fl, hipStream_t st, const float* q, uint32_t n_head, uint32_t gqa, uint32_t n_kv,
                 uint32_t layer, float scale_log2, float* part) {
-  hipLaunchKernelGGL((k_fab<HD, RGW, KP>), dim3(fl.nwork, n_kv), dim3(64 * kWaves), 0, st, fl.segs, fl.work, q,
+  hipLaunchKernelGGL((k_fab<HD, RGW, KP, NS>), dim3(fl.nwork, n_kv), dim3(64 * kWaves), 0, st, fl.segs, fl.work, q,
                      n_head, gqa, n_kv, layer, fl.tps, scale_log2, part);
+}
+// One row group per wave, one key phase: the lean variant (2-deep ring, K and
+// V fragments in halves, 127 VGPRs, four workgroups per CU) unless
+// SH_FAB4=0 (3-deep ring, 147 VGPRs, three per CU). Measured at hd 128:
+// the tree step's attention 2.11 -> 1.98 ms, the MoE verify's 2.93 -> 2.81.
+static bool fab4() {
+  static const bool v = [] {
+    const char* s = getenv("SH_FAB4");
+    return !(s && std::string(s) == "0");
+  }();
+  return v;
 }
 
 template <int HD>
 void launch_fab_hd(const FabLaunch& fl, hipStream_t st, const float* q, uint32_t n_head, uint32_t gqa, uint32_t n_kv,
                    uint32_t layer, float scale_log2, float* part) {
   if (fl.kp == 2) launch_fab<HD, 1, 2>(fl, st, q, n_head, gqa, n_kv, layer, scale_log2, part);
+  else if (fl.rgw == 1 && fab4()) launch_fab<HD, 1, 1, 2>(fl, st, q, n_head, gqa, n_kv, layer, scale_log2, part);
   else if (fl.rgw == 1) launch_fab<HD, 1, 1>(fl, st, q, n_head, gqa, n_kv, layer, scale_log2, part);
   else launch_fab<HD, 2, 1>(fl, st, q, n_head, gqa, n_kv, layer, scale_log2, part);
 }
