@@ -355,7 +355,10 @@ __global__ __launch_bounds__(64 * kWaves, (KP == 1 && RGW == 1) ? (NS == 2 ? 4 :
 // column's segment gives its partials; writes attn [nc][Dq] and the column's
 // superblock of the Wo operand (with bh: the f16 row bh[c][Dq] of the wide
 // f16 GEMM instead).
-template <int HD>
+// NCH: chunks of 16 partials loaded together (sh_fa_combine4); 1 when no
+// segment has more than 17 (half the registers, no clamped repeat loads),
+// with bit-identical results.
+template <int HD, int NCH>
 __global__ __launch_bounds__(64) void k_fab_combine(const FabSeg* __restrict__ segs, const uint32_t* __restrict__ colseg,
                                                     const float* __restrict__ part, uint32_t n_head, uint32_t gqa,
                                                     uint32_t kp, float* __restrict__ attn, uint16_t* __restrict__ bx,
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(64) void k_fab_combine(const FabSeg* __restrict__ s
   const uint32_t sb = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
   const FabSeg& sg = segs[colseg[c]];
   const uint32_t Dq = n_head * HD, k = 256 * sb + 4 * lane, nsv = sg.nsplit * kp;
-  const float4 v = sh_fa_combine4<2>(part + sg.part_off, nsv, nsv, sg.rows_pad, HD, n_head, gqa, sg.ncol, sb,
+  const float4 v = sh_fa_combine4<NCH>(part + sg.part_off, nsv, nsv, sg.rows_pad, HD, n_head, gqa, sg.ncol, sb,
                                      c - sg.col0);
   if (k < Dq) *(float4*)(attn + (size_t)c * Dq + k) = v;
   if (bh) {
@@ -440,6 +443,7 @@ int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, ui
   // waves idle at the tile barriers when a chunk's count is not a multiple of 4
   // (tree verify attention 3.8 vs 4.6 ms per step, measured).
   out->kp = max_rg <= 2 ? 2 : 1;
+  out->max_nsv = 0;
   out->rgw = (out->kp == 1 && forced_rgw == 2) ? 2 : 1;
   const uint32_t rows_max = 16 * max_rg;
   // (a split's partials are rows x (hd + 4) floats against keys x 2 hd f16 of
@@ -460,6 +464,7 @@ int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, ui
     d.rows_pad = (gqa * a.ncol + 15) / 16 * 16;
     d.nsplit = (a.kvlen + SK - 1) / SK;
     SH_CHECK(d.nsplit <= 0xFFFF, SH_ERR_UNSUPPORTED, "batched attention: %u key splits", d.nsplit);
+    out->max_nsv = std::max(out->max_nsv, d.nsplit * out->kp);
     part_floats += (size_t)m->n_kv * d.nsplit * out->kp * d.rows_pad * PS;
     const uint32_t RG = d.rows_pad / 16;
     const uint32_t nch = out->kp == 1 ? (RG + 4 * out->rgw - 1) / (4 * out->rgw) : 1u;
@@ -527,12 +532,19 @@ int sh_fab_launch(sh_engine* e, const sh_model* m, const FabLaunch& fl, uint32_t
   sh_prof_end(e, "attention", 0.0, ev);
   sh_prof_begin(e, &ev);
   const dim3 cgrid((m->n_head * m->hd + 255) / 256, fl.nc);
-  if (m->hd == 128)
-    hipLaunchKernelGGL((k_fab_combine<128>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head, gqa,
-                       fl.kp, attn_out, bx, xs, cs, bh);
+  const bool one = fl.max_nsv <= 17;
+  if (m->hd == 128 && one)
+    hipLaunchKernelGGL((k_fab_combine<128, 1>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head,
+                       gqa, fl.kp, attn_out, bx, xs, cs, bh);
+  else if (m->hd == 128)
+    hipLaunchKernelGGL((k_fab_combine<128, 2>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head,
+                       gqa, fl.kp, attn_out, bx, xs, cs, bh);
+  else if (one)
+    hipLaunchKernelGGL((k_fab_combine<64, 1>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head,
+                       gqa, fl.kp, attn_out, bx, xs, cs, bh);
   else
-    hipLaunchKernelGGL((k_fab_combine<64>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head, gqa,
-                       fl.kp, attn_out, bx, xs, cs, bh);
+    hipLaunchKernelGGL((k_fab_combine<64, 2>), cgrid, dim3(64), 0, e->stream, fl.segs, fl.colseg, fl.part, m->n_head,
+                       gqa, fl.kp, attn_out, bx, xs, cs, bh);
   SH_HIP(hipGetLastError());
   sh_prof_end(e, "attn_combine", 0.0, ev);
   return SH_OK;

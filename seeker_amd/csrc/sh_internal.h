@@ -537,6 +537,7 @@ struct FabLaunch {
   const uint32_t* colseg = nullptr;  // segment of each chunk column
   float* part = nullptr;
   uint32_t nseg = 0, nwork = 0, nc = 0, tps = 0, rgw = 1, kp = 1;
+  uint32_t max_nsv = 0;  // most partials (key splits x kp) of one segment
 };
 int sh_fab_plan(sh_engine* e, sh_model* m, const FabSegIn* in, uint32_t nseg, uint32_t nc, FabLaunch* out);
 int sh_fab_launch(sh_engine* e, const sh_model* m, const FabLaunch& fl, uint32_t layer, const float* q, float* attn_out,
