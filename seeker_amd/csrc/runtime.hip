@@ -1906,8 +1906,11 @@ static int enqueue_greedy_step(sh_engine* e, sh_model* tm, sh_model* dm, sh_kv* 
                                uint32_t np, uint32_t dpos, uint32_t tpos, bool forced) {
   int rc = enqueue_drafts(e, dm, dkv, n, np, dpos, true, forced);
   if (rc) return rc;
-  if ((rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, tpos, nullptr, 2, nullptr, nullptr, nullptr))) return rc;
-  if ((rc = sh_argmax_launch(e, tm->ws.logits, tm->V, n + 1, tm->ws.amax, e->spec.samp))) return rc;
+  // ws.logits holds the last chunk's logits only: a verify of more than 8
+  // columns (k = 8) may take two chunks, whose logits are collected in tlogits
+  float* lg = n + 1 > 8 ? e->spec.tlogits : nullptr;
+  if ((rc = forward_dev(tm, tkv, e->spec.tok + np, n + 1, tpos, nullptr, 2, lg, nullptr, nullptr))) return rc;
+  if ((rc = sh_argmax_launch(e, lg ? lg : tm->ws.logits, tm->V, n + 1, tm->ws.amax, e->spec.samp))) return rc;
   SH_HIP(hipMemcpyAsync(e->spec.pinned + 16, e->spec.samp, 11 * 4, hipMemcpyDeviceToHost, e->stream));
   return SH_OK;
 }

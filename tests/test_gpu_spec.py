@@ -69,6 +69,18 @@ def test_spec_decode_config1_matches_oracle(engine, models):
     assert g == o
 
 
+def test_spec_decode_k8_two_verify_chunks(engine, models):
+    """k = 8: the 9-column verify of the Q8_0 target takes two chunks of the
+    8-column path; every column's greedy id must come from its own logits."""
+    gt, gd, ot, od = models
+    prompt = S.tokens(808, 24, gt.dims.n_vocab)
+    print("spec decode k=8 (two verify chunks): 48 tokens", flush=True)
+    g, steps = _gpu_decode(engine, gt, gd, prompt, 48, 8)
+    assert max(len(d) for _, d in steps) == 8
+    o = _oracle_decode(ot, od, prompt, 48, 8)
+    assert g == o
+
+
 def test_spec_decode_lossless_vs_plain_greedy(engine, models):
     """Spec decode emits what plain greedy decoding emits. The invariant is
     exact when the verify computes the same attention as single-token decode:
