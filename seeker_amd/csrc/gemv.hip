@@ -2685,7 +2685,17 @@ template <int T>
 static void launch_q4t_qkv(sh_engine* e, const QMat& w, const uint16_t* bx, const uint16_t* xs, uint32_t N,
                            const EpiArgs& ea) {
   const dim3 grid(w.tiles / T);
-  if (w.K == 4096)
+  // K = 4096: 16 waves of one superblock each (103 VGPRs, 4 waves per SIMD;
+  // the 8B verify's QKV 0.55 us faster per layer) unless SH_QKV16=0 (8 waves
+  // of two superblocks, 165 VGPRs: 3 waves per SIMD, one workgroup per CU)
+  static const bool q16 = [] {
+    const char* s = getenv("SH_QKV16");
+    return !(s && std::string(s) == "0");
+  }();
+  if (w.K == 4096 && q16)
+    hipLaunchKernelGGL((k_gemv_q4t<T, 1, 2, EPI_QKV, false, 16>), grid, dim3(64 * 16), 0, e->stream, w.d, w.tiles,
+                       16u, bx, xs, ea.cs, N, ea, PrepFuse{});
+  else if (w.K == 4096)
     hipLaunchKernelGGL((k_gemv_q4t<T, 2, RING_D, EPI_QKV>), grid, dim3(64 * GW), 0, e->stream, w.d, w.tiles, 16u,
                        bx, xs, ea.cs, N, ea, PrepFuse{});
   else
